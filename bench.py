@@ -1,0 +1,207 @@
+#!/usr/bin/env python3
+"""Benchmark of the hot path on one MI355X: the Qwen3-TTS-0.6B-shaped q8 talker decode step (BASELINE.json
+configs[1]): 28 layers, hidden 1024, 16 q / 8 kv heads x 128, SwiGLU FFN 3072, RoPE theta 1e6, q8 weights
+~N(0, 0.02) generated on the device, a 512-token f16 KV cache ~N(0, 1), a 3072-entry q8 head and Philox top-k 50
+sampling at T 0.9, batch 1.
+
+A step is one device-resident decode at position 512 (x already in HBM -> 28 layers -> final norm -> head ->
+sampled token in HBM), replayed as one captured HIP graph. Each step rewrites the same KV slot, so every step
+is the same work. Prints one JSON line:
+  value      tokens per second (one GPU, the whole job);
+  roofline   the dominant kernel class: algorithmic bytes of one launch / its average launch duration, with
+             durations stamped by HIP events at each kernel's start and end (hipExtLaunchKernel) on its stream;
+  cpu_baseline  the reference's own CPU step (oracle/_ref, compiled from its sources) or the C restatement,
+             timed on this host for a bounded number of steps.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "talker decode tok/s (0.6B q8, batch 1); GEMV HBM GB/s as % of peak"
+HBM_PEAK_GBS = 8000.0
+POS = 512
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(vh, dec, seconds, x):
+    """Times the reference CPU decode step (transformer_forward + head matmul + sample_logits) on this host."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as po
+    c = dec.cfg
+    threads = max(1, min(16, os.cpu_count() or 1))
+    layers = []
+    for li in range(c["layers"]):
+        d = {}
+        for n in ("q", "k", "v", "o", "gate", "up", "down"):
+            h = dec.mats[li][n]
+            rows, cols = vh.mat_shape(h)
+            data, scale, _ = vh.mat_download(h, c["wtype"])
+            d[n] = po.Mat(c["wtype"], data, rows, cols, scale)
+        d.update(dec.layers[li])
+        layers.append(d)
+    X = po.Xfmr(layers, dec.final_norm, c["hidden"], c["heads"], c["kv_heads"], c["head_dim"], c["inter"], c["eps"], dec.inv_freq)
+    kd = c["kv_heads"] * c["head_dim"]
+    kv = po.KV(c["layers"], POS + 4, kd, kv_f16=1)
+    for li in range(c["layers"]):
+        k, v = vh.seq_download(dec.seq, li, POS, kd)
+        kv.k[li, :POS], kv.v[li, :POS] = k, v
+    kv.c.len = POS
+    hd, hs, _ = vh.mat_download(dec.head, c["head_type"])
+    head = po.Mat(c["head_type"], hd, c["head_rows"], c["hidden"], hs)
+    out = np.empty(c["hidden"], np.float32)
+    u = po.uniform(0, 0, 0, 0)
+    import ctypes
+    tok = ctypes.c_int32()
+    R = po.ref()
+    times = []
+    if R is not None:
+        kind = "reference"
+        R.ref_set_threads(threads)
+        sess = R.ref_session_new(ctypes.byref(X.c), ctypes.byref(kv.c), ctypes.byref(head.c))
+        if not sess:
+            raise RuntimeError("reference session setup failed")
+        R.ref_session_step(sess, x.ctypes.data, out.ctypes.data, 0.9, 50, u, ctypes.byref(tok))  # warm
+        t_end = time.perf_counter() + seconds
+        while time.perf_counter() < t_end and len(times) < 2000:
+            t0 = time.perf_counter()
+            R.ref_session_step(sess, x.ctypes.data, out.ctypes.data, 0.9, 50, u, ctypes.byref(tok))
+            times.append(time.perf_counter() - t0)
+        R.ref_session_free(sess)
+    else:
+        kind = "port"
+        po.lib().vo_set_threads(threads)
+        t_end = time.perf_counter() + seconds
+        while time.perf_counter() < t_end and len(times) < 2000:
+            t0 = time.perf_counter()
+            kv.c.len = POS
+            o = po.transformer_forward(X, kv, x[None])
+            lg = po.matmul(head, o[None])[0]
+            po.sample_logits(lg, 0.9, 1.0, 50, 1.0, None, u)
+            times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads, "kind": kind,
+            "sample": f"{len(times)} decode steps at position {POS} (28-layer q8 talker + 3072-row q8 head + top-k 50 "
+                      f"sampling, {threads} threads, median of the steps, {sum(times):.1f} s of CPU work)"}
+
+
+def load_traffic(kernel_class):
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(p):
+        return None
+    try:
+        return json.load(open(p)).get(kernel_class)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=30)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        log("bench.py runs on one GPU only: this build's hot path (the batch-1 talker decode step) lives on a single "
+            "MI355X; the multi-GPU layout is a design note in DESIGN.md, and no figure at several GPUs is produced.")
+        sys.exit(2)
+    from vox_amd import synth
+    from vox_amd import voxhip as vh
+
+    vh.init("hip:0")
+    log("device:", vh.device_name())
+    t0 = time.perf_counter()
+    dec = synth.Decoder(synth.TALKER_0_6B, seed=0)
+    c = dec.cfg
+    log(f"synthetic talker built in {time.perf_counter() - t0:.1f} s")
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal(c["hidden"]).astype(np.float32)
+    dx, dtok = vh.DevBuf(x.nbytes), vh.DevBuf(4)
+    dx.upload(x)
+    cfg = vh.sample_cfg(0.9, 1.0, 50, seed=0, frame=0)
+
+    def step():
+        vh.decode_dev(dec.xfmr, dec.seq, POS, dx, 1, None, dec.head, None, cfg, dtok)
+
+    for _ in range(args.warmup):
+        step()
+    vh.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    vh.sync()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1000.0 / args.steps
+    tok = int(dtok.download(1, np.int32)[0])
+    log(f"timed {args.steps} steps: {ms_per_step * 1000:.1f} us/step, token {tok}")
+
+    r = vh.bench_decode(dec.xfmr, dec.seq, POS, dec.head, cfg, max(3, args.warmup // 5), args.steps)
+    classes = {}
+    for i, name in enumerate(vh.KERNEL_CLASSES):
+        n = r.class_launches[i]
+        if not n:
+            continue
+        ms = r.class_ms[i]
+        b = r.class_bytes[i]
+        classes[name] = {"launches_per_step": n, "us_per_launch": round(ms * 1000, 3), "bytes_per_launch": int(b),
+                         "GBps": round(b / (ms * 1e-3) / 1e9, 1) if ms > 0 else None}
+    dom = max(classes, key=lambda k: classes[k]["us_per_launch"] * classes[k]["launches_per_step"])
+    d = classes[dom]
+    achieved = d["GBps"]
+    gemv = [k for k in classes if k.endswith("_gemv")]
+    gemv_bytes = sum(classes[k]["bytes_per_launch"] * classes[k]["launches_per_step"] for k in gemv)
+    gemv_us = sum(classes[k]["us_per_launch"] * classes[k]["launches_per_step"] for k in gemv)
+    step_bytes = dec.step_bytes(POS)
+    log(json.dumps(classes))
+
+    cpu = None
+    if not args.no_cpu:
+        t0 = time.perf_counter()
+        cpu = cpu_baseline(vh, dec, args.cpu_seconds, x)
+        log(f"cpu baseline: {cpu} ({time.perf_counter() - t0:.1f} s incl. setup)")
+
+    line = {
+        "metric": METRIC,
+        "value": round(1000.0 / ms_per_step, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 x int8 -> int32 GEMV dots, f32 activations, f16 KV",
+        "data": "synthetic (device-generated Philox N(0,0.02) weights quantized to q8, f16 KV ~N(0,1))",
+        "config": {"workload": "qwen3-tts-0.6b-talker-decode-q8 (BASELINE configs[1])", "layers": c["layers"],
+                   "hidden": c["hidden"], "heads": c["heads"], "kv_heads": c["kv_heads"], "head_dim": c["head_dim"],
+                   "ffn": c["inter"], "kv_len": POS, "head_rows": c["head_rows"], "batch": 1, "top_k": 50,
+                   "temperature": 0.9, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(dom),
+                     "bytes_per_launch": d["bytes_per_launch"], "us_per_launch": d["us_per_launch"]},
+        "gemv": {"GBps": round(gemv_bytes / (gemv_us * 1e-6) / 1e9, 1), "frac": round(gemv_bytes / (gemv_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                 "bytes_per_step": gemv_bytes, "us_per_step": round(gemv_us, 2)},
+        "step": {"bytes": step_bytes, "GBps": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+                 "frac": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                 "kernel_us_per_step": round(r.kernel_ms_per_step * 1000, 2), "graph_us_per_step": round(r.ms_per_step * 1000, 2),
+                 "kernels_per_step": r.kernels_per_step},
+        "kernels": classes,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,245 @@
+/*
+ * voxhip.h — C ABI of the MI355X (gfx950) compute backend for Vox.
+ *
+ * This is the drop-in boundary. Every entry point flattens one function of the
+ * reference's device interface (/root/reference/src/gpu.hpp plus the gpu_* hooks
+ * declared in /root/reference/src/kernels.hpp:88-100) into plain pointers and
+ * sizes. No C++ or HIP types cross it. vox_amd/csrc/gpu_hip.cpp implements the
+ * unchanged vox::gpu_* C++ interface on top of it.
+ *
+ * Conventions (as the reference backend, gpu_vulkan.cpp:568-571, :800-803):
+ *  - no exception crosses the boundary;
+ *  - failure returns -1 (handles) or 0 (bool-like int), and the reason is
+ *    kept in voxhip_last_error();
+ *  - one device per process; every entry point takes one global lock, so the
+ *    library is thread-safe, and calls serialise.
+ * Handles are small non-negative ints, as in the reference.
+ */
+#ifndef VOXHIP_H
+#define VOXHIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VOXHIP_ABI_VERSION 1
+
+/* Weight element types, numbered as vox::WType (kernels.hpp:42). */
+enum voxhip_wtype { VOXHIP_F32 = 0, VOXHIP_F16 = 1, VOXHIP_BF16 = 2, VOXHIP_Q8 = 3, VOXHIP_Q4 = 4 };
+
+/* Host view of a weight matrix; fields as vox::Mat (kernels.hpp:44-56): [rows][cols] row-major,
+ * rows = outputs. Q8: int8 data + f32 scale [rows][cols/32]. Q4: 16 bytes per 32-block
+ * (byte j = w[j] | w[j+16] << 4, value (u - 8) * scale), f32 scale [rows][cols/32].
+ * bias: f32 [rows] or NULL. All pointers are host memory, read during the call only. */
+typedef struct voxhip_mat {
+    int32_t type;
+    const void *data;
+    const float *scale;
+    int64_t rows, cols;
+    const float *bias;
+} voxhip_mat;
+
+/* vox::GpuDeviceInfo (gpu.hpp:180-188); strings are fixed-size, NUL-terminated. */
+typedef struct voxhip_device_info {
+    int32_t index;
+    char name[256];
+    char type[16];
+    int32_t software, unified_memory;
+    uint64_t vram_total, vram_free, max_storage_range;
+    int32_t subgroup_arith, coop_matrix, memory_budget;
+    uint32_t api_version, vendor_id, driver_version;
+} voxhip_device_info;
+
+/* vox::GpuStats (gpu.hpp:174) without last_error (see voxhip_last_error). */
+typedef struct voxhip_stats {
+    int64_t mats_ok, mats_failed;
+    uint64_t bytes, bytes_failed;
+} voxhip_stats;
+
+/* vox::GpuMemInfo (gpu.hpp:193). */
+typedef struct voxhip_mem_info {
+    uint64_t used, limit, device_free, device_total;
+    int32_t device_index;
+} voxhip_mem_info;
+
+/* ---------------------------------------------------------------- device, init, accounting */
+/* gpu_enumerate (gpu.hpp:189): number of devices; 0 when the HIP runtime finds none. */
+int voxhip_device_count(void);
+/* gpu_enumerate entry `index`: 1 on success. */
+int voxhip_device_info_get(int index, voxhip_device_info *out);
+/* gpu_init (gpu.hpp:168). device: "hip", "hip:N", "gpu:N", or "vulkan:N" as family.cpp:94 passes it
+ * (N = device index, also taken from VOX_VK_DEVICE like gpu_vulkan.cpp:163). Failure is sticky,
+ * as gpu_vulkan.cpp:364. Returns 1 on success; on failure writes the reason to err. */
+int voxhip_init(const char *device, char *err, size_t err_len);
+int voxhip_active(void);                                   /* gpu_active (gpu.hpp:169) */
+const char *voxhip_device_name(void);                      /* gpu_device_name (gpu.hpp:170) */
+void voxhip_stats_get(voxhip_stats *out);                  /* gpu_stats (gpu.hpp:175) */
+const char *voxhip_last_error(void);                       /* GpuStats::last_error (gpu.hpp:174) */
+void voxhip_set_vram_limit(uint64_t bytes);                /* gpu_set_vram_limit (gpu.hpp:192) */
+void voxhip_mem_info_get(voxhip_mem_info *out);            /* gpu_mem_info (gpu.hpp:194) */
+
+/* ---------------------------------------------------------------- matrices */
+/* gpu_upload (gpu.hpp:172). n_parts > 1 stacks the parts' rows into one device matrix (same type
+ * and cols, all or none with bias), as upload_parts (gpu_vulkan.cpp:476-536). Returns a handle or -1. */
+int voxhip_upload(const voxhip_mat *parts, int n_parts);
+/* gpu_matmul (kernels.hpp:89): y[m][rows] = x[m][cols] . W^T (+ bias), host x and y.
+ * Semantics of matmul (kernels.cpp:653-705): Q8 with m <= 8 and Q4 quantize x per 32-block to int8
+ * and use integer dots; Q8 with m > 8 and F32/F16/BF16 use f32 activations. Returns 1 or 0. */
+int voxhip_matmul(int mat, const float *x, int64_t m, float *y);
+/* Rows and cols of a device matrix (0 on a bad handle). */
+int voxhip_mat_shape(int mat, int64_t *rows, int64_t *cols);
+
+/* ---------------------------------------------------------------- transformer */
+/* vox::LayerW (kernels.hpp:114-119). attn_scale / mlp_scale must be NULL (as gpu_vulkan.cpp:782). */
+typedef struct voxhip_layer {
+    voxhip_mat q, k, v, o, gate, up, down;
+    const float *qn, *kn;  /* per-head RMSNorm [head_dim] or NULL (both or none) */
+    const float *ln1, *ln2;
+    const float *attn_scale, *mlp_scale;
+} voxhip_layer;
+
+/* vox::TransformerW (kernels.hpp:120-130). window must be 0 (as gpu_vulkan.cpp:770); head_dim 64 or 128
+ * (the reference accepts any even head_dim <= 128; other sizes return -1 here and stay on the CPU);
+ * heads / kv_heads <= 8. inv_freq: [head_dim/2], as rope_inv_freq (kernels.cpp:734-738). */
+typedef struct voxhip_xfmr_desc {
+    int32_t n_layers;
+    const voxhip_layer *layers;
+    const float *final_norm;
+    int32_t hidden, heads, kv_heads, head_dim, inter;
+    float eps;
+    double theta;
+    int32_t window;
+    const float *inv_freq;
+} voxhip_xfmr_desc;
+
+/* Called once per uploaded matrix (layer, which = 0..6 for q,k,v,o,gate,up,down) right after its
+ * upload, so the caller may release the host pages (gpu.hpp:195-198, qwen3.cpp:309-316). */
+typedef void (*voxhip_uploaded_fn)(void *user, int32_t layer, int32_t which);
+
+/* gpu_xfmr_create (gpu.hpp:198). n_layers < 0 = all layers. Returns a handle or -1. */
+int voxhip_xfmr_create(const voxhip_xfmr_desc *w, const char *name, int n_layers, voxhip_uploaded_fn uploaded, void *user);
+/* gpu_seq_create (gpu.hpp:200): a KV cache of `capacity` positions (f16, on the device). The reference
+ * caps capacity at 3072 (gpu_vk_internal.hpp:34); this backend accepts up to 65536. Returns a handle or -1. */
+int voxhip_seq_create(int xfmr, int64_t capacity);
+void voxhip_seq_free(int seq);                             /* gpu_seq_free (gpu.hpp:201); buffers stay pooled */
+/* gpu_xfmr_forward (kernels.hpp:92-93): x [m][in_proj ? in_proj.cols : hidden] at positions pos0..pos0+m-1;
+ * out_last [hidden] = final RMSNorm of the last row (may be NULL); head >= 0: head_out [head.rows] = head
+ * applied to out_last. in_proj / head are matrix handles or -1. Returns 1 or 0. */
+int voxhip_xfmr_forward(int xfmr, int seq, int64_t pos0, const float *x, int64_t m, float *out_last, int in_proj,
+                        int head, float *head_out);
+/* gpu_xfmr_forward_hidden (kernels.hpp:96): the device layers only, no final norm: hidden_out [m][hidden]. */
+int voxhip_xfmr_forward_hidden(int xfmr, int seq, int64_t pos0, const float *x, int64_t m, float *hidden_out);
+/* gpu_xfmr_forward_pair (kernels.hpp:99-100): one token of each of two sequences at the same position. */
+int voxhip_xfmr_forward_pair(int xfmr, int seq0, int seq1, int64_t pos, const float *x2, int head, float *out2,
+                             float *head_out2);
+/* transformer_forward_steps (kernels.hpp:144-147) on the device: one token for each of B sequences
+ * (seqs[b] at position pos[b]); weights are read once for all B. out [B][hidden] normed; head >= 0:
+ * head_out [B][head.rows]. B <= 8. Returns 1 or 0. */
+int voxhip_xfmr_forward_steps(int xfmr, const int32_t *seqs, const int64_t *pos, int64_t B, const float *x,
+                              float *out, int head, float *head_out);
+
+/* ---------------------------------------------------------------- sampling */
+/* vox::SampleParams (sampling.hpp:52-57) + the Philox counter of DetRng::uniform (sampling.hpp:40-44)
+ * + the logit mask the engine applies before sampling code 0 (engine.cpp:664-668):
+ * logits[suppress_from .. suppress_to) = -inf except eos_code; eos_code also -inf when block_eos. */
+typedef struct voxhip_sample_cfg {
+    float temperature, top_p;
+    int32_t top_k;
+    float repetition_penalty;
+    uint32_t key0, key1;       /* DetRng key: seed low / high 32 bits */
+    uint64_t frame;
+    uint32_t codebook, draw;
+    int32_t suppress_from, suppress_to, eos_code, block_eos;
+} voxhip_sample_cfg;
+
+/* sample_logits (sampling.hpp:61-119) on the device, from host logits [n] and history [n_history].
+ * Writes the sampled index to *out_id. n <= 65536. Returns 1 or 0. */
+int voxhip_sample_logits(const float *logits, int32_t n, const voxhip_sample_cfg *cfg, const int32_t *history,
+                         int32_t n_history, int32_t *out_id);
+
+/* gpu_pred_frame (gpu.hpp:209-210), gpu_codec_* (gpu.hpp:213-219), gpu_f5_* (gpu.hpp:240-248),
+ * gpu_cosy_* (gpu.hpp:272-277) are not provided yet: gpu_hip.cpp answers them like gpu_stub.cpp
+ * (-1 / false), and the callers compute on the CPU. */
+
+/* ---------------------------------------------------------------- device-resident path
+ * Entry points for callers that keep activations in device memory (bench, tests, a device-side
+ * generate loop). Pointers named d_* are device pointers from voxhip_dev_alloc. */
+void *voxhip_dev_alloc(size_t bytes);
+void voxhip_dev_free(void *p);
+int voxhip_memcpy_h2d(void *d_dst, const void *src, size_t bytes);
+int voxhip_memcpy_d2h(void *dst, const void *d_src, size_t bytes);
+int voxhip_sync(void);
+
+/* One decode step with everything on the device: d_x [m][hidden] -> layers -> final norm of the last row
+ * (d_out_last [hidden], may be NULL) -> head (d_logits [head.rows]) -> sampler (d_token, when cfg != NULL).
+ * Launched as one captured HIP graph per (xfmr, seq, m, head, cfg != NULL); asynchronous on the library's
+ * stream. Returns 1 or 0. */
+int voxhip_decode_dev(int xfmr, int seq, int64_t pos0, const float *d_x, int64_t m, float *d_out_last, int head,
+                      float *d_logits, const voxhip_sample_cfg *cfg, int32_t *d_token);
+
+/* Synthetic weights and caches, generated on the device (Philox4x32-10 Box-Muller, mean + std * z).
+ * voxhip_mat_synthetic: f32 values, then quantized on the device to `type` with the reference's
+ * quantizer (Q8: kernels.cpp:918-929; Q4: kernels.cpp:606-645; F16/BF16: nearest even). Returns a handle. */
+int voxhip_mat_synthetic(int32_t type, int64_t rows, int64_t cols, uint64_t seed, uint32_t stream, float mean,
+                         float std, int with_bias);
+/* Copies a device matrix back in the reference host layout (data, scale, bias may be NULL). */
+int voxhip_mat_download(int mat, void *data, float *scale, float *bias);
+/* Releases a device matrix that no transformer uses (the reference keeps uploads for the process lifetime;
+ * this is for synthetic setups that restack matrices). Returns 1 or 0. */
+int voxhip_mat_free(int mat);
+/* Creates a transformer from matrices already on the device: per layer the handles of q,k,v,o,gate,up,down
+ * (7 ints per layer, in that order) and host norm vectors from desc (desc->layers[i].ln1 etc; the voxhip_mat
+ * fields of desc->layers are ignored). */
+int voxhip_xfmr_create_from_mats(const voxhip_xfmr_desc *w, const int32_t *mats, const char *name);
+/* Fills positions [0, len) of every layer of a KV cache with N(mean, std) values rounded to f16. */
+int voxhip_seq_fill_synthetic(int seq, int64_t len, uint64_t seed, uint32_t stream, float mean, float std);
+/* Copies positions [0, len) of layer `layer` of a KV cache to host f32 k, v [len][kv_heads*head_dim]. */
+int voxhip_seq_download(int seq, int32_t layer, int64_t len, float *k, float *v);
+
+/* Device quantizers of the reference formats (kernels.cpp:918-929, :606-645, :515-523) on device memory. */
+int voxhip_quantize_q8_dev(const float *d_w, int64_t rows, int64_t cols, int8_t *d_q, float *d_scale);
+int voxhip_quantize_q4_dev(const float *d_w, int64_t rows, int64_t cols, uint8_t *d_q, float *d_scale);
+int voxhip_quantize_act_dev(const float *d_x, int64_t n, int8_t *d_xq, float *d_xs);
+
+/* ---------------------------------------------------------------- measurement */
+/* Kernel classes of one decode step, for voxhip_bench_result. */
+enum voxhip_kernel_class {
+    VOXHIP_K_QKV = 0,      /* RMSNorm + q|k|v GEMV */
+    VOXHIP_K_O = 1,        /* o GEMV + residual */
+    VOXHIP_K_GATEUP = 2,   /* RMSNorm + gate|up GEMV + SwiGLU */
+    VOXHIP_K_DOWN = 3,     /* down GEMV + residual */
+    VOXHIP_K_HEAD = 4,     /* final RMSNorm + head GEMV */
+    VOXHIP_K_ATTN = 5,     /* split-K attention over the f16 cache */
+    VOXHIP_K_COMBINE = 6,  /* merge of the attention splits */
+    VOXHIP_K_QKPOST = 7,   /* q/k RMSNorm, RoPE, f16 K/V append */
+    VOXHIP_K_SAMPLE = 8,   /* device sampler */
+    VOXHIP_K_CLASSES = 9
+};
+
+/* Times `steps` replays of the captured decode graph (after `warmup` untimed ones) with HIP events on the
+ * library's stream: ms_per_step. Then runs `steps` more steps launching the same kernels one by one, each with
+ * start/stop events stamped at that kernel's own start and end (hipExtLaunchKernel): per-class average launch
+ * durations and the algorithmic bytes one launch of each class moves. */
+typedef struct voxhip_bench_result {
+    double ms_per_step;         /* whole decode step (graph replay), average */
+    double kernel_ms_per_step;  /* sum of the kernel durations of one step (event-stamped run) */
+    double step_bytes;          /* algorithmic HBM bytes per step (weights + scales, KV read + write, norms) */
+    int32_t kernels_per_step;
+    int32_t n_classes;
+    double class_ms[VOXHIP_K_CLASSES];        /* average duration of one launch of the class */
+    double class_bytes[VOXHIP_K_CLASSES];     /* algorithmic bytes of one launch of the class */
+    int32_t class_launches[VOXHIP_K_CLASSES]; /* launches per step */
+} voxhip_bench_result;
+int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, int head, const voxhip_sample_cfg *cfg, int warmup, int steps,
+                        voxhip_bench_result *out);
+
+/* Times one GEMV kernel configuration on `copies` distinct device copies of a synthetic q8 matrix
+ * (rotating, so the working set exceeds the 256 MB Infinity Cache): average ms per launch. */
+int voxhip_bench_gemv_q8(int64_t rows, int64_t cols, int copies, int warmup, int iters, double *ms_per_launch);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

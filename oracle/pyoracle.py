@@ -1,0 +1,249 @@
+"""ctypes binding of the CPU parity checker (oracle/liboracle.so) and of the
+compiled reference harness (oracle/_ref/libvoxref.so, present only where it
+was built from /root/reference).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py. The product (vox_amd/) never imports it.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libvoxref.so")
+
+F32, F16, BF16, Q8, Q4 = 0, 1, 2, 3, 4
+
+
+class VoMat(C.Structure):
+    _fields_ = [("type", C.c_int32), ("data", C.c_void_p), ("scale", C.c_void_p),
+                ("rows", C.c_int64), ("cols", C.c_int64), ("bias", C.c_void_p)]
+
+
+class VoLayer(C.Structure):
+    _fields_ = [(n, VoMat) for n in ("q", "k", "v", "o", "gate", "up", "down")] + \
+               [(n, C.c_void_p) for n in ("qn", "kn", "ln1", "ln2")]
+
+
+class VoXfmr(C.Structure):
+    _fields_ = [("n_layers", C.c_int32), ("layers", C.POINTER(VoLayer)), ("final_norm", C.c_void_p),
+                ("hidden", C.c_int32), ("heads", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
+                ("inter", C.c_int32), ("eps", C.c_float), ("inv_freq", C.c_void_p)]
+
+
+class VoKV(C.Structure):
+    _fields_ = [("k", C.c_void_p), ("v", C.c_void_p), ("cap", C.c_int64), ("len", C.c_int64),
+                ("kv_f16", C.c_int32), ("avx2", C.c_int32)]
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def _declare(lib, prefix):
+    P, I64, I32, F, D, U32, U64 = C.c_void_p, C.c_int64, C.c_int32, C.c_float, C.c_double, C.c_uint32, C.c_uint64
+    sig = {
+        "philox4x32_10" if prefix == "vo_" else "philox": (None, [P, P, P]),
+        "uniform": (F, [U64, U64, U32, U32]),
+        "sample_logits": (I32, [P, I32, F, F, I32, F, P, I32, F]),
+        "quantize_q8": (None, [P, I64, I64, P, P]),
+        "quantize_q4": (None, [P, I64, I64, P, P]),
+        "dot": (F, [P, P, I64]),
+        "rmsnorm": (None, [P, P, I64, F, P]),
+        "layernorm": (None, [P, P, P, I64, F, P]),
+        "rope_inv_freq": (None, [I64, D, P]),
+        "rope_apply": (None, [P, I64, I64, P, I64]),
+        "silu": (F, [F]),
+        "transformer_forward": (C.c_int, [P, P, P, I64, P, P]),
+        "transformer_forward_steps": (C.c_int, [P, P, I64, P, P]),
+    }
+    if prefix == "vo_":
+        sig.update({
+            "softmax": (None, [P, I64]),
+            "ras_sample": (I32, [P, I32, P, I32, F, I32, I32, F, F, F]),
+            "noise": (None, [U64, U32, C.c_size_t, P]),
+            "f16_to_f32": (F, [C.c_uint16]),
+            "f32_to_f16": (C.c_uint16, [F]),
+            "mat_row": (None, [P, I64, P]),
+            "quantize_act": (None, [P, I64, P, P]),
+            "matmul": (None, [P, P, I64, P, C.c_int]),
+            "matmul_q8_int": (None, [P, P, I64, P, C.c_int]),
+            "matmul_q4_int": (None, [P, P, I64, P, C.c_int]),
+            "matmul_f32_tiles": (None, [P, P, I64, P]),
+            "set_threads": (None, [C.c_int]),
+            "get_threads": (C.c_int, []),
+        })
+    else:
+        sig.update({
+            "softmax": (None, [P, I64]),
+            "mat_gather": (None, [P, I64, P]),
+            "matmul": (None, [P, P, I64, P]),
+            "set_threads": (None, [C.c_int]),
+            "session_new": (P, [P, P, P]),
+            "session_step": (C.c_int, [P, P, P, F, I32, F, P]),
+            "session_free": (None, [P]),
+        })
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, prefix + name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_oracle = None
+_ref = None
+
+
+def lib():
+    """The C restatement (always built by __graft_entry__.build())."""
+    global _oracle
+    if _oracle is None:
+        if not os.path.exists(ORACLE_SO):
+            raise RuntimeError(f"{ORACLE_SO} is not built; run __graft_entry__.build() or make -C oracle")
+        _oracle = _declare(C.CDLL(ORACLE_SO), "vo_")
+    return _oracle
+
+
+def ref():
+    """The compiled reference harness, or None where it was not built."""
+    global _ref
+    if _ref is None and os.path.exists(REF_SO):
+        _ref = _declare(C.CDLL(REF_SO), "ref_")
+    return _ref
+
+
+# ---------------------------------------------------------------- helpers
+class Mat:
+    """A weight matrix in the reference layout with its ctypes view."""
+
+    def __init__(self, wtype, data, rows, cols, scale=None, bias=None):
+        self.type, self.rows, self.cols = wtype, rows, cols
+        self.data = np.ascontiguousarray(data)
+        self.scale = None if scale is None else np.ascontiguousarray(scale, dtype=np.float32)
+        self.bias = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        self.c = VoMat(wtype, _p(self.data), _p(self.scale), rows, cols, _p(self.bias))
+
+
+def quantize_q8(w, use_ref=False):
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty((rows, cols // 32), np.float32)
+    getattr(ref() if use_ref else lib(), ("ref_" if use_ref else "vo_") + "quantize_q8")(_p(w), rows, cols, _p(q), _p(s))
+    return q, s
+
+
+def quantize_q4(w, use_ref=False):
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    q = np.empty((rows, cols // 2), np.uint8)
+    s = np.empty((rows, cols // 32), np.float32)
+    getattr(ref() if use_ref else lib(), ("ref_" if use_ref else "vo_") + "quantize_q4")(_p(w), rows, cols, _p(q), _p(s))
+    return q, s
+
+
+def quantize_act(x):
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    xq = np.empty(x.size, np.int8)
+    xs = np.empty(x.size // 32, np.float32)
+    lib().vo_quantize_act(_p(x), x.size, _p(xq), _p(xs))
+    return xq, xs
+
+
+def matmul(M, x, avx2=1, use_ref=False):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m = x.shape[0] if x.ndim == 2 else 1
+    y = np.empty((m, M.rows), np.float32)
+    if use_ref:
+        ref().ref_matmul(C.byref(M.c), _p(x), m, _p(y))
+    else:
+        lib().vo_matmul(C.byref(M.c), _p(x), m, _p(y), avx2)
+    return y
+
+
+def mat_row(M, r, use_ref=False):
+    out = np.empty(M.cols, np.float32)
+    if use_ref:
+        ref().ref_mat_gather(C.byref(M.c), r, _p(out))
+    else:
+        lib().vo_mat_row(C.byref(M.c), r, _p(out))
+    return out
+
+
+def sample_logits(logits, temperature=0.9, top_p=1.0, top_k=50, rep=1.0, history=None, u=0.5, use_ref=False):
+    l = np.ascontiguousarray(logits, dtype=np.float32).copy()
+    h = None if history is None else np.ascontiguousarray(history, dtype=np.int32)
+    fn = ref().ref_sample_logits if use_ref else lib().vo_sample_logits
+    return fn(_p(l), l.size, temperature, top_p, top_k, rep, _p(h), 0 if h is None else h.size, u)
+
+
+def uniform(seed, frame, cb, draw=0):
+    return lib().vo_uniform(seed, frame, cb, draw)
+
+
+def noise(seed, stream, n):
+    out = np.empty(n, np.float32)
+    lib().vo_noise(seed, stream, n, _p(out))
+    return out
+
+
+class Xfmr:
+    """A Qwen3-shaped transformer in the oracle's struct layout (keeps its arrays alive)."""
+
+    def __init__(self, layers, final_norm, hidden, heads, kv_heads, head_dim, inter, eps, inv_freq):
+        self.layers = layers  # list of dicts: q,k,v,o,gate,up,down (Mat), qn,kn,ln1,ln2 (np or None)
+        self.final_norm = np.ascontiguousarray(final_norm, np.float32)
+        self.inv_freq = np.ascontiguousarray(inv_freq, np.float32)
+        self.hidden, self.heads, self.kv_heads, self.head_dim, self.inter, self.eps = hidden, heads, kv_heads, head_dim, inter, eps
+        arr = (VoLayer * len(layers))()
+        for i, L in enumerate(layers):
+            for n in ("q", "k", "v", "o", "gate", "up", "down"):
+                setattr(arr[i], n, L[n].c)
+            for n in ("qn", "kn", "ln1", "ln2"):
+                setattr(arr[i], n, _p(L.get(n)))
+        self._arr = arr
+        self.c = VoXfmr(len(layers), arr, _p(self.final_norm), hidden, heads, kv_heads, head_dim, inter, eps,
+                        _p(self.inv_freq))
+
+
+class KV:
+    """Flat [layer][cap][kv_heads*head_dim] f32 cache."""
+
+    def __init__(self, n_layers, cap, kd, kv_f16=0, avx2=1, k=None, v=None, length=0):
+        self.k = np.zeros((n_layers, cap, kd), np.float32) if k is None else np.ascontiguousarray(k, np.float32)
+        self.v = np.zeros((n_layers, cap, kd), np.float32) if v is None else np.ascontiguousarray(v, np.float32)
+        self.c = VoKV(_p(self.k), _p(self.v), cap, length, kv_f16, avx2)
+
+    @property
+    def len(self):
+        return self.c.len
+
+    def copy(self):
+        n = KV(self.k.shape[0], self.k.shape[1], self.k.shape[2], self.c.kv_f16, self.c.avx2, self.k.copy(), self.v.copy(), self.c.len)
+        return n
+
+
+def transformer_forward(X, kv, x, want_all=False, use_ref=False):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m = x.shape[0]
+    out_last = np.empty(X.hidden, np.float32)
+    out_all = np.empty((m, X.hidden), np.float32) if want_all else None
+    fn = ref().ref_transformer_forward if use_ref else lib().vo_transformer_forward
+    rc = fn(C.byref(X.c), C.byref(kv.c), _p(x), m, _p(out_last), _p(out_all))
+    if rc != 0:
+        raise RuntimeError(f"transformer_forward failed ({rc})")
+    return (out_last, out_all) if want_all else out_last
+
+
+def transformer_forward_steps(X, kvs, x, use_ref=False):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    B = x.shape[0]
+    ptrs = (C.POINTER(VoKV) * B)(*[C.pointer(k.c) for k in kvs])
+    out = np.empty((B, X.hidden), np.float32)
+    fn = ref().ref_transformer_forward_steps if use_ref else lib().vo_transformer_forward_steps
+    rc = fn(C.byref(X.c), ptrs, B, _p(x), _p(out))
+    if rc != 0:
+        raise RuntimeError(f"transformer_forward_steps failed ({rc})")
+    return out

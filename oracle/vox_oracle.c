@@ -1,0 +1,674 @@
+/*
+ * vox_oracle.c — CPU restatement of the reference hot path (see vox_oracle.h).
+ *
+ * TEST INFRASTRUCTURE ONLY: the parity checker, never the product. Built with
+ * -ffp-contract=off; explicit fmaf() marks the places where the reference's
+ * AVX2/FMA code paths fuse.
+ */
+#define _GNU_SOURCE
+#include "vox_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ threads */
+static int g_threads = 1;
+void vo_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+int vo_get_threads(void) { return g_threads; }
+
+typedef void (*vo_range_fn)(void *ctx, int64_t r0, int64_t r1);
+typedef struct { vo_range_fn fn; void *ctx; int64_t r0, r1; } vo_job;
+static void *vo_job_run(void *p) { vo_job *j = (vo_job *)p; j->fn(j->ctx, j->r0, j->r1); return NULL; }
+
+/* Splits [0, total) into contiguous ranges, one per thread. Each output row is computed by exactly one
+ * thread with a fixed operation order, so results do not depend on the thread count (as kernels.cpp:681-685). */
+static void vo_parallel_rows(int64_t total, vo_range_fn fn, void *ctx) {
+    int nt = g_threads;
+    if (nt <= 1 || total < 64) { fn(ctx, 0, total); return; }
+    if (nt > 64) nt = 64;
+    pthread_t th[64];
+    vo_job jobs[64];
+    const int64_t per = (total + nt - 1) / nt;
+    int started = 0;
+    for (int t = 0; t < nt; ++t) {
+        int64_t a = (int64_t)t * per, b = a + per < total ? a + per : total;
+        if (a >= b) break;
+        jobs[t].fn = fn; jobs[t].ctx = ctx; jobs[t].r0 = a; jobs[t].r1 = b;
+        if (t == 0) continue;
+        if (pthread_create(&th[t], NULL, vo_job_run, &jobs[t]) != 0) { fn(ctx, a, b); jobs[t].fn = NULL; }
+        started = t;
+    }
+    fn(ctx, jobs[0].r0, jobs[0].r1);
+    for (int t = 1; t <= started; ++t) if (jobs[t].fn) pthread_join(th[t], NULL);
+}
+
+/* ------------------------------------------------------------------ Philox / DetRng (sampling.hpp:16-50) */
+void vo_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+    uint32_t k0 = key[0], k1 = key[1];
+    for (int round = 0; round < 10; ++round) {
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+        const uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+        const uint32_t n1 = (uint32_t)p1;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+        const uint32_t n3 = (uint32_t)p0;
+        c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+        if (round < 9) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+float vo_uniform(uint64_t seed, uint64_t frame, uint32_t codebook, uint32_t draw) {
+    const uint32_t ctr[4] = {(uint32_t)frame, (uint32_t)(frame >> 32), codebook, draw};
+    const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t r[4];
+    vo_philox4x32_10(ctr, key, r);
+    return (float)(r[0] >> 8) * (1.0f / 16777216.0f);
+}
+
+void vo_noise(uint64_t seed, uint32_t stream, size_t n, float *out) {
+    const double two_pi = 2.0 * 3.14159265358979323846;
+    for (size_t p = 0; p < (n + 1) / 2; ++p) {
+        const double u1 = (double)vo_uniform(seed, p, stream, 0), u2 = (double)vo_uniform(seed, p, stream, 1);
+        const double r = sqrt(-2.0 * log(1.0 - u1));
+        const double a = two_pi * u2;
+        out[2 * p] = (float)(r * cos(a));
+        if (2 * p + 1 < n) out[2 * p + 1] = (float)(r * sin(a));
+    }
+}
+
+/* ------------------------------------------------------------------ sample_logits (sampling.hpp:61-119) */
+static const float *g_sort_vals;
+/* strict total order: larger value first, lower index on equal values (sampling.hpp:83-85) */
+static int vo_better_cmp(const void *pa, const void *pb) {
+    const int32_t a = *(const int32_t *)pa, b = *(const int32_t *)pb;
+    const float va = g_sort_vals[a], vb = g_sort_vals[b];
+    if (va > vb) return -1;
+    if (vb > va) return 1;
+    if (va == vb) return a < b ? -1 : (a > b ? 1 : 0);
+    return a < b ? -1 : 1; /* NaN: keep index order (unordered in the reference) */
+}
+
+int32_t vo_sample_logits(float *l, int32_t n, float temperature, float top_p, int32_t top_k,
+                         float repetition_penalty, const int32_t *history, int32_t n_history, float u) {
+    if (n <= 0) return -1;
+    if (history && repetition_penalty != 1.0f) {
+        uint8_t *seen = (uint8_t *)calloc((size_t)n, 1);
+        for (int32_t i = 0; i < n_history; ++i) {
+            const int32_t t = history[i];
+            if (t >= 0 && t < n && !seen[t]) {
+                seen[t] = 1;
+                l[t] = l[t] > 0 ? l[t] / repetition_penalty : l[t] * repetition_penalty;
+            }
+        }
+        free(seen);
+    }
+    if (temperature <= 0.0f) { /* greedy: first maximum (std::max_element) */
+        int32_t best = 0;
+        for (int32_t i = 1; i < n; ++i) if (l[best] < l[i]) best = i;
+        return best;
+    }
+    int32_t *idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)n);
+    for (int32_t i = 0; i < n; ++i) idx[i] = i;
+    g_sort_vals = l;
+    qsort(idx, (size_t)n, sizeof(int32_t), vo_better_cmp); /* sorted prefix == partial_sort prefix (total order) */
+    const int32_t k = (top_k > 0 && top_k < n) ? top_k : n;
+    double *probs = (double *)malloc(sizeof(double) * (size_t)k);
+    const double inv_t = 1.0 / (double)temperature;
+    const double mx = (double)l[idx[0]];
+    double sum = 0;
+    for (int32_t i = 0; i < k; ++i) { probs[i] = exp(((double)l[idx[i]] - mx) * inv_t); sum += probs[i]; }
+    for (int32_t i = 0; i < k; ++i) probs[i] /= sum;
+    int32_t keep = k;
+    if (top_p > 0.0f && top_p < 1.0f) {
+        double c = 0;
+        for (int32_t i = 0; i < k; ++i) { c += probs[i]; if (c >= (double)top_p) { keep = i + 1; break; } }
+    }
+    double total = 0;
+    for (int32_t i = 0; i < keep; ++i) total += probs[i];
+    const double target = (double)u * total;
+    double acc = 0;
+    int32_t pick = idx[keep - 1];
+    for (int32_t i = 0; i < keep; ++i) { acc += probs[i]; if (target < acc) { pick = idx[i]; break; } }
+    free(probs);
+    free(idx);
+    return pick;
+}
+
+/* ------------------------------------------------------------------ RAS sampler (cosyvoice.cpp:617-664) */
+static const double *g_sort_probs;
+static int vo_prob_desc_cmp(const void *pa, const void *pb) {
+    const int a = *(const int *)pa, b = *(const int *)pb;
+    const double x = g_sort_probs[a], y = g_sort_probs[b];
+    if (x > y) return -1;
+    if (y > x) return 1;
+    return a < b ? -1 : (a > b ? 1 : 0); /* equal: original order (std::stable_sort) */
+}
+
+int32_t vo_ras_sample(float *logp, int32_t n, const int32_t *decoded, int32_t n_decoded, float top_p, int32_t top_k,
+                      int32_t win_size, float tau_r, float u0, float u1) {
+    float mx = -INFINITY;
+    for (int32_t i = 0; i < n; ++i) mx = mx < logp[i] ? logp[i] : mx; /* std::max(mx, v) */
+    double *pr = (double *)malloc(sizeof(double) * (size_t)n);
+    double sum = 0;
+    for (int32_t i = 0; i < n; ++i) { pr[i] = exp((double)(logp[i] - mx)); sum += pr[i]; }
+    for (int32_t i = 0; i < n; ++i) pr[i] /= sum;
+    int *idx = (int *)malloc(sizeof(int) * (size_t)n);
+    for (int32_t i = 0; i < n; ++i) idx[i] = i;
+    g_sort_probs = pr;
+    qsort(idx, (size_t)n, sizeof(int), vo_prob_desc_cmp);
+    int32_t nkeep = 0;
+    double cum = 0, ksum = 0;
+    for (int32_t i = 0; i < n; ++i) {
+        if (cum < (double)top_p && nkeep < top_k) { cum += pr[idx[i]]; ++nkeep; }
+        else break;
+    }
+    for (int32_t i = 0; i < nkeep; ++i) ksum += pr[idx[i]];
+    int32_t top = idx[nkeep - 1];
+    double acc = 0;
+    const double target = (double)u0 * ksum;
+    for (int32_t i = 0; i < nkeep; ++i) { acc += pr[idx[i]]; if (target < acc) { top = idx[i]; break; } }
+    int rep = 0;
+    const int32_t from = n_decoded > win_size ? n_decoded - win_size : 0;
+    for (int32_t i = from; i < n_decoded; ++i) rep += decoded[i] == top;
+    int32_t result = top;
+    if ((double)rep >= (double)win_size * (double)tau_r) {
+        logp[top] = -INFINITY;
+        double s2 = 0;
+        for (int32_t i = 0; i < n; ++i) s2 += i == top ? 0.0 : pr[i];
+        const double t2 = (double)u1 * s2;
+        double a2 = 0;
+        int32_t last = top == 0 ? 1 : 0;
+        result = -1;
+        for (int32_t i = 0; i < n; ++i) {
+            if (i == top) continue;
+            last = i;
+            a2 += pr[i];
+            if (t2 < a2) { result = i; break; }
+        }
+        if (result < 0) result = last;
+    }
+    free(idx);
+    free(pr);
+    return result;
+}
+
+/* ------------------------------------------------------------------ formats */
+float vo_f16_to_f32(uint16_t h) { /* exact widening incl. subnormals (kernels.hpp:63-75) */
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu, man = h & 0x3FFu, bits;
+    if (e == 0) {
+        if (man == 0) bits = sign;
+        else {
+            int shift = 0;
+            while (!(man & 0x400u)) { man <<= 1; ++shift; }
+            bits = sign | (uint32_t)(113 - shift) << 23 | (man & 0x3FFu) << 13;
+        }
+    } else if (e == 31) bits = sign | 0x7F800000u | man << 13;
+    else bits = sign | (e + 112) << 23 | man << 13;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+uint16_t vo_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    const uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return (uint16_t)(sign | 0x7C00u | (ax > 0x7F800000u ? 0x200u : 0u));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u); /* rounds to >= 65520 -> inf */
+    if (ax < 0x38800000u) { /* result subnormal or zero: scale by 2^24 and round to integer (nearest even) */
+        float a;
+        memcpy(&a, &ax, 4);
+        const float s = a * 16777216.0f; /* exact: a < 2^-14 */
+        return (uint16_t)(sign | (uint16_t)lrintf(s));
+    }
+    const uint32_t mant = ax & 0x7FFFFFu, e = (ax >> 23) - 112;
+    uint32_t r = e << 10 | mant >> 13;
+    const uint32_t rest = mant & 0x1FFFu;
+    if (rest > 0x1000u || (rest == 0x1000u && (r & 1u))) ++r;
+    return (uint16_t)(sign | r);
+}
+
+float vo_bf16_to_f32(uint16_t h) {
+    const uint32_t b = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+/* mat_row (kernels.cpp:432-466) */
+void vo_mat_row(const vo_mat *W, int64_t r, float *out) {
+    const int64_t c = W->cols;
+    switch (W->type) {
+        case VO_F32: memcpy(out, (const float *)W->data + r * c, sizeof(float) * (size_t)c); break;
+        case VO_F16: { const uint16_t *p = (const uint16_t *)W->data + r * c; for (int64_t i = 0; i < c; ++i) out[i] = vo_f16_to_f32(p[i]); } break;
+        case VO_BF16: { const uint16_t *p = (const uint16_t *)W->data + r * c; for (int64_t i = 0; i < c; ++i) out[i] = vo_bf16_to_f32(p[i]); } break;
+        case VO_Q8: {
+            const int8_t *p = (const int8_t *)W->data + r * c;
+            const float *s = W->scale + r * (c / 32);
+            for (int64_t i = 0; i < c; ++i) out[i] = (float)p[i] * s[i / 32];
+        } break;
+        case VO_Q4: {
+            const uint8_t *p = (const uint8_t *)W->data + r * (c / 2);
+            const float *s = W->scale + r * (c / 32);
+            for (int64_t b = 0; b < c / 32; ++b)
+                for (int j = 0; j < 16; ++j) {
+                    const uint8_t v = p[b * 16 + j];
+                    out[b * 32 + j] = (float)((int)(v & 15) - 8) * s[b];
+                    out[b * 32 + 16 + j] = (float)((int)(v >> 4) - 8) * s[b];
+                }
+        } break;
+        default: break;
+    }
+}
+
+/* quantize_q8 (kernels.cpp:918-929): scale max|x|/127, q = lround(w / s), half away from zero */
+void vo_quantize_q8(const float *w, int64_t rows, int64_t cols, int8_t *q, float *scale) {
+    const int64_t nb = cols / 32;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t b = 0; b < nb; ++b) {
+            const float *p = w + r * cols + b * 32;
+            float mx = 0;
+            for (int j = 0; j < 32; ++j) { const float a = fabsf(p[j]); mx = mx < a ? a : mx; }
+            const float s = mx / 127.0f;
+            scale[r * nb + b] = s;
+            for (int j = 0; j < 32; ++j) q[r * cols + b * 32 + j] = s > 0 ? (int8_t)lroundf(p[j] / s) : 0;
+        }
+}
+
+/* quantize_q4 (kernels.cpp:606-645): scale search d = mx / -t, t = 7 .. 9 step 0.25, then least squares */
+void vo_quantize_q4(const float *w, int64_t rows, int64_t cols, uint8_t *q, float *scale) {
+    const int64_t nb = cols / 32;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t b = 0; b < nb; ++b) {
+            const float *p = w + r * cols + b * 32;
+            float mx = 0; /* signed value of largest magnitude, first one wins */
+            for (int j = 0; j < 32; ++j) if (fabsf(p[j]) > fabsf(mx)) mx = p[j];
+            float best_d = mx / -8.0f;
+            double best_err = INFINITY;
+            int8_t best_q[32];
+            memset(best_q, 0, sizeof best_q);
+            if (mx != 0.0f)
+                for (int k = 0; k <= 8; ++k) {
+                    const float d = mx / -(7.0f + 0.25f * (float)k), inv = 1.0f / d;
+                    int8_t qq[32];
+                    double err = 0;
+                    for (int j = 0; j < 32; ++j) {
+                        float c = floorf(p[j] * inv + 8.5f);
+                        c = c < 0.0f ? 0.0f : c;
+                        c = c > 15.0f ? 15.0f : c;
+                        qq[j] = (int8_t)((int)c - 8);
+                        const double e = (double)p[j] - (double)qq[j] * (double)d;
+                        err += e * e;
+                    }
+                    if (err < best_err) { best_err = err; best_d = d; memcpy(best_q, qq, 32); }
+                }
+            if (mx != 0.0f) {
+                double num = 0, den = 0;
+                for (int j = 0; j < 32; ++j) { num += (double)p[j] * best_q[j]; den += (double)best_q[j] * best_q[j]; }
+                if (den > 0) {
+                    const float d2 = (float)(num / den);
+                    double err = 0;
+                    for (int j = 0; j < 32; ++j) { const double e = (double)p[j] - (double)best_q[j] * (double)d2; err += e * e; }
+                    if (err < best_err) best_d = d2;
+                }
+            }
+            scale[r * nb + b] = best_d;
+            uint8_t *o = q + r * (cols / 2) + b * 16;
+            for (int j = 0; j < 16; ++j) o[j] = (uint8_t)((uint8_t)(best_q[j] + 8) | (uint8_t)((best_q[j + 16] + 8) << 4));
+        }
+}
+
+/* activation quantization of matmul_q8 / matmul_q4 (kernels.cpp:515-523, :582-590) */
+void vo_quantize_act(const float *x, int64_t n, int8_t *xq, float *xs) {
+    for (int64_t b = 0; b < n / 32; ++b) {
+        const float *p = x + b * 32;
+        float mx = 0;
+        for (int j = 0; j < 32; ++j) { const float a = fabsf(p[j]); mx = mx < a ? a : mx; } /* std::max(mx, a) */
+        const float sc = mx / 127.0f, inv = sc > 0 ? 1.0f / sc : 0.0f;
+        xs[b] = sc;
+        for (int j = 0; j < 32; ++j) xq[b * 32 + j] = (int8_t)lrintf(p[j] * inv);
+    }
+}
+
+/* ------------------------------------------------------------------ integer dots */
+/* AVX2 dot (kernels.cpp:485-501): lane l of the 8-lane accumulator takes the exact int sum of block elements
+ * 4l..4l+3 and fuses it with (ws * xs); the lanes are summed as ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)). */
+static float q8dot_avx2_order(const int8_t *wq, const float *ws, const int8_t *xq, const float *xs, int64_t nb) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int64_t b = 0; b < nb; ++b) {
+        const float c = ws[b] * xs[b];
+        for (int l = 0; l < 8; ++l) {
+            int s = 0;
+            for (int t = 0; t < 4; ++t) s += (int)wq[b * 32 + 4 * l + t] * (int)xq[b * 32 + 4 * l + t];
+            acc[l] = fmaf((float)s, c, acc[l]);
+        }
+    }
+    return ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
+}
+
+/* scalar dot (kernels.cpp:475-483): s += float(acc) * ws * xs, left to right */
+static float q8dot_scalar_order(const int8_t *wq, const float *ws, const int8_t *xq, const float *xs, int64_t nb) {
+    float s = 0;
+    for (int64_t b = 0; b < nb; ++b) {
+        int acc = 0;
+        for (int j = 0; j < 32; ++j) acc += (int)wq[b * 32 + j] * (int)xq[b * 32 + j];
+        s += (float)acc * ws[b] * xs[b];
+    }
+    return s;
+}
+
+static void q4_unpack_block(const uint8_t *src, int8_t *dst) { /* kernels.hpp:46, kernels.cpp:557-562 */
+    for (int j = 0; j < 16; ++j) { dst[j] = (int8_t)((int)(src[j] & 15) - 8); dst[j + 16] = (int8_t)((int)(src[j] >> 4) - 8); }
+}
+
+typedef struct {
+    const vo_mat *W;
+    const int8_t *xq;
+    const float *xs;
+    int64_t m;
+    float *y;
+    int avx2;
+} vo_int_ctx;
+
+static void q8_rows(void *p, int64_t r0, int64_t r1) {
+    const vo_int_ctx *c = (const vo_int_ctx *)p;
+    const int64_t rows = c->W->rows, cols = c->W->cols, nb = cols / 32;
+    for (int64_t r = r0; r < r1; ++r) {
+        const int8_t *wr = (const int8_t *)c->W->data + r * cols;
+        const float *ws = c->W->scale + r * nb;
+        const float bz = c->W->bias ? c->W->bias[r] : 0.0f;
+        for (int64_t i = 0; i < c->m; ++i) {
+            const float d = c->avx2 ? q8dot_avx2_order(wr, ws, c->xq + i * cols, c->xs + i * nb, nb)
+                                    : q8dot_scalar_order(wr, ws, c->xq + i * cols, c->xs + i * nb, nb);
+            c->y[i * rows + r] = d + bz;
+        }
+    }
+}
+
+static void q4_rows(void *p, int64_t r0, int64_t r1) {
+    const vo_int_ctx *c = (const vo_int_ctx *)p;
+    const int64_t rows = c->W->rows, cols = c->W->cols, nb = cols / 32;
+    int8_t *wr = (int8_t *)malloc((size_t)cols);
+    for (int64_t r = r0; r < r1; ++r) {
+        const uint8_t *src = (const uint8_t *)c->W->data + r * (cols / 2);
+        for (int64_t b = 0; b < nb; ++b) q4_unpack_block(src + b * 16, wr + b * 32);
+        const float *ws = c->W->scale + r * nb;
+        const float bz = c->W->bias ? c->W->bias[r] : 0.0f;
+        for (int64_t i = 0; i < c->m; ++i) {
+            const float d = c->avx2 ? q8dot_avx2_order(wr, ws, c->xq + i * cols, c->xs + i * nb, nb)
+                                    : q8dot_scalar_order(wr, ws, c->xq + i * cols, c->xs + i * nb, nb);
+            c->y[i * rows + r] = d + bz;
+        }
+    }
+    free(wr);
+}
+
+static void int_path(const vo_mat *W, const float *x, int64_t m, float *y, int avx2, vo_range_fn fn) {
+    const int64_t cols = W->cols, nb = cols / 32;
+    int8_t *xq = (int8_t *)malloc((size_t)(m * cols));
+    float *xs = (float *)malloc(sizeof(float) * (size_t)(m * nb));
+    for (int64_t i = 0; i < m; ++i) vo_quantize_act(x + i * cols, cols, xq + i * cols, xs + i * nb);
+    vo_int_ctx c = {W, xq, xs, m, y, avx2};
+    vo_parallel_rows(W->rows, fn, &c);
+    free(xq);
+    free(xs);
+}
+
+void vo_matmul_q8_int(const vo_mat *W, const float *x, int64_t m, float *y, int avx2) { int_path(W, x, m, y, avx2, q8_rows); }
+void vo_matmul_q4_int(const vo_mat *W, const float *x, int64_t m, float *y, int avx2) { int_path(W, x, m, y, avx2, q4_rows); }
+
+/* ------------------------------------------------------------------ f32 tiles (kernels.cpp:230-251) */
+/* One output: 8 lanes over k (lane = k % 8), reduced as ((v0+v4)+(v1+v5))+((v2+v6)+(v3+v7)), tail added in
+ * order; every tile shape of rows_block gives this order per output. Whether a lane step fuses depends on how
+ * the reference compiles the path (g++ 11, -O3, checked bit for bit against oracle/_ref): the F16C path
+ * (kernels.cpp:389-411, built under target("avx2,fma,f16c")) fuses; the target_clones paths for F32, BF16 and
+ * dequantized Q8 (kernels.cpp:332, :413-415) multiply and add separately. */
+static float tile_dot(const float *w, const float *x, int64_t cols, int fused) {
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int64_t k = 0;
+    for (; k + 8 <= cols; k += 8)
+        for (int l = 0; l < 8; ++l) {
+            if (fused) v[l] = fmaf(w[k + l], x[k + l], v[l]);
+            else { const float pr = w[k + l] * x[k + l]; v[l] = v[l] + pr; }
+        }
+    float s = ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
+    for (; k < cols; ++k) {
+        if (fused) s = fmaf(w[k], x[k], s);
+        else { const float pr = w[k] * x[k]; s = s + pr; }
+    }
+    return s;
+}
+
+typedef struct { const vo_mat *W; const float *x; int64_t m; float *y; } vo_f32_ctx;
+
+static void f32_rows(void *p, int64_t r0, int64_t r1) {
+    const vo_f32_ctx *c = (const vo_f32_ctx *)p;
+    const int64_t rows = c->W->rows, cols = c->W->cols;
+    float *wr = (float *)malloc(sizeof(float) * (size_t)cols);
+    for (int64_t r = r0; r < r1; ++r) {
+        vo_mat_row(c->W, r, wr); /* q8 m>8: float(q) * scale, as the dequant pass of kernels.cpp:665-674 */
+        const float bz = c->W->bias ? c->W->bias[r] : 0.0f;
+        for (int64_t i = 0; i < c->m; ++i) c->y[i * rows + r] = tile_dot(wr, c->x + i * cols, cols, c->W->type == VO_F16) + bz;
+    }
+    free(wr);
+}
+
+void vo_matmul_f32_tiles(const vo_mat *W, const float *x, int64_t m, float *y) {
+    vo_f32_ctx c = {W, x, m, y};
+    vo_parallel_rows(W->rows, f32_rows, &c);
+}
+
+/* matmul dispatcher (kernels.cpp:653-705) */
+void vo_matmul(const vo_mat *W, const float *x, int64_t m, float *y, int avx2) {
+    if (W->type == VO_Q8 && m <= 8) { vo_matmul_q8_int(W, x, m, y, avx2); return; }
+    if (W->type == VO_Q4) { vo_matmul_q4_int(W, x, m, y, avx2); return; }
+    vo_matmul_f32_tiles(W, x, m, y);
+}
+
+/* dot (kernels.cpp:268-274): 8 lanes, multiply then add (no FMA in the base x86-64 build) */
+float vo_dot(const float *a, const float *b, int64_t n) {
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int64_t k = 0;
+    for (; k + 8 <= n; k += 8)
+        for (int l = 0; l < 8; ++l) { const float pr = a[k + l] * b[k + l]; v[l] = v[l] + pr; }
+    float s = ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
+    for (; k < n; ++k) { const float pr = a[k] * b[k]; s = s + pr; }
+    return s;
+}
+
+/* ------------------------------------------------------------------ elementwise (kernels.cpp:707-757) */
+void vo_rmsnorm(const float *x, const float *w, int64_t n, float eps, float *out) {
+    float ss = 0;
+    for (int64_t i = 0; i < n; ++i) { const float sq = x[i] * x[i]; ss = ss + sq; }
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int64_t i = 0; i < n; ++i) out[i] = w[i] * (x[i] * inv);
+}
+
+void vo_layernorm(const float *x, const float *w, const float *b, int64_t n, float eps, float *out) {
+    double mean = 0;
+    for (int64_t i = 0; i < n; ++i) mean += x[i];
+    mean /= (double)n;
+    double var = 0;
+    for (int64_t i = 0; i < n; ++i) { const double d = x[i] - mean; var += d * d; }
+    var /= (double)n;
+    const float inv = (float)(1.0 / sqrt(var + (double)eps));
+    const float fm = (float)mean;
+    for (int64_t i = 0; i < n; ++i) out[i] = (x[i] - fm) * inv * w[i] + (b ? b[i] : 0.0f);
+}
+
+void vo_softmax(float *x, int64_t n) {
+    float mx = -INFINITY;
+    for (int64_t i = 0; i < n; ++i) mx = mx < x[i] ? x[i] : mx;
+    float sum = 0;
+    for (int64_t i = 0; i < n; ++i) { x[i] = expf(x[i] - mx); sum += x[i]; }
+    const float inv = 1.0f / sum;
+    for (int64_t i = 0; i < n; ++i) x[i] *= inv;
+}
+
+float vo_silu(float x) { return x / (1.0f + expf(-x)); }
+
+void vo_rope_inv_freq(int64_t hd, double theta, float *out) {
+    for (int64_t i = 0; i < hd / 2; ++i) out[i] = (float)(1.0 / pow(theta, (double)(2 * i) / (double)hd));
+}
+
+void vo_rope_apply(float *x, int64_t heads, int64_t hd, const float *inv_freq, int64_t pos) {
+    const int64_t half = hd / 2;
+    float *cs = (float *)malloc(sizeof(float) * (size_t)half), *sn = (float *)malloc(sizeof(float) * (size_t)half);
+    for (int64_t i = 0; i < half; ++i) {
+        const float f = inv_freq[i] * (float)pos;
+        cs[i] = cosf(f);
+        sn[i] = sinf(f);
+    }
+    for (int64_t h = 0; h < heads; ++h) {
+        float *p = x + h * hd;
+        for (int64_t i = 0; i < half; ++i) {
+            const float a = p[i], b = p[i + half];
+            const float ac = a * cs[i], bs = b * sn[i], bc = b * cs[i], as = a * sn[i];
+            p[i] = ac - bs;
+            p[i + half] = bc + as;
+        }
+    }
+    free(cs);
+    free(sn);
+}
+
+/* ------------------------------------------------------------------ transformer (kernels.cpp:760-906) */
+static float kv_round(float v, int f16) { return f16 ? vo_f16_to_f32(vo_f32_to_f16(v)) : v; }
+
+/* One query row against keys [0, n) of a layer cache; writes oh[hd]. (kernels.cpp:809-828) */
+static void attend(const float *qh, const float *K, const float *V, int64_t n, int64_t kd, int64_t off, int64_t hd, float scale,
+                   float *sc, float *oh) {
+    for (int64_t j = 0; j < n; ++j) sc[j] = scale * vo_dot(qh, K + j * kd + off, hd);
+    vo_softmax(sc, n);
+    for (int64_t e = 0; e < hd; ++e) oh[e] = 0;
+    for (int64_t j = 0; j < n; ++j) {
+        const float p = sc[j];
+        const float *vj = V + j * kd + off;
+        for (int64_t e = 0; e < hd; ++e) { const float pv = p * vj[e]; oh[e] = oh[e] + pv; }
+    }
+}
+
+int vo_transformer_forward(const vo_xfmr *w, vo_kv *kv, const float *x_in, int64_t m, float *out_last, float *out_all) {
+    const int64_t H = w->hidden, nh = w->heads, nkv = w->kv_heads, hd = w->head_dim, I = w->inter;
+    const int64_t qd = nh * hd, kd = nkv * hd, group = nh / nkv;
+    const int64_t pos0 = kv->len;
+    if (pos0 + m > kv->cap) return -1;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float *h = (float *)malloc(sizeof(float) * (size_t)(m * H));
+    float *xn = (float *)malloc(sizeof(float) * (size_t)(m * H));
+    float *q = (float *)malloc(sizeof(float) * (size_t)(m * qd));
+    float *k = (float *)malloc(sizeof(float) * (size_t)(m * kd));
+    float *v = (float *)malloc(sizeof(float) * (size_t)(m * kd));
+    float *ao = (float *)malloc(sizeof(float) * (size_t)(m * qd));
+    float *o = (float *)malloc(sizeof(float) * (size_t)(m * H));
+    float *g = (float *)malloc(sizeof(float) * (size_t)(m * I));
+    float *u = (float *)malloc(sizeof(float) * (size_t)(m * I));
+    float *d = (float *)malloc(sizeof(float) * (size_t)(m * H));
+    float *sc = (float *)malloc(sizeof(float) * (size_t)(pos0 + m));
+    memcpy(h, x_in, sizeof(float) * (size_t)(m * H));
+    for (int32_t li = 0; li < w->n_layers; ++li) {
+        const vo_layer *L = &w->layers[li];
+        float *K = kv->k + (int64_t)li * kv->cap * kd, *V = kv->v + (int64_t)li * kv->cap * kd;
+        for (int64_t i = 0; i < m; ++i) vo_rmsnorm(h + i * H, L->ln1, H, w->eps, xn + i * H);
+        vo_matmul(&L->q, xn, m, q, kv->avx2);
+        vo_matmul(&L->k, xn, m, k, kv->avx2);
+        vo_matmul(&L->v, xn, m, v, kv->avx2);
+        for (int64_t i = 0; i < m; ++i) {
+            float *qi = q + i * qd, *ki = k + i * kd;
+            if (L->qn) for (int64_t hh = 0; hh < nh; ++hh) vo_rmsnorm(qi + hh * hd, L->qn, hd, w->eps, qi + hh * hd);
+            if (L->kn) for (int64_t hh = 0; hh < nkv; ++hh) vo_rmsnorm(ki + hh * hd, L->kn, hd, w->eps, ki + hh * hd);
+            vo_rope_apply(qi, nh, hd, w->inv_freq, pos0 + i);
+            vo_rope_apply(ki, nkv, hd, w->inv_freq, pos0 + i);
+        }
+        for (int64_t i = 0; i < m; ++i)
+            for (int64_t e = 0; e < kd; ++e) {
+                K[(pos0 + i) * kd + e] = kv_round(k[i * kd + e], kv->kv_f16);
+                V[(pos0 + i) * kd + e] = kv_round(v[i * kd + e], kv->kv_f16);
+            }
+        for (int64_t t = 0; t < m * nh; ++t) {
+            const int64_t i = t / nh, hh = t % nh, gk = hh / group;
+            attend(q + i * qd + hh * hd, K, V, pos0 + i + 1, kd, gk * hd, hd, scale, sc, ao + i * qd + hh * hd);
+        }
+        vo_matmul(&L->o, ao, m, o, kv->avx2);
+        for (int64_t i = 0; i < m * H; ++i) h[i] += o[i];
+        for (int64_t i = 0; i < m; ++i) vo_rmsnorm(h + i * H, L->ln2, H, w->eps, xn + i * H);
+        vo_matmul(&L->gate, xn, m, g, kv->avx2);
+        vo_matmul(&L->up, xn, m, u, kv->avx2);
+        for (int64_t i = 0; i < m * I; ++i) g[i] = vo_silu(g[i]) * u[i];
+        vo_matmul(&L->down, g, m, d, kv->avx2);
+        for (int64_t i = 0; i < m * H; ++i) h[i] += d[i];
+    }
+    kv->len += m;
+    if (out_last) vo_rmsnorm(h + (m - 1) * H, w->final_norm, H, w->eps, out_last);
+    if (out_all) for (int64_t i = 0; i < m; ++i) vo_rmsnorm(h + i * H, w->final_norm, H, w->eps, out_all + i * H);
+    free(h); free(xn); free(q); free(k); free(v); free(ao); free(o); free(g); free(u); free(d); free(sc);
+    return 0;
+}
+
+int vo_transformer_forward_steps(const vo_xfmr *w, vo_kv *const *kvs, int64_t B, const float *x_in, float *out) {
+    const int64_t H = w->hidden, nh = w->heads, nkv = w->kv_heads, hd = w->head_dim, I = w->inter;
+    const int64_t qd = nh * hd, kd = nkv * hd, group = nh / nkv;
+    int64_t maxn = 0;
+    for (int64_t b = 0; b < B; ++b) {
+        if (kvs[b]->len + 1 > kvs[b]->cap) return -1;
+        if (kvs[b]->len + 1 > maxn) maxn = kvs[b]->len + 1;
+    }
+    const float scale = 1.0f / sqrtf((float)hd);
+    const int avx2 = kvs[0]->avx2;
+    float *h = (float *)malloc(sizeof(float) * (size_t)(B * H));
+    float *xn = (float *)malloc(sizeof(float) * (size_t)(B * H));
+    float *q = (float *)malloc(sizeof(float) * (size_t)(B * qd));
+    float *k = (float *)malloc(sizeof(float) * (size_t)(B * kd));
+    float *v = (float *)malloc(sizeof(float) * (size_t)(B * kd));
+    float *ao = (float *)malloc(sizeof(float) * (size_t)(B * qd));
+    float *o = (float *)malloc(sizeof(float) * (size_t)(B * H));
+    float *g = (float *)malloc(sizeof(float) * (size_t)(B * I));
+    float *u = (float *)malloc(sizeof(float) * (size_t)(B * I));
+    float *d = (float *)malloc(sizeof(float) * (size_t)(B * H));
+    float *sc = (float *)malloc(sizeof(float) * (size_t)maxn);
+    memcpy(h, x_in, sizeof(float) * (size_t)(B * H));
+    for (int32_t li = 0; li < w->n_layers; ++li) {
+        const vo_layer *L = &w->layers[li];
+        for (int64_t i = 0; i < B; ++i) vo_rmsnorm(h + i * H, L->ln1, H, w->eps, xn + i * H);
+        vo_matmul(&L->q, xn, B, q, avx2);
+        vo_matmul(&L->k, xn, B, k, avx2);
+        vo_matmul(&L->v, xn, B, v, avx2);
+        for (int64_t i = 0; i < B; ++i) {
+            float *qi = q + i * qd, *ki = k + i * kd;
+            if (L->qn) for (int64_t hh = 0; hh < nh; ++hh) vo_rmsnorm(qi + hh * hd, L->qn, hd, w->eps, qi + hh * hd);
+            if (L->kn) for (int64_t hh = 0; hh < nkv; ++hh) vo_rmsnorm(ki + hh * hd, L->kn, hd, w->eps, ki + hh * hd);
+            vo_rope_apply(qi, nh, hd, w->inv_freq, kvs[i]->len);
+            vo_rope_apply(ki, nkv, hd, w->inv_freq, kvs[i]->len);
+            float *K = kvs[i]->k + (int64_t)li * kvs[i]->cap * kd, *V = kvs[i]->v + (int64_t)li * kvs[i]->cap * kd;
+            for (int64_t e = 0; e < kd; ++e) {
+                K[kvs[i]->len * kd + e] = kv_round(ki[e], kvs[i]->kv_f16);
+                V[kvs[i]->len * kd + e] = kv_round(v[i * kd + e], kvs[i]->kv_f16);
+            }
+        }
+        for (int64_t t = 0; t < B * nh; ++t) {
+            const int64_t i = t / nh, hh = t % nh, gk = hh / group;
+            const float *K = kvs[i]->k + (int64_t)li * kvs[i]->cap * kd, *V = kvs[i]->v + (int64_t)li * kvs[i]->cap * kd;
+            attend(q + i * qd + hh * hd, K, V, kvs[i]->len + 1, kd, gk * hd, hd, scale, sc, ao + i * qd + hh * hd);
+        }
+        vo_matmul(&L->o, ao, B, o, avx2);
+        for (int64_t i = 0; i < B * H; ++i) h[i] += o[i];
+        for (int64_t i = 0; i < B; ++i) vo_rmsnorm(h + i * H, L->ln2, H, w->eps, xn + i * H);
+        vo_matmul(&L->gate, xn, B, g, avx2);
+        vo_matmul(&L->up, xn, B, u, avx2);
+        for (int64_t i = 0; i < B * I; ++i) g[i] = vo_silu(g[i]) * u[i];
+        vo_matmul(&L->down, g, B, d, avx2);
+        for (int64_t i = 0; i < B * H; ++i) h[i] += d[i];
+    }
+    for (int64_t i = 0; i < B; ++i) {
+        kvs[i]->len += 1;
+        vo_rmsnorm(h + i * H, w->final_norm, H, w->eps, out + i * H);
+    }
+    free(h); free(xn); free(q); free(k); free(v); free(ao); free(o); free(g); free(u); free(d); free(sc);
+    return 0;
+}

@@ -1,0 +1,125 @@
+/*
+ * vox_oracle.h — CPU restatement of the reference's tensor-op hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the parity checker for the HIP
+ * backend in vox_amd/. It may be loaded only by tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg. The product path never links or calls it.
+ *
+ * Every function restates one reference function (cited file:line under
+ * /root/reference). Floating-point operation order follows the reference
+ * where the reference fixes it. The build uses -ffp-contract=off, so the only
+ * fused multiply-adds are explicit fmaf() calls, placed where the reference
+ * compiles to vfmadd.
+ *
+ * Parity pins: every function is checked by tests/test_oracle.py against one
+ * of these: the Random123 KAT vectors (test_core.cpp:35-43), the sampler rule
+ * tests (test_core.cpp:45-79), the Q4 bounds (test_core.cpp:461-521), golden
+ * vectors written by the compiled reference (oracle/_ref, fixtures under
+ * tests/golden/), or a float64 brute force. No function here is "parity
+ * unpinned".
+ */
+#ifndef VOX_ORACLE_H
+#define VOX_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Weight types, in the order of vox::WType (kernels.hpp:42). */
+enum { VO_F32 = 0, VO_F16 = 1, VO_BF16 = 2, VO_Q8 = 3, VO_Q4 = 4 };
+
+/* Non-owning weight view, field meaning as vox::Mat (kernels.hpp:44-56):
+ * [rows][cols] row-major, rows = outputs. Q8: int8 data + f32 scale
+ * [rows][cols/32]. Q4: 16 bytes per 32-block, byte j = w[j] | w[j+16] << 4,
+ * value (u - 8) * scale; f32 scale [rows][cols/32]. bias: [rows] or NULL. */
+typedef struct {
+    int32_t type;
+    const void *data;
+    const float *scale;
+    int64_t rows, cols;
+    const float *bias;
+} vo_mat;
+
+/* ---- counter RNG and sampling (sampling.hpp) ---- */
+void vo_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+float vo_uniform(uint64_t seed, uint64_t frame, uint32_t codebook, uint32_t draw);
+int32_t vo_sample_logits(float *logits, int32_t n, float temperature, float top_p, int32_t top_k,
+                         float repetition_penalty, const int32_t *history, int32_t n_history, float u);
+/* CosyVoice2 repetition-aware sampler (cosyvoice.cpp:617-664). logp is modified like the reference
+ * (the chosen token is set to -inf when it is resampled). */
+int32_t vo_ras_sample(float *logp, int32_t n, const int32_t *decoded, int32_t n_decoded, float top_p, int32_t top_k,
+                      int32_t win_size, float tau_r, float u0, float u1);
+/* Philox Box-Muller normal stream (f5.cpp:402-414): out[2p], out[2p+1] from draws (p, stream, 0/1). */
+void vo_noise(uint64_t seed, uint32_t stream, size_t n, float *out);
+
+/* ---- formats (kernels.hpp:59-76, kernels.cpp:432-471, :606-645, :918-929) ---- */
+float vo_f16_to_f32(uint16_t h);
+uint16_t vo_f32_to_f16(float f); /* round to nearest even (used to model an f16 KV cache) */
+float vo_bf16_to_f32(uint16_t h);
+void vo_mat_row(const vo_mat *W, int64_t r, float *out);
+void vo_quantize_q8(const float *w, int64_t rows, int64_t cols, int8_t *q, float *scale);
+void vo_quantize_q4(const float *w, int64_t rows, int64_t cols, uint8_t *q, float *scale);
+/* Per-32-block int8 activation quantization of the q8/q4 GEMV (kernels.cpp:515-523). */
+void vo_quantize_act(const float *x, int64_t n, int8_t *xq, float *xs);
+
+/* ---- matmul (kernels.cpp:475-705) ----
+ * avx2 = 1 restates the AVX2/FMA dot (kernels.cpp:485-501, :554-573), 0 the scalar one (:475-483, :541-552).
+ * Dispatch as matmul(): Q8 with m <= 8 and Q4 use int8 activations; Q8 with m > 8 and F32/F16/BF16 use the
+ * f32 tile path (kernels.cpp:230-251, :661-679); only F16 fuses its lane steps, as the F16C build does. */
+void vo_matmul(const vo_mat *W, const float *x, int64_t m, float *y, int avx2);
+void vo_matmul_q8_int(const vo_mat *W, const float *x, int64_t m, float *y, int avx2);
+void vo_matmul_q4_int(const vo_mat *W, const float *x, int64_t m, float *y, int avx2);
+void vo_matmul_f32_tiles(const vo_mat *W, const float *x, int64_t m, float *y);
+/* dot() of kernels.cpp:268-274: 8 lanes, separate multiply and add (not multiversioned, no FMA). */
+float vo_dot(const float *a, const float *b, int64_t n);
+
+/* ---- elementwise (kernels.cpp:707-757, kernels.hpp:105) ---- */
+void vo_rmsnorm(const float *x, const float *w, int64_t n, float eps, float *out);
+void vo_layernorm(const float *x, const float *w, const float *b, int64_t n, float eps, float *out);
+void vo_softmax(float *x, int64_t n);
+float vo_silu(float x);
+void vo_rope_inv_freq(int64_t hd, double theta, float *out);
+void vo_rope_apply(float *x, int64_t heads, int64_t hd, const float *inv_freq, int64_t pos);
+
+/* ---- transformer (kernels.hpp:114-147, kernels.cpp:760-906) ---- */
+typedef struct {
+    vo_mat q, k, v, o, gate, up, down;
+    const float *qn, *kn; /* per-head RMSNorm weights [head_dim] or NULL */
+    const float *ln1, *ln2;
+} vo_layer;
+
+typedef struct {
+    int32_t n_layers;
+    const vo_layer *layers;
+    const float *final_norm;
+    int32_t hidden, heads, kv_heads, head_dim, inter;
+    float eps;
+    const float *inv_freq; /* [head_dim/2] */
+} vo_xfmr;
+
+/* KV cache: k, v are [n_layers][cap][kv_heads*head_dim] floats. kv_f16 = 1 rounds every appended
+ * key/value to f16 (a cache stored in f16, read back exactly widened); 0 keeps f32 like KVCache. */
+typedef struct {
+    float *k, *v;
+    int64_t cap;
+    int64_t len;
+    int32_t kv_f16;
+    int32_t avx2;
+} vo_kv;
+
+/* transformer_forward (kernels.cpp:760-844), full attention (window 0), no layer scales.
+ * Returns 0, or -1 when the cache is too small. */
+int vo_transformer_forward(const vo_xfmr *w, vo_kv *kv, const float *x, int64_t m, float *out_last, float *out_all);
+/* transformer_forward_steps (kernels.cpp:846-906): one token for each of B sequences. */
+int vo_transformer_forward_steps(const vo_xfmr *w, vo_kv *const *kvs, int64_t B, const float *x, float *out);
+
+/* Thread count for the row-parallel loops (matmul); 1 = scalar single-thread. Results do not depend on it. */
+void vo_set_threads(int n);
+int vo_get_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,145 @@
+// test_gpu_hip.cpp — drives the drop-in through Vox's own C++ device interface, the way Vox's callers do
+// (qwen3.cpp:302-344 upload_gpu, kernels.cpp:908-916 transformer_step_fused, kernels.cpp:656 matmul), and
+// checks the results against the C oracle. Run by tests/test_gpu_dropin.py; exit status 0 = all passed.
+#include <cmath>
+#include <cstdio>
+#include <random>
+#include <vector>
+
+#include "gpu.hpp"
+#include "vox_oracle.h"
+
+using namespace vox;
+
+static int g_fail = 0, g_pass = 0;
+#define CHECK(c)                                                                                  \
+    do {                                                                                          \
+        if (c) ++g_pass;                                                                          \
+        else { ++g_fail; std::fprintf(stderr, "FAIL %s:%d: %s\n", __FILE__, __LINE__, #c); }      \
+    } while (0)
+
+static float rel(const float *a, const float *b, size_t n) {
+    double mx = 0, mb = 0;
+    for (size_t i = 0; i < n; ++i) { mx = std::max(mx, double(std::fabs(a[i] - b[i]))); mb = std::max(mb, double(std::fabs(b[i]))); }
+    return float(mx / std::max(1.0, mb));
+}
+
+struct Q8 {
+    std::vector<int8_t> q;
+    std::vector<float> s;
+    int64_t rows, cols;
+    Q8(std::mt19937 &rng, int64_t r, int64_t c) : rows(r), cols(c) {
+        std::normal_distribution<float> nd(0.f, 0.02f);
+        std::vector<float> w(static_cast<size_t>(r * c));
+        for (auto &v : w) v = nd(rng);
+        q.resize(w.size());
+        s.resize(size_t(r * (c / 32)));
+        vo_quantize_q8(w.data(), r, c, q.data(), s.data());
+    }
+    Mat mat() const {
+        Mat m;
+        m.type = WType::Q8; m.data = reinterpret_cast<const uint8_t *>(q.data()); m.scale = s.data(); m.rows = rows; m.cols = cols;
+        return m;
+    }
+    vo_mat omat() const { return vo_mat{VO_Q8, q.data(), s.data(), rows, cols, nullptr}; }
+};
+
+int main() {
+    std::string err;
+    if (!gpu_init("vulkan:0", err)) {  // the spec create_backend passes (family.cpp:94)
+        std::fprintf(stderr, "gpu_init failed: %s\n", err.c_str());
+        return 2;
+    }
+    CHECK(gpu_active());
+    auto devs = gpu_enumerate();
+    CHECK(!devs.empty() && devs[0].type == "discrete" && !devs[0].software && devs[0].vram_total > (uint64_t(100) << 30));
+    CHECK(gpu_mem_info().device_index == 0);
+    std::printf("%s", gpu_list_devices().c_str());
+
+    std::mt19937 rng(1);
+    std::normal_distribution<float> nd(0.f, 1.f);
+    const int H = 256, nh = 4, nkv = 2, hd = 128, I = 512, NL = 2, V = 200;
+    // ---- matmul through Mat::gpu (kernels.cpp:656)
+    Q8 w(rng, 300, H);
+    Mat W = w.mat();
+    W.gpu = gpu_upload(W);
+    CHECK(W.gpu >= 0);
+    std::vector<float> x(5 * H), y(5 * 300), yr(5 * 300);
+    for (auto &v : x) v = nd(rng);
+    CHECK(gpu_matmul(W, x.data(), 5, y.data()));
+    vo_mat ow = w.omat();
+    vo_matmul(&ow, x.data(), 5, yr.data(), 1);
+    CHECK(rel(y.data(), yr.data(), y.size()) < 1e-5f);
+
+    // ---- a transformer on the device (qwen3.cpp:302-344), stepped like transformer_step_fused
+    std::vector<Q8> mats;
+    std::vector<std::vector<float>> norms;
+    TransformerW T;
+    T.hidden = H; T.heads = nh; T.kv_heads = nkv; T.head_dim = hd; T.inter = I; T.eps = 1e-6f; T.theta = 1e6;
+    T.inv_freq.resize(hd / 2);
+    vo_rope_inv_freq(hd, 1e6, T.inv_freq.data());
+    auto vec = [&](int n, float mean) {
+        std::vector<float> v(static_cast<size_t>(n));
+        for (auto &e : v) e = mean + 0.02f * nd(rng);
+        norms.push_back(v);
+        return norms.size() - 1;
+    };
+    const int64_t shapes[7][2] = {{nh * hd, H}, {nkv * hd, H}, {nkv * hd, H}, {H, nh * hd}, {I, H}, {I, H}, {H, I}};
+    std::vector<size_t> nidx;
+    for (int l = 0; l < NL; ++l) {
+        for (int j = 0; j < 7; ++j) mats.emplace_back(rng, shapes[j][0], shapes[j][1]);
+        for (int j = 0; j < 2; ++j) nidx.push_back(vec(H, 1.f));
+        for (int j = 0; j < 2; ++j) nidx.push_back(vec(hd, 1.f));
+    }
+    const size_t fin = vec(H, 1.f);
+    std::vector<vo_layer> OL(NL);
+    for (int l = 0; l < NL; ++l) {
+        LayerW L;
+        Mat *dst[7] = {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down};
+        vo_mat *od[7] = {&OL[l].q, &OL[l].k, &OL[l].v, &OL[l].o, &OL[l].gate, &OL[l].up, &OL[l].down};
+        for (int j = 0; j < 7; ++j) { *dst[j] = mats[size_t(7 * l + j)].mat(); *od[j] = mats[size_t(7 * l + j)].omat(); }
+        L.ln1 = norms[nidx[size_t(4 * l)]].data(); L.ln2 = norms[nidx[size_t(4 * l + 1)]].data();
+        L.qn = norms[nidx[size_t(4 * l + 2)]].data(); L.kn = norms[nidx[size_t(4 * l + 3)]].data();
+        OL[l].ln1 = L.ln1; OL[l].ln2 = L.ln2; OL[l].qn = L.qn; OL[l].kn = L.kn;
+        T.layers.push_back(L);
+    }
+    T.final_norm = norms[fin].data();
+    int released = 0;
+    T.gpu_id = gpu_xfmr_create(T, "talker", -1, [&](const Mat &) { ++released; });
+    CHECK(T.gpu_id >= 0);
+    CHECK(released == 7 * NL);
+    Q8 hw(rng, V, H);
+    Mat head = hw.mat();
+    head.gpu = gpu_upload(head);
+    const int seq = gpu_seq_create(T.gpu_id, 64);
+    CHECK(seq >= 0);
+
+    vo_xfmr OX{NL, OL.data(), T.final_norm, H, nh, nkv, hd, I, T.eps, T.inv_freq.data()};
+    const int64_t kd = nkv * hd;
+    std::vector<float> kc(static_cast<size_t>(NL * 64 * kd)), vc(kc.size());
+    vo_kv okv{kc.data(), vc.data(), 64, 0, 1, 1};
+    vo_mat ohead = hw.omat();
+    int64_t pos = 0;
+    for (int step = 0; step < 5; ++step) {
+        const int64_t m = step == 0 ? 4 : 1;  // a prompt, then decode steps
+        std::vector<float> xi(static_cast<size_t>(m * H)), out(H), logits(V), ro(H), rl(V);
+        for (auto &v : xi) v = nd(rng);
+        CHECK(gpu_xfmr_forward(T, seq, pos, xi.data(), m, out.data(), nullptr, &head, logits.data()));
+        CHECK(vo_transformer_forward(&OX, &okv, xi.data(), m, ro.data(), nullptr) == 0);
+        vo_matmul(&ohead, ro.data(), 1, rl.data(), 1);
+        const float e1 = rel(out.data(), ro.data(), H), e2 = rel(logits.data(), rl.data(), V);
+        std::printf("step %d (m=%lld): hidden rel err %.2e, logits rel err %.2e\n", step, (long long)m, e1, e2);
+        CHECK(e1 < 1e-3f && e2 < 1e-3f);
+        pos += m;
+    }
+    // capacity is enforced, and the failure is reported as false (the caller falls back or fails loudly)
+    std::vector<float> big(static_cast<size_t>(64 * H), 0.f), o2(H);
+    CHECK(!gpu_xfmr_forward(T, seq, pos, big.data(), 64, o2.data()));
+    CHECK(!gpu_stats().last_error.empty());
+    gpu_seq_free(seq);
+    CHECK(gpu_seq_create(T.gpu_id, 32) == seq);  // pooled buffers are reused (gpu_vulkan.cpp:834-837)
+    // entry points this backend leaves to the CPU answer like gpu_stub.cpp
+    CHECK(gpu_f5_create(GpuF5Desc{}) == -1 && gpu_cosy_create(GpuCosyDesc{}) == -1);
+    std::printf("%d passed, %d failed\n", g_pass, g_fail);
+    return g_fail ? 1 : 0;
+}

@@ -1,0 +1,117 @@
+"""Writes tests/golden/golden_ref.npz from the compiled reference harness (oracle/_ref/libvoxref.so).
+
+Run here (where /root/reference exists and `make -C oracle ref` has built the harness):
+    python tests/golden/make_golden.py
+The fixture holds inputs and the reference's outputs only (data, no reference source). Tests compare the
+C restatement (oracle/liboracle.so) against it on machines without the reference.
+"""
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+import pyoracle as po  # noqa: E402
+
+OUT = os.path.join(HERE, "golden_ref.npz")
+
+
+def main():
+    R = po.ref()
+    if R is None:
+        raise SystemExit("oracle/_ref/libvoxref.so is not built")
+    po.ref().ref_set_threads(4)
+    rng = np.random.default_rng(20261201)
+    g = {}
+    # Philox / DetRng
+    ctr = rng.integers(0, 2**32, size=(64, 4), dtype=np.uint64).astype(np.uint32)
+    key = rng.integers(0, 2**32, size=(64, 2), dtype=np.uint64).astype(np.uint32)
+    outs = np.empty((64, 4), np.uint32)
+    for i in range(64):
+        c, k, o = np.ascontiguousarray(ctr[i]), np.ascontiguousarray(key[i]), np.empty(4, np.uint32)
+        R.ref_philox(c.ctypes.data, k.ctypes.data, o.ctypes.data)
+        outs[i] = o
+    g["philox_ctr"], g["philox_key"], g["philox_out"] = ctr, key, outs
+    uargs = rng.integers(0, 2**40, size=(64, 4), dtype=np.uint64)
+    g["uniform_args"] = uargs
+    g["uniform_out"] = np.array([R.ref_uniform(int(a[0]), int(a[1]), int(a[2]) & 0xFFFFFFFF, int(a[3]) & 0xFFFFFFFF)
+                                 for a in uargs], np.float32)
+    # sample_logits: random logits, ties, -inf masks, penalties
+    cases = []
+    for i in range(200):
+        n = int(rng.choice([4, 50, 100, 3072]))
+        l = (rng.standard_normal(n) * rng.uniform(0.5, 4)).astype(np.float32)
+        if i % 7 == 0:
+            l = np.round(l).astype(np.float32)  # many ties
+        if i % 5 == 0:
+            l[rng.integers(0, n, n // 4)] = -np.inf
+        T = float(rng.choice([0.0, 0.5, 0.9, 1.0, 1.3]))
+        top_k = int(rng.choice([0, 1, 5, 50, n + 3]))
+        top_p = float(rng.choice([1.0, 0.8, 0.5, 0.95]))
+        rep = float(rng.choice([1.0, 1.1, 2.0]))
+        hist = rng.integers(-2, n + 2, int(rng.integers(0, 20))).astype(np.int32)
+        u = float(np.float32(rng.uniform()))
+        ll = l.copy()
+        idx = R.ref_sample_logits(ll.ctypes.data, n, T, top_p, top_k, rep, hist.ctypes.data if hist.size else None, hist.size, u)
+        cases.append((l, T, top_p, top_k, rep, hist, u, idx))
+    g["sample_n"] = np.array([c[0].size for c in cases], np.int64)
+    g["sample_logits"] = np.concatenate([c[0] for c in cases])
+    g["sample_params"] = np.array([[c[1], c[2], c[3], c[4], c[6]] for c in cases], np.float64)
+    g["sample_hist_n"] = np.array([c[5].size for c in cases], np.int64)
+    g["sample_hist"] = np.concatenate([c[5] for c in cases]).astype(np.int32)
+    g["sample_idx"] = np.array([c[7] for c in cases], np.int32)
+    # quantizers
+    w = (rng.standard_normal((37, 160)) * np.linspace(0.01, 2, 160)).astype(np.float32)
+    w[3, :32] = 0.0
+    w[4, 32:64] = 0.5  # equal magnitudes
+    g["quant_w"] = w
+    g["q8_q"], g["q8_s"] = po.quantize_q8(w, use_ref=True)
+    g["q4_q"], g["q4_s"] = po.quantize_q4(w, use_ref=True)
+    # matmul paths
+    x = rng.standard_normal((12, 160)).astype(np.float32)
+    g["mm_x"] = x
+    bias = rng.standard_normal(37).astype(np.float32)
+    g["mm_bias"] = bias
+    for name, wt, data, scale in (("q8", po.Q8, g["q8_q"], g["q8_s"]), ("q4", po.Q4, g["q4_q"], g["q4_s"]),
+                                  ("f32", po.F32, w, None), ("f16", po.F16, w.astype(np.float16).view(np.uint16), None)):
+        M = po.Mat(wt, data, 37, 160, scale, bias)
+        for m in (1, 3, 8, 12):
+            g[f"mm_{name}_m{m}"] = po.matmul(M, x[:m], use_ref=True)
+    # norms / rope / softmax
+    v = rng.standard_normal(1024).astype(np.float32)
+    gam = (1 + 0.02 * rng.standard_normal(1024)).astype(np.float32)
+    out = np.empty(1024, np.float32)
+    R.ref_rmsnorm(v.ctypes.data, gam.ctypes.data, 1024, np.float32(1e-6), out.ctypes.data)
+    g["rms_x"], g["rms_w"], g["rms_out"] = v, gam, out.copy()
+    R.ref_layernorm(v.ctypes.data, gam.ctypes.data, None, 1024, np.float32(1e-6), out.ctypes.data)
+    g["ln_out"] = out.copy()
+    s = v[:513].copy()
+    R.ref_softmax(s.ctypes.data, 513)
+    g["softmax_out"] = s
+    inv = np.empty(64, np.float32)
+    R.ref_rope_inv_freq(128, 1e6, inv.ctypes.data)
+    g["rope_inv"] = inv
+    qh = rng.standard_normal(16 * 128).astype(np.float32)
+    g["rope_x"] = qh.copy()
+    R.ref_rope_apply(qh.ctypes.data, 16, 128, inv.ctypes.data, 512)
+    g["rope_out"] = qh
+    # tiny transformer: 2 layers, hidden 64, 4 heads / 2 kv x 32... head_dim 32, inter 96, q8, prompt of 5 then 2 tokens
+    from models import Model
+    mdl = Model(7, 2, 64, 4, 2, 32, 96, wtype=po.Q8)
+    kv = mdl.oracle_kv(16, kv_f16=0)
+    xs = rng.standard_normal((7, 64)).astype(np.float32)
+    g["xf_x"] = xs
+    o1, oa = po.transformer_forward(mdl.ox, kv, xs[:5], want_all=True, use_ref=True)
+    o2 = po.transformer_forward(mdl.ox, kv, xs[5:6], use_ref=True)
+    o3 = po.transformer_forward(mdl.ox, kv, xs[6:7], use_ref=True)
+    g["xf_out_all5"], g["xf_out6"], g["xf_out7"] = oa, o2, o3
+    np.savez_compressed(OUT, **g)
+    print("wrote", OUT, os.path.getsize(OUT), "bytes")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,68 @@
+"""BASELINE configs[1] at full size: the Qwen3-TTS-0.6B-shaped q8 talker decode step (28 layers, hidden 1024,
+16 q / 8 kv heads x 128, FFN 3072, theta 1e6, KV 512 prior tokens f16 ~N(0,1), 3072-entry head, Philox top-k 50,
+T 0.9) on the device, checked against the oracle on the same stored weights and cache.
+
+Bars: out_last and logits within 1e-3 (`vox verify` metric); the device sampler's token bit-exact with the
+oracle sampler on the device's logits, and equal to the oracle sampler on the oracle's logits.
+"""
+import numpy as np
+import pytest
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def to_oracle(oracle, hip, dec):
+    c = dec.cfg
+    L = []
+    for li in range(c["layers"]):
+        d = {}
+        for n in ("q", "k", "v", "o", "gate", "up", "down"):
+            h = dec.mats[li][n]
+            rows, cols = hip.mat_shape(h)
+            data, scale, _ = hip.mat_download(h, c["wtype"])
+            d[n] = oracle.Mat(c["wtype"], data, rows, cols, scale)
+        d.update(dec.layers[li])
+        L.append(d)
+    X = oracle.Xfmr(L, dec.final_norm, c["hidden"], c["heads"], c["kv_heads"], c["head_dim"], c["inter"], c["eps"], dec.inv_freq)
+    kd = c["kv_heads"] * c["head_dim"]
+    kv = oracle.KV(c["layers"], c["kv_len"] + 8, kd, kv_f16=1)
+    for li in range(c["layers"]):
+        k, v = hip.seq_download(dec.seq, li, c["kv_len"], kd)
+        kv.k[li, :c["kv_len"]] = k
+        kv.v[li, :c["kv_len"]] = v
+    kv.c.len = c["kv_len"]
+    hd, hs, _ = hip.mat_download(dec.head, c["head_type"])
+    head = oracle.Mat(c["head_type"], hd, c["head_rows"], c["hidden"], hs)
+    return X, kv, head
+
+
+def test_talker_0_6b_decode_step(hip, oracle):
+    from vox_amd import synth
+    oracle.lib().vo_set_threads(8)
+    dec = synth.Decoder(synth.TALKER_0_6B, seed=0)
+    c = dec.cfg
+    X, kv, head = to_oracle(oracle, hip, dec)
+    rng = np.random.default_rng(0)
+    pos = c["kv_len"]
+    for step in range(2):
+        x = rng.standard_normal((1, c["hidden"])).astype(np.float32)
+        # device-resident step with the device sampler (the benchmark's path)
+        dx, dout, dlog, dtok = hip.DevBuf(x.nbytes), hip.DevBuf(x.nbytes), hip.DevBuf(c["head_rows"] * 4), hip.DevBuf(4)
+        dx.upload(x)
+        cfg = hip.sample_cfg(0.9, 1.0, 50, seed=0, frame=step)
+        hip.decode_dev(dec.xfmr, dec.seq, pos + step, dx, 1, dout, dec.head, dlog, cfg, dtok)
+        hip.sync()
+        out = dout.download(c["hidden"], np.float32)
+        logits = dlog.download(c["head_rows"], np.float32)
+        tok = int(dtok.download(1, np.int32)[0])
+        for b in (dx, dout, dlog, dtok):
+            b.free()
+        ref = oracle.transformer_forward(X, kv, x)
+        ref_logits = oracle.matmul(head, ref[None])[0]
+        assert rel_err(out, ref) < 1e-3, rel_err(out, ref)
+        assert rel_err(logits, ref_logits) < 1e-3, rel_err(logits, ref_logits)
+        u = oracle.uniform(0, step, 0, 0)
+        assert tok == oracle.sample_logits(logits, 0.9, 1.0, 50, 1.0, None, u)
+        assert tok == oracle.sample_logits(ref_logits, 0.9, 1.0, 50, 1.0, None, u)

@@ -1,0 +1,128 @@
+"""Parity of the gfx950 kernels with the oracle, through the C ABI (libvoxhip.so).
+
+Bars: bit-exact for quantization, unpacking and sampled token ids; the GEMVs are
+f32 activations, compared with the reference's `vox verify` metric max|a-b| / max(1, max|b|) at 1e-5 (they
+differ from the CPU only in float summation order).
+"""
+import numpy as np
+import pytest
+
+from conftest import rel_err
+from models import make_mat
+
+pytestmark = pytest.mark.gpu
+
+F32, F16, BF16, Q8, Q4 = 0, 1, 2, 3, 4
+GEMV_TOL = 1e-5
+
+
+def test_device_is_gfx950(hip):
+    assert "gfx950" in hip.device_name()
+    assert hip.lib().voxhip_active() == 1
+
+
+def test_quantizers_bit_exact(hip, oracle):
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((64, 256)) * np.geomspace(1e-4, 10, 256)).astype(np.float32)
+    w[0, :32] = 0.0                       # all-zero block
+    w[1, :32] = 0.25                      # equal magnitudes
+    w[2, :32] = np.linspace(-1, 1, 32)    # exact ties at .5 steps
+    w[3, 32:64] = -w[3, 32:64]
+    q, s = hip.quantize_q8_dev(w)
+    oq, os_ = oracle.quantize_q8(w)
+    assert np.array_equal(q, oq) and np.array_equal(s.view(np.uint32), os_.view(np.uint32))
+    q, s = hip.quantize_q4_dev(w)
+    oq, os_ = oracle.quantize_q4(w)
+    assert np.array_equal(q, oq) and np.array_equal(s.view(np.uint32), os_.view(np.uint32))
+    x = rng.standard_normal(4096).astype(np.float32) * 3
+    x[:32] = 0
+    x[32:64] = np.arange(32) - 15.5  # x * inv lands on .5 for some elements
+    xq, xs = hip.quantize_act_dev(x)
+    oq, os_ = oracle.quantize_act(x)
+    assert np.array_equal(xq, oq) and np.array_equal(xs.view(np.uint32), os_.view(np.uint32))
+
+
+@pytest.mark.parametrize("wt", [Q8, Q4, F32, F16, BF16])
+@pytest.mark.parametrize("rows,cols", [(37, 160), (4096, 1024), (1024, 3072), (3072, 1024), (5, 4864), (6144, 1024)])
+def test_matmul_parity(hip, oracle, wt, rows, cols):
+    rng = np.random.default_rng(rows * 7 + cols + wt)
+    data, scale, bias = make_mat(rng, wt, rows, cols, bias=True)
+    M = oracle.Mat(wt, data, rows, cols, scale, bias)
+    h = hip.upload(hip.HostMat(wt, data, rows, cols, scale, bias))
+    for m in (1, 2, 3, 5, 8, 9, 13):
+        x = rng.standard_normal((m, cols)).astype(np.float32)
+        y = hip.matmul(h, x)
+        r = oracle.matmul(M, x)
+        assert y.shape == r.shape
+        assert rel_err(y, r) < GEMV_TOL, (wt, rows, cols, m, rel_err(y, r))
+
+
+def test_matmul_stacked_upload(hip, oracle):
+    # n_parts > 1 stacks rows like upload_parts (gpu_vulkan.cpp:476-536)
+    rng = np.random.default_rng(3)
+    parts = [make_mat(rng, Q8, r, 256, bias=True) for r in (64, 32, 32)]
+    h = hip.upload(*[hip.HostMat(Q8, d, d.shape[0], 256, s, b) for d, s, b in parts])
+    assert hip.mat_shape(h) == (128, 256)
+    x = rng.standard_normal((2, 256)).astype(np.float32)
+    y = hip.matmul(h, x)
+    r = np.concatenate([oracle.matmul(oracle.Mat(Q8, d, d.shape[0], 256, s, b), x) for d, s, b in parts], axis=1)
+    assert rel_err(y, r) < GEMV_TOL
+
+
+def test_matmul_rejects_bad_shapes(hip):
+    bad = hip.HostMat(Q8, np.zeros((4, 40), np.int8), 4, 40, np.zeros((4, 1), np.float32))
+    with pytest.raises(hip.VoxHipError):
+        hip.upload(bad)  # Q8 needs cols % 32 == 0 (kernels.cpp:655)
+    with pytest.raises(hip.VoxHipError):
+        hip.matmul(12345, np.zeros(32, np.float32))
+
+
+def masked(l, cfg):
+    """engine.cpp:664-668 applied on the host for the oracle."""
+    l = l.copy()
+    for i in range(max(0, cfg.suppress_from), min(len(l), cfg.suppress_to)):
+        if i != cfg.eos_code:
+            l[i] = -np.inf
+    if cfg.block_eos and 0 <= cfg.eos_code < len(l):
+        l[cfg.eos_code] = -np.inf
+    return l
+
+
+def test_sampler_parity(hip, oracle):
+    rng = np.random.default_rng(8)
+    for i in range(400):
+        n = int(rng.choice([2, 3, 50, 257, 3072, 6564]))
+        l = (rng.standard_normal(n) * rng.uniform(0.3, 5)).astype(np.float32)
+        if i % 4 == 0:
+            l = np.round(l).astype(np.float32)  # ties
+        if i % 5 == 0:
+            l[rng.integers(0, n, max(1, n // 3))] = -np.inf
+        T = float(rng.choice([0.0, 0.7, 0.9, 1.0, 1.5]))
+        k = int(rng.choice([0, 1, 25, 50, 4096]))
+        p = float(rng.choice([1.0, 0.8, 0.3]))
+        rep = float(rng.choice([1.0, 1.3]))
+        hist = rng.integers(0, n, int(rng.integers(0, 30))).astype(np.int32) if rep != 1.0 else None
+        seed = int(rng.integers(0, 2**63))
+        cfg = hip.sample_cfg(T, p, k, rep, seed=seed, frame=int(rng.integers(0, 1 << 40)), codebook=int(rng.integers(0, 16)))
+        if i % 3 == 0 and n > 40:
+            cfg.suppress_from, cfg.suppress_to, cfg.eos_code, cfg.block_eos = n - 20, n, n - 5, int(i % 2)
+        u = oracle.uniform(seed, cfg.frame, cfg.codebook, 0)
+        want = oracle.sample_logits(masked(l, cfg), T, p, k, rep, hist, u)
+        kk = k if 0 < k < n else n
+        if T > 0 and kk > 4096:
+            with pytest.raises(hip.VoxHipError):
+                hip.sample_logits(l, cfg, hist)
+            continue
+        assert hip.sample_logits(l, cfg, hist) == want, (i, n, T, k, p, rep)
+
+
+def test_sampler_reference_rules(hip):
+    # test_core.cpp:53-78 on the device
+    l = np.float32([0.1, 3.0, 0.2, 3.0])
+    assert hip.sample_logits(l, hip.sample_cfg(temperature=0.0)) == 1
+    for fr in range(5):
+        assert hip.sample_logits(l, hip.sample_cfg(top_k=1, frame=fr)) == 1
+    assert hip.sample_logits(l, hip.sample_cfg(temperature=0.0, repetition_penalty=10.0), [1]) == 3
+    two = np.float32([0.0, np.log(3.0)])
+    ones = sum(hip.sample_logits(two, hip.sample_cfg(temperature=1.0, top_k=0, seed=42, frame=i)) == 1 for i in range(3000))
+    assert abs(ones / 3000.0 - 0.75) < 0.03

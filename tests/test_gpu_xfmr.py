@@ -1,0 +1,194 @@
+"""Transformer parity: the device decode/prefill path against the oracle's transformer_forward.
+
+The oracle runs with an f16 KV cache model (kv_f16 = 1: appended keys/values rounded to f16, as the device
+stores them), so differences come only from float summation order and libm ulps; the bar is the north star's
+1e-3 for f32 activations with the `vox verify` metric. Against the reference's own f32 cache (kv_f16 = 0) the
+bar is the f16 class, 1e-2.
+"""
+import numpy as np
+import pytest
+
+from conftest import rel_err
+from models import Model
+
+pytestmark = pytest.mark.gpu
+
+F32, F16, BF16, Q8, Q4 = 0, 1, 2, 3, 4
+TOL = 1e-3
+
+
+def build(hip, mdl):
+    x = hip.xfmr_create(mdl.hx, "t")
+    head = hip.upload(mdl.head[1]) if mdl.head else -1
+    return x, head
+
+
+def oracle_head(oracle, mdl, out_last):
+    return oracle.matmul(mdl.head[0], out_last[None])[0]
+
+
+@pytest.mark.parametrize("wt", [Q8, Q4, BF16, F16, F32])
+def test_decode_steps(hip, oracle, wt):
+    mdl = Model(100 + wt, 2, 256, 4, 2, 128, 512, wtype=wt, head_rows=300)
+    xf, head = build(hip, mdl)
+    seq = hip.seq_create(xf, 64)
+    kv = mdl.oracle_kv(64, kv_f16=1)
+    kv32 = mdl.oracle_kv(64, kv_f16=0)
+    rng = np.random.default_rng(wt)
+    for step in range(6):
+        x = rng.standard_normal((1, 256)).astype(np.float32)
+        out, logits = hip.forward(xf, seq, step, x, 256, head=head)
+        ref = oracle.transformer_forward(mdl.ox, kv, x)
+        ref32 = oracle.transformer_forward(mdl.ox, kv32, x)
+        assert rel_err(out, ref) < TOL, (step, rel_err(out, ref))
+        assert rel_err(out, ref32) < 1e-2
+        assert rel_err(logits, oracle_head(oracle, mdl, ref)) < TOL
+    k, v = hip.seq_download(seq, 1, 6, 256)
+    assert np.array_equal(k, kv.k[1, :6]) or rel_err(k, kv.k[1, :6]) < 2e-3
+
+
+@pytest.mark.parametrize("m", [3, 8, 12])
+def test_prefill_then_decode(hip, oracle, m):
+    # m <= 8 keeps int8 activations; m > 8 switches q8 to f32 activations (kernels.cpp:660-679)
+    mdl = Model(200 + m, 2, 256, 4, 2, 128, 512, wtype=Q8, head_rows=64)
+    xf, head = build(hip, mdl)
+    seq = hip.seq_create(xf, 64)
+    kv = mdl.oracle_kv(64, kv_f16=1)
+    rng = np.random.default_rng(m)
+    x = rng.standard_normal((m, 256)).astype(np.float32)
+    out, logits = hip.forward(xf, seq, 0, x, 256, head=head)
+    ref = oracle.transformer_forward(mdl.ox, kv, x)
+    assert rel_err(out, ref) < TOL
+    assert rel_err(logits, oracle_head(oracle, mdl, ref)) < TOL
+    for step in range(3):
+        x = rng.standard_normal((1, 256)).astype(np.float32)
+        out, _ = hip.forward(xf, seq, m + step, x, 256, head=head)
+        assert rel_err(out, oracle.transformer_forward(mdl.ox, kv, x)) < TOL
+
+
+def test_gqa7_bias_hd64(hip, oracle):
+    # CosyVoice2-shaped attention: 7 query heads per kv head, head_dim 64, q/k/v biases, no q/k norm
+    mdl = Model(300, 2, 128, 7, 1, 64, 256, wtype=Q8, qk_norm=False, bias=True, head_rows=100, head_type=F32)
+    xf, head = build(hip, mdl)
+    seq = hip.seq_create(xf, 32)
+    kv = mdl.oracle_kv(32, 1)
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((5, 128)).astype(np.float32)
+    out, logits = hip.forward(xf, seq, 0, x, 128, head=head)
+    ref = oracle.transformer_forward(mdl.ox, kv, x)
+    assert rel_err(out, ref) < TOL and rel_err(logits, oracle_head(oracle, mdl, ref)) < TOL
+    for step in range(4):
+        x = rng.standard_normal((1, 128)).astype(np.float32)
+        out, logits = hip.forward(xf, seq, 5 + step, x, 128, head=head)
+        ref = oracle.transformer_forward(mdl.ox, kv, x)
+        assert rel_err(out, ref) < TOL and rel_err(logits, oracle_head(oracle, mdl, ref)) < TOL
+
+
+def test_long_context_splits(hip, oracle):
+    # 700 keys: the split-K attention uses many splits; one kv head per 2 query heads
+    mdl = Model(400, 1, 256, 4, 2, 128, 256, wtype=Q8)
+    xf, _ = build(hip, mdl)
+    seq = hip.seq_create(xf, 1024)
+    kv = mdl.oracle_kv(1024, 1)
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((699, 256)).astype(np.float32)
+    out, _ = hip.forward(xf, seq, 0, x, 256)
+    ref = oracle.transformer_forward(mdl.ox, kv, x)
+    assert rel_err(out, ref) < TOL
+    x = rng.standard_normal((1, 256)).astype(np.float32)
+    out, _ = hip.forward(xf, seq, 699, x, 256)
+    assert rel_err(out, oracle.transformer_forward(mdl.ox, kv, x)) < TOL
+
+
+def test_forward_hidden_and_in_proj(hip, oracle):
+    mdl = Model(500, 2, 128, 4, 2, 64, 256, wtype=Q8)
+    xf, _ = build(hip, mdl)
+    rng = np.random.default_rng(7)
+    # hidden states of all rows, no final norm (gpu_xfmr_forward_hidden)
+    seq = hip.seq_create(xf, 16)
+    kv = mdl.oracle_kv(16, 1)
+    x = rng.standard_normal((3, 128)).astype(np.float32)
+    hid = hip.forward_hidden(xf, seq, 0, x, 128)
+    _, all_ref = oracle.transformer_forward(mdl.ox, kv, x, want_all=True)
+    L = oracle.lib()
+    for i in range(3):
+        nrm = np.empty(128, np.float32)
+        L.vo_rmsnorm(hid[i].ctypes.data, mdl.final_norm.ctypes.data, 128, np.float32(1e-6), nrm.ctypes.data)
+        assert rel_err(nrm, all_ref[i]) < TOL
+    # input projection inside the step (transformer_step_fused with in_proj)
+    from models import make_mat
+    d, s, b = make_mat(rng, Q8, 128, 96, bias=True)
+    ip = hip.upload(hip.HostMat(Q8, d, 128, 96, s, b))
+    seq2 = hip.seq_create(xf, 16)
+    kv2 = mdl.oracle_kv(16, 1)
+    xi = rng.standard_normal((2, 96)).astype(np.float32)
+    out, _ = hip.forward(xf, seq2, 0, xi, 128, in_proj=ip)
+    h = oracle.matmul(oracle.Mat(Q8, d, 128, 96, s, b), xi)
+    assert rel_err(out, oracle.transformer_forward(mdl.ox, kv2, h)) < TOL
+
+
+def test_pair_and_steps(hip, oracle):
+    mdl = Model(600, 2, 256, 4, 2, 128, 512, wtype=Q8, head_rows=80)
+    xf, head = build(hip, mdl)
+    rng = np.random.default_rng(9)
+    seqs = [hip.seq_create(xf, 32) for _ in range(3)]
+    kvs = [mdl.oracle_kv(32, 1) for _ in range(3)]
+    lens = [4, 4, 7]
+    for s, k, n in zip(seqs, kvs, lens):
+        pre = rng.standard_normal((n, 256)).astype(np.float32)
+        hip.forward(xf, s, 0, pre, 256)
+        oracle.transformer_forward(mdl.ox, k, pre)
+    # pair: sequences 0 and 1 at the same position (gpu_xfmr_forward_pair)
+    x2 = rng.standard_normal((2, 256)).astype(np.float32)
+    out2, log2 = hip.forward_pair(xf, seqs[0], seqs[1], 4, x2, 256, head=head)
+    for i in range(2):
+        r = oracle.transformer_forward(mdl.ox, kvs[i], x2[i:i + 1])
+        assert rel_err(out2[i], r) < TOL and rel_err(log2[i], oracle_head(oracle, mdl, r)) < TOL
+    # B independent sessions at their own positions (transformer_forward_steps)
+    x3 = rng.standard_normal((3, 256)).astype(np.float32)
+    out3, log3 = hip.forward_steps(xf, seqs, [5, 5, 7], x3, 256, head=head)
+    ref3 = oracle.transformer_forward_steps(mdl.ox, kvs, x3)
+    assert rel_err(out3, ref3) < TOL
+    for i in range(3):
+        assert rel_err(log3[i], oracle_head(oracle, mdl, ref3[i])) < TOL
+
+
+def test_decode_graph_replays(hip, oracle):
+    # The captured decode step replays to the same result as the host-pointer forward, every replay.
+    mdl = Model(700, 2, 256, 4, 2, 128, 512, wtype=Q8, head_rows=256)
+    xf, head = build(hip, mdl)
+    seq_a, seq_b = hip.seq_create(xf, 32), hip.seq_create(xf, 32)
+    rng = np.random.default_rng(10)
+    pre = rng.standard_normal((5, 256)).astype(np.float32)
+    hip.forward(xf, seq_a, 0, pre, 256)
+    hip.forward(xf, seq_b, 0, pre, 256)
+    x = rng.standard_normal((1, 256)).astype(np.float32)
+    out_ref, log_ref = hip.forward(xf, seq_a, 5, x, 256, head=head)
+    dx, dout, dlog, dtok = hip.DevBuf(256 * 4), hip.DevBuf(256 * 4), hip.DevBuf(256 * 4), hip.DevBuf(4)
+    dx.upload(x)
+    cfg = hip.sample_cfg(0.9, 1.0, 50, seed=1234, frame=3)
+    toks = []
+    for rep in range(4):
+        hip.decode_dev(xf, seq_b, 5, dx, 1, dout, head, dlog, cfg, dtok)
+        hip.sync()
+        out = dout.download(256, np.float32)
+        lg = dlog.download(256, np.float32)
+        assert np.array_equal(out, out_ref) and np.array_equal(lg, log_ref), rep
+        toks.append(int(dtok.download(1, np.int32)[0]))
+    assert len(set(toks)) == 1
+    u = oracle.uniform(1234, 3, 0, 0)
+    assert toks[0] == oracle.sample_logits(log_ref, 0.9, 1.0, 50, 1.0, None, u)
+    for b in (dx, dout, dlog, dtok):
+        b.free()
+
+
+def test_errors_are_reported(hip):
+    mdl = Model(800, 1, 128, 4, 2, 64, 256, wtype=Q8)
+    xf, _ = build(hip, mdl)
+    seq = hip.seq_create(xf, 8)
+    with pytest.raises(hip.VoxHipError, match="capacity"):
+        hip.forward(xf, seq, 7, np.zeros((2, 128), np.float32), 128)
+    with pytest.raises(hip.VoxHipError):
+        hip.seq_create(xf, 0)
+    with pytest.raises(hip.VoxHipError):
+        hip.forward(xf, 999, 0, np.zeros((1, 128), np.float32), 128)

@@ -1,0 +1,388 @@
+"""Pins the CPU oracle (oracle/liboracle.so) before it is trusted as the parity checker.
+
+Each restated function is checked against at least one of:
+  - the reference's own known answers (tests/test_core.cpp of the reference: Philox KAT :35-43, sampler rules
+    :45-79, Q4 bounds :461-521, noise moments :630-645);
+  - the golden fixture written by the compiled reference (tests/golden/golden_ref.npz, bit-exact);
+  - the compiled reference harness itself when present (oracle/_ref, bit-exact);
+  - float64 / closed-form / brute-force checks that do not restate the oracle's code path.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import pyoracle as po
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "golden_ref.npz")
+
+
+@pytest.fixture(scope="module")
+def gold():
+    return np.load(GOLD, allow_pickle=False)
+
+
+def philox(c, k):
+    c = np.ascontiguousarray(c, np.uint32)
+    k = np.ascontiguousarray(k, np.uint32)
+    out = np.empty(4, np.uint32)
+    po.lib().vo_philox4x32_10(c.ctypes.data, k.ctypes.data, out.ctypes.data)
+    return out
+
+
+# ------------------------------------------------------------------ Philox / DetRng
+def test_philox_random123_kat(oracle):
+    # Random123 known-answer vectors, as the reference checks them (test_core.cpp:35-43)
+    assert list(philox([0, 0, 0, 0], [0, 0])) == [0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8]
+    assert list(philox([0xffffffff] * 4, [0xffffffff] * 2)) == [0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd]
+    assert list(philox([0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344], [0xa4093822, 0x299f31d0])) == \
+        [0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1]
+
+
+def test_philox_golden(oracle, gold):
+    for c, k, o in zip(gold["philox_ctr"], gold["philox_key"], gold["philox_out"]):
+        assert list(philox(c, k)) == list(o)
+
+
+def test_uniform_closed_form_and_golden(oracle, gold):
+    # u = (r0 >> 8) / 2^24 with counter (frame lo, frame hi, codebook, draw) under key (seed lo, seed hi):
+    # KAT vector 1 is the counter/key (0,0,0,0)/(0,0)
+    assert po.uniform(0, 0, 0, 0) == np.float32((0x6627e8d5 >> 8) / 16777216.0)
+    for a, o in zip(gold["uniform_args"], gold["uniform_out"]):
+        assert np.float32(po.uniform(int(a[0]), int(a[1]), int(a[2]) & 0xFFFFFFFF, int(a[3]) & 0xFFFFFFFF)) == o
+    assert po.uniform(42, 5, 3) == po.uniform(42, 5, 3)
+    assert po.uniform(42, 5, 3) != po.uniform(43, 5, 3)
+    assert po.uniform(42, 5, 3) != po.uniform(42, 5, 4)
+    assert 0.0 <= po.uniform(42, 0, 0) < 1.0
+
+
+# ------------------------------------------------------------------ sampler
+def test_sampler_rules(oracle):
+    # test_core.cpp:45-79
+    l = [0.1, 3.0, 0.2, 3.0]
+    assert po.sample_logits(l, temperature=0.0) == 1  # tie -> lower index
+    for u in (0.0, 0.3, 0.99):
+        assert po.sample_logits(l, top_k=1, u=u) == 1
+    assert po.sample_logits(l, temperature=0.0, rep=10.0, history=[1]) == 3
+    two = [0.0, float(np.log(3.0))]
+    ones = sum(po.sample_logits(two, temperature=1.0, top_k=0, u=po.uniform(42, i, 0)) == 1 for i in range(20000))
+    assert abs(ones / 20000.0 - 0.75) < 0.02
+
+
+def test_sampler_inverse_cdf_brute_force(oracle):
+    # With u on a fine grid, the share of draws picking token i equals its probability after top-k / top-p,
+    # computed here independently in float64.
+    rng = np.random.default_rng(1)
+    for T, k, p in ((1.0, 0, 1.0), (0.7, 5, 1.0), (1.3, 8, 0.6)):
+        l = rng.standard_normal(12).astype(np.float32) * 2
+        order = sorted(range(12), key=lambda i: (-l[i], i))
+        kk = k if 0 < k < 12 else 12
+        sel = order[:kk]
+        w = np.exp((l[sel].astype(np.float64) - l[sel[0]]) / T)
+        w /= w.sum()
+        keep = kk
+        if 0 < p < 1:
+            keep = int(np.searchsorted(np.cumsum(w), p) + 1)
+        w = w[:keep] / w[:keep].sum()
+        N = 20000
+        counts = np.zeros(12)
+        for j in range(N):
+            counts[po.sample_logits(l, temperature=T, top_k=k, top_p=p, u=(j + 0.5) / N)] += 1
+        exp = np.zeros(12)
+        exp[sel[:keep]] = w
+        assert np.max(np.abs(counts / N - exp)) < 2.0 / N + 1e-9
+
+
+def test_sampler_golden(oracle, gold):
+    off = hoff = 0
+    for i in range(len(gold["sample_idx"])):
+        n, hn = int(gold["sample_n"][i]), int(gold["sample_hist_n"][i])
+        l = gold["sample_logits"][off:off + n]
+        h = gold["sample_hist"][hoff:hoff + hn]
+        off += n
+        hoff += hn
+        T, top_p, top_k, rep, u = gold["sample_params"][i]
+        got = po.sample_logits(l, float(T), float(top_p), int(top_k), float(rep), h if hn else None, float(u))
+        assert got == gold["sample_idx"][i], i
+
+
+def test_sampler_vs_ref(ref):
+    rng = np.random.default_rng(5)
+    for i in range(300):
+        n = int(rng.choice([3, 64, 3072, 6564]))
+        l = (rng.standard_normal(n) * 3).astype(np.float32)
+        if i % 3 == 0:
+            l = np.round(l * 2).astype(np.float32)
+        T = float(rng.choice([0.0, 0.9, 1.0]))
+        k = int(rng.choice([0, 1, 25, 50]))
+        p = float(rng.choice([1.0, 0.8]))
+        u = float(np.float32(rng.uniform()))
+        assert po.sample_logits(l, T, p, k, 1.0, None, u) == po.sample_logits(l, T, p, k, 1.0, None, u, use_ref=True)
+
+
+def test_ras_sample_properties(oracle):
+    # cosyvoice.cpp:617-664: nucleus by probability, then a repetition-aware resample from the full distribution
+    rng = np.random.default_rng(3)
+    n = 40
+    lp = rng.standard_normal(n).astype(np.float32)
+    pr = np.exp(lp.astype(np.float64) - lp.max())
+    pr /= pr.sum()
+    order = np.argsort(-pr, kind="stable")
+    f = po.lib().vo_ras_sample
+
+    def ras(decoded, u0, u1, top_p=0.8, top_k=25, win=10, tau=0.1):
+        l = lp.copy()
+        d = np.ascontiguousarray(decoded, np.int32)
+        return f(l.ctypes.data, n, d.ctypes.data if d.size else None, d.size, top_p, top_k, win, tau, u0, u1)
+
+    # top_k = 1 -> the most probable token, whatever u
+    assert all(ras([], u, 0.5, top_k=1) == order[0] for u in (0.0, 0.5, 0.999))
+    # no history: the nucleus (cum < top_p, at most top_k) is sampled by inverse CDF
+    keep, cum = [], 0.0
+    for i in order:
+        if cum < 0.8 and len(keep) < 25:
+            keep.append(i)
+            cum += pr[i]
+        else:
+            break
+    w = pr[keep] / pr[keep].sum()
+    N = 4000
+    counts = np.zeros(n)
+    for j in range(N):
+        counts[ras([], (j + 0.5) / N, 0.5)] += 1
+    exp = np.zeros(n)
+    exp[keep] = w
+    assert np.max(np.abs(counts / N - exp)) < 2.0 / N + 1e-9
+    # the top token repeated in the window -> never returned; the resample follows the rest of the distribution
+    top = order[0]
+    got = [ras([top] * 10, 0.0, (j + 0.5) / 400) for j in range(400)]
+    assert top not in got
+    rest = pr.copy()
+    rest[top] = 0
+    rest /= rest.sum()
+    c = np.bincount(got, minlength=n) / 400
+    assert np.max(np.abs(c - rest)) < 2.0 / 400 + 1e-9
+
+
+def test_noise_moments(oracle):
+    # test_core.cpp:630-645
+    a = po.noise(42, 0xF5000000 + 3, 100001)
+    b = po.noise(42, 0xF5000000 + 3, 100001)
+    c = po.noise(42, 0xF5000000 + 4, 100001)
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+    m = a.astype(np.float64).mean()
+    v = ((a - m) ** 2).mean()
+    assert abs(m) < 0.02 and abs(v - 1.0) < 0.03
+
+
+# ------------------------------------------------------------------ formats
+def test_f16_conversions_exhaustive(oracle):
+    L = po.lib()
+    h = np.arange(65536, dtype=np.uint16)
+    ref = h.view(np.float16).astype(np.float32)
+    got = np.array([L.vo_f16_to_f32(int(x)) for x in h], np.float32)
+    fin = np.isfinite(ref)
+    assert np.array_equal(got[fin], ref[fin]) and np.all(np.isnan(got[~fin]) == np.isnan(ref[~fin]))
+    rng = np.random.default_rng(2)
+    f = np.concatenate([rng.standard_normal(20000).astype(np.float32) * s for s in (1e-7, 1e-5, 1e-3, 1, 1e3, 7e4)])
+    f = np.concatenate([f, np.float32([0, -0.0, 65504, 65519, 65520, 6.1035156e-05, 5.9604645e-08, 2.9802322e-08, 2.98e-08])])
+    got = np.array([L.vo_f32_to_f16(float(x)) for x in f], np.uint16)
+    assert np.array_equal(got, f.astype(np.float16).view(np.uint16))
+
+
+def test_quantize_q8_golden_and_bounds(oracle, gold):
+    q, s = po.quantize_q8(gold["quant_w"])
+    assert np.array_equal(q, gold["q8_q"]) and np.array_equal(s.view(np.uint32), gold["q8_s"].view(np.uint32))
+    w = gold["quant_w"]
+    assert np.all(np.abs(q.astype(np.int32)) <= 127)
+    deq = q.astype(np.float32).reshape(37, 5, 32) * s[:, :, None]
+    err = np.abs(deq - w.reshape(37, 5, 32))
+    assert np.all(err <= s[:, :, None] * 0.5 * (1 + 1e-6) + 1e-30)
+
+
+def test_quantize_q4_golden_and_bounds(oracle, gold):
+    q, s = po.quantize_q4(gold["quant_w"])
+    assert np.array_equal(q, gold["q4_q"]) and np.array_equal(s.view(np.uint32), gold["q4_s"].view(np.uint32))
+    # test_core.cpp:461-500: error within two quantization steps per element
+    M = po.Mat(po.Q4, q, 37, 160, s)
+    deq = np.stack([po.mat_row(M, r) for r in range(37)])
+    step = np.repeat(np.abs(s), 32, axis=1)
+    assert np.all(np.abs(deq - gold["quant_w"]) <= step * 2.001)
+
+
+def test_q4_unpack_closed_form(oracle):
+    # byte j of a block = w[j] | w[j+16] << 4, value (u - 8) * scale (kernels.hpp:44-47)
+    rng = np.random.default_rng(4)
+    u = rng.integers(0, 16, size=(3, 64)).astype(np.uint8)
+    packed = np.empty((3, 32), np.uint8)
+    for b in range(2):
+        packed[:, b * 16:(b + 1) * 16] = u[:, b * 32:b * 32 + 16] | (u[:, b * 32 + 16:b * 32 + 32] << 4)
+    s = rng.uniform(0.1, 1, size=(3, 2)).astype(np.float32)
+    M = po.Mat(po.Q4, packed, 3, 64, s)
+    for r in range(3):
+        exp = (u[r].astype(np.float32) - 8) * np.repeat(s[r], 32)
+        assert np.array_equal(po.mat_row(M, r), exp)
+
+
+# ------------------------------------------------------------------ matmul
+@pytest.mark.parametrize("name,wt", [("q8", po.Q8), ("q4", po.Q4), ("f32", po.F32), ("f16", po.F16)])
+@pytest.mark.parametrize("m", [1, 3, 8, 12])
+def test_matmul_golden(oracle, gold, name, wt, m):
+    w = gold["quant_w"]
+    data = {"q8": gold["q8_q"], "q4": gold["q4_q"], "f32": w, "f16": w.astype(np.float16).view(np.uint16)}[name]
+    scale = {"q8": gold["q8_s"], "q4": gold["q4_s"]}.get(name)
+    M = po.Mat(wt, data, 37, 160, scale, gold["mm_bias"])
+    got = po.matmul(M, gold["mm_x"][:m])
+    assert np.array_equal(got.view(np.uint32), gold[f"mm_{name}_m{m}"].view(np.uint32))
+
+
+def test_matmul_int_path_vs_float64(oracle):
+    # q8 m <= 8: exact int32 block dots on int8 activations; compare with a float64 sum over the same
+    # quantized operands (an independent evaluation order)
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal((64, 1024)) * 0.02).astype(np.float32)
+    q, s = po.quantize_q8(w)
+    x = rng.standard_normal((4, 1024)).astype(np.float32)
+    M = po.Mat(po.Q8, q, 64, 1024, s)
+    y = po.matmul(M, x)
+    for i in range(4):
+        xq, xs = po.quantize_act(x[i])
+        d = (q.reshape(64, 32, 32).astype(np.int64) * xq.reshape(32, 32).astype(np.int64)).sum(-1).astype(np.float64)
+        ref = (d * (s.astype(np.float64) * xs.astype(np.float64))).sum(-1)
+        assert np.max(np.abs(y[i] - ref)) <= 1e-5 * np.max(np.abs(ref))
+    # the activation quantizer itself: |x - xq * xs| <= xs / 2 and max |xq| == 127 per non-zero block
+    xq, xs = po.quantize_act(x[0])
+    assert np.all(np.abs(x[0] - xq.astype(np.float32) * np.repeat(xs, 32)) <= np.repeat(xs, 32) * 0.5001)
+    assert np.all(np.abs(xq.reshape(32, 32)).max(-1) == 127)
+
+
+def test_matmul_vs_ref_random(ref):
+    rng = np.random.default_rng(11)
+    for wt in (po.Q8, po.Q4, po.F32, po.F16, po.BF16):
+        for rows, cols in ((5, 32), (33, 96), (256, 1024)):
+            w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+            if wt == po.Q8:
+                data, s = po.quantize_q8(w)
+            elif wt == po.Q4:
+                data, s = po.quantize_q4(w)
+            elif wt == po.F16:
+                data, s = w.astype(np.float16).view(np.uint16), None
+            elif wt == po.BF16:
+                data, s = (w.view(np.uint32) >> 16).astype(np.uint16), None
+            else:
+                data, s = w, None
+            b = rng.standard_normal(rows).astype(np.float32)
+            M = po.Mat(wt, data, rows, cols, s, b)
+            for m in (1, 2, 8, 9, 20):
+                x = rng.standard_normal((m, cols)).astype(np.float32)
+                a, r = po.matmul(M, x), po.matmul(M, x, use_ref=True)
+                assert np.array_equal(a.view(np.uint32), r.view(np.uint32)), (wt, rows, cols, m)
+
+
+# ------------------------------------------------------------------ elementwise
+def test_norms_rope_softmax_golden(oracle, gold):
+    L = po.lib()
+    out = np.empty(1024, np.float32)
+    x, w = gold["rms_x"], gold["rms_w"]
+    L.vo_rmsnorm(x.ctypes.data, w.ctypes.data, 1024, np.float32(1e-6), out.ctypes.data)
+    assert np.array_equal(out, gold["rms_out"])
+    L.vo_layernorm(x.ctypes.data, w.ctypes.data, None, 1024, np.float32(1e-6), out.ctypes.data)
+    assert np.array_equal(out, gold["ln_out"])
+    s = x[:513].copy()
+    L.vo_softmax(s.ctypes.data, 513)
+    assert np.array_equal(s, gold["softmax_out"])
+    inv = np.empty(64, np.float32)
+    L.vo_rope_inv_freq(128, 1e6, inv.ctypes.data)
+    assert np.array_equal(inv, gold["rope_inv"])
+    q = gold["rope_x"].copy()
+    L.vo_rope_apply(q.ctypes.data, 16, 128, inv.ctypes.data, 512)
+    assert np.array_equal(q, gold["rope_out"])
+
+
+def test_norms_rope_float64(oracle):
+    # textbook formulas in float64 (independent evaluation): RMSNorm, LayerNorm, softmax, rotate-half RoPE
+    L = po.lib()
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal(1024).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(1024)).astype(np.float32)
+    out = np.empty(1024, np.float32)
+    L.vo_rmsnorm(x.ctypes.data, w.ctypes.data, 1024, np.float32(1e-6), out.ctypes.data)
+    x64 = x.astype(np.float64)
+    assert np.allclose(out, w * x64 / np.sqrt((x64 ** 2).mean() + 1e-6), rtol=2e-6, atol=1e-7)
+    L.vo_layernorm(x.ctypes.data, w.ctypes.data, None, 1024, np.float32(1e-6), out.ctypes.data)
+    assert np.allclose(out, (x64 - x64.mean()) / np.sqrt(x64.var() + 1e-6) * w, rtol=2e-6, atol=1e-6)
+    s = x[:100].copy()
+    L.vo_softmax(s.ctypes.data, 100)
+    e = np.exp(x64[:100] - x64[:100].max())
+    assert np.allclose(s, e / e.sum(), rtol=1e-5, atol=1e-9)
+    inv = np.empty(64, np.float32)
+    L.vo_rope_inv_freq(128, 1e6, inv.ctypes.data)
+    assert np.allclose(inv, 1.0 / 1e6 ** (np.arange(64) * 2 / 128.0), rtol=1e-7)
+    q = rng.standard_normal(128).astype(np.float32)
+    r = q.copy()
+    L.vo_rope_apply(r.ctypes.data, 1, 128, inv.ctypes.data, 37)
+    ang = inv.astype(np.float64) * 37
+    a, b = q[:64].astype(np.float64), q[64:].astype(np.float64)
+    assert np.allclose(r, np.concatenate([a * np.cos(ang) - b * np.sin(ang), b * np.cos(ang) + a * np.sin(ang)]), atol=1e-5)
+    assert abs(L.vo_silu(np.float32(1.5)) - 1.5 / (1 + np.exp(-1.5))) < 1e-6
+
+
+# ------------------------------------------------------------------ transformer
+def test_transformer_golden(oracle, gold):
+    from models import Model
+    mdl = Model(7, 2, 64, 4, 2, 32, 96, wtype=po.Q8)
+    kv = mdl.oracle_kv(16, kv_f16=0)
+    xs = gold["xf_x"]
+    _, oa = po.transformer_forward(mdl.ox, kv, xs[:5], want_all=True)
+    assert np.array_equal(oa, gold["xf_out_all5"])
+    assert np.array_equal(po.transformer_forward(mdl.ox, kv, xs[5:6]), gold["xf_out6"])
+    assert np.array_equal(po.transformer_forward(mdl.ox, kv, xs[6:7]), gold["xf_out7"])
+
+
+def test_transformer_vs_ref(ref):
+    from models import Model
+    rng = np.random.default_rng(13)
+    for wt, m in ((po.Q8, 1), (po.Q8, 4), (po.Q8, 11), (po.Q4, 3), (po.BF16, 2), (po.F16, 1)):
+        mdl = Model(21 + m, 2, 128, 4, 2, 64, 256, wtype=wt)
+        ka, kb = mdl.oracle_kv(64, 0), mdl.oracle_kv(64, 0)
+        for step in range(3):
+            x = rng.standard_normal((m, 128)).astype(np.float32)
+            a = po.transformer_forward(mdl.ox, ka, x)
+            b = po.transformer_forward(mdl.ox, kb, x, use_ref=True)
+            assert np.array_equal(a, b), (wt, m, step)
+        assert np.array_equal(ka.k[:, :ka.len], kb.k[:, :kb.len])
+    # B sessions in one pass (transformer_forward_steps)
+    mdl = Model(5, 2, 128, 4, 2, 64, 256, wtype=po.Q8)
+    kvs_a = [mdl.oracle_kv(16, 0) for _ in range(3)]
+    kvs_b = [mdl.oracle_kv(16, 0) for _ in range(3)]
+    for b in range(3):  # different lengths per session
+        pre = rng.standard_normal((b + 1, 128)).astype(np.float32)
+        po.transformer_forward(mdl.ox, kvs_a[b], pre)
+        po.transformer_forward(mdl.ox, kvs_b[b], pre, use_ref=True)
+    x = rng.standard_normal((3, 128)).astype(np.float32)
+    assert np.array_equal(po.transformer_forward_steps(mdl.ox, kvs_a, x), po.transformer_forward_steps(mdl.ox, kvs_b, x, use_ref=True))
+
+
+def test_transformer_steps_equal_single_calls(oracle):
+    # transformer_forward_steps == B calls of transformer_forward with m = 1 (kernels.hpp:144-146)
+    from models import Model
+    rng = np.random.default_rng(14)
+    mdl = Model(6, 2, 128, 4, 2, 64, 256, wtype=po.Q8)
+    kv1 = [mdl.oracle_kv(16, 1) for _ in range(2)]
+    kv2 = [mdl.oracle_kv(16, 1) for _ in range(2)]
+    x = rng.standard_normal((2, 128)).astype(np.float32)
+    a = po.transformer_forward_steps(mdl.ox, kv1, x)
+    b = np.stack([po.transformer_forward(mdl.ox, kv2[i], x[i:i + 1]) for i in range(2)])
+    assert np.array_equal(a, b)
+
+
+def test_transformer_kv_f16_mode(oracle):
+    # kv_f16 = 1 stores exactly the f16 rounding of what kv_f16 = 0 stores
+    from models import Model
+    rng = np.random.default_rng(15)
+    mdl = Model(8, 1, 128, 4, 2, 64, 256, wtype=po.Q8)
+    k0, k1 = mdl.oracle_kv(8, 0), mdl.oracle_kv(8, 1)
+    x = rng.standard_normal((3, 128)).astype(np.float32)
+    po.transformer_forward(mdl.ox, k0, x)
+    po.transformer_forward(mdl.ox, k1, x)
+    assert np.array_equal(k1.k[:, :3], k0.k[:, :3].astype(np.float16).astype(np.float32))

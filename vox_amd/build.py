@@ -1,0 +1,85 @@
+"""Builds the gfx950 backend in-tree.
+
+    python -m vox_amd.build            # libvoxhip.so (+ the drop-in libvox_gpu_hip.so and its test driver)
+
+Every translation unit is compiled by hipcc for --offload-arch=gfx950 in parallel, then linked into
+vox_amd/libvoxhip.so (C ABI of include/voxhip.h). gpu_hip.cpp, the C++17 implementation of the
+reference's vox::gpu_* interface on top of that ABI, is compiled by g++ into vox_amd/libvox_gpu_hip.so.
+"""
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CSRC = os.path.join(ROOT, "vox_amd", "csrc")
+OUT = os.path.join(ROOT, "vox_amd")
+BUILD = os.path.join(ROOT, "vox_amd", "_build")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+HIP_SOURCES = ["voxhip_runtime.hip", "vh_kernels_misc.hip", "vh_gemv_int_q8.hip", "vh_gemv_int_q4.hip", "vh_gemv_flt.hip"]
+HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
+             # packed FP32 instructions stay off (the compiler must not emit v_pk_{add,mul,fma}_f32)
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
+LIB = os.path.join(OUT, "libvoxhip.so")
+DROPIN = os.path.join(OUT, "libvox_gpu_hip.so")
+DROPIN_TEST = os.path.join(OUT, "_build", "test_gpu_hip")
+
+
+def _run(cmd, cwd=None):
+    p = subprocess.run(cmd, cwd=cwd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in p.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if p.returncode != 0:
+        raise RuntimeError(f"command failed ({p.returncode}): {' '.join(cmd)}\n{out}")
+    return out
+
+
+def _compile(src):
+    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+    _run([HIPCC] + HIP_FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj])
+    return obj
+
+
+def build_hip(jobs=None):
+    os.makedirs(BUILD, exist_ok=True)
+    jobs = jobs or min(len(HIP_SOURCES), max(1, (os.cpu_count() or 4)))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, HIP_SOURCES))
+    tmp = LIB + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_dropin():
+    """gpu_hip.cpp (C++17, g++) against this repo's restatement of the vox interface headers."""
+    iface = os.path.join(CSRC, "iface")
+    tmp = DROPIN + ".tmp"
+    _run(["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", "-I" + iface, "-I" + os.path.join(ROOT, "include"),
+          os.path.join(CSRC, "gpu_hip.cpp"), "-o", tmp, "-L" + OUT, "-lvoxhip", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, DROPIN)
+    os.makedirs(BUILD, exist_ok=True)
+    _run(["g++", "-std=c++17", "-O2", "-Wall", "-I" + iface, "-I" + os.path.join(ROOT, "include"),
+          "-I" + os.path.join(ROOT, "oracle"), os.path.join(ROOT, "tests", "cpp", "test_gpu_hip.cpp"), "-o", DROPIN_TEST,
+          "-L" + OUT, "-lvox_gpu_hip", "-lvoxhip", "-L" + os.path.join(ROOT, "oracle"), "-l:liboracle.so",
+          "-Wl,-rpath," + OUT + ":" + os.path.join(ROOT, "oracle"), "-lm", "-lpthread"])
+    return DROPIN
+
+
+def build_oracle():
+    _run(["make", "-s", "-C", os.path.join(ROOT, "oracle")])
+    if os.path.isdir("/root/reference/src"):
+        _run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "ref"])
+
+
+def build_all():
+    build_oracle()
+    build_hip()
+    build_dropin()
+
+
+if __name__ == "__main__":
+    what = sys.argv[1] if len(sys.argv) > 1 else "all"
+    {"all": build_all, "hip": build_hip, "dropin": build_dropin, "oracle": build_oracle}[what]()
+    print("built", what)

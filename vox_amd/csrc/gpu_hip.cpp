@@ -1,0 +1,216 @@
+// gpu_hip.cpp — Vox's device interface (src/gpu.hpp + the gpu_* hooks of src/kernels.hpp:88-100) on the
+// MI355X backend. Plain C++17: every call goes through the C ABI of include/voxhip.h (libvoxhip.so), which owns
+// the HIP context, the device memory and the gfx950 kernels. It replaces gpu_vulkan.cpp + gpu_codec.cpp +
+// gpu_f5.cpp in the Vox build the way gpu_stub.cpp does (CMakeLists.txt:42-61), so the resource planner
+// (make_plan, via gpu_enumerate) and create_backend (gpu_init("vulkan:N"), family.cpp:90-101) select it unchanged.
+//
+// Error convention of the reference backend (gpu_vulkan.cpp:568-571, :800-803): no exception escapes, false/-1
+// means "compute on the CPU", the reason is kept for gpu_stats().last_error, and one warning goes to stderr.
+// Entry points not provided by this backend yet (the predictor frame loop, the codec, F5, the CosyVoice flow)
+// answer like gpu_stub.cpp, so their callers stay on the CPU.
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "gpu.hpp"
+#include "voxhip.h"
+
+namespace vox {
+namespace {
+
+std::once_flag g_warn_once;
+
+void warn_once(const char *what) {
+    std::call_once(g_warn_once, [&] { std::fprintf(stderr, "vox: GPU %s failed (%s); falling back to CPU\n", what, voxhip_last_error()); });
+}
+
+voxhip_mat to_c(const Mat &m) {
+    voxhip_mat c;
+    c.type = int32_t(m.type);
+    c.data = m.data;
+    c.scale = m.scale;
+    c.rows = m.rows;
+    c.cols = m.cols;
+    c.bias = m.bias;
+    return c;
+}
+
+struct UploadCb {
+    const TransformerW *w;
+    const std::function<void(const Mat &)> *fn;
+};
+
+void on_uploaded(void *user, int32_t layer, int32_t which) {
+    auto *cb = static_cast<UploadCb *>(user);
+    const LayerW &L = cb->w->layers[size_t(layer)];
+    const Mat *m[7] = {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down};
+    (*cb->fn)(*m[which]);
+}
+
+}  // namespace
+
+bool gpu_init(const std::string &device, std::string &err) {
+    char buf[512] = {0};
+    if (voxhip_init(device.c_str(), buf, sizeof buf)) return true;
+    err = buf;
+    return false;
+}
+
+bool gpu_active() { return voxhip_active() != 0; }
+
+std::string gpu_device_name() { return voxhip_device_name(); }
+
+int gpu_upload(const Mat &W) {
+    const voxhip_mat m = to_c(W);
+    return voxhip_upload(&m, 1);
+}
+
+GpuStats gpu_stats() {
+    voxhip_stats s;
+    voxhip_stats_get(&s);
+    GpuStats r;
+    r.mats_ok = s.mats_ok;
+    r.mats_failed = s.mats_failed;
+    r.bytes = s.bytes;
+    r.bytes_failed = s.bytes_failed;
+    r.last_error = voxhip_last_error();
+    return r;
+}
+
+std::vector<GpuDeviceInfo> gpu_enumerate() {
+    std::vector<GpuDeviceInfo> out;
+    const int n = voxhip_device_count();
+    for (int i = 0; i < n; ++i) {
+        voxhip_device_info d;
+        if (!voxhip_device_info_get(i, &d)) continue;
+        GpuDeviceInfo g;
+        g.index = d.index;
+        g.name = d.name;
+        g.type = d.type;  // "discrete": eligible for make_plan (resources.cpp:376-395)
+        g.software = d.software != 0;
+        g.unified_memory = d.unified_memory != 0;
+        g.vram_total = d.vram_total;
+        g.vram_free = d.vram_free;
+        g.max_storage_range = d.max_storage_range;
+        g.subgroup_arith = d.subgroup_arith != 0;
+        g.coop_matrix = d.coop_matrix != 0;
+        g.memory_budget = d.memory_budget != 0;
+        g.api_version = d.api_version;
+        g.vendor_id = d.vendor_id;
+        g.driver_version = d.driver_version;
+        out.push_back(g);
+    }
+    return out;
+}
+
+std::string gpu_list_devices() {
+    const auto devs = gpu_enumerate();
+    if (devs.empty()) return "no HIP devices\n";
+    std::string out;
+    for (const auto &d : devs) {
+        char buf[640];
+        std::snprintf(buf, sizeof buf, "hip:%d  %s  [%s]  VRAM %.1f GiB, free %.1f GiB\n", d.index, d.name.c_str(), d.type.c_str(),
+                      double(d.vram_total) / (1024.0 * 1024 * 1024), double(d.vram_free) / (1024.0 * 1024 * 1024));
+        out += buf;
+    }
+    return out;
+}
+
+void gpu_set_vram_limit(uint64_t bytes) { voxhip_set_vram_limit(bytes); }
+
+GpuMemInfo gpu_mem_info() {
+    voxhip_mem_info m;
+    voxhip_mem_info_get(&m);
+    GpuMemInfo r;
+    r.used = m.used;
+    r.limit = m.limit;
+    r.device_free = m.device_free;
+    r.device_total = m.device_total;
+    r.device_index = m.device_index;
+    return r;
+}
+
+int gpu_xfmr_create(const TransformerW &w, const char *name, int n_layers, const std::function<void(const Mat &)> &uploaded) {
+    if (w.layers.empty()) return -1;
+    std::vector<voxhip_layer> L(w.layers.size());
+    for (size_t i = 0; i < w.layers.size(); ++i) {
+        const LayerW &s = w.layers[i];
+        voxhip_layer &d = L[i];
+        d.q = to_c(s.q); d.k = to_c(s.k); d.v = to_c(s.v); d.o = to_c(s.o);
+        d.gate = to_c(s.gate); d.up = to_c(s.up); d.down = to_c(s.down);
+        d.qn = s.qn; d.kn = s.kn; d.ln1 = s.ln1; d.ln2 = s.ln2;
+        d.attn_scale = s.attn_scale; d.mlp_scale = s.mlp_scale;
+    }
+    voxhip_xfmr_desc desc;
+    desc.n_layers = int32_t(L.size());
+    desc.layers = L.data();
+    desc.final_norm = w.final_norm;
+    desc.hidden = w.hidden; desc.heads = w.heads; desc.kv_heads = w.kv_heads; desc.head_dim = w.head_dim; desc.inter = w.inter;
+    desc.eps = w.eps;
+    desc.theta = w.theta;
+    desc.window = w.window;
+    desc.inv_freq = w.inv_freq.data();
+    UploadCb cb{&w, &uploaded};
+    const int id = voxhip_xfmr_create(&desc, name, n_layers, uploaded ? on_uploaded : nullptr, &cb);
+    if (id < 0) warn_once("transformer setup");
+    return id;
+}
+
+int gpu_seq_create(int xfmr, int64_t capacity) { return voxhip_seq_create(xfmr, capacity); }
+
+void gpu_seq_free(int seq) { voxhip_seq_free(seq); }
+
+bool gpu_matmul(const Mat &W, const float *x, int64_t m, float *y) {
+    if (W.gpu < 0) return false;
+    if (voxhip_matmul(W.gpu, x, m, y)) return true;
+    warn_once("matmul");
+    return false;
+}
+
+bool gpu_xfmr_forward(const TransformerW &w, int seq, int64_t pos0, const float *x, int64_t m, float *out_last, const Mat *in_proj,
+                      const Mat *head, float *head_out) {
+    if (w.gpu_id < 0) return false;
+    if (voxhip_xfmr_forward(w.gpu_id, seq, pos0, x, m, out_last, in_proj ? in_proj->gpu : -1, head ? head->gpu : -1, head_out))
+        return true;
+    std::fprintf(stderr, "vox: GPU transformer failed: %s\n", voxhip_last_error());
+    return false;
+}
+
+bool gpu_xfmr_forward_hidden(const TransformerW &w, int seq, int64_t pos0, const float *x, int64_t m, float *hidden_out) {
+    if (w.gpu_id < 0) return false;
+    if (voxhip_xfmr_forward_hidden(w.gpu_id, seq, pos0, x, m, hidden_out)) return true;
+    std::fprintf(stderr, "vox: GPU transformer failed: %s\n", voxhip_last_error());
+    return false;
+}
+
+bool gpu_xfmr_forward_pair(const TransformerW &w, int seq0, int seq1, int64_t pos, const float *x2, const Mat *head, float *out2,
+                           float *head_out2) {
+    if (w.gpu_id < 0 || (head && head->gpu < 0)) return false;
+    if (voxhip_xfmr_forward_pair(w.gpu_id, seq0, seq1, pos, x2, head ? head->gpu : -1, out2, head_out2)) return true;
+    std::fprintf(stderr, "vox: GPU transformer (pair) failed: %s\n", voxhip_last_error());
+    return false;
+}
+
+// ---- not provided by this backend yet: the callers compute on the CPU (gpu_stub.cpp behaviour)
+bool gpu_pred_frame(const TransformerW &, int, const float *, const Mat *, const std::vector<Mat> &, const std::vector<Mat> &,
+                    const GpuSampleCfg &, int32_t *) {
+    return false;
+}
+int gpu_codec_create(const Qwen3Weights &) { return -1; }
+int gpu_codec_state_new(int) { return -1; }
+int gpu_codec_state_clone(int) { return -1; }
+void gpu_codec_state_free(int) {}
+bool gpu_codec_forward(int, int, const float *, int, std::vector<float> &) { return false; }
+int gpu_f5_create(const GpuF5Desc &) { return -1; }
+bool gpu_f5_begin(int, int, int, const float *, const float *) { return false; }
+bool gpu_f5_step(int, const float *, const float *, float *) { return false; }
+bool gpu_f5_vocos(int, const float *, int, std::vector<float> &) { return false; }
+void gpu_f5_end(int) {}
+std::string gpu_gemm_choice() { return ""; }
+void gpu_gemm_preset(const std::string &) {}
+int gpu_cosy_create(const GpuCosyDesc &) { return -1; }
+bool gpu_cosy_begin(int, int, const float *) { return false; }
+bool gpu_cosy_step(int, const float *, const float *, float *) { return false; }
+void gpu_cosy_end(int) {}
+
+}  // namespace vox

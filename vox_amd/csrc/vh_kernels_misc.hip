@@ -1,0 +1,137 @@
+// Launchers of the non-GEMV kernels: q/k post-processing, attention, sampler, quantizers, synthetic data.
+#include <atomic>
+#include <mutex>
+#include <set>
+
+#include "vh_attn.hpp"
+#include "vh_launch.hpp"
+#include "vh_sample.hpp"
+#include "vh_util.hpp"
+
+namespace vh {
+
+namespace {
+std::mutex g_tmu;
+hipEvent_t g_tq[16][2];
+int g_thead = 0;
+std::atomic<int> g_tcount{0};
+}  // namespace
+
+void timing_arm(hipEvent_t start, hipEvent_t stop) {
+    std::lock_guard<std::mutex> lk(g_tmu);
+    if (g_tcount == 16) return;
+    const int i = (g_thead + g_tcount) % 16;
+    g_tq[i][0] = start;
+    g_tq[i][1] = stop;
+    ++g_tcount;
+}
+void timing_clear() {
+    std::lock_guard<std::mutex> lk(g_tmu);
+    g_tcount = 0;
+}
+bool timing_take(hipEvent_t *start, hipEvent_t *stop) {
+    if (!g_tcount) return false;  // fast path; arming and launching happen on the calling thread
+    std::lock_guard<std::mutex> lk(g_tmu);
+    if (!g_tcount) return false;
+    *start = g_tq[g_thead][0];
+    *stop = g_tq[g_thead][1];
+    g_thead = (g_thead + 1) % 16;
+    --g_tcount;
+    return true;
+}
+
+hipError_t ensure_smem(const void *kernel, size_t bytes) {
+    if (bytes <= 65536) return hipSuccess;
+    static std::mutex mu;
+    static std::set<const void *> done;
+    std::lock_guard<std::mutex> lk(mu);
+    if (done.count(kernel)) return hipSuccess;
+    hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
+    if (e == hipSuccess) done.insert(kernel);
+    return e;
+}
+
+hipError_t launch_qk_post(const QkArgs &a, int m, hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    return launch(k_qk_post, dim3(a.heads + a.kv_heads, m), dim3(64), 0, s, a);
+}
+
+template <int HD, int G>
+static hipError_t attn_hg(const AttnArgs &a, int m, hipStream_t s) {
+    constexpr int LPK = HD / 8, NGRP = 4 * (64 / LPK);
+    const size_t smem = size_t(NGRP) * G * (HD + 2) * 4;
+    const void *k = reinterpret_cast<const void *>(&k_attn_partial<HD, G>);
+    hipError_t e = ensure_smem(k, smem);
+    if (e != hipSuccess) return e;
+    e = launch(k_attn_partial<HD, G>, dim3(kAttnSplits, a.kv_heads, m), dim3(256), smem, s, a);
+    if (e != hipSuccess) return e;
+    return launch(k_attn_combine<HD>, dim3(a.heads, m), dim3(HD), 0, s, a);
+}
+
+template <int HD>
+static hipError_t attn_h(const AttnArgs &a, int group, int m, hipStream_t s) {
+    switch (group) {
+        case 1: return attn_hg<HD, 1>(a, m, s);
+        case 2: return attn_hg<HD, 2>(a, m, s);
+        case 3: return attn_hg<HD, 3>(a, m, s);
+        case 4: return attn_hg<HD, 4>(a, m, s);
+        case 5: return attn_hg<HD, 5>(a, m, s);
+        case 6: return attn_hg<HD, 6>(a, m, s);
+        case 7: return attn_hg<HD, 7>(a, m, s);
+        case 8: return attn_hg<HD, 8>(a, m, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_attention(const AttnArgs &a, int hd, int group, int m, hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    if (hd == 128) return attn_h<128>(a, group, m, s);
+    if (hd == 64) return attn_h<64>(a, group, m, s);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_sample(const SampleCfgDev *cfg, const float *logits, int n, int32_t *out, hipStream_t s) {
+    return launch(k_sample, dim3(1), dim3(kSampleThreads), 0, s, cfg, logits, n, out);
+}
+
+static dim3 grid1(int64_t n, int bs) { return dim3(unsigned((n + bs - 1) / bs)); }
+
+hipError_t launch_quant_q8(const float *w, int64_t nblocks, int8_t *q, float *scale, hipStream_t s) {
+    if (nblocks <= 0) return hipSuccess;
+    return launch(k_quant_q8, grid1(nblocks, 256), dim3(256), 0, s, w, nblocks, q, scale);
+}
+hipError_t launch_quant_q4(const float *w, int64_t nblocks, uint8_t *q, float *scale, hipStream_t s) {
+    if (nblocks <= 0) return hipSuccess;
+    return launch(k_quant_q4, grid1(nblocks, 128), dim3(128), 0, s, w, nblocks, q, scale);
+}
+hipError_t launch_quant_act(const float *x, int64_t nblocks, int8_t *xq, float *xs, hipStream_t s) {
+    if (nblocks <= 0) return hipSuccess;
+    return launch(k_quant_act, grid1(nblocks, 256), dim3(256), 0, s, x, nblocks, xq, xs);
+}
+hipError_t launch_to_f16(const float *x, int64_t n, void *y, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    return launch(k_to_f16, grid1(n, 256), dim3(256), 0, s, x, n, static_cast<_Float16 *>(y));
+}
+hipError_t launch_to_bf16(const float *x, int64_t n, void *y, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    return launch(k_to_bf16, grid1(n, 256), dim3(256), 0, s, x, n, static_cast<uint16_t *>(y));
+}
+hipError_t launch_rmsnorm_rows(const float *x, int64_t ldx, const float *w, int K, float eps, float *out, int64_t ldo,
+                               int m, hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    return launch(k_rmsnorm_rows, dim3(m), dim3(256), 0, s, x, ldx, w, K, eps, out, ldo);
+}
+hipError_t launch_fill_normal(float *out, int64_t n, uint64_t seed, uint32_t stream, float mean, float std,
+                              hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    return launch(k_fill_normal, grid1((n + 1) / 2, 256), dim3(256), 0, s, out, n, seed, stream, mean, std);
+}
+hipError_t launch_fill_cache(void *c, int64_t planes, int64_t cap, int64_t len, int hd, uint64_t seed, uint32_t stream,
+                             float mean, float std, hipStream_t s) {
+    const int64_t pairs = planes * len * hd / 2;
+    if (pairs <= 0) return hipSuccess;
+    return launch(k_fill_cache, grid1(pairs, 256), dim3(256), 0, s, static_cast<_Float16 *>(c), planes, cap, len, hd,
+                       seed, stream, mean, std);
+}
+
+}  // namespace vh

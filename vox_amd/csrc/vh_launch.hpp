@@ -1,0 +1,52 @@
+// vh_launch.hpp — host-side launchers of the gfx950 kernels (one translation unit per kernel family).
+#pragma once
+#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
+
+#include "vh_types.hpp"
+
+namespace vh {
+
+// Kernel timing hook: timing_arm() queues (start, stop) event pairs; each kernel launch takes the next pair, if
+// any, and is launched with hipExtLaunchKernel so the events are stamped at that kernel's own start and end on
+// its stream. The benchmark arms it around single launches; an empty queue costs one branch per launch.
+void timing_arm(hipEvent_t start, hipEvent_t stop);
+void timing_clear();
+bool timing_take(hipEvent_t *start, hipEvent_t *stop);
+
+template <typename K, typename... Args>
+hipError_t launch(K kernel, dim3 grid, dim3 block, size_t smem, hipStream_t s, Args... args) {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (timing_take(&e0, &e1)) hipExtLaunchKernelGGL(kernel, grid, block, uint32_t(smem), s, e0, e1, 0u, args...);
+    else hipLaunchKernelGGL(kernel, grid, block, smem, s, args...);
+    return hipGetLastError();
+}
+
+// GEMV launch: rows/K/m etc. in a; wt = weight type; int_path = int8 activations (Q8 m <= 8, Q4 always).
+// Picks the row tile (R rows per wave, IT 1 KiB chunks in flight) from the matrix shape.
+hipError_t launch_gemv(int wt, bool int_path, int pro, int epi, const GemvArgs &a, hipStream_t s);
+hipError_t launch_gemv_int_q8(int pro, int epi, int M, int R, const GemvArgs &a, hipStream_t s);
+hipError_t launch_gemv_int_q4(int pro, int epi, int M, int R, const GemvArgs &a, hipStream_t s);
+hipError_t launch_gemv_flt(int wt, int pro, int epi, int M, int R, const GemvArgs &a, hipStream_t s);
+
+hipError_t launch_qk_post(const QkArgs &a, int m, hipStream_t s);
+// Split-K attention + combine: q (a.q) against each row's cache, output in a.out.
+hipError_t launch_attention(const AttnArgs &a, int hd, int group, int m, hipStream_t s);
+hipError_t launch_sample(const SampleCfgDev *cfg, const float *logits, int n, int32_t *out, hipStream_t s);
+
+hipError_t launch_quant_q8(const float *w, int64_t nblocks, int8_t *q, float *scale, hipStream_t s);
+hipError_t launch_quant_q4(const float *w, int64_t nblocks, uint8_t *q, float *scale, hipStream_t s);
+hipError_t launch_quant_act(const float *x, int64_t nblocks, int8_t *xq, float *xs, hipStream_t s);
+hipError_t launch_to_f16(const float *x, int64_t n, void *y, hipStream_t s);
+hipError_t launch_to_bf16(const float *x, int64_t n, void *y, hipStream_t s);
+hipError_t launch_rmsnorm_rows(const float *x, int64_t ldx, const float *w, int K, float eps, float *out, int64_t ldo,
+                               int m, hipStream_t s);
+hipError_t launch_fill_normal(float *out, int64_t n, uint64_t seed, uint32_t stream, float mean, float std,
+                              hipStream_t s);
+hipError_t launch_fill_cache(void *c, int64_t planes, int64_t cap, int64_t len, int hd, uint64_t seed, uint32_t stream,
+                             float mean, float std, hipStream_t s);
+
+// Shared-memory opt-in above 64 KiB, once per kernel.
+hipError_t ensure_smem(const void *kernel, size_t bytes);
+
+}  // namespace vh

@@ -1,0 +1,127 @@
+// vh_util.hpp — device quantizers of the reference formats, RMSNorm rows, synthetic data.
+#pragma once
+#include "vh_common.hpp"
+
+namespace vh {
+
+// quantize_q8 (kernels.cpp:918-929): per 32-block s = max|w| / 127, q = round-half-away(w / s). One thread per block.
+__global__ void k_quant_q8(const float *w, int64_t nblocks, int8_t *q, float *scale) {
+    const int64_t b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const float *p = w + b * 32;
+    float mx = 0.f;
+    for (int j = 0; j < 32; ++j) { const float a = fabsf(p[j]); mx = mx < a ? a : mx; }
+    const float s = mx / 127.0f;
+    scale[b] = s;
+    for (int j = 0; j < 32; ++j) q[b * 32 + j] = s > 0.f ? int8_t(int(roundf(p[j] / s))) : int8_t(0);
+}
+
+// quantize_q4 (kernels.cpp:606-645): scale search d = mx / -t for t = 7, 7.25 .. 9 by squared error (double),
+// then the least-squares scale when it is better. Packs byte j = (q[j] + 8) | (q[j + 16] + 8) << 4.
+__global__ void k_quant_q4(const float *w, int64_t nblocks, uint8_t *q, float *scale) {
+#pragma clang fp contract(off)
+    const int64_t b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const float *p = w + b * 32;
+    float mx = 0.f;
+    for (int j = 0; j < 32; ++j) if (fabsf(p[j]) > fabsf(mx)) mx = p[j];
+    float best_d = mx / -8.0f;
+    double best_err = INFINITY;
+    int8_t best_q[32];
+    for (int j = 0; j < 32; ++j) best_q[j] = 0;
+    if (mx != 0.0f)
+        for (int k = 0; k <= 8; ++k) {
+            const float d = mx / -(7.0f + 0.25f * float(k)), inv = 1.0f / d;
+            int8_t qq[32];
+            double err = 0;
+            for (int j = 0; j < 32; ++j) {
+                float c = floorf(p[j] * inv + 8.5f);
+                c = c < 0.0f ? 0.0f : c;
+                c = c > 15.0f ? 15.0f : c;
+                qq[j] = int8_t(int(c) - 8);
+                const double e = double(p[j]) - double(qq[j]) * double(d);
+                err += e * e;
+            }
+            if (err < best_err) {
+                best_err = err; best_d = d;
+                for (int j = 0; j < 32; ++j) best_q[j] = qq[j];
+            }
+        }
+    if (mx != 0.0f) {
+        double num = 0, den = 0;
+        for (int j = 0; j < 32; ++j) { num += double(p[j]) * best_q[j]; den += double(best_q[j]) * best_q[j]; }
+        if (den > 0) {
+            const float d2 = float(num / den);
+            double err = 0;
+            for (int j = 0; j < 32; ++j) { const double e = double(p[j]) - double(best_q[j]) * double(d2); err += e * e; }
+            if (err < best_err) best_d = d2;
+        }
+    }
+    scale[b] = best_d;
+    for (int j = 0; j < 16; ++j) q[b * 16 + j] = uint8_t(uint8_t(best_q[j] + 8) | uint8_t((best_q[j + 16] + 8) << 4));
+}
+
+// Activation quantization (kernels.cpp:515-523), one thread per 32-block.
+__global__ void k_quant_act(const float *x, int64_t nblocks, int8_t *xq, float *xs) {
+    const int64_t b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    float v[32];
+    for (int j = 0; j < 32; ++j) v[j] = x[b * 32 + j];
+    quant_block32(v, xq + b * 32, xs + b);
+}
+
+__global__ void k_to_f16(const float *x, int64_t n, _Float16 *y) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = _Float16(x[i]);
+}
+__global__ void k_to_bf16(const float *x, int64_t n, uint16_t *y) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = f32_to_bf16(x[i]);
+}
+
+// rmsnorm (kernels.cpp:707-712) of rows: out[i] = w * (x[i] * inv). grid (m), block 256.
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *x, int64_t ldx, const float *w, int K, float eps,
+                                                     float *out, int64_t ldo) {
+    __shared__ float red[4];
+    const float *xr = x + int64_t(blockIdx.x) * ldx;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < K; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    ss = block_sum<256>(ss, red);
+    const float inv = 1.0f / sqrtf(ss / float(K) + eps);
+    for (int i = threadIdx.x; i < K; i += 256) out[int64_t(blockIdx.x) * ldo + i] = w[i] * (xr[i] * inv);
+}
+
+// Synthetic N(mean, std) data: Philox4x32-10 counter (pair p, stream, draw 0/1) under key (seed), Box-Muller.
+VH_DEV void normal_pair(uint64_t seed, uint32_t stream, uint64_t p, float *z0, float *z1) {
+    const float u1 = det_uniform(uint32_t(seed), uint32_t(seed >> 32), p, stream, 0);
+    const float u2 = det_uniform(uint32_t(seed), uint32_t(seed >> 32), p, stream, 1);
+    const float r = sqrtf(-2.0f * logf(1.0f - u1));
+    const float a = 6.283185307179586f * u2;
+    *z0 = r * cosf(a);
+    *z1 = r * sinf(a);
+}
+
+__global__ void k_fill_normal(float *out, int64_t n, uint64_t seed, uint32_t stream, float mean, float std) {
+    const int64_t p = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (2 * p >= n) return;
+    float z0, z1;
+    normal_pair(seed, stream, uint64_t(p), &z0, &z1);
+    out[2 * p] = mean + std * z0;
+    if (2 * p + 1 < n) out[2 * p + 1] = mean + std * z1;
+}
+
+// Fills positions [0, len) of a [layers*kvh][cap][hd] f16 cache with N(mean, std).
+__global__ void k_fill_cache(_Float16 *c, int64_t planes, int64_t cap, int64_t len, int hd, uint64_t seed,
+                             uint32_t stream, float mean, float std) {
+    const int64_t p = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;  // pair index over planes*len*hd/2
+    const int64_t per_plane = len * hd / 2;
+    if (p >= planes * per_plane) return;
+    const int64_t plane = p / per_plane, r = p % per_plane;
+    float z0, z1;
+    normal_pair(seed, stream, uint64_t(p), &z0, &z1);
+    _Float16 *dst = c + plane * cap * hd + 2 * r;
+    dst[0] = _Float16(mean + std * z0);
+    dst[1] = _Float16(mean + std * z1);
+}
+
+}  // namespace vh

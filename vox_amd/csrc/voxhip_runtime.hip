@@ -1,0 +1,1337 @@
+// voxhip_runtime.hip — host runtime of the gfx950 backend; implements the C ABI of include/voxhip.h.
+//
+// One context per process (one device, one stream, one lock), as the reference backend
+// (gpu_vulkan.cpp:361-374, one mutex taken by every entry point). Weights are copied to HBM once and stay for
+// the process lifetime; transformers keep their q|k|v and gate|up matrices stacked (gpu_vulkan.cpp:784-788),
+// gate|up interleaved by row pairs so the SwiGLU epilogue sees a (gate, up) pair in one wave. KV caches are f16
+// in HBM, [layer][kv_head][capacity][head_dim]. A decode step is a fixed launch sequence that is captured once
+// into a HIP graph and replayed; positions and sampler parameters live in small device blocks that are
+// refreshed before each replay.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <tuple>
+#include <unordered_map>
+#include <vector>
+
+#include "vh_launch.hpp"
+#include "voxhip.h"
+
+using namespace vh;
+
+namespace {
+
+struct Fail : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+#define HIPCHECK(expr)                                                                                   \
+    do {                                                                                                 \
+        hipError_t e_ = (expr);                                                                          \
+        if (e_ != hipSuccess) throw Fail(std::string(#expr) + " failed: " + hipGetErrorString(e_));      \
+    } while (0)
+
+constexpr int kMaxM = 8;          // rows per device pass (the reference uses 256 for its GEMM path)
+constexpr int64_t kMaxCap = 65536;
+
+struct GpuMat {
+    int32_t type = 0;
+    int64_t rows = 0, cols = 0;
+    uint8_t *w = nullptr;
+    float *s = nullptr;
+    float *b = nullptr;
+    uint64_t bytes = 0;  // weights + scales + bias bytes (the GEMV's algorithmic stream)
+};
+
+struct LayerDev {
+    int qkv = -1, o = -1, gu = -1, down = -1;
+    size_t ln1 = 0, ln2 = 0, qn = 0, kn = 0;
+    bool qk = false;
+};
+
+struct GraphKey {
+    int seq, m, head, sample;
+    const void *x, *out, *logits, *token;
+    bool operator<(const GraphKey &o) const {
+        return std::tie(seq, m, head, sample, x, out, logits, token) <
+               std::tie(o.seq, o.m, o.head, o.sample, o.x, o.out, o.logits, o.token);
+    }
+};
+
+struct Xfmr {
+    std::string name;
+    int layers = 0, H = 0, heads = 0, kvh = 0, hd = 0, I = 0;
+    float eps = 1e-6f;
+    double theta = 1e4;
+    std::vector<float> inv_freq;
+    std::vector<LayerDev> L;
+    float *norms = nullptr;
+    size_t final_off = 0;
+    float *rope = nullptr;
+    int64_t rope_rows = 0;
+    // scratch for kMaxM rows
+    float *h = nullptr, *xin = nullptr, *qkv = nullptr, *q = nullptr, *ao = nullptr, *g = nullptr, *xnorm = nullptr;
+    float *pm = nullptr, *pl = nullptr, *po = nullptr, *logits = nullptr;
+    int64_t xin_cols = 0, logits_cap = 0;
+    RowRef *rows_dev = nullptr, *rows_host = nullptr;
+    SampleCfgDev *scfg_dev = nullptr, *scfg_host = nullptr;
+    int32_t *token_dev = nullptr;
+    std::map<GraphKey, hipGraphExec_t> graphs;
+    std::vector<RowRef> rows_last;
+    bool rows_valid = false;
+};
+
+struct Seq {
+    int xfmr = -1;
+    int64_t cap = 0;
+    _Float16 *k = nullptr, *v = nullptr;
+    bool used = false;
+    int layers = 0, kvh = 0, hd = 0;
+};
+
+struct Ctx {
+    std::mutex mu;
+    bool ok = false;
+    std::string init_error;
+    int dev = -1;
+    std::string name;
+    hipStream_t stream = nullptr;
+    std::vector<GpuMat> mats;
+    std::vector<Xfmr *> xf;
+    std::vector<Seq> seqs;
+    std::unordered_map<void *, uint64_t> allocs;
+    uint64_t vram_used = 0, vram_limit = 0;
+    voxhip_stats stats{};
+    std::string last_error;
+    bool warned = false;
+    // staging for host-pointer entry points
+    float *pin = nullptr;
+    size_t pin_bytes = 0;
+    float *dbuf_x = nullptr, *dbuf_y = nullptr;
+    size_t dbuf_x_bytes = 0, dbuf_y_bytes = 0;
+    // sampler staging for voxhip_sample_logits
+    SampleCfgDev *scfg_dev = nullptr, *scfg_host = nullptr;
+    int32_t *hist_dev = nullptr, *tok_dev = nullptr;
+    size_t hist_cap = 0;
+};
+
+Ctx g;
+
+void set_error(const std::string &e) {
+    g.last_error = e;
+}
+
+// ------------------------------------------------------------------ device memory with accounting
+void *dalloc(size_t bytes) {
+    if (bytes == 0) bytes = 16;
+    if (g.vram_limit && g.vram_used + bytes > g.vram_limit)
+        throw Fail("VRAM limit reached: " + std::to_string(g.vram_limit >> 20) + " MiB allowed, " +
+                   std::to_string(g.vram_used >> 20) + " MiB in use, " + std::to_string((bytes + (1u << 20) - 1) >> 20) +
+                   " MiB requested");
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) throw Fail(std::string("hipMalloc of ") + std::to_string(bytes >> 20) + " MiB failed: " + hipGetErrorString(e));
+    g.allocs[p] = bytes;
+    g.vram_used += bytes;
+    return p;
+}
+void dfree(void *p) {
+    if (!p) return;
+    auto it = g.allocs.find(p);
+    if (it != g.allocs.end()) { g.vram_used -= std::min(g.vram_used, it->second); g.allocs.erase(it); }
+    (void)hipFree(p);
+}
+template <class T>
+T *dalloc_t(size_t n) { return static_cast<T *>(dalloc(n * sizeof(T))); }
+
+float *pinned(size_t bytes) {
+    if (g.pin_bytes < bytes) {
+        if (g.pin) (void)hipHostFree(g.pin);
+        g.pin = nullptr;
+        g.pin_bytes = 0;
+        HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&g.pin), bytes, hipHostMallocDefault));
+        g.pin_bytes = bytes;
+    }
+    return g.pin;
+}
+float *dev_scratch(float *&p, size_t &cap, size_t bytes) {
+    if (cap < bytes) {
+        dfree(p);
+        p = nullptr;
+        cap = 0;
+        p = static_cast<float *>(dalloc(bytes));
+        cap = bytes;
+    }
+    return p;
+}
+
+void h2d(void *dst, const void *src, size_t bytes) {
+    if (!bytes) return;
+    HIPCHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+}
+
+void require_ok() {
+    if (!g.ok) throw Fail(g.init_error.empty() ? "HIP backend is not initialised (voxhip_init)" : g.init_error);
+}
+GpuMat &mat_at(int id) {
+    if (id < 0 || size_t(id) >= g.mats.size() || !g.mats[size_t(id)].w) throw Fail("bad matrix handle " + std::to_string(id));
+    return g.mats[size_t(id)];
+}
+Xfmr &xf_at(int id) {
+    if (id < 0 || size_t(id) >= g.xf.size() || !g.xf[size_t(id)]) throw Fail("bad transformer handle " + std::to_string(id));
+    return *g.xf[size_t(id)];
+}
+Seq &seq_at(int id) {
+    if (id < 0 || size_t(id) >= g.seqs.size() || !g.seqs[size_t(id)].k) throw Fail("bad sequence handle " + std::to_string(id));
+    return g.seqs[size_t(id)];
+}
+
+size_t row_bytes(int32_t type, int64_t cols) {
+    return type == VOXHIP_F32 ? size_t(cols) * 4 : type == VOXHIP_Q8 ? size_t(cols) : type == VOXHIP_Q4 ? size_t(cols) / 2
+                                                                                                         : size_t(cols) * 2;
+}
+bool quantized(int32_t t) { return t == VOXHIP_Q8 || t == VOXHIP_Q4; }
+
+// Checks the shape rules of the GEMV kernels: Q8/Q4 need cols % 32 (as kernels.cpp:655); the f32 path
+// reads 16-byte chunks, so F32 needs cols % 4 and F16/BF16 cols % 8.
+void check_shape(int32_t type, int64_t rows, int64_t cols) {
+    if (type < VOXHIP_F32 || type > VOXHIP_Q4) throw Fail("unknown weight type " + std::to_string(type));
+    if (rows <= 0 || cols <= 0 || rows > (int64_t(1) << 30)) throw Fail("bad matrix shape");
+    if (quantized(type) && cols % 32) throw Fail("Q8/Q4 matrix needs cols % 32 == 0");
+    if (type == VOXHIP_F32 && cols % 4) throw Fail("F32 matrix needs cols % 4 == 0 on this backend");
+    if ((type == VOXHIP_F16 || type == VOXHIP_BF16) && cols % 8) throw Fail("F16/BF16 matrix needs cols % 8 == 0 on this backend");
+}
+
+int new_mat(int32_t type, int64_t rows, int64_t cols, bool bias) {
+    GpuMat m;
+    m.type = type; m.rows = rows; m.cols = cols;
+    const size_t wb = size_t(rows) * row_bytes(type, cols);
+    m.w = static_cast<uint8_t *>(dalloc(wb));
+    m.bytes = wb;
+    if (quantized(type)) {
+        m.s = dalloc_t<float>(size_t(rows) * size_t(cols / 32));
+        m.bytes += size_t(rows) * size_t(cols / 32) * 4;
+    }
+    if (bias) { m.b = dalloc_t<float>(size_t(rows)); m.bytes += size_t(rows) * 4; }
+    g.mats.push_back(m);
+    return int(g.mats.size()) - 1;
+}
+void free_mat(int id) {
+    if (id < 0 || size_t(id) >= g.mats.size()) return;
+    GpuMat &m = g.mats[size_t(id)];
+    dfree(m.w); dfree(m.s); dfree(m.b);
+    m = GpuMat();
+}
+
+// Stacks the parts' rows into one device matrix. interleave2: two parts of equal rows stored as row pairs
+// (part0 row r, part1 row r) — the gate|up layout of the SwiGLU epilogue.
+int upload_parts(const voxhip_mat *parts, int n, bool interleave2) {
+    if (n <= 0) throw Fail("no matrix parts");
+    const voxhip_mat &P0 = parts[0];
+    int64_t rows = 0;
+    bool any_bias = false, all_bias = true;
+    for (int i = 0; i < n; ++i) {
+        const voxhip_mat &p = parts[i];
+        if (p.type != P0.type || p.cols != P0.cols || !p.data) throw Fail("matrix parts differ in type/width or lack data");
+        if (quantized(p.type) && !p.scale) throw Fail("quantized matrix without scales");
+        rows += p.rows;
+        any_bias = any_bias || p.bias;
+        all_bias = all_bias && p.bias;
+    }
+    if (any_bias && !all_bias) throw Fail("bias on some stacked parts only");
+    if (interleave2 && (n != 2 || parts[0].rows != parts[1].rows)) throw Fail("interleave needs two equal parts");
+    check_shape(P0.type, rows, P0.cols);
+    const int id = new_mat(P0.type, rows, P0.cols, all_bias);
+    GpuMat &m = g.mats[size_t(id)];
+    const size_t rb = row_bytes(P0.type, P0.cols), sb = quantized(P0.type) ? size_t(P0.cols / 32) * 4 : 0;
+    if (!interleave2) {
+        int64_t r0 = 0;
+        for (int i = 0; i < n; ++i) {
+            const voxhip_mat &p = parts[i];
+            h2d(m.w + size_t(r0) * rb, p.data, size_t(p.rows) * rb);
+            if (sb) h2d(reinterpret_cast<uint8_t *>(m.s) + size_t(r0) * sb, p.scale, size_t(p.rows) * sb);
+            if (all_bias) h2d(m.b + r0, p.bias, size_t(p.rows) * 4);
+            r0 += p.rows;
+        }
+    } else {
+        const int64_t R = parts[0].rows;
+        std::vector<uint8_t> tw(size_t(rows) * rb), ts(size_t(rows) * sb);
+        std::vector<float> tb(all_bias ? size_t(rows) : 0);
+        for (int64_t r = 0; r < R; ++r)
+            for (int i = 0; i < 2; ++i) {
+                const voxhip_mat &p = parts[i];
+                std::memcpy(&tw[size_t(2 * r + i) * rb], static_cast<const uint8_t *>(p.data) + size_t(r) * rb, rb);
+                if (sb) std::memcpy(&ts[size_t(2 * r + i) * sb], reinterpret_cast<const uint8_t *>(p.scale) + size_t(r) * sb, sb);
+                if (all_bias) tb[size_t(2 * r + i)] = p.bias[r];
+            }
+        h2d(m.w, tw.data(), tw.size());
+        if (sb) h2d(m.s, ts.data(), ts.size());
+        if (all_bias) h2d(m.b, tb.data(), tb.size() * 4);
+    }
+    g.stats.mats_ok += n;
+    g.stats.bytes += m.bytes;
+    return id;
+}
+
+// ------------------------------------------------------------------ GEMV launch helpers
+// int8 activations for Q8 when the call's row count is <= 8 (kernels.cpp:647, :660) and always for Q4.
+bool int_path(const GpuMat &m, int64_t m_total) {
+    return m.type == VOXHIP_Q4 || (m.type == VOXHIP_Q8 && m_total <= kMaxM);
+}
+int rows_per_pass(const GpuMat &m, int64_t m_total) { return int_path(m, m_total) ? kMaxM : 4; }
+
+void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, int64_t ldx, int mc, float *y, int64_t ldy,
+          const float *gamma, float eps, float *xnorm, hipStream_t s) {
+    GemvArgs a;
+    a.w = m.w; a.scale = m.s; a.bias = m.b; a.x = x; a.gamma = gamma; a.y = y; a.xnorm = xnorm;
+    a.ldx = ldx; a.ldy = ldy; a.rows = int32_t(m.rows); a.K = int32_t(m.cols); a.m = mc; a.eps = eps;
+    HIPCHECK(launch_gemv(m.type, int_path(m, m_total), pro, epi, a, s));
+}
+
+// ------------------------------------------------------------------ transformer
+void ensure_rope(Xfmr &X, int64_t rows) {
+    if (X.rope_rows >= rows) return;
+    const int64_t half = X.hd / 2;
+    std::vector<float> t(size_t(rows) * size_t(half) * 2);
+    for (int64_t pos = 0; pos < rows; ++pos)
+        for (int64_t p = 0; p < half; ++p) {
+            const float f = X.inv_freq[size_t(p)] * float(pos);  // as rope_apply (kernels.cpp:744-747)
+            t[size_t((pos * half + p) * 2)] = std::cos(f);
+            t[size_t((pos * half + p) * 2 + 1)] = std::sin(f);
+        }
+    float *nr = dalloc_t<float>(t.size());
+    h2d(nr, t.data(), t.size() * 4);
+    HIPCHECK(hipStreamSynchronize(g.stream));
+    dfree(X.rope);
+    X.rope = nr;
+    X.rope_rows = rows;
+    for (auto &kv : X.graphs) (void)hipGraphExecDestroy(kv.second);  // graphs captured the old table address
+    X.graphs.clear();
+}
+
+void alloc_scratch(Xfmr &X) {
+    const size_t M = kMaxM, qd = size_t(X.heads) * X.hd, kd = size_t(X.kvh) * X.hd;
+    X.h = dalloc_t<float>(M * X.H);
+    X.qkv = dalloc_t<float>(M * (qd + 2 * kd));
+    X.q = dalloc_t<float>(M * qd);
+    X.ao = dalloc_t<float>(M * qd);
+    X.g = dalloc_t<float>(M * X.I);
+    X.xnorm = dalloc_t<float>(M * X.H);
+    X.pm = dalloc_t<float>(M * X.heads * kAttnSplits);
+    X.pl = dalloc_t<float>(M * X.heads * kAttnSplits);
+    X.po = dalloc_t<float>(M * X.heads * kAttnSplits * X.hd);
+    X.rows_dev = dalloc_t<RowRef>(M);
+    HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&X.rows_host), M * sizeof(RowRef), hipHostMallocDefault));
+    X.scfg_dev = dalloc_t<SampleCfgDev>(1);
+    HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&X.scfg_host), sizeof(SampleCfgDev), hipHostMallocDefault));
+    X.token_dev = dalloc_t<int32_t>(M);
+}
+
+float *ensure_logits(Xfmr &X, int64_t rows) {
+    if (X.logits_cap < rows) {
+        dfree(X.logits);
+        X.logits = dalloc_t<float>(size_t(kMaxM) * size_t(rows));
+        X.logits_cap = rows;
+        for (auto &kv : X.graphs) (void)hipGraphExecDestroy(kv.second);
+        X.graphs.clear();
+    }
+    return X.logits;
+}
+float *ensure_xin(Xfmr &X, int64_t cols) {
+    if (X.xin_cols < cols) {
+        dfree(X.xin);
+        X.xin = dalloc_t<float>(size_t(kMaxM) * size_t(cols));
+        X.xin_cols = cols;
+    }
+    return X.xin;
+}
+
+// Uploads the per-row cache views (positions) of the next pass; skips the copy when unchanged.
+void set_rows(Xfmr &X, const std::vector<RowRef> &rows) {
+    if (X.rows_valid && rows.size() == X.rows_last.size() &&
+        std::memcmp(rows.data(), X.rows_last.data(), rows.size() * sizeof(RowRef)) == 0)
+        return;
+    HIPCHECK(hipStreamSynchronize(g.stream));  // the pinned block may still feed an earlier copy
+    std::memcpy(X.rows_host, rows.data(), rows.size() * sizeof(RowRef));
+    HIPCHECK(hipMemcpyAsync(X.rows_dev, X.rows_host, rows.size() * sizeof(RowRef), hipMemcpyHostToDevice, g.stream));
+    X.rows_last = rows;
+    X.rows_valid = true;
+}
+
+// All layers for mc rows whose input is in X.h (row i at the position in rows_dev[i]).
+// m_total: the caller's total row count, which picks the q8 arithmetic (int8 for <= 8, f32 above).
+void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int n_layers, hipStream_t s) {
+    const int qd = X.heads * X.hd, kd = X.kvh * X.hd, ldqkv = qd + 2 * kd;
+    for (int li = 0; li < n_layers; ++li) {
+        const LayerDev &L = X.L[size_t(li)];
+        const GpuMat &Mqkv = g.mats[size_t(L.qkv)], &Mo = g.mats[size_t(L.o)], &Mgu = g.mats[size_t(L.gu)],
+                     &Md = g.mats[size_t(L.down)];
+        gemv(Mqkv, m_total, PRO_RMS, EPI_STORE, X.h, X.H, mc, X.qkv, ldqkv, X.norms + L.ln1, X.eps, nullptr, s);
+        QkArgs qa;
+        qa.qkv = X.qkv; qa.ldqkv = ldqkv; qa.q = X.q; qa.rows = X.rows_dev;
+        qa.qn = L.qk ? X.norms + L.qn : nullptr; qa.kn = L.qk ? X.norms + L.kn : nullptr;
+        qa.rope = X.rope; qa.heads = X.heads; qa.kv_heads = X.kvh; qa.hd = X.hd; qa.layer = li; qa.eps = X.eps;
+        HIPCHECK(launch_qk_post(qa, mc, s));
+        AttnArgs aa;
+        aa.q = X.q; aa.rows = X.rows_dev; aa.pm = X.pm; aa.pl = X.pl; aa.po = X.po; aa.out = X.ao;
+        aa.heads = X.heads; aa.kv_heads = X.kvh; aa.layer = li; aa.scale = 1.0f / std::sqrt(float(X.hd));
+        HIPCHECK(launch_attention(aa, X.hd, X.heads / X.kvh, mc, s));
+        gemv(Mo, m_total, PRO_X, EPI_ACC, X.ao, qd, mc, X.h, X.H, nullptr, 0.f, nullptr, s);
+        gemv(Mgu, m_total, PRO_RMS, EPI_SWIGLU, X.h, X.H, mc, X.g, X.I, X.norms + L.ln2, X.eps, nullptr, s);
+        gemv(Md, m_total, PRO_X, EPI_ACC, X.g, X.I, mc, X.h, X.H, nullptr, 0.f, nullptr, s);
+    }
+}
+
+// Final RMSNorm of rows [r0, r0 + mr) of X.h into X.xnorm, and the head on them when head >= 0.
+void enqueue_final(Xfmr &X, int r0, int mr, int head, hipStream_t s) {
+    if (head >= 0) {
+        const GpuMat &Hm = mat_at(head);
+        if (Hm.cols != X.H) throw Fail("head width differs from the hidden size");
+        float *lg = ensure_logits(X, Hm.rows);
+        gemv(Hm, mr, PRO_RMS, EPI_STORE, X.h + size_t(r0) * X.H, X.H, mr, lg, Hm.rows, X.norms + X.final_off, X.eps,
+             X.xnorm, s);
+    } else {
+        HIPCHECK(launch_rmsnorm_rows(X.h + size_t(r0) * X.H, X.H, X.norms + X.final_off, X.H, X.eps, X.xnorm, X.H, mr, s));
+    }
+}
+
+RowRef row_of(const Seq &S, int64_t pos) {
+    RowRef r;
+    r.k = S.k; r.v = S.v; r.cap = S.cap; r.pos = pos;
+    return r;
+}
+
+void check_seq_for(Xfmr &X, int xid, const Seq &S) {
+    if (S.xfmr != xid && (S.layers < X.layers || S.kvh != X.kvh || S.hd != X.hd)) throw Fail("sequence belongs to another transformer shape");
+    ensure_rope(X, S.cap);  // the RoPE table must cover every position the sequence can hold
+}
+
+// Generic host-pointer forward for up to any m rows of one sequence (or B rows of B sequences).
+// rows_of(i) gives the cache view of row i. x rows are xc wide (in_proj cols or hidden).
+template <class RowsOf>
+void forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_proj, int n_layers, int64_t m_total,
+                  float *hidden_out, float *out_last, int head, float *head_out, bool final_all) {
+    const int64_t H = X.H;
+    const GpuMat *Pm = in_proj >= 0 ? &mat_at(in_proj) : nullptr;
+    if (Pm && Pm->rows != H) throw Fail("in_proj rows differ from the hidden size");
+    const int64_t xc = Pm ? Pm->cols : H;
+    // rows per pass: the smallest of the passes the used matrices allow (f32 path holds 4 rows in LDS)
+    int chunk = kMaxM;
+    for (int li = 0; li < n_layers; ++li)
+        for (int id : {X.L[size_t(li)].qkv, X.L[size_t(li)].o, X.L[size_t(li)].gu, X.L[size_t(li)].down})
+            chunk = std::min(chunk, rows_per_pass(g.mats[size_t(id)], m_total));
+    if (Pm) chunk = std::min(chunk, rows_per_pass(*Pm, m_total));
+    if (head >= 0 && final_all) chunk = std::min(chunk, rows_per_pass(mat_at(head), m_total));
+    const int64_t V = head >= 0 ? mat_at(head).rows : 0;
+    float *pin = pinned(size_t(kMaxM) * size_t(std::max<int64_t>(std::max(xc, H), V)) * 4 + 64);
+    for (int64_t c0 = 0; c0 < m; c0 += chunk) {
+        const int mc = int(std::min<int64_t>(chunk, m - c0));
+        const bool last = c0 + mc == m;
+        std::vector<RowRef> rr(static_cast<size_t>(mc));
+        for (int i = 0; i < mc; ++i) rr[size_t(i)] = rows_of(c0 + i);
+        set_rows(X, rr);
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        std::memcpy(pin, x + c0 * xc, size_t(mc * xc) * 4);
+        if (Pm) {
+            float *xin = ensure_xin(X, xc);
+            HIPCHECK(hipMemcpyAsync(xin, pin, size_t(mc * xc) * 4, hipMemcpyHostToDevice, g.stream));
+            gemv(*Pm, m_total, PRO_X, EPI_STORE, xin, xc, mc, X.h, H, nullptr, 0.f, nullptr, g.stream);
+        } else {
+            HIPCHECK(hipMemcpyAsync(X.h, pin, size_t(mc * H) * 4, hipMemcpyHostToDevice, g.stream));
+        }
+        enqueue_layers(X, mc, m_total, n_layers, g.stream);
+        if (hidden_out) {
+            HIPCHECK(hipMemcpyAsync(pin, X.h, size_t(mc * H) * 4, hipMemcpyDeviceToHost, g.stream));
+            HIPCHECK(hipStreamSynchronize(g.stream));
+            std::memcpy(hidden_out + c0 * H, pin, size_t(mc * H) * 4);
+        }
+        if (final_all || last) {
+            const int r0 = final_all ? 0 : mc - 1, mr = final_all ? mc : 1;
+            if (out_last || head >= 0) {
+                enqueue_final(X, r0, mr, head, g.stream);
+                if (out_last) {
+                    HIPCHECK(hipMemcpyAsync(pin, X.xnorm, size_t(mr * H) * 4, hipMemcpyDeviceToHost, g.stream));
+                    HIPCHECK(hipStreamSynchronize(g.stream));
+                    std::memcpy(out_last + (final_all ? c0 * H : 0), pin, size_t(mr * H) * 4);
+                }
+                if (head >= 0 && head_out) {
+                    HIPCHECK(hipMemcpyAsync(pin, X.logits, size_t(mr * V) * 4, hipMemcpyDeviceToHost, g.stream));
+                    HIPCHECK(hipStreamSynchronize(g.stream));
+                    std::memcpy(head_out + (final_all ? c0 * V : 0), pin, size_t(mr * V) * 4);
+                }
+            }
+        }
+    }
+    HIPCHECK(hipStreamSynchronize(g.stream));
+}
+
+void fill_sample_cfg(SampleCfgDev &d, const voxhip_sample_cfg &c, const int32_t *hist_dev, int32_t n_hist) {
+    d.temperature = c.temperature; d.top_p = c.top_p; d.rep = c.repetition_penalty; d.top_k = c.top_k;
+    d.key0 = c.key0; d.key1 = c.key1; d.frame = c.frame; d.cb = c.codebook; d.draw = c.draw;
+    d.sup_from = c.suppress_from; d.sup_to = c.suppress_to; d.eos = c.eos_code; d.block_eos = c.block_eos;
+    d.n_history = n_hist; d.history = hist_dev;
+}
+
+template <class F>
+int guard_int(F &&f, int fail) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    try {
+        return f();
+    } catch (const std::exception &e) {
+        set_error(e.what());
+        return fail;
+    }
+}
+
+const char *kWhich[7] = {"q", "k", "v", "o", "gate", "up", "down"};
+
+int make_xfmr(const voxhip_xfmr_desc *w, const char *name, int use_layers, const int32_t *mats, voxhip_uploaded_fn uploaded,
+              void *user) {
+    require_ok();
+    if (!w || w->n_layers <= 0 || !w->layers || !w->final_norm || !w->inv_freq) throw Fail("incomplete transformer description");
+    if (w->window != 0) throw Fail("sliding-window attention is not supported on the device");
+    if (w->head_dim != 64 && w->head_dim != 128) throw Fail("head_dim must be 64 or 128 on this backend");
+    if (w->heads <= 0 || w->kv_heads <= 0 || w->heads % w->kv_heads || w->heads / w->kv_heads > 8)
+        throw Fail("heads / kv_heads must be an integer group of at most 8");
+    if (w->hidden % 32 || w->inter % 32) throw Fail("hidden and inter must be multiples of 32");
+    const int nl = use_layers < 0 || use_layers > w->n_layers ? w->n_layers : use_layers;
+    auto X = new Xfmr();
+    try {
+        X->name = name ? name : "xfmr";
+        X->layers = nl; X->H = w->hidden; X->heads = w->heads; X->kvh = w->kv_heads; X->hd = w->head_dim; X->I = w->inter;
+        X->eps = w->eps; X->theta = w->theta;
+        X->inv_freq.assign(w->inv_freq, w->inv_freq + w->head_dim / 2);
+        std::vector<float> nv;
+        auto push = [&](const float *p, int n) {
+            const size_t off = nv.size();
+            nv.insert(nv.end(), p, p + n);
+            return off;
+        };
+        for (int li = 0; li < nl; ++li) {
+            const voxhip_layer &L = w->layers[li];
+            if (L.attn_scale || L.mlp_scale) throw Fail("layer scales are not supported on the device");
+            if (!L.ln1 || !L.ln2) throw Fail("layer without norms");
+            if ((L.qn == nullptr) != (L.kn == nullptr)) throw Fail("q_norm and k_norm must both be present or absent");
+            LayerDev d;
+            if (mats) {
+                const int32_t *h = mats + 7 * li;
+                for (int j = 0; j < 7; ++j) mat_at(h[j]);
+                auto desc_of = [&](int id) {
+                    const GpuMat &m = g.mats[size_t(id)];
+                    return std::make_tuple(m.type, m.cols);
+                };
+                if (desc_of(h[0]) != desc_of(h[1]) || desc_of(h[0]) != desc_of(h[2]) || desc_of(h[4]) != desc_of(h[5]))
+                    throw Fail("stacked matrices differ in type or width");
+                // stack / interleave on the device
+                auto stack = [&](std::initializer_list<int> ids, bool inter) {
+                    const GpuMat &m0 = g.mats[size_t(*ids.begin())];
+                    int64_t rows = 0;
+                    bool bias = true;
+                    for (int id : ids) { rows += g.mats[size_t(id)].rows; bias = bias && g.mats[size_t(id)].b; }
+                    const int nid = new_mat(m0.type, rows, m0.cols, bias);
+                    const size_t rb = row_bytes(m0.type, m0.cols), sb = quantized(m0.type) ? size_t(m0.cols / 32) * 4 : 0;
+                    int64_t r0 = 0;
+                    int part = 0;
+                    for (int id : ids) {
+                        const GpuMat src = g.mats[size_t(id)];
+                        GpuMat &dst = g.mats[size_t(nid)];
+                        if (!inter) {
+                            HIPCHECK(hipMemcpy(dst.w + size_t(r0) * rb, src.w, size_t(src.rows) * rb, hipMemcpyDeviceToDevice));
+                            if (sb) HIPCHECK(hipMemcpy(reinterpret_cast<uint8_t *>(dst.s) + size_t(r0) * sb, src.s, size_t(src.rows) * sb, hipMemcpyDeviceToDevice));
+                            if (bias) HIPCHECK(hipMemcpy(dst.b + r0, src.b, size_t(src.rows) * 4, hipMemcpyDeviceToDevice));
+                        } else {
+                            HIPCHECK(hipMemcpy2D(dst.w + size_t(part) * rb, 2 * rb, src.w, rb, rb, size_t(src.rows), hipMemcpyDeviceToDevice));
+                            if (sb) HIPCHECK(hipMemcpy2D(reinterpret_cast<uint8_t *>(dst.s) + size_t(part) * sb, 2 * sb, src.s, sb, sb, size_t(src.rows), hipMemcpyDeviceToDevice));
+                            if (bias) HIPCHECK(hipMemcpy2D(dst.b + part, 8, src.b, 4, 4, size_t(src.rows), hipMemcpyDeviceToDevice));
+                        }
+                        r0 += src.rows;
+                        ++part;
+                    }
+                    return nid;
+                };
+                d.qkv = stack({h[0], h[1], h[2]}, false);
+                d.o = stack({h[3]}, false);
+                d.gu = stack({h[4], h[5]}, true);
+                d.down = stack({h[6]}, false);
+            } else {
+                const voxhip_mat qkv[3] = {L.q, L.k, L.v}, gu[2] = {L.gate, L.up};
+                d.qkv = upload_parts(qkv, 3, false);
+                d.o = upload_parts(&L.o, 1, false);
+                d.gu = upload_parts(gu, 2, true);
+                d.down = upload_parts(&L.down, 1, false);
+                if (uploaded)
+                    for (int j = 0; j < 7; ++j) uploaded(user, li, j);
+            }
+            const GpuMat &Q = g.mats[size_t(d.qkv)], &O = g.mats[size_t(d.o)], &GU = g.mats[size_t(d.gu)], &D = g.mats[size_t(d.down)];
+            const int64_t qd = int64_t(w->heads) * w->head_dim, kd = int64_t(w->kv_heads) * w->head_dim;
+            if (Q.rows != qd + 2 * kd || Q.cols != w->hidden || O.rows != w->hidden || O.cols != qd || GU.rows != 2 * int64_t(w->inter) ||
+                GU.cols != w->hidden || D.rows != w->hidden || D.cols != w->inter)
+                throw Fail("layer matrix shapes do not match the transformer description");
+            d.ln1 = push(L.ln1, w->hidden);
+            d.ln2 = push(L.ln2, w->hidden);
+            d.qk = L.qn && L.kn;
+            if (d.qk) { d.qn = push(L.qn, w->head_dim); d.kn = push(L.kn, w->head_dim); }
+            X->L.push_back(d);
+        }
+        X->final_off = push(w->final_norm, w->hidden);
+        X->norms = dalloc_t<float>(nv.size());
+        h2d(X->norms, nv.data(), nv.size() * 4);
+        alloc_scratch(*X);
+        ensure_rope(*X, 4096);
+    } catch (...) {
+        delete X;
+        throw;
+    }
+    g.xf.push_back(X);
+    return int(g.xf.size()) - 1;
+}
+
+int parse_index(const char *spec) {
+    int idx = 0;
+    if (spec) {
+        const char *c = std::strchr(spec, ':');
+        if (c) idx = std::atoi(c + 1);
+    }
+    if (const char *e = std::getenv("VOX_VK_DEVICE")) idx = std::atoi(e);
+    if (const char *e = std::getenv("VOX_HIP_DEVICE")) idx = std::atoi(e);
+    return idx;
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+extern "C" {
+
+int voxhip_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+int voxhip_device_info_get(int index, voxhip_device_info *out) {
+    if (!out) return 0;
+    std::memset(out, 0, sizeof *out);
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, index) != hipSuccess) return 0;
+    out->index = index;
+    std::snprintf(out->name, sizeof out->name, "%s (%s)", p.name, p.gcnArchName);
+    std::snprintf(out->type, sizeof out->type, "%s", p.integrated ? "integrated" : "discrete");
+    out->software = 0;
+    out->unified_memory = p.integrated ? 1 : 0;
+    out->vram_total = p.totalGlobalMem;
+    out->vram_free = p.totalGlobalMem;
+    int cur = -1;
+    if (hipGetDevice(&cur) == hipSuccess && cur == index) {
+        size_t f = 0, t = 0;
+        if (hipMemGetInfo(&f, &t) == hipSuccess) out->vram_free = f;
+    }
+    out->max_storage_range = p.totalGlobalMem;
+    out->subgroup_arith = 1;
+    out->coop_matrix = 1;  // MFMA
+    out->memory_budget = 1;
+    out->api_version = uint32_t(p.major * 100 + p.minor);
+    out->vendor_id = 0x1002;
+    int rt = 0;
+    (void)hipRuntimeGetVersion(&rt);
+    out->driver_version = uint32_t(rt);
+    return 1;
+}
+
+int voxhip_init(const char *device, char *err, size_t err_len) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    auto put_err = [&](const std::string &m) {
+        if (err && err_len) { std::snprintf(err, err_len, "%s", m.c_str()); }
+    };
+    if (g.ok) return 1;
+    if (!g.init_error.empty()) { put_err(g.init_error); return 0; }
+    try {
+        const int idx = parse_index(device);
+        int n = 0;
+        HIPCHECK(hipGetDeviceCount(&n));
+        if (idx < 0 || idx >= n) throw Fail("HIP device " + std::to_string(idx) + " not found (" + std::to_string(n) + " present)");
+        HIPCHECK(hipSetDevice(idx));
+        hipDeviceProp_t p;
+        HIPCHECK(hipGetDeviceProperties(&p, idx));
+        if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
+            throw Fail(std::string("device is ") + p.gcnArchName + "; this backend is built for gfx950 (MI355X)");
+        HIPCHECK(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
+        g.dev = idx;
+        g.name = std::string(p.name) + " (" + p.gcnArchName + ")";
+        g.ok = true;
+        return 1;
+    } catch (const std::exception &e) {
+        g.init_error = std::string("HIP init failed: ") + e.what();
+        put_err(g.init_error);
+        return 0;
+    }
+}
+
+int voxhip_active(void) { return g.ok ? 1 : 0; }
+const char *voxhip_device_name(void) { return g.name.c_str(); }
+void voxhip_stats_get(voxhip_stats *out) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (out) *out = g.stats;
+}
+const char *voxhip_last_error(void) { return g.last_error.c_str(); }
+void voxhip_set_vram_limit(uint64_t bytes) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    g.vram_limit = bytes;
+}
+void voxhip_mem_info_get(voxhip_mem_info *out) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!out) return;
+    std::memset(out, 0, sizeof *out);
+    out->device_index = -1;
+    if (!g.ok) return;
+    out->used = g.vram_used;
+    out->limit = g.vram_limit;
+    out->device_index = g.dev;
+    size_t f = 0, t = 0;
+    if (hipMemGetInfo(&f, &t) == hipSuccess) { out->device_free = f; out->device_total = t; }
+}
+
+int voxhip_upload(const voxhip_mat *parts, int n_parts) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    uint64_t bytes = 0;
+    try {
+        require_ok();
+        if (!parts || n_parts <= 0) throw Fail("no matrix");
+        for (int i = 0; i < n_parts; ++i) bytes += uint64_t(parts[i].rows) * row_bytes(parts[i].type, parts[i].cols);
+        return upload_parts(parts, n_parts, false);
+    } catch (const std::exception &e) {
+        g.stats.mats_failed += n_parts > 0 ? n_parts : 0;
+        g.stats.bytes_failed += bytes;
+        set_error(e.what());
+        if (!g.warned) { std::fprintf(stderr, "vox: GPU upload failed (%s); some weights will stay on CPU\n", e.what()); g.warned = true; }
+        return -1;
+    }
+}
+
+int voxhip_mat_shape(int mat, int64_t *rows, int64_t *cols) {
+    return guard_int([&] {
+        const GpuMat &m = mat_at(mat);
+        if (rows) *rows = m.rows;
+        if (cols) *cols = m.cols;
+        return 1;
+    }, 0);
+}
+
+int voxhip_matmul(int mat, const float *x, int64_t m, float *y) {
+    return guard_int([&] {
+        require_ok();
+        const GpuMat &M = mat_at(mat);
+        if (m <= 0) return 1;
+        const int chunk = rows_per_pass(M, m);
+        const size_t xb = size_t(chunk) * size_t(M.cols) * 4, yb = size_t(chunk) * size_t(M.rows) * 4;
+        float *pin = pinned(std::max(xb, yb) + 64);
+        float *dx = dev_scratch(g.dbuf_x, g.dbuf_x_bytes, xb), *dy = dev_scratch(g.dbuf_y, g.dbuf_y_bytes, yb);
+        for (int64_t c0 = 0; c0 < m; c0 += chunk) {
+            const int mc = int(std::min<int64_t>(chunk, m - c0));
+            std::memcpy(pin, x + c0 * M.cols, size_t(mc) * size_t(M.cols) * 4);
+            HIPCHECK(hipMemcpyAsync(dx, pin, size_t(mc) * size_t(M.cols) * 4, hipMemcpyHostToDevice, g.stream));
+            gemv(M, m, PRO_X, EPI_STORE, dx, M.cols, mc, dy, M.rows, nullptr, 0.f, nullptr, g.stream);
+            HIPCHECK(hipMemcpyAsync(pin, dy, size_t(mc) * size_t(M.rows) * 4, hipMemcpyDeviceToHost, g.stream));
+            HIPCHECK(hipStreamSynchronize(g.stream));
+            std::memcpy(y + c0 * M.rows, pin, size_t(mc) * size_t(M.rows) * 4);
+        }
+        return 1;
+    }, 0);
+}
+
+int voxhip_xfmr_create(const voxhip_xfmr_desc *w, const char *name, int n_layers, voxhip_uploaded_fn uploaded, void *user) {
+    return guard_int([&] { return make_xfmr(w, name, n_layers, nullptr, uploaded, user); }, -1);
+}
+
+int voxhip_xfmr_create_from_mats(const voxhip_xfmr_desc *w, const int32_t *mats, const char *name) {
+    return guard_int([&] {
+        if (!mats) throw Fail("no matrix handles");
+        return make_xfmr(w, name, -1, mats, nullptr, nullptr);
+    }, -1);
+}
+
+int voxhip_seq_create(int xfmr, int64_t capacity) {
+    return guard_int([&] {
+        require_ok();
+        Xfmr &X = xf_at(xfmr);
+        if (capacity <= 0 || capacity > kMaxCap) throw Fail("sequence capacity out of range");
+        for (size_t i = 0; i < g.seqs.size(); ++i) {
+            Seq &S = g.seqs[i];
+            if (S.k && !S.used && S.layers == X.layers && S.kvh == X.kvh && S.hd == X.hd && S.cap >= capacity) {
+                S.used = true;
+                S.xfmr = xfmr;
+                ensure_rope(X, S.cap);
+                return int(i);
+            }
+        }
+        Seq S;
+        S.xfmr = xfmr; S.cap = capacity; S.layers = X.layers; S.kvh = X.kvh; S.hd = X.hd;
+        const size_t n = size_t(X.layers) * size_t(X.kvh) * size_t(capacity) * size_t(X.hd);
+        S.k = dalloc_t<_Float16>(n);
+        try {
+            S.v = dalloc_t<_Float16>(n);
+        } catch (...) {
+            dfree(S.k);
+            throw;
+        }
+        HIPCHECK(hipMemset(S.k, 0, n * 2));
+        HIPCHECK(hipMemset(S.v, 0, n * 2));
+        S.used = true;
+        ensure_rope(X, capacity);
+        g.seqs.push_back(S);
+        return int(g.seqs.size()) - 1;
+    }, -1);
+}
+
+void voxhip_seq_free(int seq) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (seq >= 0 && size_t(seq) < g.seqs.size()) g.seqs[size_t(seq)].used = false;  // buffers stay pooled
+}
+
+int voxhip_xfmr_forward(int xfmr, int seq, int64_t pos0, const float *x, int64_t m, float *out_last, int in_proj, int head,
+                        float *head_out) {
+    return guard_int([&] {
+        require_ok();
+        Xfmr &X = xf_at(xfmr);
+        Seq &S = seq_at(seq);
+        check_seq_for(X, xfmr, S);
+        if (m <= 0) return 1;
+        if (pos0 < 0 || pos0 + m > S.cap) throw Fail("context exceeds GPU KV capacity");
+        forward_rows(X, m, [&](int64_t i) { return row_of(S, pos0 + i); }, x, in_proj, X.layers, m, nullptr, out_last, head,
+                     head_out, false);
+        return 1;
+    }, 0);
+}
+
+int voxhip_xfmr_forward_hidden(int xfmr, int seq, int64_t pos0, const float *x, int64_t m, float *hidden_out) {
+    return guard_int([&] {
+        require_ok();
+        Xfmr &X = xf_at(xfmr);
+        Seq &S = seq_at(seq);
+        check_seq_for(X, xfmr, S);
+        if (m <= 0) return 1;
+        if (pos0 < 0 || pos0 + m > S.cap) throw Fail("context exceeds GPU KV capacity");
+        forward_rows(X, m, [&](int64_t i) { return row_of(S, pos0 + i); }, x, -1, X.layers, m, hidden_out, nullptr, -1,
+                     nullptr, false);
+        return 1;
+    }, 0);
+}
+
+int voxhip_xfmr_forward_pair(int xfmr, int seq0, int seq1, int64_t pos, const float *x2, int head, float *out2,
+                             float *head_out2) {
+    return guard_int([&] {
+        require_ok();
+        Xfmr &X = xf_at(xfmr);
+        if (seq0 == seq1) throw Fail("pair needs two sequences");
+        Seq &S0 = seq_at(seq0), &S1 = seq_at(seq1);
+        check_seq_for(X, xfmr, S0);
+        check_seq_for(X, xfmr, S1);
+        if (pos < 0 || pos + 1 > S0.cap || pos + 1 > S1.cap) throw Fail("context exceeds GPU KV capacity");
+        forward_rows(X, 2, [&](int64_t i) { return row_of(i == 0 ? S0 : S1, pos); }, x2, -1, X.layers, 2, nullptr, out2, head,
+                     head_out2, true);
+        return 1;
+    }, 0);
+}
+
+int voxhip_xfmr_forward_steps(int xfmr, const int32_t *seqs, const int64_t *pos, int64_t B, const float *x, float *out, int head,
+                              float *head_out) {
+    return guard_int([&] {
+        require_ok();
+        Xfmr &X = xf_at(xfmr);
+        if (B <= 0) return 1;
+        if (B > kMaxM) throw Fail("at most 8 sequences per step");
+        for (int64_t b = 0; b < B; ++b) {
+            Seq &S = seq_at(seqs[b]);
+            check_seq_for(X, xfmr, S);
+            if (pos[b] < 0 || pos[b] + 1 > S.cap) throw Fail("context exceeds GPU KV capacity");
+            for (int64_t c = 0; c < b; ++c)
+                if (seqs[c] == seqs[b]) throw Fail("a sequence appears twice in one step");
+        }
+        forward_rows(X, B, [&](int64_t i) { return row_of(g.seqs[size_t(seqs[i])], pos[i]); }, x, -1, X.layers, B, nullptr, out,
+                     head, head_out, true);
+        return 1;
+    }, 0);
+}
+
+int voxhip_sample_logits(const float *logits, int32_t n, const voxhip_sample_cfg *cfg, const int32_t *history, int32_t n_history,
+                         int32_t *out_id) {
+    return guard_int([&] {
+        require_ok();
+        if (!cfg || !out_id || !logits) throw Fail("missing argument");
+        if (n <= 0 || n > kSampleMaxN) throw Fail("sampler supports 1..16384 logits");
+        const int k = (cfg->top_k > 0 && cfg->top_k < n) ? cfg->top_k : n;
+        if (cfg->temperature > 0.f && k > kSampleMaxK) throw Fail("sampler supports top-k up to 4096 candidates");
+        if (!g.scfg_dev) {
+            g.scfg_dev = dalloc_t<SampleCfgDev>(1);
+            HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&g.scfg_host), sizeof(SampleCfgDev), hipHostMallocDefault));
+            g.tok_dev = dalloc_t<int32_t>(1);
+        }
+        if (n_history > 0 && size_t(n_history) > g.hist_cap) {
+            dfree(g.hist_dev);
+            g.hist_dev = dalloc_t<int32_t>(size_t(n_history));
+            g.hist_cap = size_t(n_history);
+        }
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        if (n_history > 0 && history) h2d(g.hist_dev, history, size_t(n_history) * 4);
+        fill_sample_cfg(*g.scfg_host, *cfg, n_history > 0 && history ? g.hist_dev : nullptr, history ? n_history : 0);
+        HIPCHECK(hipMemcpyAsync(g.scfg_dev, g.scfg_host, sizeof(SampleCfgDev), hipMemcpyHostToDevice, g.stream));
+        float *dl = dev_scratch(g.dbuf_x, g.dbuf_x_bytes, size_t(n) * 4);
+        float *pin = pinned(size_t(n) * 4 + 64);
+        std::memcpy(pin, logits, size_t(n) * 4);
+        HIPCHECK(hipMemcpyAsync(dl, pin, size_t(n) * 4, hipMemcpyHostToDevice, g.stream));
+        HIPCHECK(launch_sample(g.scfg_dev, dl, n, g.tok_dev, g.stream));
+        int32_t tok = -1;
+        HIPCHECK(hipMemcpyAsync(pin, g.tok_dev, 4, hipMemcpyDeviceToHost, g.stream));
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        std::memcpy(&tok, pin, 4);
+        if (tok < 0) throw Fail("device sampler rejected the request");
+        *out_id = tok;
+        return 1;
+    }, 0);
+}
+
+// ---------------------------------------------------------------- device-resident path
+void *voxhip_dev_alloc(size_t bytes) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    try {
+        require_ok();
+        return dalloc(bytes);
+    } catch (const std::exception &e) {
+        set_error(e.what());
+        return nullptr;
+    }
+}
+void voxhip_dev_free(void *p) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (g.ok) { (void)hipStreamSynchronize(g.stream); dfree(p); }
+}
+int voxhip_memcpy_h2d(void *d_dst, const void *src, size_t bytes) {
+    return guard_int([&] {
+        require_ok();
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        HIPCHECK(hipMemcpy(d_dst, src, bytes, hipMemcpyHostToDevice));
+        return 1;
+    }, 0);
+}
+int voxhip_memcpy_d2h(void *dst, const void *d_src, size_t bytes) {
+    return guard_int([&] {
+        require_ok();
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        HIPCHECK(hipMemcpy(dst, d_src, bytes, hipMemcpyDeviceToHost));
+        return 1;
+    }, 0);
+}
+int voxhip_sync(void) {
+    return guard_int([&] {
+        require_ok();
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        return 1;
+    }, 0);
+}
+
+}  // extern "C"
+
+namespace {
+// Enqueues one device-resident decode step on stream s (no host copies).
+int enqueue_decode(Xfmr &X, int m, int head, const float *d_x, float *d_out_last, float *d_logits, bool sample, int32_t *d_token,
+                   hipStream_t s) {
+    int kernels = 0;
+    HIPCHECK(hipMemcpyAsync(X.h, d_x, size_t(m) * X.H * 4, hipMemcpyDeviceToDevice, s));
+    enqueue_layers(X, m, m, X.layers, s);
+    kernels += 7 * X.layers;
+    enqueue_final(X, m - 1, 1, head, s);
+    kernels += 1;
+    if (d_out_last) HIPCHECK(hipMemcpyAsync(d_out_last, X.xnorm, size_t(X.H) * 4, hipMemcpyDeviceToDevice, s));
+    if (head >= 0) {
+        const GpuMat &Hm = g.mats[size_t(head)];
+        if (d_logits) HIPCHECK(hipMemcpyAsync(d_logits, X.logits, size_t(Hm.rows) * 4, hipMemcpyDeviceToDevice, s));
+        if (sample) {
+            HIPCHECK(launch_sample(X.scfg_dev, X.logits, int(Hm.rows), d_token ? d_token : X.token_dev, s));
+            kernels += 1;
+        }
+    }
+    return kernels;
+}
+
+hipGraphExec_t decode_graph(Xfmr &X, int seq, int m, int head, const float *d_x, float *d_out_last, float *d_logits, bool sample,
+                            int32_t *d_token) {
+    GraphKey key{seq, m, head, sample ? 1 : 0, d_x, d_out_last, d_logits, d_token};
+    auto it = X.graphs.find(key);
+    if (it != X.graphs.end()) return it->second;
+    hipGraph_t graph = nullptr;
+    HIPCHECK(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal));
+    try {
+        enqueue_decode(X, m, head, d_x, d_out_last, d_logits, sample, d_token, g.stream);
+    } catch (...) {
+        (void)hipStreamEndCapture(g.stream, &graph);
+        if (graph) (void)hipGraphDestroy(graph);
+        throw;
+    }
+    HIPCHECK(hipStreamEndCapture(g.stream, &graph));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    HIPCHECK(e);
+    X.graphs[key] = exec;
+    return exec;
+}
+
+void prepare_decode(Xfmr &X, Seq &S, int64_t pos0, int64_t m, int head, const voxhip_sample_cfg *cfg) {
+    if (m <= 0 || m > kMaxM) throw Fail("decode_dev takes 1..8 rows");
+    if (pos0 < 0 || pos0 + m > S.cap) throw Fail("context exceeds GPU KV capacity");
+    if (cfg && head < 0) throw Fail("sampling needs a head");
+    if (head >= 0) {
+        const GpuMat &Hm = mat_at(head);
+        if (Hm.cols != X.H) throw Fail("head width differs from the hidden size");
+        if (cfg && Hm.rows > kSampleMaxN) throw Fail("sampler supports up to 16384 logits");
+        ensure_logits(X, Hm.rows);
+    }
+    for (const LayerDev &L : X.L)
+        for (int id : {L.qkv, L.o, L.gu, L.down})
+            if (!int_path(g.mats[size_t(id)], m) && rows_per_pass(g.mats[size_t(id)], m) < m) throw Fail("decode_dev: rows exceed the f32 pass");
+    std::vector<RowRef> rr(static_cast<size_t>(m));
+    for (int64_t i = 0; i < m; ++i) rr[size_t(i)] = row_of(S, pos0 + i);
+    set_rows(X, rr);
+    if (cfg) {
+        SampleCfgDev d;
+        fill_sample_cfg(d, *cfg, nullptr, 0);
+        if (std::memcmp(&d, X.scfg_host, sizeof d) != 0) {
+            HIPCHECK(hipStreamSynchronize(g.stream));
+            *X.scfg_host = d;
+            HIPCHECK(hipMemcpyAsync(X.scfg_dev, X.scfg_host, sizeof d, hipMemcpyHostToDevice, g.stream));
+        }
+    }
+}
+
+uint64_t gemv_stream_bytes(const Xfmr &X) {
+    uint64_t b = 0;
+    for (const LayerDev &L : X.L)
+        for (int id : {L.qkv, L.o, L.gu, L.down}) b += g.mats[size_t(id)].bytes;
+    return b;
+}
+}  // namespace
+
+extern "C" {
+
+int voxhip_decode_dev(int xfmr, int seq, int64_t pos0, const float *d_x, int64_t m, float *d_out_last, int head, float *d_logits,
+                      const voxhip_sample_cfg *cfg, int32_t *d_token) {
+    return guard_int([&] {
+        require_ok();
+        Xfmr &X = xf_at(xfmr);
+        Seq &S = seq_at(seq);
+        check_seq_for(X, xfmr, S);
+        prepare_decode(X, S, pos0, m, head, cfg);
+        hipGraphExec_t exec = decode_graph(X, seq, int(m), head, d_x, d_out_last, d_logits, cfg != nullptr, d_token);
+        HIPCHECK(hipGraphLaunch(exec, g.stream));
+        return 1;
+    }, 0);
+}
+
+int voxhip_mat_synthetic(int32_t type, int64_t rows, int64_t cols, uint64_t seed, uint32_t stream, float mean, float std,
+                         int with_bias) {
+    return guard_int([&] {
+        require_ok();
+        check_shape(type, rows, cols);
+        const int id = new_mat(type, rows, cols, with_bias != 0);
+        GpuMat &m = g.mats[size_t(id)];
+        const size_t n = size_t(rows) * size_t(cols);
+        float *tmp = type == VOXHIP_F32 ? reinterpret_cast<float *>(m.w) : dalloc_t<float>(n);
+        try {
+            HIPCHECK(launch_fill_normal(tmp, int64_t(n), seed, stream, mean, std, g.stream));
+            switch (type) {
+                case VOXHIP_Q8: HIPCHECK(launch_quant_q8(tmp, int64_t(n / 32), reinterpret_cast<int8_t *>(m.w), m.s, g.stream)); break;
+                case VOXHIP_Q4: HIPCHECK(launch_quant_q4(tmp, int64_t(n / 32), m.w, m.s, g.stream)); break;
+                case VOXHIP_F16: HIPCHECK(launch_to_f16(tmp, int64_t(n), m.w, g.stream)); break;
+                case VOXHIP_BF16: HIPCHECK(launch_to_bf16(tmp, int64_t(n), m.w, g.stream)); break;
+                default: break;
+            }
+            if (with_bias) HIPCHECK(launch_fill_normal(m.b, rows, seed, stream + 0x10000u, 0.f, std, g.stream));
+            HIPCHECK(hipStreamSynchronize(g.stream));
+        } catch (...) {
+            if (tmp != reinterpret_cast<float *>(m.w)) dfree(tmp);
+            throw;
+        }
+        if (tmp != reinterpret_cast<float *>(m.w)) dfree(tmp);
+        g.stats.mats_ok += 1;
+        g.stats.bytes += m.bytes;
+        return id;
+    }, -1);
+}
+
+int voxhip_mat_download(int mat, void *data, float *scale, float *bias) {
+    return guard_int([&] {
+        require_ok();
+        const GpuMat &m = mat_at(mat);
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        if (data) HIPCHECK(hipMemcpy(data, m.w, size_t(m.rows) * row_bytes(m.type, m.cols), hipMemcpyDeviceToHost));
+        if (scale && m.s) HIPCHECK(hipMemcpy(scale, m.s, size_t(m.rows) * size_t(m.cols / 32) * 4, hipMemcpyDeviceToHost));
+        if (bias && m.b) HIPCHECK(hipMemcpy(bias, m.b, size_t(m.rows) * 4, hipMemcpyDeviceToHost));
+        return 1;
+    }, 0);
+}
+
+int voxhip_mat_free(int mat) {
+    return guard_int([&] {
+        require_ok();
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        for (const Xfmr *X : g.xf)
+            if (X)
+                for (const LayerDev &L : X->L)
+                    if (L.qkv == mat || L.o == mat || L.gu == mat || L.down == mat) throw Fail("matrix is used by a transformer");
+        free_mat(mat);
+        return 1;
+    }, 0);
+}
+
+int voxhip_seq_fill_synthetic(int seq, int64_t len, uint64_t seed, uint32_t stream, float mean, float std) {
+    return guard_int([&] {
+        require_ok();
+        Seq &S = seq_at(seq);
+        if (len < 0 || len > S.cap) throw Fail("fill length exceeds the capacity");
+        const int64_t planes = int64_t(S.layers) * S.kvh;
+        HIPCHECK(launch_fill_cache(S.k, planes, S.cap, len, S.hd, seed, stream, mean, std, g.stream));
+        HIPCHECK(launch_fill_cache(S.v, planes, S.cap, len, S.hd, seed, stream + 1, mean, std, g.stream));
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        return 1;
+    }, 0);
+}
+
+int voxhip_seq_download(int seq, int32_t layer, int64_t len, float *k, float *v) {
+    return guard_int([&] {
+        require_ok();
+        Seq &S = seq_at(seq);
+        if (layer < 0 || layer >= S.layers || len < 0 || len > S.cap) throw Fail("bad layer or length");
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        const size_t plane = size_t(S.cap) * S.hd;
+        std::vector<_Float16> tk(static_cast<size_t>(S.kvh) * plane), tv(tk.size());
+        HIPCHECK(hipMemcpy(tk.data(), S.k + size_t(layer) * S.kvh * plane, tk.size() * 2, hipMemcpyDeviceToHost));
+        HIPCHECK(hipMemcpy(tv.data(), S.v + size_t(layer) * S.kvh * plane, tv.size() * 2, hipMemcpyDeviceToHost));
+        const size_t kd = size_t(S.kvh) * S.hd;
+        for (int64_t p = 0; p < len; ++p)
+            for (int h = 0; h < S.kvh; ++h)
+                for (int e = 0; e < S.hd; ++e) {
+                    const size_t src = size_t(h) * plane + size_t(p) * S.hd + size_t(e), dst = size_t(p) * kd + size_t(h) * S.hd + size_t(e);
+                    if (k) k[dst] = float(tk[src]);
+                    if (v) v[dst] = float(tv[src]);
+                }
+        return 1;
+    }, 0);
+}
+
+int voxhip_quantize_q8_dev(const float *d_w, int64_t rows, int64_t cols, int8_t *d_q, float *d_scale) {
+    return guard_int([&] {
+        require_ok();
+        if (cols % 32) throw Fail("cols % 32 != 0");
+        HIPCHECK(launch_quant_q8(d_w, rows * (cols / 32), d_q, d_scale, g.stream));
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        return 1;
+    }, 0);
+}
+int voxhip_quantize_q4_dev(const float *d_w, int64_t rows, int64_t cols, uint8_t *d_q, float *d_scale) {
+    return guard_int([&] {
+        require_ok();
+        if (cols % 32) throw Fail("cols % 32 != 0");
+        HIPCHECK(launch_quant_q4(d_w, rows * (cols / 32), d_q, d_scale, g.stream));
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        return 1;
+    }, 0);
+}
+int voxhip_quantize_act_dev(const float *d_x, int64_t n, int8_t *d_xq, float *d_xs) {
+    return guard_int([&] {
+        require_ok();
+        if (n % 32) throw Fail("n % 32 != 0");
+        HIPCHECK(launch_quant_act(d_x, n / 32, d_xq, d_xs, g.stream));
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        return 1;
+    }, 0);
+}
+
+int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, int head, const voxhip_sample_cfg *cfg, int warmup, int steps,
+                        voxhip_bench_result *out) {
+    return guard_int([&] {
+        require_ok();
+        if (!out || steps <= 0) throw Fail("bad bench arguments");
+        Xfmr &X = xf_at(xfmr);
+        Seq &S = seq_at(seq);
+        check_seq_for(X, xfmr, S);
+        std::memset(out, 0, sizeof *out);
+        prepare_decode(X, S, pos0, 1, head, cfg);
+        float *dx = dalloc_t<float>(size_t(X.H));
+        std::vector<hipEvent_t> ev;
+        const GraphKey key{seq, 1, head, cfg != nullptr ? 1 : 0, dx, nullptr, nullptr, nullptr};
+        auto cleanup = [&] {
+            (void)hipStreamSynchronize(g.stream);
+            timing_clear();
+            for (auto &e : ev) (void)hipEventDestroy(e);
+            auto it = X.graphs.find(key);
+            if (it != X.graphs.end()) { (void)hipGraphExecDestroy(it->second); X.graphs.erase(it); }
+            dfree(dx);
+        };
+        try {
+            HIPCHECK(launch_fill_normal(dx, X.H, 7, 0x7777u, 0.f, 1.f, g.stream));
+            // ---- region A: graph replays
+            hipGraphExec_t exec = decode_graph(X, seq, 1, head, dx, nullptr, nullptr, cfg != nullptr, nullptr);
+            for (int i = 0; i < warmup; ++i) HIPCHECK(hipGraphLaunch(exec, g.stream));
+            ev.resize(2);
+            for (auto &e : ev) HIPCHECK(hipEventCreate(&e));
+            HIPCHECK(hipStreamSynchronize(g.stream));
+            HIPCHECK(hipEventRecord(ev[0], g.stream));
+            for (int i = 0; i < steps; ++i) HIPCHECK(hipGraphLaunch(exec, g.stream));
+            HIPCHECK(hipEventRecord(ev[1], g.stream));
+            HIPCHECK(hipEventSynchronize(ev[1]));
+            float ms = 0.f;
+            HIPCHECK(hipEventElapsedTime(&ms, ev[0], ev[1]));
+            out->ms_per_step = double(ms) / steps;
+            // ---- region B: the same step launched kernel by kernel, each stamped by its own events
+            const int nl = X.layers;
+            const int per_step = 7 * nl + (head >= 0 ? 1 : 0) + (cfg && head >= 0 ? 1 : 0);
+            for (auto &e : ev) (void)hipEventDestroy(e);
+            ev.assign(size_t(2 * per_step), nullptr);
+            for (auto &e : ev) HIPCHECK(hipEventCreate(&e));
+            std::vector<int> cls(static_cast<size_t>(per_step));
+            double sum_ms[VOXHIP_K_CLASSES] = {0};
+            int cnt[VOXHIP_K_CLASSES] = {0};
+            const int qd = X.heads * X.hd, kd = X.kvh * X.hd, ldqkv = qd + 2 * kd;
+            for (int it = 0; it < warmup + steps; ++it) {
+                HIPCHECK(hipMemcpyAsync(X.h, dx, size_t(X.H) * 4, hipMemcpyDeviceToDevice, g.stream));
+                int k = 0;
+                auto arm = [&](int c) {
+                    cls[size_t(k)] = c;
+                    timing_arm(ev[size_t(2 * k)], ev[size_t(2 * k + 1)]);
+                    ++k;
+                };
+                for (int li = 0; li < nl; ++li) {
+                    const LayerDev &L = X.L[size_t(li)];
+                    arm(VOXHIP_K_QKV);
+                    gemv(g.mats[size_t(L.qkv)], 1, PRO_RMS, EPI_STORE, X.h, X.H, 1, X.qkv, ldqkv, X.norms + L.ln1, X.eps, nullptr, g.stream);
+                    QkArgs qa;
+                    qa.qkv = X.qkv; qa.ldqkv = ldqkv; qa.q = X.q; qa.rows = X.rows_dev;
+                    qa.qn = L.qk ? X.norms + L.qn : nullptr; qa.kn = L.qk ? X.norms + L.kn : nullptr;
+                    qa.rope = X.rope; qa.heads = X.heads; qa.kv_heads = X.kvh; qa.hd = X.hd; qa.layer = li; qa.eps = X.eps;
+                    arm(VOXHIP_K_QKPOST);
+                    HIPCHECK(launch_qk_post(qa, 1, g.stream));
+                    AttnArgs aa;
+                    aa.q = X.q; aa.rows = X.rows_dev; aa.pm = X.pm; aa.pl = X.pl; aa.po = X.po; aa.out = X.ao;
+                    aa.heads = X.heads; aa.kv_heads = X.kvh; aa.layer = li; aa.scale = 1.0f / std::sqrt(float(X.hd));
+                    arm(VOXHIP_K_ATTN);
+                    arm(VOXHIP_K_COMBINE);
+                    HIPCHECK(launch_attention(aa, X.hd, X.heads / X.kvh, 1, g.stream));
+                    arm(VOXHIP_K_O);
+                    gemv(g.mats[size_t(L.o)], 1, PRO_X, EPI_ACC, X.ao, qd, 1, X.h, X.H, nullptr, 0.f, nullptr, g.stream);
+                    arm(VOXHIP_K_GATEUP);
+                    gemv(g.mats[size_t(L.gu)], 1, PRO_RMS, EPI_SWIGLU, X.h, X.H, 1, X.g, X.I, X.norms + L.ln2, X.eps, nullptr, g.stream);
+                    arm(VOXHIP_K_DOWN);
+                    gemv(g.mats[size_t(L.down)], 1, PRO_X, EPI_ACC, X.g, X.I, 1, X.h, X.H, nullptr, 0.f, nullptr, g.stream);
+                }
+                if (head >= 0) {
+                    arm(VOXHIP_K_HEAD);
+                    enqueue_final(X, 0, 1, head, g.stream);
+                    if (cfg) {
+                        arm(VOXHIP_K_SAMPLE);
+                        HIPCHECK(launch_sample(X.scfg_dev, X.logits, int(g.mats[size_t(head)].rows), X.token_dev, g.stream));
+                    }
+                }
+                HIPCHECK(hipStreamSynchronize(g.stream));
+                if (k != per_step) throw Fail("bench launch count mismatch");
+                if (it < warmup) continue;
+                for (int i = 0; i < per_step; ++i) {
+                    float t = 0.f;
+                    HIPCHECK(hipEventElapsedTime(&t, ev[size_t(2 * i)], ev[size_t(2 * i + 1)]));
+                    sum_ms[cls[size_t(i)]] += t;
+                    cnt[cls[size_t(i)]] += 1;
+                }
+            }
+            // ---- algorithmic bytes per launch of each class
+            const double kv_read = 2.0 * double(pos0 + 1) * kd * 2.0;  // K and V of the visible keys, f16, one layer
+            double bytes[VOXHIP_K_CLASSES] = {0};
+            for (const LayerDev &L : X.L) {
+                bytes[VOXHIP_K_QKV] += double(g.mats[size_t(L.qkv)].bytes) + X.H * 4.0;
+                bytes[VOXHIP_K_O] += double(g.mats[size_t(L.o)].bytes);
+                bytes[VOXHIP_K_GATEUP] += double(g.mats[size_t(L.gu)].bytes) + X.H * 4.0;
+                bytes[VOXHIP_K_DOWN] += double(g.mats[size_t(L.down)].bytes);
+            }
+            for (int c = 0; c < 4; ++c) bytes[c] /= nl;
+            bytes[VOXHIP_K_ATTN] = kv_read;
+            bytes[VOXHIP_K_QKPOST] = 2.0 * kd * 2.0 + (X.L[0].qk ? 2.0 * X.hd * 4.0 : 0.0);
+            if (head >= 0) bytes[VOXHIP_K_HEAD] = double(g.mats[size_t(head)].bytes) + X.H * 4.0;
+            double total_ms = 0.0, step_bytes = 0.0;
+            for (int c = 0; c < VOXHIP_K_CLASSES; ++c) {
+                out->class_launches[c] = steps > 0 ? cnt[c] / steps : 0;
+                out->class_ms[c] = cnt[c] ? sum_ms[c] / cnt[c] : 0.0;
+                out->class_bytes[c] = bytes[c];
+                total_ms += sum_ms[c];
+                step_bytes += bytes[c] * out->class_launches[c];
+            }
+            out->kernel_ms_per_step = total_ms / steps;
+            out->step_bytes = step_bytes;
+            out->kernels_per_step = per_step;
+            out->n_classes = VOXHIP_K_CLASSES;
+        } catch (...) {
+            cleanup();
+            throw;
+        }
+        cleanup();
+        return 1;
+    }, 0);
+}
+
+int voxhip_bench_gemv_q8(int64_t rows, int64_t cols, int copies, int warmup, int iters, double *ms_per_launch) {
+    return guard_int([&] {
+        require_ok();
+        if (copies <= 0 || iters <= 0 || !ms_per_launch) throw Fail("bad bench arguments");
+        check_shape(VOXHIP_Q8, rows, cols);
+        std::vector<int> ids;
+        float *x = nullptr, *y = nullptr, *gamma = nullptr;
+        auto cleanup = [&] {
+            (void)hipStreamSynchronize(g.stream);
+            for (int id : ids) free_mat(id);
+            dfree(x); dfree(y); dfree(gamma);
+        };
+        try {
+            for (int c = 0; c < copies; ++c) {
+                const int id = new_mat(VOXHIP_Q8, rows, cols, false);
+                ids.push_back(id);
+                GpuMat &m = g.mats[size_t(id)];
+                float *tmp = dalloc_t<float>(size_t(rows) * size_t(cols));
+                HIPCHECK(launch_fill_normal(tmp, rows * cols, 1000 + c, 0x51u, 0.f, 0.02f, g.stream));
+                HIPCHECK(launch_quant_q8(tmp, rows * cols / 32, reinterpret_cast<int8_t *>(m.w), m.s, g.stream));
+                HIPCHECK(hipStreamSynchronize(g.stream));
+                dfree(tmp);
+            }
+            x = dalloc_t<float>(size_t(cols));
+            y = dalloc_t<float>(size_t(rows));
+            gamma = dalloc_t<float>(size_t(cols));
+            HIPCHECK(launch_fill_normal(x, cols, 3, 0x52u, 0.f, 1.f, g.stream));
+            HIPCHECK(launch_fill_normal(gamma, cols, 4, 0x53u, 1.f, 0.02f, g.stream));
+            for (int i = 0; i < warmup; ++i)
+                gemv(g.mats[size_t(ids[size_t(i % copies)])], 1, PRO_RMS, EPI_STORE, x, cols, 1, y, rows, gamma, 1e-6f, nullptr, g.stream);
+            hipEvent_t e0, e1;
+            HIPCHECK(hipEventCreate(&e0));
+            HIPCHECK(hipEventCreate(&e1));
+            HIPCHECK(hipEventRecord(e0, g.stream));
+            for (int i = 0; i < iters; ++i)
+                gemv(g.mats[size_t(ids[size_t(i % copies)])], 1, PRO_RMS, EPI_STORE, x, cols, 1, y, rows, gamma, 1e-6f, nullptr, g.stream);
+            HIPCHECK(hipEventRecord(e1, g.stream));
+            HIPCHECK(hipEventSynchronize(e1));
+            float ms = 0.f;
+            HIPCHECK(hipEventElapsedTime(&ms, e0, e1));
+            *ms_per_launch = double(ms) / iters;
+            (void)hipEventDestroy(e0);
+            (void)hipEventDestroy(e1);
+        } catch (...) {
+            cleanup();
+            throw;
+        }
+        cleanup();
+        return 1;
+    }, 0);
+}
+
+}  // extern "C"

@@ -1,0 +1,86 @@
+"""Synthetic decoder stacks built directly in HBM (weights generated and quantized on the device).
+
+The workloads of BASELINE.json: random-init weights ~N(0, 0.02) in the reference's storage formats, norm
+weights ~N(1, 0.02), a KV cache of prior tokens ~N(0, 1) stored in f16. Nothing here reads a checkpoint.
+"""
+import math
+
+import numpy as np
+
+from . import voxhip as vh
+
+# Qwen3-TTS-0.6B-shaped talker
+TALKER_0_6B = dict(layers=28, hidden=1024, heads=16, kv_heads=8, head_dim=128, inter=3072, theta=1e6, eps=1e-6,
+                   kv_len=512, head_rows=3072, wtype=vh.Q8, head_type=vh.Q8)
+# Qwen3-TTS-1.7B-shaped talker with q4 body
+TALKER_1_7B_Q4 = dict(layers=28, hidden=2048, heads=16, kv_heads=8, head_dim=128, inter=6144, theta=1e6, eps=1e-6,
+                      kv_len=1024, head_rows=3072, wtype=vh.Q4, head_type=vh.Q8)
+NAMES = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+def rope_inv_freq(head_dim, theta):
+    """rope_inv_freq (kernels.cpp:734-738): float(1 / theta^(2i/hd)) with the C library's pow."""
+    return np.array([1.0 / math.pow(theta, (2 * i) / head_dim) for i in range(head_dim // 2)], np.float64).astype(np.float32)
+
+
+class Decoder:
+    """A device-resident decoder stack: per-layer matrix handles, the stacked transformer, one KV sequence, a head."""
+
+    def __init__(self, cfg, seed=0, capacity=None, keep_mats=True):
+        c = dict(cfg)
+        self.cfg = c
+        H, nh, nkv, hd, I, L = c["hidden"], c["heads"], c["kv_heads"], c["head_dim"], c["inter"], c["layers"]
+        qd, kd = nh * hd, nkv * hd
+        shapes = {"q": (qd, H), "k": (kd, H), "v": (kd, H), "o": (H, qd), "gate": (I, H), "up": (I, H), "down": (H, I)}
+        rng = np.random.default_rng(seed)
+        self.mats = []
+        layers = []
+        for li in range(L):
+            ids = {}
+            for j, n in enumerate(NAMES):
+                r, cc = shapes[n]
+                ids[n] = vh.mat_synthetic(c["wtype"], r, cc, seed, 0x100 * li + j, 0.0, 0.02)
+            self.mats.append(ids)
+            norms = {n: (1.0 + 0.02 * rng.standard_normal(H)).astype(np.float32) for n in ("ln1", "ln2")}
+            norms.update({n: (1.0 + 0.02 * rng.standard_normal(hd)).astype(np.float32) for n in ("qn", "kn")})
+            layers.append(norms)
+        self.layers = layers
+        self.final_norm = (1.0 + 0.02 * rng.standard_normal(H)).astype(np.float32)
+        self.inv_freq = rope_inv_freq(hd, c["theta"])
+        self.desc = vh.XfmrHost(layers, self.final_norm, H, nh, nkv, hd, I, c["eps"], c["theta"], self.inv_freq)
+        handles = [self.mats[li][n] for li in range(L) for n in NAMES]
+        self.xfmr = vh.xfmr_create_from_mats(self.desc, handles, "talker")
+        if not keep_mats:
+            for ids in self.mats:
+                for h in ids.values():
+                    vh.mat_free(h)
+            self.mats = None
+        self.capacity = capacity or max(c["kv_len"] + 64, 1024)
+        self.seq = vh.seq_create(self.xfmr, self.capacity)
+        vh.seq_fill_synthetic(self.seq, c["kv_len"], seed, 0xC0DE, 0.0, 1.0)
+        self.head = vh.mat_synthetic(c["head_type"], c["head_rows"], H, seed, 0xF00D, 0.0, 0.02) if c.get("head_rows") else -1
+
+    def weight_bytes(self):
+        """Algorithmic bytes of one decode step's weight stream (layers + head), as stored."""
+        c = self.cfg
+        H, qd, kd, I = c["hidden"], c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"], c["inter"]
+
+        def mb(t, rows, cols):
+            if t == vh.Q8:
+                return rows * cols + rows * (cols // 32) * 4
+            if t == vh.Q4:
+                return rows * cols // 2 + rows * (cols // 32) * 4
+            return rows * cols * (4 if t == vh.F32 else 2)
+        per_layer = sum(mb(c["wtype"], r, cc) for r, cc in ((qd + 2 * kd, H), (H, qd), (2 * I, H), (H, I)))
+        head = mb(c["head_type"], c["head_rows"], H) if c.get("head_rows") else 0
+        return per_layer * c["layers"] + head
+
+    def step_bytes(self, pos):
+        """Algorithmic HBM bytes of one decode step at position pos: weights, f16 KV read (pos + 1 keys and values
+        per layer), norm weights, and the new token's f16 K/V write."""
+        c = self.cfg
+        kd = c["kv_heads"] * c["head_dim"]
+        kv = c["layers"] * 2 * (pos + 1) * kd * 2
+        norms = c["layers"] * (2 * c["hidden"] + 2 * c["head_dim"]) * 4 + c["hidden"] * 4
+        kv_write = c["layers"] * 2 * kd * 2
+        return self.weight_bytes() + kv + norms + kv_write

@@ -1,0 +1,435 @@
+"""ctypes binding of libvoxhip.so (the C ABI declared in include/voxhip.h).
+
+The names and argument meaning mirror the reference's device interface (src/gpu.hpp, src/kernels.hpp:88-100):
+upload -> gpu_upload, matmul -> gpu_matmul, xfmr_create -> gpu_xfmr_create, seq_create -> gpu_seq_create,
+forward -> gpu_xfmr_forward, ... Failures raise VoxHipError with the library's last error (the reference
+returns false and keeps the reason in gpu_stats().last_error).
+
+There is no CPU fallback here: if the library is not built, or no gfx950 device is present, every call
+raises.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libvoxhip.so")
+
+F32, F16, BF16, Q8, Q4 = 0, 1, 2, 3, 4
+
+
+class VoxHipError(RuntimeError):
+    pass
+
+
+class Mat(C.Structure):
+    _fields_ = [("type", C.c_int32), ("data", C.c_void_p), ("scale", C.c_void_p), ("rows", C.c_int64),
+                ("cols", C.c_int64), ("bias", C.c_void_p)]
+
+
+class DeviceInfo(C.Structure):
+    _fields_ = [("index", C.c_int32), ("name", C.c_char * 256), ("type", C.c_char * 16), ("software", C.c_int32),
+                ("unified_memory", C.c_int32), ("vram_total", C.c_uint64), ("vram_free", C.c_uint64),
+                ("max_storage_range", C.c_uint64), ("subgroup_arith", C.c_int32), ("coop_matrix", C.c_int32),
+                ("memory_budget", C.c_int32), ("api_version", C.c_uint32), ("vendor_id", C.c_uint32),
+                ("driver_version", C.c_uint32)]
+
+
+class Stats(C.Structure):
+    _fields_ = [("mats_ok", C.c_int64), ("mats_failed", C.c_int64), ("bytes", C.c_uint64), ("bytes_failed", C.c_uint64)]
+
+
+class MemInfo(C.Structure):
+    _fields_ = [("used", C.c_uint64), ("limit", C.c_uint64), ("device_free", C.c_uint64), ("device_total", C.c_uint64),
+                ("device_index", C.c_int32)]
+
+
+class Layer(C.Structure):
+    _fields_ = [(n, Mat) for n in ("q", "k", "v", "o", "gate", "up", "down")] + \
+               [(n, C.c_void_p) for n in ("qn", "kn", "ln1", "ln2", "attn_scale", "mlp_scale")]
+
+
+class XfmrDesc(C.Structure):
+    _fields_ = [("n_layers", C.c_int32), ("layers", C.POINTER(Layer)), ("final_norm", C.c_void_p), ("hidden", C.c_int32),
+                ("heads", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32), ("inter", C.c_int32),
+                ("eps", C.c_float), ("theta", C.c_double), ("window", C.c_int32), ("inv_freq", C.c_void_p)]
+
+
+class SampleCfg(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int32), ("repetition_penalty", C.c_float),
+                ("key0", C.c_uint32), ("key1", C.c_uint32), ("frame", C.c_uint64), ("codebook", C.c_uint32),
+                ("draw", C.c_uint32), ("suppress_from", C.c_int32), ("suppress_to", C.c_int32), ("eos_code", C.c_int32),
+                ("block_eos", C.c_int32)]
+
+
+KERNEL_CLASSES = ("qkv_gemv", "o_gemv", "gateup_gemv", "down_gemv", "head_gemv", "attention", "attn_combine", "qk_post", "sampler")
+
+
+class BenchResult(C.Structure):
+    _fields_ = [("ms_per_step", C.c_double), ("kernel_ms_per_step", C.c_double), ("step_bytes", C.c_double),
+                ("kernels_per_step", C.c_int32), ("n_classes", C.c_int32),
+                ("class_ms", C.c_double * len(KERNEL_CLASSES)), ("class_bytes", C.c_double * len(KERNEL_CLASSES)),
+                ("class_launches", C.c_int32 * len(KERNEL_CLASSES))]
+
+
+UPLOADED_FN = C.CFUNCTYPE(None, C.c_void_p, C.c_int32, C.c_int32)
+
+# every symbol include/voxhip.h declares, with (restype, argtypes)
+_P, _I, _I32, _I64, _F, _D, _U32, _U64, _S = (C.c_void_p, C.c_int, C.c_int32, C.c_int64, C.c_float, C.c_double, C.c_uint32,
+                                            C.c_uint64, C.c_size_t)
+SIGNATURES = {
+    "voxhip_device_count": (_I, []),
+    "voxhip_device_info_get": (_I, [_I, C.POINTER(DeviceInfo)]),
+    "voxhip_init": (_I, [C.c_char_p, C.c_char_p, _S]),
+    "voxhip_active": (_I, []),
+    "voxhip_device_name": (C.c_char_p, []),
+    "voxhip_stats_get": (None, [C.POINTER(Stats)]),
+    "voxhip_last_error": (C.c_char_p, []),
+    "voxhip_set_vram_limit": (None, [_U64]),
+    "voxhip_mem_info_get": (None, [C.POINTER(MemInfo)]),
+    "voxhip_upload": (_I, [C.POINTER(Mat), _I]),
+    "voxhip_matmul": (_I, [_I, _P, _I64, _P]),
+    "voxhip_mat_shape": (_I, [_I, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+    "voxhip_xfmr_create": (_I, [C.POINTER(XfmrDesc), C.c_char_p, _I, UPLOADED_FN, _P]),
+    "voxhip_seq_create": (_I, [_I, _I64]),
+    "voxhip_seq_free": (None, [_I]),
+    "voxhip_xfmr_forward": (_I, [_I, _I, _I64, _P, _I64, _P, _I, _I, _P]),
+    "voxhip_xfmr_forward_hidden": (_I, [_I, _I, _I64, _P, _I64, _P]),
+    "voxhip_xfmr_forward_pair": (_I, [_I, _I, _I, _I64, _P, _I, _P, _P]),
+    "voxhip_xfmr_forward_steps": (_I, [_I, _P, _P, _I64, _P, _P, _I, _P]),
+    "voxhip_sample_logits": (_I, [_P, _I32, C.POINTER(SampleCfg), _P, _I32, C.POINTER(C.c_int32)]),
+    "voxhip_dev_alloc": (_P, [_S]),
+    "voxhip_dev_free": (None, [_P]),
+    "voxhip_memcpy_h2d": (_I, [_P, _P, _S]),
+    "voxhip_memcpy_d2h": (_I, [_P, _P, _S]),
+    "voxhip_sync": (_I, []),
+    "voxhip_decode_dev": (_I, [_I, _I, _I64, _P, _I64, _P, _I, _P, C.POINTER(SampleCfg), _P]),
+    "voxhip_mat_synthetic": (_I, [_I32, _I64, _I64, _U64, _U32, _F, _F, _I]),
+    "voxhip_mat_download": (_I, [_I, _P, _P, _P]),
+    "voxhip_mat_free": (_I, [_I]),
+    "voxhip_xfmr_create_from_mats": (_I, [C.POINTER(XfmrDesc), _P, C.c_char_p]),
+    "voxhip_seq_fill_synthetic": (_I, [_I, _I64, _U64, _U32, _F, _F]),
+    "voxhip_seq_download": (_I, [_I, _I32, _I64, _P, _P]),
+    "voxhip_quantize_q8_dev": (_I, [_P, _I64, _I64, _P, _P]),
+    "voxhip_quantize_q4_dev": (_I, [_P, _I64, _I64, _P, _P]),
+    "voxhip_quantize_act_dev": (_I, [_P, _I64, _P, _P]),
+    "voxhip_bench_decode": (_I, [_I, _I, _I64, _I, C.POINTER(SampleCfg), _I, _I, C.POINTER(BenchResult)]),
+    "voxhip_bench_gemv_q8": (_I, [_I64, _I64, _I, _I, _I, C.POINTER(C.c_double)]),
+}
+
+_lib = None
+
+
+def lib():
+    """Loads libvoxhip.so; raises when it is not built (no fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise VoxHipError(f"{LIB_PATH} is not built: run __graft_entry__.build() or python -m vox_amd.build")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+def _err(what):
+    raise VoxHipError(f"{what}: {lib().voxhip_last_error().decode(errors='replace')}")
+
+
+def _check(rc, what):
+    if not rc:
+        _err(what)
+    return rc
+
+
+def _handle(h, what):
+    if h < 0:
+        _err(what)
+    return h
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---------------------------------------------------------------- device, init
+def device_count():
+    return lib().voxhip_device_count()
+
+
+def init(device="hip:0"):
+    err = C.create_string_buffer(512)
+    if not lib().voxhip_init(device.encode(), err, 512):
+        raise VoxHipError(err.value.decode(errors="replace"))
+
+
+def device_name():
+    return lib().voxhip_device_name().decode()
+
+
+def mem_info():
+    m = MemInfo()
+    lib().voxhip_mem_info_get(C.byref(m))
+    return m
+
+
+def stats():
+    s = Stats()
+    lib().voxhip_stats_get(C.byref(s))
+    return s
+
+
+# ---------------------------------------------------------------- matrices
+class HostMat:
+    """A weight matrix in the reference layout (vox::Mat): keeps its arrays alive for the ctypes view."""
+
+    def __init__(self, wtype, data, rows, cols, scale=None, bias=None):
+        self.type, self.rows, self.cols = wtype, int(rows), int(cols)
+        self.data = np.ascontiguousarray(data)
+        self.scale = None if scale is None else f32(scale)
+        self.bias = None if bias is None else f32(bias)
+        self.c = Mat(wtype, self.data.ctypes.data, None if self.scale is None else self.scale.ctypes.data, self.rows, self.cols,
+                     None if self.bias is None else self.bias.ctypes.data)
+
+
+def upload(*parts):
+    arr = (Mat * len(parts))(*[p.c for p in parts])
+    return _handle(lib().voxhip_upload(arr, len(parts)), "upload")
+
+
+def matmul(mat, x):
+    x = f32(x)
+    m = 1 if x.ndim == 1 else x.shape[0]
+    rows, cols = C.c_int64(), C.c_int64()
+    _check(lib().voxhip_mat_shape(mat, C.byref(rows), C.byref(cols)), "mat_shape")
+    y = np.empty((m, rows.value), np.float32)
+    _check(lib().voxhip_matmul(mat, _p(x), m, _p(y)), "matmul")
+    return y
+
+
+def mat_shape(mat):
+    rows, cols = C.c_int64(), C.c_int64()
+    _check(lib().voxhip_mat_shape(mat, C.byref(rows), C.byref(cols)), "mat_shape")
+    return rows.value, cols.value
+
+
+def mat_synthetic(wtype, rows, cols, seed, stream, mean=0.0, std=0.02, bias=False):
+    return _handle(lib().voxhip_mat_synthetic(wtype, rows, cols, seed, stream, mean, std, int(bias)), "mat_synthetic")
+
+
+def mat_download(mat, wtype):
+    rows, cols = mat_shape(mat)
+    if wtype == Q8:
+        data = np.empty((rows, cols), np.int8)
+    elif wtype == Q4:
+        data = np.empty((rows, cols // 2), np.uint8)
+    elif wtype == F32:
+        data = np.empty((rows, cols), np.float32)
+    else:
+        data = np.empty((rows, cols), np.uint16)
+    scale = np.empty((rows, cols // 32), np.float32) if wtype in (Q8, Q4) else None
+    bias = np.empty(rows, np.float32)
+    _check(lib().voxhip_mat_download(mat, _p(data), _p(scale), _p(bias)), "mat_download")
+    return data, scale, bias
+
+
+def mat_free(mat):
+    _check(lib().voxhip_mat_free(mat), "mat_free")
+
+
+# ---------------------------------------------------------------- transformer
+class XfmrHost:
+    """Host description of a Qwen3-shaped transformer (vox::TransformerW) for xfmr_create."""
+
+    def __init__(self, layers, final_norm, hidden, heads, kv_heads, head_dim, inter, eps, theta, inv_freq):
+        self.layers = layers  # list of dicts: q,k,v,o,gate,up,down -> HostMat (or None for *_from_mats), qn,kn,ln1,ln2 -> arrays
+        self.final_norm = f32(final_norm)
+        self.inv_freq = f32(inv_freq)
+        arr = (Layer * len(layers))()
+        for i, L in enumerate(layers):
+            for n in ("q", "k", "v", "o", "gate", "up", "down"):
+                if L.get(n) is not None:
+                    setattr(arr[i], n, L[n].c)
+            for n in ("qn", "kn", "ln1", "ln2"):
+                v = L.get(n)
+                setattr(arr[i], n, None if v is None else v.ctypes.data)
+        self._arr = arr
+        self.c = XfmrDesc(len(layers), arr, self.final_norm.ctypes.data, hidden, heads, kv_heads, head_dim, inter, eps, theta, 0,
+                          self.inv_freq.ctypes.data)
+        self.hidden, self.heads, self.kv_heads, self.head_dim, self.inter = hidden, heads, kv_heads, head_dim, inter
+
+
+def xfmr_create(desc, name="xfmr", n_layers=-1, uploaded=None):
+    cb = UPLOADED_FN(uploaded) if uploaded else UPLOADED_FN()
+    h = lib().voxhip_xfmr_create(C.byref(desc.c), name.encode(), n_layers, cb, None)
+    return _handle(h, "xfmr_create")
+
+
+def xfmr_create_from_mats(desc, mats, name="xfmr"):
+    ids = np.ascontiguousarray(mats, dtype=np.int32)
+    return _handle(lib().voxhip_xfmr_create_from_mats(C.byref(desc.c), _p(ids), name.encode()), "xfmr_create_from_mats")
+
+
+def seq_create(xfmr, capacity):
+    return _handle(lib().voxhip_seq_create(xfmr, capacity), "seq_create")
+
+
+def seq_free(seq):
+    lib().voxhip_seq_free(seq)
+
+
+def seq_fill_synthetic(seq, length, seed, stream, mean=0.0, std=1.0):
+    _check(lib().voxhip_seq_fill_synthetic(seq, length, seed, stream, mean, std), "seq_fill_synthetic")
+
+
+def seq_download(seq, layer, length, kd):
+    k = np.empty((length, kd), np.float32)
+    v = np.empty((length, kd), np.float32)
+    _check(lib().voxhip_seq_download(seq, layer, length, _p(k), _p(v)), "seq_download")
+    return k, v
+
+
+def forward(xfmr, seq, pos0, x, hidden, in_proj=-1, head=-1):
+    x = f32(x)
+    m = x.shape[0]
+    out = np.empty(hidden, np.float32)
+    head_out = None
+    if head >= 0:
+        head_out = np.empty(mat_shape(head)[0], np.float32)
+    _check(lib().voxhip_xfmr_forward(xfmr, seq, pos0, _p(x), m, _p(out), in_proj, head, _p(head_out)), "xfmr_forward")
+    return out, head_out
+
+
+def forward_hidden(xfmr, seq, pos0, x, hidden):
+    x = f32(x)
+    out = np.empty((x.shape[0], hidden), np.float32)
+    _check(lib().voxhip_xfmr_forward_hidden(xfmr, seq, pos0, _p(x), x.shape[0], _p(out)), "xfmr_forward_hidden")
+    return out
+
+
+def forward_pair(xfmr, seq0, seq1, pos, x2, hidden, head=-1):
+    x2 = f32(x2)
+    out = np.empty((2, hidden), np.float32)
+    head_out = np.empty((2, mat_shape(head)[0]), np.float32) if head >= 0 else None
+    _check(lib().voxhip_xfmr_forward_pair(xfmr, seq0, seq1, pos, _p(x2), head, _p(out), _p(head_out)), "xfmr_forward_pair")
+    return out, head_out
+
+
+def forward_steps(xfmr, seqs, pos, x, hidden, head=-1):
+    x = f32(x)
+    B = x.shape[0]
+    s = np.ascontiguousarray(seqs, dtype=np.int32)
+    p = np.ascontiguousarray(pos, dtype=np.int64)
+    out = np.empty((B, hidden), np.float32)
+    head_out = np.empty((B, mat_shape(head)[0]), np.float32) if head >= 0 else None
+    _check(lib().voxhip_xfmr_forward_steps(xfmr, _p(s), _p(p), B, _p(x), _p(out), head, _p(head_out)), "xfmr_forward_steps")
+    return out, head_out
+
+
+# ---------------------------------------------------------------- sampling
+def sample_cfg(temperature=0.9, top_p=1.0, top_k=50, repetition_penalty=1.0, seed=0, frame=0, codebook=0, draw=0,
+               suppress_from=0, suppress_to=0, eos_code=-1, block_eos=0):
+    return SampleCfg(temperature, top_p, top_k, repetition_penalty, seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF, frame, codebook,
+                     draw, suppress_from, suppress_to, eos_code, block_eos)
+
+
+def sample_logits(logits, cfg, history=None):
+    l = f32(logits)
+    h = None if history is None else np.ascontiguousarray(history, dtype=np.int32)
+    out = C.c_int32(-1)
+    _check(lib().voxhip_sample_logits(_p(l), l.size, C.byref(cfg), _p(h), 0 if h is None else h.size, C.byref(out)),
+           "sample_logits")
+    return out.value
+
+
+# ---------------------------------------------------------------- device-resident
+class DevBuf:
+    def __init__(self, nbytes):
+        self.nbytes = nbytes
+        self.ptr = lib().voxhip_dev_alloc(nbytes)
+        if not self.ptr:
+            _err("dev_alloc")
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        _check(lib().voxhip_memcpy_h2d(self.ptr, _p(arr), arr.nbytes), "memcpy_h2d")
+
+    def download(self, shape, dtype):
+        out = np.empty(shape, dtype)
+        _check(lib().voxhip_memcpy_d2h(_p(out), self.ptr, out.nbytes), "memcpy_d2h")
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib().voxhip_dev_free(self.ptr)
+            self.ptr = None
+
+
+def decode_dev(xfmr, seq, pos0, d_x, m=1, d_out=None, head=-1, d_logits=None, cfg=None, d_token=None):
+    _check(lib().voxhip_decode_dev(xfmr, seq, pos0, d_x.ptr, m, None if d_out is None else d_out.ptr, head,
+                                   None if d_logits is None else d_logits.ptr, None if cfg is None else C.byref(cfg),
+                                   None if d_token is None else d_token.ptr), "decode_dev")
+
+
+def sync():
+    _check(lib().voxhip_sync(), "sync")
+
+
+def quantize_q8_dev(w):
+    w = f32(w)
+    rows, cols = w.shape
+    dw, dq, ds = DevBuf(w.nbytes), DevBuf(rows * cols), DevBuf(rows * cols // 32 * 4)
+    try:
+        dw.upload(w)
+        _check(lib().voxhip_quantize_q8_dev(dw.ptr, rows, cols, dq.ptr, ds.ptr), "quantize_q8_dev")
+        return dq.download((rows, cols), np.int8), ds.download((rows, cols // 32), np.float32)
+    finally:
+        for b in (dw, dq, ds):
+            b.free()
+
+
+def quantize_q4_dev(w):
+    w = f32(w)
+    rows, cols = w.shape
+    dw, dq, ds = DevBuf(w.nbytes), DevBuf(rows * cols // 2), DevBuf(rows * cols // 32 * 4)
+    try:
+        dw.upload(w)
+        _check(lib().voxhip_quantize_q4_dev(dw.ptr, rows, cols, dq.ptr, ds.ptr), "quantize_q4_dev")
+        return dq.download((rows, cols // 2), np.uint8), ds.download((rows, cols // 32), np.float32)
+    finally:
+        for b in (dw, dq, ds):
+            b.free()
+
+
+def quantize_act_dev(x):
+    x = f32(x).ravel()
+    n = x.size
+    dx, dq, ds = DevBuf(x.nbytes), DevBuf(n), DevBuf(n // 32 * 4)
+    try:
+        dx.upload(x)
+        _check(lib().voxhip_quantize_act_dev(dx.ptr, n, dq.ptr, ds.ptr), "quantize_act_dev")
+        return dq.download(n, np.int8), ds.download(n // 32, np.float32)
+    finally:
+        for b in (dx, dq, ds):
+            b.free()
+
+
+def bench_decode(xfmr, seq, pos0, head, cfg, warmup, steps):
+    r = BenchResult()
+    _check(lib().voxhip_bench_decode(xfmr, seq, pos0, head, None if cfg is None else C.byref(cfg), warmup, steps, C.byref(r)),
+           "bench_decode")
+    return r
+
+
+def bench_gemv_q8(rows, cols, copies, warmup, iters):
+    ms = C.c_double()
+    _check(lib().voxhip_bench_gemv_q8(rows, cols, copies, warmup, iters, C.byref(ms)), "bench_gemv_q8")
+    return ms.value
