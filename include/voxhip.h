@@ -131,6 +131,11 @@ int voxhip_xfmr_forward(int xfmr, int seq, int64_t pos0, const float *x, int64_t
                         int head, float *head_out);
 /* gpu_xfmr_forward_hidden (kernels.hpp:96): the device layers only, no final norm: hidden_out [m][hidden]. */
 int voxhip_xfmr_forward_hidden(int xfmr, int seq, int64_t pos0, const float *x, int64_t m, float *hidden_out);
+/* Layers [first, first + count) only, on the residual stream x [m][hidden] (no input projection, no final norm):
+ * hidden_out [m][hidden]. Generalizes the hybrid placement of gpu_xfmr_forward_hidden (the reference runs the first
+ * gpu_layers layers on the device and the rest on the CPU, kernels.cpp:764-791) to any contiguous range. */
+int voxhip_xfmr_forward_layers(int xfmr, int seq, int64_t pos0, const float *x, int64_t m, int32_t first, int32_t count,
+                               float *hidden_out);
 /* gpu_xfmr_forward_pair (kernels.hpp:99-100): one token of each of two sequences at the same position. */
 int voxhip_xfmr_forward_pair(int xfmr, int seq0, int seq1, int64_t pos, const float *x2, int head, float *out2,
                              float *head_out2);
@@ -228,6 +233,8 @@ typedef struct voxhip_bench_result {
     double step_bytes;          /* algorithmic HBM bytes per step (weights + scales, KV read + write, norms) */
     int32_t kernels_per_step;
     int32_t n_classes;
+    int32_t kernel_stamped;     /* 1: hipExtLaunchKernel events at kernel start/end; 0: stream events around each launch
+                                   (used when a profiler intercepts launches) */
     double class_ms[VOXHIP_K_CLASSES];        /* average duration of one launch of the class */
     double class_bytes[VOXHIP_K_CLASSES];     /* algorithmic bytes of one launch of the class */
     int32_t class_launches[VOXHIP_K_CLASSES]; /* launches per step */

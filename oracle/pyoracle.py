@@ -74,6 +74,7 @@ def _declare(lib, prefix):
             "matmul_f32_tiles": (None, [P, P, I64, P]),
             "set_threads": (None, [C.c_int]),
             "get_threads": (C.c_int, []),
+            "transformer_layers": (C.c_int, [P, P, P, I64, I32, I32, P]),
         })
     else:
         sig.update({
@@ -235,6 +236,15 @@ def transformer_forward(X, kv, x, want_all=False, use_ref=False):
     if rc != 0:
         raise RuntimeError(f"transformer_forward failed ({rc})")
     return (out_last, out_all) if want_all else out_last
+
+
+def transformer_layers(X, kv, x, first, count):
+    """Residual stream after layers [first, first + count) (no final norm); kv.len is not advanced."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    h = np.empty_like(x)
+    if lib().vo_transformer_layers(C.byref(X.c), C.byref(kv.c), _p(x), x.shape[0], first, count, _p(h)) != 0:
+        raise RuntimeError("transformer_layers failed")
+    return h
 
 
 def transformer_forward_steps(X, kvs, x, use_ref=False):

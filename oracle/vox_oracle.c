@@ -554,13 +554,13 @@ static void attend(const float *qh, const float *K, const float *V, int64_t n, i
     }
 }
 
-int vo_transformer_forward(const vo_xfmr *w, vo_kv *kv, const float *x_in, int64_t m, float *out_last, float *out_all) {
+/* Layers [l0, l1) of transformer_forward (kernels.cpp:791-840) on the residual stream h [m][hidden], rows at
+ * positions pos0.. (= kv->len); appends their keys/values but does not advance kv->len. */
+static void run_layers(const vo_xfmr *w, vo_kv *kv, float *h, int64_t m, int32_t l0, int32_t l1) {
     const int64_t H = w->hidden, nh = w->heads, nkv = w->kv_heads, hd = w->head_dim, I = w->inter;
     const int64_t qd = nh * hd, kd = nkv * hd, group = nh / nkv;
     const int64_t pos0 = kv->len;
-    if (pos0 + m > kv->cap) return -1;
     const float scale = 1.0f / sqrtf((float)hd);
-    float *h = (float *)malloc(sizeof(float) * (size_t)(m * H));
     float *xn = (float *)malloc(sizeof(float) * (size_t)(m * H));
     float *q = (float *)malloc(sizeof(float) * (size_t)(m * qd));
     float *k = (float *)malloc(sizeof(float) * (size_t)(m * kd));
@@ -571,8 +571,7 @@ int vo_transformer_forward(const vo_xfmr *w, vo_kv *kv, const float *x_in, int64
     float *u = (float *)malloc(sizeof(float) * (size_t)(m * I));
     float *d = (float *)malloc(sizeof(float) * (size_t)(m * H));
     float *sc = (float *)malloc(sizeof(float) * (size_t)(pos0 + m));
-    memcpy(h, x_in, sizeof(float) * (size_t)(m * H));
-    for (int32_t li = 0; li < w->n_layers; ++li) {
+    for (int32_t li = l0; li < l1; ++li) {
         const vo_layer *L = &w->layers[li];
         float *K = kv->k + (int64_t)li * kv->cap * kd, *V = kv->v + (int64_t)li * kv->cap * kd;
         for (int64_t i = 0; i < m; ++i) vo_rmsnorm(h + i * H, L->ln1, H, w->eps, xn + i * H);
@@ -604,10 +603,26 @@ int vo_transformer_forward(const vo_xfmr *w, vo_kv *kv, const float *x_in, int64
         vo_matmul(&L->down, g, m, d, kv->avx2);
         for (int64_t i = 0; i < m * H; ++i) h[i] += d[i];
     }
+    free(xn); free(q); free(k); free(v); free(ao); free(o); free(g); free(u); free(d); free(sc);
+}
+
+int vo_transformer_forward(const vo_xfmr *w, vo_kv *kv, const float *x_in, int64_t m, float *out_last, float *out_all) {
+    const int64_t H = w->hidden;
+    if (kv->len + m > kv->cap) return -1;
+    float *h = (float *)malloc(sizeof(float) * (size_t)(m * H));
+    memcpy(h, x_in, sizeof(float) * (size_t)(m * H));
+    run_layers(w, kv, h, m, 0, w->n_layers);
     kv->len += m;
     if (out_last) vo_rmsnorm(h + (m - 1) * H, w->final_norm, H, w->eps, out_last);
     if (out_all) for (int64_t i = 0; i < m; ++i) vo_rmsnorm(h + i * H, w->final_norm, H, w->eps, out_all + i * H);
-    free(h); free(xn); free(q); free(k); free(v); free(ao); free(o); free(g); free(u); free(d); free(sc);
+    free(h);
+    return 0;
+}
+
+int vo_transformer_layers(const vo_xfmr *w, vo_kv *kv, const float *x_in, int64_t m, int32_t first, int32_t count, float *h_out) {
+    if (kv->len + m > kv->cap || first < 0 || count < 0 || first + count > w->n_layers) return -1;
+    memcpy(h_out, x_in, sizeof(float) * (size_t)(m * w->hidden));
+    run_layers(w, kv, h_out, m, first, first + count);
     return 0;
 }
 

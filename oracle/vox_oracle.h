@@ -112,6 +112,11 @@ typedef struct {
 /* transformer_forward (kernels.cpp:760-844), full attention (window 0), no layer scales.
  * Returns 0, or -1 when the cache is too small. */
 int vo_transformer_forward(const vo_xfmr *w, vo_kv *kv, const float *x, int64_t m, float *out_last, float *out_all);
+/* Layers [first, first + count) of transformer_forward on the residual stream x [m][hidden] (rows at positions
+ * kv->len ..), writing the residual stream after them to h_out (no final norm) and their keys/values to the cache;
+ * kv->len is not advanced. The CPU side of the reference's hybrid placement (kernels.cpp:764-791) and the
+ * per-layer parity probe of the tests. */
+int vo_transformer_layers(const vo_xfmr *w, vo_kv *kv, const float *x, int64_t m, int32_t first, int32_t count, float *h_out);
 /* transformer_forward_steps (kernels.cpp:846-906): one token for each of B sequences. */
 int vo_transformer_forward_steps(const vo_xfmr *w, vo_kv *const *kvs, int64_t B, const float *x, float *out);
 

@@ -386,3 +386,19 @@ def test_transformer_kv_f16_mode(oracle):
     po.transformer_forward(mdl.ox, k0, x)
     po.transformer_forward(mdl.ox, k1, x)
     assert np.array_equal(k1.k[:, :3], k0.k[:, :3].astype(np.float16).astype(np.float32))
+
+
+def test_transformer_layers_compose(oracle):
+    # layers [0, a) then [a, L) == layers [0, L); final norm of that == transformer_forward (bit-exact)
+    from models import Model
+    rng = np.random.default_rng(16)
+    mdl = Model(9, 3, 128, 4, 2, 64, 256, wtype=po.Q8)
+    x = rng.standard_normal((2, 128)).astype(np.float32)
+    k1, k2, k3 = mdl.oracle_kv(8, 1), mdl.oracle_kv(8, 1), mdl.oracle_kv(8, 1)
+    full = po.transformer_layers(mdl.ox, k1, x, 0, 3)
+    part = po.transformer_layers(mdl.ox, k2, po.transformer_layers(mdl.ox, k2, x, 0, 1), 1, 2)
+    assert np.array_equal(full, part)
+    out = po.transformer_forward(mdl.ox, k3, x)
+    nrm = np.empty(128, np.float32)
+    po.lib().vo_rmsnorm(full[1].ctypes.data, mdl.final_norm.ctypes.data, 128, np.float32(1e-6), nrm.ctypes.data)
+    assert np.array_equal(nrm, out)

@@ -19,6 +19,7 @@ std::atomic<int> g_tcount{0};
 
 void timing_arm(hipEvent_t start, hipEvent_t stop) {
     std::lock_guard<std::mutex> lk(g_tmu);
+    if (!stop) return;
     if (g_tcount == 16) return;
     const int i = (g_thead + g_tcount) % 16;
     g_tq[i][0] = start;

@@ -368,9 +368,9 @@ void set_rows(Xfmr &X, const std::vector<RowRef> &rows) {
 
 // All layers for mc rows whose input is in X.h (row i at the position in rows_dev[i]).
 // m_total: the caller's total row count, which picks the q8 arithmetic (int8 for <= 8, f32 above).
-void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int n_layers, hipStream_t s) {
+void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipStream_t s) {
     const int qd = X.heads * X.hd, kd = X.kvh * X.hd, ldqkv = qd + 2 * kd;
-    for (int li = 0; li < n_layers; ++li) {
+    for (int li = first; li < first + count; ++li) {
         const LayerDev &L = X.L[size_t(li)];
         const GpuMat &Mqkv = g.mats[size_t(L.qkv)], &Mo = g.mats[size_t(L.o)], &Mgu = g.mats[size_t(L.gu)],
                      &Md = g.mats[size_t(L.down)];
@@ -417,7 +417,7 @@ void check_seq_for(Xfmr &X, int xid, const Seq &S) {
 // Generic host-pointer forward for up to any m rows of one sequence (or B rows of B sequences).
 // rows_of(i) gives the cache view of row i. x rows are xc wide (in_proj cols or hidden).
 template <class RowsOf>
-void forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_proj, int n_layers, int64_t m_total,
+void forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_proj, int first_layer, int n_layers, int64_t m_total,
                   float *hidden_out, float *out_last, int head, float *head_out, bool final_all) {
     const int64_t H = X.H;
     const GpuMat *Pm = in_proj >= 0 ? &mat_at(in_proj) : nullptr;
@@ -425,7 +425,7 @@ void forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_pro
     const int64_t xc = Pm ? Pm->cols : H;
     // rows per pass: the smallest of the passes the used matrices allow (f32 path holds 4 rows in LDS)
     int chunk = kMaxM;
-    for (int li = 0; li < n_layers; ++li)
+    for (int li = first_layer; li < first_layer + n_layers; ++li)
         for (int id : {X.L[size_t(li)].qkv, X.L[size_t(li)].o, X.L[size_t(li)].gu, X.L[size_t(li)].down})
             chunk = std::min(chunk, rows_per_pass(g.mats[size_t(id)], m_total));
     if (Pm) chunk = std::min(chunk, rows_per_pass(*Pm, m_total));
@@ -447,7 +447,7 @@ void forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_pro
         } else {
             HIPCHECK(hipMemcpyAsync(X.h, pin, size_t(mc * H) * 4, hipMemcpyHostToDevice, g.stream));
         }
-        enqueue_layers(X, mc, m_total, n_layers, g.stream);
+        enqueue_layers(X, mc, m_total, first_layer, n_layers, g.stream);
         if (hidden_out) {
             HIPCHECK(hipMemcpyAsync(pin, X.h, size_t(mc * H) * 4, hipMemcpyDeviceToHost, g.stream));
             HIPCHECK(hipStreamSynchronize(g.stream));
@@ -804,7 +804,7 @@ int voxhip_xfmr_forward(int xfmr, int seq, int64_t pos0, const float *x, int64_t
         check_seq_for(X, xfmr, S);
         if (m <= 0) return 1;
         if (pos0 < 0 || pos0 + m > S.cap) throw Fail("context exceeds GPU KV capacity");
-        forward_rows(X, m, [&](int64_t i) { return row_of(S, pos0 + i); }, x, in_proj, X.layers, m, nullptr, out_last, head,
+        forward_rows(X, m, [&](int64_t i) { return row_of(S, pos0 + i); }, x, in_proj, 0, X.layers, m, nullptr, out_last, head,
                      head_out, false);
         return 1;
     }, 0);
@@ -818,7 +818,23 @@ int voxhip_xfmr_forward_hidden(int xfmr, int seq, int64_t pos0, const float *x, 
         check_seq_for(X, xfmr, S);
         if (m <= 0) return 1;
         if (pos0 < 0 || pos0 + m > S.cap) throw Fail("context exceeds GPU KV capacity");
-        forward_rows(X, m, [&](int64_t i) { return row_of(S, pos0 + i); }, x, -1, X.layers, m, hidden_out, nullptr, -1,
+        forward_rows(X, m, [&](int64_t i) { return row_of(S, pos0 + i); }, x, -1, 0, X.layers, m, hidden_out, nullptr, -1,
+                     nullptr, false);
+        return 1;
+    }, 0);
+}
+
+int voxhip_xfmr_forward_layers(int xfmr, int seq, int64_t pos0, const float *x, int64_t m, int32_t first, int32_t count,
+                               float *hidden_out) {
+    return guard_int([&] {
+        require_ok();
+        Xfmr &X = xf_at(xfmr);
+        Seq &S = seq_at(seq);
+        check_seq_for(X, xfmr, S);
+        if (m <= 0 || count == 0) return 1;
+        if (first < 0 || count < 0 || first + count > X.layers) throw Fail("layer range outside the transformer");
+        if (pos0 < 0 || pos0 + m > S.cap) throw Fail("context exceeds GPU KV capacity");
+        forward_rows(X, m, [&](int64_t i) { return row_of(S, pos0 + i); }, x, -1, first, count, m, hidden_out, nullptr, -1,
                      nullptr, false);
         return 1;
     }, 0);
@@ -834,7 +850,7 @@ int voxhip_xfmr_forward_pair(int xfmr, int seq0, int seq1, int64_t pos, const fl
         check_seq_for(X, xfmr, S0);
         check_seq_for(X, xfmr, S1);
         if (pos < 0 || pos + 1 > S0.cap || pos + 1 > S1.cap) throw Fail("context exceeds GPU KV capacity");
-        forward_rows(X, 2, [&](int64_t i) { return row_of(i == 0 ? S0 : S1, pos); }, x2, -1, X.layers, 2, nullptr, out2, head,
+        forward_rows(X, 2, [&](int64_t i) { return row_of(i == 0 ? S0 : S1, pos); }, x2, -1, 0, X.layers, 2, nullptr, out2, head,
                      head_out2, true);
         return 1;
     }, 0);
@@ -854,7 +870,7 @@ int voxhip_xfmr_forward_steps(int xfmr, const int32_t *seqs, const int64_t *pos,
             for (int64_t c = 0; c < b; ++c)
                 if (seqs[c] == seqs[b]) throw Fail("a sequence appears twice in one step");
         }
-        forward_rows(X, B, [&](int64_t i) { return row_of(g.seqs[size_t(seqs[i])], pos[i]); }, x, -1, X.layers, B, nullptr, out,
+        forward_rows(X, B, [&](int64_t i) { return row_of(g.seqs[size_t(seqs[i])], pos[i]); }, x, -1, 0, X.layers, B, nullptr, out,
                      head, head_out, true);
         return 1;
     }, 0);
@@ -944,7 +960,7 @@ int enqueue_decode(Xfmr &X, int m, int head, const float *d_x, float *d_out_last
                    hipStream_t s) {
     int kernels = 0;
     HIPCHECK(hipMemcpyAsync(X.h, d_x, size_t(m) * X.H * 4, hipMemcpyDeviceToDevice, s));
-    enqueue_layers(X, m, m, X.layers, s);
+    enqueue_layers(X, m, m, 0, X.layers, s);
     kernels += 7 * X.layers;
     enqueue_final(X, m - 1, 1, head, s);
     kernels += 1;
@@ -1153,6 +1169,19 @@ int voxhip_quantize_act_dev(const float *d_x, int64_t n, int8_t *d_xq, float *d_
     }, 0);
 }
 
+}  // extern "C"
+
+namespace {
+// rocprofv3 preloads its tool library; kernel-stamped events (hipExtLaunchKernel) are not used under it.
+bool profiler_attached() {
+    const char *pre = std::getenv("LD_PRELOAD");
+    if (pre && std::strstr(pre, "rocprof")) return true;
+    return std::getenv("ROCPROF_OUTPUT_PATH") || std::getenv("ROCP_TOOL_LIBRARIES") || std::getenv("ROCPROFILER_LIBRARY_CTOR");
+}
+}  // namespace
+
+extern "C" {
+
 int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, int head, const voxhip_sample_cfg *cfg, int warmup, int steps,
                         voxhip_bench_result *out) {
     return guard_int([&] {
@@ -1192,6 +1221,7 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, int head, const voxhip_
             // ---- region B: the same step launched kernel by kernel, each stamped by its own events
             const int nl = X.layers;
             const int per_step = 7 * nl + (head >= 0 ? 1 : 0) + (cfg && head >= 0 ? 1 : 0);
+            const bool stamp = !profiler_attached();
             for (auto &e : ev) (void)hipEventDestroy(e);
             ev.assign(size_t(2 * per_step), nullptr);
             for (auto &e : ev) HIPCHECK(hipEventCreate(&e));
@@ -1202,50 +1232,73 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, int head, const voxhip_
             for (int it = 0; it < warmup + steps; ++it) {
                 HIPCHECK(hipMemcpyAsync(X.h, dx, size_t(X.H) * 4, hipMemcpyDeviceToDevice, g.stream));
                 int k = 0;
+                // kernel-stamped events (hipExtLaunchKernel) unless a profiler intercepts the launches, where plain
+                // stream events bracket each launch instead
                 auto arm = [&](int c) {
                     cls[size_t(k)] = c;
-                    timing_arm(ev[size_t(2 * k)], ev[size_t(2 * k + 1)]);
+                    if (stamp) timing_arm(ev[size_t(2 * k)], ev[size_t(2 * k + 1)]);
+                    else HIPCHECK(hipEventRecord(ev[size_t(2 * k)], g.stream));
                     ++k;
+                };
+                auto done = [&] {
+                    if (!stamp) HIPCHECK(hipEventRecord(ev[size_t(2 * (k - 1) + 1)], g.stream));
                 };
                 for (int li = 0; li < nl; ++li) {
                     const LayerDev &L = X.L[size_t(li)];
                     arm(VOXHIP_K_QKV);
                     gemv(g.mats[size_t(L.qkv)], 1, PRO_RMS, EPI_STORE, X.h, X.H, 1, X.qkv, ldqkv, X.norms + L.ln1, X.eps, nullptr, g.stream);
+                    done();
                     QkArgs qa;
                     qa.qkv = X.qkv; qa.ldqkv = ldqkv; qa.q = X.q; qa.rows = X.rows_dev;
                     qa.qn = L.qk ? X.norms + L.qn : nullptr; qa.kn = L.qk ? X.norms + L.kn : nullptr;
                     qa.rope = X.rope; qa.heads = X.heads; qa.kv_heads = X.kvh; qa.hd = X.hd; qa.layer = li; qa.eps = X.eps;
                     arm(VOXHIP_K_QKPOST);
                     HIPCHECK(launch_qk_post(qa, 1, g.stream));
+                    done();
                     AttnArgs aa;
                     aa.q = X.q; aa.rows = X.rows_dev; aa.pm = X.pm; aa.pl = X.pl; aa.po = X.po; aa.out = X.ao;
                     aa.heads = X.heads; aa.kv_heads = X.kvh; aa.layer = li; aa.scale = 1.0f / std::sqrt(float(X.hd));
-                    arm(VOXHIP_K_ATTN);
-                    arm(VOXHIP_K_COMBINE);
+                    if (stamp) {
+                        arm(VOXHIP_K_ATTN);
+                        arm(VOXHIP_K_COMBINE);
+                    } else {  // both kernels inside one bracket; split evenly between the two classes below
+                        arm(VOXHIP_K_ATTN);
+                        cls[size_t(k - 1)] = -1;
+                    }
                     HIPCHECK(launch_attention(aa, X.hd, X.heads / X.kvh, 1, g.stream));
+                    if (!stamp) done();
                     arm(VOXHIP_K_O);
                     gemv(g.mats[size_t(L.o)], 1, PRO_X, EPI_ACC, X.ao, qd, 1, X.h, X.H, nullptr, 0.f, nullptr, g.stream);
+                    done();
                     arm(VOXHIP_K_GATEUP);
                     gemv(g.mats[size_t(L.gu)], 1, PRO_RMS, EPI_SWIGLU, X.h, X.H, 1, X.g, X.I, X.norms + L.ln2, X.eps, nullptr, g.stream);
+                    done();
                     arm(VOXHIP_K_DOWN);
                     gemv(g.mats[size_t(L.down)], 1, PRO_X, EPI_ACC, X.g, X.I, 1, X.h, X.H, nullptr, 0.f, nullptr, g.stream);
+                    done();
                 }
                 if (head >= 0) {
                     arm(VOXHIP_K_HEAD);
                     enqueue_final(X, 0, 1, head, g.stream);
+                    done();
                     if (cfg) {
                         arm(VOXHIP_K_SAMPLE);
                         HIPCHECK(launch_sample(X.scfg_dev, X.logits, int(g.mats[size_t(head)].rows), X.token_dev, g.stream));
+                        done();
                     }
                 }
                 HIPCHECK(hipStreamSynchronize(g.stream));
-                if (k != per_step) throw Fail("bench launch count mismatch");
+                if (k != (stamp ? per_step : per_step - nl)) throw Fail("bench launch count mismatch");
                 if (it < warmup) continue;
-                for (int i = 0; i < per_step; ++i) {
+                for (int i = 0; i < k; ++i) {
                     float t = 0.f;
                     HIPCHECK(hipEventElapsedTime(&t, ev[size_t(2 * i)], ev[size_t(2 * i + 1)]));
-                    sum_ms[cls[size_t(i)]] += t;
-                    cnt[cls[size_t(i)]] += 1;
+                    if (cls[size_t(i)] < 0) {
+                        for (int c : {int(VOXHIP_K_ATTN), int(VOXHIP_K_COMBINE)}) { sum_ms[c] += t / 2; cnt[c] += 1; }
+                    } else {
+                        sum_ms[cls[size_t(i)]] += t;
+                        cnt[cls[size_t(i)]] += 1;
+                    }
                 }
             }
             // ---- algorithmic bytes per launch of each class
@@ -1273,6 +1326,7 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, int head, const voxhip_
             out->step_bytes = step_bytes;
             out->kernels_per_step = per_step;
             out->n_classes = VOXHIP_K_CLASSES;
+            out->kernel_stamped = stamp ? 1 : 0;
         } catch (...) {
             cleanup();
             throw;

@@ -68,7 +68,7 @@ KERNEL_CLASSES = ("qkv_gemv", "o_gemv", "gateup_gemv", "down_gemv", "head_gemv",
 
 class BenchResult(C.Structure):
     _fields_ = [("ms_per_step", C.c_double), ("kernel_ms_per_step", C.c_double), ("step_bytes", C.c_double),
-                ("kernels_per_step", C.c_int32), ("n_classes", C.c_int32),
+                ("kernels_per_step", C.c_int32), ("n_classes", C.c_int32), ("kernel_stamped", C.c_int32),
                 ("class_ms", C.c_double * len(KERNEL_CLASSES)), ("class_bytes", C.c_double * len(KERNEL_CLASSES)),
                 ("class_launches", C.c_int32 * len(KERNEL_CLASSES))]
 
@@ -96,6 +96,7 @@ SIGNATURES = {
     "voxhip_seq_free": (None, [_I]),
     "voxhip_xfmr_forward": (_I, [_I, _I, _I64, _P, _I64, _P, _I, _I, _P]),
     "voxhip_xfmr_forward_hidden": (_I, [_I, _I, _I64, _P, _I64, _P]),
+    "voxhip_xfmr_forward_layers": (_I, [_I, _I, _I64, _P, _I64, _I32, _I32, _P]),
     "voxhip_xfmr_forward_pair": (_I, [_I, _I, _I, _I64, _P, _I, _P, _P]),
     "voxhip_xfmr_forward_steps": (_I, [_I, _P, _P, _I64, _P, _P, _I, _P]),
     "voxhip_sample_logits": (_I, [_P, _I32, C.POINTER(SampleCfg), _P, _I32, C.POINTER(C.c_int32)]),
@@ -312,6 +313,13 @@ def forward_hidden(xfmr, seq, pos0, x, hidden):
     x = f32(x)
     out = np.empty((x.shape[0], hidden), np.float32)
     _check(lib().voxhip_xfmr_forward_hidden(xfmr, seq, pos0, _p(x), x.shape[0], _p(out)), "xfmr_forward_hidden")
+    return out
+
+
+def forward_layers(xfmr, seq, pos0, x, first, count):
+    x = f32(x)
+    out = np.empty_like(x)
+    _check(lib().voxhip_xfmr_forward_layers(xfmr, seq, pos0, _p(x), x.shape[0], first, count, _p(out)), "xfmr_forward_layers")
     return out
 
 
