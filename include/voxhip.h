@@ -239,8 +239,8 @@ typedef struct voxhip_bench_result {
     double class_bytes[VOXHIP_K_CLASSES];     /* algorithmic bytes of one launch of the class */
     int32_t class_launches[VOXHIP_K_CLASSES]; /* launches per step */
 } voxhip_bench_result;
-int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, int head, const voxhip_sample_cfg *cfg, int warmup, int steps,
-                        voxhip_bench_result *out);
+int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, const float *d_x, int head, const voxhip_sample_cfg *cfg,
+                        int32_t *d_token, int warmup, int steps, voxhip_bench_result *out);
 
 /* Times one GEMV kernel configuration on `copies` distinct device copies of a synthetic q8 matrix
  * (rotating, so the working set exceeds the 256 MB Infinity Cache): average ms per launch. */

@@ -43,7 +43,10 @@ def test_quantizers_bit_exact(hip, oracle):
 
 
 @pytest.mark.parametrize("wt", [Q8, Q4, F32, F16, BF16])
-@pytest.mark.parametrize("rows,cols", [(37, 160), (4096, 1024), (1024, 3072), (3072, 1024), (5, 4864), (6144, 1024)])
+# tiles: (37,160) R1; (4096,1024) R4; (1024,3072) IT3; (3072,1024) R3; (5,4864) IT4 over two passes; (6144,1024) R6;
+# (8192,256) R8; (2048,2048) IT2 (R2 for m > 1)
+@pytest.mark.parametrize("rows,cols", [(37, 160), (4096, 1024), (1024, 3072), (3072, 1024), (5, 4864), (6144, 1024),
+                                       (8192, 256), (2048, 2048)])
 def test_matmul_parity(hip, oracle, wt, rows, cols):
     rng = np.random.default_rng(rows * 7 + cols + wt)
     data, scale, bias = make_mat(rng, wt, rows, cols, bias=True)
@@ -91,14 +94,14 @@ def masked(l, cfg):
 def test_sampler_parity(hip, oracle):
     rng = np.random.default_rng(8)
     for i in range(400):
-        n = int(rng.choice([2, 3, 50, 257, 3072, 6564]))
+        n = int(rng.choice([2, 3, 50, 64, 65, 257, 3072, 6564, 16384]))
         l = (rng.standard_normal(n) * rng.uniform(0.3, 5)).astype(np.float32)
         if i % 4 == 0:
             l = np.round(l).astype(np.float32)  # ties
         if i % 5 == 0:
             l[rng.integers(0, n, max(1, n // 3))] = -np.inf
         T = float(rng.choice([0.0, 0.7, 0.9, 1.0, 1.5]))
-        k = int(rng.choice([0, 1, 25, 50, 4096]))
+        k = int(rng.choice([0, 1, 25, 50, 64, 65, 4096]))
         p = float(rng.choice([1.0, 0.8, 0.3]))
         rep = float(rng.choice([1.0, 1.3]))
         hist = rng.integers(0, n, int(rng.integers(0, 30))).astype(np.int32) if rep != 1.0 else None
@@ -108,12 +111,14 @@ def test_sampler_parity(hip, oracle):
             cfg.suppress_from, cfg.suppress_to, cfg.eos_code, cfg.block_eos = n - 20, n, n - 5, int(i % 2)
         u = oracle.uniform(seed, cfg.frame, cfg.codebook, 0)
         want = oracle.sample_logits(masked(l, cfg), T, p, k, rep, hist, u)
-        kk = k if 0 < k < n else n
-        if T > 0 and kk > 4096:
-            with pytest.raises(hip.VoxHipError):
-                hip.sample_logits(l, cfg, hist)
-            continue
         assert hip.sample_logits(l, cfg, hist) == want, (i, n, T, k, p, rep)
+
+
+def test_sampler_limits(hip):
+    with pytest.raises(hip.VoxHipError):
+        hip.sample_logits(np.zeros(16385, np.float32), hip.sample_cfg())
+    with pytest.raises(hip.VoxHipError):
+        hip.sample_logits(np.zeros(0, np.float32), hip.sample_cfg())
 
 
 def test_sampler_reference_rules(hip):

@@ -1,20 +1,25 @@
 // vh_attn.hpp — decode/prefill attention on an f16 KV cache (gfx950, wave64).
 //
 // Semantics follow transformer_forward (kernels.cpp:797-828): per-head RMSNorm of q and k (q_norm/k_norm),
-// rotate-half RoPE with a host-built cos/sin table (the table rows are computed like rope_apply,
-// kernels.cpp:740-757: angle float(inv_freq[i] * float(pos)), cosf/sinf), the new key/value appended at the
-// row's position, then causal GQA softmax attention with scale 1/sqrt(hd) over keys 0..pos.
+// rotate-half RoPE with a host-built cos/sin table (rows computed like rope_apply, kernels.cpp:740-757:
+// angle float(inv_freq[i] * float(pos)), cosf/sinf), the new key/value appended at the row's position, then
+// causal GQA softmax attention with scale 1/sqrt(hd) over keys 0..pos (kernels.cpp:812-826).
 //
-// The cache lives in HBM as f16 [layer][kv_head][cap][head_dim] per sequence (K and V separate), so one
-// kv head's keys are contiguous. Attention is split-K ("flash-decode"): block (split, kv_head, row) runs an
-// online softmax over its key range for all G = heads/kv_heads query heads that share the kv head, and
-// k_attn_combine merges the splits in a fixed order (deterministic).
+// The cache lives in HBM as f16 [layer][kv_head][cap][head_dim] per sequence (K and V separate), so one kv head's
+// keys are contiguous. Attention is split-K: block (split, kv_head, row) runs an online softmax over its key range
+// for the G = heads / kv_heads query heads sharing the kv head and writes unnormalized partials (max, denominator,
+// weighted value sum). The consumer (the o-projection GEMV's prologue) merges the splits in split order.
+//
+// FUSED (decode, and rows of distinct sequences): the kernel also does k_qk_post's work for its row. Every split
+// block normalizes and rotates its G query heads itself; the last split, whose range holds the new key at `pos`,
+// writes the new key/value to the cache and uses them from LDS, so no block reads a cache entry written by
+// another block of the same launch. Not FUSED (prefill of one sequence): k_qk_post has already written q and the
+// pass's keys, and every key is read from the cache.
 #pragma once
 #include "vh_common.hpp"
 #include "vh_types.hpp"
 
 namespace vh {
-
 
 // grid (heads + kv_heads, m), block 64. Thread t handles the rotate-half pair (t, t + hd/2).
 __global__ __launch_bounds__(64) void k_qk_post(QkArgs a) {
@@ -50,105 +55,191 @@ __global__ __launch_bounds__(64) void k_qk_post(QkArgs a) {
     }
 }
 
-
-// Keys per split for n visible keys: at least one block step, at most kAttnSplits splits.
-VH_DEV int split_len(int64_t n, int kpb) {
-    int64_t c = (n + kAttnSplits - 1) / kAttnSplits;
-    c = (c + kpb - 1) / kpb * kpb;
-    return int(c);
+// One rotate-half pair of a head: optional RMSNorm over the head (the HALF lanes of a group hold its pairs),
+// then RoPE. Rounding as rope_apply: products and the difference/sum each rounded (no contraction).
+template <int HALF>
+VH_DEV void norm_rope(float &x0, float &x1, const float *nw, int p, float eps, float c, float s) {
+    if (nw) {
+        const float ss = group_sum<HALF>(x0 * x0 + x1 * x1);
+        const float inv = 1.0f / sqrtf(ss / float(2 * HALF) + eps);
+        x0 = nw[p] * (x0 * inv);
+        x1 = nw[p + HALF] * (x1 * inv);
+    }
+    const float r0 = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
+    const float r1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, s));
+    x0 = r0;
+    x1 = r1;
 }
 
-// grid (kAttnSplits, kv_heads, m), block 256. Each lane holds 8 consecutive elements of one key row;
-// LPK = HD/8 lanes share a key, a wave covers 64/LPK keys per step.
 template <int HD, int G>
-__global__ __launch_bounds__(256) void k_attn_partial(AttnArgs a) {
-    constexpr int LPK = HD / 8, KPW = 64 / LPK, NGRP = 4 * KPW;
-    extern __shared__ __align__(16) float st[];  // [NGRP][G] m, [NGRP][G] l, [NGRP][G][HD] o
-    const int s = blockIdx.x, g = blockIdx.y, i = blockIdx.z;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane % LPK, kg = lane / LPK;
-    const RowRef rr = a.rows[i];
+struct AttnSmem {
+    static constexpr int LPK = HD / 8, KPW = 64 / LPK, NGRP = 4 * KPW;
+    float q[G][HD];
+    float knew[HD], vnew[HD];  // the new key (f16-rounded) and value, last split of a fused row
+    float m[NGRP][G], l[NGRP][G], w[NGRP][G];
+    float o[NGRP][G][HD];
+};
+
+// grid (kAttnMaxSplits, kv_heads, m), block 256. Each lane holds 8 consecutive elements of one key row;
+// LPK = HD / 8 lanes share a key, a wave covers 64 / LPK keys per step, a block NGRP keys.
+template <int HD, int G, bool FUSED>
+__global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
+    using Sm = AttnSmem<HD, G>;
+    constexpr int LPK = Sm::LPK, KPW = Sm::KPW, NGRP = Sm::NGRP, HALF = HD / 2, U = 4;
+    extern __shared__ __align__(16) uint8_t attn_smem[];
+    Sm &sm = *reinterpret_cast<Sm *>(attn_smem);
+    const int s = blockIdx.x, g = blockIdx.y, i = blockIdx.z, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, sub = lane % LPK, grp = wave * KPW + lane / LPK;
+    const AttnPartials &P = a.part;
+    const RowRef rr = P.rows[i];
     const int64_t n = rr.pos + 1;
-    const int C = split_len(n, NGRP);
-    const int64_t k0 = int64_t(s) * C, k1 = k0 + C < n ? k0 + C : n;
-    const int qd = a.heads * HD;
-    const int64_t pbase = (int64_t(i) * a.heads + g * G) * kAttnSplits + s;
-    if (k0 >= n) return;  // unused split: k_attn_combine never reads it
+    const int S = attn_splits(n);
+    if (s >= S) return;  // the consumer reads splits < S only
+    const int64_t C = (n + S - 1) / S, k0 = int64_t(s) * C, k1 = k0 + C < n ? k0 + C : n;
+    const int qd = P.heads * HD, kd = a.kv_heads * HD;
+    const bool last = FUSED && s == S - 1;
+    const int64_t cbase = (int64_t(a.layer) * a.kv_heads + g) * rr.cap * HD;
+    const _Float16 *K = rr.k + cbase, *V = rr.v + cbase;
+
+    // keys read from the cache: all of [k0, k1), except the new key of a fused row (processed from LDS below)
+    const int64_t kend = last ? k1 - 1 : k1;
+    // issue the first batch of cache loads before the q prologue, which does not depend on them
+    f16x8 kb[U], vb[U];
+    const int64_t j0 = k0 + grp;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t j = j0 + int64_t(u) * NGRP;
+        if (j < kend) {
+            kb[u] = *reinterpret_cast<const f16x8 *>(K + j * HD + sub * 8);
+            vb[u] = *reinterpret_cast<const f16x8 *>(V + j * HD + sub * 8);
+        }
+    }
+
+    const float *row = a.qkv + int64_t(i) * a.ldqkv;
+    if (FUSED) {
+        const float *cs = a.rope + rr.pos * HD;  // [HALF][2] (cos, sin) at pos
+        for (int t = tid; t < G * HALF; t += 256) {
+            const int h = t / HALF, p = t % HALF;
+            const float *src = row + (g * G + h) * HD;
+            float x0 = src[p], x1 = src[p + HALF];
+            norm_rope<HALF>(x0, x1, a.qn, p, a.eps, cs[2 * p], cs[2 * p + 1]);
+            sm.q[h][p] = x0;
+            sm.q[h][p + HALF] = x1;
+        }
+        if (last && tid >= 256 - 64 && tid - (256 - 64) < HALF) {  // last wave: the new key and value
+            const int p = tid - (256 - 64);
+            const float *src = row + qd + g * HD;
+            float x0 = src[p], x1 = src[p + HALF];
+            norm_rope<HALF>(x0, x1, a.kn, p, a.eps, cs[2 * p], cs[2 * p + 1]);
+            const _Float16 k0h = _Float16(x0), k1h = _Float16(x1);
+            const _Float16 v0h = _Float16(src[kd + p]), v1h = _Float16(src[kd + p + HALF]);
+            const int64_t off = rr.pos * HD;
+            _Float16 *Kw = rr.k + cbase, *Vw = rr.v + cbase;
+            Kw[off + p] = k0h;
+            Kw[off + p + HALF] = k1h;
+            Vw[off + p] = v0h;
+            Vw[off + p + HALF] = v1h;
+            sm.knew[p] = float(k0h);
+            sm.knew[p + HALF] = float(k1h);
+            sm.vnew[p] = float(v0h);
+            sm.vnew[p + HALF] = float(v1h);
+        }
+    } else {
+        for (int t = tid; t < G * HD; t += 256) {
+            const int h = t / HD, e = t % HD;
+            sm.q[h][e] = a.q[int64_t(i) * qd + (g * G + h) * HD + e];
+        }
+    }
+    __syncthreads();
 
     float qh[G][8];
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qh[h][e] = a.q[int64_t(i) * qd + (g * G + h) * HD + sub * 8 + e];
+        for (int e = 0; e < 8; ++e) qh[h][e] = sm.q[h][sub * 8 + e];
     float mh[G], lh[G], acc[G][8];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        mh[h] = -INFINITY; lh[h] = 0.f;
+        mh[h] = -INFINITY;
+        lh[h] = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
     }
-    const int64_t cbase = (int64_t(a.layer) * a.kv_heads + g) * rr.cap * HD;
-    const _Float16 *K = rr.k + cbase, *V = rr.v + cbase;
-    for (int64_t j = k0 + wave * KPW + kg; j < k1; j += NGRP) {
-        const f16x8 kv = *reinterpret_cast<const f16x8 *>(K + j * HD + sub * 8);
-        const f16x8 vv = *reinterpret_cast<const f16x8 *>(V + j * HD + sub * 8);
+    // online softmax update with one key; all LPK lanes of the group call it together
+    auto consume = [&](const float (&kf)[8], const float (&vf)[8]) {
 #pragma unroll
         for (int h = 0; h < G; ++h) {
             float d = 0.f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) d = fmaf(qh[h][e], float(kv[e]), d);
+            for (int e = 0; e < 8; ++e) d = fmaf(qh[h][e], kf[e], d);
             d = group_sum<LPK>(d);
             const float sc = a.scale * d;
             const float mnew = fmaxf(mh[h], sc);
             const float corr = expf(mh[h] - mnew), p = expf(sc - mnew);
-            lh[h] = lh[h] * corr + p;
+            lh[h] = fmaf(lh[h], corr, p);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] = acc[h][e] * corr + p * float(vv[e]);
+            for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(acc[h][e], corr, p * vf[e]);
             mh[h] = mnew;
         }
+    };
+    for (int64_t jb = j0; jb < kend; jb += int64_t(U) * NGRP) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t j = jb + int64_t(u) * NGRP;
+            if (j < kend) {
+                float kf[8], vf[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) { kf[e] = float(kb[u][e]); vf[e] = float(vb[u][e]); }
+                consume(kf, vf);
+            }
+        }
+        // next batch
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t j = jb + int64_t(U + u) * NGRP;
+            if (j < kend) {
+                kb[u] = *reinterpret_cast<const f16x8 *>(K + j * HD + sub * 8);
+                vb[u] = *reinterpret_cast<const f16x8 *>(V + j * HD + sub * 8);
+            }
+        }
     }
-    float *sm = st, *sl = st + NGRP * G, *so = st + 2 * NGRP * G;
-    const int grp = wave * KPW + kg;
+    if (last && grp == 0) {  // the new key at pos, from LDS
+        float kf[8], vf[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { kf[e] = sm.knew[sub * 8 + e]; vf[e] = sm.vnew[sub * 8 + e]; }
+        consume(kf, vf);
+    }
+
+    // merge the NGRP key groups in LDS, in group order
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        if (sub == 0) { sm[grp * G + h] = mh[h]; sl[grp * G + h] = lh[h]; }
+        if (sub == 0) { sm.m[grp][h] = mh[h]; sm.l[grp][h] = lh[h]; }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) so[(grp * G + h) * HD + sub * 8 + e] = acc[h][e];
+        for (int e = 0; e < 8; ++e) sm.o[grp][h][sub * 8 + e] = acc[h][e];
     }
     __syncthreads();
-    for (int t = threadIdx.x; t < G * HD; t += 256) {
-        const int h = t / HD, e = t % HD;
+    for (int t = tid; t < NGRP * G; t += 256) {
+        const int q = t / G, h = t % G;
         float M = -INFINITY;
-        for (int q = 0; q < NGRP; ++q) M = fmaxf(M, sm[q * G + h]);
-        float L = 0.f, O = 0.f;
-        for (int q = 0; q < NGRP; ++q) {
-            const float w = sm[q * G + h] == -INFINITY ? 0.f : expf(sm[q * G + h] - M);
-            L += w * sl[q * G + h];
-            O += w * so[(q * G + h) * HD + e];
+        for (int r = 0; r < NGRP; ++r) M = fmaxf(M, sm.m[r][h]);
+        sm.w[q][h] = sm.m[q][h] == -INFINITY ? 0.f : expf(sm.m[q][h] - M);
+    }
+    __syncthreads();
+    const int64_t pb = (int64_t(i) * P.heads + g * G) * kAttnMaxSplits + s;  // + h * kAttnMaxSplits
+    for (int t = tid; t < G * HD; t += 256) {
+        const int h = t / HD, e = t % HD;
+        float O = 0.f;
+        for (int r = 0; r < NGRP; ++r) O = fmaf(sm.w[r][h], sm.o[r][h][e], O);
+        const int64_t pidx = pb + int64_t(h) * kAttnMaxSplits;
+        P.po[pidx * HD + e] = O;
+        if (e == 0) {
+            float M = -INFINITY, L = 0.f;
+            for (int r = 0; r < NGRP; ++r) M = fmaxf(M, sm.m[r][h]);
+            for (int r = 0; r < NGRP; ++r) L = fmaf(sm.w[r][h], sm.l[r][h], L);
+            P.pm[pidx] = M;
+            P.pl[pidx] = L;
         }
-        const int64_t pidx = pbase + int64_t(h) * kAttnSplits;
-        a.po[pidx * HD + e] = O;
-        if (e == 0) { a.pm[pidx] = M; a.pl[pidx] = L; }
     }
-}
-
-// grid (heads, m), block HD: merges the used splits of k_attn_partial in split order.
-template <int HD>
-__global__ __launch_bounds__(HD) void k_attn_combine(AttnArgs a) {
-    constexpr int LPK = HD / 8, NGRP = 4 * (64 / LPK);
-    const int h = blockIdx.x, i = blockIdx.y, e = threadIdx.x;
-    const int64_t n = a.rows[i].pos + 1;
-    const int C = split_len(n, NGRP);
-    const int used = int((n + C - 1) / C);
-    const int64_t base = (int64_t(i) * a.heads + h) * kAttnSplits;
-    float M = -INFINITY;
-    for (int s = 0; s < used; ++s) M = fmaxf(M, a.pm[base + s]);
-    float L = 0.f, O = 0.f;
-    for (int s = 0; s < used; ++s) {
-        const float w = expf(a.pm[base + s] - M);
-        L += w * a.pl[base + s];
-        O += w * a.po[(base + s) * HD + e];
-    }
-    a.out[int64_t(i) * a.heads * HD + h * HD + e] = O / L;
 }
 
 }  // namespace vh

@@ -1,17 +1,21 @@
 // vh_gemv.hpp — weight-streaming GEMV kernels for gfx950 (decode, m <= 8 rows).
 //
 // y[i][r] (+)= sum_k W[r][k] * x[i][k] (+ bias[r]) for i < m, the device counterpart of matmul()
-// (kernels.cpp:653-705). The weights are the HBM stream: each lane issues 16-byte non-temporal loads,
-// 64 consecutive lanes cover 1 KiB of one row, and every wave keeps R rows x IT chunks of loads in
-// flight. The first loads are issued before the activation prologue, since they do not depend on it.
+// (kernels.cpp:653-705). The weights are the HBM stream: each lane issues 16-byte non-temporal loads, 64
+// consecutive lanes cover 1 KiB of one row, and every wave keeps R rows x IT such chunks in flight. The tile
+// (R, IT) is picked so one launch is one round of blocks over the 256 CUs, and the weight loads are issued
+// before the activation prologue, which does not depend on them.
 //
 // Two arithmetic families, as the reference dispatcher chooses them:
-//  - k_gemv_int: Q8 (m <= 8) and Q4. x is quantized per 32-block to int8 in LDS exactly as
+//  - k_gemv_int: Q8 (m <= 8) and Q4. The input is quantized per 32-block to int8 in LDS exactly as
 //    kernels.cpp:515-523; block dots are exact int32 (v_dot4_i32_i8), then float(dot) * (ws * xs).
 //  - k_gemv_flt: F32 / F16 / BF16 and Q8 with m > 8: f32 activations in LDS, weights widened
 //    (Q8: float(q) * scale as kernels.cpp:665-674), f32 FMA accumulation.
-// Prologues: PRO_X reads x as is; PRO_RMS applies RMSNorm(x, gamma, eps) first (kernels.cpp:707-712),
-// every block recomputing it (a 4 KiB L2-resident read), and block 0 stores the normed rows when asked.
+// Prologues (one global round trip each, every block computing its own copy of the input):
+//  PRO_X     x as given;
+//  PRO_RMS   RMSNorm(x, gamma, eps) first (kernels.cpp:707-712);
+//  PRO_ATTN  x = merge of the split-K attention partials of each head (the softmax-weighted sum over keys of
+//            kernels.cpp:818-826, finished here instead of in a separate kernel).
 // Epilogues: store, accumulate (the residual add of kernels.cpp:831/:839), or SwiGLU over interleaved
 // (gate, up) row pairs (kernels.cpp:836).
 #pragma once
@@ -20,20 +24,123 @@
 
 namespace vh {
 
-
-// RMSNorm scale of row mm (all threads get it): 1 / sqrt(sum(x^2)/K + eps).
-template <int NT>
-VH_DEV float rms_inv(const float *x, int K, float eps, float *red) {
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < K; i += NT) ss = fmaf(x[i], x[i], ss);
-    ss = block_sum<NT>(ss, red);
-    return 1.0f / sqrtf(ss / float(K) + eps);
-}
-
-// Bytes of one weight row.
 template <int WT>
 VH_DEV int64_t row_bytes(int K) {
     return WT == WT_F32 ? int64_t(K) * 4 : WT == WT_Q8 ? int64_t(K) : WT == WT_Q4 ? int64_t(K) / 2 : int64_t(K) * 2;
+}
+
+// ---------------------------------------------------------------------------------------------- prologue
+// Produces the f32 input rows v[mm][K] (mm < a.m; rows a.m..M-1 are zeros) in 8-element slots: slot s of row mm
+// holds elements 8s..8s+7, a 32-block is 4 consecutive slots handled by 4 consecutive lanes. `sink(mm, s, v)`
+// receives each slot; it runs with all 4 lanes of a block active.
+template <int M, int PRO, class Sink>
+VH_DEV void prologue(const GemvArgs &a, float *red, Sink &&sink) {
+    const int K = a.K, spr = K / 8;  // slots per row
+    float inv[M];
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) inv[mm] = 1.f;
+    if (PRO == PRO_RMS) {
+        // pass 1: sum of squares of every row (kernels.cpp:709-710)
+        float ss[M];
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) {
+            ss[mm] = 0.f;
+            if (mm < a.m)
+                for (int i = threadIdx.x; i < K / 4; i += kGemvThreads) {
+                    const f32x4 t = *reinterpret_cast<const f32x4 *>(a.x + int64_t(mm) * a.ldx + 4 * i);
+                    ss[mm] = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, ss[mm]))));
+                }
+            ss[mm] = wave_sum(ss[mm]);
+        }
+        if ((threadIdx.x & 63) == 0)
+#pragma unroll
+            for (int mm = 0; mm < M; ++mm) red[mm * 4 + (threadIdx.x >> 6)] = ss[mm];
+        __syncthreads();
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) {
+            const float s = red[mm * 4] + red[mm * 4 + 1] + red[mm * 4 + 2] + red[mm * 4 + 3];
+            inv[mm] = 1.0f / sqrtf(s / float(K) + a.eps);
+        }
+    }
+    for (int s = threadIdx.x; s < M * spr; s += kGemvThreads) {
+        const int mm = s / spr, sl = s % spr;
+        float v[8];
+        if (mm >= a.m) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = 0.f;
+        } else if (PRO == PRO_ATTN) {
+            const AttnPartials &P = a.attn;
+            const int e0 = sl * 8, h = e0 / P.hd, d0 = e0 % P.hd;
+            const int S = attn_splits(P.rows[mm].pos + 1);
+            const int64_t base = (int64_t(mm) * P.heads + h) * kAttnMaxSplits;
+            float pm[kAttnMaxSplits], pl[kAttnMaxSplits];
+            f32x4 o0[kAttnMaxSplits], o1[kAttnMaxSplits];
+#pragma unroll
+            for (int q = 0; q < kAttnMaxSplits; ++q)
+                if (q < S) {
+                    pm[q] = P.pm[base + q];
+                    pl[q] = P.pl[base + q];
+                    o0[q] = *reinterpret_cast<const f32x4 *>(P.po + (base + q) * P.hd + d0);
+                    o1[q] = *reinterpret_cast<const f32x4 *>(P.po + (base + q) * P.hd + d0 + 4);
+                }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int q = 0; q < kAttnMaxSplits; ++q)
+                if (q < S) mx = fmaxf(mx, pm[q]);
+            float L = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = 0.f;
+#pragma unroll
+            for (int q = 0; q < kAttnMaxSplits; ++q)
+                if (q < S) {
+                    const float w = expf(pm[q] - mx);
+                    L = fmaf(w, pl[q], L);
+                    v[0] = fmaf(w, o0[q].x, v[0]); v[1] = fmaf(w, o0[q].y, v[1]); v[2] = fmaf(w, o0[q].z, v[2]); v[3] = fmaf(w, o0[q].w, v[3]);
+                    v[4] = fmaf(w, o1[q].x, v[4]); v[5] = fmaf(w, o1[q].y, v[5]); v[6] = fmaf(w, o1[q].z, v[6]); v[7] = fmaf(w, o1[q].w, v[7]);
+                }
+            const float il = 1.0f / L;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] *= il;
+        } else {
+            const float *xr = a.x + int64_t(mm) * a.ldx + sl * 8;
+            const f32x4 t0 = *reinterpret_cast<const f32x4 *>(xr), t1 = *reinterpret_cast<const f32x4 *>(xr + 4);
+            v[0] = t0.x; v[1] = t0.y; v[2] = t0.z; v[3] = t0.w; v[4] = t1.x; v[5] = t1.y; v[6] = t1.z; v[7] = t1.w;
+            if (PRO == PRO_RMS) {
+                const f32x4 g0 = *reinterpret_cast<const f32x4 *>(a.gamma + sl * 8),
+                            g1 = *reinterpret_cast<const f32x4 *>(a.gamma + sl * 8 + 4);
+                const float gm[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = gm[j] * (v[j] * inv[mm]);  // w * (x * inv), kernels.cpp:711
+            }
+        }
+        if (PRO != PRO_X && a.xnorm && blockIdx.x == 0 && mm < a.m)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a.xnorm[int64_t(mm) * K + sl * 8 + j] = v[j];
+        sink(mm, sl, v);
+    }
+}
+
+// Quantizes one 8-element slot of a 32-block held by 4 consecutive lanes (kernels.cpp:515-523): the block max
+// is exact under any reduction order; sc = max/127, inv = 1/sc, q = rint(v * inv).
+VH_DEV void quant_slot(const float (&v)[8], uint32_t *q2, float *sc_out) {
+    float mx = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float t = fabsf(v[j]);
+        mx = mx < t ? t : mx;
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 1, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, kWave));
+    const float sc = mx / 127.0f, inv = sc > 0.f ? 1.0f / sc : 0.0f;
+    *sc_out = sc;
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int qi = int(__builtin_rintf(__fmul_rn(v[j], inv)));
+        w[j >> 2] |= uint32_t(uint8_t(int8_t(qi))) << (8 * (j & 3));
+    }
+    q2[0] = w[0];
+    q2[1] = w[1];
 }
 
 // Epilogue: lane r*M + mm holds the total of (row0 + r, input row mm). SwiGLU pairs rows (2u, 2u+1) =
@@ -52,6 +159,18 @@ VH_DEV void store_out(const GemvArgs &a, float out, int lane, int row0) {
     }
 }
 
+template <int R, int M>
+VH_DEV void reduce_store_prep(float (&acc)[R][M], float &out, int lane) {
+    out = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) {
+            const float s = wave_sum(acc[r][mm]);
+            if (lane == r * M + mm) out = s;
+        }
+}
+
 // ------------------------------------------------------------------------------------------ int8 path
 template <int WT, int M, int R, int IT, int PRO, int EPI>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(GemvArgs a) {
@@ -60,7 +179,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(GemvArgs a) {
     const int K = a.K, nb = K / 32;
     int8_t *xq = reinterpret_cast<int8_t *>(smem);                 // [M][K]
     float *xs = reinterpret_cast<float *>(smem + M * K);           // [M][nb]
-    float *red = xs + M * nb;                                      // [4]
+    float *red = xs + M * nb;                                      // [M][4]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * (kGemvThreads / 64) + wave) * R;
     constexpr int EPC = WT == WT_Q8 ? 16 : 32;  // weight elements per 16-byte chunk
@@ -86,41 +205,13 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(GemvArgs a) {
     };
     load(0);
 
-    // ---- prologue: int8-quantize the m input rows into LDS
-    for (int mm = 0; mm < M; ++mm) {
-        const float *xr = a.x + int64_t(mm) * a.ldx;
-        float inv = 1.f;
-        if (PRO == PRO_RMS && mm < a.m) inv = rms_inv<kGemvThreads>(xr, K, a.eps, red);
-        for (int b = threadIdx.x; b < nb; b += kGemvThreads) {
-            float v[32];
-            if (mm < a.m) {
-#pragma unroll
-                for (int j = 0; j < 32; j += 4) {
-                    const f32x4 t = *reinterpret_cast<const f32x4 *>(xr + b * 32 + j);
-                    v[j] = t.x; v[j + 1] = t.y; v[j + 2] = t.z; v[j + 3] = t.w;
-                }
-                if (PRO == PRO_RMS) {
-#pragma unroll
-                    for (int j = 0; j < 32; ++j) v[j] = a.gamma[b * 32 + j] * (v[j] * inv);
-                    if (a.xnorm && blockIdx.x == 0)
-#pragma unroll
-                        for (int j = 0; j < 32; ++j) a.xnorm[int64_t(mm) * K + b * 32 + j] = v[j];
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < 32; ++j) v[j] = 0.f;
-            }
-            int8_t q[32];
-            float sc;
-            quant_block32(v, q, &sc);
-            uint32_t *dst = reinterpret_cast<uint32_t *>(xq + mm * K + b * 32);
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                dst[j] = uint32_t(uint8_t(q[4 * j])) | uint32_t(uint8_t(q[4 * j + 1])) << 8 |
-                         uint32_t(uint8_t(q[4 * j + 2])) << 16 | uint32_t(uint8_t(q[4 * j + 3])) << 24;
-            xs[mm * nb + b] = sc;
-        }
-    }
+    prologue<M, PRO>(a, red, [&](int mm, int sl, const float (&v)[8]) {
+        uint32_t q2[2];
+        float sc;
+        quant_slot(v, q2, &sc);
+        *reinterpret_cast<uint2 *>(xq + mm * K + sl * 8) = make_uint2(q2[0], q2[1]);
+        if ((sl & 3) == 0) xs[mm * nb + (sl >> 2)] = sc;
+    });
     __syncthreads();
 
     float acc[R][M];
@@ -182,16 +273,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(GemvArgs a) {
             }
         }
     }
-
-    // ---- reduce over the wave and write
-    float out = 0.f;
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int mm = 0; mm < M; ++mm) {
-            const float s = wave_sum(acc[r][mm]);
-            if (lane == r * M + mm) out = s;
-        }
+    float out;
+    reduce_store_prep<R, M>(acc, out, lane);
     store_out<M, R, EPI>(a, out, lane, row0);
 }
 
@@ -202,7 +285,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_flt(GemvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int K = a.K;
     float *xf = reinterpret_cast<float *>(smem);  // [M][K]
-    float *red = xf + M * K;                      // [4]
+    float *red = xf + M * K;                      // [M][4]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * (kGemvThreads / 64) + wave) * R;
     constexpr int EPC = WT == WT_F32 ? 4 : WT == WT_Q8 ? 16 : 8;
@@ -228,22 +311,10 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_flt(GemvArgs a) {
     };
     load(0);
 
-    for (int mm = 0; mm < M; ++mm) {
-        const float *xr = a.x + int64_t(mm) * a.ldx;
-        float inv = 1.f;
-        if (PRO == PRO_RMS && mm < a.m) inv = rms_inv<kGemvThreads>(xr, K, a.eps, red);
-        for (int i = threadIdx.x; i < K; i += kGemvThreads) {
-            float v = 0.f;
-            if (mm < a.m) {
-                v = xr[i];
-                if (PRO == PRO_RMS) {
-                    v = a.gamma[i] * (v * inv);
-                    if (a.xnorm && blockIdx.x == 0) a.xnorm[int64_t(mm) * K + i] = v;
-                }
-            }
-            xf[mm * K + i] = v;
-        }
-    }
+    prologue<M, PRO>(a, red, [&](int mm, int sl, const float (&v)[8]) {
+        *reinterpret_cast<f32x4 *>(xf + mm * K + sl * 8) = f32x4{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4 *>(xf + mm * K + sl * 8 + 4) = f32x4{v[4], v[5], v[6], v[7]};
+    });
     __syncthreads();
 
     float acc[R][M];
@@ -290,15 +361,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_flt(GemvArgs a) {
             }
         }
     }
-
-    float out = 0.f;
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int mm = 0; mm < M; ++mm) {
-            const float s = wave_sum(acc[r][mm]);
-            if (lane == r * M + mm) out = s;
-        }
+    float out;
+    reduce_store_prep<R, M>(acc, out, lane);
     store_out<M, R, EPI>(a, out, lane, row0);
 }
 

@@ -1,74 +1,82 @@
-// vh_gemv_dispatch.hpp — template dispatch from runtime (prologue, epilogue, M, R) to GEMV instantiations.
-// Included by the vh_gemv_*.hip translation units, each instantiating one weight family.
+// vh_gemv_dispatch.hpp — template dispatch from runtime (prologue, epilogue, M, R, IT) to GEMV instantiations.
+// Included by the vh_gemv_*.hip translation units, each instantiating one weight family (VH_GEMV_WT) on one
+// activation path (VH_GEMV_INT).
 #pragma once
 #include "vh_gemv.hpp"
 #include "vh_launch.hpp"
 
 namespace vh {
 
-template <int WT, int M, int R, int IT, int PRO, int EPI>
-hipError_t run_int(const GemvArgs &a, hipStream_t s) {
-    const void *k = reinterpret_cast<const void *>(&k_gemv_int<WT, M, R, IT, PRO, EPI>);
-    const size_t smem = size_t(M) * a.K + size_t(M) * (a.K / 32) * 4 + 16;
-    hipError_t e = ensure_smem(k, smem);
-    if (e != hipSuccess) return e;
-    const int per_block = (kGemvThreads / 64) * R;
-    return launch(k_gemv_int<WT, M, R, IT, PRO, EPI>, dim3((a.rows + per_block - 1) / per_block), dim3(kGemvThreads), smem, s, a);
-}
-
-template <int WT, int M, int R, int IT, int PRO, int EPI>
-hipError_t run_flt(const GemvArgs &a, hipStream_t s) {
-    const void *k = reinterpret_cast<const void *>(&k_gemv_flt<WT, M, R, IT, PRO, EPI>);
-    const size_t smem = size_t(M) * a.K * 4 + 16;
-    hipError_t e = ensure_smem(k, smem);
-    if (e != hipSuccess) return e;
-    const int per_block = (kGemvThreads / 64) * R;
-    return launch(k_gemv_flt<WT, M, R, IT, PRO, EPI>, dim3((a.rows + per_block - 1) / per_block), dim3(kGemvThreads), smem, s, a);
-}
-
 template <int WT, int M, int R, int IT, int PRO, int EPI, bool INT>
-hipError_t run_any(const GemvArgs &a, hipStream_t s) {
-    if constexpr (INT) return run_int<WT, M, R, IT, PRO, EPI>(a, s);
-    else return run_flt<WT, M, R, IT, PRO, EPI>(a, s);
+hipError_t gemv_run(const GemvArgs &a, hipStream_t s) {
+    const int per_block = (kGemvThreads / 64) * R;
+    const dim3 grid((a.rows + per_block - 1) / per_block), block(kGemvThreads);
+    if constexpr (INT) {
+        const size_t smem = size_t(M) * a.K + size_t(M) * (a.K / 32) * 4 + size_t(M) * 16;
+        hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_gemv_int<WT, M, R, IT, PRO, EPI>), smem);
+        if (e != hipSuccess) return e;
+        return launch(k_gemv_int<WT, M, R, IT, PRO, EPI>, grid, block, smem, s, a);
+    } else {
+        const size_t smem = size_t(M) * a.K * 4 + size_t(M) * 16;
+        hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_gemv_flt<WT, M, R, IT, PRO, EPI>), smem);
+        if (e != hipSuccess) return e;
+        return launch(k_gemv_flt<WT, M, R, IT, PRO, EPI>, grid, block, smem, s, a);
+    }
 }
 
+// The (R, IT) tiles instantiated; gemv_tile() (vh_gemv_tile.cpp) picks only these.
 template <int WT, int M, int PRO, int EPI, bool INT>
-hipError_t by_r(int R, const GemvArgs &a, hipStream_t s) {
-    if (R == 4) return run_any<WT, M, 4, 1, PRO, EPI, INT>(a, s);
-    if (R == 2) return run_any<WT, M, 2, 2, PRO, EPI, INT>(a, s);
-    if constexpr (EPI != EPI_SWIGLU) return run_any<WT, M, 1, 4, PRO, EPI, INT>(a, s);
+hipError_t gemv_by_tile(int R, int IT, const GemvArgs &a, hipStream_t s) {
+#define VH_TILE(r, it) \
+    if (R == r && IT == it) return gemv_run<WT, M, r, it, PRO, EPI, INT>(a, s);
+    if constexpr (M == 1) {
+        if constexpr (EPI == EPI_SWIGLU) {
+            VH_TILE(2, 1) VH_TILE(4, 1) VH_TILE(6, 1) VH_TILE(8, 1) VH_TILE(2, 2) VH_TILE(2, 3)
+        } else {
+            VH_TILE(1, 1) VH_TILE(2, 1) VH_TILE(3, 1) VH_TILE(4, 1) VH_TILE(6, 1) VH_TILE(8, 1)
+            VH_TILE(1, 2) VH_TILE(1, 3) VH_TILE(1, 4)
+        }
+    } else {
+        if constexpr (EPI == EPI_SWIGLU) {
+            VH_TILE(2, 1)
+        } else {
+            VH_TILE(1, 1) VH_TILE(2, 1) VH_TILE(1, 2)
+        }
+    }
+#undef VH_TILE
     return hipErrorInvalidValue;
 }
 
 template <int WT, int PRO, int EPI, bool INT>
-hipError_t by_m(int M, int R, const GemvArgs &a, hipStream_t s) {
+hipError_t gemv_by_m(int M, int R, int IT, const GemvArgs &a, hipStream_t s) {
     switch (M) {
-        case 1: return by_r<WT, 1, PRO, EPI, INT>(R, a, s);
-        case 2: if constexpr (INT) return by_r<WT, 2, PRO, EPI, INT>(R, a, s); else return hipErrorInvalidValue;
-        case 4: return by_r<WT, 4, PRO, EPI, INT>(R, a, s);
-        case 8: if constexpr (INT) return by_r<WT, 8, PRO, EPI, INT>(R, a, s); else return hipErrorInvalidValue;
+        case 1: return gemv_by_tile<WT, 1, PRO, EPI, INT>(R, IT, a, s);
+        case 2: if constexpr (INT) return gemv_by_tile<WT, 2, PRO, EPI, INT>(R, IT, a, s); else return hipErrorInvalidValue;
+        case 4: return gemv_by_tile<WT, 4, PRO, EPI, INT>(R, IT, a, s);
+        case 8: if constexpr (INT) return gemv_by_tile<WT, 8, PRO, EPI, INT>(R, IT, a, s); else return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }
 
-// (prologue, epilogue) pairs the backend uses: RMS+store (qkv, head), X+acc (o, down: residual),
-// RMS+swiglu (gate|up), X+store (in_proj, plain matmul).
+// (prologue, epilogue) pairs the backend uses: RMS+store (q|k|v, head), ATTN+acc (o: attention merge and
+// residual), RMS+swiglu (gate|up), X+acc (down: residual), X+store (in_proj, plain matmul).
 template <int WT, bool INT>
-hipError_t by_pe(int pro, int epi, int M, int R, const GemvArgs &a, hipStream_t s) {
-    if (pro == PRO_RMS && epi == EPI_STORE) return by_m<WT, PRO_RMS, EPI_STORE, INT>(M, R, a, s);
-    if (pro == PRO_X && epi == EPI_ACC) return by_m<WT, PRO_X, EPI_ACC, INT>(M, R, a, s);
-    if (pro == PRO_RMS && epi == EPI_SWIGLU) return by_m<WT, PRO_RMS, EPI_SWIGLU, INT>(M, R, a, s);
-    if (pro == PRO_X && epi == EPI_STORE) return by_m<WT, PRO_X, EPI_STORE, INT>(M, R, a, s);
+hipError_t gemv_dispatch(int pro, int epi, int M, int R, int IT, const GemvArgs &a, hipStream_t s) {
+    if (pro == PRO_RMS && epi == EPI_STORE) return gemv_by_m<WT, PRO_RMS, EPI_STORE, INT>(M, R, IT, a, s);
+    if (pro == PRO_ATTN && epi == EPI_ACC) return gemv_by_m<WT, PRO_ATTN, EPI_ACC, INT>(M, R, IT, a, s);
+    if (pro == PRO_RMS && epi == EPI_SWIGLU) return gemv_by_m<WT, PRO_RMS, EPI_SWIGLU, INT>(M, R, IT, a, s);
+    if (pro == PRO_X && epi == EPI_ACC) return gemv_by_m<WT, PRO_X, EPI_ACC, INT>(M, R, IT, a, s);
+    if (pro == PRO_X && epi == EPI_STORE) return gemv_by_m<WT, PRO_X, EPI_STORE, INT>(M, R, IT, a, s);
     return hipErrorInvalidValue;
 }
 
-template <int WT>
-hipError_t dispatch_int(int pro, int epi, int M, int R, const GemvArgs &a, hipStream_t s) {
-    return by_pe<WT, true>(pro, epi, M, R, a, s);
-}
-template <int WT>
-hipError_t dispatch_flt(int pro, int epi, int M, int R, const GemvArgs &a, hipStream_t s) {
-    return by_pe<WT, false>(pro, epi, M, R, a, s);
-}
-
 }  // namespace vh
+
+// One translation unit per (weight type, activation path): defines its launch entry point.
+#if defined(VH_GEMV_WT) && defined(VH_GEMV_INT) && defined(VH_GEMV_ENTRY)
+namespace vh {
+hipError_t VH_GEMV_ENTRY(int pro, int epi, int M, int R, int IT, const GemvArgs &a, hipStream_t s) {
+    return gemv_dispatch<VH_GEMV_WT, VH_GEMV_INT>(pro, epi, M, R, IT, a, s);
+}
+}  // namespace vh
+#endif

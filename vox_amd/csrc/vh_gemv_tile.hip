@@ -1,0 +1,77 @@
+// GEMV launch: picks the activation path's row block M and the (R, IT) tile from the matrix shape, then calls the
+// translation unit that instantiates the weight family.
+#include <cstdlib>
+
+#include "vh_launch.hpp"
+
+namespace vh {
+
+hipError_t launch_gemv_int_q8(int pro, int epi, int M, int R, int IT, const GemvArgs &a, hipStream_t s);
+hipError_t launch_gemv_int_q4(int pro, int epi, int M, int R, int IT, const GemvArgs &a, hipStream_t s);
+hipError_t launch_gemv_flt_q8(int pro, int epi, int M, int R, int IT, const GemvArgs &a, hipStream_t s);
+hipError_t launch_gemv_flt_f32(int pro, int epi, int M, int R, int IT, const GemvArgs &a, hipStream_t s);
+hipError_t launch_gemv_flt_f16(int pro, int epi, int M, int R, int IT, const GemvArgs &a, hipStream_t s);
+hipError_t launch_gemv_flt_bf16(int pro, int epi, int M, int R, int IT, const GemvArgs &a, hipStream_t s);
+
+// Waves one launch aims for: 256 CUs x 4 waves, so a decode GEMV is one round of blocks in which every lane
+// issues all of its weight loads before the activation prologue. VOXHIP_GEMV_WAVES overrides it (tuning).
+static int target_waves() {
+    static const int w = [] {
+        const char *e = std::getenv("VOXHIP_GEMV_WAVES");
+        const int v = e ? std::atoi(e) : 0;
+        return v >= 64 ? v : 1024;
+    }();
+    return w;
+}
+
+void gemv_tile(int rows, int nchunk, int M, bool swiglu, int *R, int *IT) {
+    if (M > 1) {  // tiles (1,1) (2,1) (1,2); swiglu (2,1)
+        *IT = !swiglu && nchunk > 64 ? 2 : 1;
+        *R = swiglu ? 2 : (*IT == 1 && rows >= 2048) ? 2 : 1;
+        return;
+    }
+    int it = (nchunk + 63) / 64;
+    it = it < 1 ? 1 : it > 4 ? 4 : it;
+    if (it > 1) {  // (1,2) (1,3) (1,4); swiglu (2,2) (2,3)
+        *R = swiglu ? 2 : 1;
+        *IT = swiglu && it > 3 ? 3 : it;
+        return;
+    }
+    const int need = (rows + target_waves() - 1) / target_waves();
+    static const int kR[] = {1, 2, 3, 4, 6, 8}, kRs[] = {2, 4, 6, 8};
+    const int *set = swiglu ? kRs : kR;
+    const int n = swiglu ? 4 : 6;
+    int r = set[n - 1];
+    for (int i = 0; i < n; ++i)
+        if (set[i] >= need) { r = set[i]; break; }
+    *R = r;
+    *IT = 1;
+}
+
+hipError_t launch_gemv(int wt, bool int_path, int pro, int epi, const GemvArgs &a, hipStream_t s) {
+    if (a.m <= 0) return hipSuccess;
+    const int epc = int_path ? (wt == WT_Q4 ? 32 : 16) : (wt == WT_F32 ? 4 : wt == WT_Q8 ? 16 : 8);
+    const int nchunk = a.K / epc;
+    int M, R, IT;
+    if (int_path) {
+        M = a.m <= 1 ? 1 : a.m <= 2 ? 2 : a.m <= 4 ? 4 : a.m <= 8 ? 8 : 0;
+    } else {
+        M = a.m <= 1 ? 1 : a.m <= 4 ? 4 : 0;
+    }
+    if (!M) return hipErrorInvalidValue;
+    gemv_tile(a.rows, nchunk, M, epi == EPI_SWIGLU, &R, &IT);
+    if (int_path) {
+        if (wt == WT_Q8) return launch_gemv_int_q8(pro, epi, M, R, IT, a, s);
+        if (wt == WT_Q4) return launch_gemv_int_q4(pro, epi, M, R, IT, a, s);
+        return hipErrorInvalidValue;
+    }
+    switch (wt) {
+        case WT_F32: return launch_gemv_flt_f32(pro, epi, M, R, IT, a, s);
+        case WT_F16: return launch_gemv_flt_f16(pro, epi, M, R, IT, a, s);
+        case WT_BF16: return launch_gemv_flt_bf16(pro, epi, M, R, IT, a, s);
+        case WT_Q8: return launch_gemv_flt_q8(pro, epi, M, R, IT, a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace vh

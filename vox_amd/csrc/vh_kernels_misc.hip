@@ -1,7 +1,7 @@
 // Launchers of the non-GEMV kernels: q/k post-processing, attention, sampler, quantizers, synthetic data.
 #include <atomic>
 #include <mutex>
-#include <set>
+#include <map>
 
 #include "vh_attn.hpp"
 #include "vh_launch.hpp"
@@ -44,11 +44,12 @@ bool timing_take(hipEvent_t *start, hipEvent_t *stop) {
 hipError_t ensure_smem(const void *kernel, size_t bytes) {
     if (bytes <= 65536) return hipSuccess;
     static std::mutex mu;
-    static std::set<const void *> done;
+    static std::map<const void *, size_t> done;  // largest size opted in per kernel
     std::lock_guard<std::mutex> lk(mu);
-    if (done.count(kernel)) return hipSuccess;
+    auto it = done.find(kernel);
+    if (it != done.end() && it->second >= bytes) return hipSuccess;
     hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
-    if (e == hipSuccess) done.insert(kernel);
+    if (e == hipSuccess) done[kernel] = bytes;
     return e;
 }
 
@@ -58,41 +59,47 @@ hipError_t launch_qk_post(const QkArgs &a, int m, hipStream_t s) {
 }
 
 template <int HD, int G>
-static hipError_t attn_hg(const AttnArgs &a, int m, hipStream_t s) {
-    constexpr int LPK = HD / 8, NGRP = 4 * (64 / LPK);
-    const size_t smem = size_t(NGRP) * G * (HD + 2) * 4;
-    const void *k = reinterpret_cast<const void *>(&k_attn_partial<HD, G>);
-    hipError_t e = ensure_smem(k, smem);
+static hipError_t attn_hg(const AttnArgs &a, int m, bool fused, hipStream_t s) {
+    const size_t smem = sizeof(AttnSmem<HD, G>);
+    const dim3 grid(kAttnMaxSplits, a.kv_heads, m);
+    if (fused) {
+        hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_attn<HD, G, true>), smem);
+        if (e != hipSuccess) return e;
+        return launch(k_attn<HD, G, true>, grid, dim3(256), smem, s, a);
+    }
+    hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_attn<HD, G, false>), smem);
     if (e != hipSuccess) return e;
-    e = launch(k_attn_partial<HD, G>, dim3(kAttnSplits, a.kv_heads, m), dim3(256), smem, s, a);
-    if (e != hipSuccess) return e;
-    return launch(k_attn_combine<HD>, dim3(a.heads, m), dim3(HD), 0, s, a);
+    return launch(k_attn<HD, G, false>, grid, dim3(256), smem, s, a);
 }
 
 template <int HD>
-static hipError_t attn_h(const AttnArgs &a, int group, int m, hipStream_t s) {
+static hipError_t attn_h(const AttnArgs &a, int group, int m, bool fused, hipStream_t s) {
     switch (group) {
-        case 1: return attn_hg<HD, 1>(a, m, s);
-        case 2: return attn_hg<HD, 2>(a, m, s);
-        case 3: return attn_hg<HD, 3>(a, m, s);
-        case 4: return attn_hg<HD, 4>(a, m, s);
-        case 5: return attn_hg<HD, 5>(a, m, s);
-        case 6: return attn_hg<HD, 6>(a, m, s);
-        case 7: return attn_hg<HD, 7>(a, m, s);
-        case 8: return attn_hg<HD, 8>(a, m, s);
+        case 1: return attn_hg<HD, 1>(a, m, fused, s);
+        case 2: return attn_hg<HD, 2>(a, m, fused, s);
+        case 3: return attn_hg<HD, 3>(a, m, fused, s);
+        case 4: return attn_hg<HD, 4>(a, m, fused, s);
+        case 5: return attn_hg<HD, 5>(a, m, fused, s);
+        case 6: return attn_hg<HD, 6>(a, m, fused, s);
+        case 7: return attn_hg<HD, 7>(a, m, fused, s);
+        case 8: return attn_hg<HD, 8>(a, m, fused, s);
         default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_attention(const AttnArgs &a, int hd, int group, int m, hipStream_t s) {
+hipError_t launch_attention(const AttnArgs &a, int hd, int group, int m, bool fused, hipStream_t s) {
     if (m <= 0) return hipSuccess;
-    if (hd == 128) return attn_h<128>(a, group, m, s);
-    if (hd == 64) return attn_h<64>(a, group, m, s);
+    if (hd == 128) return attn_h<128>(a, group, m, fused, s);
+    if (hd == 64) return attn_h<64>(a, group, m, fused, s);
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_sample(const SampleCfgDev *cfg, const float *logits, int n, int32_t *out, hipStream_t s) {
-    return launch(k_sample, dim3(1), dim3(kSampleThreads), 0, s, cfg, logits, n, out);
+    if (n <= 0 || n > kSampleMaxN) return hipErrorInvalidValue;
+    const size_t smem = sample_smem_bytes(n);
+    hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_sample), smem);
+    if (e != hipSuccess) return e;
+    return launch(k_sample, dim3(1), dim3(kSampleThreads), smem, s, cfg, logits, n, out);
 }
 
 static dim3 grid1(int64_t n, int bs) { return dim3(unsigned((n + bs - 1) / bs)); }

@@ -23,15 +23,14 @@ hipError_t launch(K kernel, dim3 grid, dim3 block, size_t smem, hipStream_t s, A
 }
 
 // GEMV launch: rows/K/m etc. in a; wt = weight type; int_path = int8 activations (Q8 m <= 8, Q4 always).
-// Picks the row tile (R rows per wave, IT 1 KiB chunks in flight) from the matrix shape.
+// Picks the row block M and the tile (R rows per wave, IT 1 KiB chunks in flight per row) from the shape.
 hipError_t launch_gemv(int wt, bool int_path, int pro, int epi, const GemvArgs &a, hipStream_t s);
-hipError_t launch_gemv_int_q8(int pro, int epi, int M, int R, const GemvArgs &a, hipStream_t s);
-hipError_t launch_gemv_int_q4(int pro, int epi, int M, int R, const GemvArgs &a, hipStream_t s);
-hipError_t launch_gemv_flt(int wt, int pro, int epi, int M, int R, const GemvArgs &a, hipStream_t s);
+void gemv_tile(int rows, int nchunk, int M, bool swiglu, int *R, int *IT);
 
 hipError_t launch_qk_post(const QkArgs &a, int m, hipStream_t s);
-// Split-K attention + combine: q (a.q) against each row's cache, output in a.out.
-hipError_t launch_attention(const AttnArgs &a, int hd, int group, int m, hipStream_t s);
+// Split-K attention partials of m rows (merged by the PRO_ATTN GEMV prologue). fused: rows of distinct sequences,
+// q/k post-processing and the K/V append happen inside; otherwise k_qk_post ran first.
+hipError_t launch_attention(const AttnArgs &a, int hd, int group, int m, bool fused, hipStream_t s);
 hipError_t launch_sample(const SampleCfgDev *cfg, const float *logits, int n, int32_t *out, hipStream_t s);
 
 hipError_t launch_quant_q8(const float *w, int64_t nblocks, int8_t *q, float *scale, hipStream_t s);

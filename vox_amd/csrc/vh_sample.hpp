@@ -4,15 +4,19 @@
 //   mask [suppress_from, suppress_to) except eos, block eos -> repetition penalty (each seen token once)
 //   -> greedy (T <= 0: first maximum) | top-k by (value desc, index asc) -> softmax in double over the
 //   top-k at 1/T -> top-p minimal prefix -> inverse CDF with u = Philox(frame, codebook, draw).
-// Exactness: the top-k set and its order are exact (64-bit keys (ordered value, ~index), radix select, bitonic
-// sort); the probabilities are double; every sum runs sequentially in sorted order like the reference
-// (one wave, values staged through lane reads). Only exp() may differ from glibc by an ulp of a double.
+// Exactness: the top-k set and its order are exact (64-bit keys (ordered value, ~index): a radix select finds
+// the k-th key, the k selected keys are bitonic-sorted); the probabilities are double; every sum runs
+// sequentially in sorted order like the reference (one wave, values broadcast lane by lane). Only exp() may
+// differ from glibc by an ulp of a double.
+//
+// Cost shape for the talker head (n = 3072, k = 50): one radix pass per 8 key bits until the k-th key's bucket
+// holds exactly the keys still needed (usually 2-3 passes; each pass is one LDS-atomic histogram and one wave
+// scan of its 256 bins), then a register bitonic sort of 64 lanes in one wave. k > 64 sorts in LDS.
 #pragma once
 #include "vh_common.hpp"
 #include "vh_types.hpp"
 
 namespace vh {
-
 
 // Order-preserving map of a float to uint32 (larger value -> larger key); -0 == +0; NaN lowest.
 VH_DEV uint32_t ord_key(float f) {
@@ -29,46 +33,42 @@ VH_DEV double readlane_d(double v, int j) {
     const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b >> 32)), j));
     return __longlong_as_double(int64_t(uint64_t(hi) << 32 | lo));
 }
-
-// Exclusive block scan of one int per thread (1024 threads). tmp: 16 ints.
-VH_DEV int block_excl_scan(int v, int *tmp, int *total) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    int inc = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int t = __shfl_up(inc, o, 64);
-        if (lane >= o) inc += t;
-    }
-    __syncthreads();
-    if (lane == 63) tmp[w] = inc;
-    __syncthreads();
-    int before = 0, all = 0;
-    for (int i = 0; i < kSampleThreads / 64; ++i) {
-        if (i < w) before += tmp[i];
-        all += tmp[i];
-    }
-    *total = all;
-    return before + inc - v;
+VH_DEV uint64_t readlane_u64(uint64_t v, int j) {
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v)), j));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v >> 32)), j));
+    return uint64_t(hi) << 32 | lo;
+}
+VH_DEV uint64_t shfl_xor_u64(uint64_t v, int m) {
+    const uint32_t lo = uint32_t(__shfl_xor(int(uint32_t(v)), m, kWave));
+    const uint32_t hi = uint32_t(__shfl_xor(int(uint32_t(v >> 32)), m, kWave));
+    return uint64_t(hi) << 32 | lo;
 }
 
-// out[0] = sampled index (or -1 when the request exceeds the kernel's limits).
+// Dynamic LDS of k_sample in bytes for n logits: room for the sorted keys of the LDS path.
+inline size_t sample_smem_bytes(int n) {
+    size_t k2 = 64;
+    while (k2 < size_t(n)) k2 <<= 1;
+    return k2 * sizeof(uint64_t);
+}
+
+// out[0] = sampled index (or -1 when n is outside 1..kSampleMaxN). Dynamic LDS: sample_smem_bytes(n).
 __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *cfgp, const float *logits, int32_t n,
                                                            int32_t *out) {
+    extern __shared__ __align__(16) uint64_t sample_keys[];
     __shared__ uint32_t seen[kSampleMaxN / 32];
     __shared__ uint32_t hist[256];
-    __shared__ int scan_tmp[16];
     __shared__ uint64_t sh_prefix;
-    __shared__ int sh_bits, sh_kk, sh_done;
-    __shared__ __align__(16) uint64_t sk[kSampleMaxK];  // selected keys; later the probabilities (double)
-    __shared__ int32_t sidx[kSampleMaxK];
+    __shared__ int sh_bits, sh_kk, sh_done, sh_cnt;
     __shared__ unsigned long long sh_best;
-    const int t = threadIdx.x, lane = t & 63;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const SampleCfgDev cfg = *cfgp;
     if (n <= 0 || n > kSampleMaxN) { if (t == 0) out[0] = -1; return; }
     constexpr int E = kSampleMaxN / kSampleThreads;
-    const int per = (n + kSampleThreads - 1) / kSampleThreads;  // contiguous indices per thread (index order)
+    const int per = (n + kSampleThreads - 1) / kSampleThreads;
 
     for (int i = t; i < kSampleMaxN / 32; i += kSampleThreads) seen[i] = 0u;
+    if (t < 256) hist[t] = 0u;
+    if (t == 0) { sh_prefix = 0ull; sh_bits = 0; sh_done = 0; sh_cnt = 0; sh_best = 0ull; }
     __syncthreads();
     if (cfg.rep != 1.0f && cfg.history)
         for (int i = t; i < cfg.n_history; i += kSampleThreads) {
@@ -77,10 +77,11 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *c
         }
     __syncthreads();
 
+    // keys of indices e * 1024 + t (coalesced); 0 marks "no logit"
     uint64_t key[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-        const int idx = t * per + e;
+        const int idx = e * kSampleThreads + t;
         key[e] = 0ull;
         if (e < per && idx < n) {
             float v = logits[idx];
@@ -92,130 +93,140 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *c
     }
 
     if (cfg.temperature <= 0.0f) {  // greedy: largest key = first maximum
-        if (t == 0) sh_best = 0ull;
-        __syncthreads();
         uint64_t b = 0;
 #pragma unroll
         for (int e = 0; e < E; ++e) b = key[e] > b ? key[e] : b;
-        atomicMax(&sh_best, (unsigned long long)b);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const uint64_t x = shfl_xor_u64(b, o);
+            b = x > b ? x : b;
+        }
+        if (lane == 0) atomicMax(&sh_best, (unsigned long long)b);
         __syncthreads();
         if (t == 0) out[0] = int32_t(0xFFFFFFFFu - uint32_t(sh_best));
         return;
     }
 
     const int k = (cfg.top_k > 0 && cfg.top_k < n) ? cfg.top_k : n;
-    if (k > kSampleMaxK) { if (t == 0) out[0] = -1; return; }
-
-    // ---- radix select: the k-th largest key's prefix, 8 bits per pass, stopping once the prefix bucket
-    // holds exactly the keys still needed.
-    if (t == 0) { sh_prefix = 0ull; sh_bits = 0; sh_kk = k; sh_done = 0; }
+    if (t == 0) sh_kk = k;
     __syncthreads();
+
+    // ---- radix select of the k-th largest key, 8 bits per pass. Wave 0 scans the histogram from the top bin
+    // down (4 bins per lane, a prefix sum over lanes) and clears each bin after reading it.
     for (int pass = 0; pass < 8; ++pass) {
-        for (int i = t; i < 256; i += kSampleThreads) hist[i] = 0u;
-        __syncthreads();
         const uint64_t P = sh_prefix;
         const int L = sh_bits, shift = 56 - 8 * pass;
 #pragma unroll
         for (int e = 0; e < E; ++e)
             if (key[e] && (L == 0 || (key[e] >> (64 - L)) == P)) atomicAdd(&hist[(key[e] >> shift) & 255u], 1u);
         __syncthreads();
-        if (t == 0) {
-            int kk = sh_kk, cum = 0, digit = 0, cnt = 0;
-            for (int d = 255; d >= 0; --d) {
-                const int c = int(hist[d]);
-                if (cum + c >= kk) { digit = d; cnt = c; break; }
-                cum += c;
+        if (wave == 0) {
+            int c[4], loc = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                c[j] = int(hist[255 - 4 * lane - j]);
+                loc += c[j];
             }
-            kk -= cum;
-            sh_prefix = (P << 8) | uint64_t(digit);
-            sh_bits = L + 8;
-            sh_kk = kk;
-            sh_done = cnt == kk;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) hist[255 - 4 * lane - j] = 0u;
+            int incl = loc;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int x = __shfl_up(incl, o, kWave);
+                if (lane >= o) incl += x;
+            }
+            const int kk = sh_kk;
+            const uint64_t bal = __ballot(incl >= kk);
+            const int first = __ffsll((long long)bal) - 1;
+            if (lane == first) {
+                int before = incl - loc, digit = 0, cnt = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (before + c[j] >= kk) { digit = 255 - 4 * lane - j; cnt = c[j]; break; }
+                    before += c[j];
+                }
+                sh_prefix = (P << 8) | uint64_t(digit);
+                sh_bits = L + 8;
+                sh_kk = kk - before;
+                sh_done = cnt == kk - before;
+            }
         }
         __syncthreads();
         if (sh_done) break;
     }
     const uint64_t P = sh_prefix;
     const int L = sh_bits;
-    auto selected = [&](uint64_t kv) { return kv != 0ull && (kv >> (64 - L)) >= P; };
-
-    // ---- compact the k selected keys (any order), pad to a power of two, bitonic sort descending
-    int mine = 0;
-#pragma unroll
-    for (int e = 0; e < E; ++e) mine += selected(key[e]) ? 1 : 0;
-    int total = 0;
-    int off = block_excl_scan(mine, scan_tmp, &total);
+    int K2 = 64;
+    while (K2 < k) K2 <<= 1;
+    // ---- the k selected keys (any order), padded with zeros (lowest) to K2
 #pragma unroll
     for (int e = 0; e < E; ++e)
-        if (selected(key[e]) && off < kSampleMaxK) sk[off++] = key[e];  // exactly k keys are selected
-    int K2 = 1;
-    while (K2 < k) K2 <<= 1;
-    for (int i = k + t; i < K2; i += kSampleThreads) sk[i] = 0ull;
+        if (key[e] && (key[e] >> (64 - L)) >= P) {
+            const int p = atomicAdd(&sh_cnt, 1);
+            if (p < K2) sample_keys[p] = key[e];
+        }
+    for (int i = k + t; i < K2; i += kSampleThreads) sample_keys[i] = 0ull;
     __syncthreads();
-    for (int size = 2; size <= K2; size <<= 1)
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = t; i < K2; i += kSampleThreads) {
-                const int l = i ^ stride;
-                if (l > i) {
-                    const uint64_t x = sk[i], y = sk[l];
-                    const bool desc = (i & size) == 0;
-                    if (desc ? (x < y) : (x > y)) { sk[i] = y; sk[l] = x; }
-                }
+
+    uint64_t v = 0ull;  // small path: lane j holds the j-th largest key
+    const bool small = K2 == 64;
+    if (small) {
+        if (wave != 0) return;
+        v = sample_keys[lane];
+#pragma unroll
+        for (int size = 2; size <= 64; size <<= 1)
+#pragma unroll
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                const uint64_t o = shfl_xor_u64(v, stride);
+                const bool keep_max = ((lane & stride) == 0) == ((lane & size) == 0);
+                v = keep_max ? (o > v ? o : v) : (o < v ? o : v);
             }
-            __syncthreads();
-        }
+    } else {
+        for (int size = 2; size <= K2; size <<= 1)
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                for (int i = t; i < K2; i += kSampleThreads) {
+                    const int l = i ^ stride;
+                    if (l > i) {
+                        const uint64_t x = sample_keys[i], y = sample_keys[l];
+                        const bool desc = (i & size) == 0;
+                        if (desc ? (x < y) : (x > y)) { sample_keys[i] = y; sample_keys[l] = x; }
+                    }
+                }
+                __syncthreads();
+            }
+        if (wave != 0) return;
+    }
 
-    // ---- probabilities in double (sampling.hpp:91-99)
+    // ---- probabilities in double (sampling.hpp:91-99), one wave, sums in sorted order
+    auto key_of = [&](int base) -> uint64_t {  // this lane's key of the chunk starting at `base`
+        if (small) return v;
+        return base + lane < k ? sample_keys[base + lane] : 0ull;
+    };
     const double inv_t = 1.0 / double(cfg.temperature);
-    const double mx = double(ord_val(uint32_t(sk[0] >> 32)));
-    double pv[kSampleMaxK / kSampleThreads];
-#pragma unroll
-    for (int r = 0; r < kSampleMaxK / kSampleThreads; ++r) {
-        const int i = t + r * kSampleThreads;
-        pv[r] = 0.0;
-        if (i < k) {
-            const uint64_t kv = sk[i];
-            sidx[i] = int32_t(0xFFFFFFFFu - uint32_t(kv));
-            pv[r] = exp((double(ord_val(uint32_t(kv >> 32))) - mx) * inv_t);
-        }
-    }
-    __syncthreads();
-    double *pr = reinterpret_cast<double *>(sk);
-#pragma unroll
-    for (int r = 0; r < kSampleMaxK / kSampleThreads; ++r) {
-        const int i = t + r * kSampleThreads;
-        if (i < k) pr[i] = pv[r];
-    }
-    __syncthreads();
-    if (t >= 64) return;
-
-    // ---- sequential sums in one wave, in sorted order
+    const double mx = double(ord_val(uint32_t((small ? readlane_u64(v, 0) : sample_keys[0]) >> 32)));
+    auto weight = [&](uint64_t kv, int i) -> double {
+        return i < k ? exp((double(ord_val(uint32_t(kv >> 32))) - mx) * inv_t) : 0.0;
+    };
     double sum = 0.0;
     for (int base = 0; base < k; base += 64) {
-        const double v = base + lane < k ? pr[base + lane] : 0.0;
+        const double w = weight(key_of(base), base + lane);
         const int cnt = k - base < 64 ? k - base : 64;
-        for (int j = 0; j < cnt; ++j) sum += readlane_d(v, j);
+        for (int j = 0; j < cnt; ++j) sum += readlane_d(w, j);
     }
-    // each lane normalizes exactly the entries it reads below (index base + lane), so no cross-lane hazard
-    for (int i = lane; i < k; i += 64) pr[i] = pr[i] / sum;
+    // top-p: the running sum that finds the minimal prefix is also the total over the kept prefix
+    const bool use_p = cfg.top_p > 0.0f && cfg.top_p < 1.0f;
     int keep = k;
-    if (cfg.top_p > 0.0f && cfg.top_p < 1.0f) {
-        double c = 0.0;
+    double tot = 0.0;
+    {
         bool found = false;
         for (int base = 0; base < k && !found; base += 64) {
-            const double v = base + lane < k ? pr[base + lane] : 0.0;
+            const double p = weight(key_of(base), base + lane) / sum;
             const int cnt = k - base < 64 ? k - base : 64;
             for (int j = 0; j < cnt; ++j) {
-                c += readlane_d(v, j);
-                if (c >= double(cfg.top_p)) { keep = base + j + 1; found = true; break; }
+                tot += readlane_d(p, j);
+                if (use_p && tot >= double(cfg.top_p)) { keep = base + j + 1; found = true; break; }
             }
         }
-    }
-    double tot = 0.0;
-    for (int base = 0; base < keep; base += 64) {
-        const double v = base + lane < keep ? pr[base + lane] : 0.0;
-        const int cnt = keep - base < 64 ? keep - base : 64;
-        for (int j = 0; j < cnt; ++j) tot += readlane_d(v, j);
     }
     const float u = det_uniform(cfg.key0, cfg.key1, cfg.frame, cfg.cb, cfg.draw);
     const double target = double(u) * tot;
@@ -223,14 +234,15 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *c
     int pick = keep - 1;
     bool hit = false;
     for (int base = 0; base < keep && !hit; base += 64) {
-        const double v = base + lane < keep ? pr[base + lane] : 0.0;
+        const double p = weight(key_of(base), base + lane) / sum;
         const int cnt = keep - base < 64 ? keep - base : 64;
         for (int j = 0; j < cnt; ++j) {
-            accp += readlane_d(v, j);
+            accp += readlane_d(p, j);
             if (target < accp) { pick = base + j; hit = true; break; }
         }
     }
-    if (lane == 0) out[0] = sidx[pick];
+    const uint64_t kp = small ? readlane_u64(v, pick) : sample_keys[pick];
+    if (lane == 0) out[0] = int32_t(0xFFFFFFFFu - uint32_t(kp));
 }
 
 }  // namespace vh

@@ -4,24 +4,10 @@
 
 namespace vh {
 
-enum { PRO_X = 0, PRO_RMS = 1 };
+// GEMV input prologues: x as is; RMSNorm(x, gamma); or the merge of split-K attention partials.
+enum { PRO_X = 0, PRO_RMS = 1, PRO_ATTN = 2 };
 enum { EPI_STORE = 0, EPI_ACC = 1, EPI_SWIGLU = 2 };
 enum { WT_F32 = 0, WT_F16 = 1, WT_BF16 = 2, WT_Q8 = 3, WT_Q4 = 4 };
-
-struct GemvArgs {
-    const uint8_t *w;     // weights, reference row layout
-    const float *scale;   // [rows][K/32] for Q8/Q4
-    const float *bias;    // [rows] or null
-    const float *x;       // [m][ldx]
-    const float *gamma;   // [K] (PRO_RMS)
-    float *y;             // [m][ldy]
-    float *xnorm;         // PRO_RMS: normed rows [m][K] written by block 0 (may be null)
-    int64_t ldx, ldy;
-    int32_t rows, K, m;
-    float eps;
-};
-
-constexpr int kGemvThreads = 256;
 
 // Cache view of one activation row: the sequence's cache bases (layer 0) and the row's absolute position.
 struct RowRef {
@@ -30,6 +16,39 @@ struct RowRef {
     int64_t cap;
     int64_t pos;
 };
+
+constexpr int kAttnMaxSplits = 8;  // split-K blocks per (row, kv head); the merge happens in the o-GEMV prologue
+constexpr int kAttnMinKeys = 64;   // fewer splits when there are fewer keys
+
+// Number of key splits for n visible keys (same on every kernel that reads the partials).
+__host__ __device__ inline int attn_splits(int64_t n) {
+    const int64_t s = (n + kAttnMinKeys - 1) / kAttnMinKeys;
+    return int(s < 1 ? 1 : s > kAttnMaxSplits ? kAttnMaxSplits : s);
+}
+
+// Split-K attention partials of m rows: running max, denominator and unnormalized output per (row, head, split).
+struct AttnPartials {
+    float *pm, *pl;  // [m][heads][kAttnMaxSplits]
+    float *po;       // [m][heads][kAttnMaxSplits][hd]
+    const RowRef *rows;
+    int32_t heads, hd;
+};
+
+struct GemvArgs {
+    const uint8_t *w;     // weights, reference row layout
+    const float *scale;   // [rows][K/32] for Q8/Q4
+    const float *bias;    // [rows] or null
+    const float *x;       // [m][ldx] (PRO_X, PRO_RMS)
+    const float *gamma;   // [K] (PRO_RMS)
+    float *y;             // [m][ldy]
+    float *xnorm;         // PRO_RMS / PRO_ATTN: block 0 writes the prologue's f32 rows [m][K] here (may be null)
+    AttnPartials attn;    // PRO_ATTN: K = heads * hd
+    int64_t ldx, ldy;
+    int32_t rows, K, m;
+    float eps;
+};
+
+constexpr int kGemvThreads = 256;
 
 struct QkArgs {
     const float *qkv;   // [m][qd + 2 kd] stacked q|k|v GEMV output
@@ -42,16 +61,18 @@ struct QkArgs {
     float eps;
 };
 
-constexpr int kAttnSplits = 64;  // grid.x of k_attn_partial; splits beyond the key count exit at once
-
+// Attention over each row's f16 cache. fused: the kernel also does what k_qk_post does (q/k RMSNorm, RoPE, K/V
+// append) for rows whose sequences differ (decode, pairs, B sessions); otherwise q comes from `q` and the keys of
+// this pass are already in the cache (prefill of one sequence).
 struct AttnArgs {
-    const float *q;      // [m][qd]
-    const RowRef *rows;  // [m]
-    float *pm, *pl;      // [m][heads][kAttnSplits]
-    float *po;           // [m][heads][kAttnSplits][hd]
-    float *out;          // [m][qd]
-    int32_t heads, kv_heads, layer;
-    float scale;
+    const float *qkv;    // fused: [m][ldqkv]
+    int64_t ldqkv;
+    const float *q;      // not fused: [m][qd]
+    const float *qn, *kn;
+    const float *rope;
+    AttnPartials part;
+    int32_t kv_heads, layer;
+    float scale, eps;
 };
 
 struct SampleCfgDev {
@@ -66,7 +87,6 @@ struct SampleCfgDev {
 };
 
 constexpr int kSampleThreads = 1024;
-constexpr int kSampleMaxN = 16384;  // 16 values per thread
-constexpr int kSampleMaxK = 4096;   // LDS sort capacity
+constexpr int kSampleMaxN = 16384;  // logits per call (keys sorted in LDS)
 
 }  // namespace vh

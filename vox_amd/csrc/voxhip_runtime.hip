@@ -78,7 +78,7 @@ struct Xfmr {
     float *rope = nullptr;
     int64_t rope_rows = 0;
     // scratch for kMaxM rows
-    float *h = nullptr, *xin = nullptr, *qkv = nullptr, *q = nullptr, *ao = nullptr, *g = nullptr, *xnorm = nullptr;
+    float *h = nullptr, *xin = nullptr, *qkv = nullptr, *q = nullptr, *g = nullptr, *xnorm = nullptr;
     float *pm = nullptr, *pl = nullptr, *po = nullptr, *logits = nullptr;
     int64_t xin_cols = 0, logits_cap = 0;
     RowRef *rows_dev = nullptr, *rows_host = nullptr;
@@ -200,14 +200,13 @@ size_t row_bytes(int32_t type, int64_t cols) {
 }
 bool quantized(int32_t t) { return t == VOXHIP_Q8 || t == VOXHIP_Q4; }
 
-// Checks the shape rules of the GEMV kernels: Q8/Q4 need cols % 32 (as kernels.cpp:655); the f32 path
-// reads 16-byte chunks, so F32 needs cols % 4 and F16/BF16 cols % 8.
+// Checks the shape rules of the GEMV kernels: Q8/Q4 need cols % 32 (as kernels.cpp:655); the activation
+// prologue stages inputs in 8-element slots, so F32/F16/BF16 need cols % 8.
 void check_shape(int32_t type, int64_t rows, int64_t cols) {
     if (type < VOXHIP_F32 || type > VOXHIP_Q4) throw Fail("unknown weight type " + std::to_string(type));
     if (rows <= 0 || cols <= 0 || rows > (int64_t(1) << 30)) throw Fail("bad matrix shape");
     if (quantized(type) && cols % 32) throw Fail("Q8/Q4 matrix needs cols % 32 == 0");
-    if (type == VOXHIP_F32 && cols % 4) throw Fail("F32 matrix needs cols % 4 == 0 on this backend");
-    if ((type == VOXHIP_F16 || type == VOXHIP_BF16) && cols % 8) throw Fail("F16/BF16 matrix needs cols % 8 == 0 on this backend");
+    if (!quantized(type) && cols % 8) throw Fail("F32/F16/BF16 matrix needs cols % 8 == 0 on this backend");
 }
 
 int new_mat(int32_t type, int64_t rows, int64_t cols, bool bias) {
@@ -289,10 +288,14 @@ bool int_path(const GpuMat &m, int64_t m_total) {
 int rows_per_pass(const GpuMat &m, int64_t m_total) { return int_path(m, m_total) ? kMaxM : 4; }
 
 void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, int64_t ldx, int mc, float *y, int64_t ldy,
-          const float *gamma, float eps, float *xnorm, hipStream_t s) {
-    GemvArgs a;
+          const float *gamma, float eps, float *xnorm, hipStream_t s, const AttnPartials *attn = nullptr) {
+    GemvArgs a{};
     a.w = m.w; a.scale = m.s; a.bias = m.b; a.x = x; a.gamma = gamma; a.y = y; a.xnorm = xnorm;
     a.ldx = ldx; a.ldy = ldy; a.rows = int32_t(m.rows); a.K = int32_t(m.cols); a.m = mc; a.eps = eps;
+    if (pro == PRO_ATTN) {
+        if (!attn || int64_t(attn->heads) * attn->hd != m.cols) throw Fail("attention partials do not match the o projection");
+        a.attn = *attn;
+    }
     HIPCHECK(launch_gemv(m.type, int_path(m, m_total), pro, epi, a, s));
 }
 
@@ -322,12 +325,11 @@ void alloc_scratch(Xfmr &X) {
     X.h = dalloc_t<float>(M * X.H);
     X.qkv = dalloc_t<float>(M * (qd + 2 * kd));
     X.q = dalloc_t<float>(M * qd);
-    X.ao = dalloc_t<float>(M * qd);
     X.g = dalloc_t<float>(M * X.I);
     X.xnorm = dalloc_t<float>(M * X.H);
-    X.pm = dalloc_t<float>(M * X.heads * kAttnSplits);
-    X.pl = dalloc_t<float>(M * X.heads * kAttnSplits);
-    X.po = dalloc_t<float>(M * X.heads * kAttnSplits * X.hd);
+    X.pm = dalloc_t<float>(M * X.heads * kAttnMaxSplits);
+    X.pl = dalloc_t<float>(M * X.heads * kAttnMaxSplits);
+    X.po = dalloc_t<float>(M * X.heads * kAttnMaxSplits * X.hd);
     X.rows_dev = dalloc_t<RowRef>(M);
     HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&X.rows_host), M * sizeof(RowRef), hipHostMallocDefault));
     X.scfg_dev = dalloc_t<SampleCfgDev>(1);
@@ -366,27 +368,60 @@ void set_rows(Xfmr &X, const std::vector<RowRef> &rows) {
     X.rows_valid = true;
 }
 
+// Observer of the launches of one pass (the benchmark's per-kernel timing): before(class) and after() bracket
+// every kernel launch enqueue_layers / enqueue_final / the sampler make.
+struct Probe {
+    virtual void before(int cls) = 0;
+    virtual void after() = 0;
+    virtual ~Probe() = default;
+};
+template <class F>
+void probed(Probe *pr, int cls, F &&f) {
+    if (pr) pr->before(cls);
+    f();
+    if (pr) pr->after();
+}
+
+AttnPartials partials_of(const Xfmr &X) {
+    AttnPartials p;
+    p.pm = X.pm; p.pl = X.pl; p.po = X.po; p.rows = X.rows_dev; p.heads = X.heads; p.hd = X.hd;
+    return p;
+}
+
+// Kernels per layer: fused (rows of distinct sequences: decode, pairs, B sessions) 5, else 6 (+ k_qk_post).
+int kernels_per_layer(bool fused) { return fused ? 5 : 6; }
+
 // All layers for mc rows whose input is in X.h (row i at the position in rows_dev[i]).
 // m_total: the caller's total row count, which picks the q8 arithmetic (int8 for <= 8, f32 above).
-void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipStream_t s) {
+// fused: every row belongs to a different sequence, so the attention kernel can append K/V itself.
+void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipStream_t s, bool fused, Probe *pr = nullptr) {
     const int qd = X.heads * X.hd, kd = X.kvh * X.hd, ldqkv = qd + 2 * kd;
+    const AttnPartials part = partials_of(X);
     for (int li = first; li < first + count; ++li) {
         const LayerDev &L = X.L[size_t(li)];
         const GpuMat &Mqkv = g.mats[size_t(L.qkv)], &Mo = g.mats[size_t(L.o)], &Mgu = g.mats[size_t(L.gu)],
                      &Md = g.mats[size_t(L.down)];
-        gemv(Mqkv, m_total, PRO_RMS, EPI_STORE, X.h, X.H, mc, X.qkv, ldqkv, X.norms + L.ln1, X.eps, nullptr, s);
-        QkArgs qa;
-        qa.qkv = X.qkv; qa.ldqkv = ldqkv; qa.q = X.q; qa.rows = X.rows_dev;
-        qa.qn = L.qk ? X.norms + L.qn : nullptr; qa.kn = L.qk ? X.norms + L.kn : nullptr;
-        qa.rope = X.rope; qa.heads = X.heads; qa.kv_heads = X.kvh; qa.hd = X.hd; qa.layer = li; qa.eps = X.eps;
-        HIPCHECK(launch_qk_post(qa, mc, s));
+        const float *qn = L.qk ? X.norms + L.qn : nullptr, *kn = L.qk ? X.norms + L.kn : nullptr;
+        probed(pr, VOXHIP_K_QKV, [&] {
+            gemv(Mqkv, m_total, PRO_RMS, EPI_STORE, X.h, X.H, mc, X.qkv, ldqkv, X.norms + L.ln1, X.eps, nullptr, s);
+        });
+        if (!fused) {
+            QkArgs qa;
+            qa.qkv = X.qkv; qa.ldqkv = ldqkv; qa.q = X.q; qa.rows = X.rows_dev; qa.qn = qn; qa.kn = kn;
+            qa.rope = X.rope; qa.heads = X.heads; qa.kv_heads = X.kvh; qa.hd = X.hd; qa.layer = li; qa.eps = X.eps;
+            probed(pr, VOXHIP_K_QKPOST, [&] { HIPCHECK(launch_qk_post(qa, mc, s)); });
+        }
         AttnArgs aa;
-        aa.q = X.q; aa.rows = X.rows_dev; aa.pm = X.pm; aa.pl = X.pl; aa.po = X.po; aa.out = X.ao;
-        aa.heads = X.heads; aa.kv_heads = X.kvh; aa.layer = li; aa.scale = 1.0f / std::sqrt(float(X.hd));
-        HIPCHECK(launch_attention(aa, X.hd, X.heads / X.kvh, mc, s));
-        gemv(Mo, m_total, PRO_X, EPI_ACC, X.ao, qd, mc, X.h, X.H, nullptr, 0.f, nullptr, s);
-        gemv(Mgu, m_total, PRO_RMS, EPI_SWIGLU, X.h, X.H, mc, X.g, X.I, X.norms + L.ln2, X.eps, nullptr, s);
-        gemv(Md, m_total, PRO_X, EPI_ACC, X.g, X.I, mc, X.h, X.H, nullptr, 0.f, nullptr, s);
+        aa.qkv = X.qkv; aa.ldqkv = ldqkv; aa.q = X.q; aa.qn = qn; aa.kn = kn; aa.rope = X.rope; aa.part = part;
+        aa.kv_heads = X.kvh; aa.layer = li; aa.scale = 1.0f / std::sqrt(float(X.hd)); aa.eps = X.eps;
+        probed(pr, VOXHIP_K_ATTN, [&] { HIPCHECK(launch_attention(aa, X.hd, X.heads / X.kvh, mc, fused, s)); });
+        probed(pr, VOXHIP_K_O, [&] {
+            gemv(Mo, m_total, PRO_ATTN, EPI_ACC, nullptr, 0, mc, X.h, X.H, nullptr, 0.f, nullptr, s, &part);
+        });
+        probed(pr, VOXHIP_K_GATEUP, [&] {
+            gemv(Mgu, m_total, PRO_RMS, EPI_SWIGLU, X.h, X.H, mc, X.g, X.I, X.norms + L.ln2, X.eps, nullptr, s);
+        });
+        probed(pr, VOXHIP_K_DOWN, [&] { gemv(Md, m_total, PRO_X, EPI_ACC, X.g, X.I, mc, X.h, X.H, nullptr, 0.f, nullptr, s); });
     }
 }
 
@@ -447,7 +482,11 @@ void forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_pro
         } else {
             HIPCHECK(hipMemcpyAsync(X.h, pin, size_t(mc * H) * 4, hipMemcpyHostToDevice, g.stream));
         }
-        enqueue_layers(X, mc, m_total, first_layer, n_layers, g.stream);
+        bool fused = true;
+        for (int i = 0; i < mc && fused; ++i)
+            for (int j = 0; j < i; ++j)
+                if (rr[size_t(i)].k == rr[size_t(j)].k) { fused = false; break; }
+        enqueue_layers(X, mc, m_total, first_layer, n_layers, g.stream, fused);
         if (hidden_out) {
             HIPCHECK(hipMemcpyAsync(pin, X.h, size_t(mc * H) * 4, hipMemcpyDeviceToHost, g.stream));
             HIPCHECK(hipStreamSynchronize(g.stream));
@@ -882,8 +921,6 @@ int voxhip_sample_logits(const float *logits, int32_t n, const voxhip_sample_cfg
         require_ok();
         if (!cfg || !out_id || !logits) throw Fail("missing argument");
         if (n <= 0 || n > kSampleMaxN) throw Fail("sampler supports 1..16384 logits");
-        const int k = (cfg->top_k > 0 && cfg->top_k < n) ? cfg->top_k : n;
-        if (cfg->temperature > 0.f && k > kSampleMaxK) throw Fail("sampler supports top-k up to 4096 candidates");
         if (!g.scfg_dev) {
             g.scfg_dev = dalloc_t<SampleCfgDev>(1);
             HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&g.scfg_host), sizeof(SampleCfgDev), hipHostMallocDefault));
@@ -955,21 +992,25 @@ int voxhip_sync(void) {
 }  // extern "C"
 
 namespace {
-// Enqueues one device-resident decode step on stream s (no host copies).
+// Enqueues one device-resident decode step on stream s (no host copies). m rows of one sequence at pos0 + i:
+// one row takes the fused attention; several rows of the same sequence append their keys first (k_qk_post).
 int enqueue_decode(Xfmr &X, int m, int head, const float *d_x, float *d_out_last, float *d_logits, bool sample, int32_t *d_token,
-                   hipStream_t s) {
+                   hipStream_t s, Probe *pr = nullptr) {
+    const bool fused = m == 1;
     int kernels = 0;
     HIPCHECK(hipMemcpyAsync(X.h, d_x, size_t(m) * X.H * 4, hipMemcpyDeviceToDevice, s));
-    enqueue_layers(X, m, m, 0, X.layers, s);
-    kernels += 7 * X.layers;
-    enqueue_final(X, m - 1, 1, head, s);
+    enqueue_layers(X, m, m, 0, X.layers, s, fused, pr);
+    kernels += kernels_per_layer(fused) * X.layers;
+    probed(head >= 0 ? pr : nullptr, VOXHIP_K_HEAD, [&] { enqueue_final(X, m - 1, 1, head, s); });
     kernels += 1;
     if (d_out_last) HIPCHECK(hipMemcpyAsync(d_out_last, X.xnorm, size_t(X.H) * 4, hipMemcpyDeviceToDevice, s));
     if (head >= 0) {
         const GpuMat &Hm = g.mats[size_t(head)];
         if (d_logits) HIPCHECK(hipMemcpyAsync(d_logits, X.logits, size_t(Hm.rows) * 4, hipMemcpyDeviceToDevice, s));
         if (sample) {
-            HIPCHECK(launch_sample(X.scfg_dev, X.logits, int(Hm.rows), d_token ? d_token : X.token_dev, s));
+            probed(pr, VOXHIP_K_SAMPLE, [&] {
+                HIPCHECK(launch_sample(X.scfg_dev, X.logits, int(Hm.rows), d_token ? d_token : X.token_dev, s));
+            });
             kernels += 1;
         }
     }
@@ -1182,31 +1223,31 @@ bool profiler_attached() {
 
 extern "C" {
 
-int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, int head, const voxhip_sample_cfg *cfg, int warmup, int steps,
-                        voxhip_bench_result *out) {
+int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, const float *d_x, int head, const voxhip_sample_cfg *cfg,
+                        int32_t *d_token, int warmup, int steps, voxhip_bench_result *out) {
     return guard_int([&] {
         require_ok();
-        if (!out || steps <= 0) throw Fail("bad bench arguments");
+        if (!out || steps <= 0 || !d_x) throw Fail("bad bench arguments");
         Xfmr &X = xf_at(xfmr);
         Seq &S = seq_at(seq);
         check_seq_for(X, xfmr, S);
         std::memset(out, 0, sizeof *out);
+        const bool trace = std::getenv("VOXHIP_TRACE") != nullptr;
+        auto mark = [&](const char *what) {
+            if (trace) std::fprintf(stderr, "[voxhip bench] %s\n", what);
+        };
         prepare_decode(X, S, pos0, 1, head, cfg);
-        float *dx = dalloc_t<float>(size_t(X.H));
+        const float *dx = d_x;
         std::vector<hipEvent_t> ev;
-        const GraphKey key{seq, 1, head, cfg != nullptr ? 1 : 0, dx, nullptr, nullptr, nullptr};
         auto cleanup = [&] {
             (void)hipStreamSynchronize(g.stream);
             timing_clear();
             for (auto &e : ev) (void)hipEventDestroy(e);
-            auto it = X.graphs.find(key);
-            if (it != X.graphs.end()) { (void)hipGraphExecDestroy(it->second); X.graphs.erase(it); }
-            dfree(dx);
         };
         try {
-            HIPCHECK(launch_fill_normal(dx, X.H, 7, 0x7777u, 0.f, 1.f, g.stream));
-            // ---- region A: graph replays
-            hipGraphExec_t exec = decode_graph(X, seq, 1, head, dx, nullptr, nullptr, cfg != nullptr, nullptr);
+            // ---- region A: graph replays (the same graph voxhip_decode_dev replays for these arguments)
+            mark("graph");
+            hipGraphExec_t exec = decode_graph(X, seq, 1, head, dx, nullptr, nullptr, cfg != nullptr, d_token);
             for (int i = 0; i < warmup; ++i) HIPCHECK(hipGraphLaunch(exec, g.stream));
             ev.resize(2);
             for (auto &e : ev) HIPCHECK(hipEventCreate(&e));
@@ -1218,102 +1259,69 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, int head, const voxhip_
             float ms = 0.f;
             HIPCHECK(hipEventElapsedTime(&ms, ev[0], ev[1]));
             out->ms_per_step = double(ms) / steps;
-            // ---- region B: the same step launched kernel by kernel, each stamped by its own events
-            const int nl = X.layers;
-            const int per_step = 7 * nl + (head >= 0 ? 1 : 0) + (cfg && head >= 0 ? 1 : 0);
+            mark("kernel by kernel");
+            // ---- region B: the same step launched kernel by kernel (same enqueue path as the graph), each launch
+            // stamped by its own events: hipExtLaunchKernel start/stop, or plain stream events around the launch
+            // when a profiler intercepts launches
+            struct Stamps : Probe {
+                std::vector<hipEvent_t> *ev;
+                std::vector<int> cls;
+                bool stamp;
+                hipStream_t s;
+                int k = 0;
+                void before(int c) override {
+                    if (size_t(2 * k + 1) >= ev->size()) throw Fail("bench: more launches than expected");
+                    cls[size_t(k)] = c;
+                    if (stamp) timing_arm((*ev)[size_t(2 * k)], (*ev)[size_t(2 * k + 1)]);
+                    else HIPCHECK(hipEventRecord((*ev)[size_t(2 * k)], s));
+                }
+                void after() override {
+                    if (!stamp) HIPCHECK(hipEventRecord((*ev)[size_t(2 * k + 1)], s));
+                    ++k;
+                }
+            };
+            const int per_step = kernels_per_layer(true) * X.layers + (head >= 0 ? 1 : 0) + (cfg && head >= 0 ? 1 : 0);
             const bool stamp = !profiler_attached();
             for (auto &e : ev) (void)hipEventDestroy(e);
             ev.assign(size_t(2 * per_step), nullptr);
             for (auto &e : ev) HIPCHECK(hipEventCreate(&e));
-            std::vector<int> cls(static_cast<size_t>(per_step));
+            Stamps st;
+            st.ev = &ev; st.cls.assign(size_t(per_step), 0); st.stamp = stamp; st.s = g.stream;
             double sum_ms[VOXHIP_K_CLASSES] = {0};
             int cnt[VOXHIP_K_CLASSES] = {0};
-            const int qd = X.heads * X.hd, kd = X.kvh * X.hd, ldqkv = qd + 2 * kd;
             for (int it = 0; it < warmup + steps; ++it) {
-                HIPCHECK(hipMemcpyAsync(X.h, dx, size_t(X.H) * 4, hipMemcpyDeviceToDevice, g.stream));
-                int k = 0;
-                // kernel-stamped events (hipExtLaunchKernel) unless a profiler intercepts the launches, where plain
-                // stream events bracket each launch instead
-                auto arm = [&](int c) {
-                    cls[size_t(k)] = c;
-                    if (stamp) timing_arm(ev[size_t(2 * k)], ev[size_t(2 * k + 1)]);
-                    else HIPCHECK(hipEventRecord(ev[size_t(2 * k)], g.stream));
-                    ++k;
-                };
-                auto done = [&] {
-                    if (!stamp) HIPCHECK(hipEventRecord(ev[size_t(2 * (k - 1) + 1)], g.stream));
-                };
-                for (int li = 0; li < nl; ++li) {
-                    const LayerDev &L = X.L[size_t(li)];
-                    arm(VOXHIP_K_QKV);
-                    gemv(g.mats[size_t(L.qkv)], 1, PRO_RMS, EPI_STORE, X.h, X.H, 1, X.qkv, ldqkv, X.norms + L.ln1, X.eps, nullptr, g.stream);
-                    done();
-                    QkArgs qa;
-                    qa.qkv = X.qkv; qa.ldqkv = ldqkv; qa.q = X.q; qa.rows = X.rows_dev;
-                    qa.qn = L.qk ? X.norms + L.qn : nullptr; qa.kn = L.qk ? X.norms + L.kn : nullptr;
-                    qa.rope = X.rope; qa.heads = X.heads; qa.kv_heads = X.kvh; qa.hd = X.hd; qa.layer = li; qa.eps = X.eps;
-                    arm(VOXHIP_K_QKPOST);
-                    HIPCHECK(launch_qk_post(qa, 1, g.stream));
-                    done();
-                    AttnArgs aa;
-                    aa.q = X.q; aa.rows = X.rows_dev; aa.pm = X.pm; aa.pl = X.pl; aa.po = X.po; aa.out = X.ao;
-                    aa.heads = X.heads; aa.kv_heads = X.kvh; aa.layer = li; aa.scale = 1.0f / std::sqrt(float(X.hd));
-                    if (stamp) {
-                        arm(VOXHIP_K_ATTN);
-                        arm(VOXHIP_K_COMBINE);
-                    } else {  // both kernels inside one bracket; split evenly between the two classes below
-                        arm(VOXHIP_K_ATTN);
-                        cls[size_t(k - 1)] = -1;
-                    }
-                    HIPCHECK(launch_attention(aa, X.hd, X.heads / X.kvh, 1, g.stream));
-                    if (!stamp) done();
-                    arm(VOXHIP_K_O);
-                    gemv(g.mats[size_t(L.o)], 1, PRO_X, EPI_ACC, X.ao, qd, 1, X.h, X.H, nullptr, 0.f, nullptr, g.stream);
-                    done();
-                    arm(VOXHIP_K_GATEUP);
-                    gemv(g.mats[size_t(L.gu)], 1, PRO_RMS, EPI_SWIGLU, X.h, X.H, 1, X.g, X.I, X.norms + L.ln2, X.eps, nullptr, g.stream);
-                    done();
-                    arm(VOXHIP_K_DOWN);
-                    gemv(g.mats[size_t(L.down)], 1, PRO_X, EPI_ACC, X.g, X.I, 1, X.h, X.H, nullptr, 0.f, nullptr, g.stream);
-                    done();
-                }
-                if (head >= 0) {
-                    arm(VOXHIP_K_HEAD);
-                    enqueue_final(X, 0, 1, head, g.stream);
-                    done();
-                    if (cfg) {
-                        arm(VOXHIP_K_SAMPLE);
-                        HIPCHECK(launch_sample(X.scfg_dev, X.logits, int(g.mats[size_t(head)].rows), X.token_dev, g.stream));
-                        done();
-                    }
-                }
+                st.k = 0;
+                enqueue_decode(X, 1, head, dx, nullptr, nullptr, cfg != nullptr, d_token, g.stream, &st);
                 HIPCHECK(hipStreamSynchronize(g.stream));
-                if (k != (stamp ? per_step : per_step - nl)) throw Fail("bench launch count mismatch");
+                if (st.k != per_step) throw Fail("bench launch count mismatch");
                 if (it < warmup) continue;
-                for (int i = 0; i < k; ++i) {
+                for (int i = 0; i < st.k; ++i) {
                     float t = 0.f;
                     HIPCHECK(hipEventElapsedTime(&t, ev[size_t(2 * i)], ev[size_t(2 * i + 1)]));
-                    if (cls[size_t(i)] < 0) {
-                        for (int c : {int(VOXHIP_K_ATTN), int(VOXHIP_K_COMBINE)}) { sum_ms[c] += t / 2; cnt[c] += 1; }
-                    } else {
-                        sum_ms[cls[size_t(i)]] += t;
-                        cnt[cls[size_t(i)]] += 1;
-                    }
+                    sum_ms[st.cls[size_t(i)]] += t;
+                    cnt[st.cls[size_t(i)]] += 1;
                 }
             }
-            // ---- algorithmic bytes per launch of each class
-            const double kv_read = 2.0 * double(pos0 + 1) * kd * 2.0;  // K and V of the visible keys, f16, one layer
+            const int nl = X.layers;
+            // ---- algorithmic bytes per launch of each class: every byte the kernel must move once
+            // (weights + scales + bias, activations in and out, cache reads and appends, attention partials)
+            const int qd = X.heads * X.hd, kd = X.kvh * X.hd;
+            const double S = attn_splits(pos0 + 1);
+            const double partials = double(X.heads) * S * (X.hd + 2) * 4.0;
             double bytes[VOXHIP_K_CLASSES] = {0};
             for (const LayerDev &L : X.L) {
-                bytes[VOXHIP_K_QKV] += double(g.mats[size_t(L.qkv)].bytes) + X.H * 4.0;
-                bytes[VOXHIP_K_O] += double(g.mats[size_t(L.o)].bytes);
-                bytes[VOXHIP_K_GATEUP] += double(g.mats[size_t(L.gu)].bytes) + X.H * 4.0;
-                bytes[VOXHIP_K_DOWN] += double(g.mats[size_t(L.down)].bytes);
+                bytes[VOXHIP_K_QKV] += double(g.mats[size_t(L.qkv)].bytes) + X.H * 4.0 + (qd + 2.0 * kd) * 4.0;
+                bytes[VOXHIP_K_O] += double(g.mats[size_t(L.o)].bytes) + partials + 2.0 * X.H * 4.0;
+                bytes[VOXHIP_K_GATEUP] += double(g.mats[size_t(L.gu)].bytes) + X.H * 4.0 + X.I * 4.0;
+                bytes[VOXHIP_K_DOWN] += double(g.mats[size_t(L.down)].bytes) + X.I * 4.0 + 2.0 * X.H * 4.0;
             }
             for (int c = 0; c < 4; ++c) bytes[c] /= nl;
-            bytes[VOXHIP_K_ATTN] = kv_read;
-            bytes[VOXHIP_K_QKPOST] = 2.0 * kd * 2.0 + (X.L[0].qk ? 2.0 * X.hd * 4.0 : 0.0);
-            if (head >= 0) bytes[VOXHIP_K_HEAD] = double(g.mats[size_t(head)].bytes) + X.H * 4.0;
+            bytes[VOXHIP_K_ATTN] = 2.0 * double(pos0) * kd * 2.0 + (qd + 2.0 * kd) * 4.0 + 2.0 * kd * 2.0 + partials;
+            if (head >= 0) {
+                const GpuMat &Hm = g.mats[size_t(head)];
+                bytes[VOXHIP_K_HEAD] = double(Hm.bytes) + X.H * 4.0 + double(Hm.rows) * 4.0;
+                if (cfg) bytes[VOXHIP_K_SAMPLE] = double(Hm.rows) * 4.0;
+            }
             double total_ms = 0.0, step_bytes = 0.0;
             for (int c = 0; c < VOXHIP_K_CLASSES; ++c) {
                 out->class_launches[c] = steps > 0 ? cnt[c] / steps : 0;
@@ -1327,6 +1335,7 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, int head, const voxhip_
             out->kernels_per_step = per_step;
             out->n_classes = VOXHIP_K_CLASSES;
             out->kernel_stamped = stamp ? 1 : 0;
+            mark("done");
         } catch (...) {
             cleanup();
             throw;

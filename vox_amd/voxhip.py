@@ -115,7 +115,7 @@ SIGNATURES = {
     "voxhip_quantize_q8_dev": (_I, [_P, _I64, _I64, _P, _P]),
     "voxhip_quantize_q4_dev": (_I, [_P, _I64, _I64, _P, _P]),
     "voxhip_quantize_act_dev": (_I, [_P, _I64, _P, _P]),
-    "voxhip_bench_decode": (_I, [_I, _I, _I64, _I, C.POINTER(SampleCfg), _I, _I, C.POINTER(BenchResult)]),
+    "voxhip_bench_decode": (_I, [_I, _I, _I64, _P, _I, C.POINTER(SampleCfg), _P, _I, _I, C.POINTER(BenchResult)]),
     "voxhip_bench_gemv_q8": (_I, [_I64, _I64, _I, _I, _I, C.POINTER(C.c_double)]),
 }
 
@@ -430,10 +430,10 @@ def quantize_act_dev(x):
             b.free()
 
 
-def bench_decode(xfmr, seq, pos0, head, cfg, warmup, steps):
+def bench_decode(xfmr, seq, pos0, d_x, head, cfg, d_token, warmup, steps):
     r = BenchResult()
-    _check(lib().voxhip_bench_decode(xfmr, seq, pos0, head, None if cfg is None else C.byref(cfg), warmup, steps, C.byref(r)),
-           "bench_decode")
+    _check(lib().voxhip_bench_decode(xfmr, seq, pos0, d_x.ptr, head, None if cfg is None else C.byref(cfg),
+                                     None if d_token is None else d_token.ptr, warmup, steps, C.byref(r)), "bench_decode")
     return r
 
 
