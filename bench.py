@@ -149,10 +149,17 @@ def main():
     tok = int(dtok.download(1, np.int32)[0])
     log(f"timed {args.steps} steps: {ms_per_step * 1000:.1f} us/step, token {tok}")
 
+    # STREAM copy of 256 MiB (the measured HBM ceiling next to the 8 TB/s spec; also the kernel that calibrates
+    # the FETCH_SIZE / WRITE_SIZE counters in profiling runs)
+    copy_bytes = 256 << 20
+    copy_ms = vh.bench_copy(copy_bytes, 3, 10)
+    stream = {"kernel": "k_copy16", "bytes_read": copy_bytes, "bytes_written": copy_bytes,
+              "us": round(copy_ms * 1000, 2), "GBps": round(2 * copy_bytes / (copy_ms * 1e-3) / 1e9, 1)}
+    log(f"stream copy: {stream}")
     if args.no_breakdown:
         print(json.dumps({"metric": METRIC, "value": round(1000.0 / ms_per_step, 2), "unit": "tok/s", "n_gpus": 1,
                           "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
-                          "note": "--no-breakdown: graph replay only"}), flush=True)
+                          "stream": stream, "note": "--no-breakdown: graph replay only"}), flush=True)
         return
     r = vh.bench_decode(dec.xfmr, dec.seq, POS, dx, dec.head, cfg, dtok, max(3, args.warmup // 5), args.steps)
     classes = {}
@@ -207,6 +214,7 @@ def main():
                  "frac": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                  "kernel_us_per_step": round(r.kernel_ms_per_step * 1000, 2), "graph_us_per_step": round(r.ms_per_step * 1000, 2),
                  "kernels_per_step": r.kernels_per_step},
+        "stream": stream,
         "kernels": classes,
         "kernel_timing": "hipExtLaunchKernel start/stop events" if r.kernel_stamped else "stream events around each launch",
         "cpu_baseline": cpu,

@@ -246,6 +246,10 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, const float *d_x, int h
  * (rotating, so the working set exceeds the 256 MB Infinity Cache): average ms per launch. */
 int voxhip_bench_gemv_q8(int64_t rows, int64_t cols, int copies, int warmup, int iters, double *ms_per_launch);
 
+/* Times a plain 16-byte device copy of `bytes` (STREAM copy; reads and writes `bytes` each): average ms per copy.
+ * The same kernel calibrates the HBM traffic counters. No reference counterpart (benchmark helper). */
+int voxhip_bench_copy(int64_t bytes, int warmup, int iters, double *ms_per_copy);
+
 #ifdef __cplusplus
 }
 #endif

@@ -81,29 +81,70 @@ struct AttnSmem {
 };
 
 // grid (kAttnMaxSplits, kv_heads, m), block 256. Each lane holds 8 consecutive elements of one key row;
-// LPK = HD / 8 lanes share a key, a wave covers 64 / LPK keys per step, a block NGRP keys.
+// LPK = HD / 8 lanes share a key, a wave covers 64 / LPK keys per step, a block NGRP keys. Splits past the row's
+// key count write empty partials. Loads that do not depend on the row's cache view (q, the new key/value, the
+// RoPE row) are issued before it arrives; each lane group then loads all of its keys in one batch of U when the
+// split holds at most U * NGRP keys.
 template <int HD, int G, bool FUSED>
 __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     using Sm = AttnSmem<HD, G>;
-    constexpr int LPK = Sm::LPK, KPW = Sm::KPW, NGRP = Sm::NGRP, HALF = HD / 2, U = 4;
+    constexpr int LPK = Sm::LPK, KPW = Sm::KPW, NGRP = Sm::NGRP, HALF = HD / 2;
+    constexpr int U = G <= 2 ? 8 : G <= 4 ? 4 : 2;
+    constexpr int NQ = (G * HALF + 255) / 256;  // q rotate-half pairs per thread
     extern __shared__ __align__(16) uint8_t attn_smem[];
     Sm &sm = *reinterpret_cast<Sm *>(attn_smem);
     const int s = blockIdx.x, g = blockIdx.y, i = blockIdx.z, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, sub = lane % LPK, grp = wave * KPW + lane / LPK;
     const AttnPartials &P = a.part;
+    const int qd = P.heads * HD, kd = a.kv_heads * HD;
+    const float *row = a.qkv + int64_t(i) * a.ldqkv;
+
+    float qx0[NQ], qx1[NQ], qc[NQ], qsn[NQ];
+    float kx0 = 0.f, kx1 = 0.f, vx0 = 0.f, vx1 = 0.f, kc = 0.f, ksn = 0.f;
+    const bool kv_lane = tid >= 192 && tid - 192 < HALF;  // last wave: the new key/value of a fused row
+    if (FUSED) {
+        const float *cs = a.rope_rows + int64_t(i) * HD;
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) {
+            const int t = tid + 256 * k, h = t / HALF, p = t % HALF;
+            qx0[k] = qx1[k] = qc[k] = qsn[k] = 0.f;
+            if (t < G * HALF) {
+                qx0[k] = row[(g * G + h) * HD + p];
+                qx1[k] = row[(g * G + h) * HD + p + HALF];
+                qc[k] = cs[2 * p];
+                qsn[k] = cs[2 * p + 1];
+            }
+        }
+        if (kv_lane) {
+            const int p = tid - 192;
+            kx0 = row[qd + g * HD + p];
+            kx1 = row[qd + g * HD + p + HALF];
+            vx0 = row[qd + kd + g * HD + p];
+            vx1 = row[qd + kd + g * HD + p + HALF];
+            kc = cs[2 * p];
+            ksn = cs[2 * p + 1];
+        }
+    }
     const RowRef rr = P.rows[i];
     const int64_t n = rr.pos + 1;
     const int S = attn_splits(n);
-    if (s >= S) return;  // the consumer reads splits < S only
+    const int64_t pb = (int64_t(i) * P.heads + g * G) * kAttnMaxSplits + s;  // + h * kAttnMaxSplits
+    if (s >= S) {  // no keys in this split
+        for (int t = tid; t < G * HD; t += 256) {
+            const int h = t / HD, e = t % HD;
+            const int64_t pidx = pb + int64_t(h) * kAttnMaxSplits;
+            P.po[pidx * HD + e] = 0.f;
+            if (e == 0) { P.pm[pidx] = -INFINITY; P.pl[pidx] = 0.f; }
+        }
+        return;
+    }
     const int64_t C = (n + S - 1) / S, k0 = int64_t(s) * C, k1 = k0 + C < n ? k0 + C : n;
-    const int qd = P.heads * HD, kd = a.kv_heads * HD;
     const bool last = FUSED && s == S - 1;
     const int64_t cbase = (int64_t(a.layer) * a.kv_heads + g) * rr.cap * HD;
     const _Float16 *K = rr.k + cbase, *V = rr.v + cbase;
 
     // keys read from the cache: all of [k0, k1), except the new key of a fused row (processed from LDS below)
     const int64_t kend = last ? k1 - 1 : k1;
-    // issue the first batch of cache loads before the q prologue, which does not depend on them
     f16x8 kb[U], vb[U];
     const int64_t j0 = k0 + grp;
 #pragma unroll
@@ -115,24 +156,20 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
         }
     }
 
-    const float *row = a.qkv + int64_t(i) * a.ldqkv;
     if (FUSED) {
-        const float *cs = a.rope + rr.pos * HD;  // [HALF][2] (cos, sin) at pos
-        for (int t = tid; t < G * HALF; t += 256) {
-            const int h = t / HALF, p = t % HALF;
-            const float *src = row + (g * G + h) * HD;
-            float x0 = src[p], x1 = src[p + HALF];
-            norm_rope<HALF>(x0, x1, a.qn, p, a.eps, cs[2 * p], cs[2 * p + 1]);
-            sm.q[h][p] = x0;
-            sm.q[h][p + HALF] = x1;
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) {
+            const int t = tid + 256 * k, h = t / HALF, p = t % HALF;
+            if (t < G * HALF) {
+                norm_rope<HALF>(qx0[k], qx1[k], a.qn, p, a.eps, qc[k], qsn[k]);
+                sm.q[h][p] = qx0[k];
+                sm.q[h][p + HALF] = qx1[k];
+            }
         }
-        if (last && tid >= 256 - 64 && tid - (256 - 64) < HALF) {  // last wave: the new key and value
-            const int p = tid - (256 - 64);
-            const float *src = row + qd + g * HD;
-            float x0 = src[p], x1 = src[p + HALF];
-            norm_rope<HALF>(x0, x1, a.kn, p, a.eps, cs[2 * p], cs[2 * p + 1]);
-            const _Float16 k0h = _Float16(x0), k1h = _Float16(x1);
-            const _Float16 v0h = _Float16(src[kd + p]), v1h = _Float16(src[kd + p + HALF]);
+        if (last && kv_lane) {
+            const int p = tid - 192;
+            norm_rope<HALF>(kx0, kx1, a.kn, p, a.eps, kc, ksn);
+            const _Float16 k0h = _Float16(kx0), k1h = _Float16(kx1), v0h = _Float16(vx0), v1h = _Float16(vx1);
             const int64_t off = rr.pos * HD;
             _Float16 *Kw = rr.k + cbase, *Vw = rr.v + cbase;
             Kw[off + p] = k0h;
@@ -225,7 +262,6 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
         sm.w[q][h] = sm.m[q][h] == -INFINITY ? 0.f : expf(sm.m[q][h] - M);
     }
     __syncthreads();
-    const int64_t pb = (int64_t(i) * P.heads + g * G) * kAttnMaxSplits + s;  // + h * kAttnMaxSplits
     for (int t = tid; t < G * HD; t += 256) {
         const int h = t / HD, e = t % HD;
         float O = 0.f;

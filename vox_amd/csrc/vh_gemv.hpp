@@ -32,91 +32,138 @@ VH_DEV int64_t row_bytes(int K) {
 // ---------------------------------------------------------------------------------------------- prologue
 // Produces the f32 input rows v[mm][K] (mm < a.m; rows a.m..M-1 are zeros) in 8-element slots: slot s of row mm
 // holds elements 8s..8s+7, a 32-block is 4 consecutive slots handled by 4 consecutive lanes. `sink(mm, s, v)`
-// receives each slot; it runs with all 4 lanes of a block active.
+// receives each slot; it runs with all 4 lanes of a block active. Every input is read from global memory once:
+// PRO_RMS keeps its slots in registers between the sum of squares and the scaling when they fit (KS per thread).
 template <int M, int PRO, class Sink>
 VH_DEV void prologue(const GemvArgs &a, float *red, Sink &&sink) {
     const int K = a.K, spr = K / 8;  // slots per row
-    float inv[M];
+    const int nslot = M * spr;
+    auto load_x = [&](int mm, int sl, float (&v)[8]) {
+        const float *xr = a.x + int64_t(mm) * a.ldx + sl * 8;
+        const f32x4 t0 = *reinterpret_cast<const f32x4 *>(xr), t1 = *reinterpret_cast<const f32x4 *>(xr + 4);
+        v[0] = t0.x; v[1] = t0.y; v[2] = t0.z; v[3] = t0.w; v[4] = t1.x; v[5] = t1.y; v[6] = t1.z; v[7] = t1.w;
+    };
+    auto emit = [&](int mm, int sl, float (&v)[8]) {
+        if (PRO != PRO_X && a.xnorm && blockIdx.x == 0 && mm < a.m)
 #pragma unroll
-    for (int mm = 0; mm < M; ++mm) inv[mm] = 1.f;
+            for (int j = 0; j < 8; ++j) a.xnorm[int64_t(mm) * K + sl * 8 + j] = v[j];
+        sink(mm, sl, v);
+    };
     if (PRO == PRO_RMS) {
-        // pass 1: sum of squares of every row (kernels.cpp:709-710)
+        constexpr int KS = 4;
+        const bool in_regs = nslot <= KS * kGemvThreads;
+        float v[KS][8], gm[KS][8];
         float ss[M];
 #pragma unroll
-        for (int mm = 0; mm < M; ++mm) {
-            ss[mm] = 0.f;
-            if (mm < a.m)
-                for (int i = threadIdx.x; i < K / 4; i += kGemvThreads) {
-                    const f32x4 t = *reinterpret_cast<const f32x4 *>(a.x + int64_t(mm) * a.ldx + 4 * i);
-                    ss[mm] = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, ss[mm]))));
-                }
-            ss[mm] = wave_sum(ss[mm]);
+        for (int mm = 0; mm < M; ++mm) ss[mm] = 0.f;
+        // pass 1: sum of squares of every row (kernels.cpp:709-710), slots kept when they fit
+        for (int k = 0, s = threadIdx.x; s < nslot; ++k, s += kGemvThreads) {
+            const int mm = s / spr, sl = s % spr;
+            float t[8];
+            if (mm < a.m) load_x(mm, sl, t);
+            else
+#pragma unroll
+                for (int j = 0; j < 8; ++j) t[j] = 0.f;
+            float q = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) q = fmaf(t[j], t[j], q);
+#pragma unroll
+            for (int r = 0; r < M; ++r)
+                if (r == mm) ss[r] += q;
+            if (in_regs) {
+#pragma unroll
+                for (int kk = 0; kk < KS; ++kk)
+                    if (kk == k) {
+                        const f32x4 g0 = *reinterpret_cast<const f32x4 *>(a.gamma + sl * 8),
+                                    g1 = *reinterpret_cast<const f32x4 *>(a.gamma + sl * 8 + 4);
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) v[kk][j] = t[j];
+                        gm[kk][0] = g0.x; gm[kk][1] = g0.y; gm[kk][2] = g0.z; gm[kk][3] = g0.w;
+                        gm[kk][4] = g1.x; gm[kk][5] = g1.y; gm[kk][6] = g1.z; gm[kk][7] = g1.w;
+                    }
+            }
         }
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) ss[mm] = wave_sum(ss[mm]);
         if ((threadIdx.x & 63) == 0)
 #pragma unroll
             for (int mm = 0; mm < M; ++mm) red[mm * 4 + (threadIdx.x >> 6)] = ss[mm];
         __syncthreads();
+        float inv[M];
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) {
-            const float s = red[mm * 4] + red[mm * 4 + 1] + red[mm * 4 + 2] + red[mm * 4 + 3];
-            inv[mm] = 1.0f / sqrtf(s / float(K) + a.eps);
+            const float t = red[mm * 4] + red[mm * 4 + 1] + red[mm * 4 + 2] + red[mm * 4 + 3];
+            inv[mm] = 1.0f / sqrtf(t / float(K) + a.eps);
         }
+        // pass 2: w * (x * inv) (kernels.cpp:711)
+        for (int k = 0, s = threadIdx.x; s < nslot; ++k, s += kGemvThreads) {
+            const int mm = s / spr, sl = s % spr;
+            float t[8], gg[8];
+            if (in_regs) {
+#pragma unroll
+                for (int kk = 0; kk < KS; ++kk)
+                    if (kk == k)
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) { t[j] = v[kk][j]; gg[j] = gm[kk][j]; }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) t[j] = 0.f;
+                if (mm < a.m) load_x(mm, sl, t);
+                const f32x4 g0 = *reinterpret_cast<const f32x4 *>(a.gamma + sl * 8),
+                            g1 = *reinterpret_cast<const f32x4 *>(a.gamma + sl * 8 + 4);
+                gg[0] = g0.x; gg[1] = g0.y; gg[2] = g0.z; gg[3] = g0.w; gg[4] = g1.x; gg[5] = g1.y; gg[6] = g1.z; gg[7] = g1.w;
+            }
+            float iv = 0.f;
+#pragma unroll
+            for (int r = 0; r < M; ++r)
+                if (r == mm) iv = inv[r];
+            float o[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = mm < a.m ? gg[j] * (t[j] * iv) : 0.f;
+            emit(mm, sl, o);
+        }
+        return;
     }
-    for (int s = threadIdx.x; s < M * spr; s += kGemvThreads) {
+    for (int s = threadIdx.x; s < nslot; s += kGemvThreads) {
         const int mm = s / spr, sl = s % spr;
         float v[8];
         if (mm >= a.m) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[j] = 0.f;
         } else if (PRO == PRO_ATTN) {
+            // merge of all kAttnMaxSplits partials (empty splits have max -inf and weigh 0)
             const AttnPartials &P = a.attn;
             const int e0 = sl * 8, h = e0 / P.hd, d0 = e0 % P.hd;
-            const int S = attn_splits(P.rows[mm].pos + 1);
             const int64_t base = (int64_t(mm) * P.heads + h) * kAttnMaxSplits;
             float pm[kAttnMaxSplits], pl[kAttnMaxSplits];
             f32x4 o0[kAttnMaxSplits], o1[kAttnMaxSplits];
 #pragma unroll
-            for (int q = 0; q < kAttnMaxSplits; ++q)
-                if (q < S) {
-                    pm[q] = P.pm[base + q];
-                    pl[q] = P.pl[base + q];
-                    o0[q] = *reinterpret_cast<const f32x4 *>(P.po + (base + q) * P.hd + d0);
-                    o1[q] = *reinterpret_cast<const f32x4 *>(P.po + (base + q) * P.hd + d0 + 4);
-                }
+            for (int q = 0; q < kAttnMaxSplits; ++q) {
+                pm[q] = P.pm[base + q];
+                pl[q] = P.pl[base + q];
+                o0[q] = *reinterpret_cast<const f32x4 *>(P.po + (base + q) * P.hd + d0);
+                o1[q] = *reinterpret_cast<const f32x4 *>(P.po + (base + q) * P.hd + d0 + 4);
+            }
             float mx = -INFINITY;
 #pragma unroll
-            for (int q = 0; q < kAttnMaxSplits; ++q)
-                if (q < S) mx = fmaxf(mx, pm[q]);
+            for (int q = 0; q < kAttnMaxSplits; ++q) mx = fmaxf(mx, pm[q]);
             float L = 0.f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[j] = 0.f;
 #pragma unroll
-            for (int q = 0; q < kAttnMaxSplits; ++q)
-                if (q < S) {
-                    const float w = expf(pm[q] - mx);
-                    L = fmaf(w, pl[q], L);
-                    v[0] = fmaf(w, o0[q].x, v[0]); v[1] = fmaf(w, o0[q].y, v[1]); v[2] = fmaf(w, o0[q].z, v[2]); v[3] = fmaf(w, o0[q].w, v[3]);
-                    v[4] = fmaf(w, o1[q].x, v[4]); v[5] = fmaf(w, o1[q].y, v[5]); v[6] = fmaf(w, o1[q].z, v[6]); v[7] = fmaf(w, o1[q].w, v[7]);
-                }
+            for (int q = 0; q < kAttnMaxSplits; ++q) {
+                const float w = pm[q] == -INFINITY ? 0.f : expf(pm[q] - mx);
+                L = fmaf(w, pl[q], L);
+                v[0] = fmaf(w, o0[q].x, v[0]); v[1] = fmaf(w, o0[q].y, v[1]); v[2] = fmaf(w, o0[q].z, v[2]); v[3] = fmaf(w, o0[q].w, v[3]);
+                v[4] = fmaf(w, o1[q].x, v[4]); v[5] = fmaf(w, o1[q].y, v[5]); v[6] = fmaf(w, o1[q].z, v[6]); v[7] = fmaf(w, o1[q].w, v[7]);
+            }
             const float il = 1.0f / L;
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[j] *= il;
         } else {
-            const float *xr = a.x + int64_t(mm) * a.ldx + sl * 8;
-            const f32x4 t0 = *reinterpret_cast<const f32x4 *>(xr), t1 = *reinterpret_cast<const f32x4 *>(xr + 4);
-            v[0] = t0.x; v[1] = t0.y; v[2] = t0.z; v[3] = t0.w; v[4] = t1.x; v[5] = t1.y; v[6] = t1.z; v[7] = t1.w;
-            if (PRO == PRO_RMS) {
-                const f32x4 g0 = *reinterpret_cast<const f32x4 *>(a.gamma + sl * 8),
-                            g1 = *reinterpret_cast<const f32x4 *>(a.gamma + sl * 8 + 4);
-                const float gm[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-#pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] = gm[j] * (v[j] * inv[mm]);  // w * (x * inv), kernels.cpp:711
-            }
+            load_x(mm, sl, v);
         }
-        if (PRO != PRO_X && a.xnorm && blockIdx.x == 0 && mm < a.m)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) a.xnorm[int64_t(mm) * K + sl * 8 + j] = v[j];
-        sink(mm, sl, v);
+        emit(mm, sl, v);
     }
 }
 

@@ -1,4 +1,5 @@
 // Launchers of the non-GEMV kernels: q/k post-processing, attention, sampler, quantizers, synthetic data.
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <map>
@@ -140,6 +141,13 @@ hipError_t launch_fill_cache(void *c, int64_t planes, int64_t cap, int64_t len, 
     if (pairs <= 0) return hipSuccess;
     return launch(k_fill_cache, grid1(pairs, 256), dim3(256), 0, s, static_cast<_Float16 *>(c), planes, cap, len, hd,
                        seed, stream, mean, std);
+}
+
+hipError_t launch_copy16(const void *src, void *dst, int64_t bytes, hipStream_t s) {
+    const int64_t n = bytes / 16;
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 256 * 16);
+    return launch(k_copy16, dim3(unsigned(blocks)), dim3(256), 0, s, static_cast<const u32x4 *>(src), static_cast<u32x4 *>(dst), n);
 }
 
 }  // namespace vh

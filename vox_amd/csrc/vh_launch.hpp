@@ -45,6 +45,8 @@ hipError_t launch_fill_normal(float *out, int64_t n, uint64_t seed, uint32_t str
 hipError_t launch_fill_cache(void *c, int64_t planes, int64_t cap, int64_t len, int hd, uint64_t seed, uint32_t stream,
                              float mean, float std, hipStream_t s);
 
+hipError_t launch_copy16(const void *src, void *dst, int64_t bytes, hipStream_t s);
+
 // Shared-memory opt-in above 64 KiB, once per kernel.
 hipError_t ensure_smem(const void *kernel, size_t bytes);
 

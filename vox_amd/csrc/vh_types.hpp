@@ -20,13 +20,15 @@ struct RowRef {
 constexpr int kAttnMaxSplits = 8;  // split-K blocks per (row, kv head); the merge happens in the o-GEMV prologue
 constexpr int kAttnMinKeys = 64;   // fewer splits when there are fewer keys
 
-// Number of key splits for n visible keys (same on every kernel that reads the partials).
+// Number of key splits holding keys for n visible keys. The attention kernel always writes all kAttnMaxSplits
+// partials (splits >= attn_splits(n) are empty: max -inf, denominator 0, output 0), so readers merge a fixed count.
 __host__ __device__ inline int attn_splits(int64_t n) {
     const int64_t s = (n + kAttnMinKeys - 1) / kAttnMinKeys;
     return int(s < 1 ? 1 : s > kAttnMaxSplits ? kAttnMaxSplits : s);
 }
 
 // Split-K attention partials of m rows: running max, denominator and unnormalized output per (row, head, split).
+// Every split of every row is written by each attention launch.
 struct AttnPartials {
     float *pm, *pl;  // [m][heads][kAttnMaxSplits]
     float *po;       // [m][heads][kAttnMaxSplits][hd]
@@ -65,11 +67,11 @@ struct QkArgs {
 // append) for rows whose sequences differ (decode, pairs, B sessions); otherwise q comes from `q` and the keys of
 // this pass are already in the cache (prefill of one sequence).
 struct AttnArgs {
-    const float *qkv;    // fused: [m][ldqkv]
+    const float *qkv;        // fused: [m][ldqkv]
     int64_t ldqkv;
-    const float *q;      // not fused: [m][qd]
+    const float *q;          // not fused: [m][qd]
     const float *qn, *kn;
-    const float *rope;
+    const float *rope_rows;  // fused: [m][hd/2][2] (cos, sin) at each row's position, staged with the row views
     AttnPartials part;
     int32_t kv_heads, layer;
     float scale, eps;

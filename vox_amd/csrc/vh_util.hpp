@@ -124,4 +124,11 @@ __global__ void k_fill_cache(_Float16 *c, int64_t planes, int64_t cap, int64_t l
     dst[1] = _Float16(mean + std * z1);
 }
 
+// Plain 16-byte copy (grid-stride): the STREAM reference of the benchmark and the calibration kernel of the
+// HBM traffic counters (FETCH_SIZE / WRITE_SIZE read n * 16 bytes each for it).
+__global__ __launch_bounds__(256) void k_copy16(const u32x4 *src, u32x4 *dst, int64_t n) {
+    const int64_t stride = int64_t(gridDim.x) * 256;
+    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) dst[i] = __builtin_nontemporal_load(src + i);
+}
+
 }  // namespace vh

@@ -81,7 +81,9 @@ struct Xfmr {
     float *h = nullptr, *xin = nullptr, *qkv = nullptr, *q = nullptr, *g = nullptr, *xnorm = nullptr;
     float *pm = nullptr, *pl = nullptr, *po = nullptr, *logits = nullptr;
     int64_t xin_cols = 0, logits_cap = 0;
+    // per-row cache views of the next pass, followed by each row's RoPE row ([kMaxM][hd] (cos, sin) pairs)
     RowRef *rows_dev = nullptr, *rows_host = nullptr;
+    float *rope_rows_dev = nullptr;
     SampleCfgDev *scfg_dev = nullptr, *scfg_host = nullptr;
     int32_t *token_dev = nullptr;
     std::map<GraphKey, hipGraphExec_t> graphs;
@@ -330,8 +332,10 @@ void alloc_scratch(Xfmr &X) {
     X.pm = dalloc_t<float>(M * X.heads * kAttnMaxSplits);
     X.pl = dalloc_t<float>(M * X.heads * kAttnMaxSplits);
     X.po = dalloc_t<float>(M * X.heads * kAttnMaxSplits * X.hd);
-    X.rows_dev = dalloc_t<RowRef>(M);
-    HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&X.rows_host), M * sizeof(RowRef), hipHostMallocDefault));
+    const size_t rows_bytes = M * sizeof(RowRef) + M * size_t(X.hd) * 4;
+    X.rows_dev = static_cast<RowRef *>(dalloc(rows_bytes));
+    X.rope_rows_dev = reinterpret_cast<float *>(X.rows_dev + M);
+    HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&X.rows_host), rows_bytes, hipHostMallocDefault));
     X.scfg_dev = dalloc_t<SampleCfgDev>(1);
     HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&X.scfg_host), sizeof(SampleCfgDev), hipHostMallocDefault));
     X.token_dev = dalloc_t<int32_t>(M);
@@ -356,14 +360,24 @@ float *ensure_xin(Xfmr &X, int64_t cols) {
     return X.xin;
 }
 
-// Uploads the per-row cache views (positions) of the next pass; skips the copy when unchanged.
+// Uploads the per-row cache views (positions) of the next pass and the RoPE rows at those positions (computed as
+// the table rows of ensure_rope); skips the copy when unchanged.
 void set_rows(Xfmr &X, const std::vector<RowRef> &rows) {
     if (X.rows_valid && rows.size() == X.rows_last.size() &&
         std::memcmp(rows.data(), X.rows_last.data(), rows.size() * sizeof(RowRef)) == 0)
         return;
     HIPCHECK(hipStreamSynchronize(g.stream));  // the pinned block may still feed an earlier copy
     std::memcpy(X.rows_host, rows.data(), rows.size() * sizeof(RowRef));
-    HIPCHECK(hipMemcpyAsync(X.rows_dev, X.rows_host, rows.size() * sizeof(RowRef), hipMemcpyHostToDevice, g.stream));
+    float *rope = reinterpret_cast<float *>(X.rows_host + kMaxM);
+    const int half = X.hd / 2;
+    for (size_t i = 0; i < rows.size(); ++i)
+        for (int p = 0; p < half; ++p) {
+            const float f = X.inv_freq[size_t(p)] * float(rows[i].pos);
+            rope[i * size_t(X.hd) + 2 * size_t(p)] = std::cos(f);
+            rope[i * size_t(X.hd) + 2 * size_t(p) + 1] = std::sin(f);
+        }
+    const size_t bytes = kMaxM * sizeof(RowRef) + rows.size() * size_t(X.hd) * 4;
+    HIPCHECK(hipMemcpyAsync(X.rows_dev, X.rows_host, bytes, hipMemcpyHostToDevice, g.stream));
     X.rows_last = rows;
     X.rows_valid = true;
 }
@@ -412,7 +426,7 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
             probed(pr, VOXHIP_K_QKPOST, [&] { HIPCHECK(launch_qk_post(qa, mc, s)); });
         }
         AttnArgs aa;
-        aa.qkv = X.qkv; aa.ldqkv = ldqkv; aa.q = X.q; aa.qn = qn; aa.kn = kn; aa.rope = X.rope; aa.part = part;
+        aa.qkv = X.qkv; aa.ldqkv = ldqkv; aa.q = X.q; aa.qn = qn; aa.kn = kn; aa.rope_rows = X.rope_rows_dev; aa.part = part;
         aa.kv_heads = X.kvh; aa.layer = li; aa.scale = 1.0f / std::sqrt(float(X.hd)); aa.eps = X.eps;
         probed(pr, VOXHIP_K_ATTN, [&] { HIPCHECK(launch_attention(aa, X.hd, X.heads / X.kvh, mc, fused, s)); });
         probed(pr, VOXHIP_K_O, [&] {
@@ -1388,6 +1402,41 @@ int voxhip_bench_gemv_q8(int64_t rows, int64_t cols, int copies, int warmup, int
             *ms_per_launch = double(ms) / iters;
             (void)hipEventDestroy(e0);
             (void)hipEventDestroy(e1);
+        } catch (...) {
+            cleanup();
+            throw;
+        }
+        cleanup();
+        return 1;
+    }, 0);
+}
+
+int voxhip_bench_copy(int64_t bytes, int warmup, int iters, double *ms_per_copy) {
+    return guard_int([&] {
+        require_ok();
+        if (bytes < 16 || iters <= 0 || !ms_per_copy) throw Fail("bad bench arguments");
+        void *a = nullptr, *b = nullptr;
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        auto cleanup = [&] {
+            (void)hipStreamSynchronize(g.stream);
+            dfree(a); dfree(b);
+            if (e0) (void)hipEventDestroy(e0);
+            if (e1) (void)hipEventDestroy(e1);
+        };
+        try {
+            a = dalloc(size_t(bytes));
+            b = dalloc(size_t(bytes));
+            HIPCHECK(launch_fill_normal(static_cast<float *>(a), bytes / 4, 5, 0x55u, 0.f, 1.f, g.stream));
+            for (int i = 0; i < warmup; ++i) HIPCHECK(launch_copy16(a, b, bytes, g.stream));
+            HIPCHECK(hipEventCreate(&e0));
+            HIPCHECK(hipEventCreate(&e1));
+            HIPCHECK(hipEventRecord(e0, g.stream));
+            for (int i = 0; i < iters; ++i) HIPCHECK(launch_copy16(a, b, bytes, g.stream));
+            HIPCHECK(hipEventRecord(e1, g.stream));
+            HIPCHECK(hipEventSynchronize(e1));
+            float ms = 0.f;
+            HIPCHECK(hipEventElapsedTime(&ms, e0, e1));
+            *ms_per_copy = double(ms) / iters;
         } catch (...) {
             cleanup();
             throw;

@@ -117,6 +117,7 @@ SIGNATURES = {
     "voxhip_quantize_act_dev": (_I, [_P, _I64, _P, _P]),
     "voxhip_bench_decode": (_I, [_I, _I, _I64, _P, _I, C.POINTER(SampleCfg), _P, _I, _I, C.POINTER(BenchResult)]),
     "voxhip_bench_gemv_q8": (_I, [_I64, _I64, _I, _I, _I, C.POINTER(C.c_double)]),
+    "voxhip_bench_copy": (_I, [_I64, _I, _I, C.POINTER(C.c_double)]),
 }
 
 _lib = None
@@ -440,4 +441,11 @@ def bench_decode(xfmr, seq, pos0, d_x, head, cfg, d_token, warmup, steps):
 def bench_gemv_q8(rows, cols, copies, warmup, iters):
     ms = C.c_double()
     _check(lib().voxhip_bench_gemv_q8(rows, cols, copies, warmup, iters, C.byref(ms)), "bench_gemv_q8")
+    return ms.value
+
+
+def bench_copy(nbytes, warmup, iters):
+    """Average ms of one device copy of nbytes (read nbytes + write nbytes)."""
+    ms = C.c_double()
+    _check(lib().voxhip_bench_copy(nbytes, warmup, iters, C.byref(ms)), "bench_copy")
     return ms.value
