@@ -41,7 +41,7 @@ typedef struct voxhip_mat {
     const float *bias;
 } voxhip_mat;
 
-/* vox::GpuDeviceInfo (gpu.hpp:180-188); strings are fixed-size, NUL-terminated. */
+/* vox::GpuDeviceInfo (gpu.hpp:22-30); strings are fixed-size, NUL-terminated. */
 typedef struct voxhip_device_info {
     int32_t index;
     char name[256];
@@ -52,36 +52,36 @@ typedef struct voxhip_device_info {
     uint32_t api_version, vendor_id, driver_version;
 } voxhip_device_info;
 
-/* vox::GpuStats (gpu.hpp:174) without last_error (see voxhip_last_error). */
+/* vox::GpuStats (gpu.hpp:16) without last_error (see voxhip_last_error). */
 typedef struct voxhip_stats {
     int64_t mats_ok, mats_failed;
     uint64_t bytes, bytes_failed;
 } voxhip_stats;
 
-/* vox::GpuMemInfo (gpu.hpp:193). */
+/* vox::GpuMemInfo (gpu.hpp:35). */
 typedef struct voxhip_mem_info {
     uint64_t used, limit, device_free, device_total;
     int32_t device_index;
 } voxhip_mem_info;
 
 /* ---------------------------------------------------------------- device, init, accounting */
-/* gpu_enumerate (gpu.hpp:189): number of devices; 0 when the HIP runtime finds none. */
+/* gpu_enumerate (gpu.hpp:31): number of devices; 0 when the HIP runtime finds none. */
 int voxhip_device_count(void);
 /* gpu_enumerate entry `index`: 1 on success. */
 int voxhip_device_info_get(int index, voxhip_device_info *out);
-/* gpu_init (gpu.hpp:168). device: "hip", "hip:N", "gpu:N", or "vulkan:N" as family.cpp:94 passes it
- * (N = device index, also taken from VOX_VK_DEVICE like gpu_vulkan.cpp:163). Failure is sticky,
+/* gpu_init (gpu.hpp:10). device: "hip", "hip:N", "gpu:N", or "vulkan:N" as family.cpp:94 passes it
+ * (N = device index, also taken from VOX_VK_DEVICE like gpu_vulkan.cpp:160). Failure is sticky,
  * as gpu_vulkan.cpp:364. Returns 1 on success; on failure writes the reason to err. */
 int voxhip_init(const char *device, char *err, size_t err_len);
-int voxhip_active(void);                                   /* gpu_active (gpu.hpp:169) */
-const char *voxhip_device_name(void);                      /* gpu_device_name (gpu.hpp:170) */
-void voxhip_stats_get(voxhip_stats *out);                  /* gpu_stats (gpu.hpp:175) */
-const char *voxhip_last_error(void);                       /* GpuStats::last_error (gpu.hpp:174) */
-void voxhip_set_vram_limit(uint64_t bytes);                /* gpu_set_vram_limit (gpu.hpp:192) */
-void voxhip_mem_info_get(voxhip_mem_info *out);            /* gpu_mem_info (gpu.hpp:194) */
+int voxhip_active(void);                                   /* gpu_active (gpu.hpp:11) */
+const char *voxhip_device_name(void);                      /* gpu_device_name (gpu.hpp:12) */
+void voxhip_stats_get(voxhip_stats *out);                  /* gpu_stats (gpu.hpp:17) */
+const char *voxhip_last_error(void);                       /* GpuStats::last_error (gpu.hpp:16) */
+void voxhip_set_vram_limit(uint64_t bytes);                /* gpu_set_vram_limit (gpu.hpp:34) */
+void voxhip_mem_info_get(voxhip_mem_info *out);            /* gpu_mem_info (gpu.hpp:36) */
 
 /* ---------------------------------------------------------------- matrices */
-/* gpu_upload (gpu.hpp:172). n_parts > 1 stacks the parts' rows into one device matrix (same type
+/* gpu_upload (gpu.hpp:14). n_parts > 1 stacks the parts' rows into one device matrix (same type
  * and cols, all or none with bias), as upload_parts (gpu_vulkan.cpp:476-536). Returns a handle or -1. */
 int voxhip_upload(const voxhip_mat *parts, int n_parts);
 /* gpu_matmul (kernels.hpp:89): y[m][rows] = x[m][cols] . W^T (+ bias), host x and y.
@@ -115,15 +115,15 @@ typedef struct voxhip_xfmr_desc {
 } voxhip_xfmr_desc;
 
 /* Called once per uploaded matrix (layer, which = 0..6 for q,k,v,o,gate,up,down) right after its
- * upload, so the caller may release the host pages (gpu.hpp:195-198, qwen3.cpp:309-316). */
+ * upload, so the caller may release the host pages (gpu.hpp:37-40, qwen3.cpp:309-316). */
 typedef void (*voxhip_uploaded_fn)(void *user, int32_t layer, int32_t which);
 
-/* gpu_xfmr_create (gpu.hpp:198). n_layers < 0 = all layers. Returns a handle or -1. */
+/* gpu_xfmr_create (gpu.hpp:40). n_layers < 0 = all layers. Returns a handle or -1. */
 int voxhip_xfmr_create(const voxhip_xfmr_desc *w, const char *name, int n_layers, voxhip_uploaded_fn uploaded, void *user);
-/* gpu_seq_create (gpu.hpp:200): a KV cache of `capacity` positions (f16, on the device). The reference
+/* gpu_seq_create (gpu.hpp:42): a KV cache of `capacity` positions (f16, on the device). The reference
  * caps capacity at 3072 (gpu_vk_internal.hpp:34); this backend accepts up to 65536. Returns a handle or -1. */
 int voxhip_seq_create(int xfmr, int64_t capacity);
-void voxhip_seq_free(int seq);                             /* gpu_seq_free (gpu.hpp:201); buffers stay pooled */
+void voxhip_seq_free(int seq);                             /* gpu_seq_free (gpu.hpp:43); buffers stay pooled */
 /* gpu_xfmr_forward (kernels.hpp:92-93): x [m][in_proj ? in_proj.cols : hidden] at positions pos0..pos0+m-1;
  * out_last [hidden] = final RMSNorm of the last row (may be NULL); head >= 0: head_out [head.rows] = head
  * applied to out_last. in_proj / head are matrix handles or -1. Returns 1 or 0. */
@@ -164,8 +164,8 @@ typedef struct voxhip_sample_cfg {
 int voxhip_sample_logits(const float *logits, int32_t n, const voxhip_sample_cfg *cfg, const int32_t *history,
                          int32_t n_history, int32_t *out_id);
 
-/* gpu_pred_frame (gpu.hpp:209-210), gpu_codec_* (gpu.hpp:213-219), gpu_f5_* (gpu.hpp:240-248),
- * gpu_cosy_* (gpu.hpp:272-277) are not provided yet: gpu_hip.cpp answers them like gpu_stub.cpp
+/* gpu_pred_frame (gpu.hpp:51-52), gpu_codec_* (gpu.hpp:55-61), gpu_f5_* (gpu.hpp:82-90),
+ * gpu_cosy_* (gpu.hpp:114-119) are not provided yet: gpu_hip.cpp answers them like gpu_stub.cpp
  * (-1 / false), and the callers compute on the CPU. */
 
 /* ---------------------------------------------------------------- device-resident path
