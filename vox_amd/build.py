@@ -22,6 +22,8 @@ HIP_SOURCES = ["voxhip_runtime.hip", "vh_kernels_misc.hip", "vh_gemv_tile.hip", 
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
              # packed FP32 instructions stay off (the compiler must not emit v_pk_{add,mul,fma}_f32)
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             # leading scalar kernel arguments arrive in SGPRs with the dispatch (gfx950 kernarg preload)
+             "-mllvm", "-amdgpu-kernarg-preload-count=16",
              "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
 LIB = os.path.join(OUT, "libvoxhip.so")
 DROPIN = os.path.join(OUT, "libvox_gpu_hip.so")

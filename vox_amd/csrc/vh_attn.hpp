@@ -16,6 +16,8 @@
 // another block of the same launch. Not FUSED (prefill of one sequence): k_qk_post has already written q and the
 // pass's keys, and every key is read from the cache.
 #pragma once
+#include <type_traits>
+
 #include "vh_common.hpp"
 #include "vh_types.hpp"
 
@@ -202,34 +204,55 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
     }
-    // online softmax update with one key; all LPK lanes of the group call it together
-    auto consume = [&](const float (&kf)[8], const float (&vf)[8]) {
+    // Online softmax update with a batch of NU keys (invalid ones masked); all LPK lanes of a group call it
+    // together. The NU x G dot products and their group sums are independent, so their latencies overlap.
+    auto consume = [&](auto nu_tag, const f16x8 *kq, const f16x8 *vq, const bool *valid) {
+        constexpr int NU = decltype(nu_tag)::value;
+        float sc[NU][G];
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) d = fmaf(qh[h][e], float(kq[u][e]), d);
+                sc[u][h] = d;
+            }
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+#pragma unroll
+            for (int h = 0; h < G; ++h) sc[u][h] = valid[u] ? a.scale * group_sum<LPK>(sc[u][h]) : -INFINITY;
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            float d = 0.f;
+            float mnew = mh[h];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) d = fmaf(qh[h][e], kf[e], d);
-            d = group_sum<LPK>(d);
-            const float sc = a.scale * d;
-            const float mnew = fmaxf(mh[h], sc);
-            const float corr = expf(mh[h] - mnew), p = expf(sc - mnew);
-            lh[h] = fmaf(lh[h], corr, p);
+            for (int u = 0; u < NU; ++u) mnew = fmaxf(mnew, sc[u][h]);
+            if (mnew == -INFINITY) continue;  // no key in this group yet
+            const float corr = expf(mh[h] - mnew);
+            float l = lh[h] * corr, o[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(acc[h][e], corr, p * vf[e]);
+            for (int e = 0; e < 8; ++e) o[e] = acc[h][e] * corr;
+#pragma unroll
+            for (int u = 0; u < NU; ++u) {
+                const float p = valid[u] ? expf(sc[u][h] - mnew) : 0.f;
+                l += p;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = fmaf(p, float(vq[u][e]), o[e]);
+            }
+            lh[h] = l;
             mh[h] = mnew;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[h][e] = o[e];
         }
     };
     for (int64_t jb = j0; jb < kend; jb += int64_t(U) * NGRP) {
+        bool valid[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t j = jb + int64_t(u) * NGRP;
-            if (j < kend) {
-                float kf[8], vf[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) { kf[e] = float(kb[u][e]); vf[e] = float(vb[u][e]); }
-                consume(kf, vf);
-            }
+            valid[u] = jb + int64_t(u) * NGRP < kend;
+            if (!valid[u]) kb[u] = vb[u] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};  // masked: finite zeros, weight 0
         }
+        consume(std::integral_constant<int, U>(), kb, vb, valid);
         // next batch
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -240,11 +263,12 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
             }
         }
     }
-    if (last && grp == 0) {  // the new key at pos, from LDS
-        float kf[8], vf[8];
+    if (last && grp == 0) {  // the new key at pos, from LDS (f16-rounded like the cache)
+        f16x8 kn1[1], vn1[1];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) { kf[e] = sm.knew[sub * 8 + e]; vf[e] = sm.vnew[sub * 8 + e]; }
-        consume(kf, vf);
+        for (int e = 0; e < 8; ++e) { kn1[0][e] = _Float16(sm.knew[sub * 8 + e]); vn1[0][e] = _Float16(sm.vnew[sub * 8 + e]); }
+        const bool v1[1] = {true};
+        consume(std::integral_constant<int, 1>(), kn1, vn1, v1);
     }
 
     // merge the NGRP key groups in LDS, in group order

@@ -13,22 +13,41 @@ namespace vh {
 
 constexpr int kWave = 64;
 
-VH_DEV float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
+// Cross-lane steps on the DPP path (no LDS round trip): quad permutations and row mirrors within 16-lane rows.
+enum : int { kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppRowHalfMirror = 0x141, kDppRowMirror = 0x140 };
+template <int CTRL>
+VH_DEV int dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
 }
-VH_DEV float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
+template <int CTRL>
+VH_DEV float dpp(float v) {
+    return __builtin_bit_cast(float, dpp<CTRL>(__builtin_bit_cast(int, v)));
 }
-// Sum over groups of `width` consecutive lanes (width a power of two <= 64); every lane gets its group's sum.
+VH_DEV float readlane(float v, int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); }
+
+// Sum over groups of W consecutive lanes (W a power of two <= 64); every lane gets its group's sum. Within a
+// 16-lane row the steps are xor 1, xor 2, mirror in 8, mirror in 16; rows are combined as (r0 + r1) + (r2 + r3).
 template <int W>
 VH_DEV float group_sum(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    if (W >= 2) v += dpp<kDppXor1>(v);
+    if (W >= 4) v += dpp<kDppXor2>(v);
+    if (W >= 8) v += dpp<kDppRowHalfMirror>(v);
+    if (W >= 16) v += dpp<kDppRowMirror>(v);
+    if (W == 32) {
+        const float a = readlane(v, 0) + readlane(v, 16), b = readlane(v, 32) + readlane(v, 48);
+        v = (threadIdx.x & 32) ? b : a;
+    } else if (W == 64) {
+        v = (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
+    }
     return v;
+}
+VH_DEV float wave_sum(float v) { return group_sum<64>(v); }
+VH_DEV float wave_max(float v) {
+    v = fmaxf(v, dpp<kDppXor1>(v));
+    v = fmaxf(v, dpp<kDppXor2>(v));
+    v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppRowMirror>(v));
+    return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
 }
 
 // Block-wide sum for blockDim.x == NT (multiple of 64). red must hold NT/64 floats. All threads get the sum.

@@ -35,11 +35,11 @@ VH_DEV int64_t row_bytes(int K) {
 // receives each slot; it runs with all 4 lanes of a block active. Every input is read from global memory once:
 // PRO_RMS keeps its slots in registers between the sum of squares and the scaling when they fit (KS per thread).
 template <int M, int PRO, class Sink>
-VH_DEV void prologue(const GemvArgs &a, float *red, Sink &&sink) {
-    const int K = a.K, spr = K / 8;  // slots per row
+VH_DEV void prologue(const GemvArgs &a, const float *x, int K, float *red, Sink &&sink) {
+    const int spr = K / 8;  // slots per row
     const int nslot = M * spr;
     auto load_x = [&](int mm, int sl, float (&v)[8]) {
-        const float *xr = a.x + int64_t(mm) * a.ldx + sl * 8;
+        const float *xr = x + int64_t(mm) * a.ldx + sl * 8;
         const f32x4 t0 = *reinterpret_cast<const f32x4 *>(xr), t1 = *reinterpret_cast<const f32x4 *>(xr + 4);
         v[0] = t0.x; v[1] = t0.y; v[2] = t0.z; v[3] = t0.w; v[4] = t1.x; v[5] = t1.y; v[6] = t1.z; v[7] = t1.w;
     };
@@ -176,8 +176,8 @@ VH_DEV void quant_slot(const float (&v)[8], uint32_t *q2, float *sc_out) {
         const float t = fabsf(v[j]);
         mx = mx < t ? t : mx;
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 1, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, 2, kWave));
+    mx = fmaxf(mx, dpp<kDppXor1>(mx));
+    mx = fmaxf(mx, dpp<kDppXor2>(mx));
     const float sc = mx / 127.0f, inv = sc > 0.f ? 1.0f / sc : 0.0f;
     *sc_out = sc;
     uint32_t w[2] = {0u, 0u};
@@ -193,9 +193,9 @@ VH_DEV void quant_slot(const float (&v)[8], uint32_t *q2, float *sc_out) {
 // Epilogue: lane r*M + mm holds the total of (row0 + r, input row mm). SwiGLU pairs rows (2u, 2u+1) =
 // (gate u, up u); the partner value is fetched with all lanes active, then only valid lanes store.
 template <int M, int R, int EPI>
-VH_DEV void store_out(const GemvArgs &a, float out, int lane, int row0) {
+VH_DEV void store_out(const GemvArgs &a, int rows, float out, int lane, int row0) {
     const int r = lane / M, mm = lane % M, row = row0 + r;
-    const bool ok = lane < R * M && row < a.rows && mm < a.m;
+    const bool ok = lane < R * M && row < rows && mm < a.m;
     const float v = out + ((ok && a.bias) ? a.bias[row] : 0.f);
     if (EPI == EPI_SWIGLU) {
         const float other = __shfl_xor(v, M, kWave);  // lane of row r ^ 1, same input row
@@ -220,10 +220,12 @@ VH_DEV void reduce_store_prep(float (&acc)[R][M], float &out, int lane) {
 
 // ------------------------------------------------------------------------------------------ int8 path
 template <int WT, int M, int R, int IT, int PRO, int EPI>
-__global__ __launch_bounds__(kGemvThreads) void k_gemv_int(GemvArgs a) {
+// The weight stream's operands come first so they are preloaded into SGPRs with the dispatch (kernarg preload).
+__global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__restrict__ w, const float *__restrict__ scale,
+                                                       const float *x, int32_t rows, int32_t K, GemvArgs a) {
     static_assert(WT == WT_Q8 || WT == WT_Q4, "int path is Q8/Q4");
     extern __shared__ __align__(16) uint8_t smem[];
-    const int K = a.K, nb = K / 32;
+    const int nb = K / 32;
     int8_t *xq = reinterpret_cast<int8_t *>(smem);                 // [M][K]
     float *xs = reinterpret_cast<float *>(smem + M * K);           // [M][nb]
     float *red = xs + M * nb;                                      // [M][4]
@@ -242,17 +244,17 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(GemvArgs a) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const int row = row0 + r;
-                const bool ok = c < nchunk && row < a.rows;
-                const u32x4 *p = reinterpret_cast<const u32x4 *>(a.w + int64_t(row) * rb) + c;
+                const bool ok = c < nchunk && row < rows;
+                const u32x4 *p = reinterpret_cast<const u32x4 *>(w + int64_t(row) * rb) + c;
                 wv[j][r] = ok ? __builtin_nontemporal_load(p) : u32x4{0u, 0u, 0u, 0u};
                 const int blk = WT == WT_Q8 ? (c >> 1) : c;
-                sv[j][r] = ok ? a.scale[int64_t(row) * nb + blk] : 0.f;
+                sv[j][r] = ok ? scale[int64_t(row) * nb + blk] : 0.f;
             }
         }
     };
     load(0);
 
-    prologue<M, PRO>(a, red, [&](int mm, int sl, const float (&v)[8]) {
+    prologue<M, PRO>(a, x, K, red, [&](int mm, int sl, const float (&v)[8]) {
         uint32_t q2[2];
         float sc;
         quant_slot(v, q2, &sc);
@@ -284,7 +286,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(GemvArgs a) {
                         d = __builtin_amdgcn_sdot4(int(wv[j][r].y), int(xv.y), d, false);
                         d = __builtin_amdgcn_sdot4(int(wv[j][r].z), int(xv.z), d, false);
                         d = __builtin_amdgcn_sdot4(int(wv[j][r].w), int(xv.w), d, false);
-                        d += __shfl_xor(d, 1, kWave);  // the two 16-byte halves of one 32-block: exact block dot
+                        d += dpp<kDppXor1>(d);  // the two 16-byte halves of one 32-block: exact block dot
                         const float f = (lane & 1) ? 0.f : float(d) * (sv[j][r] * xsv);
                         acc[r][mm] += f;
                     }
@@ -322,15 +324,16 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(GemvArgs a) {
     }
     float out;
     reduce_store_prep<R, M>(acc, out, lane);
-    store_out<M, R, EPI>(a, out, lane, row0);
+    store_out<M, R, EPI>(a, rows, out, lane, row0);
 }
 
 // ------------------------------------------------------------------------------------------ f32 path
 template <int WT, int M, int R, int IT, int PRO, int EPI>
-__global__ __launch_bounds__(kGemvThreads) void k_gemv_flt(GemvArgs a) {
+// The weight stream's operands come first so they are preloaded into SGPRs with the dispatch (kernarg preload).
+__global__ __launch_bounds__(kGemvThreads) void k_gemv_flt(const uint8_t *__restrict__ w, const float *__restrict__ scale,
+                                                       const float *x, int32_t rows, int32_t K, GemvArgs a) {
     static_assert(WT != WT_Q4, "Q4 always uses the int path");
     extern __shared__ __align__(16) uint8_t smem[];
-    const int K = a.K;
     float *xf = reinterpret_cast<float *>(smem);  // [M][K]
     float *red = xf + M * K;                      // [M][4]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -349,16 +352,16 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_flt(GemvArgs a) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const int row = row0 + r;
-                const bool ok = c < nchunk && row < a.rows;
-                const u32x4 *p = reinterpret_cast<const u32x4 *>(a.w + int64_t(row) * rb) + c;
+                const bool ok = c < nchunk && row < rows;
+                const u32x4 *p = reinterpret_cast<const u32x4 *>(w + int64_t(row) * rb) + c;
                 wv[j][r] = ok ? __builtin_nontemporal_load(p) : u32x4{0u, 0u, 0u, 0u};
-                sv[j][r] = (WT == WT_Q8 && ok) ? a.scale[int64_t(row) * nb + (c >> 1)] : 0.f;
+                sv[j][r] = (WT == WT_Q8 && ok) ? scale[int64_t(row) * nb + (c >> 1)] : 0.f;
             }
         }
     };
     load(0);
 
-    prologue<M, PRO>(a, red, [&](int mm, int sl, const float (&v)[8]) {
+    prologue<M, PRO>(a, x, K, red, [&](int mm, int sl, const float (&v)[8]) {
         *reinterpret_cast<f32x4 *>(xf + mm * K + sl * 8) = f32x4{v[0], v[1], v[2], v[3]};
         *reinterpret_cast<f32x4 *>(xf + mm * K + sl * 8 + 4) = f32x4{v[4], v[5], v[6], v[7]};
     });
@@ -410,7 +413,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_flt(GemvArgs a) {
     }
     float out;
     reduce_store_prep<R, M>(acc, out, lane);
-    store_out<M, R, EPI>(a, out, lane, row0);
+    store_out<M, R, EPI>(a, rows, out, lane, row0);
 }
 
 }  // namespace vh

@@ -15,12 +15,12 @@ hipError_t gemv_run(const GemvArgs &a, hipStream_t s) {
         const size_t smem = size_t(M) * a.K + size_t(M) * (a.K / 32) * 4 + size_t(M) * 16;
         hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_gemv_int<WT, M, R, IT, PRO, EPI>), smem);
         if (e != hipSuccess) return e;
-        return launch(k_gemv_int<WT, M, R, IT, PRO, EPI>, grid, block, smem, s, a);
+        return launch(k_gemv_int<WT, M, R, IT, PRO, EPI>, grid, block, smem, s, a.w, a.scale, a.x, a.rows, a.K, a);
     } else {
         const size_t smem = size_t(M) * a.K * 4 + size_t(M) * 16;
         hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_gemv_flt<WT, M, R, IT, PRO, EPI>), smem);
         if (e != hipSuccess) return e;
-        return launch(k_gemv_flt<WT, M, R, IT, PRO, EPI>, grid, block, smem, s, a);
+        return launch(k_gemv_flt<WT, M, R, IT, PRO, EPI>, grid, block, smem, s, a.w, a.scale, a.x, a.rows, a.K, a);
     }
 }
 

@@ -38,9 +38,26 @@ VH_DEV uint64_t readlane_u64(uint64_t v, int j) {
     const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v >> 32)), j));
     return uint64_t(hi) << 32 | lo;
 }
+// Value of lane (lane ^ m) for a 64-bit value: DPP within a 16-lane row for m <= 8, a swizzle for 16, a permute
+// for 32 (m is a compile-time constant after unrolling).
+VH_DEV int xor_lane(int x, int m) {
+    const int lane = threadIdx.x & 63;
+    switch (m) {
+        case 1: return dpp<kDppXor1>(x);
+        case 2: return dpp<kDppXor2>(x);
+        case 4: {  // both DPP reads run with every lane active (a disabled source lane would read as 0)
+            const int up = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0xF, false);  // row_shl:4 reads lane i + 4
+            const int dn = __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4 reads lane i - 4
+            return (lane & 4) ? dn : up;
+        }
+        case 8: return __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false);  // row_ror:8 = lane ^ 8 in the row
+        case 16: return __builtin_amdgcn_ds_swizzle(x, 0x401F);  // bit mode: and 0x1F, xor 0x10
+        default: return __shfl_xor(x, m, kWave);
+    }
+}
 VH_DEV uint64_t shfl_xor_u64(uint64_t v, int m) {
-    const uint32_t lo = uint32_t(__shfl_xor(int(uint32_t(v)), m, kWave));
-    const uint32_t hi = uint32_t(__shfl_xor(int(uint32_t(v >> 32)), m, kWave));
+    const uint32_t lo = uint32_t(xor_lane(int(uint32_t(v)), m));
+    const uint32_t hi = uint32_t(xor_lane(int(uint32_t(v >> 32)), m));
     return uint64_t(hi) << 32 | lo;
 }
 
@@ -61,20 +78,29 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *c
     __shared__ int sh_bits, sh_kk, sh_done, sh_cnt;
     __shared__ unsigned long long sh_best;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const SampleCfgDev cfg = *cfgp;
     if (n <= 0 || n > kSampleMaxN) { if (t == 0) out[0] = -1; return; }
     constexpr int E = kSampleMaxN / kSampleThreads;
     const int per = (n + kSampleThreads - 1) / kSampleThreads;
+    // the logits and the configuration are independent loads: issue both before using either
+    float lv[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int idx = e * kSampleThreads + t;
+        lv[e] = (e < per && idx < n) ? logits[idx] : 0.f;
+    }
+    const SampleCfgDev cfg = *cfgp;
 
-    for (int i = t; i < kSampleMaxN / 32; i += kSampleThreads) seen[i] = 0u;
     if (t < 256) hist[t] = 0u;
     if (t == 0) { sh_prefix = 0ull; sh_bits = 0; sh_done = 0; sh_cnt = 0; sh_best = 0ull; }
-    __syncthreads();
-    if (cfg.rep != 1.0f && cfg.history)
+    const bool penalty = cfg.rep != 1.0f && cfg.history && cfg.n_history > 0;  // uniform
+    if (penalty) {  // tokens seen in the history, each penalized once (sampling.hpp:65-73)
+        for (int i = t; i < kSampleMaxN / 32; i += kSampleThreads) seen[i] = 0u;
+        __syncthreads();
         for (int i = t; i < cfg.n_history; i += kSampleThreads) {
             const int32_t h = cfg.history[i];
             if (h >= 0 && h < n) atomicOr(&seen[h >> 5], 1u << (h & 31));
         }
+    }
     __syncthreads();
 
     // keys of indices e * 1024 + t (coalesced); 0 marks "no logit"
@@ -84,10 +110,10 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *c
         const int idx = e * kSampleThreads + t;
         key[e] = 0ull;
         if (e < per && idx < n) {
-            float v = logits[idx];
+            float v = lv[e];
             if (idx >= cfg.sup_from && idx < cfg.sup_to && idx != cfg.eos) v = -INFINITY;
             if (cfg.block_eos && idx == cfg.eos) v = -INFINITY;
-            if (cfg.rep != 1.0f && (seen[idx >> 5] >> (idx & 31) & 1u)) v = v > 0.f ? v / cfg.rep : v * cfg.rep;
+            if (penalty && (seen[idx >> 5] >> (idx & 31) & 1u)) v = v > 0.f ? v / cfg.rep : v * cfg.rep;
             key[e] = uint64_t(ord_key(v)) << 32 | uint64_t(0xFFFFFFFFu - uint32_t(idx));
         }
     }
@@ -158,13 +184,31 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *c
     const int L = sh_bits;
     int K2 = 64;
     while (K2 < k) K2 <<= 1;
-    // ---- the k selected keys (any order), padded with zeros (lowest) to K2
+    // ---- the k selected keys (any order), padded with zeros (lowest) to K2. One LDS atomic per wave reserves
+    // the wave's slots; lanes place their keys by ballot rank.
+    {
+        uint64_t masks[E];
+        int wave_total = 0;
 #pragma unroll
-    for (int e = 0; e < E; ++e)
-        if (key[e] && (key[e] >> (64 - L)) >= P) {
-            const int p = atomicAdd(&sh_cnt, 1);
-            if (p < K2) sample_keys[p] = key[e];
+        for (int e = 0; e < E; ++e) {
+            masks[e] = e < per ? __ballot(key[e] && (key[e] >> (64 - L)) >= P) : 0ull;
+            wave_total += __popcll(masks[e]);
         }
+        int base = 0;
+        if (wave_total) {
+            if (lane == 0) base = atomicAdd(&sh_cnt, wave_total);
+            base = __builtin_amdgcn_readfirstlane(base);
+        }
+        const uint64_t lt = (1ull << lane) - 1ull;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            if ((masks[e] >> lane) & 1ull) {
+                const int p = base + __popcll(masks[e] & lt);
+                if (p < K2) sample_keys[p] = key[e];
+            }
+            base += __popcll(masks[e]);
+        }
+    }
     for (int i = k + t; i < K2; i += kSampleThreads) sample_keys[i] = 0ull;
     __syncthreads();
 
@@ -197,7 +241,8 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *c
         if (wave != 0) return;
     }
 
-    // ---- probabilities in double (sampling.hpp:91-99), one wave, sums in sorted order
+    // ---- probabilities in double (sampling.hpp:91-99), one wave; lanes compute the terms of a chunk of 64 in
+    // parallel, the sums add them in sorted order like the reference's loops.
     auto key_of = [&](int base) -> uint64_t {  // this lane's key of the chunk starting at `base`
         if (small) return v;
         return base + lane < k ? sample_keys[base + lane] : 0ull;
@@ -207,38 +252,54 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *c
     auto weight = [&](uint64_t kv, int i) -> double {
         return i < k ? exp((double(ord_val(uint32_t(kv >> 32))) - mx) * inv_t) : 0.0;
     };
+    // Sequential sums in sorted order over chunks of 64: every lane runs the same fully unrolled chain of
+    // lane-broadcast adds (past-the-end terms are +0.0, which leaves a sum of non-negative terms unchanged).
     double sum = 0.0;
     for (int base = 0; base < k; base += 64) {
         const double w = weight(key_of(base), base + lane);
-        const int cnt = k - base < 64 ? k - base : 64;
-        for (int j = 0; j < cnt; ++j) sum += readlane_d(w, j);
+#pragma unroll
+        for (int j = 0; j < 64; ++j) sum += readlane_d(w, j);
     }
-    // top-p: the running sum that finds the minimal prefix is also the total over the kept prefix
+    // Running sums of the normalized terms, continued from `run`: lane j of the chunk gets the sum through term
+    // base + j. These are the reference's top-p sum `c` and inverse-CDF sum `acc` (both start at 0 and add
+    // probs[i] in order), and the top-p total is the running sum at the last kept term.
+    auto prefix_chunk = [&](int base, double &run) -> double {
+        const double q = weight(key_of(base), base + lane) / sum;
+        double pre = 0.0;
+#pragma unroll
+        for (int j = 0; j < 64; ++j) {
+            run += readlane_d(q, j);
+            pre = lane == j ? run : pre;
+        }
+        return pre;
+    };
     const bool use_p = cfg.top_p > 0.0f && cfg.top_p < 1.0f;
     int keep = k;
-    double tot = 0.0;
+    double tot = 0.0, pre0 = 0.0, run0 = 0.0;  // chunk 0's running sums and the sum after it, reused below
     {
-        bool found = false;
-        for (int base = 0; base < k && !found; base += 64) {
-            const double p = weight(key_of(base), base + lane) / sum;
-            const int cnt = k - base < 64 ? k - base : 64;
-            for (int j = 0; j < cnt; ++j) {
-                tot += readlane_d(p, j);
-                if (use_p && tot >= double(cfg.top_p)) { keep = base + j + 1; found = true; break; }
+        double run = 0.0;
+        for (int base = 0; base < k; base += 64) {
+            const double pre = prefix_chunk(base, run);
+            if (base == 0) { pre0 = pre; run0 = run; }
+            const uint64_t m = use_p ? __ballot(base + lane < k && pre >= double(cfg.top_p)) : 0ull;
+            if (m) {
+                const int j = __ffsll((long long)m) - 1;
+                keep = base + j + 1;
+                tot = readlane_d(pre, j);
+                break;
             }
+            if (base + 64 >= k) tot = readlane_d(pre, k - 1 - base);
         }
     }
     const float u = det_uniform(cfg.key0, cfg.key1, cfg.frame, cfg.cb, cfg.draw);
     const double target = double(u) * tot;
-    double accp = 0.0;
     int pick = keep - 1;
-    bool hit = false;
-    for (int base = 0; base < keep && !hit; base += 64) {
-        const double p = weight(key_of(base), base + lane) / sum;
-        const int cnt = keep - base < 64 ? keep - base : 64;
-        for (int j = 0; j < cnt; ++j) {
-            accp += readlane_d(p, j);
-            if (target < accp) { pick = base + j; hit = true; break; }
+    {
+        double run = run0;
+        for (int base = 0; base < keep; base += 64) {
+            const double pre = base == 0 ? pre0 : prefix_chunk(base, run);
+            const uint64_t m = __ballot(base + lane < keep && target < pre);
+            if (m) { pick = base + __ffsll((long long)m) - 1; break; }
         }
     }
     const uint64_t kp = small ? readlane_u64(v, pick) : sample_keys[pick];
