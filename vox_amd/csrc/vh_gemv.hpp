@@ -30,18 +30,115 @@ VH_DEV int64_t row_bytes(int K) {
 }
 
 // ---------------------------------------------------------------------------------------------- prologue
-// Produces the f32 input rows v[mm][K] (mm < a.m; rows a.m..M-1 are zeros) in 8-element slots: slot s of row mm
-// holds elements 8s..8s+7, a 32-block is 4 consecutive slots handled by 4 consecutive lanes. `sink(mm, s, v)`
-// receives each slot; it runs with all 4 lanes of a block active. Every input is read from global memory once:
-// PRO_RMS keeps its slots in registers between the sum of squares and the scaling when they fit (KS per thread).
-template <int M, int PRO, class Sink>
-VH_DEV void prologue(const GemvArgs &a, const float *x, int K, float *red, Sink &&sink) {
-    const int spr = K / 8;  // slots per row
-    const int nslot = M * spr;
-    auto load_x = [&](int mm, int sl, float (&v)[8]) {
-        const float *xr = x + int64_t(mm) * a.ldx + sl * 8;
-        const f32x4 t0 = *reinterpret_cast<const f32x4 *>(xr), t1 = *reinterpret_cast<const f32x4 *>(xr + 4);
-        v[0] = t0.x; v[1] = t0.y; v[2] = t0.z; v[3] = t0.w; v[4] = t1.x; v[5] = t1.y; v[6] = t1.z; v[7] = t1.w;
+// The prologue produces the f32 input rows v[mm][K] (mm < a.m; rows a.m..M-1 are zeros) in 8-element slots: slot s
+// of row mm holds elements 8s..8s+7, a 32-block is 4 consecutive slots handled by 4 consecutive lanes.
+// `sink(mm, s, v)` receives each slot with all 4 lanes of its block active.
+//
+// When its global inputs fit in registers (slot s = threadIdx.x + 256 k, k < KS), pro_stage() loads them BEFORE the
+// kernel issues its weight stream. Vector loads return in issue order, so the prologue then waits for its own
+// inputs only and the weights arrive while it computes. Larger inputs are read inside prologue(), after the weights.
+template <int M, int PRO>
+struct ProStage {
+    static constexpr int KS = PRO == PRO_ATTN ? 1 : 4;
+    float x[KS][8];  // PRO_X, PRO_RMS: input slots
+    float g[KS][8];  // PRO_RMS: gamma slots
+    float pm[kAttnMaxSplits], pl[kAttnMaxSplits];
+    f32x4 o0[kAttnMaxSplits], o1[kAttnMaxSplits];  // PRO_ATTN: the slot's split partials
+};
+
+VH_DEV void load8(const float *p, float (&v)[8]) {
+    const f32x4 t0 = *reinterpret_cast<const f32x4 *>(p), t1 = *reinterpret_cast<const f32x4 *>(p + 4);
+    v[0] = t0.x; v[1] = t0.y; v[2] = t0.z; v[3] = t0.w; v[4] = t1.x; v[5] = t1.y; v[6] = t1.z; v[7] = t1.w;
+}
+
+// Partials of one slot (row mm, elements e0..e0+7 of head e0 / hd) for all kAttnMaxSplits splits.
+template <class PM, class PO>
+VH_DEV void load_partials(const AttnPartials &P, int mm, int sl, PM &pm, PM &pl, PO &o0, PO &o1) {
+    const int e0 = sl * 8, h = e0 / P.hd, d0 = e0 % P.hd;
+    const int64_t base = (int64_t(mm) * P.heads + h) * kAttnMaxSplits;
+#pragma unroll
+    for (int q = 0; q < kAttnMaxSplits; ++q) {
+        pm[q] = P.pm[base + q];
+        pl[q] = P.pl[base + q];
+        o0[q] = *reinterpret_cast<const f32x4 *>(P.po + (base + q) * P.hd + d0);
+        o1[q] = *reinterpret_cast<const f32x4 *>(P.po + (base + q) * P.hd + d0 + 4);
+    }
+}
+
+// Merge of all kAttnMaxSplits partials (empty splits have max -inf and weigh 0): softmax-weighted value sum.
+template <class PM, class PO>
+VH_DEV void merge_partials(const PM &pm, const PM &pl, const PO &o0, const PO &o1, float (&v)[8]) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < kAttnMaxSplits; ++q) mx = fmaxf(mx, pm[q]);
+    float L = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = 0.f;
+#pragma unroll
+    for (int q = 0; q < kAttnMaxSplits; ++q) {
+        const float w = pm[q] == -INFINITY ? 0.f : expf(pm[q] - mx);
+        L = fmaf(w, pl[q], L);
+        v[0] = fmaf(w, o0[q].x, v[0]); v[1] = fmaf(w, o0[q].y, v[1]); v[2] = fmaf(w, o0[q].z, v[2]); v[3] = fmaf(w, o0[q].w, v[3]);
+        v[4] = fmaf(w, o1[q].x, v[4]); v[5] = fmaf(w, o1[q].y, v[5]); v[6] = fmaf(w, o1[q].z, v[6]); v[7] = fmaf(w, o1[q].w, v[7]);
+    }
+    const float il = 1.0f / L;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] *= il;
+}
+
+// Whether a prologue's inputs fit the staging registers (the host instantiates STAGE accordingly).
+template <int M, int PRO>
+__host__ __device__ inline bool pro_stageable(int K) {
+    return M * (K / 8) <= ProStage<M, PRO>::KS * kGemvThreads;
+}
+
+template <int M, int PRO>
+VH_DEV void pro_stage(const GemvArgs &a, const float *x, int K, ProStage<M, PRO> &st) {
+    constexpr int KS = ProStage<M, PRO>::KS;
+    const int spr = K / 8, nslot = M * spr;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+        // branch-free: slots past the end read slot 0 and are never used, so the load count is static
+        const int s = threadIdx.x + k * kGemvThreads;
+        const bool in = s < nslot;
+        const int mm = in ? s / spr : 0, sl = in ? s % spr : 0;
+        const bool on = in && mm < a.m;
+        if (PRO == PRO_ATTN) {
+            load_partials(a.attn, on ? mm : 0, sl, st.pm, st.pl, st.o0, st.o1);
+        } else {
+            // raw values only: masking them here would make the compiler wait for them before the weight stream
+            load8(x + int64_t(on ? mm : 0) * a.ldx + sl * 8, st.x[k]);
+            if (PRO == PRO_RMS) load8(a.gamma + sl * 8, st.g[k]);
+        }
+    }
+}
+
+template <int M, int PRO, bool STAGE, class Sink>
+VH_DEV void prologue(const GemvArgs &a, const float *x, int K, float *red, const ProStage<M, PRO> &st, Sink &&sink) {
+    constexpr int KS = ProStage<M, PRO>::KS;
+    const int spr = K / 8, nslot = M * spr;
+    // Runs f(k, s) over this thread's slots s = threadIdx.x + 256 k; unrolled when staged, so st.x[k] is static.
+    auto for_slots = [&](auto &&f) {
+        if constexpr (STAGE) {
+#pragma unroll
+            for (int k = 0; k < KS; ++k) {
+                const int s = threadIdx.x + k * kGemvThreads;
+                if (s < nslot) f(k, s);
+            }
+        } else {
+            for (int s = threadIdx.x; s < nslot; s += kGemvThreads) f(-1, s);
+        }
+    };
+    // slot k of this thread (k < 0: not staged, read it from global memory)
+    auto get_x = [&](int k, int mm, int sl, float (&v)[8]) {
+        if (k >= 0) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = mm < a.m ? st.x[k][j] : 0.f;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = 0.f;
+            if (mm < a.m) load8(x + int64_t(mm) * a.ldx + sl * 8, v);
+        }
     };
     auto emit = [&](int mm, int sl, float (&v)[8]) {
         if (PRO != PRO_X && a.xnorm && blockIdx.x == 0 && mm < a.m)
@@ -50,39 +147,21 @@ VH_DEV void prologue(const GemvArgs &a, const float *x, int K, float *red, Sink 
         sink(mm, sl, v);
     };
     if (PRO == PRO_RMS) {
-        constexpr int KS = 4;
-        const bool in_regs = nslot <= KS * kGemvThreads;
-        float v[KS][8], gm[KS][8];
         float ss[M];
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) ss[mm] = 0.f;
-        // pass 1: sum of squares of every row (kernels.cpp:709-710), slots kept when they fit
-        for (int k = 0, s = threadIdx.x; s < nslot; ++k, s += kGemvThreads) {
+        // pass 1: sum of squares of every row (kernels.cpp:709-710)
+        for_slots([&](int k, int s) {
             const int mm = s / spr, sl = s % spr;
             float t[8];
-            if (mm < a.m) load_x(mm, sl, t);
-            else
-#pragma unroll
-                for (int j = 0; j < 8; ++j) t[j] = 0.f;
+            get_x(k, mm, sl, t);
             float q = 0.f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) q = fmaf(t[j], t[j], q);
 #pragma unroll
             for (int r = 0; r < M; ++r)
                 if (r == mm) ss[r] += q;
-            if (in_regs) {
-#pragma unroll
-                for (int kk = 0; kk < KS; ++kk)
-                    if (kk == k) {
-                        const f32x4 g0 = *reinterpret_cast<const f32x4 *>(a.gamma + sl * 8),
-                                    g1 = *reinterpret_cast<const f32x4 *>(a.gamma + sl * 8 + 4);
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) v[kk][j] = t[j];
-                        gm[kk][0] = g0.x; gm[kk][1] = g0.y; gm[kk][2] = g0.z; gm[kk][3] = g0.w;
-                        gm[kk][4] = g1.x; gm[kk][5] = g1.y; gm[kk][6] = g1.z; gm[kk][7] = g1.w;
-                    }
-            }
-        }
+        });
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) ss[mm] = wave_sum(ss[mm]);
         if ((threadIdx.x & 63) == 0)
@@ -96,22 +175,15 @@ VH_DEV void prologue(const GemvArgs &a, const float *x, int K, float *red, Sink 
             inv[mm] = 1.0f / sqrtf(t / float(K) + a.eps);
         }
         // pass 2: w * (x * inv) (kernels.cpp:711)
-        for (int k = 0, s = threadIdx.x; s < nslot; ++k, s += kGemvThreads) {
+        for_slots([&](int k, int s) {
             const int mm = s / spr, sl = s % spr;
             float t[8], gg[8];
-            if (in_regs) {
+            get_x(k, mm, sl, t);
+            if (k >= 0) {
 #pragma unroll
-                for (int kk = 0; kk < KS; ++kk)
-                    if (kk == k)
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) { t[j] = v[kk][j]; gg[j] = gm[kk][j]; }
+                for (int j = 0; j < 8; ++j) gg[j] = st.g[k][j];
             } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) t[j] = 0.f;
-                if (mm < a.m) load_x(mm, sl, t);
-                const f32x4 g0 = *reinterpret_cast<const f32x4 *>(a.gamma + sl * 8),
-                            g1 = *reinterpret_cast<const f32x4 *>(a.gamma + sl * 8 + 4);
-                gg[0] = g0.x; gg[1] = g0.y; gg[2] = g0.z; gg[3] = g0.w; gg[4] = g1.x; gg[5] = g1.y; gg[6] = g1.z; gg[7] = g1.w;
+                load8(a.gamma + sl * 8, gg);
             }
             float iv = 0.f;
 #pragma unroll
@@ -121,50 +193,29 @@ VH_DEV void prologue(const GemvArgs &a, const float *x, int K, float *red, Sink 
 #pragma unroll
             for (int j = 0; j < 8; ++j) o[j] = mm < a.m ? gg[j] * (t[j] * iv) : 0.f;
             emit(mm, sl, o);
-        }
+        });
         return;
     }
-    for (int s = threadIdx.x; s < nslot; s += kGemvThreads) {
+    for_slots([&](int k, int s) {
         const int mm = s / spr, sl = s % spr;
         float v[8];
-        if (mm >= a.m) {
+        if (PRO == PRO_ATTN) {
+            if (mm >= a.m) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = 0.f;
-        } else if (PRO == PRO_ATTN) {
-            // merge of all kAttnMaxSplits partials (empty splits have max -inf and weigh 0)
-            const AttnPartials &P = a.attn;
-            const int e0 = sl * 8, h = e0 / P.hd, d0 = e0 % P.hd;
-            const int64_t base = (int64_t(mm) * P.heads + h) * kAttnMaxSplits;
-            float pm[kAttnMaxSplits], pl[kAttnMaxSplits];
-            f32x4 o0[kAttnMaxSplits], o1[kAttnMaxSplits];
-#pragma unroll
-            for (int q = 0; q < kAttnMaxSplits; ++q) {
-                pm[q] = P.pm[base + q];
-                pl[q] = P.pl[base + q];
-                o0[q] = *reinterpret_cast<const f32x4 *>(P.po + (base + q) * P.hd + d0);
-                o1[q] = *reinterpret_cast<const f32x4 *>(P.po + (base + q) * P.hd + d0 + 4);
+                for (int j = 0; j < 8; ++j) v[j] = 0.f;
+            } else if (k >= 0) {
+                merge_partials(st.pm, st.pl, st.o0, st.o1, v);
+            } else {
+                float pm[kAttnMaxSplits], pl[kAttnMaxSplits];
+                f32x4 o0[kAttnMaxSplits], o1[kAttnMaxSplits];
+                load_partials(a.attn, mm, sl, pm, pl, o0, o1);
+                merge_partials(pm, pl, o0, o1, v);
             }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int q = 0; q < kAttnMaxSplits; ++q) mx = fmaxf(mx, pm[q]);
-            float L = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = 0.f;
-#pragma unroll
-            for (int q = 0; q < kAttnMaxSplits; ++q) {
-                const float w = pm[q] == -INFINITY ? 0.f : expf(pm[q] - mx);
-                L = fmaf(w, pl[q], L);
-                v[0] = fmaf(w, o0[q].x, v[0]); v[1] = fmaf(w, o0[q].y, v[1]); v[2] = fmaf(w, o0[q].z, v[2]); v[3] = fmaf(w, o0[q].w, v[3]);
-                v[4] = fmaf(w, o1[q].x, v[4]); v[5] = fmaf(w, o1[q].y, v[5]); v[6] = fmaf(w, o1[q].z, v[6]); v[7] = fmaf(w, o1[q].w, v[7]);
-            }
-            const float il = 1.0f / L;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] *= il;
         } else {
-            load_x(mm, sl, v);
+            get_x(k, mm, sl, v);
         }
         emit(mm, sl, v);
-    }
+    });
 }
 
 // Quantizes one 8-element slot of a 32-block held by 4 consecutive lanes (kernels.cpp:515-523): the block max
@@ -219,7 +270,7 @@ VH_DEV void reduce_store_prep(float (&acc)[R][M], float &out, int lane) {
 }
 
 // ------------------------------------------------------------------------------------------ int8 path
-template <int WT, int M, int R, int IT, int PRO, int EPI>
+template <int WT, int M, int R, int IT, int PRO, int EPI, bool STAGE>
 // The weight stream's operands come first so they are preloaded into SGPRs with the dispatch (kernarg preload).
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__restrict__ w, const float *__restrict__ scale,
                                                        const float *x, int32_t rows, int32_t K, GemvArgs a) {
@@ -244,17 +295,22 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__rest
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const int row = row0 + r;
+                // branch-free: out-of-range lanes read row 0 and drop it, so the load count is static
                 const bool ok = c < nchunk && row < rows;
-                const u32x4 *p = reinterpret_cast<const u32x4 *>(w + int64_t(row) * rb) + c;
-                wv[j][r] = ok ? __builtin_nontemporal_load(p) : u32x4{0u, 0u, 0u, 0u};
-                const int blk = WT == WT_Q8 ? (c >> 1) : c;
-                sv[j][r] = ok ? scale[int64_t(row) * nb + blk] : 0.f;
+                const int rowc = ok ? row : 0, cc = ok ? c : 0;
+                const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w + int64_t(rowc) * rb) + cc);
+                const float sc = scale[int64_t(rowc) * nb + (WT == WT_Q8 ? (cc >> 1) : cc)];
+                wv[j][r] = ok ? t : u32x4{0u, 0u, 0u, 0u};
+                sv[j][r] = ok ? sc : 0.f;
             }
         }
     };
+    ProStage<M, PRO> st;
+    if constexpr (STAGE) pro_stage<M, PRO>(a, x, K, st);  // the prologue's inputs first: loads return in issue order
+    __builtin_amdgcn_sched_barrier(0);                    // keep the weight stream behind them
     load(0);
 
-    prologue<M, PRO>(a, x, K, red, [&](int mm, int sl, const float (&v)[8]) {
+    prologue<M, PRO, STAGE>(a, x, K, red, st, [&](int mm, int sl, const float (&v)[8]) {
         uint32_t q2[2];
         float sc;
         quant_slot(v, q2, &sc);
@@ -328,7 +384,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__rest
 }
 
 // ------------------------------------------------------------------------------------------ f32 path
-template <int WT, int M, int R, int IT, int PRO, int EPI>
+template <int WT, int M, int R, int IT, int PRO, int EPI, bool STAGE>
 // The weight stream's operands come first so they are preloaded into SGPRs with the dispatch (kernarg preload).
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_flt(const uint8_t *__restrict__ w, const float *__restrict__ scale,
                                                        const float *x, int32_t rows, int32_t K, GemvArgs a) {
@@ -353,15 +409,24 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_flt(const uint8_t *__rest
             for (int r = 0; r < R; ++r) {
                 const int row = row0 + r;
                 const bool ok = c < nchunk && row < rows;
-                const u32x4 *p = reinterpret_cast<const u32x4 *>(w + int64_t(row) * rb) + c;
-                wv[j][r] = ok ? __builtin_nontemporal_load(p) : u32x4{0u, 0u, 0u, 0u};
-                sv[j][r] = (WT == WT_Q8 && ok) ? scale[int64_t(row) * nb + (c >> 1)] : 0.f;
+                const int rowc = ok ? row : 0, cc = ok ? c : 0;
+                const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w + int64_t(rowc) * rb) + cc);
+                wv[j][r] = ok ? t : u32x4{0u, 0u, 0u, 0u};
+                if (WT == WT_Q8) {
+                    const float sc = scale[int64_t(rowc) * nb + (cc >> 1)];
+                    sv[j][r] = ok ? sc : 0.f;
+                } else {
+                    sv[j][r] = 0.f;
+                }
             }
         }
     };
+    ProStage<M, PRO> st;
+    if constexpr (STAGE) pro_stage<M, PRO>(a, x, K, st);
+    __builtin_amdgcn_sched_barrier(0);
     load(0);
 
-    prologue<M, PRO>(a, x, K, red, [&](int mm, int sl, const float (&v)[8]) {
+    prologue<M, PRO, STAGE>(a, x, K, red, st, [&](int mm, int sl, const float (&v)[8]) {
         *reinterpret_cast<f32x4 *>(xf + mm * K + sl * 8) = f32x4{v[0], v[1], v[2], v[3]};
         *reinterpret_cast<f32x4 *>(xf + mm * K + sl * 8 + 4) = f32x4{v[4], v[5], v[6], v[7]};
     });

@@ -7,21 +7,28 @@
 
 namespace vh {
 
-template <int WT, int M, int R, int IT, int PRO, int EPI, bool INT>
-hipError_t gemv_run(const GemvArgs &a, hipStream_t s) {
+template <int WT, int M, int R, int IT, int PRO, int EPI, bool INT, bool STAGE>
+hipError_t gemv_run_staged(const GemvArgs &a, hipStream_t s) {
     const int per_block = (kGemvThreads / 64) * R;
     const dim3 grid((a.rows + per_block - 1) / per_block), block(kGemvThreads);
     if constexpr (INT) {
         const size_t smem = size_t(M) * a.K + size_t(M) * (a.K / 32) * 4 + size_t(M) * 16;
-        hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_gemv_int<WT, M, R, IT, PRO, EPI>), smem);
+        hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_gemv_int<WT, M, R, IT, PRO, EPI, STAGE>), smem);
         if (e != hipSuccess) return e;
-        return launch(k_gemv_int<WT, M, R, IT, PRO, EPI>, grid, block, smem, s, a.w, a.scale, a.x, a.rows, a.K, a);
+        return launch(k_gemv_int<WT, M, R, IT, PRO, EPI, STAGE>, grid, block, smem, s, a.w, a.scale, a.x, a.rows, a.K, a);
     } else {
         const size_t smem = size_t(M) * a.K * 4 + size_t(M) * 16;
-        hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_gemv_flt<WT, M, R, IT, PRO, EPI>), smem);
+        hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_gemv_flt<WT, M, R, IT, PRO, EPI, STAGE>), smem);
         if (e != hipSuccess) return e;
-        return launch(k_gemv_flt<WT, M, R, IT, PRO, EPI>, grid, block, smem, s, a.w, a.scale, a.x, a.rows, a.K, a);
+        return launch(k_gemv_flt<WT, M, R, IT, PRO, EPI, STAGE>, grid, block, smem, s, a.w, a.scale, a.x, a.rows, a.K, a);
     }
+}
+
+// Staged prologue (inputs loaded ahead of the weight stream) when they fit the staging registers.
+template <int WT, int M, int R, int IT, int PRO, int EPI, bool INT>
+hipError_t gemv_run(const GemvArgs &a, hipStream_t s) {
+    if (pro_stageable<M, PRO>(a.K)) return gemv_run_staged<WT, M, R, IT, PRO, EPI, INT, true>(a, s);
+    return gemv_run_staged<WT, M, R, IT, PRO, EPI, INT, false>(a, s);
 }
 
 // The (R, IT) tiles instantiated; gemv_tile() (vh_gemv_tile.cpp) picks only these.
