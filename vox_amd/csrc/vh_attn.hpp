@@ -83,15 +83,17 @@ struct AttnSmem {
 };
 
 // grid (kAttnMaxSplits, kv_heads, m), block 256. Each lane holds 8 consecutive elements of one key row;
-// LPK = HD / 8 lanes share a key, a wave covers 64 / LPK keys per step, a block NGRP keys. Splits past the row's
-// key count write empty partials. Loads that do not depend on the row's cache view (q, the new key/value, the
-// RoPE row) are issued before it arrives; each lane group then loads all of its keys in one batch of U when the
-// split holds at most U * NGRP keys.
+// LPK = HD / 8 lanes share a key, a wave covers 64 / LPK keys per step, a block NGRP keys. Split s takes the keys
+// j = s + S (grp + NGRP u). Row 0's cache bases, the q|k|v input and the RoPE rows are leading scalar arguments
+// (preloaded with the dispatch): the first kAttnSpecKeys keys' loads go out before the row's position arrives and
+// are masked by it afterwards, so the cache fetch does not wait for the row view. Later keys load per batch of U.
 template <int HD, int G, bool FUSED>
-__global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
+__global__ __launch_bounds__(256) void k_attn(const _Float16 *kc0, const _Float16 *vc0, const float *qkv,
+                                              const float *rope_rows, int32_t cap0, int32_t layer, AttnArgs a) {
     using Sm = AttnSmem<HD, G>;
-    constexpr int LPK = Sm::LPK, KPW = Sm::KPW, NGRP = Sm::NGRP, HALF = HD / 2;
+    constexpr int LPK = Sm::LPK, KPW = Sm::KPW, NGRP = Sm::NGRP, HALF = HD / 2, S = kAttnMaxSplits;
     constexpr int U = G <= 2 ? 8 : G <= 4 ? 4 : 2;
+    constexpr int U1 = kAttnSpecKeys / (S * NGRP) < U ? kAttnSpecKeys / (S * NGRP) : U;  // speculative batch
     constexpr int NQ = (G * HALF + 255) / 256;  // q rotate-half pairs per thread
     extern __shared__ __align__(16) uint8_t attn_smem[];
     Sm &sm = *reinterpret_cast<Sm *>(attn_smem);
@@ -99,13 +101,27 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     const int lane = tid & 63, wave = tid >> 6, sub = lane % LPK, grp = wave * KPW + lane / LPK;
     const AttnPartials &P = a.part;
     const int qd = P.heads * HD, kd = a.kv_heads * HD;
-    const float *row = a.qkv + int64_t(i) * a.ldqkv;
+    const float *row = qkv + int64_t(i) * a.ldqkv;
+    const int64_t plane = (int64_t(layer) * a.kv_heads + g) * HD;  // x cap: offset of this kv head's plane
+
+    // row 0 (every decode step): cache bases from the arguments, speculative loads of the first keys
+    f16x8 kb[U], vb[U];
+    if (i == 0) {
+        const _Float16 *K = kc0 + plane * cap0, *V = vc0 + plane * cap0;
+#pragma unroll
+        for (int u = 0; u < U1; ++u) {
+            const int64_t j = s + int64_t(S) * (grp + NGRP * u);
+            const int64_t jc = j < cap0 ? j : 0;  // stay inside the cache; masked below
+            kb[u] = *reinterpret_cast<const f16x8 *>(K + jc * HD + sub * 8);
+            vb[u] = *reinterpret_cast<const f16x8 *>(V + jc * HD + sub * 8);
+        }
+    }
 
     float qx0[NQ], qx1[NQ], qc[NQ], qsn[NQ];
     float kx0 = 0.f, kx1 = 0.f, vx0 = 0.f, vx1 = 0.f, kc = 0.f, ksn = 0.f;
     const bool kv_lane = tid >= 192 && tid - 192 < HALF;  // last wave: the new key/value of a fused row
     if (FUSED) {
-        const float *cs = a.rope_rows + int64_t(i) * HD;
+        const float *cs = rope_rows + int64_t(i) * HD;
 #pragma unroll
         for (int k = 0; k < NQ; ++k) {
             const int t = tid + 256 * k, h = t / HALF, p = t % HALF;
@@ -129,9 +145,8 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     }
     const RowRef rr = P.rows[i];
     const int64_t n = rr.pos + 1;
-    const int S = attn_splits(n);
     const int64_t pb = (int64_t(i) * P.heads + g * G) * kAttnMaxSplits + s;  // + h * kAttnMaxSplits
-    if (s >= S) {  // no keys in this split
+    if (s >= n) {  // no keys in this split
         for (int t = tid; t < G * HD; t += 256) {
             const int h = t / HD, e = t % HD;
             const int64_t pidx = pb + int64_t(h) * kAttnMaxSplits;
@@ -140,21 +155,17 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
         }
         return;
     }
-    const int64_t C = (n + S - 1) / S, k0 = int64_t(s) * C, k1 = k0 + C < n ? k0 + C : n;
-    const bool last = FUSED && s == S - 1;
-    const int64_t cbase = (int64_t(a.layer) * a.kv_heads + g) * rr.cap * HD;
-    const _Float16 *K = rr.k + cbase, *V = rr.v + cbase;
-
-    // keys read from the cache: all of [k0, k1), except the new key of a fused row (processed from LDS below)
-    const int64_t kend = last ? k1 - 1 : k1;
-    f16x8 kb[U], vb[U];
-    const int64_t j0 = k0 + grp;
+    const bool last = FUSED && rr.pos % S == s;  // this split holds the new key at pos
+    const _Float16 *K = rr.k + plane * rr.cap, *V = rr.v + plane * rr.cap;
+    // keys read from the cache: j < kend, except the new key of a fused row (processed from LDS below)
+    const int64_t kend = last ? n - 1 : n;
+    if (i != 0) {  // other rows: their speculative batch waits for the row view
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int64_t j = j0 + int64_t(u) * NGRP;
-        if (j < kend) {
-            kb[u] = *reinterpret_cast<const f16x8 *>(K + j * HD + sub * 8);
-            vb[u] = *reinterpret_cast<const f16x8 *>(V + j * HD + sub * 8);
+        for (int u = 0; u < U1; ++u) {
+            const int64_t j = s + int64_t(S) * (grp + NGRP * u);
+            const int64_t jc = j < rr.cap ? j : 0;
+            kb[u] = *reinterpret_cast<const f16x8 *>(K + jc * HD + sub * 8);
+            vb[u] = *reinterpret_cast<const f16x8 *>(V + jc * HD + sub * 8);
         }
     }
 
@@ -173,7 +184,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
             norm_rope<HALF>(kx0, kx1, a.kn, p, a.eps, kc, ksn);
             const _Float16 k0h = _Float16(kx0), k1h = _Float16(kx1), v0h = _Float16(vx0), v1h = _Float16(vx1);
             const int64_t off = rr.pos * HD;
-            _Float16 *Kw = rr.k + cbase, *Vw = rr.v + cbase;
+            _Float16 *Kw = rr.k + plane * rr.cap, *Vw = rr.v + plane * rr.cap;
             Kw[off + p] = k0h;
             Kw[off + p + HALF] = k1h;
             Vw[off + p] = v0h;
@@ -245,23 +256,30 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
             for (int e = 0; e < 8; ++e) acc[h][e] = o[e];
         }
     };
-    for (int64_t jb = j0; jb < kend; jb += int64_t(U) * NGRP) {
+    {  // the speculative batch, masked by the row's length
+        bool valid[U1];
+#pragma unroll
+        for (int u = 0; u < U1; ++u) {
+            valid[u] = s + int64_t(S) * (grp + NGRP * u) < kend;
+            if (!valid[u]) kb[u] = vb[u] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};  // masked: finite zeros, weight 0
+        }
+        consume(std::integral_constant<int, U1>(), kb, vb, valid);
+    }
+    // keys past the speculative batch, U groups of NGRP per batch
+    for (int64_t jb = s + int64_t(S) * (grp + NGRP * U1); jb < kend; jb += int64_t(S) * NGRP * U) {
         bool valid[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            valid[u] = jb + int64_t(u) * NGRP < kend;
-            if (!valid[u]) kb[u] = vb[u] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};  // masked: finite zeros, weight 0
-        }
-        consume(std::integral_constant<int, U>(), kb, vb, valid);
-        // next batch
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t j = jb + int64_t(U + u) * NGRP;
-            if (j < kend) {
+            const int64_t j = jb + int64_t(S) * NGRP * u;
+            valid[u] = j < kend;
+            if (valid[u]) {
                 kb[u] = *reinterpret_cast<const f16x8 *>(K + j * HD + sub * 8);
                 vb[u] = *reinterpret_cast<const f16x8 *>(V + j * HD + sub * 8);
+            } else {
+                kb[u] = vb[u] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
             }
         }
+        consume(std::integral_constant<int, U>(), kb, vb, valid);
     }
     if (last && grp == 0) {  // the new key at pos, from LDS (f16-rounded like the cache)
         f16x8 kn1[1], vn1[1];

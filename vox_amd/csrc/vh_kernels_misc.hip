@@ -59,39 +59,48 @@ hipError_t launch_qk_post(const QkArgs &a, int m, hipStream_t s) {
     return launch(k_qk_post, dim3(a.heads + a.kv_heads, m), dim3(64), 0, s, a);
 }
 
+struct AttnLaunch {
+    const _Float16 *kc0, *vc0;
+    const float *qkv, *rope_rows;
+    int32_t cap0, layer;
+};
+
 template <int HD, int G>
-static hipError_t attn_hg(const AttnArgs &a, int m, bool fused, hipStream_t s) {
+static hipError_t attn_hg(const AttnArgs &a, const AttnLaunch &l, int m, bool fused, hipStream_t s) {
     const size_t smem = sizeof(AttnSmem<HD, G>);
     const dim3 grid(kAttnMaxSplits, a.kv_heads, m);
     if (fused) {
         hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_attn<HD, G, true>), smem);
         if (e != hipSuccess) return e;
-        return launch(k_attn<HD, G, true>, grid, dim3(256), smem, s, a);
+        return launch(k_attn<HD, G, true>, grid, dim3(256), smem, s, l.kc0, l.vc0, l.qkv, l.rope_rows, l.cap0, l.layer, a);
     }
     hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_attn<HD, G, false>), smem);
     if (e != hipSuccess) return e;
-    return launch(k_attn<HD, G, false>, grid, dim3(256), smem, s, a);
+    return launch(k_attn<HD, G, false>, grid, dim3(256), smem, s, l.kc0, l.vc0, l.qkv, l.rope_rows, l.cap0, l.layer, a);
 }
 
 template <int HD>
-static hipError_t attn_h(const AttnArgs &a, int group, int m, bool fused, hipStream_t s) {
+static hipError_t attn_h(const AttnArgs &a, const AttnLaunch &l, int group, int m, bool fused, hipStream_t s) {
     switch (group) {
-        case 1: return attn_hg<HD, 1>(a, m, fused, s);
-        case 2: return attn_hg<HD, 2>(a, m, fused, s);
-        case 3: return attn_hg<HD, 3>(a, m, fused, s);
-        case 4: return attn_hg<HD, 4>(a, m, fused, s);
-        case 5: return attn_hg<HD, 5>(a, m, fused, s);
-        case 6: return attn_hg<HD, 6>(a, m, fused, s);
-        case 7: return attn_hg<HD, 7>(a, m, fused, s);
-        case 8: return attn_hg<HD, 8>(a, m, fused, s);
+        case 1: return attn_hg<HD, 1>(a, l, m, fused, s);
+        case 2: return attn_hg<HD, 2>(a, l, m, fused, s);
+        case 3: return attn_hg<HD, 3>(a, l, m, fused, s);
+        case 4: return attn_hg<HD, 4>(a, l, m, fused, s);
+        case 5: return attn_hg<HD, 5>(a, l, m, fused, s);
+        case 6: return attn_hg<HD, 6>(a, l, m, fused, s);
+        case 7: return attn_hg<HD, 7>(a, l, m, fused, s);
+        case 8: return attn_hg<HD, 8>(a, l, m, fused, s);
         default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_attention(const AttnArgs &a, int hd, int group, int m, bool fused, hipStream_t s) {
+hipError_t launch_attention(const AttnArgs &a, const _Float16 *kc0, const _Float16 *vc0, int64_t cap0, const float *qkv,
+                            const float *rope_rows, int layer, int hd, int group, int m, bool fused, hipStream_t s) {
     if (m <= 0) return hipSuccess;
-    if (hd == 128) return attn_h<128>(a, group, m, fused, s);
-    if (hd == 64) return attn_h<64>(a, group, m, fused, s);
+    if (cap0 <= 0 || cap0 > INT32_MAX) return hipErrorInvalidValue;
+    const AttnLaunch l{kc0, vc0, qkv, rope_rows, int32_t(cap0), int32_t(layer)};
+    if (hd == 128) return attn_h<128>(a, l, group, m, fused, s);
+    if (hd == 64) return attn_h<64>(a, l, group, m, fused, s);
     return hipErrorInvalidValue;
 }
 

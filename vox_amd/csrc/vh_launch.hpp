@@ -29,8 +29,10 @@ void gemv_tile(int rows, int nchunk, int M, bool swiglu, int *R, int *IT);
 
 hipError_t launch_qk_post(const QkArgs &a, int m, hipStream_t s);
 // Split-K attention partials of m rows (merged by the PRO_ATTN GEMV prologue). fused: rows of distinct sequences,
-// q/k post-processing and the K/V append happen inside; otherwise k_qk_post ran first.
-hipError_t launch_attention(const AttnArgs &a, int hd, int group, int m, bool fused, hipStream_t s);
+// q/k post-processing and the K/V append happen inside; otherwise k_qk_post ran first. kc0/vc0/cap0: row 0's cache
+// (the same as the first row view); qkv: [m][a.ldqkv]; rope_rows: [m][hd] (fused).
+hipError_t launch_attention(const AttnArgs &a, const _Float16 *kc0, const _Float16 *vc0, int64_t cap0, const float *qkv,
+                            const float *rope_rows, int layer, int hd, int group, int m, bool fused, hipStream_t s);
 hipError_t launch_sample(const SampleCfgDev *cfg, const float *logits, int n, int32_t *out, hipStream_t s);
 
 hipError_t launch_quant_q8(const float *w, int64_t nblocks, int8_t *q, float *scale, hipStream_t s);

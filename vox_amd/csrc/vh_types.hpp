@@ -18,14 +18,11 @@ struct RowRef {
 };
 
 constexpr int kAttnMaxSplits = 8;  // split-K blocks per (row, kv head); the merge happens in the o-GEMV prologue
-constexpr int kAttnMinKeys = 64;   // fewer splits when there are fewer keys
+constexpr int kAttnSpecKeys = 512; // cache keys each (row, kv head) loads before its position is known
 
-// Number of key splits holding keys for n visible keys. The attention kernel always writes all kAttnMaxSplits
-// partials (splits >= attn_splits(n) are empty: max -inf, denominator 0, output 0), so readers merge a fixed count.
-__host__ __device__ inline int attn_splits(int64_t n) {
-    const int64_t s = (n + kAttnMinKeys - 1) / kAttnMinKeys;
-    return int(s < 1 ? 1 : s > kAttnMaxSplits ? kAttnMaxSplits : s);
-}
+// Split s of a row holds the keys j with j % kAttnMaxSplits == s (interleaved, so a split's key set does not
+// depend on the row's length). Every split writes partials; one with no keys (s >= n) writes an empty one
+// (max -inf, denominator 0, output 0), so readers merge a fixed count.
 
 // Split-K attention partials of m rows: running max, denominator and unnormalized output per (row, head, split).
 // Every split of every row is written by each attention launch.
@@ -67,13 +64,11 @@ struct QkArgs {
 // append) for rows whose sequences differ (decode, pairs, B sessions); otherwise q comes from `q` and the keys of
 // this pass are already in the cache (prefill of one sequence).
 struct AttnArgs {
-    const float *qkv;        // fused: [m][ldqkv]
-    int64_t ldqkv;
+    int64_t ldqkv;           // row stride of the fused q|k|v input (passed to the kernel as its own argument)
     const float *q;          // not fused: [m][qd]
     const float *qn, *kn;
-    const float *rope_rows;  // fused: [m][hd/2][2] (cos, sin) at each row's position, staged with the row views
     AttnPartials part;
-    int32_t kv_heads, layer;
+    int32_t kv_heads;
     float scale, eps;
 };
 

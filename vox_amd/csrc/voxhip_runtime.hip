@@ -426,9 +426,12 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
             probed(pr, VOXHIP_K_QKPOST, [&] { HIPCHECK(launch_qk_post(qa, mc, s)); });
         }
         AttnArgs aa;
-        aa.qkv = X.qkv; aa.ldqkv = ldqkv; aa.q = X.q; aa.qn = qn; aa.kn = kn; aa.rope_rows = X.rope_rows_dev; aa.part = part;
-        aa.kv_heads = X.kvh; aa.layer = li; aa.scale = 1.0f / std::sqrt(float(X.hd)); aa.eps = X.eps;
-        probed(pr, VOXHIP_K_ATTN, [&] { HIPCHECK(launch_attention(aa, X.hd, X.heads / X.kvh, mc, fused, s)); });
+        aa.ldqkv = ldqkv; aa.q = X.q; aa.qn = qn; aa.kn = kn; aa.part = part;
+        aa.kv_heads = X.kvh; aa.scale = 1.0f / std::sqrt(float(X.hd)); aa.eps = X.eps;
+        const RowRef &r0 = X.rows_last.at(0);
+        probed(pr, VOXHIP_K_ATTN, [&] {
+            HIPCHECK(launch_attention(aa, r0.k, r0.v, r0.cap, X.qkv, X.rope_rows_dev, li, X.hd, X.heads / X.kvh, mc, fused, s));
+        });
         probed(pr, VOXHIP_K_O, [&] {
             gemv(Mo, m_total, PRO_ATTN, EPI_ACC, nullptr, 0, mc, X.h, X.H, nullptr, 0.f, nullptr, s, &part);
         });
@@ -1320,8 +1323,7 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, const float *d_x, int h
             // ---- algorithmic bytes per launch of each class: every byte the kernel must move once
             // (weights + scales + bias, activations in and out, cache reads and appends, attention partials)
             const int qd = X.heads * X.hd, kd = X.kvh * X.hd;
-            const double S = attn_splits(pos0 + 1);
-            const double partials = double(X.heads) * S * (X.hd + 2) * 4.0;
+            const double partials = double(X.heads) * kAttnMaxSplits * (X.hd + 2) * 4.0;
             double bytes[VOXHIP_K_CLASSES] = {0};
             for (const LayerDev &L : X.L) {
                 bytes[VOXHIP_K_QKV] += double(g.mats[size_t(L.qkv)].bytes) + X.H * 4.0 + (qd + 2.0 * kd) * 4.0;
