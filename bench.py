@@ -94,6 +94,53 @@ def cpu_baseline(vh, dec, seconds, x):
                       f"sampling, {threads} threads, median of the steps, {sum(times):.1f} s of CPU work)"}
 
 
+def bench_cfg1(vh):
+    """BASELINE configs[0] on the device: one q8 FFN block (H 1024, FFN 3072), rotating over 40 weight sets
+    (425 MB, above the 256 MB Infinity Cache)."""
+    us = vh.bench_ffn_q8(1024, 3072, 40, 3, 20)
+    nbytes = 10_616_832  # gate|up + down q8 weights and scales
+    return {"workload": "q8 FFN block 1024->3072->1024 (BASELINE configs[0]), 40 rotating weight sets",
+            "us_per_block": round(us, 3), "bytes_per_block": nbytes, "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def bench_cfg3(vh, synth, steps, warmup):
+    """the 1.7B-shaped q4 talker (f16 block scales, q8 head) at KV length 1024, batch 1 and
+    8 independent sessions, device-resident graph replays."""
+    dec = synth.Decoder(synth.TALKER_1_7B_Q4, seed=0)
+    c = dec.cfg
+    pos, H = c["kv_len"], c["hidden"]
+    rng = np.random.default_rng(1)
+    out = {"workload": "qwen3-tts-1.7b-talker-decode-q4 f16 scales (BASELINE configs[2]), KV 1024"}
+    for B in (1, 8):
+        seqs = [dec.seq] + [dec.extra_seq(0xC0DE + 17 * b) for b in range(1, B)]
+        x = rng.standard_normal((B, H)).astype(np.float32)
+        dx, dtok = vh.DevBuf(x.nbytes), vh.DevBuf(4 * B)
+        dx.upload(x)
+        cfgs = [vh.sample_cfg(0.9, 1.0, 50, seed=0, frame=b) for b in range(B)]
+
+        def step():
+            if B == 1:
+                vh.decode_dev(dec.xfmr, dec.seq, pos, dx, 1, None, dec.head, None, cfgs[0], dtok)
+            else:
+                vh.decode_steps_dev(dec.xfmr, seqs, [pos] * B, dx, None, dec.head, None, cfgs, dtok)
+        for _ in range(warmup):
+            step()
+        vh.sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        vh.sync()
+        ms = (time.perf_counter() - t0) * 1000.0 / steps
+        kv = c["layers"] * 2 * (pos + 1) * c["kv_heads"] * c["head_dim"] * 2 * B
+        nbytes = dec.weight_bytes() + kv
+        out[f"b{B}"] = {"tok_s": round(B * 1000.0 / ms, 2), "ms_per_step": round(ms, 5), "bytes_per_step": nbytes,
+                        "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        dx.free()
+        dtok.free()
+    return out
+
+
 def load_traffic(kernel_class):
     p = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(p):
@@ -111,6 +158,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-other", action="store_true", help="skip the configs[0] / configs[2] measurements")
     ap.add_argument("--no-breakdown", action="store_true",
                     help="skip the event-timed per-kernel pass (for runs under rocprofv3, whose tracer does not survive "
                          "HIP events recorded around graph launches); rocprof then times the graph's kernels itself")
@@ -182,6 +230,12 @@ def main():
     step_bytes = dec.step_bytes(POS)
     log(json.dumps(classes))
 
+    other = None
+    if not args.no_other:
+        t0 = time.perf_counter()
+        other = {"configs[0]": bench_cfg1(vh), "configs[2]": bench_cfg3(vh, synth, 100, 10)}
+        log(f"other configs: {json.dumps(other)} ({time.perf_counter() - t0:.1f} s)")
+
     cpu = None
     if not args.no_cpu:
         t0 = time.perf_counter()
@@ -215,6 +269,7 @@ def main():
                  "kernel_us_per_step": round(r.kernel_ms_per_step * 1000, 2), "graph_us_per_step": round(r.ms_per_step * 1000, 2),
                  "kernels_per_step": r.kernels_per_step},
         "stream": stream,
+        "other_configs": other,
         "kernels": classes,
         "kernel_timing": "hipExtLaunchKernel start/stop events" if r.kernel_stamped else "stream events around each launch",
         "cpu_baseline": cpu,

@@ -82,7 +82,9 @@ void voxhip_mem_info_get(voxhip_mem_info *out);            /* gpu_mem_info (gpu.
 
 /* ---------------------------------------------------------------- matrices */
 /* gpu_upload (gpu.hpp:14). n_parts > 1 stacks the parts' rows into one device matrix (same type
- * and cols, all or none with bias), as upload_parts (gpu_vulkan.cpp:476-536). Returns a handle or -1. */
+ * and cols, all or none with bias), as upload_parts (gpu_vulkan.cpp:476-536). Returns a handle or -1.
+ * Q4 matrices whose block scales are all exact in f16 keep them in 2 bytes on the device (identical products,
+ * a 10% smaller stream); voxhip_mat_download returns them widened to f32. */
 int voxhip_upload(const voxhip_mat *parts, int n_parts);
 /* gpu_matmul (kernels.hpp:89): y[m][rows] = x[m][cols] . W^T (+ bias), host x and y.
  * Semantics of matmul (kernels.cpp:653-705): Q8 with m <= 8 and Q4 quantize x per 32-block to int8
@@ -184,11 +186,21 @@ int voxhip_sync(void);
 int voxhip_decode_dev(int xfmr, int seq, int64_t pos0, const float *d_x, int64_t m, float *d_out_last, int head,
                       float *d_logits, const voxhip_sample_cfg *cfg, int32_t *d_token);
 
+/* transformer_forward_steps (kernels.hpp:144-147) on device-resident inputs: one token for each of B (1..8)
+ * distinct sequences at its own position pos[b], in one captured graph per sequence list (weights read once for
+ * the B rows). d_x [B][hidden]; d_out (or NULL) [B][hidden] normed states; with head >= 0, d_logits (or NULL)
+ * [B][head rows]; with cfgs != NULL, row b is sampled with cfgs[b] into d_tokens[b]. Asynchronous. */
+int voxhip_decode_steps_dev(int xfmr, const int32_t *seqs, const int64_t *pos, int64_t B, const float *d_x, float *d_out,
+                            int head, float *d_logits, const voxhip_sample_cfg *cfgs, int32_t *d_tokens);
+
 /* Synthetic weights and caches, generated on the device (Philox4x32-10 Box-Muller, mean + std * z).
  * voxhip_mat_synthetic: f32 values, then quantized on the device to `type` with the reference's
- * quantizer (Q8: kernels.cpp:918-929; Q4: kernels.cpp:606-645; F16/BF16: nearest even). Returns a handle. */
+ * quantizer (Q8: kernels.cpp:918-929; Q4: kernels.cpp:606-645; F16/BF16: nearest even). Returns a handle.
+ * flags: VOXHIP_SYN_BIAS adds an f32 bias ~N(0, std); VOXHIP_SYN_F16_SCALES rounds Q4 block scales to f16 (the
+ * "4-bit + f16 scale" format; the matrix then stores 2-byte scales, see voxhip_upload). */
+enum { VOXHIP_SYN_BIAS = 1, VOXHIP_SYN_F16_SCALES = 2 };
 int voxhip_mat_synthetic(int32_t type, int64_t rows, int64_t cols, uint64_t seed, uint32_t stream, float mean,
-                         float std, int with_bias);
+                         float std, int flags);
 /* Copies a device matrix back in the reference host layout (data, scale, bias may be NULL). */
 int voxhip_mat_download(int mat, void *data, float *scale, float *bias);
 /* Releases a device matrix that no transformer uses (the reference keeps uploads for the process lifetime;
@@ -245,6 +257,11 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, const float *d_x, int h
 /* Times one GEMV kernel configuration on `copies` distinct device copies of a synthetic q8 matrix
  * (rotating, so the working set exceeds the 256 MB Infinity Cache): average ms per launch. */
 int voxhip_bench_gemv_q8(int64_t rows, int64_t cols, int copies, int warmup, int iters, double *ms_per_launch);
+
+/* BASELINE configs[0] on the device: one q8 FFN block (RMSNorm -> gate|up GEMV + SwiGLU -> down GEMV + residual,
+ * two kernels) over `copies` distinct weight sets in one graph, so the working set exceeds the 256 MB Infinity
+ * Cache: average microseconds per block. No reference counterpart (benchmark helper). */
+int voxhip_bench_ffn_q8(int64_t hidden, int64_t inter, int copies, int warmup, int iters, double *us_per_block);
 
 /* Times a plain 16-byte device copy of `bytes` (STREAM copy; reads and writes `bytes` each): average ms per copy.
  * The same kernel calibrates the HBM traffic counters. No reference counterpart (benchmark helper). */

@@ -15,44 +15,9 @@ import numpy as np
 import pytest
 
 from conftest import rel_err
+from talker import kl_top5, to_oracle
 
 pytestmark = pytest.mark.gpu
-
-
-def to_oracle(oracle, hip, dec):
-    c = dec.cfg
-    L = []
-    for li in range(c["layers"]):
-        d = {}
-        for n in ("q", "k", "v", "o", "gate", "up", "down"):
-            h = dec.mats[li][n]
-            rows, cols = hip.mat_shape(h)
-            data, scale, _ = hip.mat_download(h, c["wtype"])
-            d[n] = oracle.Mat(c["wtype"], data, rows, cols, scale)
-        d.update(dec.layers[li])
-        L.append(d)
-    X = oracle.Xfmr(L, dec.final_norm, c["hidden"], c["heads"], c["kv_heads"], c["head_dim"], c["inter"], c["eps"], dec.inv_freq)
-    kd = c["kv_heads"] * c["head_dim"]
-    kv = oracle.KV(c["layers"], c["kv_len"] + 8, kd, kv_f16=1)
-    for li in range(c["layers"]):
-        k, v = hip.seq_download(dec.seq, li, c["kv_len"], kd)
-        kv.k[li, :c["kv_len"]] = k
-        kv.v[li, :c["kv_len"]] = v
-    kv.c.len = c["kv_len"]
-    hd, hs, _ = hip.mat_download(dec.head, c["head_type"])
-    head = oracle.Mat(c["head_type"], hd, c["head_rows"], c["hidden"], hs)
-    return X, kv, head
-
-
-def kl_top5(ours, ref):
-    """KL(ref || ours) of softmax(logits) and whether the reference argmax is in our top-5 (cli/main.cpp:769-787)."""
-    a, b = np.asarray(ours, np.float64), np.asarray(ref, np.float64)
-    la = a.max() + np.log(np.exp(a - a.max()).sum())
-    lb = b.max() + np.log(np.exp(b - b.max()).sum())
-    lp, lq = b - lb, a - la
-    kl = float(np.sum(np.exp(lp) * (lp - lq)))
-    ib = int(np.argmax(b))
-    return kl, int(np.sum(a > a[ib])) < 5
 
 
 def test_talker_0_6b_decode_step(hip, oracle):
@@ -60,7 +25,7 @@ def test_talker_0_6b_decode_step(hip, oracle):
     oracle.lib().vo_set_threads(8)
     dec = synth.Decoder(synth.TALKER_0_6B, seed=0)
     c = dec.cfg
-    X, kv, head = to_oracle(oracle, hip, dec)
+    X, (kv,), head = to_oracle(oracle, hip, dec)
     rng = np.random.default_rng(0)
     pos = c["kv_len"]
     # per layer, teacher-forced, at the full shape (both sides write this step's K/V of the layer at `pos`)

@@ -60,6 +60,30 @@ def test_matmul_parity(hip, oracle, wt, rows, cols):
         assert rel_err(y, r) < GEMV_TOL, (wt, rows, cols, m, rel_err(y, r))
 
 
+@pytest.mark.parametrize("rows,cols", [(4096, 2048), (2048, 6144), (37, 160)])
+def test_q4_f16_scales(hip, oracle, rows, cols):
+    # Q4 scales that are exact in f16 are stored in 2 bytes on the device (the cfg 3 "4-bit + f16 scale" format):
+    # same products as the f32 scales, and the download widens them back bit-exactly.
+    rng = np.random.default_rng(rows + cols)
+    data, scale, _ = make_mat(rng, Q4, rows, cols)
+    scale = scale.astype(np.float16).astype(np.float32)
+    h = hip.upload(hip.HostMat(Q4, data, rows, cols, scale))
+    d2, s2, _ = hip.mat_download(h, Q4)
+    assert np.array_equal(d2, data) and np.array_equal(s2.view(np.uint32), scale.view(np.uint32))
+    M = oracle.Mat(Q4, data, rows, cols, scale)
+    for m in (1, 3, 8):
+        x = rng.standard_normal((m, cols)).astype(np.float32)
+        assert rel_err(hip.matmul(h, x), oracle.matmul(M, x)) < GEMV_TOL
+    # one scale that is not exact in f16 keeps the whole matrix on f32 scales, with the same results
+    scale2 = scale.copy()
+    scale2.flat[7] = np.float32(scale2.flat[7] * (1 + 2**-20))
+    h2 = hip.upload(hip.HostMat(Q4, data, rows, cols, scale2))
+    x = rng.standard_normal((2, cols)).astype(np.float32)
+    assert rel_err(hip.matmul(h2, x), oracle.matmul(oracle.Mat(Q4, data, rows, cols, scale2), x)) < GEMV_TOL
+    _, s3, _ = hip.mat_download(h2, Q4)
+    assert np.array_equal(s3.view(np.uint32), scale2.view(np.uint32))
+
+
 def test_matmul_stacked_upload(hip, oracle):
     # n_parts > 1 stacks rows like upload_parts (gpu_vulkan.cpp:476-536)
     rng = np.random.default_rng(3)

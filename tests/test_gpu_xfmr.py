@@ -156,6 +156,39 @@ def test_pair_and_steps(hip, oracle):
         assert rel_err(log3[i], oracle_head(oracle, mdl, out3[i])) < TOL
 
 
+def test_decode_steps_dev(hip, oracle):
+    # B sessions at their own positions in one device-resident graph: same states and logits as the host-pointer
+    # forward_steps, each row's token from the oracle sampler on the device logits with that row's counter.
+    mdl = Model(710, 2, 256, 4, 2, 128, 512, wtype=Q4, head_rows=200)
+    xf, head = build(hip, mdl)
+    rng = np.random.default_rng(12)
+    B = 5
+    seqs_a = [hip.seq_create(xf, 32) for _ in range(B)]
+    seqs_b = [hip.seq_create(xf, 32) for _ in range(B)]
+    lens = [3, 7, 1, 5, 9]
+    for sa, sb, n in zip(seqs_a, seqs_b, lens):
+        pre = rng.standard_normal((n, 256)).astype(np.float32)
+        hip.forward(xf, sa, 0, pre, 256)
+        hip.forward(xf, sb, 0, pre, 256)
+    x = rng.standard_normal((B, 256)).astype(np.float32)
+    out_ref, log_ref = hip.forward_steps(xf, seqs_a, lens, x, 256, head=head)
+    dx, dout, dlog, dtok = hip.DevBuf(x.nbytes), hip.DevBuf(x.nbytes), hip.DevBuf(B * 200 * 4), hip.DevBuf(B * 4)
+    dx.upload(x)
+    cfgs = [hip.sample_cfg(0.9, 0.8, 25, seed=77, frame=10 + b, codebook=b) for b in range(B)]
+    for rep in range(3):
+        hip.decode_steps_dev(xf, seqs_b, lens, dx, dout, head, dlog, cfgs, dtok)
+        hip.sync()
+        out = dout.download(B * 256, np.float32).reshape(B, 256)
+        lg = dlog.download(B * 200, np.float32).reshape(B, 200)
+        assert np.array_equal(out, out_ref) and np.array_equal(lg, log_ref), rep
+        toks = dtok.download(B, np.int32)
+        for b in range(B):
+            u = oracle.uniform(77, 10 + b, b, 0)
+            assert toks[b] == oracle.sample_logits(lg[b], 0.9, 0.8, 25, 1.0, None, u), (rep, b)
+    for bf in (dx, dout, dlog, dtok):
+        bf.free()
+
+
 def test_decode_graph_replays(hip, oracle):
     # The captured decode step replays to the same result as the host-pointer forward, every replay.
     mdl = Model(700, 2, 256, 4, 2, 128, 512, wtype=Q8, head_rows=256)

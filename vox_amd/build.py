@@ -17,7 +17,8 @@ OUT = os.path.join(ROOT, "vox_amd")
 BUILD = os.path.join(ROOT, "vox_amd", "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-HIP_SOURCES = ["voxhip_runtime.hip", "vh_kernels_misc.hip", "vh_gemv_tile.hip", "vh_gemv_q8.hip", "vh_gemv_q4.hip", "vh_gemv_q8f.hip",
+HIP_SOURCES = ["voxhip_runtime.hip", "vh_kernels_misc.hip", "vh_gemv_tile.hip", "vh_gemv_q8.hip", "vh_gemv_q4.hip", "vh_gemv_q4h.hip",
+               "vh_gemv_q8f.hip",
                "vh_gemv_f32.hip", "vh_gemv_f16.hip", "vh_gemv_bf16.hip"]
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
              # packed FP32 instructions stay off (the compiler must not emit v_pk_{add,mul,fma}_f32)

@@ -26,7 +26,7 @@ namespace vh {
 
 template <int WT>
 VH_DEV int64_t row_bytes(int K) {
-    return WT == WT_F32 ? int64_t(K) * 4 : WT == WT_Q8 ? int64_t(K) : WT == WT_Q4 ? int64_t(K) / 2 : int64_t(K) * 2;
+    return WT == WT_F32 ? int64_t(K) * 4 : WT == WT_Q8 ? int64_t(K) : (WT == WT_Q4 || WT == WT_Q4H) ? int64_t(K) / 2 : int64_t(K) * 2;
 }
 
 // ---------------------------------------------------------------------------------------------- prologue
@@ -274,7 +274,7 @@ template <int WT, int M, int R, int IT, int PRO, int EPI, bool STAGE>
 // The weight stream's operands come first so they are preloaded into SGPRs with the dispatch (kernarg preload).
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__restrict__ w, const float *__restrict__ scale,
                                                        const float *x, int32_t rows, int32_t K, GemvArgs a) {
-    static_assert(WT == WT_Q8 || WT == WT_Q4, "int path is Q8/Q4");
+    static_assert(WT == WT_Q8 || WT == WT_Q4 || WT == WT_Q4H, "int path is Q8/Q4");
     extern __shared__ __align__(16) uint8_t smem[];
     const int nb = K / 32;
     int8_t *xq = reinterpret_cast<int8_t *>(smem);                 // [M][K]
@@ -299,7 +299,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__rest
                 const bool ok = c < nchunk && row < rows;
                 const int rowc = ok ? row : 0, cc = ok ? c : 0;
                 const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w + int64_t(rowc) * rb) + cc);
-                const float sc = scale[int64_t(rowc) * nb + (WT == WT_Q8 ? (cc >> 1) : cc)];
+                const int64_t si = int64_t(rowc) * nb + (WT == WT_Q8 ? (cc >> 1) : cc);
+                const float sc = WT == WT_Q4H ? float(reinterpret_cast<const _Float16 *>(scale)[si]) : scale[si];
                 wv[j][r] = ok ? t : u32x4{0u, 0u, 0u, 0u};
                 sv[j][r] = ok ? sc : 0.f;
             }
@@ -388,7 +389,7 @@ template <int WT, int M, int R, int IT, int PRO, int EPI, bool STAGE>
 // The weight stream's operands come first so they are preloaded into SGPRs with the dispatch (kernarg preload).
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_flt(const uint8_t *__restrict__ w, const float *__restrict__ scale,
                                                        const float *x, int32_t rows, int32_t K, GemvArgs a) {
-    static_assert(WT != WT_Q4, "Q4 always uses the int path");
+    static_assert(WT != WT_Q4 && WT != WT_Q4H, "Q4 always uses the int path");
     extern __shared__ __align__(16) uint8_t smem[];
     float *xf = reinterpret_cast<float *>(smem);  // [M][K]
     float *red = xf + M * K;                      // [M][4]

@@ -8,6 +8,7 @@ namespace vh {
 
 hipError_t launch_gemv_int_q8(int pro, int epi, int M, int R, int IT, const GemvArgs &a, hipStream_t s);
 hipError_t launch_gemv_int_q4(int pro, int epi, int M, int R, int IT, const GemvArgs &a, hipStream_t s);
+hipError_t launch_gemv_int_q4h(int pro, int epi, int M, int R, int IT, const GemvArgs &a, hipStream_t s);
 hipError_t launch_gemv_flt_q8(int pro, int epi, int M, int R, int IT, const GemvArgs &a, hipStream_t s);
 hipError_t launch_gemv_flt_f32(int pro, int epi, int M, int R, int IT, const GemvArgs &a, hipStream_t s);
 hipError_t launch_gemv_flt_f16(int pro, int epi, int M, int R, int IT, const GemvArgs &a, hipStream_t s);
@@ -50,7 +51,7 @@ void gemv_tile(int rows, int nchunk, int M, bool swiglu, int *R, int *IT) {
 
 hipError_t launch_gemv(int wt, bool int_path, int pro, int epi, const GemvArgs &a, hipStream_t s) {
     if (a.m <= 0) return hipSuccess;
-    const int epc = int_path ? (wt == WT_Q4 ? 32 : 16) : (wt == WT_F32 ? 4 : wt == WT_Q8 ? 16 : 8);
+    const int epc = int_path ? ((wt == WT_Q4 || wt == WT_Q4H) ? 32 : 16) : (wt == WT_F32 ? 4 : wt == WT_Q8 ? 16 : 8);
     const int nchunk = a.K / epc;
     int M, R, IT;
     if (int_path) {
@@ -63,6 +64,7 @@ hipError_t launch_gemv(int wt, bool int_path, int pro, int epi, const GemvArgs &
     if (int_path) {
         if (wt == WT_Q8) return launch_gemv_int_q8(pro, epi, M, R, IT, a, s);
         if (wt == WT_Q4) return launch_gemv_int_q4(pro, epi, M, R, IT, a, s);
+        if (wt == WT_Q4H) return launch_gemv_int_q4h(pro, epi, M, R, IT, a, s);
         return hipErrorInvalidValue;
     }
     switch (wt) {

@@ -104,12 +104,12 @@ hipError_t launch_attention(const AttnArgs &a, const _Float16 *kc0, const _Float
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_sample(const SampleCfgDev *cfg, const float *logits, int n, int32_t *out, hipStream_t s) {
-    if (n <= 0 || n > kSampleMaxN) return hipErrorInvalidValue;
+hipError_t launch_sample(const SampleCfgDev *cfg, const float *logits, int n, int32_t *out, hipStream_t s, int rows) {
+    if (n <= 0 || n > kSampleMaxN || rows <= 0) return hipErrorInvalidValue;
     const size_t smem = sample_smem_bytes(n);
     hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_sample), smem);
     if (e != hipSuccess) return e;
-    return launch(k_sample, dim3(1), dim3(kSampleThreads), smem, s, cfg, logits, n, out);
+    return launch(k_sample, dim3(unsigned(rows)), dim3(kSampleThreads), smem, s, cfg, logits, n, out);
 }
 
 static dim3 grid1(int64_t n, int bs) { return dim3(unsigned((n + bs - 1) / bs)); }

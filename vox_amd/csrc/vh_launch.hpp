@@ -33,7 +33,8 @@ hipError_t launch_qk_post(const QkArgs &a, int m, hipStream_t s);
 // (the same as the first row view); qkv: [m][a.ldqkv]; rope_rows: [m][hd] (fused).
 hipError_t launch_attention(const AttnArgs &a, const _Float16 *kc0, const _Float16 *vc0, int64_t cap0, const float *qkv,
                             const float *rope_rows, int layer, int hd, int group, int m, bool fused, hipStream_t s);
-hipError_t launch_sample(const SampleCfgDev *cfg, const float *logits, int n, int32_t *out, hipStream_t s);
+// rows samplers at once: cfg[b], logits [b][n], out[b].
+hipError_t launch_sample(const SampleCfgDev *cfg, const float *logits, int n, int32_t *out, hipStream_t s, int rows = 1);
 
 hipError_t launch_quant_q8(const float *w, int64_t nblocks, int8_t *q, float *scale, hipStream_t s);
 hipError_t launch_quant_q4(const float *w, int64_t nblocks, uint8_t *q, float *scale, hipStream_t s);

@@ -68,9 +68,13 @@ inline size_t sample_smem_bytes(int n) {
     return k2 * sizeof(uint64_t);
 }
 
-// out[0] = sampled index (or -1 when n is outside 1..kSampleMaxN). Dynamic LDS: sample_smem_bytes(n).
-__global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *cfgp, const float *logits, int32_t n,
-                                                           int32_t *out) {
+// One block per row b: logits [b][n] with cfg[b] -> out[b] = sampled index (or -1 when n is outside
+// 1..kSampleMaxN). Dynamic LDS: sample_smem_bytes(n).
+__global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *cfgs, const float *logits_all, int32_t n,
+                                                           int32_t *outs) {
+    const SampleCfgDev *cfgp = cfgs + blockIdx.x;
+    const float *logits = logits_all + int64_t(blockIdx.x) * n;
+    int32_t *out = outs + blockIdx.x;
     extern __shared__ __align__(16) uint64_t sample_keys[];
     __shared__ uint32_t seen[kSampleMaxN / 32];
     __shared__ uint32_t hist[256];

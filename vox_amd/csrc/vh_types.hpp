@@ -7,7 +7,9 @@ namespace vh {
 // GEMV input prologues: x as is; RMSNorm(x, gamma); or the merge of split-K attention partials.
 enum { PRO_X = 0, PRO_RMS = 1, PRO_ATTN = 2 };
 enum { EPI_STORE = 0, EPI_ACC = 1, EPI_SWIGLU = 2 };
-enum { WT_F32 = 0, WT_F16 = 1, WT_BF16 = 2, WT_Q8 = 3, WT_Q4 = 4 };
+// Weight formats of the GEMV kernels: the reference's types, plus Q4 with f16 block scales (WT_Q4H), the
+// device storage of a Q4 matrix whose f32 scales are all exact in f16 (same arithmetic, 2 bytes less per block).
+enum { WT_F32 = 0, WT_F16 = 1, WT_BF16 = 2, WT_Q8 = 3, WT_Q4 = 4, WT_Q4H = 5 };
 
 // Cache view of one activation row: the sequence's cache bases (layer 0) and the row's absolute position.
 struct RowRef {
@@ -35,7 +37,7 @@ struct AttnPartials {
 
 struct GemvArgs {
     const uint8_t *w;     // weights, reference row layout
-    const float *scale;   // [rows][K/32] for Q8/Q4
+    const float *scale;   // [rows][K/32] for Q8/Q4 (f16 values for WT_Q4H)
     const float *bias;    // [rows] or null
     const float *x;       // [m][ldx] (PRO_X, PRO_RMS)
     const float *gamma;   // [K] (PRO_RMS)

@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -46,7 +47,8 @@ struct GpuMat {
     int32_t type = 0;
     int64_t rows = 0, cols = 0;
     uint8_t *w = nullptr;
-    float *s = nullptr;
+    float *s = nullptr;  // [rows][cols/32] block scales (f16 values when s16)
+    bool s16 = false;
     float *b = nullptr;
     uint64_t bytes = 0;  // weights + scales + bias bytes (the GEMV's algorithmic stream)
 };
@@ -57,12 +59,14 @@ struct LayerDev {
     bool qk = false;
 };
 
+// A captured decode step: m rows of one sequence (steps = 0), or one row for each of m sequences (steps = 1).
 struct GraphKey {
-    int seq, m, head, sample;
+    std::array<int, 8> seqs;
+    int m, head, sample, steps;
     const void *x, *out, *logits, *token;
     bool operator<(const GraphKey &o) const {
-        return std::tie(seq, m, head, sample, x, out, logits, token) <
-               std::tie(o.seq, o.m, o.head, o.sample, o.x, o.out, o.logits, o.token);
+        return std::tie(seqs, m, head, sample, steps, x, out, logits, token) <
+               std::tie(o.seqs, o.m, o.head, o.sample, o.steps, o.x, o.out, o.logits, o.token);
     }
 };
 
@@ -211,15 +215,34 @@ void check_shape(int32_t type, int64_t rows, int64_t cols) {
     if (!quantized(type) && cols % 8) throw Fail("F32/F16/BF16 matrix needs cols % 8 == 0 on this backend");
 }
 
-int new_mat(int32_t type, int64_t rows, int64_t cols, bool bias) {
+size_t scale_row_bytes(const GpuMat &m) { return quantized(m.type) ? size_t(m.cols / 32) * (m.s16 ? 2 : 4) : 0; }
+int gemv_type(const GpuMat &m) { return m.type == VOXHIP_Q4 && m.s16 ? WT_Q4H : m.type; }
+
+// f32 -> f16 bits when the value is exactly representable as a normal or zero f16 (the scales a device Q4 matrix
+// may store in 2 bytes without changing its arithmetic).
+bool f16_exact(float f, uint16_t *out) {
+    if (f == 0.f) { *out = std::signbit(f) ? 0x8000 : 0; return true; }
+    if (!std::isfinite(f)) return false;
+    int e = 0;
+    const float mant = std::frexp(std::fabs(f), &e);  // |f| = mant * 2^e, mant in [0.5, 1)
+    if (e - 1 < -14 || e - 1 > 15) return false;       // normal f16 range
+    const float scaled = std::ldexp(mant, 11);         // 11 significant bits
+    if (scaled != std::floor(scaled)) return false;
+    const uint32_t m10 = uint32_t(scaled) & 0x3FFu;
+    *out = uint16_t((f < 0 ? 0x8000u : 0u) | (uint32_t(e - 1 + 15) << 10) | m10);
+    return true;
+}
+
+int new_mat(int32_t type, int64_t rows, int64_t cols, bool bias, bool s16 = false) {
     GpuMat m;
-    m.type = type; m.rows = rows; m.cols = cols;
+    m.type = type; m.rows = rows; m.cols = cols; m.s16 = s16 && type == VOXHIP_Q4;
     const size_t wb = size_t(rows) * row_bytes(type, cols);
     m.w = static_cast<uint8_t *>(dalloc(wb));
     m.bytes = wb;
     if (quantized(type)) {
-        m.s = dalloc_t<float>(size_t(rows) * size_t(cols / 32));
-        m.bytes += size_t(rows) * size_t(cols / 32) * 4;
+        const size_t sbytes = size_t(rows) * scale_row_bytes(m);
+        m.s = static_cast<float *>(dalloc(sbytes));
+        m.bytes += sbytes;
     }
     if (bias) { m.b = dalloc_t<float>(size_t(rows)); m.bytes += size_t(rows) * 4; }
     g.mats.push_back(m);
@@ -250,15 +273,26 @@ int upload_parts(const voxhip_mat *parts, int n, bool interleave2) {
     if (any_bias && !all_bias) throw Fail("bias on some stacked parts only");
     if (interleave2 && (n != 2 || parts[0].rows != parts[1].rows)) throw Fail("interleave needs two equal parts");
     check_shape(P0.type, rows, P0.cols);
-    const int id = new_mat(P0.type, rows, P0.cols, all_bias);
+    // Q4 scales that are all exact in f16 are stored in 2 bytes (WT_Q4H): same products, less to stream
+    const int64_t nbr = P0.cols / 32;
+    std::vector<std::vector<uint16_t>> s16(static_cast<size_t>(n));
+    bool use16 = P0.type == VOXHIP_Q4;
+    for (int i = 0; i < n && use16; ++i) {
+        s16[size_t(i)].resize(size_t(parts[i].rows * nbr));
+        for (size_t j = 0; j < s16[size_t(i)].size() && use16; ++j) use16 = f16_exact(parts[i].scale[j], &s16[size_t(i)][j]);
+    }
+    const int id = new_mat(P0.type, rows, P0.cols, all_bias, use16);
     GpuMat &m = g.mats[size_t(id)];
-    const size_t rb = row_bytes(P0.type, P0.cols), sb = quantized(P0.type) ? size_t(P0.cols / 32) * 4 : 0;
+    const size_t rb = row_bytes(P0.type, P0.cols), sb = scale_row_bytes(m);
+    auto scale_src = [&](int i) -> const uint8_t * {
+        return use16 ? reinterpret_cast<const uint8_t *>(s16[size_t(i)].data()) : reinterpret_cast<const uint8_t *>(parts[i].scale);
+    };
     if (!interleave2) {
         int64_t r0 = 0;
         for (int i = 0; i < n; ++i) {
             const voxhip_mat &p = parts[i];
             h2d(m.w + size_t(r0) * rb, p.data, size_t(p.rows) * rb);
-            if (sb) h2d(reinterpret_cast<uint8_t *>(m.s) + size_t(r0) * sb, p.scale, size_t(p.rows) * sb);
+            if (sb) h2d(reinterpret_cast<uint8_t *>(m.s) + size_t(r0) * sb, scale_src(i), size_t(p.rows) * sb);
             if (all_bias) h2d(m.b + r0, p.bias, size_t(p.rows) * 4);
             r0 += p.rows;
         }
@@ -270,7 +304,7 @@ int upload_parts(const voxhip_mat *parts, int n, bool interleave2) {
             for (int i = 0; i < 2; ++i) {
                 const voxhip_mat &p = parts[i];
                 std::memcpy(&tw[size_t(2 * r + i) * rb], static_cast<const uint8_t *>(p.data) + size_t(r) * rb, rb);
-                if (sb) std::memcpy(&ts[size_t(2 * r + i) * sb], reinterpret_cast<const uint8_t *>(p.scale) + size_t(r) * sb, sb);
+                if (sb) std::memcpy(&ts[size_t(2 * r + i) * sb], scale_src(i) + size_t(r) * sb, sb);
                 if (all_bias) tb[size_t(2 * r + i)] = p.bias[r];
             }
         h2d(m.w, tw.data(), tw.size());
@@ -298,7 +332,7 @@ void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, in
         if (!attn || int64_t(attn->heads) * attn->hd != m.cols) throw Fail("attention partials do not match the o projection");
         a.attn = *attn;
     }
-    HIPCHECK(launch_gemv(m.type, int_path(m, m_total), pro, epi, a, s));
+    HIPCHECK(launch_gemv(gemv_type(m), int_path(m, m_total), pro, epi, a, s));
 }
 
 // ------------------------------------------------------------------ transformer
@@ -336,8 +370,9 @@ void alloc_scratch(Xfmr &X) {
     X.rows_dev = static_cast<RowRef *>(dalloc(rows_bytes));
     X.rope_rows_dev = reinterpret_cast<float *>(X.rows_dev + M);
     HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&X.rows_host), rows_bytes, hipHostMallocDefault));
-    X.scfg_dev = dalloc_t<SampleCfgDev>(1);
-    HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&X.scfg_host), sizeof(SampleCfgDev), hipHostMallocDefault));
+    X.scfg_dev = dalloc_t<SampleCfgDev>(M);
+    HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&X.scfg_host), M * sizeof(SampleCfgDev), hipHostMallocDefault));
+    std::memset(X.scfg_host, 0, M * sizeof(SampleCfgDev));
     X.token_dev = dalloc_t<int32_t>(M);
 }
 
@@ -592,8 +627,10 @@ int make_xfmr(const voxhip_xfmr_desc *w, const char *name, int use_layers, const
                     int64_t rows = 0;
                     bool bias = true;
                     for (int id : ids) { rows += g.mats[size_t(id)].rows; bias = bias && g.mats[size_t(id)].b; }
-                    const int nid = new_mat(m0.type, rows, m0.cols, bias);
-                    const size_t rb = row_bytes(m0.type, m0.cols), sb = quantized(m0.type) ? size_t(m0.cols / 32) * 4 : 0;
+                    for (int id : ids)
+                        if (g.mats[size_t(id)].s16 != m0.s16) throw Fail("stacked matrices differ in scale storage");
+                    const int nid = new_mat(m0.type, rows, m0.cols, bias, m0.s16);
+                    const size_t rb = row_bytes(m0.type, m0.cols), sb = scale_row_bytes(m0);
                     int64_t r0 = 0;
                     int part = 0;
                     for (int id : ids) {
@@ -1009,24 +1046,27 @@ int voxhip_sync(void) {
 }  // extern "C"
 
 namespace {
-// Enqueues one device-resident decode step on stream s (no host copies). m rows of one sequence at pos0 + i:
-// one row takes the fused attention; several rows of the same sequence append their keys first (k_qk_post).
+// Enqueues one device-resident decode step on stream s (no host copies). steps = false: m rows of one sequence at
+// pos0 + i; one row takes the fused attention, several rows of the same sequence append their keys first
+// (k_qk_post), and the head and sampler run on the last row. steps = true: one row for each of m sequences (fused
+// attention), head and sampler on every row.
 int enqueue_decode(Xfmr &X, int m, int head, const float *d_x, float *d_out_last, float *d_logits, bool sample, int32_t *d_token,
-                   hipStream_t s, Probe *pr = nullptr) {
-    const bool fused = m == 1;
+                   hipStream_t s, Probe *pr = nullptr, bool steps = false) {
+    const bool fused = steps || m == 1;
+    const int r0 = steps ? 0 : m - 1, mr = steps ? m : 1;
     int kernels = 0;
     HIPCHECK(hipMemcpyAsync(X.h, d_x, size_t(m) * X.H * 4, hipMemcpyDeviceToDevice, s));
     enqueue_layers(X, m, m, 0, X.layers, s, fused, pr);
     kernels += kernels_per_layer(fused) * X.layers;
-    probed(head >= 0 ? pr : nullptr, VOXHIP_K_HEAD, [&] { enqueue_final(X, m - 1, 1, head, s); });
+    probed(head >= 0 ? pr : nullptr, VOXHIP_K_HEAD, [&] { enqueue_final(X, r0, mr, head, s); });
     kernels += 1;
-    if (d_out_last) HIPCHECK(hipMemcpyAsync(d_out_last, X.xnorm, size_t(X.H) * 4, hipMemcpyDeviceToDevice, s));
+    if (d_out_last) HIPCHECK(hipMemcpyAsync(d_out_last, X.xnorm, size_t(mr) * X.H * 4, hipMemcpyDeviceToDevice, s));
     if (head >= 0) {
         const GpuMat &Hm = g.mats[size_t(head)];
-        if (d_logits) HIPCHECK(hipMemcpyAsync(d_logits, X.logits, size_t(Hm.rows) * 4, hipMemcpyDeviceToDevice, s));
+        if (d_logits) HIPCHECK(hipMemcpyAsync(d_logits, X.logits, size_t(mr) * size_t(Hm.rows) * 4, hipMemcpyDeviceToDevice, s));
         if (sample) {
             probed(pr, VOXHIP_K_SAMPLE, [&] {
-                HIPCHECK(launch_sample(X.scfg_dev, X.logits, int(Hm.rows), d_token ? d_token : X.token_dev, s));
+                HIPCHECK(launch_sample(X.scfg_dev, X.logits, int(Hm.rows), d_token ? d_token : X.token_dev, s, mr));
             });
             kernels += 1;
         }
@@ -1034,15 +1074,15 @@ int enqueue_decode(Xfmr &X, int m, int head, const float *d_x, float *d_out_last
     return kernels;
 }
 
-hipGraphExec_t decode_graph(Xfmr &X, int seq, int m, int head, const float *d_x, float *d_out_last, float *d_logits, bool sample,
-                            int32_t *d_token) {
-    GraphKey key{seq, m, head, sample ? 1 : 0, d_x, d_out_last, d_logits, d_token};
+hipGraphExec_t decode_graph(Xfmr &X, const std::array<int, 8> &seqs, int m, bool steps, int head, const float *d_x,
+                            float *d_out_last, float *d_logits, bool sample, int32_t *d_token) {
+    GraphKey key{seqs, m, head, sample ? 1 : 0, steps ? 1 : 0, d_x, d_out_last, d_logits, d_token};
     auto it = X.graphs.find(key);
     if (it != X.graphs.end()) return it->second;
     hipGraph_t graph = nullptr;
     HIPCHECK(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal));
     try {
-        enqueue_decode(X, m, head, d_x, d_out_last, d_logits, sample, d_token, g.stream);
+        enqueue_decode(X, m, head, d_x, d_out_last, d_logits, sample, d_token, g.stream, nullptr, steps);
     } catch (...) {
         (void)hipStreamEndCapture(g.stream, &graph);
         if (graph) (void)hipGraphDestroy(graph);
@@ -1056,32 +1096,47 @@ hipGraphExec_t decode_graph(Xfmr &X, int seq, int m, int head, const float *d_x,
     X.graphs[key] = exec;
     return exec;
 }
+std::array<int, 8> one_seq(int seq) {
+    std::array<int, 8> a;
+    a.fill(-1);
+    a[0] = seq;
+    return a;
+}
+
+void prepare_head(Xfmr &X, int head, bool sample) {
+    if (sample && head < 0) throw Fail("sampling needs a head");
+    if (head >= 0) {
+        const GpuMat &Hm = mat_at(head);
+        if (Hm.cols != X.H) throw Fail("head width differs from the hidden size");
+        if (sample && Hm.rows > kSampleMaxN) throw Fail("sampler supports up to 16384 logits");
+        ensure_logits(X, Hm.rows);
+    }
+}
+// Uploads the sampler configurations of rows 0..n-1 when they changed.
+void set_sample_cfgs(Xfmr &X, const voxhip_sample_cfg *cfgs, int n) {
+    std::vector<SampleCfgDev> d(static_cast<size_t>(n));
+    for (int i = 0; i < n; ++i) {
+        std::memset(&d[size_t(i)], 0, sizeof(SampleCfgDev));
+        fill_sample_cfg(d[size_t(i)], cfgs[i], nullptr, 0);
+    }
+    if (std::memcmp(d.data(), X.scfg_host, size_t(n) * sizeof(SampleCfgDev)) != 0) {
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        std::memcpy(X.scfg_host, d.data(), size_t(n) * sizeof(SampleCfgDev));
+        HIPCHECK(hipMemcpyAsync(X.scfg_dev, X.scfg_host, size_t(n) * sizeof(SampleCfgDev), hipMemcpyHostToDevice, g.stream));
+    }
+}
 
 void prepare_decode(Xfmr &X, Seq &S, int64_t pos0, int64_t m, int head, const voxhip_sample_cfg *cfg) {
     if (m <= 0 || m > kMaxM) throw Fail("decode_dev takes 1..8 rows");
     if (pos0 < 0 || pos0 + m > S.cap) throw Fail("context exceeds GPU KV capacity");
-    if (cfg && head < 0) throw Fail("sampling needs a head");
-    if (head >= 0) {
-        const GpuMat &Hm = mat_at(head);
-        if (Hm.cols != X.H) throw Fail("head width differs from the hidden size");
-        if (cfg && Hm.rows > kSampleMaxN) throw Fail("sampler supports up to 16384 logits");
-        ensure_logits(X, Hm.rows);
-    }
+    prepare_head(X, head, cfg != nullptr);
     for (const LayerDev &L : X.L)
         for (int id : {L.qkv, L.o, L.gu, L.down})
             if (!int_path(g.mats[size_t(id)], m) && rows_per_pass(g.mats[size_t(id)], m) < m) throw Fail("decode_dev: rows exceed the f32 pass");
     std::vector<RowRef> rr(static_cast<size_t>(m));
     for (int64_t i = 0; i < m; ++i) rr[size_t(i)] = row_of(S, pos0 + i);
     set_rows(X, rr);
-    if (cfg) {
-        SampleCfgDev d;
-        fill_sample_cfg(d, *cfg, nullptr, 0);
-        if (std::memcmp(&d, X.scfg_host, sizeof d) != 0) {
-            HIPCHECK(hipStreamSynchronize(g.stream));
-            *X.scfg_host = d;
-            HIPCHECK(hipMemcpyAsync(X.scfg_dev, X.scfg_host, sizeof d, hipMemcpyHostToDevice, g.stream));
-        }
-    }
+    if (cfg) set_sample_cfgs(X, cfg, 1);
 }
 
 uint64_t gemv_stream_bytes(const Xfmr &X) {
@@ -1102,37 +1157,78 @@ int voxhip_decode_dev(int xfmr, int seq, int64_t pos0, const float *d_x, int64_t
         Seq &S = seq_at(seq);
         check_seq_for(X, xfmr, S);
         prepare_decode(X, S, pos0, m, head, cfg);
-        hipGraphExec_t exec = decode_graph(X, seq, int(m), head, d_x, d_out_last, d_logits, cfg != nullptr, d_token);
+        hipGraphExec_t exec = decode_graph(X, one_seq(seq), int(m), false, head, d_x, d_out_last, d_logits, cfg != nullptr, d_token);
+        HIPCHECK(hipGraphLaunch(exec, g.stream));
+        return 1;
+    }, 0);
+}
+
+int voxhip_decode_steps_dev(int xfmr, const int32_t *seqs, const int64_t *pos, int64_t B, const float *d_x, float *d_out,
+                            int head, float *d_logits, const voxhip_sample_cfg *cfgs, int32_t *d_tokens) {
+    return guard_int([&] {
+        require_ok();
+        Xfmr &X = xf_at(xfmr);
+        if (!seqs || !pos || !d_x) throw Fail("missing argument");
+        if (B <= 0 || B > kMaxM) throw Fail("decode_steps_dev takes 1..8 sequences");
+        std::array<int, 8> key;
+        key.fill(-1);
+        std::vector<RowRef> rr(static_cast<size_t>(B));
+        for (int64_t b = 0; b < B; ++b) {
+            Seq &S = seq_at(seqs[b]);
+            check_seq_for(X, xfmr, S);
+            if (pos[b] < 0 || pos[b] + 1 > S.cap) throw Fail("context exceeds GPU KV capacity");
+            for (int64_t c = 0; c < b; ++c)
+                if (seqs[c] == seqs[b]) throw Fail("a sequence appears twice in one step");
+            for (const LayerDev &L : X.L)
+                for (int id : {L.qkv, L.o, L.gu, L.down})
+                    if (!int_path(g.mats[size_t(id)], B) && rows_per_pass(g.mats[size_t(id)], B) < B)
+                        throw Fail("decode_steps_dev: rows exceed the f32 pass");
+            rr[size_t(b)] = row_of(S, pos[b]);
+            key[size_t(b)] = seqs[b];
+        }
+        prepare_head(X, head, cfgs != nullptr);
+        set_rows(X, rr);
+        if (cfgs) set_sample_cfgs(X, cfgs, int(B));
+        hipGraphExec_t exec = decode_graph(X, key, int(B), true, head, d_x, d_out, d_logits, cfgs != nullptr, d_tokens);
         HIPCHECK(hipGraphLaunch(exec, g.stream));
         return 1;
     }, 0);
 }
 
 int voxhip_mat_synthetic(int32_t type, int64_t rows, int64_t cols, uint64_t seed, uint32_t stream, float mean, float std,
-                         int with_bias) {
+                         int flags) {
     return guard_int([&] {
         require_ok();
         check_shape(type, rows, cols);
-        const int id = new_mat(type, rows, cols, with_bias != 0);
+        const bool with_bias = (flags & VOXHIP_SYN_BIAS) != 0, s16 = (flags & VOXHIP_SYN_F16_SCALES) && type == VOXHIP_Q4;
+        const int id = new_mat(type, rows, cols, with_bias, s16);
         GpuMat &m = g.mats[size_t(id)];
-        const size_t n = size_t(rows) * size_t(cols);
+        const size_t n = size_t(rows) * size_t(cols), nsc = quantized(type) ? n / 32 : 0;
         float *tmp = type == VOXHIP_F32 ? reinterpret_cast<float *>(m.w) : dalloc_t<float>(n);
+        float *sc32 = nullptr;
+        auto release = [&] {
+            if (tmp != reinterpret_cast<float *>(m.w)) dfree(tmp);
+            dfree(sc32);
+        };
         try {
+            float *sdst = m.s;
+            if (s16) sdst = sc32 = dalloc_t<float>(nsc);  // quantize with f32 scales, then round them to f16
             HIPCHECK(launch_fill_normal(tmp, int64_t(n), seed, stream, mean, std, g.stream));
             switch (type) {
-                case VOXHIP_Q8: HIPCHECK(launch_quant_q8(tmp, int64_t(n / 32), reinterpret_cast<int8_t *>(m.w), m.s, g.stream)); break;
-                case VOXHIP_Q4: HIPCHECK(launch_quant_q4(tmp, int64_t(n / 32), m.w, m.s, g.stream)); break;
+                case VOXHIP_Q8: HIPCHECK(launch_quant_q8(tmp, int64_t(n / 32), reinterpret_cast<int8_t *>(m.w), sdst, g.stream)); break;
+                case VOXHIP_Q4: HIPCHECK(launch_quant_q4(tmp, int64_t(n / 32), m.w, sdst, g.stream)); break;
                 case VOXHIP_F16: HIPCHECK(launch_to_f16(tmp, int64_t(n), m.w, g.stream)); break;
                 case VOXHIP_BF16: HIPCHECK(launch_to_bf16(tmp, int64_t(n), m.w, g.stream)); break;
                 default: break;
             }
+            if (s16) HIPCHECK(launch_to_f16(sc32, int64_t(nsc), m.s, g.stream));
             if (with_bias) HIPCHECK(launch_fill_normal(m.b, rows, seed, stream + 0x10000u, 0.f, std, g.stream));
             HIPCHECK(hipStreamSynchronize(g.stream));
         } catch (...) {
-            if (tmp != reinterpret_cast<float *>(m.w)) dfree(tmp);
+            release();
             throw;
         }
-        if (tmp != reinterpret_cast<float *>(m.w)) dfree(tmp);
+        release();
         g.stats.mats_ok += 1;
         g.stats.bytes += m.bytes;
         return id;
@@ -1145,7 +1241,16 @@ int voxhip_mat_download(int mat, void *data, float *scale, float *bias) {
         const GpuMat &m = mat_at(mat);
         HIPCHECK(hipStreamSynchronize(g.stream));
         if (data) HIPCHECK(hipMemcpy(data, m.w, size_t(m.rows) * row_bytes(m.type, m.cols), hipMemcpyDeviceToHost));
-        if (scale && m.s) HIPCHECK(hipMemcpy(scale, m.s, size_t(m.rows) * size_t(m.cols / 32) * 4, hipMemcpyDeviceToHost));
+        if (scale && m.s) {
+            const size_t nsc = size_t(m.rows) * size_t(m.cols / 32);
+            if (m.s16) {  // widened exactly to the f32 scales the matrix stands for
+                std::vector<_Float16> t(nsc);
+                HIPCHECK(hipMemcpy(t.data(), m.s, nsc * 2, hipMemcpyDeviceToHost));
+                for (size_t i = 0; i < nsc; ++i) scale[i] = float(t[i]);
+            } else {
+                HIPCHECK(hipMemcpy(scale, m.s, nsc * 4, hipMemcpyDeviceToHost));
+            }
+        }
         if (bias && m.b) HIPCHECK(hipMemcpy(bias, m.b, size_t(m.rows) * 4, hipMemcpyDeviceToHost));
         return 1;
     }, 0);
@@ -1264,7 +1369,7 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, const float *d_x, int h
         try {
             // ---- region A: graph replays (the same graph voxhip_decode_dev replays for these arguments)
             mark("graph");
-            hipGraphExec_t exec = decode_graph(X, seq, 1, head, dx, nullptr, nullptr, cfg != nullptr, d_token);
+            hipGraphExec_t exec = decode_graph(X, one_seq(seq), 1, false, head, dx, nullptr, nullptr, cfg != nullptr, d_token);
             for (int i = 0; i < warmup; ++i) HIPCHECK(hipGraphLaunch(exec, g.stream));
             ev.resize(2);
             for (auto &e : ev) HIPCHECK(hipEventCreate(&e));
@@ -1404,6 +1509,79 @@ int voxhip_bench_gemv_q8(int64_t rows, int64_t cols, int copies, int warmup, int
             *ms_per_launch = double(ms) / iters;
             (void)hipEventDestroy(e0);
             (void)hipEventDestroy(e1);
+        } catch (...) {
+            cleanup();
+            throw;
+        }
+        cleanup();
+        return 1;
+    }, 0);
+}
+
+int voxhip_bench_ffn_q8(int64_t hidden, int64_t inter, int copies, int warmup, int iters, double *us_per_block) {
+    return guard_int([&] {
+        require_ok();
+        if (copies <= 0 || iters <= 0 || !us_per_block || hidden % 32 || inter % 32) throw Fail("bad bench arguments");
+        std::vector<int> ids;
+        float *x = nullptr, *h = nullptr, *gbuf = nullptr, *gamma = nullptr;
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        auto cleanup = [&] {
+            (void)hipStreamSynchronize(g.stream);
+            if (exec) (void)hipGraphExecDestroy(exec);
+            if (graph) (void)hipGraphDestroy(graph);
+            if (e0) (void)hipEventDestroy(e0);
+            if (e1) (void)hipEventDestroy(e1);
+            for (int id : ids) free_mat(id);
+            dfree(x); dfree(h); dfree(gbuf); dfree(gamma);
+        };
+        try {
+            // per copy: gate|up interleaved [2 inter][hidden] and down [hidden][inter], q8, ~N(0, 0.02)
+            for (int c = 0; c < copies; ++c)
+                for (int part = 0; part < 2; ++part) {
+                    const int64_t rows = part ? hidden : 2 * inter, cols = part ? inter : hidden;
+                    const int id = new_mat(VOXHIP_Q8, rows, cols, false);
+                    ids.push_back(id);
+                    GpuMat &m = g.mats[size_t(id)];
+                    float *tmp = dalloc_t<float>(size_t(rows) * size_t(cols));
+                    HIPCHECK(launch_fill_normal(tmp, rows * cols, 2000 + c, 0x60u + part, 0.f, 0.02f, g.stream));
+                    HIPCHECK(launch_quant_q8(tmp, rows * cols / 32, reinterpret_cast<int8_t *>(m.w), m.s, g.stream));
+                    HIPCHECK(hipStreamSynchronize(g.stream));
+                    dfree(tmp);
+                }
+            x = dalloc_t<float>(size_t(hidden));
+            h = dalloc_t<float>(size_t(hidden));
+            gbuf = dalloc_t<float>(size_t(inter));
+            gamma = dalloc_t<float>(size_t(hidden));
+            HIPCHECK(launch_fill_normal(x, hidden, 7, 0x70u, 0.f, 1.f, g.stream));
+            HIPCHECK(launch_fill_normal(gamma, hidden, 8, 0x71u, 1.f, 0.02f, g.stream));
+            HIPCHECK(hipMemcpyAsync(h, x, size_t(hidden) * 4, hipMemcpyDeviceToDevice, g.stream));
+            HIPCHECK(hipStreamSynchronize(g.stream));
+            // one graph over all copies: RMSNorm + gate|up + SwiGLU, then down + residual (two kernels per block)
+            HIPCHECK(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal));
+            try {
+                for (int c = 0; c < copies; ++c) {
+                    const GpuMat &gu = g.mats[size_t(ids[size_t(2 * c)])], &dn = g.mats[size_t(ids[size_t(2 * c + 1)])];
+                    gemv(gu, 1, PRO_RMS, EPI_SWIGLU, h, hidden, 1, gbuf, inter, gamma, 1e-6f, nullptr, g.stream);
+                    gemv(dn, 1, PRO_X, EPI_ACC, gbuf, inter, 1, h, hidden, nullptr, 0.f, nullptr, g.stream);
+                }
+            } catch (...) {
+                (void)hipStreamEndCapture(g.stream, &graph);
+                throw;
+            }
+            HIPCHECK(hipStreamEndCapture(g.stream, &graph));
+            HIPCHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+            for (int i = 0; i < warmup; ++i) HIPCHECK(hipGraphLaunch(exec, g.stream));
+            HIPCHECK(hipEventCreate(&e0));
+            HIPCHECK(hipEventCreate(&e1));
+            HIPCHECK(hipEventRecord(e0, g.stream));
+            for (int i = 0; i < iters; ++i) HIPCHECK(hipGraphLaunch(exec, g.stream));
+            HIPCHECK(hipEventRecord(e1, g.stream));
+            HIPCHECK(hipEventSynchronize(e1));
+            float ms = 0.f;
+            HIPCHECK(hipEventElapsedTime(&ms, e0, e1));
+            *us_per_block = double(ms) * 1000.0 / (double(iters) * copies);
         } catch (...) {
             cleanup();
             throw;

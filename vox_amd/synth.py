@@ -14,7 +14,7 @@ TALKER_0_6B = dict(layers=28, hidden=1024, heads=16, kv_heads=8, head_dim=128, i
                    kv_len=512, head_rows=3072, wtype=vh.Q8, head_type=vh.Q8)
 # Qwen3-TTS-1.7B-shaped talker with q4 body
 TALKER_1_7B_Q4 = dict(layers=28, hidden=2048, heads=16, kv_heads=8, head_dim=128, inter=6144, theta=1e6, eps=1e-6,
-                      kv_len=1024, head_rows=3072, wtype=vh.Q4, head_type=vh.Q8)
+                      kv_len=1024, head_rows=3072, wtype=vh.Q4, head_type=vh.Q8, f16_scales=True)
 NAMES = ("q", "k", "v", "o", "gate", "up", "down")
 
 
@@ -39,7 +39,8 @@ class Decoder:
             ids = {}
             for j, n in enumerate(NAMES):
                 r, cc = shapes[n]
-                ids[n] = vh.mat_synthetic(c["wtype"], r, cc, seed, 0x100 * li + j, 0.0, 0.02)
+                ids[n] = vh.mat_synthetic(c["wtype"], r, cc, seed, 0x100 * li + j, 0.0, 0.02,
+                                          f16_scales=c.get("f16_scales", False))
             self.mats.append(ids)
             norms = {n: (1.0 + 0.02 * rng.standard_normal(H)).astype(np.float32) for n in ("ln1", "ln2")}
             norms.update({n: (1.0 + 0.02 * rng.standard_normal(hd)).astype(np.float32) for n in ("qn", "kn")})
@@ -60,6 +61,13 @@ class Decoder:
         vh.seq_fill_synthetic(self.seq, c["kv_len"], seed, 0xC0DE, 0.0, 1.0)
         self.head = vh.mat_synthetic(c["head_type"], c["head_rows"], H, seed, 0xF00D, 0.0, 0.02) if c.get("head_rows") else -1
 
+    def extra_seq(self, stream):
+        """Another sequence of the same capacity whose first kv_len positions are filled from Philox stream `stream`
+        (independent sessions for the B-session step)."""
+        s = vh.seq_create(self.xfmr, self.capacity)
+        vh.seq_fill_synthetic(s, self.cfg["kv_len"], 0, stream, 0.0, 1.0)
+        return s
+
     def weight_bytes(self):
         """Algorithmic bytes of one decode step's weight stream (layers + head), as stored."""
         c = self.cfg
@@ -69,7 +77,7 @@ class Decoder:
             if t == vh.Q8:
                 return rows * cols + rows * (cols // 32) * 4
             if t == vh.Q4:
-                return rows * cols // 2 + rows * (cols // 32) * 4
+                return rows * cols // 2 + rows * (cols // 32) * (2 if c.get("f16_scales") else 4)
             return rows * cols * (4 if t == vh.F32 else 2)
         per_layer = sum(mb(c["wtype"], r, cc) for r, cc in ((qd + 2 * kd, H), (H, qd), (2 * I, H), (H, I)))
         head = mb(c["head_type"], c["head_rows"], H) if c.get("head_rows") else 0

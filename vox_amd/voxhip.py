@@ -106,6 +106,7 @@ SIGNATURES = {
     "voxhip_memcpy_d2h": (_I, [_P, _P, _S]),
     "voxhip_sync": (_I, []),
     "voxhip_decode_dev": (_I, [_I, _I, _I64, _P, _I64, _P, _I, _P, C.POINTER(SampleCfg), _P]),
+    "voxhip_decode_steps_dev": (_I, [_I, _P, _P, _I64, _P, _P, _I, _P, C.POINTER(SampleCfg), _P]),
     "voxhip_mat_synthetic": (_I, [_I32, _I64, _I64, _U64, _U32, _F, _F, _I]),
     "voxhip_mat_download": (_I, [_I, _P, _P, _P]),
     "voxhip_mat_free": (_I, [_I]),
@@ -118,6 +119,7 @@ SIGNATURES = {
     "voxhip_bench_decode": (_I, [_I, _I, _I64, _P, _I, C.POINTER(SampleCfg), _P, _I, _I, C.POINTER(BenchResult)]),
     "voxhip_bench_gemv_q8": (_I, [_I64, _I64, _I, _I, _I, C.POINTER(C.c_double)]),
     "voxhip_bench_copy": (_I, [_I64, _I, _I, C.POINTER(C.c_double)]),
+    "voxhip_bench_ffn_q8": (_I, [_I64, _I64, _I, _I, _I, C.POINTER(C.c_double)]),
 }
 
 _lib = None
@@ -223,8 +225,12 @@ def mat_shape(mat):
     return rows.value, cols.value
 
 
-def mat_synthetic(wtype, rows, cols, seed, stream, mean=0.0, std=0.02, bias=False):
-    return _handle(lib().voxhip_mat_synthetic(wtype, rows, cols, seed, stream, mean, std, int(bias)), "mat_synthetic")
+SYN_BIAS, SYN_F16_SCALES = 1, 2
+
+
+def mat_synthetic(wtype, rows, cols, seed, stream, mean=0.0, std=0.02, bias=False, f16_scales=False):
+    flags = (SYN_BIAS if bias else 0) | (SYN_F16_SCALES if f16_scales else 0)
+    return _handle(lib().voxhip_mat_synthetic(wtype, rows, cols, seed, stream, mean, std, flags), "mat_synthetic")
 
 
 def mat_download(mat, wtype):
@@ -388,6 +394,18 @@ def decode_dev(xfmr, seq, pos0, d_x, m=1, d_out=None, head=-1, d_logits=None, cf
                                    None if d_token is None else d_token.ptr), "decode_dev")
 
 
+def decode_steps_dev(xfmr, seqs, pos, d_x, d_out=None, head=-1, d_logits=None, cfgs=None, d_tokens=None):
+    """One token for each of B sequences at its own position (device-resident, one captured graph)."""
+    sq = np.ascontiguousarray(seqs, dtype=np.int32)
+    ps = np.ascontiguousarray(pos, dtype=np.int64)
+    carr = None
+    if cfgs is not None:
+        carr = (SampleCfg * len(cfgs))(*cfgs)
+    _check(lib().voxhip_decode_steps_dev(xfmr, _p(sq), _p(ps), sq.size, d_x.ptr, None if d_out is None else d_out.ptr, head,
+                                         None if d_logits is None else d_logits.ptr, carr,
+                                         None if d_tokens is None else d_tokens.ptr), "decode_steps_dev")
+
+
 def sync():
     _check(lib().voxhip_sync(), "sync")
 
@@ -449,3 +467,10 @@ def bench_copy(nbytes, warmup, iters):
     ms = C.c_double()
     _check(lib().voxhip_bench_copy(nbytes, warmup, iters, C.byref(ms)), "bench_copy")
     return ms.value
+
+
+def bench_ffn_q8(hidden, inter, copies, warmup, iters):
+    """Average microseconds of one q8 FFN block (two kernels) over `copies` rotating weight sets."""
+    us = C.c_double()
+    _check(lib().voxhip_bench_ffn_q8(hidden, inter, copies, warmup, iters, C.byref(us)), "bench_ffn_q8")
+    return us.value
