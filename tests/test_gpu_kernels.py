@@ -60,6 +60,22 @@ def test_matmul_parity(hip, oracle, wt, rows, cols):
         assert rel_err(y, r) < GEMV_TOL, (wt, rows, cols, m, rel_err(y, r))
 
 
+@pytest.mark.parametrize("wt", [Q8, F32, F16, BF16])
+@pytest.mark.parametrize("rows,cols", [(37, 160), (1000, 1024), (2048, 896)])
+def test_matmul_gemm_rows(hip, oracle, wt, rows, cols):
+    # f32-activation passes of more than 4 rows run on the MFMA GEMM: ragged row/column tiles, bias, and 600 rows
+    # over two passes (512 + 88)
+    rng = np.random.default_rng(rows + cols * 3 + wt)
+    data, scale, bias = make_mat(rng, wt, rows, cols, bias=True)
+    M = oracle.Mat(wt, data, rows, cols, scale, bias)
+    h = hip.upload(hip.HostMat(wt, data, rows, cols, scale, bias))
+    for m in (6, 64, 65, 200, 600):
+        x = rng.standard_normal((m, cols)).astype(np.float32)
+        y = hip.matmul(h, x)
+        r = oracle.matmul(M, x)
+        assert rel_err(y, r) < GEMV_TOL, (wt, rows, cols, m, rel_err(y, r))
+
+
 @pytest.mark.parametrize("rows,cols", [(4096, 2048), (2048, 6144), (37, 160)])
 def test_q4_f16_scales(hip, oracle, rows, cols):
     # Q4 scales that are exact in f16 are stored in 2 bytes on the device (the cfg 3 "4-bit + f16 scale" format):

@@ -69,6 +69,26 @@ def test_prefill_then_decode(hip, oracle, m):
         assert rel_err(out, oracle.transformer_forward(mdl.ox, kv, x)) < TOL
 
 
+@pytest.mark.parametrize("wt,m", [(F16, 70), (BF16, 130), (F32, 37), (Q8, 520)])
+def test_prefill_gemm(hip, oracle, wt, m):
+    # f32-activation prefill: the matrices run on the MFMA GEMM with the RMSNorm / attention-merge prologues as
+    # their own kernels; 520 rows take two passes (512 + 8). Biased q/k/v.
+    mdl = Model(500 + m, 2, 256, 4, 2, 128, 512, wtype=wt, bias=True, head_rows=96)
+    xf, head = build(hip, mdl)
+    seq = hip.seq_create(xf, 1024)
+    kv = mdl.oracle_kv(1024, kv_f16=1)
+    rng = np.random.default_rng(m)
+    x = rng.standard_normal((m, 256)).astype(np.float32)
+    out, logits = hip.forward(xf, seq, 0, x, 256, head=head)
+    ref = oracle.transformer_forward(mdl.ox, kv, x)
+    assert rel_err(out, ref) < TOL, rel_err(out, ref)
+    assert rel_err(logits, oracle_head(oracle, mdl, out)) < TOL
+    for step in range(2):
+        x = rng.standard_normal((1, 256)).astype(np.float32)
+        out, _ = hip.forward(xf, seq, m + step, x, 256, head=head)
+        assert rel_err(out, oracle.transformer_forward(mdl.ox, kv, x)) < TOL
+
+
 def test_gqa7_bias_hd64(hip, oracle):
     # CosyVoice2-shaped attention: 7 query heads per kv head, head_dim 64, q/k/v biases, no q/k norm
     mdl = Model(300, 2, 128, 7, 1, 64, 256, wtype=Q8, qk_norm=False, bias=True, head_rows=100, head_type=F32)

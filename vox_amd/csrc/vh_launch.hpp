@@ -28,6 +28,11 @@ hipError_t launch_gemv(int wt, bool int_path, int pro, int epi, const GemvArgs &
 void gemv_tile(int rows, int nchunk, int M, bool swiglu, int *R, int *IT);
 
 hipError_t launch_qk_post(const QkArgs &a, int m, hipStream_t s);
+
+// Multi-row f32 GEMM on the matrix cores (F32 / F16 / BF16 / Q8 weights).
+hipError_t launch_gemm(int wt, int epi, const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s);
+// Merge of the split attention partials of m rows into ao [m][heads * hd].
+hipError_t launch_attn_merge(const AttnPartials &P, float *ao, int m, hipStream_t s);
 // Split-K attention partials of m rows (merged by the PRO_ATTN GEMV prologue). fused: rows of distinct sequences,
 // q/k post-processing and the K/V append happen inside; otherwise k_qk_post ran first. kc0/vc0/cap0: row 0's cache
 // (the same as the first row view); qkv: [m][a.ldqkv]; rope_rows: [m][hd] (fused).

@@ -85,6 +85,14 @@ struct SampleCfgDev {
     const int32_t *history;  // device
 };
 
+// The multi-row MFMA GEMM (y[i][r] = sum_k A[i][k] W[r][k] + bias[r], then the epilogue).
+struct GemmArgs {
+    const float *bias;  // [n] or null
+    float *y;           // [m][ldy]
+    int64_t lda, ldy;
+    int32_t m, n, K;
+};
+
 constexpr int kSampleThreads = 1024;
 constexpr int kSampleMaxN = 16384;  // logits per call (keys sorted in LDS)
 
