@@ -193,6 +193,36 @@ int voxhip_decode_dev(int xfmr, int seq, int64_t pos0, const float *d_x, int64_t
 int voxhip_decode_steps_dev(int xfmr, const int32_t *seqs, const int64_t *pos, int64_t B, const float *d_x, float *d_out,
                             int head, float *d_logits, const voxhip_sample_cfg *cfgs, int32_t *d_tokens);
 
+/* ---------------------------------------------------------------- CosyVoice2 LM (cosyvoice.cpp:598-690)
+ * The reference runs this loop on the host around gpu_xfmr_forward and gpu_matmul (cosyvoice.cpp:573-575,
+ * :598-607); these entry points keep it on the device: head + bias -> lm_logp -> ras_sample with the trial loop
+ * of lm_generate -> the speech-token embedding of the pick -> the layers at the next position. */
+typedef struct voxhip_lm_cfg {
+    float top_p;            /* CosyCfg::top_p: keep while the sorted cumulative probability < top_p (> 0) */
+    int32_t top_k;          /* CosyCfg::top_k: at most top_k kept, 1..1024 */
+    int32_t win_size;       /* CosyCfg::win_size: repetition window of decoded tokens, 0..1024 */
+    float tau_r;            /* CosyCfg::tau_r: resample when the pick occurs >= win_size * tau_r times */
+    int32_t speech_tokens;  /* CosyCfg::speech_tokens: ids >= speech_tokens end the generation */
+    int32_t min_len;        /* lm_generate's min_len (text length * min_ratio): no end before this step */
+    int32_t max_len;        /* lm_generate's max_len (text length * max_ratio): at most max_len steps */
+    uint32_t piece;         /* Philox stream 0x43560000 + piece (cosyvoice.cpp:672) */
+    uint64_t seed;          /* DetRng(seed) */
+} voxhip_lm_cfg;
+/* lm_logp + the trial loop of lm_generate for step `step` (cosyvoice.cpp:598-607, :674-683) on device logits
+ * [n] (head output + bias, n 2..8192) with the decoded tokens d_decoded [n_decoded] (device). d_logp (optional,
+ * device [n]): the log-probabilities before the trials. *token: the pick (>= speech_tokens: the end). Fails
+ * (0) where the reference fails: more than 101 trials that end before min_len. */
+int voxhip_lm_sample_dev(const float *d_logits, int32_t n, const voxhip_lm_cfg *cfg, int64_t step, const int32_t *d_decoded,
+                         int32_t n_decoded, float *d_logp, int32_t *token);
+/* lm_begin's prefill + lm_generate's loop (cosyvoice.cpp:564-596, :666-690) on the device: x [n][hidden] (host,
+ * the gathered prompt embeddings) at positions 0..n-1 of seq, then up to max_len steps of final norm -> head
+ * (with its bias) -> lm_logp -> RAS trial loop -> row `token` of speech_emb -> layers at the next position.
+ * tokens [max_len] receives the decoded tokens (the end token excluded), *n_tokens their count; logp (optional,
+ * host [max_len][head rows]) the log-probabilities of every step that sampled. The sequence needs
+ * n + max_len + 1 positions (its last slot takes the writes of steps launched after the end). */
+int voxhip_lm_generate(int xfmr, int seq, const float *x, int64_t n, int head, int speech_emb, const voxhip_lm_cfg *cfg,
+                       int32_t *tokens, float *logp, int32_t *n_tokens);
+
 /* Synthetic weights and caches, generated on the device (Philox4x32-10 Box-Muller, mean + std * z).
  * voxhip_mat_synthetic: f32 values, then quantized on the device to `type` with the reference's
  * quantizer (Q8: kernels.cpp:918-929; Q4: kernels.cpp:606-645; F16/BF16: nearest even). Returns a handle.

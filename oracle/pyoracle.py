@@ -63,6 +63,8 @@ def _declare(lib, prefix):
         sig.update({
             "softmax": (None, [P, I64]),
             "ras_sample": (I32, [P, I32, P, I32, F, I32, I32, F, F, F]),
+            "lm_logp": (None, [P, I32]),
+            "lm_step": (I32, [P, I32, P, I32, I64, I32, I32, F, I32, I32, F, U64, U32]),
             "noise": (None, [U64, U32, C.c_size_t, P]),
             "f16_to_f32": (F, [C.c_uint16]),
             "f32_to_f16": (C.c_uint16, [F]),
@@ -178,6 +180,22 @@ def sample_logits(logits, temperature=0.9, top_p=1.0, top_k=50, rep=1.0, history
     h = None if history is None else np.ascontiguousarray(history, dtype=np.int32)
     fn = ref().ref_sample_logits if use_ref else lib().vo_sample_logits
     return fn(_p(l), l.size, temperature, top_p, top_k, rep, _p(h), 0 if h is None else h.size, u)
+
+
+def lm_logp(v):
+    """lm_logp after the head and bias: a log-softmax copy of v (cosyvoice.cpp:602-606)."""
+    l = np.ascontiguousarray(v, dtype=np.float32).copy()
+    lib().vo_lm_logp(_p(l), l.size)
+    return l
+
+
+def lm_step(logp, decoded, step, min_len, speech_tokens, top_p=0.8, top_k=25, win_size=10, tau_r=0.1, seed=1234, piece=0):
+    """One step of lm_generate's trial loop on log-probabilities; returns (token or -2, logp as modified)."""
+    l = np.ascontiguousarray(logp, dtype=np.float32).copy()
+    d = np.ascontiguousarray(decoded, dtype=np.int32)
+    tok = lib().vo_lm_step(_p(l), l.size, _p(d) if d.size else None, d.size, step, min_len, speech_tokens, top_p, top_k,
+                           win_size, tau_r, seed, piece)
+    return tok, l
 
 
 def uniform(seed, frame, cb, draw=0):

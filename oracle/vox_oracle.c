@@ -196,6 +196,30 @@ int32_t vo_ras_sample(float *logp, int32_t n, const int32_t *decoded, int32_t n_
     return result;
 }
 
+/* lm_logp (cosyvoice.cpp:598-607) after the head and bias */
+void vo_lm_logp(float *v, int32_t n) {
+    float mx = -INFINITY;
+    for (int32_t i = 0; i < n; ++i) mx = mx < v[i] ? v[i] : mx;
+    double sum = 0;
+    for (int32_t i = 0; i < n; ++i) sum += exp((double)(v[i] - mx));
+    const float lse = mx + (float)log(sum);
+    for (int32_t i = 0; i < n; ++i) v[i] -= lse;
+}
+
+/* the trial loop of lm_generate (cosyvoice.cpp:674-683) */
+int32_t vo_lm_step(float *logp, int32_t n, const int32_t *decoded, int32_t n_decoded, int64_t step, int32_t min_len,
+                   int32_t speech_tokens, float top_p, int32_t top_k, int32_t win_size, float tau_r, uint64_t seed,
+                   uint32_t piece) {
+    const uint32_t stream = 0x43560000u + piece;
+    for (int trial = 0;; ++trial) {
+        const float u0 = vo_uniform(seed, (uint64_t)step, stream, (uint32_t)(2 * trial));
+        const float u1 = vo_uniform(seed, (uint64_t)step, stream, (uint32_t)(2 * trial + 1));
+        const int32_t top = vo_ras_sample(logp, n, decoded, n_decoded, top_p, top_k, win_size, tau_r, u0, u1);
+        if (step >= min_len || top < speech_tokens) return top;
+        if (trial > 100) return -2;
+    }
+}
+
 /* ------------------------------------------------------------------ formats */
 float vo_f16_to_f32(uint16_t h) { /* exact widening incl. subnormals (kernels.hpp:63-75) */
     const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;

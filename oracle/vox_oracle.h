@@ -51,6 +51,15 @@ int32_t vo_sample_logits(float *logits, int32_t n, float temperature, float top_
  * (the chosen token is set to -inf when it is resampled). */
 int32_t vo_ras_sample(float *logp, int32_t n, const int32_t *decoded, int32_t n_decoded, float top_p, int32_t top_k,
                       int32_t win_size, float tau_r, float u0, float u1);
+/* lm_logp's log-softmax (cosyvoice.cpp:602-606) in place on v = head output + bias: mx = max, lse = mx +
+ * float(log(sum of exp(double(v - mx)))) summed in index order, v -= lse. */
+void vo_lm_logp(float *v, int32_t n);
+/* One step of lm_generate's trial loop (cosyvoice.cpp:677-682): u0, u1 = uniform(step, 0x43560000 + piece,
+ * 2 trial (+1)) under key seed; ras_sample until step >= min_len or the token is below speech_tokens. Returns the
+ * token (>= speech_tokens: the end), or -2 when the reference fails after trial 101. logp is modified as there. */
+int32_t vo_lm_step(float *logp, int32_t n, const int32_t *decoded, int32_t n_decoded, int64_t step, int32_t min_len,
+                   int32_t speech_tokens, float top_p, int32_t top_k, int32_t win_size, float tau_r, uint64_t seed,
+                   uint32_t piece);
 /* Philox Box-Muller normal stream (f5.cpp:402-414): out[2p], out[2p+1] from draws (p, stream, 0/1). */
 void vo_noise(uint64_t seed, uint32_t stream, size_t n, float *out);
 

@@ -164,6 +164,55 @@ def test_ras_sample_properties(oracle):
     assert np.max(np.abs(c - rest)) < 2.0 / 400 + 1e-9
 
 
+def test_lm_logp_closed_form(oracle):
+    # cosyvoice.cpp:602-606: logp = v - (mx + float(log(sum exp(double(v - mx))))): a float64 log-softmax to f32 ulps
+    rng = np.random.default_rng(11)
+    for n in (2, 300, 6564):
+        v = (rng.standard_normal(n) * 4).astype(np.float32)
+        v[rng.integers(0, n)] += 30  # a dominant entry
+        got = po.lm_logp(v)
+        v64 = v.astype(np.float64)
+        want = v64 - (v64.max() + np.log(np.exp(v64 - v64.max()).sum()))
+        assert np.max(np.abs(got - want)) <= 4 * np.spacing(np.float32(np.abs(want).max()))
+        assert abs(np.log(np.exp(got.astype(np.float64)).sum())) < 1e-5  # normalized
+        assert np.argmax(got) == np.argmax(v)
+
+
+def test_lm_step_trial_loop(oracle):
+    # lm_generate (cosyvoice.cpp:674-683): u0, u1 = DetRng(seed).uniform(step, 0x43560000 + piece, 2 trial (+1));
+    # no end token before min_len; failure after trial 101
+    rng = np.random.default_rng(12)
+    n, speech = 64, 60
+    lp = po.lm_logp(rng.standard_normal(n).astype(np.float32))
+    f = po.lib().vo_ras_sample
+    def ras(l, decoded, u0, u1):
+        l = l.copy()
+        d = np.ascontiguousarray(decoded, np.int32)
+        return f(l.ctypes.data, n, d.ctypes.data if d.size else None, d.size, 0.8, 25, 10, 0.1, u0, u1), l
+    # at or past min_len: one ras_sample draw with the trial-0 counters
+    for step in (0, 5, 17):
+        u0 = po.uniform(99, step, 0x43560000 + 7, 0)
+        u1 = po.uniform(99, step, 0x43560000 + 7, 1)
+        tok, _ = po.lm_step(lp, [], step, 0, speech, seed=99, piece=7)
+        assert tok == ras(lp, [], u0, u1)[0]
+    # only end tokens can be picked: every trial draws one, the reference fails after trial 101 (102 draws)
+    only_end = np.full(n, -np.inf, np.float32)
+    only_end[speech:] = np.log(0.25)
+    assert po.lm_step(only_end, [], 3, 10, speech)[0] == -2
+    assert po.lm_step(only_end, [], 10, 10, speech)[0] >= speech  # at min_len the end is accepted
+    # half end token, half speech token (same probability: the lower index sorts first): the loop ends at the
+    # first trial whose u0 falls in the speech token's half
+    two = np.full(n, -np.inf, np.float32)
+    two[[5, speech]] = np.log(0.5)
+    tok, _ = po.lm_step(two, [], 2, 10, speech, seed=5)
+    first = next(t for t in range(102) if po.uniform(5, 2, 0x43560000, 2 * t) * 1.0 < 0.5)
+    assert tok == 5 and first < 101
+    # the resampled pick keeps logp = -inf across trials: a token repeated twice in the window is never returned
+    rep = int(np.argmax(lp[:speech]))
+    tok, l2 = po.lm_step(lp, [rep, rep, 1, 2], 0, 5, speech)
+    assert tok != rep and tok < speech
+
+
 def test_noise_moments(oracle):
     # test_core.cpp:630-645
     a = po.noise(42, 0xF5000000 + 3, 100001)

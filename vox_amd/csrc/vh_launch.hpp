@@ -54,6 +54,10 @@ hipError_t launch_fill_cache(void *c, int64_t planes, int64_t cap, int64_t len, 
                              float mean, float std, hipStream_t s);
 
 hipError_t launch_copy16(const void *src, void *dst, int64_t bytes, hipStream_t s);
+// CosyVoice2 LM: one sampling step (log-softmax, RAS trial loop) and the next step's embedding + row advance.
+hipError_t launch_lm_sample(const float *logits, int n, const LmCfgDev *cfg, LmState *st, int32_t *decoded, float *logp_out,
+                            int64_t logp_stride, bool append, hipStream_t s);
+hipError_t launch_lm_embed(const LmEmbedArgs &a, hipStream_t s);
 
 // Shared-memory opt-in above 64 KiB, once per kernel.
 hipError_t ensure_smem(const void *kernel, size_t bytes);

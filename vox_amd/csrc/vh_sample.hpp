@@ -13,60 +13,9 @@
 // holds exactly the keys still needed (usually 2-3 passes; each pass is one LDS-atomic histogram and one wave
 // scan of its 256 bins), then a register bitonic sort of 64 lanes in one wave. k > 64 sorts in LDS.
 #pragma once
-#include "vh_common.hpp"
-#include "vh_types.hpp"
+#include "vh_topk.hpp"
 
 namespace vh {
-
-// Order-preserving map of a float to uint32 (larger value -> larger key); -0 == +0; NaN lowest.
-VH_DEV uint32_t ord_key(float f) {
-    if (f == 0.f) f = 0.f;
-    const uint32_t b = __float_as_uint(f);
-    if ((b & 0x7FFFFFFFu) > 0x7F800000u) return 0u;
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-VH_DEV float ord_val(uint32_t k) { return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k); }
-
-VH_DEV double readlane_d(double v, int j) {
-    const uint64_t b = __double_as_longlong(v);
-    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b)), j));
-    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b >> 32)), j));
-    return __longlong_as_double(int64_t(uint64_t(hi) << 32 | lo));
-}
-VH_DEV uint64_t readlane_u64(uint64_t v, int j) {
-    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v)), j));
-    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v >> 32)), j));
-    return uint64_t(hi) << 32 | lo;
-}
-// Value of lane (lane ^ m) for a 64-bit value: DPP within a 16-lane row for m <= 8, a swizzle for 16, a permute
-// for 32 (m is a compile-time constant after unrolling).
-VH_DEV int xor_lane(int x, int m) {
-    const int lane = threadIdx.x & 63;
-    switch (m) {
-        case 1: return dpp<kDppXor1>(x);
-        case 2: return dpp<kDppXor2>(x);
-        case 4: {  // both DPP reads run with every lane active (a disabled source lane would read as 0)
-            const int up = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0xF, false);  // row_shl:4 reads lane i + 4
-            const int dn = __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4 reads lane i - 4
-            return (lane & 4) ? dn : up;
-        }
-        case 8: return __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false);  // row_ror:8 = lane ^ 8 in the row
-        case 16: return __builtin_amdgcn_ds_swizzle(x, 0x401F);  // bit mode: and 0x1F, xor 0x10
-        default: return __shfl_xor(x, m, kWave);
-    }
-}
-VH_DEV uint64_t shfl_xor_u64(uint64_t v, int m) {
-    const uint32_t lo = uint32_t(xor_lane(int(uint32_t(v)), m));
-    const uint32_t hi = uint32_t(xor_lane(int(uint32_t(v >> 32)), m));
-    return uint64_t(hi) << 32 | lo;
-}
-
-// Dynamic LDS of k_sample in bytes for n logits: room for the sorted keys of the LDS path.
-inline size_t sample_smem_bytes(int n) {
-    size_t k2 = 64;
-    while (k2 < size_t(n)) k2 <<= 1;
-    return k2 * sizeof(uint64_t);
-}
 
 // One block per row b: logits [b][n] with cfg[b] -> out[b] = sampled index (or -1 when n is outside
 // 1..kSampleMaxN). Dynamic LDS: sample_smem_bytes(n).
@@ -77,9 +26,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *c
     int32_t *out = outs + blockIdx.x;
     extern __shared__ __align__(16) uint64_t sample_keys[];
     __shared__ uint32_t seen[kSampleMaxN / 32];
-    __shared__ uint32_t hist[256];
-    __shared__ uint64_t sh_prefix;
-    __shared__ int sh_bits, sh_kk, sh_done, sh_cnt;
+    __shared__ TopkSmem S;
     __shared__ unsigned long long sh_best;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     if (n <= 0 || n > kSampleMaxN) { if (t == 0) out[0] = -1; return; }
@@ -94,8 +41,8 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *c
     }
     const SampleCfgDev cfg = *cfgp;
 
-    if (t < 256) hist[t] = 0u;
-    if (t == 0) { sh_prefix = 0ull; sh_bits = 0; sh_done = 0; sh_cnt = 0; sh_best = 0ull; }
+    if (t < 256) S.hist[t] = 0u;
+    if (t == 0) { topk_reset(S); sh_best = 0ull; }
     const bool penalty = cfg.rep != 1.0f && cfg.history && cfg.n_history > 0;  // uniform
     if (penalty) {  // tokens seen in the history, each penalized once (sampling.hpp:65-73)
         for (int i = t; i < kSampleMaxN / 32; i += kSampleThreads) seen[i] = 0u;
@@ -138,112 +85,9 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *c
     }
 
     const int k = (cfg.top_k > 0 && cfg.top_k < n) ? cfg.top_k : n;
-    if (t == 0) sh_kk = k;
-    __syncthreads();
-
-    // ---- radix select of the k-th largest key, 8 bits per pass. Wave 0 scans the histogram from the top bin
-    // down (4 bins per lane, a prefix sum over lanes) and clears each bin after reading it.
-    for (int pass = 0; pass < 8; ++pass) {
-        const uint64_t P = sh_prefix;
-        const int L = sh_bits, shift = 56 - 8 * pass;
-#pragma unroll
-        for (int e = 0; e < E; ++e)
-            if (key[e] && (L == 0 || (key[e] >> (64 - L)) == P)) atomicAdd(&hist[(key[e] >> shift) & 255u], 1u);
-        __syncthreads();
-        if (wave == 0) {
-            int c[4], loc = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                c[j] = int(hist[255 - 4 * lane - j]);
-                loc += c[j];
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) hist[255 - 4 * lane - j] = 0u;
-            int incl = loc;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int x = __shfl_up(incl, o, kWave);
-                if (lane >= o) incl += x;
-            }
-            const int kk = sh_kk;
-            const uint64_t bal = __ballot(incl >= kk);
-            const int first = __ffsll((long long)bal) - 1;
-            if (lane == first) {
-                int before = incl - loc, digit = 0, cnt = 0;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (before + c[j] >= kk) { digit = 255 - 4 * lane - j; cnt = c[j]; break; }
-                    before += c[j];
-                }
-                sh_prefix = (P << 8) | uint64_t(digit);
-                sh_bits = L + 8;
-                sh_kk = kk - before;
-                sh_done = cnt == kk - before;
-            }
-        }
-        __syncthreads();
-        if (sh_done) break;
-    }
-    const uint64_t P = sh_prefix;
-    const int L = sh_bits;
-    int K2 = 64;
-    while (K2 < k) K2 <<= 1;
-    // ---- the k selected keys (any order), padded with zeros (lowest) to K2. One LDS atomic per wave reserves
-    // the wave's slots; lanes place their keys by ballot rank.
-    {
-        uint64_t masks[E];
-        int wave_total = 0;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            masks[e] = e < per ? __ballot(key[e] && (key[e] >> (64 - L)) >= P) : 0ull;
-            wave_total += __popcll(masks[e]);
-        }
-        int base = 0;
-        if (wave_total) {
-            if (lane == 0) base = atomicAdd(&sh_cnt, wave_total);
-            base = __builtin_amdgcn_readfirstlane(base);
-        }
-        const uint64_t lt = (1ull << lane) - 1ull;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            if ((masks[e] >> lane) & 1ull) {
-                const int p = base + __popcll(masks[e] & lt);
-                if (p < K2) sample_keys[p] = key[e];
-            }
-            base += __popcll(masks[e]);
-        }
-    }
-    for (int i = k + t; i < K2; i += kSampleThreads) sample_keys[i] = 0ull;
-    __syncthreads();
-
-    uint64_t v = 0ull;  // small path: lane j holds the j-th largest key
-    const bool small = K2 == 64;
-    if (small) {
-        if (wave != 0) return;
-        v = sample_keys[lane];
-#pragma unroll
-        for (int size = 2; size <= 64; size <<= 1)
-#pragma unroll
-            for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                const uint64_t o = shfl_xor_u64(v, stride);
-                const bool keep_max = ((lane & stride) == 0) == ((lane & size) == 0);
-                v = keep_max ? (o > v ? o : v) : (o < v ? o : v);
-            }
-    } else {
-        for (int size = 2; size <= K2; size <<= 1)
-            for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                for (int i = t; i < K2; i += kSampleThreads) {
-                    const int l = i ^ stride;
-                    if (l > i) {
-                        const uint64_t x = sample_keys[i], y = sample_keys[l];
-                        const bool desc = (i & size) == 0;
-                        if (desc ? (x < y) : (x > y)) { sample_keys[i] = y; sample_keys[l] = x; }
-                    }
-                }
-                __syncthreads();
-            }
-        if (wave != 0) return;
-    }
+    uint64_t v = 0ull;  // small path: lane j of wave 0 holds the j-th largest key
+    const bool small = topk_sorted<E>(key, per, k, S, sample_keys, v);
+    if (wave != 0) return;
 
     // ---- probabilities in double (sampling.hpp:91-99), one wave; lanes compute the terms of a chunk of 64 in
     // parallel, the sums add them in sorted order like the reference's loops.

@@ -93,6 +93,37 @@ struct GemmArgs {
     int32_t m, n, K;
 };
 
+// CosyVoice2 LM sampling (lm_logp + ras_sample + lm_generate's trial loop, cosyvoice.cpp:598-690).
+struct LmCfgDev {
+    float top_p, tau_r;
+    int32_t top_k, win_size;
+    int32_t speech_tokens;  // ids >= speech_tokens end the generation
+    int32_t min_len, max_len;  // lm_generate's bounds; a step at i >= max_len ends the generation
+    uint32_t key0, key1;    // DetRng(seed)
+    uint32_t stream;        // 0x43560000 + piece
+    int32_t max_trials;     // the reference fails after trial 101
+};
+// Device state of a generation: step i, decoded count, done flag, status (0 ok, 1 trial limit), last token.
+struct LmState {
+    int32_t step, n_dec, done, status, last, pad0, pad1, pad2;
+};
+struct LmEmbedArgs {
+    const uint8_t *w;
+    const void *scale;     // f32 [rows][cols/32], or f16 bits when s16 (Q4)
+    int32_t type, s16;
+    int64_t rows, cols;
+    const LmState *st;
+    const int32_t *decoded;
+    float *x;
+    RowRef *row;
+    float *rope_row;       // [hd] (cos, sin) pairs of the row
+    const float *rope;     // table [positions][hd]
+    int32_t hd;
+    int64_t spare_pos;
+};
+constexpr int kLmMaxK = 1024;  // top_k limit of the device RAS sampler (sorted in LDS above 64)
+constexpr int kLmMaxN = 8192;  // vocabulary limit of the device RAS sampler (8 entries per thread)
+
 constexpr int kSampleThreads = 1024;
 constexpr int kSampleMaxN = 16384;  // logits per call (keys sorted in LDS)
 

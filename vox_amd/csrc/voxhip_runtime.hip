@@ -95,6 +95,14 @@ struct Xfmr {
     std::map<GraphKey, hipGraphExec_t> graphs;
     std::vector<RowRef> rows_last;
     bool rows_valid = false;
+    // CosyVoice2 LM generation: config, state and decoded tokens on the device, pinned copies for the host,
+    // optional per-step log-probabilities; graphs of kLmGraphSteps steps keyed by (seq, head, embedding, logp)
+    LmCfgDev *lm_cfg = nullptr;
+    LmState *lm_state = nullptr;
+    int32_t *lm_dec = nullptr;
+    float *lm_logp = nullptr;
+    int64_t lm_dec_cap = 0, lm_logp_cap = 0;
+    std::map<std::array<int64_t, 4>, hipGraphExec_t> lm_graphs;
 };
 
 struct Seq {
@@ -129,6 +137,10 @@ struct Ctx {
     SampleCfgDev *scfg_dev = nullptr, *scfg_host = nullptr;
     int32_t *hist_dev = nullptr, *tok_dev = nullptr;
     size_t hist_cap = 0;
+    // LM sampler staging: device config + state, and their pinned host copies (config, state, two state slots)
+    LmCfgDev *lm_cfg_dev = nullptr;
+    LmState *lm_state_dev = nullptr;
+    uint8_t *lm_host = nullptr;
 };
 
 Ctx g;
@@ -362,6 +374,8 @@ void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, in
 void drop_graphs(Xfmr &X) {
     for (auto &kv : X.graphs) (void)hipGraphExecDestroy(kv.second);  // graphs captured the old buffer addresses
     X.graphs.clear();
+    for (auto &kv : X.lm_graphs) (void)hipGraphExecDestroy(kv.second);
+    X.lm_graphs.clear();
 }
 
 void ensure_rope(Xfmr &X, int64_t rows) {
@@ -545,16 +559,17 @@ void check_seq_for(Xfmr &X, int xid, const Seq &S) {
 }
 
 // Generic host-pointer forward for up to any m rows of one sequence (or B rows of B sequences).
-// rows_of(i) gives the cache view of row i. x rows are xc wide (in_proj cols or hidden).
+// rows_of(i) gives the cache view of row i. x rows are xc wide (in_proj cols or hidden). Returns the row of X.h
+// that holds the last input row's hidden state.
 template <class RowsOf>
-void forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_proj, int first_layer, int n_layers, int64_t m_total,
+int forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_proj, int first_layer, int n_layers, int64_t m_total,
                   float *hidden_out, float *out_last, int head, float *head_out, bool final_all) {
     const int64_t H = X.H;
     const GpuMat *Pm = in_proj >= 0 ? &mat_at(in_proj) : nullptr;
     if (Pm && Pm->rows != H) throw Fail("in_proj rows differ from the hidden size");
     const int64_t xc = Pm ? Pm->cols : H;
     // rows per pass: the smallest of the passes the used matrices allow (8 on the int8 path, 512 on the f32 path)
-    int chunk = kMaxPass;
+    int chunk = kMaxPass, last_row = 0;
     for (int li = first_layer; li < first_layer + n_layers; ++li)
         for (int id : {X.L[size_t(li)].qkv, X.L[size_t(li)].o, X.L[size_t(li)].gu, X.L[size_t(li)].down})
             chunk = std::min(chunk, rows_per_pass(g.mats[size_t(id)], m_total));
@@ -567,6 +582,7 @@ void forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_pro
     for (int64_t c0 = 0; c0 < m; c0 += chunk) {
         const int mc = int(std::min<int64_t>(chunk, m - c0));
         const bool last = c0 + mc == m;
+        last_row = mc - 1;
         std::vector<RowRef> rr(static_cast<size_t>(mc));
         for (int i = 0; i < mc; ++i) rr[size_t(i)] = rows_of(c0 + i);
         set_rows(X, rr);
@@ -607,6 +623,7 @@ void forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_pro
         }
     }
     HIPCHECK(hipStreamSynchronize(g.stream));
+    return last_row;
 }
 
 void fill_sample_cfg(SampleCfgDev &d, const voxhip_sample_cfg &c, const int32_t *hist_dev, int32_t n_hist) {
@@ -1229,6 +1246,195 @@ int voxhip_decode_steps_dev(int xfmr, const int32_t *seqs, const int64_t *pos, i
         if (cfgs) set_sample_cfgs(X, cfgs, int(B));
         hipGraphExec_t exec = decode_graph(X, key, int(B), true, head, d_x, d_out, d_logits, cfgs != nullptr, d_tokens);
         HIPCHECK(hipGraphLaunch(exec, g.stream));
+        return 1;
+    }, 0);
+}
+
+}  // extern "C"
+
+namespace {
+constexpr int kLmGraphSteps = 8;  // generation steps per captured graph (the host checks for the end between graphs)
+
+LmCfgDev lm_cfg_dev(const voxhip_lm_cfg &c, int32_t max_len) {
+    LmCfgDev d{};
+    d.top_p = c.top_p; d.tau_r = c.tau_r; d.top_k = c.top_k; d.win_size = c.win_size;
+    d.speech_tokens = c.speech_tokens; d.min_len = c.min_len; d.max_len = max_len;
+    d.key0 = uint32_t(c.seed); d.key1 = uint32_t(c.seed >> 32);  // DetRng(seed) (sampling.hpp:37)
+    d.stream = 0x43560000u + c.piece;                             // "CV" + piece (cosyvoice.cpp:672)
+    d.max_trials = 101;                                            // fail after trial 101 (cosyvoice.cpp:681)
+    return d;
+}
+void check_lm_cfg(const voxhip_lm_cfg &c, int64_t n) {
+    if (n < 2 || n > kLmMaxN) throw Fail("LM sampler supports 2..8192 logits");
+    if (c.top_k < 1 || c.top_k > kLmMaxK) throw Fail("LM top_k must be 1..1024");
+    if (!(c.top_p > 0.f)) throw Fail("LM top_p must be positive");
+    if (c.win_size < 0 || c.win_size > kLmMaxK) throw Fail("LM win_size must be 0..1024");
+    if (c.speech_tokens < 1 || c.speech_tokens > n) throw Fail("LM speech_tokens out of range");
+    if (c.min_len < 0 || c.max_len < 0) throw Fail("LM min_len / max_len must not be negative");
+}
+// Pinned host block of the LM staging: [LmCfgDev][LmState x 3]
+LmCfgDev *lm_host_cfg() { return reinterpret_cast<LmCfgDev *>(g.lm_host); }
+LmState *lm_host_state(int i) { return reinterpret_cast<LmState *>(g.lm_host + 256) + i; }
+void ensure_lm_staging() {
+    if (g.lm_host) return;
+    g.lm_cfg_dev = dalloc_t<LmCfgDev>(1);
+    g.lm_state_dev = dalloc_t<LmState>(1);
+    HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&g.lm_host), 256 + 3 * sizeof(LmState), hipHostMallocDefault));
+}
+
+void lm_buffers(Xfmr &X, int64_t max_len, int64_t V, bool want_logp) {
+    bool changed = false;
+    if (!X.lm_cfg) {
+        X.lm_cfg = dalloc_t<LmCfgDev>(1);
+        X.lm_state = dalloc_t<LmState>(1);
+        changed = true;
+    }
+    if (X.lm_dec_cap < max_len) {
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        dfree(X.lm_dec);
+        X.lm_dec = dalloc_t<int32_t>(size_t(max_len));
+        X.lm_dec_cap = max_len;
+        changed = true;
+    }
+    if (want_logp && X.lm_logp_cap < max_len * V) {
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        dfree(X.lm_logp);
+        X.lm_logp = dalloc_t<float>(size_t(max_len * V));
+        X.lm_logp_cap = max_len * V;
+        changed = true;
+    }
+    if (changed) drop_graphs(X);
+}
+
+// kLmGraphSteps generation steps: final norm + head (+ bias) of row 0 -> sampler -> embedding of the pick and the
+// row advanced -> the layers (one fused row). The device state ends the loop; steps after the end write only the
+// sequence's spare slot.
+hipGraphExec_t lm_graph(Xfmr &X, const Seq &S, int seq, int head, int emb, bool want_logp) {
+    const std::array<int64_t, 4> key{seq, head, emb, want_logp ? 1 : 0};
+    auto it = X.lm_graphs.find(key);
+    if (it != X.lm_graphs.end()) return it->second;
+    const GpuMat &Hm = mat_at(head), &E = mat_at(emb);
+    LmEmbedArgs ea{};
+    ea.w = E.w; ea.scale = E.s; ea.type = E.type; ea.s16 = E.s16 ? 1 : 0; ea.rows = E.rows; ea.cols = E.cols;
+    ea.st = X.lm_state; ea.decoded = X.lm_dec; ea.x = X.h; ea.row = X.rows_dev; ea.rope_row = X.rope_rows_dev;
+    ea.rope = X.rope; ea.hd = X.hd; ea.spare_pos = S.cap - 1;
+    hipGraph_t graph = nullptr;
+    HIPCHECK(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal));
+    try {
+        for (int i = 0; i < kLmGraphSteps; ++i) {
+            enqueue_final(X, 0, 1, head, g.stream);
+            HIPCHECK(launch_lm_sample(X.logits, int(Hm.rows), X.lm_cfg, X.lm_state, X.lm_dec, want_logp ? X.lm_logp : nullptr,
+                                      Hm.rows, true, g.stream));
+            HIPCHECK(launch_lm_embed(ea, g.stream));
+            enqueue_layers(X, 1, 1, 0, X.layers, g.stream, true);
+        }
+    } catch (...) {
+        (void)hipStreamEndCapture(g.stream, &graph);
+        if (graph) (void)hipGraphDestroy(graph);
+        throw;
+    }
+    HIPCHECK(hipStreamEndCapture(g.stream, &graph));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    HIPCHECK(e);
+    X.lm_graphs[key] = exec;
+    return exec;
+}
+}  // namespace
+
+extern "C" {
+
+int voxhip_lm_sample_dev(const float *d_logits, int32_t n, const voxhip_lm_cfg *cfg, int64_t step, const int32_t *d_decoded,
+                         int32_t n_decoded, float *d_logp, int32_t *token) {
+    return guard_int([&] {
+        require_ok();
+        if (!d_logits || !cfg || !token || step < 0 || n_decoded < 0 || (n_decoded > 0 && !d_decoded)) throw Fail("missing argument");
+        check_lm_cfg(*cfg, n);
+        ensure_lm_staging();
+        HIPCHECK(hipStreamSynchronize(g.stream));  // the pinned block may feed an earlier copy
+        *lm_host_cfg() = lm_cfg_dev(*cfg, INT32_MAX);
+        LmState st{};
+        st.step = int32_t(step); st.n_dec = n_decoded; st.last = -1;
+        *lm_host_state(0) = st;
+        HIPCHECK(hipMemcpyAsync(g.lm_cfg_dev, lm_host_cfg(), sizeof(LmCfgDev), hipMemcpyHostToDevice, g.stream));
+        HIPCHECK(hipMemcpyAsync(g.lm_state_dev, lm_host_state(0), sizeof(LmState), hipMemcpyHostToDevice, g.stream));
+        HIPCHECK(launch_lm_sample(d_logits, n, g.lm_cfg_dev, g.lm_state_dev, const_cast<int32_t *>(d_decoded), d_logp, 0, false,
+                                  g.stream));
+        HIPCHECK(hipMemcpyAsync(lm_host_state(1), g.lm_state_dev, sizeof(LmState), hipMemcpyDeviceToHost, g.stream));
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        const LmState r = *lm_host_state(1);
+        if (r.status) throw Fail("CosyVoice: sampling reaches max_trials and still gets eos when ignore_eos is True");
+        *token = r.last;
+        return 1;
+    }, 0);
+}
+
+int voxhip_lm_generate(int xfmr, int seq, const float *x, int64_t n, int head, int speech_emb, const voxhip_lm_cfg *cfg,
+                       int32_t *tokens, float *logp, int32_t *n_tokens) {
+    return guard_int([&] {
+        require_ok();
+        Xfmr &X = xf_at(xfmr);
+        Seq &S = seq_at(seq);
+        check_seq_for(X, xfmr, S);
+        if (!x || !cfg || !n_tokens || n <= 0 || (cfg->max_len > 0 && !tokens)) throw Fail("missing argument");
+        const GpuMat &Hm = mat_at(head), &E = mat_at(speech_emb);
+        if (Hm.cols != X.H || E.cols != X.H) throw Fail("head / embedding width differs from the hidden size");
+        const int64_t V = Hm.rows;
+        check_lm_cfg(*cfg, V);
+        if (cfg->speech_tokens > E.rows) throw Fail("speech embedding has fewer rows than speech tokens");
+        if (n + int64_t(cfg->max_len) + 1 > S.cap) throw Fail("context exceeds GPU KV capacity (prompt + max_len + 1 positions)");
+        *n_tokens = 0;
+        // lm_begin: the prompt rows at positions 0..n-1
+        const int last = forward_rows(X, n, [&](int64_t i) { return row_of(S, i); }, x, -1, 0, X.layers, n, nullptr, nullptr,
+                                      -1, nullptr, false);
+        if (cfg->max_len == 0) return 1;
+        if (last) HIPCHECK(hipMemcpyAsync(X.h, X.h + size_t(last) * X.H, size_t(X.H) * 4, hipMemcpyDeviceToDevice, g.stream));
+        prepare_head(X, head, false);
+        lm_buffers(X, cfg->max_len, V, logp != nullptr);
+        ensure_lm_staging();
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        *lm_host_cfg() = lm_cfg_dev(*cfg, cfg->max_len);
+        LmState st{};
+        st.last = -1;
+        *lm_host_state(0) = st;
+        HIPCHECK(hipMemcpyAsync(X.lm_cfg, lm_host_cfg(), sizeof(LmCfgDev), hipMemcpyHostToDevice, g.stream));
+        HIPCHECK(hipMemcpyAsync(X.lm_state, lm_host_state(0), sizeof(LmState), hipMemcpyHostToDevice, g.stream));
+        set_rows(X, {row_of(S, n - 1)});  // the first step's embedding kernel advances it to position n
+        hipGraphExec_t exec = lm_graph(X, S, seq, head, speech_emb, logp != nullptr);
+        hipEvent_t ev[2] = {nullptr, nullptr};
+        auto cleanup = [&] {
+            for (hipEvent_t e : ev)
+                if (e) (void)hipEventDestroy(e);
+            X.rows_valid = false;  // the device advanced the row table
+        };
+        try {
+            HIPCHECK(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
+            HIPCHECK(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming));
+            // one graph ahead: while graph c runs, the host reads the state after graph c - 1
+            const int chunks = (cfg->max_len + kLmGraphSteps - 1) / kLmGraphSteps;
+            for (int c = 0; c < chunks; ++c) {
+                HIPCHECK(hipGraphLaunch(exec, g.stream));
+                HIPCHECK(hipMemcpyAsync(lm_host_state(1 + (c & 1)), X.lm_state, sizeof(LmState), hipMemcpyDeviceToHost, g.stream));
+                HIPCHECK(hipEventRecord(ev[c & 1], g.stream));
+                if (c >= 1) {
+                    HIPCHECK(hipEventSynchronize(ev[(c - 1) & 1]));
+                    if (lm_host_state(1 + ((c - 1) & 1))->done) break;
+                }
+            }
+            HIPCHECK(hipMemcpyAsync(lm_host_state(0), X.lm_state, sizeof(LmState), hipMemcpyDeviceToHost, g.stream));
+            HIPCHECK(hipStreamSynchronize(g.stream));
+            const LmState r = *lm_host_state(0);
+            if (r.status) throw Fail("CosyVoice: sampling reaches max_trials and still gets eos when ignore_eos is True");
+            if (r.n_dec > 0) HIPCHECK(hipMemcpy(tokens, X.lm_dec, size_t(r.n_dec) * 4, hipMemcpyDeviceToHost));
+            const int64_t rows = std::min<int64_t>(r.n_dec + (r.last >= cfg->speech_tokens ? 1 : 0), cfg->max_len);
+            if (logp && rows > 0) HIPCHECK(hipMemcpy(logp, X.lm_logp, size_t(rows * V) * 4, hipMemcpyDeviceToHost));
+            *n_tokens = r.n_dec;
+        } catch (...) {
+            cleanup();
+            throw;
+        }
+        cleanup();
         return 1;
     }, 0);
 }

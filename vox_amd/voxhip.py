@@ -63,6 +63,13 @@ class SampleCfg(C.Structure):
                 ("block_eos", C.c_int32)]
 
 
+class LmCfg(C.Structure):
+    """voxhip_lm_cfg: CosyVoice2 LM sampling (CosyCfg top_p / top_k / win_size / tau_r, lm_generate bounds)."""
+    _fields_ = [("top_p", C.c_float), ("top_k", C.c_int32), ("win_size", C.c_int32), ("tau_r", C.c_float),
+                ("speech_tokens", C.c_int32), ("min_len", C.c_int32), ("max_len", C.c_int32), ("piece", C.c_uint32),
+                ("seed", C.c_uint64)]
+
+
 KERNEL_CLASSES = ("qkv_gemv", "o_gemv", "gateup_gemv", "down_gemv", "head_gemv", "attention", "attn_combine", "qk_post", "sampler")
 
 
@@ -107,6 +114,8 @@ SIGNATURES = {
     "voxhip_sync": (_I, []),
     "voxhip_decode_dev": (_I, [_I, _I, _I64, _P, _I64, _P, _I, _P, C.POINTER(SampleCfg), _P]),
     "voxhip_decode_steps_dev": (_I, [_I, _P, _P, _I64, _P, _P, _I, _P, C.POINTER(SampleCfg), _P]),
+    "voxhip_lm_sample_dev": (_I, [_P, C.c_int32, C.POINTER(LmCfg), _I64, _P, C.c_int32, _P, _P]),
+    "voxhip_lm_generate": (_I, [_I, _I, _P, _I64, _I, _I, C.POINTER(LmCfg), _P, _P, _P]),
     "voxhip_mat_synthetic": (_I, [_I32, _I64, _I64, _U64, _U32, _F, _F, _I]),
     "voxhip_mat_download": (_I, [_I, _P, _P, _P]),
     "voxhip_mat_free": (_I, [_I]),
@@ -404,6 +413,34 @@ def decode_steps_dev(xfmr, seqs, pos, d_x, d_out=None, head=-1, d_logits=None, c
     _check(lib().voxhip_decode_steps_dev(xfmr, _p(sq), _p(ps), sq.size, d_x.ptr, None if d_out is None else d_out.ptr, head,
                                          None if d_logits is None else d_logits.ptr, carr,
                                          None if d_tokens is None else d_tokens.ptr), "decode_steps_dev")
+
+
+def lm_cfg(top_p=0.8, top_k=25, win_size=10, tau_r=0.1, speech_tokens=6561, min_len=0, max_len=256, piece=0, seed=1234):
+    return LmCfg(top_p, top_k, win_size, tau_r, speech_tokens, min_len, max_len, piece, seed)
+
+
+def lm_sample_dev(d_logits, n, cfg, step, d_decoded=None, n_decoded=0, d_logp=None):
+    """lm_logp + the RAS trial loop of one step on device logits [n]; returns the token."""
+    tok = C.c_int32()
+    _check(lib().voxhip_lm_sample_dev(d_logits.ptr, n, C.byref(cfg), step, None if d_decoded is None else d_decoded.ptr,
+                                      n_decoded, None if d_logp is None else d_logp.ptr, C.byref(tok)), "lm_sample_dev")
+    return tok.value
+
+
+def lm_generate(xfmr, seq, x, head, speech_emb, cfg, want_logp=False):
+    """lm_begin's prefill of x [n][hidden] + lm_generate on the device: (tokens, logp [steps][V] or None)."""
+    x = f32(x)
+    tokens = np.zeros(max(cfg.max_len, 1), np.int32)
+    V = mat_shape(head)[0]
+    logp = np.zeros((max(cfg.max_len, 1), V), np.float32) if want_logp else None
+    nt = C.c_int32()
+    _check(lib().voxhip_lm_generate(xfmr, seq, _p(x), x.shape[0], head, speech_emb, C.byref(cfg), _p(tokens),
+                                    None if logp is None else _p(logp), C.byref(nt)), "lm_generate")
+    n = nt.value
+    if logp is not None:
+        rows = min(n + 1, cfg.max_len)
+        logp = logp[:rows]
+    return tokens[:n], logp
 
 
 def sync():
