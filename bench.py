@@ -26,6 +26,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "talker decode tok/s (0.6B q8, batch 1); GEMV HBM GB/s as % of peak"
 HBM_PEAK_GBS = 8000.0
+F32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
 POS = 512
 
 
@@ -141,6 +142,48 @@ def bench_cfg3(vh, synth, steps, warmup):
     return out
 
 
+def bench_cfg5(vh, synth, reps=3):
+    """the CosyVoice2-0.5B-shaped LM on the device. Prefill: 512 prompt rows (q8 weights on the
+    f32-activation MFMA GEMM, as matmul's path above 8 rows). Generation: 256 steps of q8 int8 GEMVs, f32 head + bias,
+    log-softmax, the RAS sampler with lm_generate's trial loop (top-p 0.8, top-k 25, window 10, tau 0.1, Philox seed
+    1234) and the speech-token embedding, all device-resident (min_len = max_len = 256: exactly 256 steps).
+    Times are host wall-clock around the entry points (median of reps), prompt upload included."""
+    c = synth.COSY_LM_0_5B
+    P, S = c["prefill"], c["decode_steps"]
+    dec = synth.Decoder(c, seed=0, capacity=P + S + 8)
+    emb = vh.mat_synthetic(vh.F32, c["head_rows"], c["hidden"], 0, 0xE4B, 0.0, 0.02)
+    x = np.random.default_rng(5).standard_normal((P, c["hidden"])).astype(np.float32)
+    pre = vh.lm_cfg(speech_tokens=c["speech_tokens"], min_len=0, max_len=0, seed=1234)
+    gen = vh.lm_cfg(speech_tokens=c["speech_tokens"], min_len=S, max_len=S, seed=1234)
+
+    def timed(cfg):
+        vh.sync()
+        t0 = time.perf_counter()
+        toks, _ = vh.lm_generate(dec.xfmr, dec.seq, x, dec.head, emb, cfg)
+        return (time.perf_counter() - t0) * 1000.0, toks
+    timed(pre)
+    timed(gen)
+    t_pre = float(np.median([timed(pre)[0] for _ in range(reps)]))
+    runs = [timed(gen) for _ in range(reps)]
+    t_all = float(np.median([r[0] for r in runs]))
+    ntok = int(runs[0][1].size)
+    assert all(np.array_equal(r[1], runs[0][1]) for r in runs) and ntok == S
+    flops = dec.linear_flops(P) + dec.attention_flops(P)
+    dec_ms = t_all - t_pre
+    kv_avg = c["layers"] * 2 * (P + (S + 1) / 2) * c["kv_heads"] * c["head_dim"] * 2
+    step_bytes = dec.weight_bytes() + kv_avg
+    vh.mat_free(emb)
+    return {"workload": "cosyvoice2-0.5b LM q8: prefill 512 + 256 RAS-sampled steps (BASELINE configs[4])",
+            "prefill_ms": round(t_pre, 3), "prefill_gflop": round(flops / 1e9, 1),
+            "prefill_tflops": round(flops / (t_pre * 1e-3) / 1e12, 2),
+            "prefill_frac_f32_mfma": round(flops / (t_pre * 1e-3) / 1e12 / F32_MFMA_PEAK_TFLOPS, 4),
+            "decode_ms": round(dec_ms, 3), "decode_tok_s": round(S / (dec_ms * 1e-3), 1),
+            "decode_bytes_per_step": int(step_bytes),
+            "decode_GBps": round(step_bytes * S / (dec_ms * 1e-3) / 1e9, 1),
+            "decode_frac": round(step_bytes * S / (dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "total_ms": round(t_all, 3), "tokens": ntok}
+
+
 def load_traffic(kernel_class):
     p = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(p):
@@ -233,7 +276,8 @@ def main():
     other = None
     if not args.no_other:
         t0 = time.perf_counter()
-        other = {"configs[0]": bench_cfg1(vh), "configs[2]": bench_cfg3(vh, synth, 100, 10)}
+        other = {"configs[0]": bench_cfg1(vh), "configs[2]": bench_cfg3(vh, synth, 100, 10),
+                 "configs[4]": bench_cfg5(vh, synth)}
         log(f"other configs: {json.dumps(other)} ({time.perf_counter() - t0:.1f} s)")
 
     cpu = None

@@ -223,6 +223,35 @@ int voxhip_lm_sample_dev(const float *d_logits, int32_t n, const voxhip_lm_cfg *
 int voxhip_lm_generate(int xfmr, int seq, const float *x, int64_t n, int head, int speech_emb, const voxhip_lm_cfg *cfg,
                        int32_t *tokens, float *logp, int32_t *n_tokens);
 
+/* ---------------------------------------------------------------- F5-TTS DiT step (gpu.hpp:62-91)
+ * The whole dit_forward (f5.cpp:586-725) of a sampling step on the device. Vocos stays on the CPU
+ * (gpu_f5_vocos returns false, which f5.cpp:787-791 answers with the CPU vocoder). */
+/* GpuF5Conv (gpu.hpp:66): f32 weights in Conv1d::w layout [groups][cout/groups][K][cin/groups], bias [cout] or NULL.
+ * The position convolutions need cin = cout = dim, odd K and cin/groups a multiple of 4. */
+typedef struct voxhip_f5_conv {
+    const float *w, *b;
+    int32_t cin, cout, K, groups;
+} voxhip_f5_conv;
+/* GpuF5Desc::Block (gpu.hpp:70): matrix handles of one DiT block. q, k, v are stacked on the device at create. */
+typedef struct voxhip_f5_block {
+    int32_t ada, q, k, v, o, ff1, ff2;
+} voxhip_f5_block;
+/* GpuF5Desc (gpu.hpp:67-81) without its Vocos fields. dim_head must be 64. */
+typedef struct voxhip_f5_desc {
+    int32_t dim, depth, heads, dim_head, ff_mult, mel_dim, text_dim, pe_attn_head;
+    int32_t in_proj, norm_out, proj_out;
+    const voxhip_f5_block *blocks; /* [depth] */
+    voxhip_f5_conv pos1, pos2;
+} voxhip_f5_desc;
+int voxhip_f5_create(const voxhip_f5_desc *d);  /* gpu_f5_create (gpu.hpp:82): a handle or -1 */
+/* gpu_f5_begin (gpu.hpp:85): B sequences of N rows; cat0 [B][N][2 mel + text] (zeros in the x columns),
+ * rope [N][dim_head/2][2] (cos, sin). */
+int voxhip_f5_begin(int id, int B, int N, const float *cat0, const float *rope);
+/* gpu_f5_step (gpu.hpp:87): x [N][mel] (the same for every sequence), ts [dim] = SiLU(time embedding) ->
+ * out [B][N][mel]. */
+int voxhip_f5_step(int id, const float *x, const float *ts, float *out);
+int voxhip_f5_end(int id);  /* gpu_f5_end (gpu.hpp:90): frees the step buffers, keeps the weights */
+
 /* Synthetic weights and caches, generated on the device (Philox4x32-10 Box-Muller, mean + std * z).
  * voxhip_mat_synthetic: f32 values, then quantized on the device to `type` with the reference's
  * quantizer (Q8: kernels.cpp:918-929; Q4: kernels.cpp:606-645; F16/BF16: nearest even). Returns a handle.

@@ -38,6 +38,22 @@ class VoKV(C.Structure):
                 ("kv_f16", C.c_int32), ("avx2", C.c_int32)]
 
 
+class VoConv(C.Structure):
+    _fields_ = [("w", C.c_void_p), ("b", C.c_void_p), ("cin", C.c_int32), ("cout", C.c_int32), ("K", C.c_int32),
+                ("groups", C.c_int32)]
+
+
+class VoF5Block(C.Structure):
+    _fields_ = [(n, VoMat) for n in ("ada", "q", "k", "v", "o", "ff1", "ff2")]
+
+
+class VoF5(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("dim", "depth", "heads", "dim_head", "ff_mult", "mel_dim", "text_dim",
+                                         "pe_attn_head")] + \
+               [(n, VoMat) for n in ("in_proj", "norm_out", "proj_out")] + \
+               [("blocks", C.POINTER(VoF5Block)), ("pos1", VoConv), ("pos2", VoConv)]
+
+
 def _p(a):
     return None if a is None else a.ctypes.data
 
@@ -64,6 +80,11 @@ def _declare(lib, prefix):
             "softmax": (None, [P, I64]),
             "ras_sample": (I32, [P, I32, P, I32, F, I32, I32, F, F, F]),
             "lm_logp": (None, [P, I32]),
+            "gelu_tanh": (F, [F]),
+            "mish": (F, [F]),
+            "conv1d": (None, [P, P, I32, P]),
+            "f5_modulate": (None, [P, I64, I32, P, P, P]),
+            "f5_step": (C.c_int, [P, I32, I32, P, P, P, P]),
             "lm_step": (I32, [P, I32, P, I32, I64, I32, I32, F, I32, I32, F, U64, U32]),
             "noise": (None, [U64, U32, C.c_size_t, P]),
             "f16_to_f32": (F, [C.c_uint16]),
@@ -82,6 +103,7 @@ def _declare(lib, prefix):
         sig.update({
             "softmax": (None, [P, I64]),
             "mat_gather": (None, [P, I64, P]),
+            "conv1d": (None, [P, I32, I32, I32, I32, P, P, I32, P]),
             "matmul": (None, [P, P, I64, P]),
             "set_threads": (None, [C.c_int]),
             "session_new": (P, [P, P, P]),
@@ -196,6 +218,69 @@ def lm_step(logp, decoded, step, min_len, speech_tokens, top_p=0.8, top_k=25, wi
     tok = lib().vo_lm_step(_p(l), l.size, _p(d) if d.size else None, d.size, step, min_len, speech_tokens, top_p, top_k,
                            win_size, tau_r, seed, piece)
     return tok, l
+
+
+class Conv:
+    """A Conv1d in Conv1d::w layout [groups][cout/groups][K][cin/groups] (GpuF5Conv), with its ctypes view."""
+
+    def __init__(self, w, b, cin, cout, K, groups):
+        self.w = np.ascontiguousarray(w, np.float32)
+        self.b = None if b is None else np.ascontiguousarray(b, np.float32)
+        self.cin, self.cout, self.K, self.groups = cin, cout, K, groups
+        self.c = VoConv(_p(self.w), _p(self.b), cin, cout, K, groups)
+
+    @staticmethod
+    def from_torch(w_pt, b, groups):
+        """From PyTorch Conv1d.weight [cout][cin/groups][K] (the conversion of Conv1d::load, f5_ops.cpp:86-104)."""
+        cout, cig, K = w_pt.shape
+        cog = cout // groups
+        if groups == cig * groups and cout == groups and cig == 1:  # depthwise: [C][K]
+            return Conv(w_pt.reshape(cout, K), b, groups, cout, K, groups)
+        w = w_pt.reshape(groups, cog, cig, K).transpose(0, 1, 3, 2)  # [g][o][k][i]
+        return Conv(w, b, cig * groups, cout, K, groups)
+
+
+def conv1d(cv, x, use_ref=False, w_pt=None):
+    x = np.ascontiguousarray(x, np.float32)
+    T = x.shape[0]
+    y = np.empty((T, cv.cout), np.float32)
+    if use_ref:
+        ref().ref_conv1d(_p(np.ascontiguousarray(w_pt, np.float32)), cv.cin, cv.cout, cv.K, cv.groups, _p(cv.b), _p(x), T, _p(y))
+    else:
+        lib().vo_conv1d(C.byref(cv.c), _p(x), T, _p(y))
+    return y
+
+
+def f5_modulate(x, scale, shift):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().vo_f5_modulate(_p(x), x.shape[0], x.shape[1], _p(np.ascontiguousarray(scale, np.float32)),
+                         _p(np.ascontiguousarray(shift, np.float32)), _p(y))
+    return y
+
+
+class F5:
+    """An F5-TTS DiT in the oracle's struct layout: blocks = list of dicts ada,q,k,v,o,ff1,ff2 -> Mat."""
+
+    def __init__(self, dim, depth, heads, dim_head, ff_mult, mel_dim, text_dim, pe_attn_head, in_proj, norm_out, proj_out,
+                 blocks, pos1, pos2):
+        self.keep = (in_proj, norm_out, proj_out, blocks, pos1, pos2)
+        arr = (VoF5Block * len(blocks))()
+        for i, b in enumerate(blocks):
+            for n in ("ada", "q", "k", "v", "o", "ff1", "ff2"):
+                setattr(arr[i], n, b[n].c)
+        self._arr = arr
+        self.c = VoF5(dim, depth, heads, dim_head, ff_mult, mel_dim, text_dim, pe_attn_head, in_proj.c, norm_out.c,
+                      proj_out.c, arr, pos1.c, pos2.c)
+        self.mel_dim = mel_dim
+
+
+def f5_step(m, B, N, cat, ts, rope):
+    cat = np.ascontiguousarray(cat, np.float32)
+    out = np.empty((B * N, m.mel_dim), np.float32)
+    lib().vo_f5_step(C.byref(m.c), B, N, _p(cat), _p(np.ascontiguousarray(ts, np.float32)),
+                     _p(np.ascontiguousarray(rope, np.float32)), _p(out))
+    return out
 
 
 def uniform(seed, frame, cb, draw=0):

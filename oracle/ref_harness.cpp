@@ -1,7 +1,7 @@
 // ref_harness.cpp — extern "C" wrappers around the reference's own CPU functions.
 //
 // TEST INFRASTRUCTURE ONLY. oracle/Makefile compiles this file together with
-// /root/reference/src/kernels.cpp and /root/reference/src/gpu_stub.cpp, where
+// /root/reference/src/kernels.cpp, f5_ops.cpp and gpu_stub.cpp, where
 // they lie, into oracle/_ref/libvoxref.so. tests/ use it to pin the C
 // restatement (vox_oracle.c) bit for bit and to write the golden fixtures;
 // bench.py may time it as the "reference" CPU baseline. Nothing here is part
@@ -9,6 +9,7 @@
 #include <cstring>
 #include <vector>
 
+#include "f5_ops.hpp"    // /root/reference/src (Conv1d)
 #include "kernels.hpp"   // /root/reference/src
 #include "sampling.hpp"  // /root/reference/src
 #include "vox_oracle.h"  // struct layouts shared with the restatement
@@ -65,6 +66,12 @@ void store_kv(const KVCache &kv, vo_kv &dst, int layers, int64_t kd) {
 }  // namespace
 
 extern "C" {
+// Conv1d::load + forward (f5_ops.cpp:86-147) on PyTorch-layout weights w [cout][cin/groups][K].
+void ref_conv1d(const float *w, int cin, int cout, int K, int groups, const float *bias, const float *x, int T, float *y) {
+    Conv1d c;
+    c.load(w, cin, cout, K, groups, bias);
+    c.forward(x, T, y);
+}
 void ref_set_threads(int n) { set_num_threads(n); }
 void ref_philox(const uint32_t c[4], const uint32_t k[2], uint32_t out[4]) {
     auto r = Philox4x32::block({c[0], c[1], c[2], c[3]}, {k[0], k[1]});

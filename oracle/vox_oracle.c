@@ -711,3 +711,148 @@ int vo_transformer_forward_steps(const vo_xfmr *w, vo_kv *const *kvs, int64_t B,
     free(h); free(xn); free(q); free(k); free(v); free(ao); free(o); free(g); free(u); free(d); free(sc);
     return 0;
 }
+
+/* ------------------------------------------------------------------ F5-TTS DiT (f5.cpp, f5_ops.cpp) */
+float vo_gelu_tanh(float x) { /* f5.cpp:93-96 */
+    const float k = 0.7978845608028654f;
+    return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
+}
+float vo_mish(float x) { /* f5.cpp:97-100 */
+    const float sp = x > 20.f ? x : log1pf(expf(x));
+    return x * tanhf(sp);
+}
+
+/* Conv1d::forward (f5_ops.cpp:106-147): depthwise directly, else per group im2col [T][K * cig] and the F32 matmul */
+void vo_conv1d(const vo_conv *c, const float *x, int32_t T, float *y) {
+    const int pad = c->K / 2;
+    if (c->groups == c->cin && c->cin == c->cout) { /* depthwise: w [C][K] */
+        for (int64_t t = 0; t < T; ++t)
+            for (int ch = 0; ch < c->cin; ++ch) {
+                float acc = c->b ? c->b[ch] : 0.f;
+                const float *wc = c->w + (int64_t)ch * c->K;
+                for (int k = 0; k < c->K; ++k) {
+                    const int64_t tt = t + k - pad;
+                    if (tt >= 0 && tt < T) acc += wc[k] * x[tt * c->cin + ch];
+                }
+                y[t * c->cout + ch] = acc;
+            }
+        return;
+    }
+    const int cig = c->cin / c->groups, cog = c->cout / c->groups;
+    const int64_t kc = (int64_t)c->K * cig;
+    float *col = (float *)malloc(sizeof(float) * (size_t)(T * kc));
+    float *yg = (float *)malloc(sizeof(float) * (size_t)T * (size_t)cog);
+    for (int g = 0; g < c->groups; ++g) {
+        for (int64_t t = 0; t < T; ++t)
+            for (int k = 0; k < c->K; ++k) {
+                const int64_t tt = t + k - pad;
+                float *dst = col + t * kc + (int64_t)k * cig;
+                if (tt >= 0 && tt < T) memcpy(dst, x + tt * c->cin + (int64_t)g * cig, sizeof(float) * (size_t)cig);
+                else memset(dst, 0, sizeof(float) * (size_t)cig);
+            }
+        vo_mat W = {VO_F32, c->w + (int64_t)g * cog * kc, NULL, cog, kc, NULL};
+        vo_matmul(&W, col, T, yg, 1);
+        for (int64_t t = 0; t < T; ++t)
+            for (int o = 0; o < cog; ++o)
+                y[t * c->cout + (int64_t)g * cog + o] = yg[t * cog + o] + (c->b ? c->b[g * cog + o] : 0.f);
+    }
+    free(col);
+    free(yg);
+}
+
+void vo_f5_modulate(const float *x, int64_t R, int32_t D, const float *sc, const float *sh, float *y) {
+    for (int64_t r = 0; r < R; ++r) {
+        const float *xr = x + r * D;
+        double mean = 0;
+        for (int i = 0; i < D; ++i) mean += xr[i];
+        mean /= D;
+        double var = 0;
+        for (int i = 0; i < D; ++i) { const double dd = xr[i] - mean; var += dd * dd; }
+        var /= D;
+        const float inv = (float)(1.0 / sqrt(var + 1e-6));
+        float *yr = y + r * D;
+        for (int i = 0; i < D; ++i) yr[i] = (xr[i] - (float)mean) * inv * (1.0f + sc[i]) + sh[i];
+    }
+}
+
+int vo_f5_step(const vo_f5 *m, int32_t B, int32_t N, const float *cat, const float *ts, const float *rope, float *out) {
+    const int D = m->dim, H = m->heads, HD = m->dim_head, INNER = H * HD, HH = HD / 2, FF = D * m->ff_mult;
+    const int64_t R = (int64_t)B * N;
+    float *h = (float *)malloc(sizeof(float) * (size_t)(R * D));
+    float *a = (float *)malloc(sizeof(float) * (size_t)N * D), *b2 = (float *)malloc(sizeof(float) * (size_t)N * D);
+    float *ada = (float *)malloc(sizeof(float) * 6 * (size_t)D), *nrm = (float *)malloc(sizeof(float) * (size_t)(R * D));
+    float *q = (float *)malloc(sizeof(float) * (size_t)(R * INNER)), *k = (float *)malloc(sizeof(float) * (size_t)(R * INNER));
+    float *v = (float *)malloc(sizeof(float) * (size_t)(R * INNER)), *at = (float *)malloc(sizeof(float) * (size_t)(R * INNER));
+    float *o = (float *)malloc(sizeof(float) * (size_t)(R * D)), *ff = (float *)malloc(sizeof(float) * (size_t)(R * FF));
+    float *qh = (float *)malloc(sizeof(float) * (size_t)N * HD), *kh = (float *)malloc(sizeof(float) * (size_t)N * HD);
+    float *vt = (float *)malloc(sizeof(float) * (size_t)N * HD), *oh = (float *)malloc(sizeof(float) * (size_t)N * HD);
+    float *sc = (float *)malloc(sizeof(float) * (size_t)N * N), *fin = (float *)malloc(sizeof(float) * 2 * (size_t)D);
+    vo_matmul(&m->in_proj, cat, R, h, 1);
+    for (int s = 0; s < B; ++s) { /* convolutional position embedding (f5.cpp:589-598) */
+        float *hs = h + (int64_t)s * N * D;
+        vo_conv1d(&m->pos1, hs, N, a);
+        for (int64_t i = 0; i < (int64_t)N * D; ++i) a[i] = vo_mish(a[i]);
+        vo_conv1d(&m->pos2, a, N, b2);
+        for (int64_t i = 0; i < (int64_t)N * D; ++i) hs[i] += vo_mish(b2[i]);
+    }
+    const float scale = 1.0f / sqrtf((float)HD);
+    for (int bi = 0; bi < m->depth; ++bi) {
+        const vo_f5_block *L = &m->blocks[bi];
+        vo_matmul(&L->ada, ts, 1, ada, 1);
+        const float *shift_msa = ada, *scale_msa = ada + D, *gate_msa = ada + 2 * D;
+        const float *shift_mlp = ada + 3 * D, *scale_mlp = ada + 4 * D, *gate_mlp = ada + 5 * D;
+        vo_f5_modulate(h, R, D, scale_msa, shift_msa, nrm);
+        vo_matmul(&L->q, nrm, R, q, 1);
+        vo_matmul(&L->k, nrm, R, k, 1);
+        vo_matmul(&L->v, nrm, R, v, 1);
+        for (int64_t r = 0; r < R; ++r) /* RoPE on pairs (2j, 2j+1) (f5.cpp:653-668) */
+            for (int hh = 0; hh < H; ++hh) {
+                if (m->pe_attn_head > 0 && hh >= m->pe_attn_head) continue;
+                const int pos = (int)(r % N);
+                float *bufs[2] = {q + r * INNER + (int64_t)hh * HD, k + r * INNER + (int64_t)hh * HD};
+                for (int u = 0; u < 2; ++u)
+                    for (int j = 0; j < HH; ++j) {
+                        const float c = rope[((int64_t)pos * HH + j) * 2], sn = rope[((int64_t)pos * HH + j) * 2 + 1];
+                        const float x0 = bufs[u][2 * j], x1 = bufs[u][2 * j + 1];
+                        bufs[u][2 * j] = x0 * c - x1 * sn;
+                        bufs[u][2 * j + 1] = x1 * c + x0 * sn;
+                    }
+            }
+        for (int s = 0; s < B; ++s) /* attention per head (f5.cpp:626-650) */
+            for (int hh = 0; hh < H; ++hh) {
+                const int64_t base = (int64_t)s * N * INNER + (int64_t)hh * HD;
+                for (int64_t i = 0; i < N; ++i) {
+                    memcpy(qh + i * HD, q + base + i * INNER, sizeof(float) * (size_t)HD);
+                    memcpy(kh + i * HD, k + base + i * INNER, sizeof(float) * (size_t)HD);
+                    for (int d = 0; d < HD; ++d) vt[(int64_t)d * N + i] = v[base + i * INNER + d];
+                }
+                vo_mat km = {VO_F32, kh, NULL, N, HD, NULL};
+                vo_matmul(&km, qh, N, sc, 1);
+                for (int64_t i = 0; i < N; ++i) {
+                    float *row = sc + i * N, mx = -INFINITY, sum = 0;
+                    for (int j = 0; j < N; ++j) { row[j] *= scale; mx = mx < row[j] ? row[j] : mx; }
+                    for (int j = 0; j < N; ++j) { row[j] = expf(row[j] - mx); sum += row[j]; }
+                    const float inv = 1.0f / sum;
+                    for (int j = 0; j < N; ++j) row[j] *= inv;
+                }
+                vo_mat vm = {VO_F32, vt, NULL, HD, N, NULL};
+                vo_matmul(&vm, sc, N, oh, 1);
+                for (int64_t i = 0; i < N; ++i) memcpy(at + base + i * INNER, oh + i * HD, sizeof(float) * (size_t)HD);
+            }
+        vo_matmul(&L->o, at, R, o, 1);
+        for (int64_t r = 0; r < R; ++r)
+            for (int i = 0; i < D; ++i) h[r * D + i] += gate_msa[i] * o[r * D + i];
+        vo_f5_modulate(h, R, D, scale_mlp, shift_mlp, nrm);
+        vo_matmul(&L->ff1, nrm, R, ff, 1);
+        for (int64_t i = 0; i < R * FF; ++i) ff[i] = vo_gelu_tanh(ff[i]);
+        vo_matmul(&L->ff2, ff, R, o, 1);
+        for (int64_t r = 0; r < R; ++r)
+            for (int i = 0; i < D; ++i) h[r * D + i] += gate_mlp[i] * o[r * D + i];
+    }
+    vo_matmul(&m->norm_out, ts, 1, fin, 1); /* final modulation: (scale, shift) */
+    vo_f5_modulate(h, R, D, fin, fin + D, nrm);
+    vo_matmul(&m->proj_out, nrm, R, out, 1);
+    free(h); free(a); free(b2); free(ada); free(nrm); free(q); free(k); free(v); free(at); free(o); free(ff);
+    free(qh); free(kh); free(vt); free(oh); free(sc); free(fin);
+    return 0;
+}

@@ -129,6 +129,32 @@ int vo_transformer_layers(const vo_xfmr *w, vo_kv *kv, const float *x, int64_t m
 /* transformer_forward_steps (kernels.cpp:846-906): one token for each of B sequences. */
 int vo_transformer_forward_steps(const vo_xfmr *w, vo_kv *const *kvs, int64_t B, const float *x, float *out);
 
+/* ---- F5-TTS DiT step (f5.cpp:86-106, :563-725; f5_ops.cpp:86-147) ---- */
+float vo_gelu_tanh(float x); /* f5.cpp:93-96 */
+float vo_mish(float x);      /* f5.cpp:97-100 */
+/* Conv1d with "same" zero padding (odd K) and groups (f5_ops.cpp:106-147). w in Conv1d::w layout
+ * [groups][cout/groups][K][cin/groups] (= GpuF5Conv, gpu.hpp:65), bias [cout] or NULL; x [T][cin] -> y [T][cout]. */
+typedef struct {
+    const float *w, *b;
+    int32_t cin, cout, K, groups;
+} vo_conv;
+void vo_conv1d(const vo_conv *c, const float *x, int32_t T, float *y);
+/* LayerNorm without parameters + modulation (f5.cpp:608-625): double mean / variance, eps 1e-6,
+ * y = (x - float(mean)) * float(1 / sqrt(var + eps)) * (1 + scale) + shift, per row of D. */
+void vo_f5_modulate(const float *x, int64_t R, int32_t D, const float *scale, const float *shift, float *y);
+typedef struct {
+    vo_mat ada, q, k, v, o, ff1, ff2;
+} vo_f5_block;
+typedef struct {
+    int32_t dim, depth, heads, dim_head, ff_mult, mel_dim, text_dim, pe_attn_head;
+    vo_mat in_proj, norm_out, proj_out;
+    const vo_f5_block *blocks;
+    vo_conv pos1, pos2;
+} vo_f5;
+/* dit_forward from the input projection on (f5.cpp:586-725), B batches of N rows: cat [B*N][2 mel + text] (x, cond,
+ * text), ts [dim] (SiLU of the time embedding), rope [N][dim_head/2][2] (cos, sin) -> out [B*N][mel]. */
+int vo_f5_step(const vo_f5 *m, int32_t B, int32_t N, const float *cat, const float *ts, const float *rope, float *out);
+
 /* Thread count for the row-parallel loops (matmul); 1 = scalar single-thread. Results do not depend on it. */
 void vo_set_threads(int n);
 int vo_get_threads(void);

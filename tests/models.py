@@ -75,3 +75,66 @@ class Model:
 
     def oracle_kv(self, cap, kv_f16=1):
         return po.KV(self.n_layers, cap, self.kv_heads * self.head_dim, kv_f16=kv_f16)
+
+
+def f5_rope(N, hd):
+    """The rope table of gpu_f5_begin: [N][hd/2][2] (cos, sin) at angle i * theta^(-2j/hd), theta 10000 (f5.cpp:528-539)."""
+    HH = hd // 2
+    inv = np.array([np.float32(1.0 / 10000.0 ** (2 * j / hd)) for j in range(HH)], np.float32)
+    a = (np.arange(N, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
+    return np.stack([np.cos(a), np.sin(a)], axis=-1).astype(np.float32)
+
+
+class F5Model:
+    """A random F5-TTS DiT in both descriptions: `ox` for the oracle, `hip` (create kwargs with host matrices) for the
+    backend. Linear weights of type wtype (~N(0, std)) with biases; position convolutions f32 in Conv1d::w layout."""
+
+    def __init__(self, seed, dim, depth, heads, dim_head=64, ff_mult=2, mel=20, text=32, K=7, groups=4, pe_attn_head=0,
+                 wtype=F16, std=0.05):
+        rng = np.random.default_rng(seed)
+        self.dim, self.depth, self.heads, self.hd, self.mel, self.text = dim, depth, heads, dim_head, mel, text
+        self.ff_mult, self.pe = ff_mult, pe_attn_head
+        inner, ff, W = heads * dim_head, dim * ff_mult, 2 * mel + text
+
+        def mat(rows, cols, s=std):
+            d, sc, b = make_mat(rng, wtype, rows, cols, std=s, bias=True)
+            return (wtype, d, rows, cols, sc, b)
+        self.mats = {"in_proj": mat(dim, W), "norm_out": mat(2 * dim, dim), "proj_out": mat(mel, dim)}
+        self.blocks = []
+        for _ in range(depth):
+            self.blocks.append({"ada": mat(6 * dim, dim), "q": mat(inner, dim), "k": mat(inner, dim), "v": mat(inner, dim),
+                                "o": mat(dim, inner), "ff1": mat(ff, dim), "ff2": mat(dim, ff)})
+        cig = dim // groups
+
+        def conv():
+            w = (rng.standard_normal((groups, dim // groups, K, cig)) * 0.05).astype(np.float32)
+            b = (rng.standard_normal(dim) * 0.05).astype(np.float32)
+            return (w, b, dim, dim, K, groups)
+        self.pos = [conv(), conv()]
+        om = {k: po.Mat(*v) for k, v in self.mats.items()}
+        ob = [{k: po.Mat(*v) for k, v in b.items()} for b in self.blocks]
+        oc = [po.Conv(*c) for c in self.pos]
+        self.ox = po.F5(dim, depth, heads, dim_head, ff_mult, mel, text, pe_attn_head, om["in_proj"], om["norm_out"],
+                        om["proj_out"], ob, oc[0], oc[1])
+
+    def create(self, hip):
+        h = {k: hip.upload(hip.HostMat(*v)) for k, v in self.mats.items()}
+        hb = [{k: hip.upload(hip.HostMat(*v)) for k, v in b.items()} for b in self.blocks]
+        return hip.f5_create(self.dim, self.depth, self.heads, self.hd, self.ff_mult, self.mel, self.text, self.pe,
+                             h["in_proj"], h["norm_out"], h["proj_out"], hb, self.pos[0], self.pos[1])
+
+    def inputs(self, rng, B, N):
+        """cat0 [B N][2 mel + text] with zeros in the x columns, x [N][mel], ts [dim], rope."""
+        cat0 = rng.standard_normal((B * N, 2 * self.mel + self.text)).astype(np.float32)
+        cat0[:, :self.mel] = 0.0
+        x = rng.standard_normal((N, self.mel)).astype(np.float32)
+        ts = rng.standard_normal(self.dim).astype(np.float32)
+        return cat0, x, ts, f5_rope(N, self.hd)
+
+    @staticmethod
+    def with_x(cat0, x, B):
+        cat = cat0.copy()
+        N = x.shape[0]
+        for b in range(B):
+            cat[b * N:(b + 1) * N, :x.shape[1]] = x
+        return cat

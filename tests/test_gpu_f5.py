@@ -1,0 +1,53 @@
+"""F5-TTS DiT step on the device (gpu_f5_create / begin / step / end, f5.cpp:586-725) against the oracle's vo_f5_step.
+
+Both sides consume the same stored f16 / bf16 / f32 weights and f32 position convolutions; the device runs the
+linears and the convolutions on the f32 MFMA GEMM and attention on f32 MFMA tiles with an online softmax, so the
+outputs differ only by summation order and libm ulps: the north star's 1e-3 for f32 activations with the `vox verify`
+metric.
+"""
+import numpy as np
+import pytest
+
+from conftest import rel_err
+from models import F5Model, F16, BF16, F32
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def run(hip, oracle, m, B, N, seed, steps=1):
+    f5 = m.create(hip)
+    rng = np.random.default_rng(seed)
+    cat0, x, ts, rope = m.inputs(rng, B, N)
+    hip.f5_begin(f5, B, N, cat0, rope)
+    for _ in range(steps):
+        got = hip.f5_step(f5, x, ts, B, N, m.mel)
+        want = oracle.f5_step(m.ox, B, N, m.with_x(cat0, x, B), ts, rope)
+        assert rel_err(got, want) < TOL, rel_err(got, want)
+        x = rng.standard_normal(x.shape).astype(np.float32)  # the next Euler step's x; cat0 stays
+        ts = rng.standard_normal(ts.shape).astype(np.float32)
+    hip.f5_end(f5)
+    return f5
+
+
+@pytest.mark.parametrize("wtype,pe,B,N", [(F16, 0, 2, 70), (F16, 1, 1, 130), (BF16, 0, 2, 64), (F32, 2, 2, 33)])
+def test_f5_step_small(hip, oracle, wtype, pe, B, N):
+    m = F5Model(40 + wtype + pe, 128, 2, 4, mel=20, text=32, K=7, groups=4, pe_attn_head=pe, wtype=wtype)
+    run(hip, oracle, m, B, N, seed=N, steps=2)
+
+
+def test_f5_step_full_width(hip, oracle):
+    # the configs[3] widths (dim 1024, 16 x 64 heads, FFN 2048, mel 100, text 512, position conv K 31 / 16 groups)
+    # with one block and 200 frames, so the oracle finishes in seconds
+    m = F5Model(50, 1024, 1, 16, mel=100, text=512, K=31, groups=16, wtype=F16, std=0.02)
+    run(hip, oracle, m, 2, 200, seed=3)
+
+
+def test_f5_rejects_bad_shapes(hip):
+    m = F5Model(60, 128, 1, 2, dim_head=32, wtype=F16)
+    with pytest.raises(hip.VoxHipError, match="head_dim"):
+        m.create(hip)
+    m = F5Model(61, 128, 1, 2, wtype=F16)
+    f5 = m.create(hip)
+    with pytest.raises(hip.VoxHipError, match="before begin"):
+        hip.f5_step(f5, np.zeros((10, 20), np.float32), np.zeros(128, np.float32), 1, 10, 20)

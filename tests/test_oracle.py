@@ -213,6 +213,128 @@ def test_lm_step_trial_loop(oracle):
     assert tok != rep and tok < speech
 
 
+def test_f5_activations_closed_form(oracle):
+    # f5.cpp:93-100 against float64 formulas
+    xs = np.concatenate([np.linspace(-12, 25, 2001), [-0.0, 1e-8, 19.999, 20.0, 20.001]]).astype(np.float32)
+    x64 = xs.astype(np.float64)
+    gel = 0.5 * x64 * (1 + np.tanh(np.sqrt(2 / np.pi) * (x64 + 0.044715 * x64 ** 3)))
+    mis = x64 * np.tanh(np.where(x64 > 20, x64, np.log1p(np.exp(x64))))
+    g = np.array([po.lib().vo_gelu_tanh(float(v)) for v in xs])
+    mm = np.array([po.lib().vo_mish(float(v)) for v in xs])
+    assert np.max(np.abs(g - gel) / np.maximum(1, np.abs(gel))) < 2e-6
+    assert np.max(np.abs(mm - mis) / np.maximum(1, np.abs(mis))) < 2e-6
+
+
+def test_conv1d_matches_reference_and_brute_force(oracle):
+    # Conv1d (f5_ops.cpp:86-147): grouped "same" convolution; bit-exact against the compiled reference, and a float64
+    # brute force of y[t][o] = b[o] + sum_{k,i} w[o][i][k] x[t + k - K/2][g cig + i]
+    rng = np.random.default_rng(21)
+    for cin, K, groups, T in ((64, 31, 16, 45), (48, 7, 4, 9), (32, 5, 32, 20), (16, 3, 1, 2)):
+        w = (rng.standard_normal((cin, cin // groups, K)) * 0.1).astype(np.float32)
+        b = (rng.standard_normal(cin) * 0.1).astype(np.float32)
+        x = rng.standard_normal((T, cin)).astype(np.float32)
+        cv = po.Conv.from_torch(w, b, groups)
+        y = po.conv1d(cv, x)
+        if po.ref() is not None:
+            assert np.array_equal(y, po.conv1d(cv, x, use_ref=True, w_pt=w))
+        cig, cog, pad = cin // groups, cin // groups, K // 2
+        xp = np.zeros((T + 2 * pad, cin))
+        xp[pad:pad + T] = x
+        want = np.tile(b.astype(np.float64), (T, 1))
+        for o in range(cin):
+            g = o // cog
+            for k in range(K):
+                want[:, o] += xp[k:k + T, g * cig:(g + 1) * cig] @ w[o, :, k].astype(np.float64)
+        assert np.max(np.abs(y - want)) < 1e-5
+
+
+def test_f5_modulate_closed_form(oracle):
+    # f5.cpp:608-625: LayerNorm without parameters (double statistics, eps 1e-6) then x * (1 + scale) + shift
+    rng = np.random.default_rng(22)
+    x = (rng.standard_normal((7, 96)) * 3 + 1).astype(np.float32)
+    sc, sh = rng.standard_normal(96).astype(np.float32), rng.standard_normal(96).astype(np.float32)
+    y = po.f5_modulate(x, sc, sh)
+    x64 = x.astype(np.float64)
+    want = (x64 - x64.mean(1, keepdims=True)) / np.sqrt(x64.var(1, keepdims=True) + 1e-6) * (1 + sc) + sh
+    assert np.max(np.abs(y - want)) < 1e-5
+
+
+def f5_numpy(m, B, N, cat, ts, rope):
+    """dit_forward in float64 numpy, written from the model's equations (F5-TTS DiT), for pinning vo_f5_step."""
+    D, H, HD, mel = m.dim, m.heads, m.hd, m.mel
+    INNER, HH = H * HD, HD // 2
+
+    def lin(name_or_tuple, x):
+        t, d, r, c, s, b = name_or_tuple
+        w = po.Mat(t, d, r, c, s, b)
+        W = np.stack([po.mat_row(w, i) for i in range(r)]).astype(np.float64)
+        return x @ W.T + (b.astype(np.float64) if b is not None else 0)
+
+    def conv(c, x):
+        w, b, cin, cout, K, groups = c
+        cig, pad = cin // groups, K // 2
+        xp = np.zeros((x.shape[0] + 2 * pad, cin))
+        xp[pad:pad + x.shape[0]] = x
+        y = np.tile(b.astype(np.float64), (x.shape[0], 1))
+        for g in range(groups):
+            for k in range(K):
+                y[:, g * cig:(g + 1) * cig] += xp[k:k + x.shape[0], g * cig:(g + 1) * cig] @ w[g, :, k, :].T.astype(np.float64)
+        return y
+
+    def mish(v):
+        return v * np.tanh(np.where(v > 20, v, np.log1p(np.exp(np.minimum(v, 20)))))
+
+    def modulate(x, sc, sh):
+        return (x - x.mean(1, keepdims=True)) / np.sqrt(x.var(1, keepdims=True) + 1e-6) * (1 + sc) + sh
+
+    ts = ts.astype(np.float64)
+    h = lin(m.mats["in_proj"], cat.astype(np.float64))
+    for s in range(B):
+        hs = h[s * N:(s + 1) * N]
+        hs += mish(conv(m.pos[1], mish(conv(m.pos[0], hs))))
+    cos, sin = rope[..., 0].astype(np.float64), rope[..., 1].astype(np.float64)
+    for blk in m.blocks:
+        ada = lin(blk["ada"], ts[None])[0]
+        sh1, sc1, g1, sh2, sc2, g2 = (ada[i * D:(i + 1) * D] for i in range(6))
+        nrm = modulate(h, sc1, sh1)
+        q, k, v = lin(blk["q"], nrm), lin(blk["k"], nrm), lin(blk["v"], nrm)
+        for t in (q, k):
+            for hh in range(H):
+                if m.pe > 0 and hh >= m.pe:
+                    continue
+                pos = np.arange(B * N) % N
+                x0 = t[:, hh * HD:(hh + 1) * HD:2].copy()
+                x1 = t[:, hh * HD + 1:(hh + 1) * HD:2].copy()
+                t[:, hh * HD:(hh + 1) * HD:2] = x0 * cos[pos] - x1 * sin[pos]
+                t[:, hh * HD + 1:(hh + 1) * HD:2] = x1 * cos[pos] + x0 * sin[pos]
+        at = np.zeros((B * N, INNER))
+        for s in range(B):
+            for hh in range(H):
+                rows, cols = slice(s * N, (s + 1) * N), slice(hh * HD, (hh + 1) * HD)
+                sc = q[rows, cols] @ k[rows, cols].T / np.sqrt(HD)
+                p = np.exp(sc - sc.max(1, keepdims=True))
+                at[rows, cols] = (p / p.sum(1, keepdims=True)) @ v[rows, cols]
+        h = h + g1 * lin(blk["o"], at)
+        f = lin(blk["ff1"], modulate(h, sc2, sh2))
+        f = 0.5 * f * (1 + np.tanh(np.sqrt(2 / np.pi) * (f + 0.044715 * f ** 3)))
+        h = h + g2 * lin(blk["ff2"], f)
+    fin = lin(m.mats["norm_out"], ts[None])[0]
+    return lin(m.mats["proj_out"], modulate(h, fin[:D], fin[D:]))
+
+
+@pytest.mark.parametrize("pe", [0, 1])
+def test_f5_step_against_numpy(oracle, pe):
+    import models
+    m = models.F5Model(30 + pe, 64, 2, 2, dim_head=16, mel=12, text=8, K=5, groups=4, pe_attn_head=pe, wtype=models.F16)
+    rng = np.random.default_rng(31)
+    B, N = 2, 23
+    cat0, x, ts, rope = m.inputs(rng, B, N)
+    cat = m.with_x(cat0, x, B)
+    got = po.f5_step(m.ox, B, N, cat, ts, rope)
+    want = f5_numpy(m, B, N, cat, ts, rope)
+    assert np.max(np.abs(got - want)) / max(1.0, np.max(np.abs(want))) < 2e-5
+
+
 def test_noise_moments(oracle):
     # test_core.cpp:630-645
     a = po.noise(42, 0xF5000000 + 3, 100001)

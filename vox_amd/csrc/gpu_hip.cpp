@@ -6,8 +6,8 @@
 //
 // Error convention of the reference backend (gpu_vulkan.cpp:568-571, :800-803): no exception escapes, false/-1
 // means "compute on the CPU", the reason is kept for gpu_stats().last_error, and one warning goes to stderr.
-// Entry points not provided by this backend yet (the predictor frame loop, the codec, F5, the CosyVoice flow)
-// answer like gpu_stub.cpp, so their callers stay on the CPU.
+// Entry points not provided by this backend yet (the predictor frame loop, the codec, the Vocos vocoder, the
+// CosyVoice flow) answer like gpu_stub.cpp, so their callers stay on the CPU.
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -191,6 +191,29 @@ bool gpu_xfmr_forward_pair(const TransformerW &w, int seq0, int seq1, int64_t po
     return false;
 }
 
+// ---- F5-TTS DiT step (gpu.hpp:62-91): the description maps field by field; the vocoder fields are ignored
+int gpu_f5_create(const GpuF5Desc &d) {
+    std::vector<voxhip_f5_block> blocks;
+    for (const GpuF5Desc::Block &b : d.blocks) blocks.push_back({b.ada, b.q, b.k, b.v, b.o, b.ff1, b.ff2});
+    auto conv = [](const GpuF5Conv &c) { return voxhip_f5_conv{c.w, c.b, c.cin, c.cout, c.K, c.groups}; };
+    voxhip_f5_desc c;
+    c.dim = d.dim; c.depth = d.depth; c.heads = d.heads; c.dim_head = d.dim_head; c.ff_mult = d.ff_mult;
+    c.mel_dim = d.mel_dim; c.text_dim = d.text_dim; c.pe_attn_head = d.pe_attn_head;
+    c.in_proj = d.in_proj; c.norm_out = d.norm_out; c.proj_out = d.proj_out;
+    c.blocks = blocks.data(); c.pos1 = conv(d.pos1); c.pos2 = conv(d.pos2);
+    if (int(blocks.size()) != d.depth) return -1;
+    const int id = voxhip_f5_create(&c);
+    if (id < 0) warn_once("F5 graph");
+    return id;
+}
+bool gpu_f5_begin(int id, int B, int N, const float *cat0, const float *rope) { return voxhip_f5_begin(id, B, N, cat0, rope) != 0; }
+bool gpu_f5_step(int id, const float *x, const float *ts, float *out) {
+    if (voxhip_f5_step(id, x, ts, out)) return true;
+    std::fprintf(stderr, "vox: GPU F5 step failed: %s\n", voxhip_last_error());
+    return false;
+}
+void gpu_f5_end(int id) { (void)voxhip_f5_end(id); }
+
 // ---- not provided by this backend yet: the callers compute on the CPU (gpu_stub.cpp behaviour)
 bool gpu_pred_frame(const TransformerW &, int, const float *, const Mat *, const std::vector<Mat> &, const std::vector<Mat> &,
                     const GpuSampleCfg &, int32_t *) {
@@ -201,11 +224,7 @@ int gpu_codec_state_new(int) { return -1; }
 int gpu_codec_state_clone(int) { return -1; }
 void gpu_codec_state_free(int) {}
 bool gpu_codec_forward(int, int, const float *, int, std::vector<float> &) { return false; }
-int gpu_f5_create(const GpuF5Desc &) { return -1; }
-bool gpu_f5_begin(int, int, int, const float *, const float *) { return false; }
-bool gpu_f5_step(int, const float *, const float *, float *) { return false; }
-bool gpu_f5_vocos(int, const float *, int, std::vector<float> &) { return false; }
-void gpu_f5_end(int) {}
+bool gpu_f5_vocos(int, const float *, int, std::vector<float> &) { return false; }  // Vocos stays on the CPU (f5.cpp:787-791)
 std::string gpu_gemm_choice() { return ""; }
 void gpu_gemm_preset(const std::string &) {}
 int gpu_cosy_create(const GpuCosyDesc &) { return -1; }

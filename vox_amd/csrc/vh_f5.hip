@@ -1,0 +1,27 @@
+// Launchers of the F5-TTS DiT step kernels (AdaLN modulation, attention, input columns).
+#include "vh_f5.hpp"
+#include "vh_launch.hpp"
+
+namespace vh {
+
+hipError_t launch_f5_modulate(const float *x, int64_t R, int D, const float *sc, const float *sh, float *y, hipStream_t s) {
+    if (R <= 0) return hipSuccess;
+    if (D <= 0 || R > INT32_MAX) return hipErrorInvalidValue;
+    return launch(k_f5_modulate, dim3(unsigned(R)), dim3(256), 0, s, x, int32_t(D), sc, sh, y);
+}
+
+hipError_t launch_f5_fill_x(const float *x, int N, int mel, float *cat, int W, int B, hipStream_t s) {
+    const int64_t n = int64_t(B) * N * mel;
+    if (n <= 0) return hipSuccess;
+    return launch(k_f5_fill_x, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, x, int32_t(N), int32_t(mel), cat, int32_t(W),
+                  int32_t(B));
+}
+
+hipError_t launch_f5_attn(const float *qkv, float *out, int B, int N, int heads, int hd, int ld, int ldo, float scale, hipStream_t s) {
+    if (B <= 0 || N <= 0) return hipSuccess;
+    if (hd != kF5Hd || ld % 4 || heads <= 0) return hipErrorInvalidValue;
+    F5AttnArgs a{qkv, out, int32_t(N), int32_t(ld), int32_t(ldo), int32_t(heads * hd), scale};
+    return launch(k_f5_attn, dim3(unsigned((N + 63) / 64), unsigned(heads), unsigned(B)), dim3(256), 0, s, a);
+}
+
+}  // namespace vh

@@ -1,0 +1,152 @@
+// vh_f5.hpp — F5-TTS DiT step kernels besides the GEMMs: AdaLN modulation, non-causal softmax attention on the
+// matrix cores, and the x columns of the step input.
+#pragma once
+#include "vh_common.hpp"
+#include "vh_types.hpp"
+
+namespace vh {
+
+typedef float f32x4a __attribute__((ext_vector_type(4)));
+
+// LayerNorm without parameters + modulation (f5.cpp:608-625) of one row per block (256 threads): mean and
+// variance in double, inv = float(1 / sqrt(var + 1e-6)), y = (x - float(mean)) * inv * (1 + scale) + shift.
+__global__ __launch_bounds__(256) void k_f5_modulate(const float *__restrict__ x, int32_t D, const float *__restrict__ sc,
+                                                     const float *__restrict__ sh, float *__restrict__ y) {
+    __shared__ double red[4];
+    const float *xr = x + int64_t(blockIdx.x) * D;
+    float *yr = y + int64_t(blockIdx.x) * D;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    auto bsum = [&](double v) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+        __syncthreads();
+        if (lane == 0) red[w] = v;
+        __syncthreads();
+        return (red[0] + red[1]) + (red[2] + red[3]);
+    };
+    double s = 0.0;
+    for (int i = t; i < D; i += 256) s += double(xr[i]);
+    const double mean = bsum(s) / D;
+    double v = 0.0;
+    for (int i = t; i < D; i += 256) {
+        const double dd = double(xr[i]) - mean;
+        v += dd * dd;
+    }
+    const double var = bsum(v) / D;
+    const float inv = float(1.0 / sqrt(var + 1e-6)), fm = float(mean);
+    for (int i = t; i < D; i += 256) yr[i] = (xr[i] - fm) * inv * (1.0f + sc[i]) + sh[i];
+}
+
+// cat[b][t][0..mel) = x[t][0..mel) for every batch b (the x columns of the DiT input, gpu.hpp:85-88).
+__global__ __launch_bounds__(256) void k_f5_fill_x(const float *__restrict__ x, int32_t N, int32_t mel, float *__restrict__ cat,
+                                                   int32_t W, int32_t B) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= int64_t(B) * N * mel) return;
+    const int64_t r = i / mel, c = i % mel;
+    cat[r * W + c] = x[(r % N) * mel + c];
+}
+
+// Non-causal softmax attention of one head over N keys (f5.cpp:626-650): S = (q . k) * scale, softmax per row,
+// O = P V, for head_dim 64. grid (ceil(N / 64), heads, B), block 256: each wave takes 16 query rows; key tiles of
+// 64 go through LDS; an online softmax (running max and sum per row, O rescaled) replaces the reference's
+// whole-row max, which changes only the rounding. MFMA 16x16x4 f32 for S and for P V.
+struct F5AttnArgs {
+    const float *qkv;  // [B N][ld] rows: q | k | v, head h at column h * 64 of each
+    float *out;        // [B N][ldo], head h at column h * 64
+    int32_t N, ld, ldo, inner;
+    float scale;
+};
+constexpr int kF5Hd = kF5HeadDim;
+__global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
+    __shared__ __align__(16) float Ks[64][68];   // [key][d], stride 68: the S operand reads are conflict-free
+    __shared__ __align__(16) float Vs[64][80];   // [key][d], stride 80: the P V operand reads are conflict-free
+    __shared__ __align__(16) float Ps[4][16][68];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    const int q0 = blockIdx.x * 64, h = blockIdx.y;
+    const int64_t rb = int64_t(blockIdx.z) * a.N;
+    const float *Q = a.qkv + int64_t(h) * kF5Hd, *Kp = a.qkv + a.inner + int64_t(h) * kF5Hd,
+                *Vp = a.qkv + 2 * int64_t(a.inner) + int64_t(h) * kF5Hd;
+    // A operand of S: lane holds Q[16 wave + lr][4 s + lg], s < 16
+    float qa[16];
+    {
+        const int qr = q0 + 16 * wave + lr;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) qa[s] = qr < a.N ? Q[(rb + qr) * a.ld + 4 * s + lg] : 0.f;
+    }
+    float mrow[4], lrow[4];
+    f32x4a o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { mrow[i] = -INFINITY; lrow[i] = 0.f; o[i] = f32x4a{0.f, 0.f, 0.f, 0.f}; }
+    for (int kt = 0; kt < a.N; kt += 64) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int idx = tid + 256 * q, key = idx >> 4, d4 = (idx & 15) * 4;
+            f32x4a kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+            if (kt + key < a.N) {
+                kv = *reinterpret_cast<const f32x4a *>(Kp + (rb + kt + key) * a.ld + d4);
+                vv = *reinterpret_cast<const f32x4a *>(Vp + (rb + kt + key) * a.ld + d4);
+            }
+            *reinterpret_cast<f32x4a *>(&Ks[key][d4]) = kv;
+            *reinterpret_cast<f32x4a *>(&Vs[key][d4]) = vv;
+        }
+        __syncthreads();
+        f32x4a s[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[j] = f32x4a{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < 16; ++st)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[st], Ks[16 * j + lr][4 * st + lg], s[j], 0, 0, 0);
+        // lane holds S[4 lg + i][16 j + lr]: the 16 lanes of a DPP row share the rows
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float v = kt + 16 * j + lr < a.N ? s[j][i] * a.scale : -INFINITY;
+                s[j][i] = v;
+                mx = fmaxf(mx, v);
+            }
+            mx = fmaxf(mx, dpp<kDppXor1>(mx));
+            mx = fmaxf(mx, dpp<kDppXor2>(mx));
+            mx = fmaxf(mx, dpp<kDppRowHalfMirror>(mx));
+            mx = fmaxf(mx, dpp<kDppRowMirror>(mx));
+            const float mnew = fmaxf(mrow[i], mx);
+            const float alpha = expf(mrow[i] - mnew);  // 0 on the first tile (mrow = -inf)
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float p = expf(s[j][i] - mnew);
+                sum += p;
+                Ps[wave][4 * lg + i][16 * j + lr] = p;
+            }
+            sum += dpp<kDppXor1>(sum);
+            sum += dpp<kDppXor2>(sum);
+            sum += dpp<kDppRowHalfMirror>(sum);
+            sum += dpp<kDppRowMirror>(sum);
+            lrow[i] = lrow[i] * alpha + sum;
+            mrow[i] = mnew;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) o[dt][i] *= alpha;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 64; kk += 4) {
+            const float pa = Ps[wave][lr][kk + lg];
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, Vs[kk + lg][16 * dt + lr], o[dt], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int qr = q0 + 16 * wave + 4 * lg + i;
+        if (qr >= a.N) continue;
+        const float inv = 1.0f / lrow[i];
+        float *dst = a.out + (rb + qr) * a.ldo + int64_t(h) * kF5Hd;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) dst[16 * dt + lr] = o[dt][i] * inv;
+    }
+}
+
+}  // namespace vh

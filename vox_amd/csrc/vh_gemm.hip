@@ -1,29 +1,44 @@
-// Instantiations of the f32 MFMA GEMM (multi-row passes) and the attention-partials merge.
+// Instantiations of the f32 MFMA GEMM (multi-row passes, DiT linears, grouped convolutions) and the
+// attention-partials merge.
 #include "vh_gemm.hpp"
 #include "vh_launch.hpp"
 
 namespace vh {
 
+template <int WT, int EPI, int ASRC, int T>
+static hipError_t gemm_run(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, int groups, hipStream_t s) {
+    constexpr int B = 32 * T;
+    const dim3 grid((g.n + B - 1) / B, (g.m + B - 1) / B, groups);
+    return launch(k_gemm_f32<WT, EPI, ASRC, T, T>, grid, dim3(256), 0, s, w, scale, A, g);
+}
+
+// 128 x 128 block tiles when they still give a full wave of blocks, else 64 x 64.
 template <int WT, int EPI>
-static hipError_t gemm_run(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s) {
-    const dim3 grid((g.n + kGemmBN - 1) / kGemmBN, (g.m + kGemmBM - 1) / kGemmBM);
-    return launch(k_gemm_f32<WT, EPI>, grid, dim3(256), 0, s, w, scale, A, g);
+static hipError_t gemm_tile(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s) {
+    const int64_t big = int64_t((g.n + 127) / 128) * ((g.m + 127) / 128);
+    if (big >= 256) return gemm_run<WT, EPI, ASRC_ROWS, 4>(w, scale, A, g, 1, s);
+    return gemm_run<WT, EPI, ASRC_ROWS, 2>(w, scale, A, g, 1, s);
 }
 
 template <int WT>
 static hipError_t gemm_epi(int epi, const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s) {
     switch (epi) {
-        case EPI_STORE: return gemm_run<WT, EPI_STORE>(w, scale, A, g, s);
-        case EPI_ACC: return gemm_run<WT, EPI_ACC>(w, scale, A, g, s);
-        case EPI_SWIGLU: return gemm_run<WT, EPI_SWIGLU>(w, scale, A, g, s);
+        case EPI_STORE: return gemm_tile<WT, EPI_STORE>(w, scale, A, g, s);
+        case EPI_ACC: return gemm_tile<WT, EPI_ACC>(w, scale, A, g, s);
+        case EPI_SWIGLU: return gemm_tile<WT, EPI_SWIGLU>(w, scale, A, g, s);
+        case EPI_GATED_ACC: return g.gate ? gemm_tile<WT, EPI_GATED_ACC>(w, scale, A, g, s) : hipErrorInvalidValue;
+        case EPI_GELU: return gemm_tile<WT, EPI_GELU>(w, scale, A, g, s);
+        case EPI_ROPE:
+            if (!g.rope || g.hd <= 0 || g.hd % 2 || g.seq <= 0 || g.rope_cols % (2 * g.hd)) return hipErrorInvalidValue;
+            return gemm_tile<WT, EPI_ROPE>(w, scale, A, g, s);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_gemm(int wt, int epi, const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s) {
     if (g.m <= 0) return hipSuccess;
-    if (g.K % 8 || g.n <= 0) return hipErrorInvalidValue;
-    if (epi == EPI_SWIGLU && g.n % 2) return hipErrorInvalidValue;
+    if (g.K % 8 || g.n <= 0 || g.lda % 4) return hipErrorInvalidValue;
+    if ((epi == EPI_SWIGLU || epi == EPI_ROPE) && g.n % 2) return hipErrorInvalidValue;
     switch (wt) {
         case WT_F32: return gemm_epi<WT_F32>(epi, w, scale, A, g, s);
         case WT_F16: return gemm_epi<WT_F16>(epi, w, scale, A, g, s);
@@ -31,6 +46,18 @@ hipError_t launch_gemm(int wt, int epi, const uint8_t *w, const float *scale, co
         case WT_Q8: return g.K % 32 ? hipErrorInvalidValue : gemm_epi<WT_Q8>(epi, w, scale, A, g, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_conv_gemm(int epi, const float *w, const float *A, const GemmArgs &g, int groups, hipStream_t s) {
+    if (g.m <= 0) return hipSuccess;
+    if (g.cig <= 0 || g.cig % 4 || g.ksize <= 0 || g.ksize % 2 == 0 || g.K != g.ksize * g.cig || g.K % 8 || g.seq <= 0 ||
+        g.lda % 4 || groups <= 0 || g.n <= 0)
+        return hipErrorInvalidValue;
+    const uint8_t *wb = reinterpret_cast<const uint8_t *>(w);
+    if (epi == EPI_MISH) return gemm_run<WT_F32, EPI_MISH, ASRC_CONV, 2>(wb, nullptr, A, g, groups, s);
+    if (epi == EPI_MISH_ACC) return gemm_run<WT_F32, EPI_MISH_ACC, ASRC_CONV, 2>(wb, nullptr, A, g, groups, s);
+    if (epi == EPI_STORE) return gemm_run<WT_F32, EPI_STORE, ASRC_CONV, 2>(wb, nullptr, A, g, groups, s);
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_attn_merge(const AttnPartials &P, float *ao, int m, hipStream_t s) {

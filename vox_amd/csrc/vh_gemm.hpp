@@ -1,14 +1,17 @@
-// vh_gemm.hpp — f32 GEMM on the matrix cores for multi-row passes (prefill, m > 4 on the f32-activation path).
+// vh_gemm.hpp — f32 GEMM on the matrix cores for multi-row passes: LLM prefill (matmul's f32 paths above 8 rows /
+// 4 rows), the F5 DiT linears and its grouped position convolutions.
 //
-// C[i][r] (+)= sum_k A[i][k] * W[r][k] (+ bias[r]): the device counterpart of matmul's f32 paths for m > 8 (Q8
-// dequantized as float(q) * scale, kernels.cpp:661-679) and for F32 / F16 / BF16 weights (kernels.cpp:337-412).
-// The products are the reference's (weights widened exactly to f32, f32 activations); only the summation order
-// differs (v_mfma_f32_16x16x4_f32 accumulates in f32).
+// C[i][r] = sum_k A[i][k] * W[r][k] (+ bias[r]), then an epilogue. The device counterpart of matmul's f32 paths
+// for m > 8 (Q8 dequantized as float(q) * scale, kernels.cpp:661-679) and for F32 / F16 / BF16 weights
+// (kernels.cpp:337-412), and of Conv1d::forward's per-group im2col matmul (f5_ops.cpp:128-146). The products are
+// the reference's (weights widened exactly to f32, f32 activations); only the summation order differs
+// (v_mfma_f32_16x16x4_f32 accumulates in f32).
 //
-// Block: 256 threads = 4 waves as 2 x 2, tile 64 rows of A x 64 rows of W, K step 32 staged through LDS (W
-// dequantized on the way in). Each wave owns a 32 x 32 piece of C as 2 x 2 MFMA 16x16x4 tiles. MFMA lane layouts
-// (checked on gfx950): A 16x4 -> lane l holds A[l % 16][l / 16]; B 4x16 -> lane l holds B[l / 16][l % 16];
-// D 16x16 -> lane l holds D[4 (l / 16) + i][l % 16], i < 4.
+// Block: 256 threads = 4 waves as 2 x 2; each wave owns a (16 TM) x (16 TN) piece of C as TM x TN MFMA 16x16x4
+// tiles, so the block tile is (32 TM) rows of A x (32 TN) rows of W. K steps of 32 are staged through LDS (W
+// widened on the way in); the next step's global loads are issued before the current step's MFMAs.
+// MFMA lane layouts (checked on gfx950): A 16x4 -> lane l holds A[l % 16][l / 16]; B 4x16 -> lane l holds
+// B[l / 16][l % 16]; D 16x16 -> lane l holds D[4 (l / 16) + i][l % 16], i < 4.
 #pragma once
 #include "vh_common.hpp"
 #include "vh_types.hpp"
@@ -17,103 +20,171 @@ namespace vh {
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-constexpr int kGemmBM = 64, kGemmBN = 64, kGemmBK = 32, kGemmLd = kGemmBK + 4;  // LDS row stride (bank spread)
+constexpr int kGemmBK = 32, kGemmLd = kGemmBK + 4;  // LDS row stride (bank spread)
 
 template <int WT>
 VH_DEV int64_t gemm_row_bytes(int K) {
     return WT == WT_F32 ? int64_t(K) * 4 : WT == WT_Q8 ? int64_t(K) : int64_t(K) * 2;
 }
 
-// EPI_STORE: y = C + bias; EPI_ACC: y += C + bias; EPI_SWIGLU: W rows are (gate u, up u) pairs, y[u] = silu(gate) * up.
-template <int WT, int EPI>
+VH_DEV float gelu_tanh_f(float x) {  // f5.cpp:93-96
+    const float k = 0.7978845608028654f;
+    return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
+}
+VH_DEV float mish_f(float x) {  // f5.cpp:97-100
+    const float sp = x > 20.f ? x : log1pf(expf(x));
+    return x * tanhf(sp);
+}
+
+// Four consecutive A elements of row `row`, columns k..k+3 (zeros outside the matrix / the convolution window).
+template <int ASRC>
+VH_DEV f32x4v gemm_load_a(const float *__restrict__ A, const GemmArgs &g, int row, int k) {
+    f32x4v v = {0.f, 0.f, 0.f, 0.f};
+    if (row >= g.m || k >= g.K) return v;
+    if (ASRC == ASRC_ROWS) return *reinterpret_cast<const f32x4v *>(A + int64_t(row) * g.lda + k);
+    const int s = row / g.seq, t = row % g.seq, kt = k / g.cig, i = k % g.cig;
+    const int tt = t + kt - g.ksize / 2;
+    if (tt < 0 || tt >= g.seq) return v;
+    return *reinterpret_cast<const f32x4v *>(A + (int64_t(s) * g.seq + tt) * g.lda + int64_t(blockIdx.z) * g.cig + i);
+}
+
+// Eight consecutive W elements of row `row`, columns k..k+7, widened to f32.
+template <int WT>
+VH_DEV void gemm_load_w(const uint8_t *__restrict__ w, const float *__restrict__ scale, const GemmArgs &g, int row, int k,
+                        float (&v)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = 0.f;
+    if (row >= g.n || k >= g.K) return;
+    const uint8_t *p = w + int64_t(row) * gemm_row_bytes<WT>(g.K);
+    if (WT == WT_Q8) {
+        const uint2 u = *reinterpret_cast<const uint2 *>(p + k);
+        const float s = scale[int64_t(row) * (g.K / 32) + k / 32];
+        const uint32_t uw[2] = {u.x, u.y};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = float(int8_t(uw[e >> 2] >> (8 * (e & 3)))) * s;
+    } else if (WT == WT_F32) {
+        const f32x4v a = *reinterpret_cast<const f32x4v *>(p + int64_t(k) * 4);
+        const f32x4v b = *reinterpret_cast<const f32x4v *>(p + int64_t(k) * 4 + 16);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        const u32x4 u = *reinterpret_cast<const u32x4 *>(p + int64_t(k) * 2);
+        const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint16_t h = uint16_t(uw[e >> 1] >> (16 * (e & 1)));
+            v[e] = WT == WT_F16 ? float(__builtin_bit_cast(_Float16, h)) : bf16_to_f32(h);
+        }
+    }
+}
+
+// Epilogues: EPI_STORE y = c + bias; EPI_ACC y += c + bias; EPI_SWIGLU W rows are (gate u, up u) pairs, y[u] =
+// silu(gate) * up; EPI_GATED_ACC y += gate[col] * (c + bias); EPI_GELU y = gelu_tanh(c + bias); EPI_MISH
+// y = mish(c + bias); EPI_MISH_ACC y += mish(c + bias); EPI_ROPE y = c + bias with the pairs of q | k rotated.
+// ASRC_CONV: W (F32) and y columns are those of group blockIdx.z.
+template <int WT, int EPI, int ASRC, int TM, int TN>
 __global__ __launch_bounds__(256) void k_gemm_f32(const uint8_t *__restrict__ w, const float *__restrict__ scale,
                                                   const float *__restrict__ A, GemmArgs g) {
     static_assert(WT == WT_F32 || WT == WT_F16 || WT == WT_BF16 || WT == WT_Q8, "f32-activation weight types");
-    __shared__ __align__(16) float As[kGemmBM][kGemmLd];
-    __shared__ __align__(16) float Bs[kGemmBN][kGemmLd];
+    static_assert(ASRC == ASRC_ROWS || WT == WT_F32, "convolution weights are f32");
+    constexpr int BM = 32 * TM, BN = 32 * TN;
+    constexpr int AQ = BM * kGemmBK / 4 / 256;  // f32x4 A loads per thread and K step
+    constexpr int WQ = BN * kGemmBK / 8 / 256;  // 8-element W loads per thread and K step
+    __shared__ __align__(16) float As[BM][kGemmLd];
+    __shared__ __align__(16) float Bs[BN][kGemmLd];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * kGemmBM, n0 = blockIdx.x * kGemmBN;
-    const int K = g.K, nb = K / 32;
-    const int64_t rb = gemm_row_bytes<WT>(K);
-    f32x4v acc[2][2];
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int K = g.K;
+    if (ASRC == ASRC_CONV) {
+        w += int64_t(blockIdx.z) * g.n * K * 4;
+        g.y += int64_t(blockIdx.z) * g.n;
+        if (g.bias) g.bias += int64_t(blockIdx.z) * g.n;
+    }
+    f32x4v acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
 
-    for (int k0 = 0; k0 < K; k0 += kGemmBK) {
-        // A tile: 64 rows x 32 k, two f32x4 per thread; rows past m and k past K read as zeros
+    f32x4v ra[AQ];
+    float rw[WQ][8];
+    auto fetch = [&](int k0) {
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int idx = tid + 256 * q, r = idx >> 3, kq = (idx & 7) * 4;
-            const int row = m0 + r, k = k0 + kq;
-            f32x4v v = {0.f, 0.f, 0.f, 0.f};
-            if (row < g.m && k < K) v = *reinterpret_cast<const f32x4v *>(A + int64_t(row) * g.lda + k);
-            *reinterpret_cast<f32x4v *>(&As[r][kq]) = v;
+        for (int q = 0; q < AQ; ++q) {
+            const int idx = tid + 256 * q;
+            ra[q] = gemm_load_a<ASRC>(A, g, m0 + (idx >> 3), k0 + (idx & 7) * 4);
         }
-        // W tile: 64 rows x 32 k, widened to f32; 8 elements per thread
-        {
-            const int r = tid >> 2, kq = (tid & 3) * 8, row = n0 + r, k = k0 + kq;
-            float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            if (row < g.n && k < K) {
-                const uint8_t *p = w + int64_t(row) * rb;
-                if (WT == WT_Q8) {
-                    const uint2 u = *reinterpret_cast<const uint2 *>(p + k);
-                    const float s = scale[int64_t(row) * nb + k / 32];
-                    const uint32_t uw[2] = {u.x, u.y};
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = float(int8_t(uw[e >> 2] >> (8 * (e & 3)))) * s;
-                } else if (WT == WT_F32) {
-                    const f32x4v a = *reinterpret_cast<const f32x4v *>(p + int64_t(k) * 4);
-                    const f32x4v b = *reinterpret_cast<const f32x4v *>(p + int64_t(k) * 4 + 16);
-                    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-                } else {
-                    const u32x4 u = *reinterpret_cast<const u32x4 *>(p + int64_t(k) * 2);
-                    const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+        for (int q = 0; q < WQ; ++q) {
+            const int idx = tid + 256 * q;
+            gemm_load_w<WT>(w, scale, g, n0 + (idx >> 2), k0 + (idx & 3) * 8, rw[q]);
+        }
+    };
+    fetch(0);
+    for (int k0 = 0; k0 < K; k0 += kGemmBK) {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const uint16_t h = uint16_t(uw[e >> 1] >> (16 * (e & 1)));
-                        v[e] = WT == WT_F16 ? float(__builtin_bit_cast(_Float16, h)) : bf16_to_f32(h);
-                    }
-                }
-            }
-            *reinterpret_cast<f32x4v *>(&Bs[r][kq]) = f32x4v{v[0], v[1], v[2], v[3]};
-            *reinterpret_cast<f32x4v *>(&Bs[r][kq + 4]) = f32x4v{v[4], v[5], v[6], v[7]};
+        for (int q = 0; q < AQ; ++q) {
+            const int idx = tid + 256 * q;
+            *reinterpret_cast<f32x4v *>(&As[idx >> 3][(idx & 7) * 4]) = ra[q];
+        }
+#pragma unroll
+        for (int q = 0; q < WQ; ++q) {
+            const int idx = tid + 256 * q, r = idx >> 2, kq = (idx & 3) * 8;
+            *reinterpret_cast<f32x4v *>(&Bs[r][kq]) = f32x4v{rw[q][0], rw[q][1], rw[q][2], rw[q][3]};
+            *reinterpret_cast<f32x4v *>(&Bs[r][kq + 4]) = f32x4v{rw[q][4], rw[q][5], rw[q][6], rw[q][7]};
         }
         __syncthreads();
+        if (k0 + kGemmBK < K) fetch(k0 + kGemmBK);  // in flight during the MFMAs below
 #pragma unroll
         for (int kk = 0; kk < kGemmBK; kk += 4) {
-            float a[2], b[2];
+            float a[TM], b[TN];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) a[i] = As[wm * 32 + i * 16 + (lane & 15)][kk + (lane >> 4)];
+            for (int i = 0; i < TM; ++i) a[i] = As[wm * 16 * TM + i * 16 + (lane & 15)][kk + (lane >> 4)];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) b[j] = Bs[wn * 32 + j * 16 + (lane & 15)][kk + (lane >> 4)];
+            for (int j = 0; j < TN; ++j) b[j] = Bs[wn * 16 * TN + j * 16 + (lane & 15)][kk + (lane >> 4)];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
         }
         __syncthreads();
     }
 
     // epilogue: lane holds C[row0 + 4 (lane / 16) + v][col] of each tile, col = col0 + lane % 16
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int col = n0 + wn * 32 + j * 16 + (lane & 15);
+        for (int j = 0; j < TN; ++j) {
+            const int col = n0 + wn * 16 * TN + j * 16 + (lane & 15);
             const float bz = (g.bias && col < g.n) ? g.bias[col] : 0.f;
+            const float gt = (EPI == EPI_GATED_ACC && col < g.n) ? g.gate[col] : 0.f;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int row = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + v;
+                const int row = m0 + wm * 16 * TM + i * 16 + 4 * (lane >> 4) + v;
                 const float c = acc[i][j][v] + bz;
+                const bool in = row < g.m && col < g.n;
+                float *dst = g.y + int64_t(row) * g.ldy + col;
                 if (EPI == EPI_SWIGLU) {
                     const float up = __shfl_xor(c, 1, kWave);  // column col ^ 1 of the same row
-                    if (row < g.m && col < g.n && (col & 1) == 0) g.y[int64_t(row) * g.ldy + col / 2] = silu(c) * up;
-                } else if (row < g.m && col < g.n) {
-                    float *dst = g.y + int64_t(row) * g.ldy + col;
+                    if (in && (col & 1) == 0) g.y[int64_t(row) * g.ldy + col / 2] = silu(c) * up;
+                } else if (EPI == EPI_ROPE) {
+                    const float o = __shfl_xor(c, 1, kWave);  // the pair partner (2j <-> 2j + 1)
+                    float r = c;
+                    if (col < g.rope_cols) {
+                        const int inner = g.rope_cols / 2, d = col % g.hd, head = (col % inner) / g.hd;
+                        if (g.rope_heads <= 0 || head < g.rope_heads) {
+                            const float *cs = g.rope + ((int64_t(row % g.seq) * (g.hd / 2) + d / 2) * 2);
+                            const float cc = cs[0], sn = cs[1];
+                            r = (col & 1) ? c * cc + o * sn : c * cc - o * sn;
+                        }
+                    }
+                    if (in) *dst = r;
+                } else if (in) {
                     if (EPI == EPI_STORE) *dst = c;
-                    else *dst += c;
+                    else if (EPI == EPI_ACC) *dst += c;
+                    else if (EPI == EPI_GATED_ACC) *dst += gt * c;
+                    else if (EPI == EPI_GELU) *dst = gelu_tanh_f(c);
+                    else if (EPI == EPI_MISH) *dst = mish_f(c);
+                    else if (EPI == EPI_MISH_ACC) *dst += mish_f(c);
                 }
             }
         }

@@ -31,6 +31,8 @@ hipError_t launch_qk_post(const QkArgs &a, int m, hipStream_t s);
 
 // Multi-row f32 GEMM on the matrix cores (F32 / F16 / BF16 / Q8 weights).
 hipError_t launch_gemm(int wt, int epi, const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s);
+// Grouped "same" Conv1d as an implicit-im2col GEMM (f32 weights [groups][cout/groups][K][cin/groups]).
+hipError_t launch_conv_gemm(int epi, const float *w, const float *A, const GemmArgs &g, int groups, hipStream_t s);
 // Merge of the split attention partials of m rows into ao [m][heads * hd].
 hipError_t launch_attn_merge(const AttnPartials &P, float *ao, int m, hipStream_t s);
 // Split-K attention partials of m rows (merged by the PRO_ATTN GEMV prologue). fused: rows of distinct sequences,
@@ -54,6 +56,10 @@ hipError_t launch_fill_cache(void *c, int64_t planes, int64_t cap, int64_t len, 
                              float mean, float std, hipStream_t s);
 
 hipError_t launch_copy16(const void *src, void *dst, int64_t bytes, hipStream_t s);
+// F5-TTS DiT step: AdaLN modulation of R rows of D, the step input's x columns, attention (head_dim 64).
+hipError_t launch_f5_modulate(const float *x, int64_t R, int D, const float *sc, const float *sh, float *y, hipStream_t s);
+hipError_t launch_f5_fill_x(const float *x, int N, int mel, float *cat, int W, int B, hipStream_t s);
+hipError_t launch_f5_attn(const float *qkv, float *out, int B, int N, int heads, int hd, int ld, int ldo, float scale, hipStream_t s);
 // CosyVoice2 LM: one sampling step (log-softmax, RAS trial loop) and the next step's embedding + row advance.
 hipError_t launch_lm_sample(const float *logits, int n, const LmCfgDev *cfg, LmState *st, int32_t *decoded, float *logp_out,
                             int64_t logp_stride, bool append, hipStream_t s);

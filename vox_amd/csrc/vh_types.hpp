@@ -7,6 +7,10 @@ namespace vh {
 // GEMV input prologues: x as is; RMSNorm(x, gamma); or the merge of split-K attention partials.
 enum { PRO_X = 0, PRO_RMS = 1, PRO_ATTN = 2 };
 enum { EPI_STORE = 0, EPI_ACC = 1, EPI_SWIGLU = 2 };
+// GEMM-only epilogues (F5 DiT): y += gate * c; y = gelu_tanh(c); y = mish(c); y += mish(c); RoPE on q|k columns
+enum { EPI_GATED_ACC = 3, EPI_GELU = 4, EPI_MISH = 5, EPI_MISH_ACC = 6, EPI_ROPE = 7 };
+// GEMM A operand: rows of a matrix, or the implicit im2col rows of a grouped "same" Conv1d
+enum { ASRC_ROWS = 0, ASRC_CONV = 1 };
 // Weight formats of the GEMV kernels: the reference's types, plus Q4 with f16 block scales (WT_Q4H), the
 // device storage of a Q4 matrix whose f32 scales are all exact in f16 (same arithmetic, 2 bytes less per block).
 enum { WT_F32 = 0, WT_F16 = 1, WT_BF16 = 2, WT_Q8 = 3, WT_Q4 = 4, WT_Q4H = 5 };
@@ -91,6 +95,14 @@ struct GemmArgs {
     float *y;           // [m][ldy]
     int64_t lda, ldy;
     int32_t m, n, K;
+    const float *gate;  // EPI_GATED_ACC: [n]
+    // EPI_ROPE: table [seq][hd/2][2] (cos, sin) at position row % seq; pairs (2j, 2j + 1) of the columns below
+    // rope_cols rotate (q | k heads), heads >= rope_heads of each of q and k are left as they are
+    const float *rope;
+    int32_t seq, hd, rope_cols, rope_heads;
+    // ASRC_CONV: x [m][lda] rows of `seq`-row batches; group g = blockIdx.z reads channels [g cig, (g + 1) cig) at
+    // rows t + k - ksize / 2 of the same batch (zeros outside) for A column k cig + i; W and y are offset per group
+    int32_t ksize, cig;
 };
 
 // CosyVoice2 LM sampling (lm_logp + ras_sample + lm_generate's trial loop, cosyvoice.cpp:598-690).
@@ -121,6 +133,7 @@ struct LmEmbedArgs {
     int32_t hd;
     int64_t spare_pos;
 };
+constexpr int kF5HeadDim = 64;   // head_dim of the F5 attention kernel
 constexpr int kLmMaxK = 1024;  // top_k limit of the device RAS sampler (sorted in LDS above 64)
 constexpr int kLmMaxN = 8192;  // vocabulary limit of the device RAS sampler (8 entries per thread)
 

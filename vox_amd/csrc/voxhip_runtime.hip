@@ -16,9 +16,11 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <tuple>
 #include <unordered_map>
 #include <vector>
@@ -137,6 +139,7 @@ struct Ctx {
     SampleCfgDev *scfg_dev = nullptr, *scfg_host = nullptr;
     int32_t *hist_dev = nullptr, *tok_dev = nullptr;
     size_t hist_cap = 0;
+    std::vector<struct F5 *> f5;
     // LM sampler staging: device config + state, and their pinned host copies (config, state, two state slots)
     LmCfgDev *lm_cfg_dev = nullptr;
     LmState *lm_state_dev = nullptr;
@@ -1402,24 +1405,26 @@ int voxhip_lm_generate(int xfmr, int seq, const float *x, int64_t n, int head, i
         HIPCHECK(hipMemcpyAsync(X.lm_state, lm_host_state(0), sizeof(LmState), hipMemcpyHostToDevice, g.stream));
         set_rows(X, {row_of(S, n - 1)});  // the first step's embedding kernel advances it to position n
         hipGraphExec_t exec = lm_graph(X, S, seq, head, speech_emb, logp != nullptr);
-        hipEvent_t ev[2] = {nullptr, nullptr};
-        auto cleanup = [&] {
-            for (hipEvent_t e : ev)
-                if (e) (void)hipEventDestroy(e);
-            X.rows_valid = false;  // the device advanced the row table
-        };
+        auto cleanup = [&] { X.rows_valid = false; };  // the device advanced the row table
         try {
-            HIPCHECK(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
-            HIPCHECK(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming));
-            // one graph ahead: while graph c runs, the host reads the state after graph c - 1
+            // One graph ahead: while graph c runs, the host reads the state copied after graph c - 1. The copy's
+            // arrival is seen in the pinned slot itself (pad0: -1 set by the host, 0 in the device state), so no
+            // events are recorded between graph launches.
             const int chunks = (cfg->max_len + kLmGraphSteps - 1) / kLmGraphSteps;
             for (int c = 0; c < chunks; ++c) {
+                LmState *slot = lm_host_state(1 + (c & 1));
+                __atomic_store_n(&slot->pad0, -1, __ATOMIC_RELEASE);
                 HIPCHECK(hipGraphLaunch(exec, g.stream));
-                HIPCHECK(hipMemcpyAsync(lm_host_state(1 + (c & 1)), X.lm_state, sizeof(LmState), hipMemcpyDeviceToHost, g.stream));
-                HIPCHECK(hipEventRecord(ev[c & 1], g.stream));
+                HIPCHECK(hipMemcpyAsync(slot, X.lm_state, sizeof(LmState), hipMemcpyDeviceToHost, g.stream));
                 if (c >= 1) {
-                    HIPCHECK(hipEventSynchronize(ev[(c - 1) & 1]));
-                    if (lm_host_state(1 + ((c - 1) & 1))->done) break;
+                    LmState *prev = lm_host_state(1 + ((c - 1) & 1));
+                    while (__atomic_load_n(&prev->pad0, __ATOMIC_ACQUIRE) == -1) {
+                        const hipError_t q = hipStreamQuery(g.stream);
+                        if (q == hipSuccess) break;
+                        if (q != hipErrorNotReady) HIPCHECK(q);
+                        std::this_thread::yield();
+                    }
+                    if (__atomic_load_n(&prev->done, __ATOMIC_ACQUIRE)) break;
                 }
             }
             HIPCHECK(hipMemcpyAsync(lm_host_state(0), X.lm_state, sizeof(LmState), hipMemcpyDeviceToHost, g.stream));
@@ -1435,6 +1440,225 @@ int voxhip_lm_generate(int xfmr, int seq, const float *x, int64_t n, int head, i
             throw;
         }
         cleanup();
+        return 1;
+    }, 0);
+}
+
+}  // extern "C"
+
+namespace {
+// ------------------------------------------------------------------ F5-TTS DiT step (gpu.hpp:62-91)
+struct F5Block {
+    int ada = -1, qkv = -1, o = -1, ff1 = -1, ff2 = -1;  // q | k | v stacked at create
+};
+struct F5Conv {
+    float *w = nullptr, *b = nullptr;
+    int cin = 0, cout = 0, K = 0, groups = 0;
+};
+struct F5 {
+    int dim = 0, depth = 0, heads = 0, hd = 0, ff = 0, mel = 0, text = 0, pe = 0;
+    int in_proj = -1, norm_out = -1, proj_out = -1;
+    std::vector<F5Block> blocks;
+    F5Conv pos1, pos2;
+    // step buffers of begin(B, N): rows R = B N
+    int B = 0, N = 0;
+    float *cat = nullptr, *h = nullptr, *a = nullptr, *nrm = nullptr, *qkv = nullptr, *at = nullptr, *ffb = nullptr;
+    float *ada = nullptr, *fin = nullptr, *ts = nullptr, *x = nullptr, *out = nullptr, *rope = nullptr;
+};
+
+F5 &f5_at(int id) {
+    if (id < 0 || size_t(id) >= g.f5.size() || !g.f5[size_t(id)]) throw Fail("bad F5 handle " + std::to_string(id));
+    return *g.f5[size_t(id)];
+}
+
+// Stacks matrices of one type and width by rows into a new device matrix (biases zero where a part has none).
+int stack_rows(const std::vector<int> &ids) {
+    const GpuMat m0 = mat_at(ids[0]);
+    int64_t rows = 0;
+    bool any_bias = false;
+    for (int id : ids) {
+        const GpuMat &m = mat_at(id);
+        if (m.type != m0.type || m.cols != m0.cols || m.s16 != m0.s16) throw Fail("stacked matrices differ in type or width");
+        rows += m.rows;
+        any_bias = any_bias || m.b;
+    }
+    const int nid = new_mat(m0.type, rows, m0.cols, any_bias, m0.s16);
+    const GpuMat dst = g.mats[size_t(nid)];
+    const size_t rb = row_bytes(m0.type, m0.cols), sb = scale_row_bytes(m0);
+    int64_t r0 = 0;
+    for (int id : ids) {
+        const GpuMat src = g.mats[size_t(id)];
+        HIPCHECK(hipMemcpy(dst.w + size_t(r0) * rb, src.w, size_t(src.rows) * rb, hipMemcpyDeviceToDevice));
+        if (sb) HIPCHECK(hipMemcpy(reinterpret_cast<uint8_t *>(dst.s) + size_t(r0) * sb, src.s, size_t(src.rows) * sb, hipMemcpyDeviceToDevice));
+        if (any_bias) {
+            if (src.b) HIPCHECK(hipMemcpy(dst.b + r0, src.b, size_t(src.rows) * 4, hipMemcpyDeviceToDevice));
+            else HIPCHECK(hipMemset(dst.b + r0, 0, size_t(src.rows) * 4));
+        }
+        r0 += src.rows;
+    }
+    return nid;
+}
+
+F5Conv upload_conv(const voxhip_f5_conv &c, int dim) {
+    if (!c.w || c.cin != dim || c.cout != dim || c.K <= 0 || c.K % 2 == 0 || c.groups <= 0 || c.cin % c.groups ||
+        c.cout % c.groups)
+        throw Fail("F5 position convolution: cin = cout = dim, odd K, groups dividing the channels");
+    const int cig = c.cin / c.groups;
+    if (cig % 4 || (int64_t(c.K) * cig) % 8) throw Fail("F5 position convolution: cin/groups must be a multiple of 4");
+    F5Conv d;
+    d.cin = c.cin; d.cout = c.cout; d.K = c.K; d.groups = c.groups;
+    const size_t n = size_t(c.cout) * size_t(c.K) * size_t(cig);
+    d.w = dalloc_t<float>(n);
+    h2d(d.w, c.w, n * 4);
+    if (c.b) {
+        d.b = dalloc_t<float>(size_t(c.cout));
+        h2d(d.b, c.b, size_t(c.cout) * 4);
+    }
+    return d;
+}
+
+void f5_free_step(F5 &F) {
+    for (float *p : {F.cat, F.h, F.a, F.nrm, F.qkv, F.at, F.ffb, F.ada, F.fin, F.ts, F.x, F.out, F.rope}) dfree(p);
+    F.cat = F.h = F.a = F.nrm = F.qkv = F.at = F.ffb = F.ada = F.fin = F.ts = F.x = F.out = F.rope = nullptr;
+    F.B = F.N = 0;
+}
+
+GemmArgs gemm_args(const GpuMat &m, const float *bias, float *y, int64_t lda, int64_t ldy, int64_t rows) {
+    GemmArgs ga{};
+    ga.bias = bias; ga.y = y; ga.lda = lda; ga.ldy = ldy; ga.m = int32_t(rows); ga.n = int32_t(m.rows); ga.K = int32_t(m.cols);
+    return ga;
+}
+void f5_gemm(const GpuMat &m, int epi, const float *A, GemmArgs ga, hipStream_t s) {
+    // matmul's f32-activation path for these rows (q8 above 8 rows; q4 never)
+    if (int_path(m, ga.m)) throw Fail("F5 linears need f32 / f16 / bf16 weights, or q8 with more than 8 rows");
+    HIPCHECK(launch_gemm(gemv_type(m), epi, m.w, m.s, A, ga, s));
+}
+
+// dit_forward on the device (f5.cpp:586-725) for the batches of begin; x [N][mel] and ts [dim] already on the device.
+void f5_enqueue(F5 &F, hipStream_t s) {
+    const int D = F.dim, INNER = F.heads * F.hd, W = 2 * F.mel + F.text;
+    const int64_t R = int64_t(F.B) * F.N;
+    HIPCHECK(launch_f5_fill_x(F.x, F.N, F.mel, F.cat, W, F.B, s));
+    for (int i = 0; i < F.depth; ++i) {  // the six modulation vectors of every block (f5.cpp:673)
+        const GpuMat &Ma = mat_at(F.blocks[size_t(i)].ada);
+        gemv(Ma, 1, PRO_X, EPI_STORE, F.ts, D, 1, F.ada + size_t(i) * 6 * D, 6 * D, nullptr, 0.f, nullptr, s);
+    }
+    gemv(mat_at(F.norm_out), 1, PRO_X, EPI_STORE, F.ts, D, 1, F.fin, 2 * D, nullptr, 0.f, nullptr, s);
+    const GpuMat &Mi = mat_at(F.in_proj);
+    f5_gemm(Mi, EPI_STORE, F.cat, gemm_args(Mi, Mi.b, F.h, W, D, R), s);
+    // convolutional position embedding: h += mish(conv2(mish(conv1(h)))) per batch (f5.cpp:589-598)
+    for (int c = 0; c < 2; ++c) {
+        const F5Conv &cv = c == 0 ? F.pos1 : F.pos2;
+        GemmArgs ga{};
+        ga.bias = cv.b; ga.y = c == 0 ? F.a : F.h; ga.lda = D; ga.ldy = D; ga.m = int32_t(R);
+        ga.n = cv.cout / cv.groups; ga.cig = cv.cin / cv.groups; ga.ksize = cv.K; ga.K = cv.K * ga.cig; ga.seq = F.N;
+        HIPCHECK(launch_conv_gemm(c == 0 ? EPI_MISH : EPI_MISH_ACC, cv.w, c == 0 ? F.h : F.a, ga, cv.groups, s));
+    }
+    const float scale = 1.0f / std::sqrt(float(F.hd));
+    for (int i = 0; i < F.depth; ++i) {
+        const F5Block &L = F.blocks[size_t(i)];
+        const float *ada = F.ada + size_t(i) * 6 * D;  // shift, scale, gate (msa), shift, scale, gate (mlp)
+        HIPCHECK(launch_f5_modulate(F.h, R, D, ada + D, ada, F.nrm, s));
+        const GpuMat &Mq = mat_at(L.qkv);
+        GemmArgs gq = gemm_args(Mq, Mq.b, F.qkv, D, 3 * INNER, R);
+        gq.rope = F.rope; gq.seq = F.N; gq.hd = F.hd; gq.rope_cols = 2 * INNER; gq.rope_heads = F.pe;
+        f5_gemm(Mq, EPI_ROPE, F.nrm, gq, s);
+        HIPCHECK(launch_f5_attn(F.qkv, F.at, F.B, F.N, F.heads, F.hd, 3 * INNER, INNER, scale, s));
+        const GpuMat &Mo = mat_at(L.o);
+        GemmArgs go = gemm_args(Mo, Mo.b, F.h, INNER, D, R);
+        go.gate = ada + 2 * D;
+        f5_gemm(Mo, EPI_GATED_ACC, F.at, go, s);
+        HIPCHECK(launch_f5_modulate(F.h, R, D, ada + 4 * D, ada + 3 * D, F.nrm, s));
+        const GpuMat &M1 = mat_at(L.ff1), &M2 = mat_at(L.ff2);
+        f5_gemm(M1, EPI_GELU, F.nrm, gemm_args(M1, M1.b, F.ffb, D, F.ff, R), s);
+        GemmArgs g2 = gemm_args(M2, M2.b, F.h, F.ff, D, R);
+        g2.gate = ada + 5 * D;
+        f5_gemm(M2, EPI_GATED_ACC, F.ffb, g2, s);
+    }
+    HIPCHECK(launch_f5_modulate(F.h, R, D, F.fin, F.fin + D, F.nrm, s));  // final modulation: (scale, shift)
+    const GpuMat &Mp = mat_at(F.proj_out);
+    f5_gemm(Mp, EPI_STORE, F.nrm, gemm_args(Mp, Mp.b, F.out, D, F.mel, R), s);
+}
+}  // namespace
+
+extern "C" {
+
+int voxhip_f5_create(const voxhip_f5_desc *d) {
+    return guard_int([&] {
+        require_ok();
+        if (!d || d->depth <= 0 || !d->blocks) throw Fail("missing F5 description");
+        if (d->dim_head != kF5HeadDim) throw Fail("F5 attention supports head_dim 64");
+        const int D = d->dim, INNER = d->heads * d->dim_head, FF = d->dim * d->ff_mult, W = 2 * d->mel_dim + d->text_dim;
+        if (D <= 0 || D % 8 || d->heads <= 0 || FF <= 0 || d->mel_dim <= 0 || d->text_dim < 0) throw Fail("bad F5 dimensions");
+        auto check = [&](int id, int64_t rows, int64_t cols, const char *what) {
+            const GpuMat &m = mat_at(id);
+            if (m.rows != rows || m.cols != cols) throw Fail(std::string("F5 ") + what + " has the wrong shape");
+        };
+        check(d->in_proj, D, W, "in_proj");
+        check(d->norm_out, 2 * D, D, "norm_out");
+        check(d->proj_out, d->mel_dim, D, "proj_out");
+        std::unique_ptr<F5> F(new F5());
+        F->dim = D; F->depth = d->depth; F->heads = d->heads; F->hd = d->dim_head; F->ff = FF; F->mel = d->mel_dim;
+        F->text = d->text_dim; F->pe = d->pe_attn_head;
+        F->in_proj = d->in_proj; F->norm_out = d->norm_out; F->proj_out = d->proj_out;
+        for (int i = 0; i < d->depth; ++i) {
+            const voxhip_f5_block &b = d->blocks[i];
+            check(b.ada, 6 * D, D, "ada");
+            check(b.q, INNER, D, "q"); check(b.k, INNER, D, "k"); check(b.v, INNER, D, "v");
+            check(b.o, D, INNER, "o"); check(b.ff1, FF, D, "ff1"); check(b.ff2, D, FF, "ff2");
+            F5Block fb;
+            fb.ada = b.ada; fb.o = b.o; fb.ff1 = b.ff1; fb.ff2 = b.ff2;
+            fb.qkv = stack_rows({b.q, b.k, b.v});
+            F->blocks.push_back(fb);
+        }
+        F->pos1 = upload_conv(d->pos1, D);
+        F->pos2 = upload_conv(d->pos2, D);
+        g.f5.push_back(F.release());
+        return int(g.f5.size()) - 1;
+    }, -1);
+}
+
+int voxhip_f5_begin(int id, int B, int N, const float *cat0, const float *rope) {
+    return guard_int([&] {
+        require_ok();
+        F5 &F = f5_at(id);
+        if (B <= 0 || N <= 0 || !cat0 || !rope || int64_t(B) * N > INT32_MAX / 8) throw Fail("bad F5 step shape");
+        f5_free_step(F);
+        const size_t R = size_t(B) * size_t(N), D = size_t(F.dim), INNER = size_t(F.heads) * F.hd;
+        const size_t W = 2 * size_t(F.mel) + F.text;
+        F.cat = dalloc_t<float>(R * W); F.h = dalloc_t<float>(R * D); F.a = dalloc_t<float>(R * D);
+        F.nrm = dalloc_t<float>(R * D); F.qkv = dalloc_t<float>(R * 3 * INNER); F.at = dalloc_t<float>(R * INNER);
+        F.ffb = dalloc_t<float>(R * size_t(F.ff)); F.ada = dalloc_t<float>(size_t(F.depth) * 6 * D);
+        F.fin = dalloc_t<float>(2 * D); F.ts = dalloc_t<float>(D); F.x = dalloc_t<float>(size_t(N) * F.mel);
+        F.out = dalloc_t<float>(R * size_t(F.mel)); F.rope = dalloc_t<float>(size_t(N) * size_t(F.hd));
+        h2d(F.cat, cat0, R * W * 4);
+        h2d(F.rope, rope, size_t(N) * size_t(F.hd) * 4);
+        F.B = B; F.N = N;
+        return 1;
+    }, 0);
+}
+
+int voxhip_f5_step(int id, const float *x, const float *ts, float *out) {
+    return guard_int([&] {
+        require_ok();
+        F5 &F = f5_at(id);
+        if (!F.B) throw Fail("F5 step before begin");
+        if (!x || !ts || !out) throw Fail("missing argument");
+        h2d(F.x, x, size_t(F.N) * F.mel * 4);
+        h2d(F.ts, ts, size_t(F.dim) * 4);
+        f5_enqueue(F, g.stream);
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        HIPCHECK(hipMemcpy(out, F.out, size_t(F.B) * F.N * F.mel * 4, hipMemcpyDeviceToHost));
+        return 1;
+    }, 0);
+}
+
+int voxhip_f5_end(int id) {
+    return guard_int([&] {
+        require_ok();
+        F5 &F = f5_at(id);
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        f5_free_step(F);
         return 1;
     }, 0);
 }

@@ -15,6 +15,11 @@ TALKER_0_6B = dict(layers=28, hidden=1024, heads=16, kv_heads=8, head_dim=128, i
 # Qwen3-TTS-1.7B-shaped talker with q4 body
 TALKER_1_7B_Q4 = dict(layers=28, hidden=2048, heads=16, kv_heads=8, head_dim=128, inter=6144, theta=1e6, eps=1e-6,
                       kv_len=1024, head_rows=3072, wtype=vh.Q4, head_type=vh.Q8, f16_scales=True)
+# CosyVoice2-0.5B-shaped LM: Qwen2 body (q/k/v biases, no q/k norm) in q8, f32 head 6564 x 896 with
+# bias (cosyvoice.cpp:405 keeps it out of q8), f32 speech-token embedding; prefill 512, then 256 decode steps
+COSY_LM_0_5B = dict(layers=24, hidden=896, heads=14, kv_heads=2, head_dim=64, inter=4864, theta=1e6, eps=1e-6,
+                    kv_len=0, head_rows=6564, wtype=vh.Q8, head_type=vh.F32, qkv_bias=True, qk_norm=False,
+                    head_bias=True, speech_tokens=6561, prefill=512, decode_steps=256)
 NAMES = ("q", "k", "v", "o", "gate", "up", "down")
 
 
@@ -40,10 +45,12 @@ class Decoder:
             for j, n in enumerate(NAMES):
                 r, cc = shapes[n]
                 ids[n] = vh.mat_synthetic(c["wtype"], r, cc, seed, 0x100 * li + j, 0.0, 0.02,
+                                          bias=c.get("qkv_bias", False) and n in ("q", "k", "v"),
                                           f16_scales=c.get("f16_scales", False))
             self.mats.append(ids)
             norms = {n: (1.0 + 0.02 * rng.standard_normal(H)).astype(np.float32) for n in ("ln1", "ln2")}
-            norms.update({n: (1.0 + 0.02 * rng.standard_normal(hd)).astype(np.float32) for n in ("qn", "kn")})
+            if c.get("qk_norm", True):
+                norms.update({n: (1.0 + 0.02 * rng.standard_normal(hd)).astype(np.float32) for n in ("qn", "kn")})
             layers.append(norms)
         self.layers = layers
         self.final_norm = (1.0 + 0.02 * rng.standard_normal(H)).astype(np.float32)
@@ -58,8 +65,10 @@ class Decoder:
             self.mats = None
         self.capacity = capacity or max(c["kv_len"] + 64, 1024)
         self.seq = vh.seq_create(self.xfmr, self.capacity)
-        vh.seq_fill_synthetic(self.seq, c["kv_len"], seed, 0xC0DE, 0.0, 1.0)
-        self.head = vh.mat_synthetic(c["head_type"], c["head_rows"], H, seed, 0xF00D, 0.0, 0.02) if c.get("head_rows") else -1
+        if c["kv_len"]:
+            vh.seq_fill_synthetic(self.seq, c["kv_len"], seed, 0xC0DE, 0.0, 1.0)
+        self.head = vh.mat_synthetic(c["head_type"], c["head_rows"], H, seed, 0xF00D, 0.0, 0.02,
+                                     bias=c.get("head_bias", False)) if c.get("head_rows") else -1
 
     def extra_seq(self, stream):
         """Another sequence of the same capacity whose first kv_len positions are filled from Philox stream `stream`
@@ -68,19 +77,34 @@ class Decoder:
         vh.seq_fill_synthetic(s, self.cfg["kv_len"], 0, stream, 0.0, 1.0)
         return s
 
+    def linear_flops(self, m):
+        """FLOPs of the layer matrices for m rows (2 per multiply-add)."""
+        c = self.cfg
+        H, qd, kd, I = c["hidden"], c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"], c["inter"]
+        return 2 * m * c["layers"] * ((qd + 2 * kd) * H + H * qd + 2 * I * H + H * I)
+
+    def attention_flops(self, m, pos0=0):
+        """FLOPs of causal attention for m rows at positions pos0..pos0+m-1 (scores and weighted values)."""
+        c = self.cfg
+        keys = sum(pos0 + i + 1 for i in range(m))
+        return 4 * c["layers"] * c["heads"] * c["head_dim"] * keys
+
     def weight_bytes(self):
         """Algorithmic bytes of one decode step's weight stream (layers + head), as stored."""
         c = self.cfg
         H, qd, kd, I = c["hidden"], c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"], c["inter"]
 
-        def mb(t, rows, cols):
+        def mb(t, rows, cols, bias=False):
+            b = rows * 4 if bias else 0
             if t == vh.Q8:
-                return rows * cols + rows * (cols // 32) * 4
+                return rows * cols + rows * (cols // 32) * 4 + b
             if t == vh.Q4:
-                return rows * cols // 2 + rows * (cols // 32) * (2 if c.get("f16_scales") else 4)
-            return rows * cols * (4 if t == vh.F32 else 2)
-        per_layer = sum(mb(c["wtype"], r, cc) for r, cc in ((qd + 2 * kd, H), (H, qd), (2 * I, H), (H, I)))
-        head = mb(c["head_type"], c["head_rows"], H) if c.get("head_rows") else 0
+                return rows * cols // 2 + rows * (cols // 32) * (2 if c.get("f16_scales") else 4) + b
+            return rows * cols * (4 if t == vh.F32 else 2) + b
+        qb = c.get("qkv_bias", False)
+        per_layer = sum(mb(c["wtype"], r, cc, bb) for r, cc, bb in ((qd + 2 * kd, H, qb), (H, qd, False), (2 * I, H, False),
+                                                                     (H, I, False)))
+        head = mb(c["head_type"], c["head_rows"], H, c.get("head_bias", False)) if c.get("head_rows") else 0
         return per_layer * c["layers"] + head
 
     def step_bytes(self, pos):
@@ -89,6 +113,6 @@ class Decoder:
         c = self.cfg
         kd = c["kv_heads"] * c["head_dim"]
         kv = c["layers"] * 2 * (pos + 1) * kd * 2
-        norms = c["layers"] * (2 * c["hidden"] + 2 * c["head_dim"]) * 4 + c["hidden"] * 4
+        norms = c["layers"] * (2 * c["hidden"] + (2 * c["head_dim"] if c.get("qk_norm", True) else 0)) * 4 + c["hidden"] * 4
         kv_write = c["layers"] * 2 * kd * 2
         return self.weight_bytes() + kv + norms + kv_write

@@ -70,6 +70,21 @@ class LmCfg(C.Structure):
                 ("seed", C.c_uint64)]
 
 
+class F5Conv(C.Structure):
+    _fields_ = [("w", C.c_void_p), ("b", C.c_void_p), ("cin", C.c_int32), ("cout", C.c_int32), ("K", C.c_int32),
+                ("groups", C.c_int32)]
+
+
+class F5Block(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("ada", "q", "k", "v", "o", "ff1", "ff2")]
+
+
+class F5Desc(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("dim", "depth", "heads", "dim_head", "ff_mult", "mel_dim", "text_dim",
+                                         "pe_attn_head", "in_proj", "norm_out", "proj_out")] + \
+               [("blocks", C.POINTER(F5Block)), ("pos1", F5Conv), ("pos2", F5Conv)]
+
+
 KERNEL_CLASSES = ("qkv_gemv", "o_gemv", "gateup_gemv", "down_gemv", "head_gemv", "attention", "attn_combine", "qk_post", "sampler")
 
 
@@ -114,6 +129,10 @@ SIGNATURES = {
     "voxhip_sync": (_I, []),
     "voxhip_decode_dev": (_I, [_I, _I, _I64, _P, _I64, _P, _I, _P, C.POINTER(SampleCfg), _P]),
     "voxhip_decode_steps_dev": (_I, [_I, _P, _P, _I64, _P, _P, _I, _P, C.POINTER(SampleCfg), _P]),
+    "voxhip_f5_create": (_I, [C.POINTER(F5Desc)]),
+    "voxhip_f5_begin": (_I, [_I, _I, _I, _P, _P]),
+    "voxhip_f5_step": (_I, [_I, _P, _P, _P]),
+    "voxhip_f5_end": (_I, [_I]),
     "voxhip_lm_sample_dev": (_I, [_P, C.c_int32, C.POINTER(LmCfg), _I64, _P, C.c_int32, _P, _P]),
     "voxhip_lm_generate": (_I, [_I, _I, _P, _I64, _I, _I, C.POINTER(LmCfg), _P, _P, _P]),
     "voxhip_mat_synthetic": (_I, [_I32, _I64, _I64, _U64, _U32, _F, _F, _I]),
@@ -441,6 +460,36 @@ def lm_generate(xfmr, seq, x, head, speech_emb, cfg, want_logp=False):
         rows = min(n + 1, cfg.max_len)
         logp = logp[:rows]
     return tokens[:n], logp
+
+
+def f5_create(dim, depth, heads, dim_head, ff_mult, mel_dim, text_dim, pe_attn_head, in_proj, norm_out, proj_out, blocks,
+              pos1, pos2):
+    """gpu_f5_create: blocks = list of dicts ada,q,k,v,o,ff1,ff2 -> matrix handles; pos1/pos2 = (w [groups][cout/groups]
+    [K][cin/groups] f32, bias or None, cin, cout, K, groups)."""
+    arr = (F5Block * len(blocks))(*[F5Block(*[b[n] for n in ("ada", "q", "k", "v", "o", "ff1", "ff2")]) for b in blocks])
+    convs, keep = [], []
+    for w, b, cin, cout, K, groups in (pos1, pos2):
+        w = f32(w)
+        b = None if b is None else f32(b)
+        keep += [w, b]
+        convs.append(F5Conv(_p(w), _p(b), cin, cout, K, groups))
+    d = F5Desc(dim, depth, heads, dim_head, ff_mult, mel_dim, text_dim, pe_attn_head, in_proj, norm_out, proj_out, arr,
+               convs[0], convs[1])
+    return _handle(lib().voxhip_f5_create(C.byref(d)), "f5_create")
+
+
+def f5_begin(f5, B, N, cat0, rope):
+    _check(lib().voxhip_f5_begin(f5, B, N, _p(f32(cat0)), _p(f32(rope))), "f5_begin")
+
+
+def f5_step(f5, x, ts, B, N, mel):
+    out = np.empty((B * N, mel), np.float32)
+    _check(lib().voxhip_f5_step(f5, _p(f32(x)), _p(f32(ts)), _p(out)), "f5_step")
+    return out
+
+
+def f5_end(f5):
+    _check(lib().voxhip_f5_end(f5), "f5_end")
 
 
 def sync():
