@@ -142,6 +142,45 @@ def bench_cfg3(vh, synth, steps, warmup):
     return out
 
 
+def bench_cfg4(vh, synth, reps=3):
+    """one F5-TTS DiT step (22 blocks, dim 1024, 16 x 64 heads, N = 1000 frames, f16 weights) on
+    the device, B = 2 (classifier-free guidance, the reference default) and B = 1: f32 MFMA GEMMs for the linears and
+    the grouped position convolutions, f32 MFMA attention tiles. Host wall-clock around gpu_f5_step (median of reps),
+    x / ts upload and the [B][N][100] download included."""
+    dit = synth.DiT(synth.F5_DIT, seed=0)
+    c = dit.cfg
+    N = c["frames"]
+    out = {"workload": "f5-tts DiT step, 22 x 1024, N 1000, f16 weights (BASELINE configs[3])"}
+    for B in (2, 1):
+        rng = np.random.default_rng(B)
+        W = 2 * c["mel"] + c["text"]
+        cat0 = rng.standard_normal((B * N, W)).astype(np.float32)
+        cat0[:, :c["mel"]] = 0.0
+        HH = c["dim_head"] // 2
+        inv = np.array([np.float32(1.0 / 10000.0 ** (2 * j / c["dim_head"])) for j in range(HH)], np.float32)
+        ang = (np.arange(N, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
+        rope = np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
+        x = rng.standard_normal((N, c["mel"])).astype(np.float32)
+        ts = rng.standard_normal(c["dim"]).astype(np.float32)
+        vh.f5_begin(dit.f5, B, N, cat0, rope)
+        vh.f5_step(dit.f5, x, ts, B, N, c["mel"])
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            y = vh.f5_step(dit.f5, x, ts, B, N, c["mel"])
+            times.append((time.perf_counter() - t0) * 1000.0)
+        vh.f5_end(dit.f5)
+        assert np.isfinite(y).all()
+        ms = float(np.median(times))
+        fl = dit.flops(B, N)
+        tot = sum(fl.values())
+        out[f"b{B}"] = {"ms_per_step": round(ms, 3), "gflop": round(tot / 1e9, 1),
+                        "gflop_parts": {k: round(v / 1e9, 1) for k, v in fl.items()},
+                        "tflops": round(tot / (ms * 1e-3) / 1e12, 2),
+                        "frac_f32_mfma": round(tot / (ms * 1e-3) / 1e12 / F32_MFMA_PEAK_TFLOPS, 4)}
+    return out
+
+
 def bench_cfg5(vh, synth, reps=3):
     """the CosyVoice2-0.5B-shaped LM on the device. Prefill: 512 prompt rows (q8 weights on the
     f32-activation MFMA GEMM, as matmul's path above 8 rows). Generation: 256 steps of q8 int8 GEMVs, f32 head + bias,
@@ -277,7 +316,7 @@ def main():
     if not args.no_other:
         t0 = time.perf_counter()
         other = {"configs[0]": bench_cfg1(vh), "configs[2]": bench_cfg3(vh, synth, 100, 10),
-                 "configs[4]": bench_cfg5(vh, synth)}
+                 "configs[3]": bench_cfg4(vh, synth), "configs[4]": bench_cfg5(vh, synth)}
         log(f"other configs: {json.dumps(other)} ({time.perf_counter() - t0:.1f} s)")
 
     cpu = None

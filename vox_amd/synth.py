@@ -116,3 +116,45 @@ class Decoder:
         norms = c["layers"] * (2 * c["hidden"] + (2 * c["head_dim"] if c.get("qk_norm", True) else 0)) * 4 + c["hidden"] * 4
         kv_write = c["layers"] * 2 * kd * 2
         return self.weight_bytes() + kv + norms + kv_write
+
+
+# F5-TTS-shaped DiT: 22 blocks, dim 1024, 16 x 64 heads, FFN 2048 (GELU-tanh), adaLN-zero, mel 100,
+# text 512 (in_proj 712 -> 1024), position convolutions K 31 / 16 groups (f32); f16 linear weights ~N(0, 0.02)
+F5_DIT = dict(dim=1024, depth=22, heads=16, dim_head=64, ff_mult=2, mel=100, text=512, K=31, groups=16, pe_attn_head=0,
+              wtype=vh.F16, frames=1000)
+
+
+class DiT:
+    """A device-resident F5 DiT with synthetic weights (linears generated on the device, convolutions on the host)."""
+
+    def __init__(self, cfg, seed=0):
+        c = dict(cfg)
+        self.cfg = c
+        D, H, HD, FF, mel, text = c["dim"], c["heads"], c["dim_head"], c["dim"] * c["ff_mult"], c["mel"], c["text"]
+        inner = H * HD
+        stream = [0x5000]
+
+        def mat(rows, cols):
+            stream[0] += 1
+            return vh.mat_synthetic(c["wtype"], rows, cols, seed, stream[0], 0.0, 0.02, bias=True)
+        self.in_proj, self.norm_out, self.proj_out = mat(D, 2 * mel + text), mat(2 * D, D), mat(mel, D)
+        self.blocks = [{"ada": mat(6 * D, D), "q": mat(inner, D), "k": mat(inner, D), "v": mat(inner, D), "o": mat(D, inner),
+                        "ff1": mat(FF, D), "ff2": mat(D, FF)} for _ in range(c["depth"])]
+        rng = np.random.default_rng(seed)
+        G, K = c["groups"], c["K"]
+        self.pos = [((rng.standard_normal((G, D // G, K, D // G)) * 0.02).astype(np.float32),
+                     (rng.standard_normal(D) * 0.02).astype(np.float32), D, D, K, G) for _ in range(2)]
+        self.f5 = vh.f5_create(D, c["depth"], H, HD, c["ff_mult"], mel, text, c["pe_attn_head"], self.in_proj, self.norm_out,
+                               self.proj_out, self.blocks, self.pos[0], self.pos[1])
+
+    def flops(self, B, N):
+        """FLOPs of one step (2 per multiply-add): linears, attention, position convolutions, ada / final GEMVs."""
+        c = self.cfg
+        D, HD, H, FF = c["dim"], c["dim_head"], c["heads"], c["dim"] * c["ff_mult"]
+        R, inner = B * N, H * HD
+        lin = 2 * R * c["depth"] * (3 * inner * D + inner * D + 2 * FF * D)
+        att = 4 * B * N * N * HD * H * c["depth"]
+        conv = 2 * 2 * R * D * c["K"] * (D // c["groups"])
+        io = 2 * R * (2 * c["mel"] + c["text"]) * D + 2 * R * D * c["mel"]
+        ada = 2 * c["depth"] * 6 * D * D + 2 * 2 * D * D
+        return {"linears": lin, "attention": att, "pos_conv": conv, "in_out": io, "ada": ada}
