@@ -27,6 +27,7 @@ sys.path.insert(0, ROOT)
 METRIC = "talker decode tok/s (0.6B q8, batch 1); GEMV HBM GB/s as % of peak"
 HBM_PEAK_GBS = 8000.0
 F32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
+F16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 / bf16 matrix peak
 POS = 512
 
 
@@ -144,9 +145,11 @@ def bench_cfg3(vh, synth, steps, warmup):
 
 def bench_cfg4(vh, synth, reps=3):
     """one F5-TTS DiT step (22 blocks, dim 1024, 16 x 64 heads, N = 1000 frames, f16 weights) on
-    the device, B = 2 (classifier-free guidance, the reference default) and B = 1: f32 MFMA GEMMs for the linears and
-    the grouped position convolutions, f32 MFMA attention tiles. Host wall-clock around gpu_f5_step (median of reps),
-    x / ts upload and the [B][N][100] download included."""
+    the device, B = 2 (classifier-free guidance, the reference default) and B = 1. The f16 linears run on the f16
+    matrix cores with the f32 activations split in two f16 halves (two MFMAs per product), the grouped position
+    convolutions and the attention tiles on f32 MFMA. frac_f16_mfma is against the dense f16 peak (the bound of
+    this configuration); frac_f32_mfma against the dense f32 peak. Host wall-clock around gpu_f5_step (median of
+    reps), x / ts upload and the [B][N][100] download included."""
     dit = synth.DiT(synth.F5_DIT, seed=0)
     c = dit.cfg
     N = c["frames"]
@@ -177,6 +180,7 @@ def bench_cfg4(vh, synth, reps=3):
         out[f"b{B}"] = {"ms_per_step": round(ms, 3), "gflop": round(tot / 1e9, 1),
                         "gflop_parts": {k: round(v / 1e9, 1) for k, v in fl.items()},
                         "tflops": round(tot / (ms * 1e-3) / 1e12, 2),
+                        "frac_f16_mfma": round(tot / (ms * 1e-3) / 1e12 / F16_MFMA_PEAK_TFLOPS, 4),
                         "frac_f32_mfma": round(tot / (ms * 1e-3) / 1e12 / F32_MFMA_PEAK_TFLOPS, 4)}
     return out
 
@@ -240,7 +244,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-other", action="store_true", help="skip the configs[0] / configs[2] measurements")
+    ap.add_argument("--no-other", action="store_true", help="skip the configs[0] / [2] / [3] / [4] measurements")
+    ap.add_argument("--only", choices=["configs[0]", "configs[2]", "configs[3]", "configs[4]"],
+                    help="run one of the other BASELINE configurations alone and print its JSON object (for profiling)")
     ap.add_argument("--no-breakdown", action="store_true",
                     help="skip the event-timed per-kernel pass (for runs under rocprofv3, whose tracer does not survive "
                          "HIP events recorded around graph launches); rocprof then times the graph's kernels itself")
@@ -254,6 +260,11 @@ def main():
 
     vh.init("hip:0")
     log("device:", vh.device_name())
+    if args.only:
+        legs = {"configs[0]": lambda: bench_cfg1(vh), "configs[2]": lambda: bench_cfg3(vh, synth, 100, 10),
+                "configs[3]": lambda: bench_cfg4(vh, synth), "configs[4]": lambda: bench_cfg5(vh, synth)}
+        print(json.dumps({args.only: legs[args.only]()}))
+        return
     t0 = time.perf_counter()
     dec = synth.Decoder(synth.TALKER_0_6B, seed=0)
     c = dec.cfg

@@ -77,6 +77,49 @@ VH_DEV void gemm_load_w(const uint8_t *__restrict__ w, const float *__restrict__
     }
 }
 
+// Epilogue of a wave's TM x TN accumulator tiles: lane holds C[row0 + 4 (lane / 16) + v][col], col = col0 + lane % 16.
+template <int EPI, int TM, int TN>
+VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0, int n0, int wm, int wn, int lane) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = n0 + wn * 16 * TN + j * 16 + (lane & 15);
+            const float bz = (g.bias && col < g.n) ? g.bias[col] : 0.f;
+            const float gt = (EPI == EPI_GATED_ACC && col < g.n) ? g.gate[col] : 0.f;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int row = m0 + wm * 16 * TM + i * 16 + 4 * (lane >> 4) + v;
+                const float c = acc[i][j][v] + bz;
+                const bool in = row < g.m && col < g.n;
+                float *dst = g.y + int64_t(row) * g.ldy + col;
+                if (EPI == EPI_SWIGLU) {
+                    const float up = __shfl_xor(c, 1, kWave);  // column col ^ 1 of the same row
+                    if (in && (col & 1) == 0) g.y[int64_t(row) * g.ldy + col / 2] = silu(c) * up;
+                } else if (EPI == EPI_ROPE) {
+                    const float o = __shfl_xor(c, 1, kWave);  // the pair partner (2j <-> 2j + 1)
+                    float r = c;
+                    if (col < g.rope_cols) {
+                        const int inner = g.rope_cols / 2, d = col % g.hd, head = (col % inner) / g.hd;
+                        if (g.rope_heads <= 0 || head < g.rope_heads) {
+                            const float *cs = g.rope + ((int64_t(row % g.seq) * (g.hd / 2) + d / 2) * 2);
+                            const float cc = cs[0], sn = cs[1];
+                            r = (col & 1) ? c * cc + o * sn : c * cc - o * sn;
+                        }
+                    }
+                    if (in) *dst = r;
+                } else if (in) {
+                    if (EPI == EPI_STORE) *dst = c;
+                    else if (EPI == EPI_ACC) *dst += c;
+                    else if (EPI == EPI_GATED_ACC) *dst += gt * c;
+                    else if (EPI == EPI_GELU) *dst = gelu_tanh_f(c);
+                    else if (EPI == EPI_MISH) *dst = mish_f(c);
+                    else if (EPI == EPI_MISH_ACC) *dst += mish_f(c);
+                }
+            }
+        }
+}
+
 // Epilogues: EPI_STORE y = c + bias; EPI_ACC y += c + bias; EPI_SWIGLU W rows are (gate u, up u) pairs, y[u] =
 // silu(gate) * up; EPI_GATED_ACC y += gate[col] * (c + bias); EPI_GELU y = gelu_tanh(c + bias); EPI_MISH
 // y = mish(c + bias); EPI_MISH_ACC y += mish(c + bias); EPI_ROPE y = c + bias with the pairs of q | k rotated.
@@ -149,45 +192,92 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const uint8_t *__restrict__ w,
         __syncthreads();
     }
 
-    // epilogue: lane holds C[row0 + 4 (lane / 16) + v][col] of each tile, col = col0 + lane % 16
+    gemm_epilogue<EPI, TM, TN>(acc, g, m0, n0, wm, wn, lane);
+}
+
+typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4v __attribute__((ext_vector_type(4)));
+constexpr int kH16Ld = kGemmBK + 8;  // LDS row stride in halves
+
+// F16 weights on the f16 matrix cores with the f32 activations split in two halves: a = hi + lo with
+// hi = f16(a), lo = f16(a - hi), so W a = W hi + W lo. The weights are exact in f16 and every f16 x f16 product is
+// exact in the f32 accumulator, so the result keeps the activations to about 2^-22 relative: the f32 path's
+// products up to the summation order (v_mfma_f32_16x16x32_f16, two per tile and K step). Activations must stay
+// below 65504 in magnitude (f16 range). Same tiling, prefetch and epilogues as k_gemm_f32; MFMA lane layouts
+// (checked on gfx950): A 16x32 -> lane l holds A[l % 16][8 (l / 16) + e]; B 32x16 -> lane l holds
+// B[8 (l / 16) + e][l % 16]; D as the f32 MFMA.
+template <int EPI, int TM, int TN>
+__global__ __launch_bounds__(256) void k_gemm_h16(const uint8_t *__restrict__ w, const float *__restrict__ A, GemmArgs g) {
+    constexpr int BM = 32 * TM, BN = 32 * TN;
+    constexpr int AQ = BM * kGemmBK / 4 / 256;  // f32x4 A loads per thread and K step
+    constexpr int WQ = BN * kGemmBK / 8 / 256;  // 8-half W loads per thread and K step
+    __shared__ __align__(16) _Float16 Ah[BM][kH16Ld];
+    __shared__ __align__(16) _Float16 Al[BM][kH16Ld];
+    __shared__ __align__(16) _Float16 Bs[BN][kH16Ld];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int K = g.K;
+    f32x4v acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int col = n0 + wn * 16 * TN + j * 16 + (lane & 15);
-            const float bz = (g.bias && col < g.n) ? g.bias[col] : 0.f;
-            const float gt = (EPI == EPI_GATED_ACC && col < g.n) ? g.gate[col] : 0.f;
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    f32x4v ra[AQ];
+    u32x4 rw[WQ];
+    auto fetch = [&](int k0) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int row = m0 + wm * 16 * TM + i * 16 + 4 * (lane >> 4) + v;
-                const float c = acc[i][j][v] + bz;
-                const bool in = row < g.m && col < g.n;
-                float *dst = g.y + int64_t(row) * g.ldy + col;
-                if (EPI == EPI_SWIGLU) {
-                    const float up = __shfl_xor(c, 1, kWave);  // column col ^ 1 of the same row
-                    if (in && (col & 1) == 0) g.y[int64_t(row) * g.ldy + col / 2] = silu(c) * up;
-                } else if (EPI == EPI_ROPE) {
-                    const float o = __shfl_xor(c, 1, kWave);  // the pair partner (2j <-> 2j + 1)
-                    float r = c;
-                    if (col < g.rope_cols) {
-                        const int inner = g.rope_cols / 2, d = col % g.hd, head = (col % inner) / g.hd;
-                        if (g.rope_heads <= 0 || head < g.rope_heads) {
-                            const float *cs = g.rope + ((int64_t(row % g.seq) * (g.hd / 2) + d / 2) * 2);
-                            const float cc = cs[0], sn = cs[1];
-                            r = (col & 1) ? c * cc + o * sn : c * cc - o * sn;
-                        }
-                    }
-                    if (in) *dst = r;
-                } else if (in) {
-                    if (EPI == EPI_STORE) *dst = c;
-                    else if (EPI == EPI_ACC) *dst += c;
-                    else if (EPI == EPI_GATED_ACC) *dst += gt * c;
-                    else if (EPI == EPI_GELU) *dst = gelu_tanh_f(c);
-                    else if (EPI == EPI_MISH) *dst = mish_f(c);
-                    else if (EPI == EPI_MISH_ACC) *dst += mish_f(c);
-                }
-            }
+        for (int q = 0; q < AQ; ++q) {
+            const int idx = tid + 256 * q;
+            ra[q] = gemm_load_a<ASRC_ROWS>(A, g, m0 + (idx >> 3), k0 + (idx & 7) * 4);
         }
+#pragma unroll
+        for (int q = 0; q < WQ; ++q) {
+            const int idx = tid + 256 * q, row = n0 + (idx >> 2), k = k0 + (idx & 3) * 8;
+            rw[q] = u32x4{0u, 0u, 0u, 0u};
+            if (row < g.n && k < K) rw[q] = *reinterpret_cast<const u32x4 *>(w + (int64_t(row) * K + k) * 2);
+        }
+    };
+    fetch(0);
+    for (int k0 = 0; k0 < K; k0 += kGemmBK) {
+#pragma unroll
+        for (int q = 0; q < AQ; ++q) {
+            const int idx = tid + 256 * q, r = idx >> 3, c = (idx & 7) * 4;
+            f16x4v hi, lo;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                hi[e] = _Float16(ra[q][e]);
+                lo[e] = _Float16(ra[q][e] - float(hi[e]));
+            }
+            *reinterpret_cast<f16x4v *>(&Ah[r][c]) = hi;
+            *reinterpret_cast<f16x4v *>(&Al[r][c]) = lo;
+        }
+#pragma unroll
+        for (int q = 0; q < WQ; ++q) {
+            const int idx = tid + 256 * q;
+            *reinterpret_cast<u32x4 *>(&Bs[idx >> 2][(idx & 3) * 8]) = rw[q];
+        }
+        __syncthreads();
+        if (k0 + kGemmBK < K) fetch(k0 + kGemmBK);  // in flight during the MFMAs below
+        f16x8v ah[TM], al[TM], b[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int r = wm * 16 * TM + i * 16 + (lane & 15);
+            ah[i] = *reinterpret_cast<const f16x8v *>(&Ah[r][8 * (lane >> 4)]);
+            al[i] = *reinterpret_cast<const f16x8v *>(&Al[r][8 * (lane >> 4)]);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            b[j] = *reinterpret_cast<const f16x8v *>(&Bs[wn * 16 * TN + j * 16 + (lane & 15)][8 * (lane >> 4)]);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], acc[i][j], 0, 0, 0);
+            }
+        __syncthreads();
+    }
+    gemm_epilogue<EPI, TM, TN>(acc, g, m0, n0, wm, wn, lane);
 }
 
 // Merge of the kAttnMaxSplits attention partials of m rows into ao [m][heads * hd] (the PRO_ATTN prologue of the
