@@ -49,7 +49,11 @@ __global__ __launch_bounds__(256) void k_f5_fill_x(const float *__restrict__ x, 
 // Non-causal softmax attention of one head over N keys (f5.cpp:626-650): S = (q . k) * scale, softmax per row,
 // O = P V, for head_dim 64. grid (ceil(N / 64), heads, B), block 256: each wave takes 16 query rows; key tiles of
 // 64 go through LDS; an online softmax (running max and sum per row, O rescaled) replaces the reference's
-// whole-row max, which changes only the rounding. MFMA 16x16x4 f32 for S and for P V.
+// whole-row max, which changes only the rounding.
+// Both products run on the f16 matrix cores (v_mfma_f32_16x16x32_f16) with every f32 operand split in two f16
+// halves, x = hi + lo, and three products per pair (hi.hi + hi.lo + lo.hi; the dropped lo.lo term is below 2^-22
+// relative): each product is exact in the f32 accumulator, so S and P V keep f32-level accuracy. Q, K and P are
+// O(1) after the projections and the softmax, well inside the f16 range.
 struct F5AttnArgs {
     const float *qkv;  // [B N][ld] rows: q | k | v, head h at column h * 64 of each
     float *out;        // [B N][ldo], head h at column h * 64
@@ -57,21 +61,47 @@ struct F5AttnArgs {
     float scale;
 };
 constexpr int kF5Hd = kF5HeadDim;
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
+constexpr int kF5Ld = 64 + 8;  // LDS row stride in halves
+VH_DEV void split_f16(float x, _Float16 &hi, _Float16 &lo) {
+    hi = _Float16(x);
+    lo = _Float16(x - float(hi));
+}
+VH_DEV f32x4a mfma3(h16x8 ah, h16x8 al, h16x8 bh, h16x8 bl, f32x4a c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, c, 0, 0, 0);
+}
 __global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
-    __shared__ __align__(16) float Ks[64][68];   // [key][d], stride 68: the S operand reads are conflict-free
-    __shared__ __align__(16) float Vs[64][80];   // [key][d], stride 80: the P V operand reads are conflict-free
-    __shared__ __align__(16) float Ps[4][16][68];
+    __shared__ __align__(16) _Float16 Kh[64][kF5Ld], Kl[64][kF5Ld];     // [key][d]
+    __shared__ __align__(16) _Float16 Vh[64][kF5Ld], Vl[64][kF5Ld];     // [d][key] (transposed)
+    __shared__ __align__(16) _Float16 Ph[4][16][kF5Ld], Pl[4][16][kF5Ld];  // per wave [row][key]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
     const int q0 = blockIdx.x * 64, h = blockIdx.y;
     const int64_t rb = int64_t(blockIdx.z) * a.N;
     const float *Q = a.qkv + int64_t(h) * kF5Hd, *Kp = a.qkv + a.inner + int64_t(h) * kF5Hd,
                 *Vp = a.qkv + 2 * int64_t(a.inner) + int64_t(h) * kF5Hd;
-    // A operand of S: lane holds Q[16 wave + lr][4 s + lg], s < 16
-    float qa[16];
+    // A operand of S, two K steps of 32 dims: lane holds Q[16 wave + lr][32 c + 8 lg + e] as hi / lo halves
+    h16x8 qh[2], ql[2];
     {
         const int qr = q0 + 16 * wave + lr;
 #pragma unroll
-        for (int s = 0; s < 16; ++s) qa[s] = qr < a.N ? Q[(rb + qr) * a.ld + 4 * s + lg] : 0.f;
+        for (int c = 0; c < 2; ++c) {
+            f32x4a x0 = {0.f, 0.f, 0.f, 0.f}, x1 = {0.f, 0.f, 0.f, 0.f};
+            if (qr < a.N) {
+                x0 = *reinterpret_cast<const f32x4a *>(Q + (rb + qr) * a.ld + 32 * c + 8 * lg);
+                x1 = *reinterpret_cast<const f32x4a *>(Q + (rb + qr) * a.ld + 32 * c + 8 * lg + 4);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                _Float16 hi, lo;
+                split_f16(x0[e], hi, lo);
+                qh[c][e] = hi; ql[c][e] = lo;
+                split_f16(x1[e], hi, lo);
+                qh[c][e + 4] = hi; ql[c][e + 4] = lo;
+            }
+        }
     }
     float mrow[4], lrow[4];
     f32x4a o[4];
@@ -86,17 +116,33 @@ __global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
                 kv = *reinterpret_cast<const f32x4a *>(Kp + (rb + kt + key) * a.ld + d4);
                 vv = *reinterpret_cast<const f32x4a *>(Vp + (rb + kt + key) * a.ld + d4);
             }
-            *reinterpret_cast<f32x4a *>(&Ks[key][d4]) = kv;
-            *reinterpret_cast<f32x4a *>(&Vs[key][d4]) = vv;
+            h16x4 khi, klo;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                _Float16 hi, lo;
+                split_f16(kv[e], hi, lo);
+                khi[e] = hi; klo[e] = lo;
+                _Float16 vhi, vlo;
+                split_f16(vv[e], vhi, vlo);
+                Vh[d4 + e][key] = vhi;
+                Vl[d4 + e][key] = vlo;
+            }
+            *reinterpret_cast<h16x4 *>(&Kh[key][d4]) = khi;
+            *reinterpret_cast<h16x4 *>(&Kl[key][d4]) = klo;
         }
         __syncthreads();
+        // S tiles: B operand lane holds K[16 j + lr][32 c + 8 lg + e]
         f32x4a s[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) s[j] = f32x4a{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 4; ++j) {
+            s[j] = f32x4a{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int st = 0; st < 16; ++st)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[st], Ks[16 * j + lr][4 * st + lg], s[j], 0, 0, 0);
+            for (int c = 0; c < 2; ++c) {
+                const h16x8 bh = *reinterpret_cast<const h16x8 *>(&Kh[16 * j + lr][32 * c + 8 * lg]);
+                const h16x8 bl = *reinterpret_cast<const h16x8 *>(&Kl[16 * j + lr][32 * c + 8 * lg]);
+                s[j] = mfma3(qh[c], ql[c], bh, bl, s[j]);
+            }
+        }
         // lane holds S[4 lg + i][16 j + lr]: the 16 lanes of a DPP row share the rows
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -118,7 +164,10 @@ __global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
             for (int j = 0; j < 4; ++j) {
                 const float p = expf(s[j][i] - mnew);
                 sum += p;
-                Ps[wave][4 * lg + i][16 * j + lr] = p;
+                _Float16 phi, plo;
+                split_f16(p, phi, plo);
+                Ph[wave][4 * lg + i][16 * j + lr] = phi;
+                Pl[wave][4 * lg + i][16 * j + lr] = plo;
             }
             sum += dpp<kDppXor1>(sum);
             sum += dpp<kDppXor2>(sum);
@@ -130,11 +179,17 @@ __global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
             for (int dt = 0; dt < 4; ++dt) o[dt][i] *= alpha;
         }
         __syncthreads();
+        // O += P V: A lane holds P[lr][32 c + 8 lg + e]; B lane holds V[32 c + 8 lg + e][16 dt + lr] (= Vt rows)
 #pragma unroll
-        for (int kk = 0; kk < 64; kk += 4) {
-            const float pa = Ps[wave][lr][kk + lg];
+        for (int c = 0; c < 2; ++c) {
+            const h16x8 pah = *reinterpret_cast<const h16x8 *>(&Ph[wave][lr][32 * c + 8 * lg]);
+            const h16x8 pal = *reinterpret_cast<const h16x8 *>(&Pl[wave][lr][32 * c + 8 * lg]);
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, Vs[kk + lg][16 * dt + lr], o[dt], 0, 0, 0);
+            for (int dt = 0; dt < 4; ++dt) {
+                const h16x8 bh = *reinterpret_cast<const h16x8 *>(&Vh[16 * dt + lr][32 * c + 8 * lg]);
+                const h16x8 bl = *reinterpret_cast<const h16x8 *>(&Vl[16 * dt + lr][32 * c + 8 * lg]);
+                o[dt] = mfma3(pah, pal, bh, bl, o[dt]);
+            }
         }
         __syncthreads();
     }
