@@ -12,11 +12,11 @@ static hipError_t gemm_run(const uint8_t *w, const float *scale, const float *A,
     return launch(k_gemm_f32<WT, EPI, ASRC, T, T>, grid, dim3(256), 0, s, w, scale, A, g);
 }
 
-template <int EPI, int T>
+template <int EPI, int TM, int TN>
 static hipError_t gemm_run_h16(const uint8_t *w, const float *A, const GemmArgs &g, hipStream_t s) {
-    constexpr int B = 32 * T;
-    const dim3 grid((g.n + B - 1) / B, (g.m + B - 1) / B);
-    return launch(k_gemm_h16<EPI, T, T>, grid, dim3(256), 0, s, w, A, g);
+    constexpr int BM = 32 * TM, BN = 32 * TN;
+    const dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM);
+    return launch(k_gemm_h16<EPI, TM, TN, 64>, grid, dim3(256), 0, s, w, A, g);
 }
 
 // 128 x 128 block tiles when they still give a full wave of blocks, else 64 x 64. F16 weights take the split-f16
@@ -25,8 +25,9 @@ template <int WT, int EPI>
 static hipError_t gemm_tile(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s) {
     const bool big = int64_t((g.n + 127) / 128) * ((g.m + 127) / 128) >= 256;
     if constexpr (WT == WT_F16) {
-        if (big) return gemm_run_h16<EPI, 4>(w, A, g, s);
-        return gemm_run_h16<EPI, 2>(w, A, g, s);
+        if (big) return gemm_run_h16<EPI, 4, 4>(w, A, g, s);
+        if (int64_t((g.n + 63) / 64) * ((g.m + 127) / 128) >= 256) return gemm_run_h16<EPI, 4, 2>(w, A, g, s);
+        return gemm_run_h16<EPI, 2, 2>(w, A, g, s);
     } else {
         if (big) return gemm_run<WT, EPI, ASRC_ROWS, 4>(w, scale, A, g, 1, s);
         return gemm_run<WT, EPI, ASRC_ROWS, 2>(w, scale, A, g, 1, s);

@@ -197,23 +197,23 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const uint8_t *__restrict__ w,
 
 typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4v __attribute__((ext_vector_type(4)));
-constexpr int kH16Ld = kGemmBK + 8;  // LDS row stride in halves
 
 // F16 weights on the f16 matrix cores with the f32 activations split in two halves: a = hi + lo with
 // hi = f16(a), lo = f16(a - hi), so W a = W hi + W lo. The weights are exact in f16 and every f16 x f16 product is
 // exact in the f32 accumulator, so the result keeps the activations to about 2^-22 relative: the f32 path's
-// products up to the summation order (v_mfma_f32_16x16x32_f16, two per tile and K step). Activations must stay
-// below 65504 in magnitude (f16 range). Same tiling, prefetch and epilogues as k_gemm_f32; MFMA lane layouts
-// (checked on gfx950): A 16x32 -> lane l holds A[l % 16][8 (l / 16) + e]; B 32x16 -> lane l holds
-// B[8 (l / 16) + e][l % 16]; D as the f32 MFMA.
-template <int EPI, int TM, int TN>
+// products up to the summation order (v_mfma_f32_16x16x32_f16, two per tile and 32-deep K step). Activations must
+// stay below 65504 in magnitude (f16 range). Tiles and epilogues as k_gemm_f32, K steps of BK (32 or 64) staged
+// through LDS with the next step's global loads in flight. MFMA lane layouts (checked on gfx950): A 16x32 -> lane l
+// holds A[l % 16][8 (l / 16) + e]; B 32x16 -> lane l holds B[8 (l / 16) + e][l % 16]; D as the f32 MFMA.
+template <int EPI, int TM, int TN, int BK>
 __global__ __launch_bounds__(256) void k_gemm_h16(const uint8_t *__restrict__ w, const float *__restrict__ A, GemmArgs g) {
-    constexpr int BM = 32 * TM, BN = 32 * TN;
-    constexpr int AQ = BM * kGemmBK / 4 / 256;  // f32x4 A loads per thread and K step
-    constexpr int WQ = BN * kGemmBK / 8 / 256;  // 8-half W loads per thread and K step
-    __shared__ __align__(16) _Float16 Ah[BM][kH16Ld];
-    __shared__ __align__(16) _Float16 Al[BM][kH16Ld];
-    __shared__ __align__(16) _Float16 Bs[BN][kH16Ld];
+    constexpr int BM = 32 * TM, BN = 32 * TN, LD = BK + 8;  // LDS row stride in halves
+    constexpr int AQ = BM * BK / 4 / 256;  // f32x4 A loads per thread and K step
+    constexpr int WQ = BN * BK / 8 / 256;  // 8-half W loads per thread and K step
+    constexpr int CPR = BK / 4, WPR = BK / 8;  // f32x4 / 8-half chunks per row
+    __shared__ __align__(16) _Float16 Ah[BM][LD];
+    __shared__ __align__(16) _Float16 Al[BM][LD];
+    __shared__ __align__(16) _Float16 Bs[BN][LD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int K = g.K;
@@ -228,20 +228,20 @@ __global__ __launch_bounds__(256) void k_gemm_h16(const uint8_t *__restrict__ w,
 #pragma unroll
         for (int q = 0; q < AQ; ++q) {
             const int idx = tid + 256 * q;
-            ra[q] = gemm_load_a<ASRC_ROWS>(A, g, m0 + (idx >> 3), k0 + (idx & 7) * 4);
+            ra[q] = gemm_load_a<ASRC_ROWS>(A, g, m0 + idx / CPR, k0 + (idx % CPR) * 4);
         }
 #pragma unroll
         for (int q = 0; q < WQ; ++q) {
-            const int idx = tid + 256 * q, row = n0 + (idx >> 2), k = k0 + (idx & 3) * 8;
+            const int idx = tid + 256 * q, row = n0 + idx / WPR, k = k0 + (idx % WPR) * 8;
             rw[q] = u32x4{0u, 0u, 0u, 0u};
             if (row < g.n && k < K) rw[q] = *reinterpret_cast<const u32x4 *>(w + (int64_t(row) * K + k) * 2);
         }
     };
     fetch(0);
-    for (int k0 = 0; k0 < K; k0 += kGemmBK) {
+    for (int k0 = 0; k0 < K; k0 += BK) {
 #pragma unroll
         for (int q = 0; q < AQ; ++q) {
-            const int idx = tid + 256 * q, r = idx >> 3, c = (idx & 7) * 4;
+            const int idx = tid + 256 * q, r = idx / CPR, c = (idx % CPR) * 4;
             f16x4v hi, lo;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -254,27 +254,30 @@ __global__ __launch_bounds__(256) void k_gemm_h16(const uint8_t *__restrict__ w,
 #pragma unroll
         for (int q = 0; q < WQ; ++q) {
             const int idx = tid + 256 * q;
-            *reinterpret_cast<u32x4 *>(&Bs[idx >> 2][(idx & 3) * 8]) = rw[q];
+            *reinterpret_cast<u32x4 *>(&Bs[idx / WPR][(idx % WPR) * 8]) = rw[q];
         }
         __syncthreads();
-        if (k0 + kGemmBK < K) fetch(k0 + kGemmBK);  // in flight during the MFMAs below
-        f16x8v ah[TM], al[TM], b[TN];
+        if (k0 + BK < K) fetch(k0 + BK);  // in flight during the MFMAs below
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const int r = wm * 16 * TM + i * 16 + (lane & 15);
-            ah[i] = *reinterpret_cast<const f16x8v *>(&Ah[r][8 * (lane >> 4)]);
-            al[i] = *reinterpret_cast<const f16x8v *>(&Al[r][8 * (lane >> 4)]);
-        }
+        for (int kk = 0; kk < BK; kk += 32) {
+            f16x8v ah[TM], al[TM], b[TN];
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-            b[j] = *reinterpret_cast<const f16x8v *>(&Bs[wn * 16 * TN + j * 16 + (lane & 15)][8 * (lane >> 4)]);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < TM; ++i) {
+                const int r = wm * 16 * TM + i * 16 + (lane & 15);
+                ah[i] = *reinterpret_cast<const f16x8v *>(&Ah[r][kk + 8 * (lane >> 4)]);
+                al[i] = *reinterpret_cast<const f16x8v *>(&Al[r][kk + 8 * (lane >> 4)]);
             }
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                b[j] = *reinterpret_cast<const f16x8v *>(&Bs[wn * 16 * TN + j * 16 + (lane & 15)][kk + 8 * (lane >> 4)]);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], acc[i][j], 0, 0, 0);
+                }
+        }
         __syncthreads();
     }
     gemm_epilogue<EPI, TM, TN>(acc, g, m0, n0, wm, wn, lane);
