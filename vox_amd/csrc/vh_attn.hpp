@@ -82,7 +82,8 @@ struct AttnSmem {
     float o[NGRP][G][HD];
 };
 
-// grid (kAttnMaxSplits, kv_heads, m), block 256. Each lane holds 8 consecutive elements of one key row;
+// grid (kAttnMaxSplits, kv_heads x group / G, m), block 256. A block takes G of the group's query heads (all of
+// them, or a subgroup when there are few kv heads, so that more blocks share the work). Each lane holds 8 consecutive elements of one key row;
 // LPK = HD / 8 lanes share a key, a wave covers 64 / LPK keys per step, a block NGRP keys. Split s takes the keys
 // j = s + S (grp + NGRP u). Row 0's cache bases, the q|k|v input and the RoPE rows are leading scalar arguments
 // (preloaded with the dispatch): the first kAttnSpecKeys keys' loads go out before the row's position arrives and
@@ -97,7 +98,9 @@ __global__ __launch_bounds__(256) void k_attn(const _Float16 *kc0, const _Float1
     constexpr int NQ = (G * HALF + 255) / 256;  // q rotate-half pairs per thread
     extern __shared__ __align__(16) uint8_t attn_smem[];
     Sm &sm = *reinterpret_cast<Sm *>(attn_smem);
-    const int s = blockIdx.x, g = blockIdx.y, i = blockIdx.z, tid = threadIdx.x;
+    const int s = blockIdx.x, i = blockIdx.z, tid = threadIdx.x;
+    // blockIdx.y = kv head x (group / G) + query-head subgroup: this block's query heads are h0 .. h0 + G - 1
+    const int hsplit = a.group / G, g = blockIdx.y / hsplit, hs = blockIdx.y % hsplit, h0 = g * a.group + hs * G;
     const int lane = tid & 63, wave = tid >> 6, sub = lane % LPK, grp = wave * KPW + lane / LPK;
     const AttnPartials &P = a.part;
     const int qd = P.heads * HD, kd = a.kv_heads * HD;
@@ -127,8 +130,8 @@ __global__ __launch_bounds__(256) void k_attn(const _Float16 *kc0, const _Float1
             const int t = tid + 256 * k, h = t / HALF, p = t % HALF;
             qx0[k] = qx1[k] = qc[k] = qsn[k] = 0.f;
             if (t < G * HALF) {
-                qx0[k] = row[(g * G + h) * HD + p];
-                qx1[k] = row[(g * G + h) * HD + p + HALF];
+                qx0[k] = row[(h0 + h) * HD + p];
+                qx1[k] = row[(h0 + h) * HD + p + HALF];
                 qc[k] = cs[2 * p];
                 qsn[k] = cs[2 * p + 1];
             }
@@ -145,7 +148,7 @@ __global__ __launch_bounds__(256) void k_attn(const _Float16 *kc0, const _Float1
     }
     const RowRef rr = P.rows[i];
     const int64_t n = rr.pos + 1;
-    const int64_t pb = (int64_t(i) * P.heads + g * G) * kAttnMaxSplits + s;  // + h * kAttnMaxSplits
+    const int64_t pb = (int64_t(i) * P.heads + h0) * kAttnMaxSplits + s;  // + h * kAttnMaxSplits
     if (s >= n) {  // no keys in this split
         for (int t = tid; t < G * HD; t += 256) {
             const int h = t / HD, e = t % HD;
@@ -183,12 +186,14 @@ __global__ __launch_bounds__(256) void k_attn(const _Float16 *kc0, const _Float1
             const int p = tid - 192;
             norm_rope<HALF>(kx0, kx1, a.kn, p, a.eps, kc, ksn);
             const _Float16 k0h = _Float16(kx0), k1h = _Float16(kx1), v0h = _Float16(vx0), v1h = _Float16(vx1);
-            const int64_t off = rr.pos * HD;
-            _Float16 *Kw = rr.k + plane * rr.cap, *Vw = rr.v + plane * rr.cap;
-            Kw[off + p] = k0h;
-            Kw[off + p + HALF] = k1h;
-            Vw[off + p] = v0h;
-            Vw[off + p + HALF] = v1h;
+            if (hs == 0) {  // one block of the kv head appends the new key/value
+                const int64_t off = rr.pos * HD;
+                _Float16 *Kw = rr.k + plane * rr.cap, *Vw = rr.v + plane * rr.cap;
+                Kw[off + p] = k0h;
+                Kw[off + p + HALF] = k1h;
+                Vw[off + p] = v0h;
+                Vw[off + p + HALF] = v1h;
+            }
             sm.knew[p] = float(k0h);
             sm.knew[p + HALF] = float(k1h);
             sm.vnew[p] = float(v0h);
@@ -197,7 +202,7 @@ __global__ __launch_bounds__(256) void k_attn(const _Float16 *kc0, const _Float1
     } else {
         for (int t = tid; t < G * HD; t += 256) {
             const int h = t / HD, e = t % HD;
-            sm.q[h][e] = a.q[int64_t(i) * qd + (g * G + h) * HD + e];
+            sm.q[h][e] = a.q[int64_t(i) * qd + (h0 + h) * HD + e];
         }
     }
     __syncthreads();

@@ -68,7 +68,7 @@ struct AttnLaunch {
 template <int HD, int G>
 static hipError_t attn_hg(const AttnArgs &a, const AttnLaunch &l, int m, bool fused, hipStream_t s) {
     const size_t smem = sizeof(AttnSmem<HD, G>);
-    const dim3 grid(kAttnMaxSplits, a.kv_heads, m);
+    const dim3 grid(kAttnMaxSplits, a.kv_heads * (a.group / G), m);
     if (fused) {
         hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_attn<HD, G, true>), smem);
         if (e != hipSuccess) return e;
@@ -79,9 +79,22 @@ static hipError_t attn_hg(const AttnArgs &a, const AttnLaunch &l, int m, bool fu
     return launch(k_attn<HD, G, false>, grid, dim3(256), smem, s, l.kc0, l.vc0, l.qkv, l.rope_rows, l.cap0, l.layer, a);
 }
 
+// Query heads per block: the whole group, or, when there are few kv heads, the largest divisor of the group that
+// gives at least kAttnMinBlocks blocks per row (more blocks share the work; each reads its kv head's keys).
+constexpr int kAttnMinBlocks = 64;
+static int attn_heads_per_block(int kv_heads, int group) {
+    int gb = group;
+    while (gb > 1 && kv_heads * (group / gb) * kAttnMaxSplits < kAttnMinBlocks) {
+        int d = gb - 1;
+        while (d > 1 && group % d) --d;
+        gb = d;
+    }
+    return gb;
+}
+
 template <int HD>
-static hipError_t attn_h(const AttnArgs &a, const AttnLaunch &l, int group, int m, bool fused, hipStream_t s) {
-    switch (group) {
+static hipError_t attn_h(const AttnArgs &a, const AttnLaunch &l, int m, bool fused, hipStream_t s) {
+    switch (attn_heads_per_block(a.kv_heads, a.group)) {
         case 1: return attn_hg<HD, 1>(a, l, m, fused, s);
         case 2: return attn_hg<HD, 2>(a, l, m, fused, s);
         case 3: return attn_hg<HD, 3>(a, l, m, fused, s);
@@ -98,9 +111,12 @@ hipError_t launch_attention(const AttnArgs &a, const _Float16 *kc0, const _Float
                             const float *rope_rows, int layer, int hd, int group, int m, bool fused, hipStream_t s) {
     if (m <= 0) return hipSuccess;
     if (cap0 <= 0 || cap0 > INT32_MAX) return hipErrorInvalidValue;
+    if (group < 1 || group > 8) return hipErrorInvalidValue;
     const AttnLaunch l{kc0, vc0, qkv, rope_rows, int32_t(cap0), int32_t(layer)};
-    if (hd == 128) return attn_h<128>(a, l, group, m, fused, s);
-    if (hd == 64) return attn_h<64>(a, l, group, m, fused, s);
+    AttnArgs ag = a;
+    ag.group = group;
+    if (hd == 128) return attn_h<128>(ag, l, m, fused, s);
+    if (hd == 64) return attn_h<64>(ag, l, m, fused, s);
     return hipErrorInvalidValue;
 }
 

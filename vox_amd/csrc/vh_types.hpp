@@ -75,6 +75,7 @@ struct AttnArgs {
     const float *qn, *kn;
     AttnPartials part;
     int32_t kv_heads;
+    int32_t group;           // query heads per kv head (a block takes G of them: group / G blocks per kv head)
     float scale, eps;
 };
 
