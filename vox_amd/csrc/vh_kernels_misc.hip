@@ -81,7 +81,7 @@ static hipError_t attn_hg(const AttnArgs &a, const AttnLaunch &l, int m, bool fu
 
 // Query heads per block: the whole group, or, when there are few kv heads, the largest divisor of the group that
 // gives at least kAttnMinBlocks blocks per row (more blocks share the work; each reads its kv head's keys).
-constexpr int kAttnMinBlocks = 64;
+constexpr int kAttnMinBlocks = 128;
 static int attn_heads_per_block(int kv_heads, int group) {
     int gb = group;
     while (gb > 1 && kv_heads * (group / gb) * kAttnMaxSplits < kAttnMinBlocks) {
