@@ -1,5 +1,7 @@
 // Instantiations of the f32 MFMA GEMM (multi-row passes, DiT linears, grouped convolutions) and the
 // attention-partials merge.
+#include <algorithm>
+
 #include "vh_gemm.hpp"
 #include "vh_launch.hpp"
 
@@ -12,22 +14,51 @@ static hipError_t gemm_run(const uint8_t *w, const float *scale, const float *A,
     return launch(k_gemm_f32<WT, EPI, ASRC, T, T>, grid, dim3(256), 0, s, w, scale, A, g);
 }
 
-template <int EPI, int TM, int TN>
-static hipError_t gemm_run_h16(const uint8_t *w, const float *A, const GemmArgs &g, hipStream_t s) {
+template <int WT, int EPI, int TM, int TN>
+static hipError_t gemm_run_h16(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s) {
     constexpr int BM = 32 * TM, BN = 32 * TN;
     const dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM);
-    return launch(k_gemm_h16<EPI, TM, TN, 64>, grid, dim3(256), 0, s, w, A, g);
+    return launch(k_gemm_h16<WT, EPI, TM, TN, 64>, grid, dim3(256), 0, s, w, scale, A, g);
 }
 
-// 128 x 128 block tiles when they still give a full wave of blocks, else 64 x 64. F16 weights take the split-f16
-// matrix cores.
+// Split K for a grid of 64 x 64 tiles too small to fill the CUs with a long K (prefill down projections, small
+// matrices): up to 8 slices of K, each a multiple of 64 columns, summed in order by the reduce pass.
+template <int WT, int EPI>
+static hipError_t gemm_splitk(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s, bool *done) {
+    *done = false;
+    if constexpr (EPI != EPI_STORE && EPI != EPI_ACC && EPI != EPI_GATED_ACC && EPI != EPI_SWIGLU) {
+        return hipSuccess;
+    } else {
+    const int64_t blocks = int64_t((g.n + 63) / 64) * ((g.m + 63) / 64);
+    if (!g.ws || blocks >= 192 || g.K < 512) return hipSuccess;
+    int splits = int(std::min<int64_t>(8, (256 + blocks - 1) / blocks));
+    const int kchunk = ((g.K + splits - 1) / splits + 63) / 64 * 64;
+    splits = (g.K + kchunk - 1) / kchunk;
+    if (splits < 2 || int64_t(splits) * g.m * g.n > g.ws_cap) return hipSuccess;
+    GemmArgs gs = g;
+    gs.kchunk = kchunk;
+    const dim3 grid((g.n + 63) / 64, (g.m + 63) / 64, splits);
+    hipError_t e = launch(k_gemm_h16<WT, EPI_STORE, 2, 2, 64>, grid, dim3(256), 0, s, w, scale, A, gs);
+    if (e != hipSuccess) return e;
+    const int nout = EPI == EPI_SWIGLU ? g.n / 2 : g.n;
+    const int64_t total = int64_t(g.m) * nout;
+    *done = true;
+    return launch(k_gemm_splitk_reduce<EPI>, dim3(unsigned((total + 255) / 256)), dim3(256), 0, s, g, int32_t(splits));
+    }
+}
+
+// 128 x 128 block tiles when they still give a full wave of blocks, else 128 x 64 or 64 x 64 (split K when even
+// those leave the CUs idle). F16 and Q8 weights take the split-f16 matrix cores.
 template <int WT, int EPI>
 static hipError_t gemm_tile(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s) {
     const bool big = int64_t((g.n + 127) / 128) * ((g.m + 127) / 128) >= 256;
-    if constexpr (WT == WT_F16) {
-        if (big) return gemm_run_h16<EPI, 4, 4>(w, A, g, s);
-        if (int64_t((g.n + 63) / 64) * ((g.m + 127) / 128) >= 256) return gemm_run_h16<EPI, 4, 2>(w, A, g, s);
-        return gemm_run_h16<EPI, 2, 2>(w, A, g, s);
+    if constexpr (WT == WT_F16 || WT == WT_Q8) {
+        bool split = false;
+        hipError_t e = gemm_splitk<WT, EPI>(w, scale, A, g, s, &split);
+        if (e != hipSuccess || split) return e;
+        if (big) return gemm_run_h16<WT, EPI, 4, 4>(w, scale, A, g, s);
+        if (int64_t((g.n + 63) / 64) * ((g.m + 127) / 128) >= 256) return gemm_run_h16<WT, EPI, 4, 2>(w, scale, A, g, s);
+        return gemm_run_h16<WT, EPI, 2, 2>(w, scale, A, g, s);
     } else {
         if (big) return gemm_run<WT, EPI, ASRC_ROWS, 4>(w, scale, A, g, 1, s);
         return gemm_run<WT, EPI, ASRC_ROWS, 2>(w, scale, A, g, 1, s);

@@ -198,47 +198,67 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const uint8_t *__restrict__ w,
 typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4v __attribute__((ext_vector_type(4)));
 
-// F16 weights on the f16 matrix cores with the f32 activations split in two halves: a = hi + lo with
-// hi = f16(a), lo = f16(a - hi), so W a = W hi + W lo. The weights are exact in f16 and every f16 x f16 product is
-// exact in the f32 accumulator, so the result keeps the activations to about 2^-22 relative: the f32 path's
-// products up to the summation order (v_mfma_f32_16x16x32_f16, two per tile and 32-deep K step). Activations must
-// stay below 65504 in magnitude (f16 range). Tiles and epilogues as k_gemm_f32, K steps of BK (32 or 64) staged
-// through LDS with the next step's global loads in flight. MFMA lane layouts (checked on gfx950): A 16x32 -> lane l
-// holds A[l % 16][8 (l / 16) + e]; B 32x16 -> lane l holds B[8 (l / 16) + e][l % 16]; D as the f32 MFMA.
-template <int EPI, int TM, int TN, int BK>
-__global__ __launch_bounds__(256) void k_gemm_h16(const uint8_t *__restrict__ w, const float *__restrict__ A, GemmArgs g) {
+// F16 or Q8 weights on the f16 matrix cores with the f32 activations split in two halves: a = hi + lo with
+// hi = f16(a), lo = f16(a - hi), so W a = W hi + W lo. F16 weights and the int8 values of Q8 weights are exact in
+// f16 and every f16 x f16 product is exact in the f32 accumulator, so the result keeps the activations to about
+// 2^-22 relative (v_mfma_f32_16x16x32_f16, two per tile and 32-deep K step). Q8: one 32-deep step is one scale
+// block, so its two MFMAs start from zero and the block sum is scaled by the row's block scale into the
+// accumulator: s (q . a) for the reference's (float(q) s) . a, equal up to rounding. Activations must stay below
+// 65504 in magnitude (f16 range). Tiles and epilogues as k_gemm_f32, K steps of BK (32 or 64) staged through LDS
+// with the next step's global loads in flight. MFMA lane layouts (checked on gfx950): A 16x32 -> lane l holds
+// A[l % 16][8 (l / 16) + e]; B 32x16 -> lane l holds B[8 (l / 16) + e][l % 16]; D as the f32 MFMA.
+template <int WT, int EPI, int TM, int TN, int BK>
+__global__ __launch_bounds__(256) void k_gemm_h16(const uint8_t *__restrict__ w, const float *__restrict__ scale,
+                                                  const float *__restrict__ A, GemmArgs g) {
+    static_assert(WT == WT_F16 || WT == WT_Q8, "f16 or q8 weights");
     constexpr int BM = 32 * TM, BN = 32 * TN, LD = BK + 8;  // LDS row stride in halves
     constexpr int AQ = BM * BK / 4 / 256;  // f32x4 A loads per thread and K step
-    constexpr int WQ = BN * BK / 8 / 256;  // 8-half W loads per thread and K step
-    constexpr int CPR = BK / 4, WPR = BK / 8;  // f32x4 / 8-half chunks per row
+    constexpr int WQ = BN * BK / 8 / 256;  // 8-element W loads per thread and K step
+    constexpr int CPR = BK / 4, WPR = BK / 8;  // f32x4 / 8-element chunks per row
+    constexpr int NB = BK / 32;                // scale blocks per K step (Q8)
     __shared__ __align__(16) _Float16 Ah[BM][LD];
     __shared__ __align__(16) _Float16 Al[BM][LD];
     __shared__ __align__(16) _Float16 Bs[BN][LD];
+    __shared__ float Ss[WT == WT_Q8 ? BN : 1][NB];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int K = g.K;
+    const int K = g.K;  // the row length of A and W; this block sums columns [kbeg, kend)
+    const int kbeg = g.kchunk ? int(blockIdx.z) * g.kchunk : 0, kend = g.kchunk ? min(K, kbeg + g.kchunk) : K;
     f32x4v acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
     f32x4v ra[AQ];
-    u32x4 rw[WQ];
+    u32x4 rw[WQ];  // F16: 8 halves; Q8: 8 int8 in .x .y
+    float rs = 0.f;
     auto fetch = [&](int k0) {
 #pragma unroll
         for (int q = 0; q < AQ; ++q) {
-            const int idx = tid + 256 * q;
-            ra[q] = gemm_load_a<ASRC_ROWS>(A, g, m0 + idx / CPR, k0 + (idx % CPR) * 4);
+            const int idx = tid + 256 * q, row = m0 + idx / CPR, k = k0 + (idx % CPR) * 4;
+            ra[q] = f32x4v{0.f, 0.f, 0.f, 0.f};
+            if (row < g.m && k < kend) ra[q] = *reinterpret_cast<const f32x4v *>(A + int64_t(row) * g.lda + k);
         }
 #pragma unroll
         for (int q = 0; q < WQ; ++q) {
             const int idx = tid + 256 * q, row = n0 + idx / WPR, k = k0 + (idx % WPR) * 8;
             rw[q] = u32x4{0u, 0u, 0u, 0u};
-            if (row < g.n && k < K) rw[q] = *reinterpret_cast<const u32x4 *>(w + (int64_t(row) * K + k) * 2);
+            if (row < g.n && k < kend) {
+                if (WT == WT_F16) {
+                    rw[q] = *reinterpret_cast<const u32x4 *>(w + (int64_t(row) * K + k) * 2);
+                } else {
+                    const uint2 u = *reinterpret_cast<const uint2 *>(w + int64_t(row) * K + k);
+                    rw[q].x = u.x; rw[q].y = u.y;
+                }
+            }
+        }
+        if (WT == WT_Q8 && tid < BN * NB) {
+            const int row = n0 + tid / NB, kb = k0 / 32 + tid % NB;
+            rs = (row < g.n && kb < kend / 32) ? scale[int64_t(row) * (K / 32) + kb] : 0.f;
         }
     };
-    fetch(0);
-    for (int k0 = 0; k0 < K; k0 += BK) {
+    fetch(kbeg);
+    for (int k0 = kbeg; k0 < kend; k0 += BK) {
 #pragma unroll
         for (int q = 0; q < AQ; ++q) {
             const int idx = tid + 256 * q, r = idx / CPR, c = (idx % CPR) * 4;
@@ -254,10 +274,18 @@ __global__ __launch_bounds__(256) void k_gemm_h16(const uint8_t *__restrict__ w,
 #pragma unroll
         for (int q = 0; q < WQ; ++q) {
             const int idx = tid + 256 * q;
-            *reinterpret_cast<u32x4 *>(&Bs[idx / WPR][(idx % WPR) * 8]) = rw[q];
+            if (WT == WT_F16) {
+                *reinterpret_cast<u32x4 *>(&Bs[idx / WPR][(idx % WPR) * 8]) = rw[q];
+            } else {
+                f16x8v hv;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) hv[e] = _Float16(int8_t((e < 4 ? rw[q].x : rw[q].y) >> (8 * (e & 3))));
+                *reinterpret_cast<f16x8v *>(&Bs[idx / WPR][(idx % WPR) * 8]) = hv;
+            }
         }
+        if (WT == WT_Q8 && tid < BN * NB) Ss[tid / NB][tid % NB] = rs;
         __syncthreads();
-        if (k0 + BK < K) fetch(k0 + BK);  // in flight during the MFMAs below
+        if (k0 + BK < kend) fetch(k0 + BK);  // in flight during the MFMAs below
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 32) {
             f16x8v ah[TM], al[TM], b[TN];
@@ -270,17 +298,69 @@ __global__ __launch_bounds__(256) void k_gemm_h16(const uint8_t *__restrict__ w,
 #pragma unroll
             for (int j = 0; j < TN; ++j)
                 b[j] = *reinterpret_cast<const f16x8v *>(&Bs[wn * 16 * TN + j * 16 + (lane & 15)][kk + 8 * (lane >> 4)]);
+            if (WT == WT_F16) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+                for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], acc[i][j], 0, 0, 0);
-                }
+                    for (int j = 0; j < TN; ++j) {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], acc[i][j], 0, 0, 0);
+                    }
+            } else {
+                float sc[TN];  // the block scale of this lane's W row (its C column)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) sc[j] = Ss[wn * 16 * TN + j * 16 + (lane & 15)][kk / 32];
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        f32x4v t = {0.f, 0.f, 0.f, 0.f};
+                        t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], t, 0, 0, 0);
+                        t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], t, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[i][j][v] = fmaf(t[v], sc[j], acc[i][j][v]);
+                    }
+            }
         }
         __syncthreads();
     }
+    if (g.kchunk) {  // split K: this block's partial sums, no epilogue
+        float *ws = g.ws + int64_t(blockIdx.z) * g.m * g.n;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int col = n0 + wn * 16 * TN + j * 16 + (lane & 15);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int row = m0 + wm * 16 * TM + i * 16 + 4 * (lane >> 4) + v;
+                    if (row < g.m && col < g.n) ws[int64_t(row) * g.n + col] = acc[i][j][v];
+                }
+            }
+        return;
+    }
     gemm_epilogue<EPI, TM, TN>(acc, g, m0, n0, wm, wn, lane);
+}
+
+// The split-K partial slices ws[z][m][n], added in z order, then bias and the epilogue (STORE, ACC, GATED_ACC,
+// SWIGLU: one thread per output element; SWIGLU outputs pair columns 2u, 2u + 1). grid ceil(m n' / 256).
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm_splitk_reduce(GemmArgs g, int32_t splits) {
+    const int nout = EPI == EPI_SWIGLU ? g.n / 2 : g.n;
+    const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= int64_t(g.m) * nout) return;
+    const int row = int(t / nout), c = int(t % nout);
+    const int64_t slice = int64_t(g.m) * g.n;
+    auto sum = [&](int col) {
+        float v = 0.f;
+        for (int z = 0; z < splits; ++z) v += g.ws[z * slice + int64_t(row) * g.n + col];
+        return v + (g.bias ? g.bias[col] : 0.f);
+    };
+    float *dst = g.y + int64_t(row) * g.ldy + c;
+    if (EPI == EPI_SWIGLU) *dst = silu(sum(2 * c)) * sum(2 * c + 1);
+    else if (EPI == EPI_STORE) *dst = sum(c);
+    else if (EPI == EPI_ACC) *dst += sum(c);
+    else if (EPI == EPI_GATED_ACC) *dst += g.gate[c] * sum(c);
 }
 
 // Merge of the kAttnMaxSplits attention partials of m rows into ao [m][heads * hd] (the PRO_ATTN prologue of the

@@ -79,12 +79,13 @@ static hipError_t attn_hg(const AttnArgs &a, const AttnLaunch &l, int m, bool fu
     return launch(k_attn<HD, G, false>, grid, dim3(256), smem, s, l.kc0, l.vc0, l.qkv, l.rope_rows, l.cap0, l.layer, a);
 }
 
-// Query heads per block: the whole group, or, when there are few kv heads, the largest divisor of the group that
-// gives at least kAttnMinBlocks blocks per row (more blocks share the work; each reads its kv head's keys).
+// Query heads per block: the whole group, or, when a launch has few blocks (few kv heads, few rows), the largest
+// divisor of the group that gives at least kAttnMinBlocks blocks (more blocks share the work; each reads its kv
+// head's keys, so a split multiplies the key reads by group / G).
 constexpr int kAttnMinBlocks = 128;
-static int attn_heads_per_block(int kv_heads, int group) {
+static int attn_heads_per_block(int kv_heads, int group, int m) {
     int gb = group;
-    while (gb > 1 && kv_heads * (group / gb) * kAttnMaxSplits < kAttnMinBlocks) {
+    while (gb > 1 && int64_t(m) * kv_heads * (group / gb) * kAttnMaxSplits < kAttnMinBlocks) {
         int d = gb - 1;
         while (d > 1 && group % d) --d;
         gb = d;
@@ -94,7 +95,7 @@ static int attn_heads_per_block(int kv_heads, int group) {
 
 template <int HD>
 static hipError_t attn_h(const AttnArgs &a, const AttnLaunch &l, int m, bool fused, hipStream_t s) {
-    switch (attn_heads_per_block(a.kv_heads, a.group)) {
+    switch (attn_heads_per_block(a.kv_heads, a.group, m)) {
         case 1: return attn_hg<HD, 1>(a, l, m, fused, s);
         case 2: return attn_hg<HD, 2>(a, l, m, fused, s);
         case 3: return attn_hg<HD, 3>(a, l, m, fused, s);

@@ -104,6 +104,11 @@ struct GemmArgs {
     // ASRC_CONV: x [m][lda] rows of `seq`-row batches; group g = blockIdx.z reads channels [g cig, (g + 1) cig) at
     // rows t + k - ksize / 2 of the same batch (zeros outside) for A column k cig + i; W and y are offset per group
     int32_t ksize, cig;
+    // split K (k_gemm_h16): block z sums K columns [z kchunk, (z + 1) kchunk) into ws + z m n ([m][n]); a reduce
+    // pass adds the slices in order and applies the epilogue. kchunk 0: no split.
+    int32_t kchunk;
+    float *ws;
+    int64_t ws_cap;  // floats available at ws (0: no split)
 };
 
 // CosyVoice2 LM sampling (lm_logp + ras_sample + lm_generate's trial loop, cosyvoice.cpp:598-690).

@@ -44,6 +44,7 @@ struct Fail : std::runtime_error {
 
 constexpr int kMaxM = 8;          // rows per pass on the int8-activation path; sequences per decode step
 constexpr int kMaxPass = 512;     // rows per pass on the f32-activation path (MFMA GEMM above 4 rows)
+constexpr int64_t kGemmWsFloats = int64_t(8) << 20;  // split-K workspace: 32 MB
 constexpr int64_t kMaxCap = 65536;
 
 struct GpuMat {
@@ -140,6 +141,8 @@ struct Ctx {
     int32_t *hist_dev = nullptr, *tok_dev = nullptr;
     size_t hist_cap = 0;
     std::vector<struct F5 *> f5;
+    // split-K partial sums of the MFMA GEMM (allocated at init, so captured graphs can use it)
+    float *gemm_ws = nullptr;
     // LM sampler staging: device config + state, and their pinned host copies (config, state, two state slots)
     LmCfgDev *lm_cfg_dev = nullptr;
     LmState *lm_state_dev = nullptr;
@@ -362,7 +365,9 @@ void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, in
             HIPCHECK(launch_attn_merge(*attn, pre, mc, s));
             A = pre; lda = m.cols;
         }
-        const GemmArgs ga{m.b, y, lda, ldy, mc, int32_t(m.rows), int32_t(m.cols)};
+        GemmArgs ga{};
+        ga.bias = m.b; ga.y = y; ga.lda = lda; ga.ldy = ldy; ga.m = mc; ga.n = int32_t(m.rows); ga.K = int32_t(m.cols);
+        ga.ws = g.gemm_ws; ga.ws_cap = kGemmWsFloats;
         HIPCHECK(launch_gemm(gemv_type(m), epi, m.w, m.s, A, ga, s));
         return;
     }
@@ -822,6 +827,7 @@ int voxhip_init(const char *device, char *err, size_t err_len) {
             throw Fail(std::string("device is ") + p.gcnArchName + "; this backend is built for gfx950 (MI355X)");
         HIPCHECK(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
         g.dev = idx;
+        g.gemm_ws = dalloc_t<float>(size_t(kGemmWsFloats));
         g.name = std::string(p.name) + " (" + p.gcnArchName + ")";
         g.ok = true;
         return 1;
@@ -1526,6 +1532,7 @@ void f5_free_step(F5 &F) {
 GemmArgs gemm_args(const GpuMat &m, const float *bias, float *y, int64_t lda, int64_t ldy, int64_t rows) {
     GemmArgs ga{};
     ga.bias = bias; ga.y = y; ga.lda = lda; ga.ldy = ldy; ga.m = int32_t(rows); ga.n = int32_t(m.rows); ga.K = int32_t(m.cols);
+    ga.ws = g.gemm_ws; ga.ws_cap = kGemmWsFloats;
     return ga;
 }
 void f5_gemm(const GpuMat &m, int epi, const float *A, GemmArgs ga, hipStream_t s) {
