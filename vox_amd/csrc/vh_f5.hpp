@@ -107,15 +107,25 @@ __global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
     f32x4a o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) { mrow[i] = -INFINITY; lrow[i] = 0.f; o[i] = f32x4a{0.f, 0.f, 0.f, 0.f}; }
+    // the next key tile's K / V rows are loaded into registers during the current tile's MFMAs
+    f32x4a kvr[4], vvr[4];
+    auto fetch = [&](int kt) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int idx = tid + 256 * q, key = idx >> 4, d4 = (idx & 15) * 4;
+            kvr[q] = vvr[q] = f32x4a{0.f, 0.f, 0.f, 0.f};
+            if (kt + key < a.N) {
+                kvr[q] = *reinterpret_cast<const f32x4a *>(Kp + (rb + kt + key) * a.ld + d4);
+                vvr[q] = *reinterpret_cast<const f32x4a *>(Vp + (rb + kt + key) * a.ld + d4);
+            }
+        }
+    };
+    fetch(0);
     for (int kt = 0; kt < a.N; kt += 64) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int idx = tid + 256 * q, key = idx >> 4, d4 = (idx & 15) * 4;
-            f32x4a kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
-            if (kt + key < a.N) {
-                kv = *reinterpret_cast<const f32x4a *>(Kp + (rb + kt + key) * a.ld + d4);
-                vv = *reinterpret_cast<const f32x4a *>(Vp + (rb + kt + key) * a.ld + d4);
-            }
+            const f32x4a kv = kvr[q], vv = vvr[q];
             h16x4 khi, klo;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -131,6 +141,7 @@ __global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
             *reinterpret_cast<h16x4 *>(&Kl[key][d4]) = klo;
         }
         __syncthreads();
+        if (kt + 64 < a.N) fetch(kt + 64);
         // S tiles: B operand lane holds K[16 j + lr][32 c + 8 lg + e]
         f32x4a s[4];
 #pragma unroll
