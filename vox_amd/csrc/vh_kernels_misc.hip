@@ -5,6 +5,7 @@
 #include <map>
 
 #include "vh_attn.hpp"
+#include "vh_pattn.hpp"
 #include "vh_launch.hpp"
 #include "vh_sample.hpp"
 #include "vh_util.hpp"
@@ -118,6 +119,15 @@ hipError_t launch_attention(const AttnArgs &a, const _Float16 *kc0, const _Float
     ag.group = group;
     if (hd == 128) return attn_h<128>(ag, l, m, fused, s);
     if (hd == 64) return attn_h<64>(ag, l, m, fused, s);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_prefill_attn(const PrefillAttnArgs &a, int hd, hipStream_t s) {
+    if (a.m <= 0) return hipSuccess;
+    if (a.kv_heads <= 0 || a.heads % a.kv_heads || a.pos0 < 0 || a.pos0 + a.m > a.cap) return hipErrorInvalidValue;
+    const dim3 grid(unsigned((a.m + 63) / 64), unsigned(a.heads));
+    if (hd == 64) return launch(k_prefill_attn<64>, grid, dim3(256), 0, s, a);
+    if (hd == 128) return launch(k_prefill_attn<128>, grid, dim3(256), 0, s, a);
     return hipErrorInvalidValue;
 }
 

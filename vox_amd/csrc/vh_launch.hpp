@@ -56,6 +56,8 @@ hipError_t launch_fill_cache(void *c, int64_t planes, int64_t cap, int64_t len, 
                              float mean, float std, hipStream_t s);
 
 hipError_t launch_copy16(const void *src, void *dst, int64_t bytes, hipStream_t s);
+// Causal attention of a prefill pass (consecutive rows of one sequence) on the matrix cores, head_dim 64 or 128.
+hipError_t launch_prefill_attn(const PrefillAttnArgs &a, int hd, hipStream_t s);
 // F5-TTS DiT step: AdaLN modulation of R rows of D, the step input's x columns, attention (head_dim 64).
 hipError_t launch_f5_modulate(const float *x, int64_t R, int D, const float *sc, const float *sh, float *y, hipStream_t s);
 hipError_t launch_f5_fill_x(const float *x, int N, int mel, float *cat, int W, int B, hipStream_t s);

@@ -79,6 +79,17 @@ struct AttnArgs {
     float scale, eps;
 };
 
+// Causal attention of m consecutive rows of one sequence (prefill) on the matrix cores: row r sits at position
+// pos0 + r and attends keys 0 .. pos0 + r of the f16 cache (the pass's keys already appended by k_qk_post).
+struct PrefillAttnArgs {
+    const float *q;        // [m][heads hd] normed + rotated queries
+    const _Float16 *k, *v; // the sequence's cache bases ([layer][kv_head][cap][hd])
+    float *out;            // [m][heads hd]
+    int64_t cap, pos0;
+    int32_t m, heads, kv_heads, layer;
+    float scale;
+};
+
 struct SampleCfgDev {
     float temperature, top_p, rep;
     int32_t top_k;

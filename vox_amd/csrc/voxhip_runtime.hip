@@ -511,6 +511,10 @@ int kernels_per_layer(bool fused) { return fused ? 5 : 6; }
 void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipStream_t s, bool fused, Probe *pr = nullptr) {
     const int qd = X.heads * X.hd, kd = X.kvh * X.hd, ldqkv = qd + 2 * kd;
     const AttnPartials part = partials_of(X);
+    // prefill pass of consecutive rows of one sequence: attention on the matrix cores straight into the o input
+    bool pass_attn = !fused && mc > 4 && (X.hd == 64 || X.hd == 128) && int(X.rows_last.size()) == mc;
+    for (int i = 1; i < mc && pass_attn; ++i)
+        pass_attn = X.rows_last[size_t(i)].k == X.rows_last[0].k && X.rows_last[size_t(i)].pos == X.rows_last[0].pos + i;
     for (int li = first; li < first + count; ++li) {
         const LayerDev &L = X.L[size_t(li)];
         const GpuMat &Mqkv = g.mats[size_t(L.qkv)], &Mo = g.mats[size_t(L.o)], &Mgu = g.mats[size_t(L.gu)],
@@ -525,16 +529,24 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
             qa.rope = X.rope; qa.heads = X.heads; qa.kv_heads = X.kvh; qa.hd = X.hd; qa.layer = li; qa.eps = X.eps;
             probed(pr, VOXHIP_K_QKPOST, [&] { HIPCHECK(launch_qk_post(qa, mc, s)); });
         }
-        AttnArgs aa;
-        aa.ldqkv = ldqkv; aa.q = X.q; aa.qn = qn; aa.kn = kn; aa.part = part;
-        aa.kv_heads = X.kvh; aa.scale = 1.0f / std::sqrt(float(X.hd)); aa.eps = X.eps;
         const RowRef &r0 = X.rows_last.at(0);
-        probed(pr, VOXHIP_K_ATTN, [&] {
-            HIPCHECK(launch_attention(aa, r0.k, r0.v, r0.cap, X.qkv, X.rope_rows_dev, li, X.hd, X.heads / X.kvh, mc, fused, s));
-        });
-        probed(pr, VOXHIP_K_O, [&] {
-            gemv(Mo, m_total, PRO_ATTN, EPI_ACC, nullptr, 0, mc, X.h, X.H, nullptr, 0.f, nullptr, s, &part, X.pre);
-        });
+        if (pass_attn && gemm_path(Mo, m_total, mc)) {
+            PrefillAttnArgs pa{};
+            pa.q = X.q; pa.k = r0.k; pa.v = r0.v; pa.out = X.pre; pa.cap = r0.cap; pa.pos0 = r0.pos; pa.m = mc;
+            pa.heads = X.heads; pa.kv_heads = X.kvh; pa.layer = li; pa.scale = 1.0f / std::sqrt(float(X.hd));
+            probed(pr, VOXHIP_K_ATTN, [&] { HIPCHECK(launch_prefill_attn(pa, X.hd, s)); });
+            probed(pr, VOXHIP_K_O, [&] { gemv(Mo, m_total, PRO_X, EPI_ACC, X.pre, qd, mc, X.h, X.H, nullptr, 0.f, nullptr, s); });
+        } else {
+            AttnArgs aa;
+            aa.ldqkv = ldqkv; aa.q = X.q; aa.qn = qn; aa.kn = kn; aa.part = part;
+            aa.kv_heads = X.kvh; aa.scale = 1.0f / std::sqrt(float(X.hd)); aa.eps = X.eps;
+            probed(pr, VOXHIP_K_ATTN, [&] {
+                HIPCHECK(launch_attention(aa, r0.k, r0.v, r0.cap, X.qkv, X.rope_rows_dev, li, X.hd, X.heads / X.kvh, mc, fused, s));
+            });
+            probed(pr, VOXHIP_K_O, [&] {
+                gemv(Mo, m_total, PRO_ATTN, EPI_ACC, nullptr, 0, mc, X.h, X.H, nullptr, 0.f, nullptr, s, &part, X.pre);
+            });
+        }
         probed(pr, VOXHIP_K_GATEUP, [&] {
             gemv(Mgu, m_total, PRO_RMS, EPI_SWIGLU, X.h, X.H, mc, X.g, X.I, X.norms + L.ln2, X.eps, nullptr, s, nullptr, X.pre);
         });
