@@ -47,20 +47,17 @@ static hipError_t gemm_splitk(const uint8_t *w, const float *scale, const float 
     }
 }
 
-// 128 x 128 block tiles when they still give a full wave of blocks, else 128 x 64 or 64 x 64 (split K when even
-// those leave the CUs idle). F16 and Q8 weights take the split-f16 matrix cores.
+// 64 x 64 block tiles: measured faster than 128 x 128 and 128 x 64 on the DiT and prefill shapes, because more
+// blocks per CU hide the global latency of each K step (split K when even these leave the CUs idle). F16 and Q8
+// weights take the split-f16 matrix cores.
 template <int WT, int EPI>
 static hipError_t gemm_tile(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s) {
-    const bool big = int64_t((g.n + 127) / 128) * ((g.m + 127) / 128) >= 256;
     if constexpr (WT == WT_F16 || WT == WT_Q8) {
         bool split = false;
         hipError_t e = gemm_splitk<WT, EPI>(w, scale, A, g, s, &split);
         if (e != hipSuccess || split) return e;
-        if (big) return gemm_run_h16<WT, EPI, 4, 4>(w, scale, A, g, s);
-        if (int64_t((g.n + 63) / 64) * ((g.m + 127) / 128) >= 256) return gemm_run_h16<WT, EPI, 4, 2>(w, scale, A, g, s);
         return gemm_run_h16<WT, EPI, 2, 2>(w, scale, A, g, s);
     } else {
-        if (big) return gemm_run<WT, EPI, ASRC_ROWS, 4>(w, scale, A, g, 1, s);
         return gemm_run<WT, EPI, ASRC_ROWS, 2>(w, scale, A, g, 1, s);
     }
 }
