@@ -17,10 +17,11 @@ hipError_t launch_f5_fill_x(const float *x, int N, int mel, float *cat, int W, i
                   int32_t(B));
 }
 
-hipError_t launch_f5_attn(const float *qkv, float *out, int B, int N, int heads, int hd, int ld, int ldo, float scale, hipStream_t s) {
+hipError_t launch_f5_attn(const _Float16 *qkv16, int64_t lo_off, float *out, int B, int N, int heads, int hd, int ldvt, int ldo,
+                          float scale, hipStream_t s) {
     if (B <= 0 || N <= 0) return hipSuccess;
-    if (hd != kF5Hd || ld % 4 || heads <= 0) return hipErrorInvalidValue;
-    F5AttnArgs a{qkv, out, int32_t(N), int32_t(ld), int32_t(ldo), int32_t(heads * hd), scale};
+    if (hd != kF5Hd || heads <= 0 || ldvt < N || ldvt % 8 || lo_off % 8) return hipErrorInvalidValue;
+    F5AttnArgs a{qkv16, lo_off, out, int32_t(N), int32_t(ldo), int32_t(heads * hd), int32_t(ldvt), scale};
     return launch(k_f5_attn, dim3(unsigned((N + 63) / 64), unsigned(heads), unsigned(B)), dim3(256), 0, s, a);
 }
 

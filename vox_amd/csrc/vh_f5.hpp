@@ -50,56 +50,48 @@ __global__ __launch_bounds__(256) void k_f5_fill_x(const float *__restrict__ x, 
 // O = P V, for head_dim 64. grid (ceil(N / 64), heads, B), block 256: each wave takes 16 query rows; key tiles of
 // 64 go through LDS; an online softmax (running max and sum per row, O rescaled) replaces the reference's
 // whole-row max, which changes only the rounding.
-// Both products run on the f16 matrix cores (v_mfma_f32_16x16x32_f16) with every f32 operand split in two f16
-// halves, x = hi + lo, and three products per pair (hi.hi + hi.lo + lo.hi; the dropped lo.lo term is below 2^-22
-// relative): each product is exact in the f32 accumulator, so S and P V keep f32-level accuracy. Q, K and P are
-// O(1) after the projections and the softmax, well inside the f16 range.
+// Both products run on the f16 matrix cores (v_mfma_f32_16x16x32_f16) with every f32 operand as two f16 halves,
+// x = hi + lo, and three products per pair (hi.hi + hi.lo + lo.hi; the dropped lo.lo term is below 2^-22 relative):
+// each product is exact in the f32 accumulator, so S and P V keep f32-level accuracy. q, k and v arrive already
+// split (the q|k|v GEMM's EPI_ROPE_H16 epilogue: q | k rows and v transposed to [d][key]), so key and value tiles
+// are plain 16-byte loads; the softmax weights are split here. The next tile's loads are in flight during the
+// current tile's MFMAs.
 struct F5AttnArgs {
-    const float *qkv;  // [B N][ld] rows: q | k | v, head h at column h * 64 of each
-    float *out;        // [B N][ldo], head h at column h * 64
-    int32_t N, ld, ldo, inner;
+    const _Float16 *h16;  // hi plane; the lo plane is lo_off halves further
+    int64_t lo_off;
+    float *out;           // [B N][ldo], head h at column h * 64
+    int32_t N, ldo, inner, ldvt;
     float scale;
 };
 constexpr int kF5Hd = kF5HeadDim;
 typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
 constexpr int kF5Ld = 64 + 8;  // LDS row stride in halves
-VH_DEV void split_f16(float x, _Float16 &hi, _Float16 &lo) {
-    hi = _Float16(x);
-    lo = _Float16(x - float(hi));
-}
+VH_DEV h16x8 ld16(const _Float16 *p) { return *reinterpret_cast<const h16x8 *>(p); }
 VH_DEV f32x4a mfma3(h16x8 ah, h16x8 al, h16x8 bh, h16x8 bl, f32x4a c) {
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, c, 0, 0, 0);
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, c, 0, 0, 0);
 }
 __global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
-    __shared__ __align__(16) _Float16 Kh[64][kF5Ld], Kl[64][kF5Ld];     // [key][d]
-    __shared__ __align__(16) _Float16 Vh[64][kF5Ld], Vl[64][kF5Ld];     // [d][key] (transposed)
-    __shared__ __align__(16) _Float16 Ph[4][16][kF5Ld], Pl[4][16][kF5Ld];  // per wave [row][key]
+    __shared__ __align__(16) _Float16 Kh[64][kF5Ld], Kl[64][kF5Ld];  // [key][d]
+    __shared__ __align__(16) _Float16 Vh[64][kF5Ld], Vl[64][kF5Ld];  // [d][key]
+    __shared__ __align__(16) float Ps[4][16][68];                     // per wave [row][key]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
-    const int q0 = blockIdx.x * 64, h = blockIdx.y;
-    const int64_t rb = int64_t(blockIdx.z) * a.N;
-    const float *Q = a.qkv + int64_t(h) * kF5Hd, *Kp = a.qkv + a.inner + int64_t(h) * kF5Hd,
-                *Vp = a.qkv + 2 * int64_t(a.inner) + int64_t(h) * kF5Hd;
-    // A operand of S, two K steps of 32 dims: lane holds Q[16 wave + lr][32 c + 8 lg + e] as hi / lo halves
+    const int q0 = blockIdx.x * 64, h = blockIdx.y, b = blockIdx.z, heads = gridDim.y;
+    const int64_t ldqk = 2 * int64_t(a.inner), rb = int64_t(b) * a.N;
+    const _Float16 *QK = a.h16;                                                  // q | k rows
+    const _Float16 *VT = a.h16 + int64_t(gridDim.z) * a.N * ldqk + (int64_t(b) * heads + h) * kF5Hd * a.ldvt;  // [d][key]
+    // A operand of S: lane holds q[16 wave + lr][32 c + 8 lg + e]
     h16x8 qh[2], ql[2];
     {
         const int qr = q0 + 16 * wave + lr;
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            f32x4a x0 = {0.f, 0.f, 0.f, 0.f}, x1 = {0.f, 0.f, 0.f, 0.f};
+            qh[c] = ql[c] = h16x8{0, 0, 0, 0, 0, 0, 0, 0};
             if (qr < a.N) {
-                x0 = *reinterpret_cast<const f32x4a *>(Q + (rb + qr) * a.ld + 32 * c + 8 * lg);
-                x1 = *reinterpret_cast<const f32x4a *>(Q + (rb + qr) * a.ld + 32 * c + 8 * lg + 4);
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                _Float16 hi, lo;
-                split_f16(x0[e], hi, lo);
-                qh[c][e] = hi; ql[c][e] = lo;
-                split_f16(x1[e], hi, lo);
-                qh[c][e + 4] = hi; ql[c][e + 4] = lo;
+                const _Float16 *p = QK + (rb + qr) * ldqk + h * kF5Hd + 32 * c + 8 * lg;
+                qh[c] = ld16(p);
+                ql[c] = ld16(p + a.lo_off);
             }
         }
     }
@@ -107,38 +99,30 @@ __global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
     f32x4a o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) { mrow[i] = -INFINITY; lrow[i] = 0.f; o[i] = f32x4a{0.f, 0.f, 0.f, 0.f}; }
-    // the next key tile's K / V rows are loaded into registers during the current tile's MFMAs
-    f32x4a kvr[4], vvr[4];
+    // per thread and tile: 2 chunks of 8 halves of K (hi, lo) and of v^T (hi, lo)
+    h16x8 kr[2][2], vr[2][2];
     auto fetch = [&](int kt) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int idx = tid + 256 * q, key = idx >> 4, d4 = (idx & 15) * 4;
-            kvr[q] = vvr[q] = f32x4a{0.f, 0.f, 0.f, 0.f};
-            if (kt + key < a.N) {
-                kvr[q] = *reinterpret_cast<const f32x4a *>(Kp + (rb + kt + key) * a.ld + d4);
-                vvr[q] = *reinterpret_cast<const f32x4a *>(Vp + (rb + kt + key) * a.ld + d4);
+        for (int q = 0; q < 2; ++q) {
+            const int idx = tid + 256 * q, r = idx >> 3, c8 = (idx & 7) * 8;  // r: key (K) or d (v^T); c8: d or key
+#pragma unroll
+            for (int hl = 0; hl < 2; ++hl) {
+                kr[q][hl] = vr[q][hl] = h16x8{0, 0, 0, 0, 0, 0, 0, 0};
+                const int64_t off = hl ? a.lo_off : 0;
+                if (kt + r < a.N) kr[q][hl] = ld16(QK + off + (rb + kt + r) * ldqk + a.inner + h * kF5Hd + c8);
+                if (kt + c8 < a.N) vr[q][hl] = ld16(VT + off + int64_t(r) * a.ldvt + kt + c8);
             }
         }
     };
     fetch(0);
     for (int kt = 0; kt < a.N; kt += 64) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int idx = tid + 256 * q, key = idx >> 4, d4 = (idx & 15) * 4;
-            const f32x4a kv = kvr[q], vv = vvr[q];
-            h16x4 khi, klo;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                _Float16 hi, lo;
-                split_f16(kv[e], hi, lo);
-                khi[e] = hi; klo[e] = lo;
-                _Float16 vhi, vlo;
-                split_f16(vv[e], vhi, vlo);
-                Vh[d4 + e][key] = vhi;
-                Vl[d4 + e][key] = vlo;
-            }
-            *reinterpret_cast<h16x4 *>(&Kh[key][d4]) = khi;
-            *reinterpret_cast<h16x4 *>(&Kl[key][d4]) = klo;
+        for (int q = 0; q < 2; ++q) {
+            const int idx = tid + 256 * q, r = idx >> 3, c8 = (idx & 7) * 8;
+            *reinterpret_cast<h16x8 *>(&Kh[r][c8]) = kr[q][0];
+            *reinterpret_cast<h16x8 *>(&Kl[r][c8]) = kr[q][1];
+            *reinterpret_cast<h16x8 *>(&Vh[r][c8]) = vr[q][0];
+            *reinterpret_cast<h16x8 *>(&Vl[r][c8]) = vr[q][1];
         }
         __syncthreads();
         if (kt + 64 < a.N) fetch(kt + 64);
@@ -148,11 +132,8 @@ __global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
         for (int j = 0; j < 4; ++j) {
             s[j] = f32x4a{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                const h16x8 bh = *reinterpret_cast<const h16x8 *>(&Kh[16 * j + lr][32 * c + 8 * lg]);
-                const h16x8 bl = *reinterpret_cast<const h16x8 *>(&Kl[16 * j + lr][32 * c + 8 * lg]);
-                s[j] = mfma3(qh[c], ql[c], bh, bl, s[j]);
-            }
+            for (int c = 0; c < 2; ++c)
+                s[j] = mfma3(qh[c], ql[c], ld16(&Kh[16 * j + lr][32 * c + 8 * lg]), ld16(&Kl[16 * j + lr][32 * c + 8 * lg]), s[j]);
         }
         // lane holds S[4 lg + i][16 j + lr]: the 16 lanes of a DPP row share the rows
 #pragma unroll
@@ -175,10 +156,7 @@ __global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
             for (int j = 0; j < 4; ++j) {
                 const float p = expf(s[j][i] - mnew);
                 sum += p;
-                _Float16 phi, plo;
-                split_f16(p, phi, plo);
-                Ph[wave][4 * lg + i][16 * j + lr] = phi;
-                Pl[wave][4 * lg + i][16 * j + lr] = plo;
+                Ps[wave][4 * lg + i][16 * j + lr] = p;
             }
             sum += dpp<kDppXor1>(sum);
             sum += dpp<kDppXor2>(sum);
@@ -190,17 +168,22 @@ __global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
             for (int dt = 0; dt < 4; ++dt) o[dt][i] *= alpha;
         }
         __syncthreads();
-        // O += P V: A lane holds P[lr][32 c + 8 lg + e]; B lane holds V[32 c + 8 lg + e][16 dt + lr] (= Vt rows)
+        // O += P V: A lane holds P[lr][32 c + 8 lg + e] (split here); B lane holds V[32 c + 8 lg + e][16 dt + lr]
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            const h16x8 pah = *reinterpret_cast<const h16x8 *>(&Ph[wave][lr][32 * c + 8 * lg]);
-            const h16x8 pal = *reinterpret_cast<const h16x8 *>(&Pl[wave][lr][32 * c + 8 * lg]);
+            const f32x4a p0 = *reinterpret_cast<const f32x4a *>(&Ps[wave][lr][32 * c + 8 * lg]);
+            const f32x4a p1 = *reinterpret_cast<const f32x4a *>(&Ps[wave][lr][32 * c + 8 * lg + 4]);
+            h16x8 pah, pal;
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt) {
-                const h16x8 bh = *reinterpret_cast<const h16x8 *>(&Vh[16 * dt + lr][32 * c + 8 * lg]);
-                const h16x8 bl = *reinterpret_cast<const h16x8 *>(&Vl[16 * dt + lr][32 * c + 8 * lg]);
-                o[dt] = mfma3(pah, pal, bh, bl, o[dt]);
+            for (int e = 0; e < 8; ++e) {
+                const float x = e < 4 ? p0[e] : p1[e - 4];
+                const _Float16 hi = _Float16(x);
+                pah[e] = hi;
+                pal[e] = _Float16(x - float(hi));
             }
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+                o[dt] = mfma3(pah, pal, ld16(&Vh[16 * dt + lr][32 * c + 8 * lg]), ld16(&Vl[16 * dt + lr][32 * c + 8 * lg]), o[dt]);
         }
         __syncthreads();
     }

@@ -73,6 +73,11 @@ static hipError_t gemm_epi(int epi, const uint8_t *w, const float *scale, const 
         case EPI_ROPE:
             if (!g.rope || g.hd <= 0 || g.hd % 2 || g.seq <= 0 || g.rope_cols % (2 * g.hd)) return hipErrorInvalidValue;
             return gemm_tile<WT, EPI_ROPE>(w, scale, A, g, s);
+        case EPI_ROPE_H16:
+            if (!g.rope || !g.h16 || g.hd <= 0 || g.hd % 2 || g.seq <= 0 || g.rope_cols % (2 * g.hd) || g.m % g.seq ||
+                g.n != g.rope_cols + g.rope_cols / 2 || g.ldvt < g.seq || g.ldvt % 8)
+                return hipErrorInvalidValue;
+            return gemm_tile<WT, EPI_ROPE_H16>(w, scale, A, g, s);
         default: return hipErrorInvalidValue;
     }
 }

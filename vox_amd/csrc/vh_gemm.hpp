@@ -96,7 +96,7 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
                 if (EPI == EPI_SWIGLU) {
                     const float up = __shfl_xor(c, 1, kWave);  // column col ^ 1 of the same row
                     if (in && (col & 1) == 0) g.y[int64_t(row) * g.ldy + col / 2] = silu(c) * up;
-                } else if (EPI == EPI_ROPE) {
+                } else if (EPI == EPI_ROPE || EPI == EPI_ROPE_H16) {
                     const float o = __shfl_xor(c, 1, kWave);  // the pair partner (2j <-> 2j + 1)
                     float r = c;
                     if (col < g.rope_cols) {
@@ -107,7 +107,21 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
                             r = (col & 1) ? c * cc + o * sn : c * cc - o * sn;
                         }
                     }
-                    if (in) *dst = r;
+                    if (EPI == EPI_ROPE) {
+                        if (in) *dst = r;
+                    } else if (in) {
+                        const _Float16 hi = _Float16(r), lo = _Float16(r - float(hi));
+                        int64_t idx;
+                        if (col < g.rope_cols) {
+                            idx = int64_t(row) * g.rope_cols + col;
+                        } else {  // v, transposed: [batch][head][d][key]
+                            const int cv = col - g.rope_cols, b = row / g.seq, n = row % g.seq;
+                            const int64_t vbase = int64_t(g.m) * g.rope_cols;
+                            idx = vbase + ((int64_t(b) * (g.rope_cols / 2 / g.hd) + cv / g.hd) * g.hd + cv % g.hd) * g.ldvt + n;
+                        }
+                        g.h16[idx] = hi;
+                        g.h16[g.lo_off + idx] = lo;
+                    }
                 } else if (in) {
                     if (EPI == EPI_STORE) *dst = c;
                     else if (EPI == EPI_ACC) *dst += c;

@@ -61,7 +61,8 @@ hipError_t launch_prefill_attn(const PrefillAttnArgs &a, int hd, hipStream_t s);
 // F5-TTS DiT step: AdaLN modulation of R rows of D, the step input's x columns, attention (head_dim 64).
 hipError_t launch_f5_modulate(const float *x, int64_t R, int D, const float *sc, const float *sh, float *y, hipStream_t s);
 hipError_t launch_f5_fill_x(const float *x, int N, int mel, float *cat, int W, int B, hipStream_t s);
-hipError_t launch_f5_attn(const float *qkv, float *out, int B, int N, int heads, int hd, int ld, int ldo, float scale, hipStream_t s);
+hipError_t launch_f5_attn(const _Float16 *qkv16, int64_t lo_off, float *out, int B, int N, int heads, int hd, int ldvt, int ldo,
+                          float scale, hipStream_t s);
 // CosyVoice2 LM: one sampling step (log-softmax, RAS trial loop) and the next step's embedding + row advance.
 hipError_t launch_lm_sample(const float *logits, int n, const LmCfgDev *cfg, LmState *st, int32_t *decoded, float *logp_out,
                             int64_t logp_stride, bool append, hipStream_t s);

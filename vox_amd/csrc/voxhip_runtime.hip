@@ -1480,8 +1480,12 @@ struct F5 {
     F5Conv pos1, pos2;
     // step buffers of begin(B, N): rows R = B N
     int B = 0, N = 0;
-    float *cat = nullptr, *h = nullptr, *a = nullptr, *nrm = nullptr, *qkv = nullptr, *at = nullptr, *ffb = nullptr;
+    float *cat = nullptr, *h = nullptr, *a = nullptr, *nrm = nullptr, *at = nullptr, *ffb = nullptr;
     float *ada = nullptr, *fin = nullptr, *ts = nullptr, *x = nullptr, *out = nullptr, *rope = nullptr;
+    // q | k rows and v^T ([B heads hd][ldvt], key columns padded with zeros to ldvt) as f16 hi, then lo, planes
+    _Float16 *qkv16 = nullptr;
+    int64_t lo_off = 0;
+    int ldvt = 0;
 };
 
 F5 &f5_at(int id) {
@@ -1536,9 +1540,12 @@ F5Conv upload_conv(const voxhip_f5_conv &c, int dim) {
 }
 
 void f5_free_step(F5 &F) {
-    for (float *p : {F.cat, F.h, F.a, F.nrm, F.qkv, F.at, F.ffb, F.ada, F.fin, F.ts, F.x, F.out, F.rope}) dfree(p);
-    F.cat = F.h = F.a = F.nrm = F.qkv = F.at = F.ffb = F.ada = F.fin = F.ts = F.x = F.out = F.rope = nullptr;
-    F.B = F.N = 0;
+    for (float *p : {F.cat, F.h, F.a, F.nrm, F.at, F.ffb, F.ada, F.fin, F.ts, F.x, F.out, F.rope}) dfree(p);
+    F.cat = F.h = F.a = F.nrm = F.at = F.ffb = F.ada = F.fin = F.ts = F.x = F.out = F.rope = nullptr;
+    dfree(F.qkv16);
+    F.qkv16 = nullptr;
+    F.B = F.N = F.ldvt = 0;
+    F.lo_off = 0;
 }
 
 GemmArgs gemm_args(const GpuMat &m, const float *bias, float *y, int64_t lda, int64_t ldy, int64_t rows) {
@@ -1579,10 +1586,11 @@ void f5_enqueue(F5 &F, hipStream_t s) {
         const float *ada = F.ada + size_t(i) * 6 * D;  // shift, scale, gate (msa), shift, scale, gate (mlp)
         HIPCHECK(launch_f5_modulate(F.h, R, D, ada + D, ada, F.nrm, s));
         const GpuMat &Mq = mat_at(L.qkv);
-        GemmArgs gq = gemm_args(Mq, Mq.b, F.qkv, D, 3 * INNER, R);
+        GemmArgs gq = gemm_args(Mq, Mq.b, nullptr, D, 3 * INNER, R);
         gq.rope = F.rope; gq.seq = F.N; gq.hd = F.hd; gq.rope_cols = 2 * INNER; gq.rope_heads = F.pe;
-        f5_gemm(Mq, EPI_ROPE, F.nrm, gq, s);
-        HIPCHECK(launch_f5_attn(F.qkv, F.at, F.B, F.N, F.heads, F.hd, 3 * INNER, INNER, scale, s));
+        gq.h16 = F.qkv16; gq.lo_off = F.lo_off; gq.ldvt = F.ldvt;
+        f5_gemm(Mq, EPI_ROPE_H16, F.nrm, gq, s);
+        HIPCHECK(launch_f5_attn(F.qkv16, F.lo_off, F.at, F.B, F.N, F.heads, F.hd, F.ldvt, INNER, scale, s));
         const GpuMat &Mo = mat_at(L.o);
         GemmArgs go = gemm_args(Mo, Mo.b, F.h, INNER, D, R);
         go.gate = ada + 2 * D;
@@ -1646,7 +1654,11 @@ int voxhip_f5_begin(int id, int B, int N, const float *cat0, const float *rope) 
         const size_t R = size_t(B) * size_t(N), D = size_t(F.dim), INNER = size_t(F.heads) * F.hd;
         const size_t W = 2 * size_t(F.mel) + F.text;
         F.cat = dalloc_t<float>(R * W); F.h = dalloc_t<float>(R * D); F.a = dalloc_t<float>(R * D);
-        F.nrm = dalloc_t<float>(R * D); F.qkv = dalloc_t<float>(R * 3 * INNER); F.at = dalloc_t<float>(R * INNER);
+        F.nrm = dalloc_t<float>(R * D); F.at = dalloc_t<float>(R * INNER);
+        F.ldvt = (N + 7) / 8 * 8;
+        F.lo_off = int64_t(R * 2 * INNER) + int64_t(B) * int64_t(INNER) * F.ldvt;
+        F.qkv16 = dalloc_t<_Float16>(size_t(2 * F.lo_off));
+        HIPCHECK(hipMemset(F.qkv16, 0, size_t(2 * F.lo_off) * sizeof(_Float16)));  // the v^T padding stays zero
         F.ffb = dalloc_t<float>(R * size_t(F.ff)); F.ada = dalloc_t<float>(size_t(F.depth) * 6 * D);
         F.fin = dalloc_t<float>(2 * D); F.ts = dalloc_t<float>(D); F.x = dalloc_t<float>(size_t(N) * F.mel);
         F.out = dalloc_t<float>(R * size_t(F.mel)); F.rope = dalloc_t<float>(size_t(N) * size_t(F.hd));
