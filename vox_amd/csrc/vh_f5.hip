@@ -4,10 +4,11 @@
 
 namespace vh {
 
-hipError_t launch_f5_modulate(const float *x, int64_t R, int D, const float *sc, const float *sh, float *y, hipStream_t s) {
+hipError_t launch_f5_modulate(const float *x, int64_t R, int D, const float *sc, const float *sh, float *y, _Float16 *y16,
+                              int64_t lo_off, hipStream_t s) {
     if (R <= 0) return hipSuccess;
-    if (D <= 0 || R > INT32_MAX) return hipErrorInvalidValue;
-    return launch(k_f5_modulate, dim3(unsigned(R)), dim3(256), 0, s, x, int32_t(D), sc, sh, y);
+    if (D <= 0 || R > INT32_MAX || (!y && !y16)) return hipErrorInvalidValue;
+    return launch(k_f5_modulate, dim3(unsigned(R)), dim3(256), 0, s, x, int32_t(D), sc, sh, y, y16, lo_off);
 }
 
 hipError_t launch_f5_fill_x(const float *x, int N, int mel, float *cat, int W, int B, hipStream_t s) {
@@ -17,11 +18,11 @@ hipError_t launch_f5_fill_x(const float *x, int N, int mel, float *cat, int W, i
                   int32_t(B));
 }
 
-hipError_t launch_f5_attn(const _Float16 *qkv16, int64_t lo_off, float *out, int B, int N, int heads, int hd, int ldvt, int ldo,
-                          float scale, hipStream_t s) {
+hipError_t launch_f5_attn(const _Float16 *qkv16, int64_t lo_off, float *out, _Float16 *out16, int64_t out_lo, int B, int N,
+                          int heads, int hd, int ldvt, int ldo, float scale, hipStream_t s) {
     if (B <= 0 || N <= 0) return hipSuccess;
-    if (hd != kF5Hd || heads <= 0 || ldvt < N || ldvt % 8 || lo_off % 8) return hipErrorInvalidValue;
-    F5AttnArgs a{qkv16, lo_off, out, int32_t(N), int32_t(ldo), int32_t(heads * hd), int32_t(ldvt), scale};
+    if (hd != kF5Hd || heads <= 0 || ldvt < N || ldvt % 8 || lo_off % 8 || (!out && !out16)) return hipErrorInvalidValue;
+    F5AttnArgs a{qkv16, lo_off, out, int32_t(N), int32_t(ldo), int32_t(heads * hd), int32_t(ldvt), scale, out16, out_lo};
     return launch(k_f5_attn, dim3(unsigned((N + 63) / 64), unsigned(heads), unsigned(B)), dim3(256), 0, s, a);
 }
 

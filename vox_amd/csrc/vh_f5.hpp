@@ -10,8 +10,10 @@ typedef float f32x4a __attribute__((ext_vector_type(4)));
 
 // LayerNorm without parameters + modulation (f5.cpp:608-625) of one row per block (256 threads): mean and
 // variance in double, inv = float(1 / sqrt(var + 1e-6)), y = (x - float(mean)) * inv * (1 + scale) + shift.
+// With y16 set, y goes out as f16 halves instead (hi at y16, lo at y16 + lo_off) for a split-f16 GEMM.
 __global__ __launch_bounds__(256) void k_f5_modulate(const float *__restrict__ x, int32_t D, const float *__restrict__ sc,
-                                                     const float *__restrict__ sh, float *__restrict__ y) {
+                                                     const float *__restrict__ sh, float *__restrict__ y,
+                                                     _Float16 *__restrict__ y16, int64_t lo_off) {
     __shared__ double red[4];
     const float *xr = x + int64_t(blockIdx.x) * D;
     float *yr = y + int64_t(blockIdx.x) * D;
@@ -34,6 +36,16 @@ __global__ __launch_bounds__(256) void k_f5_modulate(const float *__restrict__ x
     }
     const double var = bsum(v) / D;
     const float inv = float(1.0 / sqrt(var + 1e-6)), fm = float(mean);
+    if (y16) {
+        _Float16 *hr = y16 + int64_t(blockIdx.x) * D;
+        for (int i = t; i < D; i += 256) {
+            const float r = (xr[i] - fm) * inv * (1.0f + sc[i]) + sh[i];
+            const _Float16 hi = _Float16(r);
+            hr[i] = hi;
+            hr[lo_off + i] = _Float16(r - float(hi));
+        }
+        return;
+    }
     for (int i = t; i < D; i += 256) yr[i] = (xr[i] - fm) * inv * (1.0f + sc[i]) + sh[i];
 }
 
@@ -62,6 +74,8 @@ struct F5AttnArgs {
     float *out;           // [B N][ldo], head h at column h * 64
     int32_t N, ldo, inner, ldvt;
     float scale;
+    _Float16 *out16;      // when set: the output as f16 halves, hi at out16, lo at out16 + out_lo (rows of ldo)
+    int64_t out_lo;
 };
 constexpr int kF5Hd = kF5HeadDim;
 typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
@@ -192,9 +206,19 @@ __global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
         const int qr = q0 + 16 * wave + 4 * lg + i;
         if (qr >= a.N) continue;
         const float inv = 1.0f / lrow[i];
-        float *dst = a.out + (rb + qr) * a.ldo + int64_t(h) * kF5Hd;
+        const int64_t off = (rb + qr) * a.ldo + int64_t(h) * kF5Hd;
+        if (a.out16) {
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) dst[16 * dt + lr] = o[dt][i] * inv;
+            for (int dt = 0; dt < 4; ++dt) {
+                const float r = o[dt][i] * inv;
+                const _Float16 hi = _Float16(r);
+                a.out16[off + 16 * dt + lr] = hi;
+                a.out16[a.out_lo + off + 16 * dt + lr] = _Float16(r - float(hi));
+            }
+        } else {
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) a.out[off + 16 * dt + lr] = o[dt][i] * inv;
+        }
     }
 }
 

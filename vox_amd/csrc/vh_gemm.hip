@@ -62,6 +62,11 @@ static hipError_t gemm_tile(const uint8_t *w, const float *scale, const float *A
     }
 }
 
+static bool rope_h16_ok(const GemmArgs &g) {
+    return g.rope && g.h16 && g.hd > 0 && g.hd % 2 == 0 && g.seq > 0 && g.rope_cols % (2 * g.hd) == 0 && g.m % g.seq == 0 &&
+           g.n == g.rope_cols + g.rope_cols / 2 && g.ldvt >= g.seq && g.ldvt % 8 == 0;
+}
+
 template <int WT>
 static hipError_t gemm_epi(int epi, const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s) {
     switch (epi) {
@@ -74,10 +79,7 @@ static hipError_t gemm_epi(int epi, const uint8_t *w, const float *scale, const 
             if (!g.rope || g.hd <= 0 || g.hd % 2 || g.seq <= 0 || g.rope_cols % (2 * g.hd)) return hipErrorInvalidValue;
             return gemm_tile<WT, EPI_ROPE>(w, scale, A, g, s);
         case EPI_ROPE_H16:
-            if (!g.rope || !g.h16 || g.hd <= 0 || g.hd % 2 || g.seq <= 0 || g.rope_cols % (2 * g.hd) || g.m % g.seq ||
-                g.n != g.rope_cols + g.rope_cols / 2 || g.ldvt < g.seq || g.ldvt % 8)
-                return hipErrorInvalidValue;
-            return gemm_tile<WT, EPI_ROPE_H16>(w, scale, A, g, s);
+            return rope_h16_ok(g) ? gemm_tile<WT, EPI_ROPE_H16>(w, scale, A, g, s) : hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }
@@ -91,6 +93,29 @@ hipError_t launch_gemm(int wt, int epi, const uint8_t *w, const float *scale, co
         case WT_F16: return gemm_epi<WT_F16>(epi, w, scale, A, g, s);
         case WT_BF16: return gemm_epi<WT_BF16>(epi, w, scale, A, g, s);
         case WT_Q8: return g.K % 32 ? hipErrorInvalidValue : gemm_epi<WT_Q8>(epi, w, scale, A, g, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int EPI>
+static hipError_t gemm_hh_run(const _Float16 *w, const GemmArgs &g, hipStream_t s) {
+    const dim3 grid(unsigned((g.n + 63) / 64), unsigned((g.m + 63) / 64));
+    return launch(k_gemm_hh<EPI>, grid, dim3(256), 0, s, w, g);
+}
+
+hipError_t launch_gemm_hh(int epi, const _Float16 *w, const GemmArgs &g, hipStream_t s) {
+    if (g.m <= 0) return hipSuccess;
+    if (!w || !g.a16 || g.n <= 0 || g.K <= 0 || g.K % 64 || g.lda < g.K || g.lda % 8 || g.a_lo % 8 ||
+        int64_t(64) * g.lda * 2 > INT32_MAX || int64_t(64) * g.K * 2 > INT32_MAX)
+        return hipErrorInvalidValue;
+    const bool y_ok = g.y != nullptr;
+    switch (epi) {
+        case EPI_STORE: return y_ok ? gemm_hh_run<EPI_STORE>(w, g, s) : hipErrorInvalidValue;
+        case EPI_ACC: return y_ok ? gemm_hh_run<EPI_ACC>(w, g, s) : hipErrorInvalidValue;
+        case EPI_GATED_ACC: return y_ok && g.gate ? gemm_hh_run<EPI_GATED_ACC>(w, g, s) : hipErrorInvalidValue;
+        case EPI_GELU: return y_ok ? gemm_hh_run<EPI_GELU>(w, g, s) : hipErrorInvalidValue;
+        case EPI_GELU_H16: return g.h16 && g.ldy >= g.n ? gemm_hh_run<EPI_GELU_H16>(w, g, s) : hipErrorInvalidValue;
+        case EPI_ROPE_H16: return rope_h16_ok(g) ? gemm_hh_run<EPI_ROPE_H16>(w, g, s) : hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }

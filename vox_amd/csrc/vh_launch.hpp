@@ -32,6 +32,9 @@ hipError_t launch_qk_post(const QkArgs &a, int m, hipStream_t s);
 // Multi-row f32 GEMM on the matrix cores (F32 / F16 / BF16 / Q8 weights).
 hipError_t launch_gemm(int wt, int epi, const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s);
 // Grouped "same" Conv1d as an implicit-im2col GEMM (f32 weights [groups][cout/groups][K][cin/groups]).
+// Split-f16 GEMM with A already split by its producer (g.a16 hi, g.a16 + g.a_lo lo), F16 weights, K % 64 == 0;
+// epilogues STORE, ACC, GATED_ACC, GELU, GELU_H16, ROPE_H16.
+hipError_t launch_gemm_hh(int epi, const _Float16 *w, const GemmArgs &g, hipStream_t s);
 hipError_t launch_conv_gemm(int epi, const float *w, const float *A, const GemmArgs &g, int groups, hipStream_t s);
 // Merge of the split attention partials of m rows into ao [m][heads * hd].
 hipError_t launch_attn_merge(const AttnPartials &P, float *ao, int m, hipStream_t s);
@@ -59,10 +62,11 @@ hipError_t launch_copy16(const void *src, void *dst, int64_t bytes, hipStream_t 
 // Causal attention of a prefill pass (consecutive rows of one sequence) on the matrix cores, head_dim 64 or 128.
 hipError_t launch_prefill_attn(const PrefillAttnArgs &a, int hd, hipStream_t s);
 // F5-TTS DiT step: AdaLN modulation of R rows of D, the step input's x columns, attention (head_dim 64).
-hipError_t launch_f5_modulate(const float *x, int64_t R, int D, const float *sc, const float *sh, float *y, hipStream_t s);
+hipError_t launch_f5_modulate(const float *x, int64_t R, int D, const float *sc, const float *sh, float *y, _Float16 *y16,
+                              int64_t lo_off, hipStream_t s);
 hipError_t launch_f5_fill_x(const float *x, int N, int mel, float *cat, int W, int B, hipStream_t s);
-hipError_t launch_f5_attn(const _Float16 *qkv16, int64_t lo_off, float *out, int B, int N, int heads, int hd, int ldvt, int ldo,
-                          float scale, hipStream_t s);
+hipError_t launch_f5_attn(const _Float16 *qkv16, int64_t lo_off, float *out, _Float16 *out16, int64_t out_lo, int B, int N,
+                          int heads, int hd, int ldvt, int ldo, float scale, hipStream_t s);
 // CosyVoice2 LM: one sampling step (log-softmax, RAS trial loop) and the next step's embedding + row advance.
 hipError_t launch_lm_sample(const float *logits, int n, const LmCfgDev *cfg, LmState *st, int32_t *decoded, float *logp_out,
                             int64_t logp_stride, bool append, hipStream_t s);

@@ -8,7 +8,7 @@ namespace vh {
 enum { PRO_X = 0, PRO_RMS = 1, PRO_ATTN = 2 };
 enum { EPI_STORE = 0, EPI_ACC = 1, EPI_SWIGLU = 2 };
 // GEMM-only epilogues (F5 DiT): y += gate * c; y = gelu_tanh(c); y = mish(c); y += mish(c); RoPE on q|k columns
-enum { EPI_GATED_ACC = 3, EPI_GELU = 4, EPI_MISH = 5, EPI_MISH_ACC = 6, EPI_ROPE = 7, EPI_ROPE_H16 = 8 };
+enum { EPI_GATED_ACC = 3, EPI_GELU = 4, EPI_MISH = 5, EPI_MISH_ACC = 6, EPI_ROPE = 7, EPI_ROPE_H16 = 8, EPI_GELU_H16 = 9 };
 // GEMM A operand: rows of a matrix, or the implicit im2col rows of a grouped "same" Conv1d
 enum { ASRC_ROWS = 0, ASRC_CONV = 1 };
 // Weight formats of the GEMV kernels: the reference's types, plus Q4 with f16 block scales (WT_Q4H), the
@@ -115,9 +115,13 @@ struct GemmArgs {
     // EPI_ROPE_H16: the rotated q | k and v as f16 halves (x = hi + lo) for the attention's matrix cores, written to
     // h16 instead of y: plane hi then plane lo (lo_off halves apart), each = q | k rows [m][rope_cols] followed by
     // v transposed per batch and head, [m / seq][heads][hd][ldvt] (ldvt >= seq, a multiple of 8)
+    // EPI_GELU_H16: gelu_tanh(c + bias) as f16 halves into h16 (hi) and h16 + lo_off (lo), rows of ldy halves
     _Float16 *h16;
     int64_t lo_off;
     int32_t ldvt;
+    // k_gemm_hh: A already split into f16 halves, hi plane a16 and lo plane a16 + a_lo, rows of lda halves
+    const _Float16 *a16;
+    int64_t a_lo;
     // ASRC_CONV: x [m][lda] rows of `seq`-row batches; group g = blockIdx.z reads channels [g cig, (g + 1) cig) at
     // rows t + k - ksize / 2 of the same batch (zeros outside) for A column k cig + i; W and y are offset per group
     int32_t ksize, cig;

@@ -1478,6 +1478,9 @@ struct F5 {
     int in_proj = -1, norm_out = -1, proj_out = -1;
     std::vector<F5Block> blocks;
     F5Conv pos1, pos2;
+    // every block linear F16 and dim, inner, ff multiples of 64: the block's activations travel between kernels as
+    // f16 halves (hi, lo planes) and the linears take k_gemm_hh; otherwise f32 rows and k_gemm_h16 / k_gemm_f32
+    bool split = false;
     // step buffers of begin(B, N): rows R = B N
     int B = 0, N = 0;
     float *cat = nullptr, *h = nullptr, *a = nullptr, *nrm = nullptr, *at = nullptr, *ffb = nullptr;
@@ -1486,6 +1489,8 @@ struct F5 {
     _Float16 *qkv16 = nullptr;
     int64_t lo_off = 0;
     int ldvt = 0;
+    // split: the modulated rows, the attention output and the GELU output as hi / lo planes ([R][width] each)
+    _Float16 *nrm16 = nullptr, *at16 = nullptr, *ffb16 = nullptr;
 };
 
 F5 &f5_at(int id) {
@@ -1542,8 +1547,8 @@ F5Conv upload_conv(const voxhip_f5_conv &c, int dim) {
 void f5_free_step(F5 &F) {
     for (float *p : {F.cat, F.h, F.a, F.nrm, F.at, F.ffb, F.ada, F.fin, F.ts, F.x, F.out, F.rope}) dfree(p);
     F.cat = F.h = F.a = F.nrm = F.at = F.ffb = F.ada = F.fin = F.ts = F.x = F.out = F.rope = nullptr;
-    dfree(F.qkv16);
-    F.qkv16 = nullptr;
+    for (_Float16 *p : {F.qkv16, F.nrm16, F.at16, F.ffb16}) dfree(p);
+    F.qkv16 = F.nrm16 = F.at16 = F.ffb16 = nullptr;
     F.B = F.N = F.ldvt = 0;
     F.lo_off = 0;
 }
@@ -1558,6 +1563,15 @@ void f5_gemm(const GpuMat &m, int epi, const float *A, GemmArgs ga, hipStream_t 
     // matmul's f32-activation path for these rows (q8 above 8 rows; q4 never)
     if (int_path(m, ga.m)) throw Fail("F5 linears need f32 / f16 / bf16 weights, or q8 with more than 8 rows");
     HIPCHECK(launch_gemm(gemv_type(m), epi, m.w, m.s, A, ga, s));
+}
+// A block linear: from the f16 planes of A (width ga.K, lo plane R ga.K halves on) when the model is split,
+// else from the f32 rows A.
+void f5_lin(const F5 &F, const GpuMat &m, int epi, const float *A, const _Float16 *A16, GemmArgs ga, hipStream_t s) {
+    if (!F.split) return f5_gemm(m, epi, A, ga, s);
+    ga.a16 = A16;
+    ga.a_lo = int64_t(ga.m) * ga.K;
+    ga.lda = ga.K;
+    HIPCHECK(launch_gemm_hh(epi, reinterpret_cast<const _Float16 *>(m.w), ga, s));
 }
 
 // dit_forward on the device (f5.cpp:586-725) for the batches of begin; x [N][mel] and ts [dim] already on the device.
@@ -1584,25 +1598,29 @@ void f5_enqueue(F5 &F, hipStream_t s) {
     for (int i = 0; i < F.depth; ++i) {
         const F5Block &L = F.blocks[size_t(i)];
         const float *ada = F.ada + size_t(i) * 6 * D;  // shift, scale, gate (msa), shift, scale, gate (mlp)
-        HIPCHECK(launch_f5_modulate(F.h, R, D, ada + D, ada, F.nrm, s));
+        float *nrm = F.split ? nullptr : F.nrm;
+        HIPCHECK(launch_f5_modulate(F.h, R, D, ada + D, ada, nrm, F.nrm16, R * D, s));
         const GpuMat &Mq = mat_at(L.qkv);
         GemmArgs gq = gemm_args(Mq, Mq.b, nullptr, D, 3 * INNER, R);
         gq.rope = F.rope; gq.seq = F.N; gq.hd = F.hd; gq.rope_cols = 2 * INNER; gq.rope_heads = F.pe;
         gq.h16 = F.qkv16; gq.lo_off = F.lo_off; gq.ldvt = F.ldvt;
-        f5_gemm(Mq, EPI_ROPE_H16, F.nrm, gq, s);
-        HIPCHECK(launch_f5_attn(F.qkv16, F.lo_off, F.at, F.B, F.N, F.heads, F.hd, F.ldvt, INNER, scale, s));
+        f5_lin(F, Mq, EPI_ROPE_H16, F.nrm, F.nrm16, gq, s);
+        HIPCHECK(launch_f5_attn(F.qkv16, F.lo_off, F.split ? nullptr : F.at, F.at16, R * INNER, F.B, F.N, F.heads, F.hd,
+                                F.ldvt, INNER, scale, s));
         const GpuMat &Mo = mat_at(L.o);
         GemmArgs go = gemm_args(Mo, Mo.b, F.h, INNER, D, R);
         go.gate = ada + 2 * D;
-        f5_gemm(Mo, EPI_GATED_ACC, F.at, go, s);
-        HIPCHECK(launch_f5_modulate(F.h, R, D, ada + 4 * D, ada + 3 * D, F.nrm, s));
+        f5_lin(F, Mo, EPI_GATED_ACC, F.at, F.at16, go, s);
+        HIPCHECK(launch_f5_modulate(F.h, R, D, ada + 4 * D, ada + 3 * D, nrm, F.nrm16, R * D, s));
         const GpuMat &M1 = mat_at(L.ff1), &M2 = mat_at(L.ff2);
-        f5_gemm(M1, EPI_GELU, F.nrm, gemm_args(M1, M1.b, F.ffb, D, F.ff, R), s);
+        GemmArgs g1 = gemm_args(M1, M1.b, F.split ? nullptr : F.ffb, D, F.ff, R);
+        g1.h16 = F.ffb16; g1.lo_off = R * F.ff;
+        f5_lin(F, M1, F.split ? EPI_GELU_H16 : EPI_GELU, F.nrm, F.nrm16, g1, s);
         GemmArgs g2 = gemm_args(M2, M2.b, F.h, F.ff, D, R);
         g2.gate = ada + 5 * D;
-        f5_gemm(M2, EPI_GATED_ACC, F.ffb, g2, s);
+        f5_lin(F, M2, EPI_GATED_ACC, F.ffb, F.ffb16, g2, s);
     }
-    HIPCHECK(launch_f5_modulate(F.h, R, D, F.fin, F.fin + D, F.nrm, s));  // final modulation: (scale, shift)
+    HIPCHECK(launch_f5_modulate(F.h, R, D, F.fin, F.fin + D, F.nrm, nullptr, 0, s));  // final modulation: (scale, shift)
     const GpuMat &Mp = mat_at(F.proj_out);
     f5_gemm(Mp, EPI_STORE, F.nrm, gemm_args(Mp, Mp.b, F.out, D, F.mel, R), s);
 }
@@ -1638,6 +1656,9 @@ int voxhip_f5_create(const voxhip_f5_desc *d) {
             fb.qkv = stack_rows({b.q, b.k, b.v});
             F->blocks.push_back(fb);
         }
+        F->split = D % 64 == 0 && INNER % 64 == 0 && FF % 64 == 0;
+        for (const F5Block &fb : F->blocks)
+            for (int id : {fb.qkv, fb.o, fb.ff1, fb.ff2}) F->split = F->split && mat_at(id).type == VOXHIP_F16;
         F->pos1 = upload_conv(d->pos1, D);
         F->pos2 = upload_conv(d->pos2, D);
         g.f5.push_back(F.release());
@@ -1654,12 +1675,20 @@ int voxhip_f5_begin(int id, int B, int N, const float *cat0, const float *rope) 
         const size_t R = size_t(B) * size_t(N), D = size_t(F.dim), INNER = size_t(F.heads) * F.hd;
         const size_t W = 2 * size_t(F.mel) + F.text;
         F.cat = dalloc_t<float>(R * W); F.h = dalloc_t<float>(R * D); F.a = dalloc_t<float>(R * D);
-        F.nrm = dalloc_t<float>(R * D); F.at = dalloc_t<float>(R * INNER);
+        F.nrm = dalloc_t<float>(R * D);
+        if (F.split) {
+            F.nrm16 = dalloc_t<_Float16>(2 * R * D);
+            F.at16 = dalloc_t<_Float16>(2 * R * INNER);
+            F.ffb16 = dalloc_t<_Float16>(2 * R * size_t(F.ff));
+        } else {
+            F.at = dalloc_t<float>(R * INNER);
+            F.ffb = dalloc_t<float>(R * size_t(F.ff));
+        }
         F.ldvt = (N + 7) / 8 * 8;
         F.lo_off = int64_t(R * 2 * INNER) + int64_t(B) * int64_t(INNER) * F.ldvt;
         F.qkv16 = dalloc_t<_Float16>(size_t(2 * F.lo_off));
         HIPCHECK(hipMemset(F.qkv16, 0, size_t(2 * F.lo_off) * sizeof(_Float16)));  // the v^T padding stays zero
-        F.ffb = dalloc_t<float>(R * size_t(F.ff)); F.ada = dalloc_t<float>(size_t(F.depth) * 6 * D);
+        F.ada = dalloc_t<float>(size_t(F.depth) * 6 * D);
         F.fin = dalloc_t<float>(2 * D); F.ts = dalloc_t<float>(D); F.x = dalloc_t<float>(size_t(N) * F.mel);
         F.out = dalloc_t<float>(R * size_t(F.mel)); F.rope = dalloc_t<float>(size_t(N) * size_t(F.hd));
         h2d(F.cat, cat0, R * W * 4);
