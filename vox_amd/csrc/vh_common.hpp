@@ -12,6 +12,23 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 namespace vh {
 
 constexpr int kWave = 64;
+// MI355X hands the workgroups of a launch round-robin to its 8 XCDs (linear id % 8), and each XCD has its own L2.
+// xcd_tile maps linear id L of T blocks to a tile index so that XCD x takes the contiguous tiles
+// [x T / 8, (x + 1) T / 8): neighbouring tiles, which share operand rows, then meet in one L2 instead of every XCD
+// streaming all of them. T % 8 != 0: identity.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_tile(int L, int T) { return T % kXcds ? L : (L % kXcds) * (T / kXcds) + L / kXcds; }
+
+// Raw buffer loads: an access whose vector offset reaches `bytes` reads zeros, so tiles that overhang a matrix need
+// no per-load bounds check. Only the vector offset is relied on for the range check: a scalar offset carries a
+// uniform step that stays inside the row the vector offset selects.
+constexpr int kBufFlags = 0x00020000;  // buffer resource word 3 for gfx9 raw buffers (32-bit data format)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, int32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, kBufFlags);
+}
+__device__ __forceinline__ u32x4 buf_ld16(__amdgpu_buffer_rsrc_t r, int32_t voff, int32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
 
 // Cross-lane steps on the DPP path (no LDS round trip): quad permutations and row mirrors within 16-lane rows.
 enum : int { kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppRowHalfMirror = 0x141, kDppRowMirror = 0x140 };

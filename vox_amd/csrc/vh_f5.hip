@@ -21,7 +21,8 @@ hipError_t launch_f5_fill_x(const float *x, int N, int mel, float *cat, int W, i
 hipError_t launch_f5_attn(const _Float16 *qkv16, int64_t lo_off, float *out, _Float16 *out16, int64_t out_lo, int B, int N,
                           int heads, int hd, int ldvt, int ldo, float scale, hipStream_t s) {
     if (B <= 0 || N <= 0) return hipSuccess;
-    if (hd != kF5Hd || heads <= 0 || ldvt < N || ldvt % 8 || lo_off % 8 || (!out && !out16)) return hipErrorInvalidValue;
+    if (hd != kF5Hd || heads <= 0 || ldvt < N || ldvt % 64 || lo_off % 8 || ldo % 4 || (!out && !out16)) return hipErrorInvalidValue;
+    if ((int64_t(N) + 64) * 2 * heads * hd * 2 > INT32_MAX) return hipErrorInvalidValue;  // the q / k buffer offsets
     F5AttnArgs a{qkv16, lo_off, out, int32_t(N), int32_t(ldo), int32_t(heads * hd), int32_t(ldvt), scale, out16, out_lo};
     return launch(k_f5_attn, dim3(unsigned((N + 63) / 64), unsigned(heads), unsigned(B)), dim3(256), 0, s, a);
 }

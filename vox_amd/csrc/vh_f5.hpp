@@ -61,13 +61,16 @@ __global__ __launch_bounds__(256) void k_f5_fill_x(const float *__restrict__ x, 
 // Non-causal softmax attention of one head over N keys (f5.cpp:626-650): S = (q . k) * scale, softmax per row,
 // O = P V, for head_dim 64. grid (ceil(N / 64), heads, B), block 256: each wave takes 16 query rows; key tiles of
 // 64 go through LDS; an online softmax (running max and sum per row, O rescaled) replaces the reference's
-// whole-row max, which changes only the rounding.
+// whole-row max, which changes only the rounding; exp(x) is taken as 2^(x log2 e) on v_exp_f32.
 // Both products run on the f16 matrix cores (v_mfma_f32_16x16x32_f16) with every f32 operand as two f16 halves,
 // x = hi + lo, and three products per pair (hi.hi + hi.lo + lo.hi; the dropped lo.lo term is below 2^-22 relative):
 // each product is exact in the f32 accumulator, so S and P V keep f32-level accuracy. q, k and v arrive already
-// split (the q|k|v GEMM's EPI_ROPE_H16 epilogue: q | k rows and v transposed to [d][key]), so key and value tiles
-// are plain 16-byte loads; the softmax weights are split here. The next tile's loads are in flight during the
-// current tile's MFMAs.
+// split (the q|k|v GEMM's EPI_ROPE_H16 epilogue: q | k rows and v transposed to [d][key], its key columns padded
+// with zeros to a multiple of 64), so key and value tiles are plain 16-byte loads.
+// The products are taken transposed, S^T = K Q^T and O^T = V^T P^T, so that a lane holds one query row (lane % 16)
+// throughout: its S^T values (keys 16 j + 4 (lane / 16) + i) are already the B operand of P^T once the 32 keys
+// of a chunk are numbered in the order the lanes hold them (V^T's A operand read in that same order), P never
+// leaves registers, and the row's max, sum and rescale need only two cross-row shuffles each.
 struct F5AttnArgs {
     const _Float16 *h16;  // hi plane; the lo plane is lo_off halves further
     int64_t lo_off;
@@ -79,8 +82,13 @@ struct F5AttnArgs {
 };
 constexpr int kF5Hd = kF5HeadDim;
 typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
 constexpr int kF5Ld = 64 + 8;  // LDS row stride in halves
 VH_DEV h16x8 ld16(const _Float16 *p) { return *reinterpret_cast<const h16x8 *>(p); }
+VH_DEV h16x8 ld8x2(const _Float16 *p, const _Float16 *q) {  // halves p[0..3], q[0..3]
+    const h16x4 x = *reinterpret_cast<const h16x4 *>(p), y = *reinterpret_cast<const h16x4 *>(q);
+    return h16x8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+}
 VH_DEV f32x4a mfma3(h16x8 ah, h16x8 al, h16x8 bh, h16x8 bl, f32x4a c) {
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, c, 0, 0, 0);
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);
@@ -89,135 +97,146 @@ VH_DEV f32x4a mfma3(h16x8 ah, h16x8 al, h16x8 bh, h16x8 bl, f32x4a c) {
 __global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
     __shared__ __align__(16) _Float16 Kh[64][kF5Ld], Kl[64][kF5Ld];  // [key][d]
     __shared__ __align__(16) _Float16 Vh[64][kF5Ld], Vl[64][kF5Ld];  // [d][key]
-    __shared__ __align__(16) float Ps[4][16][68];                     // per wave [row][key]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
-    const int q0 = blockIdx.x * 64, h = blockIdx.y, b = blockIdx.z, heads = gridDim.y;
-    const int64_t ldqk = 2 * int64_t(a.inner), rb = int64_t(b) * a.N;
-    const _Float16 *QK = a.h16;                                                  // q | k rows
+    // a contiguous run of (batch, head) pairs per XCD, so each head's keys and values stay in one L2
+    const int qt = gridDim.x, heads = gridDim.y;
+    const int t = xcd_tile(int(blockIdx.x) + qt * (int(blockIdx.y) + heads * int(blockIdx.z)), qt * heads * int(gridDim.z));
+    const int q0 = (t % qt) * 64, h = (t / qt) % heads, b = t / (qt * heads);
+    const int64_t ldqk = 2 * int64_t(a.inner);
+    // this batch's q and k rows of head h as buffers ending at row N (rows past it read as zeros)
+    const _Float16 *qb = a.h16 + int64_t(b) * a.N * ldqk + h * kF5Hd, *kb = qb + a.inner;
+    const int32_t rows_bytes = int32_t(((a.N - 1) * ldqk + kF5Hd) * 2);
+    const __amdgpu_buffer_rsrc_t rqh = buf_rsrc(qb, rows_bytes), rql = buf_rsrc(qb + a.lo_off, rows_bytes);
+    const __amdgpu_buffer_rsrc_t rkh = buf_rsrc(kb, rows_bytes), rkl = buf_rsrc(kb + a.lo_off, rows_bytes);
     const _Float16 *VT = a.h16 + int64_t(gridDim.z) * a.N * ldqk + (int64_t(b) * heads + h) * kF5Hd * a.ldvt;  // [d][key]
-    // A operand of S: lane holds q[16 wave + lr][32 c + 8 lg + e]
+    // B operand of S^T: lane holds q[q0 + 16 wave + lr][32 c + 8 lg + e]
     h16x8 qh[2], ql[2];
     {
-        const int qr = q0 + 16 * wave + lr;
+        const int32_t off = int32_t(((q0 + 16 * wave + lr) * ldqk + 8 * lg) * 2);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            qh[c] = ql[c] = h16x8{0, 0, 0, 0, 0, 0, 0, 0};
-            if (qr < a.N) {
-                const _Float16 *p = QK + (rb + qr) * ldqk + h * kF5Hd + 32 * c + 8 * lg;
-                qh[c] = ld16(p);
-                ql[c] = ld16(p + a.lo_off);
-            }
+            qh[c] = __builtin_bit_cast(h16x8, buf_ld16(rqh, off + 64 * c, 0));
+            ql[c] = __builtin_bit_cast(h16x8, buf_ld16(rql, off + 64 * c, 0));
         }
     }
-    float mrow[4], lrow[4];
-    f32x4a o[4];
+    const float sl = a.scale * 1.4426950408889634f;  // scores in log2 units
+    float mrow = -INFINITY, lrow = 0.f;  // of query row lr
+    f32x4a o[4];  // O^T: lane holds O[row lr][16 dt + 4 lg + i]
 #pragma unroll
-    for (int i = 0; i < 4; ++i) { mrow[i] = -INFINITY; lrow[i] = 0.f; o[i] = f32x4a{0.f, 0.f, 0.f, 0.f}; }
-    // per thread and tile: 2 chunks of 8 halves of K (hi, lo) and of v^T (hi, lo)
-    h16x8 kr[2][2], vr[2][2];
+    for (int i = 0; i < 4; ++i) o[i] = f32x4a{0.f, 0.f, 0.f, 0.f};
+    // per thread and tile: keys / d rows r and r + 32, columns c8 .. c8 + 7, of K and v^T (hi, lo)
+    const int r = tid >> 3, c8 = (tid & 7) * 8;
+    const int32_t ko0 = int32_t((r * ldqk + c8) * 2), ko1 = int32_t(((r + 32) * ldqk + c8) * 2);
+    const _Float16 *v0 = VT + int64_t(r) * a.ldvt + c8, *v1 = v0 + 32 * int64_t(a.ldvt);
+    u32x4 kr[4], vr[4];
     auto fetch = [&](int kt) {
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int idx = tid + 256 * q, r = idx >> 3, c8 = (idx & 7) * 8;  // r: key (K) or d (v^T); c8: d or key
-#pragma unroll
-            for (int hl = 0; hl < 2; ++hl) {
-                kr[q][hl] = vr[q][hl] = h16x8{0, 0, 0, 0, 0, 0, 0, 0};
-                const int64_t off = hl ? a.lo_off : 0;
-                if (kt + r < a.N) kr[q][hl] = ld16(QK + off + (rb + kt + r) * ldqk + a.inner + h * kF5Hd + c8);
-                if (kt + c8 < a.N) vr[q][hl] = ld16(VT + off + int64_t(r) * a.ldvt + kt + c8);
-            }
-        }
+        // the key row goes in the vector offset, which the buffer's range check covers
+        const int32_t ro = int32_t(kt * ldqk * 2), k0o = ko0 + ro, k1o = ko1 + ro;
+        kr[0] = buf_ld16(rkh, k0o, 0);
+        kr[1] = buf_ld16(rkh, k1o, 0);
+        kr[2] = buf_ld16(rkl, k0o, 0);
+        kr[3] = buf_ld16(rkl, k1o, 0);
+        vr[0] = *reinterpret_cast<const u32x4 *>(v0 + kt);
+        vr[1] = *reinterpret_cast<const u32x4 *>(v1 + kt);
+        vr[2] = *reinterpret_cast<const u32x4 *>(v0 + a.lo_off + kt);
+        vr[3] = *reinterpret_cast<const u32x4 *>(v1 + a.lo_off + kt);
     };
     fetch(0);
     for (int kt = 0; kt < a.N; kt += 64) {
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int idx = tid + 256 * q, r = idx >> 3, c8 = (idx & 7) * 8;
-            *reinterpret_cast<h16x8 *>(&Kh[r][c8]) = kr[q][0];
-            *reinterpret_cast<h16x8 *>(&Kl[r][c8]) = kr[q][1];
-            *reinterpret_cast<h16x8 *>(&Vh[r][c8]) = vr[q][0];
-            *reinterpret_cast<h16x8 *>(&Vl[r][c8]) = vr[q][1];
-        }
+        *reinterpret_cast<u32x4 *>(&Kh[r][c8]) = kr[0];
+        *reinterpret_cast<u32x4 *>(&Kh[r + 32][c8]) = kr[1];
+        *reinterpret_cast<u32x4 *>(&Kl[r][c8]) = kr[2];
+        *reinterpret_cast<u32x4 *>(&Kl[r + 32][c8]) = kr[3];
+        *reinterpret_cast<u32x4 *>(&Vh[r][c8]) = vr[0];
+        *reinterpret_cast<u32x4 *>(&Vh[r + 32][c8]) = vr[1];
+        *reinterpret_cast<u32x4 *>(&Vl[r][c8]) = vr[2];
+        *reinterpret_cast<u32x4 *>(&Vl[r + 32][c8]) = vr[3];
         __syncthreads();
-        if (kt + 64 < a.N) fetch(kt + 64);
-        // S tiles: B operand lane holds K[16 j + lr][32 c + 8 lg + e]
+        fetch(min(kt + 64, a.ldvt - 64));  // unconditional (the last tile again at the end): exact wait counts
+        // S^T tiles: A operand lane holds K[16 j + lr][32 c + 8 lg + e]; lane gets S^T[16 j + 4 lg + i][lr]
         f32x4a s[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             s[j] = f32x4a{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < 2; ++c)
-                s[j] = mfma3(qh[c], ql[c], ld16(&Kh[16 * j + lr][32 * c + 8 * lg]), ld16(&Kl[16 * j + lr][32 * c + 8 * lg]), s[j]);
+                s[j] = mfma3(ld16(&Kh[16 * j + lr][32 * c + 8 * lg]), ld16(&Kl[16 * j + lr][32 * c + 8 * lg]), qh[c], ql[c], s[j]);
         }
-        // lane holds S[4 lg + i][16 j + lr]: the 16 lanes of a DPP row share the rows
+        float mx = -INFINITY;
+        if (kt + 64 <= a.N) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float mx = -INFINITY;
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float v = kt + 16 * j + lr < a.N ? s[j][i] * a.scale : -INFINITY;
-                s[j][i] = v;
-                mx = fmaxf(mx, v);
-            }
-            mx = fmaxf(mx, dpp<kDppXor1>(mx));
-            mx = fmaxf(mx, dpp<kDppXor2>(mx));
-            mx = fmaxf(mx, dpp<kDppRowHalfMirror>(mx));
-            mx = fmaxf(mx, dpp<kDppRowMirror>(mx));
-            const float mnew = fmaxf(mrow[i], mx);
-            const float alpha = expf(mrow[i] - mnew);  // 0 on the first tile (mrow = -inf)
-            float sum = 0.f;
+                for (int i = 0; i < 4; ++i) {
+                    s[j][i] *= sl;
+                    mx = fmaxf(mx, s[j][i]);
+                }
+        } else {  // the last, partial tile: keys past N drop out
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float p = expf(s[j][i] - mnew);
-                sum += p;
-                Ps[wave][4 * lg + i][16 * j + lr] = p;
-            }
-            sum += dpp<kDppXor1>(sum);
-            sum += dpp<kDppXor2>(sum);
-            sum += dpp<kDppRowHalfMirror>(sum);
-            sum += dpp<kDppRowMirror>(sum);
-            lrow[i] = lrow[i] * alpha + sum;
-            mrow[i] = mnew;
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt) o[dt][i] *= alpha;
+                for (int i = 0; i < 4; ++i) {
+                    s[j][i] = kt + 16 * j + 4 * lg + i < a.N ? s[j][i] * sl : -INFINITY;
+                    mx = fmaxf(mx, s[j][i]);
+                }
         }
-        __syncthreads();
-        // O += P V: A lane holds P[lr][32 c + 8 lg + e] (split here); B lane holds V[32 c + 8 lg + e][16 dt + lr]
+        // the row's keys sit in lanes lr, lr + 16, lr + 32, lr + 48
+        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const float mnew = fmaxf(mrow, mx);
+        const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);  // 0 on the first tile (mrow = -inf)
+        float sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                s[j][i] = __builtin_amdgcn_exp2f(s[j][i] - mnew);
+                sum += s[j][i];
+            }
+        sum += __shfl_xor(sum, 16, kWave);
+        sum += __shfl_xor(sum, 32, kWave);
+        lrow = lrow * alpha + sum;
+        mrow = mnew;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+        // O^T += V^T P^T over the 32 keys of chunk c, numbered as the lanes hold them: index 8 lg + e is key
+        // 32 c + 4 lg + e (e < 4) or 32 c + 16 + 4 lg + (e - 4); A operand lane holds V^T[16 dt + lr][those keys]
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            const f32x4a p0 = *reinterpret_cast<const f32x4a *>(&Ps[wave][lr][32 * c + 8 * lg]);
-            const f32x4a p1 = *reinterpret_cast<const f32x4a *>(&Ps[wave][lr][32 * c + 8 * lg + 4]);
-            h16x8 pah, pal;
+            h16x8 ph, pl;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float x = e < 4 ? p0[e] : p1[e - 4];
+                const float x = s[2 * c + (e >> 2)][e & 3];
                 const _Float16 hi = _Float16(x);
-                pah[e] = hi;
-                pal[e] = _Float16(x - float(hi));
+                ph[e] = hi;
+                pl[e] = _Float16(x - float(hi));
             }
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
-                o[dt] = mfma3(pah, pal, ld16(&Vh[16 * dt + lr][32 * c + 8 * lg]), ld16(&Vl[16 * dt + lr][32 * c + 8 * lg]), o[dt]);
+            for (int dt = 0; dt < 4; ++dt) {
+                const int d = 16 * dt + lr, k0 = 32 * c + 4 * lg;
+                o[dt] = mfma3(ld8x2(&Vh[d][k0], &Vh[d][k0 + 16]), ld8x2(&Vl[d][k0], &Vl[d][k0 + 16]), ph, pl, o[dt]);
+            }
         }
         __syncthreads();
     }
+    const int qr = q0 + 16 * wave + lr;
+    if (qr >= a.N) return;
+    const float inv = 1.0f / lrow;
+    const int64_t off = (int64_t(b) * a.N + qr) * a.ldo + int64_t(h) * kF5Hd + 4 * lg;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int qr = q0 + 16 * wave + 4 * lg + i;
-        if (qr >= a.N) continue;
-        const float inv = 1.0f / lrow[i];
-        const int64_t off = (rb + qr) * a.ldo + int64_t(h) * kF5Hd;
+    for (int dt = 0; dt < 4; ++dt) {
+        const f32x4a y = o[dt] * inv;
         if (a.out16) {
+            h16x4 hi, lo;
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt) {
-                const float r = o[dt][i] * inv;
-                const _Float16 hi = _Float16(r);
-                a.out16[off + 16 * dt + lr] = hi;
-                a.out16[a.out_lo + off + 16 * dt + lr] = _Float16(r - float(hi));
+            for (int i = 0; i < 4; ++i) {
+                hi[i] = _Float16(y[i]);
+                lo[i] = _Float16(y[i] - float(hi[i]));
             }
+            *reinterpret_cast<h16x4 *>(a.out16 + off + 16 * dt) = hi;
+            *reinterpret_cast<h16x4 *>(a.out16 + a.out_lo + off + 16 * dt) = lo;
         } else {
-#pragma unroll
-            for (int dt = 0; dt < 4; ++dt) a.out[off + 16 * dt + lr] = o[dt][i] * inv;
+            *reinterpret_cast<f32x4a *>(a.out + off + 16 * dt) = y;
         }
     }
 }

@@ -364,62 +364,60 @@ __global__ __launch_bounds__(256) void k_gemm_h16(const uint8_t *__restrict__ w,
     gemm_epilogue<EPI, TM, TN>(acc, g, m0, n0, wm, wn, lane);
 }
 
-constexpr int kBufFlags = 0x00020000;  // buffer resource word 3 for gfx9 raw buffers (32-bit data format)
-VH_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, int32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, kBufFlags);
-}
-VH_DEV u32x4 buf_ld16(__amdgpu_buffer_rsrc_t r, int32_t voff, int32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-}
-
 // The split-f16 GEMM of k_gemm_h16 for F16 weights when the producer has already split A: hi plane g.a16, lo
-// plane g.a16 + g.a_lo (rows of g.lda halves), K a multiple of 64. Tiles 64 x 64 (4 waves of 32 x 32), K steps of
-// 64 through LDS as 16-byte copies, no conversion. The loads go through buffer resources cut at the block's last
-// row of A and of W, so rows past m or n read as zeros without a per-load bounds check, and the K offset of a
-// step is the scalar offset: a K step costs the wave 6 buffer loads, 6 LDS stores, 12 LDS fragment reads and 16
-// MFMAs. Two K steps are in flight (two register sets alternate), so a load has two steps' MFMAs to arrive.
-template <int EPI>
+// plane g.a16 + g.a_lo (rows of g.lda halves), K a multiple of 64. Block tile 64 rows of A x 32 TN rows of W (4
+// waves of 32 x 16 TN), K steps of 64 through LDS as 16-byte copies, no conversion. The loads go through buffer
+// resources cut at the block's last row of A and of W, so rows past m or n read as zeros without a per-load bounds
+// check, and the K offset of a step is the scalar offset. Per K step a wave issues 4 + TN buffer loads, as many LDS
+// stores, 8 + 4 TN LDS fragment reads and 16 TN MFMAs: the wider W tile (TN 4) reads fewer LDS bytes per MFMA,
+// since every A fragment comes twice (hi, lo). Two K steps are in flight (two register sets alternate), so a load
+// has two steps' MFMAs to arrive.
+template <int EPI, int TN>
 __global__ __launch_bounds__(256) void k_gemm_hh(const _Float16 *__restrict__ w, GemmArgs g) {
-    constexpr int BK = 64, LD = BK + 8;
-    __shared__ __align__(16) _Float16 Ah[64][LD], Al[64][LD], Bs[64][LD];
+    constexpr int BK = 64, LD = BK + 8, BN = 32 * TN;
+    __shared__ __align__(16) _Float16 Ah[64][LD], Al[64][LD], Bs[BN][LD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64, K = g.K;
-    const int mr = min(64, g.m - m0), nr = min(64, g.n - n0);
+    // row-major tiles, a band of rows of A per XCD (its rows of A and all of W stay in that XCD's L2)
+    const int nt = gridDim.x, t = xcd_tile(blockIdx.y * nt + blockIdx.x, nt * gridDim.y);
+    const int m0 = (t / nt) * 64, n0 = (t % nt) * BN, K = g.K;
+    const int mr = min(64, g.m - m0), nr = min(BN, g.n - n0);
     const _Float16 *a0 = g.a16 + int64_t(m0) * g.lda;
     const __amdgpu_buffer_rsrc_t rah = buf_rsrc(a0, int32_t(mr * g.lda * 2));
     const __amdgpu_buffer_rsrc_t ral = buf_rsrc(a0 + g.a_lo, int32_t(mr * g.lda * 2));
     const __amdgpu_buffer_rsrc_t rw = buf_rsrc(w + int64_t(n0) * K, nr * K * 2);
-    // this thread's 8-half chunks of a 64 x 64 tile: rows r and r + 32, columns c8 .. c8 + 7
+    // this thread's 8-half chunks of a tile: rows r + 32 q, columns c8 .. c8 + 7
     const int r = tid >> 3, c8 = (tid & 7) * 8;
     const int va0 = int32_t((r * g.lda + c8) * 2), va1 = int32_t(((r + 32) * g.lda + c8) * 2);
-    const int vw0 = (r * K + c8) * 2, vw1 = ((r + 32) * K + c8) * 2;
-    f32x4v acc[2][2];
+    int vw[TN];
+#pragma unroll
+    for (int q = 0; q < TN; ++q) vw[q] = ((r + 32 * q) * K + c8) * 2;
+    f32x4v acc[2][TN];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
-    u32x4 xa0[4], xw0[2], xa1[4], xw1[2];
-    auto fetch = [&](u32x4(&a)[4], u32x4(&b)[2], int k0) {
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    u32x4 xa0[4], xw0[TN], xa1[4], xw1[TN];
+    auto fetch = [&](u32x4(&a)[4], u32x4(&b)[TN], int k0) {
         const int so = k0 * 2;
         a[0] = buf_ld16(rah, va0, so);
         a[1] = buf_ld16(rah, va1, so);
         a[2] = buf_ld16(ral, va0, so);
         a[3] = buf_ld16(ral, va1, so);
-        b[0] = buf_ld16(rw, vw0, so);
-        b[1] = buf_ld16(rw, vw1, so);
+#pragma unroll
+        for (int q = 0; q < TN; ++q) b[q] = buf_ld16(rw, vw[q], so);
     };
-    auto stage = [&](const u32x4(&a)[4], const u32x4(&b)[2]) {
+    auto stage = [&](const u32x4(&a)[4], const u32x4(&b)[TN]) {
         *reinterpret_cast<u32x4 *>(&Ah[r][c8]) = a[0];
         *reinterpret_cast<u32x4 *>(&Ah[r + 32][c8]) = a[1];
         *reinterpret_cast<u32x4 *>(&Al[r][c8]) = a[2];
         *reinterpret_cast<u32x4 *>(&Al[r + 32][c8]) = a[3];
-        *reinterpret_cast<u32x4 *>(&Bs[r][c8]) = b[0];
-        *reinterpret_cast<u32x4 *>(&Bs[r + 32][c8]) = b[1];
+#pragma unroll
+        for (int q = 0; q < TN; ++q) *reinterpret_cast<u32x4 *>(&Bs[r + 32 * q][c8]) = b[q];
     };
     auto mma = [&]() {
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 32) {
-            f16x8v ah[2], al[2], b[2];
+            f16x8v ah[2], al[2], b[TN];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int rr = wm * 32 + i * 16 + (lane & 15);
@@ -427,34 +425,41 @@ __global__ __launch_bounds__(256) void k_gemm_hh(const _Float16 *__restrict__ w,
                 al[i] = *reinterpret_cast<const f16x8v *>(&Al[rr][kk + 8 * (lane >> 4)]);
             }
 #pragma unroll
-            for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const f16x8v *>(&Bs[wn * 32 + j * 16 + (lane & 15)][kk + 8 * (lane >> 4)]);
+            for (int j = 0; j < TN; ++j)
+                b[j] = *reinterpret_cast<const f16x8v *>(&Bs[wn * 16 * TN + j * 16 + (lane & 15)][kk + 8 * (lane >> 4)]);
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < TN; ++j) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], acc[i][j], 0, 0, 0);
                 }
         }
     };
-    const int ns = K / BK;
+    // Every fetch is unconditional (steps past the end re-read the last one), so the compiler's count of loads in
+    // flight is exact: staging one set waits only for that set, the other stays in flight.
+    const int ns = K / BK, klast = K - BK;
     fetch(xa0, xw0, 0);
-    if (ns > 1) fetch(xa1, xw1, BK);
-    for (int s = 0; s < ns; s += 2) {
+    __builtin_amdgcn_sched_barrier(0);  // keep the first set's loads ahead of the second's
+    fetch(xa1, xw1, min(BK, klast));
+    for (int s = 0; s + 1 < ns; s += 2) {  // one back edge: the first set is always the older in flight
         stage(xa0, xw0);
         __syncthreads();
-        if (s + 2 < ns) fetch(xa0, xw0, (s + 2) * BK);
+        fetch(xa0, xw0, min((s + 2) * BK, klast));
         mma();
         __syncthreads();
-        if (s + 1 < ns) {
-            stage(xa1, xw1);
-            __syncthreads();
-            if (s + 3 < ns) fetch(xa1, xw1, (s + 3) * BK);
-            mma();
-            __syncthreads();
-        }
+        stage(xa1, xw1);
+        __syncthreads();
+        fetch(xa1, xw1, min((s + 3) * BK, klast));
+        mma();
+        __syncthreads();
     }
-    gemm_epilogue<EPI, 2, 2>(acc, g, m0, n0, wm, wn, lane);
+    if (ns & 1) {  // the last step, in the first set
+        stage(xa0, xw0);
+        __syncthreads();
+        mma();
+    }
+    gemm_epilogue<EPI, 2, TN>(acc, g, m0, n0, wm, wn, lane);
 }
 
 // The split-K partial slices ws[z][m][n], added in z order, then bias and the epilogue (STORE, ACC, GATED_ACC,

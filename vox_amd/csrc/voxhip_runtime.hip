@@ -1684,7 +1684,7 @@ int voxhip_f5_begin(int id, int B, int N, const float *cat0, const float *rope) 
             F.at = dalloc_t<float>(R * INNER);
             F.ffb = dalloc_t<float>(R * size_t(F.ff));
         }
-        F.ldvt = (N + 7) / 8 * 8;
+        F.ldvt = (N + 63) / 64 * 64;  // whole key tiles, the padding zero
         F.lo_off = int64_t(R * 2 * INNER) + int64_t(B) * int64_t(INNER) * F.ldvt;
         F.qkv16 = dalloc_t<_Float16>(size_t(2 * F.lo_off));
         HIPCHECK(hipMemset(F.qkv16, 0, size_t(2 * F.lo_off) * sizeof(_Float16)));  // the v^T padding stays zero
