@@ -62,11 +62,10 @@ static hipError_t gemm_tile(const uint8_t *w, const float *scale, const float *A
     }
 }
 
-constexpr int64_t kHhWideBlocks = INT64_MAX;  // 128-row W tiles measured slower on the DiT shapes: off
 
 static bool rope_h16_ok(const GemmArgs &g) {
     return g.rope && g.h16 && g.hd > 0 && g.hd % 2 == 0 && g.seq > 0 && g.rope_cols % (2 * g.hd) == 0 && g.m % g.seq == 0 &&
-           g.n == g.rope_cols + g.rope_cols / 2 && g.ldvt >= g.seq && g.ldvt % 8 == 0;
+           g.n == g.rope_cols + g.rope_cols / 2 && g.ldvt >= g.seq && g.ldvt % 8 == 0 && g.lo_off % 8 == 0;
 }
 
 template <int WT>
@@ -99,13 +98,11 @@ hipError_t launch_gemm(int wt, int epi, const uint8_t *w, const float *scale, co
     }
 }
 
-// W tiles of 128 rows when that gives kHhWideBlocks blocks, else 64.
+// 64 x 64 tiles, K steps of 64: measured faster on the DiT shapes than 64 x 128 tiles or K steps of 128.
 template <int EPI>
 static hipError_t gemm_hh_run(const _Float16 *w, const GemmArgs &g, hipStream_t s) {
     const unsigned mt = unsigned((g.m + 63) / 64);
-    if (int64_t(mt) * ((g.n + 127) / 128) >= kHhWideBlocks)
-        return launch(k_gemm_hh<EPI, 4>, dim3(unsigned((g.n + 127) / 128), mt), dim3(256), 0, s, w, g);
-    return launch(k_gemm_hh<EPI, 2>, dim3(unsigned((g.n + 63) / 64), mt), dim3(256), 0, s, w, g);
+    return launch(k_gemm_hh<EPI, 2, 2, 64>, dim3(unsigned((g.n + 63) / 64), mt), dim3(256), 0, s, w, g);
 }
 
 hipError_t launch_gemm_hh(int epi, const _Float16 *w, const GemmArgs &g, hipStream_t s) {

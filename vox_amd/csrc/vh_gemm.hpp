@@ -19,6 +19,8 @@
 namespace vh {
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4v __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmBK = 32, kGemmLd = kGemmBK + 4;  // LDS row stride (bank spread)
 
@@ -87,6 +89,26 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
             const int col = n0 + wn * 16 * TN + j * 16 + (lane & 15);
             const float bz = (g.bias && col < g.n) ? g.bias[col] : 0.f;
             const float gt = (EPI == EPI_GATED_ACC && col < g.n) ? g.gate[col] : 0.f;
+            if (EPI == EPI_ROPE_H16 && n0 + wn * 16 * TN + j * 16 >= g.rope_cols && g.rope_cols % 16 == 0 && g.seq % 4 == 0) {
+                // a tile of v columns: this lane's 4 rows are 4 consecutive keys of one batch (seq % 4 == 0), so
+                // they go to v^T as one 8-byte store per plane instead of four strided 2-byte ones
+                const int row0 = m0 + wm * 16 * TM + i * 16 + 4 * (lane >> 4);
+                if (row0 < g.m && col < g.n) {
+                    const int cv = col - g.rope_cols, b = row0 / g.seq, n = row0 % g.seq;
+                    const int64_t idx = int64_t(g.m) * g.rope_cols +
+                                        ((int64_t(b) * (g.rope_cols / 2 / g.hd) + cv / g.hd) * g.hd + cv % g.hd) * g.ldvt + n;
+                    f16x4v hi, lo;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const float c = acc[i][j][v] + bz;
+                        hi[v] = _Float16(c);
+                        lo[v] = _Float16(c - float(hi[v]));
+                    }
+                    *reinterpret_cast<f16x4v *>(g.h16 + idx) = hi;
+                    *reinterpret_cast<f16x4v *>(g.h16 + g.lo_off + idx) = lo;
+                }
+                continue;
+            }
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int row = m0 + wm * 16 * TM + i * 16 + 4 * (lane >> 4) + v;
@@ -217,8 +239,6 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const uint8_t *__restrict__ w,
     gemm_epilogue<EPI, TM, TN>(acc, g, m0, n0, wm, wn, lane);
 }
 
-typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4v __attribute__((ext_vector_type(4)));
 
 // F16 or Q8 weights on the f16 matrix cores with the f32 activations split in two halves: a = hi + lo with
 // hi = f16(a), lo = f16(a - hi), so W a = W hi + W lo. F16 weights and the int8 values of Q8 weights are exact in
@@ -365,62 +385,64 @@ __global__ __launch_bounds__(256) void k_gemm_h16(const uint8_t *__restrict__ w,
 }
 
 // The split-f16 GEMM of k_gemm_h16 for F16 weights when the producer has already split A: hi plane g.a16, lo
-// plane g.a16 + g.a_lo (rows of g.lda halves), K a multiple of 64. Block tile 64 rows of A x 32 TN rows of W (4
-// waves of 32 x 16 TN), K steps of 64 through LDS as 16-byte copies, no conversion. The loads go through buffer
+// plane g.a16 + g.a_lo (rows of g.lda halves), K a multiple of BK. Block tile 32 TM rows of A x 32 TN rows of W (4
+// waves of 16 TM x 16 TN), K steps of BK through LDS as 16-byte copies, no conversion. The loads go through buffer
 // resources cut at the block's last row of A and of W, so rows past m or n read as zeros without a per-load bounds
-// check, and the K offset of a step is the scalar offset. Per K step a wave issues 4 + TN buffer loads, as many LDS
-// stores, 8 + 4 TN LDS fragment reads and 16 TN MFMAs: the wider W tile (TN 4) reads fewer LDS bytes per MFMA,
-// since every A fragment comes twice (hi, lo). Two K steps are in flight (two register sets alternate), so a load
-// has two steps' MFMAs to arrive.
-template <int EPI, int TN>
+// check, and the K offset of a step is the scalar offset. Every A fragment is read twice (hi, lo) per W fragment
+// pass. Two K steps are in flight (two register sets alternate), so a load has two steps' MFMAs to arrive.
+template <int EPI, int TM, int TN, int BK>
 __global__ __launch_bounds__(256) void k_gemm_hh(const _Float16 *__restrict__ w, GemmArgs g) {
-    constexpr int BK = 64, LD = BK + 8, BN = 32 * TN;
-    __shared__ __align__(16) _Float16 Ah[64][LD], Al[64][LD], Bs[BN][LD];
+    constexpr int LD = BK + 8, BM = 32 * TM, BN = 32 * TN, CPR = BK / 8, RS = 256 / CPR, AQ = BM / RS, WQ = BN / RS;
+    static_assert(AQ >= 1 && WQ >= 1 && BM % RS == 0 && BN % RS == 0, "tile rows per load pass");
+    __shared__ __align__(16) _Float16 Ah[BM][LD], Al[BM][LD], Bs[BN][LD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
     // row-major tiles, a band of rows of A per XCD (its rows of A and all of W stay in that XCD's L2)
     const int nt = gridDim.x, t = xcd_tile(blockIdx.y * nt + blockIdx.x, nt * gridDim.y);
-    const int m0 = (t / nt) * 64, n0 = (t % nt) * BN, K = g.K;
-    const int mr = min(64, g.m - m0), nr = min(BN, g.n - n0);
+    const int m0 = (t / nt) * BM, n0 = (t % nt) * BN, K = g.K;
+    const int mr = min(BM, g.m - m0), nr = min(BN, g.n - n0);
     const _Float16 *a0 = g.a16 + int64_t(m0) * g.lda;
     const __amdgpu_buffer_rsrc_t rah = buf_rsrc(a0, int32_t(mr * g.lda * 2));
     const __amdgpu_buffer_rsrc_t ral = buf_rsrc(a0 + g.a_lo, int32_t(mr * g.lda * 2));
     const __amdgpu_buffer_rsrc_t rw = buf_rsrc(w + int64_t(n0) * K, nr * K * 2);
-    // this thread's 8-half chunks of a tile: rows r + 32 q, columns c8 .. c8 + 7
-    const int r = tid >> 3, c8 = (tid & 7) * 8;
-    const int va0 = int32_t((r * g.lda + c8) * 2), va1 = int32_t(((r + 32) * g.lda + c8) * 2);
-    int vw[TN];
+    // this thread's 8-half chunks of a tile: rows r + RS q, columns c8 .. c8 + 7
+    const int r = tid / CPR, c8 = (tid % CPR) * 8;
+    int va[AQ], vw[WQ];
 #pragma unroll
-    for (int q = 0; q < TN; ++q) vw[q] = ((r + 32 * q) * K + c8) * 2;
-    f32x4v acc[2][TN];
+    for (int q = 0; q < AQ; ++q) va[q] = int32_t(((r + RS * q) * g.lda + c8) * 2);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int q = 0; q < WQ; ++q) vw[q] = ((r + RS * q) * K + c8) * 2;
+    f32x4v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
-    u32x4 xa0[4], xw0[TN], xa1[4], xw1[TN];
-    auto fetch = [&](u32x4(&a)[4], u32x4(&b)[TN], int k0) {
+    u32x4 xa0[2 * AQ], xw0[WQ], xa1[2 * AQ], xw1[WQ];
+    auto fetch = [&](u32x4(&a)[2 * AQ], u32x4(&b)[WQ], int k0) {
         const int so = k0 * 2;
-        a[0] = buf_ld16(rah, va0, so);
-        a[1] = buf_ld16(rah, va1, so);
-        a[2] = buf_ld16(ral, va0, so);
-        a[3] = buf_ld16(ral, va1, so);
 #pragma unroll
-        for (int q = 0; q < TN; ++q) b[q] = buf_ld16(rw, vw[q], so);
+        for (int q = 0; q < AQ; ++q) {
+            a[q] = buf_ld16(rah, va[q], so);
+            a[AQ + q] = buf_ld16(ral, va[q], so);
+        }
+#pragma unroll
+        for (int q = 0; q < WQ; ++q) b[q] = buf_ld16(rw, vw[q], so);
     };
-    auto stage = [&](const u32x4(&a)[4], const u32x4(&b)[TN]) {
-        *reinterpret_cast<u32x4 *>(&Ah[r][c8]) = a[0];
-        *reinterpret_cast<u32x4 *>(&Ah[r + 32][c8]) = a[1];
-        *reinterpret_cast<u32x4 *>(&Al[r][c8]) = a[2];
-        *reinterpret_cast<u32x4 *>(&Al[r + 32][c8]) = a[3];
+    auto stage = [&](const u32x4(&a)[2 * AQ], const u32x4(&b)[WQ]) {
 #pragma unroll
-        for (int q = 0; q < TN; ++q) *reinterpret_cast<u32x4 *>(&Bs[r + 32 * q][c8]) = b[q];
+        for (int q = 0; q < AQ; ++q) {
+            *reinterpret_cast<u32x4 *>(&Ah[r + RS * q][c8]) = a[q];
+            *reinterpret_cast<u32x4 *>(&Al[r + RS * q][c8]) = a[AQ + q];
+        }
+#pragma unroll
+        for (int q = 0; q < WQ; ++q) *reinterpret_cast<u32x4 *>(&Bs[r + RS * q][c8]) = b[q];
     };
     auto mma = [&]() {
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 32) {
-            f16x8v ah[2], al[2], b[TN];
+            f16x8v ah[TM], al[TM], b[TN];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int rr = wm * 32 + i * 16 + (lane & 15);
+            for (int i = 0; i < TM; ++i) {
+                const int rr = wm * 16 * TM + i * 16 + (lane & 15);
                 ah[i] = *reinterpret_cast<const f16x8v *>(&Ah[rr][kk + 8 * (lane >> 4)]);
                 al[i] = *reinterpret_cast<const f16x8v *>(&Al[rr][kk + 8 * (lane >> 4)]);
             }
@@ -428,7 +450,7 @@ __global__ __launch_bounds__(256) void k_gemm_hh(const _Float16 *__restrict__ w,
             for (int j = 0; j < TN; ++j)
                 b[j] = *reinterpret_cast<const f16x8v *>(&Bs[wn * 16 * TN + j * 16 + (lane & 15)][kk + 8 * (lane >> 4)]);
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
@@ -459,7 +481,7 @@ __global__ __launch_bounds__(256) void k_gemm_hh(const _Float16 *__restrict__ w,
         __syncthreads();
         mma();
     }
-    gemm_epilogue<EPI, 2, TN>(acc, g, m0, n0, wm, wn, lane);
+    gemm_epilogue<EPI, TM, TN>(acc, g, m0, n0, wm, wn, lane);
 }
 
 // The split-K partial slices ws[z][m][n], added in z order, then bias and the epilogue (STORE, ACC, GATED_ACC,
