@@ -7,8 +7,8 @@ namespace vh {
 hipError_t launch_f5_modulate(const float *x, int64_t R, int D, const float *sc, const float *sh, float *y, _Float16 *y16,
                               int64_t lo_off, hipStream_t s) {
     if (R <= 0) return hipSuccess;
-    if (D <= 0 || R > INT32_MAX || (!y && !y16)) return hipErrorInvalidValue;
-    return launch(k_f5_modulate, dim3(unsigned(R)), dim3(256), 0, s, x, int32_t(D), sc, sh, y, y16, lo_off);
+    if (D <= 0 || D % 4 || R > INT32_MAX || (!y && !y16) || lo_off % 4) return hipErrorInvalidValue;
+    return launch(k_f5_modulate, dim3(unsigned((R + 3) / 4)), dim3(256), 0, s, x, int32_t(D), sc, sh, y, y16, lo_off, int32_t(R));
 }
 
 hipError_t launch_f5_fill_x(const float *x, int N, int mel, float *cat, int W, int B, hipStream_t s) {

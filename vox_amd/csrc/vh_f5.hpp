@@ -7,46 +7,60 @@
 namespace vh {
 
 typedef float f32x4a __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4a __attribute__((ext_vector_type(4)));
 
-// LayerNorm without parameters + modulation (f5.cpp:608-625) of one row per block (256 threads): mean and
-// variance in double, inv = float(1 / sqrt(var + 1e-6)), y = (x - float(mean)) * inv * (1 + scale) + shift.
-// With y16 set, y goes out as f16 halves instead (hi at y16, lo at y16 + lo_off) for a split-f16 GEMM.
+// LayerNorm without parameters + modulation (f5.cpp:608-625), one wave per row (4 rows per 256-thread block):
+// mean and variance in double (two passes over the row, which stays in L1), inv = float(1 / sqrt(var + 1e-6)),
+// y = (x - float(mean)) * inv * (1 + scale) + shift. With y16 set, y goes out as f16 halves instead (hi at y16, lo
+// at y16 + lo_off) for a split-f16 GEMM. D % 4 == 0.
 __global__ __launch_bounds__(256) void k_f5_modulate(const float *__restrict__ x, int32_t D, const float *__restrict__ sc,
                                                      const float *__restrict__ sh, float *__restrict__ y,
-                                                     _Float16 *__restrict__ y16, int64_t lo_off) {
-    __shared__ double red[4];
-    const float *xr = x + int64_t(blockIdx.x) * D;
-    float *yr = y + int64_t(blockIdx.x) * D;
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    auto bsum = [&](double v) {
+                                                     _Float16 *__restrict__ y16, int64_t lo_off, int32_t R) {
+    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= R) return;
+    const float *xr = x + int64_t(row) * D;
+    auto wsum = [&](double v) {
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-        __syncthreads();
-        if (lane == 0) red[w] = v;
-        __syncthreads();
-        return (red[0] + red[1]) + (red[2] + red[3]);
+        return v;
     };
     double s = 0.0;
-    for (int i = t; i < D; i += 256) s += double(xr[i]);
-    const double mean = bsum(s) / D;
-    double v = 0.0;
-    for (int i = t; i < D; i += 256) {
-        const double dd = double(xr[i]) - mean;
-        v += dd * dd;
+    for (int i = 4 * lane; i < D; i += 256) {
+        const f32x4a v = *reinterpret_cast<const f32x4a *>(xr + i);
+        s += double(v[0]) + double(v[1]) + double(v[2]) + double(v[3]);
     }
-    const double var = bsum(v) / D;
-    const float inv = float(1.0 / sqrt(var + 1e-6)), fm = float(mean);
-    if (y16) {
-        _Float16 *hr = y16 + int64_t(blockIdx.x) * D;
-        for (int i = t; i < D; i += 256) {
-            const float r = (xr[i] - fm) * inv * (1.0f + sc[i]) + sh[i];
-            const _Float16 hi = _Float16(r);
-            hr[i] = hi;
-            hr[lo_off + i] = _Float16(r - float(hi));
+    const double mean = wsum(s) / D;
+    double q = 0.0;
+    for (int i = 4 * lane; i < D; i += 256) {
+        const f32x4a v = *reinterpret_cast<const f32x4a *>(xr + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const double dd = double(v[e]) - mean;
+            q += dd * dd;
         }
-        return;
     }
-    for (int i = t; i < D; i += 256) yr[i] = (xr[i] - fm) * inv * (1.0f + sc[i]) + sh[i];
+    const double var = wsum(q) / D;
+    const float inv = float(1.0 / sqrt(var + 1e-6)), fm = float(mean);
+    for (int i = 4 * lane; i < D; i += 256) {
+        const f32x4a v = *reinterpret_cast<const f32x4a *>(xr + i);
+        const f32x4a c = *reinterpret_cast<const f32x4a *>(sc + i), t = *reinterpret_cast<const f32x4a *>(sh + i);
+        f32x4a r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = (v[e] - fm) * inv * (1.0f + c[e]) + t[e];
+        if (y16) {
+            f16x4a hi, lo;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                hi[e] = _Float16(r[e]);
+                lo[e] = _Float16(r[e] - float(hi[e]));
+            }
+            _Float16 *hr = y16 + int64_t(row) * D + i;
+            *reinterpret_cast<f16x4a *>(hr) = hi;
+            *reinterpret_cast<f16x4a *>(hr + lo_off) = lo;
+        } else {
+            *reinterpret_cast<f32x4a *>(y + int64_t(row) * D + i) = r;
+        }
+    }
 }
 
 // cat[b][t][0..mel) = x[t][0..mel) for every batch b (the x columns of the DiT input, gpu.hpp:85-88).
