@@ -1,9 +1,11 @@
 """F5-TTS DiT step on the device (gpu_f5_create / begin / step / end, f5.cpp:586-725) against the oracle's vo_f5_step.
 
-Both sides consume the same stored f16 / bf16 / f32 weights and f32 position convolutions; the device runs the
-linears and the convolutions on the f32 MFMA GEMM and attention on f32 MFMA tiles with an online softmax, so the
-outputs differ only by summation order and libm ulps: the north star's 1e-3 for f32 activations with the `vox verify`
-metric.
+Both sides consume the same stored f16 / bf16 / f32 weights and f32 position convolutions. The device runs f16
+linears on the split-f16 matrix cores (activations as f16 hi + lo halves, products exact in the f32 accumulator;
+the models here with all widths multiples of 64 take the pre-split path, the others the f32-row path), bf16 / f32
+linears and the convolutions on f32 MFMA, and attention on split-f16 MFMA tiles with an online softmax, so the
+outputs differ only by summation order, the dropped lo x lo terms (below 2^-22) and libm ulps: the north star's
+1e-3 for f32 activations with the `vox verify` metric.
 """
 import numpy as np
 import pytest
@@ -34,6 +36,12 @@ def run(hip, oracle, m, B, N, seed, steps=1):
 def test_f5_step_small(hip, oracle, wtype, pe, B, N):
     m = F5Model(40 + wtype + pe, 128, 2, 4, mel=20, text=32, K=7, groups=4, pe_attn_head=pe, wtype=wtype)
     run(hip, oracle, m, B, N, seed=N, steps=2)
+
+
+def test_f5_step_f16_row_path(hip, oracle):
+    # dim 96 is not a multiple of 64: f16 linears take the f32-row GEMM (k_gemm_h16) with the same epilogues
+    m = F5Model(47, 96, 2, 2, mel=20, text=32, K=7, groups=4, wtype=F16)
+    run(hip, oracle, m, 2, 68, seed=5, steps=2)
 
 
 def test_f5_step_full_width(hip, oracle):
