@@ -241,6 +241,51 @@ VH_DEV void quant_slot(const float (&v)[8], uint32_t *q2, float *sc_out) {
     q2[1] = w[1];
 }
 
+// Sum of the 32 quantized inputs of a block held by 4 consecutive lanes (all 4 active), each lane's 8 in q2.
+VH_DEV int block_qsum(const uint32_t (&q2)[2]) {
+    int bs = __builtin_amdgcn_sdot4(int(q2[0]), 0x01010101, 0, false);
+    bs = __builtin_amdgcn_sdot4(int(q2[1]), 0x01010101, bs, false);
+    bs += dpp<kDppXor1>(bs);
+    return bs + dpp<kDppXor2>(bs);
+}
+
+// The int path's prologue for a pass of several input rows, run once (one block per row) instead of in every block
+// of the GEMV: row blockIdx.x of x as given, of RMSNorm(x), or of the attention merge, quantized per 32-block by
+// quant_slot exactly as the fused prologue does, into q [m][K], qs [m][K/32] and qsum [m][K/32] (the GEMV then
+// takes PRO_Q). xnorm, when set, receives the f32 rows as the fused prologue writes them.
+template <int PRO>
+__global__ __launch_bounds__(kGemvThreads) void k_quant_rows(GemvArgs a, int8_t *__restrict__ q, float *__restrict__ qs,
+                                                          int32_t *__restrict__ qsum) {
+    __shared__ float red[4];
+    const int mm = blockIdx.x, K = a.K, nb = K / 32;
+    GemvArgs b = a;  // row mm as a one-row prologue
+    b.m = 1;
+    b.xnorm = nullptr;
+    const float *x = a.x ? a.x + int64_t(mm) * a.ldx : nullptr;
+    if (PRO == PRO_ATTN) {
+        const int64_t hs = int64_t(mm) * a.attn.heads * kAttnMaxSplits;
+        b.attn.pm += hs;
+        b.attn.pl += hs;
+        b.attn.po += hs * a.attn.hd;
+    }
+    float *xn = (PRO != PRO_X && a.xnorm) ? a.xnorm + int64_t(mm) * K : nullptr;
+    ProStage<1, PRO> st;
+    prologue<1, PRO, false>(b, x, K, red, st, [&](int, int sl, const float (&v)[8]) {
+        if (xn)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xn[sl * 8 + j] = v[j];
+        uint32_t q2[2];
+        float sc;
+        quant_slot(v, q2, &sc);
+        *reinterpret_cast<uint2 *>(q + int64_t(mm) * K + sl * 8) = make_uint2(q2[0], q2[1]);
+        const int bs = block_qsum(q2);
+        if ((sl & 3) == 0) {
+            qs[mm * nb + (sl >> 2)] = sc;
+            qsum[mm * nb + (sl >> 2)] = bs;
+        }
+    });
+}
+
 // Epilogue: lane r*M + mm holds the total of (row0 + r, input row mm). SwiGLU pairs rows (2u, 2u+1) =
 // (gate u, up u); the partner value is fetched with all lanes active, then only valid lanes store.
 template <int M, int R, int EPI>
@@ -280,6 +325,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__rest
     int8_t *xq = reinterpret_cast<int8_t *>(smem);                 // [M][K]
     float *xs = reinterpret_cast<float *>(smem + M * K);           // [M][nb]
     float *red = xs + M * nb;                                      // [M][4]
+    int *xsum = reinterpret_cast<int *>(red + M * 4);              // Q4: [M][nb] sums of the quantized blocks
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * (kGemvThreads / 64) + wave) * R;
     constexpr int EPC = WT == WT_Q8 ? 16 : 32;  // weight elements per 16-byte chunk
@@ -306,18 +352,34 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__rest
             }
         }
     };
-    ProStage<M, PRO> st;
-    if constexpr (STAGE) pro_stage<M, PRO>(a, x, K, st);  // the prologue's inputs first: loads return in issue order
-    __builtin_amdgcn_sched_barrier(0);                    // keep the weight stream behind them
+    constexpr int PS = PRO == PRO_Q ? PRO_X : PRO;  // PRO_Q stages nothing
+    ProStage<M, PS> st;
+    if constexpr (STAGE && PRO != PRO_Q) pro_stage<M, PS>(a, x, K, st);  // the prologue's inputs first: loads return in issue order
+    __builtin_amdgcn_sched_barrier(0);                                  // keep the weight stream behind them
     load(0);
 
-    prologue<M, PRO, STAGE>(a, x, K, red, st, [&](int mm, int sl, const float (&v)[8]) {
-        uint32_t q2[2];
-        float sc;
-        quant_slot(v, q2, &sc);
-        *reinterpret_cast<uint2 *>(xq + mm * K + sl * 8) = make_uint2(q2[0], q2[1]);
-        if ((sl & 3) == 0) xs[mm * nb + (sl >> 2)] = sc;
-    });
+    if constexpr (PRO == PRO_Q) {  // the rows come quantized: copy them (rows past a.m as zeros)
+        const int n16 = M * K / 16;
+        for (int i = threadIdx.x; i < n16; i += kGemvThreads)
+            reinterpret_cast<u32x4 *>(xq)[i] = i * 16 / K < a.m ? reinterpret_cast<const u32x4 *>(a.q)[i] : u32x4{0u, 0u, 0u, 0u};
+        for (int i = threadIdx.x; i < M * nb; i += kGemvThreads) {
+            const bool on = i / nb < a.m;
+            xs[i] = on ? a.qs[i] : 0.f;
+            if (WT != WT_Q8) xsum[i] = on ? a.qsum[i] : 0;
+        }
+    } else {
+        prologue<M, PRO, STAGE>(a, x, K, red, st, [&](int mm, int sl, const float (&v)[8]) {
+            uint32_t q2[2];
+            float sc;
+            quant_slot(v, q2, &sc);
+            *reinterpret_cast<uint2 *>(xq + mm * K + sl * 8) = make_uint2(q2[0], q2[1]);
+            if ((sl & 3) == 0) xs[mm * nb + (sl >> 2)] = sc;
+            if (WT != WT_Q8) {  // the block's sum of quantized inputs, for the (u - 8) offset of the Q4 weights
+                const int bs = block_qsum(q2);
+                if ((sl & 3) == 0) xsum[mm * nb + (sl >> 2)] = bs;
+            }
+        });
+    }
     __syncthreads();
 
     float acc[R][M];
@@ -351,14 +413,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__rest
                     const u32x4 xl = *reinterpret_cast<const u32x4 *>(xq + mm * K + cc * 32);
                     const u32x4 xh = *reinterpret_cast<const u32x4 *>(xq + mm * K + cc * 32 + 16);
                     const float xsv = xs[mm * nb + cc];
-                    int sx = __builtin_amdgcn_sdot4(0x01010101, int(xl.x), 0, false);
-                    sx = __builtin_amdgcn_sdot4(0x01010101, int(xl.y), sx, false);
-                    sx = __builtin_amdgcn_sdot4(0x01010101, int(xl.z), sx, false);
-                    sx = __builtin_amdgcn_sdot4(0x01010101, int(xl.w), sx, false);
-                    sx = __builtin_amdgcn_sdot4(0x01010101, int(xh.x), sx, false);
-                    sx = __builtin_amdgcn_sdot4(0x01010101, int(xh.y), sx, false);
-                    sx = __builtin_amdgcn_sdot4(0x01010101, int(xh.z), sx, false);
-                    sx = __builtin_amdgcn_sdot4(0x01010101, int(xh.w), sx, false);
+                    const int sx = xsum[mm * nb + cc];  // sum of the block's 32 quantized inputs
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
                         const u32x4 w = wv[j][r];

@@ -12,7 +12,8 @@ hipError_t gemv_run_staged(const GemvArgs &a, hipStream_t s) {
     const int per_block = (kGemvThreads / 64) * R;
     const dim3 grid((a.rows + per_block - 1) / per_block), block(kGemvThreads);
     if constexpr (INT) {
-        const size_t smem = size_t(M) * a.K + size_t(M) * (a.K / 32) * 4 + size_t(M) * 16;
+        // xq [M][K] int8, xs [M][K/32] f32, red [M][4], xsum [M][K/32] int32 (Q4)
+        const size_t smem = size_t(M) * a.K + size_t(M) * (a.K / 32) * 4 + size_t(M) * 16 + (WT == WT_Q8 ? 0 : size_t(M) * (a.K / 32) * 4);
         hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_gemv_int<WT, M, R, IT, PRO, EPI, STAGE>), smem);
         if (e != hipSuccess) return e;
         return launch(k_gemv_int<WT, M, R, IT, PRO, EPI, STAGE>, grid, block, smem, s, a.w, a.scale, a.x, a.rows, a.K, a);
@@ -27,7 +28,8 @@ hipError_t gemv_run_staged(const GemvArgs &a, hipStream_t s) {
 // Staged prologue (inputs loaded ahead of the weight stream) when they fit the staging registers.
 template <int WT, int M, int R, int IT, int PRO, int EPI, bool INT>
 hipError_t gemv_run(const GemvArgs &a, hipStream_t s) {
-    if (pro_stageable<M, PRO>(a.K)) return gemv_run_staged<WT, M, R, IT, PRO, EPI, INT, true>(a, s);
+    if constexpr (PRO != PRO_Q)
+        if (pro_stageable<M, PRO>(a.K)) return gemv_run_staged<WT, M, R, IT, PRO, EPI, INT, true>(a, s);
     return gemv_run_staged<WT, M, R, IT, PRO, EPI, INT, false>(a, s);
 }
 
@@ -36,7 +38,13 @@ template <int WT, int M, int PRO, int EPI, bool INT>
 hipError_t gemv_by_tile(int R, int IT, const GemvArgs &a, hipStream_t s) {
 #define VH_TILE(r, it) \
     if (R == r && IT == it) return gemv_run<WT, M, r, it, PRO, EPI, INT>(a, s);
-    if constexpr (M == 1) {
+    if constexpr (PRO == PRO_Q) {  // pre-quantized rows: larger tiles, fewer copies of the rows per launch
+        if constexpr (EPI == EPI_SWIGLU) {
+            VH_TILE(2, 1) VH_TILE(4, 1) VH_TILE(8, 1)
+        } else {
+            VH_TILE(2, 1) VH_TILE(4, 1) VH_TILE(8, 1) VH_TILE(2, 2)
+        }
+    } else if constexpr (M == 1) {
         if constexpr (EPI == EPI_SWIGLU) {
             VH_TILE(2, 1) VH_TILE(4, 1) VH_TILE(6, 1) VH_TILE(8, 1) VH_TILE(2, 2) VH_TILE(2, 3)
         } else {
@@ -56,6 +64,12 @@ hipError_t gemv_by_tile(int R, int IT, const GemvArgs &a, hipStream_t s) {
 
 template <int WT, int PRO, int EPI, bool INT>
 hipError_t gemv_by_m(int M, int R, int IT, const GemvArgs &a, hipStream_t s) {
+    if constexpr (PRO == PRO_Q) {
+        if constexpr (!INT) return hipErrorInvalidValue;
+        else if (M == 4) return gemv_by_tile<WT, 4, PRO, EPI, INT>(R, IT, a, s);
+        else if (M == 8) return gemv_by_tile<WT, 8, PRO, EPI, INT>(R, IT, a, s);
+        else return hipErrorInvalidValue;
+    }
     switch (M) {
         case 1: return gemv_by_tile<WT, 1, PRO, EPI, INT>(R, IT, a, s);
         case 2: if constexpr (INT) return gemv_by_tile<WT, 2, PRO, EPI, INT>(R, IT, a, s); else return hipErrorInvalidValue;
@@ -74,6 +88,11 @@ hipError_t gemv_dispatch(int pro, int epi, int M, int R, int IT, const GemvArgs 
     if (pro == PRO_RMS && epi == EPI_SWIGLU) return gemv_by_m<WT, PRO_RMS, EPI_SWIGLU, INT>(M, R, IT, a, s);
     if (pro == PRO_X && epi == EPI_ACC) return gemv_by_m<WT, PRO_X, EPI_ACC, INT>(M, R, IT, a, s);
     if (pro == PRO_X && epi == EPI_STORE) return gemv_by_m<WT, PRO_X, EPI_STORE, INT>(M, R, IT, a, s);
+    if constexpr (INT) {  // the same passes on rows quantized beforehand
+        if (pro == PRO_Q && epi == EPI_STORE) return gemv_by_m<WT, PRO_Q, EPI_STORE, INT>(M, R, IT, a, s);
+        if (pro == PRO_Q && epi == EPI_ACC) return gemv_by_m<WT, PRO_Q, EPI_ACC, INT>(M, R, IT, a, s);
+        if (pro == PRO_Q && epi == EPI_SWIGLU) return gemv_by_m<WT, PRO_Q, EPI_SWIGLU, INT>(M, R, IT, a, s);
+    }
     return hipErrorInvalidValue;
 }
 

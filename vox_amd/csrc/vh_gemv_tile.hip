@@ -2,6 +2,7 @@
 // translation unit that instantiates the weight family.
 #include <cstdlib>
 
+#include "vh_gemv.hpp"
 #include "vh_launch.hpp"
 
 namespace vh {
@@ -23,6 +24,15 @@ static int target_waves() {
         return v >= 64 ? v : 1024;
     }();
     return w;
+}
+
+// Pre-quantized rows (PRO_Q): each block copies the M quantized rows into LDS, so larger tiles (up to 8 rows per
+// wave) copy them fewer times, as long as the launch keeps one block per CU.
+static void gemv_tile_q(int rows, int nchunk, bool swiglu, int *R, int *IT) {
+    int r = 2;
+    while (r < 8 && int64_t(rows) / (4 * 2 * r) >= 256) r *= 2;
+    *R = r;
+    *IT = !swiglu && r == 2 && nchunk > 64 ? 2 : 1;
 }
 
 void gemv_tile(int rows, int nchunk, int M, bool swiglu, int *R, int *IT) {
@@ -60,7 +70,12 @@ hipError_t launch_gemv(int wt, bool int_path, int pro, int epi, const GemvArgs &
         M = a.m <= 1 ? 1 : a.m <= 4 ? 4 : 0;
     }
     if (!M) return hipErrorInvalidValue;
-    gemv_tile(a.rows, nchunk, M, epi == EPI_SWIGLU, &R, &IT);
+    if (pro == PRO_Q) {
+        if (!int_path || M < 4 || !a.q || !a.qs || !a.qsum) return hipErrorInvalidValue;
+        gemv_tile_q(a.rows, nchunk, epi == EPI_SWIGLU, &R, &IT);
+    } else {
+        gemv_tile(a.rows, nchunk, M, epi == EPI_SWIGLU, &R, &IT);
+    }
     if (int_path) {
         if (wt == WT_Q8) return launch_gemv_int_q8(pro, epi, M, R, IT, a, s);
         if (wt == WT_Q4) return launch_gemv_int_q4(pro, epi, M, R, IT, a, s);
@@ -72,6 +87,18 @@ hipError_t launch_gemv(int wt, bool int_path, int pro, int epi, const GemvArgs &
         case WT_F16: return launch_gemv_flt_f16(pro, epi, M, R, IT, a, s);
         case WT_BF16: return launch_gemv_flt_bf16(pro, epi, M, R, IT, a, s);
         case WT_Q8: return launch_gemv_flt_q8(pro, epi, M, R, IT, a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_quant_rows(int pro, const GemvArgs &a, int8_t *q, float *qs, int32_t *qsum, hipStream_t s) {
+    if (a.m <= 0) return hipSuccess;
+    if (a.K <= 0 || a.K % 32 || !q || !qs || !qsum) return hipErrorInvalidValue;
+    const dim3 grid(unsigned(a.m)), block(kGemvThreads);
+    switch (pro) {
+        case PRO_X: return launch(k_quant_rows<PRO_X>, grid, block, 0, s, a, q, qs, qsum);
+        case PRO_RMS: return launch(k_quant_rows<PRO_RMS>, grid, block, 0, s, a, q, qs, qsum);
+        case PRO_ATTN: return launch(k_quant_rows<PRO_ATTN>, grid, block, 0, s, a, q, qs, qsum);
         default: return hipErrorInvalidValue;
     }
 }

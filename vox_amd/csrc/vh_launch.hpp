@@ -24,6 +24,9 @@ hipError_t launch(K kernel, dim3 grid, dim3 block, size_t smem, hipStream_t s, A
 
 // GEMV launch: rows/K/m etc. in a; wt = weight type; int_path = int8 activations (Q8 m <= 8, Q4 always).
 // Picks the row block M and the tile (R rows per wave, IT 1 KiB chunks in flight per row) from the shape.
+// The int path's prologue of a pass of m rows, once per row, into q [m][K] int8, qs / qsum [m][K/32]; the GEMV
+// then runs with PRO_Q and a.q / a.qs / a.qsum set.
+hipError_t launch_quant_rows(int pro, const GemvArgs &a, int8_t *q, float *qs, int32_t *qsum, hipStream_t s);
 hipError_t launch_gemv(int wt, bool int_path, int pro, int epi, const GemvArgs &a, hipStream_t s);
 void gemv_tile(int rows, int nchunk, int M, bool swiglu, int *R, int *IT);
 

@@ -5,7 +5,8 @@
 namespace vh {
 
 // GEMV input prologues: x as is; RMSNorm(x, gamma); or the merge of split-K attention partials.
-enum { PRO_X = 0, PRO_RMS = 1, PRO_ATTN = 2 };
+// GEMV prologues; PRO_Q (int path only): the input rows arrive already quantized (k_quant_rows)
+enum { PRO_X = 0, PRO_RMS = 1, PRO_ATTN = 2, PRO_Q = 3 };
 enum { EPI_STORE = 0, EPI_ACC = 1, EPI_SWIGLU = 2 };
 // GEMM-only epilogues (F5 DiT): y += gate * c; y = gelu_tanh(c); y = mish(c); y += mish(c); RoPE on q|k columns
 enum { EPI_GATED_ACC = 3, EPI_GELU = 4, EPI_MISH = 5, EPI_MISH_ACC = 6, EPI_ROPE = 7, EPI_ROPE_H16 = 8, EPI_GELU_H16 = 9 };
@@ -51,6 +52,10 @@ struct GemvArgs {
     int64_t ldx, ldy;
     int32_t rows, K, m;
     float eps;
+    // PRO_Q: the rows quantized per 32-block, q [m][K] int8, qs [m][K/32] scales, qsum [m][K/32] block sums
+    const int8_t *q;
+    const float *qs;
+    const int32_t *qsum;
 };
 
 constexpr int kGemvThreads = 256;

@@ -45,6 +45,10 @@ struct Fail : std::runtime_error {
 constexpr int kMaxM = 8;          // rows per pass on the int8-activation path; sequences per decode step
 constexpr int kMaxPass = 512;     // rows per pass on the f32-activation path (MFMA GEMM above 4 rows)
 constexpr int64_t kGemmWsFloats = int64_t(8) << 20;  // split-K workspace: 32 MB
+// Passes of at least kQuantRowsMin rows on the int path quantize their input rows once (k_quant_rows) instead of in
+// every GEMV block; the buffer holds 8 rows of up to 32768 elements.
+constexpr int kQuantRowsMin = 5;
+constexpr int64_t kQuantRowsElems = int64_t(8) * 32768;
 constexpr int64_t kMaxCap = 65536;
 
 struct GpuMat {
@@ -143,6 +147,10 @@ struct Ctx {
     std::vector<struct F5 *> f5;
     // split-K partial sums of the MFMA GEMM (allocated at init, so captured graphs can use it)
     float *gemm_ws = nullptr;
+    // int-path input rows quantized once per pass (k_quant_rows), kQuantRowsElems elements (allocated at init)
+    int8_t *qrows = nullptr;
+    float *qrows_s = nullptr;
+    int32_t *qrows_sum = nullptr;
     // LM sampler staging: device config + state, and their pinned host copies (config, state, two state slots)
     LmCfgDev *lm_cfg_dev = nullptr;
     LmState *lm_state_dev = nullptr;
@@ -375,7 +383,16 @@ void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, in
     a.w = m.w; a.scale = m.s; a.bias = m.b; a.x = x; a.gamma = gamma; a.y = y; a.xnorm = xnorm;
     a.ldx = ldx; a.ldy = ldy; a.rows = int32_t(m.rows); a.K = int32_t(m.cols); a.m = mc; a.eps = eps;
     if (pro == PRO_ATTN) a.attn = *attn;
-    HIPCHECK(launch_gemv(gemv_type(m), int_path(m, m_total), pro, epi, a, s));
+    const bool ip = int_path(m, m_total);
+    if (ip && mc >= kQuantRowsMin && mc <= 8 && int64_t(mc) * m.cols <= kQuantRowsElems &&
+        (epi == EPI_STORE || epi == EPI_ACC || epi == EPI_SWIGLU)) {
+        // several rows: quantize them once, then every GEMV block copies them instead of recomputing them
+        HIPCHECK(launch_quant_rows(pro, a, g.qrows, g.qrows_s, g.qrows_sum, s));
+        a.q = g.qrows; a.qs = g.qrows_s; a.qsum = g.qrows_sum;
+        HIPCHECK(launch_gemv(gemv_type(m), true, PRO_Q, epi, a, s));
+        return;
+    }
+    HIPCHECK(launch_gemv(gemv_type(m), ip, pro, epi, a, s));
 }
 
 // ------------------------------------------------------------------ transformer
@@ -840,6 +857,9 @@ int voxhip_init(const char *device, char *err, size_t err_len) {
         HIPCHECK(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
         g.dev = idx;
         g.gemm_ws = dalloc_t<float>(size_t(kGemmWsFloats));
+        g.qrows = dalloc_t<int8_t>(size_t(kQuantRowsElems));
+        g.qrows_s = dalloc_t<float>(size_t(kQuantRowsElems / 32));
+        g.qrows_sum = dalloc_t<int32_t>(size_t(kQuantRowsElems / 32));
         g.name = std::string(p.name) + " (" + p.gcnArchName + ")";
         g.ok = true;
         return 1;
