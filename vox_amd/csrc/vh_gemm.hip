@@ -17,12 +17,18 @@ static hipError_t gemm_run(const uint8_t *w, const float *scale, const float *A,
 template <int WT, int EPI, int TM, int TN>
 static hipError_t gemm_run_h16(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s) {
     constexpr int BM = 32 * TM, BN = 32 * TN;
-    const dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM);
+    const dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM, g.kchunk ? (g.K + g.kchunk - 1) / g.kchunk : 1);
+    // K steps of 64 throughout (and A rows 16-byte aligned): the buffered pipeline
+    if (TM == 2 && TN == 2 && g.K % 64 == 0 && g.kchunk % 64 == 0 && g.lda % 4 == 0)
+        return launch(k_gemm_h16b<WT, EPI>, grid, dim3(256), 0, s, w, scale, A, g);
     return launch(k_gemm_h16<WT, EPI, TM, TN, 64>, grid, dim3(256), 0, s, w, scale, A, g);
 }
 
 // Split K for a grid of 64 x 64 tiles too small to fill the CUs with a long K (prefill down projections, small
-// matrices): up to 8 slices of K, each a multiple of 64 columns, summed in order by the reduce pass.
+// matrices): up to 8 slices of K, each a multiple of 64 columns, summed in order by the reduce pass. Slices are
+// added until the launch has about kSplitTargetBlocks blocks (two per CU: measured faster than one per CU on the
+// 512-row prefill shapes even with the larger reduce).
+constexpr int64_t kSplitTargetBlocks = 512;
 template <int WT, int EPI>
 static hipError_t gemm_splitk(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s, bool *done) {
     *done = false;
@@ -31,14 +37,13 @@ static hipError_t gemm_splitk(const uint8_t *w, const float *scale, const float 
     } else {
     const int64_t blocks = int64_t((g.n + 63) / 64) * ((g.m + 63) / 64);
     if (!g.ws || blocks >= 192 || g.K < 512) return hipSuccess;
-    int splits = int(std::min<int64_t>(8, (256 + blocks - 1) / blocks));
+    int splits = int(std::min<int64_t>(8, (kSplitTargetBlocks + blocks - 1) / blocks));
     const int kchunk = ((g.K + splits - 1) / splits + 63) / 64 * 64;
     splits = (g.K + kchunk - 1) / kchunk;
     if (splits < 2 || int64_t(splits) * g.m * g.n > g.ws_cap) return hipSuccess;
     GemmArgs gs = g;
     gs.kchunk = kchunk;
-    const dim3 grid((g.n + 63) / 64, (g.m + 63) / 64, splits);
-    hipError_t e = launch(k_gemm_h16<WT, EPI_STORE, 2, 2, 64>, grid, dim3(256), 0, s, w, scale, A, gs);
+    hipError_t e = gemm_run_h16<WT, EPI_STORE, 2, 2>(w, scale, A, gs, s);
     if (e != hipSuccess) return e;
     const int nout = EPI == EPI_SWIGLU ? g.n / 2 : g.n;
     const int64_t total = int64_t(g.m) * nout;

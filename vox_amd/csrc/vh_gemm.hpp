@@ -384,6 +384,161 @@ __global__ __launch_bounds__(256) void k_gemm_h16(const uint8_t *__restrict__ w,
     gemm_epilogue<EPI, TM, TN>(acc, g, m0, n0, wm, wn, lane);
 }
 
+// k_gemm_h16 for K (and the split-K chunk) a multiple of 64, with k_gemm_hh's load pipeline: buffer loads cut at
+// the tile's last row of A and of W (rows past m or n read as zeros, no per-load bounds check, the K offset in the
+// scalar operand), two K steps in flight in alternating register sets, unconditional fetches (steps past the end
+// re-read the last one) so the wait counts are exact. A arrives as f32 and is split into hi / lo at staging; Q8
+// weights are widened to f16 at staging and their block scales staged beside them. 64 x 64 tiles, K steps of 64,
+// S register sets in flight (2: three or four measured slower on the prefill shapes).
+template <int WT, int EPI, int S = 2>
+__global__ __launch_bounds__(256) void k_gemm_h16b(const uint8_t *__restrict__ w, const float *__restrict__ scale,
+                                                   const float *__restrict__ A, GemmArgs g) {
+    static_assert(WT == WT_F16 || WT == WT_Q8, "f16 or q8 weights");
+    constexpr int BK = 64, LD = BK + 8, WQ = WT == WT_F16 ? 2 : 1;
+    __shared__ __align__(16) _Float16 Ah[64][LD], Al[64][LD], Bs[64][LD];
+    __shared__ float Ss[WT == WT_Q8 ? 64 : 1][2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+    const int nt = gridDim.x, t = xcd_tile(blockIdx.y * nt + blockIdx.x, nt * gridDim.y);
+    const int m0 = (t / nt) * 64, n0 = (t % nt) * 64, K = g.K, nb = K / 32;
+    const int kbeg = g.kchunk ? int(blockIdx.z) * g.kchunk : 0, kend = g.kchunk ? min(K, kbeg + g.kchunk) : K;
+    const int mr = min(64, g.m - m0), nr = min(64, g.n - n0);
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(A + int64_t(m0) * g.lda, int32_t(mr * g.lda * 4));
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(w + int64_t(n0) * K * (WT == WT_F16 ? 2 : 1), nr * K * (WT == WT_F16 ? 2 : 1));
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(WT == WT_Q8 ? scale + int64_t(n0) * nb : scale, WT == WT_Q8 ? nr * nb * 4 : 0);
+    // A: rows ar + 16 q, columns ac .. ac + 3 (f32); W: F16 rows wr + 32 q, columns wc .. wc + 7; Q8 row wr, wc .. wc + 15
+    const int ar = tid >> 4, ac = (tid & 15) * 4;
+    const int wr = WT == WT_F16 ? tid >> 3 : tid >> 2, wc = WT == WT_F16 ? (tid & 7) * 8 : (tid & 3) * 16;
+    int va[4], vw[WQ];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) va[q] = int32_t(((ar + 16 * q) * g.lda + ac) * 4);
+#pragma unroll
+    for (int q = 0; q < WQ; ++q) vw[q] = WT == WT_F16 ? ((wr + 32 * q) * K + wc) * 2 : wr * K + wc;
+    const int vs = ((tid >> 1) * nb + (tid & 1)) * 4;  // Q8 scales: threads < 128 take row tid / 2, block tid % 2
+    f32x4v acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    u32x4 xa[S][4], xw[S][WQ];
+    float xs[S];
+    auto fetch = [&](u32x4(&a)[4], u32x4(&b)[WQ], float &sc, int k0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[q] = buf_ld16(ra, va[q], k0 * 4);
+#pragma unroll
+        for (int q = 0; q < WQ; ++q) b[q] = buf_ld16(rw, vw[q], WT == WT_F16 ? k0 * 2 : k0);
+        if (WT == WT_Q8) sc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, vs, k0 / 32 * 4, 0));
+    };
+    auto stage = [&](const u32x4(&a)[4], const u32x4(&b)[WQ], float sc) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const f32x4v x = __builtin_bit_cast(f32x4v, a[q]);
+            f16x4v hi, lo;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                hi[e] = _Float16(x[e]);
+                lo[e] = _Float16(x[e] - float(hi[e]));
+            }
+            *reinterpret_cast<f16x4v *>(&Ah[ar + 16 * q][ac]) = hi;
+            *reinterpret_cast<f16x4v *>(&Al[ar + 16 * q][ac]) = lo;
+        }
+        if (WT == WT_F16) {
+#pragma unroll
+            for (int q = 0; q < WQ; ++q) *reinterpret_cast<u32x4 *>(&Bs[wr + 32 * q][wc]) = b[q];
+        } else {
+            const uint32_t u[4] = {b[0].x, b[0].y, b[0].z, b[0].w};
+            f16x8v h0, h1;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                h0[e] = _Float16(int8_t(u[e >> 2] >> (8 * (e & 3))));
+                h1[e] = _Float16(int8_t(u[2 + (e >> 2)] >> (8 * (e & 3))));
+            }
+            *reinterpret_cast<f16x8v *>(&Bs[wr][wc]) = h0;
+            *reinterpret_cast<f16x8v *>(&Bs[wr][wc + 8]) = h1;
+            if (tid < 128) Ss[tid >> 1][tid & 1] = sc;
+        }
+    };
+    auto mma = [&]() {
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 32) {
+            f16x8v ah[2], al[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int rr = wm * 32 + i * 16 + (lane & 15);
+                ah[i] = *reinterpret_cast<const f16x8v *>(&Ah[rr][kk + 8 * (lane >> 4)]);
+                al[i] = *reinterpret_cast<const f16x8v *>(&Al[rr][kk + 8 * (lane >> 4)]);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const f16x8v *>(&Bs[wn * 32 + j * 16 + (lane & 15)][kk + 8 * (lane >> 4)]);
+            if (WT == WT_F16) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], acc[i][j], 0, 0, 0);
+                    }
+            } else {
+                float sc[2];  // the block scale of this lane's W row (its C column)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) sc[j] = Ss[wn * 32 + j * 16 + (lane & 15)][kk / 32];
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        f32x4v tt = {0.f, 0.f, 0.f, 0.f};
+                        tt = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], tt, 0, 0, 0);
+                        tt = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], tt, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[i][j][v] = fmaf(tt[v], sc[j], acc[i][j][v]);
+                    }
+            }
+        }
+    };
+    // S register sets, set i holding step s + i: one back edge, so set 0 is always the oldest in flight
+    const int ns = (kend - kbeg) / BK, klast = kend - BK;
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+        fetch(xa[i], xw[i], xs[i], min(kbeg + i * BK, klast));
+        __builtin_amdgcn_sched_barrier(0);  // keep each set's loads behind the previous set's
+    }
+    int s = 0;
+    for (; s + S <= ns; s += S) {
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            stage(xa[i], xw[i], xs[i]);
+            __syncthreads();
+            fetch(xa[i], xw[i], xs[i], min(kbeg + (s + i + S) * BK, klast));
+            mma();
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < S - 1; ++i) {  // the last ns % S steps, in sets 0 ..
+        if (s + i < ns) {
+            stage(xa[i], xw[i], xs[i]);
+            __syncthreads();
+            mma();
+            __syncthreads();
+        }
+    }
+    if (g.kchunk) {  // split K: this block's partial sums, no epilogue
+        float *ws = g.ws + int64_t(blockIdx.z) * g.m * g.n;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int col = n0 + wn * 32 + j * 16 + (lane & 15);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int row = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + v;
+                    if (row < g.m && col < g.n) ws[int64_t(row) * g.n + col] = acc[i][j][v];
+                }
+            }
+        return;
+    }
+    gemm_epilogue<EPI, 2, 2>(acc, g, m0, n0, wm, wn, lane);
+}
+
 // The split-f16 GEMM of k_gemm_h16 for F16 weights when the producer has already split A: hi plane g.a16, lo
 // plane g.a16 + g.a_lo (rows of g.lda halves), K a multiple of BK. Block tile 32 TM rows of A x 32 TN rows of W (4
 // waves of 16 TM x 16 TN), K steps of BK through LDS as 16-byte copies, no conversion. The loads go through buffer
