@@ -18,8 +18,9 @@ template <int WT, int EPI, int TM, int TN>
 static hipError_t gemm_run_h16(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s) {
     constexpr int BM = 32 * TM, BN = 32 * TN;
     const dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM, g.kchunk ? (g.K + g.kchunk - 1) / g.kchunk : 1);
-    // K steps of 64 throughout (and A rows 16-byte aligned): the buffered pipeline
-    if (TM == 2 && TN == 2 && g.K % 64 == 0 && g.kchunk % 64 == 0 && g.lda % 4 == 0)
+    // K steps of 64 throughout, A rows 16-byte aligned, and a tile's byte offsets within 32 bits: the buffered pipeline
+    if (TM == 2 && TN == 2 && g.K % 64 == 0 && g.kchunk % 64 == 0 && g.lda % 4 == 0 && int64_t(64) * g.lda * 4 <= INT32_MAX &&
+        int64_t(64) * g.K * 2 <= INT32_MAX)
         return launch(k_gemm_h16b<WT, EPI>, grid, dim3(256), 0, s, w, scale, A, g);
     return launch(k_gemm_h16<WT, EPI, TM, TN, 64>, grid, dim3(256), 0, s, w, scale, A, g);
 }
