@@ -227,6 +227,42 @@ def bench_cfg5(vh, synth, reps=3):
             "total_ms": round(t_all, 3), "tokens": ntok}
 
 
+def bench_pred(vh, synth, frames=20):
+    """The code predictor's frame on the device (gpu_pred_frame; the loop engine.cpp:676-683 runs on the CPU in the
+    reference when the device does not provide it): 15 passes of the 5-layer q8 predictor (2 rows at positions 0-1,
+    then one row per codebook), each with its codebook's q8 head, the sampler (top-k 50, T 0.9, draw (frame, cb))
+    and the next code's bf16 embedding gathered on the device, in one graph. Host wall-clock per frame (median),
+    the [2][1024] input upload and the codes download included."""
+    c = synth.PRED_0_6B
+    dec = synth.Decoder(c, seed=0, capacity=32)
+    G, V, H = c["groups"], c["vocab"], c["hidden"]
+    heads = [vh.mat_synthetic(c["head_type"], V, H, 0, 0x5000 + i, 0.0, 0.02) for i in range(G - 1)]
+    embs = [vh.mat_synthetic(c["emb_type"], V, H, 0, 0x6000 + i, 0.0, 1.0) for i in range(G - 2)]
+    rng = np.random.default_rng(11)
+    times, codes = [], None
+    for f in range(frames + 3):
+        in2 = rng.standard_normal((2, H)).astype(np.float32)
+        cfg = vh.sample_cfg(0.9, 1.0, 50, seed=1, frame=f)
+        t0 = time.perf_counter()
+        codes = vh.pred_frame(dec.xfmr, dec.seq, in2, -1, heads, embs, cfg)
+        if f >= 3:
+            times.append((time.perf_counter() - t0) * 1000.0)
+    ms = float(np.median(times))
+    layer_bytes = dec.weight_bytes()  # the 5 layers (no head in this config)
+    head_bytes = V * H + V * (H // 32) * 4
+    kd = c["kv_heads"] * c["head_dim"]
+    kv = sum(c["layers"] * 2 * (p + 1) * kd * 2 for p in range(1, G))  # keys/values read per pass (f16)
+    frame_bytes = (G - 1) * (layer_bytes + head_bytes) + (G - 2) * H * 2 + kv
+    for h in heads + embs:
+        vh.mat_free(h)
+    assert codes is not None and codes.shape == (G,)
+    return {"workload": "qwen3-tts-0.6b code-predictor frame (gpu_pred_frame): 15 passes x 5 q8 layers + q8 head "
+                        "2048 + sampler, bf16 code embeddings",
+            "ms_per_frame": round(ms, 3), "bytes_per_frame": int(frame_bytes),
+            "GBps": round(frame_bytes / (ms * 1e-3) / 1e9, 1), "frac": round(frame_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "passes_per_s": round((G - 1) / (ms * 1e-3), 1)}
+
+
 def load_traffic(kernel_class):
     p = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(p):
@@ -244,9 +280,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-other", action="store_true", help="skip the configs[0] / [2] / [3] / [4] measurements")
-    ap.add_argument("--only", choices=["configs[0]", "configs[2]", "configs[3]", "configs[4]"],
-                    help="run one of the other BASELINE configurations alone and print its JSON object (for profiling)")
+    ap.add_argument("--no-other", action="store_true",
+                    help="skip the configs[0] / [2] / [3] / [4] and code-predictor measurements")
+    ap.add_argument("--only", choices=["configs[0]", "configs[2]", "configs[3]", "configs[4]", "pred_frame"],
+                    help="run one of the other BASELINE configurations (or the code-predictor frame) alone and print "
+                         "its JSON object (for profiling)")
     ap.add_argument("--no-breakdown", action="store_true",
                     help="skip the event-timed per-kernel pass (for runs under rocprofv3, whose tracer does not survive "
                          "HIP events recorded around graph launches); rocprof then times the graph's kernels itself")
@@ -262,7 +300,8 @@ def main():
     log("device:", vh.device_name())
     if args.only:
         legs = {"configs[0]": lambda: bench_cfg1(vh), "configs[2]": lambda: bench_cfg3(vh, synth, 100, 10),
-                "configs[3]": lambda: bench_cfg4(vh, synth), "configs[4]": lambda: bench_cfg5(vh, synth)}
+                "configs[3]": lambda: bench_cfg4(vh, synth), "configs[4]": lambda: bench_cfg5(vh, synth),
+                "pred_frame": lambda: bench_pred(vh, synth)}
         print(json.dumps({args.only: legs[args.only]()}))
         return
     t0 = time.perf_counter()
@@ -327,7 +366,8 @@ def main():
     if not args.no_other:
         t0 = time.perf_counter()
         other = {"configs[0]": bench_cfg1(vh), "configs[2]": bench_cfg3(vh, synth, 100, 10),
-                 "configs[3]": bench_cfg4(vh, synth), "configs[4]": bench_cfg5(vh, synth)}
+                 "configs[3]": bench_cfg4(vh, synth), "configs[4]": bench_cfg5(vh, synth),
+                 "pred_frame": bench_pred(vh, synth)}
         log(f"other configs: {json.dumps(other)} ({time.perf_counter() - t0:.1f} s)")
 
     cpu = None

@@ -166,9 +166,17 @@ typedef struct voxhip_sample_cfg {
 int voxhip_sample_logits(const float *logits, int32_t n, const voxhip_sample_cfg *cfg, const int32_t *history,
                          int32_t n_history, int32_t *out_id);
 
-/* gpu_pred_frame (gpu.hpp:51-52), gpu_codec_* (gpu.hpp:55-61), gpu_f5_* (gpu.hpp:82-90),
- * gpu_cosy_* (gpu.hpp:114-119) are not provided yet: gpu_hip.cpp answers them like gpu_stub.cpp
- * (-1 / false), and the callers compute on the CPU. */
+/* gpu_pred_frame (gpu.hpp:51-52; gpu_vulkan.cpp:968-1045): the code predictor's whole frame on the device. With
+ * G = n_heads + 1 codebooks: pass 1 runs the 2 rows of in2 ([2][din]: the talker's hidden state and the first
+ * code's embedding) at positions 0 and 1 of seq, pass cb >= 2 one row at position cb, the embedding row
+ * embs[cb - 2][codes[cb - 1]]; each pass goes through in_proj (or none: din = hidden), the layers, the final norm
+ * and heads[cb - 1] on its last row, and sample_logits with cfg's temperature / top-k / top-p and the draw
+ * (cfg->frame, cb) into codes[cb]. codes[0] is not written. Returns 1, or 0 with the error set. */
+int voxhip_pred_frame(int xfmr, int seq, const float *in2, int in_proj, const int *heads, int n_heads, const int *embs,
+                      int n_embs, const voxhip_sample_cfg *cfg, int32_t *codes);
+
+/* gpu_codec_* (gpu.hpp:55-61), gpu_f5_vocos (gpu.hpp:88), gpu_cosy_* (gpu.hpp:114-119) are not provided yet:
+ * gpu_hip.cpp answers them like gpu_stub.cpp (-1 / false), and the callers compute on the CPU. */
 
 /* ---------------------------------------------------------------- device-resident path
  * Entry points for callers that keep activations in device memory (bench, tests, a device-side

@@ -6,8 +6,8 @@
 //
 // Error convention of the reference backend (gpu_vulkan.cpp:568-571, :800-803): no exception escapes, false/-1
 // means "compute on the CPU", the reason is kept for gpu_stats().last_error, and one warning goes to stderr.
-// Entry points not provided by this backend yet (the predictor frame loop, the codec, the Vocos vocoder, the
-// CosyVoice flow) answer like gpu_stub.cpp, so their callers stay on the CPU.
+// Entry points not provided by this backend yet (the codec, the Vocos vocoder, the CosyVoice flow) answer like
+// gpu_stub.cpp, so their callers stay on the CPU.
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -214,11 +214,31 @@ bool gpu_f5_step(int id, const float *x, const float *ts, float *out) {
 }
 void gpu_f5_end(int id) { (void)voxhip_f5_end(id); }
 
-// ---- not provided by this backend yet: the callers compute on the CPU (gpu_stub.cpp behaviour)
-bool gpu_pred_frame(const TransformerW &, int, const float *, const Mat *, const std::vector<Mat> &, const std::vector<Mat> &,
-                    const GpuSampleCfg &, int32_t *) {
+// The code predictor's frame loop (gpu_vulkan.cpp:968-1045): the same sampler settings for every codebook, the
+// draw (frame, cb) of each; matrices the backend does not hold keep the frame on the CPU.
+bool gpu_pred_frame(const TransformerW &w, int seq, const float *in2, const Mat *in_proj, const std::vector<Mat> &heads,
+                    const std::vector<Mat> &embs, const GpuSampleCfg &c, int32_t *codes) {
+    if (w.gpu_id < 0 || heads.empty() || (in_proj && in_proj->gpu < 0)) return false;
+    std::vector<int> hid, eid;
+    for (const Mat &h : heads) {
+        if (h.gpu < 0) return false;
+        hid.push_back(h.gpu);
+    }
+    for (const Mat &e : embs) {
+        if (e.gpu < 0) return false;
+        eid.push_back(e.gpu);
+    }
+    voxhip_sample_cfg sc{};
+    sc.temperature = c.temperature; sc.top_p = c.top_p; sc.top_k = c.top_k; sc.repetition_penalty = 1.0f;
+    sc.key0 = c.key0; sc.key1 = c.key1; sc.frame = c.frame; sc.eos_code = -1;
+    if (voxhip_pred_frame(w.gpu_id, seq, in2, in_proj ? in_proj->gpu : -1, hid.data(), int(hid.size()), eid.data(),
+                          int(eid.size()), &sc, codes))
+        return true;
+    std::fprintf(stderr, "vox: GPU predictor loop failed: %s\n", voxhip_last_error());
     return false;
 }
+
+// ---- not provided by this backend yet: the callers compute on the CPU (gpu_stub.cpp behaviour)
 int gpu_codec_create(const Qwen3Weights &) { return -1; }
 int gpu_codec_state_new(int) { return -1; }
 int gpu_codec_state_clone(int) { return -1; }

@@ -74,6 +74,8 @@ hipError_t launch_f5_attn(const _Float16 *qkv16, int64_t lo_off, float *out, _Fl
 hipError_t launch_lm_sample(const float *logits, int n, const LmCfgDev *cfg, LmState *st, int32_t *decoded, float *logp_out,
                             int64_t logp_stride, bool append, hipStream_t s);
 hipError_t launch_lm_embed(const LmEmbedArgs &a, hipStream_t s);
+// A pass of the code-predictor frame loop: row table + RoPE rows of the pass, the sampled code's embedding row.
+hipError_t launch_pred_embed(const PredEmbedArgs &a, hipStream_t s);
 
 // Shared-memory opt-in above 64 KiB, once per kernel.
 hipError_t ensure_smem(const void *kernel, size_t bytes);

@@ -11,6 +11,12 @@ hipError_t launch_lm_sample(const float *logits, int n, const LmCfgDev *cfg, LmS
                   logp_stride, int32_t(append));
 }
 
+hipError_t launch_pred_embed(const PredEmbedArgs &a, hipStream_t s) {
+    if (a.m <= 0 || a.hd <= 0 || (a.w && (a.cols <= 0 || !a.codes || !a.x || !a.err || (a.type == WT_Q8 || a.type == WT_Q4) && a.cols % 32)))
+        return hipErrorInvalidValue;
+    return launch(k_pred_embed, dim3(1), dim3(256), 0, s, a);
+}
+
 hipError_t launch_lm_embed(const LmEmbedArgs &a, hipStream_t s) {
     if (a.hd <= 0 || a.cols <= 0 || (a.type == WT_Q8 || a.type == WT_Q4) && a.cols % 32) return hipErrorInvalidValue;
     return launch(k_lm_embed, dim3(1), dim3(256), 0, s, a);

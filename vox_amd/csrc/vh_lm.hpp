@@ -250,6 +250,49 @@ __global__ __launch_bounds__(kLmThreads) void k_lm_sample(const float *__restric
 // decode row advanced to the next position: rows[0].pos + 1 with its RoPE row copied from the table. After the
 // end of the generation the row goes to spare_pos instead (a cache slot the generation never uses), so the rest
 // of the step writes nothing the generation keeps. Grid 1, block 256.
+// Row r of an embedding of any weight type, widened as mat_gather does (kernels.cpp:432-471), into x [cols];
+// the block's threads take the columns in turn.
+VH_DEV void gather_row(const uint8_t *w, const void *scale, int type, int s16, int64_t cols, int64_t r, float *x) {
+    const int64_t nb = cols / 32;
+    for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+        float v;
+        switch (type) {
+            case WT_F32: v = reinterpret_cast<const float *>(w)[r * cols + c]; break;
+            case WT_F16: v = float(reinterpret_cast<const _Float16 *>(w)[r * cols + c]); break;
+            case WT_BF16: v = bf16_to_f32(reinterpret_cast<const uint16_t *>(w)[r * cols + c]); break;
+            case WT_Q8: v = float(int8_t(w[r * cols + c])) * static_cast<const float *>(scale)[r * nb + c / 32]; break;
+            default: {  // Q4: 16 bytes per 32-block, byte j = w[j] | w[j + 16] << 4, value (u - 8) * scale
+                const int64_t b = c / 32, j = c % 32;
+                const uint8_t u = w[r * (cols / 2) + b * 16 + (j & 15)];
+                const int q = int(j < 16 ? (u & 15) : (u >> 4)) - 8;
+                const float sc = s16 ? float(static_cast<const _Float16 *>(scale)[r * nb + b]) : static_cast<const float *>(scale)[r * nb + b];
+                v = float(q) * sc;
+            }
+        }
+        x[c] = v;
+    }
+}
+
+// A pass of the code-predictor frame loop (gpu_vulkan.cpp:1004-1017): its rows at positions pos0 .. pos0 + m - 1
+// with their RoPE rows from the table, and, after the first pass, the embedding row of the code just sampled
+// (mat_gather of backend_qwen3.cpp:411). A code outside the embedding sets *err (check_id in the reference) and
+// leaves x as it was. Grid 1, block 256.
+__global__ __launch_bounds__(256) void k_pred_embed(PredEmbedArgs a) {
+    for (int i = threadIdx.x; i < a.m; i += 256) {
+        RowRef r = a.base;
+        r.pos = a.base.pos + i;
+        a.row[i] = r;
+    }
+    for (int j = threadIdx.x; j < a.m * a.hd; j += 256) a.rope_row[j] = a.rope[a.base.pos * a.hd + j];
+    if (!a.w) return;
+    const int64_t r = a.codes[a.code_idx];
+    if (r < 0 || r >= a.rows) {
+        if (threadIdx.x == 0) *a.err = 1;
+        return;
+    }
+    gather_row(a.w, a.scale, a.type, a.s16, a.cols, r, a.x);
+}
+
 __global__ __launch_bounds__(256) void k_lm_embed(LmEmbedArgs a) {
     const LmState s = *a.st;
     const int64_t pos0 = a.row->pos;
@@ -260,25 +303,7 @@ __global__ __launch_bounds__(256) void k_lm_embed(LmEmbedArgs a) {
     if (s.done) return;
     const int64_t r = a.decoded[s.n_dec - 1];
     if (r < 0 || r >= a.rows) return;
-    const int64_t nb = a.cols / 32;
-    for (int64_t c = threadIdx.x; c < a.cols; c += 256) {
-        float v;
-        switch (a.type) {
-            case WT_F32: v = reinterpret_cast<const float *>(a.w)[r * a.cols + c]; break;
-            case WT_F16: v = float(reinterpret_cast<const _Float16 *>(a.w)[r * a.cols + c]); break;
-            case WT_BF16: v = bf16_to_f32(reinterpret_cast<const uint16_t *>(a.w)[r * a.cols + c]); break;
-            case WT_Q8: v = float(int8_t(a.w[r * a.cols + c])) * static_cast<const float *>(a.scale)[r * nb + c / 32]; break;
-            default: {  // Q4: 16 bytes per 32-block, byte j = w[j] | w[j + 16] << 4, value (u - 8) * scale
-                const int64_t b = c / 32, j = c % 32;
-                const uint8_t u = a.w[r * (a.cols / 2) + b * 16 + (j & 15)];
-                const int q = int(j < 16 ? (u & 15) : (u >> 4)) - 8;
-                const float sc = a.s16 ? float(static_cast<const _Float16 *>(a.scale)[r * nb + b])
-                                       : static_cast<const float *>(a.scale)[r * nb + b];
-                v = float(q) * sc;
-            }
-        }
-        a.x[c] = v;
-    }
+    gather_row(a.w, a.scale, a.type, a.s16, a.cols, r, a.x);
 }
 
 }  // namespace vh

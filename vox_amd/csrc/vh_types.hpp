@@ -165,6 +165,24 @@ struct LmEmbedArgs {
     int32_t hd;
     int64_t spare_pos;
 };
+// One pass of the code-predictor frame loop (gpu_pred_frame): the pass's m rows of the sequence at positions
+// pos0 .. pos0 + m - 1 (row table + RoPE rows), and for a pass after the first the embedding row of the code the
+// previous pass sampled (codes[code_idx]) into x.
+struct PredEmbedArgs {
+    const uint8_t *w;      // embedding [rows][cols] (null: no gather)
+    const void *scale;     // f32 [rows][cols/32], or f16 bits when s16 (Q4)
+    int32_t type, s16;
+    int64_t rows, cols;
+    const int32_t *codes;
+    int32_t code_idx;
+    float *x;              // [cols]
+    RowRef *row;           // [m]
+    float *rope_row;       // [m][hd]
+    const float *rope;     // table [positions][hd]
+    int32_t hd, m;
+    RowRef base;           // cache view of the sequence; pos = pos0
+    int32_t *err;          // set to 1 when a code falls outside the embedding
+};
 constexpr int kF5HeadDim = 64;   // head_dim of the F5 attention kernel
 constexpr int kLmMaxK = 1024;  // top_k limit of the device RAS sampler (sorted in LDS above 64)
 constexpr int kLmMaxN = 8192;  // vocabulary limit of the device RAS sampler (8 entries per thread)

@@ -110,6 +110,11 @@ struct Xfmr {
     float *lm_logp = nullptr;
     int64_t lm_dec_cap = 0, lm_logp_cap = 0;
     std::map<std::array<int64_t, 4>, hipGraphExec_t> lm_graphs;
+    // code-predictor frame loop: sampled codes, per-codebook sampler configurations and the code-range flag on the
+    // device ([kPredMaxGroups] each; pinned copies for the host); one graph per (seq, in_proj, heads, embeddings)
+    int32_t *pred_codes = nullptr, *pred_err = nullptr, *pred_host = nullptr;
+    SampleCfgDev *pred_cfg = nullptr, *pred_cfg_host = nullptr;
+    std::map<std::vector<int>, hipGraphExec_t> pred_graphs;
 };
 
 struct Seq {
@@ -401,6 +406,8 @@ void drop_graphs(Xfmr &X) {
     X.graphs.clear();
     for (auto &kv : X.lm_graphs) (void)hipGraphExecDestroy(kv.second);
     X.lm_graphs.clear();
+    for (auto &kv : X.pred_graphs) (void)hipGraphExecDestroy(kv.second);
+    X.pred_graphs.clear();
 }
 
 void ensure_rope(Xfmr &X, int64_t rows) {
@@ -471,6 +478,7 @@ float *ensure_xin(Xfmr &X, int64_t elems) {
         dfree(X.xin);
         X.xin = dalloc_t<float>(size_t(elems));
         X.xin_elems = elems;
+        drop_graphs(X);  // a captured frame loop reads the old input buffer
     }
     return X.xin;
 }
@@ -1382,6 +1390,68 @@ hipGraphExec_t lm_graph(Xfmr &X, const Seq &S, int seq, int head, int emb, bool 
     X.lm_graphs[key] = exec;
     return exec;
 }
+
+// ------------------------------------------------------------------ code-predictor frame loop (gpu_pred_frame)
+constexpr int kPredMaxGroups = 64;  // the reference's bound (gpu_vulkan.cpp:977)
+
+void pred_buffers(Xfmr &X) {
+    if (X.pred_codes) return;
+    X.pred_codes = dalloc_t<int32_t>(kPredMaxGroups);
+    X.pred_err = dalloc_t<int32_t>(1);
+    X.pred_cfg = dalloc_t<SampleCfgDev>(kPredMaxGroups);
+    HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&X.pred_host), (kPredMaxGroups + 1) * sizeof(int32_t), hipHostMallocDefault));
+    HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&X.pred_cfg_host), kPredMaxGroups * sizeof(SampleCfgDev), hipHostMallocDefault));
+}
+
+// The whole frame (gpu_vulkan.cpp:1004-1036) as one graph. Pass cb (1 .. G-1) takes m rows (2 for the first: the
+// talker's hidden state and the first code's embedding, staged by the host; 1 after: the embedding of the code the
+// previous pass sampled, gathered on the device) at positions pos .. pos + m - 1 of the sequence, then in_proj (or
+// the rows as they are), the layers, the final norm and head cb - 1 on the last row, and the sampler with draw
+// (frame, cb) into codes[cb]. The first pass's two rows run the unfused layer path (q/k post-processing and the
+// K/V append before attention), so row 1 sees row 0.
+hipGraphExec_t pred_graph(Xfmr &X, const Seq &S, int seq, int in_proj, const int *heads, const int *embs, int G) {
+    std::vector<int> key{seq, in_proj, G};
+    key.insert(key.end(), heads, heads + (G - 1));
+    key.insert(key.end(), embs, embs + (G - 2));
+    auto it = X.pred_graphs.find(key);
+    if (it != X.pred_graphs.end()) return it->second;
+    const int64_t din = in_proj >= 0 ? mat_at(in_proj).cols : X.H;
+    hipGraph_t graph = nullptr;
+    HIPCHECK(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal));
+    try {
+        int64_t pos = 0;
+        for (int cb = 1; cb < G; ++cb) {
+            const int m = cb == 1 ? 2 : 1;
+            PredEmbedArgs pa{};
+            pa.codes = X.pred_codes; pa.code_idx = cb - 1; pa.err = X.pred_err;
+            pa.x = in_proj >= 0 ? X.xin : X.h;
+            pa.row = X.rows_dev; pa.rope_row = X.rope_rows_dev; pa.rope = X.rope; pa.hd = X.hd; pa.m = m;
+            pa.base = row_of(S, pos);
+            if (cb >= 2) {
+                const GpuMat &E = mat_at(embs[cb - 2]);
+                pa.w = E.w; pa.scale = E.s; pa.type = E.type; pa.s16 = E.s16 ? 1 : 0; pa.rows = E.rows; pa.cols = E.cols;
+            }
+            HIPCHECK(launch_pred_embed(pa, g.stream));
+            if (in_proj >= 0) gemv(mat_at(in_proj), m, PRO_X, EPI_STORE, X.xin, din, m, X.h, X.H, nullptr, 0.f, nullptr, g.stream);
+            enqueue_layers(X, m, m, 0, X.layers, g.stream, m == 1);
+            const GpuMat &Hm = mat_at(heads[cb - 1]);
+            enqueue_final(X, m - 1, 1, heads[cb - 1], g.stream);
+            HIPCHECK(launch_sample(X.pred_cfg + cb, X.logits, int(Hm.rows), X.pred_codes + cb, g.stream));
+            pos += m;
+        }
+    } catch (...) {
+        (void)hipStreamEndCapture(g.stream, &graph);
+        if (graph) (void)hipGraphDestroy(graph);
+        throw;
+    }
+    HIPCHECK(hipStreamEndCapture(g.stream, &graph));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    HIPCHECK(e);
+    X.pred_graphs[key] = exec;
+    return exec;
+}
 }  // namespace
 
 extern "C" {
@@ -1478,6 +1548,59 @@ int voxhip_lm_generate(int xfmr, int seq, const float *x, int64_t n, int head, i
             throw;
         }
         cleanup();
+        return 1;
+    }, 0);
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int voxhip_pred_frame(int xfmr, int seq, const float *in2, int in_proj, const int *heads, int n_heads, const int *embs,
+                      int n_embs, const voxhip_sample_cfg *cfg, int32_t *codes) {
+    return guard_int([&] {
+        require_ok();
+        Xfmr &X = xf_at(xfmr);
+        Seq &S = seq_at(seq);
+        check_seq_for(X, xfmr, S);
+        const int G = n_heads + 1;
+        if (!in2 || !heads || !cfg || !codes || n_heads < 1) throw Fail("missing argument");
+        if (G > kPredMaxGroups) throw Fail("code predictor supports up to 64 codebooks");
+        if (n_embs < G - 2 || (G > 2 && !embs)) throw Fail("code predictor needs an embedding per codebook after the first");
+        if (G + 1 > S.cap) throw Fail("context exceeds GPU KV capacity");
+        const int64_t din = in_proj >= 0 ? mat_at(in_proj).cols : X.H;
+        if (in_proj >= 0 && mat_at(in_proj).rows != X.H) throw Fail("in_proj output differs from the hidden size");
+        for (int i = 0; i < G - 1; ++i) {
+            const GpuMat &Hm = mat_at(heads[i]);
+            if (Hm.cols != X.H) throw Fail("head width differs from the hidden size");
+            if (Hm.rows > kSampleMaxN) throw Fail("sampler supports up to 16384 logits");
+        }
+        for (int i = 0; i < G - 2; ++i)
+            if (mat_at(embs[i]).cols != din) throw Fail("embedding width differs from the predictor input");
+        ensure_rows(X, 2);
+        for (int i = 0; i < G - 1; ++i) prepare_head(X, heads[i], true);
+        if (in_proj >= 0) ensure_xin(X, 2 * din);
+        pred_buffers(X);
+        HIPCHECK(hipStreamSynchronize(g.stream));  // the pinned blocks may feed an earlier copy
+        for (int cb = 0; cb < G; ++cb) {
+            voxhip_sample_cfg c = *cfg;
+            c.codebook = uint32_t(cb); c.draw = 0;
+            std::memset(&X.pred_cfg_host[cb], 0, sizeof(SampleCfgDev));
+            fill_sample_cfg(X.pred_cfg_host[cb], c, nullptr, 0);
+        }
+        HIPCHECK(hipMemcpyAsync(X.pred_cfg, X.pred_cfg_host, size_t(G) * sizeof(SampleCfgDev), hipMemcpyHostToDevice, g.stream));
+        HIPCHECK(hipMemcpyAsync(in_proj >= 0 ? X.xin : X.h, in2, size_t(2 * din) * 4, hipMemcpyHostToDevice, g.stream));
+        HIPCHECK(hipMemsetAsync(X.pred_err, 0, sizeof(int32_t), g.stream));
+        // the layer enqueue takes the first row's cache view from the host row table: this sequence's
+        set_rows(X, {row_of(S, 0), row_of(S, 1)});
+        hipGraphExec_t exec = pred_graph(X, S, seq, in_proj, heads, embs, G);
+        X.rows_valid = false;  // the graph rewrites the row table
+        HIPCHECK(hipGraphLaunch(exec, g.stream));
+        HIPCHECK(hipMemcpyAsync(X.pred_host, X.pred_codes, size_t(G) * 4, hipMemcpyDeviceToHost, g.stream));
+        HIPCHECK(hipMemcpyAsync(X.pred_host + kPredMaxGroups, X.pred_err, 4, hipMemcpyDeviceToHost, g.stream));
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        if (X.pred_host[kPredMaxGroups]) throw Fail("code out of the embedding's range");
+        for (int cb = 1; cb < G; ++cb) codes[cb] = X.pred_host[cb];
         return 1;
     }, 0);
 }

@@ -20,6 +20,11 @@ TALKER_1_7B_Q4 = dict(layers=28, hidden=2048, heads=16, kv_heads=8, head_dim=128
 COSY_LM_0_5B = dict(layers=24, hidden=896, heads=14, kv_heads=2, head_dim=64, inter=4864, theta=1e6, eps=1e-6,
                     kv_len=0, head_rows=6564, wtype=vh.Q8, head_type=vh.F32, qkv_bias=True, qk_norm=False,
                     head_bias=True, speech_tokens=6561, prefill=512, decode_steps=256)
+# Qwen3-TTS-0.6B-shaped code predictor (the frame loop of gpu_pred_frame): 5 layers of the talker's widths, 16
+# codebooks (15 passes), q8 heads of 2048 codes per codebook, bf16 code embeddings; the talker's hidden is the
+# predictor's (no in_proj)
+PRED_0_6B = dict(layers=5, hidden=1024, heads=16, kv_heads=8, head_dim=128, inter=3072, theta=1e6, eps=1e-6,
+                 kv_len=0, head_rows=0, wtype=vh.Q8, head_type=vh.Q8, groups=16, vocab=2048, emb_type=vh.BF16)
 NAMES = ("q", "k", "v", "o", "gate", "up", "down")
 
 

@@ -135,6 +135,7 @@ SIGNATURES = {
     "voxhip_f5_end": (_I, [_I]),
     "voxhip_lm_sample_dev": (_I, [_P, C.c_int32, C.POINTER(LmCfg), _I64, _P, C.c_int32, _P, _P]),
     "voxhip_lm_generate": (_I, [_I, _I, _P, _I64, _I, _I, C.POINTER(LmCfg), _P, _P, _P]),
+    "voxhip_pred_frame": (_I, [_I, _I, _P, _I, _P, _I, _P, _I, C.POINTER(SampleCfg), _P]),
     "voxhip_mat_synthetic": (_I, [_I32, _I64, _I64, _U64, _U32, _F, _F, _I]),
     "voxhip_mat_download": (_I, [_I, _P, _P, _P]),
     "voxhip_mat_free": (_I, [_I]),
@@ -460,6 +461,19 @@ def lm_generate(xfmr, seq, x, head, speech_emb, cfg, want_logp=False):
         rows = min(n + 1, cfg.max_len)
         logp = logp[:rows]
     return tokens[:n], logp
+
+
+def pred_frame(xfmr, seq, in2, in_proj, heads, embs, cfg):
+    """gpu_pred_frame: the code predictor's frame on the device. in2 [2][din]; heads / embs lists of matrix handles
+    (in_proj -1 for none); cfg a SampleCfg (temperature, top_k, top_p, seed, frame). Returns codes [len(heads) + 1]
+    with codes[0] = 0 (the talker's code is the caller's)."""
+    in2 = f32(in2)
+    h = np.ascontiguousarray(heads, dtype=np.int32)
+    e = np.ascontiguousarray(embs, dtype=np.int32) if len(embs) else np.zeros(1, np.int32)
+    codes = np.zeros(len(heads) + 1, np.int32)
+    _check(lib().voxhip_pred_frame(xfmr, seq, _p(in2), in_proj, _p(h), h.size, _p(e), len(embs), C.byref(cfg), _p(codes)),
+           "pred_frame")
+    return codes
 
 
 def f5_create(dim, depth, heads, dim_head, ff_mult, mel_dim, text_dim, pe_attn_head, in_proj, norm_out, proj_out, blocks,
