@@ -138,6 +138,58 @@ int main() {
     CHECK(!gpu_stats().last_error.empty());
     gpu_seq_free(seq);
     CHECK(gpu_seq_create(T.gpu_id, 32) == seq);  // pooled buffers are reused (gpu_vulkan.cpp:834-837)
+    // the code predictor's frame (backend_qwen3.cpp:426-445 calls gpu_pred_frame): the same transformer as a 6-codebook
+    // predictor without in_proj, f32 code embeddings; the codes must equal the loop run pass by pass through
+    // gpu_xfmr_forward with the oracle's sampler (draw (frame, cb)) and the oracle's mat_row
+    {
+        const int G = 6;
+        std::vector<Q8> hq;
+        std::vector<Mat> heads, embs;
+        for (int i = 0; i < G - 1; ++i) hq.emplace_back(rng, V, H);
+        for (auto &h : hq) {
+            heads.push_back(h.mat());
+            heads.back().gpu = gpu_upload(heads.back());
+        }
+        std::vector<std::vector<float>> ew(G - 2, std::vector<float>(size_t(V * H)));
+        for (auto &e : ew) for (auto &v : e) v = nd(rng);
+        for (auto &e : ew) {
+            Mat m;
+            m.type = WType::F32; m.data = reinterpret_cast<const uint8_t *>(e.data()); m.rows = V; m.cols = H;
+            m.gpu = gpu_upload(m);
+            embs.push_back(m);
+        }
+        GpuSampleCfg c;
+        c.temperature = 0.9f; c.top_k = 20; c.top_p = 0.95f; c.key0 = 77; c.key1 = 0; c.frame = 3;
+        std::vector<float> in2(static_cast<size_t>(2 * H));
+        for (auto &v : in2) v = nd(rng);
+        const int s1 = gpu_seq_create(T.gpu_id, 16), s2 = gpu_seq_create(T.gpu_id, 16);
+        std::vector<int32_t> codes(G, -1);
+        codes[0] = 5;
+        CHECK(gpu_pred_frame(T, s1, in2.data(), nullptr, heads, embs, c, codes.data()));
+        CHECK(codes[0] == 5);  // the talker's code stays the caller's
+        std::vector<float> xin = in2, out(H), logits(V);
+        int64_t p = 0;
+        bool same = true;
+        for (int cb = 1; cb < G; ++cb) {
+            const int64_t m = cb == 1 ? 2 : 1;
+            CHECK(gpu_xfmr_forward(T, s2, p, xin.data(), m, out.data(), nullptr, &heads[size_t(cb - 1)], logits.data()));
+            const int32_t want = vo_sample_logits(logits.data(), V, c.temperature, c.top_p, c.top_k, 1.0f, nullptr, 0,
+                                                  vo_uniform(77, 3, uint32_t(cb), 0));
+            same = same && codes[size_t(cb)] == want;
+            p += m;
+            if (cb + 1 < G) {
+                vo_mat oe{VO_F32, ew[size_t(cb - 1)].data(), nullptr, V, H, nullptr};
+                xin.assign(size_t(H), 0.f);
+                vo_mat_row(&oe, want, xin.data());
+            }
+        }
+        std::printf("pred frame codes:");
+        for (int cb = 1; cb < G; ++cb) std::printf(" %d", codes[size_t(cb)]);
+        std::printf("\n");
+        CHECK(same);
+        gpu_seq_free(s1);
+        gpu_seq_free(s2);
+    }
     // entry points this backend leaves to the CPU answer like gpu_stub.cpp
     CHECK(gpu_f5_create(GpuF5Desc{}) == -1 && gpu_cosy_create(GpuCosyDesc{}) == -1);
     std::printf("%d passed, %d failed\n", g_pass, g_fail);
