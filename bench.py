@@ -227,6 +227,26 @@ def bench_cfg5(vh, synth, reps=3):
             "total_ms": round(t_all, 3), "tokens": ntok}
 
 
+def bench_vocos(vh, synth, reps=5):
+    """F5-TTS's Vocos backbone + head (gpu_f5_vocos; the iSTFT stays on the host as in the reference) on 938 mel frames
+    (10 s of 24 kHz audio), f16 linears. Host wall-clock (median), the mel upload and the [T][1026] download included."""
+    dit = synth.DiT(dict(synth.F5_DIT, depth=1), seed=0, vocos=synth.F5_VOCOS)
+    T = synth.F5_VOCOS["frames"]
+    mel = np.random.default_rng(3).standard_normal((T, synth.F5_DIT["mel"])).astype(np.float32)
+    vh.f5_vocos(dit.f5, mel)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        out = vh.f5_vocos(dit.f5, mel)
+        times.append((time.perf_counter() - t0) * 1000.0)
+    assert np.isfinite(out).all()
+    ms = float(np.median(times))
+    fl = dit.vocos_flops(T)
+    return {"workload": "f5-tts vocos backbone + head (gpu_f5_vocos): 938 frames, dim 512, 8 ConvNeXt blocks, f16 linears",
+            "ms": round(ms, 3), "gflop": round(fl / 1e9, 2), "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
+            "audio_s_per_s": round(T * 256 / 24000 / (ms * 1e-3), 1)}
+
+
 def bench_pred(vh, synth, frames=20):
     """The code predictor's frame on the device (gpu_pred_frame; the loop engine.cpp:676-683 runs on the CPU in the
     reference when the device does not provide it): 15 passes of the 5-layer q8 predictor (2 rows at positions 0-1,
@@ -282,7 +302,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-other", action="store_true",
                     help="skip the configs[0] / [2] / [3] / [4] and code-predictor measurements")
-    ap.add_argument("--only", choices=["configs[0]", "configs[2]", "configs[3]", "configs[4]", "pred_frame"],
+    ap.add_argument("--only", choices=["configs[0]", "configs[2]", "configs[3]", "configs[4]", "pred_frame", "f5_vocos"],
                     help="run one of the other BASELINE configurations (or the code-predictor frame) alone and print "
                          "its JSON object (for profiling)")
     ap.add_argument("--no-breakdown", action="store_true",
@@ -301,7 +321,7 @@ def main():
     if args.only:
         legs = {"configs[0]": lambda: bench_cfg1(vh), "configs[2]": lambda: bench_cfg3(vh, synth, 100, 10),
                 "configs[3]": lambda: bench_cfg4(vh, synth), "configs[4]": lambda: bench_cfg5(vh, synth),
-                "pred_frame": lambda: bench_pred(vh, synth)}
+                "pred_frame": lambda: bench_pred(vh, synth), "f5_vocos": lambda: bench_vocos(vh, synth)}
         print(json.dumps({args.only: legs[args.only]()}))
         return
     t0 = time.perf_counter()
@@ -367,7 +387,7 @@ def main():
         t0 = time.perf_counter()
         other = {"configs[0]": bench_cfg1(vh), "configs[2]": bench_cfg3(vh, synth, 100, 10),
                  "configs[3]": bench_cfg4(vh, synth), "configs[4]": bench_cfg5(vh, synth),
-                 "pred_frame": bench_pred(vh, synth)}
+                 "pred_frame": bench_pred(vh, synth), "f5_vocos": bench_vocos(vh, synth)}
         log(f"other configs: {json.dumps(other)} ({time.perf_counter() - t0:.1f} s)")
 
     cpu = None

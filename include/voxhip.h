@@ -175,8 +175,8 @@ int voxhip_sample_logits(const float *logits, int32_t n, const voxhip_sample_cfg
 int voxhip_pred_frame(int xfmr, int seq, const float *in2, int in_proj, const int *heads, int n_heads, const int *embs,
                       int n_embs, const voxhip_sample_cfg *cfg, int32_t *codes);
 
-/* gpu_codec_* (gpu.hpp:55-61), gpu_f5_vocos (gpu.hpp:88), gpu_cosy_* (gpu.hpp:114-119) are not provided yet:
- * gpu_hip.cpp answers them like gpu_stub.cpp (-1 / false), and the callers compute on the CPU. */
+/* gpu_codec_* (gpu.hpp:55-61) and gpu_cosy_* (gpu.hpp:114-119) are not provided yet: gpu_hip.cpp answers them
+ * like gpu_stub.cpp (-1 / false), and the callers compute on the CPU. */
 
 /* ---------------------------------------------------------------- device-resident path
  * Entry points for callers that keep activations in device memory (bench, tests, a device-side
@@ -244,12 +244,25 @@ typedef struct voxhip_f5_conv {
 typedef struct voxhip_f5_block {
     int32_t ada, q, k, v, o, ff1, ff2;
 } voxhip_f5_block;
-/* GpuF5Desc (gpu.hpp:67-81) without its Vocos fields. dim_head must be 64. */
+/* GpuF5Desc::VBlock (gpu.hpp:78): a Vocos ConvNeXt block; dw depthwise (groups = cin = cout, w [C][K]). */
+typedef struct voxhip_f5_vblock {
+    voxhip_f5_conv dw;
+    const float *ln_w, *ln_b, *gamma; /* [vocos_dim] */
+    int32_t pw1, pw2;                 /* matrix handles: vocos_inter x vocos_dim, vocos_dim x vocos_inter */
+} voxhip_f5_vblock;
+/* GpuF5Desc (gpu.hpp:67-81). dim_head must be 64. vocos_dim 0: no Vocos (gpu_f5_vocos then fails and the caller
+ * runs the vocoder on the CPU); else v_embed (mel_dim -> vocos_dim), the norms, n_vblocks blocks and v_head
+ * (vocos_out x vocos_dim). */
 typedef struct voxhip_f5_desc {
     int32_t dim, depth, heads, dim_head, ff_mult, mel_dim, text_dim, pe_attn_head;
     int32_t in_proj, norm_out, proj_out;
     const voxhip_f5_block *blocks; /* [depth] */
     voxhip_f5_conv pos1, pos2;
+    int32_t vocos_dim, vocos_inter, vocos_out;
+    voxhip_f5_conv v_embed;
+    const float *v_ln_w, *v_ln_b, *v_fln_w, *v_fln_b;
+    const voxhip_f5_vblock *v_blocks; /* [n_vblocks] */
+    int32_t n_vblocks, v_head;
 } voxhip_f5_desc;
 int voxhip_f5_create(const voxhip_f5_desc *d);  /* gpu_f5_create (gpu.hpp:82): a handle or -1 */
 /* gpu_f5_begin (gpu.hpp:85): B sequences of N rows; cat0 [B][N][2 mel + text] (zeros in the x columns),
@@ -259,6 +272,12 @@ int voxhip_f5_begin(int id, int B, int N, const float *cat0, const float *rope);
  * out [B][N][mel]. */
 int voxhip_f5_step(int id, const float *x, const float *ts, float *out);
 int voxhip_f5_end(int id);  /* gpu_f5_end (gpu.hpp:90): frees the step buffers, keeps the weights */
+/* gpu_f5_vocos (gpu.hpp:88-89; gpu_f5.cpp:334-373, the CPU path f5.cpp:792-806): mel [T][mel_dim] -> the Vocos head
+ * output head [T][vocos_out] (log-magnitude | phase); the iSTFT stays with the caller. */
+int voxhip_f5_vocos(int id, const float *mel, int T, float *head);
+/* The Vocos head width of an F5 handle into *vout (0 when created without Vocos). Returns 1, or 0 for a bad handle.
+ * No counterpart in gpu.hpp: gpu_hip.cpp sizes gpu_f5_vocos's output with it. */
+int voxhip_f5_vocos_out(int id, int32_t *vout);
 
 /* Synthetic weights and caches, generated on the device (Philox4x32-10 Box-Muller, mean + std * z).
  * voxhip_mat_synthetic: f32 values, then quantized on the device to `type` with the reference's

@@ -54,6 +54,17 @@ class VoF5(C.Structure):
                [("blocks", C.POINTER(VoF5Block)), ("pos1", VoConv), ("pos2", VoConv)]
 
 
+class VoVocosBlock(C.Structure):
+    _fields_ = [("dw", VoConv), ("ln_w", C.c_void_p), ("ln_b", C.c_void_p), ("gamma", C.c_void_p), ("pw1", VoMat),
+                ("pw2", VoMat)]
+
+
+class VoVocos(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("dim", "inter", "mel_dim", "layers")] + \
+               [("embed", VoConv)] + [(n, C.c_void_p) for n in ("ln_w", "ln_b", "fln_w", "fln_b")] + \
+               [("blocks", C.POINTER(VoVocosBlock)), ("head", VoMat)]
+
+
 def _p(a):
     return None if a is None else a.ctypes.data
 
@@ -72,6 +83,7 @@ def _declare(lib, prefix):
         "rope_inv_freq": (None, [I64, D, P]),
         "rope_apply": (None, [P, I64, I64, P, I64]),
         "silu": (F, [F]),
+        "gelu_erf": (F, [F]),
         "transformer_forward": (C.c_int, [P, P, P, I64, P, P]),
         "transformer_forward_steps": (C.c_int, [P, P, I64, P, P]),
     }
@@ -85,6 +97,7 @@ def _declare(lib, prefix):
             "conv1d": (None, [P, P, I32, P]),
             "f5_modulate": (None, [P, I64, I32, P, P, P]),
             "f5_step": (C.c_int, [P, I32, I32, P, P, P, P]),
+            "vocos_head": (C.c_int, [P, P, I32, P]),
             "lm_step": (I32, [P, I32, P, I32, I64, I32, I32, F, I32, I32, F, U64, U32]),
             "noise": (None, [U64, U32, C.c_size_t, P]),
             "f16_to_f32": (F, [C.c_uint16]),
@@ -280,6 +293,36 @@ def f5_step(m, B, N, cat, ts, rope):
     out = np.empty((B * N, m.mel_dim), np.float32)
     lib().vo_f5_step(C.byref(m.c), B, N, _p(cat), _p(np.ascontiguousarray(ts, np.float32)),
                      _p(np.ascontiguousarray(rope, np.float32)), _p(out))
+    return out
+
+
+def gelu_erf(x, use_ref=False):
+    return (ref().ref_gelu_erf if use_ref else lib().vo_gelu_erf)(x)
+
+
+class Vocos:
+    """F5's Vocos backbone + head in the oracle's struct layout: embed Conv, ln (w, b), blocks = list of dicts
+    dw (Conv), ln_w, ln_b, gamma, pw1, pw2 (Mat), fln (w, b), head Mat."""
+
+    def __init__(self, dim, inter, mel_dim, embed, ln_w, ln_b, blocks, fln_w, fln_b, head):
+        f = lambda a: np.ascontiguousarray(a, np.float32)
+        self.vecs = [f(a) for a in (ln_w, ln_b, fln_w, fln_b)]
+        self.bvecs = [[f(b[n]) for n in ("ln_w", "ln_b", "gamma")] for b in blocks]
+        self.keep = (embed, blocks, head)
+        arr = (VoVocosBlock * max(1, len(blocks)))()
+        for i, b in enumerate(blocks):
+            arr[i] = VoVocosBlock(b["dw"].c, _p(self.bvecs[i][0]), _p(self.bvecs[i][1]), _p(self.bvecs[i][2]), b["pw1"].c,
+                                  b["pw2"].c)
+        self._arr = arr
+        self.c = VoVocos(dim, inter, mel_dim, len(blocks), embed.c, *[_p(a) for a in self.vecs], arr, head.c)
+        self.out = head.rows
+
+
+def vocos_head(v, mel):
+    mel = np.ascontiguousarray(mel, np.float32)
+    out = np.empty((mel.shape[0], v.out), np.float32)
+    rc = lib().vo_vocos_head(C.byref(v.c), _p(mel), mel.shape[0], _p(out))
+    assert rc == 0
     return out
 
 

@@ -72,6 +72,7 @@ void ref_conv1d(const float *w, int cin, int cout, int K, int groups, const floa
     c.load(w, cin, cout, K, groups, bias);
     c.forward(x, T, y);
 }
+float ref_gelu_erf(float x) { return gelu_erf(x); }
 void ref_set_threads(int n) { set_num_threads(n); }
 void ref_philox(const uint32_t c[4], const uint32_t k[2], uint32_t out[4]) {
     auto r = Philox4x32::block({c[0], c[1], c[2], c[3]}, {k[0], k[1]});

@@ -775,6 +775,33 @@ void vo_f5_modulate(const float *x, int64_t R, int32_t D, const float *sc, const
     }
 }
 
+float vo_gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f)); } /* kernels.hpp:106 */
+
+/* F5Model::vocode (f5.cpp:779-806) up to the head: embed conv, LayerNorm, the ConvNeXt blocks (depthwise conv,
+ * LayerNorm, pw1 + GELU-erf, pw2, x += gamma * z), final LayerNorm, head. */
+int vo_vocos_head(const vo_vocos *v, const float *mel, int32_t T, float *head) {
+    const int D = v->dim, I = v->inter;
+    float *x = (float *)malloc(sizeof(float) * (size_t)T * D), *y = (float *)malloc(sizeof(float) * (size_t)T * D);
+    float *h = (float *)malloc(sizeof(float) * (size_t)T * I), *z = (float *)malloc(sizeof(float) * (size_t)T * D);
+    if (!x || !y || !h || !z) { free(x); free(y); free(h); free(z); return -1; }
+    vo_conv1d(&v->embed, mel, T, x);
+    for (int64_t t = 0; t < T; ++t) vo_layernorm(x + t * D, v->ln_w, v->ln_b, D, 1e-6f, x + t * D);
+    for (int i = 0; i < v->layers; ++i) {
+        const vo_vocos_block *b = &v->blocks[i];
+        vo_conv1d(&b->dw, x, T, y);
+        for (int64_t t = 0; t < T; ++t) vo_layernorm(y + t * D, b->ln_w, b->ln_b, D, 1e-6f, y + t * D);
+        vo_matmul(&b->pw1, y, T, h, 1);
+        for (int64_t j = 0; j < (int64_t)T * I; ++j) h[j] = vo_gelu_erf(h[j]);
+        vo_matmul(&b->pw2, h, T, z, 1);
+        for (int64_t t = 0; t < T; ++t)
+            for (int c = 0; c < D; ++c) x[t * D + c] += b->gamma[c] * z[t * D + c];
+    }
+    for (int64_t t = 0; t < T; ++t) vo_layernorm(x + t * D, v->fln_w, v->fln_b, D, 1e-6f, x + t * D);
+    vo_matmul(&v->head, x, T, head, 1);
+    free(x); free(y); free(h); free(z);
+    return 0;
+}
+
 int vo_f5_step(const vo_f5 *m, int32_t B, int32_t N, const float *cat, const float *ts, const float *rope, float *out) {
     const int D = m->dim, H = m->heads, HD = m->dim_head, INNER = H * HD, HH = HD / 2, FF = D * m->ff_mult;
     const int64_t R = (int64_t)B * N;

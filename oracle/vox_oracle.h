@@ -155,6 +155,23 @@ typedef struct {
  * text), ts [dim] (SiLU of the time embedding), rope [N][dim_head/2][2] (cos, sin) -> out [B*N][mel]. */
 int vo_f5_step(const vo_f5 *m, int32_t B, int32_t N, const float *cat, const float *ts, const float *rope, float *out);
 
+/* ---- F5-TTS Vocos backbone and head (f5.cpp:779-806), the iSTFT left out ---- */
+float vo_gelu_erf(float x); /* kernels.hpp:106 */
+typedef struct {
+    vo_conv dw; /* depthwise, K 7 */
+    const float *ln_w, *ln_b, *gamma;
+    vo_mat pw1, pw2;
+} vo_vocos_block;
+typedef struct {
+    int32_t dim, inter, mel_dim, layers;
+    vo_conv embed;
+    const float *ln_w, *ln_b, *fln_w, *fln_b;
+    const vo_vocos_block *blocks;
+    vo_mat head;
+} vo_vocos;
+/* F5Model::vocode up to the head output: mel [T][mel_dim] -> head [T][head.rows] (log-magnitude | phase). */
+int vo_vocos_head(const vo_vocos *v, const float *mel, int32_t T, float *head);
+
 /* Thread count for the row-parallel loops (matmul); 1 = scalar single-thread. Results do not depend on it. */
 void vo_set_threads(int n);
 int vo_get_threads(void);

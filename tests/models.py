@@ -90,7 +90,7 @@ class F5Model:
     backend. Linear weights of type wtype (~N(0, std)) with biases; position convolutions f32 in Conv1d::w layout."""
 
     def __init__(self, seed, dim, depth, heads, dim_head=64, ff_mult=2, mel=20, text=32, K=7, groups=4, pe_attn_head=0,
-                 wtype=F16, std=0.05):
+                 wtype=F16, std=0.05, vocos=None):
         rng = np.random.default_rng(seed)
         self.dim, self.depth, self.heads, self.hd, self.mel, self.text = dim, depth, heads, dim_head, mel, text
         self.ff_mult, self.pe = ff_mult, pe_attn_head
@@ -116,12 +116,43 @@ class F5Model:
         oc = [po.Conv(*c) for c in self.pos]
         self.ox = po.F5(dim, depth, heads, dim_head, ff_mult, mel, text, pe_attn_head, om["in_proj"], om["norm_out"],
                         om["proj_out"], ob, oc[0], oc[1])
+        self.vocos = None
+        if vocos:  # dict(dim, inter, layers, out[, wtype]): Vocos backbone + head (f5.cpp:333-346)
+            vd, vi, vt = vocos["dim"], vocos["inter"], vocos.get("wtype", wtype)
+
+            def vmat(rows, cols, s=0.05):
+                d, sc, b = make_mat(rng, vt, rows, cols, std=s, bias=True)
+                return (vt, d, rows, cols, sc, b)
+
+            def vec(n, mean, sd):
+                return (mean + sd * rng.standard_normal(n)).astype(np.float32)
+            v = {"dim": vd, "inter": vi, "out": vocos["out"],
+                 "embed": ((rng.standard_normal((1, vd, 7, mel)) * 0.1).astype(np.float32), vec(vd, 0, 0.05), mel, vd, 7, 1),
+                 "ln_w": vec(vd, 1, 0.1), "ln_b": vec(vd, 0, 0.1), "fln_w": vec(vd, 1, 0.1), "fln_b": vec(vd, 0, 0.1),
+                 "head": vmat(vocos["out"], vd), "blocks": []}
+            for _ in range(vocos["layers"]):
+                v["blocks"].append({"dw": ((rng.standard_normal((vd, 7)) * 0.3).astype(np.float32), vec(vd, 0, 0.05), vd, vd, 7, vd),
+                                    "ln_w": vec(vd, 1, 0.1), "ln_b": vec(vd, 0, 0.1), "gamma": vec(vd, 0, 0.1),
+                                    "pw1": vmat(vi, vd), "pw2": vmat(vd, vi)})
+            self.vocos = v
+            self.vox = po.Vocos(vd, vi, mel, po.Conv(*v["embed"]), v["ln_w"], v["ln_b"],
+                                [{"dw": po.Conv(*b["dw"]), "ln_w": b["ln_w"], "ln_b": b["ln_b"], "gamma": b["gamma"],
+                                  "pw1": po.Mat(*b["pw1"]), "pw2": po.Mat(*b["pw2"])} for b in v["blocks"]],
+                                v["fln_w"], v["fln_b"], po.Mat(*v["head"]))
 
     def create(self, hip):
         h = {k: hip.upload(hip.HostMat(*v)) for k, v in self.mats.items()}
         hb = [{k: hip.upload(hip.HostMat(*v)) for k, v in b.items()} for b in self.blocks]
+        vk = {}
+        if self.vocos:
+            v = self.vocos
+            vk = dict(vocos=dict(dim=v["dim"], inter=v["inter"], out=v["out"], embed=v["embed"], ln_w=v["ln_w"],
+                                 ln_b=v["ln_b"], fln_w=v["fln_w"], fln_b=v["fln_b"], head=hip.upload(hip.HostMat(*v["head"])),
+                                 blocks=[dict(dw=b["dw"], ln_w=b["ln_w"], ln_b=b["ln_b"], gamma=b["gamma"],
+                                              pw1=hip.upload(hip.HostMat(*b["pw1"])), pw2=hip.upload(hip.HostMat(*b["pw2"])))
+                                         for b in v["blocks"]]))
         return hip.f5_create(self.dim, self.depth, self.heads, self.hd, self.ff_mult, self.mel, self.text, self.pe,
-                             h["in_proj"], h["norm_out"], h["proj_out"], hb, self.pos[0], self.pos[1])
+                             h["in_proj"], h["norm_out"], h["proj_out"], hb, self.pos[0], self.pos[1], **vk)
 
     def inputs(self, rng, B, N):
         """cat0 [B N][2 mel + text] with zeros in the x columns, x [N][mel], ts [dim], rope."""

@@ -59,3 +59,33 @@ def test_f5_rejects_bad_shapes(hip):
     f5 = m.create(hip)
     with pytest.raises(hip.VoxHipError, match="before begin"):
         hip.f5_step(f5, np.zeros((10, 20), np.float32), np.zeros(128, np.float32), 1, 10, 20)
+
+
+@pytest.mark.parametrize("wtype", [F16, BF16, F32])
+def test_f5_vocos(hip, oracle, wtype):
+    # gpu_f5_vocos (gpu_f5.cpp:334-373): the Vocos backbone and head on the device against the oracle's restatement of
+    # F5Model::vocode (f5.cpp:792-806); the embed conv's rows (K 7 x mel 20 = 140) are zero-padded to 144 on the device
+    m = F5Model(70 + wtype, 128, 1, 2, mel=20, text=32, K=7, groups=4, wtype=wtype,
+                vocos=dict(dim=64, inter=192, layers=2, out=34))
+    f5 = m.create(hip)
+    rng = np.random.default_rng(wtype)
+    for T in (57, 9):
+        mel = rng.standard_normal((T, 20)).astype(np.float32)
+        got = hip.f5_vocos(f5, mel)
+        want = oracle.vocos_head(m.vox, mel)
+        assert got.shape == want.shape and rel_err(got, want) < TOL, (T, rel_err(got, want))
+
+
+def test_f5_vocos_full_width(hip, oracle):
+    # F5-TTS's Vocos widths (mel 100, dim 512, intermediate 1536, 8 blocks, head 2 x 513) on 100 frames
+    m = F5Model(80, 128, 1, 2, mel=100, text=32, K=7, groups=4, wtype=F16,
+                vocos=dict(dim=512, inter=1536, layers=8, out=1026))
+    f5 = m.create(hip)
+    mel = np.random.default_rng(8).standard_normal((100, 100)).astype(np.float32)
+    got = hip.f5_vocos(f5, mel)
+    want = oracle.vocos_head(m.vox, mel)
+    assert rel_err(got, want) < TOL, rel_err(got, want)
+    # a model created without Vocos reports it instead of running
+    plain = F5Model(81, 128, 1, 2, wtype=F16).create(hip)
+    with pytest.raises(hip.VoxHipError, match="Vocos"):
+        hip.f5_vocos(plain, mel[:, :20])

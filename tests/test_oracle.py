@@ -259,6 +259,68 @@ def test_f5_modulate_closed_form(oracle):
     assert np.max(np.abs(y - want)) < 1e-5
 
 
+def test_gelu_erf_pinned(oracle):
+    # kernels.hpp:106: 0.5 x (1 + erf(x / sqrt 2)); bit-exact against the compiled reference, within float rounding of the
+    # float64 closed form (absolute: the formula's own cancellation near x = -5.5, where the value is ~1e-7), and the
+    # identity gelu(x) - gelu(-x) = x
+    import math
+    xs = np.concatenate([np.linspace(-9, 9, 3001), np.random.default_rng(5).standard_normal(500) * 3]).astype(np.float32)
+    for x in xs:
+        g = po.gelu_erf(float(x))
+        if po.ref() is not None:
+            assert np.float32(g) == np.float32(po.gelu_erf(float(x), use_ref=True))
+        want = 0.5 * float(x) * (1 + math.erf(float(x) / math.sqrt(2)))
+        assert abs(g - want) <= 3e-7 * max(1.0, abs(float(x))), (x, g, want)
+        assert abs((g - po.gelu_erf(float(-x))) - float(x)) <= 4e-7 * max(1.0, abs(float(x)))
+    assert po.gelu_erf(0.0) == 0.0
+
+
+def vocos_numpy(v, mel):
+    """F5Model::vocode up to the head in float64 numpy, written from the Vocos equations (ConvNeXt blocks), for pinning
+    vo_vocos_head."""
+    from scipy.special import erf
+
+    def conv(c, x):
+        w, b, cin, cout, K, groups = c
+        if groups == cin and w.ndim == 2:  # depthwise [C][K]
+            w = w.reshape(groups, 1, K, 1)
+        cig, pad = cin // groups, K // 2
+        cog = cout // groups
+        xp = np.zeros((x.shape[0] + 2 * pad, cin))
+        xp[pad:pad + x.shape[0]] = x
+        y = np.tile(b.astype(np.float64), (x.shape[0], 1))
+        for g in range(groups):
+            for k in range(K):
+                y[:, g * cog:(g + 1) * cog] += xp[k:k + x.shape[0], g * cig:(g + 1) * cig] @ w[g, :, k, :].T.astype(np.float64)
+        return y
+
+    def ln(x, w, b):
+        return (x - x.mean(1, keepdims=True)) / np.sqrt(x.var(1, keepdims=True) + 1e-6) * w + b
+
+    def lin(t, x):
+        typ, d, r, c, s, b = t
+        W = np.stack([po.mat_row(po.Mat(typ, d, r, c, s, b), i) for i in range(r)]).astype(np.float64)
+        return x @ W.T + (b.astype(np.float64) if b is not None else 0)
+    x = ln(conv(v["embed"], mel.astype(np.float64)), v["ln_w"], v["ln_b"])
+    for blk in v["blocks"]:
+        y = ln(conv(blk["dw"], x), blk["ln_w"], blk["ln_b"])
+        h = lin(blk["pw1"], y)
+        h = 0.5 * h * (1 + erf(h / np.sqrt(2)))
+        x = x + blk["gamma"] * lin(blk["pw2"], h)
+    return lin(v["head"], ln(x, v["fln_w"], v["fln_b"]))
+
+
+@pytest.mark.parametrize("wt", [0, 1, 2])
+def test_vocos_head_against_numpy(oracle, wt):
+    import models
+    m = models.F5Model(40 + wt, 32, 1, 2, dim_head=16, mel=12, text=8, K=5, groups=4, wtype=wt,
+                       vocos=dict(dim=48, inter=96, layers=2, out=18))
+    mel = np.random.default_rng(wt).standard_normal((37, 12)).astype(np.float32)
+    got = po.vocos_head(m.vox, mel)
+    want = vocos_numpy(m.vocos, mel)
+    assert np.max(np.abs(got - want)) / max(1.0, np.max(np.abs(want))) < 1e-5
+
+
 def f5_numpy(m, B, N, cat, ts, rope):
     """dit_forward in float64 numpy, written from the model's equations (F5-TTS DiT), for pinning vo_f5_step."""
     D, H, HD, mel = m.dim, m.heads, m.hd, m.mel

@@ -6,8 +6,8 @@
 //
 // Error convention of the reference backend (gpu_vulkan.cpp:568-571, :800-803): no exception escapes, false/-1
 // means "compute on the CPU", the reason is kept for gpu_stats().last_error, and one warning goes to stderr.
-// Entry points not provided by this backend yet (the codec, the Vocos vocoder, the CosyVoice flow) answer like
-// gpu_stub.cpp, so their callers stay on the CPU.
+// Entry points not provided by this backend yet (the codec, the CosyVoice flow) answer like gpu_stub.cpp, so their
+// callers stay on the CPU.
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -196,12 +196,19 @@ int gpu_f5_create(const GpuF5Desc &d) {
     std::vector<voxhip_f5_block> blocks;
     for (const GpuF5Desc::Block &b : d.blocks) blocks.push_back({b.ada, b.q, b.k, b.v, b.o, b.ff1, b.ff2});
     auto conv = [](const GpuF5Conv &c) { return voxhip_f5_conv{c.w, c.b, c.cin, c.cout, c.K, c.groups}; };
-    voxhip_f5_desc c;
+    voxhip_f5_desc c{};
     c.dim = d.dim; c.depth = d.depth; c.heads = d.heads; c.dim_head = d.dim_head; c.ff_mult = d.ff_mult;
     c.mel_dim = d.mel_dim; c.text_dim = d.text_dim; c.pe_attn_head = d.pe_attn_head;
     c.in_proj = d.in_proj; c.norm_out = d.norm_out; c.proj_out = d.proj_out;
     c.blocks = blocks.data(); c.pos1 = conv(d.pos1); c.pos2 = conv(d.pos2);
     if (int(blocks.size()) != d.depth) return -1;
+    // Vocos (vocos_dim 0: the vocoder stays on the CPU, f5.cpp:381-385)
+    std::vector<voxhip_f5_vblock> vb;
+    for (const GpuF5Desc::VBlock &b : d.v_blocks) vb.push_back({conv(b.dw), b.ln_w, b.ln_b, b.gamma, b.pw1, b.pw2});
+    c.vocos_dim = d.vocos_dim; c.vocos_inter = d.vocos_inter; c.vocos_out = d.vocos_out;
+    c.v_embed = conv(d.v_embed);
+    c.v_ln_w = d.v_ln_w; c.v_ln_b = d.v_ln_b; c.v_fln_w = d.v_fln_w; c.v_fln_b = d.v_fln_b;
+    c.v_blocks = vb.data(); c.n_vblocks = int32_t(vb.size()); c.v_head = d.v_head;
     const int id = voxhip_f5_create(&c);
     if (id < 0) warn_once("F5 graph");
     return id;
@@ -213,6 +220,16 @@ bool gpu_f5_step(int id, const float *x, const float *ts, float *out) {
     return false;
 }
 void gpu_f5_end(int id) { (void)voxhip_f5_end(id); }
+// Vocos up to the head on the device (gpu_f5.cpp:334-373); false keeps it on the CPU (f5.cpp:787-791)
+bool gpu_f5_vocos(int id, const float *mel, int T, std::vector<float> &head) {
+    if (id < 0 || T <= 0) return false;
+    int vout = 0;
+    if (!voxhip_f5_vocos_out(id, &vout) || vout <= 0) return false;  // created without Vocos: the CPU runs it
+    head.resize(size_t(T) * size_t(vout));
+    if (voxhip_f5_vocos(id, mel, T, head.data())) return true;
+    std::fprintf(stderr, "vox: Vocos on the GPU failed: %s\n", voxhip_last_error());
+    return false;
+}
 
 // The code predictor's frame loop (gpu_vulkan.cpp:968-1045): the same sampler settings for every codebook, the
 // draw (frame, cb) of each; matrices the backend does not hold keep the frame on the CPU.
@@ -244,7 +261,6 @@ int gpu_codec_state_new(int) { return -1; }
 int gpu_codec_state_clone(int) { return -1; }
 void gpu_codec_state_free(int) {}
 bool gpu_codec_forward(int, int, const float *, int, std::vector<float> &) { return false; }
-bool gpu_f5_vocos(int, const float *, int, std::vector<float> &) { return false; }  // Vocos stays on the CPU (f5.cpp:787-791)
 std::string gpu_gemm_choice() { return ""; }
 void gpu_gemm_preset(const std::string &) {}
 int gpu_cosy_create(const GpuCosyDesc &) { return -1; }

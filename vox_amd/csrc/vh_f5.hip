@@ -7,8 +7,23 @@ namespace vh {
 hipError_t launch_f5_modulate(const float *x, int64_t R, int D, const float *sc, const float *sh, float *y, _Float16 *y16,
                               int64_t lo_off, hipStream_t s) {
     if (R <= 0) return hipSuccess;
-    if (D <= 0 || D % 4 || R > INT32_MAX || (!y && !y16) || lo_off % 4) return hipErrorInvalidValue;
-    return launch(k_f5_modulate, dim3(unsigned((R + 3) / 4)), dim3(256), 0, s, x, int32_t(D), sc, sh, y, y16, lo_off, int32_t(R));
+    if (D <= 0 || D % 4 || R > INT32_MAX || (!y && !y16) || lo_off % 4 || !sc || !sh) return hipErrorInvalidValue;
+    return launch(k_f5_modulate, dim3(unsigned((R + 3) / 4)), dim3(256), 0, s, x, int32_t(D), sc, sh, y, y16, lo_off, int32_t(R),
+                  int32_t(0));
+}
+
+hipError_t launch_layernorm_rows(const float *x, int64_t R, int D, const float *w, const float *b, float *y, hipStream_t s) {
+    if (R <= 0) return hipSuccess;
+    if (D <= 0 || D % 4 || R > INT32_MAX || !y || !w) return hipErrorInvalidValue;
+    return launch(k_f5_modulate, dim3(unsigned((R + 3) / 4)), dim3(256), 0, s, x, int32_t(D), w, b, y,
+                  static_cast<_Float16 *>(nullptr), int64_t(0), int32_t(R), int32_t(1));
+}
+
+hipError_t launch_dwconv(const float *x, const float *w, const float *b, float *y, int64_t R, int C, int K, int seq, hipStream_t s) {
+    if (R <= 0) return hipSuccess;
+    if (C <= 0 || K <= 0 || K % 2 == 0 || seq <= 0 || R % seq || !w) return hipErrorInvalidValue;
+    const int64_t n = R * C;
+    return launch(k_dwconv, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, x, w, b, y, R, int32_t(C), int32_t(K), int32_t(seq));
 }
 
 hipError_t launch_f5_fill_x(const float *x, int N, int mel, float *cat, int W, int B, hipStream_t s) {

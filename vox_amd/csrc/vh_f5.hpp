@@ -11,11 +11,12 @@ typedef _Float16 f16x4a __attribute__((ext_vector_type(4)));
 
 // LayerNorm without parameters + modulation (f5.cpp:608-625), one wave per row (4 rows per 256-thread block):
 // mean and variance in double (two passes over the row, which stays in L1), inv = float(1 / sqrt(var + 1e-6)),
-// y = (x - float(mean)) * inv * (1 + scale) + shift. With y16 set, y goes out as f16 halves instead (hi at y16, lo
-// at y16 + lo_off) for a split-f16 GEMM. D % 4 == 0.
+// y = (x - float(mean)) * inv * (1 + scale) + shift. affine: LayerNorm with weight and bias instead
+// (kernels.cpp:714-723, the Vocos norms), y = (x - float(mean)) * inv * scale + shift (shift null: 0). With y16 set,
+// y goes out as f16 halves instead (hi at y16, lo at y16 + lo_off) for a split-f16 GEMM. D % 4 == 0.
 __global__ __launch_bounds__(256) void k_f5_modulate(const float *__restrict__ x, int32_t D, const float *__restrict__ sc,
                                                      const float *__restrict__ sh, float *__restrict__ y,
-                                                     _Float16 *__restrict__ y16, int64_t lo_off, int32_t R) {
+                                                     _Float16 *__restrict__ y16, int64_t lo_off, int32_t R, int32_t affine) {
     const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= R) return;
     const float *xr = x + int64_t(row) * D;
@@ -40,13 +41,16 @@ __global__ __launch_bounds__(256) void k_f5_modulate(const float *__restrict__ x
         }
     }
     const double var = wsum(q) / D;
-    const float inv = float(1.0 / sqrt(var + 1e-6)), fm = float(mean);
+    // the modulation adds the double 1e-6 (f5.cpp:608-625); LayerNorm double(eps) of its float eps 1e-6f (kernels.cpp:721)
+    const double eps = affine ? double(1e-6f) : 1e-6;
+    const float inv = float(1.0 / sqrt(var + eps)), fm = float(mean);
     for (int i = 4 * lane; i < D; i += 256) {
         const f32x4a v = *reinterpret_cast<const f32x4a *>(xr + i);
-        const f32x4a c = *reinterpret_cast<const f32x4a *>(sc + i), t = *reinterpret_cast<const f32x4a *>(sh + i);
+        const f32x4a c = *reinterpret_cast<const f32x4a *>(sc + i);
+        const f32x4a t = sh ? *reinterpret_cast<const f32x4a *>(sh + i) : f32x4a{0.f, 0.f, 0.f, 0.f};
         f32x4a r;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = (v[e] - fm) * inv * (1.0f + c[e]) + t[e];
+        for (int e = 0; e < 4; ++e) r[e] = (v[e] - fm) * inv * (affine ? c[e] : 1.0f + c[e]) + t[e];
         if (y16) {
             f16x4a hi, lo;
 #pragma unroll
@@ -61,6 +65,24 @@ __global__ __launch_bounds__(256) void k_f5_modulate(const float *__restrict__ x
             *reinterpret_cast<f32x4a *>(y + int64_t(row) * D + i) = r;
         }
     }
+}
+
+// Depthwise "same" Conv1d (f5_ops.cpp:106-147 with groups = channels: the Vocos blocks' dwconv, f5.cpp:341) over
+// batches of seq rows: y[t][c] = b[c] + sum_k w[c][k] x[t + k - K/2][c], zeros outside the batch, k in order. One
+// thread per output, consecutive threads on consecutive channels.
+__global__ __launch_bounds__(256) void k_dwconv(const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ b,
+                                                float *__restrict__ y, int64_t R, int32_t C, int32_t K, int32_t seq) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= R * C) return;
+    const int64_t r = i / C;
+    const int c = int(i % C), t = int(r % seq);
+    const int64_t r0 = r - t;
+    float acc = b ? b[c] : 0.f;
+    for (int k = 0; k < K; ++k) {
+        const int tt = t + k - K / 2;
+        if (tt >= 0 && tt < seq) acc += w[int64_t(c) * K + k] * x[(r0 + tt) * C + c];
+    }
+    y[i] = acc;
 }
 
 // cat[b][t][0..mel) = x[t][0..mel) for every batch b (the x columns of the DiT input, gpu.hpp:85-88).

@@ -82,6 +82,7 @@ static hipError_t gemm_epi(int epi, const uint8_t *w, const float *scale, const 
         case EPI_SWIGLU: return gemm_tile<WT, EPI_SWIGLU>(w, scale, A, g, s);
         case EPI_GATED_ACC: return g.gate ? gemm_tile<WT, EPI_GATED_ACC>(w, scale, A, g, s) : hipErrorInvalidValue;
         case EPI_GELU: return gemm_tile<WT, EPI_GELU>(w, scale, A, g, s);
+        case EPI_GELU_ERF: return gemm_tile<WT, EPI_GELU_ERF>(w, scale, A, g, s);
         case EPI_ROPE:
             if (!g.rope || g.hd <= 0 || g.hd % 2 || g.seq <= 0 || g.rope_cols % (2 * g.hd)) return hipErrorInvalidValue;
             return gemm_tile<WT, EPI_ROPE>(w, scale, A, g, s);
@@ -130,8 +131,9 @@ hipError_t launch_gemm_hh(int epi, const _Float16 *w, const GemmArgs &g, hipStre
 
 hipError_t launch_conv_gemm(int epi, const float *w, const float *A, const GemmArgs &g, int groups, hipStream_t s) {
     if (g.m <= 0) return hipSuccess;
-    if (g.cig <= 0 || g.cig % 4 || g.ksize <= 0 || g.ksize % 2 == 0 || g.K != g.ksize * g.cig || g.K % 8 || g.seq <= 0 ||
-        g.lda % 4 || groups <= 0 || g.n <= 0)
+    // K: ksize * cig, rounded up to a multiple of 8 with zero weights (the A loader reads zeros there)
+    if (g.cig <= 0 || g.cig % 4 || g.ksize <= 0 || g.ksize % 2 == 0 || g.K < g.ksize * g.cig || g.K >= g.ksize * g.cig + 8 ||
+        g.K % 8 || g.seq <= 0 || g.lda % 4 || groups <= 0 || g.n <= 0)
         return hipErrorInvalidValue;
     const uint8_t *wb = reinterpret_cast<const uint8_t *>(w);
     if (epi == EPI_MISH) return gemm_run<WT_F32, EPI_MISH, ASRC_CONV, 2>(wb, nullptr, A, g, groups, s);

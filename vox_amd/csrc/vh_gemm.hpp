@@ -33,6 +33,7 @@ VH_DEV float gelu_tanh_f(float x) {  // f5.cpp:93-96
     const float k = 0.7978845608028654f;
     return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
 }
+VH_DEV float gelu_erf_f(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f)); }  // kernels.hpp:106
 VH_DEV float mish_f(float x) {  // f5.cpp:97-100
     const float sp = x > 20.f ? x : log1pf(expf(x));
     return x * tanhf(sp);
@@ -46,7 +47,7 @@ VH_DEV f32x4v gemm_load_a(const float *__restrict__ A, const GemmArgs &g, int ro
     if (ASRC == ASRC_ROWS) return *reinterpret_cast<const f32x4v *>(A + int64_t(row) * g.lda + k);
     const int s = row / g.seq, t = row % g.seq, kt = k / g.cig, i = k % g.cig;
     const int tt = t + kt - g.ksize / 2;
-    if (tt < 0 || tt >= g.seq) return v;
+    if (kt >= g.ksize || tt < 0 || tt >= g.seq) return v;  // kt >= ksize: the zero padding of a weight row
     return *reinterpret_cast<const f32x4v *>(A + (int64_t(s) * g.seq + tt) * g.lda + int64_t(blockIdx.z) * g.cig + i);
 }
 
@@ -149,6 +150,7 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
                     else if (EPI == EPI_ACC) *dst += c;
                     else if (EPI == EPI_GATED_ACC) *dst += gt * c;
                     else if (EPI == EPI_GELU) *dst = gelu_tanh_f(c);
+                    else if (EPI == EPI_GELU_ERF) *dst = gelu_erf_f(c);
                     else if (EPI == EPI_GELU_H16) {
                         const float r = gelu_tanh_f(c);
                         const _Float16 hi = _Float16(r);
@@ -165,7 +167,8 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
 
 // Epilogues: EPI_STORE y = c + bias; EPI_ACC y += c + bias; EPI_SWIGLU W rows are (gate u, up u) pairs, y[u] =
 // silu(gate) * up; EPI_GATED_ACC y += gate[col] * (c + bias); EPI_GELU y = gelu_tanh(c + bias); EPI_MISH
-// y = mish(c + bias); EPI_MISH_ACC y += mish(c + bias); EPI_ROPE y = c + bias with the pairs of q | k rotated;
+// y = mish(c + bias); EPI_MISH_ACC y += mish(c + bias); EPI_GELU_ERF y = gelu_erf(c + bias); EPI_ROPE y = c + bias
+// with the pairs of q | k rotated;
 // EPI_ROPE_H16 and EPI_GELU_H16 write their results as f16 halves (hi, lo) for a following split-f16 product.
 // ASRC_CONV: W (F32) and y columns are those of group blockIdx.z.
 template <int WT, int EPI, int ASRC, int TM, int TN>

@@ -68,6 +68,10 @@ hipError_t launch_prefill_attn(const PrefillAttnArgs &a, int hd, hipStream_t s);
 hipError_t launch_f5_modulate(const float *x, int64_t R, int D, const float *sc, const float *sh, float *y, _Float16 *y16,
                               int64_t lo_off, hipStream_t s);
 hipError_t launch_f5_fill_x(const float *x, int N, int mel, float *cat, int W, int B, hipStream_t s);
+// Vocos: LayerNorm with weight and bias (double statistics, eps 1e-6) of R rows of D; depthwise "same" conv over
+// batches of seq rows (w [C][K], bias or null).
+hipError_t launch_layernorm_rows(const float *x, int64_t R, int D, const float *w, const float *b, float *y, hipStream_t s);
+hipError_t launch_dwconv(const float *x, const float *w, const float *b, float *y, int64_t R, int C, int K, int seq, hipStream_t s);
 hipError_t launch_f5_attn(const _Float16 *qkv16, int64_t lo_off, float *out, _Float16 *out16, int64_t out_lo, int B, int N,
                           int heads, int hd, int ldvt, int ldo, float scale, hipStream_t s);
 // CosyVoice2 LM: one sampling step (log-softmax, RAS trial loop) and the next step's embedding + row advance.

@@ -8,8 +8,10 @@ namespace vh {
 // GEMV prologues; PRO_Q (int path only): the input rows arrive already quantized (k_quant_rows)
 enum { PRO_X = 0, PRO_RMS = 1, PRO_ATTN = 2, PRO_Q = 3 };
 enum { EPI_STORE = 0, EPI_ACC = 1, EPI_SWIGLU = 2 };
-// GEMM-only epilogues (F5 DiT): y += gate * c; y = gelu_tanh(c); y = mish(c); y += mish(c); RoPE on q|k columns
-enum { EPI_GATED_ACC = 3, EPI_GELU = 4, EPI_MISH = 5, EPI_MISH_ACC = 6, EPI_ROPE = 7, EPI_ROPE_H16 = 8, EPI_GELU_H16 = 9 };
+// GEMM-only epilogues (F5 DiT, Vocos): y += gate * c; y = gelu_tanh(c); y = mish(c); y += mish(c); RoPE on q|k
+// columns; y = gelu_erf(c)
+enum { EPI_GATED_ACC = 3, EPI_GELU = 4, EPI_MISH = 5, EPI_MISH_ACC = 6, EPI_ROPE = 7, EPI_ROPE_H16 = 8, EPI_GELU_H16 = 9,
+       EPI_GELU_ERF = 10 };
 // GEMM A operand: rows of a matrix, or the implicit im2col rows of a grouped "same" Conv1d
 enum { ASRC_ROWS = 0, ASRC_CONV = 1 };
 // Weight formats of the GEMV kernels: the reference's types, plus Q4 with f16 block scales (WT_Q4H), the

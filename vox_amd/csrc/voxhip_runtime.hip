@@ -1613,8 +1613,13 @@ struct F5Block {
     int ada = -1, qkv = -1, o = -1, ff1 = -1, ff2 = -1;  // q | k | v stacked at create
 };
 struct F5Conv {
-    float *w = nullptr, *b = nullptr;
-    int cin = 0, cout = 0, K = 0, groups = 0;
+    float *w = nullptr, *b = nullptr;  // w [groups][cout/groups][kpad] (K * cin/groups, zero-padded to a multiple of 8)
+    int cin = 0, cout = 0, K = 0, groups = 0, kpad = 0;
+};
+struct F5VBlock {  // a Vocos ConvNeXt block (f5.cpp:235-240)
+    F5Conv dw;     // depthwise, w [C][K]
+    float *ln_w = nullptr, *ln_b = nullptr, *gamma = nullptr;
+    int pw1 = -1, pw2 = -1;
 };
 struct F5 {
     int dim = 0, depth = 0, heads = 0, hd = 0, ff = 0, mel = 0, text = 0, pe = 0;
@@ -1624,6 +1629,13 @@ struct F5 {
     // every block linear F16 and dim, inner, ff multiples of 64: the block's activations travel between kernels as
     // f16 halves (hi, lo planes) and the linears take k_gemm_hh; otherwise f32 rows and k_gemm_h16 / k_gemm_f32
     bool split = false;
+    // Vocos (vdim 0: none): embed conv, norms, blocks, head; buffers of the last vocode length vT
+    int vdim = 0, vinter = 0, vout = 0, v_head = -1;
+    F5Conv v_embed;
+    float *v_ln_w = nullptr, *v_ln_b = nullptr, *v_fln_w = nullptr, *v_fln_b = nullptr;
+    std::vector<F5VBlock> vblocks;
+    int vT = 0;
+    float *vm = nullptr, *vx = nullptr, *vy = nullptr, *vh = nullptr, *vhead = nullptr;
     // step buffers of begin(B, N): rows R = B N
     int B = 0, N = 0;
     float *cat = nullptr, *h = nullptr, *a = nullptr, *nrm = nullptr, *at = nullptr, *ffb = nullptr;
@@ -1669,21 +1681,49 @@ int stack_rows(const std::vector<int> &ids) {
     return nid;
 }
 
-F5Conv upload_conv(const voxhip_f5_conv &c, int dim) {
-    if (!c.w || c.cin != dim || c.cout != dim || c.K <= 0 || c.K % 2 == 0 || c.groups <= 0 || c.cin % c.groups ||
-        c.cout % c.groups)
-        throw Fail("F5 position convolution: cin = cout = dim, odd K, groups dividing the channels");
-    const int cig = c.cin / c.groups;
-    if (cig % 4 || (int64_t(c.K) * cig) % 8) throw Fail("F5 position convolution: cin/groups must be a multiple of 4");
+// A "same" Conv1d for the implicit-im2col GEMM: Conv1d::w rows [K][cin/groups] (f5_ops.cpp:86-104) padded with zero
+// weights to a multiple of 8 (the GEMM's K step), which the A loader meets with zeros.
+F5Conv upload_conv_gemm(const voxhip_f5_conv &c, const char *what) {
+    if (!c.w || c.cin <= 0 || c.cout <= 0 || c.K <= 0 || c.K % 2 == 0 || c.groups <= 0 || c.cin % c.groups || c.cout % c.groups)
+        throw Fail(std::string(what) + ": odd K, groups dividing the channels");
+    const int cig = c.cin / c.groups, cog = c.cout / c.groups;
+    if (cig % 4) throw Fail(std::string(what) + ": cin/groups must be a multiple of 4");
     F5Conv d;
     d.cin = c.cin; d.cout = c.cout; d.K = c.K; d.groups = c.groups;
-    const size_t n = size_t(c.cout) * size_t(c.K) * size_t(cig);
-    d.w = dalloc_t<float>(n);
-    h2d(d.w, c.w, n * 4);
+    const int64_t kc = int64_t(c.K) * cig;
+    d.kpad = int((kc + 7) / 8 * 8);
+    std::vector<float> w(size_t(c.cout) * size_t(d.kpad), 0.f);
+    for (int64_t r = 0; r < int64_t(c.groups) * cog; ++r) std::memcpy(&w[size_t(r * d.kpad)], c.w + r * kc, size_t(kc) * 4);
+    d.w = dalloc_t<float>(w.size());
+    h2d(d.w, w.data(), w.size() * 4);
     if (c.b) {
         d.b = dalloc_t<float>(size_t(c.cout));
         h2d(d.b, c.b, size_t(c.cout) * 4);
     }
+    return d;
+}
+F5Conv upload_conv(const voxhip_f5_conv &c, int dim) {
+    if (c.cin != dim || c.cout != dim) throw Fail("F5 position convolution: cin = cout = dim");
+    return upload_conv_gemm(c, "F5 position convolution");
+}
+// A depthwise "same" Conv1d (groups = cin = cout = dim): w [C][K].
+F5Conv upload_dwconv(const voxhip_f5_conv &c, int dim) {
+    if (!c.w || c.cin != dim || c.cout != dim || c.groups != dim || c.K <= 0 || c.K % 2 == 0)
+        throw Fail("Vocos depthwise convolution: cin = cout = groups = vocos_dim, odd K");
+    F5Conv d;
+    d.cin = c.cin; d.cout = c.cout; d.K = c.K; d.groups = c.groups; d.kpad = c.K;
+    d.w = dalloc_t<float>(size_t(dim) * size_t(c.K));
+    h2d(d.w, c.w, size_t(dim) * size_t(c.K) * 4);
+    if (c.b) {
+        d.b = dalloc_t<float>(size_t(dim));
+        h2d(d.b, c.b, size_t(dim) * 4);
+    }
+    return d;
+}
+float *upload_vec(const float *v, int n, const char *what) {
+    if (!v) throw Fail(std::string("missing ") + what);
+    float *d = dalloc_t<float>(size_t(n));
+    h2d(d, v, size_t(n) * 4);
     return d;
 }
 
@@ -1734,7 +1774,7 @@ void f5_enqueue(F5 &F, hipStream_t s) {
         const F5Conv &cv = c == 0 ? F.pos1 : F.pos2;
         GemmArgs ga{};
         ga.bias = cv.b; ga.y = c == 0 ? F.a : F.h; ga.lda = D; ga.ldy = D; ga.m = int32_t(R);
-        ga.n = cv.cout / cv.groups; ga.cig = cv.cin / cv.groups; ga.ksize = cv.K; ga.K = cv.K * ga.cig; ga.seq = F.N;
+        ga.n = cv.cout / cv.groups; ga.cig = cv.cin / cv.groups; ga.ksize = cv.K; ga.K = cv.kpad; ga.seq = F.N;
         HIPCHECK(launch_conv_gemm(c == 0 ? EPI_MISH : EPI_MISH_ACC, cv.w, c == 0 ? F.h : F.a, ga, cv.groups, s));
     }
     const float scale = 1.0f / std::sqrt(float(F.hd));
@@ -1804,6 +1844,31 @@ int voxhip_f5_create(const voxhip_f5_desc *d) {
             for (int id : {fb.qkv, fb.o, fb.ff1, fb.ff2}) F->split = F->split && mat_at(id).type == VOXHIP_F16;
         F->pos1 = upload_conv(d->pos1, D);
         F->pos2 = upload_conv(d->pos2, D);
+        if (d->vocos_dim > 0) {  // Vocos (f5.cpp:333-346): the linears are matrix handles, the rest host arrays
+            const int VD = d->vocos_dim, VI = d->vocos_inter, VO = d->vocos_out;
+            if (VD % 4 || VI <= 0 || VO <= 0 || d->n_vblocks < 0 || (d->n_vblocks > 0 && !d->v_blocks))
+                throw Fail("bad Vocos dimensions (vocos_dim a multiple of 4)");
+            check(d->v_head, VO, VD, "Vocos head");
+            if (d->v_embed.cin != d->mel_dim || d->v_embed.cout != VD) throw Fail("Vocos embed: mel_dim -> vocos_dim");
+            F->v_embed = upload_conv_gemm(d->v_embed, "Vocos embed");
+            F->v_ln_w = upload_vec(d->v_ln_w, VD, "Vocos norm weight");
+            F->v_ln_b = d->v_ln_b ? upload_vec(d->v_ln_b, VD, "Vocos norm bias") : nullptr;
+            F->v_fln_w = upload_vec(d->v_fln_w, VD, "Vocos final norm weight");
+            F->v_fln_b = d->v_fln_b ? upload_vec(d->v_fln_b, VD, "Vocos final norm bias") : nullptr;
+            for (int i = 0; i < d->n_vblocks; ++i) {
+                const voxhip_f5_vblock &b = d->v_blocks[i];
+                check(b.pw1, VI, VD, "Vocos pwconv1");
+                check(b.pw2, VD, VI, "Vocos pwconv2");
+                F5VBlock vb;
+                vb.dw = upload_dwconv(b.dw, VD);
+                vb.ln_w = upload_vec(b.ln_w, VD, "Vocos block norm weight");
+                vb.ln_b = b.ln_b ? upload_vec(b.ln_b, VD, "Vocos block norm bias") : nullptr;
+                vb.gamma = upload_vec(b.gamma, VD, "Vocos gamma");
+                vb.pw1 = b.pw1; vb.pw2 = b.pw2;
+                F->vblocks.push_back(vb);
+            }
+            F->vdim = VD; F->vinter = VI; F->vout = VO; F->v_head = d->v_head;
+        }
         g.f5.push_back(F.release());
         return int(g.f5.size()) - 1;
     }, -1);
@@ -1852,6 +1917,57 @@ int voxhip_f5_step(int id, const float *x, const float *ts, float *out) {
         f5_enqueue(F, g.stream);
         HIPCHECK(hipStreamSynchronize(g.stream));
         HIPCHECK(hipMemcpy(out, F.out, size_t(F.B) * F.N * F.mel * 4, hipMemcpyDeviceToHost));
+        return 1;
+    }, 0);
+}
+
+// F5Model::vocode up to the head (f5.cpp:792-806; gpu_f5.cpp:334-373): embed conv, LayerNorm, the ConvNeXt blocks
+// (depthwise conv, LayerNorm, pwconv1 + GELU-erf, pwconv2 with x += gamma * (.)), final LayerNorm, head.
+int voxhip_f5_vocos(int id, const float *mel, int T, float *head) {
+    return guard_int([&] {
+        require_ok();
+        F5 &F = f5_at(id);
+        if (!F.vdim) throw Fail("this F5 model has no Vocos on the device");
+        if (!mel || !head || T <= 0 || int64_t(T) * std::max(F.vinter, F.vout) > INT32_MAX / 2) throw Fail("bad Vocos input");
+        const int VD = F.vdim;
+        if (F.vT < T) {
+            HIPCHECK(hipStreamSynchronize(g.stream));
+            for (float *p : {F.vm, F.vx, F.vy, F.vh, F.vhead}) dfree(p);
+            F.vm = dalloc_t<float>(size_t(T) * F.mel); F.vx = dalloc_t<float>(size_t(T) * VD); F.vy = dalloc_t<float>(size_t(T) * VD);
+            F.vh = dalloc_t<float>(size_t(T) * F.vinter); F.vhead = dalloc_t<float>(size_t(T) * F.vout);
+            F.vT = T;
+        }
+        hipStream_t s = g.stream;
+        h2d(F.vm, mel, size_t(T) * F.mel * 4);
+        const F5Conv &ce = F.v_embed;
+        GemmArgs ge{};
+        ge.bias = ce.b; ge.y = F.vx; ge.lda = ce.cin; ge.ldy = VD; ge.m = T; ge.n = ce.cout / ce.groups;
+        ge.cig = ce.cin / ce.groups; ge.ksize = ce.K; ge.K = ce.kpad; ge.seq = T;
+        HIPCHECK(launch_conv_gemm(EPI_STORE, ce.w, F.vm, ge, ce.groups, s));
+        HIPCHECK(launch_layernorm_rows(F.vx, T, VD, F.v_ln_w, F.v_ln_b, F.vx, s));
+        for (const F5VBlock &b : F.vblocks) {
+            HIPCHECK(launch_dwconv(F.vx, b.dw.w, b.dw.b, F.vy, T, VD, b.dw.K, T, s));
+            HIPCHECK(launch_layernorm_rows(F.vy, T, VD, b.ln_w, b.ln_b, F.vy, s));
+            const GpuMat &M1 = mat_at(b.pw1), &M2 = mat_at(b.pw2);
+            f5_gemm(M1, EPI_GELU_ERF, F.vy, gemm_args(M1, M1.b, F.vh, VD, F.vinter, T), s);
+            GemmArgs g2 = gemm_args(M2, M2.b, F.vx, F.vinter, VD, T);
+            g2.gate = b.gamma;
+            f5_gemm(M2, EPI_GATED_ACC, F.vh, g2, s);
+        }
+        HIPCHECK(launch_layernorm_rows(F.vx, T, VD, F.v_fln_w, F.v_fln_b, F.vx, s));
+        const GpuMat &Mh = mat_at(F.v_head);
+        f5_gemm(Mh, EPI_STORE, F.vx, gemm_args(Mh, Mh.b, F.vhead, VD, F.vout, T), s);
+        HIPCHECK(hipStreamSynchronize(s));
+        HIPCHECK(hipMemcpy(head, F.vhead, size_t(T) * F.vout * 4, hipMemcpyDeviceToHost));
+        return 1;
+    }, 0);
+}
+
+int voxhip_f5_vocos_out(int id, int32_t *vout) {
+    return guard_int([&] {
+        require_ok();
+        if (!vout) throw Fail("missing argument");
+        *vout = f5_at(id).vout;
         return 1;
     }, 0);
 }

@@ -127,12 +127,15 @@ class Decoder:
 # text 512 (in_proj 712 -> 1024), position convolutions K 31 / 16 groups (f32); f16 linear weights ~N(0, 0.02)
 F5_DIT = dict(dim=1024, depth=22, heads=16, dim_head=64, ff_mult=2, mel=100, text=512, K=31, groups=16, pe_attn_head=0,
               wtype=vh.F16, frames=1000)
+# F5-TTS's Vocos (mel 100, dim 512, intermediate 1536, 8 ConvNeXt blocks, head 2 x (n_fft 1024 / 2 + 1)); 938 frames
+# of hop 256 at 24 kHz are 10 s of audio
+F5_VOCOS = dict(dim=512, inter=1536, layers=8, out=1026, frames=938)
 
 
 class DiT:
     """A device-resident F5 DiT with synthetic weights (linears generated on the device, convolutions on the host)."""
 
-    def __init__(self, cfg, seed=0):
+    def __init__(self, cfg, seed=0, vocos=None):
         c = dict(cfg)
         self.cfg = c
         D, H, HD, FF, mel, text = c["dim"], c["heads"], c["dim_head"], c["dim"] * c["ff_mult"], c["mel"], c["text"]
@@ -149,8 +152,31 @@ class DiT:
         G, K = c["groups"], c["K"]
         self.pos = [((rng.standard_normal((G, D // G, K, D // G)) * 0.02).astype(np.float32),
                      (rng.standard_normal(D) * 0.02).astype(np.float32), D, D, K, G) for _ in range(2)]
+        self.vocos = None
+        vk = {}
+        if vocos:  # the vocoder's linears on the device, its convolutions and norms from the host
+            v = dict(vocos)
+            VD, VI = v["dim"], v["inter"]
+            vec = lambda n, m, sd: (m + sd * rng.standard_normal(n)).astype(np.float32)
+            self.vocos = v
+            self.vmats = [mat(VI, VD) if i % 2 == 0 else mat(VD, VI) for i in range(2 * v["layers"])] + [mat(v["out"], VD)]
+            vk = dict(vocos=dict(dim=VD, inter=VI, out=v["out"],
+                                 embed=((rng.standard_normal((1, VD, 7, mel)) * 0.02).astype(np.float32), vec(VD, 0, 0.02),
+                                        mel, VD, 7, 1),
+                                 ln_w=vec(VD, 1, 0.02), ln_b=vec(VD, 0, 0.02), fln_w=vec(VD, 1, 0.02), fln_b=vec(VD, 0, 0.02),
+                                 head=self.vmats[-1],
+                                 blocks=[dict(dw=((rng.standard_normal((VD, 7)) * 0.1).astype(np.float32), vec(VD, 0, 0.02),
+                                                  VD, VD, 7, VD),
+                                              ln_w=vec(VD, 1, 0.02), ln_b=vec(VD, 0, 0.02), gamma=vec(VD, 0, 0.1),
+                                              pw1=self.vmats[2 * i], pw2=self.vmats[2 * i + 1]) for i in range(v["layers"])]))
         self.f5 = vh.f5_create(D, c["depth"], H, HD, c["ff_mult"], mel, text, c["pe_attn_head"], self.in_proj, self.norm_out,
-                               self.proj_out, self.blocks, self.pos[0], self.pos[1])
+                               self.proj_out, self.blocks, self.pos[0], self.pos[1], **vk)
+
+    def vocos_flops(self, T):
+        """FLOPs of the Vocos backbone and head for T frames (2 per multiply-add)."""
+        v, mel = self.vocos, self.cfg["mel"]
+        VD, VI = v["dim"], v["inter"]
+        return 2 * T * (VD * 7 * mel + v["layers"] * (VD * 7 + 2 * VD * VI) + v["out"] * VD)
 
     def flops(self, B, N):
         """FLOPs of one step (2 per multiply-add): linears, attention, position convolutions, ada / final GEMVs."""

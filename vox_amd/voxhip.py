@@ -79,10 +79,18 @@ class F5Block(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("ada", "q", "k", "v", "o", "ff1", "ff2")]
 
 
+class F5VBlock(C.Structure):
+    _fields_ = [("dw", F5Conv), ("ln_w", C.c_void_p), ("ln_b", C.c_void_p), ("gamma", C.c_void_p), ("pw1", C.c_int32),
+                ("pw2", C.c_int32)]
+
+
 class F5Desc(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("dim", "depth", "heads", "dim_head", "ff_mult", "mel_dim", "text_dim",
                                          "pe_attn_head", "in_proj", "norm_out", "proj_out")] + \
-               [("blocks", C.POINTER(F5Block)), ("pos1", F5Conv), ("pos2", F5Conv)]
+               [("blocks", C.POINTER(F5Block)), ("pos1", F5Conv), ("pos2", F5Conv)] + \
+               [(n, C.c_int32) for n in ("vocos_dim", "vocos_inter", "vocos_out")] + [("v_embed", F5Conv)] + \
+               [(n, C.c_void_p) for n in ("v_ln_w", "v_ln_b", "v_fln_w", "v_fln_b")] + \
+               [("v_blocks", C.POINTER(F5VBlock)), ("n_vblocks", C.c_int32), ("v_head", C.c_int32)]
 
 
 KERNEL_CLASSES = ("qkv_gemv", "o_gemv", "gateup_gemv", "down_gemv", "head_gemv", "attention", "attn_combine", "qk_post", "sampler")
@@ -133,6 +141,8 @@ SIGNATURES = {
     "voxhip_f5_begin": (_I, [_I, _I, _I, _P, _P]),
     "voxhip_f5_step": (_I, [_I, _P, _P, _P]),
     "voxhip_f5_end": (_I, [_I]),
+    "voxhip_f5_vocos": (_I, [_I, _P, _I, _P]),
+    "voxhip_f5_vocos_out": (_I, [_I, _P]),
     "voxhip_lm_sample_dev": (_I, [_P, C.c_int32, C.POINTER(LmCfg), _I64, _P, C.c_int32, _P, _P]),
     "voxhip_lm_generate": (_I, [_I, _I, _P, _I64, _I, _I, C.POINTER(LmCfg), _P, _P, _P]),
     "voxhip_pred_frame": (_I, [_I, _I, _P, _I, _P, _I, _P, _I, C.POINTER(SampleCfg), _P]),
@@ -477,19 +487,47 @@ def pred_frame(xfmr, seq, in2, in_proj, heads, embs, cfg):
 
 
 def f5_create(dim, depth, heads, dim_head, ff_mult, mel_dim, text_dim, pe_attn_head, in_proj, norm_out, proj_out, blocks,
-              pos1, pos2):
+              pos1, pos2, vocos=None):
     """gpu_f5_create: blocks = list of dicts ada,q,k,v,o,ff1,ff2 -> matrix handles; pos1/pos2 = (w [groups][cout/groups]
-    [K][cin/groups] f32, bias or None, cin, cout, K, groups)."""
+    [K][cin/groups] f32, bias or None, cin, cout, K, groups). vocos: dict dim, inter, out, embed (a conv tuple), ln_w,
+    ln_b, fln_w, fln_b (arrays), head (handle), blocks = list of dicts dw (conv tuple, w [C][K]), ln_w, ln_b, gamma,
+    pw1, pw2 (handles)."""
     arr = (F5Block * len(blocks))(*[F5Block(*[b[n] for n in ("ada", "q", "k", "v", "o", "ff1", "ff2")]) for b in blocks])
-    convs, keep = [], []
-    for w, b, cin, cout, K, groups in (pos1, pos2):
+    keep = []
+
+    def conv(c):
+        w, b, cin, cout, K, groups = c
         w = f32(w)
         b = None if b is None else f32(b)
-        keep += [w, b]
-        convs.append(F5Conv(_p(w), _p(b), cin, cout, K, groups))
+        keep.extend([w, b])
+        return F5Conv(_p(w), _p(b), cin, cout, K, groups)
+
+    def vec(a):
+        a = None if a is None else f32(a)
+        keep.append(a)
+        return _p(a)
     d = F5Desc(dim, depth, heads, dim_head, ff_mult, mel_dim, text_dim, pe_attn_head, in_proj, norm_out, proj_out, arr,
-               convs[0], convs[1])
+               conv(pos1), conv(pos2))
+    if vocos:
+        vb = (F5VBlock * max(1, len(vocos["blocks"])))()
+        for i, b in enumerate(vocos["blocks"]):
+            vb[i] = F5VBlock(conv(b["dw"]), vec(b["ln_w"]), vec(b["ln_b"]), vec(b["gamma"]), b["pw1"], b["pw2"])
+        keep.append(vb)
+        d.vocos_dim, d.vocos_inter, d.vocos_out = vocos["dim"], vocos["inter"], vocos["out"]
+        d.v_embed = conv(vocos["embed"])
+        d.v_ln_w, d.v_ln_b, d.v_fln_w, d.v_fln_b = (vec(vocos[n]) for n in ("ln_w", "ln_b", "fln_w", "fln_b"))
+        d.v_blocks, d.n_vblocks, d.v_head = vb, len(vocos["blocks"]), vocos["head"]
     return _handle(lib().voxhip_f5_create(C.byref(d)), "f5_create")
+
+
+def f5_vocos(f5, mel):
+    """gpu_f5_vocos: mel [T][mel_dim] -> the Vocos head output [T][vocos_out]."""
+    mel = f32(mel)
+    vout = C.c_int32()
+    _check(lib().voxhip_f5_vocos_out(f5, C.byref(vout)), "f5_vocos_out")
+    out = np.empty((mel.shape[0], vout.value), np.float32)
+    _check(lib().voxhip_f5_vocos(f5, _p(mel), mel.shape[0], _p(out)), "f5_vocos")
+    return out
 
 
 def f5_begin(f5, B, N, cat0, rope):
