@@ -247,6 +247,37 @@ def bench_vocos(vh, synth, reps=5):
             "audio_s_per_s": round(T * 256 / 24000 / (ms * 1e-3), 1)}
 
 
+def bench_cosy(vh, synth, reps=5):
+    """CosyVoice2's flow estimator (gpu_cosy_step; cosyvoice.cpp:822-863): one Euler step = the conditional and the
+    unconditional pass over 512 mel frames (the 256 speech tokens of configs[4]), f16 linears, f32 causal
+    convolutions. Host wall-clock per step (median), the x / time-bias upload and the [2][512][80] download included."""
+    c = synth.COSY_FLOW
+    flow = synth.CosyFlow(c, seed=0)
+    T, M, C = c["frames"], c["M"], c["C"]
+    rng = np.random.default_rng(4)
+    in0 = np.zeros((2 * T, 4 * M), np.float32)
+    in0[:T, M:] = rng.standard_normal((T, 3 * M)).astype(np.float32)
+    vh.cosy_begin(flow.est, T, in0)
+    x = rng.standard_normal((T, M)).astype(np.float32)
+    tb = (rng.standard_normal((2 + c["n_mid"], C)) * 0.1).astype(np.float32)
+    vh.cosy_step(flow.est, x, tb, T, M)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        out = vh.cosy_step(flow.est, x, tb, T, M)
+        times.append((time.perf_counter() - t0) * 1000.0)
+    vh.cosy_end(flow.est)
+    for h in flow.mats:
+        vh.mat_free(h)
+    assert np.isfinite(out).all()
+    ms = float(np.median(times))
+    fl = flow.flops(T)
+    return {"workload": "cosyvoice2 flow estimator step (gpu_cosy_step): 2 x 512 frames, 256 ch, 14 causal resnets, "
+                        "56 transformer blocks (8 x 64 heads, FFN 1024), f16 linears",
+            "ms_per_step": round(ms, 3), "gflop": round(fl / 1e9, 2), "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
+            "flow_ms_10_steps": round(10 * ms, 2)}
+
+
 def bench_pred(vh, synth, frames=20):
     """The code predictor's frame on the device (gpu_pred_frame; the loop engine.cpp:676-683 runs on the CPU in the
     reference when the device does not provide it): 15 passes of the 5-layer q8 predictor (2 rows at positions 0-1,
@@ -302,7 +333,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-other", action="store_true",
                     help="skip the configs[0] / [2] / [3] / [4] and code-predictor measurements")
-    ap.add_argument("--only", choices=["configs[0]", "configs[2]", "configs[3]", "configs[4]", "pred_frame", "f5_vocos"],
+    ap.add_argument("--only", choices=["configs[0]", "configs[2]", "configs[3]", "configs[4]", "pred_frame", "f5_vocos",
+                                       "cosy_flow"],
                     help="run one of the other BASELINE configurations (or the code-predictor frame) alone and print "
                          "its JSON object (for profiling)")
     ap.add_argument("--no-breakdown", action="store_true",
@@ -321,7 +353,8 @@ def main():
     if args.only:
         legs = {"configs[0]": lambda: bench_cfg1(vh), "configs[2]": lambda: bench_cfg3(vh, synth, 100, 10),
                 "configs[3]": lambda: bench_cfg4(vh, synth), "configs[4]": lambda: bench_cfg5(vh, synth),
-                "pred_frame": lambda: bench_pred(vh, synth), "f5_vocos": lambda: bench_vocos(vh, synth)}
+                "pred_frame": lambda: bench_pred(vh, synth), "f5_vocos": lambda: bench_vocos(vh, synth),
+                "cosy_flow": lambda: bench_cosy(vh, synth)}
         print(json.dumps({args.only: legs[args.only]()}))
         return
     t0 = time.perf_counter()
@@ -387,7 +420,8 @@ def main():
         t0 = time.perf_counter()
         other = {"configs[0]": bench_cfg1(vh), "configs[2]": bench_cfg3(vh, synth, 100, 10),
                  "configs[3]": bench_cfg4(vh, synth), "configs[4]": bench_cfg5(vh, synth),
-                 "pred_frame": bench_pred(vh, synth), "f5_vocos": bench_vocos(vh, synth)}
+                 "pred_frame": bench_pred(vh, synth), "f5_vocos": bench_vocos(vh, synth),
+                 "cosy_flow": bench_cosy(vh, synth)}
         log(f"other configs: {json.dumps(other)} ({time.perf_counter() - t0:.1f} s)")
 
     cpu = None

@@ -232,8 +232,7 @@ int voxhip_lm_generate(int xfmr, int seq, const float *x, int64_t n, int head, i
                        int32_t *tokens, float *logp, int32_t *n_tokens);
 
 /* ---------------------------------------------------------------- F5-TTS DiT step (gpu.hpp:62-91)
- * The whole dit_forward (f5.cpp:586-725) of a sampling step on the device. Vocos stays on the CPU
- * (gpu_f5_vocos returns false, which f5.cpp:787-791 answers with the CPU vocoder). */
+ * The whole dit_forward (f5.cpp:586-725) of a sampling step on the device, and Vocos up to its head. */
 /* GpuF5Conv (gpu.hpp:66): f32 weights in Conv1d::w layout [groups][cout/groups][K][cin/groups], bias [cout] or NULL.
  * The position convolutions need cin = cout = dim, odd K and cin/groups a multiple of 4. */
 typedef struct voxhip_f5_conv {
@@ -278,6 +277,45 @@ int voxhip_f5_vocos(int id, const float *mel, int T, float *head);
 /* The Vocos head width of an F5 handle into *vout (0 when created without Vocos). Returns 1, or 0 for a bad handle.
  * No counterpart in gpu.hpp: gpu_hip.cpp sizes gpu_f5_vocos's output with it. */
 int voxhip_f5_vocos_out(int id, int32_t *vout);
+
+/* ---------------------------------------------------------------- CosyVoice2 / Chatterbox flow estimator
+ * (gpu.hpp:100-119; the CPU estimator cosyvoice.cpp:126-221, :822-863). One Euler step runs the conditional and the
+ * unconditional pass together as sequences 0 and 1 of T rows each (rows R = 2 T). Convolutions are f32 in
+ * Conv1d::w layout [cout][K][cin] (groups 1), causal (left zero padding K - 1 per sequence) for the K-3 block and
+ * level convolutions, K 1 for res and final_proj; linears are matrix handles (q, k, v without bias). */
+/* GpuCosyDesc::Res (gpu.hpp:105): CausalResnetBlock1D, c1 (cin -> C), c2 (C -> C), res (cin -> C, K 1), the two
+ * LayerNorms (weight, bias [C]). */
+typedef struct voxhip_cosy_res {
+    voxhip_f5_conv c1, c2, res;
+    const float *n1w, *n1b, *n2w, *n2b;
+} voxhip_cosy_res;
+/* GpuCosyDesc::X (gpu.hpp:106): a BasicTransformerBlock, norms [C] and matrix handles (q, k, v: inner x C; o:
+ * C x inner; ff1: ff_dim x C; ff2: C x ff_dim). */
+typedef struct voxhip_cosy_x {
+    const float *n1w, *n1b, *n3w, *n3b;
+    int32_t q, k, v, o, ff1, ff2, ff_dim;
+} voxhip_cosy_x;
+/* GpuCosyDesc (gpu.hpp:103-113). The reference's vector of mid transformer lists is flattened: mid block i owns
+ * mid_x_count[i] consecutive entries of mid_x. head_dim must be 64, C a multiple of 4. */
+typedef struct voxhip_cosy_desc {
+    int32_t M, C, heads, head_dim;
+    voxhip_cosy_res down_res, up_res;
+    const voxhip_cosy_res *mid_res; /* [n_mid] */
+    int32_t n_mid;
+    const voxhip_cosy_x *down_x, *up_x, *mid_x;
+    int32_t n_down_x, n_up_x;
+    const int32_t *mid_x_count; /* [n_mid] */
+    voxhip_f5_conv down_conv, up_out, final_conv, final_proj;
+    const float *fn_w, *fn_b;
+} voxhip_cosy_desc;
+int voxhip_cosy_create(const voxhip_cosy_desc *d); /* gpu_cosy_create (gpu.hpp:114): a handle or -1 */
+/* gpu_cosy_begin (gpu.hpp:116): in0 [2][T][4 M], the estimator input [x | mu | spks | cond] of both passes with the
+ * x columns left zero. */
+int voxhip_cosy_begin(int id, int T, const float *in0);
+/* gpu_cosy_step (gpu.hpp:118): x [T][M] (the same for both passes), tb [2 + n_mid][C] the time-embedding bias of
+ * every resnet (down, mid..., up) -> out [2][T][M]. */
+int voxhip_cosy_step(int id, const float *x, const float *tb, float *out);
+int voxhip_cosy_end(int id); /* gpu_cosy_end (gpu.hpp:119): frees the step buffers, keeps the weights */
 
 /* Synthetic weights and caches, generated on the device (Philox4x32-10 Box-Muller, mean + std * z).
  * voxhip_mat_synthetic: f32 values, then quantized on the device to `type` with the reference's

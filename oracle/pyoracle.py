@@ -65,6 +65,24 @@ class VoVocos(C.Structure):
                [("blocks", C.POINTER(VoVocosBlock)), ("head", VoMat)]
 
 
+class VoCosyRes(C.Structure):
+    _fields_ = [("c1", VoConv), ("c2", VoConv), ("res", VoConv)] + [(n, C.c_void_p) for n in ("n1w", "n1b", "n2w", "n2b")]
+
+
+class VoCosyX(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("n1w", "n1b", "n3w", "n3b")] + \
+               [(n, VoMat) for n in ("q", "k", "v", "o", "ff1", "ff2")]
+
+
+class VoCosy(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("M", "C", "heads", "head_dim")] + \
+               [("down_res", VoCosyRes), ("up_res", VoCosyRes), ("mid_res", C.POINTER(VoCosyRes)), ("n_mid", C.c_int32),
+                ("down_x", C.POINTER(VoCosyX)), ("up_x", C.POINTER(VoCosyX)), ("mid_x", C.POINTER(VoCosyX)),
+                ("n_down_x", C.c_int32), ("n_up_x", C.c_int32), ("mid_x_count", C.c_void_p)] + \
+               [(n, VoConv) for n in ("down_conv", "up_out", "final_conv", "final_proj")] + \
+               [("fn_w", C.c_void_p), ("fn_b", C.c_void_p)]
+
+
 def _p(a):
     return None if a is None else a.ctypes.data
 
@@ -98,6 +116,14 @@ def _declare(lib, prefix):
             "f5_modulate": (None, [P, I64, I32, P, P, P]),
             "f5_step": (C.c_int, [P, I32, I32, P, P, P, P]),
             "vocos_head": (C.c_int, [P, P, I32, P]),
+            "exp_poly": (F, [F]),
+            "gelu_poly": (F, [F]),
+            "mish_nn": (F, [F]),
+            "layer_norm_nn": (None, [P, I64, I32, P, P, F]),
+            "softmax_fast": (None, [P, I64]),
+            "attention_nn": (None, [P, P, P, I32, I32, I32, I32, F, P]),
+            "causal_conv": (None, [P, P, I32, P]),
+            "cosy_step": (C.c_int, [P, I32, P, P, P]),
             "lm_step": (I32, [P, I32, P, I32, I64, I32, I32, F, I32, I32, F, U64, U32]),
             "noise": (None, [U64, U32, C.c_size_t, P]),
             "f16_to_f32": (F, [C.c_uint16]),
@@ -122,6 +148,12 @@ def _declare(lib, prefix):
             "session_new": (P, [P, P, P]),
             "session_step": (C.c_int, [P, P, P, F, I32, F, P]),
             "session_free": (None, [P]),
+            "gelu_inplace": (None, [P, I64]),
+            "mish_nn": (F, [F]),
+            "layer_norm_nn": (None, [P, I32, I32, P, P, F]),
+            "attention_nn": (None, [P, P, P, I32, I32, I32, I32, F, P]),
+            "causal_conv": (None, [P, P, I32, P]),
+            "cosy_step": (C.c_int, [P, I32, P, P, P]),
         })
     for name, (res, args) in sig.items():
         fn = getattr(lib, prefix + name)
@@ -402,4 +434,88 @@ def transformer_forward_steps(X, kvs, x, use_ref=False):
     rc = fn(C.byref(X.c), ptrs, B, _p(x), _p(out))
     if rc != 0:
         raise RuntimeError(f"transformer_forward_steps failed ({rc})")
+    return out
+
+
+# ---- the CosyVoice2 / Chatterbox flow estimator (cosyvoice.cpp:126-221, :839-863)
+def gelu_poly(x, use_ref=False):
+    """nn.cpp's GELU on an array: the oracle's scalar restatement, or the reference's gelu_inplace."""
+    x = np.array(x, np.float32, copy=True).ravel()
+    if use_ref:
+        ref().ref_gelu_inplace(_p(x), x.size)
+        return x
+    return np.array([lib().vo_gelu_poly(float(v)) for v in x], np.float32)
+
+
+def mish_nn(x, use_ref=False):
+    return (ref().ref_mish_nn if use_ref else lib().vo_mish_nn)(x)
+
+
+def layer_norm_nn(x, w, b, eps, use_ref=False):
+    y = np.array(x, np.float32, copy=True)
+    f = np.ascontiguousarray
+    (ref().ref_layer_norm_nn if use_ref else lib().vo_layer_norm_nn)(_p(y), y.shape[0], y.shape[1], _p(f(w, np.float32)),
+                                                                     _p(None if b is None else f(b, np.float32)), eps)
+    return y
+
+
+def attention_nn(q, k, v, H, dh, scale, use_ref=False):
+    q, k, v = (np.ascontiguousarray(a, np.float32) for a in (q, k, v))
+    out = np.empty_like(q)
+    (ref().ref_attention_nn if use_ref else lib().vo_attention_nn)(_p(q), _p(k), _p(v), q.shape[0], k.shape[0], H, dh,
+                                                                   scale, _p(out))
+    return out
+
+
+def causal_conv(cv, x, use_ref=False):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty((x.shape[0], cv.cout), np.float32)
+    (ref().ref_causal_conv if use_ref else lib().vo_causal_conv)(C.byref(cv.c), _p(x), x.shape[0], _p(y))
+    return y
+
+
+class Cosy:
+    """The estimator in the oracle's struct layout. res: dict c1, c2, res (Conv), n1w, n1b, n2w, n2b; x: dict n1w,
+    n1b, n3w, n3b, q, k, v, o, ff1, ff2 (Mat); mid_x: a list per mid block."""
+
+    def __init__(self, M, C_, heads, head_dim, down_res, up_res, mid_res, down_x, up_x, mid_x, down_conv, up_out,
+                 final_conv, final_proj, fn_w, fn_b):
+        f = lambda a: np.ascontiguousarray(a, np.float32)
+        self.keep = []
+
+        def res(r):
+            v = [f(r[n]) for n in ("n1w", "n1b", "n2w", "n2b")]
+            self.keep += [r, v]
+            return VoCosyRes(r["c1"].c, r["c2"].c, r["res"].c, *[_p(a) for a in v])
+
+        def xs(lst):
+            arr = (VoCosyX * max(1, len(lst)))()
+            for i, x in enumerate(lst):
+                v = [f(x[n]) for n in ("n1w", "n1b", "n3w", "n3b")]
+                self.keep += [x, v]
+                arr[i] = VoCosyX(*[_p(a) for a in v], *[x[n].c for n in ("q", "k", "v", "o", "ff1", "ff2")])
+            self.keep.append(arr)
+            return arr
+
+        mids = (VoCosyRes * max(1, len(mid_res)))()
+        for i, r in enumerate(mid_res):
+            mids[i] = res(r)
+        self.counts = np.array([len(v) for v in mid_x] or [0], np.int32)
+        flat = [x for v in mid_x for x in v]
+        self.fn = [f(fn_w), f(fn_b)]
+        self.keep += [mids, down_conv, up_out, final_conv, final_proj]
+        self.c = VoCosy(M, C_, heads, head_dim, res(down_res), res(up_res), mids, len(mid_res), xs(down_x), xs(up_x),
+                        xs(flat), len(down_x), len(up_x), _p(self.counts), down_conv.c, up_out.c, final_conv.c,
+                        final_proj.c, _p(self.fn[0]), _p(self.fn[1]))
+        self.M, self.C, self.n_res = M, C_, 2 + len(mid_res)
+
+
+def cosy_step(m, T, inp, tb, use_ref=False):
+    """One estimator call: inp [2 T][4 M], tb [2 + n_mid][C] -> [2 T][M]."""
+    inp = np.ascontiguousarray(inp, np.float32)
+    tb = np.ascontiguousarray(tb, np.float32)
+    assert inp.shape == (2 * T, 4 * m.M) and tb.shape == (m.n_res, m.C)
+    out = np.empty((2 * T, m.M), np.float32)
+    rc = (ref().ref_cosy_step if use_ref else lib().vo_cosy_step)(C.byref(m.c), T, _p(inp), _p(tb), _p(out))
+    assert rc == 0, rc
     return out

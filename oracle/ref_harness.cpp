@@ -1,8 +1,8 @@
 // ref_harness.cpp — extern "C" wrappers around the reference's own CPU functions.
 //
 // TEST INFRASTRUCTURE ONLY. oracle/Makefile compiles this file together with
-// /root/reference/src/kernels.cpp, f5_ops.cpp and gpu_stub.cpp, where
-// they lie, into oracle/_ref/libvoxref.so. tests/ use it to pin the C
+// /root/reference/src/kernels.cpp, f5_ops.cpp, gpu_stub.cpp, nn.cpp, formats.cpp
+// and resources.cpp, where they lie, into oracle/_ref/libvoxref.so. tests/ use it to pin the C
 // restatement (vox_oracle.c) bit for bit and to write the golden fixtures;
 // bench.py may time it as the "reference" CPU baseline. Nothing here is part
 // of the product, and no reference source is copied into this repository.
@@ -11,6 +11,7 @@
 
 #include "f5_ops.hpp"    // /root/reference/src (Conv1d)
 #include "kernels.hpp"   // /root/reference/src
+#include "nn.hpp"        // /root/reference/src (the vocoder / estimator layers)
 #include "sampling.hpp"  // /root/reference/src
 #include "vox_oracle.h"  // struct layouts shared with the restatement
 
@@ -43,6 +44,35 @@ TransformerW to_xfmr(const vo_xfmr &x, double theta) {
         w.layers.push_back(L);
     }
     return w;
+}
+
+// An nn::Conv (groups 1, stride 1, no padding) over a vo_conv's weights in Conv::w layout [cout][K][cin].
+nn::Conv to_nn_conv(const vo_conv &c) {
+    nn::Conv o;
+    o.cin = c.cin; o.cout = c.cout; o.K = c.K; o.stride = 1; o.pad = 0; o.dil = 1;
+    o.w.assign(c.w, c.w + size_t(c.cout) * size_t(c.K) * size_t(c.cin));
+    if (c.b) o.b.assign(c.b, c.b + c.cout);
+    o.m.type = WType::F32; o.m.data = reinterpret_cast<const uint8_t *>(o.w.data()); o.m.rows = c.cout;
+    o.m.cols = int64_t(c.K) * c.cin; o.m.gpu = -1;
+    return o;
+}
+nn::Linear to_linear(const vo_mat &m) {
+    nn::Linear L;
+    L.w = to_mat(m);
+    L.w.bias = nullptr;
+    if (m.bias) L.b.assign(m.bias, m.bias + m.rows);
+    L.in = m.cols; L.out = m.rows;
+    return L;
+}
+// causal_conv_b (cosyvoice.cpp:127-144) through nn::Conv::forward: K - 1 zero rows in front of each sequence
+void ref_causal_conv_b(const nn::Conv &c, const float *x, int T, int B, float *y) {
+    std::vector<float> xp, yv;
+    for (int b = 0; b < B; ++b) {
+        xp.assign(size_t(T + c.K - 1) * size_t(c.cin), 0.f);
+        std::memcpy(&xp[size_t(c.K - 1) * size_t(c.cin)], x + size_t(b) * T * c.cin, size_t(T) * c.cin * 4);
+        c.forward(xp.data(), T + c.K - 1, yv);
+        std::memcpy(y + size_t(b) * T * c.cout, yv.data(), yv.size() * 4);
+    }
 }
 
 // Fills a KVCache from a flat [layer][cap][kd] array holding `len` positions.
@@ -183,6 +213,91 @@ int ref_transformer_forward_steps(const vo_xfmr *x, vo_kv *const *kvs, int64_t B
         }
         transformer_forward_steps(w, ps.data(), B, in, out);
         for (int64_t b = 0; b < B; ++b) store_kv(cs[size_t(b)], *kvs[b], x->n_layers, kd);
+        return 0;
+    } catch (...) {
+        return -2;
+    }
+}
+
+// ---- nn.cpp layers (the CosyVoice2 / Chatterbox estimator's)
+void ref_gelu_inplace(float *x, int64_t n) { nn::gelu_inplace(x, n); }
+float ref_mish_nn(float x) { return nn::mish(x); }
+void ref_layer_norm_nn(float *x, int T, int C, const float *w, const float *b, float eps) { nn::layer_norm(x, T, C, w, b, eps); }
+void ref_attention_nn(const float *q, const float *k, const float *v, int Tq, int Tk, int H, int dh, float scale, float *out) {
+    const int64_t st = int64_t(H) * dh;
+    nn::attention(q, st, k, st, v, st, Tq, Tk, H, dh, scale, out);
+}
+void ref_causal_conv(const vo_conv *c, const float *x, int T, float *y) { ref_causal_conv_b(to_nn_conv(*c), x, T, 1, y); }
+// The estimator call of cosyvoice.cpp:839-863 (CResnet :169-180, XBlock :197-220, CBlock :147-157) on the reference's
+// own layers, two sequences of T rows.
+int ref_cosy_step(const vo_cosy *m, int T, const float *in, const float *tb, float *out) {
+    try {
+        const int B = 2, C = m->C, R = B * T;
+        auto block = [&](const vo_conv &cv, const float *w, const float *b, const float *x, std::vector<float> &y) {
+            const nn::Conv c = to_nn_conv(cv);
+            y.resize(size_t(R) * size_t(c.cout));
+            ref_causal_conv_b(c, x, T, B, y.data());
+            nn::layer_norm(y.data(), R, c.cout, w, b, 1e-5f);
+            for (float &z : y) z = nn::mish(z);
+        };
+        auto resnet = [&](const vo_cosy_res &r, const float *x, const float *tbj, std::vector<float> &o) {
+            std::vector<float> h, h2, rr;
+            block(r.c1, r.n1w, r.n1b, x, h);
+            for (int t = 0; t < R; ++t)
+                for (int c = 0; c < C; ++c) h[size_t(t) * C + c] += tbj[c];
+            block(r.c2, r.n2w, r.n2b, h.data(), h2);
+            to_nn_conv(r.res).forward(x, R, rr);
+            o.resize(h2.size());
+            for (size_t i = 0; i < o.size(); ++i) o[i] = h2[i] + rr[i];
+        };
+        auto xblock = [&](const vo_cosy_x &L, std::vector<float> &x) {
+            const nn::Linear q = to_linear(L.q), k = to_linear(L.k), v = to_linear(L.v), o = to_linear(L.o);
+            const nn::Linear f1 = to_linear(L.ff1), f2 = to_linear(L.ff2);
+            const int inner = int(q.out), H = m->heads, dh = inner / H;
+            std::vector<float> xn = x, Q(size_t(R) * inner), K(Q.size()), V(Q.size()), A(Q.size()), y(size_t(R) * C);
+            nn::layer_norm(xn.data(), R, C, L.n1w, L.n1b, 1e-5f);
+            q.forward(xn.data(), R, Q.data()); k.forward(xn.data(), R, K.data()); v.forward(xn.data(), R, V.data());
+            for (int b = 0; b < B; ++b) {
+                const size_t off = size_t(b) * T * inner;
+                nn::attention(Q.data() + off, inner, K.data() + off, inner, V.data() + off, inner, T, T, H, dh,
+                              1.0f / std::sqrt(float(dh)), A.data() + off);
+            }
+            o.forward(A.data(), R, y.data());
+            for (size_t i = 0; i < x.size(); ++i) x[i] += y[i];
+            xn = x;
+            nn::layer_norm(xn.data(), R, C, L.n3w, L.n3b, 1e-5f);
+            std::vector<float> hd(size_t(R) * size_t(f1.out));
+            f1.forward(xn.data(), R, hd.data());
+            nn::gelu_inplace(hd.data(), int64_t(hd.size()));
+            f2.forward(hd.data(), R, y.data());
+            for (size_t i = 0; i < x.size(); ++i) x[i] += y[i];
+        };
+        std::vector<float> a, b;
+        resnet(m->down_res, in, tb, a);
+        for (int i = 0; i < m->n_down_x; ++i) xblock(m->down_x[i], a);
+        const std::vector<float> skip = a;
+        b.resize(a.size());
+        ref_causal_conv_b(to_nn_conv(m->down_conv), a.data(), T, B, b.data());
+        int64_t off = 0;
+        for (int i = 0; i < m->n_mid; ++i) {
+            resnet(m->mid_res[i], b.data(), tb + size_t(1 + i) * C, a);
+            for (int j = 0; j < m->mid_x_count[i]; ++j) xblock(m->mid_x[off + j], a);
+            off += m->mid_x_count[i];
+            b.swap(a);
+        }
+        std::vector<float> cat(size_t(R) * 2 * C);
+        for (int r = 0; r < R; ++r) {
+            std::memcpy(&cat[size_t(r) * 2 * C], &b[size_t(r) * C], size_t(C) * 4);
+            std::memcpy(&cat[size_t(r) * 2 * C + C], &skip[size_t(r) * C], size_t(C) * 4);
+        }
+        resnet(m->up_res, cat.data(), tb + size_t(1 + m->n_mid) * C, a);
+        for (int i = 0; i < m->n_up_x; ++i) xblock(m->up_x[i], a);
+        b.resize(a.size());
+        ref_causal_conv_b(to_nn_conv(m->up_out), a.data(), T, B, b.data());
+        block(m->final_conv, m->fn_w, m->fn_b, b.data(), a);
+        std::vector<float> o;
+        to_nn_conv(m->final_proj).forward(a.data(), R, o);
+        std::memcpy(out, o.data(), o.size() * 4);
         return 0;
     } catch (...) {
         return -2;

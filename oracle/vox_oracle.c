@@ -883,3 +883,192 @@ int vo_f5_step(const vo_f5 *m, int32_t B, int32_t N, const float *cat, const flo
     free(qh); free(kh); free(vt); free(oh); free(sc); free(fin);
     return 0;
 }
+
+/* ------------------------------------------------------------------ CosyVoice2 flow estimator */
+float vo_exp_poly(float x) { /* nn.cpp:16-29: x = n ln2 + r, Cephes' degree-6 polynomial for e^r, 2^n in the exponent */
+    x = fminf(fmaxf(x, -87.3f), 88.7f);
+    const float fn = floorf(x * 1.44269504088896341f + 0.5f);
+    const float r = (x - fn * 0.693359375f) - fn * -2.12194440e-4f;
+    float p = 1.9875691500e-4f;
+    p = p * r + 1.3981999507e-3f;
+    p = p * r + 8.3334519073e-3f;
+    p = p * r + 4.1665795894e-2f;
+    p = p * r + 1.6666665459e-1f;
+    p = p * r + 5.0000001201e-1f;
+    p = p * r * r + r + 1.0f;
+    const int32_t e = ((int32_t)fn + 127) << 23;
+    float sc;
+    memcpy(&sc, &e, 4);
+    return p * sc;
+}
+
+float vo_gelu_poly(float x) { /* nn.cpp:31-38 */
+    const float z = fabsf(x) * 0.70710678118654752f;
+    const float t = 1.0f / (1.0f + 0.5f * z);
+    const float y = t * vo_exp_poly(-z * z - 1.26551223f + t * (1.00002368f + t * (0.37409196f + t * (0.09678418f + t * (-0.18628806f +
+                    t * (0.27886807f + t * (-1.13520398f + t * (1.48851587f + t * (-0.82215223f + t * 0.17087277f)))))))));
+    const float erf_abs = 1.0f - y;
+    return 0.5f * x * (1.0f + (x < 0.f ? -erf_abs : erf_abs));
+}
+
+float vo_mish_nn(float x) { /* nn.hpp:103-107 */
+    if (x > 20.f) return x;
+    const float e = expf(x), n = e * (e + 2.0f);
+    return x * (n / (n + 2.0f));
+}
+
+void vo_layer_norm_nn(float *x, int64_t T, int32_t C, const float *w, const float *b, float eps) {
+    for (int64_t t = 0; t < T; ++t) {
+        float *r = x + t * C;
+        double mean = 0;
+        for (int c = 0; c < C; ++c) mean += r[c];
+        mean /= C;
+        double var = 0;
+        for (int c = 0; c < C; ++c) { const double d = r[c] - mean; var += d * d; }
+        var /= C;
+        const float inv = (float)(1.0 / sqrt(var + eps));
+        for (int c = 0; c < C; ++c) {
+            const float n = (r[c] - (float)mean) * inv;
+            r[c] = n * w[c] + (b ? b[c] : 0.f);
+        }
+    }
+}
+
+void vo_softmax_fast(float *x, int64_t n) {
+    float mx = -INFINITY;
+    for (int64_t i = 0; i < n; ++i) mx = mx < x[i] ? x[i] : mx;
+    for (int64_t i = 0; i < n; ++i) x[i] -= mx;
+    for (int64_t i = 0; i < n; ++i) x[i] = vo_exp_poly(x[i]);
+    float sum = 0.f;
+    for (int64_t i = 0; i < n; ++i) sum += x[i];
+    const float inv = 1.0f / sum;
+    for (int64_t i = 0; i < n; ++i) x[i] *= inv;
+}
+
+void vo_attention_nn(const float *q, const float *k, const float *v, int32_t Tq, int32_t Tk, int32_t H, int32_t dh,
+                     float scale, float *out) {
+    const int64_t st = (int64_t)H * dh;
+    float *Q = (float *)malloc(sizeof(float) * (size_t)Tq * dh), *K = (float *)malloc(sizeof(float) * (size_t)Tk * dh);
+    float *Vt = (float *)malloc(sizeof(float) * (size_t)dh * Tk), *S = (float *)malloc(sizeof(float) * (size_t)Tq * Tk);
+    float *O = (float *)malloc(sizeof(float) * (size_t)Tq * dh);
+    for (int h = 0; h < H; ++h) {
+        for (int64_t t = 0; t < Tq; ++t)
+            for (int d = 0; d < dh; ++d) Q[t * dh + d] = q[t * st + (int64_t)h * dh + d] * scale;
+        for (int64_t t = 0; t < Tk; ++t)
+            for (int d = 0; d < dh; ++d) {
+                K[t * dh + d] = k[t * st + (int64_t)h * dh + d];
+                Vt[(int64_t)d * Tk + t] = v[t * st + (int64_t)h * dh + d];
+            }
+        const vo_mat km = {VO_F32, K, NULL, Tk, dh, NULL};
+        vo_matmul(&km, Q, Tq, S, 1);
+        for (int64_t i = 0; i < Tq; ++i) vo_softmax_fast(S + i * Tk, Tk);
+        const vo_mat vm = {VO_F32, Vt, NULL, dh, Tk, NULL};
+        vo_matmul(&vm, S, Tq, O, 1);
+        for (int64_t t = 0; t < Tq; ++t) memcpy(out + t * st + (int64_t)h * dh, O + t * dh, sizeof(float) * (size_t)dh);
+    }
+    free(Q); free(K); free(Vt); free(S); free(O);
+}
+
+void vo_causal_conv(const vo_conv *c, const float *x, int32_t T, float *y) {
+    const int64_t kc = (int64_t)c->K * c->cin;
+    float *col = (float *)calloc((size_t)(T * kc) + 1, sizeof(float));
+    if (!col) return;
+    for (int64_t t = 0; t < T; ++t)
+        for (int k = 0; k < c->K; ++k) {
+            const int64_t s = t + k - (c->K - 1);
+            float *dst = col + t * kc + (int64_t)k * c->cin;
+            if (s >= 0) memcpy(dst, x + s * c->cin, sizeof(float) * (size_t)c->cin);
+            else memset(dst, 0, sizeof(float) * (size_t)c->cin);
+        }
+    const vo_mat W = {VO_F32, c->w, NULL, c->cout, kc, NULL};
+    vo_matmul(&W, col, T, y, 1);
+    if (c->b)
+        for (int64_t t = 0; t < T; ++t)
+            for (int o = 0; o < c->cout; ++o) y[t * c->cout + o] += c->b[o];
+    free(col);
+}
+
+/* causal_conv_b (cosyvoice.cpp:134-144): per sequence of T rows */
+static void cosy_conv_b(const vo_conv *c, const float *x, int32_t T, float *y) {
+    for (int b = 0; b < 2; ++b) vo_causal_conv(c, x + (int64_t)b * T * c->cin, T, y + (int64_t)b * T * c->cout);
+}
+
+/* CausalBlock1D (cosyvoice.cpp:147-157): causal conv -> LayerNorm (1e-5) -> mish */
+static void cosy_block(const vo_conv *c, const float *w, const float *b, const float *x, int32_t T, float *y) {
+    cosy_conv_b(c, x, T, y);
+    vo_layer_norm_nn(y, 2 * (int64_t)T, c->cout, w, b, 1e-5f);
+    for (int64_t i = 0; i < 2 * (int64_t)T * c->cout; ++i) y[i] = vo_mish_nn(y[i]);
+}
+
+/* CausalResnetBlock1D::forward (cosyvoice.cpp:169-180) */
+static void cosy_resnet(const vo_cosy_res *r, const float *x, int32_t T, const float *tb, float *out) {
+    const int C = r->c1.cout;
+    const int64_t R = 2 * (int64_t)T;
+    float *h = (float *)malloc(sizeof(float) * (size_t)(R * C)), *h2 = (float *)malloc(sizeof(float) * (size_t)(R * C));
+    float *rr = (float *)malloc(sizeof(float) * (size_t)(R * C));
+    cosy_block(&r->c1, r->n1w, r->n1b, x, T, h);
+    for (int64_t t = 0; t < R; ++t)
+        for (int c = 0; c < C; ++c) h[t * C + c] += tb[c];
+    cosy_block(&r->c2, r->n2w, r->n2b, h, T, h2);
+    vo_causal_conv(&r->res, x, (int32_t)R, rr); /* K 1: the linear over all rows (res.forward(x, B T)) */
+    for (int64_t i = 0; i < R * C; ++i) out[i] = h2[i] + rr[i];
+    free(h); free(h2); free(rr);
+}
+
+/* XBlock::forward (cosyvoice.cpp:197-220) on x [2 T][C] in place */
+static void cosy_xblock(const vo_cosy_x *L, float *x, int32_t T, int32_t H) {
+    const int C = (int)L->o.rows, inner = (int)L->q.rows, dh = inner / H, FF = (int)L->ff1.rows;
+    const int64_t R = 2 * (int64_t)T;
+    float *xn = (float *)malloc(sizeof(float) * (size_t)(R * C)), *y = (float *)malloc(sizeof(float) * (size_t)(R * C));
+    float *Q = (float *)malloc(sizeof(float) * (size_t)(R * inner)), *K = (float *)malloc(sizeof(float) * (size_t)(R * inner));
+    float *V = (float *)malloc(sizeof(float) * (size_t)(R * inner)), *A = (float *)malloc(sizeof(float) * (size_t)(R * inner));
+    float *hd = (float *)malloc(sizeof(float) * (size_t)(R * FF));
+    memcpy(xn, x, sizeof(float) * (size_t)(R * C));
+    vo_layer_norm_nn(xn, R, C, L->n1w, L->n1b, 1e-5f);
+    vo_matmul(&L->q, xn, R, Q, 1);
+    vo_matmul(&L->k, xn, R, K, 1);
+    vo_matmul(&L->v, xn, R, V, 1);
+    for (int b = 0; b < 2; ++b) {
+        const int64_t off = (int64_t)b * T * inner;
+        vo_attention_nn(Q + off, K + off, V + off, T, T, H, dh, 1.0f / sqrtf((float)dh), A + off);
+    }
+    vo_matmul(&L->o, A, R, y, 1);
+    for (int64_t i = 0; i < R * C; ++i) x[i] += y[i];
+    memcpy(xn, x, sizeof(float) * (size_t)(R * C));
+    vo_layer_norm_nn(xn, R, C, L->n3w, L->n3b, 1e-5f);
+    vo_matmul(&L->ff1, xn, R, hd, 1);
+    for (int64_t i = 0; i < R * FF; ++i) hd[i] = vo_gelu_poly(hd[i]);
+    vo_matmul(&L->ff2, hd, R, y, 1);
+    for (int64_t i = 0; i < R * C; ++i) x[i] += y[i];
+    free(xn); free(y); free(Q); free(K); free(V); free(A); free(hd);
+}
+
+int vo_cosy_step(const vo_cosy *m, int32_t T, const float *in, const float *tb, float *out) {
+    const int C = m->C;
+    const int64_t R = 2 * (int64_t)T;
+    float *a = (float *)malloc(sizeof(float) * (size_t)(R * C)), *b = (float *)malloc(sizeof(float) * (size_t)(R * C));
+    float *skip = (float *)malloc(sizeof(float) * (size_t)(R * C)), *cat = (float *)malloc(sizeof(float) * (size_t)(R * 2 * C));
+    if (!a || !b || !skip || !cat) { free(a); free(b); free(skip); free(cat); return -1; }
+    cosy_resnet(&m->down_res, in, T, tb, a);
+    for (int i = 0; i < m->n_down_x; ++i) cosy_xblock(&m->down_x[i], a, T, m->heads);
+    memcpy(skip, a, sizeof(float) * (size_t)(R * C));
+    cosy_conv_b(&m->down_conv, a, T, b);
+    int64_t off = 0;
+    for (int i = 0; i < m->n_mid; ++i) {
+        cosy_resnet(&m->mid_res[i], b, T, tb + (int64_t)(1 + i) * C, a);
+        for (int j = 0; j < m->mid_x_count[i]; ++j) cosy_xblock(&m->mid_x[off + j], a, T, m->heads);
+        off += m->mid_x_count[i];
+        float *t = a; a = b; b = t;
+    }
+    for (int64_t r = 0; r < R; ++r) {
+        memcpy(cat + r * 2 * C, b + r * C, sizeof(float) * (size_t)C);
+        memcpy(cat + r * 2 * C + C, skip + r * C, sizeof(float) * (size_t)C);
+    }
+    cosy_resnet(&m->up_res, cat, T, tb + (int64_t)(1 + m->n_mid) * C, a);
+    for (int i = 0; i < m->n_up_x; ++i) cosy_xblock(&m->up_x[i], a, T, m->heads);
+    cosy_conv_b(&m->up_out, a, T, b);
+    cosy_block(&m->final_conv, m->fn_w, m->fn_b, b, T, a);
+    vo_causal_conv(&m->final_proj, a, (int32_t)R, out); /* K 1 over all rows */
+    free(a); free(b); free(skip); free(cat);
+    return 0;
+}

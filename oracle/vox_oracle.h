@@ -172,6 +172,44 @@ typedef struct {
 /* F5Model::vocode up to the head output: mel [T][mel_dim] -> head [T][head.rows] (log-magnitude | phase). */
 int vo_vocos_head(const vo_vocos *v, const float *mel, int32_t T, float *head);
 
+/* ---- CosyVoice2 / Chatterbox flow estimator (cosyvoice.cpp:126-221, :839-863; nn.cpp, nn.hpp) ---- */
+float vo_exp_poly(float x);  /* nn.cpp:16-29 */
+float vo_gelu_poly(float x); /* nn.cpp:31-38: erf GELU through Numerical Recipes' erfc fit */
+float vo_mish_nn(float x);   /* nn.hpp:103-107 */
+/* LayerNorm with weight and bias over channels of [T][C] rows, in place (nn.cpp:248-265, modulate false). */
+void vo_layer_norm_nn(float *x, int64_t T, int32_t C, const float *w, const float *b, float eps);
+/* softmax_fast (nn.cpp:97-106): max, subtract, exp_poly, sum, * (1 / sum). */
+void vo_softmax_fast(float *x, int64_t n);
+/* attention without the score term (nn.cpp:448-500 from :473): per head, Q * scale, S = Q K^T through the F32
+ * matmul, softmax_fast rows, O = S V; q/k/v/out rows of H dh floats. */
+void vo_attention_nn(const float *q, const float *k, const float *v, int32_t Tq, int32_t Tk, int32_t H, int32_t dh,
+                     float scale, float *out);
+/* causal_conv (cosyvoice.cpp:127-131): Conv::forward (nn.cpp:179-202, groups 1, w [cout][K][cin]) of x [T][cin]
+ * with K - 1 zero rows in front, bias added after the product (nn.cpp:146-155). K 1: the plain linear. */
+void vo_causal_conv(const vo_conv *c, const float *x, int32_t T, float *y);
+typedef struct {
+    vo_conv c1, c2, res;
+    const float *n1w, *n1b, *n2w, *n2b;
+} vo_cosy_res;
+typedef struct {
+    const float *n1w, *n1b, *n3w, *n3b;
+    vo_mat q, k, v, o, ff1, ff2; /* q, k, v without bias */
+} vo_cosy_x;
+typedef struct {
+    int32_t M, C, heads, head_dim;
+    vo_cosy_res down_res, up_res;
+    const vo_cosy_res *mid_res;
+    int32_t n_mid;
+    const vo_cosy_x *down_x, *up_x, *mid_x; /* mid block i: mid_x_count[i] consecutive entries of mid_x */
+    int32_t n_down_x, n_up_x;
+    const int32_t *mid_x_count;
+    vo_conv down_conv, up_out, final_conv, final_proj;
+    const float *fn_w, *fn_b;
+} vo_cosy;
+/* One estimator call (cosyvoice.cpp:839-863): in [2][T][4 M] ([x | mu | spks | cond] of both passes), tb
+ * [2 + n_mid][C] (the resnets' time biases) -> out [2][T][M]. */
+int vo_cosy_step(const vo_cosy *m, int32_t T, const float *in, const float *tb, float *out);
+
 /* Thread count for the row-parallel loops (matmul); 1 = scalar single-thread. Results do not depend on it. */
 void vo_set_threads(int n);
 int vo_get_threads(void);

@@ -1,8 +1,10 @@
 """Writes tests/golden/golden_ref.npz from the compiled reference harness (oracle/_ref/libvoxref.so).
 
 Run here (where /root/reference exists and `make -C oracle ref` has built the harness):
-    python tests/golden/make_golden.py
-The fixture holds inputs and the reference's outputs only (data, no reference source). Tests compare the
+    python tests/golden/make_golden.py          # golden_ref.npz
+    python tests/golden/make_golden.py cosy     # golden_cosy.npz (the flow estimator's nn.cpp layers)
+The fixtures hold inputs and the reference's outputs only (data, no reference source; the estimator's weights are
+regenerated from a seed by tests/models.py's CosyModel). Tests compare the
 C restatement (oracle/liboracle.so) against it on machines without the reference.
 """
 import os
@@ -18,6 +20,8 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 import pyoracle as po  # noqa: E402
 
 OUT = os.path.join(HERE, "golden_ref.npz")
+OUT_COSY = os.path.join(HERE, "golden_cosy.npz")
+COSY_SEED, COSY_T = 77, 13  # CosyModel(COSY_SEED, n_mid=1, n_x=1) at T frames
 
 
 def main():
@@ -113,5 +117,41 @@ def main():
     print("wrote", OUT, os.path.getsize(OUT), "bytes")
 
 
+def main_cosy():
+    """The nn.cpp layers of the CosyVoice2 / Chatterbox estimator (gelu_inplace, mish, layer_norm, attention,
+    Conv::forward on a causally padded input) and one whole estimator call composed from them."""
+    R = po.ref()
+    if R is None:
+        raise SystemExit("oracle/_ref/libvoxref.so is not built")
+    R.ref_set_threads(4)
+    rng = np.random.default_rng(20261202)
+    g = {}
+    x = np.concatenate([rng.standard_normal(997) * 3, [0.0, -0.0, 1e-30, -1e-30, 9.0, -9.0, 30.0, -30.0, 87.0, -87.0],
+                        np.linspace(-6, 6, 61)]).astype(np.float32)
+    g["act_x"] = x
+    g["gelu_out"] = po.gelu_poly(x, use_ref=True)
+    g["mish_out"] = np.array([po.mish_nn(float(v), use_ref=True) for v in x], np.float32)
+    ln_x = (rng.standard_normal((9, 72)) * 2 + 0.5).astype(np.float32)
+    ln_w, ln_b = (1 + 0.1 * rng.standard_normal(72)).astype(np.float32), (0.1 * rng.standard_normal(72)).astype(np.float32)
+    g["ln_x"], g["ln_w"], g["ln_b"] = ln_x, ln_w, ln_b
+    g["ln_out"] = po.layer_norm_nn(ln_x, ln_w, ln_b, 1e-5, use_ref=True)
+    q, k, v = (rng.standard_normal((11, 3 * 16)).astype(np.float32) for _ in range(3))
+    g["attn_q"], g["attn_k"], g["attn_v"] = q, k, v
+    g["attn_out"] = po.attention_nn(q, k, v, 3, 16, 0.25, use_ref=True)
+    w = (rng.standard_normal((6, 3, 8)) * 0.3).astype(np.float32)
+    b = (rng.standard_normal(6) * 0.1).astype(np.float32)
+    cx = rng.standard_normal((10, 8)).astype(np.float32)
+    g["conv_w"], g["conv_b"], g["conv_x"] = w, b, cx
+    g["conv_out"] = po.causal_conv(po.Conv(w, b, 8, 6, 3, 1), cx, use_ref=True)
+    from models import CosyModel
+    m = CosyModel(COSY_SEED, n_mid=1, n_x=1)
+    in0, xx, tb = m.inputs(np.random.default_rng(COSY_SEED), COSY_T)
+    inp = m.with_x(in0, xx)
+    g["cosy_in"], g["cosy_tb"] = inp, tb
+    g["cosy_out"] = po.cosy_step(m.ox, COSY_T, inp, tb, use_ref=True)
+    np.savez_compressed(OUT_COSY, **g)
+    print("wrote", OUT_COSY, os.path.getsize(OUT_COSY), "bytes")
+
+
 if __name__ == "__main__":
-    main()
+    main_cosy() if sys.argv[1:] == ["cosy"] else main()

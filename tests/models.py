@@ -169,3 +169,82 @@ class F5Model:
         for b in range(B):
             cat[b * N:(b + 1) * N, :x.shape[1]] = x
         return cat
+
+
+class CosyModel:
+    """A random CosyVoice2 / Chatterbox flow estimator (CausalConditionalDecoder with one channel level) in both
+    descriptions: `ox` for the oracle, `create(hip)` for the backend. Convolutions f32 in Conv::w layout
+    [cout][K][cin] with std 1 / sqrt(K cin); linears of type wtype, q / k / v without bias."""
+
+    def __init__(self, seed, M=8, C=64, heads=2, head_dim=64, n_mid=1, n_x=1, ff=128, wtype=F32, std=None):
+        rng = np.random.default_rng(seed)
+        self.M, self.C, self.heads, self.hd, self.ff, self.wtype = M, C, heads, head_dim, ff, wtype
+        inner = heads * head_dim
+
+        def conv(cin, cout, K):
+            w = (rng.standard_normal((cout, K, cin)) / np.sqrt(K * cin)).astype(np.float32)
+            return (w, (rng.standard_normal(cout) * 0.05).astype(np.float32), cin, cout, K, 1)
+
+        def vec(n, mean, sd):
+            return (mean + sd * rng.standard_normal(n)).astype(np.float32)
+
+        def mat(rows, cols, bias):
+            d, sc, b = make_mat(rng, wtype, rows, cols, std=std or 1.0 / np.sqrt(cols), bias=bias)
+            if b is not None:
+                b = (b * 0.05 * np.sqrt(cols)).astype(np.float32)
+            return (wtype, d, rows, cols, sc, b)
+
+        def res(cin):
+            return {"c1": conv(cin, C, 3), "c2": conv(C, C, 3), "res": conv(cin, C, 1), "n1w": vec(C, 1, 0.1),
+                    "n1b": vec(C, 0, 0.1), "n2w": vec(C, 1, 0.1), "n2b": vec(C, 0, 0.1)}
+
+        def xb():
+            return {"n1w": vec(C, 1, 0.1), "n1b": vec(C, 0, 0.1), "n3w": vec(C, 1, 0.1), "n3b": vec(C, 0, 0.1),
+                    "q": mat(inner, C, False), "k": mat(inner, C, False), "v": mat(inner, C, False), "o": mat(C, inner, True),
+                    "ff1": mat(ff, C, True), "ff2": mat(C, ff, True)}
+        self.down_res, self.up_res = res(4 * M), res(2 * C)
+        self.mid_res = [res(C) for _ in range(n_mid)]
+        self.down_x, self.up_x = [xb() for _ in range(n_x)], [xb() for _ in range(n_x)]
+        self.mid_x = [[xb() for _ in range(n_x)] for _ in range(n_mid)]
+        self.convs = {"down_conv": conv(C, C, 3), "up_out": conv(C, C, 3), "final_conv": conv(C, C, 3),
+                      "final_proj": conv(C, M, 1)}
+        self.fn = (vec(C, 1, 0.1), vec(C, 0, 0.1))
+        self.n_res = 2 + n_mid
+
+        def ores(r):
+            return {**{k: po.Conv(*r[k]) for k in ("c1", "c2", "res")}, **{k: r[k] for k in ("n1w", "n1b", "n2w", "n2b")}}
+
+        def ox(x):
+            return {k: (po.Mat(*v) if isinstance(v, tuple) else v) for k, v in x.items()}
+        oc = {k: po.Conv(*v) for k, v in self.convs.items()}
+        self.ox = po.Cosy(M, C, heads, head_dim, ores(self.down_res), ores(self.up_res), [ores(r) for r in self.mid_res],
+                          [ox(x) for x in self.down_x], [ox(x) for x in self.up_x], [[ox(x) for x in v] for v in self.mid_x],
+                          oc["down_conv"], oc["up_out"], oc["final_conv"], oc["final_proj"], *self.fn)
+
+    def create(self, hip):
+        def hx(x):
+            d = {k: (hip.upload(hip.HostMat(*v)) if isinstance(v, tuple) else v) for k, v in x.items()}
+            d["ff_dim"] = self.ff
+            return d
+        return hip.cosy_create(self.M, self.C, self.heads, self.hd, self.down_res, self.up_res, self.mid_res,
+                               [hx(x) for x in self.down_x], [hx(x) for x in self.up_x], [[hx(x) for x in v] for v in self.mid_x],
+                               self.convs["down_conv"], self.convs["up_out"], self.convs["final_conv"],
+                               self.convs["final_proj"], *self.fn)
+
+    def inputs(self, rng, T):
+        """in0 [2 T][4 M] as cosyvoice.cpp:806-815 fills it (pass 0: [0 | mu | spks | cond], pass 1 all zero),
+        x [T][M], tb [2 + n_mid][C]."""
+        M = self.M
+        in0 = np.zeros((2 * T, 4 * M), np.float32)
+        in0[:T, M:] = rng.standard_normal((T, 3 * M)).astype(np.float32)
+        in0[:T, 2 * M:3 * M] = in0[0, 2 * M:3 * M]  # spks: one vector for every row
+        x = rng.standard_normal((T, M)).astype(np.float32)
+        tb = (rng.standard_normal((self.n_res, self.C)) * 0.5).astype(np.float32)
+        return in0, x, tb
+
+    def with_x(self, in0, x):
+        inp = in0.copy()
+        T = x.shape[0]
+        inp[:T, :self.M] = x
+        inp[T:, :self.M] = x
+        return inp

@@ -635,3 +635,85 @@ def test_transformer_layers_compose(oracle):
     nrm = np.empty(128, np.float32)
     po.lib().vo_rmsnorm(full[1].ctypes.data, mdl.final_norm.ctypes.data, 128, np.float32(1e-6), nrm.ctypes.data)
     assert np.array_equal(nrm, out)
+
+
+# ------------------------------------------------------------------ CosyVoice2 / Chatterbox flow estimator
+COSY_GOLD = os.path.join(os.path.dirname(__file__), "golden", "golden_cosy.npz")
+
+
+@pytest.fixture(scope="module")
+def cgold():
+    return np.load(COSY_GOLD, allow_pickle=False)
+
+
+def test_cosy_layers_golden(oracle, cgold):
+    # nn.cpp's layers against the compiled reference's outputs, bit for bit: gelu_inplace (vector and scalar paths),
+    # mish, layer_norm, attention, Conv::forward on a causally padded input
+    x = cgold["act_x"]
+    assert np.array_equal(po.gelu_poly(x), cgold["gelu_out"])
+    assert np.array_equal(np.array([po.mish_nn(float(v)) for v in x], np.float32), cgold["mish_out"])
+    assert np.array_equal(po.layer_norm_nn(cgold["ln_x"], cgold["ln_w"], cgold["ln_b"], 1e-5), cgold["ln_out"])
+    assert np.array_equal(po.attention_nn(cgold["attn_q"], cgold["attn_k"], cgold["attn_v"], 3, 16, 0.25), cgold["attn_out"])
+    cv = po.Conv(cgold["conv_w"], cgold["conv_b"], 8, 6, 3, 1)
+    assert np.array_equal(po.causal_conv(cv, cgold["conv_x"]), cgold["conv_out"])
+
+
+def test_cosy_step_golden(oracle, cgold):
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+    import make_golden
+    import models
+    # the weights come back from the fixture's seed; the inputs are checked against the stored ones
+    T = make_golden.COSY_T
+    m = models.CosyModel(make_golden.COSY_SEED, n_mid=1, n_x=1)
+    in0, x, tb = m.inputs(np.random.default_rng(make_golden.COSY_SEED), T)
+    assert np.array_equal(m.with_x(in0, x), cgold["cosy_in"]) and np.array_equal(tb, cgold["cosy_tb"])
+    assert np.array_equal(po.cosy_step(m.ox, T, cgold["cosy_in"], tb), cgold["cosy_out"])
+
+
+def test_cosy_layers_closed_forms(oracle):
+    # what the mathematics fixes, independent of the restated code: gelu_poly is the erf GELU within its erfc fit
+    # (1.2e-7 relative), mish is x tanh(softplus x), the causal conv never reads later rows, attention is
+    # softmax(q k^T s) v
+    import math
+    rng = np.random.default_rng(8)
+    xs = np.concatenate([np.linspace(-10, 10, 2001), rng.standard_normal(300) * 4]).astype(np.float32)
+    g = po.gelu_poly(xs)
+    for x, y in zip(xs.astype(np.float64), g):
+        want = 0.5 * x * (1 + math.erf(x / math.sqrt(2)))
+        assert abs(y - want) <= 2e-7 * max(1.0, abs(x)), (x, y, want)
+    for x in xs.astype(np.float64):
+        want = x if x > 20 else x * math.tanh(math.log1p(math.exp(x)))
+        assert abs(po.mish_nn(float(x)) - want) <= 1e-6 * max(1.0, abs(x)), x
+    w = (rng.standard_normal((5, 3, 8)) * 0.3).astype(np.float32)
+    b = rng.standard_normal(5).astype(np.float32)
+    cv = po.Conv(w, b, 8, 5, 3, 1)
+    x = rng.standard_normal((9, 8)).astype(np.float32)
+    y = po.causal_conv(cv, x)
+    xp = np.concatenate([np.zeros((2, 8)), x]).astype(np.float64)
+    want = np.stack([sum(w[:, k, :].astype(np.float64) @ xp[t + k] for k in range(3)) + b for t in range(9)])
+    assert np.max(np.abs(y - want)) < 1e-5
+    x2 = x.copy()
+    x2[6:] += 1.0  # later rows change, earlier outputs do not
+    assert np.array_equal(po.causal_conv(cv, x2)[:6], y[:6])
+    q, k, v = (rng.standard_normal((7, 2 * 16)).astype(np.float32) for _ in range(3))
+    out = po.attention_nn(q, k, v, 2, 16, 0.25)
+    for h in range(2):
+        sl = slice(16 * h, 16 * h + 16)
+        s = q[:, sl].astype(np.float64) @ k[:, sl].T.astype(np.float64) * 0.25
+        p = np.exp(s - s.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        assert np.max(np.abs(out[:, sl] - p @ v[:, sl])) < 1e-5
+
+
+@pytest.mark.parametrize("wt", [0, 1, 3])
+def test_cosy_step_against_reference(ref, wt):
+    # the whole estimator call, restated, against the same call composed from the compiled reference's own layers
+    # (ref_cosy_step: nn.cpp's Conv, layer_norm, mish, Linear, attention and gelu_inplace in cosyvoice.cpp's order)
+    import models
+    m = models.CosyModel(60 + wt, M=8, C=64, heads=2, head_dim=32, n_mid=2, n_x=2, ff=96, wtype=wt)
+    rng = np.random.default_rng(wt)
+    for T in (1, 5, 16):
+        in0, x, tb = m.inputs(rng, T)
+        inp = m.with_x(in0, x)
+        assert np.array_equal(po.cosy_step(m.ox, T, inp, tb), po.cosy_step(m.ox, T, inp, tb, use_ref=True)), T

@@ -6,8 +6,8 @@
 //
 // Error convention of the reference backend (gpu_vulkan.cpp:568-571, :800-803): no exception escapes, false/-1
 // means "compute on the CPU", the reason is kept for gpu_stats().last_error, and one warning goes to stderr.
-// Entry points not provided by this backend yet (the codec, the CosyVoice flow) answer like gpu_stub.cpp, so their
-// callers stay on the CPU.
+// Entry points not provided by this backend yet (the codec) answer like gpu_stub.cpp, so their callers stay on the
+// CPU.
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -231,6 +231,50 @@ bool gpu_f5_vocos(int id, const float *mel, int T, std::vector<float> &head) {
     return false;
 }
 
+// The CosyVoice2 / Chatterbox flow estimator (gpu_f5.cpp:382-556): the description flattened for the C ABI (mid
+// block i's transformer list as mid_x_count[i] consecutive entries); -1 / false keeps the flow on the CPU
+// (cosyvoice.cpp:557, :828-830).
+int gpu_cosy_create(const GpuCosyDesc &d) {
+    auto conv = [](const GpuF5Conv &c) { return voxhip_f5_conv{c.w, c.b, c.cin, c.cout, c.K, c.groups}; };
+    auto res = [&](const GpuCosyDesc::Res &r) {
+        return voxhip_cosy_res{conv(r.c1), conv(r.c2), conv(r.res), r.n1w, r.n1b, r.n2w, r.n2b};
+    };
+    auto xb = [](const GpuCosyDesc::X &x) {
+        return voxhip_cosy_x{x.n1w, x.n1b, x.n3w, x.n3b, x.q, x.k, x.v, x.o, x.ff1, x.ff2, x.ff_dim};
+    };
+    std::vector<voxhip_cosy_res> mid;
+    for (const GpuCosyDesc::Res &r : d.mid_res) mid.push_back(res(r));
+    std::vector<voxhip_cosy_x> down, up, midx;
+    std::vector<int32_t> counts;
+    for (const GpuCosyDesc::X &x : d.down_x) down.push_back(xb(x));
+    for (const GpuCosyDesc::X &x : d.up_x) up.push_back(xb(x));
+    for (const std::vector<GpuCosyDesc::X> &v : d.mid_x) {
+        counts.push_back(int32_t(v.size()));
+        for (const GpuCosyDesc::X &x : v) midx.push_back(xb(x));
+    }
+    if (d.mid_x.size() != d.mid_res.size()) return -1;
+    voxhip_cosy_desc c{};
+    c.M = d.M; c.C = d.C; c.heads = d.heads; c.head_dim = d.head_dim;
+    c.down_res = res(d.down_res); c.up_res = res(d.up_res);
+    c.mid_res = mid.data(); c.n_mid = int32_t(mid.size());
+    c.down_x = down.data(); c.n_down_x = int32_t(down.size());
+    c.up_x = up.data(); c.n_up_x = int32_t(up.size());
+    c.mid_x = midx.data(); c.mid_x_count = counts.data();
+    c.down_conv = conv(d.down_conv); c.up_out = conv(d.up_out); c.final_conv = conv(d.final_conv);
+    c.final_proj = conv(d.final_proj);
+    c.fn_w = d.fn_w; c.fn_b = d.fn_b;
+    const int id = voxhip_cosy_create(&c);
+    if (id < 0) warn_once("flow estimator");
+    return id;
+}
+bool gpu_cosy_begin(int id, int T, const float *in0) { return voxhip_cosy_begin(id, T, in0) != 0; }
+bool gpu_cosy_step(int id, const float *x, const float *tb, float *out) {
+    if (voxhip_cosy_step(id, x, tb, out)) return true;
+    std::fprintf(stderr, "vox: GPU flow estimator step failed: %s\n", voxhip_last_error());
+    return false;
+}
+void gpu_cosy_end(int id) { (void)voxhip_cosy_end(id); }
+
 // The code predictor's frame loop (gpu_vulkan.cpp:968-1045): the same sampler settings for every codebook, the
 // draw (frame, cb) of each; matrices the backend does not hold keep the frame on the CPU.
 bool gpu_pred_frame(const TransformerW &w, int seq, const float *in2, const Mat *in_proj, const std::vector<Mat> &heads,
@@ -263,9 +307,5 @@ void gpu_codec_state_free(int) {}
 bool gpu_codec_forward(int, int, const float *, int, std::vector<float> &) { return false; }
 std::string gpu_gemm_choice() { return ""; }
 void gpu_gemm_preset(const std::string &) {}
-int gpu_cosy_create(const GpuCosyDesc &) { return -1; }
-bool gpu_cosy_begin(int, int, const float *) { return false; }
-bool gpu_cosy_step(int, const float *, const float *, float *) { return false; }
-void gpu_cosy_end(int) {}
 
 }  // namespace vox

@@ -4,19 +4,30 @@
 
 namespace vh {
 
+hipError_t launch_norm_rows(const NormArgs &a, hipStream_t s) {
+    if (a.R <= 0) return hipSuccess;
+    if (a.D <= 0 || a.D % 4 || !a.x || (!a.y && !a.y16) || a.lo_off % 4 || !a.sc || (!a.affine && !a.sh) || !(a.eps > 0.0))
+        return hipErrorInvalidValue;
+    return launch(k_f5_modulate, dim3(unsigned((a.R + 3) / 4)), dim3(256), 0, s, a);
+}
+
 hipError_t launch_f5_modulate(const float *x, int64_t R, int D, const float *sc, const float *sh, float *y, _Float16 *y16,
                               int64_t lo_off, hipStream_t s) {
-    if (R <= 0) return hipSuccess;
-    if (D <= 0 || D % 4 || R > INT32_MAX || (!y && !y16) || lo_off % 4 || !sc || !sh) return hipErrorInvalidValue;
-    return launch(k_f5_modulate, dim3(unsigned((R + 3) / 4)), dim3(256), 0, s, x, int32_t(D), sc, sh, y, y16, lo_off, int32_t(R),
-                  int32_t(0));
+    if (R > INT32_MAX) return hipErrorInvalidValue;
+    NormArgs a{};
+    a.x = x; a.y = y; a.y16 = y16; a.lo_off = lo_off; a.sc = sc; a.sh = sh;
+    a.eps = 1e-6;  // the modulation adds the double 1e-6 (f5.cpp:608-625)
+    a.R = int32_t(R); a.D = D;
+    return launch_norm_rows(a, s);
 }
 
 hipError_t launch_layernorm_rows(const float *x, int64_t R, int D, const float *w, const float *b, float *y, hipStream_t s) {
-    if (R <= 0) return hipSuccess;
-    if (D <= 0 || D % 4 || R > INT32_MAX || !y || !w) return hipErrorInvalidValue;
-    return launch(k_f5_modulate, dim3(unsigned((R + 3) / 4)), dim3(256), 0, s, x, int32_t(D), w, b, y,
-                  static_cast<_Float16 *>(nullptr), int64_t(0), int32_t(R), int32_t(1));
+    if (R > INT32_MAX || !y) return hipErrorInvalidValue;
+    NormArgs a{};
+    a.x = x; a.y = y; a.sc = w; a.sh = b;
+    a.eps = double(1e-6f);  // LayerNorm's float eps 1e-6f, widened (kernels.cpp:721)
+    a.R = int32_t(R); a.D = D; a.affine = 1;
+    return launch_norm_rows(a, s);
 }
 
 hipError_t launch_dwconv(const float *x, const float *w, const float *b, float *y, int64_t R, int C, int K, int seq, hipStream_t s) {

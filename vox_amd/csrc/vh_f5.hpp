@@ -9,17 +9,25 @@ namespace vh {
 typedef float f32x4a __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4a __attribute__((ext_vector_type(4)));
 
-// LayerNorm without parameters + modulation (f5.cpp:608-625), one wave per row (4 rows per 256-thread block):
-// mean and variance in double (two passes over the row, which stays in L1), inv = float(1 / sqrt(var + 1e-6)),
-// y = (x - float(mean)) * inv * (1 + scale) + shift. affine: LayerNorm with weight and bias instead
-// (kernels.cpp:714-723, the Vocos norms), y = (x - float(mean)) * inv * scale + shift (shift null: 0). With y16 set,
-// y goes out as f16 halves instead (hi at y16, lo at y16 + lo_off) for a split-f16 GEMM. D % 4 == 0.
-__global__ __launch_bounds__(256) void k_f5_modulate(const float *__restrict__ x, int32_t D, const float *__restrict__ sc,
-                                                     const float *__restrict__ sh, float *__restrict__ y,
-                                                     _Float16 *__restrict__ y16, int64_t lo_off, int32_t R, int32_t affine) {
+// mish as nn.hpp:103-107 (the CosyVoice2 / Chatterbox estimator's): x tanh(softplus(x)) with tanh(log(1 + e)) =
+// n / (n + 2), n = e (e + 2), and x itself above 20.
+VH_DEV float mish_nn_f(float x) {
+    if (x > 20.f) return x;
+    const float e = expf(x), n = e * (e + 2.0f);
+    return x * (n / (n + 2.0f));
+}
+
+// Row LayerNorm (NormArgs), one wave per row (4 rows per 256-thread block): mean and variance in double (two passes
+// over the row, which stays in L1), inv = float(1 / sqrt(var + eps)). The forms: AdaLN modulation without
+// parameters (f5.cpp:608-625, eps 1e-6), y = (x - float(mean)) * inv * (1 + scale) + shift; LayerNorm with weight
+// and bias (kernels.cpp:714-723 and nn.cpp:248-265, which compute alike), y = (x - float(mean)) * inv * w + b; then
+// mish and a per-channel bias when asked (the estimator's CausalBlock1D and its time bias, cosyvoice.cpp:155-178).
+// D % 4 == 0.
+__global__ __launch_bounds__(256) void k_f5_modulate(NormArgs a) {
     const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= R) return;
-    const float *xr = x + int64_t(row) * D;
+    if (row >= a.R) return;
+    const int D = a.D;
+    const float *xr = a.x + int64_t(row) * D;
     auto wsum = [&](double v) {
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
@@ -41,28 +49,35 @@ __global__ __launch_bounds__(256) void k_f5_modulate(const float *__restrict__ x
         }
     }
     const double var = wsum(q) / D;
-    // the modulation adds the double 1e-6 (f5.cpp:608-625); LayerNorm double(eps) of its float eps 1e-6f (kernels.cpp:721)
-    const double eps = affine ? double(1e-6f) : 1e-6;
-    const float inv = float(1.0 / sqrt(var + eps)), fm = float(mean);
+    const float inv = float(1.0 / sqrt(var + a.eps)), fm = float(mean);
     for (int i = 4 * lane; i < D; i += 256) {
         const f32x4a v = *reinterpret_cast<const f32x4a *>(xr + i);
-        const f32x4a c = *reinterpret_cast<const f32x4a *>(sc + i);
-        const f32x4a t = sh ? *reinterpret_cast<const f32x4a *>(sh + i) : f32x4a{0.f, 0.f, 0.f, 0.f};
+        const f32x4a c = *reinterpret_cast<const f32x4a *>(a.sc + i);
+        const f32x4a t = a.sh ? *reinterpret_cast<const f32x4a *>(a.sh + i) : f32x4a{0.f, 0.f, 0.f, 0.f};
         f32x4a r;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = (v[e] - fm) * inv * (affine ? c[e] : 1.0f + c[e]) + t[e];
-        if (y16) {
+        for (int e = 0; e < 4; ++e) r[e] = (v[e] - fm) * inv * (a.affine ? c[e] : 1.0f + c[e]) + t[e];
+        if (a.mish) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r[e] = mish_nn_f(r[e]);
+        }
+        if (a.tb) {
+            const f32x4a b = *reinterpret_cast<const f32x4a *>(a.tb + i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r[e] += b[e];
+        }
+        if (a.y16) {
             f16x4a hi, lo;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 hi[e] = _Float16(r[e]);
                 lo[e] = _Float16(r[e] - float(hi[e]));
             }
-            _Float16 *hr = y16 + int64_t(row) * D + i;
+            _Float16 *hr = a.y16 + int64_t(row) * D + i;
             *reinterpret_cast<f16x4a *>(hr) = hi;
-            *reinterpret_cast<f16x4a *>(hr + lo_off) = lo;
+            *reinterpret_cast<f16x4a *>(hr + a.lo_off) = lo;
         } else {
-            *reinterpret_cast<f32x4a *>(y + int64_t(row) * D + i) = r;
+            *reinterpret_cast<f32x4a *>(a.y + int64_t(row) * D + i) = r;
         }
     }
 }

@@ -70,7 +70,7 @@ static hipError_t gemm_tile(const uint8_t *w, const float *scale, const float *A
 
 
 static bool rope_h16_ok(const GemmArgs &g) {
-    return g.rope && g.h16 && g.hd > 0 && g.hd % 2 == 0 && g.seq > 0 && g.rope_cols % (2 * g.hd) == 0 && g.m % g.seq == 0 &&
+    return g.h16 && g.hd > 0 && g.hd % 2 == 0 && g.seq > 0 && g.rope_cols % (2 * g.hd) == 0 && g.m % g.seq == 0 &&
            g.n == g.rope_cols + g.rope_cols / 2 && g.ldvt >= g.seq && g.ldvt % 8 == 0 && g.lo_off % 8 == 0;
 }
 
@@ -139,6 +139,7 @@ hipError_t launch_conv_gemm(int epi, const float *w, const float *A, const GemmA
     if (epi == EPI_MISH) return gemm_run<WT_F32, EPI_MISH, ASRC_CONV, 2>(wb, nullptr, A, g, groups, s);
     if (epi == EPI_MISH_ACC) return gemm_run<WT_F32, EPI_MISH_ACC, ASRC_CONV, 2>(wb, nullptr, A, g, groups, s);
     if (epi == EPI_STORE) return gemm_run<WT_F32, EPI_STORE, ASRC_CONV, 2>(wb, nullptr, A, g, groups, s);
+    if (epi == EPI_ACC) return gemm_run<WT_F32, EPI_ACC, ASRC_CONV, 2>(wb, nullptr, A, g, groups, s);
     return hipErrorInvalidValue;
 }
 

@@ -46,7 +46,7 @@ VH_DEV f32x4v gemm_load_a(const float *__restrict__ A, const GemmArgs &g, int ro
     if (row >= g.m || k >= g.K) return v;
     if (ASRC == ASRC_ROWS) return *reinterpret_cast<const f32x4v *>(A + int64_t(row) * g.lda + k);
     const int s = row / g.seq, t = row % g.seq, kt = k / g.cig, i = k % g.cig;
-    const int tt = t + kt - g.ksize / 2;
+    const int tt = t + kt - (g.causal ? g.ksize - 1 : g.ksize / 2);
     if (kt >= g.ksize || tt < 0 || tt >= g.seq) return v;  // kt >= ksize: the zero padding of a weight row
     return *reinterpret_cast<const f32x4v *>(A + (int64_t(s) * g.seq + tt) * g.lda + int64_t(blockIdx.z) * g.cig + i);
 }
@@ -122,7 +122,7 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
                 } else if (EPI == EPI_ROPE || EPI == EPI_ROPE_H16) {
                     const float o = __shfl_xor(c, 1, kWave);  // the pair partner (2j <-> 2j + 1)
                     float r = c;
-                    if (col < g.rope_cols) {
+                    if (col < g.rope_cols && g.rope) {
                         const int inner = g.rope_cols / 2, d = col % g.hd, head = (col % inner) / g.hd;
                         if (g.rope_heads <= 0 || head < g.rope_heads) {
                             const float *cs = g.rope + ((int64_t(row % g.seq) * (g.hd / 2) + d / 2) * 2);
@@ -152,7 +152,7 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
                     else if (EPI == EPI_GELU) *dst = gelu_tanh_f(c);
                     else if (EPI == EPI_GELU_ERF) *dst = gelu_erf_f(c);
                     else if (EPI == EPI_GELU_H16) {
-                        const float r = gelu_tanh_f(c);
+                        const float r = g.gelu_erf ? gelu_erf_f(c) : gelu_tanh_f(c);
                         const _Float16 hi = _Float16(r);
                         const int64_t idx = int64_t(row) * g.ldy + col;
                         g.h16[idx] = hi;

@@ -71,6 +71,8 @@ hipError_t launch_f5_fill_x(const float *x, int N, int mel, float *cat, int W, i
 // Vocos: LayerNorm with weight and bias (double statistics, eps 1e-6) of R rows of D; depthwise "same" conv over
 // batches of seq rows (w [C][K], bias or null).
 hipError_t launch_layernorm_rows(const float *x, int64_t R, int D, const float *w, const float *b, float *y, hipStream_t s);
+// Any row norm of NormArgs (LayerNorm / modulation, optional mish and channel bias; the CosyVoice2 estimator's blocks).
+hipError_t launch_norm_rows(const NormArgs &a, hipStream_t s);
 hipError_t launch_dwconv(const float *x, const float *w, const float *b, float *y, int64_t R, int C, int K, int seq, hipStream_t s);
 hipError_t launch_f5_attn(const _Float16 *qkv16, int64_t lo_off, float *out, _Float16 *out16, int64_t out_lo, int B, int N,
                           int heads, int hd, int ldvt, int ldo, float scale, hipStream_t s);

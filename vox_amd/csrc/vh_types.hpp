@@ -121,8 +121,10 @@ struct GemmArgs {
     int32_t seq, hd, rope_cols, rope_heads;
     // EPI_ROPE_H16: the rotated q | k and v as f16 halves (x = hi + lo) for the attention's matrix cores, written to
     // h16 instead of y: plane hi then plane lo (lo_off halves apart), each = q | k rows [m][rope_cols] followed by
-    // v transposed per batch and head, [m / seq][heads][hd][ldvt] (ldvt >= seq, a multiple of 8)
-    // EPI_GELU_H16: gelu_tanh(c + bias) as f16 halves into h16 (hi) and h16 + lo_off (lo), rows of ldy halves
+    // v transposed per batch and head, [m / seq][heads][hd][ldvt] (ldvt >= seq, a multiple of 8); rope null: the
+    // same layout without the rotation
+    // EPI_GELU_H16: gelu(c + bias) as f16 halves into h16 (hi) and h16 + lo_off (lo), rows of ldy halves; the tanh
+    // form, or the erf form when gelu_erf is set
     _Float16 *h16;
     int64_t lo_off;
     int32_t ldvt;
@@ -130,8 +132,10 @@ struct GemmArgs {
     const _Float16 *a16;
     int64_t a_lo;
     // ASRC_CONV: x [m][lda] rows of `seq`-row batches; group g = blockIdx.z reads channels [g cig, (g + 1) cig) at
-    // rows t + k - ksize / 2 of the same batch (zeros outside) for A column k cig + i; W and y are offset per group
-    int32_t ksize, cig;
+    // rows t + k - ksize / 2 of the same batch (causal: t + k - (ksize - 1)) (zeros outside) for A column k cig + i;
+    // W and y are offset per group
+    int32_t ksize, cig, causal;
+    int32_t gelu_erf;
     // split K (k_gemm_h16): block z sums K columns [z kchunk, (z + 1) kchunk) into ws + z m n ([m][n]); a reduce
     // pass adds the slices in order and applies the epilogue. kchunk 0: no split.
     int32_t kchunk;
@@ -167,6 +171,20 @@ struct LmEmbedArgs {
     int32_t hd;
     int64_t spare_pos;
 };
+// Row LayerNorm of R rows of D (k_f5_modulate), one wave per row, double statistics:
+// n = (x - float(mean)) * float(1 / sqrt(var + eps)); modulate (affine 0): y = n * (1 + sc) + sh; affine:
+// y = n * sc + sh (sh null: 0); then mish (the nn.hpp form) when set, then + tb (null: none). y as f32 rows, or as
+// f16 halves (hi at y16, lo at y16 + lo_off) when y16 is set. x and y may be the same rows.
+struct NormArgs {
+    const float *x;
+    float *y;
+    _Float16 *y16;
+    int64_t lo_off;
+    const float *sc, *sh, *tb;
+    double eps;
+    int32_t R, D, affine, mish;
+};
+
 // One pass of the code-predictor frame loop (gpu_pred_frame): the pass's m rows of the sequence at positions
 // pos0 .. pos0 + m - 1 (row table + RoPE rows), and for a pass after the first the embedding row of the code the
 // previous pass sampled (codes[code_idx]) into x.

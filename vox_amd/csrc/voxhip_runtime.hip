@@ -150,6 +150,7 @@ struct Ctx {
     int32_t *hist_dev = nullptr, *tok_dev = nullptr;
     size_t hist_cap = 0;
     std::vector<struct F5 *> f5;
+    std::vector<struct Cosy *> cosy;
     // split-K partial sums of the MFMA GEMM (allocated at init, so captured graphs can use it)
     float *gemm_ws = nullptr;
     // int-path input rows quantized once per pass (k_quant_rows), kQuantRowsElems elements (allocated at init)
@@ -1744,17 +1745,20 @@ GemmArgs gemm_args(const GpuMat &m, const float *bias, float *y, int64_t lda, in
 }
 void f5_gemm(const GpuMat &m, int epi, const float *A, GemmArgs ga, hipStream_t s) {
     // matmul's f32-activation path for these rows (q8 above 8 rows; q4 never)
-    if (int_path(m, ga.m)) throw Fail("F5 linears need f32 / f16 / bf16 weights, or q8 with more than 8 rows");
+    if (int_path(m, ga.m)) throw Fail("DiT / flow estimator linears need f32 / f16 / bf16 weights, or q8 with more than 8 rows");
     HIPCHECK(launch_gemm(gemv_type(m), epi, m.w, m.s, A, ga, s));
 }
 // A block linear: from the f16 planes of A (width ga.K, lo plane R ga.K halves on) when the model is split,
 // else from the f32 rows A.
-void f5_lin(const F5 &F, const GpuMat &m, int epi, const float *A, const _Float16 *A16, GemmArgs ga, hipStream_t s) {
-    if (!F.split) return f5_gemm(m, epi, A, ga, s);
+void split_lin(bool split, const GpuMat &m, int epi, const float *A, const _Float16 *A16, GemmArgs ga, hipStream_t s) {
+    if (!split) return f5_gemm(m, epi, A, ga, s);
     ga.a16 = A16;
     ga.a_lo = int64_t(ga.m) * ga.K;
     ga.lda = ga.K;
     HIPCHECK(launch_gemm_hh(epi, reinterpret_cast<const _Float16 *>(m.w), ga, s));
+}
+void f5_lin(const F5 &F, const GpuMat &m, int epi, const float *A, const _Float16 *A16, GemmArgs ga, hipStream_t s) {
+    split_lin(F.split, m, epi, A, A16, ga, s);
 }
 
 // dit_forward on the device (f5.cpp:586-725) for the batches of begin; x [N][mel] and ts [dim] already on the device.
@@ -1978,6 +1982,284 @@ int voxhip_f5_end(int id) {
         F5 &F = f5_at(id);
         HIPCHECK(hipStreamSynchronize(g.stream));
         f5_free_step(F);
+        return 1;
+    }, 0);
+}
+
+}  // extern "C"
+
+namespace {
+// ------------------------------------------------------------------ CosyVoice2 / Chatterbox flow estimator
+// (gpu.hpp:100-119; cosyvoice.cpp:126-221 the CPU blocks, :822-863 the step)
+struct CosyRes {  // CausalResnetBlock1D
+    F5Conv c1, c2, res;
+    float *n1w = nullptr, *n1b = nullptr, *n2w = nullptr, *n2b = nullptr;
+};
+struct CosyX {  // BasicTransformerBlock; q | k | v stacked at create
+    float *n1w = nullptr, *n1b = nullptr, *n3w = nullptr, *n3b = nullptr;
+    int qkv = -1, o = -1, ff1 = -1, ff2 = -1, ff = 0;
+};
+struct Cosy {
+    int M = 0, C = 0, heads = 0, hd = 0, inner = 0, ffmax = 0;
+    CosyRes down_res, up_res;
+    std::vector<CosyRes> mid_res;
+    std::vector<CosyX> down_x, up_x;
+    std::vector<std::vector<CosyX>> mid_x;
+    F5Conv down_conv, up_out, final_conv, final_proj;
+    float *fn_w = nullptr, *fn_b = nullptr;
+    // every transformer linear F16 and C, inner, ff multiples of 64: the block activations travel as f16 halves
+    // and the linears take k_gemm_hh; otherwise f32 rows
+    bool split = false;
+    // step buffers of begin(T): rows R = 2 T
+    int T = 0;
+    float *in = nullptr, *a = nullptr, *b = nullptr, *h = nullptr, *cat = nullptr, *xn = nullptr, *at = nullptr,
+          *ff = nullptr, *tb = nullptr, *x = nullptr, *out = nullptr;
+    _Float16 *qkv16 = nullptr, *xn16 = nullptr, *at16 = nullptr, *ff16 = nullptr;
+    int64_t lo_off = 0;
+    int ldvt = 0;
+};
+
+Cosy &cosy_at(int id) {
+    if (id < 0 || size_t(id) >= g.cosy.size() || !g.cosy[size_t(id)]) throw Fail("bad flow estimator handle " + std::to_string(id));
+    return *g.cosy[size_t(id)];
+}
+
+void cosy_free_step(Cosy &E) {
+    for (float *p : {E.in, E.a, E.b, E.h, E.cat, E.xn, E.at, E.ff, E.tb, E.x, E.out}) dfree(p);
+    E.in = E.a = E.b = E.h = E.cat = E.xn = E.at = E.ff = E.tb = E.x = E.out = nullptr;
+    for (_Float16 *p : {E.qkv16, E.xn16, E.at16, E.ff16}) dfree(p);
+    E.qkv16 = E.xn16 = E.at16 = E.ff16 = nullptr;
+    E.T = E.ldvt = 0;
+    E.lo_off = 0;
+}
+
+F5Conv cosy_conv_up(const voxhip_f5_conv &c, int cin, int cout, bool k1, const char *what) {
+    if (c.groups != 1 || c.cin != cin || c.cout != cout || (k1 && c.K != 1))
+        throw Fail(std::string("flow estimator ") + what + ": wrong shape (groups 1" + (k1 ? ", K 1)" : ")"));
+    return upload_conv_gemm(c, what);
+}
+
+CosyRes cosy_res_up(const voxhip_cosy_res &r, int cin, int C) {
+    CosyRes o;
+    o.c1 = cosy_conv_up(r.c1, cin, C, false, "resnet conv 1");
+    o.c2 = cosy_conv_up(r.c2, C, C, false, "resnet conv 2");
+    o.res = cosy_conv_up(r.res, cin, C, true, "resnet res conv");
+    o.n1w = upload_vec(r.n1w, C, "resnet norm 1 weight");
+    o.n1b = upload_vec(r.n1b, C, "resnet norm 1 bias");
+    o.n2w = upload_vec(r.n2w, C, "resnet norm 2 weight");
+    o.n2b = upload_vec(r.n2b, C, "resnet norm 2 bias");
+    return o;
+}
+
+CosyX cosy_x_up(const voxhip_cosy_x &x, int C, int inner) {
+    auto check = [&](int id, int64_t rows, int64_t cols, const char *what) {
+        const GpuMat &m = mat_at(id);
+        if (m.rows != rows || m.cols != cols) throw Fail(std::string("flow estimator ") + what + " has the wrong shape");
+    };
+    if (x.ff_dim <= 0 || x.ff_dim % 4) throw Fail("flow estimator: ff_dim must be a positive multiple of 4");
+    check(x.q, inner, C, "to_q"); check(x.k, inner, C, "to_k"); check(x.v, inner, C, "to_v");
+    check(x.o, C, inner, "to_out"); check(x.ff1, x.ff_dim, C, "ff.0"); check(x.ff2, C, x.ff_dim, "ff.2");
+    CosyX o;
+    o.n1w = upload_vec(x.n1w, C, "norm1 weight"); o.n1b = upload_vec(x.n1b, C, "norm1 bias");
+    o.n3w = upload_vec(x.n3w, C, "norm3 weight"); o.n3b = upload_vec(x.n3b, C, "norm3 bias");
+    o.qkv = stack_rows({x.q, x.k, x.v});
+    o.o = x.o; o.ff1 = x.ff1; o.ff2 = x.ff2; o.ff = x.ff_dim;
+    return o;
+}
+
+// A causal (or K-1) convolution of the R = 2 T rows X (row stride ldx) into Y (row stride ldy) on the conv GEMM.
+void cosy_conv(const Cosy &E, const F5Conv &cv, int epi, const float *X, int64_t ldx, float *Y, int64_t ldy, hipStream_t s) {
+    GemmArgs ga{};
+    ga.bias = cv.b; ga.y = Y; ga.lda = ldx; ga.ldy = ldy; ga.m = int32_t(2 * E.T); ga.n = cv.cout;
+    ga.cig = cv.cin; ga.ksize = cv.K; ga.K = cv.kpad; ga.seq = E.T; ga.causal = 1;
+    HIPCHECK(launch_conv_gemm(epi, cv.w, X, ga, 1, s));
+}
+
+// LayerNorm (eps 1e-5f, cosyvoice.cpp:156, :205, :213) of the R rows of C at x into y (or y16 planes), then mish and
+// the channel bias tb when given.
+void cosy_norm(const Cosy &E, const float *x, const float *w, const float *b, bool mish, const float *tb, float *y,
+               _Float16 *y16, hipStream_t s) {
+    NormArgs a{};
+    a.x = x; a.y = y; a.y16 = y16; a.lo_off = int64_t(2) * E.T * E.C; a.sc = w; a.sh = b; a.tb = tb;
+    a.eps = double(1e-5f); a.R = 2 * E.T; a.D = E.C; a.affine = 1; a.mish = mish;
+    HIPCHECK(launch_norm_rows(a, s));
+}
+
+// CausalResnetBlock1D (cosyvoice.cpp:158-180): O = block2(block1(X) + tb) + res(X), block = causal conv -> LayerNorm
+// -> mish; tb the time bias of resnet j.
+void cosy_resnet(const Cosy &E, const CosyRes &r, int j, const float *X, int64_t ldx, float *O, hipStream_t s) {
+    const int C = E.C;
+    cosy_conv(E, r.c1, EPI_STORE, X, ldx, E.h, C, s);
+    cosy_norm(E, E.h, r.n1w, r.n1b, true, E.tb + size_t(j) * C, E.h, nullptr, s);
+    cosy_conv(E, r.c2, EPI_STORE, E.h, C, O, C, s);
+    cosy_norm(E, O, r.n2w, r.n2b, true, nullptr, O, nullptr, s);
+    cosy_conv(E, r.res, EPI_ACC, X, ldx, O, C, s);
+}
+
+// BasicTransformerBlock (cosyvoice.cpp:182-221) on the rows A in place: LayerNorm -> q | k | v (no bias) -> full
+// attention per sequence -> to_out + residual -> LayerNorm -> ff.0 + GELU (erf) -> ff.2 + residual.
+void cosy_xblock(const Cosy &E, const CosyX &L, float *A, hipStream_t s) {
+    const int C = E.C, INNER = E.inner;
+    const int64_t R = int64_t(2) * E.T;
+    float *xn = E.split ? nullptr : E.xn;
+    cosy_norm(E, A, L.n1w, L.n1b, false, nullptr, xn, E.xn16, s);
+    const GpuMat &Mq = mat_at(L.qkv);
+    GemmArgs gq = gemm_args(Mq, Mq.b, nullptr, C, 3 * INNER, R);
+    gq.rope = nullptr; gq.seq = E.T; gq.hd = E.hd; gq.rope_cols = 2 * INNER;
+    gq.h16 = E.qkv16; gq.lo_off = E.lo_off; gq.ldvt = E.ldvt;
+    split_lin(E.split, Mq, EPI_ROPE_H16, E.xn, E.xn16, gq, s);
+    HIPCHECK(launch_f5_attn(E.qkv16, E.lo_off, E.split ? nullptr : E.at, E.at16, R * INNER, 2, E.T, E.heads, E.hd, E.ldvt,
+                            INNER, 1.0f / std::sqrt(float(E.hd)), s));
+    const GpuMat &Mo = mat_at(L.o);
+    split_lin(E.split, Mo, EPI_ACC, E.at, E.at16, gemm_args(Mo, Mo.b, A, INNER, C, R), s);
+    cosy_norm(E, A, L.n3w, L.n3b, false, nullptr, xn, E.xn16, s);
+    const GpuMat &M1 = mat_at(L.ff1), &M2 = mat_at(L.ff2);
+    GemmArgs g1 = gemm_args(M1, M1.b, E.split ? nullptr : E.ff, C, L.ff, R);
+    g1.h16 = E.ff16; g1.lo_off = R * L.ff; g1.gelu_erf = 1;
+    split_lin(E.split, M1, E.split ? EPI_GELU_H16 : EPI_GELU_ERF, E.xn, E.xn16, g1, s);
+    split_lin(E.split, M2, EPI_ACC, E.ff, E.ff16, gemm_args(M2, M2.b, A, L.ff, C, R), s);
+}
+
+// The estimator of one Euler step (cosyvoice.cpp:839-863; gpu_f5.cpp:490-547): x and the time biases already on
+// the device.
+void cosy_enqueue(Cosy &E, hipStream_t s) {
+    const int C = E.C, M = E.M;
+    const int64_t R = int64_t(2) * E.T;
+    HIPCHECK(launch_f5_fill_x(E.x, E.T, M, E.in, 4 * M, 2, s));
+    cosy_resnet(E, E.down_res, 0, E.in, 4 * M, E.a, s);
+    for (const CosyX &L : E.down_x) cosy_xblock(E, L, E.a, s);
+    // the skip half of the up block's input [x | skip]
+    HIPCHECK(hipMemcpy2DAsync(E.cat + C, size_t(2 * C) * 4, E.a, size_t(C) * 4, size_t(C) * 4, size_t(R), hipMemcpyDeviceToDevice, s));
+    cosy_conv(E, E.down_conv, EPI_STORE, E.a, C, E.b, C, s);
+    float *cur = E.b, *oth = E.a;
+    for (size_t i = 0; i < E.mid_res.size(); ++i) {
+        cosy_resnet(E, E.mid_res[i], int(1 + i), cur, C, oth, s);
+        for (const CosyX &L : E.mid_x[i]) cosy_xblock(E, L, oth, s);
+        std::swap(cur, oth);
+    }
+    HIPCHECK(hipMemcpy2DAsync(E.cat, size_t(2 * C) * 4, cur, size_t(C) * 4, size_t(C) * 4, size_t(R), hipMemcpyDeviceToDevice, s));
+    cosy_resnet(E, E.up_res, int(1 + E.mid_res.size()), E.cat, 2 * C, oth, s);
+    for (const CosyX &L : E.up_x) cosy_xblock(E, L, oth, s);
+    cosy_conv(E, E.up_out, EPI_STORE, oth, C, cur, C, s);
+    cosy_conv(E, E.final_conv, EPI_STORE, cur, C, oth, C, s);
+    cosy_norm(E, oth, E.fn_w, E.fn_b, true, nullptr, oth, nullptr, s);
+    cosy_conv(E, E.final_proj, EPI_STORE, oth, C, E.out, M, s);
+}
+}  // namespace
+
+extern "C" {
+
+int voxhip_cosy_create(const voxhip_cosy_desc *d) {
+    return guard_int([&] {
+        require_ok();
+        if (!d) throw Fail("missing flow estimator description");
+        if (d->head_dim != kF5HeadDim) throw Fail("the flow estimator's attention supports head_dim 64");
+        const int C = d->C, M = d->M;
+        if (C <= 0 || C % 4 || M <= 0 || M % 4 || d->heads <= 0 || d->n_mid < 0 || d->n_down_x < 0 || d->n_up_x < 0)
+            throw Fail("bad flow estimator dimensions (C and M multiples of 4)");
+        if ((d->n_mid && (!d->mid_res || !d->mid_x_count)) || (d->n_down_x && !d->down_x) || (d->n_up_x && !d->up_x))
+            throw Fail("missing flow estimator blocks");
+        std::unique_ptr<Cosy> E(new Cosy());
+        E->M = M; E->C = C; E->heads = d->heads; E->hd = d->head_dim; E->inner = d->heads * d->head_dim;
+        E->down_res = cosy_res_up(d->down_res, 4 * M, C);
+        E->up_res = cosy_res_up(d->up_res, 2 * C, C);
+        for (int i = 0; i < d->n_mid; ++i) E->mid_res.push_back(cosy_res_up(d->mid_res[i], C, C));
+        auto xs = [&](const voxhip_cosy_x *v, int n) {
+            std::vector<CosyX> o;
+            for (int i = 0; i < n; ++i) {
+                o.push_back(cosy_x_up(v[i], C, E->inner));
+                E->ffmax = std::max(E->ffmax, v[i].ff_dim);
+            }
+            return o;
+        };
+        E->down_x = xs(d->down_x, d->n_down_x);
+        E->up_x = xs(d->up_x, d->n_up_x);
+        int64_t off = 0;
+        for (int i = 0; i < d->n_mid; ++i) {
+            if (d->mid_x_count[i] < 0 || (d->mid_x_count[i] && !d->mid_x)) throw Fail("bad mid_x_count");
+            E->mid_x.push_back(xs(d->mid_x + off, d->mid_x_count[i]));
+            off += d->mid_x_count[i];
+        }
+        E->down_conv = cosy_conv_up(d->down_conv, C, C, false, "down conv");
+        E->up_out = cosy_conv_up(d->up_out, C, C, false, "up conv");
+        E->final_conv = cosy_conv_up(d->final_conv, C, C, false, "final block conv");
+        E->final_proj = cosy_conv_up(d->final_proj, C, M, true, "final_proj");
+        E->fn_w = upload_vec(d->fn_w, C, "final block norm weight");
+        E->fn_b = upload_vec(d->fn_b, C, "final block norm bias");
+        bool split = C % 64 == 0 && E->inner % 64 == 0;
+        for (const auto *v : {&E->down_x, &E->up_x})
+            for (const CosyX &x : *v) split = split && x.ff % 64 == 0;
+        for (const auto &v : E->mid_x)
+            for (const CosyX &x : v) split = split && x.ff % 64 == 0;
+        auto all_f16 = [&](const std::vector<CosyX> &v) {
+            for (const CosyX &x : v)
+                for (int id : {x.qkv, x.o, x.ff1, x.ff2})
+                    if (mat_at(id).type != VOXHIP_F16) return false;
+            return true;
+        };
+        split = split && all_f16(E->down_x) && all_f16(E->up_x);
+        for (const auto &v : E->mid_x) split = split && all_f16(v);
+        E->split = split;
+        g.cosy.push_back(E.release());
+        return int(g.cosy.size()) - 1;
+    }, -1);
+}
+
+int voxhip_cosy_begin(int id, int T, const float *in0) {
+    return guard_int([&] {
+        require_ok();
+        Cosy &E = cosy_at(id);
+        if (T <= 0 || !in0 || int64_t(T) * 2 * std::max({E.C * 2, E.inner * 3, E.ffmax, 4 * E.M}) > INT32_MAX / 2)
+            throw Fail("bad flow estimator length");
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        cosy_free_step(E);
+        const size_t R = size_t(2) * size_t(T), C = size_t(E.C), INNER = size_t(E.inner), FF = size_t(std::max(E.ffmax, 1));
+        E.in = dalloc_t<float>(R * 4 * E.M);
+        E.a = dalloc_t<float>(R * C); E.b = dalloc_t<float>(R * C); E.h = dalloc_t<float>(R * C);
+        E.cat = dalloc_t<float>(R * 2 * C);
+        if (E.split) {
+            E.xn16 = dalloc_t<_Float16>(2 * R * C);
+            E.at16 = dalloc_t<_Float16>(2 * R * INNER);
+            E.ff16 = dalloc_t<_Float16>(2 * R * FF);
+        } else {
+            E.xn = dalloc_t<float>(R * C);
+            E.at = dalloc_t<float>(R * INNER);
+            E.ff = dalloc_t<float>(R * FF);
+        }
+        E.ldvt = (T + 63) / 64 * 64;  // whole key tiles, the padding zero
+        E.lo_off = int64_t(R * 2 * INNER) + int64_t(2) * int64_t(INNER) * E.ldvt;
+        E.qkv16 = dalloc_t<_Float16>(size_t(2 * E.lo_off));
+        HIPCHECK(hipMemset(E.qkv16, 0, size_t(2 * E.lo_off) * sizeof(_Float16)));  // the v^T padding stays zero
+        E.tb = dalloc_t<float>((2 + E.mid_res.size()) * C);
+        E.x = dalloc_t<float>(size_t(T) * E.M);
+        E.out = dalloc_t<float>(R * E.M);
+        h2d(E.in, in0, R * 4 * E.M * 4);
+        E.T = T;
+        return 1;
+    }, 0);
+}
+
+int voxhip_cosy_step(int id, const float *x, const float *tb, float *out) {
+    return guard_int([&] {
+        require_ok();
+        Cosy &E = cosy_at(id);
+        if (!E.T) throw Fail("flow estimator step before begin");
+        if (!x || !tb || !out) throw Fail("missing argument");
+        h2d(E.x, x, size_t(E.T) * E.M * 4);
+        h2d(E.tb, tb, (2 + E.mid_res.size()) * size_t(E.C) * 4);
+        cosy_enqueue(E, g.stream);
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        HIPCHECK(hipMemcpy(out, E.out, size_t(2) * E.T * E.M * 4, hipMemcpyDeviceToHost));
+        return 1;
+    }, 0);
+}
+
+int voxhip_cosy_end(int id) {
+    return guard_int([&] {
+        require_ok();
+        Cosy &E = cosy_at(id);
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        cosy_free_step(E);
         return 1;
     }, 0);
 }

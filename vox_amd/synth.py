@@ -132,6 +132,62 @@ F5_DIT = dict(dim=1024, depth=22, heads=16, dim_head=64, ff_mult=2, mel=100, tex
 F5_VOCOS = dict(dim=512, inter=1536, layers=8, out=1026, frames=938)
 
 
+# CosyVoice2's flow estimator (CosyCfg, cosyvoice.hpp:30-33): mel 80, 256 channels, 8 x 64 heads, FFN 1024 (erf GELU),
+# 4 transformer blocks per level, 12 mid resnets; 512 frames = the mel of configs[4]'s 256 speech tokens
+# (token_mel_ratio 2); 10 Euler steps per utterance
+COSY_FLOW = dict(M=80, C=256, heads=8, head_dim=64, ff=1024, n_x=4, n_mid=12, frames=512, steps=10, wtype=vh.F16)
+
+
+class CosyFlow:
+    """A device-resident CosyVoice2 flow estimator with synthetic weights (linears generated on the device, the causal
+    convolutions and the norms on the host)."""
+
+    def __init__(self, cfg, seed=0):
+        c = dict(cfg)
+        self.cfg = c
+        M, C, inner, FF = c["M"], c["C"], c["heads"] * c["head_dim"], c["ff"]
+        rng = np.random.default_rng(seed)
+        stream = [0x7000]
+        self.mats = []
+
+        def mat(rows, cols, bias):
+            stream[0] += 1
+            h = vh.mat_synthetic(c["wtype"], rows, cols, seed, stream[0], 0.0, 1.0 / np.sqrt(cols), bias=bias)
+            self.mats.append(h)
+            return h
+
+        def conv(cin, cout, K):
+            return ((rng.standard_normal((cout, K, cin)) / np.sqrt(K * cin)).astype(np.float32),
+                    (rng.standard_normal(cout) * 0.02).astype(np.float32), cin, cout, K, 1)
+
+        def vec(n, m, sd):
+            return (m + sd * rng.standard_normal(n)).astype(np.float32)
+
+        def res(cin):
+            return dict(c1=conv(cin, C, 3), c2=conv(C, C, 3), res=conv(cin, C, 1), n1w=vec(C, 1, 0.02), n1b=vec(C, 0, 0.02),
+                        n2w=vec(C, 1, 0.02), n2b=vec(C, 0, 0.02))
+
+        def xb():
+            return dict(n1w=vec(C, 1, 0.02), n1b=vec(C, 0, 0.02), n3w=vec(C, 1, 0.02), n3b=vec(C, 0, 0.02),
+                        q=mat(inner, C, False), k=mat(inner, C, False), v=mat(inner, C, False), o=mat(C, inner, True),
+                        ff1=mat(FF, C, True), ff2=mat(C, FF, True), ff_dim=FF)
+        n_x, n_mid = c["n_x"], c["n_mid"]
+        self.est = vh.cosy_create(M, C, c["heads"], c["head_dim"], res(4 * M), res(2 * C), [res(C) for _ in range(n_mid)],
+                                  [xb() for _ in range(n_x)], [xb() for _ in range(n_x)],
+                                  [[xb() for _ in range(n_x)] for _ in range(n_mid)], conv(C, C, 3), conv(C, C, 3),
+                                  conv(C, C, 3), conv(C, M, 1), vec(C, 1, 0.02), vec(C, 0, 0.02))
+
+    def flops(self, T):
+        """FLOPs of one estimator call (both passes, 2 T rows; 2 per multiply-add)."""
+        c = self.cfg
+        M, C, inner, FF, R = c["M"], c["C"], c["heads"] * c["head_dim"], c["ff"], 2 * T
+        resnet = lambda cin: 2 * R * C * (3 * cin + 3 * C + cin)
+        xblock = 2 * R * (3 * inner * C + inner * C + 2 * FF * C) + 2 * 4 * T * T * inner
+        n_x = c["n_x"] * (2 + c["n_mid"])
+        convs = 3 * 2 * R * C * 3 * C + 2 * R * M * C
+        return resnet(4 * M) + resnet(2 * C) + c["n_mid"] * resnet(C) + n_x * xblock + convs
+
+
 class DiT:
     """A device-resident F5 DiT with synthetic weights (linears generated on the device, convolutions on the host)."""
 

@@ -93,6 +93,24 @@ class F5Desc(C.Structure):
                [("v_blocks", C.POINTER(F5VBlock)), ("n_vblocks", C.c_int32), ("v_head", C.c_int32)]
 
 
+class CosyRes(C.Structure):
+    _fields_ = [("c1", F5Conv), ("c2", F5Conv), ("res", F5Conv)] + [(n, C.c_void_p) for n in ("n1w", "n1b", "n2w", "n2b")]
+
+
+class CosyX(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("n1w", "n1b", "n3w", "n3b")] + \
+               [(n, C.c_int32) for n in ("q", "k", "v", "o", "ff1", "ff2", "ff_dim")]
+
+
+class CosyDesc(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("M", "C", "heads", "head_dim")] + \
+               [("down_res", CosyRes), ("up_res", CosyRes), ("mid_res", C.POINTER(CosyRes)), ("n_mid", C.c_int32),
+                ("down_x", C.POINTER(CosyX)), ("up_x", C.POINTER(CosyX)), ("mid_x", C.POINTER(CosyX)),
+                ("n_down_x", C.c_int32), ("n_up_x", C.c_int32), ("mid_x_count", C.c_void_p)] + \
+               [(n, F5Conv) for n in ("down_conv", "up_out", "final_conv", "final_proj")] + \
+               [("fn_w", C.c_void_p), ("fn_b", C.c_void_p)]
+
+
 KERNEL_CLASSES = ("qkv_gemv", "o_gemv", "gateup_gemv", "down_gemv", "head_gemv", "attention", "attn_combine", "qk_post", "sampler")
 
 
@@ -143,6 +161,10 @@ SIGNATURES = {
     "voxhip_f5_end": (_I, [_I]),
     "voxhip_f5_vocos": (_I, [_I, _P, _I, _P]),
     "voxhip_f5_vocos_out": (_I, [_I, _P]),
+    "voxhip_cosy_create": (_I, [C.POINTER(CosyDesc)]),
+    "voxhip_cosy_begin": (_I, [_I, _I, _P]),
+    "voxhip_cosy_step": (_I, [_I, _P, _P, _P]),
+    "voxhip_cosy_end": (_I, [_I]),
     "voxhip_lm_sample_dev": (_I, [_P, C.c_int32, C.POINTER(LmCfg), _I64, _P, C.c_int32, _P, _P]),
     "voxhip_lm_generate": (_I, [_I, _I, _P, _I64, _I, _I, C.POINTER(LmCfg), _P, _P, _P]),
     "voxhip_pred_frame": (_I, [_I, _I, _P, _I, _P, _I, _P, _I, C.POINTER(SampleCfg), _P]),
@@ -542,6 +564,57 @@ def f5_step(f5, x, ts, B, N, mel):
 
 def f5_end(f5):
     _check(lib().voxhip_f5_end(f5), "f5_end")
+
+
+def cosy_create(M, C_, heads, head_dim, down_res, up_res, mid_res, down_x, up_x, mid_x, down_conv, up_out, final_conv,
+                final_proj, fn_w, fn_b):
+    """gpu_cosy_create: resnets = dicts c1, c2, res (conv tuples (w [cout][K][cin] f32, bias or None, cin, cout, K, 1)),
+    n1w, n1b, n2w, n2b; transformer blocks = dicts n1w, n1b, n3w, n3b, q, k, v, o, ff1, ff2 (handles), ff_dim;
+    mid_x a list of such lists, one per mid resnet."""
+    keep = []
+
+    def vec(a):
+        a = f32(a)
+        keep.append(a)
+        return _p(a)
+
+    def conv(c):
+        w, b, cin, cout, K, groups = c
+        return F5Conv(vec(w), None if b is None else vec(b), cin, cout, K, groups)
+
+    def res(r):
+        return CosyRes(conv(r["c1"]), conv(r["c2"]), conv(r["res"]), *[vec(r[n]) for n in ("n1w", "n1b", "n2w", "n2b")])
+
+    def xs(lst):
+        arr = (CosyX * max(1, len(lst)))()
+        for i, x in enumerate(lst):
+            arr[i] = CosyX(*[vec(x[n]) for n in ("n1w", "n1b", "n3w", "n3b")],
+                           *[x[n] for n in ("q", "k", "v", "o", "ff1", "ff2", "ff_dim")])
+        keep.append(arr)
+        return arr
+    mids = (CosyRes * max(1, len(mid_res)))(*[res(r) for r in mid_res])
+    counts = np.array([len(v) for v in mid_x] or [0], np.int32)
+    keep += [mids, counts]
+    d = CosyDesc(M, C_, heads, head_dim, res(down_res), res(up_res), mids, len(mid_res), xs(down_x), xs(up_x),
+                 xs([x for v in mid_x for x in v]), len(down_x), len(up_x), _p(counts), conv(down_conv), conv(up_out),
+                 conv(final_conv), conv(final_proj), vec(fn_w), vec(fn_b))
+    return _handle(lib().voxhip_cosy_create(C.byref(d)), "cosy_create")
+
+
+def cosy_begin(cosy, T, in0):
+    """gpu_cosy_begin: in0 [2 T][4 M], the x columns zero."""
+    _check(lib().voxhip_cosy_begin(cosy, T, _p(f32(in0))), "cosy_begin")
+
+
+def cosy_step(cosy, x, tb, T, M):
+    """gpu_cosy_step: x [T][M], tb [2 + n_mid][C] -> [2 T][M] (conditional pass, then unconditional)."""
+    out = np.empty((2 * T, M), np.float32)
+    _check(lib().voxhip_cosy_step(cosy, _p(f32(x)), _p(f32(tb)), _p(out)), "cosy_step")
+    return out
+
+
+def cosy_end(cosy):
+    _check(lib().voxhip_cosy_end(cosy), "cosy_end")
 
 
 def sync():
