@@ -110,8 +110,9 @@ __global__ __launch_bounds__(256) void k_f5_fill_x(const float *__restrict__ x, 
 }
 
 // Non-causal softmax attention of one head over N keys (f5.cpp:626-650): S = (q . k) * scale, softmax per row,
-// O = P V, for head_dim 64. grid (ceil(N / 64), heads, B), block 256: each wave takes 16 query rows; key tiles of
-// 64 go through LDS; an online softmax (running max and sum per row, O rescaled) replaces the reference's
+// O = P V, for head_dim 64. grid (ceil(N / (16 W)), heads, B), block 64 W: each of the W waves takes 16 query rows
+// (W = 2 doubles the blocks of a short sequence, the flow estimator's, at the cost of staging each key tile for half
+// as many rows); key tiles of 64 go through LDS; an online softmax (running max and sum per row, O rescaled) replaces the reference's
 // whole-row max, which changes only the rounding; exp(x) is taken as 2^(x log2 e) on v_exp_f32.
 // Both products run on the f16 matrix cores (v_mfma_f32_16x16x32_f16) with every f32 operand as two f16 halves,
 // x = hi + lo, and three products per pair (hi.hi + hi.lo + lo.hi; the dropped lo.lo term is below 2^-22 relative):
@@ -145,14 +146,16 @@ VH_DEV f32x4a mfma3(h16x8 ah, h16x8 al, h16x8 bh, h16x8 bl, f32x4a c) {
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, c, 0, 0, 0);
 }
-__global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
+template <int W>
+__global__ __launch_bounds__(64 * W) void k_f5_attn(F5AttnArgs a) {
+    constexpr int RS = 8 * W, RPT = 64 / RS;  // tile rows: thread rows r + RS q, q < RPT
     __shared__ __align__(16) _Float16 Kh[64][kF5Ld], Kl[64][kF5Ld];  // [key][d]
     __shared__ __align__(16) _Float16 Vh[64][kF5Ld], Vl[64][kF5Ld];  // [d][key]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
     // a contiguous run of (batch, head) pairs per XCD, so each head's keys and values stay in one L2
     const int qt = gridDim.x, heads = gridDim.y;
     const int t = xcd_tile(int(blockIdx.x) + qt * (int(blockIdx.y) + heads * int(blockIdx.z)), qt * heads * int(gridDim.z));
-    const int q0 = (t % qt) * 64, h = (t / qt) % heads, b = t / (qt * heads);
+    const int q0 = (t % qt) * (16 * W), h = (t / qt) % heads, b = t / (qt * heads);
     const int64_t ldqk = 2 * int64_t(a.inner);
     // this batch's q and k rows of head h as buffers ending at row N (rows past it read as zeros)
     const _Float16 *qb = a.h16 + int64_t(b) * a.N * ldqk + h * kF5Hd, *kb = qb + a.inner;
@@ -175,33 +178,36 @@ __global__ __launch_bounds__(256) void k_f5_attn(F5AttnArgs a) {
     f32x4a o[4];  // O^T: lane holds O[row lr][16 dt + 4 lg + i]
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = f32x4a{0.f, 0.f, 0.f, 0.f};
-    // per thread and tile: keys / d rows r and r + 32, columns c8 .. c8 + 7, of K and v^T (hi, lo)
+    // per thread and tile: keys / d rows r + RS q, columns c8 .. c8 + 7, of K and v^T (hi, lo)
     const int r = tid >> 3, c8 = (tid & 7) * 8;
-    const int32_t ko0 = int32_t((r * ldqk + c8) * 2), ko1 = int32_t(((r + 32) * ldqk + c8) * 2);
-    const _Float16 *v0 = VT + int64_t(r) * a.ldvt + c8, *v1 = v0 + 32 * int64_t(a.ldvt);
-    u32x4 kr[4], vr[4];
+    int32_t ko[RPT];
+    const _Float16 *vp[RPT];
+#pragma unroll
+    for (int q = 0; q < RPT; ++q) {
+        ko[q] = int32_t(((r + RS * q) * ldqk + c8) * 2);
+        vp[q] = VT + int64_t(r + RS * q) * a.ldvt + c8;
+    }
+    u32x4 kr[2 * RPT], vr[2 * RPT];
     auto fetch = [&](int kt) {
         // the key row goes in the vector offset, which the buffer's range check covers
-        const int32_t ro = int32_t(kt * ldqk * 2), k0o = ko0 + ro, k1o = ko1 + ro;
-        kr[0] = buf_ld16(rkh, k0o, 0);
-        kr[1] = buf_ld16(rkh, k1o, 0);
-        kr[2] = buf_ld16(rkl, k0o, 0);
-        kr[3] = buf_ld16(rkl, k1o, 0);
-        vr[0] = *reinterpret_cast<const u32x4 *>(v0 + kt);
-        vr[1] = *reinterpret_cast<const u32x4 *>(v1 + kt);
-        vr[2] = *reinterpret_cast<const u32x4 *>(v0 + a.lo_off + kt);
-        vr[3] = *reinterpret_cast<const u32x4 *>(v1 + a.lo_off + kt);
+        const int32_t ro = int32_t(kt * ldqk * 2);
+#pragma unroll
+        for (int q = 0; q < RPT; ++q) {
+            kr[q] = buf_ld16(rkh, ko[q] + ro, 0);
+            kr[RPT + q] = buf_ld16(rkl, ko[q] + ro, 0);
+            vr[q] = *reinterpret_cast<const u32x4 *>(vp[q] + kt);
+            vr[RPT + q] = *reinterpret_cast<const u32x4 *>(vp[q] + a.lo_off + kt);
+        }
     };
     fetch(0);
     for (int kt = 0; kt < a.N; kt += 64) {
-        *reinterpret_cast<u32x4 *>(&Kh[r][c8]) = kr[0];
-        *reinterpret_cast<u32x4 *>(&Kh[r + 32][c8]) = kr[1];
-        *reinterpret_cast<u32x4 *>(&Kl[r][c8]) = kr[2];
-        *reinterpret_cast<u32x4 *>(&Kl[r + 32][c8]) = kr[3];
-        *reinterpret_cast<u32x4 *>(&Vh[r][c8]) = vr[0];
-        *reinterpret_cast<u32x4 *>(&Vh[r + 32][c8]) = vr[1];
-        *reinterpret_cast<u32x4 *>(&Vl[r][c8]) = vr[2];
-        *reinterpret_cast<u32x4 *>(&Vl[r + 32][c8]) = vr[3];
+#pragma unroll
+        for (int q = 0; q < RPT; ++q) {
+            *reinterpret_cast<u32x4 *>(&Kh[r + RS * q][c8]) = kr[q];
+            *reinterpret_cast<u32x4 *>(&Kl[r + RS * q][c8]) = kr[RPT + q];
+            *reinterpret_cast<u32x4 *>(&Vh[r + RS * q][c8]) = vr[q];
+            *reinterpret_cast<u32x4 *>(&Vl[r + RS * q][c8]) = vr[RPT + q];
+        }
         __syncthreads();
         fetch(min(kt + 64, a.ldvt - 64));  // unconditional (the last tile again at the end): exact wait counts
         // S^T tiles: A operand lane holds K[16 j + lr][32 c + 8 lg + e]; lane gets S^T[16 j + 4 lg + i][lr]

@@ -30,26 +30,36 @@ static hipError_t gemm_run_h16(const uint8_t *w, const float *scale, const float
 // added until the launch has about kSplitTargetBlocks blocks (two per CU: measured faster than one per CU on the
 // 512-row prefill shapes even with the larger reduce).
 constexpr int64_t kSplitTargetBlocks = 512;
+// The K slices for a split of g (64 x 64 tiles): 0 when the tiles already fill the CUs, K is short or the workspace
+// is too small; else the slice count, with *kchunk the slice width (a multiple of 64).
+static int split_plan(const GemmArgs &g, int *kchunk) {
+    const int64_t blocks = int64_t((g.n + 63) / 64) * ((g.m + 63) / 64);
+    if (!g.ws || blocks >= 192 || g.K < 512) return 0;
+    int splits = int(std::min<int64_t>(8, (kSplitTargetBlocks + blocks - 1) / blocks));
+    *kchunk = ((g.K + splits - 1) / splits + 63) / 64 * 64;
+    splits = (g.K + *kchunk - 1) / *kchunk;
+    if (splits < 2 || int64_t(splits) * g.m * g.n > g.ws_cap) return 0;
+    return splits;
+}
+template <int EPI>
+static hipError_t splitk_reduce(const GemmArgs &g, int splits, hipStream_t s) {
+    const int nout = EPI == EPI_SWIGLU ? g.n / 2 : g.n;
+    const int64_t total = int64_t(g.m) * nout;
+    return launch(k_gemm_splitk_reduce<EPI>, dim3(unsigned((total + 255) / 256)), dim3(256), 0, s, g, int32_t(splits));
+}
 template <int WT, int EPI>
 static hipError_t gemm_splitk(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s, bool *done) {
     *done = false;
     if constexpr (EPI != EPI_STORE && EPI != EPI_ACC && EPI != EPI_GATED_ACC && EPI != EPI_SWIGLU) {
         return hipSuccess;
     } else {
-    const int64_t blocks = int64_t((g.n + 63) / 64) * ((g.m + 63) / 64);
-    if (!g.ws || blocks >= 192 || g.K < 512) return hipSuccess;
-    int splits = int(std::min<int64_t>(8, (kSplitTargetBlocks + blocks - 1) / blocks));
-    const int kchunk = ((g.K + splits - 1) / splits + 63) / 64 * 64;
-    splits = (g.K + kchunk - 1) / kchunk;
-    if (splits < 2 || int64_t(splits) * g.m * g.n > g.ws_cap) return hipSuccess;
-    GemmArgs gs = g;
-    gs.kchunk = kchunk;
-    hipError_t e = gemm_run_h16<WT, EPI_STORE, 2, 2>(w, scale, A, gs, s);
-    if (e != hipSuccess) return e;
-    const int nout = EPI == EPI_SWIGLU ? g.n / 2 : g.n;
-    const int64_t total = int64_t(g.m) * nout;
-    *done = true;
-    return launch(k_gemm_splitk_reduce<EPI>, dim3(unsigned((total + 255) / 256)), dim3(256), 0, s, g, int32_t(splits));
+        GemmArgs gs = g;
+        const int splits = split_plan(g, &gs.kchunk);
+        if (!splits) return hipSuccess;
+        hipError_t e = gemm_run_h16<WT, EPI_STORE, 2, 2>(w, scale, A, gs, s);
+        if (e != hipSuccess) return e;
+        *done = true;
+        return splitk_reduce<EPI>(g, splits, s);
     }
 }
 
@@ -106,10 +116,21 @@ hipError_t launch_gemm(int wt, int epi, const uint8_t *w, const float *scale, co
 }
 
 // 64 x 64 tiles, K steps of 64: measured faster on the DiT shapes than 64 x 128 tiles or K steps of 128.
+// Tiles by how many 64 x 64 tiles the product has (measured on the flow estimator's and the DiT's shapes): below 256
+// the 32 x 32 tiles (the 1024 x 256 projections: 4.4 against 8.0 us, and faster than splitting K), below 512 with
+// K <= 512 the 32 x 64 ones (1024 x 1536, K 256: 7.0 against 8.4 us), else 64 x 64 (2000 x 1024, K 1024: 19.0
+// against 21-25 us for the smaller tiles).
+template <int EPI, int TM, int TN>
+static hipError_t gemm_hh_tiles(const _Float16 *w, const GemmArgs &g, hipStream_t s) {
+    const dim3 grid(unsigned((g.n + 32 * TN - 1) / (32 * TN)), unsigned((g.m + 32 * TM - 1) / (32 * TM)));
+    return launch(k_gemm_hh<EPI, TM, TN, 64>, grid, dim3(256), 0, s, w, g);
+}
 template <int EPI>
 static hipError_t gemm_hh_run(const _Float16 *w, const GemmArgs &g, hipStream_t s) {
-    const unsigned mt = unsigned((g.m + 63) / 64);
-    return launch(k_gemm_hh<EPI, 2, 2, 64>, dim3(unsigned((g.n + 63) / 64), mt), dim3(256), 0, s, w, g);
+    const int64_t blocks = int64_t((g.n + 63) / 64) * ((g.m + 63) / 64);
+    if (blocks < 256) return gemm_hh_tiles<EPI, 1, 1>(w, g, s);
+    if (blocks < 512 && g.K <= 512) return gemm_hh_tiles<EPI, 1, 2>(w, g, s);
+    return gemm_hh_tiles<EPI, 2, 2>(w, g, s);
 }
 
 hipError_t launch_gemm_hh(int epi, const _Float16 *w, const GemmArgs &g, hipStream_t s) {
@@ -136,6 +157,15 @@ hipError_t launch_conv_gemm(int epi, const float *w, const float *A, const GemmA
         g.K % 8 || g.seq <= 0 || g.lda % 4 || groups <= 0 || g.n <= 0)
         return hipErrorInvalidValue;
     const uint8_t *wb = reinterpret_cast<const uint8_t *>(w);
+    if (groups == 1 && (epi == EPI_STORE || epi == EPI_ACC)) {  // one group: K slices in place of groups when idle
+        GemmArgs gs = g;
+        const int splits = split_plan(g, &gs.kchunk);
+        if (splits) {
+            hipError_t e = gemm_run<WT_F32, EPI_STORE, ASRC_CONV, 2>(wb, nullptr, A, gs, splits, s);
+            if (e != hipSuccess) return e;
+            return epi == EPI_STORE ? splitk_reduce<EPI_STORE>(g, splits, s) : splitk_reduce<EPI_ACC>(g, splits, s);
+        }
+    }
     if (epi == EPI_MISH) return gemm_run<WT_F32, EPI_MISH, ASRC_CONV, 2>(wb, nullptr, A, g, groups, s);
     if (epi == EPI_MISH_ACC) return gemm_run<WT_F32, EPI_MISH_ACC, ASRC_CONV, 2>(wb, nullptr, A, g, groups, s);
     if (epi == EPI_STORE) return gemm_run<WT_F32, EPI_STORE, ASRC_CONV, 2>(wb, nullptr, A, g, groups, s);

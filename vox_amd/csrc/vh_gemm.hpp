@@ -41,14 +41,14 @@ VH_DEV float mish_f(float x) {  // f5.cpp:97-100
 
 // Four consecutive A elements of row `row`, columns k..k+3 (zeros outside the matrix / the convolution window).
 template <int ASRC>
-VH_DEV f32x4v gemm_load_a(const float *__restrict__ A, const GemmArgs &g, int row, int k) {
+VH_DEV f32x4v gemm_load_a(const float *__restrict__ A, const GemmArgs &g, int row, int k, int grp) {
     f32x4v v = {0.f, 0.f, 0.f, 0.f};
     if (row >= g.m || k >= g.K) return v;
     if (ASRC == ASRC_ROWS) return *reinterpret_cast<const f32x4v *>(A + int64_t(row) * g.lda + k);
     const int s = row / g.seq, t = row % g.seq, kt = k / g.cig, i = k % g.cig;
     const int tt = t + kt - (g.causal ? g.ksize - 1 : g.ksize / 2);
     if (kt >= g.ksize || tt < 0 || tt >= g.seq) return v;  // kt >= ksize: the zero padding of a weight row
-    return *reinterpret_cast<const f32x4v *>(A + (int64_t(s) * g.seq + tt) * g.lda + int64_t(blockIdx.z) * g.cig + i);
+    return *reinterpret_cast<const f32x4v *>(A + (int64_t(s) * g.seq + tt) * g.lda + int64_t(grp) * g.cig + i);
 }
 
 // Eight consecutive W elements of row `row`, columns k..k+7, widened to f32.
@@ -165,6 +165,24 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
         }
 }
 
+// Split K: a block's TM x TN accumulator tiles as partial sums into slice blockIdx.z of ws ([m][n] per slice), no
+// bias or epilogue (k_gemm_splitk_reduce applies them).
+template <int TM, int TN>
+VH_DEV void gemm_store_partial(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0, int n0, int wm, int wn, int lane) {
+    float *ws = g.ws + int64_t(blockIdx.z) * g.m * g.n;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = n0 + wn * 16 * TN + j * 16 + (lane & 15);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int row = m0 + wm * 16 * TM + i * 16 + 4 * (lane >> 4) + v;
+                if (row < g.m && col < g.n) ws[int64_t(row) * g.n + col] = acc[i][j][v];
+            }
+        }
+}
+
 // Epilogues: EPI_STORE y = c + bias; EPI_ACC y += c + bias; EPI_SWIGLU W rows are (gate u, up u) pairs, y[u] =
 // silu(gate) * up; EPI_GATED_ACC y += gate[col] * (c + bias); EPI_GELU y = gelu_tanh(c + bias); EPI_MISH
 // y = mish(c + bias); EPI_MISH_ACC y += mish(c + bias); EPI_GELU_ERF y = gelu_erf(c + bias); EPI_ROPE y = c + bias
@@ -184,10 +202,13 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const uint8_t *__restrict__ w,
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int K = g.K;
+    // blockIdx.z: the K slice of a split (kchunk set, one group), else the convolution group
+    const int grp = g.kchunk ? 0 : int(blockIdx.z);
+    const int kbeg = g.kchunk ? int(blockIdx.z) * g.kchunk : 0, kend = g.kchunk ? min(K, kbeg + g.kchunk) : K;
     if (ASRC == ASRC_CONV) {
-        w += int64_t(blockIdx.z) * g.n * K * 4;
-        g.y += int64_t(blockIdx.z) * g.n;
-        if (g.bias) g.bias += int64_t(blockIdx.z) * g.n;
+        w += int64_t(grp) * g.n * K * 4;
+        g.y += int64_t(grp) * g.n;
+        if (g.bias) g.bias += int64_t(grp) * g.n;
     }
     f32x4v acc[TM][TN];
 #pragma unroll
@@ -201,7 +222,7 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const uint8_t *__restrict__ w,
 #pragma unroll
         for (int q = 0; q < AQ; ++q) {
             const int idx = tid + 256 * q;
-            ra[q] = gemm_load_a<ASRC>(A, g, m0 + (idx >> 3), k0 + (idx & 7) * 4);
+            ra[q] = gemm_load_a<ASRC>(A, g, m0 + (idx >> 3), k0 + (idx & 7) * 4, grp);
         }
 #pragma unroll
         for (int q = 0; q < WQ; ++q) {
@@ -209,8 +230,8 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const uint8_t *__restrict__ w,
             gemm_load_w<WT>(w, scale, g, n0 + (idx >> 2), k0 + (idx & 3) * 8, rw[q]);
         }
     };
-    fetch(0);
-    for (int k0 = 0; k0 < K; k0 += kGemmBK) {
+    fetch(kbeg);
+    for (int k0 = kbeg; k0 < kend; k0 += kGemmBK) {
 #pragma unroll
         for (int q = 0; q < AQ; ++q) {
             const int idx = tid + 256 * q;
@@ -223,7 +244,7 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const uint8_t *__restrict__ w,
             *reinterpret_cast<f32x4v *>(&Bs[r][kq + 4]) = f32x4v{rw[q][4], rw[q][5], rw[q][6], rw[q][7]};
         }
         __syncthreads();
-        if (k0 + kGemmBK < K) fetch(k0 + kGemmBK);  // in flight during the MFMAs below
+        if (k0 + kGemmBK < kend) fetch(k0 + kGemmBK);  // in flight during the MFMAs below
 #pragma unroll
         for (int kk = 0; kk < kGemmBK; kk += 4) {
             float a[TM], b[TN];
@@ -239,6 +260,7 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const uint8_t *__restrict__ w,
         __syncthreads();
     }
 
+    if (g.kchunk) return gemm_store_partial<TM, TN>(acc, g, m0, n0, wm, wn, lane);
     gemm_epilogue<EPI, TM, TN>(acc, g, m0, n0, wm, wn, lane);
 }
 
@@ -369,21 +391,7 @@ __global__ __launch_bounds__(256) void k_gemm_h16(const uint8_t *__restrict__ w,
         }
         __syncthreads();
     }
-    if (g.kchunk) {  // split K: this block's partial sums, no epilogue
-        float *ws = g.ws + int64_t(blockIdx.z) * g.m * g.n;
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int col = n0 + wn * 16 * TN + j * 16 + (lane & 15);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const int row = m0 + wm * 16 * TM + i * 16 + 4 * (lane >> 4) + v;
-                    if (row < g.m && col < g.n) ws[int64_t(row) * g.n + col] = acc[i][j][v];
-                }
-            }
-        return;
-    }
+    if (g.kchunk) return gemm_store_partial<TM, TN>(acc, g, m0, n0, wm, wn, lane);
     gemm_epilogue<EPI, TM, TN>(acc, g, m0, n0, wm, wn, lane);
 }
 
@@ -524,21 +532,7 @@ __global__ __launch_bounds__(256) void k_gemm_h16b(const uint8_t *__restrict__ w
             __syncthreads();
         }
     }
-    if (g.kchunk) {  // split K: this block's partial sums, no epilogue
-        float *ws = g.ws + int64_t(blockIdx.z) * g.m * g.n;
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int col = n0 + wn * 32 + j * 16 + (lane & 15);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const int row = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + v;
-                    if (row < g.m && col < g.n) ws[int64_t(row) * g.n + col] = acc[i][j][v];
-                }
-            }
-        return;
-    }
+    if (g.kchunk) return gemm_store_partial<2, 2>(acc, g, m0, n0, wm, wn, lane);
     gemm_epilogue<EPI, 2, 2>(acc, g, m0, n0, wm, wn, lane);
 }
 

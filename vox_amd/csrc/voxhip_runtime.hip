@@ -2072,6 +2072,7 @@ void cosy_conv(const Cosy &E, const F5Conv &cv, int epi, const float *X, int64_t
     GemmArgs ga{};
     ga.bias = cv.b; ga.y = Y; ga.lda = ldx; ga.ldy = ldy; ga.m = int32_t(2 * E.T); ga.n = cv.cout;
     ga.cig = cv.cin; ga.ksize = cv.K; ga.K = cv.kpad; ga.seq = E.T; ga.causal = 1;
+    ga.ws = g.gemm_ws; ga.ws_cap = kGemmWsFloats;  // split K when the 64 x 64 tiles leave the CUs idle
     HIPCHECK(launch_conv_gemm(epi, cv.w, X, ga, 1, s));
 }
 
