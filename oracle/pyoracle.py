@@ -24,13 +24,41 @@ class VoMat(C.Structure):
 
 class VoLayer(C.Structure):
     _fields_ = [(n, VoMat) for n in ("q", "k", "v", "o", "gate", "up", "down")] + \
-               [(n, C.c_void_p) for n in ("qn", "kn", "ln1", "ln2")]
+               [(n, C.c_void_p) for n in ("qn", "kn", "ln1", "ln2", "attn_scale", "mlp_scale")]
 
 
 class VoXfmr(C.Structure):
     _fields_ = [("n_layers", C.c_int32), ("layers", C.POINTER(VoLayer)), ("final_norm", C.c_void_p),
                 ("hidden", C.c_int32), ("heads", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
-                ("inter", C.c_int32), ("eps", C.c_float), ("inv_freq", C.c_void_p)]
+                ("inter", C.c_int32), ("eps", C.c_float), ("inv_freq", C.c_void_p), ("window", C.c_int32)]
+
+
+class VoCConv(C.Structure):
+    _fields_ = [("w", VoMat), ("K", C.c_int32), ("cin", C.c_int32), ("cout", C.c_int32), ("dil", C.c_int32)]
+
+
+class VoSnake(C.Structure):
+    _fields_ = [("a", C.c_void_p), ("inv_b", C.c_void_p)]
+
+
+class VoCodecUp(C.Structure):
+    _fields_ = [("tr", VoMat), ("tr_b", C.c_void_p), ("K", C.c_int32), ("dw_w", C.c_void_p), ("dw_b", C.c_void_p),
+                ("dw_K", C.c_int32), ("ln_w", C.c_void_p), ("ln_b", C.c_void_p), ("gamma", C.c_void_p), ("pw1", VoMat),
+                ("pw2", VoMat)]
+
+
+class VoCodecBlock(C.Structure):
+    _fields_ = [("act", VoSnake), ("tr", VoMat), ("tr_b", C.c_void_p), ("K", C.c_int32), ("stride", C.c_int32),
+                ("cin", C.c_int32), ("cout", C.c_int32), ("a1", VoSnake * 3), ("a2", VoSnake * 3), ("c1", VoCConv * 3),
+                ("c2", VoCConv * 3)]
+
+
+class VoCodec(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("codebook_size", "codebook_dim", "latent", "quantizers", "n_up", "n_blocks")] + \
+               [("q_first", C.POINTER(VoMat)), ("q_rest", C.POINTER(VoMat)), ("q_first_out", VoMat), ("q_rest_out", VoMat),
+                ("pre_conv", VoCConv), ("pt_in", VoMat), ("pt_out", VoMat), ("pt", VoXfmr),
+                ("ups", C.POINTER(VoCodecUp)), ("conv0", VoCConv), ("blocks", C.POINTER(VoCodecBlock)),
+                ("final_act", VoSnake), ("final_conv", VoCConv)]
 
 
 class VoKV(C.Structure):
@@ -124,6 +152,13 @@ def _declare(lib, prefix):
             "attention_nn": (None, [P, P, P, I32, I32, I32, I32, F, P]),
             "causal_conv": (None, [P, P, I32, P]),
             "cosy_step": (C.c_int, [P, I32, P, P, P]),
+            "snake_params": (None, [P, P, I64, P, P]),
+            "codec_state_new": (P, [P, I64]),
+            "codec_state_clone": (P, [P]),
+            "codec_state_free": (None, [P]),
+            "codec_quantize": (C.c_int, [P, P, I32, P]),
+            "codec_forward": (I64, [P, P, P, I32, P]),
+            "codec_spf": (I64, [P]),
             "lm_step": (I32, [P, I32, P, I32, I64, I32, I32, F, I32, I32, F, U64, U32]),
             "noise": (None, [U64, U32, C.c_size_t, P]),
             "f16_to_f32": (F, [C.c_uint16]),
@@ -154,6 +189,13 @@ def _declare(lib, prefix):
             "attention_nn": (None, [P, P, P, I32, I32, I32, I32, F, P]),
             "causal_conv": (None, [P, P, I32, P]),
             "cosy_step": (C.c_int, [P, I32, P, P, P]),
+            "tmod_write": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int, P, P, P, P, P, P]),
+            "codec_open": (P, [C.c_char_p]),
+            "codec_close": (None, [P]),
+            "codec_state_new": (P, [P]),
+            "codec_state_clone": (P, [P, P]),
+            "codec_state_free": (None, [P]),
+            "codec_forward": (I64, [P, P, P, C.c_int, P]),
         })
     for name, (res, args) in sig.items():
         fn = getattr(lib, prefix + name)
@@ -519,3 +561,163 @@ def cosy_step(m, T, inp, tb, use_ref=False):
     rc = (ref().ref_cosy_step if use_ref else lib().vo_cosy_step)(C.byref(m.c), T, _p(inp), _p(tb), _p(out))
     assert rc == 0, rc
     return out
+
+
+# ---- the Qwen3-TTS codec decoder (qwen3.cpp:225-283 load_codec, :366-481 codec_forward)
+class Codec:
+    """The codec decoder in the oracle's struct layout, from its tensors by .tmod name (t: name -> f32 array, 2-D
+    weights as qwen3.cpp reads them) and the codec config cc (the manifest's codec keys)."""
+
+    def __init__(self, cc, t):
+        f = lambda a: np.ascontiguousarray(a, np.float32)
+        self.keep = []
+        self.cc = cc
+
+        def mat(name, bias=None):
+            w = f(t[name])
+            b = None if bias is None else f(t[bias])
+            m = Mat(F32, w, w.shape[0], w.shape[1] if w.ndim > 1 else 1, None, b)
+            self.keep.append(m)
+            return m.c
+
+        def vec(name):
+            a = f(t[name]).ravel()
+            self.keep.append(a)
+            return _p(a)
+
+        def conv(p, K, cin, cout, dil=1):
+            return VoCConv(mat(p + ".weight", p + ".bias"), K, cin, cout, dil)
+
+        def snake(p):
+            al, be = f(t[p + ".alpha"]).ravel(), f(t[p + ".beta"]).ravel()
+            a, ib = np.empty_like(al), np.empty_like(be)
+            lib().vo_snake_params(_p(al), _p(be), al.size, _p(a), _p(ib))
+            self.keep += [a, ib]
+            return VoSnake(_p(a), _p(ib))
+        Q, CD, L = cc["num_quantizers"], cc["codebook_dim"], cc["latent_dim"]
+        H, heads, kvh = cc["hidden_size"], cc["num_attention_heads"], cc["num_key_value_heads"]
+        hd = cc.get("head_dim", H // heads)
+        qf = (VoMat * 1)(mat("codec.quantizer.rvq_first.vq.layers.0._codebook.embedding"))
+        qr = (VoMat * max(1, Q - 1))(*[mat(f"codec.quantizer.rvq_rest.vq.layers.{i}._codebook.embedding") for i in range(Q - 1)])
+        layers = (VoLayer * cc["num_hidden_layers"])()
+        for i in range(cc["num_hidden_layers"]):
+            p = f"codec.pre_transformer.layers.{i}."
+            lw = layers[i]
+            for n, k in (("q", "self_attn.q_proj"), ("k", "self_attn.k_proj"), ("v", "self_attn.v_proj"), ("o", "self_attn.o_proj"),
+                         ("gate", "mlp.gate_proj"), ("up", "mlp.up_proj"), ("down", "mlp.down_proj")):
+                setattr(lw, n, mat(p + k + ".weight"))
+            lw.ln1, lw.ln2 = vec(p + "input_layernorm.weight"), vec(p + "post_attention_layernorm.weight")
+            lw.attn_scale, lw.mlp_scale = vec(p + "self_attn_layer_scale.scale"), vec(p + "mlp_layer_scale.scale")
+        theta = cc.get("rope_theta", 10000.0)
+        inv = np.empty(hd // 2, np.float32)
+        lib().vo_rope_inv_freq(hd, theta, _p(inv))
+        self.keep += [qf, qr, layers, inv]
+        pt = VoXfmr(cc["num_hidden_layers"], layers, vec("codec.pre_transformer.norm.weight"), H, heads, kvh, hd,
+                    cc["intermediate_size"], cc.get("rms_norm_eps", 1e-5), _p(inv), cc["sliding_window"])
+        ratios, rates, dec = cc["upsampling_ratios"], cc["upsample_rates"], cc["decoder_dim"]
+        ups = (VoCodecUp * max(1, len(ratios)))()
+        for s_, r in enumerate(ratios):
+            p = f"codec.upsample.{s_}."
+            ups[s_] = VoCodecUp(mat(p + "0.conv.weight"), vec(p + "0.conv.bias"), r, vec(p + "1.dwconv.conv.weight"),
+                                vec(p + "1.dwconv.conv.bias"), 7, vec(p + "1.norm.weight"), vec(p + "1.norm.bias"),
+                                vec(p + "1.gamma"), mat(p + "1.pwconv1.weight", p + "1.pwconv1.bias"),
+                                mat(p + "1.pwconv2.weight", p + "1.pwconv2.bias"))
+        blocks = (VoCodecBlock * max(1, len(rates)))()
+        for b, r in enumerate(rates):
+            ind, outd = dec >> b, dec >> (b + 1)
+            p = f"codec.decoder.{b + 1}.block."
+            blk = blocks[b]
+            blk.act = snake(p + "0")
+            blk.tr, blk.tr_b, blk.K, blk.stride, blk.cin, blk.cout = mat(p + "1.conv.weight"), vec(p + "1.conv.bias"), 2 * r, r, ind, outd
+            for u, dil in enumerate((1, 3, 9)):
+                q = p + f"{u + 2}."
+                blk.a1[u], blk.a2[u] = snake(q + "act1"), snake(q + "act2")
+                blk.c1[u] = conv(q + "conv1.conv", 7, outd, outd, dil)
+                blk.c2[u] = conv(q + "conv2.conv", 1, outd, outd)
+        nb = len(rates)
+        self.keep += [ups, blocks]
+        self.c = VoCodec(cc["codebook_size"], CD, L, Q, len(ratios), nb, qf, qr,
+                         mat("codec.quantizer.rvq_first.output_proj.weight"), mat("codec.quantizer.rvq_rest.output_proj.weight"),
+                         conv("codec.pre_conv.conv", 3, CD, L), mat("codec.pre_transformer.input_proj.weight",
+                                                                    "codec.pre_transformer.input_proj.bias"),
+                         mat("codec.pre_transformer.output_proj.weight", "codec.pre_transformer.output_proj.bias"), pt, ups,
+                         conv("codec.decoder.0.conv", 7, L, dec), blocks, snake(f"codec.decoder.{nb + 1}"),
+                         conv(f"codec.decoder.{nb + 2}.conv", 7, dec >> nb, 1))
+        self.spf = lib().vo_codec_spf(C.byref(self.c))
+
+
+class CodecState:
+    """The oracle's streaming state of a Codec (cap: transformer positions it can hold)."""
+
+    def __init__(self, codec, cap=512, _ptr=None):
+        self.codec = codec
+        self.p = _ptr if _ptr else lib().vo_codec_state_new(C.byref(codec.c), cap)
+
+    def clone(self):
+        return CodecState(self.codec, _ptr=lib().vo_codec_state_clone(self.p))
+
+    def __del__(self):
+        if getattr(self, "p", None):
+            lib().vo_codec_state_free(self.p)
+            self.p = None
+
+
+def codec_quantize(codec, codes):
+    codes = np.ascontiguousarray(codes, np.int16)
+    z = np.empty((codes.shape[0], codec.cc["codebook_dim"]), np.float32)
+    assert lib().vo_codec_quantize(C.byref(codec.c), _p(codes), codes.shape[0], _p(z)) == 0
+    return z
+
+
+def codec_forward(state, z):
+    """z [F][codebook_dim] -> pcm [F * spf]; the state advances."""
+    z = np.ascontiguousarray(z, np.float32)
+    out = np.empty(z.shape[0] * state.codec.spf, np.float32)
+    n = lib().vo_codec_forward(C.byref(state.codec.c), state.p, _p(z), z.shape[0], _p(out))
+    assert n == out.size, n
+    return out
+
+
+def tmod_write(path, manifest, tensors):
+    """Writes a .tmod with the compiled reference's tmod_write (f32 tensors by name)."""
+    import json
+    names = sorted(tensors)
+    arrs = [np.ascontiguousarray(tensors[n], np.float32) for n in names]
+    nm = (C.c_char_p * len(names))(*[n.encode() for n in names])
+    dt = np.zeros(len(names), np.int32)  # DType::F32
+    nd = np.array([a.ndim for a in arrs], np.int32)
+    sh = np.array([d for a in arrs for d in a.shape], np.int64)
+    ptr = (C.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+    nb = np.array([a.nbytes for a in arrs], np.int64)
+    rc = ref().ref_tmod_write(path.encode(), json.dumps(manifest).encode(), len(names), nm, _p(dt), _p(nd), _p(sh), ptr, _p(nb))
+    assert rc == 0, rc
+
+
+class RefCodec:
+    """The reference's Qwen3Weights (codec_forward on the CPU) loaded from a .tmod written by tmod_write."""
+
+    def __init__(self, path, spf):
+        self.h = ref().ref_codec_open(path.encode())
+        assert self.h, "the reference could not load " + path
+        self.spf = spf
+
+    def state(self):
+        return ref().ref_codec_state_new(self.h)
+
+    def clone(self, s):
+        return ref().ref_codec_state_clone(self.h, s)
+
+    def free_state(self, s):
+        ref().ref_codec_state_free(s)
+
+    def forward(self, s, codes):
+        codes = np.ascontiguousarray(codes, np.int16)
+        out = np.empty(codes.shape[0] * self.spf, np.float32)
+        n = ref().ref_codec_forward(self.h, s, _p(codes), codes.shape[0], _p(out))
+        assert n == out.size, n
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            ref().ref_codec_close(self.h)
+            self.h = None

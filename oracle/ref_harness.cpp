@@ -1,8 +1,8 @@
 // ref_harness.cpp — extern "C" wrappers around the reference's own CPU functions.
 //
 // TEST INFRASTRUCTURE ONLY. oracle/Makefile compiles this file together with
-// /root/reference/src/kernels.cpp, f5_ops.cpp, gpu_stub.cpp, nn.cpp, formats.cpp
-// and resources.cpp, where they lie, into oracle/_ref/libvoxref.so. tests/ use it to pin the C
+// /root/reference/src/kernels.cpp, f5_ops.cpp, gpu_stub.cpp, nn.cpp, formats.cpp,
+// resources.cpp and qwen3.cpp, where they lie, into oracle/_ref/libvoxref.so. tests/ use it to pin the C
 // restatement (vox_oracle.c) bit for bit and to write the golden fixtures;
 // bench.py may time it as the "reference" CPU baseline. Nothing here is part
 // of the product, and no reference source is copied into this repository.
@@ -12,6 +12,7 @@
 #include "f5_ops.hpp"    // /root/reference/src (Conv1d)
 #include "kernels.hpp"   // /root/reference/src
 #include "nn.hpp"        // /root/reference/src (the vocoder / estimator layers)
+#include "qwen3.hpp"     // /root/reference/src (Qwen3Weights::codec_forward)
 #include "sampling.hpp"  // /root/reference/src
 #include "vox_oracle.h"  // struct layouts shared with the restatement
 
@@ -33,7 +34,7 @@ Mat to_mat(const vo_mat &m) {
 TransformerW to_xfmr(const vo_xfmr &x, double theta) {
     TransformerW w;
     w.hidden = x.hidden; w.heads = x.heads; w.kv_heads = x.kv_heads; w.head_dim = x.head_dim; w.inter = x.inter;
-    w.eps = x.eps; w.theta = theta; w.final_norm = x.final_norm;
+    w.eps = x.eps; w.theta = theta; w.final_norm = x.final_norm; w.window = x.window;
     w.inv_freq.assign(x.inv_freq, x.inv_freq + x.head_dim / 2);
     for (int i = 0; i < x.n_layers; ++i) {
         const vo_layer &l = x.layers[i];
@@ -41,6 +42,7 @@ TransformerW to_xfmr(const vo_xfmr &x, double theta) {
         L.q = to_mat(l.q); L.k = to_mat(l.k); L.v = to_mat(l.v); L.o = to_mat(l.o);
         L.gate = to_mat(l.gate); L.up = to_mat(l.up); L.down = to_mat(l.down);
         L.qn = l.qn; L.kn = l.kn; L.ln1 = l.ln1; L.ln2 = l.ln2;
+        L.attn_scale = l.attn_scale; L.mlp_scale = l.mlp_scale;
         w.layers.push_back(L);
     }
     return w;
@@ -299,6 +301,59 @@ int ref_cosy_step(const vo_cosy *m, int T, const float *in, const float *tb, flo
         to_nn_conv(m->final_proj).forward(a.data(), R, o);
         std::memcpy(out, o.data(), o.size() * 4);
         return 0;
+    } catch (...) {
+        return -2;
+    }
+}
+
+// ---- Qwen3-TTS codec decoder: a .tmod written by the reference's own tmod_write, loaded as Qwen3Weights, decoded by
+// Qwen3Weights::codec_forward on the CPU (qwen3.cpp:366-481)
+// tensors: n entries of name, DType index, ndim, shape (flat), data pointer and byte count
+int ref_tmod_write(const char *path, const char *manifest, int n, const char *const *names, const int32_t *dtypes,
+                   const int32_t *ndims, const int64_t *shapes, const void *const *data, const int64_t *nbytes) {
+    try {
+        std::map<std::string, Tensor> blobs;
+        int64_t so = 0;
+        for (int i = 0; i < n; ++i) {
+            Tensor t;
+            t.dtype = DType(dtypes[i]);
+            t.shape.assign(shapes + so, shapes + so + ndims[i]);
+            so += ndims[i];
+            const uint8_t *p = static_cast<const uint8_t *>(data[i]);
+            t.bytes.assign(p, p + nbytes[i]);
+            blobs[names[i]] = std::move(t);
+        }
+        tmod_write(path, json::parse(manifest), blobs);
+        return 0;
+    } catch (...) {
+        return -2;
+    }
+}
+struct RefCodec {
+    std::unique_ptr<Qwen3Weights> w;
+};
+void *ref_codec_open(const char *path) {
+    try {
+        RefCodec *c = new RefCodec();
+        c->w.reset(new Qwen3Weights(std::make_shared<TmodFile>(path)));
+        return c;
+    } catch (...) {
+        return nullptr;
+    }
+}
+void ref_codec_close(void *c) { delete static_cast<RefCodec *>(c); }
+void *ref_codec_state_new(void *c) { return new CodecState(static_cast<RefCodec *>(c)->w->new_codec_state()); }
+void *ref_codec_state_clone(void *c, void *s) {
+    return new CodecState(static_cast<RefCodec *>(c)->w->clone_codec_state(*static_cast<CodecState *>(s)));
+}
+void ref_codec_state_free(void *s) { delete static_cast<CodecState *>(s); }
+// codes [F][quantizers] -> pcm (F * samples per frame); returns the sample count, -2 on an error
+int64_t ref_codec_forward(void *c, void *s, const int16_t *codes, int F, float *pcm) {
+    try {
+        std::vector<float> out;
+        static_cast<RefCodec *>(c)->w->codec_forward(*static_cast<CodecState *>(s), codes, F, out);
+        std::memcpy(pcm, out.data(), out.size() * 4);
+        return int64_t(out.size());
     } catch (...) {
         return -2;
     }

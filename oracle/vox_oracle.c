@@ -615,16 +615,24 @@ static void run_layers(const vo_xfmr *w, vo_kv *kv, float *h, int64_t m, int32_t
                 V[(pos0 + i) * kd + e] = kv_round(v[i * kd + e], kv->kv_f16);
             }
         for (int64_t t = 0; t < m * nh; ++t) {
-            const int64_t i = t / nh, hh = t % nh, gk = hh / group;
-            attend(q + i * qd + hh * hd, K, V, pos0 + i + 1, kd, gk * hd, hd, scale, sc, ao + i * qd + hh * hd);
+            const int64_t i = t / nh, hh = t % nh, gk = hh / group, last = pos0 + i;
+            const int64_t first = w->window > 0 && last - w->window + 1 > 0 ? last - w->window + 1 : 0;
+            attend(q + i * qd + hh * hd, K + first * kd, V + first * kd, last - first + 1, kd, gk * hd, hd, scale, sc,
+                   ao + i * qd + hh * hd);
         }
         vo_matmul(&L->o, ao, m, o, kv->avx2);
+        if (L->attn_scale)
+            for (int64_t i = 0; i < m; ++i)
+                for (int64_t e = 0; e < H; ++e) o[i * H + e] *= L->attn_scale[e];
         for (int64_t i = 0; i < m * H; ++i) h[i] += o[i];
         for (int64_t i = 0; i < m; ++i) vo_rmsnorm(h + i * H, L->ln2, H, w->eps, xn + i * H);
         vo_matmul(&L->gate, xn, m, g, kv->avx2);
         vo_matmul(&L->up, xn, m, u, kv->avx2);
         for (int64_t i = 0; i < m * I; ++i) g[i] = vo_silu(g[i]) * u[i];
         vo_matmul(&L->down, g, m, d, kv->avx2);
+        if (L->mlp_scale)
+            for (int64_t i = 0; i < m; ++i)
+                for (int64_t e = 0; e < H; ++e) d[i * H + e] *= L->mlp_scale[e];
         for (int64_t i = 0; i < m * H; ++i) h[i] += d[i];
     }
     free(xn); free(q); free(k); free(v); free(ao); free(o); free(g); free(u); free(d); free(sc);
@@ -1071,4 +1079,241 @@ int vo_cosy_step(const vo_cosy *m, int32_t T, const float *in, const float *tb, 
     vo_causal_conv(&m->final_proj, a, (int32_t)R, out); /* K 1 over all rows */
     free(a); free(b); free(skip); free(cat);
     return 0;
+}
+
+/* ------------------------------------------------------------------ Qwen3-TTS codec decoder */
+struct vo_codec_state {
+    const vo_codec *c;
+    float *pre_h, *conv0_h, *final_h; /* conv histories [(K - 1) dil][cin] */
+    float **up_dw_h;                  /* [n_up][(dw_K - 1)][latent] */
+    float **tail;                     /* [n_blocks][(K - stride)][cout] */
+    float **ru_h;                     /* [n_blocks * 3][(K - 1) dil][cout] */
+    vo_kv kv;                         /* f32, [layers][cap][kd] */
+    int64_t frames;
+};
+
+static size_t hist_elems(const vo_cconv *c) { return (size_t)(c->K - 1) * (size_t)c->dil * (size_t)c->cin; }
+static float *zalloc(size_t n) { return (float *)calloc(n ? n : 1, sizeof(float)); }
+
+vo_codec_state *vo_codec_state_new(const vo_codec *c, int64_t cap) {
+    vo_codec_state *s = (vo_codec_state *)calloc(1, sizeof(vo_codec_state));
+    s->c = c;
+    s->pre_h = zalloc(hist_elems(&c->pre_conv));
+    s->conv0_h = zalloc(hist_elems(&c->conv0));
+    s->final_h = zalloc(hist_elems(&c->final_conv));
+    s->up_dw_h = (float **)calloc((size_t)c->n_up + 1, sizeof(float *));
+    for (int i = 0; i < c->n_up; ++i) s->up_dw_h[i] = zalloc((size_t)(c->ups[i].dw_K - 1) * (size_t)c->latent);
+    s->tail = (float **)calloc((size_t)c->n_blocks + 1, sizeof(float *));
+    s->ru_h = (float **)calloc(3 * (size_t)c->n_blocks + 1, sizeof(float *));
+    for (int b = 0; b < c->n_blocks; ++b) {
+        const vo_codec_block *d = &c->blocks[b];
+        s->tail[b] = zalloc((size_t)(d->K - d->stride) * (size_t)d->cout);
+        for (int u = 0; u < 3; ++u) s->ru_h[3 * b + u] = zalloc(hist_elems(&d->c1[u]));
+    }
+    const int64_t kd = (int64_t)c->pt.kv_heads * c->pt.head_dim;
+    s->kv.k = zalloc((size_t)(c->pt.n_layers * cap * kd));
+    s->kv.v = zalloc((size_t)(c->pt.n_layers * cap * kd));
+    s->kv.cap = cap;
+    return s;
+}
+
+static float *dup(const float *p, size_t n) {
+    float *d = zalloc(n);
+    memcpy(d, p, n * sizeof(float));
+    return d;
+}
+
+vo_codec_state *vo_codec_state_clone(const vo_codec_state *src) {
+    const vo_codec *c = src->c;
+    vo_codec_state *s = (vo_codec_state *)calloc(1, sizeof(vo_codec_state));
+    *s = *src;
+    s->pre_h = dup(src->pre_h, hist_elems(&c->pre_conv));
+    s->conv0_h = dup(src->conv0_h, hist_elems(&c->conv0));
+    s->final_h = dup(src->final_h, hist_elems(&c->final_conv));
+    s->up_dw_h = (float **)calloc((size_t)c->n_up + 1, sizeof(float *));
+    for (int i = 0; i < c->n_up; ++i) s->up_dw_h[i] = dup(src->up_dw_h[i], (size_t)(c->ups[i].dw_K - 1) * (size_t)c->latent);
+    s->tail = (float **)calloc((size_t)c->n_blocks + 1, sizeof(float *));
+    s->ru_h = (float **)calloc(3 * (size_t)c->n_blocks + 1, sizeof(float *));
+    for (int b = 0; b < c->n_blocks; ++b) {
+        const vo_codec_block *d = &c->blocks[b];
+        s->tail[b] = dup(src->tail[b], (size_t)(d->K - d->stride) * (size_t)d->cout);
+        for (int u = 0; u < 3; ++u) s->ru_h[3 * b + u] = dup(src->ru_h[3 * b + u], hist_elems(&d->c1[u]));
+    }
+    const int64_t kd = (int64_t)c->pt.kv_heads * c->pt.head_dim;
+    s->kv.k = dup(src->kv.k, (size_t)(c->pt.n_layers * src->kv.cap * kd));
+    s->kv.v = dup(src->kv.v, (size_t)(c->pt.n_layers * src->kv.cap * kd));
+    return s;
+}
+
+void vo_codec_state_free(vo_codec_state *s) {
+    if (!s) return;
+    const vo_codec *c = s->c;
+    free(s->pre_h); free(s->conv0_h); free(s->final_h);
+    for (int i = 0; i < c->n_up; ++i) free(s->up_dw_h[i]);
+    for (int b = 0; b < c->n_blocks; ++b) {
+        free(s->tail[b]);
+        for (int u = 0; u < 3; ++u) free(s->ru_h[3 * b + u]);
+    }
+    free(s->up_dw_h); free(s->tail); free(s->ru_h); free(s->kv.k); free(s->kv.v);
+    free(s);
+}
+
+int64_t vo_codec_spf(const vo_codec *c) {
+    int64_t p = 1;
+    for (int i = 0; i < c->n_up; ++i) p *= c->ups[i].K;
+    for (int b = 0; b < c->n_blocks; ++b) p *= c->blocks[b].stride;
+    return p;
+}
+
+int vo_codec_quantize(const vo_codec *c, const int16_t *codes, int32_t F, float *z) {
+    const int Q = c->quantizers, dim = c->codebook_dim / 2, CD = c->codebook_dim;
+    float *s1 = zalloc((size_t)F * dim), *s2 = zalloc((size_t)F * dim), *tmp = zalloc((size_t)dim), *z2 = zalloc((size_t)F * CD);
+    int rc = 0;
+    for (int t = 0; t < F && !rc; ++t) {
+        const int16_t *cd = codes + (size_t)t * Q;
+        for (int q = 0; q < Q; ++q)
+            if (cd[q] < 0 || cd[q] >= c->codebook_size) rc = -1;
+        if (rc) break;
+        vo_mat_row(&c->q_first[0], cd[0], s1 + (size_t)t * dim);
+        for (int q = 1; q < Q; ++q) {
+            vo_mat_row(&c->q_rest[q - 1], cd[q], tmp);
+            for (int i = 0; i < dim; ++i) s2[(size_t)t * dim + i] += tmp[i];
+        }
+    }
+    if (!rc) {
+        vo_matmul(&c->q_first_out, s1, F, z, 1);
+        vo_matmul(&c->q_rest_out, s2, F, z2, 1);
+        for (size_t i = 0; i < (size_t)F * CD; ++i) z[i] += z2[i];
+    }
+    free(s1); free(s2); free(tmp); free(z2);
+    return rc;
+}
+
+/* conv_stream (qwen3.cpp:102-121): y = conv([hist; x]) (+ bias through the matmul), hist <- the last rows */
+static void conv_stream(const vo_cconv *c, float *hist, const float *x, int64_t T, float *y) {
+    const int64_t ctx = (int64_t)(c->K - 1) * c->dil, cin = c->cin;
+    if (c->K == 1) { vo_matmul(&c->w, x, T, y, 1); return; }
+    float *ext = zalloc((size_t)((ctx + T) * cin)), *col = zalloc((size_t)(T * c->K * cin));
+    memcpy(ext, hist, sizeof(float) * (size_t)(ctx * cin));
+    memcpy(ext + ctx * cin, x, sizeof(float) * (size_t)(T * cin));
+    for (int64_t t = 0; t < T; ++t)
+        for (int k = 0; k < c->K; ++k)
+            memcpy(col + (t * c->K + k) * cin, ext + (t + (int64_t)k * c->dil) * cin, sizeof(float) * (size_t)cin);
+    vo_matmul(&c->w, col, T, y, 1);
+    memcpy(hist, ext + T * cin, sizeof(float) * (size_t)(ctx * cin));
+    free(ext); free(col);
+}
+
+/* dwconv_stream (qwen3.cpp:123-137) */
+static void dwconv_stream(const vo_codec_up *u, int C, float *hist, const float *x, int64_t T, float *y) {
+    const int64_t ctx = u->dw_K - 1;
+    float *ext = zalloc((size_t)((ctx + T) * C));
+    memcpy(ext, hist, sizeof(float) * (size_t)(ctx * C));
+    memcpy(ext + ctx * C, x, sizeof(float) * (size_t)(T * C));
+    for (int64_t t = 0; t < T; ++t)
+        for (int ch = 0; ch < C; ++ch) {
+            float acc = u->dw_b[ch];
+            for (int k = 0; k < u->dw_K; ++k) acc += u->dw_w[(size_t)ch * u->dw_K + k] * ext[(t + k) * C + ch];
+            y[t * C + ch] = acc;
+        }
+    memcpy(hist, ext + T * C, sizeof(float) * (size_t)(ctx * C));
+    free(ext);
+}
+
+/* trans_stream (qwen3.cpp:139-161): K <= 2 stride; output p gathers frames p / s and p / s - 1; the last K - s rows go
+ * to the tail */
+static void trans_stream(const vo_mat *w, const float *bias, int K, int s, int co, float *tail, const float *x, int64_t T,
+                         float *y) {
+    const int64_t tr = K - s;
+    float *tmp = zalloc((size_t)(T * K * co)), *nt = zalloc((size_t)(tr * co));
+    vo_matmul(w, x, T, tmp, 1);
+    for (int64_t p = 0; p < T * s + tr; ++p) {
+        const int64_t t = p / s, k = p - t * s;
+        for (int o = 0; o < co; ++o) {
+            float v = p < tr ? tail[p * co + o] : 0.f;
+            if (t < T && k < K) v += tmp[(t * K + k) * co + o];
+            if (t >= 1 && k + s < K) v += tmp[((t - 1) * K + k + s) * co + o];
+            if (p < T * s) y[p * co + o] = v + bias[o];
+            else nt[(p - T * s) * co + o] = v;
+        }
+    }
+    memcpy(tail, nt, sizeof(float) * (size_t)(tr * co));
+    free(tmp); free(nt);
+}
+
+/* snake_apply (qwen3.cpp:80-89): x + inv_b sin(a x)^2 */
+static void snake(const vo_snake *s, float *x, int64_t T, int C) {
+    for (int64_t t = 0; t < T; ++t)
+        for (int c = 0; c < C; ++c) {
+            const float v = x[t * C + c], sn = sinf(v * s->a[c]);
+            x[t * C + c] = v + s->inv_b[c] * sn * sn;
+        }
+}
+
+int64_t vo_codec_forward(const vo_codec *c, vo_codec_state *s, const float *z, int32_t F, float *pcm) {
+    const int L = c->latent, H = c->pt.hidden;
+    const int64_t T = F;
+    if (s->kv.len + T > s->kv.cap) return -1;
+    float *lat = zalloc((size_t)(T * L)), *hin = zalloc((size_t)(T * H)), *hout = zalloc((size_t)(T * H));
+    conv_stream(&c->pre_conv, s->pre_h, z, T, lat);
+    vo_matmul(&c->pt_in, lat, T, hin, 1);
+    vo_transformer_forward(&c->pt, &s->kv, hin, T, NULL, hout);
+    vo_matmul(&c->pt_out, hout, T, lat, 1);
+    free(hin); free(hout);
+    float *cur = lat;
+    int64_t len = T;
+    for (int si = 0; si < c->n_up; ++si) { /* qwen3.cpp:416-441 */
+        const vo_codec_up *u = &c->ups[si];
+        float *y = zalloc((size_t)(len * u->K * L));
+        trans_stream(&u->tr, u->tr_b, u->K, u->K, L, NULL, cur, len, y);
+        len *= u->K;
+        float *dw = zalloc((size_t)(len * L)), *nrm = zalloc((size_t)(len * L)), *h1 = zalloc((size_t)(len * u->pw1.rows));
+        float *h2 = zalloc((size_t)(len * L));
+        dwconv_stream(u, L, s->up_dw_h[si], y, len, dw);
+        for (int64_t t = 0; t < len; ++t) vo_layernorm(dw + t * L, u->ln_w, u->ln_b, L, 1e-6f, nrm + t * L);
+        vo_matmul(&u->pw1, nrm, len, h1, 1);
+        for (int64_t i = 0; i < len * u->pw1.rows; ++i) h1[i] = vo_gelu_erf(h1[i]);
+        vo_matmul(&u->pw2, h1, len, h2, 1);
+        for (int64_t t = 0; t < len; ++t)
+            for (int i = 0; i < L; ++i) y[t * L + i] += u->gamma[i] * h2[t * L + i];
+        free(dw); free(nrm); free(h1); free(h2); free(cur);
+        cur = y;
+    }
+    float *x = zalloc((size_t)(len * c->conv0.cout));
+    conv_stream(&c->conv0, s->conv0_h, cur, len, x);
+    free(cur);
+    int ch = c->conv0.cout;
+    for (int b = 0; b < c->n_blocks; ++b) { /* qwen3.cpp:446-472 */
+        const vo_codec_block *d = &c->blocks[b];
+        const int out = d->cout;
+        snake(&d->act, x, len, ch);
+        float *y = zalloc((size_t)(len * d->stride * out));
+        trans_stream(&d->tr, d->tr_b, d->K, d->stride, out, s->tail[b], x, len, y);
+        len *= d->stride;
+        ch = out;
+        float *t1 = zalloc((size_t)(len * ch)), *t2 = zalloc((size_t)(len * ch));
+        for (int u = 0; u < 3; ++u) {
+            memcpy(t1, y, sizeof(float) * (size_t)(len * ch));
+            snake(&d->a1[u], t1, len, ch);
+            conv_stream(&d->c1[u], s->ru_h[3 * b + u], t1, len, t2);
+            snake(&d->a2[u], t2, len, ch);
+            conv_stream(&d->c2[u], NULL, t2, len, t1);
+            for (int64_t i = 0; i < len * ch; ++i) y[i] += t1[i];
+        }
+        free(t1); free(t2); free(x);
+        x = y;
+    }
+    snake(&c->final_act, x, len, ch);
+    conv_stream(&c->final_conv, s->final_h, x, len, pcm);
+    for (int64_t i = 0; i < len; ++i) pcm[i] = fminf(1.0f, fmaxf(-1.0f, pcm[i]));
+    free(x);
+    s->frames += F;
+    return len;
+}
+
+void vo_snake_params(const float *alpha, const float *beta, int64_t n, float *a, float *inv_b) {
+    for (int64_t i = 0; i < n; ++i) {
+        a[i] = expf(alpha[i]);
+        inv_b[i] = 1.0f / (expf(beta[i]) + 1e-9f);
+    }
 }

@@ -97,6 +97,7 @@ typedef struct {
     vo_mat q, k, v, o, gate, up, down;
     const float *qn, *kn; /* per-head RMSNorm weights [head_dim] or NULL */
     const float *ln1, *ln2;
+    const float *attn_scale, *mlp_scale; /* layer scales [hidden] or NULL (the codec's pre-transformer) */
 } vo_layer;
 
 typedef struct {
@@ -106,6 +107,7 @@ typedef struct {
     int32_t hidden, heads, kv_heads, head_dim, inter;
     float eps;
     const float *inv_freq; /* [head_dim/2] */
+    int32_t window;        /* sliding window (0: full attention): a row at position p sees keys (p - window, p] */
 } vo_xfmr;
 
 /* KV cache: k, v are [n_layers][cap][kv_heads*head_dim] floats. kv_f16 = 1 rounds every appended
@@ -118,7 +120,7 @@ typedef struct {
     int32_t avx2;
 } vo_kv;
 
-/* transformer_forward (kernels.cpp:760-844), full attention (window 0), no layer scales.
+/* transformer_forward (kernels.cpp:760-844), with its sliding window and layer scales.
  * Returns 0, or -1 when the cache is too small. */
 int vo_transformer_forward(const vo_xfmr *w, vo_kv *kv, const float *x, int64_t m, float *out_last, float *out_all);
 /* Layers [first, first + count) of transformer_forward on the residual stream x [m][hidden] (rows at positions
@@ -209,6 +211,67 @@ typedef struct {
 /* One estimator call (cosyvoice.cpp:839-863): in [2][T][4 M] ([x | mu | spks | cond] of both passes), tb
  * [2 + n_mid][C] (the resnets' time biases) -> out [2][T][M]. */
 int vo_cosy_step(const vo_cosy *m, int32_t T, const float *in, const float *tb, float *out);
+
+/* ---- Qwen3-TTS codec decoder (qwen3.cpp:102-161, :366-481) ---- */
+/* A streaming conv: w [cout][K * cin] (+ bias in w.bias), dilation dil, causal with a history of (K - 1) dil rows. */
+typedef struct {
+    vo_mat w;
+    int32_t K, cin, cout, dil;
+} vo_cconv;
+/* Snake: a = exp(alpha), inv_b = 1 / (exp(beta) + 1e-9) per channel (qwen3.cpp:80-89). */
+typedef struct {
+    const float *a, *inv_b;
+} vo_snake;
+/* An upsample stage (qwen3.cpp:254-267): transposed conv K = stride, w [K latent][latent] + bias tr_b, then a
+ * ConvNeXt block: causal depthwise conv (w [C][dw_K], bias), LayerNorm (1e-6), pw1 + GELU-erf, pw2, x += gamma (.). */
+typedef struct {
+    vo_mat tr;
+    const float *tr_b;
+    int32_t K;
+    const float *dw_w, *dw_b;
+    int32_t dw_K;
+    const float *ln_w, *ln_b, *gamma;
+    vo_mat pw1, pw2;
+} vo_codec_up;
+/* A decoder block (qwen3.cpp:269-283): Snake, transposed conv (K = 2 stride, w [K cout][cin] + tr_b) with its
+ * overlap tail, three residual units (Snake, conv K 7 dilation 1 / 3 / 9, Snake, conv K 1). */
+typedef struct {
+    vo_snake act;
+    vo_mat tr;
+    const float *tr_b;
+    int32_t K, stride, cin, cout;
+    vo_snake a1[3], a2[3];
+    vo_cconv c1[3], c2[3];
+} vo_codec_block;
+typedef struct {
+    int32_t codebook_size, codebook_dim, latent, quantizers, n_up, n_blocks;
+    const vo_mat *q_first, *q_rest; /* [1], [quantizers - 1]: [codebook_size][codebook_dim / 2] */
+    vo_mat q_first_out, q_rest_out; /* [codebook_dim][codebook_dim / 2] */
+    vo_cconv pre_conv;
+    vo_mat pt_in, pt_out;
+    vo_xfmr pt; /* window, layer scales, no q/k norm */
+    const vo_codec_up *ups;
+    vo_cconv conv0;
+    const vo_codec_block *blocks;
+    vo_snake final_act;
+    vo_cconv final_conv;
+} vo_codec;
+/* Streaming state (CodecState, qwen3.hpp:58-66): histories, transposed-conv tails, the transformer's f32 cache.
+ * Created zeroed for a codec and a cache capacity (positions); vo_codec_state_free releases it. */
+typedef struct vo_codec_state vo_codec_state;
+vo_codec_state *vo_codec_state_new(const vo_codec *c, int64_t cap);
+vo_codec_state *vo_codec_state_clone(const vo_codec_state *s);
+void vo_codec_state_free(vo_codec_state *s);
+/* The quantizer of codec_forward (qwen3.cpp:371-388): codes [F][quantizers] -> z [F][codebook_dim]. Returns -1 for a
+ * code out of range. */
+int vo_codec_quantize(const vo_codec *c, const int16_t *codes, int32_t F, float *z);
+/* The rest of codec_forward (qwen3.cpp:405-480): z [F][codebook_dim] -> pcm [F * samples per frame], clamped to
+ * [-1, 1]; the state advances. Returns the sample count, or -1 when the cache is full. */
+int64_t vo_codec_forward(const vo_codec *c, vo_codec_state *s, const float *z, int32_t F, float *pcm);
+/* load_snake (qwen3.cpp:80-89): a = exp(alpha), inv_b = 1 / (exp(beta) + 1e-9), in float. */
+void vo_snake_params(const float *alpha, const float *beta, int64_t n, float *a, float *inv_b);
+/* Samples per codec frame (the product of the upsample strides). */
+int64_t vo_codec_spf(const vo_codec *c);
 
 /* Thread count for the row-parallel loops (matmul); 1 = scalar single-thread. Results do not depend on it. */
 void vo_set_threads(int n);

@@ -3,6 +3,7 @@
 Run here (where /root/reference exists and `make -C oracle ref` has built the harness):
     python tests/golden/make_golden.py          # golden_ref.npz
     python tests/golden/make_golden.py cosy     # golden_cosy.npz (the flow estimator's nn.cpp layers)
+    python tests/golden/make_golden.py codec    # golden_codec.npz (the Qwen3-TTS codec decoder)
 The fixtures hold inputs and the reference's outputs only (data, no reference source; the estimator's weights are
 regenerated from a seed by tests/models.py's CosyModel). Tests compare the
 C restatement (oracle/liboracle.so) against it on machines without the reference.
@@ -22,6 +23,8 @@ import pyoracle as po  # noqa: E402
 OUT = os.path.join(HERE, "golden_ref.npz")
 OUT_COSY = os.path.join(HERE, "golden_cosy.npz")
 COSY_SEED, COSY_T = 77, 13  # CosyModel(COSY_SEED, n_mid=1, n_x=1) at T frames
+OUT_CODEC = os.path.join(HERE, "golden_codec.npz")
+CODEC_SEED, CODEC_F = 91, 9  # CodecModel(CODEC_SEED) on F frames, decoded as 4 + 5
 
 
 def main():
@@ -153,5 +156,27 @@ def main_cosy():
     print("wrote", OUT_COSY, os.path.getsize(OUT_COSY), "bytes")
 
 
+def main_codec():
+    """Qwen3Weights::codec_forward of the compiled reference on a CodecModel written as a .tmod by its own tmod_write:
+    the codes, the quantizer output and the PCM of two streaming calls."""
+    import tempfile
+    if po.ref() is None:
+        raise SystemExit("oracle/_ref/libvoxref.so is not built")
+    from models import CodecModel
+    m = CodecModel(CODEC_SEED)
+    codes = m.codes(np.random.default_rng(CODEC_SEED), CODEC_F)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "codec.tmod")
+        m.write_tmod(path)
+        R = po.RefCodec(path, m.spf)
+        s = R.state()
+        pcm = np.concatenate([R.forward(s, codes[:4]), R.forward(s, codes[4:])])
+        R.free_state(s)
+        del R
+    np.savez_compressed(OUT_CODEC, codes=codes, pcm=pcm)
+    print("wrote", OUT_CODEC, os.path.getsize(OUT_CODEC), "bytes")
+
+
 if __name__ == "__main__":
-    main_cosy() if sys.argv[1:] == ["cosy"] else main()
+    mode = sys.argv[1:]
+    main_cosy() if mode == ["cosy"] else main_codec() if mode == ["codec"] else main()

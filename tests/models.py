@@ -248,3 +248,125 @@ class CosyModel:
         inp[:T, :self.M] = x
         inp[T:, :self.M] = x
         return inp
+
+
+CODEC_TINY = dict(codebook_size=16, hidden_size=32, latent_dim=16, num_attention_heads=2, num_key_value_heads=2,
+                  head_dim=16, sliding_window=5, intermediate_size=48, layer_scale_initial_scale=0.5, rms_norm_eps=1e-5,
+                  num_hidden_layers=2, num_quantizers=4, upsample_rates=[2, 3], upsampling_ratios=[2, 2],
+                  decoder_dim=32, codebook_dim=16, rope_theta=10000.0)
+
+
+class CodecModel:
+    """A random Qwen3-TTS codec decoder by .tmod tensor name (f32, the layouts qwen3.cpp:225-283 reads): `t` the
+    tensors, `ox` the oracle's Codec, `write_tmod` a whole Qwen3-TTS .tmod for the compiled reference (a minimal
+    talker and predictor beside the codec, which Qwen3Weights loads too)."""
+
+    def __init__(self, seed, cc=None):
+        cc = dict(CODEC_TINY if cc is None else cc)
+        self.cc = cc
+        rng = np.random.default_rng(seed)
+        t = {}
+
+        def w(name, rows, cols, std=None):
+            t[name] = (rng.standard_normal((rows, cols)) * (std or 1.0 / np.sqrt(cols))).astype(np.float32)
+
+        def v(name, n, mean=0.0, sd=0.1):
+            t[name] = (mean + sd * rng.standard_normal(n)).astype(np.float32)
+        Q, CD, L, H = cc["num_quantizers"], cc["codebook_dim"], cc["latent_dim"], cc["hidden_size"]
+        heads, kvh, hd, I = cc["num_attention_heads"], cc["num_key_value_heads"], cc["head_dim"], cc["intermediate_size"]
+        dim, cs = CD // 2, cc["codebook_size"]
+        w("codec.quantizer.rvq_first.vq.layers.0._codebook.embedding", cs, dim, 1.0)
+        for i in range(Q - 1):
+            w(f"codec.quantizer.rvq_rest.vq.layers.{i}._codebook.embedding", cs, dim, 0.5)
+        w("codec.quantizer.rvq_first.output_proj.weight", CD, dim)
+        w("codec.quantizer.rvq_rest.output_proj.weight", CD, dim)
+
+        def conv(p, K, cin, cout, std=None):
+            w(p + ".weight", cout, K * cin, std)
+            v(p + ".bias", cout, 0.0, 0.05)
+        conv("codec.pre_conv.conv", 3, CD, L)
+        w("codec.pre_transformer.input_proj.weight", H, L)
+        v("codec.pre_transformer.input_proj.bias", H)
+        w("codec.pre_transformer.output_proj.weight", L, H)
+        v("codec.pre_transformer.output_proj.bias", L)
+        for i in range(cc["num_hidden_layers"]):
+            p = f"codec.pre_transformer.layers.{i}."
+            w(p + "self_attn.q_proj.weight", heads * hd, H)
+            w(p + "self_attn.k_proj.weight", kvh * hd, H)
+            w(p + "self_attn.v_proj.weight", kvh * hd, H)
+            w(p + "self_attn.o_proj.weight", H, heads * hd)
+            w(p + "mlp.gate_proj.weight", I, H)
+            w(p + "mlp.up_proj.weight", I, H)
+            w(p + "mlp.down_proj.weight", H, I)
+            v(p + "input_layernorm.weight", H, 1.0)
+            v(p + "post_attention_layernorm.weight", H, 1.0)
+            v(p + "self_attn_layer_scale.scale", H, cc["layer_scale_initial_scale"], 0.1)
+            v(p + "mlp_layer_scale.scale", H, cc["layer_scale_initial_scale"], 0.1)
+        v("codec.pre_transformer.norm.weight", H, 1.0)
+        for s_, r in enumerate(cc["upsampling_ratios"]):
+            p = f"codec.upsample.{s_}."
+            w(p + "0.conv.weight", r * L, L)
+            v(p + "0.conv.bias", L)
+            w(p + "1.dwconv.conv.weight", L, 7, 0.3)
+            v(p + "1.dwconv.conv.bias", L)
+            v(p + "1.norm.weight", L, 1.0)
+            v(p + "1.norm.bias", L)
+            v(p + "1.gamma", L, 0.0, 0.3)
+            w(p + "1.pwconv1.weight", 4 * L, L)
+            v(p + "1.pwconv1.bias", 4 * L)
+            w(p + "1.pwconv2.weight", L, 4 * L)
+            v(p + "1.pwconv2.bias", L)
+        dec = cc["decoder_dim"]
+        conv("codec.decoder.0.conv", 7, L, dec)
+
+        def snake(p, C):
+            v(p + ".alpha", C, 0.0, 0.3)
+            v(p + ".beta", C, 0.0, 0.3)
+        for b, r in enumerate(cc["upsample_rates"]):
+            ind, outd = dec >> b, dec >> (b + 1)
+            p = f"codec.decoder.{b + 1}.block."
+            snake(p + "0", ind)
+            w(p + "1.conv.weight", 2 * r * outd, ind)
+            v(p + "1.conv.bias", outd)
+            for u in range(3):
+                q = p + f"{u + 2}."
+                snake(q + "act1", outd)
+                conv(q + "conv1.conv", 7, outd, outd)
+                snake(q + "act2", outd)
+                conv(q + "conv2.conv", 1, outd, outd)
+        nb = len(cc["upsample_rates"])
+        snake(f"codec.decoder.{nb + 1}", dec >> nb)
+        conv(f"codec.decoder.{nb + 2}.conv", 7, dec >> nb, 1, 0.0005)
+        self.t = t
+        self.ox = po.Codec(cc, t)
+        self.spf = self.ox.spf
+
+    def codes(self, rng, F):
+        return rng.integers(0, self.cc["codebook_size"], (F, self.cc["num_quantizers"])).astype(np.int16)
+
+    def write_tmod(self, path):
+        hid = 8
+        tc = dict(hidden_size=hid, intermediate_size=hid, num_hidden_layers=1, num_attention_heads=1, num_key_value_heads=1,
+                  head_dim=hid, vocab_size=8, text_hidden_size=hid, text_vocab_size=8, num_code_groups=2,
+                  codec_eos_token_id=1, codec_think_id=2, codec_nothink_id=3, codec_think_bos_id=4, codec_think_eos_id=5,
+                  codec_pad_id=6, codec_bos_id=7)
+        pc = dict(hidden_size=hid, intermediate_size=hid, num_hidden_layers=1, num_attention_heads=1, num_key_value_heads=1,
+                  head_dim=hid, vocab_size=8)
+        ids = dict(im_start=0, im_end=1, tts_pad=2, tts_bos=3, tts_eos=4)
+        t = dict(self.t)
+        z = lambda *s: np.zeros(s, np.float32)
+        for p in ("talker.model.", "talker.code_predictor.model."):
+            L = p + "layers.0."
+            for n in ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "mlp.gate_proj",
+                      "mlp.up_proj", "mlp.down_proj"):
+                t[L + n + ".weight"] = z(hid, hid)
+            for n in ("input_layernorm", "post_attention_layernorm", "self_attn.q_norm", "self_attn.k_norm"):
+                t[L + n + ".weight"] = z(hid)
+            t[p + "norm.weight"] = z(hid)
+        for n in ("talker.model.codec_embedding.weight", "talker.model.text_embedding.weight", "talker.codec_head.weight",
+                  "talker.text_projection.linear_fc1.weight", "talker.text_projection.linear_fc2.weight",
+                  "talker.code_predictor.model.codec_embedding.0.weight", "talker.code_predictor.lm_head.0.weight"):
+            t[n] = z(8, hid)
+        t["talker.text_projection.linear_fc1.weight"] = z(hid, hid)
+        t["talker.text_projection.linear_fc2.weight"] = z(hid, hid)
+        po.tmod_write(path, {"qwen3": {"talker": tc, "predictor": pc, "codec": self.cc, "ids": ids}}, t)

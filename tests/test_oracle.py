@@ -717,3 +717,90 @@ def test_cosy_step_against_reference(ref, wt):
         in0, x, tb = m.inputs(rng, T)
         inp = m.with_x(in0, x)
         assert np.array_equal(po.cosy_step(m.ox, T, inp, tb), po.cosy_step(m.ox, T, inp, tb, use_ref=True)), T
+
+
+# ------------------------------------------------------------------ Qwen3-TTS codec decoder
+def test_codec_golden(oracle):
+    # the whole codec_forward (quantizer, pre_conv, windowed transformer with layer scales, upsampling ConvNeXt,
+    # decoder blocks, clamp) against the compiled reference's Qwen3Weights::codec_forward, bit for bit, two calls
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+    import make_golden
+    import models
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden_codec.npz"), allow_pickle=False)
+    m = models.CodecModel(make_golden.CODEC_SEED)
+    assert np.array_equal(m.codes(np.random.default_rng(make_golden.CODEC_SEED), make_golden.CODEC_F), g["codes"])
+    st = po.CodecState(m.ox)
+    z = po.codec_quantize(m.ox, g["codes"])
+    pcm = np.concatenate([po.codec_forward(st, z[:4]), po.codec_forward(st, z[4:])])
+    assert np.array_equal(pcm, g["pcm"])
+
+
+def test_codec_streaming_and_clone(oracle):
+    # a causal streaming decoder: any split of the frames into calls gives the same samples (the histories, tails
+    # and cache carry exactly), and a cloned state continues like the original
+    import models
+    m = models.CodecModel(8)
+    z = po.codec_quantize(m.ox, m.codes(np.random.default_rng(1), 11))
+    whole = po.codec_forward(po.CodecState(m.ox), z)
+    st = po.CodecState(m.ox)
+    parts = [po.codec_forward(st, z[a:b]) for a, b in ((0, 1), (1, 4), (4, 5), (5, 11))]
+    assert np.array_equal(np.concatenate(parts), whole)
+    st = po.CodecState(m.ox)
+    po.codec_forward(st, z[:6])
+    cl = st.clone()
+    assert np.array_equal(po.codec_forward(st, z[6:]), po.codec_forward(cl, z[6:]))
+    assert np.array_equal(po.codec_forward(po.CodecState(m.ox), z[:6]), whole[:6 * m.spf])
+    assert np.max(np.abs(whole)) < 1.0  # the model stays inside the clamp, so the comparisons see the signal
+
+
+def test_codec_window_and_scale_pins(oracle):
+    # the transformer's sliding window and layer scales against float64 brute force on one layer: window 3 at
+    # positions 0..5 (rows see at most 3 keys), scales applied to the o and down outputs before the residual add
+    import models
+    rng = np.random.default_rng(4)
+    H, heads, hd, I, W = 16, 2, 8, 24, 3
+    mk = lambda r, c: (rng.standard_normal((r, c)) / np.sqrt(c)).astype(np.float32)
+    mats = {n: mk(*s) for n, s in (("q", (16, H)), ("k", (16, H)), ("v", (16, H)), ("o", (H, 16)), ("gate", (I, H)),
+                                   ("up", (I, H)), ("down", (H, I)))}
+    ln1, ln2, fn = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32), np.ones(H, np.float32), np.ones(H, np.float32)
+    sa, sm = (0.5 + 0.1 * rng.standard_normal(H)).astype(np.float32), (0.5 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    om = {n: po.Mat(po.F32, a, a.shape[0], a.shape[1]) for n, a in mats.items()}
+    lay = (po.VoLayer * 1)()
+    for n in mats:
+        setattr(lay[0], n, om[n].c)
+    lay[0].ln1, lay[0].ln2, lay[0].attn_scale, lay[0].mlp_scale = ln1.ctypes.data, ln2.ctypes.data, sa.ctypes.data, sm.ctypes.data
+    inv = np.empty(hd // 2, np.float32)
+    po.lib().vo_rope_inv_freq(hd, 1e4, inv.ctypes.data)
+    xf = po.VoXfmr(1, lay, fn.ctypes.data, H, heads, heads, hd, I, 1e-5, inv.ctypes.data, W)
+    x = rng.standard_normal((6, H)).astype(np.float32)
+    k = np.zeros((1, 8, 16), np.float32)
+    v = np.zeros_like(k)
+    kv = po.VoKV(k.ctypes.data, v.ctypes.data, 8, 0, 0, 0)
+    h = np.empty_like(x)
+    assert po.lib().vo_transformer_layers(po.C.byref(xf), po.C.byref(kv), x.ctypes.data, 6, 0, 1, h.ctypes.data) == 0
+    X = x.astype(np.float64)
+    rms = lambda a, w: a / np.sqrt((a * a).mean(-1, keepdims=True) + 1e-5) * w
+    xn = rms(X, ln1)
+    q, kk, vv = xn @ mats["q"].T, xn @ mats["k"].T, xn @ mats["v"].T
+    def rope(a, pos):
+        a = a.reshape(heads, hd).copy()
+        ang = np.float32(inv * np.float32(pos)).astype(np.float64)
+        c, s = np.cos(ang), np.sin(ang)
+        x0, x1 = a[:, :hd // 2].copy(), a[:, hd // 2:].copy()  # rotate-half pairs (i, i + hd / 2)
+        a[:, :hd // 2], a[:, hd // 2:] = x0 * c - x1 * s, x1 * c + x0 * s
+        return a
+    Qr = np.stack([rope(q[i], i) for i in range(6)])
+    Kr = np.stack([rope(kk[i], i) for i in range(6)])
+    ao = np.zeros((6, heads, hd))
+    for i in range(6):
+        f = max(0, i - W + 1)
+        for hh in range(heads):
+            sc = Kr[f:i + 1, hh] @ Qr[i, hh] / np.sqrt(hd)
+            p = np.exp(sc - sc.max())
+            ao[i, hh] = (p / p.sum()) @ vv[f:i + 1].reshape(-1, heads, hd)[:, hh]
+    X = X + (ao.reshape(6, -1) @ mats["o"].T) * sa
+    xn = rms(X, ln2)
+    g_ = xn @ mats["gate"].T
+    X = X + (((g_ / (1 + np.exp(-g_))) * (xn @ mats["up"].T)) @ mats["down"].T) * sm
+    assert np.max(np.abs(h - X)) < 1e-4
