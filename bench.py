@@ -278,6 +278,36 @@ def bench_cosy(vh, synth, reps=5):
             "flow_ms_10_steps": round(10 * ms, 2)}
 
 
+def bench_codec(vh, synth, reps=10):
+    """Qwen3-TTS's codec decoder (gpu_codec_forward; qwen3.cpp:390-480 on the CPU) at its full widths with synthetic f32
+    weights: chunks of 16 frames (1.28 s of 24 kHz audio per call) and single frames (streaming). Host wall-clock per
+    call (median), the z upload and the PCM download included; the ring wraps during the run."""
+    c = synth.QWEN3_CODEC
+    dec = synth.CodecDec(c, seed=0)
+    rng = np.random.default_rng(9)
+    st = vh.codec_state_new(dec.codec)
+    out = {}
+    for F in (16, 1):
+        z = (rng.standard_normal((F, c["codebook_dim"])) * 0.5).astype(np.float32)
+        for _ in range(3):
+            vh.codec_forward(dec.codec, st, z)
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            pcm = vh.codec_forward(dec.codec, st, z)
+            times.append((time.perf_counter() - t0) * 1000.0)
+        assert pcm.size == F * dec.spf and np.isfinite(pcm).all()
+        ms = float(np.median(times))
+        fl = F * dec.flops_per_frame()
+        out[f"f{F}"] = {"ms_per_call": round(ms, 3), "gflop": round(fl / 1e9, 2), "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
+                        "audio_s_per_s": round(F * dec.spf / 24000 / (ms * 1e-3), 1)}
+    vh.codec_state_free(st)
+    for h in dec.mats:
+        vh.mat_free(h)
+    return {"workload": "qwen3-tts codec decoder (gpu_codec_forward): 8-layer windowed transformer + 2 upsample + 4 "
+                        "decoder blocks (1536 ch, 1920 samples per frame), f32 weights", **out}
+
+
 def bench_pred(vh, synth, frames=20):
     """The code predictor's frame on the device (gpu_pred_frame; the loop engine.cpp:676-683 runs on the CPU in the
     reference when the device does not provide it): 15 passes of the 5-layer q8 predictor (2 rows at positions 0-1,
@@ -334,7 +364,7 @@ def main():
     ap.add_argument("--no-other", action="store_true",
                     help="skip the configs[0] / [2] / [3] / [4] and code-predictor measurements")
     ap.add_argument("--only", choices=["configs[0]", "configs[2]", "configs[3]", "configs[4]", "pred_frame", "f5_vocos",
-                                       "cosy_flow"],
+                                       "cosy_flow", "codec"],
                     help="run one of the other BASELINE configurations (or the code-predictor frame) alone and print "
                          "its JSON object (for profiling)")
     ap.add_argument("--no-breakdown", action="store_true",
@@ -354,7 +384,7 @@ def main():
         legs = {"configs[0]": lambda: bench_cfg1(vh), "configs[2]": lambda: bench_cfg3(vh, synth, 100, 10),
                 "configs[3]": lambda: bench_cfg4(vh, synth), "configs[4]": lambda: bench_cfg5(vh, synth),
                 "pred_frame": lambda: bench_pred(vh, synth), "f5_vocos": lambda: bench_vocos(vh, synth),
-                "cosy_flow": lambda: bench_cosy(vh, synth)}
+                "cosy_flow": lambda: bench_cosy(vh, synth), "codec": lambda: bench_codec(vh, synth)}
         print(json.dumps({args.only: legs[args.only]()}))
         return
     t0 = time.perf_counter()
@@ -421,7 +451,7 @@ def main():
         other = {"configs[0]": bench_cfg1(vh), "configs[2]": bench_cfg3(vh, synth, 100, 10),
                  "configs[3]": bench_cfg4(vh, synth), "configs[4]": bench_cfg5(vh, synth),
                  "pred_frame": bench_pred(vh, synth), "f5_vocos": bench_vocos(vh, synth),
-                 "cosy_flow": bench_cosy(vh, synth)}
+                 "cosy_flow": bench_cosy(vh, synth), "codec": bench_codec(vh, synth)}
         log(f"other configs: {json.dumps(other)} ({time.perf_counter() - t0:.1f} s)")
 
     cpu = None

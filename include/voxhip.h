@@ -317,6 +317,63 @@ int voxhip_cosy_begin(int id, int T, const float *in0);
 int voxhip_cosy_step(int id, const float *x, const float *tb, float *out);
 int voxhip_cosy_end(int id); /* gpu_cosy_end (gpu.hpp:119): frees the step buffers, keeps the weights */
 
+/* ---------------------------------------------------------------- Qwen3-TTS codec decoder (gpu.hpp:53-60)
+ * gpu_codec_forward's chain (gpu_codec.cpp:400-556; the CPU path qwen3.cpp:390-480) from the quantizer output z on:
+ * pre_conv (causal K 3) -> pre-transformer (sliding window, layer scales, an f32 ring cache) -> upsample stages
+ * (transposed conv K = stride + causal ConvNeXt) -> conv0 -> decoder blocks (Snake, transposed conv K = 2 stride
+ * with its overlap tail, 3 residual units) -> Snake -> final conv -> clamp. Streaming state (conv histories, tails,
+ * ring) lives on the device. Weights are matrix handles of F32 / F16 / BF16 type; the rest host arrays. */
+typedef struct voxhip_codec_conv {
+    int32_t mat;              /* [cout][K cin] with its bias (CConv::w, qwen3.hpp:45) */
+    int32_t K, cin, cout, dil;
+} voxhip_codec_conv;
+typedef struct voxhip_codec_snake {
+    const float *a, *inv_b;   /* exp(alpha), 1 / (exp(beta) + 1e-9) [C] (Snake, qwen3.hpp:48) */
+} voxhip_codec_snake;
+/* Qwen3Weights::UpStage (qwen3.hpp:96): tr [K latent][latent], K = stride. */
+typedef struct voxhip_codec_up {
+    int32_t tr, K;
+    const float *tr_b;          /* [latent] */
+    const float *dw_w, *dw_b;   /* depthwise [latent][dw_K], [latent] */
+    int32_t dw_K;
+    const float *ln_w, *ln_b, *gamma;
+    int32_t pw1, pw2;
+} voxhip_codec_up;
+/* Qwen3Weights::DecBlock (qwen3.hpp:99): tr [K cout][cin], stride < K <= 2 stride. */
+typedef struct voxhip_codec_block {
+    voxhip_codec_snake act;
+    int32_t tr, K, stride, cin, cout;
+    const float *tr_b;          /* [cout] */
+    voxhip_codec_snake a1[3], a2[3];
+    voxhip_codec_conv c1[3], c2[3];
+} voxhip_codec_block;
+/* The decoder of Qwen3Weights (qwen3.hpp:90-104, CodecCfg :29-41). pt: the pre-transformer's TransformerW (window,
+ * eps, inv_freq, norms and layer scales; its voxhip_mat entries are ignored), pt_mats its matrix handles [layers][7]
+ * (q, k, v, o, gate, up, down; no biases, no q / k norm). */
+typedef struct voxhip_codec_desc {
+    int32_t codebook_dim, latent;
+    voxhip_codec_conv pre_conv;
+    int32_t pt_in, pt_out;
+    voxhip_xfmr_desc pt;
+    const int32_t *pt_mats;
+    const voxhip_codec_up *ups;
+    int32_t n_ups;
+    voxhip_codec_conv conv0;
+    const voxhip_codec_block *blocks;
+    int32_t n_blocks;
+    voxhip_codec_snake final_act;
+    voxhip_codec_conv final_conv;
+} voxhip_codec_desc;
+int voxhip_codec_create(const voxhip_codec_desc *d);   /* gpu_codec_create (gpu.hpp:55): a handle or -1 */
+int voxhip_codec_state_new(int codec);                 /* gpu_codec_state_new (gpu.hpp:56): zeroed state, or -1 */
+int voxhip_codec_state_clone(int state);               /* gpu_codec_state_clone (gpu.hpp:57): a deep copy, or -1 */
+int voxhip_codec_state_free(int state);                /* gpu_codec_state_free (gpu.hpp:58) */
+/* gpu_codec_forward (gpu.hpp:60): z [F][codebook_dim], 1 <= F <= 16 (kGpuCodecMaxFrames, gpu.hpp:61) -> pcm
+ * [F samples_per_frame] (clamped), *n_out the count; the state advances. */
+int voxhip_codec_forward(int codec, int state, const float *z, int F, float *pcm, int64_t *n_out);
+/* Samples per codec frame into *spf (no counterpart in gpu.hpp: the adapter sizes gpu_codec_forward's output). */
+int voxhip_codec_spf(int codec, int32_t *spf);
+
 /* Synthetic weights and caches, generated on the device (Philox4x32-10 Box-Muller, mean + std * z).
  * voxhip_mat_synthetic: f32 values, then quantized on the device to `type` with the reference's
  * quantizer (Q8: kernels.cpp:918-929; Q4: kernels.cpp:606-645; F16/BF16: nearest even). Returns a handle.

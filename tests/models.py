@@ -16,6 +16,12 @@ def to_bf16_bits(w):
     return r
 
 
+def bf16_round(w):
+    """w rounded to bfloat16 values (nearest even), as f32."""
+    b = to_bf16_bits(np.ascontiguousarray(w, np.float32)).astype(np.uint32) << 16
+    return b.view(np.float32).reshape(w.shape)
+
+
 def make_mat(rng, wtype, rows, cols, std=0.02, bias=False):
     """Returns (data, scale, bias) in the reference layout for wtype."""
     w = (rng.standard_normal((rows, cols)) * std).astype(np.float32)
@@ -251,7 +257,7 @@ class CosyModel:
 
 
 CODEC_TINY = dict(codebook_size=16, hidden_size=32, latent_dim=16, num_attention_heads=2, num_key_value_heads=2,
-                  head_dim=16, sliding_window=5, intermediate_size=48, layer_scale_initial_scale=0.5, rms_norm_eps=1e-5,
+                  head_dim=16, sliding_window=5, intermediate_size=64, layer_scale_initial_scale=0.5, rms_norm_eps=1e-5,
                   num_hidden_layers=2, num_quantizers=4, upsample_rates=[2, 3], upsampling_ratios=[2, 2],
                   decoder_dim=32, codebook_dim=16, rope_theta=10000.0)
 
@@ -261,7 +267,7 @@ class CodecModel:
     tensors, `ox` the oracle's Codec, `write_tmod` a whole Qwen3-TTS .tmod for the compiled reference (a minimal
     talker and predictor beside the codec, which Qwen3Weights loads too)."""
 
-    def __init__(self, seed, cc=None):
+    def __init__(self, seed, cc=None, wround=F32):
         cc = dict(CODEC_TINY if cc is None else cc)
         self.cc = cc
         rng = np.random.default_rng(seed)
@@ -326,20 +332,82 @@ class CodecModel:
             ind, outd = dec >> b, dec >> (b + 1)
             p = f"codec.decoder.{b + 1}.block."
             snake(p + "0", ind)
-            w(p + "1.conv.weight", 2 * r * outd, ind)
+            w(p + "1.conv.weight", 2 * r * outd, ind, 1.0 / np.sqrt(2 * ind))  # two taps overlap per output
             v(p + "1.conv.bias", outd)
-            for u in range(3):
+            for u in range(3):  # residual units scaled down so the stack keeps unit-size activations
                 q = p + f"{u + 2}."
                 snake(q + "act1", outd)
-                conv(q + "conv1.conv", 7, outd, outd)
+                conv(q + "conv1.conv", 7, outd, outd, 0.3 / np.sqrt(7 * outd))
                 snake(q + "act2", outd)
-                conv(q + "conv2.conv", 1, outd, outd)
+                conv(q + "conv2.conv", 1, outd, outd, 0.3 / np.sqrt(outd))
         nb = len(cc["upsample_rates"])
         snake(f"codec.decoder.{nb + 1}", dec >> nb)
-        conv(f"codec.decoder.{nb + 2}.conv", 7, dec >> nb, 1, 0.0005)
+        conv(f"codec.decoder.{nb + 2}.conv", 7, dec >> nb, 1, 0.1 / np.sqrt(7 * (dec >> nb)))
+        if wround == F16:  # the matrices as the device stores them, so both sides see the same weights
+            t = {k: (a.astype(np.float16).astype(np.float32) if a.ndim == 2 else a) for k, a in t.items()}
+        elif wround == BF16:
+            t = {k: (bf16_round(a) if a.ndim == 2 else a) for k, a in t.items()}
         self.t = t
         self.ox = po.Codec(cc, t)
         self.spf = self.ox.spf
+
+    def create(self, hip, wtype=F32):
+        """The device codec (gpu_codec_create) over the same tensors, linears and convs uploaded as wtype."""
+        cc, t = self.cc, self.t
+        mats = []
+
+        def up(name, bias=None):
+            w = t[name]
+            d = w.astype(np.float16).view(np.uint16) if wtype == F16 else (to_bf16_bits(w) if wtype == BF16 else w)
+            h = hip.upload(hip.HostMat(wtype, d, w.shape[0], w.shape[1], None, None if bias is None else t[bias]))
+            mats.append(h)
+            return h
+
+        def conv(p, K, cin, cout, dil=1):
+            return (up(p + ".weight", p + ".bias"), K, cin, cout, dil)
+
+        def snake(p):
+            a = np.empty(t[p + ".alpha"].size, np.float32)
+            ib = np.empty_like(a)
+            po.lib().vo_snake_params(t[p + ".alpha"].ctypes.data, t[p + ".beta"].ctypes.data, a.size, a.ctypes.data,
+                                     ib.ctypes.data)
+            return (a, ib)
+        CD, L, H = cc["codebook_dim"], cc["latent_dim"], cc["hidden_size"]
+        heads, hd = cc["num_attention_heads"], cc["head_dim"]
+        layers, ids = [], []
+        for i in range(cc["num_hidden_layers"]):
+            p = f"codec.pre_transformer.layers.{i}."
+            ids.append([up(p + k + ".weight") for k in ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj",
+                                                        "self_attn.o_proj", "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")])
+            layers.append(dict(ln1=t[p + "input_layernorm.weight"], ln2=t[p + "post_attention_layernorm.weight"],
+                               attn_scale=t[p + "self_attn_layer_scale.scale"], mlp_scale=t[p + "mlp_layer_scale.scale"]))
+        inv = np.empty(hd // 2, np.float32)
+        po.lib().vo_rope_inv_freq(hd, cc.get("rope_theta", 10000.0), inv.ctypes.data)
+        pt = dict(hidden=H, heads=heads, kv_heads=cc["num_key_value_heads"], head_dim=hd, inter=cc["intermediate_size"],
+                  eps=cc.get("rms_norm_eps", 1e-5), theta=cc.get("rope_theta", 10000.0), window=cc["sliding_window"],
+                  inv_freq=inv, final_norm=t["codec.pre_transformer.norm.weight"], layers=layers)
+        ups = []
+        for s_, r in enumerate(cc["upsampling_ratios"]):
+            p = f"codec.upsample.{s_}."
+            ups.append(dict(tr=up(p + "0.conv.weight"), K=r, tr_b=t[p + "0.conv.bias"], dw_w=t[p + "1.dwconv.conv.weight"],
+                            dw_b=t[p + "1.dwconv.conv.bias"], dw_K=7, ln_w=t[p + "1.norm.weight"], ln_b=t[p + "1.norm.bias"],
+                            gamma=t[p + "1.gamma"], pw1=up(p + "1.pwconv1.weight", p + "1.pwconv1.bias"),
+                            pw2=up(p + "1.pwconv2.weight", p + "1.pwconv2.bias")))
+        dec, blocks = cc["decoder_dim"], []
+        for b, r in enumerate(cc["upsample_rates"]):
+            ind, outd = dec >> b, dec >> (b + 1)
+            p = f"codec.decoder.{b + 1}.block."
+            blocks.append(dict(act=snake(p + "0"), tr=up(p + "1.conv.weight"), K=2 * r, stride=r, cin=ind, cout=outd,
+                               tr_b=t[p + "1.conv.bias"], a1=[snake(p + f"{u + 2}.act1") for u in range(3)],
+                               a2=[snake(p + f"{u + 2}.act2") for u in range(3)],
+                               c1=[conv(p + f"{u + 2}.conv1.conv", 7, outd, outd, dil) for u, dil in enumerate((1, 3, 9))],
+                               c2=[conv(p + f"{u + 2}.conv2.conv", 1, outd, outd) for u in range(3)]))
+        nb = len(cc["upsample_rates"])
+        self.mats = mats
+        return hip.codec_create(CD, L, conv("codec.pre_conv.conv", 3, CD, L), up("codec.pre_transformer.input_proj.weight",
+                                "codec.pre_transformer.input_proj.bias"), up("codec.pre_transformer.output_proj.weight",
+                                "codec.pre_transformer.output_proj.bias"), pt, ids, ups, conv("codec.decoder.0.conv", 7, L, dec),
+                                blocks, snake(f"codec.decoder.{nb + 1}"), conv(f"codec.decoder.{nb + 2}.conv", 7, dec >> nb, 1))
 
     def codes(self, rng, F):
         return rng.integers(0, self.cc["codebook_size"], (F, self.cc["num_quantizers"])).astype(np.int16)

@@ -1,0 +1,151 @@
+// vh_codec.hpp — Qwen3-TTS codec decoder kernels besides the GEMMs (qwen3.cpp:80-161, :366-481; the Vulkan shaders
+// snake / hist / dwconv / ola / ringput / attnw of gpu_codec.cpp): Snake, streaming histories, the causal depthwise
+// conv, the transposed conv's overlap-add with its tail, the pre-transformer's RoPE + ring append and sliding-window
+// attention over the ring, layer-scaled residual adds and the final clamp. Activations are time-major f32 rows.
+#pragma once
+#include "vh_common.hpp"
+#include "vh_types.hpp"
+
+namespace vh {
+
+// Snake (qwen3.cpp:80-89): y = x + inv_b[c] sin(a[c] x)^2 over n = R C elements (x and y may be the same).
+__global__ __launch_bounds__(256) void k_snake(const float *__restrict__ x, const float *__restrict__ a,
+                                               const float *__restrict__ inv_b, float *__restrict__ y, int64_t n, int32_t C) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    const int c = int(i % C);
+    const float v = x[i], sn = sinf(v * a[c]);
+    y[i] = v + inv_b[c] * sn * sn;
+}
+
+// A streaming history after a call of T rows: the last ctx rows of [old (ctx rows); x (T rows, stride ldx)] into
+// dst (another buffer than old). qwen3.cpp:120, :136.
+__global__ __launch_bounds__(256) void k_hist_shift(float *__restrict__ dst, const float *__restrict__ old,
+                                                    const float *__restrict__ x, int64_t ldx, int32_t T, int32_t ctx,
+                                                    int32_t C) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= int64_t(ctx) * C) return;
+    const int j = int(i / C), c = int(i % C), r = j + T;  // row r of the extended sequence
+    dst[i] = r < ctx ? old[int64_t(r) * C + c] : x[int64_t(r - ctx) * ldx + c];
+}
+
+// dwconv_stream (qwen3.cpp:123-137): y[t][c] = b[c] + sum_k w[c][k] ext[t + k][c] over ext = [hist (K - 1 rows); x],
+// taps in order. One thread per output.
+__global__ __launch_bounds__(256) void k_dwconv_causal(const float *__restrict__ x, const float *__restrict__ hist,
+                                                       const float *__restrict__ w, const float *__restrict__ b,
+                                                       float *__restrict__ y, int32_t T, int32_t C, int32_t K) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= int64_t(T) * C) return;
+    const int t = int(i / C), c = int(i % C), ctx = K - 1;
+    float acc = b[c];
+    for (int k = 0; k < K; ++k) {
+        const int r = t + k;
+        const float v = r < ctx ? hist[int64_t(r) * C + c] : x[int64_t(r - ctx) * C + c];
+        acc += w[int64_t(c) * K + k] * v;
+    }
+    y[i] = acc;
+}
+
+// trans_stream's overlap-add (qwen3.cpp:139-161) from the GEMM output tmp [T][K co] (row k co + o of frame t): output
+// row p (of T s + K - s) takes frame p / s at tap p % s and frame p / s - 1 at tap p % s + s (K <= 2 s), plus the old
+// tail's row p; rows below T s go to y with the bias, the rest to the new tail (another buffer than the old one).
+__global__ __launch_bounds__(256) void k_ola(const float *__restrict__ tmp, const float *__restrict__ tail_old,
+                                             float *__restrict__ tail_new, const float *__restrict__ bias,
+                                             float *__restrict__ y, int32_t T, int32_t s, int32_t K, int32_t co) {
+    const int tr = K - s;
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= (int64_t(T) * s + tr) * co) return;
+    const int64_t p = i / co;
+    const int o = int(i % co);
+    const int64_t t = p / s;
+    const int k = int(p - t * s);
+    float v = p < tr ? tail_old[p * co + o] : 0.f;
+    if (t < T && k < K) v += tmp[(t * K + k) * co + o];
+    if (t >= 1 && k + s < K) v += tmp[((t - 1) * K + k + s) * co + o];
+    if (p < int64_t(T) * s) y[p * co + o] = v + bias[o];
+    else tail_new[(p - int64_t(T) * s) * co + o] = v;
+}
+
+// The pre-transformer's q / k rotation (rope_apply, kernels.cpp:740-757: pairs (d, d + hd / 2)) with the host table
+// rope [F][hd / 2][2] of positions pos0 + i, and the append of row i's keys and values to ring slot (pos0 + i) % R of
+// the layer's f32 ring [R][kv_heads hd]. grid F, block 256; qkv rows [F][ld] = q | k | v.
+__global__ __launch_bounds__(256) void k_codec_rope_ring(float *__restrict__ qkv, int32_t ld, int32_t heads, int32_t kvh,
+                                                         int32_t hd, const float *__restrict__ rope,
+                                                         float *__restrict__ ring_k, float *__restrict__ ring_v,
+                                                         int32_t R, int64_t pos0) {
+    const int i = blockIdx.x, half = hd / 2, qd = heads * hd, kd = kvh * hd;
+    float *row = qkv + int64_t(i) * ld;
+    const float *cs = rope + int64_t(i) * hd;
+    const int64_t slot = (pos0 + i) % R;
+    for (int e = threadIdx.x; e < (heads + kvh) * half; e += 256) {
+        const int h = e / half, d = e % half;
+        float *p = h < heads ? row + h * hd : row + qd + (h - heads) * hd;
+        const float a = p[d], b = p[d + half], c = cs[2 * d], s = cs[2 * d + 1];
+        const float r0 = a * c - b * s, r1 = b * c + a * s;
+        if (h < heads) {
+            p[d] = r0;
+            p[d + half] = r1;
+        } else {
+            float *kr = ring_k + slot * kd + (h - heads) * hd;
+            kr[d] = r0;
+            kr[d + half] = r1;
+        }
+    }
+    for (int e = threadIdx.x; e < kd; e += 256) ring_v[slot * kd + e] = row[qd + kd + e];
+}
+
+// Sliding-window attention of row i (position pos0 + i) and head h over the ring (kernels.cpp:809-828 with the window
+// of :814): keys of positions (p - W, p], scores scale (q . k), softmax, sum p v. One wave per (row, head): lanes
+// take keys for the scores and head dimensions for the output. W <= 1024, hd <= 128.
+__global__ __launch_bounds__(64) void k_codec_attn(const float *__restrict__ qkv, int32_t ld, const float *__restrict__ ring_k,
+                                                   const float *__restrict__ ring_v, int32_t R, int32_t heads, int32_t kvh,
+                                                   int32_t hd, int64_t pos0, int32_t W, float scale, float *__restrict__ ao) {
+    __shared__ float p[1024];
+    __shared__ float q[128];
+    const int i = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, kd = kvh * hd, gk = h / (heads / kvh);
+    const int64_t last = pos0 + i, first = last - W + 1 > 0 ? last - W + 1 : 0;
+    const int n = int(last - first + 1);
+    for (int d = lane; d < hd; d += 64) q[d] = qkv[int64_t(i) * ld + h * hd + d];
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int j = lane; j < n; j += 64) {
+        const float *kr = ring_k + ((first + j) % R) * kd + gk * hd;
+        float dot = 0.f;
+        for (int d = 0; d < hd; ++d) dot += q[d] * kr[d];
+        p[j] = scale * dot;
+        mx = fmaxf(mx, p[j]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+    float sum = 0.f;
+    for (int j = lane; j < n; j += 64) {
+        p[j] = expf(p[j] - mx);
+        sum += p[j];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, kWave);
+    __syncthreads();
+    const float inv = 1.0f / sum;
+    for (int d = lane; d < hd; d += 64) {
+        float acc = 0.f;
+        for (int j = 0; j < n; ++j) acc += p[j] * ring_v[((first + j) % R) * kd + gk * hd + d];
+        ao[int64_t(i) * heads * hd + h * hd + d] = acc * inv;
+    }
+}
+
+// h += s[e] t over rows of H (the layer scales of kernels.cpp:830, :838: the projection scaled, then added).
+__global__ __launch_bounds__(256) void k_scale_acc(float *__restrict__ h, const float *__restrict__ t,
+                                                   const float *__restrict__ s, int64_t n, int32_t H) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    h[i] += t[i] * s[int(i % H)];
+}
+
+// The final clamp to [-1, 1] (qwen3.cpp:478).
+__global__ __launch_bounds__(256) void k_clamp1(float *__restrict__ y, int64_t n) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    y[i] = fminf(1.0f, fmaxf(-1.0f, y[i]));
+}
+
+}  // namespace vh

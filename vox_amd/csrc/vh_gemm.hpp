@@ -45,6 +45,11 @@ VH_DEV f32x4v gemm_load_a(const float *__restrict__ A, const GemmArgs &g, int ro
     f32x4v v = {0.f, 0.f, 0.f, 0.f};
     if (row >= g.m || k >= g.K) return v;
     if (ASRC == ASRC_ROWS) return *reinterpret_cast<const f32x4v *>(A + int64_t(row) * g.lda + k);
+    if (ASRC == ASRC_STREAM) {
+        const int kt = k / g.cig, i = k % g.cig, r = row + kt * g.dil;
+        if (r < g.ctx) return *reinterpret_cast<const f32x4v *>(g.hist + int64_t(r) * g.cig + i);
+        return *reinterpret_cast<const f32x4v *>(A + int64_t(r - g.ctx) * g.lda + i);
+    }
     const int s = row / g.seq, t = row % g.seq, kt = k / g.cig, i = k % g.cig;
     const int tt = t + kt - (g.causal ? g.ksize - 1 : g.ksize / 2);
     if (kt >= g.ksize || tt < 0 || tt >= g.seq) return v;  // kt >= ksize: the zero padding of a weight row
@@ -193,7 +198,7 @@ template <int WT, int EPI, int ASRC, int TM, int TN>
 __global__ __launch_bounds__(256) void k_gemm_f32(const uint8_t *__restrict__ w, const float *__restrict__ scale,
                                                   const float *__restrict__ A, GemmArgs g) {
     static_assert(WT == WT_F32 || WT == WT_F16 || WT == WT_BF16 || WT == WT_Q8, "f32-activation weight types");
-    static_assert(ASRC == ASRC_ROWS || WT == WT_F32, "convolution weights are f32");
+    static_assert(ASRC != ASRC_CONV || WT == WT_F32, "grouped convolution weights are f32");
     constexpr int BM = 32 * TM, BN = 32 * TN;
     constexpr int AQ = BM * kGemmBK / 4 / 256;  // f32x4 A loads per thread and K step
     constexpr int WQ = BN * kGemmBK / 8 / 256;  // 8-element W loads per thread and K step

@@ -76,6 +76,22 @@ hipError_t launch_norm_rows(const NormArgs &a, hipStream_t s);
 hipError_t launch_dwconv(const float *x, const float *w, const float *b, float *y, int64_t R, int C, int K, int seq, hipStream_t s);
 hipError_t launch_f5_attn(const _Float16 *qkv16, int64_t lo_off, float *out, _Float16 *out16, int64_t out_lo, int B, int N,
                           int heads, int hd, int ldvt, int ldo, float scale, hipStream_t s);
+// Qwen3-TTS codec decoder: Snake, streaming histories (dst != old), the causal depthwise conv, the transposed conv's
+// overlap-add (tail_old -> tail_new, K <= 2 stride), the pre-transformer's RoPE + ring append and windowed attention,
+// layer-scaled residual adds, the final clamp; and the streaming conv GEMM (A = im2col of [hist; x]).
+hipError_t launch_snake(const float *x, const float *a, const float *inv_b, float *y, int64_t rows, int C, hipStream_t s);
+hipError_t launch_hist_shift(float *dst, const float *old, const float *x, int64_t ldx, int T, int ctx, int C, hipStream_t s);
+hipError_t launch_dwconv_causal(const float *x, const float *hist, const float *w, const float *b, float *y, int T, int C, int K,
+                                hipStream_t s);
+hipError_t launch_ola(const float *tmp, const float *tail_old, float *tail_new, const float *bias, float *y, int T, int stride,
+                      int K, int co, hipStream_t s);
+hipError_t launch_codec_rope_ring(float *qkv, int ld, int F, int heads, int kvh, int hd, const float *rope, float *ring_k,
+                                  float *ring_v, int R, int64_t pos0, hipStream_t s);
+hipError_t launch_codec_attn(const float *qkv, int ld, const float *ring_k, const float *ring_v, int R, int F, int heads, int kvh,
+                             int hd, int64_t pos0, int W, float scale, float *ao, hipStream_t s);
+hipError_t launch_scale_acc(float *h, const float *t, const float *sc, int64_t rows, int H, hipStream_t s);
+hipError_t launch_clamp1(float *y, int64_t n, hipStream_t s);
+hipError_t launch_stream_conv(int wt, const uint8_t *w, const float *scale, const float *x, const GemmArgs &g, hipStream_t s);
 // CosyVoice2 LM: one sampling step (log-softmax, RAS trial loop) and the next step's embedding + row advance.
 hipError_t launch_lm_sample(const float *logits, int n, const LmCfgDev *cfg, LmState *st, int32_t *decoded, float *logp_out,
                             int64_t logp_stride, bool append, hipStream_t s);

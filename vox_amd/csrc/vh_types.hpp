@@ -13,7 +13,7 @@ enum { EPI_STORE = 0, EPI_ACC = 1, EPI_SWIGLU = 2 };
 enum { EPI_GATED_ACC = 3, EPI_GELU = 4, EPI_MISH = 5, EPI_MISH_ACC = 6, EPI_ROPE = 7, EPI_ROPE_H16 = 8, EPI_GELU_H16 = 9,
        EPI_GELU_ERF = 10 };
 // GEMM A operand: rows of a matrix, or the implicit im2col rows of a grouped "same" Conv1d
-enum { ASRC_ROWS = 0, ASRC_CONV = 1 };
+enum { ASRC_ROWS = 0, ASRC_CONV = 1, ASRC_STREAM = 2 };
 // Weight formats of the GEMV kernels: the reference's types, plus Q4 with f16 block scales (WT_Q4H), the
 // device storage of a Q4 matrix whose f32 scales are all exact in f16 (same arithmetic, 2 bytes less per block).
 enum { WT_F32 = 0, WT_F16 = 1, WT_BF16 = 2, WT_Q8 = 3, WT_Q4 = 4, WT_Q4H = 5 };
@@ -136,6 +136,10 @@ struct GemmArgs {
     // W and y are offset per group
     int32_t ksize, cig, causal;
     int32_t gelu_erf;
+    // ASRC_STREAM (the codec's streaming convolutions): A column k cig + i of row t is channel i of row t + k dil of
+    // [hist (ctx rows of cig); x (rows of lda)], ctx = (ksize - 1) dil
+    const float *hist;
+    int32_t ctx, dil;
     // split K (k_gemm_h16): block z sums K columns [z kchunk, (z + 1) kchunk) into ws + z m n ([m][n]); a reduce
     // pass adds the slices in order and applies the epilogue. kchunk 0: no split.
     int32_t kchunk;

@@ -151,6 +151,8 @@ struct Ctx {
     size_t hist_cap = 0;
     std::vector<struct F5 *> f5;
     std::vector<struct Cosy *> cosy;
+    std::vector<struct Codec *> codecs;
+    std::vector<struct CodecSt *> cstates;
     // split-K partial sums of the MFMA GEMM (allocated at init, so captured graphs can use it)
     float *gemm_ws = nullptr;
     // int-path input rows quantized once per pass (k_quant_rows), kQuantRowsElems elements (allocated at init)
@@ -692,12 +694,14 @@ int guard_int(F &&f, int fail) {
 
 const char *kWhich[7] = {"q", "k", "v", "o", "gate", "up", "down"};
 
+// codec: the codec's pre-transformer, whose forward (sliding window, layer scales, f32 ring) is the codec's own; only
+// its matrices, norms and scratch come from here.
 int make_xfmr(const voxhip_xfmr_desc *w, const char *name, int use_layers, const int32_t *mats, voxhip_uploaded_fn uploaded,
-              void *user) {
+              void *user, bool codec = false) {
     require_ok();
     if (!w || w->n_layers <= 0 || !w->layers || !w->final_norm || !w->inv_freq) throw Fail("incomplete transformer description");
-    if (w->window != 0) throw Fail("sliding-window attention is not supported on the device");
-    if (w->head_dim != 64 && w->head_dim != 128) throw Fail("head_dim must be 64 or 128 on this backend");
+    if (w->window != 0 && !codec) throw Fail("sliding-window attention is not supported on the device");
+    if (w->head_dim != 64 && w->head_dim != 128 && !codec) throw Fail("head_dim must be 64 or 128 on this backend");
     if (w->heads <= 0 || w->kv_heads <= 0 || w->heads % w->kv_heads || w->heads / w->kv_heads > 8)
         throw Fail("heads / kv_heads must be an integer group of at most 8");
     if (w->hidden % 32 || w->inter % 32) throw Fail("hidden and inter must be multiples of 32");
@@ -716,7 +720,7 @@ int make_xfmr(const voxhip_xfmr_desc *w, const char *name, int use_layers, const
         };
         for (int li = 0; li < nl; ++li) {
             const voxhip_layer &L = w->layers[li];
-            if (L.attn_scale || L.mlp_scale) throw Fail("layer scales are not supported on the device");
+            if ((L.attn_scale || L.mlp_scale) && !codec) throw Fail("layer scales are not supported on the device");
             if (!L.ln1 || !L.ln2) throw Fail("layer without norms");
             if ((L.qn == nullptr) != (L.kn == nullptr)) throw Fail("q_norm and k_norm must both be present or absent");
             LayerDev d;
@@ -2261,6 +2265,421 @@ int voxhip_cosy_end(int id) {
         Cosy &E = cosy_at(id);
         HIPCHECK(hipStreamSynchronize(g.stream));
         cosy_free_step(E);
+        return 1;
+    }, 0);
+}
+
+}  // extern "C"
+
+namespace {
+// ------------------------------------------------------------------ Qwen3-TTS codec decoder (gpu.hpp:53-60)
+constexpr int kCodecMaxFrames = 16;  // kGpuCodecMaxFrames (gpu.hpp:61)
+struct CodecConv {
+    int mat = -1, K = 1, cin = 0, cout = 0, dil = 1;
+};
+struct CodecSnake {
+    float *a = nullptr, *inv_b = nullptr;
+};
+struct CodecUp {
+    int tr = -1, K = 0, pw1 = -1, pw2 = -1, dwK = 0;
+    float *tr_b = nullptr, *dw_w = nullptr, *dw_b = nullptr, *ln_w = nullptr, *ln_b = nullptr, *gamma = nullptr;
+};
+struct CodecBlk {
+    CodecSnake act, a1[3], a2[3];
+    int tr = -1, K = 0, s = 0, cin = 0, cout = 0;
+    float *tr_b = nullptr;
+    CodecConv c1[3], c2[3];
+};
+struct Codec {
+    int cdim = 0, latent = 0, H = 0, heads = 0, kvh = 0, hd = 0, I = 0, W = 0, R = 0, layers = 0, spf = 0, dec = 0;
+    float eps = 1e-5f;
+    std::vector<float> inv_freq;
+    int xf = -1;  // the pre-transformer's stacked matrices and norms
+    std::vector<float *> sa, sm;  // layer scales [H] or null
+    CodecConv pre_conv, conv0, fin;
+    int pt_in = -1, pt_out = -1;
+    std::vector<CodecUp> ups;
+    std::vector<CodecBlk> blocks;
+    CodecSnake fin_act;
+    // scratch for kCodecMaxFrames frames: S activations (each smax floats), the transformer rows, z, the RoPE rows
+    float *S[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+    int64_t smax = 0;
+    float *qkv = nullptr, *ao = nullptr, *act = nullptr, *tmp = nullptr, *h = nullptr, *pre = nullptr, *rope = nullptr, *z = nullptr;
+};
+struct Hist2 {  // a streaming history as two buffers: the current one and the next call's
+    float *b[2] = {nullptr, nullptr};
+    int cur = 0, rows = 0, C = 0;
+};
+struct CodecSt {
+    int codec = -1;
+    int64_t len = 0;  // positions already in the transformer
+    Hist2 pre, c0, fin;
+    std::vector<Hist2> dw, tail, ru;
+    std::vector<float *> kr, vr;  // ring caches [R][kv_heads hd] per layer
+};
+
+Codec &codec_at(int id) {
+    if (id < 0 || size_t(id) >= g.codecs.size() || !g.codecs[size_t(id)]) throw Fail("bad codec handle " + std::to_string(id));
+    return *g.codecs[size_t(id)];
+}
+CodecSt &cstate_at(int id) {
+    if (id < 0 || size_t(id) >= g.cstates.size() || !g.cstates[size_t(id)]) throw Fail("bad codec state " + std::to_string(id));
+    return *g.cstates[size_t(id)];
+}
+
+CodecConv codec_conv_up(const voxhip_codec_conv &c, const char *what) {
+    const GpuMat &m = mat_at(c.mat);
+    if (c.K <= 0 || c.dil <= 0 || c.cin <= 0 || c.cin % 4 || m.rows != c.cout || m.cols != int64_t(c.K) * c.cin)
+        throw Fail(std::string("codec ") + what + ": weight must be [cout][K cin], cin a multiple of 4");
+    if (m.type != VOXHIP_F32 && m.type != VOXHIP_F16 && m.type != VOXHIP_BF16)
+        throw Fail(std::string("codec ") + what + ": f32 / f16 / bf16 weights only");
+    CodecConv o;
+    o.mat = c.mat; o.K = c.K; o.cin = c.cin; o.cout = c.cout; o.dil = c.dil;
+    return o;
+}
+CodecSnake codec_snake_up(const voxhip_codec_snake &s, int C) {
+    CodecSnake o;
+    o.a = upload_vec(s.a, C, "Snake a");
+    o.inv_b = upload_vec(s.inv_b, C, "Snake inv_b");
+    return o;
+}
+void codec_check_mat(int id, int64_t rows, int64_t cols, const char *what) {
+    const GpuMat &m = mat_at(id);
+    if (m.rows != rows || m.cols != cols) throw Fail(std::string("codec ") + what + " has the wrong shape");
+    if (m.type != VOXHIP_F32 && m.type != VOXHIP_F16 && m.type != VOXHIP_BF16)
+        throw Fail(std::string("codec ") + what + ": f32 / f16 / bf16 weights only");
+}
+
+Hist2 hist_new(int rows, int C) {
+    Hist2 h;
+    h.rows = rows; h.C = C;
+    for (float *&b : h.b) {
+        b = dalloc_t<float>(size_t(std::max(rows, 1)) * size_t(C));
+        HIPCHECK(hipMemset(b, 0, size_t(std::max(rows, 1)) * size_t(C) * 4));
+    }
+    return h;
+}
+Hist2 hist_clone(const Hist2 &src) {
+    Hist2 h = hist_new(src.rows, src.C);
+    HIPCHECK(hipMemcpy(h.b[0], src.b[src.cur], size_t(std::max(src.rows, 1)) * size_t(src.C) * 4, hipMemcpyDeviceToDevice));
+    return h;
+}
+void hist_free(Hist2 &h) {
+    for (float *&b : h.b) { dfree(b); b = nullptr; }
+}
+
+// A streaming convolution of T rows X (row stride ldx) into Y (row stride ldy): the conv GEMM over [hist; X], then the
+// history moves on (into the other buffer).
+void codec_conv(const CodecConv &c, Hist2 *h, const float *X, int64_t ldx, int T, float *Y, int64_t ldy, hipStream_t s) {
+    const GpuMat &M = mat_at(c.mat);
+    GemmArgs ga{};
+    ga.bias = M.b; ga.y = Y; ga.lda = ldx; ga.ldy = ldy; ga.m = T; ga.n = c.cout; ga.K = c.K * c.cin;
+    ga.cig = c.cin; ga.ksize = c.K; ga.dil = c.dil; ga.ctx = (c.K - 1) * c.dil; ga.hist = h ? h->b[h->cur] : nullptr;
+    ga.ws = g.gemm_ws; ga.ws_cap = kGemmWsFloats;
+    if (ga.ctx && !h) throw Fail("codec convolution without its history");
+    HIPCHECK(launch_stream_conv(gemv_type(M), M.w, M.s, X, ga, s));
+    if (ga.ctx) {
+        HIPCHECK(launch_hist_shift(h->b[1 - h->cur], h->b[h->cur], X, ldx, T, ga.ctx, c.cin, s));
+        h->cur = 1 - h->cur;
+    }
+}
+// y (=, +=, gelu, gamma-gated +=) W x + bias over rows of the f32-activation GEMM (the f32 tile semantics of matmul
+// for F32 / F16 / BF16 weights at any row count).
+void codec_gemm(int mat, int epi, const float *A, int64_t lda, int64_t rows, float *Y, int64_t ldy, const float *gate,
+                hipStream_t s) {
+    const GpuMat &M = mat_at(mat);
+    GemmArgs ga = gemm_args(M, M.b, Y, lda, ldy, rows);
+    ga.gate = gate;
+    HIPCHECK(launch_gemm(gemv_type(M), epi, M.w, M.s, A, ga, s));
+}
+
+// gpu_codec_forward's chain for T <= kCodecMaxFrames frames of z already on the device (E.z) and their RoPE rows
+// (E.rope); returns the sample count, left in E.S[4].
+int64_t codec_enqueue(Codec &E, CodecSt &St, int T, hipStream_t s) {
+    Xfmr &X = xf_at(E.xf);
+    const int L = E.latent, H = E.H, qd = E.heads * E.hd, QW = (E.heads + 2 * E.kvh) * E.hd;
+    float *A = E.S[0], *B = E.S[1];
+    // 1) pre_conv -> A [T][latent]; 2) the pre-transformer (kernels.cpp:760-844 with window and layer scales)
+    codec_conv(E.pre_conv, &St.pre, E.z, E.cdim, T, A, L, s);
+    gemv(mat_at(E.pt_in), T, PRO_X, EPI_STORE, A, L, T, E.h, H, nullptr, 0.f, nullptr, s);
+    const float scale = 1.0f / std::sqrt(float(E.hd));
+    for (int li = 0; li < E.layers; ++li) {
+        const LayerDev &d = X.L[size_t(li)];
+        gemv(mat_at(d.qkv), T, PRO_RMS, EPI_STORE, E.h, H, T, E.qkv, QW, X.norms + d.ln1, E.eps, nullptr, s, nullptr, E.pre);
+        HIPCHECK(launch_codec_rope_ring(E.qkv, QW, T, E.heads, E.kvh, E.hd, E.rope, St.kr[size_t(li)], St.vr[size_t(li)], E.R,
+                                        St.len, s));
+        HIPCHECK(launch_codec_attn(E.qkv, QW, St.kr[size_t(li)], St.vr[size_t(li)], E.R, T, E.heads, E.kvh, E.hd, St.len, E.W,
+                                   scale, E.ao, s));
+        if (E.sa[size_t(li)]) {
+            gemv(mat_at(d.o), T, PRO_X, EPI_STORE, E.ao, qd, T, E.tmp, H, nullptr, 0.f, nullptr, s);
+            HIPCHECK(launch_scale_acc(E.h, E.tmp, E.sa[size_t(li)], T, H, s));
+        } else {
+            gemv(mat_at(d.o), T, PRO_X, EPI_ACC, E.ao, qd, T, E.h, H, nullptr, 0.f, nullptr, s);
+        }
+        gemv(mat_at(d.gu), T, PRO_RMS, EPI_SWIGLU, E.h, H, T, E.act, E.I, X.norms + d.ln2, E.eps, nullptr, s, nullptr, E.pre);
+        if (E.sm[size_t(li)]) {
+            gemv(mat_at(d.down), T, PRO_X, EPI_STORE, E.act, E.I, T, E.tmp, H, nullptr, 0.f, nullptr, s);
+            HIPCHECK(launch_scale_acc(E.h, E.tmp, E.sm[size_t(li)], T, H, s));
+        } else {
+            gemv(mat_at(d.down), T, PRO_X, EPI_ACC, E.act, E.I, T, E.h, H, nullptr, 0.f, nullptr, s);
+        }
+    }
+    gemv(mat_at(E.pt_out), T, PRO_RMS, EPI_STORE, E.h, H, T, A, L, X.norms + X.final_off, E.eps, nullptr, s, nullptr, E.pre);
+    St.len += T;
+    // 3) upsample stages: transposed conv (K = stride: the overlap-add has no tail) + ConvNeXt
+    int64_t len = T;
+    float *cur = A;
+    for (size_t si = 0; si < E.ups.size(); ++si) {
+        const CodecUp &U = E.ups[si];
+        float *y = cur == A ? B : A;
+        codec_gemm(U.tr, EPI_STORE, cur, L, len, E.S[2], int64_t(U.K) * L, nullptr, s);
+        HIPCHECK(launch_ola(E.S[2], nullptr, nullptr, U.tr_b, y, int(len), U.K, U.K, L, s));
+        len *= U.K;
+        Hist2 &hd = St.dw[si];
+        HIPCHECK(launch_dwconv_causal(y, hd.b[hd.cur], U.dw_w, U.dw_b, E.S[2], int(len), L, U.dwK, s));
+        HIPCHECK(launch_hist_shift(hd.b[1 - hd.cur], hd.b[hd.cur], y, L, int(len), U.dwK - 1, L, s));
+        hd.cur = 1 - hd.cur;
+        HIPCHECK(launch_layernorm_rows(E.S[2], len, L, U.ln_w, U.ln_b, E.S[3], s));
+        codec_gemm(U.pw1, EPI_GELU_ERF, E.S[3], L, len, E.S[4], 4 * int64_t(L), nullptr, s);
+        codec_gemm(U.pw2, EPI_GATED_ACC, E.S[4], 4 * int64_t(L), len, y, L, U.gamma, s);
+        cur = y;
+    }
+    // 4) conv0 -> blocks -> Snake -> final conv -> clamp
+    float *x = cur == A ? B : A;
+    codec_conv(E.conv0, &St.c0, cur, L, int(len), x, E.dec, s);
+    int ch = E.dec;
+    for (size_t bi = 0; bi < E.blocks.size(); ++bi) {
+        const CodecBlk &Bk = E.blocks[bi];
+        float *sa = x == A ? B : A;
+        HIPCHECK(launch_snake(x, Bk.act.a, Bk.act.inv_b, sa, len, ch, s));
+        codec_gemm(Bk.tr, EPI_STORE, sa, ch, len, E.S[2], int64_t(Bk.K) * Bk.cout, nullptr, s);
+        float *y = x;  // x is consumed
+        Hist2 &tl = St.tail[bi];
+        HIPCHECK(launch_ola(E.S[2], tl.b[tl.cur], tl.b[1 - tl.cur], Bk.tr_b, y, int(len), Bk.s, Bk.K, Bk.cout, s));
+        tl.cur = 1 - tl.cur;
+        len *= Bk.s;
+        ch = Bk.cout;
+        for (int u = 0; u < 3; ++u) {
+            HIPCHECK(launch_snake(y, Bk.a1[u].a, Bk.a1[u].inv_b, sa, len, ch, s));
+            codec_conv(Bk.c1[u], &St.ru[bi * 3 + size_t(u)], sa, ch, int(len), E.S[3], ch, s);
+            HIPCHECK(launch_snake(E.S[3], Bk.a2[u].a, Bk.a2[u].inv_b, E.S[3], len, ch, s));
+            codec_gemm(Bk.c2[u].mat, EPI_ACC, E.S[3], ch, len, y, ch, nullptr, s);
+        }
+        x = y;
+    }
+    float *sa = x == A ? B : A;
+    HIPCHECK(launch_snake(x, E.fin_act.a, E.fin_act.inv_b, sa, len, ch, s));
+    codec_conv(E.fin, &St.fin, sa, ch, int(len), E.S[4], 1, s);
+    HIPCHECK(launch_clamp1(E.S[4], len, s));
+    return len;
+}
+}  // namespace
+
+extern "C" {
+
+int voxhip_codec_create(const voxhip_codec_desc *d) {
+    return guard_int([&] {
+        require_ok();
+        if (!d || !d->pt_mats || d->pt.n_layers <= 0 || (d->n_ups && !d->ups) || (d->n_blocks && !d->blocks) || d->n_ups < 0 ||
+            d->n_blocks < 0)
+            throw Fail("incomplete codec description");
+        const voxhip_xfmr_desc &pt = d->pt;
+        if (pt.window <= 0 || pt.window > 1024 || pt.head_dim <= 0 || pt.head_dim > 128 || pt.head_dim % 2)
+            throw Fail("codec transformer: window 1..1024, even head_dim <= 128");
+        for (int li = 0; li < pt.n_layers; ++li) {
+            const voxhip_layer &L = pt.layers[li];
+            if (L.qn || L.kn) throw Fail("codec transformer with q / k norm is not supported");
+            for (int j = 0; j < 7; ++j)
+                if (mat_at(d->pt_mats[li * 7 + j]).b) throw Fail("codec transformer with biased projections is not supported");
+        }
+        std::unique_ptr<Codec> E(new Codec());
+        E->cdim = d->codebook_dim; E->latent = d->latent; E->H = pt.hidden; E->heads = pt.heads; E->kvh = pt.kv_heads;
+        E->hd = pt.head_dim; E->I = pt.inter; E->W = pt.window; E->R = pt.window + kCodecMaxFrames; E->layers = pt.n_layers;
+        E->eps = pt.eps;
+        E->inv_freq.assign(pt.inv_freq, pt.inv_freq + pt.head_dim / 2);
+        if (E->cdim <= 0 || E->cdim % 4 || E->latent <= 0 || E->latent % 4) throw Fail("codec: codebook_dim and latent multiples of 4");
+        E->xf = make_xfmr(&pt, "codec", -1, d->pt_mats, nullptr, nullptr, true);
+        for (int li = 0; li < pt.n_layers; ++li) {
+            const voxhip_layer &L = pt.layers[li];
+            E->sa.push_back(L.attn_scale ? upload_vec(L.attn_scale, pt.hidden, "attn scale") : nullptr);
+            E->sm.push_back(L.mlp_scale ? upload_vec(L.mlp_scale, pt.hidden, "mlp scale") : nullptr);
+        }
+        E->pre_conv = codec_conv_up(d->pre_conv, "pre_conv");
+        if (E->pre_conv.cin != E->cdim || E->pre_conv.cout != E->latent) throw Fail("codec pre_conv: codebook_dim -> latent");
+        codec_check_mat(d->pt_in, pt.hidden, E->latent, "pre_transformer.input_proj");
+        codec_check_mat(d->pt_out, E->latent, pt.hidden, "pre_transformer.output_proj");
+        E->pt_in = d->pt_in; E->pt_out = d->pt_out;
+        const int L = E->latent;
+        int64_t len = kCodecMaxFrames, mx = int64_t(kCodecMaxFrames) * std::max({E->cdim, L, E->H, E->I});
+        for (int i = 0; i < d->n_ups; ++i) {
+            const voxhip_codec_up &u = d->ups[i];
+            if (u.K <= 0 || u.dw_K <= 0) throw Fail("codec upsample stage: K and dw_K positive");
+            codec_check_mat(u.tr, int64_t(u.K) * L, L, "upsample transposed conv");
+            codec_check_mat(u.pw1, 4 * int64_t(L), L, "upsample pwconv1");
+            codec_check_mat(u.pw2, L, 4 * int64_t(L), "upsample pwconv2");
+            CodecUp U;
+            U.tr = u.tr; U.K = u.K; U.pw1 = u.pw1; U.pw2 = u.pw2; U.dwK = u.dw_K;
+            U.tr_b = upload_vec(u.tr_b, L, "upsample bias");
+            U.dw_w = upload_vec(u.dw_w, L * u.dw_K, "depthwise weight");
+            U.dw_b = upload_vec(u.dw_b, L, "depthwise bias");
+            U.ln_w = upload_vec(u.ln_w, L, "norm weight");
+            U.ln_b = upload_vec(u.ln_b, L, "norm bias");
+            U.gamma = upload_vec(u.gamma, L, "gamma");
+            E->ups.push_back(U);
+            mx = std::max(mx, len * u.K * L);
+            len *= u.K;
+            mx = std::max(mx, len * 4 * L);
+        }
+        E->conv0 = codec_conv_up(d->conv0, "conv0");
+        if (E->conv0.cin != L) throw Fail("codec conv0: latent input");
+        E->dec = E->conv0.cout;
+        mx = std::max(mx, len * E->dec);
+        int ch = E->dec;
+        for (int b = 0; b < d->n_blocks; ++b) {
+            const voxhip_codec_block &k = d->blocks[b];
+            if (k.cin != ch || k.stride <= 0 || k.K < k.stride || k.K > 2 * k.stride || k.cout <= 0 || k.cout % 4)
+                throw Fail("codec decoder block: cin = the previous width, stride < K <= 2 stride, cout a multiple of 4");
+            codec_check_mat(k.tr, int64_t(k.K) * k.cout, k.cin, "decoder transposed conv");
+            CodecBlk Bk;
+            Bk.act = codec_snake_up(k.act, k.cin);
+            Bk.tr = k.tr; Bk.K = k.K; Bk.s = k.stride; Bk.cin = k.cin; Bk.cout = k.cout;
+            Bk.tr_b = upload_vec(k.tr_b, k.cout, "decoder transposed conv bias");
+            for (int u = 0; u < 3; ++u) {
+                Bk.a1[u] = codec_snake_up(k.a1[u], k.cout);
+                Bk.a2[u] = codec_snake_up(k.a2[u], k.cout);
+                Bk.c1[u] = codec_conv_up(k.c1[u], "residual conv 1");
+                Bk.c2[u] = codec_conv_up(k.c2[u], "residual conv 2");
+                if (Bk.c1[u].cin != k.cout || Bk.c1[u].cout != k.cout || Bk.c2[u].cin != k.cout || Bk.c2[u].cout != k.cout ||
+                    Bk.c2[u].K != 1)
+                    throw Fail("codec residual unit: cout -> cout, conv 2 with K 1");
+            }
+            E->blocks.push_back(Bk);
+            mx = std::max(mx, len * k.K * k.cout);
+            len *= k.stride;
+            mx = std::max(mx, len * k.cout);
+            ch = k.cout;
+        }
+        E->fin_act = codec_snake_up(d->final_act, ch);
+        E->fin = codec_conv_up(d->final_conv, "final conv");
+        if (E->fin.cin != ch || E->fin.cout != 1) throw Fail("codec final conv: the last width -> 1");
+        E->spf = int(len / kCodecMaxFrames);
+        E->smax = mx;
+        for (float *&p : E->S) p = dalloc_t<float>(size_t(mx));
+        const size_t F = kCodecMaxFrames;
+        E->qkv = dalloc_t<float>(F * size_t((E->heads + 2 * E->kvh) * E->hd));
+        E->ao = dalloc_t<float>(F * size_t(E->heads * E->hd));
+        E->act = dalloc_t<float>(F * size_t(E->I));
+        E->tmp = dalloc_t<float>(F * size_t(E->H));
+        E->h = dalloc_t<float>(F * size_t(E->H));
+        E->pre = dalloc_t<float>(F * size_t(std::max(E->H, E->I)));
+        E->rope = dalloc_t<float>(F * size_t(E->hd));
+        E->z = dalloc_t<float>(F * size_t(E->cdim));
+        g.codecs.push_back(E.release());
+        return int(g.codecs.size()) - 1;
+    }, -1);
+}
+
+int voxhip_codec_spf(int codec, int32_t *spf) {
+    return guard_int([&] {
+        require_ok();
+        if (!spf) throw Fail("missing argument");
+        *spf = codec_at(codec).spf;
+        return 1;
+    }, 0);
+}
+
+int voxhip_codec_state_new(int codec) {
+    return guard_int([&] {
+        require_ok();
+        const Codec &E = codec_at(codec);
+        std::unique_ptr<CodecSt> S(new CodecSt());
+        S->codec = codec;
+        S->pre = hist_new((E.pre_conv.K - 1) * E.pre_conv.dil, E.pre_conv.cin);
+        const size_t kd = size_t(E.kvh) * E.hd;
+        for (int l = 0; l < E.layers; ++l) {
+            S->kr.push_back(dalloc_t<float>(size_t(E.R) * kd));
+            S->vr.push_back(dalloc_t<float>(size_t(E.R) * kd));
+            HIPCHECK(hipMemset(S->kr.back(), 0, size_t(E.R) * kd * 4));
+            HIPCHECK(hipMemset(S->vr.back(), 0, size_t(E.R) * kd * 4));
+        }
+        for (const CodecUp &u : E.ups) S->dw.push_back(hist_new(u.dwK - 1, E.latent));
+        S->c0 = hist_new((E.conv0.K - 1) * E.conv0.dil, E.conv0.cin);
+        for (const CodecBlk &b : E.blocks) {
+            S->tail.push_back(hist_new(b.K - b.s, b.cout));
+            for (int u = 0; u < 3; ++u) S->ru.push_back(hist_new((b.c1[u].K - 1) * b.c1[u].dil, b.c1[u].cin));
+        }
+        S->fin = hist_new((E.fin.K - 1) * E.fin.dil, E.fin.cin);
+        g.cstates.push_back(S.release());
+        return int(g.cstates.size()) - 1;
+    }, -1);
+}
+
+int voxhip_codec_state_clone(int state) {
+    return guard_int([&] {
+        require_ok();
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        const CodecSt &src = cstate_at(state);
+        const Codec &E = codec_at(src.codec);
+        std::unique_ptr<CodecSt> S(new CodecSt());
+        S->codec = src.codec;
+        S->len = src.len;
+        S->pre = hist_clone(src.pre);
+        S->c0 = hist_clone(src.c0);
+        S->fin = hist_clone(src.fin);
+        for (const Hist2 &h : src.dw) S->dw.push_back(hist_clone(h));
+        for (const Hist2 &h : src.tail) S->tail.push_back(hist_clone(h));
+        for (const Hist2 &h : src.ru) S->ru.push_back(hist_clone(h));
+        const size_t kd = size_t(E.kvh) * E.hd;
+        for (size_t l = 0; l < src.kr.size(); ++l) {
+            S->kr.push_back(dalloc_t<float>(size_t(E.R) * kd));
+            S->vr.push_back(dalloc_t<float>(size_t(E.R) * kd));
+            HIPCHECK(hipMemcpy(S->kr.back(), src.kr[l], size_t(E.R) * kd * 4, hipMemcpyDeviceToDevice));
+            HIPCHECK(hipMemcpy(S->vr.back(), src.vr[l], size_t(E.R) * kd * 4, hipMemcpyDeviceToDevice));
+        }
+        g.cstates.push_back(S.release());
+        return int(g.cstates.size()) - 1;
+    }, -1);
+}
+
+int voxhip_codec_state_free(int state) {
+    return guard_int([&] {
+        require_ok();
+        CodecSt &S = cstate_at(state);
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        for (Hist2 *h : {&S.pre, &S.c0, &S.fin}) hist_free(*h);
+        for (auto *v : {&S.dw, &S.tail, &S.ru})
+            for (Hist2 &h : *v) hist_free(h);
+        for (float *p : S.kr) dfree(p);
+        for (float *p : S.vr) dfree(p);
+        delete g.cstates[size_t(state)];
+        g.cstates[size_t(state)] = nullptr;
+        return 1;
+    }, 0);
+}
+
+int voxhip_codec_forward(int codec, int state, const float *z, int F, float *pcm, int64_t *n_out) {
+    return guard_int([&] {
+        require_ok();
+        Codec &E = codec_at(codec);
+        CodecSt &St = cstate_at(state);
+        if (St.codec != codec) throw Fail("the codec state belongs to another codec");
+        if (F <= 0 || F > kCodecMaxFrames) throw Fail("codec forward: 1 to 16 frames per call");
+        if (!z || !pcm) throw Fail("missing argument");
+        // the RoPE rows of positions len .. len + F - 1 on the host, as rope_apply takes them (kernels.cpp:744-747)
+        const int half = E.hd / 2;
+        std::vector<float> cs(size_t(F) * size_t(E.hd));
+        for (int i = 0; i < F; ++i)
+            for (int p = 0; p < half; ++p) {
+                const float f = E.inv_freq[size_t(p)] * float(St.len + i);
+                cs[size_t(i * E.hd + 2 * p)] = std::cos(f);
+                cs[size_t(i * E.hd + 2 * p + 1)] = std::sin(f);
+            }
+        h2d(E.z, z, size_t(F) * size_t(E.cdim) * 4);
+        h2d(E.rope, cs.data(), cs.size() * 4);
+        const int64_t n = codec_enqueue(E, St, F, g.stream);
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        HIPCHECK(hipMemcpy(pcm, E.S[4], size_t(n) * 4, hipMemcpyDeviceToHost));
+        if (n_out) *n_out = n;
         return 1;
     }, 0);
 }

@@ -138,6 +138,90 @@ F5_VOCOS = dict(dim=512, inter=1536, layers=8, out=1026, frames=938)
 COSY_FLOW = dict(M=80, C=256, heads=8, head_dim=64, ff=1024, n_x=4, n_mid=12, frames=512, steps=10, wtype=vh.F16)
 
 
+# Qwen3-TTS's codec decoder (the 12 Hz tokenizer, python/vox/build.py:35-38 CODEC_DEFAULTS, codebook_dim 512): 16
+# codebooks of 2048, pre_conv 512 -> 1024, an 8-layer windowed transformer (hidden 1024, 16 x 64 heads, window 72,
+# FFN 3072, layer scales), upsampling ratios [2, 2], decoder 1536 channels with rates [8, 5, 4, 3]: 1920 samples of
+# 24 kHz per frame (80 ms); f32 weights (the converter's default codec precision)
+QWEN3_CODEC = dict(codebook_dim=512, latent=1024, hidden=1024, heads=16, kv_heads=16, head_dim=64, window=72, inter=3072,
+                   layers=8, ratios=[2, 2], rates=[8, 5, 4, 3], dec=1536, wtype=vh.F32)
+
+
+class CodecDec:
+    """A device-resident Qwen3-TTS codec decoder with synthetic weights (matrices generated on the device, the norms,
+    Snake parameters and depthwise taps on the host)."""
+
+    def __init__(self, cfg, seed=0):
+        c = dict(cfg)
+        self.cfg = c
+        rng = np.random.default_rng(seed)
+        stream = [0x9000]
+        self.mats = []
+        CD, L, H, hd, I, dec = c["codebook_dim"], c["latent"], c["hidden"], c["head_dim"], c["inter"], c["dec"]
+
+        def mat(rows, cols, std, bias):
+            stream[0] += 1
+            h = vh.mat_synthetic(c["wtype"], rows, cols, seed, stream[0], 0.0, std, bias=bias)
+            self.mats.append(h)
+            return h
+
+        def conv(K, cin, cout, dil=1, gain=1.0):
+            return (mat(cout, K * cin, gain / np.sqrt(K * cin), True), K, cin, cout, dil)
+
+        def vec(n, m, sd):
+            return (m + sd * rng.standard_normal(n)).astype(np.float32)
+
+        def snake(C):
+            return (np.exp(vec(C, 0, 0.3)).astype(np.float32), (1.0 / (np.exp(vec(C, 0, 0.3)) + 1e-9)).astype(np.float32))
+        qd, kd = c["heads"] * hd, c["kv_heads"] * hd
+        ids, layers = [], []
+        for _ in range(c["layers"]):
+            ids.append([mat(qd, H, H ** -0.5, False), mat(kd, H, H ** -0.5, False), mat(kd, H, H ** -0.5, False),
+                        mat(H, qd, qd ** -0.5, False), mat(I, H, H ** -0.5, False), mat(I, H, H ** -0.5, False),
+                        mat(H, I, I ** -0.5, False)])
+            layers.append(dict(ln1=vec(H, 1, 0.1), ln2=vec(H, 1, 0.1), attn_scale=vec(H, 0.01, 0.001),
+                               mlp_scale=vec(H, 0.01, 0.001)))
+        inv = (1.0 / (10000.0 ** (np.arange(0, hd, 2, dtype=np.float64) / hd))).astype(np.float32)
+        pt = dict(hidden=H, heads=c["heads"], kv_heads=c["kv_heads"], head_dim=hd, inter=I, eps=1e-5, theta=10000.0,
+                  window=c["window"], inv_freq=inv, final_norm=vec(H, 1, 0.1), layers=layers)
+        ups = [dict(tr=mat(r * L, L, L ** -0.5, False), K=r, tr_b=vec(L, 0, 0.02), dw_w=vec(L * 7, 0, 0.3),
+                    dw_b=vec(L, 0, 0.02), dw_K=7, ln_w=vec(L, 1, 0.1), ln_b=vec(L, 0, 0.1), gamma=vec(L, 0, 0.1),
+                    pw1=mat(4 * L, L, L ** -0.5, True), pw2=mat(L, 4 * L, (4 * L) ** -0.5, True)) for r in c["ratios"]]
+        blocks = []
+        for b, r in enumerate(c["rates"]):
+            ind, outd = dec >> b, dec >> (b + 1)
+            blocks.append(dict(act=snake(ind), tr=mat(2 * r * outd, ind, (2 * ind) ** -0.5, False), K=2 * r, stride=r, cin=ind,
+                               cout=outd, tr_b=vec(outd, 0, 0.02), a1=[snake(outd) for _ in range(3)],
+                               a2=[snake(outd) for _ in range(3)],
+                               c1=[conv(7, outd, outd, dil, 0.3) for dil in (1, 3, 9)],
+                               c2=[conv(1, outd, outd, 1, 0.3) for _ in range(3)]))
+        nb = len(c["rates"])
+        self.codec = vh.codec_create(CD, L, conv(3, CD, L), mat(H, L, L ** -0.5, True), mat(L, H, H ** -0.5, True), pt, ids,
+                                     ups, conv(7, L, dec), blocks, snake(dec >> nb), conv(7, dec >> nb, 1, 1, 0.1))
+        self.spf = vh.codec_spf(self.codec)
+
+    def flops_per_frame(self):
+        """FLOPs of one frame (2 per multiply-add), as the layers run: pre_conv, transformer, upsampling, conv0, blocks."""
+        c = self.cfg
+        CD, L, H, hd, I, dec = c["codebook_dim"], c["latent"], c["hidden"], c["head_dim"], c["inter"], c["dec"]
+        qd, kd = c["heads"] * hd, c["kv_heads"] * hd
+        fl = 2 * 3 * CD * L + 2 * 2 * L * H
+        fl += c["layers"] * (2 * H * (qd + 2 * kd + 2 * I) + 2 * qd * H + 2 * I * H + 4 * c["window"] * qd)
+        pos = 1
+        for r in c["ratios"]:
+            fl += 2 * L * L * r * pos
+            pos *= r
+            fl += pos * (2 * 7 * L + 2 * 2 * 4 * L * L)
+        fl += pos * 2 * 7 * L * dec
+        ch = dec
+        for r in c["rates"]:
+            out = ch // 2
+            fl += pos * 2 * ch * out * 2 * r
+            pos *= r
+            fl += pos * 3 * (2 * 7 * out * out + 2 * out * out)
+            ch = out
+        return fl + pos * 2 * 7 * ch
+
+
 class CosyFlow:
     """A device-resident CosyVoice2 flow estimator with synthetic weights (linears generated on the device, the causal
     convolutions and the norms on the host)."""

@@ -111,6 +111,33 @@ class CosyDesc(C.Structure):
                [("fn_w", C.c_void_p), ("fn_b", C.c_void_p)]
 
 
+class CodecConv(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("mat", "K", "cin", "cout", "dil")]
+
+
+class CodecSnake(C.Structure):
+    _fields_ = [("a", C.c_void_p), ("inv_b", C.c_void_p)]
+
+
+class CodecUp(C.Structure):
+    _fields_ = [("tr", C.c_int32), ("K", C.c_int32), ("tr_b", C.c_void_p), ("dw_w", C.c_void_p), ("dw_b", C.c_void_p),
+                ("dw_K", C.c_int32), ("ln_w", C.c_void_p), ("ln_b", C.c_void_p), ("gamma", C.c_void_p), ("pw1", C.c_int32),
+                ("pw2", C.c_int32)]
+
+
+class CodecBlock(C.Structure):
+    _fields_ = [("act", CodecSnake)] + [(n, C.c_int32) for n in ("tr", "K", "stride", "cin", "cout")] + \
+               [("tr_b", C.c_void_p), ("a1", CodecSnake * 3), ("a2", CodecSnake * 3), ("c1", CodecConv * 3),
+                ("c2", CodecConv * 3)]
+
+
+class CodecDesc(C.Structure):
+    _fields_ = [("codebook_dim", C.c_int32), ("latent", C.c_int32), ("pre_conv", CodecConv), ("pt_in", C.c_int32),
+                ("pt_out", C.c_int32), ("pt", XfmrDesc), ("pt_mats", C.c_void_p), ("ups", C.POINTER(CodecUp)),
+                ("n_ups", C.c_int32), ("conv0", CodecConv), ("blocks", C.POINTER(CodecBlock)), ("n_blocks", C.c_int32),
+                ("final_act", CodecSnake), ("final_conv", CodecConv)]
+
+
 KERNEL_CLASSES = ("qkv_gemv", "o_gemv", "gateup_gemv", "down_gemv", "head_gemv", "attention", "attn_combine", "qk_post", "sampler")
 
 
@@ -162,6 +189,12 @@ SIGNATURES = {
     "voxhip_f5_vocos": (_I, [_I, _P, _I, _P]),
     "voxhip_f5_vocos_out": (_I, [_I, _P]),
     "voxhip_cosy_create": (_I, [C.POINTER(CosyDesc)]),
+    "voxhip_codec_create": (_I, [C.POINTER(CodecDesc)]),
+    "voxhip_codec_state_new": (_I, [_I]),
+    "voxhip_codec_state_clone": (_I, [_I]),
+    "voxhip_codec_state_free": (_I, [_I]),
+    "voxhip_codec_forward": (_I, [_I, _I, _P, _I, _P, _P]),
+    "voxhip_codec_spf": (_I, [_I, _P]),
     "voxhip_cosy_begin": (_I, [_I, _I, _P]),
     "voxhip_cosy_step": (_I, [_I, _P, _P, _P]),
     "voxhip_cosy_end": (_I, [_I]),
@@ -615,6 +648,75 @@ def cosy_step(cosy, x, tb, T, M):
 
 def cosy_end(cosy):
     _check(lib().voxhip_cosy_end(cosy), "cosy_end")
+
+
+def codec_create(codebook_dim, latent, pre_conv, pt_in, pt_out, pt, pt_mats, ups, conv0, blocks, final_act, final_conv):
+    """gpu_codec_create: convs = (handle, K, cin, cout, dil); snakes = (a, inv_b) arrays; pt = dict of the pre-
+    transformer (hidden, heads, kv_heads, head_dim, inter, eps, theta, window, inv_freq, final_norm, layers = list of
+    dicts ln1, ln2, attn_scale, mlp_scale); pt_mats [layers][7] handles; ups = dicts tr, K, tr_b, dw_w, dw_b, dw_K, ln_w,
+    ln_b, gamma, pw1, pw2; blocks = dicts act, tr, K, stride, cin, cout, tr_b, a1, a2 (3 snakes), c1, c2 (3 convs)."""
+    keep = []
+
+    def vec(a):
+        a = f32(a)
+        keep.append(a)
+        return _p(a)
+
+    def snake(sn):
+        return CodecSnake(vec(sn[0]), vec(sn[1]))
+    lay = (Layer * len(pt["layers"]))()
+    for i, L in enumerate(pt["layers"]):
+        for n in ("ln1", "ln2", "attn_scale", "mlp_scale"):
+            if L.get(n) is not None:
+                setattr(lay[i], n, vec(L[n]))
+    keep.append(lay)
+    xd = XfmrDesc(len(pt["layers"]), lay, vec(pt["final_norm"]), pt["hidden"], pt["heads"], pt["kv_heads"], pt["head_dim"],
+                  pt["inter"], pt["eps"], pt["theta"], pt["window"], vec(pt["inv_freq"]))
+    ids = np.ascontiguousarray(pt_mats, np.int32)
+    keep.append(ids)
+    ua = (CodecUp * max(1, len(ups)))()
+    for i, u in enumerate(ups):
+        ua[i] = CodecUp(u["tr"], u["K"], vec(u["tr_b"]), vec(u["dw_w"]), vec(u["dw_b"]), u["dw_K"], vec(u["ln_w"]),
+                        vec(u["ln_b"]), vec(u["gamma"]), u["pw1"], u["pw2"])
+    ba = (CodecBlock * max(1, len(blocks)))()
+    for i, b in enumerate(blocks):
+        blk = ba[i]
+        blk.act = snake(b["act"])
+        blk.tr, blk.K, blk.stride, blk.cin, blk.cout, blk.tr_b = b["tr"], b["K"], b["stride"], b["cin"], b["cout"], vec(b["tr_b"])
+        for u in range(3):
+            blk.a1[u], blk.a2[u] = snake(b["a1"][u]), snake(b["a2"][u])
+            blk.c1[u], blk.c2[u] = CodecConv(*b["c1"][u]), CodecConv(*b["c2"][u])
+    keep += [ua, ba]
+    d = CodecDesc(codebook_dim, latent, CodecConv(*pre_conv), pt_in, pt_out, xd, _p(ids), ua, len(ups), CodecConv(*conv0), ba,
+                  len(blocks), snake(final_act), CodecConv(*final_conv))
+    return _handle(lib().voxhip_codec_create(C.byref(d)), "codec_create")
+
+
+def codec_spf(codec):
+    v = C.c_int32()
+    _check(lib().voxhip_codec_spf(codec, C.byref(v)), "codec_spf")
+    return v.value
+
+
+def codec_state_new(codec):
+    return _handle(lib().voxhip_codec_state_new(codec), "codec_state_new")
+
+
+def codec_state_clone(state):
+    return _handle(lib().voxhip_codec_state_clone(state), "codec_state_clone")
+
+
+def codec_state_free(state):
+    _check(lib().voxhip_codec_state_free(state), "codec_state_free")
+
+
+def codec_forward(codec, state, z):
+    """gpu_codec_forward: z [F][codebook_dim] (F <= 16) -> pcm [F spf]."""
+    z = f32(z)
+    out = np.empty(z.shape[0] * codec_spf(codec), np.float32)
+    n = C.c_int64()
+    _check(lib().voxhip_codec_forward(codec, state, _p(z), z.shape[0], _p(out), C.byref(n)), "codec_forward")
+    return out[:n.value]
 
 
 def sync():
