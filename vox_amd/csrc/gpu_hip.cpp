@@ -6,13 +6,13 @@
 //
 // Error convention of the reference backend (gpu_vulkan.cpp:568-571, :800-803): no exception escapes, false/-1
 // means "compute on the CPU", the reason is kept for gpu_stats().last_error, and one warning goes to stderr.
-// Entry points not provided by this backend yet (the codec) answer like gpu_stub.cpp, so their callers stay on the
-// CPU.
+// gpu_gemm_choice / gpu_gemm_preset (the Vulkan backend's F5 GEMM tuning) answer like gpu_stub.cpp.
 #include <cstdio>
 #include <cstring>
 #include <mutex>
 
 #include "gpu.hpp"
+#include "qwen3.hpp"
 #include "voxhip.h"
 
 namespace vox {
@@ -231,6 +231,72 @@ bool gpu_f5_vocos(int id, const float *mel, int T, std::vector<float> &head) {
     return false;
 }
 
+// The Qwen3-TTS codec decoder (gpu_codec.cpp:205-556): the layers of Qwen3Weights (their matrices already uploaded by
+// Qwen3Weights::upload_gpu, qwen3.cpp:326-331) flattened for the C ABI; -1 / false keeps the decoder on the CPU
+// (qwen3.cpp:332-338, :396-400).
+int gpu_codec_create(const Qwen3Weights &w) {
+    auto conv = [](const CConv &c) { return voxhip_codec_conv{c.w.gpu, c.K, c.cin, c.cout, c.dil}; };
+    auto snake = [](const Snake &s) { return voxhip_codec_snake{s.a.data(), s.inv_b.data()}; };
+    const TransformerW &pt = w.pt;
+    std::vector<voxhip_layer> L(pt.layers.size());
+    std::vector<int32_t> ids;
+    for (size_t i = 0; i < pt.layers.size(); ++i) {
+        const LayerW &s = pt.layers[i];
+        for (const Mat *m : {&s.q, &s.k, &s.v, &s.o, &s.gate, &s.up, &s.down}) ids.push_back(m->gpu);
+        L[i].qn = s.qn; L[i].kn = s.kn; L[i].ln1 = s.ln1; L[i].ln2 = s.ln2;
+        L[i].attn_scale = s.attn_scale; L[i].mlp_scale = s.mlp_scale;
+    }
+    std::vector<voxhip_codec_up> ups;
+    for (const Qwen3Weights::UpStage &u : w.up) {
+        if (u.tr.K != u.tr.stride) return -1;  // as gpu_codec.cpp:246
+        ups.push_back({u.tr.w.gpu, u.tr.K, u.tr_b, u.dw.w, u.dw.b, u.dw.K, u.ln_w, u.ln_b, u.gamma, u.pw1.gpu, u.pw2.gpu});
+    }
+    std::vector<voxhip_codec_block> blocks;
+    for (const Qwen3Weights::DecBlock &d : w.blocks) {
+        voxhip_codec_block b{};
+        b.act = snake(d.act);
+        b.tr = d.tr.w.gpu; b.K = d.tr.K; b.stride = d.tr.stride; b.cin = d.tr.cin; b.cout = d.tr.cout; b.tr_b = d.tr_b;
+        for (int u = 0; u < 3; ++u) {
+            b.a1[u] = snake(d.a1[u]); b.a2[u] = snake(d.a2[u]);
+            b.c1[u] = conv(d.c1[u]); b.c2[u] = conv(d.c2[u]);
+        }
+        blocks.push_back(b);
+    }
+    voxhip_codec_desc c{};
+    c.codebook_dim = w.cc.codebook_dim; c.latent = w.cc.latent;
+    c.pre_conv = conv(w.pre_conv); c.pt_in = w.pt_in.gpu; c.pt_out = w.pt_out.gpu;
+    c.pt.n_layers = int32_t(L.size()); c.pt.layers = L.data(); c.pt.final_norm = pt.final_norm;
+    c.pt.hidden = pt.hidden; c.pt.heads = pt.heads; c.pt.kv_heads = pt.kv_heads; c.pt.head_dim = pt.head_dim; c.pt.inter = pt.inter;
+    c.pt.eps = pt.eps; c.pt.theta = pt.theta; c.pt.window = pt.window; c.pt.inv_freq = pt.inv_freq.data();
+    c.pt_mats = ids.data();
+    c.ups = ups.data(); c.n_ups = int32_t(ups.size());
+    c.conv0 = conv(w.conv0);
+    c.blocks = blocks.data(); c.n_blocks = int32_t(blocks.size());
+    c.final_act = snake(w.final_act); c.final_conv = conv(w.final_conv);
+    const int id = voxhip_codec_create(&c);
+    if (id < 0) warn_once("codec decoder");
+    return id;
+}
+int gpu_codec_state_new(int codec) { return voxhip_codec_state_new(codec); }
+int gpu_codec_state_clone(int state) { return voxhip_codec_state_clone(state); }
+void gpu_codec_state_free(int state) { (void)voxhip_codec_state_free(state); }
+// Appends F frames of PCM (F <= kGpuCodecMaxFrames; codec_forward, qwen3.cpp:396-400, calls in such chunks).
+bool gpu_codec_forward(int codec, int state, const float *z, int F, std::vector<float> &pcm) {
+    if (F <= 0) return true;
+    int32_t spf = 0;
+    if (!voxhip_codec_spf(codec, &spf)) return false;
+    const size_t off = pcm.size();
+    pcm.resize(off + size_t(F) * size_t(spf));
+    int64_t n = 0;
+    if (!voxhip_codec_forward(codec, state, z, F, pcm.data() + off, &n)) {
+        pcm.resize(off);
+        std::fprintf(stderr, "vox: GPU codec decoder failed: %s\n", voxhip_last_error());
+        return false;
+    }
+    pcm.resize(off + size_t(n));
+    return true;
+}
+
 // The CosyVoice2 / Chatterbox flow estimator (gpu_f5.cpp:382-556): the description flattened for the C ABI (mid
 // block i's transformer list as mid_x_count[i] consecutive entries); -1 / false keeps the flow on the CPU
 // (cosyvoice.cpp:557, :828-830).
@@ -300,11 +366,6 @@ bool gpu_pred_frame(const TransformerW &w, int seq, const float *in2, const Mat 
 }
 
 // ---- not provided by this backend yet: the callers compute on the CPU (gpu_stub.cpp behaviour)
-int gpu_codec_create(const Qwen3Weights &) { return -1; }
-int gpu_codec_state_new(int) { return -1; }
-int gpu_codec_state_clone(int) { return -1; }
-void gpu_codec_state_free(int) {}
-bool gpu_codec_forward(int, int, const float *, int, std::vector<float> &) { return false; }
 std::string gpu_gemm_choice() { return ""; }
 void gpu_gemm_preset(const std::string &) {}
 
