@@ -74,6 +74,14 @@ static hipError_t gemm_tile(const uint8_t *w, const float *scale, const float *A
         if (e != hipSuccess || split) return e;
         return gemm_run_h16<WT, EPI, 2, 2>(w, scale, A, g, s);
     } else {
+        if constexpr (EPI == EPI_STORE || EPI == EPI_ACC || EPI == EPI_GATED_ACC || EPI == EPI_SWIGLU) {
+            GemmArgs gs = g;  // the same K slices on the f32 kernel (few-row passes over f32 / bf16 weights)
+            const int splits = split_plan(g, &gs.kchunk);
+            if (splits) {
+                hipError_t e = gemm_run<WT, EPI_STORE, ASRC_ROWS, 2>(w, scale, A, gs, splits, s);
+                return e != hipSuccess ? e : splitk_reduce<EPI>(g, splits, s);
+            }
+        }
         return gemm_run<WT, EPI, ASRC_ROWS, 2>(w, scale, A, g, 1, s);
     }
 }
