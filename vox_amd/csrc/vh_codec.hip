@@ -47,7 +47,7 @@ hipError_t launch_codec_attn(const float *qkv, int ld, const float *ring_k, cons
                              int hd, int64_t pos0, int W, float scale, float *ao, hipStream_t s) {
     if (F <= 0) return hipSuccess;
     // the ring holds the window of every row of the call: R >= W + F - 1
-    if (hd <= 0 || hd > 128 || heads <= 0 || kvh <= 0 || heads % kvh || W <= 0 || W > 1024 || R < W + F - 1)
+    if (hd <= 0 || hd > 128 || hd % 4 || heads <= 0 || kvh <= 0 || heads % kvh || W <= 0 || W > 1024 || R < W + F - 1)
         return hipErrorInvalidValue;
     return launch(k_codec_attn, dim3(unsigned(F), unsigned(heads)), dim3(64), 0, s, qkv, int32_t(ld), ring_k, ring_v, int32_t(R),
                   int32_t(heads), int32_t(kvh), int32_t(hd), pos0, int32_t(W), scale, ao);

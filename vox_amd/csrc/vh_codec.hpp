@@ -95,23 +95,31 @@ __global__ __launch_bounds__(256) void k_codec_rope_ring(float *__restrict__ qkv
 }
 
 // Sliding-window attention of row i (position pos0 + i) and head h over the ring (kernels.cpp:809-828 with the window
-// of :814): keys of positions (p - W, p], scores scale (q . k), softmax, sum p v. One wave per (row, head): lanes
-// take keys for the scores and head dimensions for the output. W <= 1024, hd <= 128.
+// of :814): keys of positions (p - W, p], scores scale (q . k), softmax, sum p v. One wave per (row, head): lanes take
+// keys for the scores (a key row read as float4s) and head dimensions for the output (the value rows read across the
+// wave, eight positions in flight). Ring slots advance from the first one without a division per position.
+// W <= 1024, hd <= 128, hd % 4 == 0.
 __global__ __launch_bounds__(64) void k_codec_attn(const float *__restrict__ qkv, int32_t ld, const float *__restrict__ ring_k,
                                                    const float *__restrict__ ring_v, int32_t R, int32_t heads, int32_t kvh,
                                                    int32_t hd, int64_t pos0, int32_t W, float scale, float *__restrict__ ao) {
     __shared__ float p[1024];
-    __shared__ float q[128];
-    const int i = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, kd = kvh * hd, gk = h / (heads / kvh);
+    __shared__ __align__(16) float q[128];
+    const int i = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, kd = kvh * hd, off = (h / (heads / kvh)) * hd;
     const int64_t last = pos0 + i, first = last - W + 1 > 0 ? last - W + 1 : 0;
-    const int n = int(last - first + 1);
+    const int n = int(last - first + 1), s0 = int(first % R);
     for (int d = lane; d < hd; d += 64) q[d] = qkv[int64_t(i) * ld + h * hd + d];
     __syncthreads();
     float mx = -INFINITY;
     for (int j = lane; j < n; j += 64) {
-        const float *kr = ring_k + ((first + j) % R) * kd + gk * hd;
+        int slot = s0 + j;
+        if (slot >= R) slot -= R;
+        const f32x4 *kr = reinterpret_cast<const f32x4 *>(ring_k + int64_t(slot) * kd + off);
+        const f32x4 *qv = reinterpret_cast<const f32x4 *>(q);
         float dot = 0.f;
-        for (int d = 0; d < hd; ++d) dot += q[d] * kr[d];
+        for (int d4 = 0; d4 < hd / 4; ++d4) {
+            const f32x4 a = kr[d4], b = qv[d4];
+            dot += b[0] * a[0] + b[1] * a[1] + b[2] * a[2] + b[3] * a[3];
+        }
         p[j] = scale * dot;
         mx = fmaxf(mx, p[j]);
     }
@@ -127,8 +135,14 @@ __global__ __launch_bounds__(64) void k_codec_attn(const float *__restrict__ qkv
     __syncthreads();
     const float inv = 1.0f / sum;
     for (int d = lane; d < hd; d += 64) {
+        const float *vb = ring_v + off + d;
         float acc = 0.f;
-        for (int j = 0; j < n; ++j) acc += p[j] * ring_v[((first + j) % R) * kd + gk * hd + d];
+        int slot = s0;
+#pragma unroll 8
+        for (int j = 0; j < n; ++j) {
+            acc += p[j] * vb[int64_t(slot) * kd];
+            if (++slot == R) slot = 0;
+        }
         ao[int64_t(i) * heads * hd + h * hd + d] = acc * inv;
     }
 }
