@@ -14,6 +14,13 @@ static hipError_t gemm_run(const uint8_t *w, const float *scale, const float *A,
     return launch(k_gemm_f32<WT, EPI, ASRC, T, T>, grid, dim3(256), 0, s, w, scale, A, g);
 }
 
+// F32 weights: the three-product split-f16 kernel (z: groups of a grouped conv, or K slices when g.kchunk is set).
+template <int EPI, int ASRC>
+static hipError_t x3_run(const uint8_t *w, const float *A, const GemmArgs &g, int z, hipStream_t s) {
+    const dim3 grid((g.n + 63) / 64, (g.m + 63) / 64, z);
+    return launch(k_gemm_x3<EPI, ASRC>, grid, dim3(256), 0, s, w, A, g);
+}
+
 template <int WT, int EPI, int TM, int TN>
 static hipError_t gemm_run_h16(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s) {
     constexpr int BM = 32 * TM, BN = 32 * TN;
@@ -75,13 +82,15 @@ static hipError_t gemm_tile(const uint8_t *w, const float *scale, const float *A
         return gemm_run_h16<WT, EPI, 2, 2>(w, scale, A, g, s);
     } else {
         if constexpr (EPI == EPI_STORE || EPI == EPI_ACC || EPI == EPI_GATED_ACC || EPI == EPI_SWIGLU) {
-            GemmArgs gs = g;  // the same K slices on the f32 kernel (few-row passes over f32 / bf16 weights)
+            GemmArgs gs = g;  // the same K slices (few-row passes over f32 / bf16 weights)
             const int splits = split_plan(g, &gs.kchunk);
             if (splits) {
-                hipError_t e = gemm_run<WT, EPI_STORE, ASRC_ROWS, 2>(w, scale, A, gs, splits, s);
+                hipError_t e = WT == WT_F32 ? x3_run<EPI_STORE, ASRC_ROWS>(w, A, gs, splits, s)
+                                            : gemm_run<WT, EPI_STORE, ASRC_ROWS, 2>(w, scale, A, gs, splits, s);
                 return e != hipSuccess ? e : splitk_reduce<EPI>(g, splits, s);
             }
         }
+        if constexpr (WT == WT_F32) return x3_run<EPI, ASRC_ROWS>(w, A, g, 1, s);
         return gemm_run<WT, EPI, ASRC_ROWS, 2>(w, scale, A, g, 1, s);
     }
 }
@@ -169,15 +178,15 @@ hipError_t launch_conv_gemm(int epi, const float *w, const float *A, const GemmA
         GemmArgs gs = g;
         const int splits = split_plan(g, &gs.kchunk);
         if (splits) {
-            hipError_t e = gemm_run<WT_F32, EPI_STORE, ASRC_CONV, 2>(wb, nullptr, A, gs, splits, s);
+            hipError_t e = x3_run<EPI_STORE, ASRC_CONV>(wb, A, gs, splits, s);
             if (e != hipSuccess) return e;
             return epi == EPI_STORE ? splitk_reduce<EPI_STORE>(g, splits, s) : splitk_reduce<EPI_ACC>(g, splits, s);
         }
     }
-    if (epi == EPI_MISH) return gemm_run<WT_F32, EPI_MISH, ASRC_CONV, 2>(wb, nullptr, A, g, groups, s);
-    if (epi == EPI_MISH_ACC) return gemm_run<WT_F32, EPI_MISH_ACC, ASRC_CONV, 2>(wb, nullptr, A, g, groups, s);
-    if (epi == EPI_STORE) return gemm_run<WT_F32, EPI_STORE, ASRC_CONV, 2>(wb, nullptr, A, g, groups, s);
-    if (epi == EPI_ACC) return gemm_run<WT_F32, EPI_ACC, ASRC_CONV, 2>(wb, nullptr, A, g, groups, s);
+    if (epi == EPI_MISH) return x3_run<EPI_MISH, ASRC_CONV>(wb, A, g, groups, s);
+    if (epi == EPI_MISH_ACC) return x3_run<EPI_MISH_ACC, ASRC_CONV>(wb, A, g, groups, s);
+    if (epi == EPI_STORE) return x3_run<EPI_STORE, ASRC_CONV>(wb, A, g, groups, s);
+    if (epi == EPI_ACC) return x3_run<EPI_ACC, ASRC_CONV>(wb, A, g, groups, s);
     return hipErrorInvalidValue;
 }
 
@@ -188,9 +197,11 @@ static hipError_t stream_conv(const uint8_t *w, const float *scale, const float 
     GemmArgs gs = g;
     const int splits = split_plan(g, &gs.kchunk);
     if (splits) {
-        hipError_t e = gemm_run<WT, EPI_STORE, ASRC_STREAM, 2>(w, scale, x, gs, splits, s);
+        hipError_t e = WT == WT_F32 ? x3_run<EPI_STORE, ASRC_STREAM>(w, x, gs, splits, s)
+                                    : gemm_run<WT, EPI_STORE, ASRC_STREAM, 2>(w, scale, x, gs, splits, s);
         return e != hipSuccess ? e : splitk_reduce<EPI_STORE>(g, splits, s);
     }
+    if constexpr (WT == WT_F32) return x3_run<EPI_STORE, ASRC_STREAM>(w, x, g, 1, s);
     return gemm_run<WT, EPI_STORE, ASRC_STREAM, 2>(w, scale, x, g, 1, s);
 }
 hipError_t launch_stream_conv(int wt, const uint8_t *w, const float *scale, const float *x, const GemmArgs &g, hipStream_t s) {

@@ -270,6 +270,106 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const uint8_t *__restrict__ w,
 }
 
 
+// F32 weights and f32 activations on the f16 matrix cores: both operands split at staging into f16 halves, x = hi + lo,
+// and three products per pair (hi.hi + hi.lo + lo.hi; the dropped lo.lo term is below 2^-22 relative), each exact in
+// the f32 accumulator. The weights are scaled by 2^10 before the split, so that the lo half of weights down to about
+// 1e-4 stays a normal f16, and the sum is scaled back (exactly) before the epilogue. Any A source of k_gemm_f32 (rows,
+// grouped conv, causal conv, streaming conv), split K, its tiles (64 x 64, K steps of 32) and epilogues; activations
+// below 65504 in magnitude (f16 range) and weights below 64. The convolutions' f32 products run at the f16 rate.
+template <int EPI, int ASRC>
+__global__ __launch_bounds__(256) void k_gemm_x3(const uint8_t *__restrict__ w, const float *__restrict__ A, GemmArgs g) {
+    constexpr int BM = 64, BN = 64, BK = 32, LD = BK + 8;
+    constexpr float kWs = 1024.0f, kWsInv = 1.0f / 1024.0f;
+    __shared__ __align__(16) _Float16 Ah[BM][LD], Al[BM][LD], Bh[BN][LD], Bl[BN][LD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN, K = g.K;
+    const int grp = g.kchunk ? 0 : int(blockIdx.z);
+    const int kbeg = g.kchunk ? int(blockIdx.z) * g.kchunk : 0, kend = g.kchunk ? min(K, kbeg + g.kchunk) : K;
+    if (ASRC == ASRC_CONV) {
+        w += int64_t(grp) * g.n * K * 4;
+        g.y += int64_t(grp) * g.n;
+        if (g.bias) g.bias += int64_t(grp) * g.n;
+    }
+    f32x4v acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    // per thread and K step: A rows tid / 8 and tid / 8 + 32, columns (tid % 8) 4 .. + 3; W row tid / 4, columns
+    // (tid % 4) 8 .. + 7
+    f32x4v ra[2];
+    float rw[8];
+    const int ar = tid >> 3, ac = (tid & 7) * 4, wr = tid >> 2, wc = (tid & 3) * 8;
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int k = k0 + ac;
+            ra[q] = k < kend ? gemm_load_a<ASRC>(A, g, m0 + ar + 32 * q, k, grp) : f32x4v{0.f, 0.f, 0.f, 0.f};
+        }
+        if (k0 + wc < kend) {
+            gemm_load_w<WT_F32>(w, nullptr, g, n0 + wr, k0 + wc, rw);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) rw[e] = 0.f;
+        }
+    };
+    fetch(kbeg);
+    for (int k0 = kbeg; k0 < kend; k0 += BK) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            f16x4v hi, lo;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                hi[e] = _Float16(ra[q][e]);
+                lo[e] = _Float16(ra[q][e] - float(hi[e]));
+            }
+            *reinterpret_cast<f16x4v *>(&Ah[ar + 32 * q][ac]) = hi;
+            *reinterpret_cast<f16x4v *>(&Al[ar + 32 * q][ac]) = lo;
+        }
+        {
+            f16x8v hi, lo;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v = rw[e] * kWs;
+                hi[e] = _Float16(v);
+                lo[e] = _Float16(v - float(hi[e]));
+            }
+            *reinterpret_cast<f16x8v *>(&Bh[wr][wc]) = hi;
+            *reinterpret_cast<f16x8v *>(&Bl[wr][wc]) = lo;
+        }
+        __syncthreads();
+        if (k0 + BK < kend) fetch(k0 + BK);  // in flight during the products below
+        f16x8v ah[2], al[2], bh[2], bl[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int r = wm * 32 + i * 16 + (lane & 15), c = 8 * (lane >> 4);
+            ah[i] = *reinterpret_cast<const f16x8v *>(&Ah[r][c]);
+            al[i] = *reinterpret_cast<const f16x8v *>(&Al[r][c]);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int r = wn * 32 + j * 16 + (lane & 15), c = 8 * (lane >> 4);
+            bh[j] = *reinterpret_cast<const f16x8v *>(&Bh[r][c]);
+            bl[j] = *reinterpret_cast<const f16x8v *>(&Bl[r][c]);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
+            }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] *= kWsInv;
+    if (g.kchunk) return gemm_store_partial<2, 2>(acc, g, m0, n0, wm, wn, lane);
+    gemm_epilogue<EPI, 2, 2>(acc, g, m0, n0, wm, wn, lane);
+}
+
 // F16 or Q8 weights on the f16 matrix cores with the f32 activations split in two halves: a = hi + lo with
 // hi = f16(a), lo = f16(a - hi), so W a = W hi + W lo. F16 weights and the int8 values of Q8 weights are exact in
 // f16 and every f16 x f16 product is exact in the f32 accumulator, so the result keeps the activations to about
