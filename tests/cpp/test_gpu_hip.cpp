@@ -1,12 +1,13 @@
 // test_gpu_hip.cpp — drives the drop-in through Vox's own C++ device interface, the way Vox's callers do
-// (qwen3.cpp:302-344 upload_gpu, kernels.cpp:908-916 transformer_step_fused, kernels.cpp:656 matmul), and
-// checks the results against the C oracle. Run by tests/test_gpu_dropin.py; exit status 0 = all passed.
+// (qwen3.cpp:302-344 upload_gpu, kernels.cpp:908-916 transformer_step_fused, kernels.cpp:656 matmul, qwen3.cpp:396-400
+// the codec decoder's chunks), and checks the results against the C oracle. Run by tests/test_gpu_dropin.py; exit status 0 = all passed.
 #include <cmath>
 #include <cstdio>
 #include <random>
 #include <vector>
 
 #include "gpu.hpp"
+#include "qwen3.hpp"
 #include "vox_oracle.h"
 
 using namespace vox;
@@ -192,6 +193,113 @@ int main() {
     }
     // entry points this backend leaves to the CPU answer like gpu_stub.cpp
     CHECK(gpu_f5_create(GpuF5Desc{}) == -1 && gpu_cosy_create(GpuCosyDesc{}) == -1);
+
+    // ---- the codec decoder: a Qwen3Weights as upload_gpu leaves it (matrices on the device), decoded in two chunks
+    {
+        std::vector<std::vector<float>> keep;  // host arrays of the weights (the "mmap")
+        auto arr = [&](size_t n, float sd, float mean = 0.f) {
+            std::normal_distribution<float> d(mean, sd);
+            keep.emplace_back(n);
+            for (auto &v : keep.back()) v = d(rng);
+            return keep.back().data();
+        };
+        auto fmat = [&](int64_t r, int64_t c, float sd, bool bias) {
+            Mat m;
+            m.type = WType::F32; m.data = reinterpret_cast<const uint8_t *>(arr(size_t(r * c), sd)); m.rows = r; m.cols = c;
+            if (bias) m.bias = arr(size_t(r), 0.05f);
+            m.gpu = gpu_upload(m);
+            return m;
+        };
+        auto omat = [](const Mat &m) { return vo_mat{VO_F32, m.data, nullptr, m.rows, m.cols, m.bias}; };
+        auto cconv = [&](int K, int cin, int cout, int dil, float gain) {
+            CConv c;
+            c.w = fmat(cout, int64_t(K) * cin, gain / std::sqrt(float(K * cin)), true);
+            c.K = K; c.cin = cin; c.cout = cout; c.dil = dil;
+            return c;
+        };
+        auto snake = [&](int C) {
+            Snake sn;
+            const float *al = arr(size_t(C), 0.3f), *be = arr(size_t(C), 0.3f);
+            sn.a.resize(size_t(C)); sn.inv_b.resize(size_t(C));
+            vo_snake_params(al, be, C, sn.a.data(), sn.inv_b.data());
+            return sn;
+        };
+        const int CD = 16, L = 16, HH = 32, heads = 2, hdc = 16, IC = 64, W = 5;
+        Qwen3Weights qw;
+        qw.cc.codebook_dim = CD; qw.cc.latent = L; qw.cc.hidden = HH; qw.cc.heads = heads; qw.cc.kv_heads = heads;
+        qw.cc.head_dim = hdc; qw.cc.window = W; qw.cc.inter = IC; qw.cc.layers = 1; qw.cc.decoder_dim = 16;
+        qw.cc.up_rates = {2}; qw.cc.up_ratios = {2};
+        qw.pre_conv = cconv(3, CD, L, 1, 1.f);
+        qw.pt_in = fmat(HH, L, 0.25f, true);
+        qw.pt_out = fmat(L, HH, 0.18f, true);
+        TransformerW &pt = qw.pt;
+        pt.hidden = HH; pt.heads = heads; pt.kv_heads = heads; pt.head_dim = hdc; pt.inter = IC; pt.eps = 1e-5f;
+        pt.theta = 10000.0; pt.window = W;
+        pt.inv_freq.resize(size_t(hdc / 2));
+        vo_rope_inv_freq(hdc, 10000.0, pt.inv_freq.data());
+        LayerW Lw;
+        Lw.q = fmat(heads * hdc, HH, 0.18f, false); Lw.k = fmat(heads * hdc, HH, 0.18f, false);
+        Lw.v = fmat(heads * hdc, HH, 0.18f, false); Lw.o = fmat(HH, heads * hdc, 0.18f, false);
+        Lw.gate = fmat(IC, HH, 0.18f, false); Lw.up = fmat(IC, HH, 0.18f, false); Lw.down = fmat(HH, IC, 0.12f, false);
+        Lw.ln1 = arr(size_t(HH), 0.1f, 1.f); Lw.ln2 = arr(size_t(HH), 0.1f, 1.f);
+        Lw.attn_scale = arr(size_t(HH), 0.1f, 0.5f); Lw.mlp_scale = arr(size_t(HH), 0.1f, 0.5f);
+        pt.layers.push_back(Lw);
+        pt.final_norm = arr(size_t(HH), 0.1f, 1.f);
+        Qwen3Weights::UpStage u;
+        u.tr.w = fmat(2 * L, L, 0.25f, false); u.tr.K = 2; u.tr.stride = 2; u.tr.cin = L; u.tr.cout = L;
+        u.tr_b = arr(size_t(L), 0.05f);
+        u.dw.w = arr(size_t(L) * 7, 0.3f); u.dw.b = arr(size_t(L), 0.05f); u.dw.K = 7; u.dw.C = L;
+        u.ln_w = arr(size_t(L), 0.1f, 1.f); u.ln_b = arr(size_t(L), 0.1f); u.gamma = arr(size_t(L), 0.3f);
+        u.pw1 = fmat(4 * L, L, 0.25f, true); u.pw2 = fmat(L, 4 * L, 0.12f, true);
+        qw.up.push_back(u);
+        qw.conv0 = cconv(7, L, 16, 1, 1.f);
+        Qwen3Weights::DecBlock db;
+        db.act = snake(16);
+        db.tr.w = fmat(4 * 8, 16, 0.18f, false); db.tr.K = 4; db.tr.stride = 2; db.tr.cin = 16; db.tr.cout = 8;
+        db.tr_b = arr(8, 0.05f);
+        for (int k = 0; k < 3; ++k) {
+            db.a1[k] = snake(8); db.a2[k] = snake(8);
+            db.c1[k] = cconv(7, 8, 8, k == 0 ? 1 : k == 1 ? 3 : 9, 0.3f);
+            db.c2[k] = cconv(1, 8, 8, 1, 0.3f);
+        }
+        qw.blocks.push_back(db);
+        qw.final_act = snake(8);
+        qw.final_conv = cconv(7, 8, 1, 1, 0.1f);
+        const int codec = gpu_codec_create(qw);
+        CHECK(codec >= 0);
+        // the same decoder for the oracle
+        auto ocv = [&](const CConv &c) { return vo_cconv{omat(c.w), c.K, c.cin, c.cout, c.dil}; };
+        auto osn = [](const Snake &sn) { return vo_snake{sn.a.data(), sn.inv_b.data()}; };
+        vo_layer ol{};
+        ol.q = omat(Lw.q); ol.k = omat(Lw.k); ol.v = omat(Lw.v); ol.o = omat(Lw.o);
+        ol.gate = omat(Lw.gate); ol.up = omat(Lw.up); ol.down = omat(Lw.down);
+        ol.ln1 = Lw.ln1; ol.ln2 = Lw.ln2; ol.attn_scale = Lw.attn_scale; ol.mlp_scale = Lw.mlp_scale;
+        vo_codec_up ou{omat(u.tr.w), u.tr_b, 2, u.dw.w, u.dw.b, 7, u.ln_w, u.ln_b, u.gamma, omat(u.pw1), omat(u.pw2)};
+        vo_codec_block ob{};
+        ob.act = osn(db.act); ob.tr = omat(db.tr.w); ob.tr_b = db.tr_b; ob.K = 4; ob.stride = 2; ob.cin = 16; ob.cout = 8;
+        for (int k = 0; k < 3; ++k) { ob.a1[k] = osn(db.a1[k]); ob.a2[k] = osn(db.a2[k]); ob.c1[k] = ocv(db.c1[k]); ob.c2[k] = ocv(db.c2[k]); }
+        vo_codec oc{};
+        oc.codebook_dim = CD; oc.latent = L; oc.n_up = 1; oc.n_blocks = 1;
+        oc.pre_conv = ocv(qw.pre_conv); oc.pt_in = omat(qw.pt_in); oc.pt_out = omat(qw.pt_out);
+        oc.pt = vo_xfmr{1, &ol, pt.final_norm, HH, heads, heads, hdc, IC, 1e-5f, pt.inv_freq.data(), W};
+        oc.ups = &ou; oc.conv0 = ocv(qw.conv0); oc.blocks = &ob; oc.final_act = osn(qw.final_act); oc.final_conv = ocv(qw.final_conv);
+        const int F = 11;
+        std::vector<float> z(size_t(F) * CD);
+        for (auto &v : z) v = nd(rng);
+        vo_codec_state *os = vo_codec_state_new(&oc, 64);
+        std::vector<float> want(size_t(F) * size_t(vo_codec_spf(&oc)));
+        CHECK(vo_codec_forward(&oc, os, z.data(), F, want.data()) == int64_t(want.size()));
+        vo_codec_state_free(os);
+        if (codec >= 0) {
+            const int st = gpu_codec_state_new(codec);
+            CHECK(st >= 0);
+            std::vector<float> pcm;
+            CHECK(gpu_codec_forward(codec, st, z.data(), 6, pcm) && gpu_codec_forward(codec, st, z.data() + 6 * CD, F - 6, pcm));
+            CHECK(pcm.size() == want.size() && rel(pcm.data(), want.data(), want.size()) < 1e-3f);
+            CHECK(!gpu_codec_forward(codec, st, z.data(), kGpuCodecMaxFrames + 1, pcm));  // more than a chunk: false
+            gpu_codec_state_free(st);
+        }
+    }
     std::printf("%d passed, %d failed\n", g_pass, g_fail);
     return g_fail ? 1 : 0;
 }
