@@ -50,10 +50,11 @@ hipError_t launch_f5_attn(const _Float16 *qkv16, int64_t lo_off, float *out, _Fl
     if (hd != kF5Hd || heads <= 0 || ldvt < N || ldvt % 64 || lo_off % 8 || ldo % 4 || (!out && !out16)) return hipErrorInvalidValue;
     if ((int64_t(N) + 64) * 2 * heads * hd * 2 > INT32_MAX) return hipErrorInvalidValue;  // the q / k buffer offsets
     F5AttnArgs a{qkv16, lo_off, out, int32_t(N), int32_t(ldo), int32_t(heads * hd), int32_t(ldvt), scale, out16, out_lo};
-    // 4 waves (64 query rows) per block, or 2 when that leaves fewer blocks than CUs
+    // 4 query waves (64 rows) per block; when that leaves fewer blocks than CUs, 2 query waves (32 rows) times 2 key
+    // halves
     if (int64_t((N + 63) / 64) * heads * B >= 256)
-        return launch(k_f5_attn<4>, dim3(unsigned((N + 63) / 64), unsigned(heads), unsigned(B)), dim3(256), 0, s, a);
-    return launch(k_f5_attn<2>, dim3(unsigned((N + 31) / 32), unsigned(heads), unsigned(B)), dim3(128), 0, s, a);
+        return launch(k_f5_attn<4, 1>, dim3(unsigned((N + 63) / 64), unsigned(heads), unsigned(B)), dim3(256), 0, s, a);
+    return launch(k_f5_attn<2, 2>, dim3(unsigned((N + 31) / 32), unsigned(heads), unsigned(B)), dim3(256), 0, s, a);
 }
 
 }  // namespace vh

@@ -146,12 +146,15 @@ VH_DEV f32x4a mfma3(h16x8 ah, h16x8 al, h16x8 bh, h16x8 bl, f32x4a c) {
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, c, 0, 0, 0);
 }
-template <int W>
-__global__ __launch_bounds__(64 * W) void k_f5_attn(F5AttnArgs a) {
-    constexpr int RS = 8 * W, RPT = 64 / RS;  // tile rows: thread rows r + RS q, q < RPT
-    __shared__ __align__(16) _Float16 Kh[64][kF5Ld], Kl[64][kF5Ld];  // [key][d]
-    __shared__ __align__(16) _Float16 Vh[64][kF5Ld], Vl[64][kF5Ld];  // [d][key]
+template <int W, int KS>
+__global__ __launch_bounds__(64 * W * KS) void k_f5_attn(F5AttnArgs a) {
+    constexpr int RS = 8 * W, RPT = 64 / RS;  // tile rows of a key half's threads: rows r + RS q, q < RPT
+    __shared__ __align__(16) _Float16 Kh[KS][64][kF5Ld], Kl[KS][64][kF5Ld];  // [half][key][d]
+    __shared__ __align__(16) _Float16 Vh[KS][64][kF5Ld], Vl[KS][64][kF5Ld];  // [half][d][key]
+    // waves: query group qw (16 rows each), key half kh (KS = 2: the halves take alternate key tiles and are merged
+    // at the end, doubling the waves of a short sequence without staging a tile twice)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    const int qw = KS == 1 ? wave : wave % W, kh = KS == 1 ? 0 : wave / W, ht = KS == 1 ? tid : tid % (64 * W);
     // a contiguous run of (batch, head) pairs per XCD, so each head's keys and values stay in one L2
     const int qt = gridDim.x, heads = gridDim.y;
     const int t = xcd_tile(int(blockIdx.x) + qt * (int(blockIdx.y) + heads * int(blockIdx.z)), qt * heads * int(gridDim.z));
@@ -166,7 +169,7 @@ __global__ __launch_bounds__(64 * W) void k_f5_attn(F5AttnArgs a) {
     // B operand of S^T: lane holds q[q0 + 16 wave + lr][32 c + 8 lg + e]
     h16x8 qh[2], ql[2];
     {
-        const int32_t off = int32_t(((q0 + 16 * wave + lr) * ldqk + 8 * lg) * 2);
+        const int32_t off = int32_t(((q0 + 16 * qw + lr) * ldqk + 8 * lg) * 2);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             qh[c] = __builtin_bit_cast(h16x8, buf_ld16(rqh, off + 64 * c, 0));
@@ -179,7 +182,7 @@ __global__ __launch_bounds__(64 * W) void k_f5_attn(F5AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = f32x4a{0.f, 0.f, 0.f, 0.f};
     // per thread and tile: keys / d rows r + RS q, columns c8 .. c8 + 7, of K and v^T (hi, lo)
-    const int r = tid >> 3, c8 = (tid & 7) * 8;
+    const int r = ht >> 3, c8 = (ht & 7) * 8;
     int32_t ko[RPT];
     const _Float16 *vp[RPT];
 #pragma unroll
@@ -199,17 +202,20 @@ __global__ __launch_bounds__(64 * W) void k_f5_attn(F5AttnArgs a) {
             vr[RPT + q] = *reinterpret_cast<const u32x4 *>(vp[q] + a.lo_off + kt);
         }
     };
-    fetch(0);
-    for (int kt = 0; kt < a.N; kt += 64) {
+    const int niter = ((a.N + 63) / 64 + KS - 1) / KS;  // the same count in both halves: barriers stay uniform
+    fetch(min(64 * kh, a.ldvt - 64));
+    for (int it = 0; it < niter; ++it) {
+        const int kt = 64 * (it * KS + kh);
 #pragma unroll
         for (int q = 0; q < RPT; ++q) {
-            *reinterpret_cast<u32x4 *>(&Kh[r + RS * q][c8]) = kr[q];
-            *reinterpret_cast<u32x4 *>(&Kl[r + RS * q][c8]) = kr[RPT + q];
-            *reinterpret_cast<u32x4 *>(&Vh[r + RS * q][c8]) = vr[q];
-            *reinterpret_cast<u32x4 *>(&Vl[r + RS * q][c8]) = vr[RPT + q];
+            *reinterpret_cast<u32x4 *>(&Kh[kh][r + RS * q][c8]) = kr[q];
+            *reinterpret_cast<u32x4 *>(&Kl[kh][r + RS * q][c8]) = kr[RPT + q];
+            *reinterpret_cast<u32x4 *>(&Vh[kh][r + RS * q][c8]) = vr[q];
+            *reinterpret_cast<u32x4 *>(&Vl[kh][r + RS * q][c8]) = vr[RPT + q];
         }
         __syncthreads();
-        fetch(min(kt + 64, a.ldvt - 64));  // unconditional (the last tile again at the end): exact wait counts
+        fetch(min(kt + 64 * KS, a.ldvt - 64));  // unconditional (the last tile again at the end): exact wait counts
+        if (KS == 1 || kt < a.N) {  // a half whose tile lies past the keys only keeps the barriers
         // S^T tiles: A operand lane holds K[16 j + lr][32 c + 8 lg + e]; lane gets S^T[16 j + 4 lg + i][lr]
         f32x4a s[4];
 #pragma unroll
@@ -217,7 +223,8 @@ __global__ __launch_bounds__(64 * W) void k_f5_attn(F5AttnArgs a) {
             s[j] = f32x4a{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < 2; ++c)
-                s[j] = mfma3(ld16(&Kh[16 * j + lr][32 * c + 8 * lg]), ld16(&Kl[16 * j + lr][32 * c + 8 * lg]), qh[c], ql[c], s[j]);
+                s[j] = mfma3(ld16(&Kh[kh][16 * j + lr][32 * c + 8 * lg]), ld16(&Kl[kh][16 * j + lr][32 * c + 8 * lg]), qh[c],
+                             ql[c], s[j]);
         }
         float mx = -INFINITY;
         if (kt + 64 <= a.N) {
@@ -271,12 +278,34 @@ __global__ __launch_bounds__(64 * W) void k_f5_attn(F5AttnArgs a) {
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
                 const int d = 16 * dt + lr, k0 = 32 * c + 4 * lg;
-                o[dt] = mfma3(ld8x2(&Vh[d][k0], &Vh[d][k0 + 16]), ld8x2(&Vl[d][k0], &Vl[d][k0 + 16]), ph, pl, o[dt]);
+                o[dt] = mfma3(ld8x2(&Vh[kh][d][k0], &Vh[kh][d][k0 + 16]), ld8x2(&Vl[kh][d][k0], &Vl[kh][d][k0 + 16]), ph,
+                              pl, o[dt]);
             }
+        }
         }
         __syncthreads();
     }
-    const int qr = q0 + 16 * wave + lr;
+    if constexpr (KS == 2) {  // merge the second half's (max, sum, O) into the first's through LDS
+        float *mg = reinterpret_cast<float *>(&Kh[0][0][0]) + (qw * 64 + lane) * 18;
+        if (kh == 1) {
+            mg[0] = mrow;
+            mg[1] = lrow;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) mg[2 + 4 * dt + i] = o[dt][i];
+        }
+        __syncthreads();
+        if (kh == 1) return;
+        const float m1 = mg[0], l1 = mg[1], mn = fmaxf(mrow, m1);
+        const float a0 = __builtin_amdgcn_exp2f(mrow - mn), a1 = __builtin_amdgcn_exp2f(m1 - mn);
+        lrow = lrow * a0 + l1 * a1;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[dt][i] = o[dt][i] * a0 + mg[2 + 4 * dt + i] * a1;
+    }
+    const int qr = q0 + 16 * qw + lr;
     if (qr >= a.N) return;
     const float inv = 1.0f / lrow;
     const int64_t off = (int64_t(b) * a.N + qr) * a.ldo + int64_t(h) * kF5Hd + 4 * lg;
