@@ -23,6 +23,7 @@ VH_DEV float mish_nn_f(float x) {
 // and bias (kernels.cpp:714-723 and nn.cpp:248-265, which compute alike), y = (x - float(mean)) * inv * w + b; then
 // mish and a per-channel bias when asked (the estimator's CausalBlock1D and its time bias, cosyvoice.cpp:155-178).
 // D % 4 == 0.
+constexpr int kNormRegChunks = 8;  // rows up to 8 x 256 = 2048 values stay in registers between the passes
 __global__ __launch_bounds__(256) void k_f5_modulate(NormArgs a) {
     const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= a.R) return;
@@ -33,14 +34,35 @@ __global__ __launch_bounds__(256) void k_f5_modulate(NormArgs a) {
         for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
         return v;
     };
+    // the row is read once: chunk c of this lane is columns 4 lane + 256 c .. + 3; the first kNormRegChunks chunks
+    // stay in registers (fully unrolled loops), columns beyond 2048 are read again from memory
+    f32x4a reg[kNormRegChunks];
+#pragma unroll
+    for (int c = 0; c < kNormRegChunks; ++c) {
+        const int i = 4 * lane + 256 * c;
+        reg[c] = i < D ? *reinterpret_cast<const f32x4a *>(xr + i) : f32x4a{0.f, 0.f, 0.f, 0.f};
+    }
+    const int tail0 = 256 * kNormRegChunks;
     double s = 0.0;
-    for (int i = 4 * lane; i < D; i += 256) {
+#pragma unroll
+    for (int c = 0; c < kNormRegChunks; ++c)
+        s += double(reg[c][0]) + double(reg[c][1]) + double(reg[c][2]) + double(reg[c][3]);  // zeros past D
+    for (int i = tail0 + 4 * lane; i < D; i += 256) {
         const f32x4a v = *reinterpret_cast<const f32x4a *>(xr + i);
         s += double(v[0]) + double(v[1]) + double(v[2]) + double(v[3]);
     }
     const double mean = wsum(s) / D;
     double q = 0.0;
-    for (int i = 4 * lane; i < D; i += 256) {
+#pragma unroll
+    for (int c = 0; c < kNormRegChunks; ++c) {
+        if (4 * lane + 256 * c >= D) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const double dd = double(reg[c][e]) - mean;
+            q += dd * dd;
+        }
+    }
+    for (int i = tail0 + 4 * lane; i < D; i += 256) {
         const f32x4a v = *reinterpret_cast<const f32x4a *>(xr + i);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -50,13 +72,12 @@ __global__ __launch_bounds__(256) void k_f5_modulate(NormArgs a) {
     }
     const double var = wsum(q) / D;
     const float inv = float(1.0 / sqrt(var + a.eps)), fm = float(mean);
-    for (int i = 4 * lane; i < D; i += 256) {
-        const f32x4a v = *reinterpret_cast<const f32x4a *>(xr + i);
-        const f32x4a c = *reinterpret_cast<const f32x4a *>(a.sc + i);
+    auto emit = [&](int i, const f32x4a &v) {
+        const f32x4a cs = *reinterpret_cast<const f32x4a *>(a.sc + i);
         const f32x4a t = a.sh ? *reinterpret_cast<const f32x4a *>(a.sh + i) : f32x4a{0.f, 0.f, 0.f, 0.f};
         f32x4a r;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = (v[e] - fm) * inv * (a.affine ? c[e] : 1.0f + c[e]) + t[e];
+        for (int e = 0; e < 4; ++e) r[e] = (v[e] - fm) * inv * (a.affine ? cs[e] : 1.0f + cs[e]) + t[e];
         if (a.mish) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) r[e] = mish_nn_f(r[e]);
@@ -79,7 +100,11 @@ __global__ __launch_bounds__(256) void k_f5_modulate(NormArgs a) {
         } else {
             *reinterpret_cast<f32x4a *>(a.y + int64_t(row) * D + i) = r;
         }
-    }
+    };
+#pragma unroll
+    for (int c = 0; c < kNormRegChunks; ++c)
+        if (4 * lane + 256 * c < D) emit(4 * lane + 256 * c, reg[c]);
+    for (int i = tail0 + 4 * lane; i < D; i += 256) emit(i, *reinterpret_cast<const f32x4a *>(xr + i));
 }
 
 // Depthwise "same" Conv1d (f5_ops.cpp:106-147 with groups = channels: the Vocos blocks' dwconv, f5.cpp:341) over
