@@ -373,7 +373,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         log("bench.py runs on one GPU only: this build's hot path (the batch-1 talker decode step) lives on a single "
-            "MI355X; the multi-GPU layout is a design note in DESIGN.md, and no figure at several GPUs is produced.")
+            "MI355X, and no figure at several GPUs is produced.")
         sys.exit(2)
     from vox_amd import synth
     from vox_amd import voxhip as vh
