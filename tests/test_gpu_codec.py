@@ -34,19 +34,21 @@ def decode(hip, oracle, m, codec, chunks, seed):
 
 @pytest.mark.parametrize("wtype", [F32, F16, BF16])
 def test_codec_stream(hip, oracle, wtype):
-    # 40 frames in calls of 1..16: the histories, tails and the ring (21 slots for window 5) wrap several times
+    # 48 frames in calls of 1..16: the histories, tails and the ring (21 slots for window 5) wrap several times; a call
+    # is a graph per (frame count, buffer parity), so the repeated (3, even) and (1, odd) calls replay one
     m = CodecModel(30 + wtype, wround=wtype)
     codec = m.create(hip, wtype)
     assert hip.codec_spf(codec) == m.spf
-    st, _, _ = decode(hip, oracle, m, codec, [3, 1, 16, 5, 7, 8], seed=wtype)
+    st, _, _ = decode(hip, oracle, m, codec, [3, 1, 16, 5, 7, 8, 3, 3, 1, 1], seed=wtype)
     hip.codec_state_free(st)
 
 
 def test_codec_clone_and_states(hip, oracle):
-    # a cloned state continues like the original; two states decode independently
+    # a cloned state continues like the original (cloned after an odd number of calls, so from the second buffers);
+    # two states decode independently
     m = CodecModel(40)
     codec = m.create(hip)
-    st, ost, _ = decode(hip, oracle, m, codec, [6, 4], seed=1)
+    st, ost, _ = decode(hip, oracle, m, codec, [6, 4, 2], seed=1)
     z = oracle.codec_quantize(m.ox, m.codes(np.random.default_rng(2), 9))
     cl = hip.codec_state_clone(st)
     ocl = ost.clone()

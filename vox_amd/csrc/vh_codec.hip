@@ -36,21 +36,21 @@ hipError_t launch_ola(const float *tmp, const float *tail_old, float *tail_new, 
 }
 
 hipError_t launch_codec_rope_ring(float *qkv, int ld, int F, int heads, int kvh, int hd, const float *rope, float *ring_k,
-                                  float *ring_v, int R, int64_t pos0, hipStream_t s) {
+                                  float *ring_v, int R, const int64_t *pos, hipStream_t s) {
     if (F <= 0) return hipSuccess;
-    if (hd <= 0 || hd % 2 || heads <= 0 || kvh <= 0 || ld < (heads + 2 * kvh) * hd || R < F || pos0 < 0) return hipErrorInvalidValue;
+    if (hd <= 0 || hd % 2 || heads <= 0 || kvh <= 0 || ld < (heads + 2 * kvh) * hd || R < F || !pos) return hipErrorInvalidValue;
     return launch(k_codec_rope_ring, dim3(unsigned(F)), dim3(256), 0, s, qkv, int32_t(ld), int32_t(heads), int32_t(kvh),
-                  int32_t(hd), rope, ring_k, ring_v, int32_t(R), pos0);
+                  int32_t(hd), rope, ring_k, ring_v, int32_t(R), pos);
 }
 
 hipError_t launch_codec_attn(const float *qkv, int ld, const float *ring_k, const float *ring_v, int R, int F, int heads, int kvh,
-                             int hd, int64_t pos0, int W, float scale, float *ao, hipStream_t s) {
+                             int hd, const int64_t *pos, int W, float scale, float *ao, hipStream_t s) {
     if (F <= 0) return hipSuccess;
     // the ring holds the window of every row of the call: R >= W + F - 1
-    if (hd <= 0 || hd > 128 || hd % 4 || heads <= 0 || kvh <= 0 || heads % kvh || W <= 0 || W > 1024 || R < W + F - 1)
+    if (hd <= 0 || hd > 128 || hd % 4 || heads <= 0 || kvh <= 0 || heads % kvh || W <= 0 || W > 1024 || R < W + F - 1 || !pos)
         return hipErrorInvalidValue;
     return launch(k_codec_attn, dim3(unsigned(F), unsigned(heads)), dim3(64), 0, s, qkv, int32_t(ld), ring_k, ring_v, int32_t(R),
-                  int32_t(heads), int32_t(kvh), int32_t(hd), pos0, int32_t(W), scale, ao);
+                  int32_t(heads), int32_t(kvh), int32_t(hd), pos, int32_t(W), scale, ao);
 }
 
 hipError_t launch_scale_acc(float *h, const float *t, const float *sc, int64_t rows, int H, hipStream_t s) {

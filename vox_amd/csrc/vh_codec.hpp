@@ -68,12 +68,14 @@ __global__ __launch_bounds__(256) void k_ola(const float *__restrict__ tmp, cons
 
 // The pre-transformer's q / k rotation (rope_apply, kernels.cpp:740-757: pairs (d, d + hd / 2)) with the host table
 // rope [F][hd / 2][2] of positions pos0 + i, and the append of row i's keys and values to ring slot (pos0 + i) % R of
-// the layer's f32 ring [R][kv_heads hd]. grid F, block 256; qkv rows [F][ld] = q | k | v.
+// the layer's f32 ring [R][kv_heads hd]. grid F, block 256; qkv rows [F][ld] = q | k | v; the call's first position
+// pos0 is read from device memory (*pos), so a captured call replays at any position.
 __global__ __launch_bounds__(256) void k_codec_rope_ring(float *__restrict__ qkv, int32_t ld, int32_t heads, int32_t kvh,
                                                          int32_t hd, const float *__restrict__ rope,
                                                          float *__restrict__ ring_k, float *__restrict__ ring_v,
-                                                         int32_t R, int64_t pos0) {
+                                                         int32_t R, const int64_t *__restrict__ pos) {
     const int i = blockIdx.x, half = hd / 2, qd = heads * hd, kd = kvh * hd;
+    const int64_t pos0 = *pos;
     float *row = qkv + int64_t(i) * ld;
     const float *cs = rope + int64_t(i) * hd;
     const int64_t slot = (pos0 + i) % R;
@@ -101,10 +103,12 @@ __global__ __launch_bounds__(256) void k_codec_rope_ring(float *__restrict__ qkv
 // W <= 1024, hd <= 128, hd % 4 == 0.
 __global__ __launch_bounds__(64) void k_codec_attn(const float *__restrict__ qkv, int32_t ld, const float *__restrict__ ring_k,
                                                    const float *__restrict__ ring_v, int32_t R, int32_t heads, int32_t kvh,
-                                                   int32_t hd, int64_t pos0, int32_t W, float scale, float *__restrict__ ao) {
+                                                   int32_t hd, const int64_t *__restrict__ pos, int32_t W, float scale,
+                                                   float *__restrict__ ao) {
     __shared__ float p[1024];
     __shared__ __align__(16) float q[128];
     const int i = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, kd = kvh * hd, off = (h / (heads / kvh)) * hd;
+    const int64_t pos0 = *pos;
     const int64_t last = pos0 + i, first = last - W + 1 > 0 ? last - W + 1 : 0;
     const int n = int(last - first + 1), s0 = int(first % R);
     for (int d = lane; d < hd; d += 64) q[d] = qkv[int64_t(i) * ld + h * hd + d];

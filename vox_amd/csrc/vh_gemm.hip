@@ -190,31 +190,39 @@ hipError_t launch_conv_gemm(int epi, const float *w, const float *A, const GemmA
     return hipErrorInvalidValue;
 }
 
-// The codec's streaming convolution: y = W im2col([hist; x]) + bias (qwen3.cpp:102-121), F32 / F16 / BF16 weights
-// [cout][K cin] on the f32 MFMA GEMM, split K when the 64 x 64 tiles leave the CUs idle.
-template <int WT>
+// The codec's streaming convolution: y = W im2col([hist; x]) + bias (qwen3.cpp:102-121), or Snake of it (EPI_SNAKE),
+// F32 / F16 / BF16 weights [cout][K cin] on the MFMA GEMMs (f32 weights: three f16 products), split K when the
+// 64 x 64 tiles leave the CUs idle.
+template <int WT, int EPI>
 static hipError_t stream_conv(const uint8_t *w, const float *scale, const float *x, const GemmArgs &g, hipStream_t s) {
     GemmArgs gs = g;
     const int splits = split_plan(g, &gs.kchunk);
     if (splits) {
         hipError_t e = WT == WT_F32 ? x3_run<EPI_STORE, ASRC_STREAM>(w, x, gs, splits, s)
                                     : gemm_run<WT, EPI_STORE, ASRC_STREAM, 2>(w, scale, x, gs, splits, s);
-        return e != hipSuccess ? e : splitk_reduce<EPI_STORE>(g, splits, s);
+        return e != hipSuccess ? e : splitk_reduce<EPI>(g, splits, s);
     }
-    if constexpr (WT == WT_F32) return x3_run<EPI_STORE, ASRC_STREAM>(w, x, g, 1, s);
-    return gemm_run<WT, EPI_STORE, ASRC_STREAM, 2>(w, scale, x, g, 1, s);
+    if constexpr (WT == WT_F32) return x3_run<EPI, ASRC_STREAM>(w, x, g, 1, s);
+    return gemm_run<WT, EPI, ASRC_STREAM, 2>(w, scale, x, g, 1, s);
 }
-hipError_t launch_stream_conv(int wt, const uint8_t *w, const float *scale, const float *x, const GemmArgs &g, hipStream_t s) {
+template <int EPI>
+static hipError_t stream_conv_wt(int wt, const uint8_t *w, const float *scale, const float *x, const GemmArgs &g, hipStream_t s) {
+    switch (wt) {
+        case WT_F32: return stream_conv<WT_F32, EPI>(w, scale, x, g, s);
+        case WT_F16: return stream_conv<WT_F16, EPI>(w, scale, x, g, s);
+        case WT_BF16: return stream_conv<WT_BF16, EPI>(w, scale, x, g, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+hipError_t launch_stream_conv(int wt, int epi, const uint8_t *w, const float *scale, const float *x, const GemmArgs &g,
+                              hipStream_t s) {
     if (g.m <= 0) return hipSuccess;
     if (g.cig <= 0 || g.cig % 4 || g.ksize <= 0 || g.dil <= 0 || g.K != g.ksize * g.cig || g.K % 8 || g.lda % 4 || g.n <= 0 ||
         g.ctx != (g.ksize - 1) * g.dil || (g.ctx && !g.hist) || !g.y)
         return hipErrorInvalidValue;
-    switch (wt) {
-        case WT_F32: return stream_conv<WT_F32>(w, scale, x, g, s);
-        case WT_F16: return stream_conv<WT_F16>(w, scale, x, g, s);
-        case WT_BF16: return stream_conv<WT_BF16>(w, scale, x, g, s);
-        default: return hipErrorInvalidValue;
-    }
+    if (epi == EPI_STORE) return stream_conv_wt<EPI_STORE>(wt, w, scale, x, g, s);
+    if (epi == EPI_SNAKE) return g.snake_a && g.snake_ib ? stream_conv_wt<EPI_SNAKE>(wt, w, scale, x, g, s) : hipErrorInvalidValue;
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_attn_merge(const AttnPartials &P, float *ao, int m, hipStream_t s) {

@@ -163,6 +163,10 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
                         g.h16[idx] = hi;
                         g.h16[g.lo_off + idx] = _Float16(r - float(hi));
                     }
+                    else if (EPI == EPI_SNAKE) {
+                        const float sn = sinf(c * g.snake_a[col]);
+                        *dst = c + g.snake_ib[col] * sn * sn;
+                    }
                     else if (EPI == EPI_MISH) *dst = mish_f(c);
                     else if (EPI == EPI_MISH_ACC) *dst += mish_f(c);
                 }
@@ -760,6 +764,10 @@ __global__ __launch_bounds__(256) void k_gemm_splitk_reduce(GemmArgs g, int32_t 
     else if (EPI == EPI_STORE) *dst = sum(c);
     else if (EPI == EPI_ACC) *dst += sum(c);
     else if (EPI == EPI_GATED_ACC) *dst += g.gate[c] * sum(c);
+    else if (EPI == EPI_SNAKE) {
+        const float v = sum(c), sn = sinf(v * g.snake_a[c]);
+        *dst = v + g.snake_ib[c] * sn * sn;
+    }
 }
 
 // Merge of the kAttnMaxSplits attention partials of m rows into ao [m][heads * hd] (the PRO_ATTN prologue of the

@@ -86,12 +86,13 @@ hipError_t launch_dwconv_causal(const float *x, const float *hist, const float *
 hipError_t launch_ola(const float *tmp, const float *tail_old, float *tail_new, const float *bias, float *y, int T, int stride,
                       int K, int co, hipStream_t s);
 hipError_t launch_codec_rope_ring(float *qkv, int ld, int F, int heads, int kvh, int hd, const float *rope, float *ring_k,
-                                  float *ring_v, int R, int64_t pos0, hipStream_t s);
+                                  float *ring_v, int R, const int64_t *pos, hipStream_t s);
 hipError_t launch_codec_attn(const float *qkv, int ld, const float *ring_k, const float *ring_v, int R, int F, int heads, int kvh,
-                             int hd, int64_t pos0, int W, float scale, float *ao, hipStream_t s);
+                             int hd, const int64_t *pos, int W, float scale, float *ao, hipStream_t s);
 hipError_t launch_scale_acc(float *h, const float *t, const float *sc, int64_t rows, int H, hipStream_t s);
 hipError_t launch_clamp1(float *y, int64_t n, hipStream_t s);
-hipError_t launch_stream_conv(int wt, const uint8_t *w, const float *scale, const float *x, const GemmArgs &g, hipStream_t s);
+hipError_t launch_stream_conv(int wt, int epi, const uint8_t *w, const float *scale, const float *x, const GemmArgs &g,
+                              hipStream_t s);
 // CosyVoice2 LM: one sampling step (log-softmax, RAS trial loop) and the next step's embedding + row advance.
 hipError_t launch_lm_sample(const float *logits, int n, const LmCfgDev *cfg, LmState *st, int32_t *decoded, float *logp_out,
                             int64_t logp_stride, bool append, hipStream_t s);

@@ -8,10 +8,10 @@ namespace vh {
 // GEMV prologues; PRO_Q (int path only): the input rows arrive already quantized (k_quant_rows)
 enum { PRO_X = 0, PRO_RMS = 1, PRO_ATTN = 2, PRO_Q = 3 };
 enum { EPI_STORE = 0, EPI_ACC = 1, EPI_SWIGLU = 2 };
-// GEMM-only epilogues (F5 DiT, Vocos): y += gate * c; y = gelu_tanh(c); y = mish(c); y += mish(c); RoPE on q|k
-// columns; y = gelu_erf(c)
+// GEMM-only epilogues (F5 DiT, Vocos, the codec): y += gate * c; y = gelu_tanh(c); y = mish(c); y += mish(c); RoPE on
+// q|k columns; y = gelu_erf(c); y = snake(c)
 enum { EPI_GATED_ACC = 3, EPI_GELU = 4, EPI_MISH = 5, EPI_MISH_ACC = 6, EPI_ROPE = 7, EPI_ROPE_H16 = 8, EPI_GELU_H16 = 9,
-       EPI_GELU_ERF = 10 };
+       EPI_GELU_ERF = 10, EPI_SNAKE = 11 };
 // GEMM A operand: rows of a matrix, or the implicit im2col rows of a grouped "same" Conv1d
 enum { ASRC_ROWS = 0, ASRC_CONV = 1, ASRC_STREAM = 2 };
 // Weight formats of the GEMV kernels: the reference's types, plus Q4 with f16 block scales (WT_Q4H), the
@@ -140,6 +140,8 @@ struct GemmArgs {
     // [hist (ctx rows of cig); x (rows of lda)], ctx = (ksize - 1) dil
     const float *hist;
     int32_t ctx, dil;
+    // EPI_SNAKE: y = v + snake_ib[col] sin(snake_a[col] v)^2 of v = c + bias (the codec's Snake after a convolution)
+    const float *snake_a, *snake_ib;
     // split K (k_gemm_h16): block z sums K columns [z kchunk, (z + 1) kchunk) into ws + z m n ([m][n]); a reduce
     // pass adds the slices in order and applies the epilogue. kchunk 0: no split.
     int32_t kchunk;

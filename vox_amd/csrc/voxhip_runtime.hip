@@ -2306,16 +2306,22 @@ struct Codec {
     int64_t smax = 0;
     float *qkv = nullptr, *ao = nullptr, *act = nullptr, *tmp = nullptr, *h = nullptr, *pre = nullptr, *rope = nullptr, *z = nullptr;
 };
-struct Hist2 {  // a streaming history as two buffers: the current one and the next call's
+// A streaming history (or transposed-conv tail) as two buffers: a call reads b[parity] and writes the next call's into
+// b[1 - parity]; the state's parity flips after every call, so a call's buffers depend only on (T, parity) and a
+// captured call replays.
+struct Hist2 {
     float *b[2] = {nullptr, nullptr};
-    int cur = 0, rows = 0, C = 0;
+    int rows = 0, C = 0;
 };
 struct CodecSt {
     int codec = -1;
-    int64_t len = 0;  // positions already in the transformer
+    int64_t len = 0;   // positions already in the transformer
+    int parity = 0;
+    int64_t *pos_dev = nullptr;  // len on the device, for the captured kernels
     Hist2 pre, c0, fin;
     std::vector<Hist2> dw, tail, ru;
     std::vector<float *> kr, vr;  // ring caches [R][kv_heads hd] per layer
+    std::map<int, hipGraphExec_t> graphs;  // by 2 T + parity
 };
 
 Codec &codec_at(int id) {
@@ -2359,9 +2365,9 @@ Hist2 hist_new(int rows, int C) {
     }
     return h;
 }
-Hist2 hist_clone(const Hist2 &src) {
+Hist2 hist_clone(const Hist2 &src, int parity) {  // the current buffer into b[0] of a state of parity 0
     Hist2 h = hist_new(src.rows, src.C);
-    HIPCHECK(hipMemcpy(h.b[0], src.b[src.cur], size_t(std::max(src.rows, 1)) * size_t(src.C) * 4, hipMemcpyDeviceToDevice));
+    HIPCHECK(hipMemcpy(h.b[0], src.b[parity], size_t(std::max(src.rows, 1)) * size_t(src.C) * 4, hipMemcpyDeviceToDevice));
     return h;
 }
 void hist_free(Hist2 &h) {
@@ -2370,18 +2376,18 @@ void hist_free(Hist2 &h) {
 
 // A streaming convolution of T rows X (row stride ldx) into Y (row stride ldy): the conv GEMM over [hist; X], then the
 // history moves on (into the other buffer).
-void codec_conv(const CodecConv &c, Hist2 *h, const float *X, int64_t ldx, int T, float *Y, int64_t ldy, hipStream_t s) {
+// snake: Snake applied in the epilogue (the output then holds Snake(conv(.)), as the residual units consume it).
+void codec_conv(const CodecConv &c, Hist2 *h, int par, const float *X, int64_t ldx, int T, float *Y, int64_t ldy, hipStream_t s,
+                const CodecSnake *snake = nullptr) {
     const GpuMat &M = mat_at(c.mat);
     GemmArgs ga{};
+    if (snake) { ga.snake_a = snake->a; ga.snake_ib = snake->inv_b; }
     ga.bias = M.b; ga.y = Y; ga.lda = ldx; ga.ldy = ldy; ga.m = T; ga.n = c.cout; ga.K = c.K * c.cin;
-    ga.cig = c.cin; ga.ksize = c.K; ga.dil = c.dil; ga.ctx = (c.K - 1) * c.dil; ga.hist = h ? h->b[h->cur] : nullptr;
+    ga.cig = c.cin; ga.ksize = c.K; ga.dil = c.dil; ga.ctx = (c.K - 1) * c.dil; ga.hist = h ? h->b[par] : nullptr;
     ga.ws = g.gemm_ws; ga.ws_cap = kGemmWsFloats;
     if (ga.ctx && !h) throw Fail("codec convolution without its history");
-    HIPCHECK(launch_stream_conv(gemv_type(M), M.w, M.s, X, ga, s));
-    if (ga.ctx) {
-        HIPCHECK(launch_hist_shift(h->b[1 - h->cur], h->b[h->cur], X, ldx, T, ga.ctx, c.cin, s));
-        h->cur = 1 - h->cur;
-    }
+    HIPCHECK(launch_stream_conv(gemv_type(M), snake ? EPI_SNAKE : EPI_STORE, M.w, M.s, X, ga, s));
+    if (ga.ctx) HIPCHECK(launch_hist_shift(h->b[1 - par], h->b[par], X, ldx, T, ga.ctx, c.cin, s));
 }
 // y (=, +=, gelu, gamma-gated +=) W x + bias over rows of the f32-activation GEMM (the f32 tile semantics of matmul
 // for F32 / F16 / BF16 weights at any row count).
@@ -2397,18 +2403,18 @@ void codec_gemm(int mat, int epi, const float *A, int64_t lda, int64_t rows, flo
 // (E.rope); returns the sample count, left in E.S[4].
 int64_t codec_enqueue(Codec &E, CodecSt &St, int T, hipStream_t s) {
     Xfmr &X = xf_at(E.xf);
-    const int L = E.latent, H = E.H, qd = E.heads * E.hd, QW = (E.heads + 2 * E.kvh) * E.hd;
+    const int L = E.latent, H = E.H, qd = E.heads * E.hd, QW = (E.heads + 2 * E.kvh) * E.hd, par = St.parity;
     float *A = E.S[0], *B = E.S[1];
     // 1) pre_conv -> A [T][latent]; 2) the pre-transformer (kernels.cpp:760-844 with window and layer scales)
-    codec_conv(E.pre_conv, &St.pre, E.z, E.cdim, T, A, L, s);
+    codec_conv(E.pre_conv, &St.pre, par, E.z, E.cdim, T, A, L, s);
     gemv(mat_at(E.pt_in), T, PRO_X, EPI_STORE, A, L, T, E.h, H, nullptr, 0.f, nullptr, s);
     const float scale = 1.0f / std::sqrt(float(E.hd));
     for (int li = 0; li < E.layers; ++li) {
         const LayerDev &d = X.L[size_t(li)];
         gemv(mat_at(d.qkv), T, PRO_RMS, EPI_STORE, E.h, H, T, E.qkv, QW, X.norms + d.ln1, E.eps, nullptr, s, nullptr, E.pre);
         HIPCHECK(launch_codec_rope_ring(E.qkv, QW, T, E.heads, E.kvh, E.hd, E.rope, St.kr[size_t(li)], St.vr[size_t(li)], E.R,
-                                        St.len, s));
-        HIPCHECK(launch_codec_attn(E.qkv, QW, St.kr[size_t(li)], St.vr[size_t(li)], E.R, T, E.heads, E.kvh, E.hd, St.len, E.W,
+                                        St.pos_dev, s));
+        HIPCHECK(launch_codec_attn(E.qkv, QW, St.kr[size_t(li)], St.vr[size_t(li)], E.R, T, E.heads, E.kvh, E.hd, St.pos_dev, E.W,
                                    scale, E.ao, s));
         if (E.sa[size_t(li)]) {
             gemv(mat_at(d.o), T, PRO_X, EPI_STORE, E.ao, qd, T, E.tmp, H, nullptr, 0.f, nullptr, s);
@@ -2425,7 +2431,6 @@ int64_t codec_enqueue(Codec &E, CodecSt &St, int T, hipStream_t s) {
         }
     }
     gemv(mat_at(E.pt_out), T, PRO_RMS, EPI_STORE, E.h, H, T, A, L, X.norms + X.final_off, E.eps, nullptr, s, nullptr, E.pre);
-    St.len += T;
     // 3) upsample stages: transposed conv (K = stride: the overlap-add has no tail) + ConvNeXt
     int64_t len = T;
     float *cur = A;
@@ -2436,9 +2441,8 @@ int64_t codec_enqueue(Codec &E, CodecSt &St, int T, hipStream_t s) {
         HIPCHECK(launch_ola(E.S[2], nullptr, nullptr, U.tr_b, y, int(len), U.K, U.K, L, s));
         len *= U.K;
         Hist2 &hd = St.dw[si];
-        HIPCHECK(launch_dwconv_causal(y, hd.b[hd.cur], U.dw_w, U.dw_b, E.S[2], int(len), L, U.dwK, s));
-        HIPCHECK(launch_hist_shift(hd.b[1 - hd.cur], hd.b[hd.cur], y, L, int(len), U.dwK - 1, L, s));
-        hd.cur = 1 - hd.cur;
+        HIPCHECK(launch_dwconv_causal(y, hd.b[par], U.dw_w, U.dw_b, E.S[2], int(len), L, U.dwK, s));
+        HIPCHECK(launch_hist_shift(hd.b[1 - par], hd.b[par], y, L, int(len), U.dwK - 1, L, s));
         HIPCHECK(launch_layernorm_rows(E.S[2], len, L, U.ln_w, U.ln_b, E.S[3], s));
         codec_gemm(U.pw1, EPI_GELU_ERF, E.S[3], L, len, E.S[4], 4 * int64_t(L), nullptr, s);
         codec_gemm(U.pw2, EPI_GATED_ACC, E.S[4], 4 * int64_t(L), len, y, L, U.gamma, s);
@@ -2446,7 +2450,7 @@ int64_t codec_enqueue(Codec &E, CodecSt &St, int T, hipStream_t s) {
     }
     // 4) conv0 -> blocks -> Snake -> final conv -> clamp
     float *x = cur == A ? B : A;
-    codec_conv(E.conv0, &St.c0, cur, L, int(len), x, E.dec, s);
+    codec_conv(E.conv0, &St.c0, par, cur, L, int(len), x, E.dec, s);
     int ch = E.dec;
     for (size_t bi = 0; bi < E.blocks.size(); ++bi) {
         const CodecBlk &Bk = E.blocks[bi];
@@ -2455,21 +2459,19 @@ int64_t codec_enqueue(Codec &E, CodecSt &St, int T, hipStream_t s) {
         codec_gemm(Bk.tr, EPI_STORE, sa, ch, len, E.S[2], int64_t(Bk.K) * Bk.cout, nullptr, s);
         float *y = x;  // x is consumed
         Hist2 &tl = St.tail[bi];
-        HIPCHECK(launch_ola(E.S[2], tl.b[tl.cur], tl.b[1 - tl.cur], Bk.tr_b, y, int(len), Bk.s, Bk.K, Bk.cout, s));
-        tl.cur = 1 - tl.cur;
+        HIPCHECK(launch_ola(E.S[2], tl.b[par], tl.b[1 - par], Bk.tr_b, y, int(len), Bk.s, Bk.K, Bk.cout, s));
         len *= Bk.s;
         ch = Bk.cout;
         for (int u = 0; u < 3; ++u) {
             HIPCHECK(launch_snake(y, Bk.a1[u].a, Bk.a1[u].inv_b, sa, len, ch, s));
-            codec_conv(Bk.c1[u], &St.ru[bi * 3 + size_t(u)], sa, ch, int(len), E.S[3], ch, s);
-            HIPCHECK(launch_snake(E.S[3], Bk.a2[u].a, Bk.a2[u].inv_b, E.S[3], len, ch, s));
+            codec_conv(Bk.c1[u], &St.ru[bi * 3 + size_t(u)], par, sa, ch, int(len), E.S[3], ch, s, &Bk.a2[u]);  // + Snake a2
             codec_gemm(Bk.c2[u].mat, EPI_ACC, E.S[3], ch, len, y, ch, nullptr, s);
         }
         x = y;
     }
     float *sa = x == A ? B : A;
     HIPCHECK(launch_snake(x, E.fin_act.a, E.fin_act.inv_b, sa, len, ch, s));
-    codec_conv(E.fin, &St.fin, sa, ch, int(len), E.S[4], 1, s);
+    codec_conv(E.fin, &St.fin, par, sa, ch, int(len), E.S[4], 1, s);
     HIPCHECK(launch_clamp1(E.S[4], len, s));
     return len;
 }
@@ -2609,6 +2611,7 @@ int voxhip_codec_state_new(int codec) {
             for (int u = 0; u < 3; ++u) S->ru.push_back(hist_new((b.c1[u].K - 1) * b.c1[u].dil, b.c1[u].cin));
         }
         S->fin = hist_new((E.fin.K - 1) * E.fin.dil, E.fin.cin);
+        S->pos_dev = static_cast<int64_t *>(dalloc(sizeof(int64_t)));
         g.cstates.push_back(S.release());
         return int(g.cstates.size()) - 1;
     }, -1);
@@ -2623,12 +2626,14 @@ int voxhip_codec_state_clone(int state) {
         std::unique_ptr<CodecSt> S(new CodecSt());
         S->codec = src.codec;
         S->len = src.len;
-        S->pre = hist_clone(src.pre);
-        S->c0 = hist_clone(src.c0);
-        S->fin = hist_clone(src.fin);
-        for (const Hist2 &h : src.dw) S->dw.push_back(hist_clone(h));
-        for (const Hist2 &h : src.tail) S->tail.push_back(hist_clone(h));
-        for (const Hist2 &h : src.ru) S->ru.push_back(hist_clone(h));
+        const int par = src.parity;
+        S->pre = hist_clone(src.pre, par);
+        S->c0 = hist_clone(src.c0, par);
+        S->fin = hist_clone(src.fin, par);
+        for (const Hist2 &h : src.dw) S->dw.push_back(hist_clone(h, par));
+        for (const Hist2 &h : src.tail) S->tail.push_back(hist_clone(h, par));
+        for (const Hist2 &h : src.ru) S->ru.push_back(hist_clone(h, par));
+        S->pos_dev = static_cast<int64_t *>(dalloc(sizeof(int64_t)));
         const size_t kd = size_t(E.kvh) * E.hd;
         for (size_t l = 0; l < src.kr.size(); ++l) {
             S->kr.push_back(dalloc_t<float>(size_t(E.R) * kd));
@@ -2651,6 +2656,8 @@ int voxhip_codec_state_free(int state) {
             for (Hist2 &h : *v) hist_free(h);
         for (float *p : S.kr) dfree(p);
         for (float *p : S.vr) dfree(p);
+        dfree(S.pos_dev);
+        for (auto &kv : S.graphs) (void)hipGraphExecDestroy(kv.second);
         delete g.cstates[size_t(state)];
         g.cstates[size_t(state)] = nullptr;
         return 1;
@@ -2676,9 +2683,34 @@ int voxhip_codec_forward(int codec, int state, const float *z, int F, float *pcm
             }
         h2d(E.z, z, size_t(F) * size_t(E.cdim) * 4);
         h2d(E.rope, cs.data(), cs.size() * 4);
-        const int64_t n = codec_enqueue(E, St, F, g.stream);
+        h2d(St.pos_dev, &St.len, sizeof(int64_t));
+        // the call's ~150 launches as one graph per (F, parity): the buffers, the weights and the scratch are fixed,
+        // the position comes from pos_dev
+        const int key = 2 * F + St.parity;
+        auto it = St.graphs.find(key);
+        if (it == St.graphs.end()) {
+            hipGraph_t graph = nullptr;
+            HIPCHECK(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal));
+            try {
+                codec_enqueue(E, St, F, g.stream);
+            } catch (...) {
+                (void)hipStreamEndCapture(g.stream, &graph);
+                if (graph) (void)hipGraphDestroy(graph);
+                throw;
+            }
+            HIPCHECK(hipStreamEndCapture(g.stream, &graph));
+            hipGraphExec_t exec = nullptr;
+            hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            HIPCHECK(e);
+            it = St.graphs.emplace(key, exec).first;
+        }
+        HIPCHECK(hipGraphLaunch(it->second, g.stream));
         HIPCHECK(hipStreamSynchronize(g.stream));
+        const int64_t n = int64_t(F) * E.spf;
         HIPCHECK(hipMemcpy(pcm, E.S[4], size_t(n) * 4, hipMemcpyDeviceToHost));
+        St.len += F;
+        St.parity ^= 1;
         if (n_out) *n_out = n;
         return 1;
     }, 0);
