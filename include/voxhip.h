@@ -76,7 +76,9 @@ int voxhip_init(const char *device, char *err, size_t err_len);
 int voxhip_active(void);                                   /* gpu_active (gpu.hpp:11) */
 const char *voxhip_device_name(void);                      /* gpu_device_name (gpu.hpp:12) */
 void voxhip_stats_get(voxhip_stats *out);                  /* gpu_stats (gpu.hpp:17) */
-const char *voxhip_last_error(void);                       /* GpuStats::last_error (gpu.hpp:16) */
+/* GpuStats::last_error (gpu.hpp:16): copied under the library lock into a buffer of the calling thread, valid
+ * until that thread's next voxhip_last_error call (a failure on another thread cannot change it). */
+const char *voxhip_last_error(void);
 void voxhip_set_vram_limit(uint64_t bytes);                /* gpu_set_vram_limit (gpu.hpp:34) */
 void voxhip_mem_info_get(voxhip_mem_info *out);            /* gpu_mem_info (gpu.hpp:36) */
 
@@ -90,6 +92,11 @@ int voxhip_upload(const voxhip_mat *parts, int n_parts);
  * Semantics of matmul (kernels.cpp:653-705): Q8 with m <= 8 and Q4 quantize x per 32-block to int8
  * and use integer dots; Q8 with m > 8 and F32/F16/BF16 use f32 activations. Returns 1 or 0. */
 int voxhip_matmul(int mat, const float *x, int64_t m, float *y);
+/* mat_gather (kernels.cpp:468-471, through mat_row :432-466) on the device: out [n][cols] = row ids[i] of the
+ * matrix widened to f32 (F16 / BF16 exactly, Q8 float(q) * s, Q4 float(u - 8) * s), the unpack the device
+ * embedding gathers of the LM and the code predictor use. Host ids and out; an id outside the rows fails (0) before
+ * anything is written, as check_id does before the gathers (backend_qwen3.cpp:305-306). No counterpart in gpu.hpp. */
+int voxhip_mat_gather(int mat, const int32_t *ids, int64_t n, float *out);
 /* Rows and cols of a device matrix (0 on a bad handle). */
 int voxhip_mat_shape(int mat, int64_t *rows, int64_t *cols);
 
@@ -174,9 +181,6 @@ int voxhip_sample_logits(const float *logits, int32_t n, const voxhip_sample_cfg
  * (cfg->frame, cb) into codes[cb]. codes[0] is not written. Returns 1, or 0 with the error set. */
 int voxhip_pred_frame(int xfmr, int seq, const float *in2, int in_proj, const int *heads, int n_heads, const int *embs,
                       int n_embs, const voxhip_sample_cfg *cfg, int32_t *codes);
-
-/* gpu_codec_* (gpu.hpp:55-61) and gpu_cosy_* (gpu.hpp:114-119) are not provided yet: gpu_hip.cpp answers them
- * like gpu_stub.cpp (-1 / false), and the callers compute on the CPU. */
 
 /* ---------------------------------------------------------------- device-resident path
  * Entry points for callers that keep activations in device memory (bench, tests, a device-side

@@ -191,7 +191,7 @@ int main() {
         gpu_seq_free(s1);
         gpu_seq_free(s2);
     }
-    // entry points this backend leaves to the CPU answer like gpu_stub.cpp
+    // an empty F5 / estimator descriptor (no blocks, no matrices) is refused with -1, so the caller keeps its CPU path
     CHECK(gpu_f5_create(GpuF5Desc{}) == -1 && gpu_cosy_create(GpuCosyDesc{}) == -1);
 
     // ---- the codec decoder: a Qwen3Weights as upload_gpu leaves it (matrices on the device), decoded in two chunks

@@ -42,6 +42,27 @@ def test_quantizers_bit_exact(hip, oracle):
     assert np.array_equal(xq, oq) and np.array_equal(xs.view(np.uint32), os_.view(np.uint32))
 
 
+@pytest.mark.parametrize("wt", [Q8, Q4, F32, F16, BF16, "q4h"])
+def test_mat_gather_bit_exact(hip, oracle, wt):
+    # mat_row / mat_gather (kernels.cpp:432-471): the device unpack of every weight type, the one the LM and code
+    # predictor embedding gathers use, equals the oracle's row bit for bit (q4h: Q4 whose scales are all exact in
+    # f16, stored in 2 bytes on the device)
+    rng = np.random.default_rng(31 + (wt if isinstance(wt, int) else 9))
+    t = Q4 if wt == "q4h" else wt
+    rows, cols = 300, 896
+    data, scale, _ = make_mat(rng, t, rows, cols, std=0.5)
+    if wt == "q4h":
+        scale = scale.astype(np.float16).astype(np.float32)
+    M = oracle.Mat(t, data, rows, cols, scale, None)
+    h = hip.upload(hip.HostMat(t, data, rows, cols, scale, None))
+    ids = np.concatenate([[0, rows - 1, 7, 7], rng.integers(0, rows, 60)]).astype(np.int32)
+    got = hip.mat_gather(h, ids, cols)
+    want = np.stack([oracle.mat_row(M, int(r)) for r in ids])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    with pytest.raises(hip.VoxHipError, match="outside"):
+        hip.mat_gather(h, np.array([0, rows], np.int32), cols)
+
+
 @pytest.mark.parametrize("wt", [Q8, Q4, F32, F16, BF16])
 # tiles: (37,160) R1; (4096,1024) R4; (1024,3072) IT3; (3072,1024) R3; (5,4864) IT4 over two passes; (6144,1024) R6;
 # (8192,256) R8; (2048,2048) IT2 (R2 for m > 1)

@@ -238,6 +238,34 @@ def test_decode_graph_replays(hip, oracle):
         b.free()
 
 
+@pytest.mark.parametrize("wt", [F16, Q8])
+def test_decode_dev_rows_new_position(hip, oracle, wt):
+    # m = 6 rows of one sequence per captured step, replayed at a later position: F16 takes the prefill attention
+    # kernel (q8 the int path), which must take the pass's first position from the device row table, not from the
+    # capture. Both replays against the oracle continuing the same sequence.
+    mdl = Model(720 + wt, 2, 256, 4, 2, 128, 512, wtype=wt, head_rows=128)
+    xf, head = build(hip, mdl)
+    seq = hip.seq_create(xf, 32)
+    kv = mdl.oracle_kv(32, kv_f16=1)
+    rng = np.random.default_rng(20 + wt)
+    pre = rng.standard_normal((3, 256)).astype(np.float32)
+    hip.forward(xf, seq, 0, pre, 256)
+    oracle.transformer_forward(mdl.ox, kv, pre)
+    dx, dout, dlog = hip.DevBuf(6 * 256 * 4), hip.DevBuf(256 * 4), hip.DevBuf(128 * 4)
+    for pos0 in (3, 9, 15):
+        x = rng.standard_normal((6, 256)).astype(np.float32)
+        dx.upload(x)
+        hip.decode_dev(xf, seq, pos0, dx, 6, dout, head, dlog)
+        hip.sync()
+        out = dout.download(256, np.float32)
+        lg = dlog.download(128, np.float32)
+        ref = oracle.transformer_forward(mdl.ox, kv, x)
+        assert rel_err(out, ref) < TOL, (pos0, rel_err(out, ref))
+        assert rel_err(lg, oracle_head(oracle, mdl, out)) < TOL, pos0
+    for b in (dx, dout, dlog):
+        b.free()
+
+
 def test_layer_ranges_compose(hip, oracle):
     # forward_layers over [0, 1) then [1, 2) equals the oracle's layers, teacher-forced per layer
     mdl = Model(900, 2, 256, 4, 2, 128, 512, wtype=Q8)

@@ -97,6 +97,9 @@ hipError_t launch_stream_conv(int wt, int epi, const uint8_t *w, const float *sc
 hipError_t launch_lm_sample(const float *logits, int n, const LmCfgDev *cfg, LmState *st, int32_t *decoded, float *logp_out,
                             int64_t logp_stride, bool append, hipStream_t s);
 hipError_t launch_lm_embed(const LmEmbedArgs &a, hipStream_t s);
+// mat_gather of n rows ids[0..n) (device, already range-checked) into out [n][cols]; wt a WT_* weight format.
+hipError_t launch_mat_gather(const uint8_t *w, const void *scale, int wt, int s16, int64_t cols, const int32_t *ids,
+                             int64_t n, float *out, hipStream_t s);
 // A pass of the code-predictor frame loop: row table + RoPE rows of the pass, the sampled code's embedding row.
 hipError_t launch_pred_embed(const PredEmbedArgs &a, hipStream_t s);
 

@@ -17,6 +17,13 @@ hipError_t launch_pred_embed(const PredEmbedArgs &a, hipStream_t s) {
     return launch(k_pred_embed, dim3(1), dim3(256), 0, s, a);
 }
 
+hipError_t launch_mat_gather(const uint8_t *w, const void *scale, int type, int s16, int64_t cols, const int32_t *ids,
+                             int64_t n, float *out, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    if (n > INT32_MAX || cols <= 0 || (type == WT_Q8 || type == WT_Q4) && cols % 32) return hipErrorInvalidValue;
+    return launch(k_mat_gather, dim3(unsigned(n)), dim3(256), 0, s, w, scale, int32_t(type), int32_t(s16), cols, ids, out);
+}
+
 hipError_t launch_lm_embed(const LmEmbedArgs &a, hipStream_t s) {
     if (a.hd <= 0 || a.cols <= 0 || (a.type == WT_Q8 || a.type == WT_Q4) && a.cols % 32) return hipErrorInvalidValue;
     return launch(k_lm_embed, dim3(1), dim3(256), 0, s, a);

@@ -273,6 +273,13 @@ VH_DEV void gather_row(const uint8_t *w, const void *scale, int type, int s16, i
     }
 }
 
+// mat_gather (kernels.cpp:468-471) of n rows: block i widens row ids[i] of the matrix into out + i cols. The host
+// checks every id against the row count before the launch. Grid n, block 256.
+__global__ __launch_bounds__(256) void k_mat_gather(const uint8_t *w, const void *scale, int type, int s16, int64_t cols,
+                                                    const int32_t *ids, float *out) {
+    gather_row(w, scale, type, s16, cols, ids[blockIdx.x], out + int64_t(blockIdx.x) * cols);
+}
+
 // A pass of the code-predictor frame loop (gpu_vulkan.cpp:1004-1017): its rows at positions pos0 .. pos0 + m - 1
 // with their RoPE rows from the table, and, after the first pass, the embedding row of the code just sampled
 // (mat_gather of backend_qwen3.cpp:411). A code outside the embedding sets *err (check_id in the reference) and

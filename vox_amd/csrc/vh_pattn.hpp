@@ -62,8 +62,9 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
     for (int i = 0; i < 4; ++i) { mrow[i] = -INFINITY; lrow[i] = 0.f; }
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt) o[dt] = pf32x4{0.f, 0.f, 0.f, 0.f};
+    const int64_t pos0 = a.rows[0].pos;
     const int64_t last_row = r0 + 63 < a.m - 1 ? r0 + 63 : a.m - 1;
-    const int64_t kend = a.pos0 + last_row + 1;  // keys [0, kend) reach some row of this block
+    const int64_t kend = pos0 + last_row + 1;  // keys [0, kend) reach some row of this block
     u32x4 kr[KQ], vr[KQ];
     auto fetch = [&](int64_t kt) {
 #pragma unroll
@@ -102,7 +103,7 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
         // lane holds S[4 lg + i][16 j + lr]; row 4 lg + i of the wave sits at position pos0 + r0 + 16 wave + 4 lg + i
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int64_t pos = a.pos0 + r0 + 16 * wave + 4 * lg + i;
+            const int64_t pos = pos0 + r0 + 16 * wave + 4 * lg + i;
             float mx = -INFINITY;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {

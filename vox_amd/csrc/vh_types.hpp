@@ -92,7 +92,9 @@ struct PrefillAttnArgs {
     const float *q;        // [m][heads hd] normed + rotated queries
     const _Float16 *k, *v; // the sequence's cache bases ([layer][kv_head][cap][hd])
     float *out;            // [m][heads hd]
-    int64_t cap, pos0;
+    const RowRef *rows;    // the pass's row table: the kernel takes pos0 from rows[0].pos, so a captured pass
+                           // replays at whatever position the host last wrote there
+    int64_t cap, pos0;     // pos0: the host's copy of rows[0].pos at launch, checked against cap
     int32_t m, heads, kv_heads, layer;
     float scale;
 };

@@ -560,7 +560,8 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
         const RowRef &r0 = X.rows_last.at(0);
         if (pass_attn && gemm_path(Mo, m_total, mc)) {
             PrefillAttnArgs pa{};
-            pa.q = X.q; pa.k = r0.k; pa.v = r0.v; pa.out = X.pre; pa.cap = r0.cap; pa.pos0 = r0.pos; pa.m = mc;
+            pa.q = X.q; pa.k = r0.k; pa.v = r0.v; pa.out = X.pre; pa.rows = X.rows_dev; pa.cap = r0.cap; pa.pos0 = r0.pos;
+            pa.m = mc;
             pa.heads = X.heads; pa.kv_heads = X.kvh; pa.layer = li; pa.scale = 1.0f / std::sqrt(float(X.hd));
             probed(pr, VOXHIP_K_ATTN, [&] { HIPCHECK(launch_prefill_attn(pa, X.hd, s)); });
             probed(pr, VOXHIP_K_O, [&] { gemv(Mo, m_total, PRO_X, EPI_ACC, X.pre, qd, mc, X.h, X.H, nullptr, 0.f, nullptr, s); });
@@ -799,6 +800,18 @@ int make_xfmr(const voxhip_xfmr_desc *w, const char *name, int use_layers, const
     return int(g.xf.size()) - 1;
 }
 
+// "<marketing name> (<arch>)". Some driver stacks report an empty marketing name; the label then names the
+// product family of the architecture, so device lists and GpuDeviceInfo::name still say what the card is.
+std::string device_label(const hipDeviceProp_t &p) {
+    std::string name(p.name, strnlen(p.name, sizeof p.name));
+    while (!name.empty() && (name.back() == ' ' || name.back() == '\n')) name.pop_back();
+    if (name.empty()) {
+        if (std::strncmp(p.gcnArchName, "gfx950", 6) == 0) name = "AMD Instinct MI350 series (MI350X / MI355X)";
+        else name = "AMD GPU";
+    }
+    return name + " (" + p.gcnArchName + ")";
+}
+
 int parse_index(const char *spec) {
     int idx = 0;
     if (spec) {
@@ -827,7 +840,7 @@ int voxhip_device_info_get(int index, voxhip_device_info *out) {
     hipDeviceProp_t p;
     if (hipGetDeviceProperties(&p, index) != hipSuccess) return 0;
     out->index = index;
-    std::snprintf(out->name, sizeof out->name, "%s (%s)", p.name, p.gcnArchName);
+    std::snprintf(out->name, sizeof out->name, "%s", device_label(p).c_str());
     std::snprintf(out->type, sizeof out->type, "%s", p.integrated ? "integrated" : "discrete");
     out->software = 0;
     out->unified_memory = p.integrated ? 1 : 0;
@@ -873,7 +886,7 @@ int voxhip_init(const char *device, char *err, size_t err_len) {
         g.qrows = dalloc_t<int8_t>(size_t(kQuantRowsElems));
         g.qrows_s = dalloc_t<float>(size_t(kQuantRowsElems / 32));
         g.qrows_sum = dalloc_t<int32_t>(size_t(kQuantRowsElems / 32));
-        g.name = std::string(p.name) + " (" + p.gcnArchName + ")";
+        g.name = device_label(p);
         g.ok = true;
         return 1;
     } catch (const std::exception &e) {
@@ -889,7 +902,13 @@ void voxhip_stats_get(voxhip_stats *out) {
     std::lock_guard<std::mutex> lk(g.mu);
     if (out) *out = g.stats;
 }
-const char *voxhip_last_error(void) { return g.last_error.c_str(); }
+const char *voxhip_last_error(void) {
+    // a copy taken under the lock: another thread's failure may replace g.last_error meanwhile
+    thread_local std::string copy;
+    std::lock_guard<std::mutex> lk(g.mu);
+    copy = g.last_error;
+    return copy.c_str();
+}
 void voxhip_set_vram_limit(uint64_t bytes) {
     std::lock_guard<std::mutex> lk(g.mu);
     g.vram_limit = bytes;
@@ -950,6 +969,31 @@ int voxhip_matmul(int mat, const float *x, int64_t m, float *y) {
             HIPCHECK(hipMemcpyAsync(pin, dy, size_t(mc) * size_t(M.rows) * 4, hipMemcpyDeviceToHost, g.stream));
             HIPCHECK(hipStreamSynchronize(g.stream));
             std::memcpy(y + c0 * M.rows, pin, size_t(mc) * size_t(M.rows) * 4);
+        }
+        return 1;
+    }, 0);
+}
+
+int voxhip_mat_gather(int mat, const int32_t *ids, int64_t n, float *out) {
+    return guard_int([&] {
+        require_ok();
+        const GpuMat &M = mat_at(mat);
+        if (n < 0 || (n > 0 && (!ids || !out))) throw Fail("mat_gather: missing argument");
+        for (int64_t i = 0; i < n; ++i)  // check_id before any gather (backend_qwen3.cpp:305-306)
+            if (ids[i] < 0 || ids[i] >= M.rows) throw Fail("mat_gather: row " + std::to_string(ids[i]) + " outside the matrix");
+        const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n, (int64_t(64) << 20) / (M.cols * 4)));
+        const size_t ob = size_t(chunk) * size_t(M.cols) * 4, ib = size_t(chunk) * 4;
+        float *pin = pinned(std::max(ob, ib) + 64);
+        int32_t *dids = reinterpret_cast<int32_t *>(dev_scratch(g.dbuf_x, g.dbuf_x_bytes, ib));
+        float *dout = dev_scratch(g.dbuf_y, g.dbuf_y_bytes, ob);
+        for (int64_t c0 = 0; c0 < n; c0 += chunk) {
+            const int64_t nc = std::min(chunk, n - c0);
+            std::memcpy(pin, ids + c0, size_t(nc) * 4);
+            HIPCHECK(hipMemcpyAsync(dids, pin, size_t(nc) * 4, hipMemcpyHostToDevice, g.stream));
+            HIPCHECK(launch_mat_gather(M.w, M.s, gemv_type(M), M.s16 ? 1 : 0, M.cols, dids, nc, dout, g.stream));
+            HIPCHECK(hipMemcpyAsync(pin, dout, size_t(nc) * size_t(M.cols) * 4, hipMemcpyDeviceToHost, g.stream));
+            HIPCHECK(hipStreamSynchronize(g.stream));
+            std::memcpy(out + c0 * M.cols, pin, size_t(nc) * size_t(M.cols) * 4);
         }
         return 1;
     }, 0);
@@ -2477,6 +2521,47 @@ int64_t codec_enqueue(Codec &E, CodecSt &St, int T, hipStream_t s) {
 }
 }  // namespace
 
+namespace {
+// The object that keeps device pointers into matrix `mat` (a transformer layer, an F5 / estimator / codec instance,
+// whose launches or captured graphs read it), or null when none does.
+const char *mat_user(int mat) {
+    for (const Xfmr *X : g.xf)
+        if (X)
+            for (const LayerDev &L : X->L)
+                if (L.qkv == mat || L.o == mat || L.gu == mat || L.down == mat) return "a transformer";
+    for (const F5 *F : g.f5) {
+        if (!F) continue;
+        if (F->in_proj == mat || F->norm_out == mat || F->proj_out == mat || F->v_head == mat) return "an F5 model";
+        for (const F5Block &b : F->blocks)
+            if (b.ada == mat || b.qkv == mat || b.o == mat || b.ff1 == mat || b.ff2 == mat) return "an F5 model";
+        for (const F5VBlock &b : F->vblocks)
+            if (b.pw1 == mat || b.pw2 == mat) return "an F5 model";
+    }
+    for (const Cosy *E : g.cosy) {
+        if (!E) continue;
+        for (const auto *xs : {&E->down_x, &E->up_x})
+            for (const CosyX &x : *xs)
+                if (x.qkv == mat || x.o == mat || x.ff1 == mat || x.ff2 == mat) return "a flow estimator";
+        for (const auto &xs : E->mid_x)
+            for (const CosyX &x : xs)
+                if (x.qkv == mat || x.o == mat || x.ff1 == mat || x.ff2 == mat) return "a flow estimator";
+    }
+    for (const Codec *C : g.codecs) {
+        if (!C) continue;
+        if (C->pre_conv.mat == mat || C->conv0.mat == mat || C->fin.mat == mat || C->pt_in == mat || C->pt_out == mat)
+            return "a codec decoder";
+        for (const CodecUp &u : C->ups)
+            if (u.tr == mat || u.pw1 == mat || u.pw2 == mat) return "a codec decoder";
+        for (const CodecBlk &b : C->blocks) {
+            if (b.tr == mat) return "a codec decoder";
+            for (int i = 0; i < 3; ++i)
+                if (b.c1[i].mat == mat || b.c2[i].mat == mat) return "a codec decoder";
+        }
+    }
+    return nullptr;
+}
+}  // namespace
+
 extern "C" {
 
 int voxhip_codec_create(const voxhip_codec_desc *d) {
@@ -2780,11 +2865,13 @@ int voxhip_mat_download(int mat, void *data, float *scale, float *bias) {
 int voxhip_mat_free(int mat) {
     return guard_int([&] {
         require_ok();
+        mat_at(mat);
         HIPCHECK(hipStreamSynchronize(g.stream));
-        for (const Xfmr *X : g.xf)
-            if (X)
-                for (const LayerDev &L : X->L)
-                    if (L.qkv == mat || L.o == mat || L.gu == mat || L.down == mat) throw Fail("matrix is used by a transformer");
+        const char *user = mat_user(mat);
+        if (user) throw Fail(std::string("matrix is used by ") + user);
+        // decode, generation and frame graphs captured a head, embedding or input projection by address
+        for (Xfmr *X : g.xf)
+            if (X) drop_graphs(*X);
         free_mat(mat);
         return 1;
     }, 0);

@@ -204,6 +204,7 @@ SIGNATURES = {
     "voxhip_mat_synthetic": (_I, [_I32, _I64, _I64, _U64, _U32, _F, _F, _I]),
     "voxhip_mat_download": (_I, [_I, _P, _P, _P]),
     "voxhip_mat_free": (_I, [_I]),
+    "voxhip_mat_gather": (_I, [_I, _P, C.c_int64, _P]),
     "voxhip_xfmr_create_from_mats": (_I, [C.POINTER(XfmrDesc), _P, C.c_char_p]),
     "voxhip_seq_fill_synthetic": (_I, [_I, _I64, _U64, _U32, _F, _F]),
     "voxhip_seq_download": (_I, [_I, _I32, _I64, _P, _P]),
@@ -341,6 +342,14 @@ def mat_download(mat, wtype):
     bias = np.empty(rows, np.float32)
     _check(lib().voxhip_mat_download(mat, _p(data), _p(scale), _p(bias)), "mat_download")
     return data, scale, bias
+
+
+def mat_gather(mat, ids, cols):
+    """mat_gather of rows ids on the device -> f32 [len(ids)][cols]."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    out = np.empty((ids.size, cols), np.float32)
+    _check(lib().voxhip_mat_gather(mat, _p(ids), ids.size, _p(out)), "mat_gather")
+    return out
 
 
 def mat_free(mat):
