@@ -445,8 +445,12 @@ int voxhip_bench_gemv_q8(int64_t rows, int64_t cols, int copies, int warmup, int
 
 /* BASELINE configs[0] on the device: one q8 FFN block (RMSNorm -> gate|up GEMV + SwiGLU -> down GEMV + residual,
  * two kernels) over `copies` distinct weight sets in one graph, so the working set exceeds the 256 MB Infinity
- * Cache: average microseconds per block. No reference counterpart (benchmark helper). */
-int voxhip_bench_ffn_q8(int64_t hidden, int64_t inter, int copies, int warmup, int iters, double *us_per_block);
+ * Cache: average microseconds per block. Copy c's gate|up matrix [2 inter][hidden] (gate row u at row 2u, up row u
+ * at 2u + 1) is voxhip_mat_synthetic(Q8, 2 inter, hidden, 2000 + c, 0x60, 0, 0.02), its down matrix the same with
+ * (hidden, inter, stream 0x61); x ~N(0, 1) and gamma ~N(1, 0.02) come from the same generator (seeds 7 / 8, streams
+ * 0x70 / 0x71), eps 1e-6. check (host, may be NULL): [3][hidden] = x, gamma and copy 0's block applied once to x,
+ * for the parity test. No reference counterpart (benchmark helper). */
+int voxhip_bench_ffn_q8(int64_t hidden, int64_t inter, int copies, int warmup, int iters, double *us_per_block, float *check);
 
 /* Times a plain 16-byte device copy of `bytes` (STREAM copy; reads and writes `bytes` each): average ms per copy.
  * The same kernel calibrates the HBM traffic counters. No reference counterpart (benchmark helper). */

@@ -51,6 +51,16 @@ def test_f5_step_full_width(hip, oracle):
     run(hip, oracle, m, 2, 200, seed=3)
 
 
+@pytest.mark.parametrize("B", [2, 1])
+def test_f5_step_cfg4_shape(hip, oracle, B):
+    # configs[3]'s benchmarked step shape: N = 1000 frames (the attention's last key tile holds 40 keys), B = 2 (CFG)
+    # and B = 1, at the full widths; two of the 22 blocks (every block takes the same kernels and tiles, which depend
+    # on the rows B N, not on the depth), so the 16-thread oracle finishes in about 10 s
+    oracle.lib().vo_set_threads(16)
+    m = F5Model(51, 1024, 2, 16, mel=100, text=512, K=31, groups=16, wtype=F16, std=0.02)
+    run(hip, oracle, m, B, 1000, seed=4 + B)
+
+
 def test_f5_rejects_bad_shapes(hip):
     m = F5Model(60, 128, 1, 2, dim_head=32, wtype=F16)
     with pytest.raises(hip.VoxHipError, match="head_dim"):

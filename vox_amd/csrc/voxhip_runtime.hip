@@ -196,6 +196,8 @@ T *dalloc_t(size_t n) { return static_cast<T *>(dalloc(n * sizeof(T))); }
 
 float *pinned(size_t bytes) {
     if (g.pin_bytes < bytes) {
+        // an asynchronous copy queued by an earlier call may still read the old block
+        if (g.pin) HIPCHECK(hipStreamSynchronize(g.stream));
         if (g.pin) (void)hipHostFree(g.pin);
         g.pin = nullptr;
         g.pin_bytes = 0;
@@ -3126,7 +3128,7 @@ int voxhip_bench_gemv_q8(int64_t rows, int64_t cols, int copies, int warmup, int
     }, 0);
 }
 
-int voxhip_bench_ffn_q8(int64_t hidden, int64_t inter, int copies, int warmup, int iters, double *us_per_block) {
+int voxhip_bench_ffn_q8(int64_t hidden, int64_t inter, int copies, int warmup, int iters, double *us_per_block, float *check) {
     return guard_int([&] {
         require_ok();
         if (copies <= 0 || iters <= 0 || !us_per_block || hidden % 32 || inter % 32) throw Fail("bad bench arguments");
@@ -3165,6 +3167,14 @@ int voxhip_bench_ffn_q8(int64_t hidden, int64_t inter, int copies, int warmup, i
             HIPCHECK(launch_fill_normal(x, hidden, 7, 0x70u, 0.f, 1.f, g.stream));
             HIPCHECK(launch_fill_normal(gamma, hidden, 8, 0x71u, 1.f, 0.02f, g.stream));
             HIPCHECK(hipMemcpyAsync(h, x, size_t(hidden) * 4, hipMemcpyDeviceToDevice, g.stream));
+            if (check) {  // copy 0's block once on x, as the graph launches it: x, gamma and the block's output
+                gemv(g.mats[size_t(ids[0])], 1, PRO_RMS, EPI_SWIGLU, h, hidden, 1, gbuf, inter, gamma, 1e-6f, nullptr, g.stream);
+                gemv(g.mats[size_t(ids[1])], 1, PRO_X, EPI_ACC, gbuf, inter, 1, h, hidden, nullptr, 0.f, nullptr, g.stream);
+                HIPCHECK(hipMemcpyAsync(check, x, size_t(hidden) * 4, hipMemcpyDeviceToHost, g.stream));
+                HIPCHECK(hipMemcpyAsync(check + hidden, gamma, size_t(hidden) * 4, hipMemcpyDeviceToHost, g.stream));
+                HIPCHECK(hipMemcpyAsync(check + 2 * hidden, h, size_t(hidden) * 4, hipMemcpyDeviceToHost, g.stream));
+                HIPCHECK(hipMemcpyAsync(h, x, size_t(hidden) * 4, hipMemcpyDeviceToDevice, g.stream));
+            }
             HIPCHECK(hipStreamSynchronize(g.stream));
             // one graph over all copies: RMSNorm + gate|up + SwiGLU, then down + residual (two kernels per block)
             HIPCHECK(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal));

@@ -214,7 +214,7 @@ SIGNATURES = {
     "voxhip_bench_decode": (_I, [_I, _I, _I64, _P, _I, C.POINTER(SampleCfg), _P, _I, _I, C.POINTER(BenchResult)]),
     "voxhip_bench_gemv_q8": (_I, [_I64, _I64, _I, _I, _I, C.POINTER(C.c_double)]),
     "voxhip_bench_copy": (_I, [_I64, _I, _I, C.POINTER(C.c_double)]),
-    "voxhip_bench_ffn_q8": (_I, [_I64, _I64, _I, _I, _I, C.POINTER(C.c_double)]),
+    "voxhip_bench_ffn_q8": (_I, [_I64, _I64, _I, _I, _I, C.POINTER(C.c_double), _P]),
 }
 
 _lib = None
@@ -339,7 +339,7 @@ def mat_download(mat, wtype):
     else:
         data = np.empty((rows, cols), np.uint16)
     scale = np.empty((rows, cols // 32), np.float32) if wtype in (Q8, Q4) else None
-    bias = np.empty(rows, np.float32)
+    bias = np.zeros(rows, np.float32)  # stays zero for a matrix without bias
     _check(lib().voxhip_mat_download(mat, _p(data), _p(scale), _p(bias)), "mat_download")
     return data, scale, bias
 
@@ -791,8 +791,11 @@ def bench_copy(nbytes, warmup, iters):
     return ms.value
 
 
-def bench_ffn_q8(hidden, inter, copies, warmup, iters):
-    """Average microseconds of one q8 FFN block (two kernels) over `copies` rotating weight sets."""
+def bench_ffn_q8(hidden, inter, copies, warmup, iters, check=False):
+    """Average microseconds of one q8 FFN block (two kernels) over `copies` rotating weight sets; with check, also
+    (x, gamma, out) of copy 0's block applied once to x."""
     us = C.c_double()
-    _check(lib().voxhip_bench_ffn_q8(hidden, inter, copies, warmup, iters, C.byref(us)), "bench_ffn_q8")
-    return us.value
+    chk = np.zeros((3, hidden), np.float32) if check else None
+    _check(lib().voxhip_bench_ffn_q8(hidden, inter, copies, warmup, iters, C.byref(us), None if chk is None else _p(chk)),
+           "bench_ffn_q8")
+    return (us.value, chk[0], chk[1], chk[2]) if check else us.value
