@@ -92,6 +92,17 @@ int voxhip_upload(const voxhip_mat *parts, int n_parts);
  * Semantics of matmul (kernels.cpp:653-705): Q8 with m <= 8 and Q4 quantize x per 32-block to int8
  * and use integer dots; Q8 with m > 8 and F32/F16/BF16 use f32 activations. Returns 1 or 0. */
 int voxhip_matmul(int mat, const float *x, int64_t m, float *y);
+/* voxhip_matmul on device-resident rows, allocating nothing: d_y [m][rows] = d_x [m][cols] . W^T (+ bias), with the
+ * arithmetic of voxhip_matmul (the same kernels and m-dependent paths). No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). It calls no hipMalloc / hipFree: the split-K partial sums and the int path's once-quantized
+ * input rows live in a fixed 6.3 MiB array in the library's code object (one copy per device, held until the
+ * process ends); passes whose scratch would not fit (more than 1.5 Mi floats of partials, or more than 8 x 32768
+ * quantized elements) run the same kernels without it, so no size is refused for lack of scratch. Every call on a
+ * device shares that array: calls are serialised on the library's stream, and calls that overlap on one GPU (for
+ * example the same call captured into graphs replayed on two streams at once) race on it. Asynchronous on the
+ * library's stream (voxhip_sync waits). Returns 1 or 0. */
+int voxhip_matmul_dev_noalloc(int mat, const float *d_x, int64_t m, float *d_y);
 /* mat_gather (kernels.cpp:468-471, through mat_row :432-466) on the device: out [n][cols] = row ids[i] of the
  * matrix widened to f32 (F16 / BF16 exactly, Q8 float(q) * s, Q4 float(u - 8) * s), the unpack the device
  * embedding gathers of the LM and the code predictor use. Host ids and out; an id outside the rows fails (0) before

@@ -30,6 +30,15 @@
 
 using namespace vh;
 
+// Scratch of voxhip_matmul_dev_noalloc, the entry point that allocates nothing: split-K partial sums and the int
+// path's once-quantized input rows of one matrix pass. A fixed array in the code object, so each device the library
+// runs on holds its own copy (6.3 MiB) until the process ends. Host code reaches it only through the address
+// hipGetSymbolAddress returns for the current device (Ctx::noalloc), never through the array's name.
+constexpr int64_t kNoAllocWsFloats = int64_t(3) << 19;               // 1.5 Mi floats of split-K partials (6 MiB)
+constexpr int64_t kNoAllocQElems = int64_t(8) * 32768;               // 8 quantized rows of up to 32768 elements
+constexpr size_t kNoAllocBytes = size_t(kNoAllocWsFloats) * 4 + size_t(kNoAllocQElems) + size_t(kNoAllocQElems / 32) * 8;
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+
 namespace {
 
 struct Fail : std::runtime_error {
@@ -159,6 +168,8 @@ struct Ctx {
     int8_t *qrows = nullptr;
     float *qrows_s = nullptr;
     int32_t *qrows_sum = nullptr;
+    // per device index: the device address of `scratch` (hipGetSymbolAddress at init, with that device current)
+    std::array<uint8_t *, 64> noalloc{};
     // LM sampler staging: device config + state, and their pinned host copies (config, state, two state slots)
     LmCfgDev *lm_cfg_dev = nullptr;
     LmState *lm_state_dev = nullptr;
@@ -363,11 +374,27 @@ int rows_per_pass(const GpuMat &m, int64_t m_total) { return int_path(m, m_total
 // f32-activation passes of more than 4 rows run on the MFMA GEMM (the GEMV holds at most 4 f32 rows in LDS).
 bool gemm_path(const GpuMat &m, int64_t m_total, int mc) { return !int_path(m, m_total) && mc > 4; }
 
+// Device scratch of one matrix pass beyond its inputs and outputs: the split-K partial sums of the GEMM (ws_cap
+// floats at ws; the launcher splits K only as far as they fit) and the int path's once-quantized input rows
+// (q_elems int8 at q, q_elems / 32 scales and block sums; used only when the pass's rows fit).
+struct PassScratch {
+    float *ws;
+    int64_t ws_cap;
+    int8_t *q;
+    float *qs;
+    int32_t *qsum;
+    int64_t q_elems;
+};
+// The library's own scratch, allocated at init.
+PassScratch lib_scratch() { return {g.gemm_ws, kGemmWsFloats, g.qrows, g.qrows_s, g.qrows_sum, kQuantRowsElems}; }
+
 // One matrix pass: y (=, +=, swiglu) W * prologue(x) for mc rows. On the GEMM path the prologue runs as its own
-// kernel into pre ([mc][cols]; xnorm instead when the normed rows are wanted).
+// kernel into pre ([mc][cols]; xnorm instead when the normed rows are wanted). sc: the pass's scratch (null: the
+// library's).
 void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, int64_t ldx, int mc, float *y, int64_t ldy,
           const float *gamma, float eps, float *xnorm, hipStream_t s, const AttnPartials *attn = nullptr,
-          float *pre = nullptr) {
+          float *pre = nullptr, const PassScratch *scp = nullptr) {
+    const PassScratch sc = scp ? *scp : lib_scratch();
     if (pro == PRO_ATTN && (!attn || int64_t(attn->heads) * attn->hd != m.cols))
         throw Fail("attention partials do not match the o projection");
     if (gemm_path(m, m_total, mc)) {
@@ -385,7 +412,7 @@ void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, in
         }
         GemmArgs ga{};
         ga.bias = m.b; ga.y = y; ga.lda = lda; ga.ldy = ldy; ga.m = mc; ga.n = int32_t(m.rows); ga.K = int32_t(m.cols);
-        ga.ws = g.gemm_ws; ga.ws_cap = kGemmWsFloats;
+        ga.ws = sc.ws; ga.ws_cap = sc.ws_cap;
         HIPCHECK(launch_gemm(gemv_type(m), epi, m.w, m.s, A, ga, s));
         return;
     }
@@ -394,11 +421,11 @@ void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, in
     a.ldx = ldx; a.ldy = ldy; a.rows = int32_t(m.rows); a.K = int32_t(m.cols); a.m = mc; a.eps = eps;
     if (pro == PRO_ATTN) a.attn = *attn;
     const bool ip = int_path(m, m_total);
-    if (ip && mc >= kQuantRowsMin && mc <= 8 && int64_t(mc) * m.cols <= kQuantRowsElems &&
+    if (ip && mc >= kQuantRowsMin && mc <= 8 && int64_t(mc) * m.cols <= sc.q_elems &&
         (epi == EPI_STORE || epi == EPI_ACC || epi == EPI_SWIGLU)) {
         // several rows: quantize them once, then every GEMV block copies them instead of recomputing them
-        HIPCHECK(launch_quant_rows(pro, a, g.qrows, g.qrows_s, g.qrows_sum, s));
-        a.q = g.qrows; a.qs = g.qrows_s; a.qsum = g.qrows_sum;
+        HIPCHECK(launch_quant_rows(pro, a, sc.q, sc.qs, sc.qsum, s));
+        a.q = sc.q; a.qs = sc.qs; a.qsum = sc.qsum;
         HIPCHECK(launch_gemv(gemv_type(m), true, PRO_Q, epi, a, s));
         return;
     }
@@ -888,6 +915,11 @@ int voxhip_init(const char *device, char *err, size_t err_len) {
         g.qrows = dalloc_t<int8_t>(size_t(kQuantRowsElems));
         g.qrows_s = dalloc_t<float>(size_t(kQuantRowsElems / 32));
         g.qrows_sum = dalloc_t<int32_t>(size_t(kQuantRowsElems / 32));
+        if (idx >= int(g.noalloc.size())) throw Fail("device index above the scratch table");
+        void *sp = nullptr;
+        HIPCHECK(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)));
+        if (!sp || reinterpret_cast<uintptr_t>(sp) % 256) throw Fail("no device address for the no-alloc scratch");
+        g.noalloc[size_t(idx)] = static_cast<uint8_t *>(sp);
         g.name = device_label(p);
         g.ok = true;
         return 1;
@@ -971,6 +1003,32 @@ int voxhip_matmul(int mat, const float *x, int64_t m, float *y) {
             HIPCHECK(hipMemcpyAsync(pin, dy, size_t(mc) * size_t(M.rows) * 4, hipMemcpyDeviceToHost, g.stream));
             HIPCHECK(hipStreamSynchronize(g.stream));
             std::memcpy(y + c0 * M.rows, pin, size_t(mc) * size_t(M.rows) * 4);
+        }
+        return 1;
+    }, 0);
+}
+
+int voxhip_matmul_dev_noalloc(int mat, const float *d_x, int64_t m, float *d_y) {
+    return guard_int([&] {
+        require_ok();
+        const GpuMat &M = mat_at(mat);
+        if (m < 0 || (m > 0 && (!d_x || !d_y))) throw Fail("matmul_dev_noalloc: missing argument");
+        if (m == 0) return 1;
+        uint8_t *base = g.noalloc[size_t(g.dev)];
+        if (!base) throw Fail("matmul_dev_noalloc: no scratch address for this device");
+        // the fixed scratch: split-K partials, then the quantized rows, their scales and block sums
+        PassScratch sc;
+        sc.ws = reinterpret_cast<float *>(base);
+        sc.ws_cap = kNoAllocWsFloats;
+        sc.q = reinterpret_cast<int8_t *>(base + kNoAllocWsFloats * 4);
+        sc.qs = reinterpret_cast<float *>(base + kNoAllocWsFloats * 4 + kNoAllocQElems);
+        sc.qsum = reinterpret_cast<int32_t *>(base + kNoAllocWsFloats * 4 + kNoAllocQElems + (kNoAllocQElems / 32) * 4);
+        sc.q_elems = kNoAllocQElems;
+        const int chunk = rows_per_pass(M, m);
+        for (int64_t c0 = 0; c0 < m; c0 += chunk) {
+            const int mc = int(std::min<int64_t>(chunk, m - c0));
+            gemv(M, m, PRO_X, EPI_STORE, d_x + c0 * M.cols, M.cols, mc, d_y + c0 * M.rows, M.rows, nullptr, 0.f, nullptr,
+                 g.stream, nullptr, nullptr, &sc);
         }
         return 1;
     }, 0);

@@ -205,6 +205,7 @@ SIGNATURES = {
     "voxhip_mat_download": (_I, [_I, _P, _P, _P]),
     "voxhip_mat_free": (_I, [_I]),
     "voxhip_mat_gather": (_I, [_I, _P, C.c_int64, _P]),
+    "voxhip_matmul_dev_noalloc": (_I, [_I, _P, C.c_int64, _P]),
     "voxhip_xfmr_create_from_mats": (_I, [C.POINTER(XfmrDesc), _P, C.c_char_p]),
     "voxhip_seq_fill_synthetic": (_I, [_I, _I64, _U64, _U32, _F, _F]),
     "voxhip_seq_download": (_I, [_I, _I32, _I64, _P, _P]),
@@ -342,6 +343,11 @@ def mat_download(mat, wtype):
     bias = np.zeros(rows, np.float32)  # stays zero for a matrix without bias
     _check(lib().voxhip_mat_download(mat, _p(data), _p(scale), _p(bias)), "mat_download")
     return data, scale, bias
+
+
+def matmul_dev_noalloc(mat, d_x, m, d_y):
+    """matmul on device rows d_x [m][cols] -> d_y [m][rows] with the library's fixed scratch (no allocation)."""
+    _check(lib().voxhip_matmul_dev_noalloc(mat, d_x.ptr, m, d_y.ptr), "matmul_dev_noalloc")
 
 
 def mat_gather(mat, ids, cols):
