@@ -8,8 +8,9 @@ A step is one device-resident decode at position 512 (x already in HBM -> 28 lay
 sampled token in HBM), replayed as one captured HIP graph. Each step rewrites the same KV slot, so every step
 is the same work. Prints one JSON line:
   value      tokens per second (one GPU, the whole job);
-  roofline   the dominant kernel class: algorithmic bytes of one launch / its average launch duration, with
-             durations stamped by HIP events at each kernel's start and end (hipExtLaunchKernel) on its stream;
+  roofline   the dominant kernel, k_gemv_int (the step's q8 GEMVs, 113 of its 142 launches): algorithmic bytes per
+             launch / average launch duration, summed over those launches, with durations stamped by HIP events at
+             each kernel's start and end (hipExtLaunchKernel) on its stream; traffic from profiles/traffic.json;
   cpu_baseline  the reference's own CPU step (oracle/_ref, compiled from its sources) or the C restatement,
              timed on this host for a bounded number of steps.
 """
@@ -90,7 +91,9 @@ def cpu_baseline(vh, dec, seconds, x):
             po.sample_logits(lg, 0.9, 1.0, 50, 1.0, None, u)
             times.append(time.perf_counter() - t0)
     med = float(np.median(times))
-    return {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads, "kind": kind,
+    model, simd = host_cpu()
+    return {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads, "kind": kind, "cpu_model": model,
+            "simd": simd, "nproc": os.cpu_count(),
             "sample": f"{len(times)} decode steps at position {POS} (28-layer q8 talker + 3072-row q8 head + top-k 50 "
                       f"sampling, {threads} threads, median of the steps, {sum(times):.1f} s of CPU work)"}
 
@@ -344,14 +347,33 @@ def bench_pred(vh, synth, frames=20):
             "passes_per_s": round((G - 1) / (ms * 1e-3), 1)}
 
 
-def load_traffic(kernel_class):
+def load_traffic(kernel_classes, launches):
+    """Calibrated HBM bytes (FETCH_SIZE + WRITE_SIZE) per launch, averaged over the launches of kernel_classes in one
+    step, from profiles/traffic.json (the counter passes of the same benchmark); None when a class is missing."""
     p = os.path.join(ROOT, "profiles", "traffic.json")
-    if not os.path.exists(p):
-        return None
     try:
-        return json.load(open(p)).get(kernel_class)
+        t = json.load(open(p))
     except (OSError, ValueError):
         return None
+    if any(k not in t for k in kernel_classes):
+        return None
+    n = sum(launches[k] for k in kernel_classes)
+    return int(round(sum(t[k] * launches[k] for k in kernel_classes) / n)) if n else None
+
+
+def host_cpu():
+    """CPU model and the SIMD extensions the reference's kernels can use, from /proc/cpuinfo."""
+    model, flags = "unknown", set()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name") and model == "unknown":
+                model = line.split(":", 1)[1].strip()
+            elif line.startswith("flags") and not flags:
+                flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    simd = [f for f in ("sse4_2", "avx", "avx2", "fma", "f16c", "avx512f", "avx512bw", "avx512_vnni", "avx_vnni") if f in flags]
+    return model, simd
 
 
 def main():
@@ -434,14 +456,13 @@ def main():
         b = r.class_bytes[i]
         classes[name] = {"launches_per_step": n, "us_per_launch": round(ms * 1000, 3), "bytes_per_launch": int(b),
                          "GBps": round(b / (ms * 1e-3) / 1e9, 1) if ms > 0 else None}
-    # the dominant kernel: the HBM-streaming class (algorithmic bytes > 0) with the largest time per step
-    dom = max((k for k in classes if classes[k]["bytes_per_launch"] > 0),
-              key=lambda k: classes[k]["us_per_launch"] * classes[k]["launches_per_step"])
-    d = classes[dom]
-    achieved = d["GBps"]
+    # the dominant kernel: k_gemv_int, the int8 GEMV that makes 113 of the step's 142 launches (q|k|v, o, gate|up and
+    # down of every layer, and the head); its algorithmic bytes and durations are summed over those launches
     gemv = [k for k in classes if k.endswith("_gemv")]
+    gemv_launches = sum(classes[k]["launches_per_step"] for k in gemv)
     gemv_bytes = sum(classes[k]["bytes_per_launch"] * classes[k]["launches_per_step"] for k in gemv)
     gemv_us = sum(classes[k]["us_per_launch"] * classes[k]["launches_per_step"] for k in gemv)
+    achieved = round(gemv_bytes / (gemv_us * 1e-6) / 1e9, 1)
     step_bytes = dec.step_bytes(POS)
     log(json.dumps(classes))
 
@@ -477,9 +498,11 @@ def main():
                    "hidden": c["hidden"], "heads": c["heads"], "kv_heads": c["kv_heads"], "head_dim": c["head_dim"],
                    "ffn": c["inter"], "kv_len": POS, "head_rows": c["head_rows"], "batch": 1, "top_k": 50,
                    "temperature": 0.9, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(dom),
-                     "bytes_per_launch": d["bytes_per_launch"], "us_per_launch": d["us_per_launch"]},
+        "roofline": {"bound": "hbm", "kernel": "k_gemv_int (the step's q8 GEMVs: q|k|v, o, gate|up, down x 28, head)",
+                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic(gemv, {k: classes[k]["launches_per_step"] for k in gemv}),
+                     "launches_per_step": gemv_launches, "bytes_per_launch": int(gemv_bytes / gemv_launches),
+                     "us_per_launch": round(gemv_us / gemv_launches, 3)},
         "gemv": {"GBps": round(gemv_bytes / (gemv_us * 1e-6) / 1e9, 1), "frac": round(gemv_bytes / (gemv_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                  "bytes_per_step": gemv_bytes, "us_per_step": round(gemv_us, 2)},
         "step": {"bytes": step_bytes, "GBps": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),

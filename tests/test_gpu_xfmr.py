@@ -266,6 +266,31 @@ def test_decode_dev_rows_new_position(hip, oracle, wt):
         b.free()
 
 
+@pytest.mark.parametrize("wt,m", [(F16, 70), (Q8, 6), (Q8, 1)])
+def test_layer_pass_graph_replays(hip, oracle, wt, m):
+    # forward_rows runs a layer pass eagerly the first time its shape is seen, captures it the second time and replays
+    # the graph after: three identical passes over the same positions of one sequence, with other work (a pass of
+    # another shape on another sequence) between them, give identical results, equal to the oracle.
+    mdl = Model(730 + m, 2, 256, 4, 2, 128, 512, wtype=wt, head_rows=64)
+    xf, head = build(hip, mdl)
+    seq, other = hip.seq_create(xf, 128), hip.seq_create(xf, 128)
+    rng = np.random.default_rng(40 + m)
+    pre = rng.standard_normal((3, 256)).astype(np.float32)
+    hip.forward(xf, seq, 0, pre, 256)
+    kv = mdl.oracle_kv(128, kv_f16=1)
+    oracle.transformer_forward(mdl.ox, kv, pre)
+    x = rng.standard_normal((m, 256)).astype(np.float32)
+    ref = oracle.transformer_forward(mdl.ox, kv, x)
+    outs = []
+    for rep in range(3):
+        out, logits = hip.forward(xf, seq, 3, x, 256, head=head)
+        outs.append((out, logits))
+        hip.forward(xf, other, rep, rng.standard_normal((2, 256)).astype(np.float32), 256)
+    for out, logits in outs:
+        assert np.array_equal(out, outs[0][0]) and np.array_equal(logits, outs[0][1])
+    assert rel_err(outs[0][0], ref) < TOL, rel_err(outs[0][0], ref)
+
+
 def test_layer_ranges_compose(hip, oracle):
     # forward_layers over [0, 1) then [1, 2) equals the oracle's layers, teacher-forced per layer
     mdl = Model(900, 2, 256, 4, 2, 128, 512, wtype=Q8)

@@ -87,6 +87,19 @@ struct GraphKey {
     }
 };
 
+// A captured layer pass of forward_rows: the launch sequence of enqueue_layers depends on the pass's row count,
+// the caller's row count class (<= 8 rows: int8 path), the layer range, the attention form and row 0's cache view.
+struct LayersKey {
+    int mc, mt, first, count, fused, pass_attn;
+    const void *k, *v;
+    int64_t cap;
+    bool operator<(const LayersKey &o) const {
+        return std::tie(mc, mt, first, count, fused, pass_attn, k, v, cap) <
+               std::tie(o.mc, o.mt, o.first, o.count, o.fused, o.pass_attn, o.k, o.v, o.cap);
+    }
+};
+constexpr int kMaxLayerGraphs = 64;  // captured layer passes kept per transformer
+
 struct Xfmr {
     std::string name;
     int layers = 0, H = 0, heads = 0, kvh = 0, hd = 0, I = 0;
@@ -109,6 +122,9 @@ struct Xfmr {
     SampleCfgDev *scfg_dev = nullptr, *scfg_host = nullptr;
     int32_t *token_dev = nullptr;
     std::map<GraphKey, hipGraphExec_t> graphs;
+    // forward_rows' layer passes: captured on the second use of a key, replayed after
+    std::map<LayersKey, hipGraphExec_t> layer_graphs;
+    std::map<LayersKey, int> layer_uses;
     std::vector<RowRef> rows_last;
     bool rows_valid = false;
     // CosyVoice2 LM generation: config, state and decoded tokens on the device, pinned copies for the host,
@@ -436,6 +452,9 @@ void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, in
 void drop_graphs(Xfmr &X) {
     for (auto &kv : X.graphs) (void)hipGraphExecDestroy(kv.second);  // graphs captured the old buffer addresses
     X.graphs.clear();
+    for (auto &kv : X.layer_graphs) (void)hipGraphExecDestroy(kv.second);
+    X.layer_graphs.clear();
+    X.layer_uses.clear();
     for (auto &kv : X.lm_graphs) (void)hipGraphExecDestroy(kv.second);
     X.lm_graphs.clear();
     for (auto &kv : X.pred_graphs) (void)hipGraphExecDestroy(kv.second);
@@ -565,13 +584,18 @@ int kernels_per_layer(bool fused) { return fused ? 5 : 6; }
 // All layers for mc rows whose input is in X.h (row i at the position in rows_dev[i]).
 // m_total: the caller's total row count, which picks the q8 arithmetic (int8 for <= 8, f32 above).
 // fused: every row belongs to a different sequence, so the attention kernel can append K/V itself.
-void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipStream_t s, bool fused, Probe *pr = nullptr) {
-    const int qd = X.heads * X.hd, kd = X.kvh * X.hd, ldqkv = qd + 2 * kd;
-    const AttnPartials part = partials_of(X);
-    // prefill pass of consecutive rows of one sequence: attention on the matrix cores straight into the o input
+// A prefill pass of consecutive rows of one sequence takes attention on the matrix cores straight into the o input.
+bool pass_attn_of(const Xfmr &X, int mc, bool fused) {
     bool pass_attn = !fused && mc > 4 && (X.hd == 64 || X.hd == 128) && int(X.rows_last.size()) == mc;
     for (int i = 1; i < mc && pass_attn; ++i)
         pass_attn = X.rows_last[size_t(i)].k == X.rows_last[0].k && X.rows_last[size_t(i)].pos == X.rows_last[0].pos + i;
+    return pass_attn;
+}
+
+void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipStream_t s, bool fused, Probe *pr = nullptr) {
+    const int qd = X.heads * X.hd, kd = X.kvh * X.hd, ldqkv = qd + 2 * kd;
+    const AttnPartials part = partials_of(X);
+    const bool pass_attn = pass_attn_of(X, mc, fused);
     for (int li = first; li < first + count; ++li) {
         const LayerDev &L = X.L[size_t(li)];
         const GpuMat &Mqkv = g.mats[size_t(L.qkv)], &Mo = g.mats[size_t(L.o)], &Mgu = g.mats[size_t(L.gu)],
@@ -623,6 +647,40 @@ void enqueue_final(Xfmr &X, int r0, int mr, int head, hipStream_t s) {
     } else {
         HIPCHECK(launch_rmsnorm_rows(X.h + size_t(r0) * X.H, X.H, X.norms + X.final_off, X.H, X.eps, X.xnorm, X.H, mr, s));
     }
+}
+
+// enqueue_layers on the library stream for forward_rows, through a captured graph once the same pass shape has been
+// seen before. Every launch reads positions, RoPE rows and cache views from the device row table, so a graph replays
+// at any position of the same sequence; its buffers are the transformer's row scratch, whose growth drops the graphs.
+void run_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, bool fused) {
+    const RowRef &r0 = X.rows_last.at(0);
+    const LayersKey key{mc, int(std::min<int64_t>(m_total, kMaxM + 1)), first, count, fused ? 1 : 0,
+                        pass_attn_of(X, mc, fused) ? 1 : 0, r0.k, r0.v, r0.cap};
+    auto it = X.layer_graphs.find(key);
+    if (it != X.layer_graphs.end()) {
+        HIPCHECK(hipGraphLaunch(it->second, g.stream));
+        return;
+    }
+    if (++X.layer_uses[key] < 2 || int(X.layer_graphs.size()) >= kMaxLayerGraphs) {  // one-off shapes run eagerly
+        enqueue_layers(X, mc, m_total, first, count, g.stream, fused);
+        return;
+    }
+    hipGraph_t graph = nullptr;
+    HIPCHECK(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal));
+    try {
+        enqueue_layers(X, mc, m_total, first, count, g.stream, fused);
+    } catch (...) {
+        (void)hipStreamEndCapture(g.stream, &graph);
+        if (graph) (void)hipGraphDestroy(graph);
+        throw;
+    }
+    HIPCHECK(hipStreamEndCapture(g.stream, &graph));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    HIPCHECK(e);
+    X.layer_graphs[key] = exec;
+    HIPCHECK(hipGraphLaunch(exec, g.stream));
 }
 
 RowRef row_of(const Seq &S, int64_t pos) {
@@ -677,7 +735,7 @@ int forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_proj
         for (int i = 0; i < mc && fused; ++i)
             for (int j = 0; j < i; ++j)
                 if (rr[size_t(i)].k == rr[size_t(j)].k) { fused = false; break; }
-        enqueue_layers(X, mc, m_total, first_layer, n_layers, g.stream, fused);
+        run_layers(X, mc, m_total, first_layer, n_layers, fused);
         if (hidden_out) {
             HIPCHECK(hipMemcpyAsync(pin, X.h, size_t(mc * H) * 4, hipMemcpyDeviceToHost, g.stream));
             HIPCHECK(hipStreamSynchronize(g.stream));
