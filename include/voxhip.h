@@ -110,6 +110,13 @@ int voxhip_matmul_dev_noalloc(int mat, const float *d_x, int64_t m, float *d_y);
 int voxhip_mat_gather(int mat, const int32_t *ids, int64_t n, float *out);
 /* Rows and cols of a device matrix (0 on a bad handle). */
 int voxhip_mat_shape(int mat, int64_t *rows, int64_t *cols);
+/* nn::ConvT::forward (nn.cpp:217-245; ConvTranspose1d, groups 1) on the device: `mat` holds the transposed conv's
+ * weights as ConvT::load lays them out (nn.cpp:205-215), K cout rows of cin (row k cout + o; the reference's ConvT
+ * matrix is F32, any uploaded type is accepted) and no bias. x [T][cin] (host) -> y [To][cout] (host),
+ * To = (T - 1) stride - 2 pad + K + out_pad; bias [cout] or NULL is added after the overlap-add. 1 on success, 0 on
+ * error (voxhip_last_error). */
+int voxhip_convt(int mat, int32_t K, int32_t stride, int32_t pad, int32_t out_pad, const float *bias, const float *x, int32_t T,
+                 float *y);
 
 /* ---------------------------------------------------------------- transformer */
 /* vox::LayerW (kernels.hpp:114-119). attn_scale / mlp_scale must be NULL (as gpu_vulkan.cpp:782). */
@@ -120,8 +127,8 @@ typedef struct voxhip_layer {
     const float *attn_scale, *mlp_scale;
 } voxhip_layer;
 
-/* vox::TransformerW (kernels.hpp:120-130). window must be 0 (as gpu_vulkan.cpp:770); head_dim 64 or 128
- * (the reference accepts any even head_dim <= 128; other sizes return -1 here and stay on the CPU);
+/* vox::TransformerW (kernels.hpp:120-130). window must be 0 and head_dim even and <= 128 (as gpu_vulkan.cpp:770;
+ * 64 and 128 run the split-K decode and MFMA prefill attention, other sizes a one-block-per-head kernel);
  * heads / kv_heads <= 8. inv_freq: [head_dim/2], as rope_inv_freq (kernels.cpp:734-738). */
 typedef struct voxhip_xfmr_desc {
     int32_t n_layers;

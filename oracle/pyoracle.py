@@ -151,6 +151,7 @@ def _declare(lib, prefix):
             "softmax_fast": (None, [P, I64]),
             "attention_nn": (None, [P, P, P, I32, I32, I32, I32, F, P]),
             "causal_conv": (None, [P, P, I32, P]),
+            "convt": (I32, [P, I32, I32, I32, I32, I32, I32, P, P, I32, P]),
             "cosy_step": (C.c_int, [P, I32, P, P, P]),
             "snake_params": (None, [P, P, I64, P, P]),
             "codec_state_new": (P, [P, I64]),
@@ -188,6 +189,7 @@ def _declare(lib, prefix):
             "layer_norm_nn": (None, [P, I32, I32, P, P, F]),
             "attention_nn": (None, [P, P, P, I32, I32, I32, I32, F, P]),
             "causal_conv": (None, [P, P, I32, P]),
+            "convt": (I32, [P, I32, I32, I32, I32, I32, I32, P, P, I32, P]),
             "cosy_step": (C.c_int, [P, I32, P, P, P]),
             "tmod_write": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int, P, P, P, P, P, P]),
             "codec_open": (P, [C.c_char_p]),
@@ -335,6 +337,23 @@ def conv1d(cv, x, use_ref=False, w_pt=None):
         ref().ref_conv1d(_p(np.ascontiguousarray(w_pt, np.float32)), cv.cin, cv.cout, cv.K, cv.groups, _p(cv.b), _p(x), T, _p(y))
     else:
         lib().vo_conv1d(C.byref(cv.c), _p(x), T, _p(y))
+    return y
+
+
+def convt(w_pt, bias, x, stride, pad, out_pad=0, use_ref=False):
+    """nn::ConvT (nn.cpp:205-245) of x [T][cin] with PyTorch's ConvTranspose1d weight [cin][cout][K] and bias [cout]
+    (or None): y [(T - 1) stride - 2 pad + K + out_pad][cout]. use_ref runs the compiled reference instead."""
+    w_pt = np.ascontiguousarray(w_pt, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    cin, cout, K = w_pt.shape
+    T = x.shape[0]
+    To = (T - 1) * stride - 2 * pad + K + out_pad
+    y = np.empty((max(To, 1), cout), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    fn = ref().ref_convt if use_ref else lib().vo_convt
+    n = fn(_p(w_pt), cin, cout, K, stride, pad, out_pad, _p(b) if b is not None else None, _p(x), T, _p(y))
+    if n != To:
+        raise ValueError(f"convt: bad arguments (output length {n})")
     return y
 
 

@@ -104,6 +104,25 @@ void ref_conv1d(const float *w, int cin, int cout, int K, int groups, const floa
     c.load(w, cin, cout, K, groups, bias);
     c.forward(x, T, y);
 }
+// nn::ConvT with its members set as ConvT::load sets them (nn.cpp:205-215) from PyTorch's weight [cin][cout][K],
+// then ConvT::forward (nn.cpp:217-245); returns the output length.
+int32_t ref_convt(const float *w_pt, int cin, int cout, int K, int stride, int pad, int out_pad, const float *bias,
+                  const float *x, int T, float *y) {
+    nn::ConvT c;
+    c.cin = cin; c.cout = cout; c.K = K; c.stride = stride; c.pad = pad; c.out_pad = out_pad;
+    c.w.resize(size_t(cin) * size_t(cout) * size_t(K));
+    for (int ci = 0; ci < cin; ++ci)
+        for (int o = 0; o < cout; ++o)
+            for (int k = 0; k < K; ++k)
+                c.w[(size_t(k) * size_t(cout) + size_t(o)) * size_t(cin) + size_t(ci)] =
+                    w_pt[(size_t(ci) * size_t(cout) + size_t(o)) * size_t(K) + size_t(k)];
+    if (bias) c.b.assign(bias, bias + cout);
+    c.m.type = WType::F32; c.m.data = reinterpret_cast<const uint8_t *>(c.w.data()); c.m.rows = int64_t(K) * cout; c.m.cols = cin;
+    std::vector<float> out;
+    c.forward(x, T, out);
+    std::memcpy(y, out.data(), out.size() * 4);
+    return int32_t(out.size() / size_t(cout));
+}
 float ref_gelu_erf(float x) { return gelu_erf(x); }
 void ref_set_threads(int n) { set_num_threads(n); }
 void ref_philox(const uint32_t c[4], const uint32_t k[2], uint32_t out[4]) {

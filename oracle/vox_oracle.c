@@ -996,6 +996,45 @@ void vo_causal_conv(const vo_conv *c, const float *x, int32_t T, float *y) {
     free(col);
 }
 
+int32_t vo_convt(const float *w_pt, int32_t cin, int32_t cout, int32_t K, int32_t stride, int32_t pad, int32_t out_pad,
+                 const float *bias, const float *x, int32_t T, float *y) {
+    if (cin < 1 || cout < 1 || K < 1 || stride < 1 || pad < 0 || out_pad < 0 || T < 1) return -1;
+    const int64_t To = (int64_t)(T - 1) * stride - 2 * (int64_t)pad + K + out_pad;
+    if (To < 1) return -1;
+    const int64_t KO = (int64_t)K * cout;
+    float *w = (float *)malloc(sizeof(float) * (size_t)(KO * cin));
+    if (!w) return -1;
+    for (int c = 0; c < cin; ++c) /* ConvT::load (nn.cpp:205-215) */
+        for (int o = 0; o < cout; ++o)
+            for (int k = 0; k < K; ++k) w[((int64_t)k * cout + o) * cin + c] = w_pt[((int64_t)c * cout + o) * K + k];
+    const vo_mat W = {VO_F32, w, NULL, KO, cin, NULL};
+    int64_t blk = ((int64_t)4 << 20) / KO; /* ConvT::forward (nn.cpp:217-245) */
+    if (blk < 16) blk = 16;
+    float *z = (float *)malloc(sizeof(float) * (size_t)((blk < T ? blk : T) * KO));
+    if (!z) { free(w); return -1; }
+    memset(y, 0, sizeof(float) * (size_t)(To * cout));
+    for (int64_t t0 = 0; t0 < T; t0 += blk) {
+        const int64_t n = blk < T - t0 ? blk : T - t0;
+        vo_matmul(&W, x + t0 * cin, n, z, 1);
+        for (int64_t i = 0; i < n; ++i) {
+            const int64_t t = t0 + i;
+            for (int k = 0; k < K; ++k) {
+                const int64_t to = t * stride + k - pad;
+                if (to < 0 || to >= To) continue;
+                const float *zr = z + i * KO + (int64_t)k * cout;
+                float *yr = y + to * cout;
+                for (int o = 0; o < cout; ++o) yr[o] += zr[o];
+            }
+        }
+    }
+    if (bias)
+        for (int64_t t = 0; t < To; ++t)
+            for (int o = 0; o < cout; ++o) y[t * cout + o] += bias[o];
+    free(z);
+    free(w);
+    return (int32_t)To;
+}
+
 /* causal_conv_b (cosyvoice.cpp:134-144): per sequence of T rows */
 static void cosy_conv_b(const vo_conv *c, const float *x, int32_t T, float *y) {
     for (int b = 0; b < 2; ++b) vo_causal_conv(c, x + (int64_t)b * T * c->cin, T, y + (int64_t)b * T * c->cout);

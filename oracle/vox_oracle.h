@@ -189,6 +189,12 @@ void vo_attention_nn(const float *q, const float *k, const float *v, int32_t Tq,
 /* causal_conv (cosyvoice.cpp:127-131): Conv::forward (nn.cpp:179-202, groups 1, w [cout][K][cin]) of x [T][cin]
  * with K - 1 zero rows in front, bias added after the product (nn.cpp:146-155). K 1: the plain linear. */
 void vo_causal_conv(const vo_conv *c, const float *x, int32_t T, float *y);
+/* nn::ConvT, ConvTranspose1d with groups 1 (nn.cpp:205-245): w_pt in PyTorch's layout [cin][cout][K] is laid out as
+ * rows k cout + o of cin (ConvT::load), z = x W^T through the F32 matmul in blocks of max(16, 4 Mi / (K cout)) input
+ * rows, then y[t s + k - pad] += z[t][k][o] in the order t, k for 0 <= t s + k - pad < To, and the bias last.
+ * x [T][cin] -> y [To][cout], To = (T - 1) s - 2 pad + K + out_pad; returns To (or -1 on bad arguments). */
+int32_t vo_convt(const float *w_pt, int32_t cin, int32_t cout, int32_t K, int32_t stride, int32_t pad, int32_t out_pad,
+                 const float *bias, const float *x, int32_t T, float *y);
 typedef struct {
     vo_conv c1, c2, res;
     const float *n1w, *n1b, *n2w, *n2b;

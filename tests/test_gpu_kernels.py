@@ -97,6 +97,54 @@ def test_matmul_gemm_rows(hip, oracle, wt, rows, cols):
         assert rel_err(y, r) < GEMV_TOL, (wt, rows, cols, m, rel_err(y, r))
 
 
+# (cin, cout, K, stride, pad, out_pad, T, bias): HiFT's three upsample stages (CosyVoice2: rates 8 / 5 / 3, kernels
+# 16 / 11 / 7, channels 512 -> 64) at 640 and 1200 frames (the GEMM over two and three 512-frame passes), Kokoro's
+# first stage (rate 10, kernel 20), output padding, K < stride, pad >= K / 2, one frame and a GEMV-sized product
+CONVT_GPU_CASES = [(512, 256, 16, 8, 4, 0, 80, True), (256, 128, 11, 5, 3, 0, 640, True), (128, 64, 7, 3, 2, 0, 1200, True),
+                   (512, 256, 20, 10, 5, 0, 50, True), (64, 48, 5, 2, 2, 1, 33, False), (32, 16, 4, 3, 1, 2, 17, True),
+                   (16, 8, 3, 5, 0, 0, 9, True), (8, 8, 4, 1, 3, 0, 12, True), (40, 24, 6, 3, 1, 0, 1, True),
+                   (96, 64, 8, 4, 2, 0, 3, True)]
+
+
+@pytest.mark.parametrize("cin,cout,K,s,pad,op,T,bias", CONVT_GPU_CASES)
+def test_convt_parity(hip, oracle, cin, cout, K, s, pad, op, T, bias):
+    # nn::ConvT (nn.cpp:205-245): the F32 product on the device (GEMV up to 4 frames, MFMA GEMM above) and the padded
+    # overlap-add in the reference's order, against the oracle's restatement at the GEMV bar
+    rng = np.random.default_rng(cin + 3 * K + 11 * T)
+    w = (rng.standard_normal((cin, cout, K)) * (1.0 / np.sqrt(cin))).astype(np.float32)
+    b = rng.standard_normal(cout).astype(np.float32) if bias else None
+    x = rng.standard_normal((T, cin)).astype(np.float32)
+    ct = hip.ConvT().load(w, b, s, pad, op)
+    try:
+        y = ct.forward(x)
+        want = oracle.convt(w, b, x, s, pad, op)
+        assert y.shape == want.shape == (ct.out_len(T), cout)
+        assert rel_err(y, want) < GEMV_TOL, rel_err(y, want)
+    finally:
+        hip.mat_free(ct.mat)
+
+
+def test_convt_rejects_bad_calls(hip):
+    rng = np.random.default_rng(3)
+    w = rng.standard_normal((8, 4, 3)).astype(np.float32)
+    ct = hip.ConvT().load(w, None, 2, 0)
+    try:
+        x = rng.standard_normal((1, 8)).astype(np.float32)
+        with pytest.raises(hip.VoxHipError, match="no output frames"):
+            hip.convt(ct.mat, 3, 1, 3, 0, None, x)
+        with pytest.raises(hip.VoxHipError, match="K cout"):
+            hip.convt(ct.mat, 5, 2, 0, 0, None, x)
+    finally:
+        hip.mat_free(ct.mat)
+    withb = hip.upload(hip.HostMat(F32, rng.standard_normal((12, 8)).astype(np.float32), 12, 8, None,
+                                   np.ones(12, np.float32)))
+    try:
+        with pytest.raises(hip.VoxHipError, match="bias"):
+            hip.convt(withb, 3, 2, 0, 0, None, rng.standard_normal((4, 8)).astype(np.float32))
+    finally:
+        hip.mat_free(withb)
+
+
 @pytest.mark.parametrize("rows,cols", [(4096, 2048), (2048, 6144), (37, 160)])
 def test_q4_f16_scales(hip, oracle, rows, cols):
     # Q4 scales that are exact in f16 are stored in 2 bytes on the device (the cfg 3 "4-bit + f16 scale" format):

@@ -291,6 +291,47 @@ def test_layer_pass_graph_replays(hip, oracle, wt, m):
     assert rel_err(outs[0][0], ref) < TOL, rel_err(outs[0][0], ref)
 
 
+# head_dim other than 64 / 128 (the reference's device path takes any even head_dim <= 128, gpu_vulkan.cpp:770):
+# (wtype, heads, kv_heads, head_dim, qk_norm); the q|k|v and o widths satisfy the matrix column rules
+@pytest.mark.parametrize("wt,heads,kvh,hd,qkn", [(Q8, 4, 2, 96, True), (BF16, 4, 1, 80, True), (F16, 4, 2, 34, False),
+                                                  (F32, 4, 4, 2, True), (Q8, 8, 2, 32, True)])
+def test_any_head_dim(hip, oracle, wt, heads, kvh, hd, qkn):
+    # prefill of 9 rows, host-pointer decode steps, a captured device decode step replayed at new positions, and two
+    # sessions in one step, all against the oracle continuing the same sequences
+    mdl = Model(740 + hd, 2, 256, heads, kvh, hd, 512, wtype=wt, qk_norm=qkn, head_rows=96)
+    xf, head = build(hip, mdl)
+    seq, seq2 = hip.seq_create(xf, 64), hip.seq_create(xf, 64)
+    kv, kv2 = mdl.oracle_kv(64, 1), mdl.oracle_kv(64, 1)
+    rng = np.random.default_rng(hd)
+    x = rng.standard_normal((9, 256)).astype(np.float32)
+    out, logits = hip.forward(xf, seq, 0, x, 256, head=head)
+    ref = oracle.transformer_forward(mdl.ox, kv, x)
+    assert rel_err(out, ref) < TOL, rel_err(out, ref)
+    assert rel_err(logits, oracle_head(oracle, mdl, out)) < TOL
+    for step in range(2):
+        x = rng.standard_normal((1, 256)).astype(np.float32)
+        out, _ = hip.forward(xf, seq, 9 + step, x, 256, head=head)
+        assert rel_err(out, oracle.transformer_forward(mdl.ox, kv, x)) < TOL, step
+    dx, dout, dlog = hip.DevBuf(256 * 4), hip.DevBuf(256 * 4), hip.DevBuf(96 * 4)
+    for pos in (11, 12, 13):
+        x = rng.standard_normal((1, 256)).astype(np.float32)
+        dx.upload(x)
+        hip.decode_dev(xf, seq, pos, dx, 1, dout, head, dlog)
+        hip.sync()
+        out = dout.download(256, np.float32)
+        ref = oracle.transformer_forward(mdl.ox, kv, x)
+        assert rel_err(out, ref) < TOL, (pos, rel_err(out, ref))
+        assert rel_err(dlog.download(96, np.float32), oracle_head(oracle, mdl, out)) < TOL, pos
+    for b in (dx, dout, dlog):
+        b.free()
+    pre = rng.standard_normal((5, 256)).astype(np.float32)
+    hip.forward(xf, seq2, 0, pre, 256)
+    oracle.transformer_forward(mdl.ox, kv2, pre)
+    x2 = rng.standard_normal((2, 256)).astype(np.float32)
+    out2, _ = hip.forward_steps(xf, [seq, seq2], [14, 5], x2, 256, head=head)
+    assert rel_err(out2, oracle.transformer_forward_steps(mdl.ox, [kv, kv2], x2)) < TOL
+
+
 def test_layer_ranges_compose(hip, oracle):
     # forward_layers over [0, 1) then [1, 2) equals the oracle's layers, teacher-forced per layer
     mdl = Model(900, 2, 256, 4, 2, 128, 512, wtype=Q8)

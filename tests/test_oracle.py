@@ -248,6 +248,48 @@ def test_conv1d_matches_reference_and_brute_force(oracle):
         assert np.max(np.abs(y - want)) < 1e-5
 
 
+def convt_brute(w, b, x, s, pad, out_pad):
+    """ConvTranspose1d in float64 from its definition: y[t s + k - pad][o] += sum_i x[t][i] w[i][o][k], kept where
+    0 <= t s + k - pad < To, plus the bias."""
+    cin, cout, K = w.shape
+    T = x.shape[0]
+    To = (T - 1) * s - 2 * pad + K + out_pad
+    y = np.zeros((To, cout)) + (0 if b is None else b.astype(np.float64))
+    x64, w64 = x.astype(np.float64), w.astype(np.float64)
+    for t in range(T):
+        for k in range(K):
+            r = t * s + k - pad
+            if 0 <= r < To:
+                y[r] += x64[t] @ w64[:, :, k]
+    return y
+
+
+# (cin, cout, K, stride, pad, out_pad, T, bias): HiFT's and Kokoro's upsample stages (pad (K - stride) / 2), output
+# padding, K < stride (frames that no tap reaches carry only the bias), pad >= K / 2, one frame, and 300 frames at
+# K cout = 14336 (the reference's 292-frame product blocks, so two blocks)
+CONVT_CASES = [(64, 32, 16, 8, 4, 0, 12, True), (48, 24, 11, 5, 3, 0, 9, True), (40, 20, 20, 10, 5, 0, 6, True),
+               (24, 16, 5, 2, 2, 1, 13, False), (16, 8, 4, 3, 1, 2, 7, True), (16, 8, 3, 5, 0, 0, 9, True),
+               (8, 8, 4, 1, 3, 0, 12, True), (20, 12, 6, 3, 1, 0, 1, True), (12, 1024, 14, 7, 3, 0, 300, True)]
+
+
+@pytest.mark.parametrize("cin,cout,K,s,pad,op,T,bias", CONVT_CASES)
+def test_convt_matches_reference_and_brute_force(oracle, cin, cout, K, s, pad, op, T, bias):
+    # nn::ConvT (nn.cpp:205-245): bit-exact against the compiled reference's ConvT::forward, and within float rounding
+    # of the float64 definition
+    rng = np.random.default_rng(cin * 31 + K * 7 + T)
+    w = (rng.standard_normal((cin, cout, K)) * 0.2).astype(np.float32)
+    b = rng.standard_normal(cout).astype(np.float32) if bias else None
+    x = rng.standard_normal((T, cin)).astype(np.float32)
+    y = po.convt(w, b, x, s, pad, op)
+    want = convt_brute(w, b, x, s, pad, op)
+    assert y.shape == want.shape
+    assert np.max(np.abs(y - want)) < 1e-5 * max(1.0, np.abs(want).max())
+    if po.ref() is not None:
+        assert np.array_equal(y.view(np.uint32), po.convt(w, b, x, s, pad, op, use_ref=True).view(np.uint32))
+    with pytest.raises(ValueError):
+        po.convt(w, b, x[:1], 1, K + 1, 0)  # no output frames
+
+
 def test_f5_modulate_closed_form(oracle):
     # f5.cpp:608-625: LayerNorm without parameters (double statistics, eps 1e-6) then x * (1 + scale) + shift
     rng = np.random.default_rng(22)

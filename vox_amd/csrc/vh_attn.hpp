@@ -57,6 +57,49 @@ __global__ __launch_bounds__(64) void k_qk_post(QkArgs a) {
     }
 }
 
+// Attention for the head sizes the split-K and MFMA kernels are not built for (any even hd <= 128): grid (heads, m),
+// block 256. Lane l of each wave holds dims l and l + 64; wave w takes keys w, w + 4, ... of the row's cache with an
+// online softmax (score = scale * q.k, as kernels.cpp:818-819), and the four waves are merged through LDS.
+__global__ __launch_bounds__(256) void k_attn_rows(AttnRowsArgs a) {
+    const int h = blockIdx.x, i = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int hd = a.hd, qd = a.heads * hd, g = h / (a.heads / a.kv_heads);
+    const RowRef rr = a.rows[i];
+    const float *q = a.q + int64_t(i) * qd + h * hd;
+    const int d0 = lane, d1 = lane + 64;
+    const bool on0 = d0 < hd, on1 = d1 < hd;
+    const float q0 = on0 ? q[d0] : 0.f, q1 = on1 ? q[d1] : 0.f;
+    const int64_t plane = ((int64_t(a.layer) * a.kv_heads + g) * rr.cap) * hd;
+    const _Float16 *K = rr.k + plane, *V = rr.v + plane;
+    const int64_t n = rr.pos + 1;
+    float mx = -INFINITY, l = 0.f, o0 = 0.f, o1 = 0.f;
+    for (int64_t j = w; j < n; j += 4) {
+        const _Float16 *kr = K + j * hd, *vr = V + j * hd;
+        const float k0 = on0 ? float(kr[d0]) : 0.f, k1 = on1 ? float(kr[d1]) : 0.f;
+        const float v0 = on0 ? float(vr[d0]) : 0.f, v1 = on1 ? float(vr[d1]) : 0.f;
+        const float sc = a.scale * wave_sum(q0 * k0 + q1 * k1);
+        const float mn = fmaxf(mx, sc), corr = expf(mx - mn), p = expf(sc - mn);
+        o0 = o0 * corr + p * v0;
+        o1 = o1 * corr + p * v1;
+        l = l * corr + p;
+        mx = mn;
+    }
+    __shared__ float sm_m[4], sm_l[4], sm_o[4][128];
+    if (lane == 0) { sm_m[w] = mx; sm_l[w] = l; }
+    sm_o[w][d0] = o0;
+    sm_o[w][d1] = o1;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(sm_m[0], sm_m[1]), fmaxf(sm_m[2], sm_m[3]));  // wave 0 holds key 0: finite
+    float e[4], L = 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) { e[u] = expf(sm_m[u] - M); L += sm_l[u] * e[u]; }
+    for (int d = threadIdx.x; d < hd; d += 256) {
+        float O = 0.f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) O += sm_o[u][d] * e[u];
+        a.out[int64_t(i) * qd + h * hd + d] = O / L;
+    }
+}
+
 // One rotate-half pair of a head: optional RMSNorm over the head (the HALF lanes of a group hold its pairs),
 // then RoPE. Rounding as rope_apply: products and the difference/sum each rounded (no contraction).
 template <int HALF>

@@ -35,6 +35,14 @@ hipError_t launch_ola(const float *tmp, const float *tail_old, float *tail_new, 
                   int32_t(T), int32_t(stride), int32_t(K), int32_t(co));
 }
 
+hipError_t launch_convt_gather(const float *z, const float *bias, float *y, int T, int To, int stride, int K, int pad, int co,
+                               hipStream_t s) {
+    if (T <= 0 || To <= 0) return hipSuccess;
+    if (stride <= 0 || K <= 0 || pad < 0 || co <= 0 || !z || !y) return hipErrorInvalidValue;
+    return launch(k_convt_gather, blocks_of(int64_t(To) * co), dim3(256), 0, s, z, bias, y, int32_t(T), int32_t(To),
+                  int32_t(stride), int32_t(K), int32_t(pad), int32_t(co));
+}
+
 hipError_t launch_codec_rope_ring(float *qkv, int ld, int F, int heads, int kvh, int hd, const float *rope, float *ring_k,
                                   float *ring_v, int R, const int64_t *pos, hipStream_t s) {
     if (F <= 0) return hipSuccess;

@@ -66,6 +66,25 @@ __global__ __launch_bounds__(256) void k_ola(const float *__restrict__ tmp, cons
     else tail_new[(p - int64_t(T) * s) * co + o] = v;
 }
 
+// nn::ConvT's overlap-add with padding (nn.cpp:217-245) in gather form, from the GEMM output z [T][K co] (row k co + o
+// of input frame t): output row r of To takes z[t][r + pad - t s] for every frame t with 0 <= r + pad - t s < K, summed
+// in increasing t (the order the reference adds them in), then the bias (or nothing). One thread per output element.
+__global__ __launch_bounds__(256) void k_convt_gather(const float *__restrict__ z, const float *__restrict__ bias,
+                                                      float *__restrict__ y, int32_t T, int32_t To, int32_t s, int32_t K,
+                                                      int32_t pad, int32_t co) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= int64_t(To) * co) return;
+    const int64_t r = i / co;
+    const int o = int(i - r * co);
+    const int64_t q = r + pad;
+    const int64_t lo_num = q - K + 1;
+    const int64_t t_lo = lo_num <= 0 ? 0 : (lo_num + s - 1) / s;
+    const int64_t t_hi = min(int64_t(T) - 1, q / s);
+    float v = 0.f;
+    for (int64_t t = t_lo; t <= t_hi; ++t) v += z[(t * K + (q - t * s)) * co + o];
+    y[i] = bias ? v + bias[o] : v;
+}
+
 // The pre-transformer's q / k rotation (rope_apply, kernels.cpp:740-757: pairs (d, d + hd / 2)) with the host table
 // rope [F][hd / 2][2] of positions pos0 + i, and the append of row i's keys and values to ring slot (pos0 + i) % R of
 // the layer's f32 ring [R][kv_heads hd]. grid F, block 256; qkv rows [F][ld] = q | k | v; the call's first position

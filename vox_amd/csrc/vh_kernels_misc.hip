@@ -131,6 +131,13 @@ hipError_t launch_prefill_attn(const PrefillAttnArgs &a, int hd, hipStream_t s) 
     return hipErrorInvalidValue;
 }
 
+hipError_t launch_attn_rows(const AttnRowsArgs &a, int m, hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    if (a.hd <= 0 || a.hd > 128 || a.hd % 2 || a.kv_heads <= 0 || a.heads % a.kv_heads || !a.q || !a.out || !a.rows)
+        return hipErrorInvalidValue;
+    return launch(k_attn_rows, dim3(unsigned(a.heads), unsigned(m)), dim3(256), 0, s, a);
+}
+
 hipError_t launch_sample(const SampleCfgDev *cfg, const float *logits, int n, int32_t *out, hipStream_t s, int rows) {
     if (n <= 0 || n > kSampleMaxN || rows <= 0) return hipErrorInvalidValue;
     const size_t smem = sample_smem_bytes(n);

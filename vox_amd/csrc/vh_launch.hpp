@@ -62,6 +62,8 @@ hipError_t launch_fill_cache(void *c, int64_t planes, int64_t cap, int64_t len, 
                              float mean, float std, hipStream_t s);
 
 hipError_t launch_copy16(const void *src, void *dst, int64_t bytes, hipStream_t s);
+// Attention one block per (head, row) for any even head_dim <= 128 (q from k_qk_post, keys from each row's cache).
+hipError_t launch_attn_rows(const AttnRowsArgs &a, int m, hipStream_t s);
 // Causal attention of a prefill pass (consecutive rows of one sequence) on the matrix cores, head_dim 64 or 128.
 hipError_t launch_prefill_attn(const PrefillAttnArgs &a, int hd, hipStream_t s);
 // F5-TTS DiT step: AdaLN modulation of R rows of D, the step input's x columns, attention (head_dim 64).
@@ -85,6 +87,9 @@ hipError_t launch_dwconv_causal(const float *x, const float *hist, const float *
                                 hipStream_t s);
 hipError_t launch_ola(const float *tmp, const float *tail_old, float *tail_new, const float *bias, float *y, int T, int stride,
                       int K, int co, hipStream_t s);
+// nn::ConvT's padded overlap-add (gather form) from the GEMM output z [T][K co] to y [To][co] (+ bias when not null).
+hipError_t launch_convt_gather(const float *z, const float *bias, float *y, int T, int To, int stride, int K, int pad, int co,
+                               hipStream_t s);
 hipError_t launch_codec_rope_ring(float *qkv, int ld, int F, int heads, int kvh, int hd, const float *rope, float *ring_k,
                                   float *ring_v, int R, const int64_t *pos, hipStream_t s);
 hipError_t launch_codec_attn(const float *qkv, int ld, const float *ring_k, const float *ring_v, int R, int F, int heads, int kvh,

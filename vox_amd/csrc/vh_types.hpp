@@ -99,6 +99,16 @@ struct PrefillAttnArgs {
     float scale;
 };
 
+// Attention of m rows, one block per (head, row), for any even head_dim <= 128: q [m][heads hd] already normed and
+// rotated (k_qk_post), each row over keys 0 .. rows[i].pos of its own cache, output [m][heads hd] normalized.
+struct AttnRowsArgs {
+    const float *q;
+    float *out;
+    const RowRef *rows;
+    int32_t heads, kv_heads, hd, layer;
+    float scale;
+};
+
 struct SampleCfgDev {
     float temperature, top_p, rep;
     int32_t top_k;

@@ -168,8 +168,8 @@ struct Ctx {
     // staging for host-pointer entry points
     float *pin = nullptr;
     size_t pin_bytes = 0;
-    float *dbuf_x = nullptr, *dbuf_y = nullptr;
-    size_t dbuf_x_bytes = 0, dbuf_y_bytes = 0;
+    float *dbuf_x = nullptr, *dbuf_y = nullptr, *dbuf_z = nullptr;
+    size_t dbuf_x_bytes = 0, dbuf_y_bytes = 0, dbuf_z_bytes = 0;
     // sampler staging for voxhip_sample_logits
     SampleCfgDev *scfg_dev = nullptr, *scfg_host = nullptr;
     int32_t *hist_dev = nullptr, *tok_dev = nullptr;
@@ -592,9 +592,14 @@ bool pass_attn_of(const Xfmr &X, int mc, bool fused) {
     return pass_attn;
 }
 
+// Head sizes other than 64 and 128 take k_qk_post, then k_attn_rows into X.pre, then the o GEMV on those rows.
+bool any_hd(const Xfmr &X) { return X.hd != 64 && X.hd != 128; }
+
 void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipStream_t s, bool fused, Probe *pr = nullptr) {
     const int qd = X.heads * X.hd, kd = X.kvh * X.hd, ldqkv = qd + 2 * kd;
     const AttnPartials part = partials_of(X);
+    const bool rows_attn = any_hd(X);
+    if (rows_attn) fused = false;
     const bool pass_attn = pass_attn_of(X, mc, fused);
     for (int li = first; li < first + count; ++li) {
         const LayerDev &L = X.L[size_t(li)];
@@ -611,7 +616,13 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
             probed(pr, VOXHIP_K_QKPOST, [&] { HIPCHECK(launch_qk_post(qa, mc, s)); });
         }
         const RowRef &r0 = X.rows_last.at(0);
-        if (pass_attn && gemm_path(Mo, m_total, mc)) {
+        if (rows_attn) {
+            AttnRowsArgs ra{};
+            ra.q = X.q; ra.out = X.pre; ra.rows = X.rows_dev; ra.heads = X.heads; ra.kv_heads = X.kvh; ra.hd = X.hd;
+            ra.layer = li; ra.scale = 1.0f / std::sqrt(float(X.hd));
+            probed(pr, VOXHIP_K_ATTN, [&] { HIPCHECK(launch_attn_rows(ra, mc, s)); });
+            probed(pr, VOXHIP_K_O, [&] { gemv(Mo, m_total, PRO_X, EPI_ACC, X.pre, qd, mc, X.h, X.H, nullptr, 0.f, nullptr, s); });
+        } else if (pass_attn && gemm_path(Mo, m_total, mc)) {
             PrefillAttnArgs pa{};
             pa.q = X.q; pa.k = r0.k; pa.v = r0.v; pa.out = X.pre; pa.rows = X.rows_dev; pa.cap = r0.cap; pa.pos0 = r0.pos;
             pa.m = mc;
@@ -789,7 +800,7 @@ int make_xfmr(const voxhip_xfmr_desc *w, const char *name, int use_layers, const
     require_ok();
     if (!w || w->n_layers <= 0 || !w->layers || !w->final_norm || !w->inv_freq) throw Fail("incomplete transformer description");
     if (w->window != 0 && !codec) throw Fail("sliding-window attention is not supported on the device");
-    if (w->head_dim != 64 && w->head_dim != 128 && !codec) throw Fail("head_dim must be 64 or 128 on this backend");
+    if (w->head_dim <= 0 || w->head_dim > 128 || w->head_dim % 2) throw Fail("head_dim must be even and at most 128");
     if (w->heads <= 0 || w->kv_heads <= 0 || w->heads % w->kv_heads || w->heads / w->kv_heads > 8)
         throw Fail("heads / kv_heads must be an integer group of at most 8");
     if (w->hidden % 32 || w->inter % 32) throw Fail("hidden and inter must be multiples of 32");
@@ -1113,6 +1124,43 @@ int voxhip_mat_gather(int mat, const int32_t *ids, int64_t n, float *out) {
             HIPCHECK(hipStreamSynchronize(g.stream));
             std::memcpy(out + c0 * M.cols, pin, size_t(nc) * size_t(M.cols) * 4);
         }
+        return 1;
+    }, 0);
+}
+
+int voxhip_convt(int mat, int32_t K, int32_t stride, int32_t pad, int32_t out_pad, const float *bias, const float *x, int32_t T,
+                 float *y) {
+    return guard_int([&] {
+        require_ok();
+        const GpuMat &M = mat_at(mat);
+        if (K < 1 || stride < 1 || pad < 0 || out_pad < 0 || T < 1 || !x || !y)
+            throw Fail("convt: K, stride and T must be positive, pad and out_pad not negative, x and y given");
+        if (M.rows % K) throw Fail("convt: the matrix rows are not K cout");
+        if (M.b) throw Fail("convt: the matrix carries a bias; the transposed conv's bias is added after the overlap-add");
+        const int64_t cout = M.rows / K, cin = M.cols, KO = M.rows;
+        const int64_t To = int64_t(T - 1) * stride - 2 * int64_t(pad) + K + out_pad;
+        if (To < 1) throw Fail("convt: no output frames");
+        if (To * cout > (int64_t(1) << 31) || int64_t(T) * KO > (int64_t(1) << 31))
+            throw Fail("convt: more than 2^31 output or product elements in one call");
+        const size_t xb = size_t(T) * size_t(cin) * 4, bb = bias ? size_t(cout) * 4 : 0, zb = size_t(T) * size_t(KO) * 4;
+        const size_t yb = size_t(To) * size_t(cout) * 4;
+        float *pin = pinned(std::max(xb + bb, yb) + 64);
+        float *dx = dev_scratch(g.dbuf_x, g.dbuf_x_bytes, xb + bb), *dz = dev_scratch(g.dbuf_z, g.dbuf_z_bytes, zb);
+        float *dy = dev_scratch(g.dbuf_y, g.dbuf_y_bytes, yb);
+        float *dbias = bias ? dx + size_t(T) * size_t(cin) : nullptr;
+        std::memcpy(pin, x, xb);
+        if (bias) std::memcpy(pin + size_t(T) * size_t(cin), bias, bb);
+        HIPCHECK(hipMemcpyAsync(dx, pin, xb + bb, hipMemcpyHostToDevice, g.stream));
+        // z = x W^T, frames in passes of the matrix's pass height, then the padded overlap-add + bias
+        const int chunk = rows_per_pass(M, T);
+        for (int64_t c0 = 0; c0 < T; c0 += chunk) {
+            const int mc = int(std::min<int64_t>(chunk, T - c0));
+            gemv(M, T, PRO_X, EPI_STORE, dx + c0 * cin, cin, mc, dz + c0 * KO, KO, nullptr, 0.f, nullptr, g.stream);
+        }
+        HIPCHECK(launch_convt_gather(dz, dbias, dy, T, int(To), stride, K, pad, int(cout), g.stream));
+        HIPCHECK(hipMemcpyAsync(pin, dy, yb, hipMemcpyDeviceToHost, g.stream));
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        std::memcpy(y, pin, yb);
         return 1;
     }, 0);
 }

@@ -206,6 +206,7 @@ SIGNATURES = {
     "voxhip_mat_free": (_I, [_I]),
     "voxhip_mat_gather": (_I, [_I, _P, C.c_int64, _P]),
     "voxhip_matmul_dev_noalloc": (_I, [_I, _P, C.c_int64, _P]),
+    "voxhip_convt": (_I, [_I, _I32, _I32, _I32, _I32, _P, _P, _I32, _P]),
     "voxhip_xfmr_create_from_mats": (_I, [C.POINTER(XfmrDesc), _P, C.c_char_p]),
     "voxhip_seq_fill_synthetic": (_I, [_I, _I64, _U64, _U32, _F, _F]),
     "voxhip_seq_download": (_I, [_I, _I32, _I64, _P, _P]),
@@ -360,6 +361,47 @@ def mat_gather(mat, ids, cols):
 
 def mat_free(mat):
     _check(lib().voxhip_mat_free(mat), "mat_free")
+
+
+class ConvT:
+    """nn::ConvT (nn.hpp:64-71; ConvTranspose1d, groups 1) with its weights on the device. load() takes PyTorch's
+    weight [cin][cout][K] and lays it out as ConvT::load does (nn.cpp:205-215): K cout rows of cin, row k cout + o;
+    forward(x [T][cin]) returns y [(T - 1) stride - 2 pad + K + out_pad][cout] (nn.cpp:217-245)."""
+
+    def __init__(self):
+        self.cin = self.cout = 0
+        self.K = self.stride = 1
+        self.pad = self.out_pad = 0
+        self.b = None
+        self.mat = -1
+
+    def load(self, weight, bias, stride, pad, out_pad=0):
+        w = np.asarray(weight, np.float32)
+        self.cin, self.cout, self.K = (int(d) for d in w.shape)
+        self.stride, self.pad, self.out_pad = int(stride), int(pad), int(out_pad)
+        self.b = None if bias is None else f32(bias)
+        rows = np.ascontiguousarray(w.transpose(2, 1, 0).reshape(self.K * self.cout, self.cin))
+        self.mat = upload(HostMat(F32, rows, self.K * self.cout, self.cin))
+        return self
+
+    def out_len(self, T):
+        return (T - 1) * self.stride - 2 * self.pad + self.K + self.out_pad
+
+    def forward(self, x):
+        return convt(self.mat, self.K, self.stride, self.pad, self.out_pad, self.b, x)
+
+
+def convt(mat, K, stride, pad, out_pad, bias, x):
+    """voxhip_convt: the transposed conv of x [T][cin] with the matrix `mat` (K cout rows of cin) -> y [To][cout]."""
+    x = f32(x)
+    T = x.shape[0]
+    rows, _ = mat_shape(mat)
+    cout = rows // K
+    To = (T - 1) * stride - 2 * pad + K + out_pad
+    y = np.empty((max(To, 1), cout), np.float32)
+    b = None if bias is None else f32(bias)
+    _check(lib().voxhip_convt(mat, K, stride, pad, out_pad, _p(b), _p(x), T, _p(y)), "convt")
+    return y
 
 
 # ---------------------------------------------------------------- transformer
