@@ -26,6 +26,7 @@
 #include <vector>
 
 #include "vh_launch.hpp"
+#include "vh_devinfo.hpp"
 #include "voxhip.h"
 
 using namespace vh;
@@ -901,13 +902,7 @@ int make_xfmr(const voxhip_xfmr_desc *w, const char *name, int use_layers, const
 // "<marketing name> (<arch>)". Some driver stacks report an empty marketing name; the label then names the
 // product family of the architecture, so device lists and GpuDeviceInfo::name still say what the card is.
 std::string device_label(const hipDeviceProp_t &p) {
-    std::string name(p.name, strnlen(p.name, sizeof p.name));
-    while (!name.empty() && (name.back() == ' ' || name.back() == '\n')) name.pop_back();
-    if (name.empty()) {
-        if (std::strncmp(p.gcnArchName, "gfx950", 6) == 0) name = "AMD Instinct MI350 series (MI350X / MI355X)";
-        else name = "AMD GPU";
-    }
-    return name + " (" + p.gcnArchName + ")";
+    return vh::device_label(std::string(p.name, strnlen(p.name, sizeof p.name)), p.gcnArchName);
 }
 
 int parse_index(const char *spec) {
@@ -937,27 +932,20 @@ int voxhip_device_info_get(int index, voxhip_device_info *out) {
     std::memset(out, 0, sizeof *out);
     hipDeviceProp_t p;
     if (hipGetDeviceProperties(&p, index) != hipSuccess) return 0;
-    out->index = index;
-    std::snprintf(out->name, sizeof out->name, "%s", device_label(p).c_str());
-    std::snprintf(out->type, sizeof out->type, "%s", p.integrated ? "integrated" : "discrete");
-    out->software = 0;
-    out->unified_memory = p.integrated ? 1 : 0;
-    out->vram_total = p.totalGlobalMem;
-    out->vram_free = p.totalGlobalMem;
+    DevProps d;
+    d.name.assign(p.name, strnlen(p.name, sizeof p.name));
+    d.arch = p.gcnArchName;
+    d.total = d.free = p.totalGlobalMem;
     int cur = -1;
     if (hipGetDevice(&cur) == hipSuccess && cur == index) {
         size_t f = 0, t = 0;
-        if (hipMemGetInfo(&f, &t) == hipSuccess) out->vram_free = f;
+        if (hipMemGetInfo(&f, &t) == hipSuccess) d.free = f;
     }
-    out->max_storage_range = p.totalGlobalMem;
-    out->subgroup_arith = 1;
-    out->coop_matrix = 1;  // MFMA
-    out->memory_budget = 1;
-    out->api_version = uint32_t(p.major * 100 + p.minor);
-    out->vendor_id = 0x1002;
-    int rt = 0;
-    (void)hipRuntimeGetVersion(&rt);
-    out->driver_version = uint32_t(rt);
+    d.integrated = p.integrated;
+    d.major = p.major;
+    d.minor = p.minor;
+    (void)hipRuntimeGetVersion(&d.runtime);
+    device_info_of(index, d, out);
     return 1;
 }
 
