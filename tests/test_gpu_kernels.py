@@ -223,6 +223,22 @@ def test_sampler_parity(hip, oracle):
         assert hip.sample_logits(l, cfg, hist) == want, (i, n, T, k, p, rep)
 
 
+@pytest.mark.parametrize("n,k", [(3072, 50), (16384, 64), (2048, 17)])
+def test_sampler_skewed_blocks(hip, oracle, n, k):
+    # the sampler instance for each vocabulary size (1, 2, 4, 8 or 16 logits per thread), with the logits of one
+    # wave (indices i with i % 1024 < 64) pushed far down in half the cases, so the radix select's first buckets
+    # are split unevenly across waves
+    rng = np.random.default_rng(n + k)
+    for case in range(12):
+        l = (rng.standard_normal(n) * 2).astype(np.float32)
+        if case % 2 == 0:
+            idx = np.arange(n)
+            l[idx % 1024 < 64] -= 50.0
+        cfg = hip.sample_cfg(0.9, 1.0 if case % 3 else 0.8, k, seed=case, frame=case)
+        u = oracle.uniform(case, case, 0, 0)
+        assert hip.sample_logits(l, cfg) == oracle.sample_logits(l, 0.9, cfg.top_p, k, 1.0, None, u), case
+
+
 def test_sampler_limits(hip):
     with pytest.raises(hip.VoxHipError):
         hip.sample_logits(np.zeros(16385, np.float32), hip.sample_cfg())

@@ -138,12 +138,23 @@ hipError_t launch_attn_rows(const AttnRowsArgs &a, int m, hipStream_t s) {
     return launch(k_attn_rows, dim3(unsigned(a.heads), unsigned(m)), dim3(256), 0, s, a);
 }
 
+template <int E>
+static hipError_t sample_e(const SampleCfgDev *cfg, const float *logits, int n, int32_t *out, hipStream_t s, int rows) {
+    const size_t smem = sample_smem_bytes(n);
+    hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_sample<E>), smem);
+    if (e != hipSuccess) return e;
+    return launch(k_sample<E>, dim3(unsigned(rows)), dim3(kSampleThreads), smem, s, cfg, logits, n, out);
+}
+
 hipError_t launch_sample(const SampleCfgDev *cfg, const float *logits, int n, int32_t *out, hipStream_t s, int rows) {
     if (n <= 0 || n > kSampleMaxN || rows <= 0) return hipErrorInvalidValue;
-    const size_t smem = sample_smem_bytes(n);
-    hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_sample), smem);
-    if (e != hipSuccess) return e;
-    return launch(k_sample, dim3(unsigned(rows)), dim3(kSampleThreads), smem, s, cfg, logits, n, out);
+    const int per = (n + kSampleThreads - 1) / kSampleThreads;
+    if (per <= 1) return sample_e<1>(cfg, logits, n, out, s, rows);
+    if (per <= 2) return sample_e<2>(cfg, logits, n, out, s, rows);
+    if (per <= 4) return sample_e<4>(cfg, logits, n, out, s, rows);
+    if (per <= 8) return sample_e<8>(cfg, logits, n, out, s, rows);
+    static_assert(kSampleMaxN == 16 * kSampleThreads, "the sampler's largest instance holds 16 logits per thread");
+    return sample_e<16>(cfg, logits, n, out, s, rows);
 }
 
 static dim3 grid1(int64_t n, int bs) { return dim3(unsigned((n + bs - 1) / bs)); }

@@ -6,19 +6,22 @@
 //   top-k at 1/T -> top-p minimal prefix -> inverse CDF with u = Philox(frame, codebook, draw).
 // Exactness: the top-k set and its order are exact (64-bit keys (ordered value, ~index): a radix select finds
 // the k-th key, the k selected keys are bitonic-sorted); the probabilities are double; every sum runs
-// sequentially in sorted order like the reference (one wave, values broadcast lane by lane). Only exp() may
+// sequentially in sorted order like the reference (one wave, terms broadcast from LDS). Only exp() may
 // differ from glibc by an ulp of a double.
 //
-// Cost shape for the talker head (n = 3072, k = 50): one radix pass per 8 key bits until the k-th key's bucket
-// holds exactly the keys still needed (usually 2-3 passes; each pass is one LDS-atomic histogram and one wave
-// scan of its 256 bins), then a register bitonic sort of 64 lanes in one wave. k > 64 sorts in LDS.
+// Cost shape for the talker head (n = 3072, k = 50; about 10 us): one radix pass per 8 key bits until the k-th
+// key's bucket holds exactly the keys still needed (usually 2-3 passes; each pass is one LDS-atomic histogram and
+// one wave scan of its 256 bins), then a register bitonic sort of 64 lanes in one wave (k > 64 sorts in LDS), then
+// the double-precision sums, whose 64-term chains read the terms from LDS so that no register spills.
 #pragma once
 #include "vh_topk.hpp"
 
 namespace vh {
 
 // One block per row b: logits [b][n] with cfg[b] -> out[b] = sampled index (or -1 when n is outside
-// 1..kSampleMaxN). Dynamic LDS: sample_smem_bytes(n).
+// 1..E kSampleThreads). E: logits per thread, the launcher's smallest power of two >= ceil(n / kSampleThreads), so
+// the keys of small vocabularies stay in registers. Dynamic LDS: sample_smem_bytes(n).
+template <int E>
 __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *cfgs, const float *logits_all, int32_t n,
                                                            int32_t *outs) {
     const SampleCfgDev *cfgp = cfgs + blockIdx.x;
@@ -28,9 +31,9 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *c
     __shared__ uint32_t seen[kSampleMaxN / 32];
     __shared__ TopkSmem S;
     __shared__ unsigned long long sh_best;
+    __shared__ double sd[64];  // one chunk of the sequential sums
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    if (n <= 0 || n > kSampleMaxN) { if (t == 0) out[0] = -1; return; }
-    constexpr int E = kSampleMaxN / kSampleThreads;
+    if (n <= 0 || n > E * kSampleThreads) { if (t == 0) out[0] = -1; return; }
     const int per = (n + kSampleThreads - 1) / kSampleThreads;
     // the logits and the configuration are independent loads: issue both before using either
     float lv[E];
@@ -100,26 +103,28 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *c
     auto weight = [&](uint64_t kv, int i) -> double {
         return i < k ? exp((double(ord_val(uint32_t(kv >> 32))) - mx) * inv_t) : 0.0;
     };
-    // Sequential sums in sorted order over chunks of 64: every lane runs the same fully unrolled chain of
-    // lane-broadcast adds (past-the-end terms are +0.0, which leaves a sum of non-negative terms unchanged).
+    // Sequential sums in sorted order over chunks of 64: the lanes put a chunk's terms in LDS and every lane adds
+    // them in order from broadcast reads, continuing `run`; lane j keeps the running sum through term j of the
+    // chunk. Past-the-end terms are +0.0, which leaves a sum of non-negative terms unchanged.
+    auto seq_chunk = [&](double x, double &run) -> double {
+        wave_lds_sync();
+        sd[lane] = x;
+        wave_lds_sync();
+        double pre = 0.0;
+#pragma unroll 8
+        for (int j = 0; j < 64; ++j) {
+            run += sd[j];
+            pre = lane == j ? run : pre;
+        }
+        return pre;
+    };
     double sum = 0.0;
-    for (int base = 0; base < k; base += 64) {
-        const double w = weight(key_of(base), base + lane);
-#pragma unroll
-        for (int j = 0; j < 64; ++j) sum += readlane_d(w, j);
-    }
+    for (int base = 0; base < k; base += 64) (void)seq_chunk(weight(key_of(base), base + lane), sum);
     // Running sums of the normalized terms, continued from `run`: lane j of the chunk gets the sum through term
     // base + j. These are the reference's top-p sum `c` and inverse-CDF sum `acc` (both start at 0 and add
     // probs[i] in order), and the top-p total is the running sum at the last kept term.
     auto prefix_chunk = [&](int base, double &run) -> double {
-        const double q = weight(key_of(base), base + lane) / sum;
-        double pre = 0.0;
-#pragma unroll
-        for (int j = 0; j < 64; ++j) {
-            run += readlane_d(q, j);
-            pre = lane == j ? run : pre;
-        }
-        return pre;
+        return seq_chunk(weight(key_of(base), base + lane) / sum, run);
     };
     const bool use_p = cfg.top_p > 0.0f && cfg.top_p < 1.0f;
     int keep = k;

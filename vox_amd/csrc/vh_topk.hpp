@@ -49,6 +49,14 @@ VH_DEV uint64_t shfl_xor_u64(uint64_t v, int m) {
     return uint64_t(hi) << 32 | lo;
 }
 
+// Orders one wave's LDS accesses around a cross-lane exchange (a write by one lane read by another): fences at
+// wavefront scope and a code-motion barrier, so no access moves across it.
+VH_DEV void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Dynamic LDS of k_sample in bytes for n logits: room for the sorted keys of the LDS path.
 inline size_t sample_smem_bytes(int n) {
     size_t k2 = 64;
