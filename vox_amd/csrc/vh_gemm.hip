@@ -136,33 +136,53 @@ hipError_t launch_gemm(int wt, int epi, const uint8_t *w, const float *scale, co
 // Tiles by how many 64 x 64 tiles the product has (measured on the flow estimator's and the DiT's shapes): below 256
 // the 32 x 32 tiles (the 1024 x 256 projections: 4.4 against 8.0 us, and faster than splitting K), below 512 with
 // K <= 512 the 32 x 64 ones (1024 x 1536, K 256: 7.0 against 8.4 us), else 64 x 64 (2000 x 1024, K 1024: 19.0
-// against 21-25 us for the smaller tiles).
-template <int EPI, int TM, int TN>
-static hipError_t gemm_hh_tiles(const _Float16 *w, const GemmArgs &g, hipStream_t s) {
-    const dim3 grid(unsigned((g.n + 32 * TN - 1) / (32 * TN)), unsigned((g.m + 32 * TM - 1) / (32 * TM)));
-    return launch(k_gemm_hh<EPI, TM, TN, 64>, grid, dim3(256), 0, s, w, g);
+// against 21-25 us for the smaller tiles). Below 256 tiles with K >= 2048 (the 512-row prefill's down projection,
+// K 4864) the 64 x 64 tiles split K instead, as the f32-activation GEMM does. Q8: the int8 values as f16 in w, the
+// block scales in q8_scale.
+template <int EPI, int TM, int TN, bool Q8>
+static hipError_t gemm_hh_tiles(const _Float16 *w, const float *q8_scale, const GemmArgs &g, hipStream_t s) {
+    const dim3 grid(unsigned((g.n + 32 * TN - 1) / (32 * TN)), unsigned((g.m + 32 * TM - 1) / (32 * TM)),
+                    unsigned(g.kchunk ? (g.K + g.kchunk - 1) / g.kchunk : 1));
+    return launch(k_gemm_hh<EPI, TM, TN, 64, Q8>, grid, dim3(256), 0, s, w, q8_scale, g);
+}
+template <int EPI, bool Q8>
+static hipError_t gemm_hh_run(const _Float16 *w, const float *q8_scale, const GemmArgs &g, hipStream_t s) {
+    const int64_t blocks = int64_t((g.n + 63) / 64) * ((g.m + 63) / 64);
+    if constexpr (EPI == EPI_STORE || EPI == EPI_ACC || EPI == EPI_GATED_ACC || EPI == EPI_SWIGLU) {
+        GemmArgs gs = g;
+        const int splits = blocks < 256 && g.K >= 2048 ? split_plan(g, &gs.kchunk) : 0;
+        if (splits) {
+            hipError_t e = gemm_hh_tiles<EPI_STORE, 2, 2, Q8>(w, q8_scale, gs, s);
+            return e != hipSuccess ? e : splitk_reduce<EPI>(g, splits, s);
+        }
+    }
+    if (blocks < 256) return gemm_hh_tiles<EPI, 1, 1, Q8>(w, q8_scale, g, s);
+    if (blocks < 512 && g.K <= 512) return gemm_hh_tiles<EPI, 1, 2, Q8>(w, q8_scale, g, s);
+    return gemm_hh_tiles<EPI, 2, 2, Q8>(w, q8_scale, g, s);
 }
 template <int EPI>
-static hipError_t gemm_hh_run(const _Float16 *w, const GemmArgs &g, hipStream_t s) {
-    const int64_t blocks = int64_t((g.n + 63) / 64) * ((g.m + 63) / 64);
-    if (blocks < 256) return gemm_hh_tiles<EPI, 1, 1>(w, g, s);
-    if (blocks < 512 && g.K <= 512) return gemm_hh_tiles<EPI, 1, 2>(w, g, s);
-    return gemm_hh_tiles<EPI, 2, 2>(w, g, s);
+static hipError_t gemm_hh_wt(const _Float16 *w, const float *q8_scale, const GemmArgs &g, hipStream_t s) {
+    return q8_scale ? gemm_hh_run<EPI, true>(w, q8_scale, g, s) : gemm_hh_run<EPI, false>(w, nullptr, g, s);
 }
 
-hipError_t launch_gemm_hh(int epi, const _Float16 *w, const GemmArgs &g, hipStream_t s) {
+hipError_t launch_gemm_hh(int epi, const _Float16 *w, const float *q8_scale, const GemmArgs &g, hipStream_t s) {
     if (g.m <= 0) return hipSuccess;
     if (!w || !g.a16 || g.n <= 0 || g.K <= 0 || g.K % 64 || g.lda < g.K || g.lda % 8 || g.a_lo % 8 ||
-        int64_t(64) * g.lda * 2 > INT32_MAX || int64_t(64) * g.K * 2 > INT32_MAX)
+        int64_t(64) * g.lda * 2 > INT32_MAX || int64_t(64) * g.K * 2 > INT32_MAX ||
+        (q8_scale && int64_t(64) * (g.K / 32) * 4 > INT32_MAX))
         return hipErrorInvalidValue;
+    if ((epi == EPI_SWIGLU || epi == EPI_SWIGLU_H16) && g.n % 2) return hipErrorInvalidValue;
     const bool y_ok = g.y != nullptr;
     switch (epi) {
-        case EPI_STORE: return y_ok ? gemm_hh_run<EPI_STORE>(w, g, s) : hipErrorInvalidValue;
-        case EPI_ACC: return y_ok ? gemm_hh_run<EPI_ACC>(w, g, s) : hipErrorInvalidValue;
-        case EPI_GATED_ACC: return y_ok && g.gate ? gemm_hh_run<EPI_GATED_ACC>(w, g, s) : hipErrorInvalidValue;
-        case EPI_GELU: return y_ok ? gemm_hh_run<EPI_GELU>(w, g, s) : hipErrorInvalidValue;
-        case EPI_GELU_H16: return g.h16 && g.ldy >= g.n ? gemm_hh_run<EPI_GELU_H16>(w, g, s) : hipErrorInvalidValue;
-        case EPI_ROPE_H16: return rope_h16_ok(g) ? gemm_hh_run<EPI_ROPE_H16>(w, g, s) : hipErrorInvalidValue;
+        case EPI_STORE: return y_ok ? gemm_hh_wt<EPI_STORE>(w, q8_scale, g, s) : hipErrorInvalidValue;
+        case EPI_ACC: return y_ok ? gemm_hh_wt<EPI_ACC>(w, q8_scale, g, s) : hipErrorInvalidValue;
+        case EPI_GATED_ACC: return y_ok && g.gate ? gemm_hh_wt<EPI_GATED_ACC>(w, q8_scale, g, s) : hipErrorInvalidValue;
+        case EPI_GELU: return y_ok ? gemm_hh_wt<EPI_GELU>(w, q8_scale, g, s) : hipErrorInvalidValue;
+        case EPI_SWIGLU: return y_ok && g.ldy >= g.n / 2 ? gemm_hh_wt<EPI_SWIGLU>(w, q8_scale, g, s) : hipErrorInvalidValue;
+        case EPI_GELU_H16: return g.h16 && g.ldy >= g.n ? gemm_hh_wt<EPI_GELU_H16>(w, q8_scale, g, s) : hipErrorInvalidValue;
+        case EPI_SWIGLU_H16:
+            return g.h16 && g.ldy >= g.n / 2 ? gemm_hh_wt<EPI_SWIGLU_H16>(w, q8_scale, g, s) : hipErrorInvalidValue;
+        case EPI_ROPE_H16: return rope_h16_ok(g) ? gemm_hh_wt<EPI_ROPE_H16>(w, q8_scale, g, s) : hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }

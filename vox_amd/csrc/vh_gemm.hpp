@@ -121,9 +121,19 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
                 const float c = acc[i][j][v] + bz;
                 const bool in = row < g.m && col < g.n;
                 float *dst = g.y + int64_t(row) * g.ldy + col;
-                if (EPI == EPI_SWIGLU) {
+                if (EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_H16) {
                     const float up = __shfl_xor(c, 1, kWave);  // column col ^ 1 of the same row
-                    if (in && (col & 1) == 0) g.y[int64_t(row) * g.ldy + col / 2] = silu(c) * up;
+                    if (in && (col & 1) == 0) {
+                        const float r = silu(c) * up;
+                        if (EPI == EPI_SWIGLU) {
+                            g.y[int64_t(row) * g.ldy + col / 2] = r;
+                        } else {
+                            const _Float16 hi = _Float16(r);
+                            const int64_t idx = int64_t(row) * g.ldy + col / 2;
+                            g.h16[idx] = hi;
+                            g.h16[g.lo_off + idx] = _Float16(r - float(hi));
+                        }
+                    }
                 } else if (EPI == EPI_ROPE || EPI == EPI_ROPE_H16) {
                     const float o = __shfl_xor(c, 1, kWave);  // the pair partner (2j <-> 2j + 1)
                     float r = c;
@@ -645,26 +655,34 @@ __global__ __launch_bounds__(256) void k_gemm_h16b(const uint8_t *__restrict__ w
     gemm_epilogue<EPI, 2, 2>(acc, g, m0, n0, wm, wn, lane);
 }
 
-// The split-f16 GEMM of k_gemm_h16 for F16 weights when the producer has already split A: hi plane g.a16, lo
-// plane g.a16 + g.a_lo (rows of g.lda halves), K a multiple of BK. Block tile 32 TM rows of A x 32 TN rows of W (4
-// waves of 16 TM x 16 TN), K steps of BK through LDS as 16-byte copies, no conversion. The loads go through buffer
-// resources cut at the block's last row of A and of W, so rows past m or n read as zeros without a per-load bounds
-// check, and the K offset of a step is the scalar offset. Every A fragment is read twice (hi, lo) per W fragment
-// pass. Two K steps are in flight (two register sets alternate), so a load has two steps' MFMAs to arrive.
-template <int EPI, int TM, int TN, int BK>
-__global__ __launch_bounds__(256) void k_gemm_hh(const _Float16 *__restrict__ w, GemmArgs g) {
-    constexpr int LD = BK + 8, BM = 32 * TM, BN = 32 * TN, CPR = BK / 8, RS = 256 / CPR, AQ = BM / RS, WQ = BN / RS;
+// The split-f16 GEMM of k_gemm_h16 when the producer has already split A: hi plane g.a16, lo plane g.a16 + g.a_lo
+// (rows of g.lda halves), K a multiple of BK. Weights: F16, or (Q8) the int8 values of Q8 weights widened once to f16
+// (exact) with their block scales `scale` [n][K / 32], applied per 32-deep block as k_gemm_h16 does (the block's
+// two MFMAs start from zero, s (q . a) goes into the accumulator). Block tile 32 TM rows of A x 32 TN rows of W (4
+// waves of 16 TM x 16 TN), K steps of BK through LDS as 16-byte copies (rows padded by 16 halves: fewer LDS bank
+// conflicts than 8 on the DiT shapes), no conversion. The loads go through buffer resources cut at the block's last
+// row of A and of W, so rows past m or n read as zeros without a per-load bounds check, and the K offset of a step
+// is the scalar offset. Two K steps are in flight (two register sets alternate), so a load has two steps' MFMAs to
+// arrive. g.kchunk: slice blockIdx.z of K (a multiple of BK) as partial sums into g.ws (k_gemm_splitk_reduce).
+template <int EPI, int TM, int TN, int BK, bool Q8 = false>
+__global__ __launch_bounds__(256) void k_gemm_hh(const _Float16 *__restrict__ w, const float *__restrict__ scale, GemmArgs g) {
+    constexpr int LD = BK + 16, BM = 32 * TM, BN = 32 * TN, CPR = BK / 8, RS = 256 / CPR, AQ = BM / RS, WQ = BN / RS;
+    constexpr int SB = BK / 32;  // scale blocks per K step
     static_assert(AQ >= 1 && WQ >= 1 && BM % RS == 0 && BN % RS == 0, "tile rows per load pass");
+    static_assert(!Q8 || BN * SB <= 256, "one scale per thread per K step");
     __shared__ __align__(16) _Float16 Ah[BM][LD], Al[BM][LD], Bs[BN][LD];
+    __shared__ float Ss[Q8 ? BN : 1][SB];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
     // row-major tiles, a band of rows of A per XCD (its rows of A and all of W stay in that XCD's L2)
     const int nt = gridDim.x, t = xcd_tile(blockIdx.y * nt + blockIdx.x, nt * gridDim.y);
-    const int m0 = (t / nt) * BM, n0 = (t % nt) * BN, K = g.K;
+    const int m0 = (t / nt) * BM, n0 = (t % nt) * BN, K = g.K, nb = K / 32;
+    const int kbeg = g.kchunk ? int(blockIdx.z) * g.kchunk : 0, kend = g.kchunk ? min(K, kbeg + g.kchunk) : K;
     const int mr = min(BM, g.m - m0), nr = min(BN, g.n - n0);
     const _Float16 *a0 = g.a16 + int64_t(m0) * g.lda;
     const __amdgpu_buffer_rsrc_t rah = buf_rsrc(a0, int32_t(mr * g.lda * 2));
     const __amdgpu_buffer_rsrc_t ral = buf_rsrc(a0 + g.a_lo, int32_t(mr * g.lda * 2));
     const __amdgpu_buffer_rsrc_t rw = buf_rsrc(w + int64_t(n0) * K, nr * K * 2);
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(Q8 ? scale + int64_t(n0) * nb : scale, Q8 ? nr * nb * 4 : 0);
     // this thread's 8-half chunks of a tile: rows r + RS q, columns c8 .. c8 + 7
     const int r = tid / CPR, c8 = (tid % CPR) * 8;
     int va[AQ], vw[WQ];
@@ -672,13 +690,15 @@ __global__ __launch_bounds__(256) void k_gemm_hh(const _Float16 *__restrict__ w,
     for (int q = 0; q < AQ; ++q) va[q] = int32_t(((r + RS * q) * g.lda + c8) * 2);
 #pragma unroll
     for (int q = 0; q < WQ; ++q) vw[q] = ((r + RS * q) * K + c8) * 2;
+    const int vs = ((tid / SB) * nb + tid % SB) * 4;  // Q8: threads < BN SB take row tid / SB, block tid % SB
     f32x4v acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
     u32x4 xa0[2 * AQ], xw0[WQ], xa1[2 * AQ], xw1[WQ];
-    auto fetch = [&](u32x4(&a)[2 * AQ], u32x4(&b)[WQ], int k0) {
+    float xs0 = 0.f, xs1 = 0.f;
+    auto fetch = [&](u32x4(&a)[2 * AQ], u32x4(&b)[WQ], float &sc, int k0) {
         const int so = k0 * 2;
 #pragma unroll
         for (int q = 0; q < AQ; ++q) {
@@ -687,8 +707,9 @@ __global__ __launch_bounds__(256) void k_gemm_hh(const _Float16 *__restrict__ w,
         }
 #pragma unroll
         for (int q = 0; q < WQ; ++q) b[q] = buf_ld16(rw, vw[q], so);
+        if (Q8) sc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, vs, k0 / 32 * 4, 0));
     };
-    auto stage = [&](const u32x4(&a)[2 * AQ], const u32x4(&b)[WQ]) {
+    auto stage = [&](const u32x4(&a)[2 * AQ], const u32x4(&b)[WQ], float sc) {
 #pragma unroll
         for (int q = 0; q < AQ; ++q) {
             *reinterpret_cast<u32x4 *>(&Ah[r + RS * q][c8]) = a[q];
@@ -696,6 +717,7 @@ __global__ __launch_bounds__(256) void k_gemm_hh(const _Float16 *__restrict__ w,
         }
 #pragma unroll
         for (int q = 0; q < WQ; ++q) *reinterpret_cast<u32x4 *>(&Bs[r + RS * q][c8]) = b[q];
+        if (Q8 && tid < BN * SB) Ss[tid / SB][tid % SB] = sc;
     };
     auto mma = [&]() {
 #pragma unroll
@@ -710,38 +732,55 @@ __global__ __launch_bounds__(256) void k_gemm_hh(const _Float16 *__restrict__ w,
 #pragma unroll
             for (int j = 0; j < TN; ++j)
                 b[j] = *reinterpret_cast<const f16x8v *>(&Bs[wn * 16 * TN + j * 16 + (lane & 15)][kk + 8 * (lane >> 4)]);
+            if (Q8) {
+                float sc[TN];  // the block scale of this lane's W row (its C column)
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+                for (int j = 0; j < TN; ++j) sc[j] = Ss[wn * 16 * TN + j * 16 + (lane & 15)][kk / 32];
 #pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], acc[i][j], 0, 0, 0);
-                }
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        f32x4v tt = {0.f, 0.f, 0.f, 0.f};
+                        tt = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], tt, 0, 0, 0);
+                        tt = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], tt, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[i][j][v] = fmaf(tt[v], sc[j], acc[i][j][v]);
+                    }
+            } else {
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], acc[i][j], 0, 0, 0);
+                    }
+            }
         }
     };
     // Every fetch is unconditional (steps past the end re-read the last one), so the compiler's count of loads in
     // flight is exact: staging one set waits only for that set, the other stays in flight.
-    const int ns = K / BK, klast = K - BK;
-    fetch(xa0, xw0, 0);
+    const int ns = (kend - kbeg) / BK, klast = kend - BK;
+    fetch(xa0, xw0, xs0, kbeg);
     __builtin_amdgcn_sched_barrier(0);  // keep the first set's loads ahead of the second's
-    fetch(xa1, xw1, min(BK, klast));
+    fetch(xa1, xw1, xs1, min(kbeg + BK, klast));
     for (int s = 0; s + 1 < ns; s += 2) {  // one back edge: the first set is always the older in flight
-        stage(xa0, xw0);
+        stage(xa0, xw0, xs0);
         __syncthreads();
-        fetch(xa0, xw0, min((s + 2) * BK, klast));
+        fetch(xa0, xw0, xs0, min(kbeg + (s + 2) * BK, klast));
         mma();
         __syncthreads();
-        stage(xa1, xw1);
+        stage(xa1, xw1, xs1);
         __syncthreads();
-        fetch(xa1, xw1, min((s + 3) * BK, klast));
+        fetch(xa1, xw1, xs1, min(kbeg + (s + 3) * BK, klast));
         mma();
         __syncthreads();
     }
     if (ns & 1) {  // the last step, in the first set
-        stage(xa0, xw0);
+        stage(xa0, xw0, xs0);
         __syncthreads();
         mma();
     }
+    if (g.kchunk) return gemm_store_partial<TM, TN>(acc, g, m0, n0, wm, wn, lane);
     gemm_epilogue<EPI, TM, TN>(acc, g, m0, n0, wm, wn, lane);
 }
 

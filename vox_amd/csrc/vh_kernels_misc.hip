@@ -184,6 +184,17 @@ hipError_t launch_rmsnorm_rows(const float *x, int64_t ldx, const float *w, int 
     if (m <= 0) return hipSuccess;
     return launch(k_rmsnorm_rows, dim3(m), dim3(256), 0, s, x, ldx, w, K, eps, out, ldo);
 }
+hipError_t launch_rmsnorm_rows_h16(const float *x, int64_t ldx, const float *w, int K, float eps, _Float16 *out16,
+                                   int64_t ldo, int64_t lo_off, int m, hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    if (!out16 || ldo < K || lo_off < int64_t(m) * ldo) return hipErrorInvalidValue;
+    return launch(k_rmsnorm_rows_h16, dim3(m), dim3(256), 0, s, x, ldx, w, K, eps, out16, ldo, lo_off);
+}
+hipError_t launch_q8_to_f16(const int8_t *q, _Float16 *out, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    if (n % 8) return hipErrorInvalidValue;
+    return launch(k_q8_to_f16, grid1(n / 8, 256), dim3(256), 0, s, q, out, n);
+}
 hipError_t launch_fill_normal(float *out, int64_t n, uint64_t seed, uint32_t stream, float mean, float std,
                               hipStream_t s) {
     if (n <= 0) return hipSuccess;

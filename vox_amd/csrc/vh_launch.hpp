@@ -35,9 +35,10 @@ hipError_t launch_qk_post(const QkArgs &a, int m, hipStream_t s);
 // Multi-row f32 GEMM on the matrix cores (F32 / F16 / BF16 / Q8 weights).
 hipError_t launch_gemm(int wt, int epi, const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s);
 // Grouped "same" Conv1d as an implicit-im2col GEMM (f32 weights [groups][cout/groups][K][cin/groups]).
-// Split-f16 GEMM with A already split by its producer (g.a16 hi, g.a16 + g.a_lo lo), F16 weights, K % 64 == 0;
-// epilogues STORE, ACC, GATED_ACC, GELU, GELU_H16, ROPE_H16.
-hipError_t launch_gemm_hh(int epi, const _Float16 *w, const GemmArgs &g, hipStream_t s);
+// Split-f16 GEMM with A already split by its producer (g.a16 hi, g.a16 + g.a_lo lo), K % 64 == 0: F16 weights
+// (q8_scale null), or Q8 weights as their int8 values widened to f16 with the block scales [n][K / 32] in q8_scale;
+// epilogues STORE, ACC, GATED_ACC, GELU, SWIGLU, GELU_H16, SWIGLU_H16, ROPE_H16 (split K uses g.ws).
+hipError_t launch_gemm_hh(int epi, const _Float16 *w, const float *q8_scale, const GemmArgs &g, hipStream_t s);
 hipError_t launch_conv_gemm(int epi, const float *w, const float *A, const GemmArgs &g, int groups, hipStream_t s);
 // Merge of the split attention partials of m rows into ao [m][heads * hd].
 hipError_t launch_attn_merge(const AttnPartials &P, float *ao, int m, hipStream_t s);
@@ -56,6 +57,11 @@ hipError_t launch_to_f16(const float *x, int64_t n, void *y, hipStream_t s);
 hipError_t launch_to_bf16(const float *x, int64_t n, void *y, hipStream_t s);
 hipError_t launch_rmsnorm_rows(const float *x, int64_t ldx, const float *w, int K, float eps, float *out, int64_t ldo,
                                int m, hipStream_t s);
+// The same RMSNorm written as f16 halves (hi rows of ldo halves at out16, lo rows at out16 + lo_off).
+hipError_t launch_rmsnorm_rows_h16(const float *x, int64_t ldx, const float *w, int K, float eps, _Float16 *out16,
+                                   int64_t ldo, int64_t lo_off, int m, hipStream_t s);
+// int8 values widened to f16 (n a multiple of 8).
+hipError_t launch_q8_to_f16(const int8_t *q, _Float16 *out, int64_t n, hipStream_t s);
 hipError_t launch_fill_normal(float *out, int64_t n, uint64_t seed, uint32_t stream, float mean, float std,
                               hipStream_t s);
 hipError_t launch_fill_cache(void *c, int64_t planes, int64_t cap, int64_t len, int hd, uint64_t seed, uint32_t stream,

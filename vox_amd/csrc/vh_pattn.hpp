@@ -157,9 +157,19 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
         const int row = r0 + 16 * wave + 4 * lg + i;
         if (row >= a.m) continue;
         const float inv = 1.0f / lrow[i];
-        float *dst = a.out + row * qd + int64_t(h) * HD;
+        const int64_t off = row * qd + int64_t(h) * HD;
+        if (a.out16) {  // f16 halves for the o projection's split-f16 product
 #pragma unroll
-        for (int dt = 0; dt < ND; ++dt) dst[16 * dt + lr] = o[dt][i] * inv;
+            for (int dt = 0; dt < ND; ++dt) {
+                const float x = o[dt][i] * inv;
+                const _Float16 hi = _Float16(x);
+                a.out16[off + 16 * dt + lr] = hi;
+                a.out16[a.lo_off + off + 16 * dt + lr] = _Float16(x - float(hi));
+            }
+        } else {
+#pragma unroll
+            for (int dt = 0; dt < ND; ++dt) a.out[off + 16 * dt + lr] = o[dt][i] * inv;
+        }
     }
 }
 

@@ -11,7 +11,7 @@ enum { EPI_STORE = 0, EPI_ACC = 1, EPI_SWIGLU = 2 };
 // GEMM-only epilogues (F5 DiT, Vocos, the codec): y += gate * c; y = gelu_tanh(c); y = mish(c); y += mish(c); RoPE on
 // q|k columns; y = gelu_erf(c); y = snake(c)
 enum { EPI_GATED_ACC = 3, EPI_GELU = 4, EPI_MISH = 5, EPI_MISH_ACC = 6, EPI_ROPE = 7, EPI_ROPE_H16 = 8, EPI_GELU_H16 = 9,
-       EPI_GELU_ERF = 10, EPI_SNAKE = 11 };
+       EPI_GELU_ERF = 10, EPI_SNAKE = 11, EPI_SWIGLU_H16 = 12 };
 // GEMM A operand: rows of a matrix, or the implicit im2col rows of a grouped "same" Conv1d
 enum { ASRC_ROWS = 0, ASRC_CONV = 1, ASRC_STREAM = 2 };
 // Weight formats of the GEMV kernels: the reference's types, plus Q4 with f16 block scales (WT_Q4H), the
@@ -92,6 +92,8 @@ struct PrefillAttnArgs {
     const float *q;        // [m][heads hd] normed + rotated queries
     const _Float16 *k, *v; // the sequence's cache bases ([layer][kv_head][cap][hd])
     float *out;            // [m][heads hd]
+    _Float16 *out16;       // or, when set, the output as f16 halves: hi [m][heads hd] at out16, lo at out16 + lo_off
+    int64_t lo_off;
     const RowRef *rows;    // the pass's row table: the kernel takes pos0 from rows[0].pos, so a captured pass
                            // replays at whatever position the host last wrote there
     int64_t cap, pos0;     // pos0: the host's copy of rows[0].pos at launch, checked against cap
@@ -136,7 +138,7 @@ struct GemmArgs {
     // v transposed per batch and head, [m / seq][heads][hd][ldvt] (ldvt >= seq, a multiple of 8); rope null: the
     // same layout without the rotation
     // EPI_GELU_H16: gelu(c + bias) as f16 halves into h16 (hi) and h16 + lo_off (lo), rows of ldy halves; the tanh
-    // form, or the erf form when gelu_erf is set
+    // form, or the erf form when gelu_erf is set. EPI_SWIGLU_H16: EPI_SWIGLU's silu(gate) up written the same way.
     _Float16 *h16;
     int64_t lo_off;
     int32_t ldvt;

@@ -91,6 +91,35 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *x, int64_t ld
     for (int i = threadIdx.x; i < K; i += 256) out[int64_t(blockIdx.x) * ldo + i] = w[i] * (xr[i] * inv);
 }
 
+// k_rmsnorm_rows with the normed rows written as f16 halves for a split-f16 product: x = hi + lo, hi = f16(x),
+// lo = f16(x - hi); hi rows of ldo halves at out16, lo rows at out16 + lo_off.
+__global__ __launch_bounds__(256) void k_rmsnorm_rows_h16(const float *x, int64_t ldx, const float *w, int K, float eps,
+                                                         _Float16 *out16, int64_t ldo, int64_t lo_off) {
+    __shared__ float red[4];
+    const float *xr = x + int64_t(blockIdx.x) * ldx;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < K; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    ss = block_sum<256>(ss, red);
+    const float inv = 1.0f / sqrtf(ss / float(K) + eps);
+    for (int i = threadIdx.x; i < K; i += 256) {
+        const float v = w[i] * (xr[i] * inv);
+        const _Float16 hi = _Float16(v);
+        out16[int64_t(blockIdx.x) * ldo + i] = hi;
+        out16[lo_off + int64_t(blockIdx.x) * ldo + i] = _Float16(v - float(hi));
+    }
+}
+
+// int8 weight values widened to f16 (exact: |q| <= 127), 8 per thread; n a multiple of 8.
+__global__ __launch_bounds__(256) void k_q8_to_f16(const int8_t *q, _Float16 *out, int64_t n) {
+    const int64_t i = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 8;
+    if (i >= n) return;
+    const uint2 u = *reinterpret_cast<const uint2 *>(q + i);
+    _Float16 h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = _Float16(int8_t((e < 4 ? u.x : u.y) >> (8 * (e & 3))));
+    *reinterpret_cast<uint4 *>(out + i) = *reinterpret_cast<const uint4 *>(h);
+}
+
 // Synthetic N(mean, std) data: Philox4x32-10 counter (pair p, stream, draw 0/1) under key (seed), Box-Muller.
 VH_DEV void normal_pair(uint64_t seed, uint32_t stream, uint64_t p, float *z0, float *z1) {
     const float u1 = det_uniform(uint32_t(seed), uint32_t(seed >> 32), p, stream, 0);

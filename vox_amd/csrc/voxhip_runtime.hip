@@ -69,6 +69,7 @@ struct GpuMat {
     bool s16 = false;
     float *b = nullptr;
     uint64_t bytes = 0;  // weights + scales + bias bytes (the GEMV's algorithmic stream)
+    _Float16 *w16 = nullptr;  // Q8: the int8 values widened to f16 for the split-f16 GEMM, made on first use
 };
 
 struct LayerDev {
@@ -115,6 +116,9 @@ struct Xfmr {
     // scratch for cap_rows rows (grown by ensure_rows); pre: the GEMM path's prologue output (normed or merged rows)
     int cap_rows = 0;
     float *h = nullptr, *xin = nullptr, *qkv = nullptr, *q = nullptr, *g = nullptr, *xnorm = nullptr, *pre = nullptr;
+    // f16 halves (hi plane, then lo plane) of the GEMM inputs of a planes pass: pa16 the normed rows and the attention
+    // output (planes of cap_rows x max(H, qd)), pb16 the SwiGLU output (planes of cap_rows x I)
+    _Float16 *pa16 = nullptr, *pb16 = nullptr;
     float *pm = nullptr, *pl = nullptr, *po = nullptr, *logits = nullptr;
     int64_t xin_elems = 0, logits_elems = 0;
     // per-row cache views of the next pass, followed by each row's RoPE row ([cap_rows][hd] (cos, sin) pairs)
@@ -317,7 +321,7 @@ int new_mat(int32_t type, int64_t rows, int64_t cols, bool bias, bool s16 = fals
 void free_mat(int id) {
     if (id < 0 || size_t(id) >= g.mats.size()) return;
     GpuMat &m = g.mats[size_t(id)];
-    dfree(m.w); dfree(m.s); dfree(m.b);
+    dfree(m.w); dfree(m.s); dfree(m.b); dfree(m.w16);
     m = GpuMat();
 }
 
@@ -489,6 +493,7 @@ void ensure_rows(Xfmr &X, int rows) {
     if (X.cap_rows) HIPCHECK(hipStreamSynchronize(g.stream));
     drop_graphs(X);
     for (float *p : {X.h, X.qkv, X.q, X.g, X.xnorm, X.pre, X.pm, X.pl, X.po}) dfree(p);
+    dfree(X.pa16); dfree(X.pb16);
     dfree(X.rows_dev); dfree(X.scfg_dev); dfree(X.token_dev);
     if (X.rows_host) (void)hipHostFree(X.rows_host);
     if (X.scfg_host) (void)hipHostFree(X.scfg_host);
@@ -499,6 +504,8 @@ void ensure_rows(Xfmr &X, int rows) {
     X.g = dalloc_t<float>(M * X.I);
     X.xnorm = dalloc_t<float>(M * X.H);
     X.pre = dalloc_t<float>(M * std::max<size_t>(size_t(X.H), qd));
+    X.pa16 = dalloc_t<_Float16>(2 * M * std::max<size_t>(size_t(X.H), qd));
+    X.pb16 = dalloc_t<_Float16>(2 * M * size_t(X.I));
     X.pm = dalloc_t<float>(M * X.heads * kAttnMaxSplits);
     X.pl = dalloc_t<float>(M * X.heads * kAttnMaxSplits);
     X.po = dalloc_t<float>(M * X.heads * kAttnMaxSplits * X.hd);
@@ -596,6 +603,40 @@ bool pass_attn_of(const Xfmr &X, int mc, bool fused) {
 // Head sizes other than 64 and 128 take k_qk_post, then k_attn_rows into X.pre, then the o GEMV on those rows.
 bool any_hd(const Xfmr &X) { return X.hd != 64 && X.hd != 128; }
 
+// Planes passes: a prefill pass of one sequence on the f32-activation GEMM whose four matrices are F16 or Q8 with K a
+// multiple of 64 runs its GEMMs on f16 halves of their inputs that the producers write (the RMSNorms, the attention,
+// the SwiGLU epilogue), so no GEMM block splits its A tile again, and Q8 weights as their int8 values widened to f16
+// once (planes_weights). The products and their order are those of the f32-activation GEMM.
+bool planes_mat(const GpuMat &m, int64_t m_total, int mc) {
+    return (m.type == VOXHIP_F16 || m.type == VOXHIP_Q8) && m.cols % 64 == 0 && gemm_path(m, m_total, mc);
+}
+bool planes_layer(const Xfmr &X, int li, int64_t m_total, int mc, bool need_ready) {
+    const LayerDev &L = X.L[size_t(li)];
+    for (int id : {L.qkv, L.o, L.gu, L.down}) {
+        const GpuMat &m = g.mats[size_t(id)];
+        if (!planes_mat(m, m_total, mc) || (need_ready && m.type == VOXHIP_Q8 && !m.w16)) return false;
+    }
+    return true;
+}
+// The f16 weights of a planes GEMM: F16 as stored; Q8's int8 values widened into m.w16 on first use (outside any
+// graph capture: forward_rows prepares them before its passes).
+const _Float16 *planes_weights(GpuMat &m, hipStream_t s) {
+    if (m.type == VOXHIP_F16) return reinterpret_cast<const _Float16 *>(m.w);
+    if (!m.w16) {
+        _Float16 *w16 = dalloc_t<_Float16>(size_t(m.rows) * size_t(m.cols));
+        HIPCHECK(launch_q8_to_f16(reinterpret_cast<const int8_t *>(m.w), w16, m.rows * m.cols, s));
+        m.w16 = w16;
+    }
+    return m.w16;
+}
+void prepare_planes(Xfmr &X, int first, int count, int64_t m_total, int mc, hipStream_t s) {
+    for (int li = first; li < first + count; ++li)
+        if (planes_layer(X, li, m_total, mc, false)) {
+            const LayerDev &L = X.L[size_t(li)];
+            for (int id : {L.qkv, L.o, L.gu, L.down}) (void)planes_weights(g.mats[size_t(id)], s);
+        }
+}
+
 void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipStream_t s, bool fused, Probe *pr = nullptr) {
     const int qd = X.heads * X.hd, kd = X.kvh * X.hd, ldqkv = qd + 2 * kd;
     const AttnPartials part = partials_of(X);
@@ -607,8 +648,26 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
         const GpuMat &Mqkv = g.mats[size_t(L.qkv)], &Mo = g.mats[size_t(L.o)], &Mgu = g.mats[size_t(L.gu)],
                      &Md = g.mats[size_t(L.down)];
         const float *qn = L.qk ? X.norms + L.qn : nullptr, *kn = L.qk ? X.norms + L.kn : nullptr;
+        // planes pass: GEMM inputs as f16 halves, hi plane then lo plane PA (PB) halves on
+        const bool planes = pass_attn && !rows_attn && planes_layer(X, li, m_total, mc, true);
+        const int64_t PA = int64_t(X.cap_rows) * std::max<int64_t>(X.H, qd), PB = int64_t(X.cap_rows) * X.I;
+        auto hh = [&](const GpuMat &M, int epi, const _Float16 *a16, int64_t a_lo, float *y, int64_t ldy) {
+            const PassScratch sc = lib_scratch();
+            GemmArgs ga{};
+            ga.bias = M.b; ga.y = y; ga.ldy = ldy; ga.m = mc; ga.n = int32_t(M.rows); ga.K = int32_t(M.cols);
+            ga.a16 = a16; ga.a_lo = a_lo; ga.lda = M.cols; ga.ws = sc.ws; ga.ws_cap = sc.ws_cap;
+            if (epi == EPI_SWIGLU_H16) { ga.y = nullptr; ga.h16 = X.pb16; ga.lo_off = PB; }
+            const _Float16 *w16 = M.type == VOXHIP_F16 ? reinterpret_cast<const _Float16 *>(M.w) : M.w16;
+            HIPCHECK(launch_gemm_hh(epi, w16, M.type == VOXHIP_Q8 ? M.s : nullptr, ga, s));
+        };
         probed(pr, VOXHIP_K_QKV, [&] {
-            gemv(Mqkv, m_total, PRO_RMS, EPI_STORE, X.h, X.H, mc, X.qkv, ldqkv, X.norms + L.ln1, X.eps, nullptr, s, nullptr, X.pre);
+            if (planes) {
+                HIPCHECK(launch_rmsnorm_rows_h16(X.h, X.H, X.norms + L.ln1, int(X.H), X.eps, X.pa16, X.H, PA, mc, s));
+                hh(Mqkv, EPI_STORE, X.pa16, PA, X.qkv, ldqkv);
+            } else {
+                gemv(Mqkv, m_total, PRO_RMS, EPI_STORE, X.h, X.H, mc, X.qkv, ldqkv, X.norms + L.ln1, X.eps, nullptr, s, nullptr,
+                     X.pre);
+            }
         });
         if (!fused) {
             QkArgs qa;
@@ -628,8 +687,12 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
             pa.q = X.q; pa.k = r0.k; pa.v = r0.v; pa.out = X.pre; pa.rows = X.rows_dev; pa.cap = r0.cap; pa.pos0 = r0.pos;
             pa.m = mc;
             pa.heads = X.heads; pa.kv_heads = X.kvh; pa.layer = li; pa.scale = 1.0f / std::sqrt(float(X.hd));
+            if (planes) { pa.out16 = X.pa16; pa.lo_off = PA; }
             probed(pr, VOXHIP_K_ATTN, [&] { HIPCHECK(launch_prefill_attn(pa, X.hd, s)); });
-            probed(pr, VOXHIP_K_O, [&] { gemv(Mo, m_total, PRO_X, EPI_ACC, X.pre, qd, mc, X.h, X.H, nullptr, 0.f, nullptr, s); });
+            probed(pr, VOXHIP_K_O, [&] {
+                if (planes) hh(Mo, EPI_ACC, X.pa16, PA, X.h, X.H);
+                else gemv(Mo, m_total, PRO_X, EPI_ACC, X.pre, qd, mc, X.h, X.H, nullptr, 0.f, nullptr, s);
+            });
         } else {
             AttnArgs aa;
             aa.ldqkv = ldqkv; aa.q = X.q; aa.qn = qn; aa.kn = kn; aa.part = part;
@@ -642,9 +705,17 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
             });
         }
         probed(pr, VOXHIP_K_GATEUP, [&] {
-            gemv(Mgu, m_total, PRO_RMS, EPI_SWIGLU, X.h, X.H, mc, X.g, X.I, X.norms + L.ln2, X.eps, nullptr, s, nullptr, X.pre);
+            if (planes) {
+                HIPCHECK(launch_rmsnorm_rows_h16(X.h, X.H, X.norms + L.ln2, int(X.H), X.eps, X.pa16, X.H, PA, mc, s));
+                hh(Mgu, EPI_SWIGLU_H16, X.pa16, PA, nullptr, X.I);
+            } else {
+                gemv(Mgu, m_total, PRO_RMS, EPI_SWIGLU, X.h, X.H, mc, X.g, X.I, X.norms + L.ln2, X.eps, nullptr, s, nullptr, X.pre);
+            }
         });
-        probed(pr, VOXHIP_K_DOWN, [&] { gemv(Md, m_total, PRO_X, EPI_ACC, X.g, X.I, mc, X.h, X.H, nullptr, 0.f, nullptr, s); });
+        probed(pr, VOXHIP_K_DOWN, [&] {
+            if (planes) hh(Md, EPI_ACC, X.pb16, PB, X.h, X.H);
+            else gemv(Md, m_total, PRO_X, EPI_ACC, X.g, X.I, mc, X.h, X.H, nullptr, 0.f, nullptr, s);
+        });
     }
 }
 
@@ -747,6 +818,7 @@ int forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_proj
         for (int i = 0; i < mc && fused; ++i)
             for (int j = 0; j < i; ++j)
                 if (rr[size_t(i)].k == rr[size_t(j)].k) { fused = false; break; }
+        if (pass_attn_of(X, mc, fused)) prepare_planes(X, first_layer, n_layers, m_total, mc, g.stream);
         run_layers(X, mc, m_total, first_layer, n_layers, fused);
         if (hidden_out) {
             HIPCHECK(hipMemcpyAsync(pin, X.h, size_t(mc * H) * 4, hipMemcpyDeviceToHost, g.stream));
@@ -1957,7 +2029,7 @@ void split_lin(bool split, const GpuMat &m, int epi, const float *A, const _Floa
     ga.a16 = A16;
     ga.a_lo = int64_t(ga.m) * ga.K;
     ga.lda = ga.K;
-    HIPCHECK(launch_gemm_hh(epi, reinterpret_cast<const _Float16 *>(m.w), ga, s));
+    HIPCHECK(launch_gemm_hh(epi, reinterpret_cast<const _Float16 *>(m.w), nullptr, ga, s));
 }
 void f5_lin(const F5 &F, const GpuMat &m, int epi, const float *A, const _Float16 *A16, GemmArgs ga, hipStream_t s) {
     split_lin(F.split, m, epi, A, A16, ga, s);
