@@ -230,6 +230,34 @@ def bench_cfg5(vh, synth, reps=3):
             "total_ms": round(t_all, 3), "tokens": ntok}
 
 
+def bench_cfg5_prefill(vh, synth, reps=10):
+    """The 512-row prefill of BASELINE configs[4]'s LM alone, through voxhip_xfmr_forward_layers over the 24 layers
+    (the same layer passes as lm_generate's prefill: one 512-row pass per layer, its GEMMs on f16 halves of their
+    inputs, q8 weights as widened int8 values with the block-scale step). Host wall-clock (median of reps, after
+    the pass has been captured as a graph), the 512 x 896 upload and download included; per_layer_us is the slope
+    between 24 and 1 layers, which cancels the copies."""
+    c = synth.COSY_LM_0_5B
+    P = c["prefill"]
+    dec = synth.Decoder(c, seed=0, capacity=P + 8)
+    x = np.random.default_rng(5).standard_normal((P, c["hidden"])).astype(np.float32)
+
+    def timed(count):
+        for _ in range(3):
+            vh.forward_layers(dec.xfmr, dec.seq, 0, x, 0, count)
+        ts = []
+        for _ in range(reps):
+            vh.sync()
+            t0 = time.perf_counter()
+            vh.forward_layers(dec.xfmr, dec.seq, 0, x, 0, count)
+            ts.append((time.perf_counter() - t0) * 1000.0)
+        return float(np.median(ts))
+    t_all, t_one = timed(c["layers"]), timed(1)
+    flops = dec.linear_flops(P) + dec.attention_flops(P)
+    return {"workload": "cosyvoice2-0.5b LM q8: the 512-row prefill's 24 layers (BASELINE configs[4])",
+            "ms": round(t_all, 3), "per_layer_us": round((t_all - t_one) / (c["layers"] - 1) * 1000.0, 1),
+            "gflop": round(flops / 1e9, 1), "tflops": round(flops / (t_all * 1e-3) / 1e12, 2)}
+
+
 def bench_vocos(vh, synth, reps=5):
     """F5-TTS's Vocos backbone + head (gpu_f5_vocos; the iSTFT stays on the host as in the reference) on 938 mel frames
     (10 s of 24 kHz audio), f16 linears. Host wall-clock (median), the mel upload and the [T][1026] download included."""
@@ -385,8 +413,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-other", action="store_true",
                     help="skip the configs[0] / [2] / [3] / [4] and code-predictor measurements")
-    ap.add_argument("--only", choices=["configs[0]", "configs[2]", "configs[3]", "configs[4]", "pred_frame", "f5_vocos",
-                                       "cosy_flow", "codec"],
+    ap.add_argument("--only", choices=["configs[0]", "configs[2]", "configs[3]", "configs[4]", "cfg5_prefill", "pred_frame",
+                                       "f5_vocos", "cosy_flow", "codec"],
                     help="run one of the other BASELINE configurations (or the code-predictor frame) alone and print "
                          "its JSON object (for profiling)")
     ap.add_argument("--no-breakdown", action="store_true",
@@ -406,6 +434,7 @@ def main():
         legs = {"configs[0]": lambda: bench_cfg1(vh), "configs[2]": lambda: bench_cfg3(vh, synth, 100, 10),
                 "configs[3]": lambda: bench_cfg4(vh, synth), "configs[4]": lambda: bench_cfg5(vh, synth),
                 "pred_frame": lambda: bench_pred(vh, synth), "f5_vocos": lambda: bench_vocos(vh, synth),
+                "cfg5_prefill": lambda: bench_cfg5_prefill(vh, synth),
                 "cosy_flow": lambda: bench_cosy(vh, synth), "codec": lambda: bench_codec(vh, synth)}
         print(json.dumps({args.only: legs[args.only]()}))
         return

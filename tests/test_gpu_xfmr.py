@@ -291,6 +291,27 @@ def test_layer_pass_graph_replays(hip, oracle, wt, m):
     assert rel_err(outs[0][0], ref) < TOL, rel_err(outs[0][0], ref)
 
 
+@pytest.mark.parametrize("wt", [F16, Q8])
+def test_prefill_key_splits(hip, oracle, wt):
+    # prefill passes whose grid of 64-row query tiles leaves CUs idle split each tile's keys into runs merged by
+    # k_pattn_merge: 300 rows from position 0 (8 runs, the last ones empty for the early tiles), then 100 rows at
+    # position 300 (7 non-empty runs and an empty one), then the same 100-row pass again: captured, then replayed
+    mdl = Model(760 + wt, 2, 256, 4, 2, 128, 512, wtype=wt, head_rows=64)
+    xf, head = build(hip, mdl)
+    seq = hip.seq_create(xf, 512)
+    kv = mdl.oracle_kv(512, kv_f16=1)
+    rng = np.random.default_rng(61 + wt)
+    x = rng.standard_normal((300, 256)).astype(np.float32)
+    out, _ = hip.forward(xf, seq, 0, x, 256, head=head)
+    assert rel_err(out, oracle.transformer_forward(mdl.ox, kv, x)) < TOL
+    x2 = rng.standard_normal((100, 256)).astype(np.float32)
+    ref = oracle.transformer_forward(mdl.ox, kv, x2)
+    outs = [hip.forward(xf, seq, 300, x2, 256, head=head) for _ in range(3)]
+    assert rel_err(outs[0][0], ref) < TOL, rel_err(outs[0][0], ref)
+    for out, logits in outs[1:]:
+        assert np.array_equal(out, outs[0][0]) and np.array_equal(logits, outs[0][1])
+
+
 # head_dim other than 64 / 128 (the reference's device path takes any even head_dim <= 128, gpu_vulkan.cpp:770):
 # (wtype, heads, kv_heads, head_dim, qk_norm); the q|k|v and o widths satisfy the matrix column rules
 @pytest.mark.parametrize("wt,heads,kvh,hd,qkn", [(Q8, 4, 2, 96, True), (BF16, 4, 1, 80, True), (F16, 4, 2, 34, False),

@@ -122,12 +122,28 @@ hipError_t launch_attention(const AttnArgs &a, const _Float16 *kc0, const _Float
     return hipErrorInvalidValue;
 }
 
+// Key splits for a prefill attention grid of tiles x heads blocks: when that leaves most CUs idle and the longest
+// query tile has at least 4 key tiles (positions from the host's pos0; a captured pass replayed elsewhere keeps its
+// count, which changes only the speed), up to kAttnMaxSplits runs per query tile, about 512 blocks in all.
+static int pattn_splits(const PrefillAttnArgs &a) {
+    const int64_t blocks = int64_t((a.m + 63) / 64) * a.heads;
+    if (!a.part.pm || !a.part.pl || !a.part.po || blocks >= 256 || a.pos0 + a.m < 256) return 1;
+    return int(std::min<int64_t>(kAttnMaxSplits, std::max<int64_t>(2, 512 / blocks)));
+}
+template <int HD>
+static hipError_t prefill_attn_hd(const PrefillAttnArgs &a0, hipStream_t s) {
+    PrefillAttnArgs a = a0;
+    a.splits = pattn_splits(a0);
+    const dim3 grid(unsigned((a.m + 63) / 64), unsigned(a.heads), unsigned(a.splits));
+    hipError_t e = launch(k_prefill_attn<HD>, grid, dim3(256), 0, s, a);
+    if (e != hipSuccess || a.splits == 1) return e;
+    return launch(k_pattn_merge<HD>, dim3(unsigned(a.heads), unsigned(a.m)), dim3(HD), 0, s, a);
+}
 hipError_t launch_prefill_attn(const PrefillAttnArgs &a, int hd, hipStream_t s) {
     if (a.m <= 0) return hipSuccess;
     if (a.kv_heads <= 0 || a.heads % a.kv_heads || a.pos0 < 0 || a.pos0 + a.m > a.cap) return hipErrorInvalidValue;
-    const dim3 grid(unsigned((a.m + 63) / 64), unsigned(a.heads));
-    if (hd == 64) return launch(k_prefill_attn<64>, grid, dim3(256), 0, s, a);
-    if (hd == 128) return launch(k_prefill_attn<128>, grid, dim3(256), 0, s, a);
+    if (hd == 64) return prefill_attn_hd<64>(a, s);
+    if (hd == 128) return prefill_attn_hd<128>(a, s);
     return hipErrorInvalidValue;
 }
 

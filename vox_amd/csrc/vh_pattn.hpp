@@ -65,6 +65,10 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
     const int64_t pos0 = a.rows[0].pos;
     const int64_t last_row = r0 + 63 < a.m - 1 ? r0 + 63 : a.m - 1;
     const int64_t kend = pos0 + last_row + 1;  // keys [0, kend) reach some row of this block
+    // this block's key tiles: all of them, or the z-th of gridDim.z contiguous runs
+    const int64_t ntile = (kend + 63) / 64, per = (ntile + gridDim.z - 1) / gridDim.z;
+    const int64_t kt_begin = int64_t(blockIdx.z) * per * 64;
+    const int64_t kt_end = (int64_t(blockIdx.z) + 1) * per * 64 < kend ? (int64_t(blockIdx.z) + 1) * per * 64 : kend;
     u32x4 kr[KQ], vr[KQ];
     auto fetch = [&](int64_t kt) {
 #pragma unroll
@@ -77,8 +81,8 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
             }
         }
     };
-    fetch(0);
-    for (int64_t kt = 0; kt < kend; kt += 64) {
+    if (kt_begin < kt_end) fetch(kt_begin);
+    for (int64_t kt = kt_begin; kt < kt_end; kt += 64) {
 #pragma unroll
         for (int q = 0; q < KQ; ++q) {
             const int idx = tid + 256 * q, key = idx / (HD / 8), d8 = (idx % (HD / 8)) * 8;
@@ -88,7 +92,7 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
             for (int e = 0; e < 8; ++e) Vt[d8 + e][key] = vv[e];
         }
         __syncthreads();
-        if (kt + 64 < kend) fetch(kt + 64);
+        if (kt + 64 < kt_end) fetch(kt + 64);
         pf32x4 s[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -152,6 +156,22 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
         }
         __syncthreads();
     }
+    if (gridDim.z > 1) {  // this run's partials: max, sum and the unnormalized output per row (slot z)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = r0 + 16 * wave + 4 * lg + i;
+            if (row >= a.m) continue;
+            const int64_t pidx = (int64_t(row) * a.heads + h) * kAttnMaxSplits + blockIdx.z;
+            if (lr == 0) {
+                a.part.pm[pidx] = mrow[i];
+                a.part.pl[pidx] = lrow[i];
+            }
+            if (mrow[i] != -INFINITY)  // the merge reads no output of a run without keys for the row
+#pragma unroll
+                for (int dt = 0; dt < ND; ++dt) a.part.po[pidx * HD + 16 * dt + lr] = o[dt][i];
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int row = r0 + 16 * wave + 4 * lg + i;
@@ -170,6 +190,34 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
 #pragma unroll
             for (int dt = 0; dt < ND; ++dt) a.out[off + 16 * dt + lr] = o[dt][i] * inv;
         }
+    }
+}
+
+// The runs of a key-split prefill attention merged per (row, head): M = the runs' largest max, the sums and
+// outputs scaled by exp(max - M) and added in run order, then out = O (1 / L) as f32 or as f16 halves (hi at out16,
+// lo at out16 + lo_off). grid (heads, m), block HD.
+template <int HD>
+__global__ __launch_bounds__(HD) void k_pattn_merge(PrefillAttnArgs a) {
+    const int h = blockIdx.x, i = blockIdx.y, e = threadIdx.x;
+    const int64_t base = (int64_t(i) * a.heads + h) * kAttnMaxSplits;
+    float mx = -INFINITY;
+    for (int z = 0; z < a.splits; ++z) mx = fmaxf(mx, a.part.pm[base + z]);
+    float L = 0.f, O = 0.f;
+    for (int z = 0; z < a.splits; ++z) {
+        const float pmz = a.part.pm[base + z];
+        if (pmz == -INFINITY) continue;
+        const float w = expf(pmz - mx);
+        L = fmaf(w, a.part.pl[base + z], L);
+        O = fmaf(w, a.part.po[(base + z) * HD + e], O);
+    }
+    const float x = O * (1.0f / L);
+    const int64_t off = int64_t(i) * a.heads * HD + int64_t(h) * HD + e;
+    if (a.out16) {
+        const _Float16 hi = _Float16(x);
+        a.out16[off] = hi;
+        a.out16[a.lo_off + off] = _Float16(x - float(hi));
+    } else {
+        a.out[off] = x;
     }
 }
 

@@ -99,6 +99,10 @@ struct PrefillAttnArgs {
     int64_t cap, pos0;     // pos0: the host's copy of rows[0].pos at launch, checked against cap
     int32_t m, heads, kv_heads, layer;
     float scale;
+    // key splits: with splits > 1 block z of a query tile takes the z-th of `splits` contiguous runs of its key tiles
+    // and writes (max, sum, unnormalized output) to part's slot z; k_pattn_merge then writes out / out16
+    AttnPartials part;
+    int32_t splits;
 };
 
 // Attention of m rows, one block per (head, row), for any even head_dim <= 128: q [m][heads hd] already normed and

@@ -688,6 +688,7 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
             pa.m = mc;
             pa.heads = X.heads; pa.kv_heads = X.kvh; pa.layer = li; pa.scale = 1.0f / std::sqrt(float(X.hd));
             if (planes) { pa.out16 = X.pa16; pa.lo_off = PA; }
+            pa.part = part;  // key-split runs (the partial buffers hold cap_rows rows)
             probed(pr, VOXHIP_K_ATTN, [&] { HIPCHECK(launch_prefill_attn(pa, X.hd, s)); });
             probed(pr, VOXHIP_K_O, [&] {
                 if (planes) hh(Mo, EPI_ACC, X.pa16, PA, X.h, X.H);
