@@ -195,20 +195,31 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
 
 // The runs of a key-split prefill attention merged per (row, head): M = the runs' largest max, the sums and
 // outputs scaled by exp(max - M) and added in run order, then out = O (1 / L) as f32 or as f16 halves (hi at out16,
-// lo at out16 + lo_off). grid (heads, m), block HD.
+// lo at out16 + lo_off). grid (heads, m), block HD; every run's values are loaded before any is used.
 template <int HD>
 __global__ __launch_bounds__(HD) void k_pattn_merge(PrefillAttnArgs a) {
     const int h = blockIdx.x, i = blockIdx.y, e = threadIdx.x;
     const int64_t base = (int64_t(i) * a.heads + h) * kAttnMaxSplits;
+    float pm[kAttnMaxSplits], pl[kAttnMaxSplits], po[kAttnMaxSplits];
+#pragma unroll
+    for (int z = 0; z < kAttnMaxSplits; ++z) {
+        const bool in = z < a.splits;
+        pm[z] = in ? a.part.pm[base + z] : -INFINITY;
+        pl[z] = in ? a.part.pl[base + z] : 0.f;
+    }
+#pragma unroll
+    for (int z = 0; z < kAttnMaxSplits; ++z)  // a run without keys for the row left no output
+        po[z] = pm[z] != -INFINITY ? a.part.po[(base + z) * HD + e] : 0.f;
     float mx = -INFINITY;
-    for (int z = 0; z < a.splits; ++z) mx = fmaxf(mx, a.part.pm[base + z]);
+#pragma unroll
+    for (int z = 0; z < kAttnMaxSplits; ++z) mx = fmaxf(mx, pm[z]);
     float L = 0.f, O = 0.f;
-    for (int z = 0; z < a.splits; ++z) {
-        const float pmz = a.part.pm[base + z];
-        if (pmz == -INFINITY) continue;
-        const float w = expf(pmz - mx);
-        L = fmaf(w, a.part.pl[base + z], L);
-        O = fmaf(w, a.part.po[(base + z) * HD + e], O);
+#pragma unroll
+    for (int z = 0; z < kAttnMaxSplits; ++z) {
+        if (pm[z] == -INFINITY) continue;
+        const float w = expf(pm[z] - mx);
+        L = fmaf(w, pl[z], L);
+        O = fmaf(w, po[z], O);
     }
     const float x = O * (1.0f / L);
     const int64_t off = int64_t(i) * a.heads * HD + int64_t(h) * HD + e;
