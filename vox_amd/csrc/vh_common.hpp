@@ -18,6 +18,14 @@ constexpr int kWave = 64;
 // streaming all of them. T % 8 != 0: identity.
 constexpr int kXcds = 8;
 __device__ __forceinline__ int xcd_tile(int L, int T) { return T % kXcds ? L : (L % kXcds) * (T / kXcds) + L / kXcds; }
+// Origin (tm, tn) of GEMM block (x, y) of an nt x mt tile grid through xcd_tile: row-major order (each XCD takes a
+// band of A rows and streams all of W) unless w_band, column-major (a band of W rows per XCD, all of A). Each XCD
+// then fetches A / 8 + W or A + W / 8 bytes; callers set w_band when W is the larger operand.
+__device__ __forceinline__ void gemm_tile(int nt, int mt, bool w_band, int &tm, int &tn) {
+    const int t = xcd_tile(int(blockIdx.y) * nt + int(blockIdx.x), nt * mt);
+    tm = w_band ? t % mt : t / nt;
+    tn = w_band ? t / mt : t % nt;
+}
 
 // Raw buffer loads: an access whose vector offset reaches `bytes` reads zeros, so tiles that overhang a matrix need
 // no per-load bounds check. Only the vector offset is relied on for the range check: a scalar offset carries a

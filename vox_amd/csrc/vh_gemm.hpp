@@ -528,8 +528,9 @@ __global__ __launch_bounds__(256) void k_gemm_h16b(const uint8_t *__restrict__ w
     __shared__ __align__(16) _Float16 Ah[64][LD], Al[64][LD], Bs[64][LD];
     __shared__ float Ss[WT == WT_Q8 ? 64 : 1][2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
-    const int nt = gridDim.x, t = xcd_tile(blockIdx.y * nt + blockIdx.x, nt * gridDim.y);
-    const int m0 = (t / nt) * 64, n0 = (t % nt) * 64, K = g.K, nb = K / 32;
+    int tm, tn;  // A f32 (4 bytes an element) against W f16 (2) or q8 (1)
+    gemm_tile(gridDim.x, gridDim.y, int64_t(g.n) * (WT == WT_F16 ? 2 : 1) > int64_t(g.m) * 4, tm, tn);
+    const int m0 = tm * 64, n0 = tn * 64, K = g.K, nb = K / 32;
     const int kbeg = g.kchunk ? int(blockIdx.z) * g.kchunk : 0, kend = g.kchunk ? min(K, kbeg + g.kchunk) : K;
     const int mr = min(64, g.m - m0), nr = min(64, g.n - n0);
     const __amdgpu_buffer_rsrc_t ra = buf_rsrc(A + int64_t(m0) * g.lda, int32_t(mr * g.lda * 4));
@@ -665,7 +666,9 @@ __global__ __launch_bounds__(256) void k_gemm_h16b(const uint8_t *__restrict__ w
 // is the scalar offset. Two K steps are in flight (two register sets alternate), so a load has two steps' MFMAs to
 // arrive. g.kchunk: slice blockIdx.z of K (a multiple of BK) as partial sums into g.ws (k_gemm_splitk_reduce).
 template <int EPI, int TM, int TN, int BK, bool Q8 = false>
-__global__ __launch_bounds__(256) void k_gemm_hh(const _Float16 *__restrict__ w, const float *__restrict__ scale, GemmArgs g) {
+// The q8 instances hold the accumulators in VGPRs for the scale FMA; asking for 4 waves per SIMD (128 VGPRs, a
+// register or two spilled) measured faster on the prefill shapes than the 3 their unconstrained 165 registers allow.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Q8 ? 4 : 1))) void k_gemm_hh(const _Float16 *__restrict__ w, const float *__restrict__ scale, GemmArgs g) {
     constexpr int LD = BK + 16, BM = 32 * TM, BN = 32 * TN, CPR = BK / 8, RS = 256 / CPR, AQ = BM / RS, WQ = BN / RS;
     constexpr int SB = BK / 32;  // scale blocks per K step
     static_assert(AQ >= 1 && WQ >= 1 && BM % RS == 0 && BN % RS == 0, "tile rows per load pass");
@@ -673,9 +676,9 @@ __global__ __launch_bounds__(256) void k_gemm_hh(const _Float16 *__restrict__ w,
     __shared__ __align__(16) _Float16 Ah[BM][LD], Al[BM][LD], Bs[BN][LD];
     __shared__ float Ss[Q8 ? BN : 1][SB];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
-    // row-major tiles, a band of rows of A per XCD (its rows of A and all of W stay in that XCD's L2)
-    const int nt = gridDim.x, t = xcd_tile(blockIdx.y * nt + blockIdx.x, nt * gridDim.y);
-    const int m0 = (t / nt) * BM, n0 = (t % nt) * BN, K = g.K, nb = K / 32;
+    int tm, tn;  // A as two f16 planes (4 bytes an element) against W f16 (2)
+    gemm_tile(gridDim.x, gridDim.y, g.n > 2 * g.m, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN, K = g.K, nb = K / 32;
     const int kbeg = g.kchunk ? int(blockIdx.z) * g.kchunk : 0, kend = g.kchunk ? min(K, kbeg + g.kchunk) : K;
     const int mr = min(BM, g.m - m0), nr = min(BN, g.n - n0);
     const _Float16 *a0 = g.a16 + int64_t(m0) * g.lda;
