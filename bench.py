@@ -297,9 +297,7 @@ def bench_cosy(vh, synth, reps=5):
         t0 = time.perf_counter()
         out = vh.cosy_step(flow.est, x, tb, T, M)
         times.append((time.perf_counter() - t0) * 1000.0)
-    vh.cosy_end(flow.est)
-    for h in flow.mats:
-        vh.mat_free(h)
+    vh.cosy_end(flow.est)  # the estimator keeps its matrices (mat_free refuses a matrix an estimator uses)
     assert np.isfinite(out).all()
     ms = float(np.median(times))
     fl = flow.flops(T)
@@ -332,9 +330,7 @@ def bench_codec(vh, synth, reps=10):
         fl = F * dec.flops_per_frame()
         out[f"f{F}"] = {"ms_per_call": round(ms, 3), "gflop": round(fl / 1e9, 2), "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
                         "audio_s_per_s": round(F * dec.spf / 24000 / (ms * 1e-3), 1)}
-    vh.codec_state_free(st)
-    for h in dec.mats:
-        vh.mat_free(h)
+    vh.codec_state_free(st)  # the decoder keeps its matrices (mat_free refuses a matrix a decoder uses)
     return {"workload": "qwen3-tts codec decoder (gpu_codec_forward): 8-layer windowed transformer + 2 upsample + 4 "
                         "decoder blocks (1536 ch, 1920 samples per frame), f32 weights", **out}
 

@@ -312,6 +312,29 @@ def test_prefill_key_splits(hip, oracle, wt):
         assert np.array_equal(out, outs[0][0]) and np.array_equal(logits, outs[0][1])
 
 
+@pytest.mark.parametrize("wt", [F16, Q8])
+def test_prefill_down_reduce_norms(hip, oracle, wt):
+    # planes prefill of 3 layers whose down projection (K 2048, 8 tiles) splits K: the split-K reduce of layers 0 and
+    # 1 also writes the next layer's first RMSNorm; the last layer's reduce does not. Against the oracle, then the
+    # same pass captured and replayed (bit-identical).
+    mdl = Model(820 + wt, 3, 256, 4, 2, 64, 2048, wtype=wt, bias=True, head_rows=64)
+    xf, head = build(hip, mdl)
+    seq = hip.seq_create(xf, 512)
+    kv = mdl.oracle_kv(512, kv_f16=1)
+    rng = np.random.default_rng(83 + wt)
+    x = rng.standard_normal((128, 256)).astype(np.float32)
+    out, logits = hip.forward(xf, seq, 0, x, 256, head=head)
+    ref = oracle.transformer_forward(mdl.ox, kv, x)
+    assert rel_err(out, ref) < TOL, rel_err(out, ref)
+    assert rel_err(logits, oracle_head(oracle, mdl, out)) < TOL
+    x2 = rng.standard_normal((96, 256)).astype(np.float32)
+    ref2 = oracle.transformer_forward(mdl.ox, kv, x2)
+    outs = [hip.forward(xf, seq, 128, x2, 256, head=head) for _ in range(3)]
+    assert rel_err(outs[0][0], ref2) < TOL, rel_err(outs[0][0], ref2)
+    for o, lg in outs[1:]:
+        assert np.array_equal(o, outs[0][0]) and np.array_equal(lg, outs[0][1])
+
+
 # head_dim other than 64 / 128 (the reference's device path takes any even head_dim <= 128, gpu_vulkan.cpp:770):
 # (wtype, heads, kv_heads, head_dim, qk_norm); the q|k|v and o widths satisfy the matrix column rules
 @pytest.mark.parametrize("wt,heads,kvh,hd,qkn", [(Q8, 4, 2, 96, True), (BF16, 4, 1, 80, True), (F16, 4, 2, 34, False),

@@ -165,12 +165,36 @@ static hipError_t gemm_hh_wt(const _Float16 *w, const float *q8_scale, const Gem
     return q8_scale ? gemm_hh_run<EPI, true>(w, q8_scale, g, s) : gemm_hh_run<EPI, false>(w, nullptr, g, s);
 }
 
+static bool hh_args_ok(const _Float16 *w, const float *q8_scale, const GemmArgs &g) {
+    return w && g.a16 && g.n > 0 && g.K > 0 && g.K % 64 == 0 && g.lda >= g.K && g.lda % 8 == 0 && g.a_lo % 8 == 0 &&
+           int64_t(64) * g.lda * 2 <= INT32_MAX && int64_t(64) * g.K * 2 <= INT32_MAX &&
+           (!q8_scale || int64_t(64) * (g.K / 32) * 4 <= INT32_MAX);
+}
+
+hipError_t launch_gemm_hh_acc_rms(const _Float16 *w, const float *q8_scale, const GemmArgs &g, const float *gamma, float eps,
+                                  _Float16 *out16, int64_t ldo, int64_t lo_off, hipStream_t s, bool *normed) {
+    *normed = false;
+    if (g.m <= 0) return hipSuccess;
+    if (!hh_args_ok(w, q8_scale, g) || !g.y) return hipErrorInvalidValue;
+    const int64_t blocks = int64_t((g.n + 63) / 64) * ((g.m + 63) / 64);
+    GemmArgs gs = g;
+    const int splits = blocks < 256 && g.K >= 2048 ? split_plan(g, &gs.kchunk) : 0;
+    // the row pass holds 8 columns per thread; without a split the ACC epilogue already wrote y
+    if (!splits || splits > 8 || g.n > 8 * 256 || !gamma || !out16 || ldo < g.n || lo_off % 8)
+        return launch_gemm_hh(EPI_ACC, w, q8_scale, g, s);
+    hipError_t e = q8_scale ? gemm_hh_tiles<EPI_STORE, 2, 2, true>(w, q8_scale, gs, s)
+                            : gemm_hh_tiles<EPI_STORE, 2, 2, false>(w, nullptr, gs, s);
+    if (e != hipSuccess) return e;
+    const dim3 grid(unsigned(g.m));
+    if (g.n <= 4 * 256) e = launch(k_splitk_acc_rms_h16<4>, grid, dim3(256), 0, s, g, int32_t(splits), gamma, eps, out16, ldo, lo_off);
+    else e = launch(k_splitk_acc_rms_h16<8>, grid, dim3(256), 0, s, g, int32_t(splits), gamma, eps, out16, ldo, lo_off);
+    if (e == hipSuccess) *normed = true;
+    return e;
+}
+
 hipError_t launch_gemm_hh(int epi, const _Float16 *w, const float *q8_scale, const GemmArgs &g, hipStream_t s) {
     if (g.m <= 0) return hipSuccess;
-    if (!w || !g.a16 || g.n <= 0 || g.K <= 0 || g.K % 64 || g.lda < g.K || g.lda % 8 || g.a_lo % 8 ||
-        int64_t(64) * g.lda * 2 > INT32_MAX || int64_t(64) * g.K * 2 > INT32_MAX ||
-        (q8_scale && int64_t(64) * (g.K / 32) * 4 > INT32_MAX))
-        return hipErrorInvalidValue;
+    if (!hh_args_ok(w, q8_scale, g)) return hipErrorInvalidValue;
     if ((epi == EPI_SWIGLU || epi == EPI_SWIGLU_H16) && g.n % 2) return hipErrorInvalidValue;
     const bool y_ok = g.y != nullptr;
     switch (epi) {

@@ -787,8 +787,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Q8 ? 4 : 1)
     gemm_epilogue<EPI, TM, TN>(acc, g, m0, n0, wm, wn, lane);
 }
 
-// The split-K partial slices ws[z][m][n], added in z order, then bias and the epilogue (STORE, ACC, GATED_ACC,
-// SWIGLU: one thread per output element; SWIGLU outputs pair columns 2u, 2u + 1). grid ceil(m n' / 256).
+// The split-K partial slices ws[z][m][n] (at most 8), added in z order, then bias and the epilogue (STORE, ACC,
+// GATED_ACC, SWIGLU: one thread per output element; SWIGLU outputs pair columns 2u, 2u + 1). grid ceil(m n' / 256).
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm_splitk_reduce(GemmArgs g, int32_t splits) {
     const int nout = EPI == EPI_SWIGLU ? g.n / 2 : g.n;
@@ -796,9 +796,14 @@ __global__ __launch_bounds__(256) void k_gemm_splitk_reduce(GemmArgs g, int32_t 
     if (t >= int64_t(g.m) * nout) return;
     const int row = int(t / nout), c = int(t % nout);
     const int64_t slice = int64_t(g.m) * g.n;
-    auto sum = [&](int col) {
+    auto sum = [&](int col) {  // every slice's load in flight at once (past `splits`, slice 0, left out), added in order
+        float t[8];
+#pragma unroll
+        for (int z = 0; z < 8; ++z) t[z] = g.ws[(z < splits ? z : 0) * slice + int64_t(row) * g.n + col];
         float v = 0.f;
-        for (int z = 0; z < splits; ++z) v += g.ws[z * slice + int64_t(row) * g.n + col];
+#pragma unroll
+        for (int z = 0; z < 8; ++z)
+            if (z < splits) v += t[z];
         return v + (g.bias ? g.bias[col] : 0.f);
     };
     float *dst = g.y + int64_t(row) * g.ldy + c;
@@ -809,6 +814,59 @@ __global__ __launch_bounds__(256) void k_gemm_splitk_reduce(GemmArgs g, int32_t 
     else if (EPI == EPI_SNAKE) {
         const float v = sum(c), sn = sinf(v * g.snake_a[c]);
         *dst = v + g.snake_ib[c] * sn * sn;
+    }
+}
+
+// The split-K slices of an EPI_ACC product added into its rows, y[row][c] += (sum_z ws[z][row][c]) + bias[c], as
+// k_gemm_splitk_reduce<EPI_ACC> does, then the RMSNorm (gamma, eps) of each updated row written as f16 halves (hi at
+// out16, lo at out16 + lo_off, rows of ldo halves) with k_rmsnorm_rows_h16's arithmetic: the residual add and the
+// next norm in one pass over the row. grid m, block 256, n <= 256 NV, splits <= 8.
+template <int NV>
+__global__ __launch_bounds__(256) void k_splitk_acc_rms_h16(GemmArgs g, int32_t splits, const float *gamma, float eps,
+                                                           _Float16 *out16, int64_t ldo, int64_t lo_off) {
+    __shared__ float red[4];
+    const int row = int(blockIdx.x);
+    const int64_t slice = int64_t(g.m) * g.n;
+    float *yr = g.y + int64_t(row) * g.ldy;
+    // every slice's value and the row's own first, so the loads are in flight together (slices past `splits`, at
+    // most kMaxSplits, read slice 0 and are left out), then the sums in split order as the reduce kernel adds them
+    constexpr int kMaxSplits = 8;
+    float t[NV][kMaxSplits], hv[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int c = min(int(threadIdx.x) + 256 * k, g.n - 1);
+        hv[k] = yr[c];
+#pragma unroll
+        for (int z = 0; z < kMaxSplits; ++z) t[k][z] = g.ws[(z < splits ? z : 0) * slice + int64_t(row) * g.n + c];
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int c = int(threadIdx.x) + 256 * k;
+        if (c < g.n) {
+            float v = 0.f;
+#pragma unroll
+            for (int z = 0; z < kMaxSplits; ++z)
+                if (z < splits) v += t[k][z];
+            v = v + (g.bias ? g.bias[c] : 0.f);
+            hv[k] = hv[k] + v;
+            yr[c] = hv[k];
+            ss = fmaf(hv[k], hv[k], ss);
+        } else {
+            hv[k] = 0.f;
+        }
+    }
+    ss = block_sum<256>(ss, red);
+    const float inv = 1.0f / sqrtf(ss / float(g.n) + eps);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int c = int(threadIdx.x) + 256 * k;
+        if (c < g.n) {
+            const float v = gamma[c] * (hv[k] * inv);
+            const _Float16 hi = _Float16(v);
+            out16[int64_t(row) * ldo + c] = hi;
+            out16[lo_off + int64_t(row) * ldo + c] = _Float16(v - float(hi));
+        }
     }
 }
 

@@ -39,6 +39,11 @@ hipError_t launch_gemm(int wt, int epi, const uint8_t *w, const float *scale, co
 // (q8_scale null), or Q8 weights as their int8 values widened to f16 with the block scales [n][K / 32] in q8_scale;
 // epilogues STORE, ACC, GATED_ACC, GELU, SWIGLU, GELU_H16, SWIGLU_H16, ROPE_H16 (split K uses g.ws).
 hipError_t launch_gemm_hh(int epi, const _Float16 *w, const float *q8_scale, const GemmArgs &g, hipStream_t s);
+// The same with EPI_ACC, and when the product splits K, the next RMSNorm (gamma, eps) of the updated rows of y written
+// as f16 halves (out16, ldo, lo_off as launch_rmsnorm_rows_h16) by the split-K reduce itself: *normed tells whether
+// it did (otherwise the caller runs the norm).
+hipError_t launch_gemm_hh_acc_rms(const _Float16 *w, const float *q8_scale, const GemmArgs &g, const float *gamma, float eps,
+                                  _Float16 *out16, int64_t ldo, int64_t lo_off, hipStream_t s, bool *normed);
 hipError_t launch_conv_gemm(int epi, const float *w, const float *A, const GemmArgs &g, int groups, hipStream_t s);
 // Merge of the split attention partials of m rows into ao [m][heads * hd].
 hipError_t launch_attn_merge(const AttnPartials &P, float *ao, int m, hipStream_t s);

@@ -643,6 +643,7 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
     const bool rows_attn = any_hd(X);
     if (rows_attn) fused = false;
     const bool pass_attn = pass_attn_of(X, mc, fused);
+    bool pa_normed = false;  // planes: the previous layer's down reduce already wrote this layer's first RMSNorm
     for (int li = first; li < first + count; ++li) {
         const LayerDev &L = X.L[size_t(li)];
         const GpuMat &Mqkv = g.mats[size_t(L.qkv)], &Mo = g.mats[size_t(L.o)], &Mgu = g.mats[size_t(L.gu)],
@@ -651,18 +652,24 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
         // planes pass: GEMM inputs as f16 halves, hi plane then lo plane PA (PB) halves on
         const bool planes = pass_attn && !rows_attn && planes_layer(X, li, m_total, mc, true);
         const int64_t PA = int64_t(X.cap_rows) * std::max<int64_t>(X.H, qd), PB = int64_t(X.cap_rows) * X.I;
-        auto hh = [&](const GpuMat &M, int epi, const _Float16 *a16, int64_t a_lo, float *y, int64_t ldy) {
+        auto hh_args = [&](const GpuMat &M, const _Float16 *a16, int64_t a_lo, float *y, int64_t ldy) {
             const PassScratch sc = lib_scratch();
             GemmArgs ga{};
             ga.bias = M.b; ga.y = y; ga.ldy = ldy; ga.m = mc; ga.n = int32_t(M.rows); ga.K = int32_t(M.cols);
             ga.a16 = a16; ga.a_lo = a_lo; ga.lda = M.cols; ga.ws = sc.ws; ga.ws_cap = sc.ws_cap;
+            return ga;
+        };
+        auto w16_of = [](const GpuMat &M) {
+            return M.type == VOXHIP_F16 ? reinterpret_cast<const _Float16 *>(M.w) : static_cast<const _Float16 *>(M.w16);
+        };
+        auto hh = [&](const GpuMat &M, int epi, const _Float16 *a16, int64_t a_lo, float *y, int64_t ldy) {
+            GemmArgs ga = hh_args(M, a16, a_lo, y, ldy);
             if (epi == EPI_SWIGLU_H16) { ga.y = nullptr; ga.h16 = X.pb16; ga.lo_off = PB; }
-            const _Float16 *w16 = M.type == VOXHIP_F16 ? reinterpret_cast<const _Float16 *>(M.w) : M.w16;
-            HIPCHECK(launch_gemm_hh(epi, w16, M.type == VOXHIP_Q8 ? M.s : nullptr, ga, s));
+            HIPCHECK(launch_gemm_hh(epi, w16_of(M), M.type == VOXHIP_Q8 ? M.s : nullptr, ga, s));
         };
         probed(pr, VOXHIP_K_QKV, [&] {
             if (planes) {
-                HIPCHECK(launch_rmsnorm_rows_h16(X.h, X.H, X.norms + L.ln1, int(X.H), X.eps, X.pa16, X.H, PA, mc, s));
+                if (!pa_normed) HIPCHECK(launch_rmsnorm_rows_h16(X.h, X.H, X.norms + L.ln1, int(X.H), X.eps, X.pa16, X.H, PA, mc, s));
                 hh(Mqkv, EPI_STORE, X.pa16, PA, X.qkv, ldqkv);
             } else {
                 gemv(Mqkv, m_total, PRO_RMS, EPI_STORE, X.h, X.H, mc, X.qkv, ldqkv, X.norms + L.ln1, X.eps, nullptr, s, nullptr,
@@ -713,9 +720,18 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
                 gemv(Mgu, m_total, PRO_RMS, EPI_SWIGLU, X.h, X.H, mc, X.g, X.I, X.norms + L.ln2, X.eps, nullptr, s, nullptr, X.pre);
             }
         });
+        pa_normed = false;
         probed(pr, VOXHIP_K_DOWN, [&] {
-            if (planes) hh(Md, EPI_ACC, X.pb16, PB, X.h, X.H);
-            else gemv(Md, m_total, PRO_X, EPI_ACC, X.g, X.I, mc, X.h, X.H, nullptr, 0.f, nullptr, s);
+            // the next layer's first RMSNorm rides on this split-K reduce when that layer is a planes pass too
+            if (planes && li + 1 < first + count && planes_layer(X, li + 1, m_total, mc, true)) {
+                const GemmArgs ga = hh_args(Md, X.pb16, PB, X.h, X.H);
+                HIPCHECK(launch_gemm_hh_acc_rms(w16_of(Md), Md.type == VOXHIP_Q8 ? Md.s : nullptr, ga,
+                                                X.norms + X.L[size_t(li + 1)].ln1, X.eps, X.pa16, X.H, PA, s, &pa_normed));
+            } else if (planes) {
+                hh(Md, EPI_ACC, X.pb16, PB, X.h, X.H);
+            } else {
+                gemv(Md, m_total, PRO_X, EPI_ACC, X.g, X.I, mc, X.h, X.H, nullptr, 0.f, nullptr, s);
+            }
         });
     }
 }
@@ -1815,6 +1831,10 @@ int voxhip_lm_generate(int xfmr, int seq, const float *x, int64_t n, int head, i
             HIPCHECK(hipStreamSynchronize(g.stream));
             const LmState r = *lm_host_state(0);
             if (r.status) throw Fail("CosyVoice: sampling reaches max_trials and still gets eos when ignore_eos is True");
+            // the counts come from device memory and size the copies into the caller's buffers (max_len entries,
+            // max_len x V log-probs): a count outside them is an error, never a copy
+            if (r.n_dec < 0 || r.n_dec > cfg->max_len) throw Fail("LM state reports " + std::to_string(r.n_dec) + " tokens of " +
+                                                                  std::to_string(cfg->max_len));
             if (r.n_dec > 0) HIPCHECK(hipMemcpy(tokens, X.lm_dec, size_t(r.n_dec) * 4, hipMemcpyDeviceToHost));
             const int64_t rows = std::min<int64_t>(r.n_dec + (r.last >= cfg->speech_tokens ? 1 : 0), cfg->max_len);
             if (logp && rows > 0) HIPCHECK(hipMemcpy(logp, X.lm_logp, size_t(rows * V) * 4, hipMemcpyDeviceToHost));
