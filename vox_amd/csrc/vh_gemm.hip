@@ -139,11 +139,11 @@ hipError_t launch_gemm(int wt, int epi, const uint8_t *w, const float *scale, co
 // against 21-25 us for the smaller tiles). Below 256 tiles with K >= 2048 (the 512-row prefill's down projection,
 // K 4864) the 64 x 64 tiles split K instead, as the f32-activation GEMM does. Q8: the int8 values as f16 in w, the
 // block scales in q8_scale.
-template <int EPI, int TM, int TN, bool Q8>
+template <int EPI, int TM, int TN, bool Q8, int WN = 2>
 static hipError_t gemm_hh_tiles(const _Float16 *w, const float *q8_scale, const GemmArgs &g, hipStream_t s) {
-    const dim3 grid(unsigned((g.n + 32 * TN - 1) / (32 * TN)), unsigned((g.m + 32 * TM - 1) / (32 * TM)),
+    const dim3 grid(unsigned((g.n + 16 * TN * WN - 1) / (16 * TN * WN)), unsigned((g.m + 32 * TM - 1) / (32 * TM)),
                     unsigned(g.kchunk ? (g.K + g.kchunk - 1) / g.kchunk : 1));
-    return launch(k_gemm_hh<EPI, TM, TN, 64, Q8>, grid, dim3(256), 0, s, w, q8_scale, g);
+    return launch(k_gemm_hh<EPI, TM, TN, 64, Q8, WN>, grid, dim3(128 * WN), 0, s, w, q8_scale, g);
 }
 template <int EPI, bool Q8>
 static hipError_t gemm_hh_run(const _Float16 *w, const float *q8_scale, const GemmArgs &g, hipStream_t s) {
@@ -158,6 +158,12 @@ static hipError_t gemm_hh_run(const _Float16 *w, const float *q8_scale, const Ge
     }
     if (blocks < 256) return gemm_hh_tiles<EPI, 1, 1, Q8>(w, q8_scale, g, s);
     if (blocks < 512 && g.K <= 512) return gemm_hh_tiles<EPI, 1, 2, Q8>(w, q8_scale, g, s);
+    // f16 weights: 64 x 128 tiles of 8 waves while they still make 256 blocks (the DiT's 2000 x 3072 x 1024 q|k|v
+    // 36.5 against 42.2 us, 2000 x 1024 x 2048 27.9 against 31.2 us, 1000 x 2048 x 1024 16.7 against 19.0 us; at 128
+    // blocks they lose, 1000 x 1024 x 2048 24.9 against 21.6 us; the q8 prefill shapes measured slower, 37.2 against
+    // 36.1 us for 512 x 9728 x 896)
+    if constexpr (!Q8)
+        if (int64_t((g.n + 127) / 128) * ((g.m + 63) / 64) >= 256) return gemm_hh_tiles<EPI, 2, 2, Q8, 4>(w, q8_scale, g, s);
     return gemm_hh_tiles<EPI, 2, 2, Q8>(w, q8_scale, g, s);
 }
 template <int EPI>

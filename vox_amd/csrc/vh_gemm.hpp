@@ -665,17 +665,20 @@ __global__ __launch_bounds__(256) void k_gemm_h16b(const uint8_t *__restrict__ w
 // row of A and of W, so rows past m or n read as zeros without a per-load bounds check, and the K offset of a step
 // is the scalar offset. Two K steps are in flight (two register sets alternate), so a load has two steps' MFMAs to
 // arrive. g.kchunk: slice blockIdx.z of K (a multiple of BK) as partial sums into g.ws (k_gemm_splitk_reduce).
-template <int EPI, int TM, int TN, int BK, bool Q8 = false>
+template <int EPI, int TM, int TN, int BK, bool Q8 = false, int WN = 2>
 // The q8 instances hold the accumulators in VGPRs for the scale FMA; asking for 4 waves per SIMD (128 VGPRs, a
 // register or two spilled) measured faster on the prefill shapes than the 3 their unconstrained 165 registers allow.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Q8 ? 4 : 1))) void k_gemm_hh(const _Float16 *__restrict__ w, const float *__restrict__ scale, GemmArgs g) {
-    constexpr int LD = BK + 16, BM = 32 * TM, BN = 32 * TN, CPR = BK / 8, RS = 256 / CPR, AQ = BM / RS, WQ = BN / RS;
+__global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(Q8 ? 4 : 1))) void k_gemm_hh(const _Float16 *__restrict__ w, const float *__restrict__ scale, GemmArgs g) {
+    // 2 x WN waves of 16 TM x 16 TN outputs each (WN = 2: 64 x 64 tiles for TM = TN = 2, 256 threads; WN = 4: 64 x 128,
+    // 512 threads, so each block's A tile serves twice the columns)
+    constexpr int NT = 128 * WN, LD = BK + 16, BM = 32 * TM, BN = 16 * TN * WN, CPR = BK / 8, RS = NT / CPR, AQ = BM / RS,
+                  WQ = BN / RS;
     constexpr int SB = BK / 32;  // scale blocks per K step
     static_assert(AQ >= 1 && WQ >= 1 && BM % RS == 0 && BN % RS == 0, "tile rows per load pass");
-    static_assert(!Q8 || BN * SB <= 256, "one scale per thread per K step");
+    static_assert(!Q8 || BN * SB <= NT, "one scale per thread per K step");
     __shared__ __align__(16) _Float16 Ah[BM][LD], Al[BM][LD], Bs[BN][LD];
     __shared__ float Ss[Q8 ? BN : 1][SB];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave / WN, wn = wave % WN;
     int tm, tn;  // A as two f16 planes (4 bytes an element) against W f16 (2)
     gemm_tile(gridDim.x, gridDim.y, g.n > 2 * g.m, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN, K = g.K, nb = K / 32;
