@@ -2312,6 +2312,8 @@ struct Cosy {
     _Float16 *qkv16 = nullptr, *xn16 = nullptr, *at16 = nullptr, *ff16 = nullptr;
     int64_t lo_off = 0;
     int ldvt = 0;
+    // the step's launches as one graph over the buffers of this begin (captured by the first step after it)
+    hipGraphExec_t step_graph = nullptr;
 };
 
 Cosy &cosy_at(int id) {
@@ -2320,6 +2322,8 @@ Cosy &cosy_at(int id) {
 }
 
 void cosy_free_step(Cosy &E) {
+    if (E.step_graph) (void)hipGraphExecDestroy(E.step_graph);
+    E.step_graph = nullptr;
     for (float *p : {E.in, E.a, E.b, E.h, E.cat, E.xn, E.at, E.ff, E.tb, E.x, E.out}) dfree(p);
     E.in = E.a = E.b = E.h = E.cat = E.xn = E.at = E.ff = E.tb = E.x = E.out = nullptr;
     for (_Float16 *p : {E.qkv16, E.xn16, E.at16, E.ff16}) dfree(p);
@@ -2543,7 +2547,25 @@ int voxhip_cosy_step(int id, const float *x, const float *tb, float *out) {
         if (!x || !tb || !out) throw Fail("missing argument");
         h2d(E.x, x, size_t(E.T) * E.M * 4);
         h2d(E.tb, tb, (2 + E.mid_res.size()) * size_t(E.C) * 4);
-        cosy_enqueue(E, g.stream);
+        // the step's ~560 launches as one graph: the buffers of this begin, the weights and the scratch are fixed
+        if (!E.step_graph) {
+            hipGraph_t graph = nullptr;
+            HIPCHECK(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal));
+            try {
+                cosy_enqueue(E, g.stream);
+            } catch (...) {
+                (void)hipStreamEndCapture(g.stream, &graph);
+                if (graph) (void)hipGraphDestroy(graph);
+                throw;
+            }
+            HIPCHECK(hipStreamEndCapture(g.stream, &graph));
+            hipGraphExec_t exec = nullptr;
+            const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            HIPCHECK(e);
+            E.step_graph = exec;
+        }
+        HIPCHECK(hipGraphLaunch(E.step_graph, g.stream));
         HIPCHECK(hipStreamSynchronize(g.stream));
         HIPCHECK(hipMemcpy(out, E.out, size_t(2) * E.T * E.M * 4, hipMemcpyDeviceToHost));
         return 1;
