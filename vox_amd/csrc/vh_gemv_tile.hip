@@ -43,8 +43,8 @@ void gemv_tile(int rows, int nchunk, int M, bool swiglu, int *R, int *IT) {
         return;
     }
     int it = (nchunk + 63) / 64;
-    it = it < 1 ? 1 : it > 4 ? 4 : it;
-    if (it > 1) {  // (1,2) (1,3) (1,4); swiglu (2,2) (2,3)
+    it = it < 1 ? 1 : it > 6 ? 6 : it;
+    if (it > 1) {  // (1,2) .. (1,6): one pass of chunks up to K = 384 16-byte chunks (q8 K 6144); swiglu (2,2) (2,3)
         *R = swiglu ? 2 : 1;
         *IT = swiglu && it > 3 ? 3 : it;
         return;
