@@ -61,6 +61,15 @@ def test_f5_step_cfg4_shape(hip, oracle, B):
     run(hip, oracle, m, B, 1000, seed=4 + B)
 
 
+def test_f5_step_wide_tiles_partial(hip, oracle):
+    # dim 320 (5 x 64 heads) at B = 2, N = 1000: the q|k|v product (n 960) runs 64 x 128 tiles of 8 waves, 8 x 32 = 256
+    # blocks, whose last column tile is half past n and whose tiles straddle the q|k / v boundary of the RoPE epilogue;
+    # o (n 320) and the FFN (n 640) keep 64 x 64 tiles
+    oracle.lib().vo_set_threads(16)
+    m = F5Model(52, 320, 1, 5, mel=100, text=512, K=31, groups=16, wtype=F16, std=0.02)
+    run(hip, oracle, m, 2, 1000, seed=9)
+
+
 def test_f5_rejects_bad_shapes(hip):
     m = F5Model(60, 128, 1, 2, dim_head=32, wtype=F16)
     with pytest.raises(hip.VoxHipError, match="head_dim"):
