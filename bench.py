@@ -533,6 +533,7 @@ def main():
         "step": {"bytes": step_bytes, "GBps": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
                  "frac": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                  "kernel_us_per_step": round(r.kernel_ms_per_step * 1000, 2), "graph_us_per_step": round(r.ms_per_step * 1000, 2),
+                 "host_launch_us_per_step": round(r.launch_ms_per_step * 1000, 2),
                  "kernels_per_step": r.kernels_per_step},
         "stream": stream,
         "other_configs": other,

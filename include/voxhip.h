@@ -435,7 +435,9 @@ enum voxhip_kernel_class {
     VOXHIP_K_COMBINE = 6,  /* merge of the attention splits */
     VOXHIP_K_QKPOST = 7,   /* q/k RMSNorm, RoPE, f16 K/V append */
     VOXHIP_K_SAMPLE = 8,   /* device sampler */
-    VOXHIP_K_CLASSES = 9
+    VOXHIP_K_FFN = 9,      /* one-row FFN in one launch: RMSNorm + gate|up + SwiGLU + down, product into accumulators */
+    VOXHIP_K_FOLD = 10,    /* the last layer's accumulated FFN product into h */
+    VOXHIP_K_CLASSES = 11
 };
 
 /* Times `steps` replays of the captured decode graph (after `warmup` untimed ones) with HIP events on the
@@ -444,6 +446,8 @@ enum voxhip_kernel_class {
  * durations and the algorithmic bytes one launch of each class moves. */
 typedef struct voxhip_bench_result {
     double ms_per_step;         /* whole decode step (graph replay), average */
+    double launch_ms_per_step;  /* host time of one hipGraphLaunch call in the timed loop (a step is host-bound when this
+                                   approaches ms_per_step) */
     double kernel_ms_per_step;  /* sum of the kernel durations of one step (event-stamped run) */
     double step_bytes;          /* algorithmic HBM bytes per step (weights + scales, KV read + write, norms) */
     int32_t kernels_per_step;

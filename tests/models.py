@@ -43,7 +43,7 @@ class Model:
     """A transformer in both host descriptions: `ox` for the oracle, `hx` for the HIP backend."""
 
     def __init__(self, seed, n_layers, hidden, heads, kv_heads, head_dim, inter, wtype=Q8, qk_norm=True, bias=False, theta=1e6,
-                 eps=1e-6, head_rows=0, head_type=None):
+                 eps=1e-6, head_rows=0, head_type=None, ffn_bias=False):
         from vox_amd import voxhip
         rng = np.random.default_rng(seed)
         self.hidden, self.heads, self.kv_heads, self.head_dim, self.inter = hidden, heads, kv_heads, head_dim, inter
@@ -58,7 +58,7 @@ class Model:
         for _ in range(n_layers):
             oL, hL = {}, {}
             for n, (r, c) in shapes.items():
-                d, s, b = make_mat(rng, wtype, r, c, bias=bias and n in ("q", "k", "v"))
+                d, s, b = make_mat(rng, wtype, r, c, bias=(bias and n in ("q", "k", "v")) or (ffn_bias and n in ("gate", "up", "down")))
                 oL[n] = po.Mat(wtype, d, r, c, s, b)
                 hL[n] = voxhip.HostMat(wtype, d, r, c, s, b)
             for n in ("ln1", "ln2"):

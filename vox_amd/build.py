@@ -17,7 +17,7 @@ OUT = os.path.join(ROOT, "vox_amd")
 BUILD = os.path.join(ROOT, "vox_amd", "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-HIP_SOURCES = ["voxhip_runtime.hip", "vh_kernels_misc.hip", "vh_gemm.hip", "vh_lm.hip", "vh_f5.hip", "vh_codec.hip", "vh_gemv_tile.hip", "vh_gemv_q8.hip", "vh_gemv_q4.hip", "vh_gemv_q4h.hip",
+HIP_SOURCES = ["voxhip_runtime.hip", "vh_kernels_misc.hip", "vh_gemm.hip", "vh_lm.hip", "vh_f5.hip", "vh_codec.hip", "vh_gemv_tile.hip", "vh_ffn.hip", "vh_gemv_q8.hip", "vh_gemv_q4.hip", "vh_gemv_q4h.hip",
                "vh_gemv_q8f.hip",
                "vh_gemv_f32.hip", "vh_gemv_f16.hip", "vh_gemv_bf16.hip"]
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",

@@ -286,10 +286,43 @@ __global__ __launch_bounds__(kGemvThreads) void k_quant_rows(GemvArgs a, int8_t 
     });
 }
 
+// Fixed-point form of the FFN's down product: units of 2^-32, summed exactly (and so in any order) by integer
+// atomics. |v| must stay below 2^31.
+constexpr float kFixOne = 4294967296.0f;
+VH_DEV int64_t fix_of(float v) { return int64_t(__builtin_rintf(v * kFixOne)); }
+// The pending value of element i: the kAccCopies partial sums added as integers, then one rounding to float.
+VH_DEV float acc_value(const int64_t (&c)[kAccCopies]) {
+    int64_t t = 0;
+#pragma unroll
+    for (int k = 0; k < kAccCopies; ++k) t += c[k];
+    return float(t) * (1.0f / kFixOne);
+}
+
+// The residual an EPI_ACC lane adds to, read with the prologue's inputs at kernel start (the epilogue would otherwise
+// wait one more global round trip at the end), plus, with ACC, the rows' pending FFN sums. Lane r*M + mm holds
+// row0 + r, input row mm.
+template <int M, int R, int EPI, bool ACC>
+struct EpiPre {
+    float y = 0.f;
+    int64_t c[kAccCopies];
+};
+template <int M, int R, int EPI, bool ACC>
+VH_DEV void epi_prefetch(const GemvArgs &a, int rows, int lane, int row0, EpiPre<M, R, EPI, ACC> &e) {
+    if constexpr (EPI == EPI_ACC) {
+        const int r = lane / M, mm = lane % M, row = row0 + r;
+        const bool ok = lane < R * M && row < rows && mm < a.m;
+        const float *src = a.res ? a.res : a.y;
+        e.y = src[ok ? int64_t(mm) * a.ldy + row : 0];  // branch-free: other lanes read element 0 and drop it
+        if constexpr (ACC)
+#pragma unroll
+            for (int k = 0; k < kAccCopies; ++k) e.c[k] = a.acc[k * a.acc_ld + (ok ? row : 0)];
+    }
+}
+
 // Epilogue: lane r*M + mm holds the total of (row0 + r, input row mm). SwiGLU pairs rows (2u, 2u+1) =
 // (gate u, up u); the partner value is fetched with all lanes active, then only valid lanes store.
-template <int M, int R, int EPI>
-VH_DEV void store_out(const GemvArgs &a, int rows, float out, int lane, int row0) {
+template <int M, int R, int EPI, bool ACC>
+VH_DEV void store_out(const GemvArgs &a, int rows, float out, int lane, int row0, const EpiPre<M, R, EPI, ACC> &e) {
     const int r = lane / M, mm = lane % M, row = row0 + r;
     const bool ok = lane < R * M && row < rows && mm < a.m;
     const float v = out + ((ok && a.bias) ? a.bias[row] : 0.f);
@@ -297,8 +330,17 @@ VH_DEV void store_out(const GemvArgs &a, int rows, float out, int lane, int row0
         const float other = __shfl_xor(v, M, kWave);  // lane of row r ^ 1, same input row
         if (ok && (r & 1) == 0) a.y[int64_t(mm) * a.ldy + row / 2] = silu(v) * other;
     } else if (ok) {
-        if (EPI == EPI_STORE) a.y[int64_t(mm) * a.ldy + row] = v;
-        else a.y[int64_t(mm) * a.ldy + row] += v;
+        if (EPI == EPI_STORE) {
+            a.y[int64_t(mm) * a.ldy + row] = v;
+        } else {
+            float base = e.y;
+            if constexpr (ACC) {  // the FFN's residual add first, then this product's (one row: mm == 0)
+                base = base + acc_value(e.c);
+#pragma unroll
+                for (int k = 0; k < kAccCopies; ++k) a.acc[k * a.acc_ld + row] = 0;
+            }
+            a.y[int64_t(mm) * a.ldy + row] = base + v;
+        }
     }
 }
 
@@ -315,11 +357,13 @@ VH_DEV void reduce_store_prep(float (&acc)[R][M], float &out, int lane) {
 }
 
 // ------------------------------------------------------------------------------------------ int8 path
-template <int WT, int M, int R, int IT, int PRO, int EPI, bool STAGE>
+// ACC (one row): the input or the residual carries pending FFN sums (GemvArgs::acc).
+template <int WT, int M, int R, int IT, int PRO, int EPI, bool STAGE, bool ACC = false>
 // The weight stream's operands come first so they are preloaded into SGPRs with the dispatch (kernarg preload).
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__restrict__ w, const float *__restrict__ scale,
                                                        const float *x, int32_t rows, int32_t K, GemvArgs a) {
     static_assert(WT == WT_Q8 || WT == WT_Q4 || WT == WT_Q4H, "int path is Q8/Q4");
+    static_assert(!ACC || (M == 1 && STAGE && (PRO == PRO_RMS || EPI == EPI_ACC)), "pending sums: one staged row");
     extern __shared__ __align__(16) uint8_t smem[];
     const int nb = K / 32;
     int8_t *xq = reinterpret_cast<int8_t *>(smem);                 // [M][K]
@@ -354,9 +398,32 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__rest
     };
     constexpr int PS = PRO == PRO_Q ? PRO_X : PRO;  // PRO_Q stages nothing
     ProStage<M, PS> st;
+    EpiPre<M, R, EPI, ACC> ep;
+    int64_t xa[kAccCopies][8];  // ACC + PRO_RMS: the pending sums of this thread's slot (K <= 8 * kGemvThreads)
     if constexpr (STAGE && PRO != PRO_Q) pro_stage<M, PS>(a, x, K, st);  // the prologue's inputs first: loads return in issue order
+    if constexpr (ACC && PRO == PRO_RMS) {
+        const int sl = int(threadIdx.x) < K / 8 ? int(threadIdx.x) : 0;
+#pragma unroll
+        for (int k = 0; k < kAccCopies; ++k)
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                const i64x2 t = *reinterpret_cast<const i64x2 *>(a.acc + k * a.acc_ld + sl * 8 + j);
+                xa[k][j] = t.x;
+                xa[k][j + 1] = t.y;
+            }
+    }
+    epi_prefetch(a, rows, lane, row0, ep);
     __builtin_amdgcn_sched_barrier(0);                                  // keep the weight stream behind them
     load(0);
+    if constexpr (ACC && PRO == PRO_RMS) {  // x + the FFN's pending residual sums, as the reference's residual add
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            int64_t c[kAccCopies];
+#pragma unroll
+            for (int k = 0; k < kAccCopies; ++k) c[k] = xa[k][j];
+            st.x[0][j] = st.x[0][j] + acc_value(c);
+        }
+    }
 
     if constexpr (PRO == PRO_Q) {  // the rows come quantized: copy them (rows past a.m as zeros)
         const int n16 = M * K / 16;
@@ -436,7 +503,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__rest
     }
     float out;
     reduce_store_prep<R, M>(acc, out, lane);
-    store_out<M, R, EPI>(a, rows, out, lane, row0);
+    store_out<M, R, EPI, ACC>(a, rows, out, lane, row0, ep);
 }
 
 // ------------------------------------------------------------------------------------------ f32 path
@@ -478,7 +545,9 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_flt(const uint8_t *__rest
         }
     };
     ProStage<M, PRO> st;
+    EpiPre<M, R, EPI, false> ep;
     if constexpr (STAGE) pro_stage<M, PRO>(a, x, K, st);
+    epi_prefetch(a, rows, lane, row0, ep);
     __builtin_amdgcn_sched_barrier(0);
     load(0);
 
@@ -534,7 +603,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_flt(const uint8_t *__rest
     }
     float out;
     reduce_store_prep<R, M>(acc, out, lane);
-    store_out<M, R, EPI>(a, rows, out, lane, row0);
+    store_out<M, R, EPI, false>(a, rows, out, lane, row0, ep);
 }
 
 }  // namespace vh

@@ -7,16 +7,18 @@
 
 namespace vh {
 
-template <int WT, int M, int R, int IT, int PRO, int EPI, bool INT, bool STAGE>
+template <int WT, int M, int R, int IT, int PRO, int EPI, bool INT, bool STAGE, bool ACC>
 hipError_t gemv_run_staged(const GemvArgs &a, hipStream_t s) {
     const int per_block = (kGemvThreads / 64) * R;
     const dim3 grid((a.rows + per_block - 1) / per_block), block(kGemvThreads);
     if constexpr (INT) {
         // xq [M][K] int8, xs [M][K/32] f32, red [M][4], xsum [M][K/32] int32 (Q4)
         const size_t smem = size_t(M) * a.K + size_t(M) * (a.K / 32) * 4 + size_t(M) * 16 + (WT == WT_Q8 ? 0 : size_t(M) * (a.K / 32) * 4);
-        hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_gemv_int<WT, M, R, IT, PRO, EPI, STAGE>), smem);
+        hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_gemv_int<WT, M, R, IT, PRO, EPI, STAGE, ACC>), smem);
         if (e != hipSuccess) return e;
-        return launch(k_gemv_int<WT, M, R, IT, PRO, EPI, STAGE>, grid, block, smem, s, a.w, a.scale, a.x, a.rows, a.K, a);
+        return launch(k_gemv_int<WT, M, R, IT, PRO, EPI, STAGE, ACC>, grid, block, smem, s, a.w, a.scale, a.x, a.rows, a.K, a);
+    } else if constexpr (ACC) {
+        return hipErrorInvalidValue;  // pending FFN sums come with int-path layers only
     } else {
         const size_t smem = size_t(M) * a.K * 4 + size_t(M) * 16;
         hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_gemv_flt<WT, M, R, IT, PRO, EPI, STAGE>), smem);
@@ -25,19 +27,25 @@ hipError_t gemv_run_staged(const GemvArgs &a, hipStream_t s) {
     }
 }
 
-// Staged prologue (inputs loaded ahead of the weight stream) when they fit the staging registers.
-template <int WT, int M, int R, int IT, int PRO, int EPI, bool INT>
+// Staged prologue (inputs loaded ahead of the weight stream) when they fit the staging registers. ACC: the row's
+// pending FFN sums, staged with one input slot per thread.
+template <int WT, int M, int R, int IT, int PRO, int EPI, bool INT, bool ACC>
 hipError_t gemv_run(const GemvArgs &a, hipStream_t s) {
-    if constexpr (PRO != PRO_Q)
-        if (pro_stageable<M, PRO>(a.K)) return gemv_run_staged<WT, M, R, IT, PRO, EPI, INT, true>(a, s);
-    return gemv_run_staged<WT, M, R, IT, PRO, EPI, INT, false>(a, s);
+    if constexpr (ACC) {
+        if (a.K / 8 > kGemvThreads || a.m != 1) return hipErrorInvalidValue;
+        return gemv_run_staged<WT, M, R, IT, PRO, EPI, INT, true, true>(a, s);
+    } else {
+        if constexpr (PRO != PRO_Q)
+            if (pro_stageable<M, PRO>(a.K)) return gemv_run_staged<WT, M, R, IT, PRO, EPI, INT, true, false>(a, s);
+        return gemv_run_staged<WT, M, R, IT, PRO, EPI, INT, false, false>(a, s);
+    }
 }
 
 // The (R, IT) tiles instantiated; gemv_tile() (vh_gemv_tile.cpp) picks only these.
-template <int WT, int M, int PRO, int EPI, bool INT>
+template <int WT, int M, int PRO, int EPI, bool INT, bool ACC = false>
 hipError_t gemv_by_tile(int R, int IT, const GemvArgs &a, hipStream_t s) {
 #define VH_TILE(r, it) \
-    if (R == r && IT == it) return gemv_run<WT, M, r, it, PRO, EPI, INT>(a, s);
+    if (R == r && IT == it) return gemv_run<WT, M, r, it, PRO, EPI, INT, ACC>(a, s);
     if constexpr (PRO == PRO_Q) {  // pre-quantized rows: larger tiles, fewer copies of the rows per launch
         if constexpr (EPI == EPI_SWIGLU) {
             VH_TILE(2, 1) VH_TILE(4, 1) VH_TILE(8, 1)
@@ -71,7 +79,12 @@ hipError_t gemv_by_m(int M, int R, int IT, const GemvArgs &a, hipStream_t s) {
         else return hipErrorInvalidValue;
     }
     switch (M) {
-        case 1: return gemv_by_tile<WT, 1, PRO, EPI, INT>(R, IT, a, s);
+        case 1:
+            // one row after a fused FFN: q|k|v (RMS + store) and o (attention merge + residual) add its pending sums
+            if constexpr (INT && ((PRO == PRO_RMS && EPI == EPI_STORE) || (PRO == PRO_ATTN && EPI == EPI_ACC)))
+                if (a.acc) return gemv_by_tile<WT, 1, PRO, EPI, INT, true>(R, IT, a, s);
+            if (a.acc) return hipErrorInvalidValue;
+            return gemv_by_tile<WT, 1, PRO, EPI, INT>(R, IT, a, s);
         case 2: if constexpr (INT) return gemv_by_tile<WT, 2, PRO, EPI, INT>(R, IT, a, s); else return hipErrorInvalidValue;
         case 4: return gemv_by_tile<WT, 4, PRO, EPI, INT>(R, IT, a, s);
         case 8: if constexpr (INT) return gemv_by_tile<WT, 8, PRO, EPI, INT>(R, IT, a, s); else return hipErrorInvalidValue;

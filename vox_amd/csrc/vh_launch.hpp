@@ -119,6 +119,16 @@ hipError_t launch_mat_gather(const uint8_t *w, const void *scale, int wt, int s1
 // A pass of the code-predictor frame loop: row table + RoPE rows of the pass, the sampled code's embedding row.
 hipError_t launch_pred_embed(const PredEmbedArgs &a, hipStream_t s);
 
+// The fused one-row FFN (k_ffn_int): Q8 / Q4 / Q4H layers with H % 32 == 0, I % 32 == 0, H <= 4096; the down weights
+// as panels (launch_panel_pack); adds its down product to a.acc (zero on entry) in fixed point.
+bool ffn_shape_ok(int wt, int H, int I);
+int ffn_parts();
+hipError_t launch_ffn(int wt, const FfnArgs &a, hipStream_t s);
+// Down weights [H][I] + scales [H][I/32] into panels [I/32][H][32 columns] + [I/32][H] (pw, ps hold as many bytes).
+hipError_t launch_panel_pack(int wt, const uint8_t *w, const void *scale, int H, int I, uint8_t *pw, void *ps, hipStream_t s);
+// h += the pending sums of acc [kAccCopies][H]; acc back to zero.
+hipError_t launch_acc_fold(float *h, int64_t *acc, int H, hipStream_t s);
+
 // Shared-memory opt-in above 64 KiB, once per kernel.
 hipError_t ensure_smem(const void *kernel, size_t bytes);
 

@@ -58,6 +58,35 @@ struct GemvArgs {
     const int8_t *q;
     const float *qs;
     const int32_t *qsum;
+    // One-row passes after a fused FFN (k_ffn_int): the FFN's down product still pending as fixed-point sums
+    // [kAccCopies][acc_ld]. PRO_RMS adds them to x before the norm; EPI_ACC adds them to y before its own product
+    // (the two residual adds in the reference's order) and sets the rows it consumed to zero.
+    int64_t *acc;
+    int64_t acc_ld;
+    // EPI_ACC: the residual rows to add to ([m][ldy]); null: y itself (y += product)
+    const float *res;
+};
+
+// Copies of the fixed-point down accumulators: FFN blocks of group g add into copy g % kAccCopies, so fewer
+// blocks meet on one cache line; readers sum the copies.
+constexpr int kAccCopies = 4;
+
+// The decode FFN of one row as one launch (k_ffn_int): RMSNorm(x, gamma), the gate|up GEMV, SwiGLU, the
+// activation quantization of the SwiGLU output per 32-block, and the down product split by its input columns:
+// block group g owns SwiGLU outputs 32g .. 32g+31 (one quantization block) and adds its share of every down row
+// into acc. The down weights come repacked as panels of 32 columns, so a group's share is contiguous.
+struct FfnArgs {
+    const uint8_t *gu;    // gate|up rows (2u, 2u + 1) = (gate u, up u), [2I][row bytes of H]
+    const float *gu_s;    // [2I][H/32] block scales (f16 values for WT_Q4H)
+    const float *gu_b;    // [2I] or null
+    const uint8_t *dp;    // down panels [I/32][H][row bytes of 32 columns]
+    const float *dp_s;    // panel scales [I/32][H] (f16 values for WT_Q4H)
+    const float *d_b;     // down bias [H] or null (added once, by group 0)
+    const float *x;       // the input row [H]
+    const float *gamma;   // [H]
+    int64_t *acc;         // [kAccCopies][H] fixed-point (2^-32) sums of the down product
+    int32_t H, I, parts;  // parts: blocks per group, each taking H / parts of the down rows
+    float eps;
 };
 
 constexpr int kGemvThreads = 256;

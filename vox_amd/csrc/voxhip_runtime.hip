@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <array>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -76,6 +77,9 @@ struct LayerDev {
     int qkv = -1, o = -1, gu = -1, down = -1;
     size_t ln1 = 0, ln2 = 0, qn = 0, kn = 0;
     bool qk = false;
+    // the down weights as 32-column panels for the fused one-row FFN (k_ffn_int), when the transformer has it
+    uint8_t *pan = nullptr;
+    void *pan_s = nullptr;
 };
 
 // A captured decode step: m rows of one sequence (steps = 0), or one row for each of m sequences (steps = 1).
@@ -121,6 +125,10 @@ struct Xfmr {
     _Float16 *pa16 = nullptr, *pb16 = nullptr;
     float *pm = nullptr, *pl = nullptr, *po = nullptr, *logits = nullptr;
     int64_t xin_elems = 0, logits_elems = 0;
+    // fused one-row FFN: every layer's FFN is one k_ffn_int launch whose down product reaches h through acc
+    // ([kAccCopies][H] fixed-point sums, zero between passes)
+    bool ffn_fuse = false;
+    int64_t *acc = nullptr;
     // per-row cache views of the next pass, followed by each row's RoPE row ([cap_rows][hd] (cos, sin) pairs)
     RowRef *rows_dev = nullptr, *rows_host = nullptr;
     float *rope_rows_dev = nullptr;
@@ -412,10 +420,15 @@ PassScratch lib_scratch() { return {g.gemm_ws, kGemmWsFloats, g.qrows, g.qrows_s
 // One matrix pass: y (=, +=, swiglu) W * prologue(x) for mc rows. On the GEMM path the prologue runs as its own
 // kernel into pre ([mc][cols]; xnorm instead when the normed rows are wanted). sc: the pass's scratch (null: the
 // library's).
+// acc (one row on the int path): the fused FFN's pending sums, added to x (PRO_RMS) or to y before the product
+// (EPI_ACC, which also clears the rows it consumed).
 void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, int64_t ldx, int mc, float *y, int64_t ldy,
           const float *gamma, float eps, float *xnorm, hipStream_t s, const AttnPartials *attn = nullptr,
-          float *pre = nullptr, const PassScratch *scp = nullptr) {
+          float *pre = nullptr, const PassScratch *scp = nullptr, int64_t *acc = nullptr, const float *res = nullptr) {
     const PassScratch sc = scp ? *scp : lib_scratch();
+    if (acc && (mc != 1 || !int_path(m, m_total) || !(pro == PRO_RMS || epi == EPI_ACC)))
+        throw Fail("pending FFN sums on a pass that cannot take them");
+    if (res && (epi != EPI_ACC || gemm_path(m, m_total, mc))) throw Fail("separate residual on a pass that cannot take it");
     if (pro == PRO_ATTN && (!attn || int64_t(attn->heads) * attn->hd != m.cols))
         throw Fail("attention partials do not match the o projection");
     if (gemm_path(m, m_total, mc)) {
@@ -441,6 +454,9 @@ void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, in
     a.w = m.w; a.scale = m.s; a.bias = m.b; a.x = x; a.gamma = gamma; a.y = y; a.xnorm = xnorm;
     a.ldx = ldx; a.ldy = ldy; a.rows = int32_t(m.rows); a.K = int32_t(m.cols); a.m = mc; a.eps = eps;
     if (pro == PRO_ATTN) a.attn = *attn;
+    a.acc = acc;
+    a.acc_ld = pro == PRO_RMS ? m.cols : m.rows;
+    a.res = res;
     const bool ip = int_path(m, m_total);
     if (ip && mc >= kQuantRowsMin && mc <= 8 && int64_t(mc) * m.cols <= sc.q_elems &&
         (epi == EPI_STORE || epi == EPI_ACC || epi == EPI_SWIGLU)) {
@@ -586,8 +602,11 @@ AttnPartials partials_of(const Xfmr &X) {
     return p;
 }
 
-// Kernels per layer: fused (rows of distinct sequences: decode, pairs, B sessions) 5, else 6 (+ k_qk_post).
-int kernels_per_layer(bool fused) { return fused ? 5 : 6; }
+// Whether a pass takes the fused one-row FFN: one row, the fused attention, a transformer that has the panels.
+bool ffn_pass(const Xfmr &X, int mc, int64_t m_total, bool fused) { return X.ffn_fuse && fused && mc == 1 && m_total == 1; }
+// Kernels per layer: fused (rows of distinct sequences: decode, pairs, B sessions) 5, else 6 (+ k_qk_post); the
+// fused FFN makes it 4 (and adds one accumulator fold per pass).
+int kernels_per_layer(const Xfmr &X, int mc, bool fused) { return ffn_pass(X, mc, mc, fused) ? 4 : fused ? 5 : 6; }
 
 // All layers for mc rows whose input is in X.h (row i at the position in rows_dev[i]).
 // m_total: the caller's total row count, which picks the q8 arithmetic (int8 for <= 8, f32 above).
@@ -637,13 +656,20 @@ void prepare_planes(Xfmr &X, int first, int count, int64_t m_total, int mc, hipS
         }
 }
 
-void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipStream_t s, bool fused, Probe *pr = nullptr) {
+// x0 (optional): the input rows ([mc][H]) when they are not in X.h yet. The first layer's q|k|v GEMV then reads them
+// and its o GEMV adds its product to them into X.h, where the fused attention path allows; otherwise they are copied.
+void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipStream_t s, bool fused, Probe *pr = nullptr,
+                    const float *x0 = nullptr) {
     const int qd = X.heads * X.hd, kd = X.kvh * X.hd, ldqkv = qd + 2 * kd;
     const AttnPartials part = partials_of(X);
     const bool rows_attn = any_hd(X);
     if (rows_attn) fused = false;
     const bool pass_attn = pass_attn_of(X, mc, fused);
+    const bool direct = x0 && count > 0 && !rows_attn && !pass_attn && !gemm_path(g.mats[size_t(X.L[size_t(first)].o)], m_total, mc);
+    if (x0 && !direct) HIPCHECK(hipMemcpyAsync(X.h, x0, size_t(mc) * X.H * 4, hipMemcpyDeviceToDevice, s));
+    const bool ffn = !rows_attn && !pass_attn && ffn_pass(X, mc, m_total, fused);
     bool pa_normed = false;  // planes: the previous layer's down reduce already wrote this layer's first RMSNorm
+    bool acc_live = false;   // the previous layer's fused FFN left its down product in X.acc (added by q|k|v and o)
     for (int li = first; li < first + count; ++li) {
         const LayerDev &L = X.L[size_t(li)];
         const GpuMat &Mqkv = g.mats[size_t(L.qkv)], &Mo = g.mats[size_t(L.o)], &Mgu = g.mats[size_t(L.gu)],
@@ -672,8 +698,8 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
                 if (!pa_normed) HIPCHECK(launch_rmsnorm_rows_h16(X.h, X.H, X.norms + L.ln1, int(X.H), X.eps, X.pa16, X.H, PA, mc, s));
                 hh(Mqkv, EPI_STORE, X.pa16, PA, X.qkv, ldqkv);
             } else {
-                gemv(Mqkv, m_total, PRO_RMS, EPI_STORE, X.h, X.H, mc, X.qkv, ldqkv, X.norms + L.ln1, X.eps, nullptr, s, nullptr,
-                     X.pre);
+                gemv(Mqkv, m_total, PRO_RMS, EPI_STORE, direct && li == first ? x0 : X.h, X.H, mc, X.qkv, ldqkv, X.norms + L.ln1, X.eps,
+                     nullptr, s, nullptr, X.pre, nullptr, acc_live ? X.acc : nullptr);
             }
         });
         if (!fused) {
@@ -709,8 +735,20 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
                 HIPCHECK(launch_attention(aa, r0.k, r0.v, r0.cap, X.qkv, X.rope_rows_dev, li, X.hd, X.heads / X.kvh, mc, fused, s));
             });
             probed(pr, VOXHIP_K_O, [&] {
-                gemv(Mo, m_total, PRO_ATTN, EPI_ACC, nullptr, 0, mc, X.h, X.H, nullptr, 0.f, nullptr, s, &part, X.pre);
+                gemv(Mo, m_total, PRO_ATTN, EPI_ACC, nullptr, 0, mc, X.h, X.H, nullptr, 0.f, nullptr, s, &part, X.pre, nullptr,
+                     acc_live ? X.acc : nullptr, direct && li == first ? x0 : nullptr);
             });
+            acc_live = false;
+        }
+        if (ffn) {  // RMSNorm, gate|up, SwiGLU and the down product in one launch; h gets the product via X.acc
+            FfnArgs fa{};
+            fa.gu = Mgu.w; fa.gu_s = Mgu.s; fa.gu_b = Mgu.b;
+            fa.dp = L.pan; fa.dp_s = static_cast<const float *>(L.pan_s); fa.d_b = Md.b;
+            fa.x = X.h; fa.gamma = X.norms + L.ln2; fa.acc = X.acc;
+            fa.H = X.H; fa.I = X.I; fa.parts = ffn_parts(); fa.eps = X.eps;
+            probed(pr, VOXHIP_K_FFN, [&] { HIPCHECK(launch_ffn(gemv_type(Mgu), fa, s)); });
+            acc_live = true;
+            continue;
         }
         probed(pr, VOXHIP_K_GATEUP, [&] {
             if (planes) {
@@ -734,6 +772,8 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
             }
         });
     }
+    // the last fused FFN's product into h, so every pass leaves h whole and the accumulators at zero
+    if (acc_live) probed(pr, VOXHIP_K_FOLD, [&] { HIPCHECK(launch_acc_fold(X.h, X.acc, X.H, s)); });
 }
 
 // Final RMSNorm of rows [r0, r0 + mr) of X.h into X.xnorm, and the head on them when head >= 0.
@@ -885,6 +925,38 @@ const char *kWhich[7] = {"q", "k", "v", "o", "gate", "up", "down"};
 
 // codec: the codec's pre-transformer, whose forward (sliding window, layer scales, f32 ring) is the codec's own; only
 // its matrices, norms and scratch come from here.
+// The fused one-row FFN applies when every layer's four matrices take the int path at one row (Q8 / Q4), gate|up
+// and down share a format and the shapes fit k_ffn_int and the staged q|k|v prologue that adds the pending sums
+// (H <= 8 * 256); the attention is the fused kernel (head_dim 64 or 128). The down weights are then also kept as
+// panels (one more copy of them).
+void make_ffn_panels(Xfmr &X) {
+    const char *env = std::getenv("VOXHIP_FFN_FUSED");
+    // Where it pays: the next layer's q|k|v GEMV must then read the pending sums, which costs about what the second
+    // launch saved at FFN width 3 H (the Qwen3-TTS talker and code predictor), while FFNs of 4 H and wider (the
+    // CosyVoice2 LM's 896 -> 4864) gain. VOXHIP_FFN_FUSED=1 forces it on, =0 off.
+    const bool force = env && env[0] == '1';
+    bool ok = !(env && env[0] == '0') && (force || int64_t(X.I) >= 4 * int64_t(X.H)) && (X.hd == 64 || X.hd == 128) &&
+              X.H <= 8 * kGemvThreads && !X.L.empty();
+    for (const LayerDev &L : X.L) {
+        if (!ok) break;
+        for (int id : {L.qkv, L.o, L.gu, L.down}) ok = ok && quantized(g.mats[size_t(id)].type);
+        const GpuMat &GU = g.mats[size_t(L.gu)], &D = g.mats[size_t(L.down)];
+        ok = ok && gemv_type(GU) == gemv_type(D) && ffn_shape_ok(gemv_type(D), X.H, X.I);
+    }
+    if (!ok) return;
+    for (LayerDev &L : X.L) {
+        const GpuMat &D = g.mats[size_t(L.down)];
+        const size_t nbytes = size_t(D.rows) * row_bytes(D.type, D.cols), sbytes = size_t(D.rows) * scale_row_bytes(D);
+        L.pan = static_cast<uint8_t *>(dalloc(nbytes));
+        L.pan_s = dalloc(sbytes);
+        HIPCHECK(launch_panel_pack(gemv_type(D), D.w, D.s, X.H, X.I, L.pan, L.pan_s, g.stream));
+    }
+    X.acc = static_cast<int64_t *>(dalloc(size_t(kAccCopies) * size_t(X.H) * sizeof(int64_t)));
+    HIPCHECK(hipMemsetAsync(X.acc, 0, size_t(kAccCopies) * size_t(X.H) * sizeof(int64_t), g.stream));
+    HIPCHECK(hipStreamSynchronize(g.stream));
+    X.ffn_fuse = true;
+}
+
 int make_xfmr(const voxhip_xfmr_desc *w, const char *name, int use_layers, const int32_t *mats, voxhip_uploaded_fn uploaded,
               void *user, bool codec = false) {
     require_ok();
@@ -978,6 +1050,7 @@ int make_xfmr(const voxhip_xfmr_desc *w, const char *name, int use_layers, const
         X->final_off = push(w->final_norm, w->hidden);
         X->norms = dalloc_t<float>(nv.size());
         h2d(X->norms, nv.data(), nv.size() * 4);
+        make_ffn_panels(*X);
         ensure_rows(*X, kMaxM);
         ensure_rope(*X, 4096);
     } catch (...) {
@@ -1458,9 +1531,8 @@ int enqueue_decode(Xfmr &X, int m, int head, const float *d_x, float *d_out_last
     const bool fused = steps || m == 1;
     const int r0 = steps ? 0 : m - 1, mr = steps ? m : 1;
     int kernels = 0;
-    HIPCHECK(hipMemcpyAsync(X.h, d_x, size_t(m) * X.H * 4, hipMemcpyDeviceToDevice, s));
-    enqueue_layers(X, m, m, 0, X.layers, s, fused, pr);
-    kernels += kernels_per_layer(fused) * X.layers;
+    enqueue_layers(X, m, m, 0, X.layers, s, fused, pr, d_x);
+    kernels += kernels_per_layer(X, m, fused) * X.layers + (ffn_pass(X, m, m, fused) ? 1 : 0);
     probed(head >= 0 ? pr : nullptr, VOXHIP_K_HEAD, [&] { enqueue_final(X, r0, mr, head, s); });
     kernels += 1;
     if (d_out_last) HIPCHECK(hipMemcpyAsync(d_out_last, X.xnorm, size_t(mr) * X.H * 4, hipMemcpyDeviceToDevice, s));
@@ -3252,12 +3324,15 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, const float *d_x, int h
             for (auto &e : ev) HIPCHECK(hipEventCreate(&e));
             HIPCHECK(hipStreamSynchronize(g.stream));
             HIPCHECK(hipEventRecord(ev[0], g.stream));
+            const auto h0 = std::chrono::steady_clock::now();
             for (int i = 0; i < steps; ++i) HIPCHECK(hipGraphLaunch(exec, g.stream));
+            const auto h1 = std::chrono::steady_clock::now();
             HIPCHECK(hipEventRecord(ev[1], g.stream));
             HIPCHECK(hipEventSynchronize(ev[1]));
             float ms = 0.f;
             HIPCHECK(hipEventElapsedTime(&ms, ev[0], ev[1]));
             out->ms_per_step = double(ms) / steps;
+            out->launch_ms_per_step = std::chrono::duration<double, std::milli>(h1 - h0).count() / steps;
             mark("kernel by kernel");
             // ---- region B: the same step launched kernel by kernel (same enqueue path as the graph), each launch
             // stamped by its own events: hipExtLaunchKernel start/stop, or plain stream events around the launch
@@ -3279,7 +3354,8 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, const float *d_x, int h
                     ++k;
                 }
             };
-            const int per_step = kernels_per_layer(true) * X.layers + (head >= 0 ? 1 : 0) + (cfg && head >= 0 ? 1 : 0);
+            const int per_step = kernels_per_layer(X, 1, true) * X.layers + (ffn_pass(X, 1, 1, true) ? 1 : 0) + (head >= 0 ? 1 : 0) +
+                                 (cfg && head >= 0 ? 1 : 0);
             const bool stamp = !profiler_attached();
             for (auto &e : ev) (void)hipEventDestroy(e);
             ev.assign(size_t(2 * per_step), nullptr);
@@ -3312,8 +3388,12 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, const float *d_x, int h
                 bytes[VOXHIP_K_O] += double(g.mats[size_t(L.o)].bytes) + partials + 2.0 * X.H * 4.0;
                 bytes[VOXHIP_K_GATEUP] += double(g.mats[size_t(L.gu)].bytes) + X.H * 4.0 + X.I * 4.0;
                 bytes[VOXHIP_K_DOWN] += double(g.mats[size_t(L.down)].bytes) + X.I * 4.0 + 2.0 * X.H * 4.0;
+                // fused FFN: both matrices, the input row in, the down product out
+                bytes[VOXHIP_K_FFN] += double(g.mats[size_t(L.gu)].bytes) + double(g.mats[size_t(L.down)].bytes) + 2.0 * X.H * 4.0;
             }
             for (int c = 0; c < 4; ++c) bytes[c] /= nl;
+            bytes[VOXHIP_K_FFN] /= nl;
+            bytes[VOXHIP_K_FOLD] = X.H * (2.0 * 4.0 + 2.0 * kAccCopies * 8.0);
             bytes[VOXHIP_K_ATTN] = 2.0 * double(pos0) * kd * 2.0 + (qd + 2.0 * kd) * 4.0 + 2.0 * kd * 2.0 + partials;
             if (head >= 0) {
                 const GpuMat &Hm = g.mats[size_t(head)];

@@ -138,11 +138,13 @@ class CodecDesc(C.Structure):
                 ("final_act", CodecSnake), ("final_conv", CodecConv)]
 
 
-KERNEL_CLASSES = ("qkv_gemv", "o_gemv", "gateup_gemv", "down_gemv", "head_gemv", "attention", "attn_combine", "qk_post", "sampler")
+KERNEL_CLASSES = ("qkv_gemv", "o_gemv", "gateup_gemv", "down_gemv", "head_gemv", "attention", "attn_combine", "qk_post", "sampler",
+                  "ffn", "acc_fold")
 
 
 class BenchResult(C.Structure):
-    _fields_ = [("ms_per_step", C.c_double), ("kernel_ms_per_step", C.c_double), ("step_bytes", C.c_double),
+    _fields_ = [("ms_per_step", C.c_double), ("launch_ms_per_step", C.c_double), ("kernel_ms_per_step", C.c_double),
+                ("step_bytes", C.c_double),
                 ("kernels_per_step", C.c_int32), ("n_classes", C.c_int32), ("kernel_stamped", C.c_int32),
                 ("class_ms", C.c_double * len(KERNEL_CLASSES)), ("class_bytes", C.c_double * len(KERNEL_CLASSES)),
                 ("class_launches", C.c_int32 * len(KERNEL_CLASSES))]
