@@ -13,8 +13,7 @@ Bars:
   f16-class `vox verify` max error (cli/main.cpp:796-803) <= 1e-2 as a gross-error guard;
 - whole steps by the reference's quantized-model criterion (KL <= 0.02, reference argmax in our top-5,
   cli/main.cpp:764-790, :826-827);
-- the head on the device's own state within 1e-3; sampled tokens bit-exact on the device's logits;
-- each session's batch-1 step (fused FFN) against its row of the batch-8 step by the same quantized criterion.
+- the head on the device's own state within 1e-3; sampled tokens bit-exact on the device's logits.
 """
 import numpy as np
 import pytest
@@ -73,19 +72,16 @@ def test_talker_1_7b_q4_b1_b8(hip, oracle):
     for b in range(B):
         assert rel_err(logits[b], oracle.matmul(head, out[b][None])[0]) < 1e-3
         assert toks[b] == oracle.sample_logits(logits[b], 0.9, 1.0, 50, 1.0, None, oracle.uniform(5, b, 0, 0)), b
-    # every row against a batch-1 step of the same session on the device. The batch-1 step takes the fused FFN, whose
-    # down product is summed in fixed point instead of float; over 28 requantizing layers that rounding difference
-    # grows as the device-vs-oracle difference does, so the bar is the same quantized-model criterion
+    # every row against a batch-1 step of the same session on the device (the B-row GEMVs give each row the
+    # same int8 arithmetic; only float summation order may differ)
     for b in range(B):
-        d1, o1, l1 = hip.DevBuf(H * 4), hip.DevBuf(H * 4), hip.DevBuf(V * 4)
+        d1 = hip.DevBuf(H * 4)
         d1.upload(x[b])
-        hip.decode_dev(dec.xfmr, seqs[b], pos, d1, 1, o1, dec.head, l1)
+        o1 = hip.DevBuf(H * 4)
+        hip.decode_dev(dec.xfmr, seqs[b], pos, d1, 1, o1)
         hip.sync()
-        h1, lg1 = o1.download(H, np.float32), l1.download(V, np.float32)
-        kl, top5 = kl_top5(lg1, logits[b])
-        print(f"row {b}: batch-1 vs batch-{B} hidden rel err {rel_err(h1, out[b]):.3e}, logits KL {kl:.2e}, top-5 {top5}")
-        assert kl <= 0.02 and top5 and rel_err(h1, out[b]) < 0.1, b
-        for bf in (d1, o1, l1):
-            bf.free()
+        assert rel_err(o1.download(H, np.float32), out[b]) < 1e-3, b
+        d1.free()
+        o1.free()
     for bf in (dx, dout, dlog, dtok):
         bf.free()
