@@ -43,7 +43,9 @@ int pow2_at_least(int v) {
 }  // namespace
 
 bool ffn_shape_ok(int wt, int H, int I) {
-    return (wt == WT_Q8 || wt == WT_Q4 || wt == WT_Q4H) && H > 0 && I > 0 && H % 32 == 0 && I % 32 == 0 && H <= kFfnMaxH;
+    // I <= 32768: at most 1024 groups add into one accumulator row (the fixed-point terms' range)
+    return (wt == WT_Q8 || wt == WT_Q4 || wt == WT_Q4H) && H > 0 && I > 0 && H % 32 == 0 && I % 32 == 0 && H <= kFfnMaxH &&
+           I <= 32 * 1024;
 }
 
 hipError_t launch_ffn(int wt, const FfnArgs &a, hipStream_t s) {

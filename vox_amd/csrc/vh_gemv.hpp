@@ -287,9 +287,15 @@ __global__ __launch_bounds__(kGemvThreads) void k_quant_rows(GemvArgs a, int8_t 
 }
 
 // Fixed-point form of the FFN's down product: units of 2^-32, summed exactly (and so in any order) by integer
-// atomics. |v| must stay below 2^31.
+// atomics. A term is clamped to +-2^21 (far outside activation ranges), so the sum of up to 1024 of them stays
+// inside int64; NaN becomes 0.
 constexpr float kFixOne = 4294967296.0f;
-VH_DEV int64_t fix_of(float v) { return int64_t(__builtin_rintf(v * kFixOne)); }
+VH_DEV int64_t fix_of(float v) {
+    const float lim = 9007199254740992.0f;  // 2^53 units = 2^21
+    float t = __builtin_rintf(v * kFixOne);
+    t = t == t ? fminf(fmaxf(t, -lim), lim) : 0.f;
+    return int64_t(t);
+}
 // The pending value of element i: the kAccCopies partial sums added as integers, then one rounding to float.
 VH_DEV float acc_value(const int64_t (&c)[kAccCopies]) {
     int64_t t = 0;

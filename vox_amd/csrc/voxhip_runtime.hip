@@ -944,16 +944,27 @@ void make_ffn_panels(Xfmr &X) {
         ok = ok && gemv_type(GU) == gemv_type(D) && ffn_shape_ok(gemv_type(D), X.H, X.I);
     }
     if (!ok) return;
-    for (LayerDev &L : X.L) {
-        const GpuMat &D = g.mats[size_t(L.down)];
-        const size_t nbytes = size_t(D.rows) * row_bytes(D.type, D.cols), sbytes = size_t(D.rows) * scale_row_bytes(D);
-        L.pan = static_cast<uint8_t *>(dalloc(nbytes));
-        L.pan_s = dalloc(sbytes);
-        HIPCHECK(launch_panel_pack(gemv_type(D), D.w, D.s, X.H, X.I, L.pan, L.pan_s, g.stream));
+    try {
+        for (LayerDev &L : X.L) {
+            const GpuMat &D = g.mats[size_t(L.down)];
+            const size_t nbytes = size_t(D.rows) * row_bytes(D.type, D.cols), sbytes = size_t(D.rows) * scale_row_bytes(D);
+            L.pan = static_cast<uint8_t *>(dalloc(nbytes));
+            L.pan_s = dalloc(sbytes);
+            HIPCHECK(launch_panel_pack(gemv_type(D), D.w, D.s, X.H, X.I, L.pan, L.pan_s, g.stream));
+        }
+        X.acc = static_cast<int64_t *>(dalloc(size_t(kAccCopies) * size_t(X.H) * sizeof(int64_t)));
+        HIPCHECK(hipMemsetAsync(X.acc, 0, size_t(kAccCopies) * size_t(X.H) * sizeof(int64_t), g.stream));
+        HIPCHECK(hipStreamSynchronize(g.stream));
+    } catch (const Fail &) {  // no room for the panels under the VRAM limit: the two-GEMV FFN needs none
+        (void)hipStreamSynchronize(g.stream);
+        for (LayerDev &L : X.L) {
+            dfree(L.pan); dfree(L.pan_s);
+            L.pan = nullptr; L.pan_s = nullptr;
+        }
+        dfree(X.acc);
+        X.acc = nullptr;
+        return;
     }
-    X.acc = static_cast<int64_t *>(dalloc(size_t(kAccCopies) * size_t(X.H) * sizeof(int64_t)));
-    HIPCHECK(hipMemsetAsync(X.acc, 0, size_t(kAccCopies) * size_t(X.H) * sizeof(int64_t), g.stream));
-    HIPCHECK(hipStreamSynchronize(g.stream));
     X.ffn_fuse = true;
 }
 
