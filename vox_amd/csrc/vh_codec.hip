@@ -1,4 +1,6 @@
 // Launchers of the Qwen3-TTS codec decoder kernels.
+#include <algorithm>
+
 #include "vh_codec.hpp"
 #include "vh_launch.hpp"
 
@@ -20,10 +22,11 @@ hipError_t launch_hist_shift(float *dst, const float *old, const float *x, int64
 }
 
 hipError_t launch_dwconv_causal(const float *x, const float *hist, const float *w, const float *b, float *y, int T, int C, int K,
-                                hipStream_t s) {
+                                hipStream_t s, float *hist_next) {
     if (T <= 0) return hipSuccess;
-    if (C <= 0 || K <= 0 || !w || !b || (K > 1 && !hist)) return hipErrorInvalidValue;
-    return launch(k_dwconv_causal, blocks_of(int64_t(T) * C), dim3(256), 0, s, x, hist, w, b, y, int32_t(T), int32_t(C), int32_t(K));
+    if (C <= 0 || K <= 0 || !w || !b || (K > 1 && !hist) || (hist_next && hist_next == hist)) return hipErrorInvalidValue;
+    const int64_t n = std::max<int64_t>(int64_t(T), hist_next ? int64_t(K - 1) : 0) * C;
+    return launch(k_dwconv_causal, blocks_of(n), dim3(256), 0, s, x, hist, w, b, y, int32_t(T), int32_t(C), int32_t(K), hist_next);
 }
 
 hipError_t launch_ola(const float *tmp, const float *tail_old, float *tail_new, const float *bias, float *y, int T, int stride,

@@ -31,10 +31,16 @@ __global__ __launch_bounds__(256) void k_hist_shift(float *__restrict__ dst, con
 
 // dwconv_stream (qwen3.cpp:123-137): y[t][c] = b[c] + sum_k w[c][k] ext[t + k][c] over ext = [hist (K - 1 rows); x],
 // taps in order. One thread per output.
+// hist_next (may be null): also written, the next call's history (k_hist_shift's rows) by threads i < (K - 1) C.
 __global__ __launch_bounds__(256) void k_dwconv_causal(const float *__restrict__ x, const float *__restrict__ hist,
                                                        const float *__restrict__ w, const float *__restrict__ b,
-                                                       float *__restrict__ y, int32_t T, int32_t C, int32_t K) {
+                                                       float *__restrict__ y, int32_t T, int32_t C, int32_t K,
+                                                       float *__restrict__ hist_next) {
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (hist_next && i < int64_t(K - 1) * C) {
+        const int j = int(i / C), c = int(i % C), r = j + T;  // row r of [hist; x]
+        hist_next[i] = r < K - 1 ? hist[int64_t(r) * C + c] : x[int64_t(r - (K - 1)) * C + c];
+    }
     if (i >= int64_t(T) * C) return;
     const int t = int(i / C), c = int(i % C), ctx = K - 1;
     float acc = b[c];

@@ -268,7 +268,8 @@ hipError_t launch_stream_conv(int wt, int epi, const uint8_t *w, const float *sc
                               hipStream_t s) {
     if (g.m <= 0) return hipSuccess;
     if (g.cig <= 0 || g.cig % 4 || g.ksize <= 0 || g.dil <= 0 || g.K != g.ksize * g.cig || g.K % 8 || g.lda % 4 || g.n <= 0 ||
-        g.ctx != (g.ksize - 1) * g.dil || (g.ctx && !g.hist) || !g.y)
+        g.ctx != (g.ksize - 1) * g.dil || (g.ctx && !g.hist) || !g.y ||
+        (g.hist_next && (!g.ctx || g.hist_next == g.hist)))
         return hipErrorInvalidValue;
     if (epi == EPI_STORE) return stream_conv_wt<EPI_STORE>(wt, w, scale, x, g, s);
     if (epi == EPI_SNAKE) return g.snake_a && g.snake_ib ? stream_conv_wt<EPI_SNAKE>(wt, w, scale, x, g, s) : hipErrorInvalidValue;

@@ -56,6 +56,19 @@ VH_DEV f32x4v gemm_load_a(const float *__restrict__ A, const GemmArgs &g, int ro
     return *reinterpret_cast<const f32x4v *>(A + (int64_t(s) * g.seq + tt) * g.lda + int64_t(grp) * g.cig + i);
 }
 
+// ASRC_STREAM with g.hist_next: this block's share of the next call's history, the last ctx rows of [hist; x]
+// (k_hist_shift's rows), split evenly over every block of the launch (x, y and the K slices of z).
+VH_DEV void stream_hist_next(const float *__restrict__ x, const GemmArgs &g) {
+    const int64_t total = int64_t(g.ctx) * g.cig;
+    const int64_t nb = int64_t(gridDim.x) * gridDim.y * gridDim.z;
+    const int64_t b = (int64_t(blockIdx.z) * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    const int64_t per = (total + nb - 1) / nb, i0 = b * per, i1 = min(total, i0 + per);
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+        const int j = int(i / g.cig), c = int(i % g.cig), r = j + g.m;  // row r of [hist; x]
+        g.hist_next[i] = r < g.ctx ? g.hist[int64_t(r) * g.cig + c] : x[int64_t(r - g.ctx) * g.lda + c];
+    }
+}
+
 // Eight consecutive W elements of row `row`, columns k..k+7, widened to f32.
 template <int WT>
 VH_DEV void gemm_load_w(const uint8_t *__restrict__ w, const float *__restrict__ scale, const GemmArgs &g, int row, int k,
@@ -249,6 +262,7 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const uint8_t *__restrict__ w,
             gemm_load_w<WT>(w, scale, g, n0 + (idx >> 2), k0 + (idx & 3) * 8, rw[q]);
         }
     };
+    if (ASRC == ASRC_STREAM && g.hist_next) stream_hist_next(A, g);  // the history moves on in the same launch
     fetch(kbeg);
     for (int k0 = kbeg; k0 < kend; k0 += kGemmBK) {
 #pragma unroll
@@ -327,6 +341,7 @@ __global__ __launch_bounds__(256) void k_gemm_x3(const uint8_t *__restrict__ w, 
             for (int e = 0; e < 8; ++e) rw[e] = 0.f;
         }
     };
+    if (ASRC == ASRC_STREAM && g.hist_next) stream_hist_next(A, g);  // the history moves on in the same launch
     fetch(kbeg);
     for (int k0 = kbeg; k0 < kend; k0 += BK) {
 #pragma unroll

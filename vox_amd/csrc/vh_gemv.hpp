@@ -345,7 +345,7 @@ VH_DEV void store_out(const GemvArgs &a, int rows, float out, int lane, int row0
 #pragma unroll
                 for (int k = 0; k < kAccCopies; ++k) a.acc[k * a.acc_ld + row] = 0;
             }
-            a.y[int64_t(mm) * a.ldy + row] = base + v;
+            a.y[int64_t(mm) * a.ldy + row] = base + (a.yscale ? v * a.yscale[row] : v);
         }
     }
 }

@@ -95,7 +95,7 @@ hipError_t launch_f5_attn(const _Float16 *qkv16, int64_t lo_off, float *out, _Fl
 hipError_t launch_snake(const float *x, const float *a, const float *inv_b, float *y, int64_t rows, int C, hipStream_t s);
 hipError_t launch_hist_shift(float *dst, const float *old, const float *x, int64_t ldx, int T, int ctx, int C, hipStream_t s);
 hipError_t launch_dwconv_causal(const float *x, const float *hist, const float *w, const float *b, float *y, int T, int C, int K,
-                                hipStream_t s);
+                                hipStream_t s, float *hist_next = nullptr);
 hipError_t launch_ola(const float *tmp, const float *tail_old, float *tail_new, const float *bias, float *y, int T, int stride,
                       int K, int co, hipStream_t s);
 // nn::ConvT's padded overlap-add (gather form) from the GEMM output z [T][K co] to y [To][co] (+ bias when not null).

@@ -65,6 +65,9 @@ struct GemvArgs {
     int64_t acc_ld;
     // EPI_ACC: the residual rows to add to ([m][ldy]); null: y itself (y += product)
     const float *res;
+    // EPI_ACC: per output row scale of the product, y = residual + yscale[r] (product + bias) (the codec's layer
+    // scales); null: 1
+    const float *yscale;
 };
 
 // Copies of the fixed-point down accumulators: FFN blocks of group g add into copy g % kAccCopies, so fewer
@@ -189,6 +192,9 @@ struct GemmArgs {
     int32_t ctx, dil;
     // EPI_SNAKE: y = v + snake_ib[col] sin(snake_a[col] v)^2 of v = c + bias (the codec's Snake after a convolution)
     const float *snake_a, *snake_ib;
+    // ASRC_STREAM: when set, the launch also writes the history of the next call, the last ctx rows of [hist; x], to
+    // hist_next (another buffer than hist), each block a share
+    float *hist_next;
     // split K (k_gemm_h16): block z sums K columns [z kchunk, (z + 1) kchunk) into ws + z m n ([m][n]); a reduce
     // pass adds the slices in order and applies the epilogue. kchunk 0: no split.
     int32_t kchunk;

@@ -424,11 +424,13 @@ PassScratch lib_scratch() { return {g.gemm_ws, kGemmWsFloats, g.qrows, g.qrows_s
 // (EPI_ACC, which also clears the rows it consumed).
 void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, int64_t ldx, int mc, float *y, int64_t ldy,
           const float *gamma, float eps, float *xnorm, hipStream_t s, const AttnPartials *attn = nullptr,
-          float *pre = nullptr, const PassScratch *scp = nullptr, int64_t *acc = nullptr, const float *res = nullptr) {
+          float *pre = nullptr, const PassScratch *scp = nullptr, int64_t *acc = nullptr, const float *res = nullptr,
+          const float *yscale = nullptr) {
     const PassScratch sc = scp ? *scp : lib_scratch();
     if (acc && (mc != 1 || !int_path(m, m_total) || !(pro == PRO_RMS || epi == EPI_ACC)))
         throw Fail("pending FFN sums on a pass that cannot take them");
     if (res && (epi != EPI_ACC || gemm_path(m, m_total, mc))) throw Fail("separate residual on a pass that cannot take it");
+    if (yscale && epi != EPI_ACC) throw Fail("a row scale needs the residual epilogue");
     if (pro == PRO_ATTN && (!attn || int64_t(attn->heads) * attn->hd != m.cols))
         throw Fail("attention partials do not match the o projection");
     if (gemm_path(m, m_total, mc)) {
@@ -447,7 +449,8 @@ void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, in
         GemmArgs ga{};
         ga.bias = m.b; ga.y = y; ga.lda = lda; ga.ldy = ldy; ga.m = mc; ga.n = int32_t(m.rows); ga.K = int32_t(m.cols);
         ga.ws = sc.ws; ga.ws_cap = sc.ws_cap;
-        HIPCHECK(launch_gemm(gemv_type(m), epi, m.w, m.s, A, ga, s));
+        ga.gate = yscale;  // a row scale of the GEMV is the GEMM's gated residual (y += gate[col] (c + bias))
+        HIPCHECK(launch_gemm(gemv_type(m), yscale ? EPI_GATED_ACC : epi, m.w, m.s, A, ga, s));
         return;
     }
     GemvArgs a{};
@@ -457,6 +460,7 @@ void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, in
     a.acc = acc;
     a.acc_ld = pro == PRO_RMS ? m.cols : m.rows;
     a.res = res;
+    a.yscale = yscale;
     const bool ip = int_path(m, m_total);
     if (ip && mc >= kQuantRowsMin && mc <= 8 && int64_t(mc) * m.cols <= sc.q_elems &&
         (epi == EPI_STORE || epi == EPI_ACC || epi == EPI_SWIGLU)) {
@@ -2770,8 +2774,8 @@ void hist_free(Hist2 &h) {
     for (float *&b : h.b) { dfree(b); b = nullptr; }
 }
 
-// A streaming convolution of T rows X (row stride ldx) into Y (row stride ldy): the conv GEMM over [hist; X], then the
-// history moves on (into the other buffer).
+// A streaming convolution of T rows X (row stride ldx) into Y (row stride ldy): the conv GEMM over [hist; X]; the same
+// launch moves the history on (into the other buffer).
 // snake: Snake applied in the epilogue (the output then holds Snake(conv(.)), as the residual units consume it).
 void codec_conv(const CodecConv &c, Hist2 *h, int par, const float *X, int64_t ldx, int T, float *Y, int64_t ldy, hipStream_t s,
                 const CodecSnake *snake = nullptr) {
@@ -2782,8 +2786,8 @@ void codec_conv(const CodecConv &c, Hist2 *h, int par, const float *X, int64_t l
     ga.cig = c.cin; ga.ksize = c.K; ga.dil = c.dil; ga.ctx = (c.K - 1) * c.dil; ga.hist = h ? h->b[par] : nullptr;
     ga.ws = g.gemm_ws; ga.ws_cap = kGemmWsFloats;
     if (ga.ctx && !h) throw Fail("codec convolution without its history");
+    if (ga.ctx) ga.hist_next = h->b[1 - par];
     HIPCHECK(launch_stream_conv(gemv_type(M), snake ? EPI_SNAKE : EPI_STORE, M.w, M.s, X, ga, s));
-    if (ga.ctx) HIPCHECK(launch_hist_shift(h->b[1 - par], h->b[par], X, ldx, T, ga.ctx, c.cin, s));
 }
 // y (=, +=, gelu, gamma-gated +=) W x + bias over rows of the f32-activation GEMM (the f32 tile semantics of matmul
 // for F32 / F16 / BF16 weights at any row count).
@@ -2812,19 +2816,12 @@ int64_t codec_enqueue(Codec &E, CodecSt &St, int T, hipStream_t s) {
                                         St.pos_dev, s));
         HIPCHECK(launch_codec_attn(E.qkv, QW, St.kr[size_t(li)], St.vr[size_t(li)], E.R, T, E.heads, E.kvh, E.hd, St.pos_dev, E.W,
                                    scale, E.ao, s));
-        if (E.sa[size_t(li)]) {
-            gemv(mat_at(d.o), T, PRO_X, EPI_STORE, E.ao, qd, T, E.tmp, H, nullptr, 0.f, nullptr, s);
-            HIPCHECK(launch_scale_acc(E.h, E.tmp, E.sa[size_t(li)], T, H, s));
-        } else {
-            gemv(mat_at(d.o), T, PRO_X, EPI_ACC, E.ao, qd, T, E.h, H, nullptr, 0.f, nullptr, s);
-        }
+        // the layer scales (null: none) ride on the residual epilogue: h += scale (W x + b)
+        gemv(mat_at(d.o), T, PRO_X, EPI_ACC, E.ao, qd, T, E.h, H, nullptr, 0.f, nullptr, s, nullptr, nullptr, nullptr, nullptr,
+             nullptr, E.sa[size_t(li)]);
         gemv(mat_at(d.gu), T, PRO_RMS, EPI_SWIGLU, E.h, H, T, E.act, E.I, X.norms + d.ln2, E.eps, nullptr, s, nullptr, E.pre);
-        if (E.sm[size_t(li)]) {
-            gemv(mat_at(d.down), T, PRO_X, EPI_STORE, E.act, E.I, T, E.tmp, H, nullptr, 0.f, nullptr, s);
-            HIPCHECK(launch_scale_acc(E.h, E.tmp, E.sm[size_t(li)], T, H, s));
-        } else {
-            gemv(mat_at(d.down), T, PRO_X, EPI_ACC, E.act, E.I, T, E.h, H, nullptr, 0.f, nullptr, s);
-        }
+        gemv(mat_at(d.down), T, PRO_X, EPI_ACC, E.act, E.I, T, E.h, H, nullptr, 0.f, nullptr, s, nullptr, nullptr, nullptr, nullptr,
+             nullptr, E.sm[size_t(li)]);
     }
     gemv(mat_at(E.pt_out), T, PRO_RMS, EPI_STORE, E.h, H, T, A, L, X.norms + X.final_off, E.eps, nullptr, s, nullptr, E.pre);
     // 3) upsample stages: transposed conv (K = stride: the overlap-add has no tail) + ConvNeXt
@@ -2837,8 +2834,7 @@ int64_t codec_enqueue(Codec &E, CodecSt &St, int T, hipStream_t s) {
         HIPCHECK(launch_ola(E.S[2], nullptr, nullptr, U.tr_b, y, int(len), U.K, U.K, L, s));
         len *= U.K;
         Hist2 &hd = St.dw[si];
-        HIPCHECK(launch_dwconv_causal(y, hd.b[par], U.dw_w, U.dw_b, E.S[2], int(len), L, U.dwK, s));
-        HIPCHECK(launch_hist_shift(hd.b[1 - par], hd.b[par], y, L, int(len), U.dwK - 1, L, s));
+        HIPCHECK(launch_dwconv_causal(y, hd.b[par], U.dw_w, U.dw_b, E.S[2], int(len), L, U.dwK, s, U.dwK > 1 ? hd.b[1 - par] : nullptr));
         HIPCHECK(launch_layernorm_rows(E.S[2], len, L, U.ln_w, U.ln_b, E.S[3], s));
         codec_gemm(U.pw1, EPI_GELU_ERF, E.S[3], L, len, E.S[4], 4 * int64_t(L), nullptr, s);
         codec_gemm(U.pw2, EPI_GATED_ACC, E.S[4], 4 * int64_t(L), len, y, L, U.gamma, s);
