@@ -304,21 +304,27 @@ VH_DEV float acc_value(const int64_t (&c)[kAccCopies]) {
     return float(t) * (1.0f / kFixOne);
 }
 
-// The residual an EPI_ACC lane adds to, read with the prologue's inputs at kernel start (the epilogue would otherwise
-// wait one more global round trip at the end), plus, with ACC, the rows' pending FFN sums. Lane r*M + mm holds
-// row0 + r, input row mm.
+// What the epilogue reads besides the totals, loaded with the prologue's inputs at kernel start (the epilogue would
+// otherwise wait one more global round trip at the end): the row's bias, and for EPI_ACC the residual, the row scale
+// and, with ACC, the rows' pending FFN sums. Lane r*M + mm holds row0 + r, input row mm.
 template <int M, int R, int EPI, bool ACC>
 struct EpiPre {
-    float y = 0.f;
+    float y = 0.f, b = 0.f, ys = 1.f;  // residual, bias, row scale (b and ys as loaded: used only where set)
     int64_t c[kAccCopies];
 };
 template <int M, int R, int EPI, bool ACC>
 VH_DEV void epi_prefetch(const GemvArgs &a, int rows, int lane, int row0, EpiPre<M, R, EPI, ACC> &e) {
+    const int r = lane / M, mm = lane % M, row = row0 + r;
+    const bool ok = lane < R * M && row < rows && mm < a.m;
+    // Every load is issued, from element 0 of a valid array when unused, so the count in flight stays static; the
+    // values are used as loaded only in the epilogue (a select here would wait for them before the weight stream).
+    const float *bp = a.bias ? a.bias : a.y;
+    e.b = bp[ok && a.bias ? row : 0];
     if constexpr (EPI == EPI_ACC) {
-        const int r = lane / M, mm = lane % M, row = row0 + r;
-        const bool ok = lane < R * M && row < rows && mm < a.m;
         const float *src = a.res ? a.res : a.y;
-        e.y = src[ok ? int64_t(mm) * a.ldy + row : 0];  // branch-free: other lanes read element 0 and drop it
+        e.y = src[ok ? int64_t(mm) * a.ldy + row : 0];
+        const float *sp = a.yscale ? a.yscale : a.y;
+        e.ys = sp[ok && a.yscale ? row : 0];
         if constexpr (ACC)
 #pragma unroll
             for (int k = 0; k < kAccCopies; ++k) e.c[k] = a.acc[k * a.acc_ld + (ok ? row : 0)];
@@ -331,7 +337,7 @@ template <int M, int R, int EPI, bool ACC>
 VH_DEV void store_out(const GemvArgs &a, int rows, float out, int lane, int row0, const EpiPre<M, R, EPI, ACC> &e) {
     const int r = lane / M, mm = lane % M, row = row0 + r;
     const bool ok = lane < R * M && row < rows && mm < a.m;
-    const float v = out + ((ok && a.bias) ? a.bias[row] : 0.f);
+    const float v = out + ((ok && a.bias) ? e.b : 0.f);
     if (EPI == EPI_SWIGLU) {
         const float other = __shfl_xor(v, M, kWave);  // lane of row r ^ 1, same input row
         if (ok && (r & 1) == 0) a.y[int64_t(mm) * a.ldy + row / 2] = silu(v) * other;
@@ -345,7 +351,7 @@ VH_DEV void store_out(const GemvArgs &a, int rows, float out, int lane, int row0
 #pragma unroll
                 for (int k = 0; k < kAccCopies; ++k) a.acc[k * a.acc_ld + row] = 0;
             }
-            a.y[int64_t(mm) * a.ldy + row] = base + (a.yscale ? v * a.yscale[row] : v);
+            a.y[int64_t(mm) * a.ldy + row] = base + (a.yscale ? v * e.ys : v);
         }
     }
 }
