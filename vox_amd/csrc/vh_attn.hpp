@@ -102,13 +102,20 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnRowsArgs a) {
 
 // One rotate-half pair of a head: optional RMSNorm over the head (the HALF lanes of a group hold its pairs),
 // then RoPE. Rounding as rope_apply: products and the difference/sum each rounded (no contraction).
+// Eight f16 of a KV cache through the global address space: the cache pointers of the row table are generic, and a
+// flat load would make every later wait count for all outstanding loads (flat also counts as an LDS access).
+VH_DEV f16x8 ld_cache8(const _Float16 *p) {
+    return *(const __attribute__((address_space(1))) f16x8 *)(p);
+}
+
+// norm: whether the head has a norm; w0, w1: its weights at p and p + HALF (loaded by the caller).
 template <int HALF>
-VH_DEV void norm_rope(float &x0, float &x1, const float *nw, int p, float eps, float c, float s) {
-    if (nw) {
+VH_DEV void norm_rope(float &x0, float &x1, bool norm, float w0, float w1, float eps, float c, float s) {
+    if (norm) {
         const float ss = group_sum<HALF>(x0 * x0 + x1 * x1);
         const float inv = 1.0f / sqrtf(ss / float(2 * HALF) + eps);
-        x0 = nw[p] * (x0 * inv);
-        x1 = nw[p + HALF] * (x1 * inv);
+        x0 = w0 * (x0 * inv);
+        x1 = w1 * (x1 * inv);
     }
     const float r0 = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
     const float r1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, s));
@@ -131,7 +138,9 @@ struct AttnSmem {
 // j = s + S (grp + NGRP u). Row 0's cache bases, the q|k|v input and the RoPE rows are leading scalar arguments
 // (preloaded with the dispatch): the first kAttnSpecKeys keys' loads go out before the row's position arrives and
 // are masked by it afterwards, so the cache fetch does not wait for the row view. Later keys load per batch of U.
-template <int HD, int G, bool FUSED>
+// ONE_ROW (launches of one row, m == 1): only row 0's path is compiled, so the compiler's wait counts follow one
+// static load sequence.
+template <int HD, int G, bool FUSED, bool ONE_ROW = false>
 __global__ __launch_bounds__(256) void k_attn(const _Float16 *kc0, const _Float16 *vc0, const float *qkv,
                                               const float *rope_rows, int32_t cap0, int32_t layer, AttnArgs a) {
     using Sm = AttnSmem<HD, G>;
@@ -150,46 +159,54 @@ __global__ __launch_bounds__(256) void k_attn(const _Float16 *kc0, const _Float1
     const float *row = qkv + int64_t(i) * a.ldqkv;
     const int64_t plane = (int64_t(layer) * a.kv_heads + g) * HD;  // x cap: offset of this kv head's plane
 
+    // Every small input first (q/k/v of the row, its RoPE row, the q/k norm weights, the row view), then the
+    // speculative cache loads: loads return in issue order, so the q/k work below waits only for the small ones and
+    // runs while the keys are in flight.
+    float qx0[NQ], qx1[NQ], qc[NQ], qsn[NQ], qg0[NQ], qg1[NQ];
+    float kx0 = 0.f, kx1 = 0.f, vx0 = 0.f, vx1 = 0.f, kc = 0.f, ksn = 0.f, kg0 = 0.f, kg1 = 0.f;
+    const bool kv_lane = tid >= 192 && tid - 192 < HALF;  // last wave: the new key/value of a fused row
+    if (FUSED) {
+        // branch-free: lanes without a pair load pair 0 and never use it, so every wave issues the same loads
+        const float *cs = rope_rows + int64_t(i) * HD;
+        const float *qn = a.qn ? a.qn : cs, *kn = a.kn ? a.kn : cs;  // without norms: loaded from cs, never used
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) {
+            const int t = tid + 256 * k, tq = t < G * HALF ? t : 0, h = tq / HALF, p = tq % HALF;
+            qx0[k] = row[(h0 + h) * HD + p];
+            qx1[k] = row[(h0 + h) * HD + p + HALF];
+            qc[k] = cs[2 * p];
+            qsn[k] = cs[2 * p + 1];
+            qg0[k] = qn[p];
+            qg1[k] = qn[p + HALF];
+        }
+        const int p = kv_lane ? tid - 192 : 0;
+        kx0 = row[qd + g * HD + p];
+        kx1 = row[qd + g * HD + p + HALF];
+        vx0 = row[qd + kd + g * HD + p];
+        vx1 = row[qd + kd + g * HD + p + HALF];
+        kc = cs[2 * p];
+        ksn = cs[2 * p + 1];
+        kg0 = kn[p];
+        kg1 = kn[p + HALF];
+    }
+    const RowRef rr = P.rows[i];
+
     // row 0 (every decode step): cache bases from the arguments, speculative loads of the first keys
     f16x8 kb[U], vb[U];
-    if (i == 0) {
+    if (ONE_ROW || i == 0) {
         const _Float16 *K = kc0 + plane * cap0, *V = vc0 + plane * cap0;
 #pragma unroll
         for (int u = 0; u < U1; ++u) {
             const int64_t j = s + int64_t(S) * (grp + NGRP * u);
             const int64_t jc = j < cap0 ? j : 0;  // stay inside the cache; masked below
-            kb[u] = *reinterpret_cast<const f16x8 *>(K + jc * HD + sub * 8);
-            vb[u] = *reinterpret_cast<const f16x8 *>(V + jc * HD + sub * 8);
+            kb[u] = ld_cache8(K + jc * HD + sub * 8);
+            vb[u] = ld_cache8(V + jc * HD + sub * 8);
         }
     }
+    // the new value's f16 bits (the last split's kv lanes use them), converted only after the cache loads are issued
+    __builtin_amdgcn_sched_barrier(0);
+    const _Float16 v0h = _Float16(vx0), v1h = _Float16(vx1);
 
-    float qx0[NQ], qx1[NQ], qc[NQ], qsn[NQ];
-    float kx0 = 0.f, kx1 = 0.f, vx0 = 0.f, vx1 = 0.f, kc = 0.f, ksn = 0.f;
-    const bool kv_lane = tid >= 192 && tid - 192 < HALF;  // last wave: the new key/value of a fused row
-    if (FUSED) {
-        const float *cs = rope_rows + int64_t(i) * HD;
-#pragma unroll
-        for (int k = 0; k < NQ; ++k) {
-            const int t = tid + 256 * k, h = t / HALF, p = t % HALF;
-            qx0[k] = qx1[k] = qc[k] = qsn[k] = 0.f;
-            if (t < G * HALF) {
-                qx0[k] = row[(h0 + h) * HD + p];
-                qx1[k] = row[(h0 + h) * HD + p + HALF];
-                qc[k] = cs[2 * p];
-                qsn[k] = cs[2 * p + 1];
-            }
-        }
-        if (kv_lane) {
-            const int p = tid - 192;
-            kx0 = row[qd + g * HD + p];
-            kx1 = row[qd + g * HD + p + HALF];
-            vx0 = row[qd + kd + g * HD + p];
-            vx1 = row[qd + kd + g * HD + p + HALF];
-            kc = cs[2 * p];
-            ksn = cs[2 * p + 1];
-        }
-    }
-    const RowRef rr = P.rows[i];
     const int64_t n = rr.pos + 1;
     const int64_t pb = (int64_t(i) * P.heads + h0) * kAttnMaxSplits + s;  // + h * kAttnMaxSplits
     if (s >= n) {  // no keys in this split
@@ -205,13 +222,13 @@ __global__ __launch_bounds__(256) void k_attn(const _Float16 *kc0, const _Float1
     const _Float16 *K = rr.k + plane * rr.cap, *V = rr.v + plane * rr.cap;
     // keys read from the cache: j < kend, except the new key of a fused row (processed from LDS below)
     const int64_t kend = last ? n - 1 : n;
-    if (i != 0) {  // other rows: their speculative batch waits for the row view
+    if (!ONE_ROW && i != 0) {  // other rows: their speculative batch waits for the row view
 #pragma unroll
         for (int u = 0; u < U1; ++u) {
             const int64_t j = s + int64_t(S) * (grp + NGRP * u);
             const int64_t jc = j < rr.cap ? j : 0;
-            kb[u] = *reinterpret_cast<const f16x8 *>(K + jc * HD + sub * 8);
-            vb[u] = *reinterpret_cast<const f16x8 *>(V + jc * HD + sub * 8);
+            kb[u] = ld_cache8(K + jc * HD + sub * 8);
+            vb[u] = ld_cache8(V + jc * HD + sub * 8);
         }
     }
 
@@ -220,15 +237,15 @@ __global__ __launch_bounds__(256) void k_attn(const _Float16 *kc0, const _Float1
         for (int k = 0; k < NQ; ++k) {
             const int t = tid + 256 * k, h = t / HALF, p = t % HALF;
             if (t < G * HALF) {
-                norm_rope<HALF>(qx0[k], qx1[k], a.qn, p, a.eps, qc[k], qsn[k]);
+                norm_rope<HALF>(qx0[k], qx1[k], a.qn != nullptr, qg0[k], qg1[k], a.eps, qc[k], qsn[k]);
                 sm.q[h][p] = qx0[k];
                 sm.q[h][p + HALF] = qx1[k];
             }
         }
         if (last && kv_lane) {
             const int p = tid - 192;
-            norm_rope<HALF>(kx0, kx1, a.kn, p, a.eps, kc, ksn);
-            const _Float16 k0h = _Float16(kx0), k1h = _Float16(kx1), v0h = _Float16(vx0), v1h = _Float16(vx1);
+            norm_rope<HALF>(kx0, kx1, a.kn != nullptr, kg0, kg1, a.eps, kc, ksn);
+            const _Float16 k0h = _Float16(kx0), k1h = _Float16(kx1);
             if (hs == 0) {  // one block of the kv head appends the new key/value
                 const int64_t off = rr.pos * HD;
                 _Float16 *Kw = rr.k + plane * rr.cap, *Vw = rr.v + plane * rr.cap;
@@ -321,8 +338,8 @@ __global__ __launch_bounds__(256) void k_attn(const _Float16 *kc0, const _Float1
             const int64_t j = jb + int64_t(S) * NGRP * u;
             valid[u] = j < kend;
             if (valid[u]) {
-                kb[u] = *reinterpret_cast<const f16x8 *>(K + j * HD + sub * 8);
-                vb[u] = *reinterpret_cast<const f16x8 *>(V + j * HD + sub * 8);
+                kb[u] = ld_cache8(K + j * HD + sub * 8);
+                vb[u] = ld_cache8(V + j * HD + sub * 8);
             } else {
                 kb[u] = vb[u] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
             }

@@ -70,6 +70,11 @@ template <int HD, int G>
 static hipError_t attn_hg(const AttnArgs &a, const AttnLaunch &l, int m, bool fused, hipStream_t s) {
     const size_t smem = sizeof(AttnSmem<HD, G>);
     const dim3 grid(kAttnMaxSplits, a.kv_heads * (a.group / G), m);
+    if (fused && m == 1) {
+        hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_attn<HD, G, true, true>), smem);
+        if (e != hipSuccess) return e;
+        return launch(k_attn<HD, G, true, true>, grid, dim3(256), smem, s, l.kc0, l.vc0, l.qkv, l.rope_rows, l.cap0, l.layer, a);
+    }
     if (fused) {
         hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_attn<HD, G, true>), smem);
         if (e != hipSuccess) return e;
