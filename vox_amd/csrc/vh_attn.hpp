@@ -248,7 +248,8 @@ __global__ __launch_bounds__(256) void k_attn(const _Float16 *kc0, const _Float1
             const _Float16 k0h = _Float16(kx0), k1h = _Float16(kx1);
             if (hs == 0) {  // one block of the kv head appends the new key/value
                 const int64_t off = rr.pos * HD;
-                _Float16 *Kw = rr.k + plane * rr.cap, *Vw = rr.v + plane * rr.cap;
+                typedef __attribute__((address_space(1))) _Float16 gf16;  // a global store, as ld_cache8's loads
+                gf16 *Kw = (gf16 *)(rr.k + plane * rr.cap), *Vw = (gf16 *)(rr.v + plane * rr.cap);
                 Kw[off + p] = k0h;
                 Kw[off + p + HALF] = k1h;
                 Vw[off + p] = v0h;

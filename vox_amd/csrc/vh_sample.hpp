@@ -51,7 +51,9 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *c
         for (int i = t; i < kSampleMaxN / 32; i += kSampleThreads) seen[i] = 0u;
         __syncthreads();
         for (int i = t; i < cfg.n_history; i += kSampleThreads) {
-            const int32_t h = cfg.history[i];
+            // a global load (the history pointer comes from memory, so it would otherwise be a flat access, which
+            // makes every later wait count conservative)
+            const int32_t h = ((const __attribute__((address_space(1))) int32_t *)cfg.history)[i];
             if (h >= 0 && h < n) atomicOr(&seen[h >> 5], 1u << (h & 31));
         }
     }
