@@ -91,6 +91,16 @@ __global__ __launch_bounds__(kFfnThreads) void k_ffn_int(FfnArgs a) {
         dw[i] = ok ? t : u32x4{0u, 0u, 0u, 0u};
         ds[i] = ok ? sc : 0.f;
     }
+    // the biases this thread adds, loaded now and used as loaded at the end (a load inside the atomics loop would
+    // make each atomic wait for everything issued before it); without a bias, element 0 of x, never used
+    const float *gbp = a.gu_b ? a.gu_b : a.x, *dbp = a.d_b ? a.d_b : a.x;
+    const float gbias = gbp[a.gu_b ? gr0 + (lane < GR ? lane : 0) : 0];
+    float dbias[DL];
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        const int ci = i * kFfnThreads + int(threadIdx.x);
+        dbias[i] = dbp[a.d_b && ci < nd ? p * HP + ci / F::CPR : 0];
+    }
 
     // --- prologue: RMSNorm of the row (kernels.cpp:707-712), quantized per 32-block into LDS (kernels.cpp:515-523)
     {
@@ -172,8 +182,7 @@ __global__ __launch_bounds__(kFfnThreads) void k_ffn_int(FfnArgs a) {
         const float s = wave_sum(acc[r]);
         if (lane == r) out = s;
     }
-    const int row = gr0 + (lane < GR ? lane : 0);
-    const float v = out + (a.gu_b ? a.gu_b[row] : 0.f);
+    const float v = out + (a.gu_b ? gbias : 0.f);
     const float other = __shfl_xor(v, 1, 64);
     if (lane < GR && (lane & 1) == 0) hv[(wave * GR + lane) >> 1] = silu(v) * other;
     __syncthreads();
@@ -193,13 +202,13 @@ __global__ __launch_bounds__(kFfnThreads) void k_ffn_int(FfnArgs a) {
     }
     const int hsum = WT == WT_Q8 ? 0 : block_qsum(q2);
 
-    // --- down block dots of the panel share, added to the accumulators in fixed point
+    // --- down block dots of the panel share, added to the accumulators in fixed point: every term first, then the
+    // atomics back to back (an atomic issued between them would make the next term's wait include it)
     int64_t *accp = a.acc + int64_t(g % kAccCopies) * H;
+    int64_t terms[DL];
 #pragma unroll
     for (int i = 0; i < DL; ++i) {
         const int ci = i * kFfnThreads + int(threadIdx.x);
-        const bool ok = ci < nd;
-        const int drow = p * HP + (ok ? ci : 0) / F::CPR;
         float f;
         if (WT == WT_Q8) {  // two lanes per row: even lane bytes 0..15, odd lane 16..31
             const bool hi = ci & 1;
@@ -224,11 +233,13 @@ __global__ __launch_bounds__(kFfnThreads) void k_ffn_int(FfnArgs a) {
             d -= 8 * hsum;
             f = float(d) * (ds[i] * hsc);
         }
-        if (ok && (F::CPR == 1 || (ci & 1) == 0)) {
-            int64_t t = fix_of(f);
-            if (g == 0 && a.d_b) t += fix_of(a.d_b[drow]);
-            __hip_atomic_fetch_add(accp + drow, t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        terms[i] = fix_of(f) + ((g == 0 && a.d_b) ? fix_of(dbias[i]) : 0);
+    }
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        const int ci = i * kFfnThreads + int(threadIdx.x);
+        if (ci < nd && (F::CPR == 1 || (ci & 1) == 0))
+            __hip_atomic_fetch_add(accp + p * HP + ci / F::CPR, terms[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
