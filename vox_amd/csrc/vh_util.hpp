@@ -93,11 +93,38 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *x, int64_t ld
 
 // k_rmsnorm_rows with the normed rows written as f16 halves for a split-f16 product: x = hi + lo, hi = f16(x),
 // lo = f16(x - hi); hi rows of ldo halves at out16, lo rows at out16 + lo_off.
+// Rows of up to 8 x 256 values keep the row and the weights in registers, both loaded before the sum, so the
+// weights' round trip overlaps the row's; the sums and products are those of the loop below.
 __global__ __launch_bounds__(256) void k_rmsnorm_rows_h16(const float *x, int64_t ldx, const float *w, int K, float eps,
                                                          _Float16 *out16, int64_t ldo, int64_t lo_off) {
     __shared__ float red[4];
     const float *xr = x + int64_t(blockIdx.x) * ldx;
     float ss = 0.f;
+    if (K <= 8 * 256) {
+        float xv[8], wv[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const int i = threadIdx.x + 256 * c;
+            const int j = i < K ? i : 0;
+            xv[c] = xr[j];
+            wv[c] = w[j];
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            if (threadIdx.x + 256 * c < K) ss = fmaf(xv[c], xv[c], ss);
+        ss = block_sum<256>(ss, red);
+        const float inv = 1.0f / sqrtf(ss / float(K) + eps);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const int i = threadIdx.x + 256 * c;
+            if (i >= K) continue;
+            const float v = wv[c] * (xv[c] * inv);
+            const _Float16 hi = _Float16(v);
+            out16[int64_t(blockIdx.x) * ldo + i] = hi;
+            out16[lo_off + int64_t(blockIdx.x) * ldo + i] = _Float16(v - float(hi));
+        }
+        return;
+    }
     for (int i = threadIdx.x; i < K; i += 256) ss = fmaf(xr[i], xr[i], ss);
     ss = block_sum<256>(ss, red);
     const float inv = 1.0f / sqrtf(ss / float(K) + eps);
