@@ -33,14 +33,23 @@ __global__ __launch_bounds__(64) void k_qk_post(QkArgs a) {
     const float *src = a.qkv + int64_t(i) * a.ldqkv + (is_q ? hh * hd : qd + g * hd);
     const float *nw = is_q ? a.qn : a.kn;
     const bool on = t < half;
-    float x0 = on ? src[t] : 0.f, x1 = on ? src[t + half] : 0.f;
+    // Every input that does not depend on the row reference (the q|k|v values, the norm weights, the v values) is
+    // loaded with it, then the RoPE row it names: two round trips. Lanes past half read element 0 and drop it.
+    const int tt = on ? t : 0;
+    const float *nwp = nw ? nw : src;
+    const float *vs = a.qkv + int64_t(i) * a.ldqkv + qd + kd + (is_q ? 0 : g * hd);
+    const float lx0 = src[tt], lx1 = src[tt + half];
+    const float lw0 = nwp[tt], lw1 = nwp[tt + half];
+    const float v0 = vs[tt], v1 = vs[tt + half];
+    const float c = a.rope[(rr.pos * half + tt) * 2], s = a.rope[(rr.pos * half + tt) * 2 + 1];
+    float x0 = on ? lx0 : 0.f, x1 = on ? lx1 : 0.f;
     if (nw) {
         const float ss = wave_sum(x0 * x0 + x1 * x1);
         const float inv = 1.0f / sqrtf(ss / float(hd) + a.eps);
-        if (on) { x0 = nw[t] * (x0 * inv); x1 = nw[t + half] * (x1 * inv); }
+        x0 = lw0 * (x0 * inv);
+        x1 = lw1 * (x1 * inv);
     }
     if (!on) return;
-    const float c = a.rope[(rr.pos * half + t) * 2], s = a.rope[(rr.pos * half + t) * 2 + 1];
     const float r0 = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
     const float r1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, s));
     if (is_q) {
@@ -51,9 +60,8 @@ __global__ __launch_bounds__(64) void k_qk_post(QkArgs a) {
         const int64_t off = ((int64_t(a.layer) * a.kv_heads + g) * rr.cap + rr.pos) * hd;
         rr.k[off + t] = _Float16(r0);
         rr.k[off + t + half] = _Float16(r1);
-        const float *vs = a.qkv + int64_t(i) * a.ldqkv + qd + kd + g * hd;
-        rr.v[off + t] = _Float16(vs[t]);
-        rr.v[off + t + half] = _Float16(vs[t + half]);
+        rr.v[off + t] = _Float16(v0);
+        rr.v[off + t + half] = _Float16(v1);
     }
 }
 

@@ -201,15 +201,15 @@ __global__ __launch_bounds__(HD) void k_pattn_merge(PrefillAttnArgs a) {
     const int h = blockIdx.x, i = blockIdx.y, e = threadIdx.x;
     const int64_t base = (int64_t(i) * a.heads + h) * kAttnMaxSplits;
     float pm[kAttnMaxSplits], pl[kAttnMaxSplits], po[kAttnMaxSplits];
+    // every run's partial output is loaded with its max and sum (the choice depends only on the run count), so the
+    // loads share one round trip; a run without keys for the row left no output, and its value is skipped below
 #pragma unroll
     for (int z = 0; z < kAttnMaxSplits; ++z) {
         const bool in = z < a.splits;
         pm[z] = in ? a.part.pm[base + z] : -INFINITY;
         pl[z] = in ? a.part.pl[base + z] : 0.f;
+        po[z] = in ? a.part.po[(base + z) * HD + e] : 0.f;
     }
-#pragma unroll
-    for (int z = 0; z < kAttnMaxSplits; ++z)  // a run without keys for the row left no output
-        po[z] = pm[z] != -INFINITY ? a.part.po[(base + z) * HD + e] : 0.f;
     float mx = -INFINITY;
 #pragma unroll
     for (int z = 0; z < kAttnMaxSplits; ++z) mx = fmaxf(mx, pm[z]);
