@@ -107,26 +107,31 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(const SampleCfgDev *c
     };
     // Sequential sums in sorted order over chunks of 64: the lanes put a chunk's terms in LDS and every lane adds
     // them in order from broadcast reads, continuing `run`; lane j keeps the running sum through term j of the
-    // chunk. Past-the-end terms are +0.0, which leaves a sum of non-negative terms unchanged.
-    auto seq_chunk = [&](double x, double &run) -> double {
+    // chunk. Only the chunk's cnt terms below k are added (past-the-end terms are +0.0 and would leave the sum of
+    // non-negative terms unchanged); lanes from cnt on keep 0, and no reader looks at them.
+    auto seq_chunk = [&](double x, double &run, int cnt) -> double {
         wave_lds_sync();
         sd[lane] = x;
         wave_lds_sync();
         double pre = 0.0;
 #pragma unroll 8
-        for (int j = 0; j < 64; ++j) {
+        for (int j = 0; j < cnt; ++j) {
             run += sd[j];
             pre = lane == j ? run : pre;
         }
         return pre;
     };
-    double sum = 0.0;
-    for (int base = 0; base < k; base += 64) (void)seq_chunk(weight(key_of(base), base + lane), sum);
+    double sum = 0.0, w0 = 0.0;  // w0: this lane's term of the first chunk, reused by its prefix sums
+    for (int base = 0; base < k; base += 64) {
+        const double w = weight(key_of(base), base + lane);
+        if (base == 0) w0 = w;
+        (void)seq_chunk(w, sum, min(64, k - base));
+    }
     // Running sums of the normalized terms, continued from `run`: lane j of the chunk gets the sum through term
     // base + j. These are the reference's top-p sum `c` and inverse-CDF sum `acc` (both start at 0 and add
     // probs[i] in order), and the top-p total is the running sum at the last kept term.
     auto prefix_chunk = [&](int base, double &run) -> double {
-        return seq_chunk(weight(key_of(base), base + lane) / sum, run);
+        return seq_chunk((base == 0 ? w0 : weight(key_of(base), base + lane)) / sum, run, min(64, k - base));
     };
     const bool use_p = cfg.top_p > 0.0f && cfg.top_p < 1.0f;
     int keep = k;
