@@ -313,8 +313,9 @@ void vo_quantize_q4(const float *w, int64_t rows, int64_t cols, uint8_t *q, floa
             const float *p = w + r * cols + b * 32;
             float mx = 0; /* signed value of largest magnitude, first one wins */
             for (int j = 0; j < 32; ++j) if (fabsf(p[j]) > fabsf(mx)) mx = p[j];
-            float best_d = mx / -8.0f;
-            double best_err = INFINITY;
+            /* best_err is a float as at kernels.cpp:616: each candidate's double error is rounded when stored (:629),
+               and the later comparisons (:629, :638) widen that float back to double */
+            float best_d = mx / -8.0f, best_err = INFINITY;
             int8_t best_q[32];
             memset(best_q, 0, sizeof best_q);
             if (mx != 0.0f)
@@ -330,7 +331,7 @@ void vo_quantize_q4(const float *w, int64_t rows, int64_t cols, uint8_t *q, floa
                         const double e = (double)p[j] - (double)qq[j] * (double)d;
                         err += e * e;
                     }
-                    if (err < best_err) { best_err = err; best_d = d; memcpy(best_q, qq, 32); }
+                    if (err < (double)best_err) { best_err = (float)err; best_d = d; memcpy(best_q, qq, 32); }
                 }
             if (mx != 0.0f) {
                 double num = 0, den = 0;
@@ -339,7 +340,7 @@ void vo_quantize_q4(const float *w, int64_t rows, int64_t cols, uint8_t *q, floa
                     const float d2 = (float)(num / den);
                     double err = 0;
                     for (int j = 0; j < 32; ++j) { const double e = (double)p[j] - (double)best_q[j] * (double)d2; err += e * e; }
-                    if (err < best_err) best_d = d2;
+                    if (err < (double)best_err) best_d = d2;
                 }
             }
             scale[r * nb + b] = best_d;

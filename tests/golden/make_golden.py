@@ -4,6 +4,7 @@ Run here (where /root/reference exists and `make -C oracle ref` has built the ha
     python tests/golden/make_golden.py          # golden_ref.npz
     python tests/golden/make_golden.py cosy     # golden_cosy.npz (the flow estimator's nn.cpp layers)
     python tests/golden/make_golden.py codec    # golden_codec.npz (the Qwen3-TTS codec decoder)
+    python tests/golden/make_golden.py q4       # golden_q4.npz (quantize_q4 blocks on float-rounding ties)
 The fixtures hold inputs and the reference's outputs only (data, no reference source; the estimator's weights are
 regenerated from a seed by tests/models.py's CosyModel). Tests compare the
 C restatement (oracle/liboracle.so) against it on machines without the reference.
@@ -24,6 +25,7 @@ OUT = os.path.join(HERE, "golden_ref.npz")
 OUT_COSY = os.path.join(HERE, "golden_cosy.npz")
 COSY_SEED, COSY_T = 77, 13  # CosyModel(COSY_SEED, n_mid=1, n_x=1) at T frames
 OUT_CODEC = os.path.join(HERE, "golden_codec.npz")
+OUT_Q4 = os.path.join(HERE, "golden_q4.npz")
 CODEC_SEED, CODEC_F = 91, 9  # CodecModel(CODEC_SEED) on F frames, decoded as 4 + 5
 
 
@@ -177,6 +179,58 @@ def main_codec():
     print("wrote", OUT_CODEC, os.path.getsize(OUT_CODEC), "bytes")
 
 
+def q4_block_errors(p):
+    """Float64 squared errors of quantize_q4's nine candidate scales and of the least-squares refit of the best one
+    (kernels.cpp:606-645), for blocks p [n][32] f32. Numpy sums in its own order, so the values are close to the
+    reference's, not equal: they only rank blocks by how near a rounding of the stored error they are."""
+    a = np.abs(p)
+    mx = p[np.arange(p.shape[0]), np.argmax(a, axis=1)]  # first value of largest magnitude
+    errs, qs = [], []
+    for k in range(9):
+        d = (mx / np.float32(-(7.0 + 0.25 * k))).astype(np.float32)
+        inv = (np.float32(1) / d).astype(np.float32)
+        c = np.clip(np.floor((p * inv[:, None]).astype(np.float32) + np.float32(8.5)), 0, 15)
+        q = c.astype(np.int64) - 8
+        errs.append(((p.astype(np.float64) - q * d[:, None].astype(np.float64)) ** 2).sum(1))
+        qs.append(q)
+    errs = np.stack(errs, 1)
+    best = np.argmin(errs, 1)
+    bq = np.stack(qs, 1)[np.arange(p.shape[0]), best]
+    num = (p.astype(np.float64) * bq).sum(1)
+    den = (bq * bq).sum(1).astype(np.float64)
+    d2 = (num / np.where(den > 0, den, 1)).astype(np.float32)
+    ls = ((p.astype(np.float64) - bq * d2[:, None].astype(np.float64)) ** 2).sum(1)
+    return errs, ls
+
+
+def main_q4():
+    """quantize_q4 on blocks where the float best_err of kernels.cpp:616 decides: the best candidate's error and a
+    rival (another candidate or the least-squares refit) lie within a few float ulps of each other, so storing the
+    double error as a float can flip the choice. Drawn from N(0, 0.02), U(-1, 1) and near-grid matrices."""
+    if po.ref() is None:
+        raise SystemExit("oracle/_ref/libvoxref.so is not built")
+    rng = np.random.default_rng(20261203)
+    picked = []
+    for kind in range(3):
+        n = 1 << 20
+        if kind == 0:
+            p = (rng.standard_normal((n, 32)) * 0.02).astype(np.float32)
+        elif kind == 1:
+            p = rng.uniform(-1, 1, (n, 32)).astype(np.float32)
+        else:
+            p = (rng.integers(-8, 8, (n, 32)) * 0.01 + rng.standard_normal((n, 32)) * 1e-6).astype(np.float32)
+        errs, ls = q4_block_errors(p)
+        srt = np.sort(errs, 1)
+        best = srt[:, 0]
+        gap = np.minimum(np.abs(srt[:, 1] - best), np.abs(ls - best)) / np.maximum(best, 1e-300)
+        sel = np.nonzero(gap < 2.0 ** -22)[0]
+        picked.append(p[sel[:700]])
+    w = np.ascontiguousarray(np.concatenate(picked), np.float32)
+    q, s = po.quantize_q4(w, use_ref=True)
+    np.savez_compressed(OUT_Q4, w=w, q=q, s=s)
+    print("wrote", OUT_Q4, w.shape[0], "blocks", os.path.getsize(OUT_Q4), "bytes")
+
+
 if __name__ == "__main__":
     mode = sys.argv[1:]
-    main_cosy() if mode == ["cosy"] else main_codec() if mode == ["codec"] else main()
+    {"cosy": main_cosy, "codec": main_codec, "q4": main_q4}.get(mode[0] if mode else "", main)()

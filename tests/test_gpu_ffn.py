@@ -126,9 +126,10 @@ def kernels_per_step(hip, xf, seq, head, hidden, pos):
 
 
 def test_fused_ffn_default_policy(hip):
-    """By default the fused FFN is taken for FFNs of at least 4x the hidden width, and not below."""
-    for inter, per_layer in ((1024, 4), (768, 5)):
-        mdl = Model(31, 2, 256, 4, 2, 64, inter, wtype=Q8, head_rows=64)
+    """By default the fused FFN is taken for FFNs of at least 4x the hidden width, and not below; nor when the
+    attention width (heads x head_dim 3072) exceeds what the o GEMV's pending-sum prologue stages (2048)."""
+    for inter, heads, kvh, hd, per_layer in ((1024, 4, 2, 64, 4), (768, 4, 2, 64, 5), (1024, 24, 3, 128, 5)):
+        mdl = Model(31, 2, 256, heads, kvh, hd, inter, wtype=Q8, head_rows=64)
         xf = hip.xfmr_create(mdl.hx, "ffn_default")
         head = hip.upload(mdl.head[1])
         seq = hip.seq_create(xf, 8)

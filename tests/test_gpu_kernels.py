@@ -42,6 +42,27 @@ def test_quantizers_bit_exact(hip, oracle):
     assert np.array_equal(xq, oq) and np.array_equal(xs.view(np.uint32), os_.view(np.uint32))
 
 
+def test_quantizers_bit_exact_large(hip, oracle):
+    # 4 x 131,072 random blocks, then the blocks where kernels.cpp:616's float best_err decides the q4 scale
+    # (tests/golden/golden_q4.npz holds the compiled reference's output for them)
+    import os
+    rng = np.random.default_rng(5)
+    mats = [(rng.standard_normal((4096, 1024)) * 0.02).astype(np.float32),
+            rng.uniform(-1, 1, (4096, 1024)).astype(np.float32),
+            (rng.integers(-8, 8, (4096, 1024)) * 0.01 + rng.standard_normal((4096, 1024)) * 1e-6).astype(np.float32),
+            (rng.standard_normal((4096, 1024)) * np.geomspace(1e-6, 1e3, 1024)).astype(np.float32)]
+    for w in mats:
+        q, s = hip.quantize_q4_dev(w)
+        oq, os_ = oracle.quantize_q4(w)
+        assert np.array_equal(s.view(np.uint32), os_.view(np.uint32)) and np.array_equal(q, oq)
+        q, s = hip.quantize_q8_dev(w)
+        oq, os_ = oracle.quantize_q8(w)
+        assert np.array_equal(s.view(np.uint32), os_.view(np.uint32)) and np.array_equal(q, oq)
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden_q4.npz"), allow_pickle=False)
+    q, s = hip.quantize_q4_dev(g["w"])
+    assert np.array_equal(s.view(np.uint32), g["s"].view(np.uint32)) and np.array_equal(q, g["q"])
+
+
 @pytest.mark.parametrize("wt", [Q8, Q4, F32, F16, BF16, "q4h"])
 def test_mat_gather_bit_exact(hip, oracle, wt):
     # mat_row / mat_gather (kernels.cpp:432-471): the device unpack of every weight type, the one the LM and code

@@ -291,6 +291,34 @@ def test_layer_pass_graph_replays(hip, oracle, wt, m):
     assert rel_err(outs[0][0], ref) < TOL, rel_err(outs[0][0], ref)
 
 
+def test_prefill_planes_under_vram_limit(hip, oracle):
+    # a Q8 prefill of more than 8 rows takes the planes path, which widens every matrix to f16 once (26 MB here);
+    # with a VRAM limit just above the weights those copies cannot be made, and the pass must still run (on the
+    # f32-activation GEMM) with the same results
+    warm = Model(840, 1, 256, 4, 2, 64, 512, wtype=Q8)  # allocates the library's pass scratch first
+    wx, _ = build(hip, warm)
+    hip.forward(wx, hip.seq_create(wx, 64), 0, np.ones((9, 256), np.float32), 256)
+    mdl = Model(841, 2, 512, 8, 2, 64, 4096, wtype=Q8, head_rows=64)
+    xf, head = build(hip, mdl)
+    seq = hip.seq_create(xf, 64)
+    kv = mdl.oracle_kv(64, kv_f16=1)
+    used = hip.mem_info().used
+    hip.lib().voxhip_set_vram_limit(used + (4 << 20))
+    try:
+        rng = np.random.default_rng(17)
+        x = rng.standard_normal((9, 512)).astype(np.float32)
+        out, logits = hip.forward(xf, seq, 0, x, 512, head=head)
+        assert hip.mem_info().used < used + (4 << 20)
+        ref = oracle.transformer_forward(mdl.ox, kv, x)
+        assert rel_err(out, ref) < TOL, rel_err(out, ref)
+        assert rel_err(logits, oracle_head(oracle, mdl, out)) < TOL
+        x = rng.standard_normal((1, 512)).astype(np.float32)
+        out, _ = hip.forward(xf, seq, 9, x, 512, head=head)
+        assert rel_err(out, oracle.transformer_forward(mdl.ox, kv, x)) < TOL
+    finally:
+        hip.lib().voxhip_set_vram_limit(0)
+
+
 @pytest.mark.parametrize("wt", [F16, Q8])
 def test_prefill_key_splits(hip, oracle, wt):
     # prefill passes whose grid of 64-row query tiles leaves CUs idle split each tile's keys into runs merged by

@@ -485,6 +485,69 @@ def test_quantize_q4_golden_and_bounds(oracle, gold):
     assert np.all(np.abs(deq - gold["quant_w"]) <= step * 2.001)
 
 
+GOLD_Q4 = os.path.join(os.path.dirname(__file__), "golden", "golden_q4.npz")
+
+
+def test_quantize_q4_float_rounding_golden(oracle):
+    # blocks whose best candidate error and a rival lie within float rounding of each other: the reference keeps
+    # best_err as a float (kernels.cpp:616, :629, :638), which decides these blocks (tests/golden/make_golden.py q4)
+    g = np.load(GOLD_Q4, allow_pickle=False)
+    q, s = po.quantize_q4(g["w"])
+    assert g["w"].shape[0] >= 2000
+    assert np.array_equal(s.view(np.uint32), g["s"].view(np.uint32))
+    assert np.array_equal(q, g["q"])
+
+
+def _random_quant_matrices(rng):
+    """N(0, 0.02), U(-1, 1), near-grid and wide-range 4096 x 1024 matrices (131,072 blocks each)."""
+    yield (rng.standard_normal((4096, 1024)) * 0.02).astype(np.float32)
+    yield rng.uniform(-1, 1, (4096, 1024)).astype(np.float32)
+    yield (rng.integers(-8, 8, (4096, 1024)) * 0.01 + rng.standard_normal((4096, 1024)) * 1e-6).astype(np.float32)
+    yield (rng.standard_normal((4096, 1024)) * np.geomspace(1e-6, 1e3, 1024)).astype(np.float32)
+
+
+@pytest.mark.ref
+def test_quantizers_vs_ref_random(ref):
+    # >= 1M random blocks per quantizer against the compiled reference (kernels.cpp:606-645, :918-929); the
+    # seed-0 N(0, 0.02) matrix held 77 blocks a double best_err got wrong
+    rng = np.random.default_rng(0)
+    n = 0
+    for _ in range(2):
+        for w in _random_quant_matrices(rng):
+            q, s = po.quantize_q4(w)
+            rq, rs = po.quantize_q4(w, use_ref=True)
+            assert np.array_equal(s.view(np.uint32), rs.view(np.uint32)) and np.array_equal(q, rq)
+            q, s = po.quantize_q8(w)
+            rq, rs = po.quantize_q8(w, use_ref=True)
+            assert np.array_equal(s.view(np.uint32), rs.view(np.uint32)) and np.array_equal(q, rq)
+            n += w.size // 32
+    assert n >= 1 << 20
+
+
+@pytest.mark.ref
+@pytest.mark.parametrize("wt", [po.Q8, po.Q4, po.F32, po.F16, po.BF16])
+def test_mat_row_vs_ref_random(ref, wt):
+    # mat_row / mat_gather (kernels.cpp:432-471) on every type, f16 subnormals and infinities included
+    rng = np.random.default_rng(40 + wt)
+    rows, cols = 2048, 1024
+    w = (rng.standard_normal((rows, cols)) * np.geomspace(1e-7, 1e4, cols)).astype(np.float32)
+    if wt == po.Q8:
+        data, s = po.quantize_q8(w)
+    elif wt == po.Q4:
+        data, s = po.quantize_q4(w)
+    elif wt == po.F16:
+        data, s = rng.integers(0, 1 << 16, (rows, cols)).astype(np.uint16), None
+        data[:, :4] = [0x7c00, 0xfc00, 0x0001, 0x83ff]
+    elif wt == po.BF16:
+        data, s = (w.view(np.uint32) >> 16).astype(np.uint16), None
+    else:
+        data, s = w, None
+    M = po.Mat(wt, data, rows, cols, s)
+    for r in range(rows):
+        a, b = po.mat_row(M, r), po.mat_row(M, r, use_ref=True)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), r
+
+
 def test_q4_unpack_closed_form(oracle):
     # byte j of a block = w[j] | w[j+16] << 4, value (u - 8) * scale (kernels.hpp:44-47)
     rng = np.random.default_rng(4)

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "vh_types.hpp"
+
 #define VH_DEV __device__ __forceinline__
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -13,6 +15,18 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 namespace vh {
 
 constexpr int kWave = 64;
+
+// f32 -> the f16 halves of a split-f16 product, x = hi + lo to about 2^-22 relative. True when x is finite but
+// outside the f16 range (|x| >= 65520 rounds hi to infinity), which the product cannot represent.
+__device__ __forceinline__ bool split_f16(float x, _Float16 &hi, _Float16 &lo) {
+    hi = _Float16(x);
+    lo = _Float16(x - float(hi));
+    return __builtin_isinf(float(hi)) && !__builtin_isinf(x);
+}
+// Sets `bit` in the status word when `bad` (a vector atomic; the common path is one predicated branch).
+__device__ __forceinline__ void raise_status(int32_t *status, bool bad, int32_t bit) {
+    if (__builtin_expect(bad, 0) && status) __hip_atomic_fetch_or(status, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 // MI355X hands the workgroups of a launch round-robin to its 8 XCDs (linear id % 8), and each XCD has its own L2.
 // xcd_tile maps linear id L of T blocks to a tile index so that XCD x takes the contiguous tiles
 // [x T / 8, (x + 1) T / 8): neighbouring tiles, which share operand rows, then meet in one L2 instead of every XCD

@@ -4,7 +4,9 @@
 
 namespace vh {
 
-hipError_t launch_norm_rows(const NormArgs &a, hipStream_t s) {
+hipError_t launch_norm_rows(const NormArgs &a0, hipStream_t s) {
+    NormArgs a = a0;
+    a.status = status_word();
     if (a.R <= 0) return hipSuccess;
     if (a.D <= 0 || a.D % 4 || !a.x || (!a.y && !a.y16) || a.lo_off % 4 || !a.sc || (!a.affine && !a.sh) || !(a.eps > 0.0))
         return hipErrorInvalidValue;

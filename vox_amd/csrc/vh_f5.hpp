@@ -89,11 +89,15 @@ __global__ __launch_bounds__(256) void k_f5_modulate(NormArgs a) {
         }
         if (a.y16) {
             f16x4a hi, lo;
+            bool bad = false;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                hi[e] = _Float16(r[e]);
-                lo[e] = _Float16(r[e] - float(hi[e]));
+                _Float16 h, l;
+                bad |= split_f16(r[e], h, l);
+                hi[e] = h;
+                lo[e] = l;
             }
+            raise_status(a.status, bad, kStatusF16Range);
             _Float16 *hr = a.y16 + int64_t(row) * D + i;
             *reinterpret_cast<f16x4a *>(hr) = hi;
             *reinterpret_cast<f16x4a *>(hr + a.lo_off) = lo;

@@ -48,7 +48,9 @@ bool ffn_shape_ok(int wt, int H, int I) {
            I <= 32 * 1024;
 }
 
-hipError_t launch_ffn(int wt, const FfnArgs &a, hipStream_t s) {
+hipError_t launch_ffn(int wt, const FfnArgs &a0, hipStream_t s) {
+    FfnArgs a = a0;
+    a.status = status_word();
     if (!ffn_shape_ok(wt, a.H, a.I) || !a.gu || !a.gu_s || !a.dp || !a.dp_s || !a.x || !a.gamma || !a.acc)
         return hipErrorInvalidValue;
     if (a.parts != 1 && a.parts != 2 && a.parts != 4) return hipErrorInvalidValue;

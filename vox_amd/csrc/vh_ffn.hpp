@@ -206,6 +206,7 @@ __global__ __launch_bounds__(kFfnThreads) void k_ffn_int(FfnArgs a) {
     // atomics back to back (an atomic issued between them would make the next term's wait include it)
     int64_t *accp = a.acc + int64_t(g % kAccCopies) * H;
     int64_t terms[DL];
+    bool bad = false;  // a term outside the fixed-point range
 #pragma unroll
     for (int i = 0; i < DL; ++i) {
         const int ci = i * kFfnThreads + int(threadIdx.x);
@@ -233,8 +234,9 @@ __global__ __launch_bounds__(kFfnThreads) void k_ffn_int(FfnArgs a) {
             d -= 8 * hsum;
             f = float(d) * (ds[i] * hsc);
         }
-        terms[i] = fix_of(f) + ((g == 0 && a.d_b) ? fix_of(dbias[i]) : 0);
+        terms[i] = fix_of(f, bad) + ((g == 0 && a.d_b) ? fix_of(dbias[i], bad) : 0);
     }
+    raise_status(a.status, bad, kStatusFixRange);
 #pragma unroll
     for (int i = 0; i < DL; ++i) {
         const int ci = i * kFfnThreads + int(threadIdx.x);

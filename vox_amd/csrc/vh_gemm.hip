@@ -21,6 +21,14 @@ static hipError_t x3_run(const uint8_t *w, const float *A, const GemmArgs &g, in
     return launch(k_gemm_x3<EPI, ASRC>, grid, dim3(256), 0, s, w, A, g);
 }
 
+// F32 weights: the split kernel, or k_gemm_f32 (f32 matrix cores, one product) when the weights are too large for
+// its scaled f16 halves (g.f32_wide).
+template <int EPI, int ASRC>
+static hipError_t f32w_run(const uint8_t *w, const float *A, const GemmArgs &g, int z, hipStream_t s) {
+    if (g.f32_wide) return gemm_run<WT_F32, EPI, ASRC, 2>(w, nullptr, A, g, z, s);
+    return x3_run<EPI, ASRC>(w, A, g, z, s);
+}
+
 template <int WT, int EPI, int TM, int TN>
 static hipError_t gemm_run_h16(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s) {
     constexpr int BM = 32 * TM, BN = 32 * TN;
@@ -85,12 +93,12 @@ static hipError_t gemm_tile(const uint8_t *w, const float *scale, const float *A
             GemmArgs gs = g;  // the same K slices (few-row passes over f32 / bf16 weights)
             const int splits = split_plan(g, &gs.kchunk);
             if (splits) {
-                hipError_t e = WT == WT_F32 ? x3_run<EPI_STORE, ASRC_ROWS>(w, A, gs, splits, s)
+                hipError_t e = WT == WT_F32 ? f32w_run<EPI_STORE, ASRC_ROWS>(w, A, gs, splits, s)
                                             : gemm_run<WT, EPI_STORE, ASRC_ROWS, 2>(w, scale, A, gs, splits, s);
                 return e != hipSuccess ? e : splitk_reduce<EPI>(g, splits, s);
             }
         }
-        if constexpr (WT == WT_F32) return x3_run<EPI, ASRC_ROWS>(w, A, g, 1, s);
+        if constexpr (WT == WT_F32) return f32w_run<EPI, ASRC_ROWS>(w, A, g, 1, s);
         return gemm_run<WT, EPI, ASRC_ROWS, 2>(w, scale, A, g, 1, s);
     }
 }
@@ -119,7 +127,9 @@ static hipError_t gemm_epi(int epi, const uint8_t *w, const float *scale, const 
     }
 }
 
-hipError_t launch_gemm(int wt, int epi, const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s) {
+hipError_t launch_gemm(int wt, int epi, const uint8_t *w, const float *scale, const float *A, const GemmArgs &g0, hipStream_t s) {
+    GemmArgs g = g0;
+    g.status = status_word();
     if (g.m <= 0) return hipSuccess;
     if (g.K % 8 || g.n <= 0 || g.lda % 4) return hipErrorInvalidValue;
     if ((epi == EPI_SWIGLU || epi == EPI_ROPE) && g.n % 2) return hipErrorInvalidValue;
@@ -177,8 +187,10 @@ static bool hh_args_ok(const _Float16 *w, const float *q8_scale, const GemmArgs 
            (!q8_scale || int64_t(64) * (g.K / 32) * 4 <= INT32_MAX);
 }
 
-hipError_t launch_gemm_hh_acc_rms(const _Float16 *w, const float *q8_scale, const GemmArgs &g, const float *gamma, float eps,
+hipError_t launch_gemm_hh_acc_rms(const _Float16 *w, const float *q8_scale, const GemmArgs &g0, const float *gamma, float eps,
                                   _Float16 *out16, int64_t ldo, int64_t lo_off, hipStream_t s, bool *normed) {
+    GemmArgs g = g0;
+    g.status = status_word();
     *normed = false;
     if (g.m <= 0) return hipSuccess;
     if (!hh_args_ok(w, q8_scale, g) || !g.y) return hipErrorInvalidValue;
@@ -198,7 +210,9 @@ hipError_t launch_gemm_hh_acc_rms(const _Float16 *w, const float *q8_scale, cons
     return e;
 }
 
-hipError_t launch_gemm_hh(int epi, const _Float16 *w, const float *q8_scale, const GemmArgs &g, hipStream_t s) {
+hipError_t launch_gemm_hh(int epi, const _Float16 *w, const float *q8_scale, const GemmArgs &g0, hipStream_t s) {
+    GemmArgs g = g0;
+    g.status = status_word();
     if (g.m <= 0) return hipSuccess;
     if (!hh_args_ok(w, q8_scale, g)) return hipErrorInvalidValue;
     if ((epi == EPI_SWIGLU || epi == EPI_SWIGLU_H16) && g.n % 2) return hipErrorInvalidValue;
@@ -217,7 +231,9 @@ hipError_t launch_gemm_hh(int epi, const _Float16 *w, const float *q8_scale, con
     }
 }
 
-hipError_t launch_conv_gemm(int epi, const float *w, const float *A, const GemmArgs &g, int groups, hipStream_t s) {
+hipError_t launch_conv_gemm(int epi, const float *w, const float *A, const GemmArgs &g0, int groups, hipStream_t s) {
+    GemmArgs g = g0;
+    g.status = status_word();
     if (g.m <= 0) return hipSuccess;
     // K: ksize * cig, rounded up to a multiple of 8 with zero weights (the A loader reads zeros there)
     if (g.cig <= 0 || g.cig % 4 || g.ksize <= 0 || g.ksize % 2 == 0 || g.K < g.ksize * g.cig || g.K >= g.ksize * g.cig + 8 ||
@@ -228,15 +244,15 @@ hipError_t launch_conv_gemm(int epi, const float *w, const float *A, const GemmA
         GemmArgs gs = g;
         const int splits = split_plan(g, &gs.kchunk);
         if (splits) {
-            hipError_t e = x3_run<EPI_STORE, ASRC_CONV>(wb, A, gs, splits, s);
+            hipError_t e = f32w_run<EPI_STORE, ASRC_CONV>(wb, A, gs, splits, s);
             if (e != hipSuccess) return e;
             return epi == EPI_STORE ? splitk_reduce<EPI_STORE>(g, splits, s) : splitk_reduce<EPI_ACC>(g, splits, s);
         }
     }
-    if (epi == EPI_MISH) return x3_run<EPI_MISH, ASRC_CONV>(wb, A, g, groups, s);
-    if (epi == EPI_MISH_ACC) return x3_run<EPI_MISH_ACC, ASRC_CONV>(wb, A, g, groups, s);
-    if (epi == EPI_STORE) return x3_run<EPI_STORE, ASRC_CONV>(wb, A, g, groups, s);
-    if (epi == EPI_ACC) return x3_run<EPI_ACC, ASRC_CONV>(wb, A, g, groups, s);
+    if (epi == EPI_MISH) return f32w_run<EPI_MISH, ASRC_CONV>(wb, A, g, groups, s);
+    if (epi == EPI_MISH_ACC) return f32w_run<EPI_MISH_ACC, ASRC_CONV>(wb, A, g, groups, s);
+    if (epi == EPI_STORE) return f32w_run<EPI_STORE, ASRC_CONV>(wb, A, g, groups, s);
+    if (epi == EPI_ACC) return f32w_run<EPI_ACC, ASRC_CONV>(wb, A, g, groups, s);
     return hipErrorInvalidValue;
 }
 
@@ -248,11 +264,11 @@ static hipError_t stream_conv(const uint8_t *w, const float *scale, const float 
     GemmArgs gs = g;
     const int splits = split_plan(g, &gs.kchunk);
     if (splits) {
-        hipError_t e = WT == WT_F32 ? x3_run<EPI_STORE, ASRC_STREAM>(w, x, gs, splits, s)
+        hipError_t e = WT == WT_F32 ? f32w_run<EPI_STORE, ASRC_STREAM>(w, x, gs, splits, s)
                                     : gemm_run<WT, EPI_STORE, ASRC_STREAM, 2>(w, scale, x, gs, splits, s);
         return e != hipSuccess ? e : splitk_reduce<EPI>(g, splits, s);
     }
-    if constexpr (WT == WT_F32) return x3_run<EPI, ASRC_STREAM>(w, x, g, 1, s);
+    if constexpr (WT == WT_F32) return f32w_run<EPI, ASRC_STREAM>(w, x, g, 1, s);
     return gemm_run<WT, EPI, ASRC_STREAM, 2>(w, scale, x, g, 1, s);
 }
 template <int EPI>
@@ -264,8 +280,10 @@ static hipError_t stream_conv_wt(int wt, const uint8_t *w, const float *scale, c
         default: return hipErrorInvalidValue;
     }
 }
-hipError_t launch_stream_conv(int wt, int epi, const uint8_t *w, const float *scale, const float *x, const GemmArgs &g,
+hipError_t launch_stream_conv(int wt, int epi, const uint8_t *w, const float *scale, const float *x, const GemmArgs &g0,
                               hipStream_t s) {
+    GemmArgs g = g0;
+    g.status = status_word();
     if (g.m <= 0) return hipSuccess;
     if (g.cig <= 0 || g.cig % 4 || g.ksize <= 0 || g.dil <= 0 || g.K != g.ksize * g.cig || g.K % 8 || g.lda % 4 || g.n <= 0 ||
         g.ctx != (g.ksize - 1) * g.dil || (g.ctx && !g.hist) || !g.y ||

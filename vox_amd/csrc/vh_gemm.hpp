@@ -101,6 +101,7 @@ VH_DEV void gemm_load_w(const uint8_t *__restrict__ w, const float *__restrict__
 // Epilogue of a wave's TM x TN accumulator tiles: lane holds C[row0 + 4 (lane / 16) + v][col], col = col0 + lane % 16.
 template <int EPI, int TM, int TN>
 VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0, int n0, int wm, int wn, int lane) {
+    bool bad = false;  // an f16-halves output beyond the f16 range
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -119,9 +120,10 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
                     f16x4v hi, lo;
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
-                        const float c = acc[i][j][v] + bz;
-                        hi[v] = _Float16(c);
-                        lo[v] = _Float16(c - float(hi[v]));
+                        _Float16 h, l;
+                        bad |= split_f16(acc[i][j][v] + bz, h, l);
+                        hi[v] = h;
+                        lo[v] = l;
                     }
                     *reinterpret_cast<f16x4v *>(g.h16 + idx) = hi;
                     *reinterpret_cast<f16x4v *>(g.h16 + g.lo_off + idx) = lo;
@@ -141,10 +143,11 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
                         if (EPI == EPI_SWIGLU) {
                             g.y[int64_t(row) * g.ldy + col / 2] = r;
                         } else {
-                            const _Float16 hi = _Float16(r);
+                            _Float16 hi, lo;
+                            bad |= split_f16(r, hi, lo);
                             const int64_t idx = int64_t(row) * g.ldy + col / 2;
                             g.h16[idx] = hi;
-                            g.h16[g.lo_off + idx] = _Float16(r - float(hi));
+                            g.h16[g.lo_off + idx] = lo;
                         }
                     }
                 } else if (EPI == EPI_ROPE || EPI == EPI_ROPE_H16) {
@@ -161,7 +164,8 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
                     if (EPI == EPI_ROPE) {
                         if (in) *dst = r;
                     } else if (in) {
-                        const _Float16 hi = _Float16(r), lo = _Float16(r - float(hi));
+                        _Float16 hi, lo;
+                        bad |= split_f16(r, hi, lo);
                         int64_t idx;
                         if (col < g.rope_cols) {
                             idx = int64_t(row) * g.rope_cols + col;
@@ -181,10 +185,11 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
                     else if (EPI == EPI_GELU_ERF) *dst = gelu_erf_f(c);
                     else if (EPI == EPI_GELU_H16) {
                         const float r = g.gelu_erf ? gelu_erf_f(c) : gelu_tanh_f(c);
-                        const _Float16 hi = _Float16(r);
+                        _Float16 hi, lo;
+                        bad |= split_f16(r, hi, lo);
                         const int64_t idx = int64_t(row) * g.ldy + col;
                         g.h16[idx] = hi;
-                        g.h16[g.lo_off + idx] = _Float16(r - float(hi));
+                        g.h16[g.lo_off + idx] = lo;
                     }
                     else if (EPI == EPI_SNAKE) {
                         const float sn = sinf(c * g.snake_a[col]);
@@ -195,6 +200,7 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
                 }
             }
         }
+    raise_status(g.status, bad, kStatusF16Range);
 }
 
 // Split K: a block's TM x TN accumulator tiles as partial sums into slice blockIdx.z of ws ([m][n] per slice), no
@@ -343,14 +349,17 @@ __global__ __launch_bounds__(256) void k_gemm_x3(const uint8_t *__restrict__ w, 
     };
     if (ASRC == ASRC_STREAM && g.hist_next) stream_hist_next(A, g);  // the history moves on in the same launch
     fetch(kbeg);
+    bool bad = false;  // an activation beyond the f16 range
     for (int k0 = kbeg; k0 < kend; k0 += BK) {
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             f16x4v hi, lo;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                hi[e] = _Float16(ra[q][e]);
-                lo[e] = _Float16(ra[q][e] - float(hi[e]));
+                _Float16 h, l;
+                bad |= split_f16(ra[q][e], h, l);
+                hi[e] = h;
+                lo[e] = l;
             }
             *reinterpret_cast<f16x4v *>(&Ah[ar + 32 * q][ac]) = hi;
             *reinterpret_cast<f16x4v *>(&Al[ar + 32 * q][ac]) = lo;
@@ -359,9 +368,10 @@ __global__ __launch_bounds__(256) void k_gemm_x3(const uint8_t *__restrict__ w, 
             f16x8v hi, lo;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float v = rw[e] * kWs;
-                hi[e] = _Float16(v);
-                lo[e] = _Float16(v - float(hi[e]));
+                _Float16 h, l;
+                bad |= split_f16(rw[e] * kWs, h, l);  // |w| >= 64 (the callers route such weights to k_gemm_f32)
+                hi[e] = h;
+                lo[e] = l;
             }
             *reinterpret_cast<f16x8v *>(&Bh[wr][wc]) = hi;
             *reinterpret_cast<f16x8v *>(&Bl[wr][wc]) = lo;
@@ -395,6 +405,7 @@ __global__ __launch_bounds__(256) void k_gemm_x3(const uint8_t *__restrict__ w, 
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] *= kWsInv;
+    raise_status(g.status, bad, kStatusF16Range);
     if (g.kchunk) return gemm_store_partial<2, 2>(acc, g, m0, n0, wm, wn, lane);
     gemm_epilogue<EPI, 2, 2>(acc, g, m0, n0, wm, wn, lane);
 }
@@ -459,6 +470,7 @@ __global__ __launch_bounds__(256) void k_gemm_h16(const uint8_t *__restrict__ w,
         }
     };
     fetch(kbeg);
+    bool bad = false;  // an activation beyond the f16 range
     for (int k0 = kbeg; k0 < kend; k0 += BK) {
 #pragma unroll
         for (int q = 0; q < AQ; ++q) {
@@ -466,8 +478,10 @@ __global__ __launch_bounds__(256) void k_gemm_h16(const uint8_t *__restrict__ w,
             f16x4v hi, lo;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                hi[e] = _Float16(ra[q][e]);
-                lo[e] = _Float16(ra[q][e] - float(hi[e]));
+                _Float16 h, l;
+                bad |= split_f16(ra[q][e], h, l);
+                hi[e] = h;
+                lo[e] = l;
             }
             *reinterpret_cast<f16x4v *>(&Ah[r][c]) = hi;
             *reinterpret_cast<f16x4v *>(&Al[r][c]) = lo;
@@ -525,6 +539,7 @@ __global__ __launch_bounds__(256) void k_gemm_h16(const uint8_t *__restrict__ w,
         }
         __syncthreads();
     }
+    raise_status(g.status, bad, kStatusF16Range);
     if (g.kchunk) return gemm_store_partial<TM, TN>(acc, g, m0, n0, wm, wn, lane);
     gemm_epilogue<EPI, TM, TN>(acc, g, m0, n0, wm, wn, lane);
 }
@@ -567,6 +582,7 @@ __global__ __launch_bounds__(256) void k_gemm_h16b(const uint8_t *__restrict__ w
         for (int j = 0; j < 2; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
     u32x4 xa[S][4], xw[S][WQ];
     float xs[S];
+    bool bad = false;  // an activation beyond the f16 range
     auto fetch = [&](u32x4(&a)[4], u32x4(&b)[WQ], float &sc, int k0) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) a[q] = buf_ld16(ra, va[q], k0 * 4);
@@ -581,8 +597,10 @@ __global__ __launch_bounds__(256) void k_gemm_h16b(const uint8_t *__restrict__ w
             f16x4v hi, lo;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                hi[e] = _Float16(x[e]);
-                lo[e] = _Float16(x[e] - float(hi[e]));
+                _Float16 h, l;
+                bad |= split_f16(x[e], h, l);
+                hi[e] = h;
+                lo[e] = l;
             }
             *reinterpret_cast<f16x4v *>(&Ah[ar + 16 * q][ac]) = hi;
             *reinterpret_cast<f16x4v *>(&Al[ar + 16 * q][ac]) = lo;
@@ -667,6 +685,7 @@ __global__ __launch_bounds__(256) void k_gemm_h16b(const uint8_t *__restrict__ w
             __syncthreads();
         }
     }
+    raise_status(g.status, bad, kStatusF16Range);
     if (g.kchunk) return gemm_store_partial<2, 2>(acc, g, m0, n0, wm, wn, lane);
     gemm_epilogue<EPI, 2, 2>(acc, g, m0, n0, wm, wn, lane);
 }
@@ -876,16 +895,18 @@ __global__ __launch_bounds__(256) void k_splitk_acc_rms_h16(GemmArgs g, int32_t 
     }
     ss = block_sum<256>(ss, red);
     const float inv = 1.0f / sqrtf(ss / float(g.n) + eps);
+    bool bad = false;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         const int c = int(threadIdx.x) + 256 * k;
         if (c < g.n) {
-            const float v = gamma[c] * (hv[k] * inv);
-            const _Float16 hi = _Float16(v);
+            _Float16 hi, lo;
+            bad |= split_f16(gamma[c] * (hv[k] * inv), hi, lo);
             out16[int64_t(row) * ldo + c] = hi;
-            out16[lo_off + int64_t(row) * ldo + c] = _Float16(v - float(hi));
+            out16[lo_off + int64_t(row) * ldo + c] = lo;
         }
     }
+    raise_status(g.status, bad, kStatusF16Range);
 }
 
 // Merge of the kAttnMaxSplits attention partials of m rows into ao [m][heads * hd] (the PRO_ATTN prologue of the

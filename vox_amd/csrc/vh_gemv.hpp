@@ -287,14 +287,17 @@ __global__ __launch_bounds__(kGemvThreads) void k_quant_rows(GemvArgs a, int8_t 
 }
 
 // Fixed-point form of the FFN's down product: units of 2^-32, summed exactly (and so in any order) by integer
-// atomics. A term is clamped to +-2^21 (far outside activation ranges), so the sum of up to 1024 of them stays
-// inside int64; NaN becomes 0.
+// atomics. A term may span +-2^18 (2^50 units): with at most 1024 groups plus the bias, any sum of terms, and the
+// sum of the kAccCopies planes, stays below 2^61 units, inside int64. A term outside that range, infinite or NaN
+// cannot be represented: it is clamped, so every sum stays defined, and `bad` is set, so the call fails
+// (kStatusFixRange) and the caller computes the FFN another way instead of using a masked value.
 constexpr float kFixOne = 4294967296.0f;
-VH_DEV int64_t fix_of(float v) {
-    const float lim = 9007199254740992.0f;  // 2^53 units = 2^21
-    float t = __builtin_rintf(v * kFixOne);
-    t = t == t ? fminf(fmaxf(t, -lim), lim) : 0.f;
-    return int64_t(t);
+VH_DEV int64_t fix_of(float v, bool &bad) {
+    const float lim = 1125899906842624.0f;  // 2^50 units = 2^18
+    const float t = __builtin_rintf(v * kFixOne);
+    const bool in = fabsf(t) <= lim;  // false for infinities and NaN
+    bad |= !in;
+    return int64_t(in ? t : (t > 0.f ? lim : -lim));
 }
 // The pending value of element i: the kAccCopies partial sums added as integers, then one rounding to float.
 VH_DEV float acc_value(const int64_t (&c)[kAccCopies]) {

@@ -139,6 +139,7 @@ template <int HD>
 static hipError_t prefill_attn_hd(const PrefillAttnArgs &a0, hipStream_t s) {
     PrefillAttnArgs a = a0;
     a.splits = pattn_splits(a0);
+    a.status = status_word();
     const dim3 grid(unsigned((a.m + 63) / 64), unsigned(a.heads), unsigned(a.splits));
     hipError_t e = launch(k_prefill_attn<HD>, grid, dim3(256), 0, s, a);
     if (e != hipSuccess || a.splits == 1) return e;
@@ -209,7 +210,7 @@ hipError_t launch_rmsnorm_rows_h16(const float *x, int64_t ldx, const float *w, 
                                    int64_t ldo, int64_t lo_off, int m, hipStream_t s) {
     if (m <= 0) return hipSuccess;
     if (!out16 || ldo < K || lo_off < int64_t(m) * ldo) return hipErrorInvalidValue;
-    return launch(k_rmsnorm_rows_h16, dim3(m), dim3(256), 0, s, x, ldx, w, K, eps, out16, ldo, lo_off);
+    return launch(k_rmsnorm_rows_h16, dim3(m), dim3(256), 0, s, x, ldx, w, K, eps, out16, ldo, lo_off, status_word());
 }
 hipError_t launch_q8_to_f16(const int8_t *q, _Float16 *out, int64_t n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
@@ -227,6 +228,11 @@ hipError_t launch_fill_cache(void *c, int64_t planes, int64_t cap, int64_t len, 
     if (pairs <= 0) return hipSuccess;
     return launch(k_fill_cache, grid1(pairs, 256), dim3(256), 0, s, static_cast<_Float16 *>(c), planes, cap, len, hd,
                        seed, stream, mean, std);
+}
+
+hipError_t launch_absmax(const float *x, int64_t n, uint32_t *out, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    return launch(k_absmax, dim3(unsigned(std::min<int64_t>(1024, (n + 255) / 256))), dim3(256), 0, s, x, n, out);
 }
 
 hipError_t launch_copy16(const void *src, void *dst, int64_t bytes, hipStream_t s) {

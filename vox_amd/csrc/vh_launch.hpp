@@ -22,6 +22,10 @@ hipError_t launch(K kernel, dim3 grid, dim3 block, size_t smem, hipStream_t s, A
     return hipGetLastError();
 }
 
+// The library's range-status word (kStatusF16Range, kStatusFixRange), in device memory; null before init. The
+// launchers of kernels that can meet an unrepresentable value hand it to them.
+int32_t *status_word();
+
 // GEMV launch: rows/K/m etc. in a; wt = weight type; int_path = int8 activations (Q8 m <= 8, Q4 always).
 // Picks the row block M and the tile (R rows per wave, IT 1 KiB chunks in flight per row) from the shape.
 // The int path's prologue of a pass of m rows, once per row, into q [m][K] int8, qs / qsum [m][K/32]; the GEMV
@@ -72,6 +76,8 @@ hipError_t launch_fill_normal(float *out, int64_t n, uint64_t seed, uint32_t str
 hipError_t launch_fill_cache(void *c, int64_t planes, int64_t cap, int64_t len, int hd, uint64_t seed, uint32_t stream,
                              float mean, float std, hipStream_t s);
 
+// max |x| over n floats into *out as float bits (the caller zeroes *out; NaN reads as above every value)
+hipError_t launch_absmax(const float *x, int64_t n, uint32_t *out, hipStream_t s);
 hipError_t launch_copy16(const void *src, void *dst, int64_t bytes, hipStream_t s);
 // Attention one block per (head, row) for any even head_dim <= 128 (q from k_qk_post, keys from each row's cache).
 hipError_t launch_attn_rows(const AttnRowsArgs &a, int m, hipStream_t s);
@@ -119,7 +125,7 @@ hipError_t launch_mat_gather(const uint8_t *w, const void *scale, int wt, int s1
 // A pass of the code-predictor frame loop: row table + RoPE rows of the pass, the sampled code's embedding row.
 hipError_t launch_pred_embed(const PredEmbedArgs &a, hipStream_t s);
 
-// The fused one-row FFN (k_ffn_int): Q8 / Q4 / Q4H layers with H % 32 == 0, I % 32 == 0, H <= 4096; the down weights
+// The fused one-row FFN (k_ffn_int): Q8 / Q4 / Q4H layers with H % 32 == 0, I % 32 == 0, H <= kFfnMaxH (2048); the down weights
 // as panels (launch_panel_pack); adds its down product to a.acc (zero on entry) in fixed point.
 bool ffn_shape_ok(int wt, int H, int I);
 int ffn_parts();

@@ -47,13 +47,15 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
                 x0 = *reinterpret_cast<const pf32x4 *>(src);
                 x1 = *reinterpret_cast<const pf32x4 *>(src + 4);
             }
+            bool bad = false;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float x = e < 4 ? x0[e] : x1[e - 4];
-                const _Float16 hi = _Float16(x);
+                _Float16 hi, lo;
+                bad |= split_f16(e < 4 ? x0[e] : x1[e - 4], hi, lo);
                 qh[c][e] = hi;
-                ql[c][e] = _Float16(x - float(hi));
+                ql[c][e] = lo;
             }
+            raise_status(a.status, bad, kStatusF16Range);
         }
     }
     float mrow[4], lrow[4];

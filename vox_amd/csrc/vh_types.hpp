@@ -4,6 +4,10 @@
 
 namespace vh {
 
+// The library's range-status word: a kernel whose arithmetic cannot represent a value it was given sets a bit, and
+// the synchronous entry points fail the call when one is set (so the engine computes it on the CPU instead).
+enum : int32_t { kStatusF16Range = 1, kStatusFixRange = 2 };
+
 // GEMV input prologues: x as is; RMSNorm(x, gamma); or the merge of split-K attention partials.
 // GEMV prologues; PRO_Q (int path only): the input rows arrive already quantized (k_quant_rows)
 enum { PRO_X = 0, PRO_RMS = 1, PRO_ATTN = 2, PRO_Q = 3 };
@@ -90,6 +94,7 @@ struct FfnArgs {
     int64_t *acc;         // [kAccCopies][H] fixed-point (2^-32) sums of the down product
     int32_t H, I, parts;  // parts: blocks per group, each taking H / parts of the down rows
     float eps;
+    int32_t *status;      // the range-status word (a down term outside the fixed-point range); set by the launcher
 };
 
 constexpr int kGemvThreads = 256;
@@ -135,6 +140,7 @@ struct PrefillAttnArgs {
     // and writes (max, sum, unnormalized output) to part's slot z; k_pattn_merge then writes out / out16
     AttnPartials part;
     int32_t splits;
+    int32_t *status;  // the range-status word (queries beyond the f16 range of the split products)
 };
 
 // Attention of m rows, one block per (head, row), for any even head_dim <= 128: q [m][heads hd] already normed and
@@ -200,6 +206,12 @@ struct GemmArgs {
     int32_t kchunk;
     float *ws;
     int64_t ws_cap;  // floats available at ws (0: no split)
+    // the range-status word (kStatusF16Range when a value split into f16 halves is beyond the f16 range); the public
+    // launchers set it
+    int32_t *status;
+    // F32 weights with max |w| >= 63 (or NaN): the split kernel's 2^10-scaled f16 halves cannot hold them, so they
+    // take k_gemm_f32
+    int32_t f32_wide;
 };
 
 // CosyVoice2 LM sampling (lm_logp + ras_sample + lm_generate's trial loop, cosyvoice.cpp:598-690).
@@ -242,6 +254,7 @@ struct NormArgs {
     const float *sc, *sh, *tb;
     double eps;
     int32_t R, D, affine, mish;
+    int32_t *status;  // the range-status word (y16 values beyond the f16 range); set by the launcher
 };
 
 // One pass of the code-predictor frame loop (gpu_pred_frame): the pass's m rows of the sequence at positions

@@ -16,8 +16,9 @@ __global__ void k_quant_q8(const float *w, int64_t nblocks, int8_t *q, float *sc
     for (int j = 0; j < 32; ++j) q[b * 32 + j] = s > 0.f ? int8_t(int(roundf(p[j] / s))) : int8_t(0);
 }
 
-// quantize_q4 (kernels.cpp:606-645): scale search d = mx / -t for t = 7, 7.25 .. 9 by squared error (double),
-// then the least-squares scale when it is better. Packs byte j = (q[j] + 8) | (q[j + 16] + 8) << 4.
+// quantize_q4 (kernels.cpp:606-645): scale search d = mx / -t for t = 7, 7.25 .. 9 by squared error (summed in
+// double, kept as a float as kernels.cpp:616 declares it, so a stored error is rounded and later compared widened),
+// then the least-squares scale when its double error is below that float. Packs byte j = (q[j] + 8) | (q[j + 16] + 8) << 4.
 __global__ void k_quant_q4(const float *w, int64_t nblocks, uint8_t *q, float *scale) {
 #pragma clang fp contract(off)
     const int64_t b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -25,8 +26,7 @@ __global__ void k_quant_q4(const float *w, int64_t nblocks, uint8_t *q, float *s
     const float *p = w + b * 32;
     float mx = 0.f;
     for (int j = 0; j < 32; ++j) if (fabsf(p[j]) > fabsf(mx)) mx = p[j];
-    float best_d = mx / -8.0f;
-    double best_err = INFINITY;
+    float best_d = mx / -8.0f, best_err = INFINITY;
     int8_t best_q[32];
     for (int j = 0; j < 32; ++j) best_q[j] = 0;
     if (mx != 0.0f)
@@ -42,8 +42,8 @@ __global__ void k_quant_q4(const float *w, int64_t nblocks, uint8_t *q, float *s
                 const double e = double(p[j]) - double(qq[j]) * double(d);
                 err += e * e;
             }
-            if (err < best_err) {
-                best_err = err; best_d = d;
+            if (err < double(best_err)) {
+                best_err = float(err); best_d = d;
                 for (int j = 0; j < 32; ++j) best_q[j] = qq[j];
             }
         }
@@ -54,7 +54,7 @@ __global__ void k_quant_q4(const float *w, int64_t nblocks, uint8_t *q, float *s
             const float d2 = float(num / den);
             double err = 0;
             for (int j = 0; j < 32; ++j) { const double e = double(p[j]) - double(best_q[j]) * double(d2); err += e * e; }
-            if (err < best_err) best_d = d2;
+            if (err < double(best_err)) best_d = d2;
         }
     }
     scale[b] = best_d;
@@ -96,10 +96,11 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *x, int64_t ld
 // Rows of up to 8 x 256 values keep the row and the weights in registers, both loaded before the sum, so the
 // weights' round trip overlaps the row's; the sums and products are those of the loop below.
 __global__ __launch_bounds__(256) void k_rmsnorm_rows_h16(const float *x, int64_t ldx, const float *w, int K, float eps,
-                                                         _Float16 *out16, int64_t ldo, int64_t lo_off) {
+                                                         _Float16 *out16, int64_t ldo, int64_t lo_off, int32_t *status) {
     __shared__ float red[4];
     const float *xr = x + int64_t(blockIdx.x) * ldx;
     float ss = 0.f;
+    bool bad = false;  // a normed value beyond the f16 range
     if (K <= 8 * 256) {
         float xv[8], wv[8];
 #pragma unroll
@@ -118,22 +119,24 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows_h16(const float *x, int64_
         for (int c = 0; c < 8; ++c) {
             const int i = threadIdx.x + 256 * c;
             if (i >= K) continue;
-            const float v = wv[c] * (xv[c] * inv);
-            const _Float16 hi = _Float16(v);
+            _Float16 hi, lo;
+            bad |= split_f16(wv[c] * (xv[c] * inv), hi, lo);
             out16[int64_t(blockIdx.x) * ldo + i] = hi;
-            out16[lo_off + int64_t(blockIdx.x) * ldo + i] = _Float16(v - float(hi));
+            out16[lo_off + int64_t(blockIdx.x) * ldo + i] = lo;
         }
+        raise_status(status, bad, kStatusF16Range);
         return;
     }
     for (int i = threadIdx.x; i < K; i += 256) ss = fmaf(xr[i], xr[i], ss);
     ss = block_sum<256>(ss, red);
     const float inv = 1.0f / sqrtf(ss / float(K) + eps);
     for (int i = threadIdx.x; i < K; i += 256) {
-        const float v = w[i] * (xr[i] * inv);
-        const _Float16 hi = _Float16(v);
+        _Float16 hi, lo;
+        bad |= split_f16(w[i] * (xr[i] * inv), hi, lo);
         out16[int64_t(blockIdx.x) * ldo + i] = hi;
-        out16[lo_off + int64_t(blockIdx.x) * ldo + i] = _Float16(v - float(hi));
+        out16[lo_off + int64_t(blockIdx.x) * ldo + i] = lo;
     }
+    raise_status(status, bad, kStatusF16Range);
 }
 
 // int8 weight values widened to f16 (exact: |q| <= 127), 8 per thread; n a multiple of 8.
@@ -164,6 +167,15 @@ __global__ void k_fill_normal(float *out, int64_t n, uint64_t seed, uint32_t str
     normal_pair(seed, stream, uint64_t(p), &z0, &z1);
     out[2 * p] = mean + std * z0;
     if (2 * p + 1 < n) out[2 * p + 1] = mean + std * z1;
+}
+
+// max |x| of n floats as the bits of a non-negative float in *out (zero on entry): non-negative floats order as
+// their bits, and a NaN's |x| bits (0x7fc00000 and up) exceed every finite value's and infinity's. Grid-stride.
+__global__ void k_absmax(const float *x, int64_t n, uint32_t *out) {
+    uint32_t m = 0;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
+        m = max(m, __float_as_uint(x[i]) & 0x7fffffffu);
+    if (m) atomicMax(out, m);
 }
 
 // Fills positions [0, len) of a [layers*kvh][cap][hd] f16 cache with N(mean, std).

@@ -71,6 +71,7 @@ struct GpuMat {
     float *b = nullptr;
     uint64_t bytes = 0;  // weights + scales + bias bytes (the GEMV's algorithmic stream)
     _Float16 *w16 = nullptr;  // Q8: the int8 values widened to f16 for the split-f16 GEMM, made on first use
+    float wmax = 0.f;  // F32: max |w| (NaN when a weight is NaN), which picks the GEMM kernel (f32_wide)
 };
 
 struct LayerDev {
@@ -203,6 +204,9 @@ struct Ctx {
     LmCfgDev *lm_cfg_dev = nullptr;
     LmState *lm_state_dev = nullptr;
     uint8_t *lm_host = nullptr;
+    // the range-status word (allocated and zeroed at init) and its pinned host copy; word 1 of the device block is
+    // the scratch of the weight max |w| reduction
+    int32_t *status_dev = nullptr, *status_pin = nullptr;
 };
 
 Ctx g;
@@ -210,6 +214,13 @@ Ctx g;
 void set_error(const std::string &e) {
     g.last_error = e;
 }
+}  // namespace
+
+namespace vh {
+int32_t *status_word() { return g.status_dev; }
+}  // namespace vh
+
+namespace {
 
 // ------------------------------------------------------------------ device memory with accounting
 void *dalloc(size_t bytes) {
@@ -257,6 +268,25 @@ float *dev_scratch(float *&p, size_t &cap, size_t bytes) {
     return p;
 }
 
+// The end of a synchronous call: waits for the stream, then fails the call when one of its kernels set the
+// range-status word (an activation beyond the f16 range of a split-f16 product, or a fused-FFN term outside the
+// fixed-point range), clearing the word for the next call. The engine then computes the call on the CPU, as for any
+// failed device call. Device-resident calls (decode_dev, the no-alloc matmul) are reported by voxhip_sync.
+void sync_status() {
+    HIPCHECK(hipMemcpyAsync(g.status_pin, g.status_dev, sizeof(int32_t), hipMemcpyDeviceToHost, g.stream));
+    HIPCHECK(hipStreamSynchronize(g.stream));
+    const int32_t v = g.status_pin[0];
+    if (!v) return;
+    g.status_pin[0] = 0;
+    HIPCHECK(hipMemsetAsync(g.status_dev, 0, sizeof(int32_t), g.stream));
+    HIPCHECK(hipStreamSynchronize(g.stream));
+    std::string what;
+    if (v & vh::kStatusF16Range) what = "an activation beyond the f16 range of the split-f16 matrix products";
+    if (v & vh::kStatusFixRange)
+        what += std::string(what.empty() ? "" : "; ") + "a fused-FFN term that is not finite or beyond +-2^18 (fixed-point range)";
+    throw Fail("value outside the device arithmetic's range: " + what);
+}
+
 void h2d(void *dst, const void *src, size_t bytes) {
     if (!bytes) return;
     HIPCHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
@@ -295,6 +325,21 @@ void check_shape(int32_t type, int64_t rows, int64_t cols) {
 
 size_t scale_row_bytes(const GpuMat &m) { return quantized(m.type) ? size_t(m.cols / 32) * (m.s16 ? 2 : 4) : 0; }
 int gemv_type(const GpuMat &m) { return m.type == VOXHIP_Q4 && m.s16 ? WT_Q4H : m.type; }
+// F32 weights the split-f16 kernel cannot hold (its f16 halves of 2^10 w overflow from |w| >= 64; NaN counts): they
+// take the f32 matrix cores (GemmArgs::f32_wide).
+constexpr float kF32SplitMaxW = 63.0f;
+bool f32_wide(float wmax) { return !(wmax < kF32SplitMaxW); }
+bool f32_wide(const GpuMat &m) { return m.type == VOXHIP_F32 && f32_wide(m.wmax); }
+// max |w| of n host floats (NaN when one is NaN)
+float host_absmax(const float *w, size_t n) {
+    float mx = 0.f;
+    for (size_t i = 0; i < n; ++i) {
+        const float a = std::fabs(w[i]);
+        if (!(a <= mx)) mx = a;  // a NaN replaces the max and is never replaced (nothing compares above it)
+        if (std::isnan(mx)) break;
+    }
+    return mx;
+}
 
 // f32 -> f16 bits when the value is exactly representable as a normal or zero f16 (the scales a device Q4 matrix
 // may store in 2 bytes without changing its arithmetic).
@@ -361,6 +406,10 @@ int upload_parts(const voxhip_mat *parts, int n, bool interleave2) {
     }
     const int id = new_mat(P0.type, rows, P0.cols, all_bias, use16);
     GpuMat &m = g.mats[size_t(id)];
+    if (P0.type == VOXHIP_F32)
+        for (int i = 0; i < n; ++i)
+            m.wmax = std::max(m.wmax, host_absmax(static_cast<const float *>(parts[i].data), size_t(parts[i].rows * P0.cols)),
+                              [](float a, float b) { return a < b || std::isnan(b); });
     const size_t rb = row_bytes(P0.type, P0.cols), sb = scale_row_bytes(m);
     auto scale_src = [&](int i) -> const uint8_t * {
         return use16 ? reinterpret_cast<const uint8_t *>(s16[size_t(i)].data()) : reinterpret_cast<const uint8_t *>(parts[i].scale);
@@ -450,6 +499,7 @@ void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, in
         ga.bias = m.b; ga.y = y; ga.lda = lda; ga.ldy = ldy; ga.m = mc; ga.n = int32_t(m.rows); ga.K = int32_t(m.cols);
         ga.ws = sc.ws; ga.ws_cap = sc.ws_cap;
         ga.gate = yscale;  // a row scale of the GEMV is the GEMM's gated residual (y += gate[col] (c + bias))
+        ga.f32_wide = f32_wide(m);
         HIPCHECK(launch_gemm(gemv_type(m), yscale ? EPI_GATED_ACC : epi, m.w, m.s, A, ga, s));
         return;
     }
@@ -652,11 +702,19 @@ const _Float16 *planes_weights(GpuMat &m, hipStream_t s) {
     }
     return m.w16;
 }
+// The widened copies are an optimisation: when one cannot be allocated (VRAM limit or device memory), its matrix keeps
+// m.w16 null, planes_layer(need_ready) then sends that layer to the f32-activation GEMM, and the pass still runs.
 void prepare_planes(Xfmr &X, int first, int count, int64_t m_total, int mc, hipStream_t s) {
     for (int li = first; li < first + count; ++li)
         if (planes_layer(X, li, m_total, mc, false)) {
             const LayerDev &L = X.L[size_t(li)];
-            for (int id : {L.qkv, L.o, L.gu, L.down}) (void)planes_weights(g.mats[size_t(id)], s);
+            for (int id : {L.qkv, L.o, L.gu, L.down}) {
+                try {
+                    (void)planes_weights(g.mats[size_t(id)], s);
+                } catch (const Fail &) {
+                    (void)hipGetLastError();  // a failed hipMalloc leaves its error for the next query
+                }
+            }
         }
 }
 
@@ -903,7 +961,7 @@ int forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_proj
             }
         }
     }
-    HIPCHECK(hipStreamSynchronize(g.stream));
+    sync_status();
     return last_row;
 }
 
@@ -939,8 +997,10 @@ void make_ffn_panels(Xfmr &X) {
     // launch saved at FFN width 3 H (the Qwen3-TTS talker and code predictor), while FFNs of 4 H and wider (the
     // CosyVoice2 LM's 896 -> 4864) gain. VOXHIP_FFN_FUSED=1 forces it on, =0 off.
     const bool force = env && env[0] == '1';
+    // The q|k|v and o GEMVs that add the pending sums stage their input rows (K = H and K = heads x hd) with one
+    // 8-value slot per thread, so both widths must fit 8 x kGemvThreads.
     bool ok = !(env && env[0] == '0') && (force || int64_t(X.I) >= 4 * int64_t(X.H)) && (X.hd == 64 || X.hd == 128) &&
-              X.H <= 8 * kGemvThreads && !X.L.empty();
+              X.H <= 8 * kGemvThreads && int64_t(X.heads) * X.hd <= 8 * kGemvThreads && !X.L.empty();
     for (const LayerDev &L : X.L) {
         if (!ok) break;
         for (int id : {L.qkv, L.o, L.gu, L.down}) ok = ok && quantized(g.mats[size_t(id)].type);
@@ -1018,6 +1078,8 @@ int make_xfmr(const voxhip_xfmr_desc *w, const char *name, int use_layers, const
                     for (int id : ids)
                         if (g.mats[size_t(id)].s16 != m0.s16) throw Fail("stacked matrices differ in scale storage");
                     const int nid = new_mat(m0.type, rows, m0.cols, bias, m0.s16);
+                    for (int id : ids) g.mats[size_t(nid)].wmax = std::max(g.mats[size_t(nid)].wmax, g.mats[size_t(id)].wmax,
+                                                                          [](float a, float b) { return a < b || std::isnan(b); });
                     const size_t rb = row_bytes(m0.type, m0.cols), sb = scale_row_bytes(m0);
                     int64_t r0 = 0;
                     int part = 0;
@@ -1149,6 +1211,10 @@ int voxhip_init(const char *device, char *err, size_t err_len) {
         g.qrows = dalloc_t<int8_t>(size_t(kQuantRowsElems));
         g.qrows_s = dalloc_t<float>(size_t(kQuantRowsElems / 32));
         g.qrows_sum = dalloc_t<int32_t>(size_t(kQuantRowsElems / 32));
+        g.status_dev = dalloc_t<int32_t>(2);
+        HIPCHECK(hipMemset(g.status_dev, 0, 2 * sizeof(int32_t)));
+        HIPCHECK(hipHostMalloc(reinterpret_cast<void **>(&g.status_pin), 2 * sizeof(int32_t), hipHostMallocDefault));
+        g.status_pin[0] = g.status_pin[1] = 0;
         if (idx >= int(g.noalloc.size())) throw Fail("device index above the scratch table");
         void *sp = nullptr;
         HIPCHECK(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)));
@@ -1238,6 +1304,7 @@ int voxhip_matmul(int mat, const float *x, int64_t m, float *y) {
             HIPCHECK(hipStreamSynchronize(g.stream));
             std::memcpy(y + c0 * M.rows, pin, size_t(mc) * size_t(M.rows) * 4);
         }
+        sync_status();
         return 1;
     }, 0);
 }
@@ -1324,7 +1391,7 @@ int voxhip_convt(int mat, int32_t K, int32_t stride, int32_t pad, int32_t out_pa
         }
         HIPCHECK(launch_convt_gather(dz, dbias, dy, T, int(To), stride, K, pad, int(cout), g.stream));
         HIPCHECK(hipMemcpyAsync(pin, dy, yb, hipMemcpyDeviceToHost, g.stream));
-        HIPCHECK(hipStreamSynchronize(g.stream));
+        sync_status();
         std::memcpy(y, pin, yb);
         return 1;
     }, 0);
@@ -1529,7 +1596,7 @@ int voxhip_memcpy_d2h(void *dst, const void *d_src, size_t bytes) {
 int voxhip_sync(void) {
     return guard_int([&] {
         require_ok();
-        HIPCHECK(hipStreamSynchronize(g.stream));
+        sync_status();
         return 1;
     }, 0);
 }
@@ -1915,7 +1982,7 @@ int voxhip_lm_generate(int xfmr, int seq, const float *x, int64_t n, int head, i
                 }
             }
             HIPCHECK(hipMemcpyAsync(lm_host_state(0), X.lm_state, sizeof(LmState), hipMemcpyDeviceToHost, g.stream));
-            HIPCHECK(hipStreamSynchronize(g.stream));
+            sync_status();
             const LmState r = *lm_host_state(0);
             if (r.status) throw Fail("CosyVoice: sampling reaches max_trials and still gets eos when ignore_eos is True");
             // the counts come from device memory and size the copies into the caller's buffers (max_len entries,
@@ -1981,7 +2048,7 @@ int voxhip_pred_frame(int xfmr, int seq, const float *in2, int in_proj, const in
         HIPCHECK(hipGraphLaunch(exec, g.stream));
         HIPCHECK(hipMemcpyAsync(X.pred_host, X.pred_codes, size_t(G) * 4, hipMemcpyDeviceToHost, g.stream));
         HIPCHECK(hipMemcpyAsync(X.pred_host + kPredMaxGroups, X.pred_err, 4, hipMemcpyDeviceToHost, g.stream));
-        HIPCHECK(hipStreamSynchronize(g.stream));
+        sync_status();
         if (X.pred_host[kPredMaxGroups]) throw Fail("code out of the embedding's range");
         for (int cb = 1; cb < G; ++cb) codes[cb] = X.pred_host[cb];
         return 1;
@@ -1998,6 +2065,7 @@ struct F5Block {
 struct F5Conv {
     float *w = nullptr, *b = nullptr;  // w [groups][cout/groups][kpad] (K * cin/groups, zero-padded to a multiple of 8)
     int cin = 0, cout = 0, K = 0, groups = 0, kpad = 0;
+    bool wide = false;  // max |w| >= 63 or NaN: the conv GEMM on f32 matrix cores (GemmArgs::f32_wide)
 };
 struct F5VBlock {  // a Vocos ConvNeXt block (f5.cpp:235-240)
     F5Conv dw;     // depthwise, w [C][K]
@@ -2048,6 +2116,8 @@ int stack_rows(const std::vector<int> &ids) {
         any_bias = any_bias || m.b;
     }
     const int nid = new_mat(m0.type, rows, m0.cols, any_bias, m0.s16);
+    for (int id : ids) g.mats[size_t(nid)].wmax = std::max(g.mats[size_t(nid)].wmax, mat_at(id).wmax,
+                                                          [](float a, float b) { return a < b || std::isnan(b); });
     const GpuMat dst = g.mats[size_t(nid)];
     const size_t rb = row_bytes(m0.type, m0.cols), sb = scale_row_bytes(m0);
     int64_t r0 = 0;
@@ -2077,6 +2147,7 @@ F5Conv upload_conv_gemm(const voxhip_f5_conv &c, const char *what) {
     d.kpad = int((kc + 7) / 8 * 8);
     std::vector<float> w(size_t(c.cout) * size_t(d.kpad), 0.f);
     for (int64_t r = 0; r < int64_t(c.groups) * cog; ++r) std::memcpy(&w[size_t(r * d.kpad)], c.w + r * kc, size_t(kc) * 4);
+    d.wide = f32_wide(host_absmax(w.data(), w.size()));
     d.w = dalloc_t<float>(w.size());
     h2d(d.w, w.data(), w.size() * 4);
     if (c.b) {
@@ -2123,6 +2194,7 @@ GemmArgs gemm_args(const GpuMat &m, const float *bias, float *y, int64_t lda, in
     GemmArgs ga{};
     ga.bias = bias; ga.y = y; ga.lda = lda; ga.ldy = ldy; ga.m = int32_t(rows); ga.n = int32_t(m.rows); ga.K = int32_t(m.cols);
     ga.ws = g.gemm_ws; ga.ws_cap = kGemmWsFloats;
+    ga.f32_wide = f32_wide(m);
     return ga;
 }
 void f5_gemm(const GpuMat &m, int epi, const float *A, GemmArgs ga, hipStream_t s) {
@@ -2161,6 +2233,7 @@ void f5_enqueue(F5 &F, hipStream_t s) {
         GemmArgs ga{};
         ga.bias = cv.b; ga.y = c == 0 ? F.a : F.h; ga.lda = D; ga.ldy = D; ga.m = int32_t(R);
         ga.n = cv.cout / cv.groups; ga.cig = cv.cin / cv.groups; ga.ksize = cv.K; ga.K = cv.kpad; ga.seq = F.N;
+        ga.f32_wide = cv.wide;
         HIPCHECK(launch_conv_gemm(c == 0 ? EPI_MISH : EPI_MISH_ACC, cv.w, c == 0 ? F.h : F.a, ga, cv.groups, s));
     }
     const float scale = 1.0f / std::sqrt(float(F.hd));
@@ -2301,7 +2374,7 @@ int voxhip_f5_step(int id, const float *x, const float *ts, float *out) {
         h2d(F.x, x, size_t(F.N) * F.mel * 4);
         h2d(F.ts, ts, size_t(F.dim) * 4);
         f5_enqueue(F, g.stream);
-        HIPCHECK(hipStreamSynchronize(g.stream));
+        sync_status();
         HIPCHECK(hipMemcpy(out, F.out, size_t(F.B) * F.N * F.mel * 4, hipMemcpyDeviceToHost));
         return 1;
     }, 0);
@@ -2329,6 +2402,7 @@ int voxhip_f5_vocos(int id, const float *mel, int T, float *head) {
         GemmArgs ge{};
         ge.bias = ce.b; ge.y = F.vx; ge.lda = ce.cin; ge.ldy = VD; ge.m = T; ge.n = ce.cout / ce.groups;
         ge.cig = ce.cin / ce.groups; ge.ksize = ce.K; ge.K = ce.kpad; ge.seq = T;
+        ge.f32_wide = ce.wide;
         HIPCHECK(launch_conv_gemm(EPI_STORE, ce.w, F.vm, ge, ce.groups, s));
         HIPCHECK(launch_layernorm_rows(F.vx, T, VD, F.v_ln_w, F.v_ln_b, F.vx, s));
         for (const F5VBlock &b : F.vblocks) {
@@ -2343,7 +2417,7 @@ int voxhip_f5_vocos(int id, const float *mel, int T, float *head) {
         HIPCHECK(launch_layernorm_rows(F.vx, T, VD, F.v_fln_w, F.v_fln_b, F.vx, s));
         const GpuMat &Mh = mat_at(F.v_head);
         f5_gemm(Mh, EPI_STORE, F.vx, gemm_args(Mh, Mh.b, F.vhead, VD, F.vout, T), s);
-        HIPCHECK(hipStreamSynchronize(s));
+        sync_status();
         HIPCHECK(hipMemcpy(head, F.vhead, size_t(T) * F.vout * 4, hipMemcpyDeviceToHost));
         return 1;
     }, 0);
@@ -2459,6 +2533,7 @@ void cosy_conv(const Cosy &E, const F5Conv &cv, int epi, const float *X, int64_t
     ga.bias = cv.b; ga.y = Y; ga.lda = ldx; ga.ldy = ldy; ga.m = int32_t(2 * E.T); ga.n = cv.cout;
     ga.cig = cv.cin; ga.ksize = cv.K; ga.K = cv.kpad; ga.seq = E.T; ga.causal = 1;
     ga.ws = g.gemm_ws; ga.ws_cap = kGemmWsFloats;  // split K when the 64 x 64 tiles leave the CUs idle
+    ga.f32_wide = cv.wide;
     HIPCHECK(launch_conv_gemm(epi, cv.w, X, ga, 1, s));
 }
 
@@ -2653,7 +2728,7 @@ int voxhip_cosy_step(int id, const float *x, const float *tb, float *out) {
             E.step_graph = exec;
         }
         HIPCHECK(hipGraphLaunch(E.step_graph, g.stream));
-        HIPCHECK(hipStreamSynchronize(g.stream));
+        sync_status();
         HIPCHECK(hipMemcpy(out, E.out, size_t(2) * E.T * E.M * 4, hipMemcpyDeviceToHost));
         return 1;
     }, 0);
@@ -2787,6 +2862,7 @@ void codec_conv(const CodecConv &c, Hist2 *h, int par, const float *X, int64_t l
     ga.ws = g.gemm_ws; ga.ws_cap = kGemmWsFloats;
     if (ga.ctx && !h) throw Fail("codec convolution without its history");
     if (ga.ctx) ga.hist_next = h->b[1 - par];
+    ga.f32_wide = f32_wide(M);
     HIPCHECK(launch_stream_conv(gemv_type(M), snake ? EPI_SNAKE : EPI_STORE, M.w, M.s, X, ga, s));
 }
 // y (=, +=, gelu, gamma-gated +=) W x + bias over rows of the f32-activation GEMM (the f32 tile semantics of matmul
@@ -3139,7 +3215,7 @@ int voxhip_codec_forward(int codec, int state, const float *z, int F, float *pcm
             it = St.graphs.emplace(key, exec).first;
         }
         HIPCHECK(hipGraphLaunch(it->second, g.stream));
-        HIPCHECK(hipStreamSynchronize(g.stream));
+        sync_status();  // a failure leaves the state as it was (its parity and length unchanged)
         const int64_t n = int64_t(F) * E.spf;
         HIPCHECK(hipMemcpy(pcm, E.S[4], size_t(n) * 4, hipMemcpyDeviceToHost));
         St.len += F;
@@ -3177,7 +3253,14 @@ int voxhip_mat_synthetic(int32_t type, int64_t rows, int64_t cols, uint64_t seed
             }
             if (s16) HIPCHECK(launch_to_f16(sc32, int64_t(nsc), m.s, g.stream));
             if (with_bias) HIPCHECK(launch_fill_normal(m.b, rows, seed, stream + 0x10000u, 0.f, std, g.stream));
+            if (type == VOXHIP_F32) {  // max |w|, in word 1 of the status block
+                uint32_t *mx = reinterpret_cast<uint32_t *>(g.status_dev + 1);
+                HIPCHECK(hipMemsetAsync(mx, 0, 4, g.stream));
+                HIPCHECK(launch_absmax(tmp, int64_t(n), mx, g.stream));
+                HIPCHECK(hipMemcpyAsync(g.status_pin + 1, mx, 4, hipMemcpyDeviceToHost, g.stream));
+            }
             HIPCHECK(hipStreamSynchronize(g.stream));
+            if (type == VOXHIP_F32) m.wmax = __builtin_bit_cast(float, uint32_t(g.status_pin[1]));
         } catch (...) {
             release();
             throw;
