@@ -271,7 +271,8 @@ typedef struct voxhip_f5_vblock {
     const float *ln_w, *ln_b, *gamma; /* [vocos_dim] */
     int32_t pw1, pw2;                 /* matrix handles: vocos_inter x vocos_dim, vocos_dim x vocos_inter */
 } voxhip_f5_vblock;
-/* GpuF5Desc (gpu.hpp:67-81). dim_head must be 64. vocos_dim 0: no Vocos (gpu_f5_vocos then fails and the caller
+/* GpuF5Desc (gpu.hpp:67-81). dim_head even and <= 64 (as gpu_f5.cpp:211; heads below 64 run on zero-padded
+ * attention tiles). vocos_dim 0: no Vocos (gpu_f5_vocos then fails and the caller
  * runs the vocoder on the CPU); else v_embed (mel_dim -> vocos_dim), the norms, n_vblocks blocks and v_head
  * (vocos_out x vocos_dim). */
 typedef struct voxhip_f5_desc {
@@ -318,7 +319,7 @@ typedef struct voxhip_cosy_x {
     int32_t q, k, v, o, ff1, ff2, ff_dim;
 } voxhip_cosy_x;
 /* GpuCosyDesc (gpu.hpp:103-113). The reference's vector of mid transformer lists is flattened: mid block i owns
- * mid_x_count[i] consecutive entries of mid_x. head_dim must be 64, C a multiple of 4. */
+ * mid_x_count[i] consecutive entries of mid_x. head_dim even and <= 64 (as gpu_f5.cpp:425), C a multiple of 4. */
 typedef struct voxhip_cosy_desc {
     int32_t M, C, heads, head_dim;
     voxhip_cosy_res down_res, up_res;

@@ -40,6 +40,14 @@ def test_cosy_step_small(hip, oracle, wtype, T):
     run(hip, oracle, m, T, seed=T)
 
 
+@pytest.mark.parametrize("wtype,hd,T", [(F16, 32, 40), (Q8, 32, 64), (F32, 48, 9), (BF16, 22, 33)])
+def test_cosy_step_head_dim_below_64(hip, oracle, wtype, hd, T):
+    # any even head_dim <= 64, as gpu_f5.cpp:425 (Chatterbox's estimator has 8 x 64, other checkpoints fewer dims):
+    # the attention runs on heads padded with zero dims to 64 (q8 needs whole 32-column scale blocks)
+    m = CosyModel(80 + hd, M=8, C=64, heads=4, head_dim=hd, n_mid=1, n_x=1, ff=128, wtype=wtype)
+    run(hip, oracle, m, T, seed=hd)
+
+
 def test_cosy_step_f16_row_path(hip, oracle):
     # ff 96 is not a multiple of 64: the f16 linears take the f32-row GEMM with the same epilogues
     m = CosyModel(75, M=8, C=64, heads=1, head_dim=64, n_mid=2, n_x=1, ff=96, wtype=F16)
@@ -60,8 +68,11 @@ def test_cosy_step_full_width(hip, oracle):
 
 
 def test_cosy_begin_again_and_rejects(hip, oracle):
-    m = CosyModel(78, M=8, C=64, heads=2, head_dim=32, n_mid=1, n_x=1, ff=128, wtype=F16)
+    m = CosyModel(78, M=8, C=64, heads=2, head_dim=96, n_mid=1, n_x=1, ff=128, wtype=F16)  # above 64 (gpu_f5.cpp:425)
     with pytest.raises(hip.VoxHipError, match="head_dim"):
+        m.create(hip)
+    m = CosyModel(78, M=8, C=64, heads=2, head_dim=48, n_mid=1, n_x=1, ff=128, wtype=Q8)  # q8 padding: 32-column blocks
+    with pytest.raises(hip.VoxHipError, match="multiple of 32"):
         m.create(hip)
     m = CosyModel(79, M=8, C=64, heads=2, head_dim=64, n_mid=1, n_x=1, ff=128, wtype=F16)
     est = m.create(hip)

@@ -70,10 +70,20 @@ def test_f5_step_wide_tiles_partial(hip, oracle):
     run(hip, oracle, m, 2, 1000, seed=9)
 
 
+@pytest.mark.parametrize("wtype,hd,pe,B,N", [(F16, 32, 1, 2, 70), (F16, 48, 0, 1, 130), (BF16, 34, 2, 2, 33),
+                                             (F32, 16, 0, 1, 64)])
+def test_f5_step_head_dim_below_64(hip, oracle, wtype, hd, pe, B, N):
+    # any even dim_head <= 64, as gpu_f5.cpp:211: q|k|v and to_out are padded per head to the attention tiles' 64
+    # dims with zero rows / columns at create; RoPE rotates the model's own dims from its [N][hd/2] table
+    m = F5Model(90 + hd, 128, 2, 4, dim_head=hd, mel=20, text=32, K=7, groups=4, pe_attn_head=pe, wtype=wtype)
+    run(hip, oracle, m, B, N, seed=hd, steps=2)
+
+
 def test_f5_rejects_bad_shapes(hip):
-    m = F5Model(60, 128, 1, 2, dim_head=32, wtype=F16)
-    with pytest.raises(hip.VoxHipError, match="head_dim"):
-        m.create(hip)
+    for heads, hd in ((2, 80), (8, 33)):  # above 64, odd (gpu_f5.cpp:211)
+        m = F5Model(60, 128, 1, heads, dim_head=hd, wtype=F16)
+        with pytest.raises(hip.VoxHipError, match="head_dim"):
+            m.create(hip)
     m = F5Model(61, 128, 1, 2, wtype=F16)
     f5 = m.create(hip)
     with pytest.raises(hip.VoxHipError, match="before begin"):

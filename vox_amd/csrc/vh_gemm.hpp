@@ -155,8 +155,9 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
                     float r = c;
                     if (col < g.rope_cols && g.rope) {
                         const int inner = g.rope_cols / 2, d = col % g.hd, head = (col % inner) / g.hd;
-                        if (g.rope_heads <= 0 || head < g.rope_heads) {
-                            const float *cs = g.rope + ((int64_t(row % g.seq) * (g.hd / 2) + d / 2) * 2);
+                        const int rhd = g.rope_hd ? g.rope_hd : g.hd;  // the padding dims (d >= rhd) stay zero
+                        if (d < rhd && (g.rope_heads <= 0 || head < g.rope_heads)) {
+                            const float *cs = g.rope + ((int64_t(row % g.seq) * (rhd / 2) + d / 2) * 2);
                             const float cc = cs[0], sn = cs[1];
                             r = (col & 1) ? c * cc + o * sn : c * cc - o * sn;
                         }

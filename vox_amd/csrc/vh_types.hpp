@@ -175,6 +175,9 @@ struct GemmArgs {
     // rope_cols rotate (q | k heads), heads >= rope_heads of each of q and k are left as they are
     const float *rope;
     int32_t seq, hd, rope_cols, rope_heads;
+    // heads padded with zero dims to hd (the attention tiles' 64): the table's head dim and the dims that rotate,
+    // d < rope_hd (0: hd)
+    int32_t rope_hd;
     // EPI_ROPE_H16: the rotated q | k and v as f16 halves (x = hi + lo) for the attention's matrix cores, written to
     // h16 instead of y: plane hi then plane lo (lo_off halves apart), each = q | k rows [m][rope_cols] followed by
     // v transposed per batch and head, [m / seq][heads][hd][ldvt] (ldvt >= seq, a multiple of 8); rope null: the

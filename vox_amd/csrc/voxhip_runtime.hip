@@ -2073,7 +2073,9 @@ struct F5VBlock {  // a Vocos ConvNeXt block (f5.cpp:235-240)
     int pw1 = -1, pw2 = -1;
 };
 struct F5 {
-    int dim = 0, depth = 0, heads = 0, hd = 0, ff = 0, mel = 0, text = 0, pe = 0;
+    // hd: the model's head_dim (the RoPE table, the softmax scale); hp: the attention layout's (kF5HeadDim, heads of
+    // hd < hp padded with zero dims, stack_rows_heads)
+    int dim = 0, depth = 0, heads = 0, hd = 0, hp = 0, ff = 0, mel = 0, text = 0, pe = 0;
     int in_proj = -1, norm_out = -1, proj_out = -1;
     std::vector<F5Block> blocks;
     F5Conv pos1, pos2;
@@ -2131,6 +2133,76 @@ int stack_rows(const std::vector<int> &ids) {
         }
         r0 += src.rows;
     }
+    return nid;
+}
+
+// Heads of hd < kF5HeadDim in the F5 / flow-estimator attention, whose tiles hold kF5HeadDim dims a head (the
+// reference's device path takes any even head_dim <= 64, gpu_f5.cpp:211, :425). The q | k | v parts are stacked with
+// each head's hd rows followed by hp - hd zero rows (zero scales and biases), and to_out gets hp - hd zero columns
+// after each head's hd columns: the padding dims are zero in q, k and v, add nothing to q . k, come out of attention
+// as zeros and meet zero weights in to_out, so the products are those of the unpadded model.
+int stack_rows_heads(const std::vector<int> &ids, int heads, int hd, int hp) {
+    if (hd == hp) return stack_rows(ids);
+    const GpuMat m0 = mat_at(ids[0]);
+    bool any_bias = false;
+    for (int id : ids) {
+        const GpuMat &m = mat_at(id);
+        if (m.type != m0.type || m.cols != m0.cols || m.s16 != m0.s16 || m.rows != int64_t(heads) * hd)
+            throw Fail("stacked attention matrices differ in type, width or head rows");
+        any_bias = any_bias || m.b;
+    }
+    const int64_t rows = int64_t(ids.size()) * heads * hp;
+    const int nid = new_mat(m0.type, rows, m0.cols, any_bias, m0.s16);
+    const GpuMat dst = g.mats[size_t(nid)];
+    const size_t rb = row_bytes(m0.type, m0.cols), sb = scale_row_bytes(m0);
+    HIPCHECK(hipMemset(dst.w, 0, size_t(rows) * rb));
+    if (sb) HIPCHECK(hipMemset(dst.s, 0, size_t(rows) * sb));
+    if (any_bias) HIPCHECK(hipMemset(dst.b, 0, size_t(rows) * 4));
+    float wmax = 0.f;
+    for (size_t p = 0; p < ids.size(); ++p) {
+        const GpuMat src = mat_at(ids[p]);
+        const size_t r0 = p * size_t(heads) * size_t(hp);  // head h of part p starts at row r0 + h hp
+        HIPCHECK(hipMemcpy2D(dst.w + r0 * rb, size_t(hp) * rb, src.w, size_t(hd) * rb, size_t(hd) * rb, size_t(heads),
+                             hipMemcpyDeviceToDevice));
+        if (sb)
+            HIPCHECK(hipMemcpy2D(reinterpret_cast<uint8_t *>(dst.s) + r0 * sb, size_t(hp) * sb, src.s, size_t(hd) * sb,
+                                 size_t(hd) * sb, size_t(heads), hipMemcpyDeviceToDevice));
+        if (src.b)
+            HIPCHECK(hipMemcpy2D(dst.b + r0, size_t(hp) * 4, src.b, size_t(hd) * 4, size_t(hd) * 4, size_t(heads),
+                                 hipMemcpyDeviceToDevice));
+        wmax = std::max(wmax, src.wmax, [](float a, float b) { return a < b || std::isnan(b); });
+    }
+    g.mats[size_t(nid)].wmax = wmax;
+    return nid;
+}
+// The to_out side of stack_rows_heads: a copy of m [rows][heads hd] as [rows][heads hp], each head's hd columns
+// followed by hp - hd zero columns. Q8 needs hd a multiple of 32 (whole scale blocks); Q4 is not taken.
+int pad_head_cols(int id, int heads, int hd, int hp) {
+    if (hd == hp) return id;
+    const GpuMat src = mat_at(id);
+    if (src.cols != int64_t(heads) * hd) throw Fail("attention output matrix width is not heads x head_dim");
+    int es = 0;
+    switch (src.type) {
+        case VOXHIP_F32: es = 4; break;
+        case VOXHIP_F16: case VOXHIP_BF16: es = 2; break;
+        case VOXHIP_Q8: es = 1; break;
+        default: throw Fail("head_dim below 64 needs f32 / f16 / bf16 / q8 attention weights");
+    }
+    if (src.type == VOXHIP_Q8 && hd % 32) throw Fail("q8 attention weights need head_dim a multiple of 32 below 64");
+    const int64_t cols = int64_t(heads) * hp;
+    const int nid = new_mat(src.type, src.rows, cols, src.b != nullptr);
+    const GpuMat dst = g.mats[size_t(nid)];
+    const size_t rows = size_t(src.rows);
+    HIPCHECK(hipMemset(dst.w, 0, rows * size_t(cols) * size_t(es)));
+    HIPCHECK(hipMemcpy2D(dst.w, size_t(hp) * es, src.w, size_t(hd) * es, size_t(hd) * es, rows * size_t(heads),
+                         hipMemcpyDeviceToDevice));
+    if (src.type == VOXHIP_Q8) {
+        const size_t nb = size_t(hd / 32), nbp = size_t(hp / 32);
+        HIPCHECK(hipMemset(dst.s, 0, rows * size_t(cols / 32) * 4));
+        HIPCHECK(hipMemcpy2D(dst.s, nbp * 4, src.s, nb * 4, nb * 4, rows * size_t(heads), hipMemcpyDeviceToDevice));
+    }
+    if (src.b) HIPCHECK(hipMemcpy(dst.b, src.b, rows * 4, hipMemcpyDeviceToDevice));
+    g.mats[size_t(nid)].wmax = src.wmax;
     return nid;
 }
 
@@ -2217,7 +2289,7 @@ void f5_lin(const F5 &F, const GpuMat &m, int epi, const float *A, const _Float1
 
 // dit_forward on the device (f5.cpp:586-725) for the batches of begin; x [N][mel] and ts [dim] already on the device.
 void f5_enqueue(F5 &F, hipStream_t s) {
-    const int D = F.dim, INNER = F.heads * F.hd, W = 2 * F.mel + F.text;
+    const int D = F.dim, INNER = F.heads * F.hp, W = 2 * F.mel + F.text;
     const int64_t R = int64_t(F.B) * F.N;
     HIPCHECK(launch_f5_fill_x(F.x, F.N, F.mel, F.cat, W, F.B, s));
     for (int i = 0; i < F.depth; ++i) {  // the six modulation vectors of every block (f5.cpp:673)
@@ -2244,10 +2316,10 @@ void f5_enqueue(F5 &F, hipStream_t s) {
         HIPCHECK(launch_f5_modulate(F.h, R, D, ada + D, ada, nrm, F.nrm16, R * D, s));
         const GpuMat &Mq = mat_at(L.qkv);
         GemmArgs gq = gemm_args(Mq, Mq.b, nullptr, D, 3 * INNER, R);
-        gq.rope = F.rope; gq.seq = F.N; gq.hd = F.hd; gq.rope_cols = 2 * INNER; gq.rope_heads = F.pe;
+        gq.rope = F.rope; gq.seq = F.N; gq.hd = F.hp; gq.rope_hd = F.hd; gq.rope_cols = 2 * INNER; gq.rope_heads = F.pe;
         gq.h16 = F.qkv16; gq.lo_off = F.lo_off; gq.ldvt = F.ldvt;
         f5_lin(F, Mq, EPI_ROPE_H16, F.nrm, F.nrm16, gq, s);
-        HIPCHECK(launch_f5_attn(F.qkv16, F.lo_off, F.split ? nullptr : F.at, F.at16, R * INNER, F.B, F.N, F.heads, F.hd,
+        HIPCHECK(launch_f5_attn(F.qkv16, F.lo_off, F.split ? nullptr : F.at, F.at16, R * INNER, F.B, F.N, F.heads, F.hp,
                                 F.ldvt, INNER, scale, s));
         const GpuMat &Mo = mat_at(L.o);
         GemmArgs go = gemm_args(Mo, Mo.b, F.h, INNER, D, R);
@@ -2274,7 +2346,8 @@ int voxhip_f5_create(const voxhip_f5_desc *d) {
     return guard_int([&] {
         require_ok();
         if (!d || d->depth <= 0 || !d->blocks) throw Fail("missing F5 description");
-        if (d->dim_head != kF5HeadDim) throw Fail("F5 attention supports head_dim 64");
+        if (d->dim_head <= 0 || d->dim_head > kF5HeadDim || d->dim_head % 2)
+            throw Fail("F5 attention supports even head_dim up to 64");
         const int D = d->dim, INNER = d->heads * d->dim_head, FF = d->dim * d->ff_mult, W = 2 * d->mel_dim + d->text_dim;
         if (D <= 0 || D % 8 || d->heads <= 0 || FF <= 0 || d->mel_dim <= 0 || d->text_dim < 0) throw Fail("bad F5 dimensions");
         auto check = [&](int id, int64_t rows, int64_t cols, const char *what) {
@@ -2285,7 +2358,8 @@ int voxhip_f5_create(const voxhip_f5_desc *d) {
         check(d->norm_out, 2 * D, D, "norm_out");
         check(d->proj_out, d->mel_dim, D, "proj_out");
         std::unique_ptr<F5> F(new F5());
-        F->dim = D; F->depth = d->depth; F->heads = d->heads; F->hd = d->dim_head; F->ff = FF; F->mel = d->mel_dim;
+        F->dim = D; F->depth = d->depth; F->heads = d->heads; F->hd = d->dim_head; F->hp = kF5HeadDim; F->ff = FF;
+        F->mel = d->mel_dim;
         F->text = d->text_dim; F->pe = d->pe_attn_head;
         F->in_proj = d->in_proj; F->norm_out = d->norm_out; F->proj_out = d->proj_out;
         for (int i = 0; i < d->depth; ++i) {
@@ -2294,11 +2368,12 @@ int voxhip_f5_create(const voxhip_f5_desc *d) {
             check(b.q, INNER, D, "q"); check(b.k, INNER, D, "k"); check(b.v, INNER, D, "v");
             check(b.o, D, INNER, "o"); check(b.ff1, FF, D, "ff1"); check(b.ff2, D, FF, "ff2");
             F5Block fb;
-            fb.ada = b.ada; fb.o = b.o; fb.ff1 = b.ff1; fb.ff2 = b.ff2;
-            fb.qkv = stack_rows({b.q, b.k, b.v});
+            fb.ada = b.ada; fb.ff1 = b.ff1; fb.ff2 = b.ff2;
+            fb.qkv = stack_rows_heads({b.q, b.k, b.v}, d->heads, d->dim_head, kF5HeadDim);
+            fb.o = pad_head_cols(b.o, d->heads, d->dim_head, kF5HeadDim);
             F->blocks.push_back(fb);
         }
-        F->split = D % 64 == 0 && INNER % 64 == 0 && FF % 64 == 0;
+        F->split = D % 64 == 0 && FF % 64 == 0;  // the attention width (heads x 64) always is
         for (const F5Block &fb : F->blocks)
             for (int id : {fb.qkv, fb.o, fb.ff1, fb.ff2}) F->split = F->split && mat_at(id).type == VOXHIP_F16;
         F->pos1 = upload_conv(d->pos1, D);
@@ -2339,7 +2414,7 @@ int voxhip_f5_begin(int id, int B, int N, const float *cat0, const float *rope) 
         F5 &F = f5_at(id);
         if (B <= 0 || N <= 0 || !cat0 || !rope || int64_t(B) * N > INT32_MAX / 8) throw Fail("bad F5 step shape");
         f5_free_step(F);
-        const size_t R = size_t(B) * size_t(N), D = size_t(F.dim), INNER = size_t(F.heads) * F.hd;
+        const size_t R = size_t(B) * size_t(N), D = size_t(F.dim), INNER = size_t(F.heads) * F.hp;
         const size_t W = 2 * size_t(F.mel) + F.text;
         F.cat = dalloc_t<float>(R * W); F.h = dalloc_t<float>(R * D); F.a = dalloc_t<float>(R * D);
         F.nrm = dalloc_t<float>(R * D);
@@ -2456,6 +2531,8 @@ struct CosyX {  // BasicTransformerBlock; q | k | v stacked at create
     int qkv = -1, o = -1, ff1 = -1, ff2 = -1, ff = 0;
 };
 struct Cosy {
+    // hd: the model's head_dim; inner: the attention layout's width, heads x kF5HeadDim (heads of hd < 64 padded with
+    // zero dims, stack_rows_heads)
     int M = 0, C = 0, heads = 0, hd = 0, inner = 0, ffmax = 0;
     CosyRes down_res, up_res;
     std::vector<CosyRes> mid_res;
@@ -2511,7 +2588,8 @@ CosyRes cosy_res_up(const voxhip_cosy_res &r, int cin, int C) {
     return o;
 }
 
-CosyX cosy_x_up(const voxhip_cosy_x &x, int C, int inner) {
+CosyX cosy_x_up(const voxhip_cosy_x &x, int C, int heads, int hd) {
+    const int inner = heads * hd;
     auto check = [&](int id, int64_t rows, int64_t cols, const char *what) {
         const GpuMat &m = mat_at(id);
         if (m.rows != rows || m.cols != cols) throw Fail(std::string("flow estimator ") + what + " has the wrong shape");
@@ -2522,8 +2600,9 @@ CosyX cosy_x_up(const voxhip_cosy_x &x, int C, int inner) {
     CosyX o;
     o.n1w = upload_vec(x.n1w, C, "norm1 weight"); o.n1b = upload_vec(x.n1b, C, "norm1 bias");
     o.n3w = upload_vec(x.n3w, C, "norm3 weight"); o.n3b = upload_vec(x.n3b, C, "norm3 bias");
-    o.qkv = stack_rows({x.q, x.k, x.v});
-    o.o = x.o; o.ff1 = x.ff1; o.ff2 = x.ff2; o.ff = x.ff_dim;
+    o.qkv = stack_rows_heads({x.q, x.k, x.v}, heads, hd, kF5HeadDim);
+    o.o = pad_head_cols(x.o, heads, hd, kF5HeadDim);
+    o.ff1 = x.ff1; o.ff2 = x.ff2; o.ff = x.ff_dim;
     return o;
 }
 
@@ -2567,11 +2646,11 @@ void cosy_xblock(const Cosy &E, const CosyX &L, float *A, hipStream_t s) {
     cosy_norm(E, A, L.n1w, L.n1b, false, nullptr, xn, E.xn16, s);
     const GpuMat &Mq = mat_at(L.qkv);
     GemmArgs gq = gemm_args(Mq, Mq.b, nullptr, C, 3 * INNER, R);
-    gq.rope = nullptr; gq.seq = E.T; gq.hd = E.hd; gq.rope_cols = 2 * INNER;
+    gq.rope = nullptr; gq.seq = E.T; gq.hd = kF5HeadDim; gq.rope_cols = 2 * INNER;
     gq.h16 = E.qkv16; gq.lo_off = E.lo_off; gq.ldvt = E.ldvt;
     split_lin(E.split, Mq, EPI_ROPE_H16, E.xn, E.xn16, gq, s);
-    HIPCHECK(launch_f5_attn(E.qkv16, E.lo_off, E.split ? nullptr : E.at, E.at16, R * INNER, 2, E.T, E.heads, E.hd, E.ldvt,
-                            INNER, 1.0f / std::sqrt(float(E.hd)), s));
+    HIPCHECK(launch_f5_attn(E.qkv16, E.lo_off, E.split ? nullptr : E.at, E.at16, R * INNER, 2, E.T, E.heads, kF5HeadDim,
+                            E.ldvt, INNER, 1.0f / std::sqrt(float(E.hd)), s));
     const GpuMat &Mo = mat_at(L.o);
     split_lin(E.split, Mo, EPI_ACC, E.at, E.at16, gemm_args(Mo, Mo.b, A, INNER, C, R), s);
     cosy_norm(E, A, L.n3w, L.n3b, false, nullptr, xn, E.xn16, s);
@@ -2615,21 +2694,22 @@ int voxhip_cosy_create(const voxhip_cosy_desc *d) {
     return guard_int([&] {
         require_ok();
         if (!d) throw Fail("missing flow estimator description");
-        if (d->head_dim != kF5HeadDim) throw Fail("the flow estimator's attention supports head_dim 64");
+        if (d->head_dim <= 0 || d->head_dim > kF5HeadDim || d->head_dim % 2)
+            throw Fail("the flow estimator's attention supports even head_dim up to 64");
         const int C = d->C, M = d->M;
         if (C <= 0 || C % 4 || M <= 0 || M % 4 || d->heads <= 0 || d->n_mid < 0 || d->n_down_x < 0 || d->n_up_x < 0)
             throw Fail("bad flow estimator dimensions (C and M multiples of 4)");
         if ((d->n_mid && (!d->mid_res || !d->mid_x_count)) || (d->n_down_x && !d->down_x) || (d->n_up_x && !d->up_x))
             throw Fail("missing flow estimator blocks");
         std::unique_ptr<Cosy> E(new Cosy());
-        E->M = M; E->C = C; E->heads = d->heads; E->hd = d->head_dim; E->inner = d->heads * d->head_dim;
+        E->M = M; E->C = C; E->heads = d->heads; E->hd = d->head_dim; E->inner = d->heads * kF5HeadDim;
         E->down_res = cosy_res_up(d->down_res, 4 * M, C);
         E->up_res = cosy_res_up(d->up_res, 2 * C, C);
         for (int i = 0; i < d->n_mid; ++i) E->mid_res.push_back(cosy_res_up(d->mid_res[i], C, C));
         auto xs = [&](const voxhip_cosy_x *v, int n) {
             std::vector<CosyX> o;
             for (int i = 0; i < n; ++i) {
-                o.push_back(cosy_x_up(v[i], C, E->inner));
+                o.push_back(cosy_x_up(v[i], C, d->heads, d->head_dim));
                 E->ffmax = std::max(E->ffmax, v[i].ff_dim);
             }
             return o;
