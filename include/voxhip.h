@@ -74,6 +74,14 @@ int voxhip_device_info_get(int index, voxhip_device_info *out);
  * as gpu_vulkan.cpp:364. Returns 1 on success; on failure writes the reason to err. */
 int voxhip_init(const char *device, char *err, size_t err_len);
 int voxhip_active(void);                                   /* gpu_active (gpu.hpp:11) */
+/* The GPU profile of VOX_PROFILE=gpu (gpu_vulkan.cpp:62-87, :312-326): when the variable holds "gpu" at init, every
+ * kernel launch is timed on the device and booked under "<stage>/<kernel>" (stage: the transformer's name, "matmul",
+ * "predictor", "f5.step", "f5.vocos", "flow.est", "codec", ...); this returns the table of the launches booked so far
+ * (calls, total ms, average us, share, sorted by time; launches are booked when a synchronous call or voxhip_sync
+ * returns), and the library prints it to stderr at exit. Empty when the profile is off. Graphs are not captured while
+ * it is on (stamped launches cannot be), so timings are those of launches issued one by one; the voxhip_bench_*
+ * entry points refuse to run. The text stays valid until the next call. */
+const char *voxhip_profile_report(void);
 const char *voxhip_device_name(void);                      /* gpu_device_name (gpu.hpp:12) */
 void voxhip_stats_get(voxhip_stats *out);                  /* gpu_stats (gpu.hpp:17) */
 /* GpuStats::last_error (gpu.hpp:16): copied under the library lock into a buffer of the calling thread, valid

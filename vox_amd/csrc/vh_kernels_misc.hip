@@ -1,6 +1,13 @@
 // Launchers of the non-GEMV kernels: q/k post-processing, attention, sampler, quantizers, synthetic data.
+#include <cxxabi.h>
+
 #include <algorithm>
 #include <atomic>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
 #include <mutex>
 #include <map>
 
@@ -41,6 +48,119 @@ bool timing_take(hipEvent_t *start, hipEvent_t *stop) {
     g_thead = (g_thead + 1) % 16;
     --g_tcount;
     return true;
+}
+
+// ------------------------------------------------------------------ VOX_PROFILE=gpu
+namespace {
+struct ProfRec {
+    const std::string *label;
+    hipEvent_t e0, e1;
+};
+struct ProfAcc {
+    double ns = 0.0;
+    uint64_t calls = 0;
+};
+std::atomic<bool> g_prof{false};
+std::mutex g_pmu;
+std::string g_stage = "-";
+std::vector<ProfRec> g_pending;
+std::vector<hipEvent_t> g_pool;
+std::map<std::pair<const void *, std::string>, std::string> g_labels;  // (kernel, stage) -> "<stage>/<kernel name>"
+std::vector<std::pair<std::string, ProfAcc>> g_acc;                     // first-seen order, sorted at report time
+uint64_t g_batches = 0;
+std::string g_report;
+
+// "void vh::k_gemv_int<3, 1, 4, 2, 1, 0, true, false>(vh::GemvArgs)" -> "k_gemv_int<3,1,4,2,1,0,true,false>"
+std::string kernel_name(const void *kernel, hipStream_t s) {
+    const char *m = hipKernelNameRefByPtr(kernel, s);
+    if (!m) return "kernel";
+    // the host demangler predates _Float16 ("DF16_"); spelled as the half type ("Dh") it demangles the rest
+    std::string mm = m;
+    for (size_t p; (p = mm.find("DF16_")) != std::string::npos;) mm.replace(p, 5, "Dh");
+    int st = 0;
+    char *d = abi::__cxa_demangle(mm.c_str(), nullptr, nullptr, &st);
+    std::string n = st == 0 && d ? d : m;
+    std::free(d);
+    int depth = 0;  // cut the parameter list: the first '(' outside template brackets
+    for (size_t i = 0; i < n.size(); ++i) {
+        if (n[i] == '<') ++depth;
+        else if (n[i] == '>') --depth;
+        else if (n[i] == '(' && depth == 0) { n.resize(i); break; }
+    }
+    for (const char *pre : {"void ", "vh::"})
+        for (size_t p; (p = n.find(pre)) != std::string::npos;) n.erase(p, std::strlen(pre));
+    n.erase(std::remove(n.begin(), n.end(), ' '), n.end());  // one column of the table
+    return n;
+}
+hipEvent_t pool_event() {
+    if (!g_pool.empty()) {
+        hipEvent_t e = g_pool.back();
+        g_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    (void)hipEventCreate(&e);
+    return e;
+}
+}  // namespace
+
+bool prof_on() { return g_prof.load(std::memory_order_relaxed); }
+void prof_enable() { g_prof = true; }
+void prof_stage(const char *stage) {
+    if (!prof_on()) return;
+    std::lock_guard<std::mutex> lk(g_pmu);
+    g_stage = stage && *stage ? stage : "-";
+}
+void prof_take(const void *kernel, hipStream_t s, hipEvent_t *start, hipEvent_t *stop) {
+    std::lock_guard<std::mutex> lk(g_pmu);
+    auto key = std::make_pair(kernel, g_stage);
+    auto it = g_labels.find(key);
+    if (it == g_labels.end()) it = g_labels.emplace(key, g_stage + "/" + kernel_name(kernel, s)).first;
+    *start = pool_event();
+    *stop = pool_event();
+    g_pending.push_back({&it->second, *start, *stop});
+}
+void prof_collect() {
+    if (!prof_on()) return;
+    std::lock_guard<std::mutex> lk(g_pmu);
+    if (g_pending.empty()) return;
+    for (const ProfRec &r : g_pending) {
+        float ms = 0.f;
+        if (r.e0 && r.e1 && hipEventElapsedTime(&ms, r.e0, r.e1) == hipSuccess) {
+            auto it = std::find_if(g_acc.begin(), g_acc.end(), [&](const auto &p) { return p.first == *r.label; });
+            if (it == g_acc.end()) {
+                g_acc.push_back({*r.label, ProfAcc{}});
+                it = g_acc.end() - 1;
+            }
+            it->second.ns += double(ms) * 1e6;
+            it->second.calls += 1;
+        }
+        for (hipEvent_t e : {r.e0, r.e1})
+            if (e) g_pool.push_back(e);
+    }
+    g_pending.clear();
+    g_batches += 1;
+}
+const char *prof_report(const char *device) {
+    std::lock_guard<std::mutex> lk(g_pmu);
+    g_report.clear();
+    if (!prof_on() || g_acc.empty()) return g_report.c_str();
+    auto v = g_acc;
+    std::sort(v.begin(), v.end(), [](const auto &a, const auto &b) { return a.second.ns > b.second.ns; });
+    double total = 0.0;
+    for (const auto &p : v) total += p.second.ns;
+    char line[512];
+    std::snprintf(line, sizeof line, "[vox gpu profile] %s: GPU busy %.1f ms in %llu submits\n  %-28s %8s %10s %9s %6s\n",
+                  device ? device : "", total / 1e6, (unsigned long long)g_batches, "stage/kernel", "calls", "total ms",
+                  "avg us", "share");
+    g_report += line;
+    for (const auto &p : v) {
+        std::snprintf(line, sizeof line, "  %-28s %8llu %10.2f %9.1f %5.1f%%\n", p.first.c_str(),
+                      (unsigned long long)p.second.calls, p.second.ns / 1e6,
+                      p.second.ns / 1e3 / double(std::max<uint64_t>(1, p.second.calls)), 100.0 * p.second.ns / std::max(1.0, total));
+        g_report += line;
+    }
+    return g_report.c_str();
 }
 
 hipError_t ensure_smem(const void *kernel, size_t bytes) {

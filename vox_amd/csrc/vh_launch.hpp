@@ -3,6 +3,8 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <string>
+
 #include "vh_types.hpp"
 
 namespace vh {
@@ -14,11 +16,29 @@ void timing_arm(hipEvent_t start, hipEvent_t stop);
 void timing_clear();
 bool timing_take(hipEvent_t *start, hipEvent_t *stop);
 
+// VOX_PROFILE=gpu (the reference's GPU profile, gpu_vulkan.cpp:62-87, :312-326): every launch is stamped with HIP
+// events at its own start and end and booked under "<stage>/<kernel>", the stage being the entry point's
+// (prof_stage); prof_collect() books the launches of a synchronized stream, prof_report() is the table sorted by
+// time. The library runs its graphs' launches one by one meanwhile (stamped launches cannot be captured).
+bool prof_on();
+void prof_enable();
+void prof_stage(const char *stage);
+void prof_take(const void *kernel, hipStream_t s, hipEvent_t *start, hipEvent_t *stop);
+void prof_collect();
+// The table (one line per label: calls, total ms, average us, share of the GPU busy time); empty when off.
+const char *prof_report(const char *device);
+
 template <typename K, typename... Args>
 hipError_t launch(K kernel, dim3 grid, dim3 block, size_t smem, hipStream_t s, Args... args) {
     hipEvent_t e0 = nullptr, e1 = nullptr;
-    if (timing_take(&e0, &e1)) hipExtLaunchKernelGGL(kernel, grid, block, uint32_t(smem), s, e0, e1, 0u, args...);
-    else hipLaunchKernelGGL(kernel, grid, block, smem, s, args...);
+    if (timing_take(&e0, &e1)) {
+        hipExtLaunchKernelGGL(kernel, grid, block, uint32_t(smem), s, e0, e1, 0u, args...);
+    } else if (prof_on()) {
+        prof_take(reinterpret_cast<const void *>(kernel), s, &e0, &e1);
+        hipExtLaunchKernelGGL(kernel, grid, block, uint32_t(smem), s, e0, e1, 0u, args...);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, smem, s, args...);
+    }
     return hipGetLastError();
 }
 

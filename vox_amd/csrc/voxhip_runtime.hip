@@ -275,6 +275,7 @@ float *dev_scratch(float *&p, size_t &cap, size_t bytes) {
 void sync_status() {
     HIPCHECK(hipMemcpyAsync(g.status_pin, g.status_dev, sizeof(int32_t), hipMemcpyDeviceToHost, g.stream));
     HIPCHECK(hipStreamSynchronize(g.stream));
+    vh::prof_collect();  // VOX_PROFILE=gpu: the call's stamped launches have finished
     const int32_t v = g.status_pin[0];
     if (!v) return;
     g.status_pin[0] = 0;
@@ -855,6 +856,7 @@ void enqueue_final(Xfmr &X, int r0, int mr, int head, hipStream_t s) {
 // seen before. Every launch reads positions, RoPE rows and cache views from the device row table, so a graph replays
 // at any position of the same sequence; its buffers are the transformer's row scratch, whose growth drops the graphs.
 void run_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, bool fused) {
+    if (vh::prof_on()) return enqueue_layers(X, mc, m_total, first, count, g.stream, fused);  // stamped launches
     const RowRef &r0 = X.rows_last.at(0);
     const LayersKey key{mc, int(std::min<int64_t>(m_total, kMaxM + 1)), first, count, fused ? 1 : 0,
                         pass_attn_of(X, mc, fused) ? 1 : 0, r0.k, r0.v, r0.cap};
@@ -902,6 +904,7 @@ void check_seq_for(Xfmr &X, int xid, const Seq &S) {
 template <class RowsOf>
 int forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_proj, int first_layer, int n_layers, int64_t m_total,
                   float *hidden_out, float *out_last, int head, float *head_out, bool final_all) {
+    vh::prof_stage(X.name.c_str());
     const int64_t H = X.H;
     const GpuMat *Pm = in_proj >= 0 ? &mat_at(in_proj) : nullptr;
     if (Pm && Pm->rows != H) throw Fail("in_proj rows differ from the hidden size");
@@ -1221,6 +1224,15 @@ int voxhip_init(const char *device, char *err, size_t err_len) {
         if (!sp || reinterpret_cast<uintptr_t>(sp) % 256) throw Fail("no device address for the no-alloc scratch");
         g.noalloc[size_t(idx)] = static_cast<uint8_t *>(sp);
         g.name = device_label(p);
+        // VOX_PROFILE=gpu (gpu_vulkan.cpp:312-326): per-launch GPU timestamps, the table on stderr at exit
+        const char *pe = std::getenv("VOX_PROFILE");
+        if (pe && std::strstr(pe, "gpu")) {
+            vh::prof_enable();
+            std::atexit([] {
+                const char *t = vh::prof_report(g.name.c_str());
+                if (t && *t) std::fputs(t, stderr);
+            });
+        }
         g.ok = true;
         return 1;
     } catch (const std::exception &e) {
@@ -1231,6 +1243,10 @@ int voxhip_init(const char *device, char *err, size_t err_len) {
 }
 
 int voxhip_active(void) { return g.ok ? 1 : 0; }
+const char *voxhip_profile_report(void) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    return vh::prof_report(g.name.c_str());
+}
 const char *voxhip_device_name(void) { return g.name.c_str(); }
 void voxhip_stats_get(voxhip_stats *out) {
     std::lock_guard<std::mutex> lk(g.mu);
@@ -1289,6 +1305,7 @@ int voxhip_mat_shape(int mat, int64_t *rows, int64_t *cols) {
 int voxhip_matmul(int mat, const float *x, int64_t m, float *y) {
     return guard_int([&] {
         require_ok();
+        vh::prof_stage("matmul");
         const GpuMat &M = mat_at(mat);
         if (m <= 0) return 1;
         const int chunk = rows_per_pass(M, m);
@@ -1312,6 +1329,7 @@ int voxhip_matmul(int mat, const float *x, int64_t m, float *y) {
 int voxhip_matmul_dev_noalloc(int mat, const float *d_x, int64_t m, float *d_y) {
     return guard_int([&] {
         require_ok();
+        vh::prof_stage("matmul");
         const GpuMat &M = mat_at(mat);
         if (m < 0 || (m > 0 && (!d_x || !d_y))) throw Fail("matmul_dev_noalloc: missing argument");
         if (m == 0) return 1;
@@ -1338,6 +1356,7 @@ int voxhip_matmul_dev_noalloc(int mat, const float *d_x, int64_t m, float *d_y) 
 int voxhip_mat_gather(int mat, const int32_t *ids, int64_t n, float *out) {
     return guard_int([&] {
         require_ok();
+        vh::prof_stage("gather");
         const GpuMat &M = mat_at(mat);
         if (n < 0 || (n > 0 && (!ids || !out))) throw Fail("mat_gather: missing argument");
         for (int64_t i = 0; i < n; ++i)  // check_id before any gather (backend_qwen3.cpp:305-306)
@@ -1364,6 +1383,7 @@ int voxhip_convt(int mat, int32_t K, int32_t stride, int32_t pad, int32_t out_pa
                  float *y) {
     return guard_int([&] {
         require_ok();
+        vh::prof_stage("convt");
         const GpuMat &M = mat_at(mat);
         if (K < 1 || stride < 1 || pad < 0 || out_pad < 0 || T < 1 || !x || !y)
             throw Fail("convt: K, stride and T must be positive, pad and out_pad not negative, x and y given");
@@ -1531,6 +1551,7 @@ int voxhip_sample_logits(const float *logits, int32_t n, const voxhip_sample_cfg
                          int32_t *out_id) {
     return guard_int([&] {
         require_ok();
+        vh::prof_stage("sample");
         if (!cfg || !out_id || !logits) throw Fail("missing argument");
         if (n <= 0 || n > kSampleMaxN) throw Fail("sampler supports 1..16384 logits");
         if (!g.scfg_dev) {
@@ -1711,6 +1732,11 @@ int voxhip_decode_dev(int xfmr, int seq, int64_t pos0, const float *d_x, int64_t
         Seq &S = seq_at(seq);
         check_seq_for(X, xfmr, S);
         prepare_decode(X, S, pos0, m, head, cfg);
+        vh::prof_stage(X.name.c_str());
+        if (vh::prof_on()) {  // stamped launches are not captured
+            enqueue_decode(X, int(m), head, d_x, d_out_last, d_logits, cfg != nullptr, d_token, g.stream);
+            return 1;
+        }
         hipGraphExec_t exec = decode_graph(X, one_seq(seq), int(m), false, head, d_x, d_out_last, d_logits, cfg != nullptr, d_token);
         HIPCHECK(hipGraphLaunch(exec, g.stream));
         return 1;
@@ -1739,6 +1765,11 @@ int voxhip_decode_steps_dev(int xfmr, const int32_t *seqs, const int64_t *pos, i
         prepare_head(X, head, cfgs != nullptr);
         set_rows(X, rr);
         if (cfgs) set_sample_cfgs(X, cfgs, int(B));
+        vh::prof_stage(X.name.c_str());
+        if (vh::prof_on()) {  // stamped launches are not captured
+            enqueue_decode(X, int(B), head, d_x, d_out, d_logits, cfgs != nullptr, d_tokens, g.stream, nullptr, true);
+            return 1;
+        }
         hipGraphExec_t exec = decode_graph(X, key, int(B), true, head, d_x, d_out, d_logits, cfgs != nullptr, d_tokens);
         HIPCHECK(hipGraphLaunch(exec, g.stream));
         return 1;
@@ -1804,25 +1835,28 @@ void lm_buffers(Xfmr &X, int64_t max_len, int64_t V, bool want_logp) {
 // kLmGraphSteps generation steps: final norm + head (+ bias) of row 0 -> sampler -> embedding of the pick and the
 // row advanced -> the layers (one fused row). The device state ends the loop; steps after the end write only the
 // sequence's spare slot.
-hipGraphExec_t lm_graph(Xfmr &X, const Seq &S, int seq, int head, int emb, bool want_logp) {
-    const std::array<int64_t, 4> key{seq, head, emb, want_logp ? 1 : 0};
-    auto it = X.lm_graphs.find(key);
-    if (it != X.lm_graphs.end()) return it->second;
+void enqueue_lm_steps(Xfmr &X, const Seq &S, int head, int emb, bool want_logp, hipStream_t s) {
     const GpuMat &Hm = mat_at(head), &E = mat_at(emb);
     LmEmbedArgs ea{};
     ea.w = E.w; ea.scale = E.s; ea.type = E.type; ea.s16 = E.s16 ? 1 : 0; ea.rows = E.rows; ea.cols = E.cols;
     ea.st = X.lm_state; ea.decoded = X.lm_dec; ea.x = X.h; ea.row = X.rows_dev; ea.rope_row = X.rope_rows_dev;
     ea.rope = X.rope; ea.hd = X.hd; ea.spare_pos = S.cap - 1;
+    for (int i = 0; i < kLmGraphSteps; ++i) {
+        enqueue_final(X, 0, 1, head, s);
+        HIPCHECK(launch_lm_sample(X.logits, int(Hm.rows), X.lm_cfg, X.lm_state, X.lm_dec, want_logp ? X.lm_logp : nullptr,
+                                  Hm.rows, true, s));
+        HIPCHECK(launch_lm_embed(ea, s));
+        enqueue_layers(X, 1, 1, 0, X.layers, s, true);
+    }
+}
+hipGraphExec_t lm_graph(Xfmr &X, const Seq &S, int seq, int head, int emb, bool want_logp) {
+    const std::array<int64_t, 4> key{seq, head, emb, want_logp ? 1 : 0};
+    auto it = X.lm_graphs.find(key);
+    if (it != X.lm_graphs.end()) return it->second;
     hipGraph_t graph = nullptr;
     HIPCHECK(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal));
     try {
-        for (int i = 0; i < kLmGraphSteps; ++i) {
-            enqueue_final(X, 0, 1, head, g.stream);
-            HIPCHECK(launch_lm_sample(X.logits, int(Hm.rows), X.lm_cfg, X.lm_state, X.lm_dec, want_logp ? X.lm_logp : nullptr,
-                                      Hm.rows, true, g.stream));
-            HIPCHECK(launch_lm_embed(ea, g.stream));
-            enqueue_layers(X, 1, 1, 0, X.layers, g.stream, true);
-        }
+        enqueue_lm_steps(X, S, head, emb, want_logp, g.stream);
     } catch (...) {
         (void)hipStreamEndCapture(g.stream, &graph);
         if (graph) (void)hipGraphDestroy(graph);
@@ -1855,36 +1889,39 @@ void pred_buffers(Xfmr &X) {
 // the rows as they are), the layers, the final norm and head cb - 1 on the last row, and the sampler with draw
 // (frame, cb) into codes[cb]. The first pass's two rows run the unfused layer path (q/k post-processing and the
 // K/V append before attention), so row 1 sees row 0.
+void enqueue_pred(Xfmr &X, const Seq &S, int in_proj, const int *heads, const int *embs, int G, hipStream_t s) {
+    const int64_t din = in_proj >= 0 ? mat_at(in_proj).cols : X.H;
+    int64_t pos = 0;
+    for (int cb = 1; cb < G; ++cb) {
+        const int m = cb == 1 ? 2 : 1;
+        PredEmbedArgs pa{};
+        pa.codes = X.pred_codes; pa.code_idx = cb - 1; pa.err = X.pred_err;
+        pa.x = in_proj >= 0 ? X.xin : X.h;
+        pa.row = X.rows_dev; pa.rope_row = X.rope_rows_dev; pa.rope = X.rope; pa.hd = X.hd; pa.m = m;
+        pa.base = row_of(S, pos);
+        if (cb >= 2) {
+            const GpuMat &E = mat_at(embs[cb - 2]);
+            pa.w = E.w; pa.scale = E.s; pa.type = E.type; pa.s16 = E.s16 ? 1 : 0; pa.rows = E.rows; pa.cols = E.cols;
+        }
+        HIPCHECK(launch_pred_embed(pa, s));
+        if (in_proj >= 0) gemv(mat_at(in_proj), m, PRO_X, EPI_STORE, X.xin, din, m, X.h, X.H, nullptr, 0.f, nullptr, s);
+        enqueue_layers(X, m, m, 0, X.layers, s, m == 1);
+        const GpuMat &Hm = mat_at(heads[cb - 1]);
+        enqueue_final(X, m - 1, 1, heads[cb - 1], s);
+        HIPCHECK(launch_sample(X.pred_cfg + cb, X.logits, int(Hm.rows), X.pred_codes + cb, s));
+        pos += m;
+    }
+}
 hipGraphExec_t pred_graph(Xfmr &X, const Seq &S, int seq, int in_proj, const int *heads, const int *embs, int G) {
     std::vector<int> key{seq, in_proj, G};
     key.insert(key.end(), heads, heads + (G - 1));
     key.insert(key.end(), embs, embs + (G - 2));
     auto it = X.pred_graphs.find(key);
     if (it != X.pred_graphs.end()) return it->second;
-    const int64_t din = in_proj >= 0 ? mat_at(in_proj).cols : X.H;
     hipGraph_t graph = nullptr;
     HIPCHECK(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal));
     try {
-        int64_t pos = 0;
-        for (int cb = 1; cb < G; ++cb) {
-            const int m = cb == 1 ? 2 : 1;
-            PredEmbedArgs pa{};
-            pa.codes = X.pred_codes; pa.code_idx = cb - 1; pa.err = X.pred_err;
-            pa.x = in_proj >= 0 ? X.xin : X.h;
-            pa.row = X.rows_dev; pa.rope_row = X.rope_rows_dev; pa.rope = X.rope; pa.hd = X.hd; pa.m = m;
-            pa.base = row_of(S, pos);
-            if (cb >= 2) {
-                const GpuMat &E = mat_at(embs[cb - 2]);
-                pa.w = E.w; pa.scale = E.s; pa.type = E.type; pa.s16 = E.s16 ? 1 : 0; pa.rows = E.rows; pa.cols = E.cols;
-            }
-            HIPCHECK(launch_pred_embed(pa, g.stream));
-            if (in_proj >= 0) gemv(mat_at(in_proj), m, PRO_X, EPI_STORE, X.xin, din, m, X.h, X.H, nullptr, 0.f, nullptr, g.stream);
-            enqueue_layers(X, m, m, 0, X.layers, g.stream, m == 1);
-            const GpuMat &Hm = mat_at(heads[cb - 1]);
-            enqueue_final(X, m - 1, 1, heads[cb - 1], g.stream);
-            HIPCHECK(launch_sample(X.pred_cfg + cb, X.logits, int(Hm.rows), X.pred_codes + cb, g.stream));
-            pos += m;
-        }
+        enqueue_pred(X, S, in_proj, heads, embs, G, g.stream);
     } catch (...) {
         (void)hipStreamEndCapture(g.stream, &graph);
         if (graph) (void)hipGraphDestroy(graph);
@@ -1906,6 +1943,7 @@ int voxhip_lm_sample_dev(const float *d_logits, int32_t n, const voxhip_lm_cfg *
                          int32_t n_decoded, float *d_logp, int32_t *token) {
     return guard_int([&] {
         require_ok();
+        vh::prof_stage("lm.sample");
         if (!d_logits || !cfg || !token || step < 0 || n_decoded < 0 || (n_decoded > 0 && !d_decoded)) throw Fail("missing argument");
         check_lm_cfg(*cfg, n);
         ensure_lm_staging();
@@ -1958,7 +1996,8 @@ int voxhip_lm_generate(int xfmr, int seq, const float *x, int64_t n, int head, i
         HIPCHECK(hipMemcpyAsync(X.lm_cfg, lm_host_cfg(), sizeof(LmCfgDev), hipMemcpyHostToDevice, g.stream));
         HIPCHECK(hipMemcpyAsync(X.lm_state, lm_host_state(0), sizeof(LmState), hipMemcpyHostToDevice, g.stream));
         set_rows(X, {row_of(S, n - 1)});  // the first step's embedding kernel advances it to position n
-        hipGraphExec_t exec = lm_graph(X, S, seq, head, speech_emb, logp != nullptr);
+        // VOX_PROFILE=gpu: the same steps launched one by one (stamped launches are not captured)
+        hipGraphExec_t exec = vh::prof_on() ? nullptr : lm_graph(X, S, seq, head, speech_emb, logp != nullptr);
         auto cleanup = [&] { X.rows_valid = false; };  // the device advanced the row table
         try {
             // One graph ahead: while graph c runs, the host reads the state copied after graph c - 1. The copy's
@@ -1968,7 +2007,8 @@ int voxhip_lm_generate(int xfmr, int seq, const float *x, int64_t n, int head, i
             for (int c = 0; c < chunks; ++c) {
                 LmState *slot = lm_host_state(1 + (c & 1));
                 __atomic_store_n(&slot->pad0, -1, __ATOMIC_RELEASE);
-                HIPCHECK(hipGraphLaunch(exec, g.stream));
+                if (exec) HIPCHECK(hipGraphLaunch(exec, g.stream));
+                else enqueue_lm_steps(X, S, head, speech_emb, logp != nullptr, g.stream);
                 HIPCHECK(hipMemcpyAsync(slot, X.lm_state, sizeof(LmState), hipMemcpyDeviceToHost, g.stream));
                 if (c >= 1) {
                     LmState *prev = lm_host_state(1 + ((c - 1) & 1));
@@ -2010,6 +2050,7 @@ int voxhip_pred_frame(int xfmr, int seq, const float *in2, int in_proj, const in
                       int n_embs, const voxhip_sample_cfg *cfg, int32_t *codes) {
     return guard_int([&] {
         require_ok();
+        vh::prof_stage("predictor");
         Xfmr &X = xf_at(xfmr);
         Seq &S = seq_at(seq);
         check_seq_for(X, xfmr, S);
@@ -2043,9 +2084,9 @@ int voxhip_pred_frame(int xfmr, int seq, const float *in2, int in_proj, const in
         HIPCHECK(hipMemsetAsync(X.pred_err, 0, sizeof(int32_t), g.stream));
         // the layer enqueue takes the first row's cache view from the host row table: this sequence's
         set_rows(X, {row_of(S, 0), row_of(S, 1)});
-        hipGraphExec_t exec = pred_graph(X, S, seq, in_proj, heads, embs, G);
-        X.rows_valid = false;  // the graph rewrites the row table
-        HIPCHECK(hipGraphLaunch(exec, g.stream));
+        X.rows_valid = false;  // the frame rewrites the row table
+        if (vh::prof_on()) enqueue_pred(X, S, in_proj, heads, embs, G, g.stream);  // stamped launches, not captured
+        else HIPCHECK(hipGraphLaunch(pred_graph(X, S, seq, in_proj, heads, embs, G), g.stream));
         HIPCHECK(hipMemcpyAsync(X.pred_host, X.pred_codes, size_t(G) * 4, hipMemcpyDeviceToHost, g.stream));
         HIPCHECK(hipMemcpyAsync(X.pred_host + kPredMaxGroups, X.pred_err, 4, hipMemcpyDeviceToHost, g.stream));
         sync_status();
@@ -2443,6 +2484,7 @@ int voxhip_f5_begin(int id, int B, int N, const float *cat0, const float *rope) 
 int voxhip_f5_step(int id, const float *x, const float *ts, float *out) {
     return guard_int([&] {
         require_ok();
+        vh::prof_stage("f5.step");
         F5 &F = f5_at(id);
         if (!F.B) throw Fail("F5 step before begin");
         if (!x || !ts || !out) throw Fail("missing argument");
@@ -2460,6 +2502,7 @@ int voxhip_f5_step(int id, const float *x, const float *ts, float *out) {
 int voxhip_f5_vocos(int id, const float *mel, int T, float *head) {
     return guard_int([&] {
         require_ok();
+        vh::prof_stage("f5.vocos");
         F5 &F = f5_at(id);
         if (!F.vdim) throw Fail("this F5 model has no Vocos on the device");
         if (!mel || !head || T <= 0 || int64_t(T) * std::max(F.vinter, F.vout) > INT32_MAX / 2) throw Fail("bad Vocos input");
@@ -2790,7 +2833,9 @@ int voxhip_cosy_step(int id, const float *x, const float *tb, float *out) {
         h2d(E.x, x, size_t(E.T) * E.M * 4);
         h2d(E.tb, tb, (2 + E.mid_res.size()) * size_t(E.C) * 4);
         // the step's ~560 launches as one graph: the buffers of this begin, the weights and the scratch are fixed
-        if (!E.step_graph) {
+        vh::prof_stage("flow.est");
+        if (vh::prof_on()) cosy_enqueue(E, g.stream);  // stamped launches are not captured
+        else if (!E.step_graph) {
             hipGraph_t graph = nullptr;
             HIPCHECK(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal));
             try {
@@ -2807,7 +2852,7 @@ int voxhip_cosy_step(int id, const float *x, const float *tb, float *out) {
             HIPCHECK(e);
             E.step_graph = exec;
         }
-        HIPCHECK(hipGraphLaunch(E.step_graph, g.stream));
+        if (!vh::prof_on()) HIPCHECK(hipGraphLaunch(E.step_graph, g.stream));
         sync_status();
         HIPCHECK(hipMemcpy(out, E.out, size_t(2) * E.T * E.M * 4, hipMemcpyDeviceToHost));
         return 1;
@@ -3276,8 +3321,11 @@ int voxhip_codec_forward(int codec, int state, const float *z, int F, float *pcm
         // the call's ~150 launches as one graph per (F, parity): the buffers, the weights and the scratch are fixed,
         // the position comes from pos_dev
         const int key = 2 * F + St.parity;
+        vh::prof_stage("codec");
         auto it = St.graphs.find(key);
-        if (it == St.graphs.end()) {
+        if (vh::prof_on()) {
+            codec_enqueue(E, St, F, g.stream);  // stamped launches are not captured
+        } else if (it == St.graphs.end()) {
             hipGraph_t graph = nullptr;
             HIPCHECK(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal));
             try {
@@ -3294,7 +3342,7 @@ int voxhip_codec_forward(int codec, int state, const float *z, int F, float *pcm
             HIPCHECK(e);
             it = St.graphs.emplace(key, exec).first;
         }
-        HIPCHECK(hipGraphLaunch(it->second, g.stream));
+        if (!vh::prof_on()) HIPCHECK(hipGraphLaunch(it->second, g.stream));
         sync_status();  // a failure leaves the state as it was (its parity and length unchanged)
         const int64_t n = int64_t(F) * E.spf;
         HIPCHECK(hipMemcpy(pcm, E.S[4], size_t(n) * 4, hipMemcpyDeviceToHost));
@@ -3468,6 +3516,7 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, const float *d_x, int h
                         int32_t *d_token, int warmup, int steps, voxhip_bench_result *out) {
     return guard_int([&] {
         require_ok();
+        if (vh::prof_on()) throw Fail("the benchmark entry points capture graphs, which VOX_PROFILE=gpu turns off");
         if (!out || steps <= 0 || !d_x) throw Fail("bad bench arguments");
         Xfmr &X = xf_at(xfmr);
         Seq &S = seq_at(seq);
@@ -3596,6 +3645,7 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, const float *d_x, int h
 int voxhip_bench_gemv_q8(int64_t rows, int64_t cols, int copies, int warmup, int iters, double *ms_per_launch) {
     return guard_int([&] {
         require_ok();
+        if (vh::prof_on()) throw Fail("the benchmark entry points capture graphs, which VOX_PROFILE=gpu turns off");
         if (copies <= 0 || iters <= 0 || !ms_per_launch) throw Fail("bad bench arguments");
         check_shape(VOXHIP_Q8, rows, cols);
         std::vector<int> ids;
@@ -3648,6 +3698,7 @@ int voxhip_bench_gemv_q8(int64_t rows, int64_t cols, int copies, int warmup, int
 int voxhip_bench_ffn_q8(int64_t hidden, int64_t inter, int copies, int warmup, int iters, double *us_per_block, float *check) {
     return guard_int([&] {
         require_ok();
+        if (vh::prof_on()) throw Fail("the benchmark entry points capture graphs, which VOX_PROFILE=gpu turns off");
         if (copies <= 0 || iters <= 0 || !us_per_block || hidden % 32 || inter % 32) throw Fail("bad bench arguments");
         std::vector<int> ids;
         float *x = nullptr, *h = nullptr, *gbuf = nullptr, *gamma = nullptr;
@@ -3729,6 +3780,7 @@ int voxhip_bench_ffn_q8(int64_t hidden, int64_t inter, int copies, int warmup, i
 int voxhip_bench_copy(int64_t bytes, int warmup, int iters, double *ms_per_copy) {
     return guard_int([&] {
         require_ok();
+        if (vh::prof_on()) throw Fail("the benchmark entry points capture graphs, which VOX_PROFILE=gpu turns off");
         if (bytes < 16 || iters <= 0 || !ms_per_copy) throw Fail("bad bench arguments");
         void *a = nullptr, *b = nullptr;
         hipEvent_t e0 = nullptr, e1 = nullptr;

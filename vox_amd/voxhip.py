@@ -160,6 +160,7 @@ SIGNATURES = {
     "voxhip_device_info_get": (_I, [_I, C.POINTER(DeviceInfo)]),
     "voxhip_init": (_I, [C.c_char_p, C.c_char_p, _S]),
     "voxhip_active": (_I, []),
+    "voxhip_profile_report": (C.c_char_p, []),
     "voxhip_device_name": (C.c_char_p, []),
     "voxhip_stats_get": (None, [C.POINTER(Stats)]),
     "voxhip_last_error": (C.c_char_p, []),
@@ -282,6 +283,11 @@ def mem_info():
     m = MemInfo()
     lib().voxhip_mem_info_get(C.byref(m))
     return m
+
+
+def profile_report():
+    """The VOX_PROFILE=gpu table of the launches booked so far (empty when the profile is off)."""
+    return lib().voxhip_profile_report().decode()
 
 
 def stats():
