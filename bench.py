@@ -385,6 +385,32 @@ def load_traffic(kernel_classes, launches):
     return int(round(sum(t[k] * launches[k] for k in kernel_classes) / n)) if n else None
 
 
+def write_classes(path, classes, gemv, gemv_bytes, gemv_us, achieved, ms_per_step, step_bytes, r):
+    """The per-class pass behind `roofline` as markdown: each class's launches per step, average event-stamped
+    duration, algorithmic bytes per launch and GB/s, then the GEMV sums that `roofline.achieved` divides."""
+    rows = ["| class | launches per step | us per launch | algorithmic bytes per launch | GB/s |", "|---|---|---|---|---|"]
+    for name, c in classes.items():
+        rows.append(f"| {name} | {c['launches_per_step']} | {c['us_per_launch']:.3f} | {c['bytes_per_launch']:,} | "
+                    f"{c['GBps'] if c['GBps'] is not None else '-'} |")
+    timing = "hipExtLaunchKernel start/stop events" if r.kernel_stamped else "stream events around each launch"
+    text = "\n".join([
+        "# Decode-step kernel classes, event-stamped (`bench.py` per-class pass)",
+        "",
+        f"Every kernel of one decode step launched on its own stream, timed by {timing}, averaged over the timed",
+        f"steps; the same enqueue path as the captured graph. Graph replay: {ms_per_step * 1000:.1f} us per step; the",
+        f"kernels summed: {r.kernel_ms_per_step * 1000:.1f} us per step ({r.kernels_per_step} launches).",
+        "",
+        *rows,
+        "",
+        f"GEMV classes ({', '.join(gemv)}): {gemv_bytes:,.0f} algorithmic bytes in {gemv_us:.2f} us per step = "
+        f"{achieved} GB/s, {achieved / HBM_PEAK_GBS:.4f} of {HBM_PEAK_GBS:.0f} GB/s (`roofline.achieved`, `frac`).",
+        f"Whole step: {step_bytes:,.0f} bytes in {ms_per_step * 1000:.1f} us = "
+        f"{step_bytes / (ms_per_step * 1e-3) / 1e9:.1f} GB/s.",
+        ""])
+    with open(path, "w") as f:
+        f.write(text)
+
+
 def host_cpu():
     """CPU model and the SIMD extensions the reference's kernels can use, from /proc/cpuinfo."""
     model, flags = "unknown", set()
@@ -413,6 +439,9 @@ def main():
                                        "f5_vocos", "cosy_flow", "codec"],
                     help="run one of the other BASELINE configurations (or the code-predictor frame) alone and print "
                          "its JSON object (for profiling)")
+    ap.add_argument("--classes-out", metavar="PATH",
+                    help="also write the event-stamped per-class pass (launches, us, algorithmic bytes, GB/s) and the "
+                         "roofline figures it gives as a markdown table to PATH")
     ap.add_argument("--no-breakdown", action="store_true",
                     help="skip the event-timed per-kernel pass (for runs under rocprofv3, whose tracer does not survive "
                          "HIP events recorded around graph launches); rocprof then times the graph's kernels itself")
@@ -490,6 +519,8 @@ def main():
     achieved = round(gemv_bytes / (gemv_us * 1e-6) / 1e9, 1)
     step_bytes = dec.step_bytes(POS)
     log(json.dumps(classes))
+    if args.classes_out:
+        write_classes(args.classes_out, classes, gemv, gemv_bytes, gemv_us, achieved, ms_per_step, step_bytes, r)
 
     other = None
     if not args.no_other:
@@ -527,7 +558,9 @@ def main():
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic(gemv, {k: classes[k]["launches_per_step"] for k in gemv}),
                      "launches_per_step": gemv_launches, "bytes_per_launch": int(gemv_bytes / gemv_launches),
-                     "us_per_launch": round(gemv_us / gemv_launches, 3)},
+                     "us_per_launch": round(gemv_us / gemv_launches, 3),
+                     "source": "per-class pass (bench.py --classes-out), committed as profiles/decode_q8_0p6b_event_classes.md; "
+                               "traffic: profiles/decode_q8_0p6b_hbm_traffic.md"},
         "gemv": {"GBps": round(gemv_bytes / (gemv_us * 1e-6) / 1e9, 1), "frac": round(gemv_bytes / (gemv_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                  "bytes_per_step": gemv_bytes, "us_per_step": round(gemv_us, 2)},
         "step": {"bytes": step_bytes, "GBps": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),

@@ -3539,17 +3539,25 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, const float *d_x, int h
             mark("graph");
             hipGraphExec_t exec = decode_graph(X, one_seq(seq), 1, false, head, dx, nullptr, nullptr, cfg != nullptr, d_token);
             for (int i = 0; i < warmup; ++i) HIPCHECK(hipGraphLaunch(exec, g.stream));
+            // under a profiler the replays are timed by the host clock around a synchronized stream: the tracer does
+            // not survive events recorded around graph launches
+            const bool prof = profiler_attached();
             ev.resize(2);
             for (auto &e : ev) HIPCHECK(hipEventCreate(&e));
             HIPCHECK(hipStreamSynchronize(g.stream));
-            HIPCHECK(hipEventRecord(ev[0], g.stream));
+            if (!prof) HIPCHECK(hipEventRecord(ev[0], g.stream));
             const auto h0 = std::chrono::steady_clock::now();
             for (int i = 0; i < steps; ++i) HIPCHECK(hipGraphLaunch(exec, g.stream));
             const auto h1 = std::chrono::steady_clock::now();
-            HIPCHECK(hipEventRecord(ev[1], g.stream));
-            HIPCHECK(hipEventSynchronize(ev[1]));
             float ms = 0.f;
-            HIPCHECK(hipEventElapsedTime(&ms, ev[0], ev[1]));
+            if (!prof) {
+                HIPCHECK(hipEventRecord(ev[1], g.stream));
+                HIPCHECK(hipEventSynchronize(ev[1]));
+                HIPCHECK(hipEventElapsedTime(&ms, ev[0], ev[1]));
+            } else {
+                HIPCHECK(hipStreamSynchronize(g.stream));
+                ms = float(std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - h0).count());
+            }
             out->ms_per_step = double(ms) / steps;
             out->launch_ms_per_step = std::chrono::duration<double, std::milli>(h1 - h0).count() / steps;
             mark("kernel by kernel");
