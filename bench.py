@@ -98,6 +98,20 @@ def cpu_baseline(vh, dec, seconds, x):
                       f"sampling, {threads} threads, median of the steps, {sum(times):.1f} s of CPU work)"}
 
 
+def classes_of(vh, r):
+    """The per-class table of a bench_decode / bench_decode_steps result: launches per step, event-stamped us per
+    launch, algorithmic bytes per launch and GB/s, for every class the step launches."""
+    out = {}
+    for i, name in enumerate(vh.KERNEL_CLASSES):
+        n = r.class_launches[i]
+        if not n:
+            continue
+        ms, b = r.class_ms[i], r.class_bytes[i]
+        out[name] = {"launches_per_step": n, "us_per_launch": round(ms * 1000, 3), "bytes_per_launch": int(b),
+                     "GBps": round(b / (ms * 1e-3) / 1e9, 1) if ms > 0 else None}
+    return out
+
+
 def bench_cfg1(vh):
     """BASELINE configs[0] on the device: one q8 FFN block (H 1024, FFN 3072), rotating over 40 weight sets
     (425 MB, above the 256 MB Infinity Cache)."""
@@ -140,6 +154,14 @@ def bench_cfg3(vh, synth, steps, warmup):
         nbytes = dec.weight_bytes() + kv
         out[f"b{B}"] = {"tok_s": round(B * 1000.0 / ms, 2), "ms_per_step": round(ms, 5), "bytes_per_step": nbytes,
                         "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        # the same step's kernels launched one by one, event-stamped (the per-class evidence of this leg)
+        if B == 1:
+            r = vh.bench_decode(dec.xfmr, dec.seq, pos, dx, dec.head, cfgs[0], dtok, 3, 20)
+        else:
+            r = vh.bench_decode_steps(dec.xfmr, seqs, [pos] * B, dx, dec.head, cfgs, dtok, 3, 20)
+        out[f"b{B}"]["kernels"] = classes_of(vh, r)
+        out[f"b{B}"]["kernel_us_per_step"] = round(r.kernel_ms_per_step * 1000, 2)
+        out[f"b{B}"]["kernels_per_step"] = r.kernels_per_step
         dx.free()
         dtok.free()
     return out
@@ -218,6 +240,12 @@ def bench_cfg5(vh, synth, reps=3):
     dec_ms = t_all - t_pre
     kv_avg = c["layers"] * 2 * (P + (S + 1) / 2) * c["kv_heads"] * c["head_dim"] * 2
     step_bytes = dec.weight_bytes() + kv_avg
+    # one generation step's layers and head launched one by one, event-stamped, at the middle of the generation (the
+    # RAS sampler and the embedding gather, which lm_generate adds, are not in this pass)
+    dx = vh.DevBuf(c["hidden"] * 4)
+    dx.upload(x[0])
+    r = vh.bench_decode(dec.xfmr, dec.seq, P + S // 2, dx, dec.head, None, None, 3, 20)
+    dx.free()
     vh.mat_free(emb)
     return {"workload": "cosyvoice2-0.5b LM q8: prefill 512 + 256 RAS-sampled steps (BASELINE configs[4])",
             "prefill_ms": round(t_pre, 3), "prefill_gflop": round(flops / 1e9, 1),
@@ -227,7 +255,8 @@ def bench_cfg5(vh, synth, reps=3):
             "decode_bytes_per_step": int(step_bytes),
             "decode_GBps": round(step_bytes * S / (dec_ms * 1e-3) / 1e9, 1),
             "decode_frac": round(step_bytes * S / (dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "total_ms": round(t_all, 3), "tokens": ntok}
+            "total_ms": round(t_all, 3), "tokens": ntok,
+            "decode_kernels": classes_of(vh, r), "decode_kernel_us_per_step": round(r.kernel_ms_per_step * 1000, 2)}
 
 
 def bench_cfg5_prefill(vh, synth, reps=10):
@@ -501,15 +530,7 @@ def main():
                           "stream": stream, "note": "--no-breakdown: graph replay only"}), flush=True)
         return
     r = vh.bench_decode(dec.xfmr, dec.seq, POS, dx, dec.head, cfg, dtok, max(3, args.warmup // 5), args.steps)
-    classes = {}
-    for i, name in enumerate(vh.KERNEL_CLASSES):
-        n = r.class_launches[i]
-        if not n:
-            continue
-        ms = r.class_ms[i]
-        b = r.class_bytes[i]
-        classes[name] = {"launches_per_step": n, "us_per_launch": round(ms * 1000, 3), "bytes_per_launch": int(b),
-                         "GBps": round(b / (ms * 1e-3) / 1e9, 1) if ms > 0 else None}
+    classes = classes_of(vh, r)
     # the dominant kernel: k_gemv_int, the int8 GEMV that makes 113 of the step's 142 launches (q|k|v, o, gate|up and
     # down of every layer, and the head); its algorithmic bytes and durations are summed over those launches
     gemv = [k for k in classes if k.endswith("_gemv")]

@@ -446,7 +446,8 @@ enum voxhip_kernel_class {
     VOXHIP_K_SAMPLE = 8,   /* device sampler */
     VOXHIP_K_FFN = 9,      /* one-row FFN in one launch: RMSNorm + gate|up + SwiGLU + down, product into accumulators */
     VOXHIP_K_FOLD = 10,    /* the last layer's accumulated FFN product into h */
-    VOXHIP_K_CLASSES = 11
+    VOXHIP_K_QUANT = 11,   /* the input rows of a several-row int-path GEMV quantized once (k_quant_rows) */
+    VOXHIP_K_CLASSES = 12
 };
 
 /* Times `steps` replays of the captured decode graph (after `warmup` untimed ones) with HIP events on the
@@ -469,6 +470,11 @@ typedef struct voxhip_bench_result {
 } voxhip_bench_result;
 int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, const float *d_x, int head, const voxhip_sample_cfg *cfg,
                         int32_t *d_token, int warmup, int steps, voxhip_bench_result *out);
+/* The same for a step of B sessions (voxhip_decode_steps_dev: row b at position pos[b] of sequence seqs[b]); the
+ * per-class bytes count every row's activations and cache. */
+int voxhip_bench_decode_steps(int xfmr, const int32_t *seqs, const int64_t *pos, int64_t B, const float *d_x, int head,
+                              const voxhip_sample_cfg *cfgs, int32_t *d_tokens, int warmup, int steps,
+                              voxhip_bench_result *out);
 
 /* Times one GEMV kernel configuration on `copies` distinct device copies of a synthetic q8 matrix
  * (rotating, so the working set exceeds the 256 MB Infinity Cache): average ms per launch. */

@@ -372,6 +372,9 @@ VH_DEV void reduce_store_prep(float (&acc)[R][M], float &out, int lane) {
 }
 
 // ------------------------------------------------------------------------------------------ int8 path
+// PRO_Q staging per thread: 16-byte chunks of the quantized rows and block scales / sums; STAGE picks the deeper set
+// (8 rows of K 6144), otherwise the shallow one (8 rows of K 2048), so no lane issues loads it does not use.
+constexpr int kQStageChunks = 12, kQStageScales = 6, kQStageChunksLo = 4, kQStageScalesLo = 2;
 // ACC (one row): the input or the residual carries pending FFN sums (GemvArgs::acc).
 template <int WT, int M, int R, int IT, int PRO, int EPI, bool STAGE, bool ACC = false>
 // The weight stream's operands come first so they are preloaded into SGPRs with the dispatch (kernarg preload).
@@ -411,11 +414,37 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__rest
             }
         }
     };
-    constexpr int PS = PRO == PRO_Q ? PRO_X : PRO;  // PRO_Q stages nothing
+    constexpr int PS = PRO == PRO_Q ? PRO_X : PRO;  // PRO_Q stages its rows below instead
     ProStage<M, PS> st;
     EpiPre<M, R, EPI, ACC> ep;
     int64_t xa[kAccCopies][8];  // ACC + PRO_RMS: the pending sums of this thread's slot (K <= 8 * kGemvThreads)
     if constexpr (STAGE && PRO != PRO_Q) pro_stage<M, PS>(a, x, K, st);  // the prologue's inputs first: loads return in issue order
+    // PRO_Q: the quantized rows, their scales and block sums are loaded into registers ahead of the weight stream
+    // too (16-byte chunk i = threadIdx.x + 256 u), so the copy into LDS waits for one round trip that overlaps the
+    // weights' instead of one per chunk after them; rows past a.m read row 0 and are stored as zeros
+    constexpr int QC = PRO != PRO_Q ? 1 : STAGE ? kQStageChunks : kQStageChunksLo;
+    constexpr int QSC = PRO != PRO_Q ? 1 : STAGE ? kQStageScales : kQStageScalesLo;
+    u32x4 qv[QC];
+    float qsv[QSC];
+    int qzv[QSC];
+    const int qn16 = M * K / 16, qns = M * nb;
+    const bool qstaged = PRO == PRO_Q && qn16 <= QC * kGemvThreads && qns <= QSC * kGemvThreads;
+    if constexpr (PRO == PRO_Q) {
+        if (qstaged) {
+#pragma unroll
+            for (int u = 0; u < QC; ++u) {
+                const int i = int(threadIdx.x) + u * kGemvThreads;
+                qv[u] = reinterpret_cast<const u32x4 *>(a.q)[i < qn16 && i * 16 / K < a.m ? i : 0];
+            }
+#pragma unroll
+            for (int u = 0; u < QSC; ++u) {
+                const int i = int(threadIdx.x) + u * kGemvThreads;
+                const int ii = i < qns && i / nb < a.m ? i : 0;
+                qsv[u] = a.qs[ii];
+                qzv[u] = WT != WT_Q8 ? a.qsum[ii] : 0;
+            }
+        }
+    }
     if constexpr (ACC && PRO == PRO_RMS) {
         const int sl = int(threadIdx.x) < K / 8 ? int(threadIdx.x) : 0;
 #pragma unroll
@@ -441,13 +470,29 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__rest
     }
 
     if constexpr (PRO == PRO_Q) {  // the rows come quantized: copy them (rows past a.m as zeros)
-        const int n16 = M * K / 16;
-        for (int i = threadIdx.x; i < n16; i += kGemvThreads)
-            reinterpret_cast<u32x4 *>(xq)[i] = i * 16 / K < a.m ? reinterpret_cast<const u32x4 *>(a.q)[i] : u32x4{0u, 0u, 0u, 0u};
-        for (int i = threadIdx.x; i < M * nb; i += kGemvThreads) {
-            const bool on = i / nb < a.m;
-            xs[i] = on ? a.qs[i] : 0.f;
-            if (WT != WT_Q8) xsum[i] = on ? a.qsum[i] : 0;
+        if (qstaged) {
+#pragma unroll
+            for (int u = 0; u < QC; ++u) {
+                const int i = int(threadIdx.x) + u * kGemvThreads;
+                if (i < qn16) reinterpret_cast<u32x4 *>(xq)[i] = i * 16 / K < a.m ? qv[u] : u32x4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int u = 0; u < QSC; ++u) {
+                const int i = int(threadIdx.x) + u * kGemvThreads;
+                if (i < qns) {
+                    const bool on = i / nb < a.m;
+                    xs[i] = on ? qsv[u] : 0.f;
+                    if (WT != WT_Q8) xsum[i] = on ? qzv[u] : 0;
+                }
+            }
+        } else {
+            for (int i = threadIdx.x; i < qn16; i += kGemvThreads)
+                reinterpret_cast<u32x4 *>(xq)[i] = i * 16 / K < a.m ? reinterpret_cast<const u32x4 *>(a.q)[i] : u32x4{0u, 0u, 0u, 0u};
+            for (int i = threadIdx.x; i < qns; i += kGemvThreads) {
+                const bool on = i / nb < a.m;
+                xs[i] = on ? a.qs[i] : 0.f;
+                if (WT != WT_Q8) xsum[i] = on ? a.qsum[i] : 0;
+            }
         }
     } else {
         prologue<M, PRO, STAGE>(a, x, K, red, st, [&](int mm, int sl, const float (&v)[8]) {

@@ -35,8 +35,12 @@ hipError_t gemv_run(const GemvArgs &a, hipStream_t s) {
         if (a.K / 8 > kGemvThreads || a.m != 1) return hipErrorInvalidValue;
         return gemv_run_staged<WT, M, R, IT, PRO, EPI, INT, true, true>(a, s);
     } else {
-        if constexpr (PRO != PRO_Q)
+        if constexpr (PRO != PRO_Q) {
             if (pro_stageable<M, PRO>(a.K)) return gemv_run_staged<WT, M, R, IT, PRO, EPI, INT, true, false>(a, s);
+        } else {  // the deeper staging of the quantized rows only where the shallow one does not hold them
+            if (int64_t(M) * a.K / 16 > int64_t(kQStageChunksLo) * kGemvThreads || int64_t(M) * (a.K / 32) > int64_t(kQStageScalesLo) * kGemvThreads)
+                return gemv_run_staged<WT, M, R, IT, PRO, EPI, INT, true, false>(a, s);
+        }
         return gemv_run_staged<WT, M, R, IT, PRO, EPI, INT, false, false>(a, s);
     }
 }
@@ -50,7 +54,7 @@ hipError_t gemv_by_tile(int R, int IT, const GemvArgs &a, hipStream_t s) {
         if constexpr (EPI == EPI_SWIGLU) {
             VH_TILE(2, 1) VH_TILE(4, 1) VH_TILE(8, 1)
         } else {
-            VH_TILE(2, 1) VH_TILE(4, 1) VH_TILE(8, 1) VH_TILE(2, 2)
+            VH_TILE(2, 1) VH_TILE(4, 1) VH_TILE(8, 1) VH_TILE(2, 2) VH_TILE(2, 3)
         }
     } else if constexpr (M == 1) {
         if constexpr (EPI == EPI_SWIGLU) {

@@ -33,7 +33,8 @@ static void gemv_tile_q(int rows, int nchunk, bool swiglu, int *R, int *IT) {
     int r = 2;
     while (r < 8 && int64_t(rows) / (4 * 2 * r) >= 256) r *= 2;
     *R = r;
-    *IT = !swiglu && r == 2 && nchunk > 64 ? 2 : 1;
+    // one pass of chunks where the tile allows it: every weight load of a wave in flight at once (K 6144 q4: 3)
+    *IT = swiglu || r != 2 || nchunk <= 64 ? 1 : nchunk <= 128 ? 2 : 3;
 }
 
 void gemv_tile(int rows, int nchunk, int M, bool swiglu, int *R, int *IT) {

@@ -467,6 +467,32 @@ struct PassScratch {
 // The library's own scratch, allocated at init.
 PassScratch lib_scratch() { return {g.gemm_ws, kGemmWsFloats, g.qrows, g.qrows_s, g.qrows_sum, kQuantRowsElems}; }
 
+// Observer of the launches of one pass (the benchmark's per-kernel timing): before(class) and after() bracket
+// every kernel launch enqueue_layers / enqueue_final / the sampler make.
+struct Probe {
+    virtual void before(int cls) = 0;
+    virtual void after() = 0;
+    // the launch just made in the current bracket was of class `done`: book it so, and open a new bracket of the
+    // bracket's class for the launches that follow (a GEMV pass that quantizes its rows first)
+    virtual void split(int done) = 0;
+    virtual ~Probe() = default;
+};
+thread_local Probe *t_probe = nullptr;  // the probe of the bracket being enqueued (gemv() splits it)
+template <class F>
+void probed(Probe *pr, int cls, F &&f) {
+    if (pr) pr->before(cls);
+    Probe *prev = t_probe;
+    t_probe = pr;
+    try {
+        f();
+    } catch (...) {
+        t_probe = prev;
+        throw;
+    }
+    t_probe = prev;
+    if (pr) pr->after();
+}
+
 // One matrix pass: y (=, +=, swiglu) W * prologue(x) for mc rows. On the GEMM path the prologue runs as its own
 // kernel into pre ([mc][cols]; xnorm instead when the normed rows are wanted). sc: the pass's scratch (null: the
 // library's).
@@ -517,6 +543,7 @@ void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, in
         (epi == EPI_STORE || epi == EPI_ACC || epi == EPI_SWIGLU)) {
         // several rows: quantize them once, then every GEMV block copies them instead of recomputing them
         HIPCHECK(launch_quant_rows(pro, a, sc.q, sc.qs, sc.qsum, s));
+        if (t_probe) t_probe->split(VOXHIP_K_QUANT);
         a.q = sc.q; a.qs = sc.qs; a.qsum = sc.qsum;
         HIPCHECK(launch_gemv(gemv_type(m), true, PRO_Q, epi, a, s));
         return;
@@ -637,19 +664,6 @@ void set_rows(Xfmr &X, const std::vector<RowRef> &rows) {
     X.rows_valid = true;
 }
 
-// Observer of the launches of one pass (the benchmark's per-kernel timing): before(class) and after() bracket
-// every kernel launch enqueue_layers / enqueue_final / the sampler make.
-struct Probe {
-    virtual void before(int cls) = 0;
-    virtual void after() = 0;
-    virtual ~Probe() = default;
-};
-template <class F>
-void probed(Probe *pr, int cls, F &&f) {
-    if (pr) pr->before(cls);
-    f();
-    if (pr) pr->after();
-}
 
 AttnPartials partials_of(const Xfmr &X) {
     AttnPartials p;
@@ -3512,6 +3526,158 @@ bool profiler_attached() {
 
 extern "C" {
 
+}  // extern "C"
+
+namespace {
+// The decode benchmark for m rows: of one sequence at pos[0] .. (steps_mode false, m = 1 here), or one row of each of
+// m sequences at pos[i] (steps_mode true). Region A times the captured graph's replays; region B launches the same
+// kernels one by one, each stamped by its own events, for per-class durations and algorithmic bytes.
+void bench_decode_impl(Xfmr &X, const std::array<int, 8> &key, int m, bool steps_mode, const std::vector<int64_t> &pos,
+                       const float *dx, int head, bool sample, int32_t *d_token, int warmup, int steps, voxhip_bench_result *out) {
+    std::memset(out, 0, sizeof *out);
+    const bool trace = std::getenv("VOXHIP_TRACE") != nullptr;
+    auto mark = [&](const char *what) {
+        if (trace) std::fprintf(stderr, "[voxhip bench] %s\n", what);
+    };
+    std::vector<hipEvent_t> ev;
+    auto cleanup = [&] {
+        (void)hipStreamSynchronize(g.stream);
+        timing_clear();
+        for (auto &e : ev) (void)hipEventDestroy(e);
+    };
+    try {
+        // ---- region A: graph replays (the same graph voxhip_decode_dev / _steps_dev replays for these arguments)
+        mark("graph");
+        hipGraphExec_t exec = decode_graph(X, key, m, steps_mode, head, dx, nullptr, nullptr, sample, d_token);
+        for (int i = 0; i < warmup; ++i) HIPCHECK(hipGraphLaunch(exec, g.stream));
+        // under a profiler the replays are timed by the host clock around a synchronized stream: the tracer does
+        // not survive events recorded around graph launches
+        const bool prof = profiler_attached();
+        ev.resize(2);
+        for (auto &e : ev) HIPCHECK(hipEventCreate(&e));
+        HIPCHECK(hipStreamSynchronize(g.stream));
+        if (!prof) HIPCHECK(hipEventRecord(ev[0], g.stream));
+        const auto h0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < steps; ++i) HIPCHECK(hipGraphLaunch(exec, g.stream));
+        const auto h1 = std::chrono::steady_clock::now();
+        float ms = 0.f;
+        if (!prof) {
+            HIPCHECK(hipEventRecord(ev[1], g.stream));
+            HIPCHECK(hipEventSynchronize(ev[1]));
+            HIPCHECK(hipEventElapsedTime(&ms, ev[0], ev[1]));
+        } else {
+            HIPCHECK(hipStreamSynchronize(g.stream));
+            ms = float(std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - h0).count());
+        }
+        out->ms_per_step = double(ms) / steps;
+        out->launch_ms_per_step = std::chrono::duration<double, std::milli>(h1 - h0).count() / steps;
+        mark("kernel by kernel");
+        // ---- region B: the same step launched kernel by kernel (same enqueue path as the graph), each launch
+        // stamped by its own events: hipExtLaunchKernel start/stop, or plain stream events around the launch
+        // when a profiler intercepts launches
+        for (auto &e : ev) (void)hipEventDestroy(e);
+        ev.clear();
+        struct Stamps : Probe {
+            std::vector<hipEvent_t> *ev;
+            std::vector<int> cls;
+            bool stamp;
+            hipStream_t s;
+            int k = 0, open = -1;
+            void before(int c) override {
+                while (ev->size() < size_t(2 * k + 2)) {
+                    hipEvent_t e = nullptr;
+                    HIPCHECK(hipEventCreate(&e));
+                    ev->push_back(e);
+                }
+                if (cls.size() <= size_t(k)) cls.resize(size_t(k) + 1);
+                cls[size_t(k)] = c;
+                open = c;
+                if (stamp) timing_arm((*ev)[size_t(2 * k)], (*ev)[size_t(2 * k + 1)]);
+                else HIPCHECK(hipEventRecord((*ev)[size_t(2 * k)], s));
+            }
+            void after() override {
+                if (!stamp) HIPCHECK(hipEventRecord((*ev)[size_t(2 * k + 1)], s));
+                ++k;
+            }
+            void split(int done) override {
+                const int c = open;
+                cls[size_t(k)] = done;
+                after();
+                before(c);
+            }
+        };
+        const bool stamp = !profiler_attached();
+        Stamps st;
+        st.ev = &ev; st.stamp = stamp; st.s = g.stream;
+        double sum_ms[VOXHIP_K_CLASSES] = {0};
+        int cnt[VOXHIP_K_CLASSES] = {0};
+        int per_step = -1;
+        for (int it = 0; it < warmup + steps; ++it) {
+            st.k = 0;
+            enqueue_decode(X, m, head, dx, nullptr, nullptr, sample, d_token, g.stream, &st, steps_mode);
+            HIPCHECK(hipStreamSynchronize(g.stream));
+            if (per_step < 0) per_step = st.k;
+            if (st.k != per_step) throw Fail("bench launch count mismatch");
+            if (it < warmup) continue;
+            for (int i = 0; i < st.k; ++i) {
+                float t = 0.f;
+                HIPCHECK(hipEventElapsedTime(&t, ev[size_t(2 * i)], ev[size_t(2 * i + 1)]));
+                sum_ms[st.cls[size_t(i)]] += t;
+                cnt[st.cls[size_t(i)]] += 1;
+            }
+        }
+        const int nl = X.layers;
+        // ---- algorithmic bytes per launch of each class: every byte the kernel must move once
+        // (weights + scales + bias, every row's activations in and out, cache reads and appends, attention partials)
+        const int qd = X.heads * X.hd, kd = X.kvh * X.hd;
+        const double partials = double(X.heads) * kAttnMaxSplits * (X.hd + 2) * 4.0;
+        double bytes[VOXHIP_K_CLASSES] = {0};
+        for (const LayerDev &L : X.L) {
+            bytes[VOXHIP_K_QKV] += double(g.mats[size_t(L.qkv)].bytes) + m * (X.H * 4.0 + (qd + 2.0 * kd) * 4.0);
+            bytes[VOXHIP_K_O] += double(g.mats[size_t(L.o)].bytes) + m * (partials + 2.0 * X.H * 4.0);
+            bytes[VOXHIP_K_GATEUP] += double(g.mats[size_t(L.gu)].bytes) + m * (X.H * 4.0 + X.I * 4.0);
+            bytes[VOXHIP_K_DOWN] += double(g.mats[size_t(L.down)].bytes) + m * (X.I * 4.0 + 2.0 * X.H * 4.0);
+            // fused FFN: both matrices, the input row in, the down product out
+            bytes[VOXHIP_K_FFN] += double(g.mats[size_t(L.gu)].bytes) + double(g.mats[size_t(L.down)].bytes) + 2.0 * X.H * 4.0;
+        }
+        for (int c = 0; c < 4; ++c) bytes[c] /= nl;
+        bytes[VOXHIP_K_FFN] /= nl;
+        bytes[VOXHIP_K_FOLD] = X.H * (2.0 * 4.0 + 2.0 * kAccCopies * 8.0);
+        // quantized input rows, averaged over a layer's four (K = H, heads x hd, H, I): f32 rows in, int8 rows, block
+        // scales and sums out
+        bytes[VOXHIP_K_QUANT] = m * (2.0 * X.H + qd + X.I) / 4.0 * (4.0 + 1.0 + 8.0 / 32.0);
+        for (int i = 0; i < m; ++i)  // one launch covers every row: each row's cache, q|k|v row, appended K/V, partials
+            bytes[VOXHIP_K_ATTN] += 2.0 * double(pos[size_t(i)]) * kd * 2.0 + (qd + 2.0 * kd) * 4.0 + 2.0 * kd * 2.0 + partials;
+        const int mr = steps_mode ? m : 1;  // rows through the head and the sampler
+        if (head >= 0) {
+            const GpuMat &Hm = g.mats[size_t(head)];
+            bytes[VOXHIP_K_HEAD] = double(Hm.bytes) + mr * (X.H * 4.0 + double(Hm.rows) * 4.0);
+            if (sample) bytes[VOXHIP_K_SAMPLE] = mr * double(Hm.rows) * 4.0;
+        }
+        double total_ms = 0.0, step_bytes = 0.0;
+        for (int c = 0; c < VOXHIP_K_CLASSES; ++c) {
+            out->class_launches[c] = steps > 0 ? cnt[c] / steps : 0;
+            out->class_ms[c] = cnt[c] ? sum_ms[c] / cnt[c] : 0.0;
+            out->class_bytes[c] = bytes[c];
+            total_ms += sum_ms[c];
+            step_bytes += bytes[c] * out->class_launches[c];
+        }
+        out->kernel_ms_per_step = total_ms / steps;
+        out->step_bytes = step_bytes;
+        out->kernels_per_step = per_step;
+        out->n_classes = VOXHIP_K_CLASSES;
+        out->kernel_stamped = stamp ? 1 : 0;
+        mark("done");
+    } catch (...) {
+        cleanup();
+        throw;
+    }
+    cleanup();
+}
+}  // namespace
+
+extern "C" {
+
 int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, const float *d_x, int head, const voxhip_sample_cfg *cfg,
                         int32_t *d_token, int warmup, int steps, voxhip_bench_result *out) {
     return guard_int([&] {
@@ -3521,131 +3687,39 @@ int voxhip_bench_decode(int xfmr, int seq, int64_t pos0, const float *d_x, int h
         Xfmr &X = xf_at(xfmr);
         Seq &S = seq_at(seq);
         check_seq_for(X, xfmr, S);
-        std::memset(out, 0, sizeof *out);
-        const bool trace = std::getenv("VOXHIP_TRACE") != nullptr;
-        auto mark = [&](const char *what) {
-            if (trace) std::fprintf(stderr, "[voxhip bench] %s\n", what);
-        };
         prepare_decode(X, S, pos0, 1, head, cfg);
-        const float *dx = d_x;
-        std::vector<hipEvent_t> ev;
-        auto cleanup = [&] {
-            (void)hipStreamSynchronize(g.stream);
-            timing_clear();
-            for (auto &e : ev) (void)hipEventDestroy(e);
-        };
-        try {
-            // ---- region A: graph replays (the same graph voxhip_decode_dev replays for these arguments)
-            mark("graph");
-            hipGraphExec_t exec = decode_graph(X, one_seq(seq), 1, false, head, dx, nullptr, nullptr, cfg != nullptr, d_token);
-            for (int i = 0; i < warmup; ++i) HIPCHECK(hipGraphLaunch(exec, g.stream));
-            // under a profiler the replays are timed by the host clock around a synchronized stream: the tracer does
-            // not survive events recorded around graph launches
-            const bool prof = profiler_attached();
-            ev.resize(2);
-            for (auto &e : ev) HIPCHECK(hipEventCreate(&e));
-            HIPCHECK(hipStreamSynchronize(g.stream));
-            if (!prof) HIPCHECK(hipEventRecord(ev[0], g.stream));
-            const auto h0 = std::chrono::steady_clock::now();
-            for (int i = 0; i < steps; ++i) HIPCHECK(hipGraphLaunch(exec, g.stream));
-            const auto h1 = std::chrono::steady_clock::now();
-            float ms = 0.f;
-            if (!prof) {
-                HIPCHECK(hipEventRecord(ev[1], g.stream));
-                HIPCHECK(hipEventSynchronize(ev[1]));
-                HIPCHECK(hipEventElapsedTime(&ms, ev[0], ev[1]));
-            } else {
-                HIPCHECK(hipStreamSynchronize(g.stream));
-                ms = float(std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - h0).count());
-            }
-            out->ms_per_step = double(ms) / steps;
-            out->launch_ms_per_step = std::chrono::duration<double, std::milli>(h1 - h0).count() / steps;
-            mark("kernel by kernel");
-            // ---- region B: the same step launched kernel by kernel (same enqueue path as the graph), each launch
-            // stamped by its own events: hipExtLaunchKernel start/stop, or plain stream events around the launch
-            // when a profiler intercepts launches
-            struct Stamps : Probe {
-                std::vector<hipEvent_t> *ev;
-                std::vector<int> cls;
-                bool stamp;
-                hipStream_t s;
-                int k = 0;
-                void before(int c) override {
-                    if (size_t(2 * k + 1) >= ev->size()) throw Fail("bench: more launches than expected");
-                    cls[size_t(k)] = c;
-                    if (stamp) timing_arm((*ev)[size_t(2 * k)], (*ev)[size_t(2 * k + 1)]);
-                    else HIPCHECK(hipEventRecord((*ev)[size_t(2 * k)], s));
-                }
-                void after() override {
-                    if (!stamp) HIPCHECK(hipEventRecord((*ev)[size_t(2 * k + 1)], s));
-                    ++k;
-                }
-            };
-            const int per_step = kernels_per_layer(X, 1, true) * X.layers + (ffn_pass(X, 1, 1, true) ? 1 : 0) + (head >= 0 ? 1 : 0) +
-                                 (cfg && head >= 0 ? 1 : 0);
-            const bool stamp = !profiler_attached();
-            for (auto &e : ev) (void)hipEventDestroy(e);
-            ev.assign(size_t(2 * per_step), nullptr);
-            for (auto &e : ev) HIPCHECK(hipEventCreate(&e));
-            Stamps st;
-            st.ev = &ev; st.cls.assign(size_t(per_step), 0); st.stamp = stamp; st.s = g.stream;
-            double sum_ms[VOXHIP_K_CLASSES] = {0};
-            int cnt[VOXHIP_K_CLASSES] = {0};
-            for (int it = 0; it < warmup + steps; ++it) {
-                st.k = 0;
-                enqueue_decode(X, 1, head, dx, nullptr, nullptr, cfg != nullptr, d_token, g.stream, &st);
-                HIPCHECK(hipStreamSynchronize(g.stream));
-                if (st.k != per_step) throw Fail("bench launch count mismatch");
-                if (it < warmup) continue;
-                for (int i = 0; i < st.k; ++i) {
-                    float t = 0.f;
-                    HIPCHECK(hipEventElapsedTime(&t, ev[size_t(2 * i)], ev[size_t(2 * i + 1)]));
-                    sum_ms[st.cls[size_t(i)]] += t;
-                    cnt[st.cls[size_t(i)]] += 1;
-                }
-            }
-            const int nl = X.layers;
-            // ---- algorithmic bytes per launch of each class: every byte the kernel must move once
-            // (weights + scales + bias, activations in and out, cache reads and appends, attention partials)
-            const int qd = X.heads * X.hd, kd = X.kvh * X.hd;
-            const double partials = double(X.heads) * kAttnMaxSplits * (X.hd + 2) * 4.0;
-            double bytes[VOXHIP_K_CLASSES] = {0};
-            for (const LayerDev &L : X.L) {
-                bytes[VOXHIP_K_QKV] += double(g.mats[size_t(L.qkv)].bytes) + X.H * 4.0 + (qd + 2.0 * kd) * 4.0;
-                bytes[VOXHIP_K_O] += double(g.mats[size_t(L.o)].bytes) + partials + 2.0 * X.H * 4.0;
-                bytes[VOXHIP_K_GATEUP] += double(g.mats[size_t(L.gu)].bytes) + X.H * 4.0 + X.I * 4.0;
-                bytes[VOXHIP_K_DOWN] += double(g.mats[size_t(L.down)].bytes) + X.I * 4.0 + 2.0 * X.H * 4.0;
-                // fused FFN: both matrices, the input row in, the down product out
-                bytes[VOXHIP_K_FFN] += double(g.mats[size_t(L.gu)].bytes) + double(g.mats[size_t(L.down)].bytes) + 2.0 * X.H * 4.0;
-            }
-            for (int c = 0; c < 4; ++c) bytes[c] /= nl;
-            bytes[VOXHIP_K_FFN] /= nl;
-            bytes[VOXHIP_K_FOLD] = X.H * (2.0 * 4.0 + 2.0 * kAccCopies * 8.0);
-            bytes[VOXHIP_K_ATTN] = 2.0 * double(pos0) * kd * 2.0 + (qd + 2.0 * kd) * 4.0 + 2.0 * kd * 2.0 + partials;
-            if (head >= 0) {
-                const GpuMat &Hm = g.mats[size_t(head)];
-                bytes[VOXHIP_K_HEAD] = double(Hm.bytes) + X.H * 4.0 + double(Hm.rows) * 4.0;
-                if (cfg) bytes[VOXHIP_K_SAMPLE] = double(Hm.rows) * 4.0;
-            }
-            double total_ms = 0.0, step_bytes = 0.0;
-            for (int c = 0; c < VOXHIP_K_CLASSES; ++c) {
-                out->class_launches[c] = steps > 0 ? cnt[c] / steps : 0;
-                out->class_ms[c] = cnt[c] ? sum_ms[c] / cnt[c] : 0.0;
-                out->class_bytes[c] = bytes[c];
-                total_ms += sum_ms[c];
-                step_bytes += bytes[c] * out->class_launches[c];
-            }
-            out->kernel_ms_per_step = total_ms / steps;
-            out->step_bytes = step_bytes;
-            out->kernels_per_step = per_step;
-            out->n_classes = VOXHIP_K_CLASSES;
-            out->kernel_stamped = stamp ? 1 : 0;
-            mark("done");
-        } catch (...) {
-            cleanup();
-            throw;
+        bench_decode_impl(X, one_seq(seq), 1, false, {pos0}, d_x, head, cfg != nullptr, d_token, warmup, steps, out);
+        return 1;
+    }, 0);
+}
+
+int voxhip_bench_decode_steps(int xfmr, const int32_t *seqs, const int64_t *pos, int64_t B, const float *d_x, int head,
+                              const voxhip_sample_cfg *cfgs, int32_t *d_tokens, int warmup, int steps,
+                              voxhip_bench_result *out) {
+    return guard_int([&] {
+        require_ok();
+        if (vh::prof_on()) throw Fail("the benchmark entry points capture graphs, which VOX_PROFILE=gpu turns off");
+        if (!out || steps <= 0 || !d_x || !seqs || !pos) throw Fail("bad bench arguments");
+        Xfmr &X = xf_at(xfmr);
+        if (B <= 0 || B > kMaxM) throw Fail("bench_decode_steps takes 1..8 sequences");
+        std::array<int, 8> key;
+        key.fill(-1);
+        std::vector<RowRef> rr(static_cast<size_t>(B));
+        std::vector<int64_t> ps(static_cast<size_t>(B));
+        for (int64_t b = 0; b < B; ++b) {
+            Seq &S = seq_at(seqs[b]);
+            check_seq_for(X, xfmr, S);
+            if (pos[b] < 0 || pos[b] + 1 > S.cap) throw Fail("context exceeds GPU KV capacity");
+            for (int64_t c = 0; c < b; ++c)
+                if (seqs[c] == seqs[b]) throw Fail("a sequence appears twice in one step");
+            rr[size_t(b)] = row_of(S, pos[b]);
+            ps[size_t(b)] = pos[b];
+            key[size_t(b)] = seqs[b];
         }
-        cleanup();
+        prepare_head(X, head, cfgs != nullptr);
+        set_rows(X, rr);
+        if (cfgs) set_sample_cfgs(X, cfgs, int(B));
+        bench_decode_impl(X, key, int(B), true, ps, d_x, head, cfgs != nullptr, d_tokens, warmup, steps, out);
         return 1;
     }, 0);
 }

@@ -139,7 +139,7 @@ class CodecDesc(C.Structure):
 
 
 KERNEL_CLASSES = ("qkv_gemv", "o_gemv", "gateup_gemv", "down_gemv", "head_gemv", "attention", "attn_combine", "qk_post", "sampler",
-                  "ffn", "acc_fold")
+                  "ffn", "acc_fold", "quant_rows")
 
 
 class BenchResult(C.Structure):
@@ -217,6 +217,7 @@ SIGNATURES = {
     "voxhip_quantize_q4_dev": (_I, [_P, _I64, _I64, _P, _P]),
     "voxhip_quantize_act_dev": (_I, [_P, _I64, _P, _P]),
     "voxhip_bench_decode": (_I, [_I, _I, _I64, _P, _I, C.POINTER(SampleCfg), _P, _I, _I, C.POINTER(BenchResult)]),
+    "voxhip_bench_decode_steps": (_I, [_I, _P, _P, _I64, _P, _I, _P, _P, _I, _I, C.POINTER(BenchResult)]),
     "voxhip_bench_gemv_q8": (_I, [_I64, _I64, _I, _I, _I, C.POINTER(C.c_double)]),
     "voxhip_bench_copy": (_I, [_I64, _I, _I, C.POINTER(C.c_double)]),
     "voxhip_bench_ffn_q8": (_I, [_I64, _I64, _I, _I, _I, C.POINTER(C.c_double), _P]),
@@ -831,6 +832,19 @@ def bench_decode(xfmr, seq, pos0, d_x, head, cfg, d_token, warmup, steps):
     r = BenchResult()
     _check(lib().voxhip_bench_decode(xfmr, seq, pos0, d_x.ptr, head, None if cfg is None else C.byref(cfg),
                                      None if d_token is None else d_token.ptr, warmup, steps, C.byref(r)), "bench_decode")
+    return r
+
+
+def bench_decode_steps(xfmr, seqs, pos, d_x, head, cfgs, d_tokens, warmup, steps):
+    """voxhip_bench_decode for a step of len(seqs) sessions (decode_steps_dev)."""
+    B = len(seqs)
+    s = np.ascontiguousarray(seqs, np.int32)
+    p = np.ascontiguousarray(pos, np.int64)
+    arr = (SampleCfg * B)(*cfgs) if cfgs is not None else None
+    r = BenchResult()
+    _check(lib().voxhip_bench_decode_steps(xfmr, _p(s), _p(p), B, d_x.ptr, head, arr,
+                                           None if d_tokens is None else d_tokens.ptr, warmup, steps, C.byref(r)),
+           "bench_decode_steps")
     return r
 
 
