@@ -29,9 +29,21 @@ static int target_waves() {
 // Pre-quantized rows (PRO_Q): each block copies the M quantized rows into LDS, so larger tiles (up to 8 rows per
 // wave) copy them fewer times, as long as the launch keeps one block per CU. (The same tiles with the fused prologue
 // measured slower than quantizing once: 2.58 against 2.00 ms for the 1.7B q4 step at 8 sessions.)
+static int q_rmax() {  // VOXHIP_GEMVQ_RMAX caps the rows per wave of these tiles (2 or 4; tuning)
+    static const int r = [] {
+        const char *e = std::getenv("VOXHIP_GEMVQ_RMAX");
+        const int v = e ? std::atoi(e) : 0;
+        return v == 2 || v == 4 ? v : 8;
+    }();
+    return r;
+}
+// Rows per wave: 2, and 4 for the SwiGLU pass while that still makes 256 blocks. Measured on configs[2] at 8 rows
+// (1.7B q4, graph step 1.747 / 1.672 / 1.653 ms with at most 8 / 4 / 2 rows a wave): gate|up 12.7 / 10.1 / 11.1 us,
+// q|k|v, o and down fastest at 2 (a block's copy of the rows serves fewer weight rows, but more blocks share the
+// stream).
 static void gemv_tile_q(int rows, int nchunk, bool swiglu, int *R, int *IT) {
     int r = 2;
-    while (r < 8 && int64_t(rows) / (4 * 2 * r) >= 256) r *= 2;
+    if (swiglu && q_rmax() >= 4 && int64_t(rows) / (4 * 4) >= 256) r = 4;
     *R = r;
     // one pass of chunks where the tile allows it: every weight load of a wave in flight at once (K 6144 q4: 3)
     *IT = swiglu || r != 2 || nchunk <= 64 ? 1 : nchunk <= 128 ? 2 : 3;
