@@ -270,7 +270,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_quant_rows(GemvArgs a, int8_t 
     }
     float *xn = (PRO != PRO_X && a.xnorm) ? a.xnorm + int64_t(mm) * K : nullptr;
     ProStage<1, PRO> st;
-    prologue<1, PRO, false>(b, x, K, red, st, [&](int, int sl, const float (&v)[8]) {
+    auto sink = [&](int, int sl, const float (&v)[8]) {
         if (xn)
 #pragma unroll
             for (int j = 0; j < 8; ++j) xn[sl * 8 + j] = v[j];
@@ -283,7 +283,15 @@ __global__ __launch_bounds__(kGemvThreads) void k_quant_rows(GemvArgs a, int8_t 
             qs[mm * nb + (sl >> 2)] = sc;
             qsum[mm * nb + (sl >> 2)] = bs;
         }
-    });
+    };
+    // every input load issued first and kept in registers for both passes of the RMSNorm (one round trip), when the
+    // row fits the staging slots; the same arithmetic either way
+    if (pro_stageable<1, PRO>(K)) {
+        pro_stage<1, PRO>(b, x, K, st);
+        prologue<1, PRO, true>(b, x, K, red, st, sink);
+    } else {
+        prologue<1, PRO, false>(b, x, K, red, st, sink);
+    }
 }
 
 // Fixed-point form of the FFN's down product: units of 2^-32, summed exactly (and so in any order) by integer
