@@ -480,6 +480,17 @@ int voxhip_bench_decode_steps(int xfmr, const int32_t *seqs, const int64_t *pos,
  * (rotating, so the working set exceeds the 256 MB Infinity Cache): average ms per launch. */
 int voxhip_bench_gemv_q8(int64_t rows, int64_t cols, int copies, int warmup, int iters, double *ms_per_launch);
 
+/* Times the split-f16 MFMA GEMM of the multi-row passes (prefill, DiT and flow-estimator linears) on one product
+ * shape: y [m][n] = (A_hi + A_lo) [m][K] . W [n][K]^T, A_hi ~N(0, 1) and A_lo ~N(0, 1e-3) as f16 planes, W ~N(0,
+ * 0.02) as f16 or (q8 != 0) in its q8 form (int8 values widened to f16, per-32 block scales). tile 0 takes the
+ * library's shape policy; 1..4 force one of its block tiles (rows of A x rows of W: 32x32, 32x64, 64x64, 64x128 of
+ * 8 waves); every tile gives the same bits (the same MFMA sequence per output). The inputs are those of
+ * voxhip_mat_synthetic(F16, m, K, 11, 0x90, 0, 1) (A_hi), (F16, m, K, 12, 0x91, 0, 1e-3) (A_lo) and (F16 or Q8, n, K,
+ * 13, 0x92, 0, 0.02) (W). Average microseconds per launch; y_out (host, may be NULL) receives y of
+ * the last launch. K must be a multiple of 64. No reference counterpart (benchmark helper). */
+int voxhip_bench_gemm_hh(int64_t m, int64_t n, int64_t K, int q8, int tile, int warmup, int iters, double *us_per_launch,
+                         float *y_out);
+
 /* BASELINE configs[0] on the device: one q8 FFN block (RMSNorm -> gate|up GEMV + SwiGLU -> down GEMV + residual,
  * two kernels) over `copies` distinct weight sets in one graph, so the working set exceeds the 256 MB Infinity
  * Cache: average microseconds per block. Copy c's gate|up matrix [2 inter][hidden] (gate row u at row 2u, up row u

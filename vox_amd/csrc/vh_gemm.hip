@@ -1,5 +1,6 @@
 // Instantiations of the f32 MFMA GEMM (multi-row passes, DiT linears, grouped convolutions) and the
 // attention-partials merge.
+#include <atomic>
 #include <algorithm>
 
 #include "vh_gemm.hpp"
@@ -155,8 +156,23 @@ static hipError_t gemm_hh_tiles(const _Float16 *w, const float *q8_scale, const 
                     unsigned(g.kchunk ? (g.K + g.kchunk - 1) / g.kchunk : 1));
     return launch(k_gemm_hh<EPI, TM, TN, 64, Q8, WN>, grid, dim3(128 * WN), 0, s, w, q8_scale, g);
 }
+// A tile forced by voxhip_bench_gemm_hh (0: the policy below): 1 32 x 32, 2 32 x 64, 3 64 x 64, 4 64 x 128 (8
+// waves), as rows of A x rows of W.
+static std::atomic<int> g_hh_tile{0};
+void set_gemm_hh_tile(int tile) { g_hh_tile.store(tile); }
+template <int EPI, bool Q8>
+static hipError_t gemm_hh_forced(int tile, const _Float16 *w, const float *q8_scale, const GemmArgs &g, hipStream_t s) {
+    switch (tile) {
+        case 1: return gemm_hh_tiles<EPI, 1, 1, Q8>(w, q8_scale, g, s);
+        case 2: return gemm_hh_tiles<EPI, 1, 2, Q8>(w, q8_scale, g, s);
+        case 3: return gemm_hh_tiles<EPI, 2, 2, Q8>(w, q8_scale, g, s);
+        case 4: return gemm_hh_tiles<EPI, 2, 2, Q8, 4>(w, q8_scale, g, s);
+        default: return hipErrorInvalidValue;
+    }
+}
 template <int EPI, bool Q8>
 static hipError_t gemm_hh_run(const _Float16 *w, const float *q8_scale, const GemmArgs &g, hipStream_t s) {
+    if (const int tile = g_hh_tile.load()) return gemm_hh_forced<EPI, Q8>(tile, w, q8_scale, g, s);
     const int64_t blocks = int64_t((g.n + 63) / 64) * ((g.m + 63) / 64);
     if constexpr (EPI == EPI_STORE || EPI == EPI_ACC || EPI == EPI_GATED_ACC || EPI == EPI_SWIGLU) {
         GemmArgs gs = g;

@@ -63,6 +63,8 @@ hipError_t launch_gemm(int wt, int epi, const uint8_t *w, const float *scale, co
 // (q8_scale null), or Q8 weights as their int8 values widened to f16 with the block scales [n][K / 32] in q8_scale;
 // epilogues STORE, ACC, GATED_ACC, GELU, SWIGLU, GELU_H16, SWIGLU_H16, ROPE_H16 (split K uses g.ws).
 hipError_t launch_gemm_hh(int epi, const _Float16 *w, const float *q8_scale, const GemmArgs &g, hipStream_t s);
+// Forces launch_gemm_hh's block tile (0: its shape policy); voxhip_bench_gemm_hh only.
+void set_gemm_hh_tile(int tile);
 // The same with EPI_ACC, and when the product splits K, the next RMSNorm (gamma, eps) of the updated rows of y written
 // as f16 halves (out16, ldo, lo_off as launch_rmsnorm_rows_h16) by the split-K reduce itself: *normed tells whether
 // it did (otherwise the caller runs the norm).

@@ -3859,6 +3859,77 @@ int voxhip_bench_ffn_q8(int64_t hidden, int64_t inter, int copies, int warmup, i
     }, 0);
 }
 
+int voxhip_bench_gemm_hh(int64_t m, int64_t n, int64_t K, int q8, int tile, int warmup, int iters, double *us_per_launch,
+                         float *y_out) {
+    return guard_int([&] {
+        require_ok();
+        if (vh::prof_on()) throw Fail("the benchmark entry points time launches, which VOX_PROFILE=gpu serialises");
+        if (m <= 0 || n <= 0 || K <= 0 || K % 64 || tile < 0 || tile > 4 || warmup < 0 || iters <= 0 || !us_per_launch)
+            throw Fail("bad bench arguments");
+        if (m > (int64_t(1) << 20) || n > (int64_t(1) << 20) || m * K > (int64_t(1) << 28) || n * K > (int64_t(1) << 28))
+            throw Fail("bench_gemm_hh: shape too large");
+        _Float16 *a16 = nullptr, *w16 = nullptr;
+        float *tmp = nullptr, *sc = nullptr, *y = nullptr;
+        int8_t *q = nullptr;
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        auto cleanup = [&] {
+            (void)hipStreamSynchronize(g.stream);
+            vh::set_gemm_hh_tile(0);
+            dfree(a16); dfree(w16); dfree(tmp); dfree(sc); dfree(y); dfree(q);
+            if (e0) (void)hipEventDestroy(e0);
+            if (e1) (void)hipEventDestroy(e1);
+        };
+        try {
+            // A: hi plane ~N(0, 1) as f16, lo plane ~N(0, 1e-3) as f16; W: ~N(0, 0.02) as f16, or its q8 form (int8
+            // values as f16 and the block scales)
+            a16 = dalloc_t<_Float16>(size_t(2 * m * K));
+            w16 = dalloc_t<_Float16>(size_t(n * K));
+            tmp = dalloc_t<float>(size_t(std::max(m, n) * K));
+            y = dalloc_t<float>(size_t(m * n));
+            HIPCHECK(launch_fill_normal(tmp, m * K, 11, 0x90u, 0.f, 1.f, g.stream));
+            HIPCHECK(launch_to_f16(tmp, m * K, a16, g.stream));
+            HIPCHECK(launch_fill_normal(tmp, m * K, 12, 0x91u, 0.f, 1e-3f, g.stream));
+            HIPCHECK(launch_to_f16(tmp, m * K, a16 + m * K, g.stream));
+            HIPCHECK(launch_fill_normal(tmp, n * K, 13, 0x92u, 0.f, 0.02f, g.stream));
+            if (q8) {
+                q = dalloc_t<int8_t>(size_t(n * K));
+                sc = dalloc_t<float>(size_t(n * K / 32));
+                HIPCHECK(launch_quant_q8(tmp, n * K / 32, q, sc, g.stream));
+                HIPCHECK(launch_q8_to_f16(q, w16, n * K, g.stream));
+            } else {
+                HIPCHECK(launch_to_f16(tmp, n * K, w16, g.stream));
+            }
+            GemmArgs ga{};
+            ga.m = int32_t(m);
+            ga.n = int32_t(n);
+            ga.K = int32_t(K);
+            ga.a16 = a16;
+            ga.a_lo = m * K;
+            ga.lda = int32_t(K);
+            ga.y = y;
+            ga.ldy = int32_t(n);
+            vh::set_gemm_hh_tile(tile);
+            for (int i = 0; i < warmup; ++i) HIPCHECK(launch_gemm_hh(EPI_STORE, w16, sc, ga, g.stream));
+            HIPCHECK(hipEventCreate(&e0));
+            HIPCHECK(hipEventCreate(&e1));
+            HIPCHECK(hipEventRecord(e0, g.stream));
+            for (int i = 0; i < iters; ++i) HIPCHECK(launch_gemm_hh(EPI_STORE, w16, sc, ga, g.stream));
+            HIPCHECK(hipEventRecord(e1, g.stream));
+            HIPCHECK(hipEventSynchronize(e1));
+            float ms = 0.f;
+            HIPCHECK(hipEventElapsedTime(&ms, e0, e1));
+            *us_per_launch = double(ms) * 1000.0 / iters;
+            if (y_out) HIPCHECK(hipMemcpy(y_out, y, size_t(m * n) * 4, hipMemcpyDeviceToHost));
+            sync_status();
+        } catch (...) {
+            cleanup();
+            throw;
+        }
+        cleanup();
+        return 1;
+    }, 0);
+}
+
 int voxhip_bench_copy(int64_t bytes, int warmup, int iters, double *ms_per_copy) {
     return guard_int([&] {
         require_ok();

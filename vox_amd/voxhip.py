@@ -220,6 +220,7 @@ SIGNATURES = {
     "voxhip_bench_decode_steps": (_I, [_I, _P, _P, _I64, _P, _I, _P, _P, _I, _I, C.POINTER(BenchResult)]),
     "voxhip_bench_gemv_q8": (_I, [_I64, _I64, _I, _I, _I, C.POINTER(C.c_double)]),
     "voxhip_bench_copy": (_I, [_I64, _I, _I, C.POINTER(C.c_double)]),
+    "voxhip_bench_gemm_hh": (_I, [_I64, _I64, _I64, _I, _I, _I, _I, C.POINTER(C.c_double), _P]),
     "voxhip_bench_ffn_q8": (_I, [_I64, _I64, _I, _I, _I, C.POINTER(C.c_double), _P]),
 }
 
@@ -852,6 +853,16 @@ def bench_gemv_q8(rows, cols, copies, warmup, iters):
     ms = C.c_double()
     _check(lib().voxhip_bench_gemv_q8(rows, cols, copies, warmup, iters, C.byref(ms)), "bench_gemv_q8")
     return ms.value
+
+
+def bench_gemm_hh(m, n, K, q8=False, tile=0, warmup=3, iters=20, out=False):
+    """Average microseconds of one split-f16 MFMA GEMM launch on an (m, n, K) product (tile 0: the library's policy,
+    1..4 a forced block tile); with out, also y [m][n] of the last launch."""
+    us = C.c_double()
+    y = np.empty((m, n), np.float32) if out else None
+    _check(lib().voxhip_bench_gemm_hh(m, n, K, int(bool(q8)), tile, warmup, iters, C.byref(us),
+                                      y.ctypes.data if out else None), "bench_gemm_hh")
+    return (us.value, y) if out else us.value
 
 
 def bench_copy(nbytes, warmup, iters):
