@@ -207,6 +207,8 @@ struct Ctx {
     // the range-status word (allocated and zeroed at init) and its pinned host copy; word 1 of the device block is
     // the scratch of the weight max |w| reduction
     int32_t *status_dev = nullptr, *status_pin = nullptr;
+    // VOXHIP_CHECK_HOST=1 at a voxhip_init call: copy_h2d / copy_d2h check each side's memory type (check_copy_side)
+    bool check_copies = false;
 };
 
 Ctx g;
@@ -268,12 +270,42 @@ float *dev_scratch(float *&p, size_t &cap, size_t bytes) {
     return p;
 }
 
+// Every copy between host and device memory goes through copy_h2d / copy_d2h. With VOXHIP_CHECK_HOST=1 (read by
+// each voxhip_init call) each checks, by hipPointerGetAttributes, that its device side is device memory and its host side is not
+// (pinned or unregistered host memory), and fails the call naming the copy otherwise: a device address handed to
+// the runtime as host memory would be read or written by the host. s == nullptr: a synchronous copy.
+void check_copy_side(const void *p, bool want_device, const char *copy, const char *side) {
+    hipPointerAttribute_t a{};
+    const hipError_t e = hipPointerGetAttributes(&a, p);
+    const bool dev = e == hipSuccess && a.type == hipMemoryTypeDevice;
+    if (e != hipSuccess) (void)hipGetLastError();  // unregistered host memory reports an error; clear it
+    if (dev != want_device)
+        throw Fail(std::string(copy) + ": the " + side + " is " + (dev ? "device" : "host") + " memory, " +
+                   (want_device ? "device" : "host") + " memory expected");
+}
+hipError_t copy_h2d(void *dst, const void *src, size_t bytes, hipStream_t s) {
+    if (!bytes) return hipSuccess;
+    if (g.check_copies) {
+        check_copy_side(dst, true, "host-to-device copy", "destination");
+        check_copy_side(src, false, "host-to-device copy", "source");
+    }
+    return s ? hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s) : hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice);
+}
+hipError_t copy_d2h(void *dst, const void *src, size_t bytes, hipStream_t s) {
+    if (!bytes) return hipSuccess;
+    if (g.check_copies) {
+        check_copy_side(src, true, "device-to-host copy", "source");
+        check_copy_side(dst, false, "device-to-host copy", "destination");
+    }
+    return s ? hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s) : hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
+}
+
 // The end of a synchronous call: waits for the stream, then fails the call when one of its kernels set the
 // range-status word (an activation beyond the f16 range of a split-f16 product, or a fused-FFN term outside the
 // fixed-point range), clearing the word for the next call. The engine then computes the call on the CPU, as for any
 // failed device call. Device-resident calls (decode_dev, the no-alloc matmul) are reported by voxhip_sync.
 void sync_status() {
-    HIPCHECK(hipMemcpyAsync(g.status_pin, g.status_dev, sizeof(int32_t), hipMemcpyDeviceToHost, g.stream));
+    HIPCHECK(copy_d2h(g.status_pin, g.status_dev, sizeof(int32_t), g.stream));
     HIPCHECK(hipStreamSynchronize(g.stream));
     vh::prof_collect();  // VOX_PROFILE=gpu: the call's stamped launches have finished
     const int32_t v = g.status_pin[0];
@@ -290,7 +322,7 @@ void sync_status() {
 
 void h2d(void *dst, const void *src, size_t bytes) {
     if (!bytes) return;
-    HIPCHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    HIPCHECK(copy_h2d(dst, src, bytes, nullptr));
 }
 
 void require_ok() {
@@ -658,8 +690,8 @@ void set_rows(Xfmr &X, const std::vector<RowRef> &rows) {
             rope[i * size_t(X.hd) + 2 * size_t(p) + 1] = std::sin(f);
         }
     // the row table and the RoPE rows follow each other only up to the pass rows; copy the two spans
-    HIPCHECK(hipMemcpyAsync(X.rows_dev, X.rows_host, rows.size() * sizeof(RowRef), hipMemcpyHostToDevice, g.stream));
-    HIPCHECK(hipMemcpyAsync(X.rope_rows_dev, rope, rows.size() * size_t(X.hd) * 4, hipMemcpyHostToDevice, g.stream));
+    HIPCHECK(copy_h2d(X.rows_dev, X.rows_host, rows.size() * sizeof(RowRef), g.stream));
+    HIPCHECK(copy_h2d(X.rope_rows_dev, rope, rows.size() * size_t(X.hd) * 4, g.stream));
     X.rows_last = rows;
     X.rows_valid = true;
 }
@@ -945,10 +977,10 @@ int forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_proj
         std::memcpy(pin, x + c0 * xc, size_t(mc * xc) * 4);
         if (Pm) {
             float *xin = ensure_xin(X, int64_t(chunk) * xc);
-            HIPCHECK(hipMemcpyAsync(xin, pin, size_t(mc * xc) * 4, hipMemcpyHostToDevice, g.stream));
+            HIPCHECK(copy_h2d(xin, pin, size_t(mc * xc) * 4, g.stream));
             gemv(*Pm, m_total, PRO_X, EPI_STORE, xin, xc, mc, X.h, H, nullptr, 0.f, nullptr, g.stream);
         } else {
-            HIPCHECK(hipMemcpyAsync(X.h, pin, size_t(mc * H) * 4, hipMemcpyHostToDevice, g.stream));
+            HIPCHECK(copy_h2d(X.h, pin, size_t(mc * H) * 4, g.stream));
         }
         bool fused = true;
         for (int i = 0; i < mc && fused; ++i)
@@ -957,7 +989,7 @@ int forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_proj
         if (pass_attn_of(X, mc, fused)) prepare_planes(X, first_layer, n_layers, m_total, mc, g.stream);
         run_layers(X, mc, m_total, first_layer, n_layers, fused);
         if (hidden_out) {
-            HIPCHECK(hipMemcpyAsync(pin, X.h, size_t(mc * H) * 4, hipMemcpyDeviceToHost, g.stream));
+            HIPCHECK(copy_d2h(pin, X.h, size_t(mc * H) * 4, g.stream));
             HIPCHECK(hipStreamSynchronize(g.stream));
             std::memcpy(hidden_out + c0 * H, pin, size_t(mc * H) * 4);
         }
@@ -966,12 +998,12 @@ int forward_rows(Xfmr &X, int64_t m, RowsOf rows_of, const float *x, int in_proj
             if (out_last || head >= 0) {
                 enqueue_final(X, r0, mr, head, g.stream);
                 if (out_last) {
-                    HIPCHECK(hipMemcpyAsync(pin, X.xnorm, size_t(mr * H) * 4, hipMemcpyDeviceToHost, g.stream));
+                    HIPCHECK(copy_d2h(pin, X.xnorm, size_t(mr * H) * 4, g.stream));
                     HIPCHECK(hipStreamSynchronize(g.stream));
                     std::memcpy(out_last + (final_all ? c0 * H : 0), pin, size_t(mr * H) * 4);
                 }
                 if (head >= 0 && head_out) {
-                    HIPCHECK(hipMemcpyAsync(pin, X.logits, size_t(mr * V) * 4, hipMemcpyDeviceToHost, g.stream));
+                    HIPCHECK(copy_d2h(pin, X.logits, size_t(mr * V) * 4, g.stream));
                     HIPCHECK(hipStreamSynchronize(g.stream));
                     std::memcpy(head_out + (final_all ? c0 * V : 0), pin, size_t(mr * V) * 4);
                 }
@@ -1210,6 +1242,8 @@ int voxhip_init(const char *device, char *err, size_t err_len) {
     auto put_err = [&](const std::string &m) {
         if (err && err_len) { std::snprintf(err, err_len, "%s", m.c_str()); }
     };
+    const char *ch = std::getenv("VOXHIP_CHECK_HOST");  // re-read by every call, also after a successful init
+    g.check_copies = ch && ch[0] == '1';
     if (g.ok) return 1;
     if (!g.init_error.empty()) { put_err(g.init_error); return 0; }
     try {
@@ -1329,9 +1363,9 @@ int voxhip_matmul(int mat, const float *x, int64_t m, float *y) {
         for (int64_t c0 = 0; c0 < m; c0 += chunk) {
             const int mc = int(std::min<int64_t>(chunk, m - c0));
             std::memcpy(pin, x + c0 * M.cols, size_t(mc) * size_t(M.cols) * 4);
-            HIPCHECK(hipMemcpyAsync(dx, pin, size_t(mc) * size_t(M.cols) * 4, hipMemcpyHostToDevice, g.stream));
+            HIPCHECK(copy_h2d(dx, pin, size_t(mc) * size_t(M.cols) * 4, g.stream));
             gemv(M, m, PRO_X, EPI_STORE, dx, M.cols, mc, dy, M.rows, nullptr, 0.f, nullptr, g.stream);
-            HIPCHECK(hipMemcpyAsync(pin, dy, size_t(mc) * size_t(M.rows) * 4, hipMemcpyDeviceToHost, g.stream));
+            HIPCHECK(copy_d2h(pin, dy, size_t(mc) * size_t(M.rows) * 4, g.stream));
             HIPCHECK(hipStreamSynchronize(g.stream));
             std::memcpy(y + c0 * M.rows, pin, size_t(mc) * size_t(M.rows) * 4);
         }
@@ -1383,9 +1417,9 @@ int voxhip_mat_gather(int mat, const int32_t *ids, int64_t n, float *out) {
         for (int64_t c0 = 0; c0 < n; c0 += chunk) {
             const int64_t nc = std::min(chunk, n - c0);
             std::memcpy(pin, ids + c0, size_t(nc) * 4);
-            HIPCHECK(hipMemcpyAsync(dids, pin, size_t(nc) * 4, hipMemcpyHostToDevice, g.stream));
+            HIPCHECK(copy_h2d(dids, pin, size_t(nc) * 4, g.stream));
             HIPCHECK(launch_mat_gather(M.w, M.s, gemv_type(M), M.s16 ? 1 : 0, M.cols, dids, nc, dout, g.stream));
-            HIPCHECK(hipMemcpyAsync(pin, dout, size_t(nc) * size_t(M.cols) * 4, hipMemcpyDeviceToHost, g.stream));
+            HIPCHECK(copy_d2h(pin, dout, size_t(nc) * size_t(M.cols) * 4, g.stream));
             HIPCHECK(hipStreamSynchronize(g.stream));
             std::memcpy(out + c0 * M.cols, pin, size_t(nc) * size_t(M.cols) * 4);
         }
@@ -1416,7 +1450,7 @@ int voxhip_convt(int mat, int32_t K, int32_t stride, int32_t pad, int32_t out_pa
         float *dbias = bias ? dx + size_t(T) * size_t(cin) : nullptr;
         std::memcpy(pin, x, xb);
         if (bias) std::memcpy(pin + size_t(T) * size_t(cin), bias, bb);
-        HIPCHECK(hipMemcpyAsync(dx, pin, xb + bb, hipMemcpyHostToDevice, g.stream));
+        HIPCHECK(copy_h2d(dx, pin, xb + bb, g.stream));
         // z = x W^T, frames in passes of the matrix's pass height, then the padded overlap-add + bias
         const int chunk = rows_per_pass(M, T);
         for (int64_t c0 = 0; c0 < T; c0 += chunk) {
@@ -1424,7 +1458,7 @@ int voxhip_convt(int mat, int32_t K, int32_t stride, int32_t pad, int32_t out_pa
             gemv(M, T, PRO_X, EPI_STORE, dx + c0 * cin, cin, mc, dz + c0 * KO, KO, nullptr, 0.f, nullptr, g.stream);
         }
         HIPCHECK(launch_convt_gather(dz, dbias, dy, T, int(To), stride, K, pad, int(cout), g.stream));
-        HIPCHECK(hipMemcpyAsync(pin, dy, yb, hipMemcpyDeviceToHost, g.stream));
+        HIPCHECK(copy_d2h(pin, dy, yb, g.stream));
         sync_status();
         std::memcpy(y, pin, yb);
         return 1;
@@ -1581,14 +1615,14 @@ int voxhip_sample_logits(const float *logits, int32_t n, const voxhip_sample_cfg
         HIPCHECK(hipStreamSynchronize(g.stream));
         if (n_history > 0 && history) h2d(g.hist_dev, history, size_t(n_history) * 4);
         fill_sample_cfg(*g.scfg_host, *cfg, n_history > 0 && history ? g.hist_dev : nullptr, history ? n_history : 0);
-        HIPCHECK(hipMemcpyAsync(g.scfg_dev, g.scfg_host, sizeof(SampleCfgDev), hipMemcpyHostToDevice, g.stream));
+        HIPCHECK(copy_h2d(g.scfg_dev, g.scfg_host, sizeof(SampleCfgDev), g.stream));
         float *dl = dev_scratch(g.dbuf_x, g.dbuf_x_bytes, size_t(n) * 4);
         float *pin = pinned(size_t(n) * 4 + 64);
         std::memcpy(pin, logits, size_t(n) * 4);
-        HIPCHECK(hipMemcpyAsync(dl, pin, size_t(n) * 4, hipMemcpyHostToDevice, g.stream));
+        HIPCHECK(copy_h2d(dl, pin, size_t(n) * 4, g.stream));
         HIPCHECK(launch_sample(g.scfg_dev, dl, n, g.tok_dev, g.stream));
         int32_t tok = -1;
-        HIPCHECK(hipMemcpyAsync(pin, g.tok_dev, 4, hipMemcpyDeviceToHost, g.stream));
+        HIPCHECK(copy_d2h(pin, g.tok_dev, 4, g.stream));
         HIPCHECK(hipStreamSynchronize(g.stream));
         std::memcpy(&tok, pin, 4);
         if (tok < 0) throw Fail("device sampler rejected the request");
@@ -1616,7 +1650,7 @@ int voxhip_memcpy_h2d(void *d_dst, const void *src, size_t bytes) {
     return guard_int([&] {
         require_ok();
         HIPCHECK(hipStreamSynchronize(g.stream));
-        HIPCHECK(hipMemcpy(d_dst, src, bytes, hipMemcpyHostToDevice));
+        HIPCHECK(copy_h2d(d_dst, src, bytes, nullptr));
         return 1;
     }, 0);
 }
@@ -1624,7 +1658,7 @@ int voxhip_memcpy_d2h(void *dst, const void *d_src, size_t bytes) {
     return guard_int([&] {
         require_ok();
         HIPCHECK(hipStreamSynchronize(g.stream));
-        HIPCHECK(hipMemcpy(dst, d_src, bytes, hipMemcpyDeviceToHost));
+        HIPCHECK(copy_d2h(dst, d_src, bytes, nullptr));
         return 1;
     }, 0);
 }
@@ -1714,7 +1748,7 @@ void set_sample_cfgs(Xfmr &X, const voxhip_sample_cfg *cfgs, int n) {
     if (std::memcmp(d.data(), X.scfg_host, size_t(n) * sizeof(SampleCfgDev)) != 0) {
         HIPCHECK(hipStreamSynchronize(g.stream));
         std::memcpy(X.scfg_host, d.data(), size_t(n) * sizeof(SampleCfgDev));
-        HIPCHECK(hipMemcpyAsync(X.scfg_dev, X.scfg_host, size_t(n) * sizeof(SampleCfgDev), hipMemcpyHostToDevice, g.stream));
+        HIPCHECK(copy_h2d(X.scfg_dev, X.scfg_host, size_t(n) * sizeof(SampleCfgDev), g.stream));
     }
 }
 
@@ -1966,11 +2000,11 @@ int voxhip_lm_sample_dev(const float *d_logits, int32_t n, const voxhip_lm_cfg *
         LmState st{};
         st.step = int32_t(step); st.n_dec = n_decoded; st.last = -1;
         *lm_host_state(0) = st;
-        HIPCHECK(hipMemcpyAsync(g.lm_cfg_dev, lm_host_cfg(), sizeof(LmCfgDev), hipMemcpyHostToDevice, g.stream));
-        HIPCHECK(hipMemcpyAsync(g.lm_state_dev, lm_host_state(0), sizeof(LmState), hipMemcpyHostToDevice, g.stream));
+        HIPCHECK(copy_h2d(g.lm_cfg_dev, lm_host_cfg(), sizeof(LmCfgDev), g.stream));
+        HIPCHECK(copy_h2d(g.lm_state_dev, lm_host_state(0), sizeof(LmState), g.stream));
         HIPCHECK(launch_lm_sample(d_logits, n, g.lm_cfg_dev, g.lm_state_dev, const_cast<int32_t *>(d_decoded), d_logp, 0, false,
                                   g.stream));
-        HIPCHECK(hipMemcpyAsync(lm_host_state(1), g.lm_state_dev, sizeof(LmState), hipMemcpyDeviceToHost, g.stream));
+        HIPCHECK(copy_d2h(lm_host_state(1), g.lm_state_dev, sizeof(LmState), g.stream));
         HIPCHECK(hipStreamSynchronize(g.stream));
         const LmState r = *lm_host_state(1);
         if (r.status) throw Fail("CosyVoice: sampling reaches max_trials and still gets eos when ignore_eos is True");
@@ -2007,8 +2041,8 @@ int voxhip_lm_generate(int xfmr, int seq, const float *x, int64_t n, int head, i
         LmState st{};
         st.last = -1;
         *lm_host_state(0) = st;
-        HIPCHECK(hipMemcpyAsync(X.lm_cfg, lm_host_cfg(), sizeof(LmCfgDev), hipMemcpyHostToDevice, g.stream));
-        HIPCHECK(hipMemcpyAsync(X.lm_state, lm_host_state(0), sizeof(LmState), hipMemcpyHostToDevice, g.stream));
+        HIPCHECK(copy_h2d(X.lm_cfg, lm_host_cfg(), sizeof(LmCfgDev), g.stream));
+        HIPCHECK(copy_h2d(X.lm_state, lm_host_state(0), sizeof(LmState), g.stream));
         set_rows(X, {row_of(S, n - 1)});  // the first step's embedding kernel advances it to position n
         // VOX_PROFILE=gpu: the same steps launched one by one (stamped launches are not captured)
         hipGraphExec_t exec = vh::prof_on() ? nullptr : lm_graph(X, S, seq, head, speech_emb, logp != nullptr);
@@ -2023,7 +2057,7 @@ int voxhip_lm_generate(int xfmr, int seq, const float *x, int64_t n, int head, i
                 __atomic_store_n(&slot->pad0, -1, __ATOMIC_RELEASE);
                 if (exec) HIPCHECK(hipGraphLaunch(exec, g.stream));
                 else enqueue_lm_steps(X, S, head, speech_emb, logp != nullptr, g.stream);
-                HIPCHECK(hipMemcpyAsync(slot, X.lm_state, sizeof(LmState), hipMemcpyDeviceToHost, g.stream));
+                HIPCHECK(copy_d2h(slot, X.lm_state, sizeof(LmState), g.stream));
                 if (c >= 1) {
                     LmState *prev = lm_host_state(1 + ((c - 1) & 1));
                     while (__atomic_load_n(&prev->pad0, __ATOMIC_ACQUIRE) == -1) {
@@ -2035,7 +2069,7 @@ int voxhip_lm_generate(int xfmr, int seq, const float *x, int64_t n, int head, i
                     if (__atomic_load_n(&prev->done, __ATOMIC_ACQUIRE)) break;
                 }
             }
-            HIPCHECK(hipMemcpyAsync(lm_host_state(0), X.lm_state, sizeof(LmState), hipMemcpyDeviceToHost, g.stream));
+            HIPCHECK(copy_d2h(lm_host_state(0), X.lm_state, sizeof(LmState), g.stream));
             sync_status();
             const LmState r = *lm_host_state(0);
             if (r.status) throw Fail("CosyVoice: sampling reaches max_trials and still gets eos when ignore_eos is True");
@@ -2043,9 +2077,9 @@ int voxhip_lm_generate(int xfmr, int seq, const float *x, int64_t n, int head, i
             // max_len x V log-probs): a count outside them is an error, never a copy
             if (r.n_dec < 0 || r.n_dec > cfg->max_len) throw Fail("LM state reports " + std::to_string(r.n_dec) + " tokens of " +
                                                                   std::to_string(cfg->max_len));
-            if (r.n_dec > 0) HIPCHECK(hipMemcpy(tokens, X.lm_dec, size_t(r.n_dec) * 4, hipMemcpyDeviceToHost));
+            if (r.n_dec > 0) HIPCHECK(copy_d2h(tokens, X.lm_dec, size_t(r.n_dec) * 4, nullptr));
             const int64_t rows = std::min<int64_t>(r.n_dec + (r.last >= cfg->speech_tokens ? 1 : 0), cfg->max_len);
-            if (logp && rows > 0) HIPCHECK(hipMemcpy(logp, X.lm_logp, size_t(rows * V) * 4, hipMemcpyDeviceToHost));
+            if (logp && rows > 0) HIPCHECK(copy_d2h(logp, X.lm_logp, size_t(rows * V) * 4, nullptr));
             *n_tokens = r.n_dec;
         } catch (...) {
             cleanup();
@@ -2093,16 +2127,16 @@ int voxhip_pred_frame(int xfmr, int seq, const float *in2, int in_proj, const in
             std::memset(&X.pred_cfg_host[cb], 0, sizeof(SampleCfgDev));
             fill_sample_cfg(X.pred_cfg_host[cb], c, nullptr, 0);
         }
-        HIPCHECK(hipMemcpyAsync(X.pred_cfg, X.pred_cfg_host, size_t(G) * sizeof(SampleCfgDev), hipMemcpyHostToDevice, g.stream));
-        HIPCHECK(hipMemcpyAsync(in_proj >= 0 ? X.xin : X.h, in2, size_t(2 * din) * 4, hipMemcpyHostToDevice, g.stream));
+        HIPCHECK(copy_h2d(X.pred_cfg, X.pred_cfg_host, size_t(G) * sizeof(SampleCfgDev), g.stream));
+        HIPCHECK(copy_h2d(in_proj >= 0 ? X.xin : X.h, in2, size_t(2 * din) * 4, g.stream));
         HIPCHECK(hipMemsetAsync(X.pred_err, 0, sizeof(int32_t), g.stream));
         // the layer enqueue takes the first row's cache view from the host row table: this sequence's
         set_rows(X, {row_of(S, 0), row_of(S, 1)});
         X.rows_valid = false;  // the frame rewrites the row table
         if (vh::prof_on()) enqueue_pred(X, S, in_proj, heads, embs, G, g.stream);  // stamped launches, not captured
         else HIPCHECK(hipGraphLaunch(pred_graph(X, S, seq, in_proj, heads, embs, G), g.stream));
-        HIPCHECK(hipMemcpyAsync(X.pred_host, X.pred_codes, size_t(G) * 4, hipMemcpyDeviceToHost, g.stream));
-        HIPCHECK(hipMemcpyAsync(X.pred_host + kPredMaxGroups, X.pred_err, 4, hipMemcpyDeviceToHost, g.stream));
+        HIPCHECK(copy_d2h(X.pred_host, X.pred_codes, size_t(G) * 4, g.stream));
+        HIPCHECK(copy_d2h(X.pred_host + kPredMaxGroups, X.pred_err, 4, g.stream));
         sync_status();
         if (X.pred_host[kPredMaxGroups]) throw Fail("code out of the embedding's range");
         for (int cb = 1; cb < G; ++cb) codes[cb] = X.pred_host[cb];
@@ -2506,7 +2540,7 @@ int voxhip_f5_step(int id, const float *x, const float *ts, float *out) {
         h2d(F.ts, ts, size_t(F.dim) * 4);
         f5_enqueue(F, g.stream);
         sync_status();
-        HIPCHECK(hipMemcpy(out, F.out, size_t(F.B) * F.N * F.mel * 4, hipMemcpyDeviceToHost));
+        HIPCHECK(copy_d2h(out, F.out, size_t(F.B) * F.N * F.mel * 4, nullptr));
         return 1;
     }, 0);
 }
@@ -2550,7 +2584,7 @@ int voxhip_f5_vocos(int id, const float *mel, int T, float *head) {
         const GpuMat &Mh = mat_at(F.v_head);
         f5_gemm(Mh, EPI_STORE, F.vx, gemm_args(Mh, Mh.b, F.vhead, VD, F.vout, T), s);
         sync_status();
-        HIPCHECK(hipMemcpy(head, F.vhead, size_t(T) * F.vout * 4, hipMemcpyDeviceToHost));
+        HIPCHECK(copy_d2h(head, F.vhead, size_t(T) * F.vout * 4, nullptr));
         return 1;
     }, 0);
 }
@@ -2868,7 +2902,7 @@ int voxhip_cosy_step(int id, const float *x, const float *tb, float *out) {
         }
         if (!vh::prof_on()) HIPCHECK(hipGraphLaunch(E.step_graph, g.stream));
         sync_status();
-        HIPCHECK(hipMemcpy(out, E.out, size_t(2) * E.T * E.M * 4, hipMemcpyDeviceToHost));
+        HIPCHECK(copy_d2h(out, E.out, size_t(2) * E.T * E.M * 4, nullptr));
         return 1;
     }, 0);
 }
@@ -3359,7 +3393,7 @@ int voxhip_codec_forward(int codec, int state, const float *z, int F, float *pcm
         if (!vh::prof_on()) HIPCHECK(hipGraphLaunch(it->second, g.stream));
         sync_status();  // a failure leaves the state as it was (its parity and length unchanged)
         const int64_t n = int64_t(F) * E.spf;
-        HIPCHECK(hipMemcpy(pcm, E.S[4], size_t(n) * 4, hipMemcpyDeviceToHost));
+        HIPCHECK(copy_d2h(pcm, E.S[4], size_t(n) * 4, nullptr));
         St.len += F;
         St.parity ^= 1;
         if (n_out) *n_out = n;
@@ -3399,7 +3433,7 @@ int voxhip_mat_synthetic(int32_t type, int64_t rows, int64_t cols, uint64_t seed
                 uint32_t *mx = reinterpret_cast<uint32_t *>(g.status_dev + 1);
                 HIPCHECK(hipMemsetAsync(mx, 0, 4, g.stream));
                 HIPCHECK(launch_absmax(tmp, int64_t(n), mx, g.stream));
-                HIPCHECK(hipMemcpyAsync(g.status_pin + 1, mx, 4, hipMemcpyDeviceToHost, g.stream));
+                HIPCHECK(copy_d2h(g.status_pin + 1, mx, 4, g.stream));
             }
             HIPCHECK(hipStreamSynchronize(g.stream));
             if (type == VOXHIP_F32) m.wmax = __builtin_bit_cast(float, uint32_t(g.status_pin[1]));
@@ -3419,18 +3453,18 @@ int voxhip_mat_download(int mat, void *data, float *scale, float *bias) {
         require_ok();
         const GpuMat &m = mat_at(mat);
         HIPCHECK(hipStreamSynchronize(g.stream));
-        if (data) HIPCHECK(hipMemcpy(data, m.w, size_t(m.rows) * row_bytes(m.type, m.cols), hipMemcpyDeviceToHost));
+        if (data) HIPCHECK(copy_d2h(data, m.w, size_t(m.rows) * row_bytes(m.type, m.cols), nullptr));
         if (scale && m.s) {
             const size_t nsc = size_t(m.rows) * size_t(m.cols / 32);
             if (m.s16) {  // widened exactly to the f32 scales the matrix stands for
                 std::vector<_Float16> t(nsc);
-                HIPCHECK(hipMemcpy(t.data(), m.s, nsc * 2, hipMemcpyDeviceToHost));
+                HIPCHECK(copy_d2h(t.data(), m.s, nsc * 2, nullptr));
                 for (size_t i = 0; i < nsc; ++i) scale[i] = float(t[i]);
             } else {
-                HIPCHECK(hipMemcpy(scale, m.s, nsc * 4, hipMemcpyDeviceToHost));
+                HIPCHECK(copy_d2h(scale, m.s, nsc * 4, nullptr));
             }
         }
-        if (bias && m.b) HIPCHECK(hipMemcpy(bias, m.b, size_t(m.rows) * 4, hipMemcpyDeviceToHost));
+        if (bias && m.b) HIPCHECK(copy_d2h(bias, m.b, size_t(m.rows) * 4, nullptr));
         return 1;
     }, 0);
 }
@@ -3471,8 +3505,8 @@ int voxhip_seq_download(int seq, int32_t layer, int64_t len, float *k, float *v)
         HIPCHECK(hipStreamSynchronize(g.stream));
         const size_t plane = size_t(S.cap) * S.hd;
         std::vector<_Float16> tk(static_cast<size_t>(S.kvh) * plane), tv(tk.size());
-        HIPCHECK(hipMemcpy(tk.data(), S.k + size_t(layer) * S.kvh * plane, tk.size() * 2, hipMemcpyDeviceToHost));
-        HIPCHECK(hipMemcpy(tv.data(), S.v + size_t(layer) * S.kvh * plane, tv.size() * 2, hipMemcpyDeviceToHost));
+        HIPCHECK(copy_d2h(tk.data(), S.k + size_t(layer) * S.kvh * plane, tk.size() * 2, nullptr));
+        HIPCHECK(copy_d2h(tv.data(), S.v + size_t(layer) * S.kvh * plane, tv.size() * 2, nullptr));
         const size_t kd = size_t(S.kvh) * S.hd;
         for (int64_t p = 0; p < len; ++p)
             for (int h = 0; h < S.kvh; ++h)
@@ -3820,9 +3854,9 @@ int voxhip_bench_ffn_q8(int64_t hidden, int64_t inter, int copies, int warmup, i
             if (check) {  // copy 0's block once on x, as the graph launches it: x, gamma and the block's output
                 gemv(g.mats[size_t(ids[0])], 1, PRO_RMS, EPI_SWIGLU, h, hidden, 1, gbuf, inter, gamma, 1e-6f, nullptr, g.stream);
                 gemv(g.mats[size_t(ids[1])], 1, PRO_X, EPI_ACC, gbuf, inter, 1, h, hidden, nullptr, 0.f, nullptr, g.stream);
-                HIPCHECK(hipMemcpyAsync(check, x, size_t(hidden) * 4, hipMemcpyDeviceToHost, g.stream));
-                HIPCHECK(hipMemcpyAsync(check + hidden, gamma, size_t(hidden) * 4, hipMemcpyDeviceToHost, g.stream));
-                HIPCHECK(hipMemcpyAsync(check + 2 * hidden, h, size_t(hidden) * 4, hipMemcpyDeviceToHost, g.stream));
+                HIPCHECK(copy_d2h(check, x, size_t(hidden) * 4, g.stream));
+                HIPCHECK(copy_d2h(check + hidden, gamma, size_t(hidden) * 4, g.stream));
+                HIPCHECK(copy_d2h(check + 2 * hidden, h, size_t(hidden) * 4, g.stream));
                 HIPCHECK(hipMemcpyAsync(h, x, size_t(hidden) * 4, hipMemcpyDeviceToDevice, g.stream));
             }
             HIPCHECK(hipStreamSynchronize(g.stream));
@@ -3919,7 +3953,7 @@ int voxhip_bench_gemm_hh(int64_t m, int64_t n, int64_t K, int q8, int tile, int 
             float ms = 0.f;
             HIPCHECK(hipEventElapsedTime(&ms, e0, e1));
             *us_per_launch = double(ms) * 1000.0 / iters;
-            if (y_out) HIPCHECK(hipMemcpy(y_out, y, size_t(m * n) * 4, hipMemcpyDeviceToHost));
+            if (y_out) HIPCHECK(copy_d2h(y_out, y, size_t(m * n) * 4, nullptr));
             sync_status();
         } catch (...) {
             cleanup();
