@@ -2166,6 +2166,9 @@ struct F5 {
     // hd < hp padded with zero dims, stack_rows_heads)
     int dim = 0, depth = 0, heads = 0, hd = 0, hp = 0, ff = 0, mel = 0, text = 0, pe = 0;
     int in_proj = -1, norm_out = -1, proj_out = -1;
+    // every block's ada matrix and norm_out stacked at create, when they share a type: one GEMV writes all the
+    // step's modulation vectors (they depend only on the time embedding) instead of depth + 1 launches; -1: none
+    int ada_all = -1;
     std::vector<F5Block> blocks;
     F5Conv pos1, pos2;
     // every block linear F16 and dim, inner, ff multiples of 64: the block's activations travel between kernels as
@@ -2343,7 +2346,7 @@ float *upload_vec(const float *v, int n, const char *what) {
 }
 
 void f5_free_step(F5 &F) {
-    for (float *p : {F.cat, F.h, F.a, F.nrm, F.at, F.ffb, F.ada, F.fin, F.ts, F.x, F.out, F.rope}) dfree(p);
+    for (float *p : {F.cat, F.h, F.a, F.nrm, F.at, F.ffb, F.ada, F.ts, F.x, F.out, F.rope}) dfree(p);  // fin is in ada
     F.cat = F.h = F.a = F.nrm = F.at = F.ffb = F.ada = F.fin = F.ts = F.x = F.out = F.rope = nullptr;
     for (_Float16 *p : {F.qkv16, F.nrm16, F.at16, F.ffb16}) dfree(p);
     F.qkv16 = F.nrm16 = F.at16 = F.ffb16 = nullptr;
@@ -2381,11 +2384,16 @@ void f5_enqueue(F5 &F, hipStream_t s) {
     const int D = F.dim, INNER = F.heads * F.hp, W = 2 * F.mel + F.text;
     const int64_t R = int64_t(F.B) * F.N;
     HIPCHECK(launch_f5_fill_x(F.x, F.N, F.mel, F.cat, W, F.B, s));
-    for (int i = 0; i < F.depth; ++i) {  // the six modulation vectors of every block (f5.cpp:673)
-        const GpuMat &Ma = mat_at(F.blocks[size_t(i)].ada);
-        gemv(Ma, 1, PRO_X, EPI_STORE, F.ts, D, 1, F.ada + size_t(i) * 6 * D, 6 * D, nullptr, 0.f, nullptr, s);
+    if (F.ada_all >= 0) {  // the six modulation vectors of every block (f5.cpp:673) and the final (scale, shift)
+        const GpuMat &Ma = mat_at(F.ada_all);
+        gemv(Ma, 1, PRO_X, EPI_STORE, F.ts, D, 1, F.ada, Ma.rows, nullptr, 0.f, nullptr, s);
+    } else {
+        for (int i = 0; i < F.depth; ++i) {
+            const GpuMat &Ma = mat_at(F.blocks[size_t(i)].ada);
+            gemv(Ma, 1, PRO_X, EPI_STORE, F.ts, D, 1, F.ada + size_t(i) * 6 * D, 6 * D, nullptr, 0.f, nullptr, s);
+        }
+        gemv(mat_at(F.norm_out), 1, PRO_X, EPI_STORE, F.ts, D, 1, F.fin, 2 * D, nullptr, 0.f, nullptr, s);
     }
-    gemv(mat_at(F.norm_out), 1, PRO_X, EPI_STORE, F.ts, D, 1, F.fin, 2 * D, nullptr, 0.f, nullptr, s);
     const GpuMat &Mi = mat_at(F.in_proj);
     f5_gemm(Mi, EPI_STORE, F.cat, gemm_args(Mi, Mi.b, F.h, W, D, R), s);
     // convolutional position embedding: h += mish(conv2(mish(conv1(h)))) per batch (f5.cpp:589-598)
@@ -2462,6 +2470,14 @@ int voxhip_f5_create(const voxhip_f5_desc *d) {
             fb.o = pad_head_cols(b.o, d->heads, d->dim_head, kF5HeadDim);
             F->blocks.push_back(fb);
         }
+        try {  // one modulation GEMV per step; when the matrices differ in type (or VRAM is short) one per block
+            std::vector<int> ids;
+            for (int i = 0; i < d->depth; ++i) ids.push_back(d->blocks[i].ada);
+            ids.push_back(d->norm_out);
+            F->ada_all = stack_rows(ids);
+        } catch (const Fail &) {
+            F->ada_all = -1;
+        }
         F->split = D % 64 == 0 && FF % 64 == 0;  // the attention width (heads x 64) always is
         for (const F5Block &fb : F->blocks)
             for (int id : {fb.qkv, fb.o, fb.ff1, fb.ff2}) F->split = F->split && mat_at(id).type == VOXHIP_F16;
@@ -2519,8 +2535,9 @@ int voxhip_f5_begin(int id, int B, int N, const float *cat0, const float *rope) 
         F.lo_off = int64_t(R * 2 * INNER) + int64_t(B) * int64_t(INNER) * F.ldvt;
         F.qkv16 = dalloc_t<_Float16>(size_t(2 * F.lo_off));
         HIPCHECK(hipMemset(F.qkv16, 0, size_t(2 * F.lo_off) * sizeof(_Float16)));  // the v^T padding stays zero
-        F.ada = dalloc_t<float>(size_t(F.depth) * 6 * D);
-        F.fin = dalloc_t<float>(2 * D); F.ts = dalloc_t<float>(D); F.x = dalloc_t<float>(size_t(N) * F.mel);
+        F.ada = dalloc_t<float>((size_t(F.depth) * 6 + 2) * D);  // the blocks' vectors, then fin: one GEMV's rows
+        F.fin = F.ada + size_t(F.depth) * 6 * D;
+        F.ts = dalloc_t<float>(D); F.x = dalloc_t<float>(size_t(N) * F.mel);
         F.out = dalloc_t<float>(R * size_t(F.mel)); F.rope = dalloc_t<float>(size_t(N) * size_t(F.hd));
         h2d(F.cat, cat0, R * W * 4);
         h2d(F.rope, rope, size_t(N) * size_t(F.hd) * 4);
@@ -3128,7 +3145,8 @@ const char *mat_user(int mat) {
                 if (L.qkv == mat || L.o == mat || L.gu == mat || L.down == mat) return "a transformer";
     for (const F5 *F : g.f5) {
         if (!F) continue;
-        if (F->in_proj == mat || F->norm_out == mat || F->proj_out == mat || F->v_head == mat) return "an F5 model";
+        if (F->in_proj == mat || F->norm_out == mat || F->proj_out == mat || F->v_head == mat || F->ada_all == mat)
+            return "an F5 model";
         for (const F5Block &b : F->blocks)
             if (b.ada == mat || b.qkv == mat || b.o == mat || b.ff1 == mat || b.ff2 == mat) return "an F5 model";
         for (const F5VBlock &b : F->vblocks)
