@@ -10,7 +10,8 @@ hipError_t launch_norm_rows(const NormArgs &a0, hipStream_t s) {
     if (a.R <= 0) return hipSuccess;
     if (a.D <= 0 || a.D % 4 || !a.x || (!a.y && !a.y16) || a.lo_off % 4 || !a.sc || (!a.affine && !a.sh) || !(a.eps > 0.0))
         return hipErrorInvalidValue;
-    return launch(k_f5_modulate, dim3(unsigned((a.R + 3) / 4)), dim3(256), 0, s, a);
+    if (a.D <= 4 * 256) return launch(k_f5_modulate<4, true>, dim3(unsigned((a.R + 3) / 4)), dim3(256), 0, s, a);
+    return launch(k_f5_modulate<kNormRegChunks, false>, dim3(unsigned((a.R + 3) / 4)), dim3(256), 0, s, a);
 }
 
 hipError_t launch_f5_modulate(const float *x, int64_t R, int D, const float *sc, const float *sh, float *y, _Float16 *y16,

@@ -23,8 +23,13 @@ VH_DEV float mish_nn_f(float x) {
 // and bias (kernels.cpp:714-723 and nn.cpp:248-265, which compute alike), y = (x - float(mean)) * inv * w + b; then
 // mish and a per-channel bias when asked (the estimator's CausalBlock1D and its time bias, cosyvoice.cpp:155-178).
 // D % 4 == 0.
-constexpr int kNormRegChunks = 8;  // rows up to 8 x 256 = 2048 values stay in registers between the passes
+// NC chunks of 4 columns per lane stay in registers between the passes (NC = 8: rows up to 2048 values, longer rows
+// are read again); PRE (rows of at most 4 x 256 = 1024 values): the row's parameters (scale, shift, time bias) are
+// loaded with the row, before the statistics, instead of one more round trip after them; the arithmetic is the same.
+constexpr int kNormRegChunks = 8;
+template <int NC, bool PRE>
 __global__ __launch_bounds__(256) void k_f5_modulate(NormArgs a) {
+    static_assert(!PRE || NC <= 4, "parameters in registers only for short rows");
     const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= a.R) return;
     const int D = a.D;
@@ -34,18 +39,30 @@ __global__ __launch_bounds__(256) void k_f5_modulate(NormArgs a) {
         for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
         return v;
     };
-    // the row is read once: chunk c of this lane is columns 4 lane + 256 c .. + 3; the first kNormRegChunks chunks
-    // stay in registers (fully unrolled loops), columns beyond 2048 are read again from memory
-    f32x4a reg[kNormRegChunks];
+    // the row is read once: chunk c of this lane is columns 4 lane + 256 c .. + 3; the first NC chunks stay in
+    // registers (fully unrolled loops), columns beyond 256 NC are read again from memory
+    f32x4a reg[NC];
 #pragma unroll
-    for (int c = 0; c < kNormRegChunks; ++c) {
+    for (int c = 0; c < NC; ++c) {
         const int i = 4 * lane + 256 * c;
         reg[c] = i < D ? *reinterpret_cast<const f32x4a *>(xr + i) : f32x4a{0.f, 0.f, 0.f, 0.f};
     }
-    const int tail0 = 256 * kNormRegChunks;
+    // PRE: the parameters of this lane's chunks (shift / time bias read from the scale row when absent, never used)
+    f32x4a pcs[PRE ? NC : 1], psh[PRE ? NC : 1], ptb[PRE ? NC : 1];
+    if constexpr (PRE) {
+        const float *shp = a.sh ? a.sh : a.sc, *tbp = a.tb ? a.tb : a.sc;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int i = 4 * lane + 256 * c < D ? 4 * lane + 256 * c : 0;
+            pcs[c] = *reinterpret_cast<const f32x4a *>(a.sc + i);
+            psh[c] = *reinterpret_cast<const f32x4a *>(shp + i);
+            ptb[c] = *reinterpret_cast<const f32x4a *>(tbp + i);
+        }
+    }
+    const int tail0 = 256 * NC;
     double s = 0.0;
 #pragma unroll
-    for (int c = 0; c < kNormRegChunks; ++c)
+    for (int c = 0; c < NC; ++c)
         s += double(reg[c][0]) + double(reg[c][1]) + double(reg[c][2]) + double(reg[c][3]);  // zeros past D
     for (int i = tail0 + 4 * lane; i < D; i += 256) {
         const f32x4a v = *reinterpret_cast<const f32x4a *>(xr + i);
@@ -54,7 +71,7 @@ __global__ __launch_bounds__(256) void k_f5_modulate(NormArgs a) {
     const double mean = wsum(s) / D;
     double q = 0.0;
 #pragma unroll
-    for (int c = 0; c < kNormRegChunks; ++c) {
+    for (int c = 0; c < NC; ++c) {
         if (4 * lane + 256 * c >= D) continue;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -72,18 +89,15 @@ __global__ __launch_bounds__(256) void k_f5_modulate(NormArgs a) {
     }
     const double var = wsum(q) / D;
     const float inv = float(1.0 / sqrt(var + a.eps)), fm = float(mean);
-    auto emit = [&](int i, const f32x4a &v) {
-        const f32x4a cs = *reinterpret_cast<const f32x4a *>(a.sc + i);
-        const f32x4a t = a.sh ? *reinterpret_cast<const f32x4a *>(a.sh + i) : f32x4a{0.f, 0.f, 0.f, 0.f};
+    auto emit = [&](int i, const f32x4a &v, const f32x4a &cs, const f32x4a &t, const f32x4a &b) {
         f32x4a r;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = (v[e] - fm) * inv * (a.affine ? cs[e] : 1.0f + cs[e]) + t[e];
+        for (int e = 0; e < 4; ++e) r[e] = (v[e] - fm) * inv * (a.affine ? cs[e] : 1.0f + cs[e]) + (a.sh ? t[e] : 0.f);
         if (a.mish) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) r[e] = mish_nn_f(r[e]);
         }
         if (a.tb) {
-            const f32x4a b = *reinterpret_cast<const f32x4a *>(a.tb + i);
 #pragma unroll
             for (int e = 0; e < 4; ++e) r[e] += b[e];
         }
@@ -105,10 +119,19 @@ __global__ __launch_bounds__(256) void k_f5_modulate(NormArgs a) {
             *reinterpret_cast<f32x4a *>(a.y + int64_t(row) * D + i) = r;
         }
     };
+    auto emit_load = [&](int i, const f32x4a &v) {  // the parameters read here, after the statistics
+        const f32x4a cs = *reinterpret_cast<const f32x4a *>(a.sc + i);
+        const f32x4a t = a.sh ? *reinterpret_cast<const f32x4a *>(a.sh + i) : f32x4a{0.f, 0.f, 0.f, 0.f};
+        const f32x4a b = a.tb ? *reinterpret_cast<const f32x4a *>(a.tb + i) : f32x4a{0.f, 0.f, 0.f, 0.f};
+        emit(i, v, cs, t, b);
+    };
 #pragma unroll
-    for (int c = 0; c < kNormRegChunks; ++c)
-        if (4 * lane + 256 * c < D) emit(4 * lane + 256 * c, reg[c]);
-    for (int i = tail0 + 4 * lane; i < D; i += 256) emit(i, *reinterpret_cast<const f32x4a *>(xr + i));
+    for (int c = 0; c < NC; ++c) {
+        if (4 * lane + 256 * c >= D) continue;
+        if constexpr (PRE) emit(4 * lane + 256 * c, reg[c], pcs[c], psh[c], ptb[c]);
+        else emit_load(4 * lane + 256 * c, reg[c]);
+    }
+    for (int i = tail0 + 4 * lane; i < D; i += 256) emit_load(i, *reinterpret_cast<const f32x4a *>(xr + i));
 }
 
 // Depthwise "same" Conv1d (f5_ops.cpp:106-147 with groups = channels: the Vocos blocks' dwconv, f5.cpp:341) over
