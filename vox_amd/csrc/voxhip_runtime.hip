@@ -2199,6 +2199,18 @@ F5 &f5_at(int id) {
 }
 
 // Stacks matrices of one type and width by rows into a new device matrix (biases zero where a part has none).
+// A matrix made by a helper below, freed again when a later step of the helper throws.
+struct NewMatGuard {
+    int id;
+    ~NewMatGuard() {
+        if (id >= 0) free_mat(id);
+    }
+    int release() {
+        const int r = id;
+        id = -1;
+        return r;
+    }
+};
 int stack_rows(const std::vector<int> &ids) {
     const GpuMat m0 = mat_at(ids[0]);
     int64_t rows = 0;
@@ -2210,6 +2222,7 @@ int stack_rows(const std::vector<int> &ids) {
         any_bias = any_bias || m.b;
     }
     const int nid = new_mat(m0.type, rows, m0.cols, any_bias, m0.s16);
+    NewMatGuard keep{nid};
     for (int id : ids) g.mats[size_t(nid)].wmax = std::max(g.mats[size_t(nid)].wmax, mat_at(id).wmax,
                                                           [](float a, float b) { return a < b || std::isnan(b); });
     const GpuMat dst = g.mats[size_t(nid)];
@@ -2225,7 +2238,7 @@ int stack_rows(const std::vector<int> &ids) {
         }
         r0 += src.rows;
     }
-    return nid;
+    return keep.release();
 }
 
 // Heads of hd < kF5HeadDim in the F5 / flow-estimator attention, whose tiles hold kF5HeadDim dims a head (the
@@ -2245,6 +2258,7 @@ int stack_rows_heads(const std::vector<int> &ids, int heads, int hd, int hp) {
     }
     const int64_t rows = int64_t(ids.size()) * heads * hp;
     const int nid = new_mat(m0.type, rows, m0.cols, any_bias, m0.s16);
+    NewMatGuard keep{nid};
     const GpuMat dst = g.mats[size_t(nid)];
     const size_t rb = row_bytes(m0.type, m0.cols), sb = scale_row_bytes(m0);
     HIPCHECK(hipMemset(dst.w, 0, size_t(rows) * rb));
@@ -2265,7 +2279,7 @@ int stack_rows_heads(const std::vector<int> &ids, int heads, int hd, int hp) {
         wmax = std::max(wmax, src.wmax, [](float a, float b) { return a < b || std::isnan(b); });
     }
     g.mats[size_t(nid)].wmax = wmax;
-    return nid;
+    return keep.release();
 }
 // The to_out side of stack_rows_heads: a copy of m [rows][heads hd] as [rows][heads hp], each head's hd columns
 // followed by hp - hd zero columns. Q8 needs hd a multiple of 32 (whole scale blocks); Q4 is not taken.
@@ -2283,6 +2297,7 @@ int pad_head_cols(int id, int heads, int hd, int hp) {
     if (src.type == VOXHIP_Q8 && hd % 32) throw Fail("q8 attention weights need head_dim a multiple of 32 below 64");
     const int64_t cols = int64_t(heads) * hp;
     const int nid = new_mat(src.type, src.rows, cols, src.b != nullptr);
+    NewMatGuard keep{nid};
     const GpuMat dst = g.mats[size_t(nid)];
     const size_t rows = size_t(src.rows);
     HIPCHECK(hipMemset(dst.w, 0, rows * size_t(cols) * size_t(es)));
@@ -2295,7 +2310,7 @@ int pad_head_cols(int id, int heads, int hd, int hp) {
     }
     if (src.b) HIPCHECK(hipMemcpy(dst.b, src.b, rows * 4, hipMemcpyDeviceToDevice));
     g.mats[size_t(nid)].wmax = src.wmax;
-    return nid;
+    return keep.release();
 }
 
 // A "same" Conv1d for the implicit-im2col GEMM: Conv1d::w rows [K][cin/groups] (f5_ops.cpp:86-104) padded with zero
