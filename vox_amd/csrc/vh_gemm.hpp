@@ -700,12 +700,10 @@ __global__ __launch_bounds__(256) void k_gemm_h16b(const uint8_t *__restrict__ w
 // row of A and of W, so rows past m or n read as zeros without a per-load bounds check, and the K offset of a step
 // is the scalar offset. Two K steps are in flight (two register sets alternate), so a load has two steps' MFMAs to
 // arrive. g.kchunk: slice blockIdx.z of K (a multiple of BK) as partial sums into g.ws (k_gemm_splitk_reduce).
-// The q8 instances hold the accumulators in VGPRs for the scale FMA, and each tile's block product in registers of
-// its own until the scale step: 3 waves per SIMD (at 4, 128 VGPRs, every tile's MFMA pair and scale FMAs shared one
-// register set, so each MFMA waited for the VALU reads of the previous tile's product).
-// D register sets of K steps in flight: 2 (3 and 4 measured no faster on the prefill and DiT shapes).
-template <int EPI, int TM, int TN, int BK, bool Q8 = false, int WN = 2, int D = 2>
-__global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(Q8 ? 3 : 1))) void k_gemm_hh(const _Float16 *__restrict__ w, const float *__restrict__ scale, GemmArgs g) {
+template <int EPI, int TM, int TN, int BK, bool Q8 = false, int WN = 2>
+// The q8 instances hold the accumulators in VGPRs for the scale FMA; asking for 4 waves per SIMD (128 VGPRs, a
+// register or two spilled) measured faster on the prefill shapes than the 3 their unconstrained 165 registers allow.
+__global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(Q8 ? 4 : 1))) void k_gemm_hh(const _Float16 *__restrict__ w, const float *__restrict__ scale, GemmArgs g) {
     // 2 x WN waves of 16 TM x 16 TN outputs each (WN = 2: 64 x 64 tiles for TM = TN = 2, 256 threads; WN = 4: 64 x 128,
     // 512 threads, so each block's A tile serves twice the columns)
     constexpr int NT = 128 * WN, LD = BK + 16, BM = 32 * TM, BN = 16 * TN * WN, CPR = BK / 8, RS = NT / CPR, AQ = BM / RS,
@@ -739,8 +737,8 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(Q8 ? 3
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
-    u32x4 xa[D][2 * AQ], xw[D][WQ];
-    float xs[D];
+    u32x4 xa0[2 * AQ], xw0[WQ], xa1[2 * AQ], xw1[WQ];
+    float xs0 = 0.f, xs1 = 0.f;
     auto fetch = [&](u32x4(&a)[2 * AQ], u32x4(&b)[WQ], float &sc, int k0) {
         const int so = k0 * 2;
 #pragma unroll
@@ -779,22 +777,16 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(Q8 ? 3
                 float sc[TN];  // the block scale of this lane's W row (its C column)
 #pragma unroll
                 for (int j = 0; j < TN; ++j) sc[j] = Ss[wn * 16 * TN + j * 16 + (lane & 15)][kk / 32];
-                // every tile's block product first (independent MFMA pairs, one register set each), then the scale
-                // step, so no MFMA waits for a VALU read of the previous tile's product
-                f32x4v tt[TM][TN];
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
                     for (int j = 0; j < TN; ++j) {
-                        tt[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], f32x4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                        tt[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], tt[i][j], 0, 0, 0);
+                        f32x4v tt = {0.f, 0.f, 0.f, 0.f};
+                        tt = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b[j], tt, 0, 0, 0);
+                        tt = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], tt, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[i][j][v] = fmaf(tt[v], sc[j], acc[i][j][v]);
                     }
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < TN; ++j)
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) acc[i][j][v] = fmaf(tt[i][j][v], sc[j], acc[i][j][v]);
             } else {
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
@@ -806,34 +798,28 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(Q8 ? 3
             }
         }
     };
-    // D register sets of K steps in flight. Every fetch is unconditional (steps past the end re-read the last one),
-    // so the compiler's count of loads in flight is exact: staging one set waits only for that set, the other D - 1
-    // stay in flight.
+    // Every fetch is unconditional (steps past the end re-read the last one), so the compiler's count of loads in
+    // flight is exact: staging one set waits only for that set, the other stays in flight.
     const int ns = (kend - kbeg) / BK, klast = kend - BK;
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        fetch(xa[d], xw[d], xs[d], min(kbeg + d * BK, klast));
-        __builtin_amdgcn_sched_barrier(0);  // keep each set's loads ahead of the next one's
+    fetch(xa0, xw0, xs0, kbeg);
+    __builtin_amdgcn_sched_barrier(0);  // keep the first set's loads ahead of the second's
+    fetch(xa1, xw1, xs1, min(kbeg + BK, klast));
+    for (int s = 0; s + 1 < ns; s += 2) {  // one back edge: the first set is always the older in flight
+        stage(xa0, xw0, xs0);
+        __syncthreads();
+        fetch(xa0, xw0, xs0, min(kbeg + (s + 2) * BK, klast));
+        mma();
+        __syncthreads();
+        stage(xa1, xw1, xs1);
+        __syncthreads();
+        fetch(xa1, xw1, xs1, min(kbeg + (s + 3) * BK, klast));
+        mma();
+        __syncthreads();
     }
-    int s = 0;
-    for (; s + D <= ns; s += D) {  // one back edge per D steps: set d is always the oldest in flight at its turn
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            stage(xa[d], xw[d], xs[d]);
-            __syncthreads();
-            fetch(xa[d], xw[d], xs[d], min(kbeg + (s + d + D) * BK, klast));
-            mma();
-            __syncthreads();
-        }
-    }
-#pragma unroll
-    for (int d = 0; d + 1 < D; ++d) {  // the last ns % D steps, in sets 0 ..
-        if (s + d < ns) {
-            stage(xa[d], xw[d], xs[d]);
-            __syncthreads();
-            mma();
-            __syncthreads();
-        }
+    if (ns & 1) {  // the last step, in the first set
+        stage(xa0, xw0, xs0);
+        __syncthreads();
+        mma();
     }
     if (g.kchunk) return gemm_store_partial<TM, TN>(acc, g, m0, n0, wm, wn, lane);
     gemm_epilogue<EPI, TM, TN>(acc, g, m0, n0, wm, wn, lane);
