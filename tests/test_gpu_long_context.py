@@ -69,3 +69,16 @@ def test_sessions_at_long_positions(hip, oracle, dec):
     for b in (0, 2, 6):
         o1, _ = hip.forward(dec.xfmr, seqs[b], positions[b], x[b:b + 1], H)
         assert rel_err(o1, outs[b]) < 1e-3, (b, rel_err(o1, outs[b]))
+
+
+def test_prefill_rows_after_long_context(hip, oracle, dec):
+    # 300 rows at positions 7800 .. 8099 in one pass: the prefill attention's key runs span ~8K keys per query tile
+    c = dec.cfg
+    oracle.lib().vo_set_threads(8)
+    pos0, m = 7800, 300
+    s = dec.extra_seq(0xBEEF)
+    X, (kv,), _ = to_oracle(oracle, hip, dec, seqs=[s], kv_len=pos0, cap=pos0 + m + 8)
+    x = np.random.default_rng(6).standard_normal((m, c["hidden"])).astype(np.float32)
+    out, _ = hip.forward(dec.xfmr, s, pos0, x, c["hidden"])
+    ref = oracle.transformer_forward(X, kv, x)
+    assert rel_err(out, ref) < 1e-3, rel_err(out, ref)
