@@ -429,3 +429,26 @@ def test_errors_are_reported(hip):
         hip.seq_create(xf, 0)
     with pytest.raises(hip.VoxHipError):
         hip.forward(xf, 999, 0, np.zeros((1, 128), np.float32), 128)
+
+
+def test_pair_graph_replayed_with_another_second_row(hip, oracle):
+    # a pair pass is captured as a graph the second time its shape is seen, keyed by the first row's cache: the same
+    # graph replayed with another second sequence must read that sequence's keys (its attention takes every row's
+    # cache view from the device row table), so both rows agree with the oracle
+    mdl = Model(601, 2, 256, 4, 2, 128, 512, wtype=Q8)
+    xf, _ = build(hip, mdl)
+    rng = np.random.default_rng(10)
+    seqs = [hip.seq_create(xf, 32) for _ in range(3)]
+    kvs = [mdl.oracle_kv(32, 1) for _ in range(3)]
+    for s, k in zip(seqs, kvs):
+        pre = rng.standard_normal((6, 256)).astype(np.float32)
+        hip.forward(xf, s, 0, pre, 256)
+        oracle.transformer_forward(mdl.ox, k, pre)
+    for pos, (a, b) in zip((6, 7, 8, 9), ((0, 1), (0, 1), (0, 2), (0, 2))):
+        x2 = rng.standard_normal((2, 256)).astype(np.float32)
+        out2, _ = hip.forward_pair(xf, seqs[a], seqs[b], pos, x2, 256)
+        for row, sq in enumerate((a, b)):
+            kv = kvs[sq]
+            kv.c.len = pos  # the oracle appends at pos, as the device did
+            r = oracle.transformer_forward(mdl.ox, kv, x2[row:row + 1])
+            assert rel_err(out2[row], r) < TOL, (pos, a, b, row, rel_err(out2[row], r))
