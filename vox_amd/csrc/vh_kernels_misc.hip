@@ -207,8 +207,10 @@ static hipError_t attn_hg(const AttnArgs &a, const AttnLaunch &l, int m, bool fu
 
 // Query heads per block: the whole group, or, when a launch has few blocks (few kv heads, few rows), the largest
 // divisor of the group that gives at least kAttnMinBlocks blocks (more blocks share the work; each reads its kv
-// head's keys, so a split multiplies the key reads by group / G).
-constexpr int kAttnMinBlocks = 128;
+// head's keys, so a split multiplies the key reads by group / G). The attention is latency-bound: at 8 sessions of
+// the 1.7B talker (8 kv heads, group 2), one head per block (1024 blocks, twice the key reads) measured 1.586-1.590 ->
+// 1.564-1.572 ms per step against two (512 blocks); one-row launches had one head per block already.
+constexpr int kAttnMinBlocks = 1024;
 static int attn_heads_per_block(int kv_heads, int group, int m) {
     int gb = group;
     while (gb > 1 && int64_t(m) * kv_heads * (group / gb) * kAttnMaxSplits < kAttnMinBlocks) {
