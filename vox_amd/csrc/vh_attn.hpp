@@ -144,8 +144,10 @@ struct AttnSmem {
 // them, or a subgroup when there are few kv heads, so that more blocks share the work). Each lane holds 8 consecutive elements of one key row;
 // LPK = HD / 8 lanes share a key, a wave covers 64 / LPK keys per step, a block NGRP keys. Split s takes the keys
 // j = s + S (grp + NGRP u). Row 0's cache bases, the q|k|v input and the RoPE rows are leading scalar arguments
-// (preloaded with the dispatch): the first kAttnSpecKeys keys' loads go out before the row's position arrives and
-// are masked by it afterwards, so the cache fetch does not wait for the row view. Later keys load per batch of U.
+// (preloaded with the dispatch): the first batch's loads go out before the row's position arrives and are masked by
+// it afterwards, so the cache fetch does not wait for the row view. The first batch is kAttnSpecKeys keys in a
+// launch of one row and U groups (S NGRP U keys) in a launch of several, whose blocks have less to hide the
+// dependent round trip behind; later keys load per batch of U.
 // ONE_ROW (launches of one row, m == 1): only row 0's path is compiled, so the compiler's wait counts follow one
 // static load sequence.
 template <int HD, int G, bool FUSED, bool ONE_ROW = false>
@@ -154,7 +156,9 @@ __global__ __launch_bounds__(256) void k_attn(const _Float16 *kc0, const _Float1
     using Sm = AttnSmem<HD, G>;
     constexpr int LPK = Sm::LPK, KPW = Sm::KPW, NGRP = Sm::NGRP, HALF = HD / 2, S = kAttnMaxSplits;
     constexpr int U = G <= 2 ? 8 : G <= 4 ? 4 : 2;
-    constexpr int U1 = kAttnSpecKeys / (S * NGRP) < U ? kAttnSpecKeys / (S * NGRP) : U;  // speculative batch
+    // groups in the first batch: U1S (kAttnSpecKeys keys) for one row, U for several
+    constexpr int U1S = kAttnSpecKeys / (S * NGRP) < U ? kAttnSpecKeys / (S * NGRP) : U;
+    constexpr int U1 = ONE_ROW ? U1S : U;
     constexpr int NQ = (G * HALF + 255) / 256;  // q rotate-half pairs per thread
     extern __shared__ __align__(16) uint8_t attn_smem[];
     Sm &sm = *reinterpret_cast<Sm *>(attn_smem);
@@ -330,17 +334,49 @@ __global__ __launch_bounds__(256) void k_attn(const _Float16 *kc0, const _Float1
             for (int e = 0; e < 8; ++e) acc[h][e] = o[e];
         }
     };
-    {  // the speculative batch, masked by the row's length
+    // Keys are consumed (one online-softmax update per batch) in the batches of a one-row launch: groups [0, U1S),
+    // then [U1S + k U, U1S + (k + 1) U). Launches of several rows load U groups first, one round trip for up to
+    // S NGRP U keys, and consume the same batches, so one and several rows sum in the same order.
+    int64_t jb0 = s + int64_t(S) * (grp + NGRP * U1S);  // first group of the next batch to load
+    {
         bool valid[U1];
 #pragma unroll
         for (int u = 0; u < U1; ++u) {
             valid[u] = s + int64_t(S) * (grp + NGRP * u) < kend;
             if (!valid[u]) kb[u] = vb[u] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};  // masked: finite zeros, weight 0
         }
-        consume(std::integral_constant<int, U1>(), kb, vb, valid);
+        consume(std::integral_constant<int, U1S>(), kb, vb, valid);
+        if constexpr (U1 > U1S) {
+            // groups [U1S, U) are in registers: the head of batch [U1S, U1S + U). Without keys past them in this
+            // block (block-uniform) that batch is those groups alone (masked groups leave the softmax state as it
+            // is); otherwise its other U1S groups are loaded now.
+            if (s + int64_t(S) * NGRP * U < kend) {
+                bool v2[U];
+#pragma unroll
+                for (int u = 0; u < U - U1S; ++u) {
+                    kb[u] = kb[u + U1S];
+                    vb[u] = vb[u + U1S];
+                    v2[u] = valid[u + U1S];
+                }
+#pragma unroll
+                for (int u = U - U1S; u < U; ++u) {
+                    const int64_t j = jb0 + int64_t(S) * NGRP * u;
+                    v2[u] = j < kend;
+                    if (v2[u]) {
+                        kb[u] = ld_cache8(K + j * HD + sub * 8);
+                        vb[u] = ld_cache8(V + j * HD + sub * 8);
+                    } else {
+                        kb[u] = vb[u] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+                    }
+                }
+                consume(std::integral_constant<int, U>(), kb, vb, v2);
+            } else {
+                consume(std::integral_constant<int, U - U1S>(), kb + U1S, vb + U1S, valid + U1S);
+            }
+            jb0 += int64_t(S) * NGRP * U;
+        }
     }
-    // keys past the speculative batch, U groups of NGRP per batch
-    for (int64_t jb = s + int64_t(S) * (grp + NGRP * U1); jb < kend; jb += int64_t(S) * NGRP * U) {
+    for (int64_t jb = jb0; jb < kend; jb += int64_t(S) * NGRP * U) {
         bool valid[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
