@@ -384,12 +384,16 @@ VH_DEV void reduce_store_prep(float (&acc)[R][M], float &out, int lane) {
 // (8 rows of K 6144), otherwise the shallow one (8 rows of K 2048), so no lane issues loads it does not use.
 constexpr int kQStageChunks = 12, kQStageScales = 6, kQStageChunksLo = 4, kQStageScalesLo = 2;
 // ACC (one row): the input or the residual carries pending FFN sums (GemvArgs::acc).
-template <int WT, int M, int R, int IT, int PRO, int EPI, bool STAGE, bool ACC = false>
+// NT: threads per block (more than kGemvThreads only for pre-quantized rows: EPI_SWIGLU_Q takes 1024, so that one
+// block holds the 64 interleaved gate|up rows of 32 SwiGLU outputs, one quantization block of the next pass).
+template <int WT, int M, int R, int IT, int PRO, int EPI, bool STAGE, bool ACC = false, int NT = kGemvThreads>
 // The weight stream's operands come first so they are preloaded into SGPRs with the dispatch (kernarg preload).
-__global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__restrict__ w, const float *__restrict__ scale,
-                                                       const float *x, int32_t rows, int32_t K, GemvArgs a) {
+__global__ __launch_bounds__(NT) void k_gemv_int(const uint8_t *__restrict__ w, const float *__restrict__ scale,
+                                                 const float *x, int32_t rows, int32_t K, GemvArgs a) {
     static_assert(WT == WT_Q8 || WT == WT_Q4 || WT == WT_Q4H, "int path is Q8/Q4");
     static_assert(!ACC || (M == 1 && STAGE && (PRO == PRO_RMS || EPI == EPI_ACC)), "pending sums: one staged row");
+    static_assert(NT == kGemvThreads || PRO == PRO_Q, "wider blocks take pre-quantized rows");
+    static_assert(EPI != EPI_SWIGLU_Q || (PRO == PRO_Q && (NT / 64) * R == 64), "a block holds one output block");
     extern __shared__ __align__(16) uint8_t smem[];
     const int nb = K / 32;
     int8_t *xq = reinterpret_cast<int8_t *>(smem);                 // [M][K]
@@ -397,7 +401,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__rest
     float *red = xs + M * nb;                                      // [M][4]
     int *xsum = reinterpret_cast<int *>(red + M * 4);              // Q4: [M][nb] sums of the quantized blocks
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * (kGemvThreads / 64) + wave) * R;
+    const int row0 = (blockIdx.x * (NT / 64) + wave) * R;
     constexpr int EPC = WT == WT_Q8 ? 16 : 32;  // weight elements per 16-byte chunk
     const int nchunk = K / EPC;
     const int64_t rb = row_bytes<WT>(K);
@@ -430,23 +434,23 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__rest
     // PRO_Q: the quantized rows, their scales and block sums are loaded into registers ahead of the weight stream
     // too (16-byte chunk i = threadIdx.x + 256 u), so the copy into LDS waits for one round trip that overlaps the
     // weights' instead of one per chunk after them; rows past a.m read row 0 and are stored as zeros
-    constexpr int QC = PRO != PRO_Q ? 1 : STAGE ? kQStageChunks : kQStageChunksLo;
-    constexpr int QSC = PRO != PRO_Q ? 1 : STAGE ? kQStageScales : kQStageScalesLo;
+    constexpr int QC = PRO != PRO_Q ? 1 : ((STAGE ? kQStageChunks : kQStageChunksLo) * kGemvThreads + NT - 1) / NT;
+    constexpr int QSC = PRO != PRO_Q ? 1 : ((STAGE ? kQStageScales : kQStageScalesLo) * kGemvThreads + NT - 1) / NT;
     u32x4 qv[QC];
     float qsv[QSC];
     int qzv[QSC];
     const int qn16 = M * K / 16, qns = M * nb;
-    const bool qstaged = PRO == PRO_Q && qn16 <= QC * kGemvThreads && qns <= QSC * kGemvThreads;
+    const bool qstaged = PRO == PRO_Q && qn16 <= QC * NT && qns <= QSC * NT;
     if constexpr (PRO == PRO_Q) {
         if (qstaged) {
 #pragma unroll
             for (int u = 0; u < QC; ++u) {
-                const int i = int(threadIdx.x) + u * kGemvThreads;
+                const int i = int(threadIdx.x) + u * NT;
                 qv[u] = reinterpret_cast<const u32x4 *>(a.q)[i < qn16 && i * 16 / K < a.m ? i : 0];
             }
 #pragma unroll
             for (int u = 0; u < QSC; ++u) {
-                const int i = int(threadIdx.x) + u * kGemvThreads;
+                const int i = int(threadIdx.x) + u * NT;
                 const int ii = i < qns && i / nb < a.m ? i : 0;
                 qsv[u] = a.qs[ii];
                 qzv[u] = WT != WT_Q8 ? a.qsum[ii] : 0;
@@ -481,12 +485,12 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__rest
         if (qstaged) {
 #pragma unroll
             for (int u = 0; u < QC; ++u) {
-                const int i = int(threadIdx.x) + u * kGemvThreads;
+                const int i = int(threadIdx.x) + u * NT;
                 if (i < qn16) reinterpret_cast<u32x4 *>(xq)[i] = i * 16 / K < a.m ? qv[u] : u32x4{0u, 0u, 0u, 0u};
             }
 #pragma unroll
             for (int u = 0; u < QSC; ++u) {
-                const int i = int(threadIdx.x) + u * kGemvThreads;
+                const int i = int(threadIdx.x) + u * NT;
                 if (i < qns) {
                     const bool on = i / nb < a.m;
                     xs[i] = on ? qsv[u] : 0.f;
@@ -494,9 +498,9 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__rest
                 }
             }
         } else {
-            for (int i = threadIdx.x; i < qn16; i += kGemvThreads)
+            for (int i = threadIdx.x; i < qn16; i += NT)
                 reinterpret_cast<u32x4 *>(xq)[i] = i * 16 / K < a.m ? reinterpret_cast<const u32x4 *>(a.q)[i] : u32x4{0u, 0u, 0u, 0u};
-            for (int i = threadIdx.x; i < qns; i += kGemvThreads) {
+            for (int i = threadIdx.x; i < qns; i += NT) {
                 const bool on = i / nb < a.m;
                 xs[i] = on ? a.qs[i] : 0.f;
                 if (WT != WT_Q8) xsum[i] = on ? a.qsum[i] : 0;
@@ -571,7 +575,38 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_int(const uint8_t *__rest
     }
     float out;
     reduce_store_prep<R, M>(acc, out, lane);
-    store_out<M, R, EPI, ACC>(a, rows, out, lane, row0, ep);
+    if constexpr (EPI == EPI_SWIGLU_Q) {
+        // The block's 32 SwiGLU outputs u0 .. u0 + 31 of each input row (store_out's arithmetic) into LDS, then one
+        // wave quantizes them as k_quant_rows<PRO_X> would for the next pass: the same quant_slot on the same
+        // 32-block (4 lanes of 8), so the int8 rows, scales and block sums are bit-identical.
+        float *sw = reinterpret_cast<float *>(smem + M * K + M * nb * 4 + M * 16 + (WT == WT_Q8 ? 0 : M * nb * 4));  // [M][32]
+        const int r = lane / M, mm = lane % M, row = row0 + r;
+        const bool ok = lane < R * M && row < rows && mm < a.m;
+        const float v = out + ((ok && a.bias) ? ep.b : 0.f);
+        const float other = __shfl_xor(v, M, kWave);  // lane of row r ^ 1, same input row
+        if (ok && (r & 1) == 0) sw[mm * 32 + (row - int(blockIdx.x) * 64) / 2] = silu(v) * other;
+        __syncthreads();
+        if (wave == 0) {
+            const int qm = lane >> 2, sl = lane & 3, qmc = qm < M ? qm : 0;  // input row qm, 8-element slot sl
+            float vv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vv[e] = sw[qmc * 32 + sl * 8 + e];
+            uint32_t q2[2];
+            float sc;
+            quant_slot(vv, q2, &sc);
+            const int bs = block_qsum(q2);
+            const int ko = rows / 2, nbo = ko / 32, ub = int(blockIdx.x);
+            if (qm < a.m) {
+                *reinterpret_cast<uint2 *>(a.yq + int64_t(qm) * ko + ub * 32 + sl * 8) = make_uint2(q2[0], q2[1]);
+                if (sl == 0) {
+                    a.yqs[qm * nbo + ub] = sc;
+                    a.yqsum[qm * nbo + ub] = bs;
+                }
+            }
+        }
+    } else {
+        store_out<M, R, EPI, ACC>(a, rows, out, lane, row0, ep);
+    }
 }
 
 // ------------------------------------------------------------------------------------------ f32 path

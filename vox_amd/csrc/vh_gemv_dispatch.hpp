@@ -9,15 +9,18 @@ namespace vh {
 
 template <int WT, int M, int R, int IT, int PRO, int EPI, bool INT, bool STAGE, bool ACC>
 hipError_t gemv_run_staged(const GemvArgs &a, hipStream_t s) {
-    const int per_block = (kGemvThreads / 64) * R;
-    const dim3 grid((a.rows + per_block - 1) / per_block), block(kGemvThreads);
+    constexpr int NT = EPI == EPI_SWIGLU_Q ? 1024 : kGemvThreads;
+    const int per_block = (NT / 64) * R;
+    const dim3 grid((a.rows + per_block - 1) / per_block), block(NT);
     if constexpr (INT) {
-        // xq [M][K] int8, xs [M][K/32] f32, red [M][4], xsum [M][K/32] int32 (Q4)
-        const size_t smem = size_t(M) * a.K + size_t(M) * (a.K / 32) * 4 + size_t(M) * 16 + (WT == WT_Q8 ? 0 : size_t(M) * (a.K / 32) * 4);
-        hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_gemv_int<WT, M, R, IT, PRO, EPI, STAGE, ACC>), smem);
+        // xq [M][K] int8, xs [M][K/32] f32, red [M][4], xsum [M][K/32] int32 (Q4), EPI_SWIGLU_Q's outputs [M][32] f32
+        const size_t smem = size_t(M) * a.K + size_t(M) * (a.K / 32) * 4 + size_t(M) * 16 + (WT == WT_Q8 ? 0 : size_t(M) * (a.K / 32) * 4) +
+                            (EPI == EPI_SWIGLU_Q ? size_t(M) * 32 * 4 : 0);
+        if (EPI == EPI_SWIGLU_Q && (a.rows % 64 || !a.yq || !a.yqs || !a.yqsum)) return hipErrorInvalidValue;
+        hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_gemv_int<WT, M, R, IT, PRO, EPI, STAGE, ACC, NT>), smem);
         if (e != hipSuccess) return e;
-        return launch(k_gemv_int<WT, M, R, IT, PRO, EPI, STAGE, ACC>, grid, block, smem, s, a.w, a.scale, a.x, a.rows, a.K, a);
-    } else if constexpr (ACC) {
+        return launch(k_gemv_int<WT, M, R, IT, PRO, EPI, STAGE, ACC, NT>, grid, block, smem, s, a.w, a.scale, a.x, a.rows, a.K, a);
+    } else if constexpr (ACC || EPI == EPI_SWIGLU_Q) {
         return hipErrorInvalidValue;  // pending FFN sums come with int-path layers only
     } else {
         const size_t smem = size_t(M) * a.K * 4 + size_t(M) * 16;
@@ -51,7 +54,9 @@ hipError_t gemv_by_tile(int R, int IT, const GemvArgs &a, hipStream_t s) {
 #define VH_TILE(r, it) \
     if (R == r && IT == it) return gemv_run<WT, M, r, it, PRO, EPI, INT, ACC>(a, s);
     if constexpr (PRO == PRO_Q) {  // pre-quantized rows: larger tiles, fewer copies of the rows per launch
-        if constexpr (EPI == EPI_SWIGLU) {
+        if constexpr (EPI == EPI_SWIGLU_Q) {
+            VH_TILE(4, 1)
+        } else if constexpr (EPI == EPI_SWIGLU) {
             VH_TILE(2, 1) VH_TILE(4, 1) VH_TILE(8, 1)
         } else {
             VH_TILE(2, 1) VH_TILE(4, 1) VH_TILE(8, 1) VH_TILE(2, 2) VH_TILE(2, 3)
@@ -109,6 +114,7 @@ hipError_t gemv_dispatch(int pro, int epi, int M, int R, int IT, const GemvArgs 
         if (pro == PRO_Q && epi == EPI_STORE) return gemv_by_m<WT, PRO_Q, EPI_STORE, INT>(M, R, IT, a, s);
         if (pro == PRO_Q && epi == EPI_ACC) return gemv_by_m<WT, PRO_Q, EPI_ACC, INT>(M, R, IT, a, s);
         if (pro == PRO_Q && epi == EPI_SWIGLU) return gemv_by_m<WT, PRO_Q, EPI_SWIGLU, INT>(M, R, IT, a, s);
+        if (pro == PRO_Q && epi == EPI_SWIGLU_Q) return gemv_by_m<WT, PRO_Q, EPI_SWIGLU_Q, INT>(M, R, IT, a, s);
     }
     return hipErrorInvalidValue;
 }

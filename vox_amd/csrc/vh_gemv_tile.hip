@@ -87,6 +87,7 @@ hipError_t launch_gemv(int wt, bool int_path, int pro, int epi, const GemvArgs &
     if (pro == PRO_Q) {
         if (!int_path || M < 4 || !a.q || !a.qs || !a.qsum) return hipErrorInvalidValue;
         gemv_tile_q(a.rows, nchunk, epi == EPI_SWIGLU, &R, &IT);
+        if (epi == EPI_SWIGLU_Q) R = 4, IT = 1;  // 16 waves of 4 rows: one block per 32 SwiGLU outputs
     } else {
         gemv_tile(a.rows, nchunk, M, epi == EPI_SWIGLU, &R, &IT);
     }

@@ -12,6 +12,9 @@ enum : int32_t { kStatusF16Range = 1, kStatusFixRange = 2 };
 // GEMV prologues; PRO_Q (int path only): the input rows arrive already quantized (k_quant_rows)
 enum { PRO_X = 0, PRO_RMS = 1, PRO_ATTN = 2, PRO_Q = 3 };
 enum { EPI_STORE = 0, EPI_ACC = 1, EPI_SWIGLU = 2 };
+// Int-path GEMV on pre-quantized rows (PRO_Q) only: SwiGLU, then the output rows quantized per 32-block into
+// GemvArgs::yq / yqs / yqsum for the next pass (which takes them as its PRO_Q rows) instead of stored as floats
+enum { EPI_SWIGLU_Q = 13 };
 // GEMM-only epilogues (F5 DiT, Vocos, the codec): y += gate * c; y = gelu_tanh(c); y = mish(c); y += mish(c); RoPE on
 // q|k columns; y = gelu_erf(c); y = snake(c)
 enum { EPI_GATED_ACC = 3, EPI_GELU = 4, EPI_MISH = 5, EPI_MISH_ACC = 6, EPI_ROPE = 7, EPI_ROPE_H16 = 8, EPI_GELU_H16 = 9,
@@ -62,6 +65,10 @@ struct GemvArgs {
     const int8_t *q;
     const float *qs;
     const int32_t *qsum;
+    // EPI_SWIGLU_Q: the SwiGLU output rows quantized as PRO_Q takes them, yq [m][rows/2], yqs and yqsum [m][rows/64]
+    int8_t *yq;
+    float *yqs;
+    int32_t *yqsum;
     // One-row passes after a fused FFN (k_ffn_int): the FFN's down product still pending as fixed-point sums
     // [kAccCopies][acc_ld]. PRO_RMS adds them to x before the norm; EPI_ACC adds them to y before its own product
     // (the two residual adds in the reference's order) and sets the rows it consumed to zero.

@@ -525,16 +525,50 @@ void probed(Probe *pr, int cls, F &&f) {
     if (pr) pr->after();
 }
 
+// Rows quantized per 32-block as a PRO_Q pass takes them: q [m][K] int8, qs and qsum [m][K/32].
+struct QRows {
+    int8_t *q;
+    float *qs;
+    int32_t *qsum;
+};
+
+// Whether a pass of mc rows on the int path quantizes its input rows once (k_quant_rows, then PRO_Q).
+bool quant_rows_pass(const GpuMat &m, int64_t m_total, int mc, const PassScratch &sc) {
+    return int_path(m, m_total) && mc >= kQuantRowsMin && mc <= 8 && int64_t(mc) * m.cols <= sc.q_elems;
+}
+
+// The FFN of mc rows on the int path with the SwiGLU output quantized in gate|up's epilogue (EPI_SWIGLU_Q): when
+// both passes take pre-quantized rows and the scratch holds gate|up's input rows and the down pass's side by side,
+// the down pass's rows (returned in *out, after gate|up's) need no k_quant_rows launch of their own.
+// VOXHIP_FFN_QEPI=0 keeps the two quantizations apart (k_quant_rows before the down pass); the rows are the same.
+bool ffn_quant_epilogue(const GpuMat &gu, const GpuMat &dn, int64_t m_total, int mc, const PassScratch &sc, QRows *out) {
+    const char *e = std::getenv("VOXHIP_FFN_QEPI");
+    if (e && e[0] == '0') return false;
+    if (!quant_rows_pass(gu, m_total, mc, sc) || !quant_rows_pass(dn, m_total, mc, sc) || gemm_path(gu, m_total, mc) ||
+        gemm_path(dn, m_total, mc))
+        return false;
+    if (gu.rows % 64 || gu.rows / 2 != dn.cols || dn.cols % 32) return false;
+    const int64_t oq = (int64_t(mc) * gu.cols + 255) / 256 * 256, os = (int64_t(mc) * (gu.cols / 32) + 63) / 64 * 64;
+    if (oq + int64_t(mc) * dn.cols > sc.q_elems || os + int64_t(mc) * (dn.cols / 32) > sc.q_elems / 32) return false;
+    *out = {sc.q + oq, sc.qs + os, sc.qsum + os};
+    return true;
+}
+
 // One matrix pass: y (=, +=, swiglu) W * prologue(x) for mc rows. On the GEMM path the prologue runs as its own
 // kernel into pre ([mc][cols]; xnorm instead when the normed rows are wanted). sc: the pass's scratch (null: the
 // library's).
 // acc (one row on the int path): the fused FFN's pending sums, added to x (PRO_RMS) or to y before the product
 // (EPI_ACC, which also clears the rows it consumed).
+// qout (EPI_SWIGLU on pre-quantized rows): the SwiGLU output goes to these quantized rows instead of y; qin (PRO_X):
+// the input rows arrive quantized there (ffn_quant_epilogue's pair of passes).
 void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, int64_t ldx, int mc, float *y, int64_t ldy,
           const float *gamma, float eps, float *xnorm, hipStream_t s, const AttnPartials *attn = nullptr,
           float *pre = nullptr, const PassScratch *scp = nullptr, int64_t *acc = nullptr, const float *res = nullptr,
-          const float *yscale = nullptr) {
+          const float *yscale = nullptr, const QRows *qout = nullptr, const QRows *qin = nullptr) {
     const PassScratch sc = scp ? *scp : lib_scratch();
+    if ((qout || qin) && (!quant_rows_pass(m, m_total, mc, sc) || gemm_path(m, m_total, mc) || acc || res || yscale || xnorm ||
+                          (qout && (pro != PRO_RMS && pro != PRO_X)) || (qout && epi != EPI_SWIGLU) || (qin && pro != PRO_X)))
+        throw Fail("quantized rows on a pass that cannot take them");
     if (acc && (mc != 1 || !int_path(m, m_total) || !(pro == PRO_RMS || epi == EPI_ACC)))
         throw Fail("pending FFN sums on a pass that cannot take them");
     if (res && (epi != EPI_ACC || gemm_path(m, m_total, mc))) throw Fail("separate residual on a pass that cannot take it");
@@ -571,12 +605,21 @@ void gemv(const GpuMat &m, int64_t m_total, int pro, int epi, const float *x, in
     a.res = res;
     a.yscale = yscale;
     const bool ip = int_path(m, m_total);
-    if (ip && mc >= kQuantRowsMin && mc <= 8 && int64_t(mc) * m.cols <= sc.q_elems &&
-        (epi == EPI_STORE || epi == EPI_ACC || epi == EPI_SWIGLU)) {
+    if (qin) {  // the rows were quantized by the previous pass's epilogue
+        a.q = qin->q; a.qs = qin->qs; a.qsum = qin->qsum;
+        HIPCHECK(launch_gemv(gemv_type(m), true, PRO_Q, epi, a, s));
+        return;
+    }
+    if (quant_rows_pass(m, m_total, mc, sc) && (epi == EPI_STORE || epi == EPI_ACC || epi == EPI_SWIGLU)) {
         // several rows: quantize them once, then every GEMV block copies them instead of recomputing them
         HIPCHECK(launch_quant_rows(pro, a, sc.q, sc.qs, sc.qsum, s));
         if (t_probe) t_probe->split(VOXHIP_K_QUANT);
         a.q = sc.q; a.qs = sc.qs; a.qsum = sc.qsum;
+        if (qout) {
+            a.yq = qout->q; a.yqs = qout->qs; a.yqsum = qout->qsum;
+            HIPCHECK(launch_gemv(gemv_type(m), true, PRO_Q, EPI_SWIGLU_Q, a, s));
+            return;
+        }
         HIPCHECK(launch_gemv(gemv_type(m), true, PRO_Q, epi, a, s));
         return;
     }
@@ -859,12 +902,15 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
             acc_live = true;
             continue;
         }
+        QRows gq{};
+        const bool gq_on = !planes && ffn_quant_epilogue(Mgu, Md, m_total, mc, lib_scratch(), &gq);
         probed(pr, VOXHIP_K_GATEUP, [&] {
             if (planes) {
                 HIPCHECK(launch_rmsnorm_rows_h16(X.h, X.H, X.norms + L.ln2, int(X.H), X.eps, X.pa16, X.H, PA, mc, s));
                 hh(Mgu, EPI_SWIGLU_H16, X.pa16, PA, nullptr, X.I);
             } else {
-                gemv(Mgu, m_total, PRO_RMS, EPI_SWIGLU, X.h, X.H, mc, X.g, X.I, X.norms + L.ln2, X.eps, nullptr, s, nullptr, X.pre);
+                gemv(Mgu, m_total, PRO_RMS, EPI_SWIGLU, X.h, X.H, mc, X.g, X.I, X.norms + L.ln2, X.eps, nullptr, s, nullptr, X.pre,
+                     nullptr, nullptr, nullptr, nullptr, gq_on ? &gq : nullptr);
             }
         });
         pa_normed = false;
@@ -877,7 +923,8 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
             } else if (planes) {
                 hh(Md, EPI_ACC, X.pb16, PB, X.h, X.H);
             } else {
-                gemv(Md, m_total, PRO_X, EPI_ACC, X.g, X.I, mc, X.h, X.H, nullptr, 0.f, nullptr, s);
+                gemv(Md, m_total, PRO_X, EPI_ACC, X.g, X.I, mc, X.h, X.H, nullptr, 0.f, nullptr, s, nullptr, nullptr, nullptr,
+                     nullptr, nullptr, nullptr, nullptr, gq_on ? &gq : nullptr);
             }
         });
     }
