@@ -177,10 +177,14 @@ __global__ __launch_bounds__(kFfnThreads) void k_ffn_int(FfnArgs a) {
     }
     // row totals into lanes 0..GR-1, bias, SwiGLU of the (gate, up) pairs (kernels.cpp:836)
     float out = 0.f;
+    if constexpr ((GR & (GR - 1)) == 0 && GR > 1) {  // wave_sum's totals, by one reduce-scatter
+        out = wave_sums_scatter<GR>(acc, lane);
+    } else {
 #pragma unroll
-    for (int r = 0; r < GR; ++r) {
-        const float s = wave_sum(acc[r]);
-        if (lane == r) out = s;
+        for (int r = 0; r < GR; ++r) {
+            const float s = wave_sum(acc[r]);
+            if (lane == r) out = s;
+        }
     }
     const float v = out + (a.gu_b ? gbias : 0.f);
     const float other = __shfl_xor(v, 1, 64);

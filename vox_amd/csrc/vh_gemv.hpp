@@ -36,6 +36,59 @@ VH_DEV int64_t row_bytes(int K) {
 // of row mm holds elements 8s..8s+7, a 32-block is 4 consecutive slots handled by 4 consecutive lanes.
 // `sink(mm, s, v)` receives each slot with all 4 lanes of its block active.
 //
+// The partner lane of step S of wave_sum's tree: xor 1, xor 2, mirror in 8 (lane ^ 7), mirror in 16 (lane ^ 15),
+// then the rows: lane ^ 16, lane ^ 32.
+template <int S>
+VH_DEV float tree_partner(float x) {
+    if constexpr (S == 0) return dpp<kDppXor1>(x);
+    else if constexpr (S == 1) return dpp<kDppXor2>(x);
+    else if constexpr (S == 2) return dpp<kDppRowHalfMirror>(x);
+    else if constexpr (S == 3) return dpp<kDppRowMirror>(x);
+    else if constexpr (S == 4) return __shfl_xor(x, 16, kWave);
+    else return __shfl_xor(x, 32, kWave);
+}
+
+// N = 2^n values per lane (all 64 lanes active), each summed over the wave; returns the total of value `lane` to
+// lane < N. A reduce-scatter on wave_sum's tree: at step s (partner as tree_partner<s>) a lane keeps half of its
+// values and adds its partner's copies of them, so each total is the same sum, in the same order, as wave_sum's,
+// with N - 1 partner exchanges instead of 6 N. The half a lane keeps at step s is bit h_s of
+//   (b0 ^ b2, b1 ^ b2, b2 ^ b3, b3, b4, b5)   (b_i: bit i of the lane),
+// which flips between the step's partners and is the same for the partners of every later step, so both lanes of
+// every exchange hold the same values. After n steps the lane's value is number sum_s h_s 2^(n-1-s); steps n..5
+// add whole totals (wave_sum's remaining steps) and a last exchange moves value j to lane j.
+template <int N>
+VH_DEV float wave_sums_scatter(float (&v)[N], int lane) {
+    constexpr int n = N == 1 ? 0 : N == 2 ? 1 : N == 4 ? 2 : N == 8 ? 3 : N == 16 ? 4 : N == 32 ? 5 : 6;
+    static_assert((1 << n) == N && N <= 64, "a power of two up to 64");
+    const int b0 = lane & 1, b1 = (lane >> 1) & 1, b2 = (lane >> 2) & 1, b3 = (lane >> 3) & 1;
+    const bool h[6] = {(b0 ^ b2) != 0, (b1 ^ b2) != 0, (b2 ^ b3) != 0, b3 != 0, ((lane >> 4) & 1) != 0, ((lane >> 5) & 1) != 0};
+    auto step = [&](auto s_tag) {
+        constexpr int S = decltype(s_tag)::value;
+        if constexpr (S < n) {
+            constexpr int H = N >> (S + 1);  // values kept after this step
+#pragma unroll
+            for (int t = 0; t < H; ++t) {
+                const float keep = h[S] ? v[t + H] : v[t], give = h[S] ? v[t] : v[t + H];
+                v[t] = keep + tree_partner<S>(give);
+            }
+        } else {
+            v[0] = v[0] + tree_partner<S>(v[0]);
+        }
+    };
+    step(std::integral_constant<int, 0>());
+    step(std::integral_constant<int, 1>());
+    step(std::integral_constant<int, 2>());
+    step(std::integral_constant<int, 3>());
+    step(std::integral_constant<int, 4>());
+    step(std::integral_constant<int, 5>());
+    // the lane holding value j = lane: h_s = bit n-1-s of j for s < n, 0 after; solve for the lane bits
+    int hj[6] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < n; ++s) hj[s] = (lane >> (n - 1 - s)) & 1;
+    const int c3 = hj[3], c2 = hj[2] ^ c3, c1 = hj[1] ^ c2, c0 = hj[0] ^ c2;
+    return __shfl(v[0], c0 | (c1 << 1) | (c2 << 2) | (c3 << 3) | (hj[4] << 4) | (hj[5] << 5), kWave);
+}
+
 // When its global inputs fit in registers (slot s = threadIdx.x + 256 k, k < KS), pro_stage() loads them BEFORE the
 // kernel issues its weight stream. Vector loads return in issue order, so the prologue then waits for its own
 // inputs only and the weights arrive while it computes. Larger inputs are read inside prologue(), after the weights.
@@ -164,11 +217,14 @@ VH_DEV void prologue(const GemvArgs &a, const float *x, int K, float *red, const
             for (int r = 0; r < M; ++r)
                 if (r == mm) ss[r] += q;
         });
-#pragma unroll
-        for (int mm = 0; mm < M; ++mm) ss[mm] = wave_sum(ss[mm]);
-        if ((threadIdx.x & 63) == 0)
-#pragma unroll
-            for (int mm = 0; mm < M; ++mm) red[mm * 4 + (threadIdx.x >> 6)] = ss[mm];
+        if constexpr (M > 1) {  // wave_sum's totals by one reduce-scatter: lane mm holds row mm's
+            const int lane = threadIdx.x & 63;
+            const float tot = wave_sums_scatter<M>(ss, lane);
+            if (lane < M) red[lane * 4 + (threadIdx.x >> 6)] = tot;
+        } else {
+            ss[0] = wave_sum(ss[0]);
+            if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss[0];
+        }
         __syncthreads();
         float inv[M];
 #pragma unroll
@@ -367,59 +423,6 @@ VH_DEV void store_out(const GemvArgs &a, int rows, float out, int lane, int row0
             a.y[int64_t(mm) * a.ldy + row] = base + (a.yscale ? v * e.ys : v);
         }
     }
-}
-
-// The partner lane of step S of wave_sum's tree: xor 1, xor 2, mirror in 8 (lane ^ 7), mirror in 16 (lane ^ 15),
-// then the rows: lane ^ 16, lane ^ 32.
-template <int S>
-VH_DEV float tree_partner(float x) {
-    if constexpr (S == 0) return dpp<kDppXor1>(x);
-    else if constexpr (S == 1) return dpp<kDppXor2>(x);
-    else if constexpr (S == 2) return dpp<kDppRowHalfMirror>(x);
-    else if constexpr (S == 3) return dpp<kDppRowMirror>(x);
-    else if constexpr (S == 4) return __shfl_xor(x, 16, kWave);
-    else return __shfl_xor(x, 32, kWave);
-}
-
-// N = 2^n values per lane (all 64 lanes active), each summed over the wave; returns the total of value `lane` to
-// lane < N. A reduce-scatter on wave_sum's tree: at step s (partner as tree_partner<s>) a lane keeps half of its
-// values and adds its partner's copies of them, so each total is the same sum, in the same order, as wave_sum's,
-// with N - 1 partner exchanges instead of 6 N. The half a lane keeps at step s is bit h_s of
-//   (b0 ^ b2, b1 ^ b2, b2 ^ b3, b3, b4, b5)   (b_i: bit i of the lane),
-// which flips between the step's partners and is the same for the partners of every later step, so both lanes of
-// every exchange hold the same values. After n steps the lane's value is number sum_s h_s 2^(n-1-s); steps n..5
-// add whole totals (wave_sum's remaining steps) and a last exchange moves value j to lane j.
-template <int N>
-VH_DEV float wave_sums_scatter(float (&v)[N], int lane) {
-    constexpr int n = N == 1 ? 0 : N == 2 ? 1 : N == 4 ? 2 : N == 8 ? 3 : N == 16 ? 4 : N == 32 ? 5 : 6;
-    static_assert((1 << n) == N && N <= 64, "a power of two up to 64");
-    const int b0 = lane & 1, b1 = (lane >> 1) & 1, b2 = (lane >> 2) & 1, b3 = (lane >> 3) & 1;
-    const bool h[6] = {(b0 ^ b2) != 0, (b1 ^ b2) != 0, (b2 ^ b3) != 0, b3 != 0, ((lane >> 4) & 1) != 0, ((lane >> 5) & 1) != 0};
-    auto step = [&](auto s_tag) {
-        constexpr int S = decltype(s_tag)::value;
-        if constexpr (S < n) {
-            constexpr int H = N >> (S + 1);  // values kept after this step
-#pragma unroll
-            for (int t = 0; t < H; ++t) {
-                const float keep = h[S] ? v[t + H] : v[t], give = h[S] ? v[t] : v[t + H];
-                v[t] = keep + tree_partner<S>(give);
-            }
-        } else {
-            v[0] = v[0] + tree_partner<S>(v[0]);
-        }
-    };
-    step(std::integral_constant<int, 0>());
-    step(std::integral_constant<int, 1>());
-    step(std::integral_constant<int, 2>());
-    step(std::integral_constant<int, 3>());
-    step(std::integral_constant<int, 4>());
-    step(std::integral_constant<int, 5>());
-    // the lane holding value j = lane: h_s = bit n-1-s of j for s < n, 0 after; solve for the lane bits
-    int hj[6] = {0, 0, 0, 0, 0, 0};
-#pragma unroll
-    for (int s = 0; s < n; ++s) hj[s] = (lane >> (n - 1 - s)) & 1;
-    const int c3 = hj[3], c2 = hj[2] ^ c3, c1 = hj[1] ^ c2, c0 = hj[0] ^ c2;
-    return __shfl(v[0], c0 | (c1 << 1) | (c2 << 2) | (c3 << 3) | (hj[4] << 4) | (hj[5] << 5), kWave);
 }
 
 template <int R, int M>
