@@ -65,6 +65,50 @@ __global__ __launch_bounds__(64) void k_qk_post(QkArgs a) {
     }
 }
 
+// k_qk_post for head_dim 2 HALF (64 or 128) with several heads per block: grid (ceil((heads + kv_heads) / (256 /
+// HALF)), m), block 256. The HALF lanes of a head are consecutive lanes of one wave, so its norm sums over them
+// (group_sum<HALF>, the same sum of the same squares as k_qk_post's wave sum, whose other lanes add zeros, in the
+// same tree order); every lane holds one rotate-half pair, so no lane is idle.
+template <int HALF>
+__global__ __launch_bounds__(256) void k_qk_post_wide(QkArgs a) {
+    constexpr int HD = 2 * HALF;
+    const int t = int(threadIdx.x), hh = int(blockIdx.x) * (256 / HALF) + t / HALF, i = blockIdx.y, p = t % HALF;
+    const int nh = a.heads + a.kv_heads;
+    const int hc = hh < nh ? hh : nh - 1;  // lanes past the last head compute a copy of it and store nothing
+    const int qd = a.heads * HD, kd = a.kv_heads * HD;
+    const RowRef rr = a.rows[i];
+    const bool is_q = hc < a.heads;
+    const int g = hc - a.heads;
+    const float *src = a.qkv + int64_t(i) * a.ldqkv + (is_q ? hc * HD : qd + g * HD);
+    const float *nw = is_q ? a.qn : a.kn;
+    const float *nwp = nw ? nw : src;
+    const float *vs = a.qkv + int64_t(i) * a.ldqkv + qd + kd + (is_q ? 0 : g * HD);
+    float x0 = src[p], x1 = src[p + HALF];
+    const float lw0 = nwp[p], lw1 = nwp[p + HALF];
+    const float v0 = vs[p], v1 = vs[p + HALF];
+    const float c = a.rope[(rr.pos * HALF + p) * 2], sn = a.rope[(rr.pos * HALF + p) * 2 + 1];
+    if (nw) {  // a head's lanes share the branch (the head's kind decides nw)
+        const float ss = group_sum<HALF>(x0 * x0 + x1 * x1);
+        const float inv = 1.0f / sqrtf(ss / float(HD) + a.eps);
+        x0 = lw0 * (x0 * inv);
+        x1 = lw1 * (x1 * inv);
+    }
+    if (hh >= nh) return;
+    const float r0 = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
+    const float r1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, sn));
+    if (is_q) {
+        float *dst = a.q + int64_t(i) * qd + hc * HD;
+        dst[p] = r0;
+        dst[p + HALF] = r1;
+    } else {
+        const int64_t off = ((int64_t(a.layer) * a.kv_heads + g) * rr.cap + rr.pos) * HD;
+        rr.k[off + p] = _Float16(r0);
+        rr.k[off + p + HALF] = _Float16(r1);
+        rr.v[off + p] = _Float16(v0);
+        rr.v[off + p + HALF] = _Float16(v1);
+    }
+}
+
 // Attention for the head sizes the split-K and MFMA kernels are not built for (any even hd <= 128): grid (heads, m),
 // block 256. Lane l of each wave holds dims l and l + 64; wave w takes keys w, w + 4, ... of the row's cache with an
 // online softmax (score = scale * q.k, as kernels.cpp:818-819), and the four waves are merged through LDS.

@@ -177,7 +177,10 @@ hipError_t ensure_smem(const void *kernel, size_t bytes) {
 
 hipError_t launch_qk_post(const QkArgs &a, int m, hipStream_t s) {
     if (m <= 0) return hipSuccess;
-    return launch(k_qk_post, dim3(a.heads + a.kv_heads, m), dim3(64), 0, s, a);
+    const int nh = a.heads + a.kv_heads;
+    if (a.hd == 64) return launch(k_qk_post_wide<32>, dim3(unsigned((nh + 7) / 8), m), dim3(256), 0, s, a);
+    if (a.hd == 128) return launch(k_qk_post_wide<64>, dim3(unsigned((nh + 3) / 4), m), dim3(256), 0, s, a);
+    return launch(k_qk_post, dim3(nh, m), dim3(64), 0, s, a);
 }
 
 struct AttnLaunch {
@@ -265,7 +268,7 @@ static hipError_t prefill_attn_hd(const PrefillAttnArgs &a0, hipStream_t s) {
     const dim3 grid(unsigned((a.m + 63) / 64), unsigned(a.heads), unsigned(a.splits));
     hipError_t e = launch(k_prefill_attn<HD>, grid, dim3(256), 0, s, a);
     if (e != hipSuccess || a.splits == 1) return e;
-    return launch(k_pattn_merge<HD>, dim3(unsigned(a.heads), unsigned(a.m)), dim3(HD), 0, s, a);
+    return launch(k_pattn_merge<HD>, dim3(unsigned((a.heads * HD + 255) / 256), unsigned(a.m)), dim3(256), 0, s, a);
 }
 hipError_t launch_prefill_attn(const PrefillAttnArgs &a, int hd, hipStream_t s) {
     if (a.m <= 0) return hipSuccess;

@@ -197,10 +197,12 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillAttnArgs a) {
 
 // The runs of a key-split prefill attention merged per (row, head): M = the runs' largest max, the sums and
 // outputs scaled by exp(max - M) and added in run order, then out = O (1 / L) as f32 or as f16 halves (hi at out16,
-// lo at out16 + lo_off). grid (heads, m), block HD; every run's values are loaded before any is used.
+// lo at out16 + lo_off). grid (ceil(heads HD / 256), m), block 256: thread t of a block takes element t % HD of
+// head (256 blockIdx.x + t) / HD; every run's values are loaded before any is used.
 template <int HD>
-__global__ __launch_bounds__(HD) void k_pattn_merge(PrefillAttnArgs a) {
-    const int h = blockIdx.x, i = blockIdx.y, e = threadIdx.x;
+__global__ __launch_bounds__(256) void k_pattn_merge(PrefillAttnArgs a) {
+    const int t = int(blockIdx.x) * 256 + int(threadIdx.x), h = t / HD, i = blockIdx.y, e = t % HD;
+    if (h >= a.heads) return;
     const int64_t base = (int64_t(i) * a.heads + h) * kAttnMaxSplits;
     float pm[kAttnMaxSplits], pl[kAttnMaxSplits], po[kAttnMaxSplits];
     // every run's partial output is loaded with its max and sum (the choice depends only on the run count), so the
