@@ -193,16 +193,17 @@ struct AttnSmem {
 // launch of one row and U groups (S NGRP U keys) in a launch of several, whose blocks have less to hide the
 // dependent round trip behind; later keys load per batch of U.
 // ONE_ROW (launches of one row, m == 1): only row 0's path is compiled, so the compiler's wait counts follow one
-// static load sequence.
-template <int HD, int G, bool FUSED, bool ONE_ROW = false>
+// static load sequence. LONG (one row at a position past kAttnSpecKeys): the first batch is U groups, as for
+// several rows, since the keys past kAttnSpecKeys are there to be read.
+template <int HD, int G, bool FUSED, bool ONE_ROW = false, bool LONG = false>
 __global__ __launch_bounds__(256) void k_attn(const _Float16 *kc0, const _Float16 *vc0, const float *qkv,
                                               const float *rope_rows, int32_t cap0, int32_t layer, AttnArgs a) {
     using Sm = AttnSmem<HD, G>;
     constexpr int LPK = Sm::LPK, KPW = Sm::KPW, NGRP = Sm::NGRP, HALF = HD / 2, S = kAttnMaxSplits;
     constexpr int U = G <= 2 ? 8 : G <= 4 ? 4 : 2;
-    // groups in the first batch: U1S (kAttnSpecKeys keys) for one row, U for several
+    // groups in the first batch: U1S (kAttnSpecKeys keys) for one row, U for several or for one row far enough in
     constexpr int U1S = kAttnSpecKeys / (S * NGRP) < U ? kAttnSpecKeys / (S * NGRP) : U;
-    constexpr int U1 = ONE_ROW ? U1S : U;
+    constexpr int U1 = ONE_ROW && !LONG ? U1S : U;
     constexpr int NQ = (G * HALF + 255) / 256;  // q rotate-half pairs per thread
     extern __shared__ __align__(16) uint8_t attn_smem[];
     Sm &sm = *reinterpret_cast<Sm *>(attn_smem);

@@ -187,12 +187,19 @@ struct AttnLaunch {
     const _Float16 *kc0, *vc0;
     const float *qkv, *rope_rows;
     int32_t cap0, layer;
+    bool lng;  // one row at a position past kAttnSpecKeys
 };
 
 template <int HD, int G>
 static hipError_t attn_hg(const AttnArgs &a, const AttnLaunch &l, int m, bool fused, hipStream_t s) {
     const size_t smem = sizeof(AttnSmem<HD, G>);
     const dim3 grid(kAttnMaxSplits, a.kv_heads * (a.group / G), m);
+    if (fused && m == 1 && l.lng) {
+        hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_attn<HD, G, true, true, true>), smem);
+        if (e != hipSuccess) return e;
+        return launch(k_attn<HD, G, true, true, true>, grid, dim3(256), smem, s, l.kc0, l.vc0, l.qkv, l.rope_rows, l.cap0, l.layer,
+                      a);
+    }
     if (fused && m == 1) {
         hipError_t e = ensure_smem(reinterpret_cast<const void *>(&k_attn<HD, G, true, true>), smem);
         if (e != hipSuccess) return e;
@@ -240,11 +247,12 @@ static hipError_t attn_h(const AttnArgs &a, const AttnLaunch &l, int m, bool fus
 }
 
 hipError_t launch_attention(const AttnArgs &a, const _Float16 *kc0, const _Float16 *vc0, int64_t cap0, const float *qkv,
-                            const float *rope_rows, int layer, int hd, int group, int m, bool fused, hipStream_t s) {
+                            const float *rope_rows, int layer, int hd, int group, int m, bool fused, hipStream_t s,
+                            bool long_ctx) {
     if (m <= 0) return hipSuccess;
     if (cap0 <= 0 || cap0 > INT32_MAX) return hipErrorInvalidValue;
     if (group < 1 || group > 8) return hipErrorInvalidValue;
-    const AttnLaunch l{kc0, vc0, qkv, rope_rows, int32_t(cap0), int32_t(layer)};
+    const AttnLaunch l{kc0, vc0, qkv, rope_rows, int32_t(cap0), int32_t(layer), long_ctx};
     AttnArgs ag = a;
     ag.group = group;
     if (hd == 128) return attn_h<128>(ag, l, m, fused, s);

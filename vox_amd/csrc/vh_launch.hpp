@@ -75,9 +75,12 @@ hipError_t launch_conv_gemm(int epi, const float *w, const float *A, const GemmA
 hipError_t launch_attn_merge(const AttnPartials &P, float *ao, int m, hipStream_t s);
 // Split-K attention partials of m rows (merged by the PRO_ATTN GEMV prologue). fused: rows of distinct sequences,
 // q/k post-processing and the K/V append happen inside; otherwise k_qk_post ran first. kc0/vc0/cap0: row 0's cache
-// (the same as the first row view); qkv: [m][a.ldqkv]; rope_rows: [m][hd] (fused).
+// (the same as the first row view); qkv: [m][a.ldqkv]; rope_rows: [m][hd] (fused). long_ctx: a fused row at a position
+// past kAttnSpecKeys, whose first batch then holds as many keys as a launch of several rows takes (a graph
+// captured with it replays correctly at any position).
 hipError_t launch_attention(const AttnArgs &a, const _Float16 *kc0, const _Float16 *vc0, int64_t cap0, const float *qkv,
-                            const float *rope_rows, int layer, int hd, int group, int m, bool fused, hipStream_t s);
+                            const float *rope_rows, int layer, int hd, int group, int m, bool fused, hipStream_t s,
+                            bool long_ctx = false);
 // rows samplers at once: cfg[b], logits [b][n], out[b].
 hipError_t launch_sample(const SampleCfgDev *cfg, const float *logits, int n, int32_t *out, hipStream_t s, int rows = 1);
 

@@ -84,25 +84,26 @@ struct LayerDev {
 };
 
 // A captured decode step: m rows of one sequence (steps = 0), or one row for each of m sequences (steps = 1).
+// lng: one row at a position past kAttnSpecKeys (the attention's long first batch).
 struct GraphKey {
     std::array<int, 8> seqs;
-    int m, head, sample, steps;
+    int m, head, sample, steps, lng;
     const void *x, *out, *logits, *token;
     bool operator<(const GraphKey &o) const {
-        return std::tie(seqs, m, head, sample, steps, x, out, logits, token) <
-               std::tie(o.seqs, o.m, o.head, o.sample, o.steps, o.x, o.out, o.logits, o.token);
+        return std::tie(seqs, m, head, sample, steps, lng, x, out, logits, token) <
+               std::tie(o.seqs, o.m, o.head, o.sample, o.steps, o.lng, o.x, o.out, o.logits, o.token);
     }
 };
 
 // A captured layer pass of forward_rows: the launch sequence of enqueue_layers depends on the pass's row count,
 // the caller's row count class (<= 8 rows: int8 path), the layer range, the attention form and row 0's cache view.
 struct LayersKey {
-    int mc, mt, first, count, fused, pass_attn;
+    int mc, mt, first, count, fused, pass_attn, lng;
     const void *k, *v;
     int64_t cap;
     bool operator<(const LayersKey &o) const {
-        return std::tie(mc, mt, first, count, fused, pass_attn, k, v, cap) <
-               std::tie(o.mc, o.mt, o.first, o.count, o.fused, o.pass_attn, o.k, o.v, o.cap);
+        return std::tie(mc, mt, first, count, fused, pass_attn, lng, k, v, cap) <
+               std::tie(o.mc, o.mt, o.first, o.count, o.fused, o.pass_attn, o.lng, o.k, o.v, o.cap);
     }
 };
 constexpr int kMaxLayerGraphs = 64;  // captured layer passes kept per transformer
@@ -756,6 +757,13 @@ int kernels_per_layer(const Xfmr &X, int mc, bool fused) { return ffn_pass(X, mc
 // m_total: the caller's total row count, which picks the q8 arithmetic (int8 for <= 8, f32 above).
 // fused: every row belongs to a different sequence, so the attention kernel can append K/V itself.
 // A prefill pass of consecutive rows of one sequence takes attention on the matrix cores straight into the o input.
+// A pass of one row whose position (row 0 of the current row table) is past kAttnSpecKeys, so that its cache keys
+// 0 .. pos - 1 do not all fit the short first batch: its attention loads a full one (launch_attention's long_ctx).
+// Graphs are keyed by it, so a step captured before the position passed kAttnSpecKeys is not the one replayed after.
+bool long_row(const Xfmr &X, int mc) {
+    return mc == 1 && !X.rows_last.empty() && X.rows_last[0].pos > kAttnSpecKeys;
+}
+
 bool pass_attn_of(const Xfmr &X, int mc, bool fused) {
     bool pass_attn = !fused && mc > 4 && (X.hd == 64 || X.hd == 128) && int(X.rows_last.size()) == mc;
     for (int i = 1; i < mc && pass_attn; ++i)
@@ -884,7 +892,8 @@ void enqueue_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, hipS
             aa.ldqkv = ldqkv; aa.q = X.q; aa.qn = qn; aa.kn = kn; aa.part = part;
             aa.kv_heads = X.kvh; aa.scale = 1.0f / std::sqrt(float(X.hd)); aa.eps = X.eps;
             probed(pr, VOXHIP_K_ATTN, [&] {
-                HIPCHECK(launch_attention(aa, r0.k, r0.v, r0.cap, X.qkv, X.rope_rows_dev, li, X.hd, X.heads / X.kvh, mc, fused, s));
+                HIPCHECK(launch_attention(aa, r0.k, r0.v, r0.cap, X.qkv, X.rope_rows_dev, li, X.hd, X.heads / X.kvh, mc, fused, s,
+                                          long_row(X, mc)));
             });
             probed(pr, VOXHIP_K_O, [&] {
                 gemv(Mo, m_total, PRO_ATTN, EPI_ACC, nullptr, 0, mc, X.h, X.H, nullptr, 0.f, nullptr, s, &part, X.pre, nullptr,
@@ -952,7 +961,7 @@ void run_layers(Xfmr &X, int mc, int64_t m_total, int first, int count, bool fus
     if (vh::prof_on()) return enqueue_layers(X, mc, m_total, first, count, g.stream, fused);  // stamped launches
     const RowRef &r0 = X.rows_last.at(0);
     const LayersKey key{mc, int(std::min<int64_t>(m_total, kMaxM + 1)), first, count, fused ? 1 : 0,
-                        pass_attn_of(X, mc, fused) ? 1 : 0, r0.k, r0.v, r0.cap};
+                        pass_attn_of(X, mc, fused) ? 1 : 0, long_row(X, mc) ? 1 : 0, r0.k, r0.v, r0.cap};
     auto it = X.layer_graphs.find(key);
     if (it != X.layer_graphs.end()) {
         HIPCHECK(hipGraphLaunch(it->second, g.stream));
@@ -1749,7 +1758,7 @@ int enqueue_decode(Xfmr &X, int m, int head, const float *d_x, float *d_out_last
 
 hipGraphExec_t decode_graph(Xfmr &X, const std::array<int, 8> &seqs, int m, bool steps, int head, const float *d_x,
                             float *d_out_last, float *d_logits, bool sample, int32_t *d_token) {
-    GraphKey key{seqs, m, head, sample ? 1 : 0, steps ? 1 : 0, d_x, d_out_last, d_logits, d_token};
+    GraphKey key{seqs, m, head, sample ? 1 : 0, steps ? 1 : 0, long_row(X, m) ? 1 : 0, d_x, d_out_last, d_logits, d_token};
     auto it = X.graphs.find(key);
     if (it != X.graphs.end()) return it->second;
     hipGraph_t graph = nullptr;
