@@ -1,4 +1,4 @@
-"""Long contexts through the decode paths: keys far past the attention's speculative first batch (512 keys), split
+"""Long contexts through the decode paths: keys far past the attention's short first batch (512 keys), split
 over the 8 interleaved key ranges, one row and 8 sessions at different positions in one step. The reference
 (transformer_forward, kernels.cpp:797-826) attends over keys 0 .. pos of the row's cache; the oracle runs it on the
 same stored weights and f16 cache. Bar: 1e-3 (`vox verify` metric), the per-layer check teacher-forced; the
@@ -82,3 +82,26 @@ def test_prefill_rows_after_long_context(hip, oracle, dec):
     out, _ = hip.forward(dec.xfmr, s, pos0, x, c["hidden"])
     ref = oracle.transformer_forward(X, kv, x)
     assert rel_err(out, ref) < 1e-3, rel_err(out, ref)
+
+
+def test_one_row_steps_across_512(hip, oracle, dec):
+    # device-resident one-row steps at positions 508 .. 517: below 513 the attention's first batch is 512 keys, past
+    # it a full batch; the captured step is keyed by that, so the graph from before the crossing is not replayed after
+    c = dec.cfg
+    H = c["hidden"]
+    s = dec.extra_seq(0xFACE)
+    X, (kv,), _ = to_oracle(oracle, hip, dec, seqs=[s], kv_len=508, cap=528)
+    rng = np.random.default_rng(8)
+    dx, dout = hip.DevBuf(H * 4), hip.DevBuf(H * 4)
+    try:
+        for pos in range(508, 518):
+            x = rng.standard_normal((1, H)).astype(np.float32)
+            dx.upload(x)
+            hip.decode_dev(dec.xfmr, s, pos, dx, 1, dout)
+            hip.sync()
+            out = dout.download(H, np.float32)
+            ref = oracle.transformer_forward(X, kv, x)
+            assert rel_err(out, ref) < 1e-3, (pos, rel_err(out, ref))
+    finally:
+        dx.free()
+        dout.free()
