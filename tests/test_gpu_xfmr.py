@@ -89,9 +89,11 @@ def test_prefill_gemm(hip, oracle, wt, m):
         assert rel_err(out, oracle.transformer_forward(mdl.ox, kv, x)) < TOL
 
 
-def test_gqa7_bias_hd64(hip, oracle):
-    # CosyVoice2-shaped attention: 7 query heads per kv head, head_dim 64, q/k/v biases, no q/k norm
-    mdl = Model(300, 2, 128, 7, 1, 64, 256, wtype=Q8, qk_norm=False, bias=True, head_rows=100, head_type=F32)
+@pytest.mark.parametrize("qkn", [False, True])
+def test_gqa7_bias_hd64(hip, oracle, qkn):
+    # CosyVoice2-shaped attention: 7 query heads per kv head, head_dim 64, q/k/v biases, no q/k norm; and the same
+    # with q/k norms (the prefill's q/k pass sums each head's squares over its 32 lanes of a wave)
+    mdl = Model(300 + qkn, 2, 128, 7, 1, 64, 256, wtype=Q8, qk_norm=qkn, bias=True, head_rows=100, head_type=F32)
     xf, head = build(hip, mdl)
     seq = hip.seq_create(xf, 32)
     kv = mdl.oracle_kv(32, 1)
