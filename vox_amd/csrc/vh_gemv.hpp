@@ -427,14 +427,16 @@ VH_DEV void store_out(const GemvArgs &a, int rows, float out, int lane, int row0
 
 template <int R, int M>
 VH_DEV void reduce_store_prep(float (&acc)[R][M], float &out, int lane) {
-    constexpr int N = R * M;
-    if constexpr ((N & (N - 1)) == 0 && N > 1) {  // lane r M + mm gets the total of acc[r][mm]
-        float v[N];
+    constexpr int N = R * M, P = N <= 2 ? 2 : N <= 4 ? 4 : N <= 8 ? 8 : N <= 16 ? 16 : N <= 32 ? 32 : 64;
+    if constexpr (N > 1 && N <= 64) {  // lane r M + mm gets the total of acc[r][mm]; values N .. P - 1 are zero pads
+        float v[P];
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int mm = 0; mm < M; ++mm) v[r * M + mm] = acc[r][mm];
-        out = wave_sums_scatter<N>(v, lane);
+#pragma unroll
+        for (int k = N; k < P; ++k) v[k] = 0.f;
+        out = wave_sums_scatter<P>(v, lane);
         if (lane >= N) out = 0.f;
     } else {
         out = 0.f;
