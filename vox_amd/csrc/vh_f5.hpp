@@ -319,14 +319,12 @@ __global__ __launch_bounds__(64 * W * KS) void k_f5_attn(F5AttnArgs a) {
         // 32 c + 4 lg + e (e < 4) or 32 c + 16 + 4 lg + (e - 4); A operand lane holds V^T[16 dt + lr][those keys]
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            h16x8 ph, pl;
+            uint32_t hw[4], lw[4];  // elements 2u, 2u + 1 of P's hi and lo halves
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float x = s[2 * c + (e >> 2)][e & 3];
-                const _Float16 hi = _Float16(x);
-                ph[e] = hi;
-                pl[e] = _Float16(x - float(hi));
-            }
+            for (int u = 0; u < 4; ++u)
+                split_f16x2(s[2 * c + (u >> 1)][2 * (u & 1)], s[2 * c + (u >> 1)][2 * (u & 1) + 1], hw[u], lw[u]);
+            const h16x8 ph = __builtin_bit_cast(h16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
+            const h16x8 pl = __builtin_bit_cast(h16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
                 const int d = 16 * dt + lr, k0 = 32 * c + 4 * lg;
