@@ -504,6 +504,12 @@ int voxhip_bench_ffn_q8(int64_t hidden, int64_t inter, int copies, int warmup, i
  * The same kernel calibrates the HBM traffic counters. No reference counterpart (benchmark helper). */
 int voxhip_bench_copy(int64_t bytes, int warmup, int iters, double *ms_per_copy);
 
+/* Self-test of the packed f16 split the F5 / flow-estimator attention uses for P (v_cvt_pk_f16_f32 and
+ * v_fma_mix{lo,hi}_f16): `pairs` pseudo-random f32 pairs (half of them in the f16 subnormal .. overflow range) split
+ * both that way and as hi = f16(x), lo = f16(x - hi); *mismatches = the pairs whose bits differ (NaN inputs skipped).
+ * No reference counterpart (a check of this build's instruction sequence). */
+int voxhip_selftest_split_f16(int64_t pairs, int64_t *mismatches);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,6 +21,12 @@ def test_device_is_gfx950(hip):
     assert hip.lib().voxhip_active() == 1
 
 
+def test_packed_f16_split_bit_exact(hip):
+    # the attention's P split (v_cvt_pk_f16_f32, v_fma_mix{lo,hi}_f16) against hi = f16(x), lo = f16(x - hi) on 2^27
+    # pseudo-random pairs, half of them spread over the f16 subnormal, normal and overflow ranges
+    assert hip.selftest_split_f16(1 << 27) == 0
+
+
 def test_quantizers_bit_exact(hip, oracle):
     rng = np.random.default_rng(1)
     w = (rng.standard_normal((64, 256)) * np.geomspace(1e-4, 10, 256)).astype(np.float32)

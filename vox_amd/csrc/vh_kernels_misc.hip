@@ -368,6 +368,12 @@ hipError_t launch_absmax(const float *x, int64_t n, uint32_t *out, hipStream_t s
     return launch(k_absmax, dim3(unsigned(std::min<int64_t>(1024, (n + 255) / 256))), dim3(256), 0, s, x, n, out);
 }
 
+hipError_t launch_check_split(uint64_t base, uint64_t pairs, unsigned long long *bad, hipStream_t s) {
+    if (pairs == 0) return hipSuccess;
+    if (pairs > (uint64_t(1) << 31)) return hipErrorInvalidValue;
+    return launch(k_check_split, dim3(unsigned((pairs + 255) / 256)), dim3(256), 0, s, base, pairs, bad);
+}
+
 hipError_t launch_copy16(const void *src, void *dst, int64_t bytes, hipStream_t s) {
     const int64_t n = bytes / 16;
     if (n <= 0) return hipSuccess;

@@ -199,4 +199,29 @@ __global__ __launch_bounds__(256) void k_copy16(const u32x4 *src, u32x4 *dst, in
     for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) dst[i] = __builtin_nontemporal_load(src + i);
 }
 
+// Self-test of split_f16x2 against the C++ form of split_f16 (hi = f16(x), lo = f16(x - float(hi))): thread t takes
+// the pair of pseudo-random f32 bit patterns k = base + 2t, k + 1, every second pair confined to f32 exponents
+// 96 .. 150 (|x| from 2^-31 to 2^23: f16 subnormals, normals and overflow); counts the pairs that differ, NaN inputs
+// apart (their payloads may differ).
+__global__ __launch_bounds__(256) void k_check_split(uint64_t base, uint64_t pairs, unsigned long long *bad) {
+    const uint64_t t = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= pairs) return;
+    const uint64_t k = base + 2 * t;
+    uint32_t ua = uint32_t(k * 2654435761u) ^ uint32_t(k >> 7), ub = uint32_t((k + 1) * 40503u) ^ uint32_t(k >> 3);
+    if (k & 2) {
+        ua = (ua & 0x807FFFFFu) | ((96u + (ua >> 23) % 55u) << 23);
+        ub = (ub & 0x807FFFFFu) | ((96u + (ub >> 23) % 55u) << 23);
+    }
+    const float a = __builtin_bit_cast(float, ua), b = __builtin_bit_cast(float, ub);
+    if (a != a || b != b) return;
+    uint32_t hp, lp;
+    split_f16x2(a, b, hp, lp);
+    _Float16 ha, la, hb, lb;
+    (void)split_f16(a, ha, la);
+    (void)split_f16(b, hb, lb);
+    const uint32_t rh = uint32_t(__builtin_bit_cast(uint16_t, ha)) | (uint32_t(__builtin_bit_cast(uint16_t, hb)) << 16);
+    const uint32_t rl = uint32_t(__builtin_bit_cast(uint16_t, la)) | (uint32_t(__builtin_bit_cast(uint16_t, lb)) << 16);
+    if (rh != hp || rl != lp) atomicAdd(bad, 1ull);
+}
+
 }  // namespace vh

@@ -4053,6 +4053,31 @@ int voxhip_bench_gemm_hh(int64_t m, int64_t n, int64_t K, int q8, int tile, int 
     }, 0);
 }
 
+int voxhip_selftest_split_f16(int64_t pairs, int64_t *mismatches) {
+    return guard_int([&] {
+        require_ok();
+        if (pairs <= 0 || !mismatches) throw Fail("bad self-test arguments");
+        unsigned long long *bad = nullptr;
+        try {
+            bad = dalloc_t<unsigned long long>(1);
+            HIPCHECK(hipMemsetAsync(bad, 0, sizeof *bad, g.stream));
+            const int64_t chunk = int64_t(1) << 26;
+            for (int64_t p = 0; p < pairs; p += chunk)
+                HIPCHECK(launch_check_split(uint64_t(2 * p), uint64_t(std::min(chunk, pairs - p)), bad, g.stream));
+            unsigned long long h = 0;
+            HIPCHECK(copy_d2h(&h, bad, sizeof h, g.stream));
+            HIPCHECK(hipStreamSynchronize(g.stream));
+            *mismatches = int64_t(h);
+        } catch (...) {
+            (void)hipStreamSynchronize(g.stream);
+            dfree(bad);
+            throw;
+        }
+        dfree(bad);
+        return 1;
+    }, 0);
+}
+
 int voxhip_bench_copy(int64_t bytes, int warmup, int iters, double *ms_per_copy) {
     return guard_int([&] {
         require_ok();

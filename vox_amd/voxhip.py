@@ -220,6 +220,7 @@ SIGNATURES = {
     "voxhip_bench_decode_steps": (_I, [_I, _P, _P, _I64, _P, _I, _P, _P, _I, _I, C.POINTER(BenchResult)]),
     "voxhip_bench_gemv_q8": (_I, [_I64, _I64, _I, _I, _I, C.POINTER(C.c_double)]),
     "voxhip_bench_copy": (_I, [_I64, _I, _I, C.POINTER(C.c_double)]),
+    "voxhip_selftest_split_f16": (_I, [_I64, C.POINTER(C.c_int64)]),
     "voxhip_bench_gemm_hh": (_I, [_I64, _I64, _I64, _I, _I, _I, _I, C.POINTER(C.c_double), _P]),
     "voxhip_bench_ffn_q8": (_I, [_I64, _I64, _I, _I, _I, C.POINTER(C.c_double), _P]),
 }
@@ -863,6 +864,13 @@ def bench_gemm_hh(m, n, K, q8=False, tile=0, warmup=3, iters=20, out=False):
     _check(lib().voxhip_bench_gemm_hh(m, n, K, int(bool(q8)), tile, warmup, iters, C.byref(us),
                                       y.ctypes.data if out else None), "bench_gemm_hh")
     return (us.value, y) if out else us.value
+
+
+def selftest_split_f16(pairs):
+    """Pairs (of `pairs` pseudo-random f32 pairs) whose packed f16 split differs from hi = f16(x), lo = f16(x - hi)."""
+    n = C.c_int64()
+    _check(lib().voxhip_selftest_split_f16(pairs, C.byref(n)), "selftest_split_f16")
+    return n.value
 
 
 def bench_copy(nbytes, warmup, iters):
