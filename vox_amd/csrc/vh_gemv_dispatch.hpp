@@ -63,7 +63,7 @@ hipError_t gemv_by_tile(int R, int IT, const GemvArgs &a, hipStream_t s) {
         }
     } else if constexpr (M == 1) {
         if constexpr (EPI == EPI_SWIGLU) {
-            VH_TILE(2, 1) VH_TILE(4, 1) VH_TILE(6, 1) VH_TILE(8, 1) VH_TILE(2, 2) VH_TILE(2, 3)
+            VH_TILE(2, 1) VH_TILE(4, 1) VH_TILE(6, 1) VH_TILE(8, 1) VH_TILE(12, 1) VH_TILE(2, 2) VH_TILE(2, 3)
         } else {
             VH_TILE(1, 1) VH_TILE(2, 1) VH_TILE(3, 1) VH_TILE(4, 1) VH_TILE(6, 1) VH_TILE(8, 1)
             VH_TILE(1, 2) VH_TILE(1, 3) VH_TILE(1, 4) VH_TILE(1, 5) VH_TILE(1, 6)
