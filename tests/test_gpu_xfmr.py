@@ -321,12 +321,13 @@ def test_prefill_planes_under_vram_limit(hip, oracle):
         hip.lib().voxhip_set_vram_limit(0)
 
 
-@pytest.mark.parametrize("wt", [F16, Q8])
-def test_prefill_key_splits(hip, oracle, wt):
+@pytest.mark.parametrize("wt,hd", [(F16, 128), (Q8, 128), (F16, 64), (Q8, 64)])
+def test_prefill_key_splits(hip, oracle, wt, hd):
     # prefill passes whose grid of 64-row query tiles leaves CUs idle split each tile's keys into runs merged by
-    # k_pattn_merge: 300 rows from position 0 (8 runs, the last ones empty for the early tiles), then 100 rows at
-    # position 300 (7 non-empty runs and an empty one), then the same 100-row pass again: captured, then replayed
-    mdl = Model(760 + wt, 2, 256, 4, 2, 128, 512, wtype=wt, head_rows=64)
+    # k_pattn_merge, at both head dims of the kernel: 300 rows from position 0 (8 runs, the last ones empty for the
+    # early tiles), then 100 rows at position 300 (7 non-empty runs and an empty one), then the same 100-row pass
+    # again: captured, then replayed
+    mdl = Model(760 + wt + hd, 2, 256, 256 // hd * 2, 2, hd, 512, wtype=wt, head_rows=64)
     xf, head = build(hip, mdl)
     seq = hip.seq_create(xf, 512)
     kv = mdl.oracle_kv(512, kv_f16=1)
