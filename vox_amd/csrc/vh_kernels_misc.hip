@@ -374,6 +374,21 @@ hipError_t launch_check_split(uint64_t base, uint64_t pairs, unsigned long long 
     return launch(k_check_split, dim3(unsigned((pairs + 255) / 256)), dim3(256), 0, s, base, pairs, bad);
 }
 
+hipError_t launch_hold(double us, hipStream_t s) {
+    static int khz = 0;  // the real-time counter's rate
+    if (khz <= 0) {
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
+        if (e != hipSuccess) return e;
+        if (khz <= 0) return hipErrorInvalidValue;
+    }
+    if (!(us > 0.0) || us > 1e5) return hipErrorInvalidValue;
+    const uint64_t ticks = uint64_t(us * 1e-3 * double(khz));
+    // 512 cycles per sleep at most 2.5 GHz: about 0.2 us, so the cap is 4x the hold at any clock
+    const int max_iter = int(std::min(2e7, 4.0 * us / 0.2 + 64.0));
+    return launch(k_hold, dim3(1), dim3(64), 0, s, ticks, max_iter);
+}
 hipError_t launch_copy16(const void *src, void *dst, int64_t bytes, hipStream_t s) {
     const int64_t n = bytes / 16;
     if (n <= 0) return hipSuccess;

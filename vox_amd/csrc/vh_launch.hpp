@@ -104,6 +104,8 @@ hipError_t launch_fill_cache(void *c, int64_t planes, int64_t cap, int64_t len, 
 // max |x| over n floats into *out as float bits (the caller zeroes *out; NaN reads as above every value)
 hipError_t launch_absmax(const float *x, int64_t n, uint32_t *out, hipStream_t s);
 hipError_t launch_copy16(const void *src, void *dst, int64_t bytes, hipStream_t s);
+// A one-wave kernel that holds the stream for about `us` microseconds (0 < us <= 1e5), by the device's real-time clock.
+hipError_t launch_hold(double us, hipStream_t s);
 // k_check_split over pairs base/2 .. base/2 + pairs - 1; *bad (device) accumulates the pairs that differ.
 hipError_t launch_check_split(uint64_t base, uint64_t pairs, unsigned long long *bad, hipStream_t s);
 // Attention one block per (head, row) for any even head_dim <= 128 (q from k_qk_post, keys from each row's cache).

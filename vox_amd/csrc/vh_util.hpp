@@ -224,4 +224,16 @@ __global__ __launch_bounds__(256) void k_check_split(uint64_t base, uint64_t pai
     if (rh != hp || rl != lp) atomicAdd(bad, 1ull);
 }
 
+// One wave that returns once the constant-rate real-time counter has advanced by `ticks`, or after `max_iter` sleeps
+// of 64 x 8 cycles, whichever comes first (every launch ends). The decode benchmark's kernel-by-kernel pass puts it
+// ahead of each step's launches, so the host has enqueued the whole step when the first of them runs, and they run
+// back to back as in the graph instead of each waiting for the host's next launch.
+__global__ __launch_bounds__(64) void k_hold(uint64_t ticks, int max_iter) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (int i = 0; i < max_iter; ++i) {
+        if (__builtin_amdgcn_s_memrealtime() - t0 >= ticks) break;
+        __builtin_amdgcn_s_sleep(8);
+    }
+}
+
 }  // namespace vh

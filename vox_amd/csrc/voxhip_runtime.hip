@@ -3652,6 +3652,11 @@ extern "C" {
 }  // extern "C"
 
 namespace {
+// How long the kernel-by-kernel pass holds the stream before each step's launches: at first kBenchHoldUs, then 1.5x
+// the longest host enqueue of a step so far (stamped launches take the host about 10 us each: 1.5 ms for the 142 of
+// a 28-layer step), so every step after the first is enqueued whole before its first kernel runs.
+constexpr double kBenchHoldUs = 2000.0;
+
 // The decode benchmark for m rows: of one sequence at pos[0] .. (steps_mode false, m = 1 here), or one row of each of
 // m sequences at pos[i] (steps_mode true). Region A times the captured graph's replays; region B launches the same
 // kernels one by one, each stamped by its own events, for per-class durations and algorithmic bytes.
@@ -3735,9 +3740,19 @@ void bench_decode_impl(Xfmr &X, const std::array<int, 8> &key, int m, bool steps
         double sum_ms[VOXHIP_K_CLASSES] = {0};
         int cnt[VOXHIP_K_CLASSES] = {0};
         int per_step = -1;
+        double enq_us = 0.0;  // the longest host enqueue of a step so far
+        int short_holds = 0;  // timed steps whose enqueue outlasted their hold
         for (int it = 0; it < warmup + steps; ++it) {
             st.k = 0;
+            // the stream is held while the host enqueues the step, so its kernels run back to back as in the graph
+            // (without the hold each kernel waited for the host's next launch, and the durations moved with the host)
+            const double hold = std::min(1e5, std::max(kBenchHoldUs, 1.5 * enq_us));
+            HIPCHECK(launch_hold(hold, g.stream));
+            const auto e0 = std::chrono::steady_clock::now();
             enqueue_decode(X, m, head, dx, nullptr, nullptr, sample, d_token, g.stream, &st, steps_mode);
+            const double enq = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - e0).count();
+            if (it >= warmup && enq > hold) ++short_holds;
+            enq_us = std::max(enq_us, enq);
             HIPCHECK(hipStreamSynchronize(g.stream));
             if (per_step < 0) per_step = st.k;
             if (st.k != per_step) throw Fail("bench launch count mismatch");
@@ -3749,6 +3764,10 @@ void bench_decode_impl(Xfmr &X, const std::array<int, 8> &key, int m, bool steps
                 cnt[st.cls[size_t(i)]] += 1;
             }
         }
+        if (short_holds)  // the last launches of those steps still waited for the host
+            std::fprintf(stderr, "[voxhip bench] %d of %d timed steps took the host longer to enqueue than their hold\n",
+                         short_holds, steps);
+        if (trace) std::fprintf(stderr, "[voxhip bench] longest host enqueue of a step: %.0f us\n", enq_us);
         const int nl = X.layers;
         // ---- algorithmic bytes per launch of each class: every byte the kernel must move once
         // (weights + scales + bias, every row's activations in and out, cache reads and appends, attention partials)
