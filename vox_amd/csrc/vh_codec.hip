@@ -8,13 +8,6 @@ namespace vh {
 
 static dim3 blocks_of(int64_t n) { return dim3(unsigned((n + 255) / 256)); }
 
-hipError_t launch_snake(const float *x, const float *a, const float *inv_b, float *y, int64_t rows, int C, hipStream_t s) {
-    const int64_t n = rows * C;
-    if (n <= 0) return hipSuccess;
-    if (C <= 0 || !a || !inv_b) return hipErrorInvalidValue;
-    return launch(k_snake, blocks_of(n), dim3(256), 0, s, x, a, inv_b, y, n, int32_t(C));
-}
-
 hipError_t launch_hist_shift(float *dst, const float *old, const float *x, int64_t ldx, int T, int ctx, int C, hipStream_t s) {
     if (ctx <= 0) return hipSuccess;
     if (T <= 0 || C <= 0 || dst == old) return hipErrorInvalidValue;
@@ -30,12 +23,13 @@ hipError_t launch_dwconv_causal(const float *x, const float *hist, const float *
 }
 
 hipError_t launch_ola(const float *tmp, const float *tail_old, float *tail_new, const float *bias, float *y, int T, int stride,
-                      int K, int co, hipStream_t s) {
+                      int K, int co, hipStream_t s, float *snake_y, const float *snake_a, const float *snake_ib) {
     if (T <= 0) return hipSuccess;
     if (stride <= 0 || K < stride || K > 2 * stride || co <= 0 || !bias || (K > stride && (!tail_old || !tail_new || tail_old == tail_new)))
         return hipErrorInvalidValue;
+    if (snake_y && (!snake_a || !snake_ib || snake_y == y)) return hipErrorInvalidValue;
     return launch(k_ola, blocks_of((int64_t(T) * stride + K - stride) * co), dim3(256), 0, s, tmp, tail_old, tail_new, bias, y,
-                  int32_t(T), int32_t(stride), int32_t(K), int32_t(co));
+                  int32_t(T), int32_t(stride), int32_t(K), int32_t(co), snake_y, snake_a, snake_ib);
 }
 
 hipError_t launch_convt_gather(const float *z, const float *bias, float *y, int T, int To, int stride, int K, int pad, int co,

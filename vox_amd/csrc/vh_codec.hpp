@@ -1,22 +1,13 @@
 // vh_codec.hpp — Qwen3-TTS codec decoder kernels besides the GEMMs (qwen3.cpp:80-161, :366-481; the Vulkan shaders
-// snake / hist / dwconv / ola / ringput / attnw of gpu_codec.cpp): Snake, streaming histories, the causal depthwise
-// conv, the transposed conv's overlap-add with its tail, the pre-transformer's RoPE + ring append and sliding-window
-// attention over the ring, layer-scaled residual adds and the final clamp. Activations are time-major f32 rows.
+// snake / hist / dwconv / ola / ringput / attnw of gpu_codec.cpp): streaming histories, the causal depthwise conv,
+// the transposed conv's overlap-add with its tail (and the Snake of its output), the pre-transformer's RoPE + ring
+// append and sliding-window attention over the ring, layer-scaled residual adds and the final clamp. The other Snakes
+// are GEMM epilogues (EPI_SNAKE, EPI_ACC_SNAKE). Activations are time-major f32 rows.
 #pragma once
 #include "vh_common.hpp"
 #include "vh_types.hpp"
 
 namespace vh {
-
-// Snake (qwen3.cpp:80-89): y = x + inv_b[c] sin(a[c] x)^2 over n = R C elements (x and y may be the same).
-__global__ __launch_bounds__(256) void k_snake(const float *__restrict__ x, const float *__restrict__ a,
-                                               const float *__restrict__ inv_b, float *__restrict__ y, int64_t n, int32_t C) {
-    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= n) return;
-    const int c = int(i % C);
-    const float v = x[i], sn = sinf(v * a[c]);
-    y[i] = v + inv_b[c] * sn * sn;
-}
 
 // A streaming history after a call of T rows: the last ctx rows of [old (ctx rows); x (T rows, stride ldx)] into
 // dst (another buffer than old). qwen3.cpp:120, :136.
@@ -55,9 +46,11 @@ __global__ __launch_bounds__(256) void k_dwconv_causal(const float *__restrict__
 // trans_stream's overlap-add (qwen3.cpp:139-161) from the GEMM output tmp [T][K co] (row k co + o of frame t): output
 // row p (of T s + K - s) takes frame p / s at tap p % s and frame p / s - 1 at tap p % s + s (K <= 2 s), plus the old
 // tail's row p; rows below T s go to y with the bias, the rest to the new tail (another buffer than the old one).
+// sy, when set: Snake(y) (per-channel sa, sib) of those rows too, the first residual unit's input.
 __global__ __launch_bounds__(256) void k_ola(const float *__restrict__ tmp, const float *__restrict__ tail_old,
                                              float *__restrict__ tail_new, const float *__restrict__ bias,
-                                             float *__restrict__ y, int32_t T, int32_t s, int32_t K, int32_t co) {
+                                             float *__restrict__ y, int32_t T, int32_t s, int32_t K, int32_t co,
+                                             float *__restrict__ sy, const float *__restrict__ sa, const float *__restrict__ sib) {
     const int tr = K - s;
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
     if (i >= (int64_t(T) * s + tr) * co) return;
@@ -68,8 +61,16 @@ __global__ __launch_bounds__(256) void k_ola(const float *__restrict__ tmp, cons
     float v = p < tr ? tail_old[p * co + o] : 0.f;
     if (t < T && k < K) v += tmp[(t * K + k) * co + o];
     if (t >= 1 && k + s < K) v += tmp[((t - 1) * K + k + s) * co + o];
-    if (p < int64_t(T) * s) y[p * co + o] = v + bias[o];
-    else tail_new[(p - int64_t(T) * s) * co + o] = v;
+    if (p < int64_t(T) * s) {
+        const float yv = v + bias[o];
+        y[p * co + o] = yv;
+        if (sy) {
+            const float sn = sinf(yv * sa[o]);
+            sy[p * co + o] = yv + sib[o] * sn * sn;
+        }
+    } else {
+        tail_new[(p - int64_t(T) * s) * co + o] = v;
+    }
 }
 
 // nn::ConvT's overlap-add with padding (nn.cpp:217-245) in gather form, from the GEMM output z [T][K co] (row k co + o

@@ -66,7 +66,7 @@ static hipError_t splitk_reduce(const GemmArgs &g, int splits, hipStream_t s) {
 template <int WT, int EPI>
 static hipError_t gemm_splitk(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s, bool *done) {
     *done = false;
-    if constexpr (EPI != EPI_STORE && EPI != EPI_ACC && EPI != EPI_GATED_ACC && EPI != EPI_SWIGLU) {
+    if constexpr (EPI != EPI_STORE && EPI != EPI_ACC && EPI != EPI_GATED_ACC && EPI != EPI_SWIGLU && EPI != EPI_ACC_SNAKE) {
         return hipSuccess;
     } else {
         GemmArgs gs = g;
@@ -90,7 +90,7 @@ static hipError_t gemm_tile(const uint8_t *w, const float *scale, const float *A
         if (e != hipSuccess || split) return e;
         return gemm_run_h16<WT, EPI, 2, 2>(w, scale, A, g, s);
     } else {
-        if constexpr (EPI == EPI_STORE || EPI == EPI_ACC || EPI == EPI_GATED_ACC || EPI == EPI_SWIGLU) {
+        if constexpr (EPI == EPI_STORE || EPI == EPI_ACC || EPI == EPI_GATED_ACC || EPI == EPI_SWIGLU || EPI == EPI_ACC_SNAKE) {
             GemmArgs gs = g;  // the same K slices (few-row passes over f32 / bf16 weights)
             const int splits = split_plan(g, &gs.kchunk);
             if (splits) {
@@ -119,6 +119,8 @@ static hipError_t gemm_epi(int epi, const uint8_t *w, const float *scale, const 
         case EPI_GATED_ACC: return g.gate ? gemm_tile<WT, EPI_GATED_ACC>(w, scale, A, g, s) : hipErrorInvalidValue;
         case EPI_GELU: return gemm_tile<WT, EPI_GELU>(w, scale, A, g, s);
         case EPI_GELU_ERF: return gemm_tile<WT, EPI_GELU_ERF>(w, scale, A, g, s);
+        case EPI_ACC_SNAKE:
+            return g.snake_a && g.snake_ib && g.snake_y ? gemm_tile<WT, EPI_ACC_SNAKE>(w, scale, A, g, s) : hipErrorInvalidValue;
         case EPI_ROPE:
             if (!g.rope || g.hd <= 0 || g.hd % 2 || g.seq <= 0 || g.rope_cols % (2 * g.hd)) return hipErrorInvalidValue;
             return gemm_tile<WT, EPI_ROPE>(w, scale, A, g, s);

@@ -196,6 +196,11 @@ VH_DEV void gemm_epilogue(const f32x4v (&acc)[TM][TN], const GemmArgs &g, int m0
                         const float sn = sinf(c * g.snake_a[col]);
                         *dst = c + g.snake_ib[col] * sn * sn;
                     }
+                    else if (EPI == EPI_ACC_SNAKE) {
+                        const float v = *dst + c, sn = sinf(v * g.snake_a[col]);
+                        *dst = v;
+                        g.snake_y[int64_t(row) * g.ldy + col] = v + g.snake_ib[col] * sn * sn;
+                    }
                     else if (EPI == EPI_MISH) *dst = mish_f(c);
                     else if (EPI == EPI_MISH_ACC) *dst += mish_f(c);
                 }
@@ -852,6 +857,11 @@ __global__ __launch_bounds__(256) void k_gemm_splitk_reduce(GemmArgs g, int32_t 
     else if (EPI == EPI_SNAKE) {
         const float v = sum(c), sn = sinf(v * g.snake_a[c]);
         *dst = v + g.snake_ib[c] * sn * sn;
+    }
+    else if (EPI == EPI_ACC_SNAKE) {
+        const float v = *dst + sum(c), sn = sinf(v * g.snake_a[c]);
+        *dst = v;
+        g.snake_y[int64_t(row) * g.ldy + c] = v + g.snake_ib[c] * sn * sn;
     }
 }
 

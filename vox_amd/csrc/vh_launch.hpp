@@ -124,15 +124,17 @@ hipError_t launch_norm_rows(const NormArgs &a, hipStream_t s);
 hipError_t launch_dwconv(const float *x, const float *w, const float *b, float *y, int64_t R, int C, int K, int seq, hipStream_t s);
 hipError_t launch_f5_attn(const _Float16 *qkv16, int64_t lo_off, float *out, _Float16 *out16, int64_t out_lo, int B, int N,
                           int heads, int hd, int ldvt, int ldo, float scale, hipStream_t s);
-// Qwen3-TTS codec decoder: Snake, streaming histories (dst != old), the causal depthwise conv, the transposed conv's
-// overlap-add (tail_old -> tail_new, K <= 2 stride), the pre-transformer's RoPE + ring append and windowed attention,
+// Qwen3-TTS codec decoder: streaming histories (dst != old), the causal depthwise conv, the transposed conv's
+// overlap-add (tail_old -> tail_new, K <= 2 stride, with an optional Snake output), the pre-transformer's RoPE + ring
+// append and windowed attention,
 // layer-scaled residual adds, the final clamp; and the streaming conv GEMM (A = im2col of [hist; x]).
-hipError_t launch_snake(const float *x, const float *a, const float *inv_b, float *y, int64_t rows, int C, hipStream_t s);
 hipError_t launch_hist_shift(float *dst, const float *old, const float *x, int64_t ldx, int T, int ctx, int C, hipStream_t s);
 hipError_t launch_dwconv_causal(const float *x, const float *hist, const float *w, const float *b, float *y, int T, int C, int K,
                                 hipStream_t s, float *hist_next = nullptr);
+// snake_y (optional, another buffer than y): Snake (snake_a, snake_ib per channel) of the rows written to y, as well.
 hipError_t launch_ola(const float *tmp, const float *tail_old, float *tail_new, const float *bias, float *y, int T, int stride,
-                      int K, int co, hipStream_t s);
+                      int K, int co, hipStream_t s, float *snake_y = nullptr, const float *snake_a = nullptr,
+                      const float *snake_ib = nullptr);
 // nn::ConvT's padded overlap-add (gather form) from the GEMM output z [T][K co] to y [To][co] (+ bias when not null).
 hipError_t launch_convt_gather(const float *z, const float *bias, float *y, int T, int To, int stride, int K, int pad, int co,
                                hipStream_t s);

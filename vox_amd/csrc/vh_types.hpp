@@ -16,9 +16,9 @@ enum { EPI_STORE = 0, EPI_ACC = 1, EPI_SWIGLU = 2 };
 // GemvArgs::yq / yqs / yqsum for the next pass (which takes them as its PRO_Q rows) instead of stored as floats
 enum { EPI_SWIGLU_Q = 13 };
 // GEMM-only epilogues (F5 DiT, Vocos, the codec): y += gate * c; y = gelu_tanh(c); y = mish(c); y += mish(c); RoPE on
-// q|k columns; y = gelu_erf(c); y = snake(c)
+// q|k columns; y = gelu_erf(c); y = snake(c); y += c, then snake(y) into snake_y as well
 enum { EPI_GATED_ACC = 3, EPI_GELU = 4, EPI_MISH = 5, EPI_MISH_ACC = 6, EPI_ROPE = 7, EPI_ROPE_H16 = 8, EPI_GELU_H16 = 9,
-       EPI_GELU_ERF = 10, EPI_SNAKE = 11, EPI_SWIGLU_H16 = 12 };
+       EPI_GELU_ERF = 10, EPI_SNAKE = 11, EPI_SWIGLU_H16 = 12, EPI_ACC_SNAKE = 14 };
 // GEMM A operand: rows of a matrix, or the implicit im2col rows of a grouped "same" Conv1d
 enum { ASRC_ROWS = 0, ASRC_CONV = 1, ASRC_STREAM = 2 };
 // Weight formats of the GEMV kernels: the reference's types, plus Q4 with f16 block scales (WT_Q4H), the
@@ -206,8 +206,11 @@ struct GemmArgs {
     // [hist (ctx rows of cig); x (rows of lda)], ctx = (ksize - 1) dil
     const float *hist;
     int32_t ctx, dil;
-    // EPI_SNAKE: y = v + snake_ib[col] sin(snake_a[col] v)^2 of v = c + bias (the codec's Snake after a convolution)
+    // EPI_SNAKE: y = v + snake_ib[col] sin(snake_a[col] v)^2 of v = c + bias (the codec's Snake after a convolution);
+    // EPI_ACC_SNAKE: y += c + bias, then the same Snake of the updated y into snake_y ([m][ldy]; the next residual
+    // unit's or block's input)
     const float *snake_a, *snake_ib;
+    float *snake_y;
     // ASRC_STREAM: when set, the launch also writes the history of the next call, the last ctx rows of [hist; x], to
     // hist_next (another buffer than hist), each block a share
     float *hist_next;

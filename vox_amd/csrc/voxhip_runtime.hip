@@ -3128,11 +3128,13 @@ void codec_conv(const CodecConv &c, Hist2 *h, int par, const float *X, int64_t l
 }
 // y (=, +=, gelu, gamma-gated +=) W x + bias over rows of the f32-activation GEMM (the f32 tile semantics of matmul
 // for F32 / F16 / BF16 weights at any row count).
+// snake / snake_y (EPI_ACC_SNAKE): Snake of the updated rows into snake_y as well.
 void codec_gemm(int mat, int epi, const float *A, int64_t lda, int64_t rows, float *Y, int64_t ldy, const float *gate,
-                hipStream_t s) {
+                hipStream_t s, const CodecSnake *snake = nullptr, float *snake_y = nullptr) {
     const GpuMat &M = mat_at(mat);
     GemmArgs ga = gemm_args(M, M.b, Y, lda, ldy, rows);
     ga.gate = gate;
+    if (snake) { ga.snake_a = snake->a; ga.snake_ib = snake->inv_b; ga.snake_y = snake_y; }
     HIPCHECK(launch_gemm(gemv_type(M), epi, M.w, M.s, A, ga, s));
 }
 
@@ -3177,29 +3179,31 @@ int64_t codec_enqueue(Codec &E, CodecSt &St, int T, hipStream_t s) {
         codec_gemm(U.pw2, EPI_GATED_ACC, E.S[4], 4 * int64_t(L), len, y, L, U.gamma, s);
         cur = y;
     }
-    // 4) conv0 -> blocks -> Snake -> final conv -> clamp
-    float *x = cur == A ? B : A;
-    codec_conv(E.conv0, &St.c0, par, cur, L, int(len), x, E.dec, s);
+    // 4) conv0 -> blocks -> Snake -> final conv -> clamp. Every Snake rides on the launch that produces its input
+    // (the same float in, the same formula): conv0's epilogue gives the first block's Snake(x) (x itself is not read
+    // again), the overlap-add gives each block's first unit its input as well as y, and each unit's residual product
+    // (EPI_ACC_SNAKE) the next unit's, the next block's or the final one's.
+    float *sa = cur == A ? B : A;  // the Snake of the rows the next product reads
+    float *x = cur;                // consumed by conv0: the blocks' rows y go here
+    auto next_act = [&](size_t bi) -> const CodecSnake & { return bi < E.blocks.size() ? E.blocks[bi].act : E.fin_act; };
+    codec_conv(E.conv0, &St.c0, par, cur, L, int(len), sa, E.dec, s, &next_act(0));
     int ch = E.dec;
     for (size_t bi = 0; bi < E.blocks.size(); ++bi) {
         const CodecBlk &Bk = E.blocks[bi];
-        float *sa = x == A ? B : A;
-        HIPCHECK(launch_snake(x, Bk.act.a, Bk.act.inv_b, sa, len, ch, s));
         codec_gemm(Bk.tr, EPI_STORE, sa, ch, len, E.S[2], int64_t(Bk.K) * Bk.cout, nullptr, s);
         float *y = x;  // x is consumed
         Hist2 &tl = St.tail[bi];
-        HIPCHECK(launch_ola(E.S[2], tl.b[par], tl.b[1 - par], Bk.tr_b, y, int(len), Bk.s, Bk.K, Bk.cout, s));
+        HIPCHECK(launch_ola(E.S[2], tl.b[par], tl.b[1 - par], Bk.tr_b, y, int(len), Bk.s, Bk.K, Bk.cout, s, sa, Bk.a1[0].a,
+                            Bk.a1[0].inv_b));
         len *= Bk.s;
         ch = Bk.cout;
         for (int u = 0; u < 3; ++u) {
-            HIPCHECK(launch_snake(y, Bk.a1[u].a, Bk.a1[u].inv_b, sa, len, ch, s));
             codec_conv(Bk.c1[u], &St.ru[bi * 3 + size_t(u)], par, sa, ch, int(len), E.S[3], ch, s, &Bk.a2[u]);  // + Snake a2
-            codec_gemm(Bk.c2[u].mat, EPI_ACC, E.S[3], ch, len, y, ch, nullptr, s);
+            const CodecSnake &nx = u < 2 ? Bk.a1[u + 1] : next_act(bi + 1);
+            codec_gemm(Bk.c2[u].mat, EPI_ACC_SNAKE, E.S[3], ch, len, y, ch, nullptr, s, &nx, sa);
         }
         x = y;
     }
-    float *sa = x == A ? B : A;
-    HIPCHECK(launch_snake(x, E.fin_act.a, E.fin_act.inv_b, sa, len, ch, s));
     codec_conv(E.fin, &St.fin, par, sa, ch, int(len), E.S[4], 1, s);
     HIPCHECK(launch_clamp1(E.S[4], len, s));
     return len;
