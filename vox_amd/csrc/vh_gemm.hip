@@ -42,20 +42,30 @@ static hipError_t gemm_run_h16(const uint8_t *w, const float *scale, const float
 }
 
 // Split K for a grid of 64 x 64 tiles too small to fill the CUs with a long K (prefill down projections, small
-// matrices): up to 8 slices of K, each a multiple of 64 columns, summed in order by the reduce pass. Slices are
+// matrices): up to 8 slices of K (32 for grids under 64 tiles), each a multiple of 64 columns, summed in order by the
+// reduce pass. Slices are
 // added until the launch has about kSplitTargetBlocks blocks (two per CU: measured faster than one per CU on the
 // 512-row prefill shapes even with the larger reduce).
 constexpr int64_t kSplitTargetBlocks = 512;
+constexpr int64_t kSplitMaxSmall = 32;
 // The K slices for a split of g (64 x 64 tiles): 0 when the tiles already fill the CUs, K is short or the workspace
-// is too small; else the slice count, with *kchunk the slice width (a multiple of 64).
+// is too small; else the slice count, with *kchunk the slice width (a multiple of 64). A grid of fewer than 192
+// tiles gets enough slices for about kSplitTargetBlocks blocks, at most 8, or at most kSplitMaxSmall for grids of
+// under 64 tiles (few-row passes over large weights, such as a streaming codec frame's convolutions, whose tiles
+// would otherwise each stream megabytes of weights) when their partials fit the workspace.
 static int split_plan(const GemmArgs &g, int *kchunk) {
     const int64_t blocks = int64_t((g.n + 63) / 64) * ((g.m + 63) / 64);
     if (!g.ws || blocks >= 192 || g.K < 512) return 0;
-    int splits = int(std::min<int64_t>(8, (kSplitTargetBlocks + blocks - 1) / blocks));
-    *kchunk = ((g.K + splits - 1) / splits + 63) / 64 * 64;
-    splits = (g.K + *kchunk - 1) / *kchunk;
-    if (splits < 2 || int64_t(splits) * g.m * g.n > g.ws_cap) return 0;
-    return splits;
+    const int64_t want = (kSplitTargetBlocks + blocks - 1) / blocks;
+    auto plan = [&](int64_t cap) {
+        int splits = int(std::min<int64_t>(cap, want));
+        *kchunk = ((g.K + splits - 1) / splits + 63) / 64 * 64;
+        splits = (g.K + *kchunk - 1) / *kchunk;
+        return splits < 2 || int64_t(splits) * g.m * g.n > g.ws_cap ? 0 : splits;
+    };
+    if (want > 8)
+        if (const int splits = plan(kSplitMaxSmall)) return splits;
+    return plan(8);
 }
 template <int EPI>
 static hipError_t splitk_reduce(const GemmArgs &g, int splits, hipStream_t s) {

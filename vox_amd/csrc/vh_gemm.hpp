@@ -830,8 +830,8 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(Q8 ? 4
     gemm_epilogue<EPI, TM, TN>(acc, g, m0, n0, wm, wn, lane);
 }
 
-// The split-K partial slices ws[z][m][n] (at most 8), added in z order, then bias and the epilogue (STORE, ACC,
-// GATED_ACC, SWIGLU: one thread per output element; SWIGLU outputs pair columns 2u, 2u + 1). grid ceil(m n' / 256).
+// The split-K partial slices ws[z][m][n], added in z order, then bias and the epilogue (STORE, ACC, GATED_ACC, SWIGLU,
+// SNAKE, ACC_SNAKE: one thread per output element; SWIGLU outputs pair columns 2u, 2u + 1). grid ceil(m n' / 256).
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm_splitk_reduce(GemmArgs g, int32_t splits) {
     const int nout = EPI == EPI_SWIGLU ? g.n / 2 : g.n;
@@ -839,14 +839,16 @@ __global__ __launch_bounds__(256) void k_gemm_splitk_reduce(GemmArgs g, int32_t 
     if (t >= int64_t(g.m) * nout) return;
     const int row = int(t / nout), c = int(t % nout);
     const int64_t slice = int64_t(g.m) * g.n;
-    auto sum = [&](int col) {  // every slice's load in flight at once (past `splits`, slice 0, left out), added in order
-        float t[8];
-#pragma unroll
-        for (int z = 0; z < 8; ++z) t[z] = g.ws[(z < splits ? z : 0) * slice + int64_t(row) * g.n + col];
+    auto sum = [&](int col) {  // 8 slices' loads in flight at once (past `splits`, slice 0, left out), added in order
         float v = 0.f;
+        for (int z0 = 0; z0 < splits; z0 += 8) {
+            float t[8];
 #pragma unroll
-        for (int z = 0; z < 8; ++z)
-            if (z < splits) v += t[z];
+            for (int z = 0; z < 8; ++z) t[z] = g.ws[(z0 + z < splits ? z0 + z : 0) * slice + int64_t(row) * g.n + col];
+#pragma unroll
+            for (int z = 0; z < 8; ++z)
+                if (z0 + z < splits) v += t[z];
+        }
         return v + (g.bias ? g.bias[col] : 0.f);
     };
     float *dst = g.y + int64_t(row) * g.ldy + c;
