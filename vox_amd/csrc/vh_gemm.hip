@@ -48,6 +48,7 @@ static hipError_t gemm_run_h16(const uint8_t *w, const float *scale, const float
 // 512-row prefill shapes even with the larger reduce).
 constexpr int64_t kSplitTargetBlocks = 512;
 constexpr int64_t kSplitMaxSmall = 32;
+constexpr int64_t kSplitTargetOneRow = 1024;
 // The K slices for a split of g (64 x 64 tiles): 0 when the tiles already fill the CUs, K is short or the workspace
 // is too small; else the slice count, with *kchunk the slice width (a multiple of 64). A grid of fewer than 192
 // tiles gets enough slices for about kSplitTargetBlocks blocks, at most 8, or at most kSplitMaxSmall for grids of
@@ -55,8 +56,12 @@ constexpr int64_t kSplitMaxSmall = 32;
 // would otherwise each stream megabytes of weights) when their partials fit the workspace.
 static int split_plan(const GemmArgs &g, int *kchunk) {
     const int64_t blocks = int64_t((g.n + 63) / 64) * ((g.m + 63) / 64);
-    if (!g.ws || blocks >= 192 || g.K < 512) return 0;
-    const int64_t want = (kSplitTargetBlocks + blocks - 1) / blocks;
+    // one row tile: every tile streams its own columns of the weights, so such grids take slices up to about
+    // kSplitTargetOneRow blocks (a streaming codec frame's transposed convolutions and pointwise products)
+    const bool one_row = g.m <= 64 && blocks < kSplitTargetOneRow / 2;
+    if (!g.ws || (blocks >= 192 && !one_row) || g.K < 512) return 0;
+    const int64_t target = one_row ? kSplitTargetOneRow : kSplitTargetBlocks;
+    const int64_t want = (target + blocks - 1) / blocks;
     auto plan = [&](int64_t cap) {
         int splits = int(std::min<int64_t>(cap, want));
         *kchunk = ((g.K + splits - 1) / splits + 63) / 64 * 64;
@@ -76,7 +81,8 @@ static hipError_t splitk_reduce(const GemmArgs &g, int splits, hipStream_t s) {
 template <int WT, int EPI>
 static hipError_t gemm_splitk(const uint8_t *w, const float *scale, const float *A, const GemmArgs &g, hipStream_t s, bool *done) {
     *done = false;
-    if constexpr (EPI != EPI_STORE && EPI != EPI_ACC && EPI != EPI_GATED_ACC && EPI != EPI_SWIGLU && EPI != EPI_ACC_SNAKE) {
+    if constexpr (EPI != EPI_STORE && EPI != EPI_ACC && EPI != EPI_GATED_ACC && EPI != EPI_SWIGLU && EPI != EPI_ACC_SNAKE &&
+                  EPI != EPI_GELU_ERF) {
         return hipSuccess;
     } else {
         GemmArgs gs = g;
@@ -100,7 +106,8 @@ static hipError_t gemm_tile(const uint8_t *w, const float *scale, const float *A
         if (e != hipSuccess || split) return e;
         return gemm_run_h16<WT, EPI, 2, 2>(w, scale, A, g, s);
     } else {
-        if constexpr (EPI == EPI_STORE || EPI == EPI_ACC || EPI == EPI_GATED_ACC || EPI == EPI_SWIGLU || EPI == EPI_ACC_SNAKE) {
+        if constexpr (EPI == EPI_STORE || EPI == EPI_ACC || EPI == EPI_GATED_ACC || EPI == EPI_SWIGLU || EPI == EPI_ACC_SNAKE ||
+                      EPI == EPI_GELU_ERF) {
             GemmArgs gs = g;  // the same K slices (few-row passes over f32 / bf16 weights)
             const int splits = split_plan(g, &gs.kchunk);
             if (splits) {

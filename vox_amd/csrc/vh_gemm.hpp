@@ -831,7 +831,8 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(Q8 ? 4
 }
 
 // The split-K partial slices ws[z][m][n], added in z order, then bias and the epilogue (STORE, ACC, GATED_ACC, SWIGLU,
-// SNAKE, ACC_SNAKE: one thread per output element; SWIGLU outputs pair columns 2u, 2u + 1). grid ceil(m n' / 256).
+// SNAKE, GELU_ERF, ACC_SNAKE: one thread per output element; SWIGLU outputs pair columns 2u, 2u + 1). grid
+// ceil(m n' / 256).
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm_splitk_reduce(GemmArgs g, int32_t splits) {
     const int nout = EPI == EPI_SWIGLU ? g.n / 2 : g.n;
@@ -860,6 +861,7 @@ __global__ __launch_bounds__(256) void k_gemm_splitk_reduce(GemmArgs g, int32_t 
         const float v = sum(c), sn = sinf(v * g.snake_a[c]);
         *dst = v + g.snake_ib[c] * sn * sn;
     }
+    else if (EPI == EPI_GELU_ERF) *dst = gelu_erf_f(sum(c));
     else if (EPI == EPI_ACC_SNAKE) {
         const float v = *dst + sum(c), sn = sinf(v * g.snake_a[c]);
         *dst = v;
